@@ -1,0 +1,218 @@
+"""Fit throughput of the binary histogram-GBM path on one MI355X.
+
+A step is one boosting round of HybridHistGBMNumbaV1_0_1.fit: gradients,
+the round's bagging sample, one leaf-wise tree, the F update over all rows
+and the training loss.  W rounds run untimed, then K rounds are timed; every
+round ends with a stream synchronisation, so wall-clock time over the K
+rounds is the device time including host work.
+
+Prints one JSON line with the fit rate (trees/s), the histogram kernel's
+roofline (algorithmic bytes per launch over its average HIP-event duration,
+against 8 TB/s HBM) and the oracle's CPU rate on a bounded sample.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "bsscl-gbm_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "fit trees/sec at 1M×28 d6 255 bins; histogram-build HBM GB/s vs peak"
+
+
+def _sigmoid(z):
+    return 1.0 / (1.0 + np.exp(-z))
+
+
+def make_workload(name, predict=False):
+    """Synthetic inputs of the benchmark shapes (float32 X, int64 y) and the
+    estimator parameters each is quoted with."""
+    if name == "cpu_plumbing":  # 10,000 x 20, 10 trees, depth 6
+        rng = np.random.default_rng(0 if not predict else 100)
+        X = rng.standard_normal((10_000, 20), dtype=np.float32)
+        w = rng.standard_normal(20)
+        y = (rng.random(10_000) < _sigmoid(X @ w)).astype(np.int64)
+        params = dict(n_estimators=10, max_depth=6, learning_rate=0.1, class_weight=None)
+    elif name == "dense_1m":  # 1,000,000 x 28, 5% NaN, 100 trees, depth 6
+        rng = np.random.default_rng(1 if not predict else 101)
+        n = 1_000_000
+        X = rng.standard_normal((n, 28), dtype=np.float32)
+        logit = sum(X[:, 2 * k].astype(np.float64) * X[:, 2 * k + 1] for k in range(5))
+        logit = logit + 0.5 * rng.standard_normal(n)
+        y = (rng.random(n) < _sigmoid(logit)).astype(np.int64)
+        X[rng.random(X.shape) < 0.05] = np.nan
+        params = dict(n_estimators=100, max_depth=6)
+    elif name == "imbalanced":  # 284,807 x 30, 0.17% positives
+        rng = np.random.default_rng(2 if not predict else 102)
+        n = 284_807
+        sig = np.linspace(2.0, 0.3, 28)
+        V = rng.standard_normal((n, 28)) * sig
+        t = rng.uniform(0, 172_792, n)
+        amt = rng.lognormal(3, 1.5, n)
+        y = np.zeros(n, np.int64)
+        y[rng.choice(n, 484, replace=False)] = 1
+        V[y == 1, :10] += 1.5 * sig[:10]
+        X = np.column_stack([t, V, amt]).astype(np.float32)
+        params = dict(n_estimators=200, max_depth=6, class_weight="balanced_sqrt")
+    elif name == "sparse_hd":  # 100,000 x 100, 90% zeros
+        rng = np.random.default_rng(3 if not predict else 103)
+        n = 100_000
+        X = np.where(rng.random((n, 100)) < 0.9, 0.0, rng.exponential(1.0, (n, 100))).astype(np.float32)
+        w = rng.standard_normal(8)
+        s = X[:, :8].astype(np.float64) @ w + rng.logistic(size=n)
+        y = (s > np.quantile(s, 0.99)).astype(np.int64)
+        flip = rng.random(n) < 0.05
+        y[flip] = 1 - y[flip]
+        params = dict(n_estimators=300, max_depth=6, class_weight="balanced_sqrt")
+    elif name == "stress_10m":  # 10,000,000 x 50, 10 columns 70% NaN, depth 8
+        rng = np.random.default_rng(4 if not predict else 5)
+        n = 10_000_000
+        X = rng.standard_normal((n, 50), dtype=np.float32)
+        X64 = X[:, :10].astype(np.float64)
+        logit = (np.sin(2 * X64[:, 0]) + X64[:, 1] * X64[:, 2] + (X64[:, 3] ** 2 - 1)
+                 + np.tanh(X64[:, 4]) + (np.abs(X64[:, 5]) - 0.798) + X64[:, 6] * X64[:, 7]
+                 + 0.5 * X64[:, 8] - 0.5 * X64[:, 9])
+        del X64
+        y = (rng.random(n) < _sigmoid(logit)).astype(np.int64)
+        block = X[:, 40:50]
+        block[rng.random(block.shape) < 0.7] = np.nan
+        X[:, 40:50] = block
+        params = dict(n_estimators=500, max_depth=8)
+    else:
+        raise SystemExit(f"unknown workload {name!r}")
+    params.update(n_bins=255, random_state=0, verbose=False)
+    return X, y, params
+
+
+def run_gpu(name, steps, warmup):
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    X, y, params = make_workload(name)
+    n, F = X.shape
+    marks = {}
+
+    def hook(m, eng):
+        if m == warmup:
+            eng.set_profiling(True)
+            marks["t0"] = time.perf_counter()
+        if m == warmup + steps:
+            marks["t1"] = time.perf_counter()
+            marks["stats"] = eng.stats()
+            eng.set_profiling(False)
+
+    params = dict(params, n_estimators=warmup + steps)
+    est = HybridHistGBMNumbaV1_0_1(**params)
+    est._round_hook = hook
+    t_fit = time.perf_counter()
+    est.fit(X, y)
+    t_fit = time.perf_counter() - t_fit
+    del est._round_hook
+    elapsed = marks["t1"] - marks["t0"]
+    st = marks["stats"]
+    # Prediction on fresh rows through the fitted trees.
+    Xp, _, _ = make_workload(name, predict=True)
+    t = time.perf_counter()
+    est.predict_proba(Xp)
+    t_pred_total = time.perf_counter() - t
+    return dict(est=est, n=n, F=F, elapsed=elapsed, stats=st, t_fit=t_fit,
+                t_pred_total=t_pred_total, pred_rows=len(Xp),
+                t_pred_dev=est.times["inference"] / 1e3, params=params)
+
+
+def run_cpu_baseline(name, rounds):
+    """The oracle (C/OpenMP restatement of the reference path, serial where
+    the reference is serial) timed on this host for `rounds` rounds."""
+    from oracle import model as om
+    X, y, params = make_workload(name)
+    p = dict(params)
+    p.pop("verbose")
+    m = om.OracleGBM(**p)
+    m.fit(X, y, max_rounds=rounds + 1)
+    t = np.diff(m.round_times_)[1:]  # first round excluded (page-in)
+    cores = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit():
+        cores = min(cores, int(omp))
+    return dict(value=float(len(t) / t.sum()), unit="trees/s", cores=cores,
+                kind="port",
+                sample=f"rounds 2-{rounds + 1} of the same {name} fit "
+                       f"({X.shape[0]}x{X.shape[1]}), oracle/oracle.c via OracleGBM")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="dense_1m")
+    ap.add_argument("--cpu-rounds", type=int, default=4)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this engine runs on one GPU; --gpus must be 1 "
+                                   "(row sharding across GPUs is not built)"}))
+        sys.exit(2)
+    r = run_gpu(a.workload, a.steps, a.warmup)
+    st = r["stats"]
+    trees_per_s = a.steps / r["elapsed"]
+    hist_s = st["hist_ms"] / 1e3
+    achieved = st["hist_bytes"] / hist_s / 1e9 if hist_s > 0 else 0.0
+    launches = max(st["hist_launches"], 1.0)
+    line = {
+        "metric": METRIC,
+        "value": round(trees_per_s, 3),
+        "unit": "trees/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(1e3 * r["elapsed"] / a.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int64",
+        "data": "synthetic",
+        "config": {
+            "workload": a.workload,
+            "rows": r["n"], "features": r["F"],
+            "max_depth": r["params"]["max_depth"], "n_bins": 255,
+            "max_leaves": int(r["est"].max_leaves),
+            "subsample": r["est"].subsample, "colsample_bytree": r["est"].colsample_bytree,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "k_hist",
+            "launches": int(st["hist_launches"]),
+            "avg_launch_us": round(1e3 * st["hist_ms"] / launches, 2),
+            "bytes_per_launch": round(st["hist_bytes"] / launches),
+        },
+        "hist_rows_x_features_per_s": round(st["hist_row_features"] / hist_s) if hist_s > 0 else None,
+        "predict_rows_per_s": round(r["pred_rows"] / r["t_pred_dev"]) if r["t_pred_dev"] > 0 else None,
+        "predict_rows_per_s_end_to_end": round(r["pred_rows"] / r["t_pred_total"]),
+        "kernel_ms_per_step": {
+            "hist": round(st["hist_ms"] / a.steps, 3),
+            "partition": round(st["part_ms"] / a.steps, 3),
+            "split": round(st["split_ms"] / a.steps, 3),
+        },
+        "nodes_expanded_per_tree": round(st["nodes_expanded"] / max(st["trees"], 1), 2),
+    }
+    if not a.no_cpu_baseline:
+        line["cpu_baseline"] = run_cpu_baseline(a.workload, a.cpu_rounds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

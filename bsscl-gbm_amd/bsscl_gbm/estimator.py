@@ -1,0 +1,608 @@
+"""Drop-in ``HybridHistGBMNumbaV1_0_1`` whose fit/predict run on the MI355X
+engine.
+
+The public surface -- constructor parameters and their 'auto' resolution,
+``fit``/``predict``/``predict_proba``, ``get_params``/``set_params``, the
+fitted attributes (``trees``, ``bin_edges``, ``feature_bin_counts``,
+``base_score_``, ``train_loss_history_``, ``feature_importances_``, the packed
+tree arrays, ``times``) -- follows the reference class
+``HybridHistGBMNumbaV1_0_1`` in src/bsscl_gbm/estimator_v1_0_1.py ("est:"
+below, class at est:1776).  Host logic that decides results (parameter
+resolution, bin edges, class weights, base score, the random stream) is the
+reference's NumPy code path; every per-row loop (binning, gradients, trees,
+F updates, prediction) runs in libbsscl_hip.so.
+
+Covered: binary classification (two classes, objective 'auto' or 'binary'),
+grow_policy='leaf', sampling_method='uniform', boosting_type='gbdt', numeric
+features with NaN, class_weight None/'balanced'/'balanced_sqrt',
+scale_pos_weight, eval_set with early stopping.  Other modes of the
+reference raise NotImplementedError instead of computing something else.
+"""
+from __future__ import annotations
+
+import os
+import time
+
+import numpy as np
+
+from . import _native
+
+__all__ = ["HybridHistGBMNumbaV1_0_1"]
+
+_ENGINES: dict = {}
+
+
+def _engine(device: int) -> _native.Engine:
+    """Per-process engine cache; a forked child creates its own."""
+    key = (os.getpid(), int(device))
+    eng = _ENGINES.get(key)
+    if eng is None:
+        for k in [k for k in _ENGINES if k[0] != os.getpid()]:
+            _ENGINES.pop(k)._h = None  # the parent's handle is not ours to free
+        eng = _native.Engine(device)
+        _ENGINES[key] = eng
+    return eng
+
+
+def _to_dense(X):
+    try:
+        import scipy.sparse
+        if scipy.sparse.issparse(X):
+            return X.toarray()
+    except ImportError:
+        pass
+    return X
+
+
+def _as_float(X):
+    """est:3197-3201: non-float and float16 inputs become float64; float32
+    and float64 are kept."""
+    X = np.asarray(X)
+    if not np.issubdtype(X.dtype, np.floating) or X.dtype == np.float16:
+        X = X.astype(np.float64)
+    return X
+
+
+def _sigmoid(F):
+    return 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
+
+
+class HybridHistGBMNumbaV1_0_1:
+    """Histogram GBM with the reference's parameters (est:1820-1923)."""
+
+    def __init__(self, n_estimators='auto', max_depth='auto', learning_rate='auto',
+                 n_bins='auto', reg_lambda=1.0, min_samples_leaf=5,
+                 min_child_weight='auto', gamma='auto',
+                 subsample='auto', colsample_bytree='auto',
+                 class_weight='balanced_sqrt',
+                 grow_policy='leaf', max_leaves=31, binning_strategy='auto',
+                 monotone_constraints=None, categorical_features=None,
+                 early_stopping_rounds=None, verbose=True, random_state=None,
+                 objective='auto', focal_gamma=2.0, loss='mse', device='cpu',
+                 sampling_method='uniform', top_rate=0.2, other_rate=0.1,
+                 scale_pos_weight=None,
+                 custom_objective=None,
+                 boosting_type='gbdt',
+                 dart_rate=0.1,
+                 interaction_constraints=None):
+        self.binning_strategy_init = binning_strategy
+        self.n_estimators_init = n_estimators
+        self.max_depth_init = max_depth
+        self.learning_rate_init = learning_rate
+        self.n_bins_init = n_bins
+        self.reg_lambda = reg_lambda
+        self.min_samples_leaf = min_samples_leaf
+        self.min_child_weight_init = min_child_weight
+        self.gamma_init = gamma
+        self.subsample_init = subsample
+        self.colsample_init = colsample_bytree
+        # The reference's 'cpu'/'cuda' selects a Numba path; here every
+        # device string runs the HIP engine.  An integer selects the GPU.
+        self.device = device
+        self.sampling_method = sampling_method
+        self.top_rate = top_rate
+        self.other_rate = other_rate
+        self.scale_pos_weight = scale_pos_weight
+        self.class_weight = class_weight
+        self.grow_policy = grow_policy
+        self.custom_objective = custom_objective
+        self.boosting_type = boosting_type
+        self.dart_rate = dart_rate
+        self.interaction_constraints = interaction_constraints
+        self.max_leaves = max_leaves
+        self.monotone_constraints = monotone_constraints
+        self.categorical_features = categorical_features
+        self.early_stopping_rounds = early_stopping_rounds
+        self.verbose = verbose
+        self.random_state = random_state
+
+        self.n_estimators = 100 if n_estimators == 'auto' else n_estimators
+        self.max_depth = 5 if max_depth == 'auto' else max_depth
+        self.learning_rate = 0.1 if learning_rate == 'auto' else learning_rate
+        self.n_bins = 256 if n_bins == 'auto' else n_bins
+        self.min_child_weight = 1.0 if min_child_weight == 'auto' else min_child_weight
+        self.gamma = 0.0 if gamma == 'auto' else gamma
+        self.subsample = 0.8 if subsample == 'auto' else subsample
+        self.colsample_bytree = 0.8 if colsample_bytree == 'auto' else colsample_bytree
+        self.objective = objective
+        self.focal_gamma = focal_gamma
+        self.loss = loss
+        self.init_score_ = 0.0
+
+        self.trees = []
+        self.bin_edges = None
+        self.feature_bin_counts = None
+        self._max_bins = 0
+        self.n_features_in_ = None
+        self.n_classes_ = 2
+        self.classes_ = None
+        self._is_multiclass = False
+        self.mc_trees = None
+        self.feature_importances_ = None
+        self.feature_split_counts_ = None
+        self.train_loss_history_ = []
+        self.val_loss_history_ = []
+        self.n_trees_fitted_ = 0
+        self.best_iteration_ = 0
+        self.times = {'binning': 0.0, 'training': 0.0, 'inference': 0.0}
+        self._packed_features = None
+        self._packed_thresholds = None
+        self._packed_values = None
+        self._packed_left = None
+        self._packed_right = None
+        self._tree_offsets = None
+        self._mc_packed = None
+        self._auto_no_weights = False
+        self._auto_full_weights = False
+        self._categorical_set = set()
+        self._is_categorical = None
+        self._nan_bin_id = None
+
+    # ------------------------------------------------------------------
+    # Pickling: no device handle is ever stored on the instance.
+    # ------------------------------------------------------------------
+    def _device_index(self):
+        return self.device if isinstance(self.device, (int, np.integer)) else 0
+
+    def _check_supported(self):
+        unsupported = []
+        if self.objective not in ('auto', 'binary'):
+            unsupported.append(f"objective={self.objective!r}")
+        if self.grow_policy != 'leaf':
+            unsupported.append(f"grow_policy={self.grow_policy!r}")
+        if self.sampling_method != 'uniform':
+            unsupported.append(f"sampling_method={self.sampling_method!r}")
+        if getattr(self, 'boosting_type', 'gbdt') != 'gbdt':
+            unsupported.append(f"boosting_type={self.boosting_type!r}")
+        if self.categorical_features is not None:
+            unsupported.append("categorical_features")
+        if self.monotone_constraints is not None:
+            unsupported.append("monotone_constraints")
+        if getattr(self, 'custom_objective', None) is not None:
+            unsupported.append("custom_objective")
+        if unsupported:
+            raise NotImplementedError(
+                "the MI355X engine covers the binary leaf-wise histogram path; "
+                "not supported: " + ", ".join(unsupported))
+
+    # ------------------------------------------------------------------
+    # est:1925-2029
+    # ------------------------------------------------------------------
+    def _compute_adaptive_hyperparameters(self, X, y):
+        n, p = X.shape
+        K = self.n_classes_
+        if self.binning_strategy_init == 'auto':
+            self.binning_strategy = 'hybrid' if (n > 20000 or p > 40) else 'standard'
+        else:
+            self.binning_strategy = self.binning_strategy_init
+        if self.max_depth_init == 'auto':
+            if K > 10:
+                self.max_depth = min(8, max(4, int(np.log2(max(n // 8, 8)))))
+            else:
+                self.max_depth = min(6, max(3, int(np.log2(max(n // 10, 8)))))
+        if self.learning_rate_init == 'auto':
+            if n > 20000:
+                # The reference also computes np.std(X) here; the value only
+                # matters for n <= 20000, so it is not computed.
+                self.learning_rate = 0.08
+            else:
+                data_std = np.std(X)
+                if data_std > 2.0:
+                    self.learning_rate = 0.10
+                elif data_std > 1.5:
+                    self.learning_rate = 0.12
+                elif data_std > 1.0:
+                    self.learning_rate = 0.15
+                elif data_std > 0.5:
+                    self.learning_rate = 0.18
+                else:
+                    self.learning_rate = 0.20
+            if K > 10:
+                self.learning_rate *= 0.75
+            elif K > 6:
+                self.learning_rate *= 0.85
+        if self.n_bins_init == 'auto':
+            self.n_bins = min(256, p * 8 + 32)
+        if self.n_estimators_init == 'auto':
+            if K <= 2:
+                self.n_estimators = 150
+            elif K <= 6:
+                self.n_estimators = max(150, min(300, n // 10))
+            elif K <= 15:
+                self.n_estimators = max(200, min(400, n // 8))
+            else:
+                self.n_estimators = max(250, min(500, n // 6))
+        if self.gamma_init == 'auto':
+            self.gamma = 0.0
+        if self.min_child_weight_init == 'auto':
+            if n > 20000:
+                self.min_child_weight = 3.0
+            elif n > 5000:
+                self.min_child_weight = 2.0
+            else:
+                self.min_child_weight = 1.0
+        if self.subsample_init == 'auto':
+            if n > 1000000:
+                self.subsample = 0.5
+            elif n > 20000:
+                self.subsample = 0.75
+            else:
+                self.subsample = 0.8
+        if n > 1000000:
+            self.reg_lambda = max(self.reg_lambda, 5.0)
+        if self.colsample_init == 'auto':
+            self.colsample_bytree = 0.7 if p > 40 else 0.8
+        if n > 10000:
+            self.max_leaves = 63
+        elif n < 2000:
+            self.max_leaves = 15
+        else:
+            self.max_leaves = 31
+        if self.verbose:
+            print("  🔧 Adaptive Hyperparameters:")
+            print(f"     n_estimators:  {self.n_estimators}")
+            print(f"     max_depth:     {self.max_depth} (from {n} samples)")
+            print(f"     learning_rate: {self.learning_rate:.4f}")
+            print(f"     n_bins:        {self.n_bins} (from {p} features)")
+            print(f"     gamma:         {self.gamma:.2f}")
+            print(f"     min_child_w:   {self.min_child_weight:.1f}")
+            print(f"     subsample:     {self.subsample}")
+            print(f"     colsample:     {self.colsample_bytree}")
+
+    # ------------------------------------------------------------------
+    # est:2073-2141 (numeric features)
+    # ------------------------------------------------------------------
+    def _build_bin_edges(self, X, sample_weight=None):
+        edges = []
+        n_features = X.shape[1]
+        bin_counts = np.zeros(n_features, dtype=np.int32)
+        self._nan_bin_id = np.full(n_features, -1, dtype=np.int32)
+        for j in range(n_features):
+            col = X[:, j]
+            nan_mask = np.isnan(col)
+            has_nan = bool(np.any(nan_mask))
+            if has_nan:
+                self._nan_bin_id[j] = 0
+                col_clean = col[~nan_mask]
+                if len(col_clean) == 0:
+                    edges.append(np.array([0.0, 1.0]))
+                    bin_counts[j] = 1
+                    continue
+            else:
+                col_clean = col
+            uniq = np.unique(col_clean)
+            n_unique = len(uniq)
+            max_numeric_bins = self.n_bins - (1 if has_nan else 0)
+            if n_unique <= max_numeric_bins:
+                e = np.sort(uniq)
+            else:
+                q = np.linspace(0, 1, min(max_numeric_bins + 1, n_unique))
+                if sample_weight is not None:
+                    sw_clean = sample_weight[~nan_mask] if has_nan else sample_weight
+                    sorter = np.argsort(col_clean)
+                    c_sorted = col_clean[sorter]
+                    sw_sorted = sw_clean[sorter]
+                    cw = np.cumsum(sw_sorted) - 0.5 * sw_sorted
+                    cw /= np.sum(sw_sorted)
+                    e = np.unique(np.interp(q, cw, c_sorted))
+                else:
+                    e = np.unique(np.percentile(col_clean, q * 100))
+            e = np.append(e, e[-1] + 1e-8)
+            edges.append(e)
+            bin_counts[j] = len(e) - 1 + (1 if has_nan else 0)
+        max_b = int(np.max(bin_counts)) + 1
+        edges_2d = np.zeros((n_features, max_b), dtype=np.float64)
+        for j, e in enumerate(edges):
+            edges_2d[j, :len(e)] = e
+            edges_2d[j, len(e):] = e[-1]
+        return edges_2d, bin_counts
+
+    # ------------------------------------------------------------------
+    # est:2570-2603
+    # ------------------------------------------------------------------
+    def _class_weight_pair(self, y):
+        """(w0, w1): the per-class values of the reference's sample_weight."""
+        if self.scale_pos_weight is not None and self.objective == 'binary':
+            return 1.0, float(self.scale_pos_weight)
+        if self.class_weight not in ('balanced', 'balanced_sqrt'):
+            return 1.0, 1.0
+        n = len(y)
+        w = []
+        for k in range(2):
+            n_k = np.sum(y == k)
+            w_k = n / (2 * max(n_k, 1))
+            if self.class_weight == 'balanced_sqrt':
+                w_k = w_k ** 0.35
+            w.append(float(w_k))
+        if self.verbose:
+            mode = "sqrt-dampened" if self.class_weight == 'balanced_sqrt' else "full"
+            print(f"  ⚖️  Class weights ({mode}): class_0={w[0]:.3f}, class_1={w[1]:.3f}")
+        return w[0], w[1]
+
+    # ------------------------------------------------------------------
+    # est:3070-3271 and est:2825-2944
+    # ------------------------------------------------------------------
+    def fit(self, X, y, group=None, X_val=None, y_val=None, group_val=None,
+            eval_set=None):
+        self._group = group
+        self._group_val = group_val
+        X = _to_dense(X)
+        if X_val is not None:
+            X_val = _to_dense(X_val)
+        if self.max_depth <= 0 and self.max_depth != 'auto':
+            raise ValueError(f"max_depth must be > 0, got {self.max_depth}")
+        if self.learning_rate <= 0:
+            raise ValueError(f"learning_rate must be > 0, got {self.learning_rate}")
+        if self.n_estimators <= 0:
+            raise ValueError(f"n_estimators must be > 0, got {self.n_estimators}")
+        if eval_set is not None and len(eval_set) > 0:
+            X_val, y_val = eval_set[0]
+            X_val = _to_dense(X_val)
+        X = np.asarray(X)
+        y = np.asarray(y)
+        if X.ndim != 2:
+            raise ValueError("X must be a 2-D array")
+        if len(y) != X.shape[0]:
+            raise ValueError(f"X has {X.shape[0]} rows but y has {len(y)} labels")
+        self._check_supported()
+
+        self.classes_ = np.unique(y)
+        self.n_classes_ = len(self.classes_)
+        self._is_multiclass = self.n_classes_ > 2
+        if self.n_classes_ != 2:
+            raise NotImplementedError(
+                "the MI355X engine covers binary classification; got "
+                f"{self.n_classes_} classes")
+        y = (y == self.classes_[1]).astype(np.int64)
+        if y_val is not None:
+            y_val = np.asarray(y_val)
+            label_map = {c: i for i, c in enumerate(self.classes_)}
+            y_val = np.array([label_map[v] for v in y_val], dtype=np.int64)
+        if self.verbose:
+            print("\n" + "=" * 70)
+            print("  Training Hybrid GBM v3.0 — Binary")
+            print("=" * 70)
+
+        self.trees = []
+        self.mc_trees = None
+        self.train_loss_history_ = []
+        self.val_loss_history_ = []
+        self.n_features_in_ = X.shape[1]
+        rng = np.random.RandomState(self.random_state)
+        self._mono_arr = None
+        self._categorical_set = set()
+        self._is_categorical = np.zeros(X.shape[1], dtype=bool)
+        X = _as_float(X)
+        if X_val is not None:
+            X_val = _as_float(X_val)
+
+        self._compute_adaptive_hyperparameters(X, y)
+        sample_weight = None
+        if self.scale_pos_weight is not None and self.objective in ('binary', 'binary_focal'):
+            sample_weight = np.ones(len(y), dtype=np.float64)
+            sample_weight[y == 1] = self.scale_pos_weight
+        t0 = time.perf_counter()
+        self.bin_edges, self.feature_bin_counts = self._build_bin_edges(X, sample_weight=sample_weight)
+        self._max_bins = int(np.max(self.feature_bin_counts))
+        if self._max_bins > 256:
+            raise NotImplementedError(
+                f"n_bins={self.n_bins} gives {self._max_bins} bins for some feature; "
+                "the MI355X engine stores uint8 codes (at most 256 bins), use n_bins <= 255")
+        eng = _engine(self._device_index())
+        eng.bin_features(0, X, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
+        self.times['binning'] = (time.perf_counter() - t0) * 1000
+        n_val = 0
+        if X_val is not None and y_val is not None:
+            eng.bin_features(1, X_val, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
+            n_val = X_val.shape[0]
+
+        t0_train = time.perf_counter()
+        self._fit_binary(eng, y, n_val, y_val, rng)
+        self.times['training'] = (time.perf_counter() - t0_train) * 1000
+
+        self._pack_trees()
+        self._compute_feature_importances()
+        if self.verbose:
+            print(f"\n  ✓ Training complete! ({self.n_trees_fitted_} trees)")
+            print(f"    Binning:  {self.times['binning']:.2f} ms")
+            print(f"    Training: {self.times['training']:.2f} ms")
+            print(f"    Total:    {self.times['binning'] + self.times['training']:.2f} ms")
+        return self
+
+    def _fit_binary(self, eng, y, n_val, y_val, rng):
+        n_samples = len(y)
+        n_features = self.n_features_in_
+        w0, w1 = self._class_weight_pair(y)
+        sw = np.where(y == 1, w1, w0)
+        weighted_mean = np.average(y, weights=sw)
+        p0 = np.clip(weighted_mean, 1e-7, 1.0 - 1e-7)
+        self.base_score_ = np.log(p0 / (1.0 - p0))
+        F_val = np.full(n_val, self.base_score_) if n_val else None
+        n_sub = max(1, int(n_samples * self.subsample))
+        f_sub = max(1, int(n_features * self.colsample_bytree))
+        do_rows = self.subsample < 1.0
+        do_feats = self.colsample_bytree < 1.0
+        eng.boost_begin(y, w0, w1, self.base_score_)
+        sampler = _native.Sampler(rng.get_state(), n_samples,
+                                  n_sub if do_rows else n_samples, do_rows,
+                                  n_features, f_sub if do_feats else n_features,
+                                  do_feats, int(self.n_estimators))
+        best_val_loss = np.inf
+        rounds_no_improve = 0
+        hook = getattr(self, '_round_hook', None)
+        try:
+            for m in range(self.n_estimators):
+                if hook is not None:
+                    hook(m, eng)
+                tree, train_loss = eng.boost_round(
+                    sampler, self.max_leaves, self.max_depth,
+                    self.min_samples_leaf, self.min_child_weight,
+                    self.feature_bin_counts, self._max_bins, self.reg_lambda,
+                    self.gamma, self.learning_rate)
+                self.trees.append(tree)
+                self.train_loss_history_.append(train_loss)
+                val_loss = None
+                if n_val:
+                    F_val += self.learning_rate * eng.predict_tree(1, n_val, tree)
+                    pv = np.clip(_sigmoid(F_val), 1e-15, 1 - 1e-15)
+                    val_loss = -np.mean(y_val * np.log(pv) + (1 - y_val) * np.log(1 - pv))
+                    self.val_loss_history_.append(val_loss)
+                if self.verbose and ((m + 1) % 20 == 0 or m == 0):
+                    msg = f"  ✓ Tree {m+1:>3}/{self.n_estimators}  |  train-loss: {train_loss:.6f}"
+                    if val_loss is not None:
+                        msg += f"  |  val-loss: {val_loss:.6f}"
+                    print(msg)
+                if self.early_stopping_rounds is not None and val_loss is not None:
+                    if val_loss < best_val_loss:
+                        best_val_loss = val_loss
+                        self.best_iteration_ = m
+                        rounds_no_improve = 0
+                    else:
+                        rounds_no_improve += 1
+                        if rounds_no_improve >= self.early_stopping_rounds:
+                            if self.verbose:
+                                print(f"\n  ⏹ Early stopping at tree {m+1} (best: {self.best_iteration_+1})")
+                            self.trees = self.trees[:self.best_iteration_ + 1]
+                            break
+        finally:
+            sampler.close()
+        if hook is not None:
+            hook(self.n_estimators, eng)
+        self.n_trees_fitted_ = len(self.trees)
+
+    # ------------------------------------------------------------------
+    # est:2192-2236, est:2343-2363
+    # ------------------------------------------------------------------
+    def _pack_tree_list(self, tree_list):
+        total_nodes = sum(t[5] for t in tree_list)
+        features = np.empty(total_nodes, dtype=np.int16)
+        thresholds = np.empty(total_nodes, dtype=np.int64)
+        values = np.empty(total_nodes, dtype=np.float64)
+        left = np.empty(total_nodes, dtype=np.int32)
+        right = np.empty(total_nodes, dtype=np.int32)
+        offsets = np.empty(len(tree_list) + 1, dtype=np.int32)
+        offset = 0
+        for t_idx, (tf, tt, tv, tl, tr, nc, _) in enumerate(tree_list):
+            offsets[t_idx] = offset
+            features[offset:offset + nc] = tf[:nc]
+            thresholds[offset:offset + nc] = tt[:nc]
+            values[offset:offset + nc] = tv[:nc]
+            left[offset:offset + nc] = tl[:nc]
+            right[offset:offset + nc] = tr[:nc]
+            offset += nc
+        offsets[len(tree_list)] = offset
+        return {'features': features, 'thresholds': thresholds,
+                'values': values, 'left': left, 'right': right,
+                'offsets': offsets}
+
+    def _pack_trees(self):
+        packed = self._pack_tree_list(self.trees)
+        self._packed_features = packed['features']
+        self._packed_thresholds = packed['thresholds']
+        self._packed_values = packed['values']
+        self._packed_left = packed['left']
+        self._packed_right = packed['right']
+        self._tree_offsets = packed['offsets']
+
+    def _compute_feature_importances(self):
+        gain_imp = np.zeros(self.n_features_in_, dtype=np.float64)
+        split_cnt = np.zeros(self.n_features_in_, dtype=np.int64)
+        for tf, tt, tv, tl, tr, nc, sg in self.trees:
+            for node_idx in range(nc):
+                feat = tf[node_idx]
+                if feat >= 0:
+                    gain_imp[feat] += sg[node_idx]
+                    split_cnt[feat] += 1
+        total = gain_imp.sum()
+        self.feature_importances_ = gain_imp / total if total > 0 else np.zeros(self.n_features_in_)
+        self.feature_split_counts_ = split_cnt
+
+    # ------------------------------------------------------------------
+    # est:3274-3368
+    # ------------------------------------------------------------------
+    def _raw_score(self, X):
+        """F = sum_t lr * value_t + base_score_ (est:3318-3324)."""
+        X = _to_dense(X)
+        if getattr(self, 'n_features_in_', None) is None:
+            raise ValueError("This HybridHistGBMNumbaV1_0_1 instance is not fitted yet.")
+        X = _as_float(X)
+        if X.ndim != 2 or X.shape[1] != self.n_features_in_:
+            raise ValueError(f"X must have {self.n_features_in_} features")
+        eng = _engine(self._device_index())
+        eng.bin_features(1, X, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
+        t0 = time.perf_counter()
+        packed = {'features': self._packed_features, 'thresholds': self._packed_thresholds,
+                  'values': self._packed_values, 'left': self._packed_left,
+                  'right': self._packed_right, 'offsets': self._tree_offsets}
+        F = eng.predict(1, X.shape[0], packed, len(self.trees),
+                        self.learning_rate) + getattr(self, 'base_score_', 0.0)
+        self.times['inference'] = (time.perf_counter() - t0) * 1000
+        return F
+
+    def predict_proba(self, X):
+        F = self._raw_score(X)
+        proba = _sigmoid(F)
+        return np.column_stack([1 - proba, proba])
+
+    def predict(self, X):
+        proba = self.predict_proba(X)
+        return self.classes_[(proba[:, 1] > 0.5).astype(int)]
+
+    # ------------------------------------------------------------------
+    # est:3773-3801
+    # ------------------------------------------------------------------
+    def get_params(self, deep=True):
+        return {
+            'n_estimators': self.n_estimators,
+            'max_depth': self.max_depth_init,
+            'learning_rate': self.learning_rate_init,
+            'n_bins': self.n_bins_init,
+            'reg_lambda': self.reg_lambda,
+            'min_samples_leaf': self.min_samples_leaf,
+            'min_child_weight': self.min_child_weight,
+            'gamma': self.gamma,
+            'subsample': self.subsample,
+            'colsample_bytree': self.colsample_bytree,
+            'class_weight': self.class_weight,
+            'monotone_constraints': self.monotone_constraints,
+            'categorical_features': self.categorical_features,
+            'early_stopping_rounds': self.early_stopping_rounds,
+            'verbose': self.verbose,
+            'random_state': self.random_state,
+        }
+
+    def set_params(self, **params):
+        for key, val in params.items():
+            setattr(self, key, val)
+        return self
+
+    def __repr__(self):
+        return (f"HybridHistGBMNumbaV1_0_1(n_estimators={self.n_estimators}, "
+                f"max_depth='{self.max_depth_init}', subsample={self.subsample}, "
+                f"colsample_bytree={self.colsample_bytree})")
+
+    def warmup(self, n_features=None):
+        """The reference compiles its Numba kernels here (est:3807); the HIP
+        kernels are compiled ahead of time, so this only opens the device."""
+        _engine(self._device_index())
+        return self

@@ -1,0 +1,1310 @@
+// Engine: device memory, the tree builder's host driver and the C ABI.
+//
+// Tree building (replaces est:517-823; "est:" is
+// src/bsscl_gbm/estimator_v1_0_1.py).
+//
+// The reference grows a tree best-first: it repeatedly splits the candidate
+// leaf with the largest gain, builds the smaller child's histogram, derives
+// the larger one by subtraction and scans both for their best splits.  A
+// node's histogram and best split depend only on its rows, never on the
+// order of the splits, so this engine computes them level by level -- one
+// batch of kernels per depth for all nodes of that depth -- and afterwards
+// replays the reference's candidate loop (slot table, tie-breaks, rejected
+// splits, node numbering) on the host with the computed values.
+//
+// Which nodes must be expanded: best-first search pops nodes in
+// non-increasing order of e(v) = min of the gains on the path from the root
+// to v (the node with the largest gain in the frontier always has the
+// largest e there).  A node v cannot be split if at least max_leaves-1 kept
+// splits u have e(u) > e(v), because all of those come first.  The level
+// loop expands every frontier node not excluded by that count; the replay
+// checks that every node it splits was expanded.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "bsscl_internal.h"
+#include "kernels.h"
+
+namespace bsscl {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int set_error(int code, const std::string &msg) {
+  g_last_error = msg;
+  return code;
+}
+
+namespace {
+
+#define HIPCHK(expr)                                                          \
+  do {                                                                        \
+    hipError_t e_ = (expr);                                                   \
+    if (e_ != hipSuccess)                                                     \
+      return set_error(BSSCL_EDEVICE,                                         \
+                       std::string(#expr) + ": " + hipGetErrorString(e_));    \
+  } while (0)
+
+#define CHK(expr)                 \
+  do {                            \
+    int rc_ = (expr);             \
+    if (rc_ != BSSCL_OK) return rc_; \
+  } while (0)
+
+template <typename T>
+struct DevBuf {
+  T *p = nullptr;
+  size_t cap = 0;
+  int ensure(size_t count) {
+    if (count <= cap && p) return BSSCL_OK;
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+    const size_t c = std::max<size_t>(count, 1);
+    hipError_t e = hipMalloc(reinterpret_cast<void **>(&p), c * sizeof(T));
+    if (e != hipSuccess)
+      return set_error(BSSCL_ENOMEM, std::string("hipMalloc of ") +
+                                         std::to_string(c * sizeof(T)) +
+                                         " bytes: " + hipGetErrorString(e));
+    cap = c;
+    return BSSCL_OK;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+  }
+};
+
+// Pinned host staging for the small per-level uploads and readbacks.  Reset
+// only after a stream synchronisation, when no copy still reads from it.
+struct PinnedArena {
+  char *base = nullptr;
+  size_t cap = 0, off = 0;
+  int reserve(size_t bytes) {
+    if (bytes <= cap) return BSSCL_OK;
+    if (base) (void)hipHostFree(base);
+    base = nullptr;
+    cap = 0;
+    hipError_t e = hipHostMalloc(reinterpret_cast<void **>(&base), bytes, hipHostMallocDefault);
+    if (e != hipSuccess)
+      return set_error(BSSCL_ENOMEM, std::string("hipHostMalloc: ") + hipGetErrorString(e));
+    cap = bytes;
+    off = 0;
+    return BSSCL_OK;
+  }
+  template <typename T>
+  T *take(size_t count) {
+    size_t o = (off + 255) & ~size_t(255);
+    size_t bytes = count * sizeof(T);
+    if (o + bytes > cap) return nullptr;
+    off = o + bytes;
+    return reinterpret_cast<T *>(base + o);
+  }
+  void reset() { off = 0; }
+  void release() {
+    if (base) (void)hipHostFree(base);
+    base = nullptr;
+    cap = off = 0;
+  }
+};
+
+struct Matrix {
+  DevBuf<uint8_t> codes;
+  int64_t n = 0, ld = 0;
+  int32_t F = 0;
+};
+
+struct HNode {
+  int32_t parent = -1, depth = 0, left = -1, right = -1;
+  int64_t start = 0, count = 0;
+  bool valid = true;
+  long long Gq = 0, Hq = 0;
+  int32_t fpos = -1, bin = 0;
+  double gain = -1.0;
+  bool expanded = false, split_ok = false;
+  int64_t nl = 0, nr = 0;
+  double e = 0.0;
+};
+
+struct TreeParams {
+  int32_t max_leaves, max_depth, min_samples_leaf;
+  double mcw, lam, gamma;
+};
+
+struct TreeOut {
+  int32_t *features;
+  int64_t *thresholds;
+  double *values;
+  int32_t *left, *right;
+  int32_t *node_count;
+  double *gains;
+};
+
+inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+}  // namespace
+}  // namespace bsscl
+
+using namespace bsscl;
+
+struct bsscl_engine {
+  int32_t device = 0;
+  hipStream_t st = nullptr;
+  int32_t n_cu = 256;
+  size_t max_lds = 64 * 1024;
+  Matrix mat[2];
+
+  // Boosting run on matrix 0.
+  bool boosting = false;
+  DevBuf<double> F;
+  DevBuf<uint8_t> y;
+  double w0 = 1.0, w1 = 1.0;
+  DevBuf<int2> ghq;
+  DevBuf<double> g64, h64;
+  double g_scale = 1.0, h_scale = 1.0;  // fixed point -> value
+
+  // Tree workspace.
+  DevBuf<uint8_t> codes_c[2];
+  DevBuf<int2> gh_c[2];
+  DevBuf<int32_t> rid_c[2];
+  int64_t ld_c = 0;
+  DevBuf<int32_t> rows32;
+  DevBuf<int64_t> rows64;
+  DevBuf<int32_t> feat_d, nb_sel_d;
+  DevBuf<unsigned long long> pool;
+  int32_t node_cap = 0;
+  int64_t node_stride = 0;  // int64 words per node histogram
+  DevBuf<NodeSeg> segs;
+  DevBuf<SplitCand> cand;
+  DevBuf<long long> totals;
+  DevBuf<PartParent> parents_d;
+  DevBuf<PartTile> tiles_d;
+  DevBuf<int32_t> tile_begin_d, tile_left_d, hist_node_d;
+  DevBuf<int64_t> tile_off_d, nleft_d;
+  DevBuf<HistTask> htasks_d;
+  DevBuf<SplitTask> stasks_d;
+  DevBuf<TreeNodeDev> tree_d;
+  DevBuf<int32_t> offsets_d;
+  DevBuf<double> partials_d, loss_d, out_d;
+  PinnedArena pin;
+
+  // Profiling.
+  bool prof = false;
+  std::vector<hipEvent_t> ev_pool;
+  size_t ev_used = 0;
+  struct Pending {
+    hipEvent_t a, b;
+    int kind;  // 0 hist, 1 partition, 2 split
+  };
+  std::vector<Pending> pending;
+  double stats[10] = {0};
+};
+
+namespace bsscl {
+namespace {
+
+int ev_pair(bsscl_engine *E, hipEvent_t &a, hipEvent_t &b) {
+  while (E->ev_pool.size() < E->ev_used + 2) {
+    hipEvent_t ev;
+    HIPCHK(hipEventCreate(&ev));
+    E->ev_pool.push_back(ev);
+  }
+  a = E->ev_pool[E->ev_used++];
+  b = E->ev_pool[E->ev_used++];
+  return BSSCL_OK;
+}
+
+// Starts a timed region of `kind` when profiling; returns the stop event.
+int prof_begin(bsscl_engine *E, int kind, hipEvent_t *stop) {
+  *stop = nullptr;
+  if (!E->prof) return BSSCL_OK;
+  hipEvent_t a, b;
+  CHK(ev_pair(E, a, b));
+  HIPCHK(hipEventRecord(a, E->st));
+  E->pending.push_back({a, b, kind});
+  *stop = b;
+  return BSSCL_OK;
+}
+
+int prof_end(bsscl_engine *E, hipEvent_t stop) {
+  if (stop) HIPCHK(hipEventRecord(stop, E->st));
+  return BSSCL_OK;
+}
+
+// After a stream synchronisation: fold the finished timings into stats.
+int prof_collect(bsscl_engine *E) {
+  for (const auto &p : E->pending) {
+    float ms = 0.f;
+    HIPCHK(hipEventElapsedTime(&ms, p.a, p.b));
+    E->stats[p.kind == 0 ? 0 : (p.kind == 1 ? 4 : 6)] += 1.0;
+    E->stats[p.kind == 0 ? 1 : (p.kind == 1 ? 5 : 7)] += (double)ms;
+  }
+  E->pending.clear();
+  E->ev_used = 0;
+  return BSSCL_OK;
+}
+
+int sync(bsscl_engine *E) {
+  HIPCHK(hipStreamSynchronize(E->st));
+  CHK(prof_collect(E));
+  E->pin.reset();
+  return BSSCL_OK;
+}
+
+template <typename T>
+int upload(bsscl_engine *E, DevBuf<T> &dst, const T *src, size_t count) {
+  CHK(dst.ensure(count));
+  if (count == 0) return BSSCL_OK;
+  T *stage = E->pin.take<T>(count);
+  if (stage) {
+    std::memcpy(stage, src, count * sizeof(T));
+    HIPCHK(hipMemcpyAsync(dst.p, stage, count * sizeof(T), hipMemcpyHostToDevice, E->st));
+  } else {
+    HIPCHK(hipMemcpyAsync(dst.p, src, count * sizeof(T), hipMemcpyHostToDevice, E->st));
+    HIPCHK(hipStreamSynchronize(E->st));
+  }
+  return BSSCL_OK;
+}
+
+int check_matrix(bsscl_engine *E, int32_t slot) {
+  if (slot < 0 || slot > 1) return set_error(BSSCL_EINVAL, "matrix slot must be 0 or 1");
+  if (!E->mat[slot].codes.p || E->mat[slot].n <= 0)
+    return set_error(BSSCL_EINVAL, "matrix slot " + std::to_string(slot) + " is empty");
+  return BSSCL_OK;
+}
+
+int alloc_matrix(bsscl_engine *E, int32_t slot, int64_t n, int32_t F) {
+  Matrix &M = E->mat[slot];
+  const int64_t ld = round_up(n + 8, 256);
+  CHK(M.codes.ensure((size_t)ld * (size_t)F));
+  HIPCHK(hipMemsetAsync(M.codes.p, 0, (size_t)ld * (size_t)F, E->st));
+  M.n = n;
+  M.ld = ld;
+  M.F = F;
+  return BSSCL_OK;
+}
+
+// Exponent s with max_abs * 2^s <= 2^30, so per-row fixed-point values fit
+// in int32 and a sum of up to 2^33 rows fits in int64.
+double fixed_mul(double max_abs) {
+  if (!(max_abs > 0.0) || !std::isfinite(max_abs)) return std::ldexp(1.0, 30);
+  int e;
+  std::frexp(max_abs, &e);  // max_abs < 2^e
+  return std::ldexp(1.0, 30 - e);
+}
+
+int ensure_nodes(bsscl_engine *E, int32_t need, int32_t F_sel) {
+  const int64_t stride = (int64_t)F_sel * kHistPerFeat;
+  if (need <= E->node_cap && stride == E->node_stride) return BSSCL_OK;
+  int32_t cap = std::max<int32_t>(need, std::max<int32_t>(256, E->node_cap));
+  if (stride == E->node_stride && E->node_cap > 0 && need > E->node_cap) {
+    cap = std::max(need, E->node_cap * 2);
+    // Grow while keeping the histograms, segments and results built so far.
+    DevBuf<unsigned long long> pool2;
+    DevBuf<NodeSeg> segs2;
+    DevBuf<SplitCand> cand2;
+    DevBuf<long long> tot2;
+    CHK(pool2.ensure((size_t)cap * stride));
+    CHK(segs2.ensure((size_t)cap));
+    CHK(cand2.ensure((size_t)cap * F_sel));
+    CHK(tot2.ensure((size_t)cap * 2));
+    HIPCHK(hipMemcpyAsync(pool2.p, E->pool.p, (size_t)E->node_cap * stride * 8, hipMemcpyDeviceToDevice, E->st));
+    HIPCHK(hipMemcpyAsync(segs2.p, E->segs.p, (size_t)E->node_cap * sizeof(NodeSeg), hipMemcpyDeviceToDevice, E->st));
+    HIPCHK(hipMemcpyAsync(cand2.p, E->cand.p, (size_t)E->node_cap * F_sel * sizeof(SplitCand), hipMemcpyDeviceToDevice, E->st));
+    HIPCHK(hipMemcpyAsync(tot2.p, E->totals.p, (size_t)E->node_cap * 2 * sizeof(long long), hipMemcpyDeviceToDevice, E->st));
+    HIPCHK(hipStreamSynchronize(E->st));
+    E->pool.release();
+    E->segs.release();
+    E->cand.release();
+    E->totals.release();
+    E->pool = pool2;
+    E->segs = segs2;
+    E->cand = cand2;
+    E->totals = tot2;
+    E->node_cap = cap;
+    return BSSCL_OK;
+  }
+  CHK(E->pool.ensure((size_t)cap * stride));
+  CHK(E->segs.ensure((size_t)cap));
+  CHK(E->cand.ensure((size_t)cap * F_sel));
+  CHK(E->totals.ensure((size_t)cap * 2));
+  E->node_cap = cap;
+  E->node_stride = stride;
+  return BSSCL_OK;
+}
+
+// Rows per histogram block: enough blocks to cover the CUs about twice.
+int32_t hist_tile_rows(bsscl_engine *E, int64_t rows) {
+  int64_t t = rows / (2 * (int64_t)E->n_cu);
+  t = round_up(std::max<int64_t>(t, 1), 1024);
+  return (int32_t)std::min<int64_t>(std::max<int64_t>(t, 1024), 1 << 20);
+}
+
+int32_t hist_fchunk(bsscl_engine *E, int32_t F_sel) {
+  // Leave 4 KB for the kernel's static LDS.
+  int32_t by_lds = (int32_t)((E->max_lds - 4096) / (kHistPerFeat * 8));
+  by_lds = std::max<int32_t>(1, std::min<int32_t>(by_lds, 40));
+  // Even chunks: ceil(F_sel / chunks) features each.
+  const int32_t chunks = (F_sel + by_lds - 1) / by_lds;
+  return (F_sel + chunks - 1) / chunks;
+}
+
+int launch_hist_tasks(bsscl_engine *E, int set, const std::vector<HistTask> &tasks,
+                      int32_t F_sel, int32_t tile_rows) {
+  if (tasks.empty()) return BSSCL_OK;
+  CHK(upload(E, E->htasks_d, tasks.data(), tasks.size()));
+  const int32_t fchunk = hist_fchunk(E, F_sel);
+  hipEvent_t stop;
+  CHK(prof_begin(E, 0, &stop));
+  HIPCHK(launch_hist(E->st, E->codes_c[set].p, E->ld_c, E->gh_c[set].p,
+                     E->htasks_d.p, (int32_t)tasks.size(), E->hist_node_d.p,
+                     E->segs.p, E->nb_sel_d.p, F_sel, fchunk, tile_rows,
+                     E->pool.p, E->node_stride,
+                     (size_t)fchunk * kHistPerFeat * 8));
+  CHK(prof_end(E, stop));
+  return BSSCL_OK;
+}
+
+int launch_split_tasks(bsscl_engine *E, const std::vector<SplitTask> &tasks,
+                       int32_t F_sel, const TreeParams &tp) {
+  if (tasks.empty()) return BSSCL_OK;
+  CHK(upload(E, E->stasks_d, tasks.data(), tasks.size()));
+  SplitParams sp;
+  sp.min_child_weight = tp.mcw;
+  sp.reg_lambda = tp.lam;
+  sp.g_scale = E->g_scale;
+  sp.h_scale = E->h_scale;
+  sp.min_samples_leaf = tp.min_samples_leaf;
+  sp.max_depth = tp.max_depth;
+  hipEvent_t stop;
+  CHK(prof_begin(E, 2, &stop));
+  HIPCHK(launch_split(E->st, E->stasks_d.p, (int32_t)tasks.size(), E->segs.p,
+                      E->pool.p, E->node_stride, E->nb_sel_d.p, F_sel, sp,
+                      E->cand.p, E->totals.p));
+  CHK(prof_end(E, stop));
+  return BSSCL_OK;
+}
+
+// Reads back segments, totals and candidates of nodes [a, b) and reduces the
+// candidates over features: the largest gain, the lowest feature position on
+// ties (est:618-621).
+int read_nodes(bsscl_engine *E, int32_t a, int32_t b, int32_t F_sel,
+               std::vector<HNode> &nodes) {
+  const int32_t cnt = b - a;
+  if (cnt <= 0) return BSSCL_OK;
+  // Uploads of this level may still read the staging arena: finish them
+  // before it can be reallocated.
+  HIPCHK(hipStreamSynchronize(E->st));
+  CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, (size_t)cnt * (sizeof(NodeSeg) + 16 + (size_t)F_sel * sizeof(SplitCand)) + 4096)));
+  NodeSeg *sg = E->pin.take<NodeSeg>(cnt);
+  long long *tt = E->pin.take<long long>(2 * (size_t)cnt);
+  SplitCand *cc = E->pin.take<SplitCand>((size_t)cnt * F_sel);
+  if (!sg || !tt || !cc) return set_error(BSSCL_EINTERNAL, "pinned staging too small");
+  HIPCHK(hipMemcpyAsync(sg, E->segs.p + a, cnt * sizeof(NodeSeg), hipMemcpyDeviceToHost, E->st));
+  HIPCHK(hipMemcpyAsync(tt, E->totals.p + 2 * (size_t)a, 2 * cnt * sizeof(long long), hipMemcpyDeviceToHost, E->st));
+  HIPCHK(hipMemcpyAsync(cc, E->cand.p + (size_t)a * F_sel, (size_t)cnt * F_sel * sizeof(SplitCand), hipMemcpyDeviceToHost, E->st));
+  HIPCHK(hipStreamSynchronize(E->st));
+  for (int32_t i = 0; i < cnt; ++i) {
+    HNode &nd = nodes[(size_t)(a + i)];
+    nd.start = sg[i].start;
+    nd.count = sg[i].count;
+    nd.valid = sg[i].valid != 0;
+    if (!nd.valid) continue;
+    nd.Gq = tt[2 * i];
+    nd.Hq = tt[2 * i + 1];
+    nd.fpos = -1;
+    nd.bin = 0;
+    nd.gain = -1e9;
+    for (int32_t f = 0; f < F_sel; ++f) {
+      const SplitCand &c = cc[(size_t)i * F_sel + f];
+      if (c.bin >= 0 && (nd.fpos < 0 || c.gain > nd.gain)) {
+        nd.fpos = f;
+        nd.bin = c.bin;
+        nd.gain = c.gain;
+      }
+    }
+  }
+  CHK(prof_collect(E));
+  E->pin.reset();
+  return BSSCL_OK;
+}
+
+// Replays est:641-820 on the computed nodes.
+int replay(bsscl_engine *E, const std::vector<HNode> &nodes,
+           const std::vector<int32_t> &feats, const TreeParams &tp,
+           TreeOut &out) {
+  const int32_t M = 2 * tp.max_leaves + 2;
+  const int32_t MAX_C = tp.max_leaves + 2;
+  for (int32_t i = 0; i < M; ++i) {
+    out.features[i] = -1;
+    out.thresholds[i] = 0;
+    out.values[i] = 0.0;
+    out.left[i] = -1;
+    out.right[i] = -1;
+    out.gains[i] = 0.0;
+  }
+  auto value = [&](const HNode &nd) {
+    const double G = (double)nd.Gq * E->g_scale;
+    const double H = (double)nd.Hq * E->h_scale;
+    return -G / (H + tp.lam);
+  };
+  int32_t node_count = 0;
+  const HNode &root = nodes[0];
+  const int32_t root_id = node_count++;
+  if (root.fpos < 0) {  // est:575-579 and est:632-637
+    out.features[root_id] = -1;
+    out.values[root_id] = value(root);
+    *out.node_count = node_count;
+    return BSSCL_OK;
+  }
+  std::vector<int32_t> c_node(MAX_C, 0), c_int(MAX_C, -1), c_feat(MAX_C, -1);
+  std::vector<double> c_gain(MAX_C, -1.0), c_val(MAX_C, 0.0);
+  std::vector<char> c_active(MAX_C, 0);
+  c_node[0] = root_id;
+  c_int[0] = 0;
+  c_gain[0] = root.gain;
+  c_feat[0] = root.fpos;
+  c_val[0] = value(root);
+  c_active[0] = 1;
+  int32_t n_splits = 0;
+  while (n_splits < tp.max_leaves - 1) {
+    int32_t best_ci = -1;
+    double best_gain = tp.gamma;
+    for (int32_t ci = 0; ci < MAX_C; ++ci)
+      if (c_active[ci] && c_feat[ci] >= 0 && c_gain[ci] > best_gain) {
+        best_gain = c_gain[ci];
+        best_ci = ci;
+      }
+    if (best_ci < 0) break;
+    const int32_t ci = best_ci;
+    const HNode &nd = nodes[(size_t)c_int[ci]];
+    const int32_t cur = c_node[ci];
+    if (!nd.expanded)
+      return set_error(BSSCL_EINTERNAL, "tree builder: node popped without expansion");
+    if (!nd.split_ok) {  // est:678-683
+      out.features[cur] = -1;
+      out.values[cur] = c_val[ci];
+      c_active[ci] = 0;
+      continue;
+    }
+    const int32_t left_id = node_count++;
+    const int32_t right_id = node_count++;
+    out.features[cur] = feats[(size_t)nd.fpos];
+    out.thresholds[cur] = nd.bin;
+    out.left[cur] = left_id;
+    out.right[cur] = right_id;
+    out.values[cur] = c_val[ci];
+    out.gains[cur] = c_gain[ci];
+    ++n_splits;
+    const bool left_small = nd.nl <= nd.nr;
+    const int32_t small_int = left_small ? nd.left : nd.right;
+    const int32_t large_int = left_small ? nd.right : nd.left;
+    const int32_t small_id = left_small ? left_id : right_id;
+    const int32_t large_id = left_small ? right_id : left_id;
+    int32_t slot_small = -1, slot_large = -1;
+    for (int32_t si = 0; si < MAX_C; ++si)
+      if (si != ci && !c_active[si]) {
+        if (slot_small < 0) slot_small = si;
+        else if (slot_large < 0) {
+          slot_large = si;
+          break;
+        }
+      }
+    if (slot_small < 0 || slot_large < 0)
+      return set_error(BSSCL_EINTERNAL, "tree builder: no free candidate slot");
+    c_active[ci] = 0;
+    for (int pass = 0; pass < 2; ++pass) {
+      const int32_t slot = pass == 0 ? slot_small : slot_large;
+      const int32_t ch = pass == 0 ? small_int : large_int;
+      const HNode &cn = nodes[(size_t)ch];
+      c_node[slot] = pass == 0 ? small_id : large_id;
+      c_int[slot] = ch;
+      c_feat[slot] = cn.fpos;
+      c_gain[slot] = cn.fpos >= 0 ? cn.gain : -1.0;
+      c_val[slot] = value(cn);
+      c_active[slot] = 1;
+    }
+  }
+  for (int32_t ci = 0; ci < MAX_C; ++ci)
+    if (c_active[ci]) {
+      out.features[c_node[ci]] = -1;
+      out.values[c_node[ci]] = c_val[ci];
+    }
+  *out.node_count = node_count;
+  return BSSCL_OK;
+}
+
+// Builds one tree from the rows already in E->rows32 (rows32 != 0) or
+// E->rows64, with quantized gradients in E->ghq.
+int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
+                    const std::vector<int32_t> &feats,
+                    const std::vector<int32_t> &nb_sel, const TreeParams &tp,
+                    TreeOut &out) {
+  const Matrix &X = E->mat[0];
+  const int32_t F_sel = (int32_t)feats.size();
+  CHK(sync(E));
+  E->ld_c = round_up(m + 8, 256);
+  for (int s = 0; s < 2; ++s) {
+    CHK(E->codes_c[s].ensure((size_t)E->ld_c * F_sel));
+    CHK(E->gh_c[s].ensure((size_t)E->ld_c));
+    CHK(E->rid_c[s].ensure((size_t)E->ld_c));
+  }
+  CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 8u << 20)));
+  CHK(ensure_nodes(E, 256, F_sel));
+  CHK(upload(E, E->feat_d, feats.data(), feats.size()));
+  CHK(upload(E, E->nb_sel_d, nb_sel.data(), nb_sel.size()));
+
+  // Root: gather the in-bag rows into set 0.
+  HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, E->feat_d.p, F_sel,
+                            use32 ? E->rows32.p : nullptr,
+                            use32 ? nullptr : E->rows64.p, m, E->ghq.p,
+                            E->codes_c[0].p, E->ld_c, E->gh_c[0].p,
+                            E->rid_c[0].p, E->ld_c));
+  std::vector<HNode> nodes(1);
+  {
+    NodeSeg rs;
+    rs.start = 0;
+    rs.count = m;
+    rs.valid = 1;
+    rs.is_small = 1;
+    CHK(upload(E, E->segs, &rs, 1));
+    int32_t zero = 0;
+    CHK(E->hist_node_d.ensure(256));
+    HIPCHK(hipMemcpyAsync(E->hist_node_d.p, &zero, sizeof(int32_t), hipMemcpyHostToDevice, E->st));
+    HIPCHK(hipMemsetAsync(E->pool.p, 0, (size_t)E->node_stride * 8, E->st));
+    const int32_t th = hist_tile_rows(E, m);
+    std::vector<HistTask> ht;
+    for (int64_t t = 0; t * th < m; ++t) ht.push_back({0, (int32_t)t});
+    CHK(launch_hist_tasks(E, 0, ht, F_sel, th));
+    if (E->prof) {
+      E->stats[2] += (double)m * F_sel;
+      E->stats[3] += (double)m * (F_sel + 8);
+    }
+    std::vector<SplitTask> stv{{0, -1, -1, 0}};
+    CHK(launch_split_tasks(E, stv, F_sel, tp));
+    CHK(read_nodes(E, 0, 1, F_sel, nodes));
+    nodes[0].e = nodes[0].gain;
+  }
+
+  std::vector<int32_t> frontier;
+  if (nodes[0].fpos >= 0 && nodes[0].gain > tp.gamma) frontier.push_back(0);
+  int level = 0;
+  std::vector<PartParent> parents;
+  std::vector<PartTile> tiles;
+  std::vector<int32_t> tile_begin;
+  std::vector<HistTask> ht;
+  std::vector<SplitTask> stv;
+  std::vector<int32_t> exp;
+  while (!frontier.empty()) {
+    // Nodes that may still be split (see the file comment).
+    exp.clear();
+    for (int32_t v : frontier) {
+      int32_t kept_before = 0;
+      for (const HNode &u : nodes)
+        if (u.expanded && u.split_ok && u.e > nodes[(size_t)v].e) ++kept_before;
+      if (kept_before < tp.max_leaves - 1) exp.push_back(v);
+    }
+    if (exp.empty()) break;
+    const int32_t first_child = (int32_t)nodes.size();
+    const int32_t end_child = first_child + 2 * (int32_t)exp.size();
+    CHK(ensure_nodes(E, end_child, F_sel));
+    nodes.resize((size_t)end_child);
+    parents.clear();
+    tiles.clear();
+    tile_begin.clear();
+    for (size_t i = 0; i < exp.size(); ++i) {
+      HNode &v = nodes[(size_t)exp[i]];
+      v.left = first_child + 2 * (int32_t)i;
+      v.right = v.left + 1;
+      parents.push_back({v.start, v.count, v.fpos, v.bin, v.left, v.right});
+      tile_begin.push_back((int32_t)tiles.size());
+      for (int64_t r = 0; r < v.count; r += kPartTile)
+        tiles.push_back({v.start + r, (int32_t)std::min<int64_t>(kPartTile, v.count - r), (int32_t)i});
+    }
+    tile_begin.push_back((int32_t)tiles.size());
+    const int src = level & 1, dst = src ^ 1;
+    CHK(upload(E, E->parents_d, parents.data(), parents.size()));
+    CHK(upload(E, E->tiles_d, tiles.data(), tiles.size()));
+    CHK(upload(E, E->tile_begin_d, tile_begin.data(), tile_begin.size()));
+    CHK(E->tile_left_d.ensure(tiles.size()));
+    CHK(E->tile_off_d.ensure(tiles.size()));
+    CHK(E->nleft_d.ensure(parents.size()));
+    CHK(E->hist_node_d.ensure(parents.size()));
+    hipEvent_t stop;
+    CHK(prof_begin(E, 1, &stop));
+    HIPCHK(launch_part_count(E->st, E->codes_c[src].p, E->ld_c, E->parents_d.p,
+                             E->tiles_d.p, (int32_t)tiles.size(), E->tile_left_d.p));
+    HIPCHK(launch_part_scan(E->st, E->parents_d.p, (int32_t)parents.size(),
+                            E->tile_begin_d.p, E->tile_left_d.p, E->tile_off_d.p,
+                            E->nleft_d.p, E->segs.p, E->hist_node_d.p,
+                            tp.min_samples_leaf));
+    HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p,
+                               E->ld_c, E->gh_c[src].p, E->gh_c[dst].p,
+                               E->rid_c[src].p, E->rid_c[dst].p,
+                               E->parents_d.p, E->tiles_d.p,
+                               (int32_t)tiles.size(), E->tile_off_d.p,
+                               E->nleft_d.p, F_sel));
+    CHK(prof_end(E, stop));
+    HIPCHK(hipMemsetAsync(E->pool.p + (size_t)first_child * E->node_stride, 0,
+                          (size_t)(end_child - first_child) * E->node_stride * 8, E->st));
+    // Histograms of the smaller children (at most half of each parent).
+    int64_t ub_rows = 0;
+    for (const auto &P : parents) ub_rows += P.count / 2;
+    const int32_t th = hist_tile_rows(E, ub_rows);
+    ht.clear();
+    for (size_t i = 0; i < parents.size(); ++i)
+      for (int64_t t = 0; t * th < parents[i].count / 2 + 1; ++t)
+        ht.push_back({(int32_t)i, (int32_t)t});
+    CHK(launch_hist_tasks(E, dst, ht, F_sel, th));
+    stv.clear();
+    for (size_t i = 0; i < exp.size(); ++i) {
+      const HNode &v = nodes[(size_t)exp[i]];
+      stv.push_back({v.left, exp[i], v.right, v.depth + 1});
+      stv.push_back({v.right, exp[i], v.left, v.depth + 1});
+    }
+    CHK(launch_split_tasks(E, stv, F_sel, tp));
+    CHK(read_nodes(E, first_child, end_child, F_sel, nodes));
+    frontier.clear();
+    for (size_t i = 0; i < exp.size(); ++i) {
+      HNode &v = nodes[(size_t)exp[i]];
+      HNode &L = nodes[(size_t)v.left];
+      HNode &R = nodes[(size_t)v.right];
+      v.expanded = true;
+      v.nl = L.count;
+      v.nr = R.count;
+      v.split_ok = L.valid;
+      if (E->prof && v.split_ok) {
+        const int64_t ms = std::min(v.nl, v.nr);
+        E->stats[2] += (double)ms * F_sel;
+        E->stats[3] += (double)ms * (F_sel + 8);
+      }
+      for (HNode *c : {&L, &R}) {
+        c->parent = exp[i];
+        c->depth = v.depth + 1;
+        if (!v.split_ok) continue;
+        c->e = std::min(c->gain, v.e);
+        if (c->fpos >= 0 && c->gain > tp.gamma)
+          frontier.push_back((int32_t)(c == &L ? v.left : v.right));
+      }
+    }
+    if (E->prof) E->stats[9] += (double)exp.size();
+    ++level;
+  }
+  if (E->prof) E->stats[8] += 1.0;
+  return replay(E, nodes, feats, tp, out);
+}
+
+int validate_tree_args(bsscl_engine *E, const int32_t *feature_indices,
+                       int32_t n_selected, int32_t max_leaves,
+                       int32_t min_samples_leaf, const int32_t *bin_counts,
+                       const TreeOut &out, std::vector<int32_t> &feats,
+                       std::vector<int32_t> &nb_sel) {
+  const Matrix &X = E->mat[0];
+  if (!feature_indices || n_selected <= 0 || !bin_counts)
+    return set_error(BSSCL_EINVAL, "feature_indices/bin_counts missing");
+  if (max_leaves < 1) return set_error(BSSCL_EINVAL, "max_leaves must be >= 1");
+  if (!out.features || !out.thresholds || !out.values || !out.left ||
+      !out.right || !out.node_count || !out.gains)
+    return set_error(BSSCL_EINVAL, "output arrays missing");
+  (void)min_samples_leaf;
+  feats.assign(feature_indices, feature_indices + n_selected);
+  nb_sel.resize((size_t)n_selected);
+  for (int32_t i = 0; i < n_selected; ++i) {
+    const int32_t f = feats[(size_t)i];
+    if (f < 0 || f >= X.F) return set_error(BSSCL_EINVAL, "feature index out of range");
+    if (i > 0 && f <= feats[(size_t)i - 1])
+      return set_error(BSSCL_EINVAL, "feature_indices must be strictly ascending");
+    const int32_t nb = bin_counts[f];
+    if (nb < 1 || nb > kBins)
+      return set_error(BSSCL_EINVAL, "bin_counts must be in [1, 256]");
+    nb_sel[(size_t)i] = nb;
+  }
+  return BSSCL_OK;
+}
+
+// Uploads host gradients/hessians and quantizes them with scales from their
+// largest magnitudes.
+int load_grad_hess(bsscl_engine *E, const double *grad, const double *hess,
+                   int64_t n) {
+  double gmax = 0.0, hmax = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    const double a = std::fabs(grad[i]), b = std::fabs(hess[i]);
+    if (!std::isfinite(a) || !std::isfinite(b))
+      return set_error(BSSCL_EINVAL, "grad/hess must be finite");
+    gmax = std::max(gmax, a);
+    hmax = std::max(hmax, b);
+  }
+  const double gm = fixed_mul(gmax), hm = fixed_mul(hmax);
+  E->g_scale = 1.0 / gm;
+  E->h_scale = 1.0 / hm;
+  CHK(E->g64.ensure((size_t)n));
+  CHK(E->h64.ensure((size_t)n));
+  CHK(E->ghq.ensure((size_t)n));
+  HIPCHK(hipMemcpyAsync(E->g64.p, grad, (size_t)n * 8, hipMemcpyHostToDevice, E->st));
+  HIPCHK(hipMemcpyAsync(E->h64.p, hess, (size_t)n * 8, hipMemcpyHostToDevice, E->st));
+  HIPCHK(launch_quantize(E->st, E->g64.p, E->h64.p, n, gm, hm, E->ghq.p));
+  return BSSCL_OK;
+}
+
+int upload_tree(bsscl_engine *E, const int32_t *features,
+                const int64_t *thresholds, const double *values,
+                const int32_t *left, const int32_t *right, int32_t node_count,
+                int32_t F) {
+  if (node_count <= 0) return set_error(BSSCL_EINVAL, "empty tree");
+  std::vector<TreeNodeDev> t((size_t)node_count);
+  for (int32_t i = 0; i < node_count; ++i) {
+    TreeNodeDev &d = t[(size_t)i];
+    d.feature = features[i];
+    d.value = values[i];
+    if (d.feature >= 0) {
+      if (d.feature >= F || left[i] <= i || right[i] <= i || left[i] >= node_count ||
+          right[i] >= node_count)
+        return set_error(BSSCL_EINVAL, "malformed tree node " + std::to_string(i));
+      d.threshold = (int32_t)std::max<int64_t>(-1, std::min<int64_t>(thresholds[i], 1 << 20));
+      d.left = left[i];
+      d.right = right[i];
+    } else {
+      d.feature = -1;
+      d.threshold = 0;
+      d.left = d.right = 0;
+    }
+  }
+  CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 8u << 20)));
+  CHK(upload(E, E->tree_d, t.data(), t.size()));
+  return BSSCL_OK;
+}
+
+}  // namespace
+}  // namespace bsscl
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+const char *bsscl_last_error(void) { return g_last_error.c_str(); }
+
+int bsscl_device_count(int32_t *out) {
+  if (!out) return set_error(BSSCL_EINVAL, "null output");
+  int c = 0;
+  hipError_t e = hipGetDeviceCount(&c);
+  *out = (e == hipSuccess) ? c : 0;
+  return BSSCL_OK;
+}
+
+int bsscl_engine_create(int32_t device, bsscl_engine **out) {
+  if (!out) return set_error(BSSCL_EINVAL, "null output");
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+    return set_error(BSSCL_EDEVICE, "no HIP device is visible");
+  if (device < 0 || device >= count)
+    return set_error(BSSCL_EINVAL, "device index out of range");
+  HIPCHK(hipSetDevice(device));
+  bsscl_engine *E = new (std::nothrow) bsscl_engine();
+  if (!E) return set_error(BSSCL_ENOMEM, "engine allocation failed");
+  E->device = device;
+  hipError_t e = hipStreamCreateWithFlags(&E->st, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete E;
+    return set_error(BSSCL_EDEVICE, std::string("hipStreamCreate: ") + hipGetErrorString(e));
+  }
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && v > 0)
+    E->n_cu = v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
+    E->max_lds = (size_t)v;
+  *out = E;
+  return BSSCL_OK;
+}
+
+void bsscl_engine_destroy(bsscl_engine *E) {
+  if (!E) return;
+  (void)hipSetDevice(E->device);
+  if (E->st) (void)hipStreamSynchronize(E->st);
+  for (auto &m : E->mat) m.codes.release();
+  E->F.release();
+  E->y.release();
+  E->ghq.release();
+  E->g64.release();
+  E->h64.release();
+  for (int s = 0; s < 2; ++s) {
+    E->codes_c[s].release();
+    E->gh_c[s].release();
+    E->rid_c[s].release();
+  }
+  E->rows32.release();
+  E->rows64.release();
+  E->feat_d.release();
+  E->nb_sel_d.release();
+  E->pool.release();
+  E->segs.release();
+  E->cand.release();
+  E->totals.release();
+  E->parents_d.release();
+  E->tiles_d.release();
+  E->tile_begin_d.release();
+  E->tile_left_d.release();
+  E->hist_node_d.release();
+  E->tile_off_d.release();
+  E->nleft_d.release();
+  E->htasks_d.release();
+  E->stasks_d.release();
+  E->tree_d.release();
+  E->offsets_d.release();
+  E->partials_d.release();
+  E->loss_d.release();
+  E->out_d.release();
+  E->pin.release();
+  for (hipEvent_t ev : E->ev_pool) (void)hipEventDestroy(ev);
+  if (E->st) (void)hipStreamDestroy(E->st);
+  delete E;
+}
+
+int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
+                       int32_t x_is_f64, int64_t n, int32_t F,
+                       const double *edges_2d, int32_t edge_stride,
+                       const int32_t *bin_counts, const int32_t *nan_bin_id,
+                       uint8_t *codes_out) {
+  if (!E || !X || !edges_2d || !bin_counts || !nan_bin_id)
+    return set_error(BSSCL_EINVAL, "bin_features: null argument");
+  if (slot < 0 || slot > 1) return set_error(BSSCL_EINVAL, "matrix slot must be 0 or 1");
+  if (n <= 0 || n > INT32_MAX || F <= 0)
+    return set_error(BSSCL_EINVAL, "bin_features: bad shape");
+  int32_t has_any_nan = 0;
+  for (int32_t j = 0; j < F; ++j) {
+    if (bin_counts[j] < 1 || bin_counts[j] >= edge_stride)
+      return set_error(BSSCL_EINVAL, "bin_features: bin_counts must be in [1, edge_stride)");
+    if (nan_bin_id[j] >= 0) has_any_nan = 1;
+  }
+  HIPCHK(hipSetDevice(E->device));
+  CHK(alloc_matrix(E, slot, n, F));
+  DevBuf<double> ed;
+  DevBuf<int32_t> nb, nid;
+  CHK(ed.ensure((size_t)F * edge_stride));
+  CHK(nb.ensure((size_t)F));
+  CHK(nid.ensure((size_t)F));
+  HIPCHK(hipMemcpyAsync(ed.p, edges_2d, (size_t)F * edge_stride * 8, hipMemcpyHostToDevice, E->st));
+  HIPCHK(hipMemcpyAsync(nb.p, bin_counts, (size_t)F * 4, hipMemcpyHostToDevice, E->st));
+  HIPCHK(hipMemcpyAsync(nid.p, nan_bin_id, (size_t)F * 4, hipMemcpyHostToDevice, E->st));
+  // Stream X through the device in row chunks of at most 256 MB.
+  const size_t esz = x_is_f64 ? 8 : 4;
+  int64_t chunk = std::max<int64_t>(64, (int64_t)((256u << 20) / (esz * (size_t)F)) / 64 * 64);
+  chunk = std::min<int64_t>(chunk, round_up(n, 64));
+  DevBuf<unsigned char> xd;
+  int rc = xd.ensure((size_t)chunk * F * esz);
+  if (rc != BSSCL_OK) { ed.release(); nb.release(); nid.release(); return rc; }
+  Matrix &M = E->mat[slot];
+  for (int64_t r0 = 0; r0 < n; r0 += chunk) {
+    const int64_t rows = std::min(chunk, n - r0);
+    hipError_t e = hipMemcpyAsync(xd.p, (const unsigned char *)X + (size_t)r0 * F * esz,
+                                  (size_t)rows * F * esz, hipMemcpyHostToDevice, E->st);
+    if (e == hipSuccess)
+      e = launch_bin(E->st, xd.p, x_is_f64, rows, F, ed.p, edge_stride, nb.p, nid.p,
+                     has_any_nan, M.codes.p + r0, M.ld);
+    if (e == hipSuccess) e = hipStreamSynchronize(E->st);
+    if (e != hipSuccess) {
+      xd.release(); ed.release(); nb.release(); nid.release();
+      return set_error(BSSCL_EDEVICE, std::string("binning: ") + hipGetErrorString(e));
+    }
+  }
+  xd.release();
+  ed.release();
+  nb.release();
+  nid.release();
+  if (codes_out) return bsscl_get_codes(E, slot, codes_out);
+  return BSSCL_OK;
+}
+
+int bsscl_load_codes(bsscl_engine *E, int32_t slot, const void *codes,
+                     int32_t codes_u16, int64_t n, int32_t F) {
+  if (!E || !codes) return set_error(BSSCL_EINVAL, "load_codes: null argument");
+  if (slot < 0 || slot > 1) return set_error(BSSCL_EINVAL, "matrix slot must be 0 or 1");
+  if (n <= 0 || n > INT32_MAX || F <= 0) return set_error(BSSCL_EINVAL, "load_codes: bad shape");
+  HIPCHK(hipSetDevice(E->device));
+  CHK(alloc_matrix(E, slot, n, F));
+  const size_t bytes = (size_t)n * F * (codes_u16 ? 2 : 1);
+  DevBuf<unsigned char> tmp;
+  CHK(tmp.ensure(bytes));
+  hipError_t e = hipMemcpyAsync(tmp.p, codes, bytes, hipMemcpyHostToDevice, E->st);
+  if (e == hipSuccess)
+    e = launch_load_codes(E->st, tmp.p, codes_u16, n, F, E->mat[slot].codes.p, E->mat[slot].ld);
+  if (e == hipSuccess) e = hipStreamSynchronize(E->st);
+  tmp.release();
+  if (e != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("load_codes: ") + hipGetErrorString(e));
+  return BSSCL_OK;
+}
+
+int bsscl_get_codes(bsscl_engine *E, int32_t slot, uint8_t *codes_out) {
+  if (!E || !codes_out) return set_error(BSSCL_EINVAL, "get_codes: null argument");
+  CHK(check_matrix(E, slot));
+  HIPCHK(hipSetDevice(E->device));
+  const Matrix &M = E->mat[slot];
+  DevBuf<uint8_t> tmp;
+  CHK(tmp.ensure((size_t)M.n * M.F));
+  hipError_t e = launch_get_codes(E->st, M.codes.p, M.ld, M.n, M.F, tmp.p);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(codes_out, tmp.p, (size_t)M.n * M.F, hipMemcpyDeviceToHost, E->st);
+  if (e == hipSuccess) e = hipStreamSynchronize(E->st);
+  tmp.release();
+  if (e != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("get_codes: ") + hipGetErrorString(e));
+  return BSSCL_OK;
+}
+
+int bsscl_build_tree(bsscl_engine *E, const double *grad, const double *hess,
+                     const int64_t *sample_indices, int64_t n_samples,
+                     const int32_t *feature_indices, int32_t n_selected,
+                     int32_t max_leaves, int32_t max_depth,
+                     int32_t min_samples_leaf, double min_child_weight,
+                     const int32_t *bin_counts, int32_t max_bins,
+                     double reg_lambda, double gamma, int32_t *out_features,
+                     int64_t *out_thresholds, double *out_values,
+                     int32_t *out_left, int32_t *out_right,
+                     int32_t *out_node_count, double *out_split_gains) {
+  if (!E || !grad || !hess || !sample_indices)
+    return set_error(BSSCL_EINVAL, "build_tree: null argument");
+  CHK(check_matrix(E, 0));
+  (void)max_bins;
+  const Matrix &X = E->mat[0];
+  if (n_samples <= 0) return set_error(BSSCL_EINVAL, "build_tree: no samples");
+  for (int64_t k = 0; k < n_samples; ++k)
+    if (sample_indices[k] < 0 || sample_indices[k] >= X.n)
+      return set_error(BSSCL_EINVAL, "build_tree: sample index out of range");
+  TreeOut out{out_features, out_thresholds, out_values, out_left, out_right,
+              out_node_count, out_split_gains};
+  std::vector<int32_t> feats, nb_sel;
+  CHK(validate_tree_args(E, feature_indices, n_selected, max_leaves,
+                         min_samples_leaf, bin_counts, out, feats, nb_sel));
+  HIPCHK(hipSetDevice(E->device));
+  CHK(load_grad_hess(E, grad, hess, X.n));
+  CHK(E->rows64.ensure((size_t)n_samples));
+  HIPCHK(hipMemcpyAsync(E->rows64.p, sample_indices, (size_t)n_samples * 8,
+                        hipMemcpyHostToDevice, E->st));
+  TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight,
+                reg_lambda, gamma};
+  return build_tree_core(E, false, n_samples, feats, nb_sel, tp, out);
+}
+
+int bsscl_boost_begin(bsscl_engine *E, const int64_t *y, int64_t n, double w0,
+                      double w1, double base_score) {
+  if (!E || !y) return set_error(BSSCL_EINVAL, "boost_begin: null argument");
+  CHK(check_matrix(E, 0));
+  if (n != E->mat[0].n) return set_error(BSSCL_EINVAL, "boost_begin: y length differs from matrix rows");
+  if (!(w0 > 0.0) || !(w1 > 0.0) || !std::isfinite(w0) || !std::isfinite(w1))
+    return set_error(BSSCL_EINVAL, "boost_begin: class weights must be positive");
+  HIPCHK(hipSetDevice(E->device));
+  std::vector<uint8_t> yb((size_t)n);
+  for (int64_t i = 0; i < n; ++i) {
+    if (y[i] != 0 && y[i] != 1) return set_error(BSSCL_EINVAL, "boost_begin: labels must be 0 or 1");
+    yb[(size_t)i] = (uint8_t)y[i];
+  }
+  CHK(E->y.ensure((size_t)n));
+  CHK(E->F.ensure((size_t)n));
+  CHK(E->ghq.ensure((size_t)n));
+  HIPCHK(hipMemcpyAsync(E->y.p, yb.data(), (size_t)n, hipMemcpyHostToDevice, E->st));
+  std::vector<double> f0((size_t)n, base_score);
+  HIPCHK(hipMemcpyAsync(E->F.p, f0.data(), (size_t)n * 8, hipMemcpyHostToDevice, E->st));
+  HIPCHK(hipStreamSynchronize(E->st));
+  E->w0 = w0;
+  E->w1 = w1;
+  E->boosting = true;
+  return BSSCL_OK;
+}
+
+int bsscl_boost_round(bsscl_engine *E, bsscl_sampler *sampler,
+                      int32_t max_leaves, int32_t max_depth,
+                      int32_t min_samples_leaf, double min_child_weight,
+                      const int32_t *bin_counts, int32_t max_bins,
+                      double reg_lambda, double gamma, double learning_rate,
+                      int32_t *out_features, int64_t *out_thresholds,
+                      double *out_values, int32_t *out_left,
+                      int32_t *out_right, int32_t *out_node_count,
+                      double *out_split_gains, double *out_train_loss) {
+  if (!E || !sampler) return set_error(BSSCL_EINVAL, "boost_round: null argument");
+  if (!E->boosting) return set_error(BSSCL_EINVAL, "boost_round: call boost_begin first");
+  (void)max_bins;
+  const Matrix &X = E->mat[0];
+  HIPCHK(hipSetDevice(E->device));
+  const int64_t m = sampler_n_sub(sampler);
+  const int32_t fsub = sampler_f_sub(sampler);
+  // Gradients from the current F: |g| <= max(w0, w1), h <= max(w0, w1)/4.
+  const double wmax = std::max(E->w0, E->w1);
+  const double gm = fixed_mul(wmax), hm = fixed_mul(0.25 * wmax);
+  E->g_scale = 1.0 / gm;
+  E->h_scale = 1.0 / hm;
+  HIPCHK(launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, gm, hm, E->ghq.p));
+  const int32_t *rows = nullptr, *feats_p = nullptr;
+  void *token = nullptr;
+  CHK(sampler_take(sampler, &rows, &feats_p, &token));
+  TreeOut out{out_features, out_thresholds, out_values, out_left, out_right,
+              out_node_count, out_split_gains};
+  std::vector<int32_t> feats, nb_sel;
+  int rc = validate_tree_args(E, feats_p, fsub, max_leaves, min_samples_leaf,
+                              bin_counts, out, feats, nb_sel);
+  if (rc == BSSCL_OK && m > X.n) rc = set_error(BSSCL_EINVAL, "boost_round: sampler rows exceed matrix");
+  if (rc == BSSCL_OK) rc = E->rows32.ensure((size_t)m);
+  if (rc == BSSCL_OK) {
+    hipError_t e = hipMemcpyAsync(E->rows32.p, rows, (size_t)m * 4, hipMemcpyHostToDevice, E->st);
+    if (e == hipSuccess) e = hipStreamSynchronize(E->st);
+    if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("row upload: ") + hipGetErrorString(e));
+  }
+  sampler_give_back(sampler, token);
+  CHK(rc);
+  TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight,
+                reg_lambda, gamma};
+  CHK(build_tree_core(E, true, m, feats, nb_sel, tp, out));
+  // F += lr * tree(X) over all rows, then the training log-loss.
+  CHK(upload_tree(E, out_features, out_thresholds, out_values, out_left,
+                  out_right, *out_node_count, X.F));
+  const int nb = update_F_blocks(X.n);
+  CHK(E->partials_d.ensure((size_t)nb));
+  CHK(E->loss_d.ensure(1));
+  HIPCHK(launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, *out_node_count,
+                         learning_rate, E->F.p, E->y.p, E->partials_d.p, nb));
+  HIPCHK(launch_sum_partials(E->st, E->partials_d.p, nb, E->loss_d.p));
+  double s = 0.0;
+  HIPCHK(hipMemcpyAsync(&s, E->loss_d.p, 8, hipMemcpyDeviceToHost, E->st));
+  CHK(sync(E));
+  if (out_train_loss) *out_train_loss = -s / (double)X.n;
+  return BSSCL_OK;
+}
+
+int bsscl_boost_get_F(bsscl_engine *E, double *F_out) {
+  if (!E || !F_out) return set_error(BSSCL_EINVAL, "boost_get_F: null argument");
+  if (!E->boosting) return set_error(BSSCL_EINVAL, "boost_get_F: no boosting run");
+  HIPCHK(hipSetDevice(E->device));
+  HIPCHK(hipMemcpyAsync(F_out, E->F.p, (size_t)E->mat[0].n * 8, hipMemcpyDeviceToHost, E->st));
+  HIPCHK(hipStreamSynchronize(E->st));
+  return BSSCL_OK;
+}
+
+int bsscl_boost_grad_hess(bsscl_engine *E, double *grad_out, double *hess_out) {
+  if (!E || !grad_out || !hess_out) return set_error(BSSCL_EINVAL, "boost_grad_hess: null argument");
+  if (!E->boosting) return set_error(BSSCL_EINVAL, "boost_grad_hess: no boosting run");
+  HIPCHK(hipSetDevice(E->device));
+  const int64_t n = E->mat[0].n;
+  CHK(E->g64.ensure((size_t)n));
+  CHK(E->h64.ensure((size_t)n));
+  HIPCHK(launch_grad_hess_f64(E->st, E->F.p, E->y.p, n, E->w0, E->w1, E->g64.p, E->h64.p));
+  HIPCHK(hipMemcpyAsync(grad_out, E->g64.p, (size_t)n * 8, hipMemcpyDeviceToHost, E->st));
+  HIPCHK(hipMemcpyAsync(hess_out, E->h64.p, (size_t)n * 8, hipMemcpyDeviceToHost, E->st));
+  HIPCHK(hipStreamSynchronize(E->st));
+  return BSSCL_OK;
+}
+
+int bsscl_predict(bsscl_engine *E, int32_t slot, const int16_t *features,
+                  const int64_t *thresholds, const double *values,
+                  const int32_t *left, const int32_t *right,
+                  const int32_t *offsets, int32_t n_trees,
+                  double learning_rate, double *out_F) {
+  if (!E || !out_F || (n_trees > 0 && (!features || !thresholds || !values || !left || !right || !offsets)))
+    return set_error(BSSCL_EINVAL, "predict: null argument");
+  CHK(check_matrix(E, slot));
+  if (n_trees < 0) return set_error(BSSCL_EINVAL, "predict: negative tree count");
+  HIPCHK(hipSetDevice(E->device));
+  const Matrix &M = E->mat[slot];
+  const int32_t total = n_trees > 0 ? offsets[n_trees] : 0;
+  std::vector<TreeNodeDev> nodes((size_t)std::max(total, 1));
+  for (int32_t t = 0; t < n_trees; ++t) {
+    const int32_t a = offsets[t], b = offsets[t + 1];
+    if (a < 0 || b <= a || b > total) return set_error(BSSCL_EINVAL, "predict: bad offsets");
+    for (int32_t i = a; i < b; ++i) {
+      TreeNodeDev &d = nodes[(size_t)i];
+      d.value = values[i];
+      d.feature = features[i];
+      if (d.feature >= 0) {
+        const int32_t l = left[i], r = right[i];
+        if (d.feature >= M.F || l < 0 || r < 0 || l >= b - a || r >= b - a || l <= i - a || r <= i - a)
+          return set_error(BSSCL_EINVAL, "predict: malformed tree " + std::to_string(t));
+        d.threshold = (int32_t)std::max<int64_t>(-1, std::min<int64_t>(thresholds[i], 1 << 20));
+        d.left = l;
+        d.right = r;
+      } else {
+        d.feature = -1;
+        d.threshold = 0;
+        d.left = d.right = 0;
+      }
+    }
+  }
+  CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 8u << 20)));
+  std::vector<int32_t> offs(offsets, offsets + n_trees + 1);
+  CHK(upload(E, E->tree_d, nodes.data(), nodes.size()));
+  CHK(upload(E, E->offsets_d, offs.data(), offs.size()));
+  CHK(E->out_d.ensure((size_t)M.n));
+  HIPCHK(launch_predict(E->st, M.codes.p, M.ld, M.n, E->tree_d.p, E->offsets_d.p,
+                        n_trees, learning_rate, E->out_d.p));
+  HIPCHK(hipMemcpyAsync(out_F, E->out_d.p, (size_t)M.n * 8, hipMemcpyDeviceToHost, E->st));
+  CHK(sync(E));
+  return BSSCL_OK;
+}
+
+int bsscl_predict_tree(bsscl_engine *E, int32_t slot, const int32_t *features,
+                       const int64_t *thresholds, const double *values,
+                       const int32_t *left, const int32_t *right,
+                       int32_t node_count, double *out) {
+  if (!E || !features || !thresholds || !values || !left || !right || !out)
+    return set_error(BSSCL_EINVAL, "predict_tree: null argument");
+  CHK(check_matrix(E, slot));
+  HIPCHK(hipSetDevice(E->device));
+  const Matrix &M = E->mat[slot];
+  CHK(upload_tree(E, features, thresholds, values, left, right, node_count, M.F));
+  CHK(E->out_d.ensure((size_t)M.n));
+  HIPCHK(launch_predict_tree(E->st, M.codes.p, M.ld, M.n, E->tree_d.p, node_count, E->out_d.p));
+  HIPCHK(hipMemcpyAsync(out, E->out_d.p, (size_t)M.n * 8, hipMemcpyDeviceToHost, E->st));
+  CHK(sync(E));
+  return BSSCL_OK;
+}
+
+int bsscl_node_split(bsscl_engine *E, const double *grad, const double *hess,
+                     const int64_t *rows, int64_t m,
+                     const int32_t *feature_indices, int32_t n_selected,
+                     const int32_t *bin_counts, double min_child_weight,
+                     double reg_lambda, double *out_G, double *out_H,
+                     double *out_gain, int32_t *out_feature, int32_t *out_bin) {
+  if (!E || !grad || !hess || !rows || !feature_indices || !bin_counts)
+    return set_error(BSSCL_EINVAL, "node_split: null argument");
+  CHK(check_matrix(E, 0));
+  const Matrix &X = E->mat[0];
+  if (m <= 0) return set_error(BSSCL_EINVAL, "node_split: no rows");
+  for (int64_t k = 0; k < m; ++k)
+    if (rows[k] < 0 || rows[k] >= X.n) return set_error(BSSCL_EINVAL, "node_split: row out of range");
+  std::vector<int32_t> feats(feature_indices, feature_indices + n_selected), nb_sel((size_t)n_selected);
+  for (int32_t i = 0; i < n_selected; ++i) {
+    if (feats[(size_t)i] < 0 || feats[(size_t)i] >= X.F) return set_error(BSSCL_EINVAL, "node_split: feature out of range");
+    nb_sel[(size_t)i] = bin_counts[feats[(size_t)i]];
+    if (nb_sel[(size_t)i] < 1 || nb_sel[(size_t)i] > kBins) return set_error(BSSCL_EINVAL, "node_split: bad bin count");
+  }
+  HIPCHK(hipSetDevice(E->device));
+  CHK(load_grad_hess(E, grad, hess, X.n));
+  CHK(E->rows64.ensure((size_t)m));
+  HIPCHK(hipMemcpyAsync(E->rows64.p, rows, (size_t)m * 8, hipMemcpyHostToDevice, E->st));
+  // A one-node tree build with max_leaves = 1 computes exactly the root
+  // histogram and split; read them back before the replay.
+  const int32_t F_sel = n_selected;
+  E->ld_c = round_up(m + 8, 256);
+  CHK(E->codes_c[0].ensure((size_t)E->ld_c * F_sel));
+  CHK(E->gh_c[0].ensure((size_t)E->ld_c));
+  CHK(E->rid_c[0].ensure((size_t)E->ld_c));
+  CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 8u << 20)));
+  CHK(ensure_nodes(E, 256, F_sel));
+  CHK(upload(E, E->feat_d, feats.data(), feats.size()));
+  CHK(upload(E, E->nb_sel_d, nb_sel.data(), nb_sel.size()));
+  HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, E->feat_d.p, F_sel, nullptr,
+                            E->rows64.p, m, E->ghq.p, E->codes_c[0].p, E->ld_c,
+                            E->gh_c[0].p, E->rid_c[0].p, E->ld_c));
+  NodeSeg rs{0, m, 1, 1};
+  CHK(upload(E, E->segs, &rs, 1));
+  int32_t zero = 0;
+  CHK(upload(E, E->hist_node_d, &zero, 1));
+  HIPCHK(hipMemsetAsync(E->pool.p, 0, (size_t)E->node_stride * 8, E->st));
+  const int32_t th = hist_tile_rows(E, m);
+  std::vector<HistTask> ht;
+  for (int64_t t = 0; t * th < m; ++t) ht.push_back({0, (int32_t)t});
+  CHK(launch_hist_tasks(E, 0, ht, F_sel, th));
+  TreeParams tp{2, 1, 0, min_child_weight, reg_lambda, 0.0};
+  std::vector<SplitTask> stv{{0, -1, -1, 0}};
+  CHK(launch_split_tasks(E, stv, F_sel, tp));
+  std::vector<HNode> nodes(1);
+  CHK(read_nodes(E, 0, 1, F_sel, nodes));
+  if (out_G || out_H) {
+    std::vector<long long> h((size_t)E->node_stride);
+    HIPCHK(hipMemcpyAsync(h.data(), E->pool.p, (size_t)E->node_stride * 8, hipMemcpyDeviceToHost, E->st));
+    HIPCHK(hipStreamSynchronize(E->st));
+    for (int64_t i = 0; i < (int64_t)F_sel * kBins; ++i) {
+      if (out_G) out_G[i] = (double)h[(size_t)(2 * i)] * E->g_scale;
+      if (out_H) out_H[i] = (double)h[(size_t)(2 * i + 1)] * E->h_scale;
+    }
+  }
+  if (out_gain) *out_gain = nodes[0].fpos >= 0 ? nodes[0].gain : -1e9;
+  if (out_feature) *out_feature = nodes[0].fpos >= 0 ? feats[(size_t)nodes[0].fpos] : -1;
+  if (out_bin) *out_bin = nodes[0].fpos >= 0 ? nodes[0].bin : 0;
+  return BSSCL_OK;
+}
+
+int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
+                    int32_t feature, int32_t bin, int64_t *out_rows,
+                    int64_t *out_n_left) {
+  if (!E || !rows || !out_rows || !out_n_left)
+    return set_error(BSSCL_EINVAL, "partition: null argument");
+  CHK(check_matrix(E, 0));
+  const Matrix &X = E->mat[0];
+  if (m <= 0) return set_error(BSSCL_EINVAL, "partition: no rows");
+  if (feature < 0 || feature >= X.F) return set_error(BSSCL_EINVAL, "partition: feature out of range");
+  for (int64_t k = 0; k < m; ++k)
+    if (rows[k] < 0 || rows[k] >= X.n) return set_error(BSSCL_EINVAL, "partition: row out of range");
+  HIPCHK(hipSetDevice(E->device));
+  if (!E->ghq.p || E->ghq.cap < (size_t)X.n) {
+    CHK(E->ghq.ensure((size_t)X.n));
+    HIPCHK(hipMemsetAsync(E->ghq.p, 0, (size_t)X.n * sizeof(int2), E->st));
+  }
+  CHK(E->rows64.ensure((size_t)m));
+  HIPCHK(hipMemcpyAsync(E->rows64.p, rows, (size_t)m * 8, hipMemcpyHostToDevice, E->st));
+  E->ld_c = round_up(m + 8, 256);
+  for (int s = 0; s < 2; ++s) {
+    CHK(E->codes_c[s].ensure((size_t)E->ld_c));
+    CHK(E->gh_c[s].ensure((size_t)E->ld_c));
+    CHK(E->rid_c[s].ensure((size_t)E->ld_c));
+  }
+  CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 8u << 20)));
+  CHK(ensure_nodes(E, 256, 1));
+  const int32_t f1 = feature;
+  CHK(upload(E, E->feat_d, &f1, 1));
+  HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, E->feat_d.p, 1, nullptr,
+                            E->rows64.p, m, E->ghq.p, E->codes_c[0].p, E->ld_c,
+                            E->gh_c[0].p, E->rid_c[0].p, E->ld_c));
+  std::vector<PartParent> parents{{0, m, 0, bin, 1, 2}};
+  std::vector<PartTile> tiles;
+  for (int64_t r = 0; r < m; r += kPartTile)
+    tiles.push_back({r, (int32_t)std::min<int64_t>(kPartTile, m - r), 0});
+  std::vector<int32_t> tb{0, (int32_t)tiles.size()};
+  CHK(upload(E, E->parents_d, parents.data(), 1));
+  CHK(upload(E, E->tiles_d, tiles.data(), tiles.size()));
+  CHK(upload(E, E->tile_begin_d, tb.data(), 2));
+  CHK(E->tile_left_d.ensure(tiles.size()));
+  CHK(E->tile_off_d.ensure(tiles.size()));
+  CHK(E->nleft_d.ensure(1));
+  CHK(E->hist_node_d.ensure(1));
+  HIPCHK(launch_part_count(E->st, E->codes_c[0].p, E->ld_c, E->parents_d.p, E->tiles_d.p,
+                           (int32_t)tiles.size(), E->tile_left_d.p));
+  HIPCHK(launch_part_scan(E->st, E->parents_d.p, 1, E->tile_begin_d.p, E->tile_left_d.p,
+                          E->tile_off_d.p, E->nleft_d.p, E->segs.p, E->hist_node_d.p, 0));
+  HIPCHK(launch_part_scatter(E->st, E->codes_c[0].p, E->codes_c[1].p, E->ld_c,
+                             E->gh_c[0].p, E->gh_c[1].p, E->rid_c[0].p, E->rid_c[1].p,
+                             E->parents_d.p, E->tiles_d.p, (int32_t)tiles.size(),
+                             E->tile_off_d.p, E->nleft_d.p, 1));
+  std::vector<int32_t> r32((size_t)m);
+  int64_t nl = 0;
+  HIPCHK(hipMemcpyAsync(r32.data(), E->rid_c[1].p, (size_t)m * 4, hipMemcpyDeviceToHost, E->st));
+  HIPCHK(hipMemcpyAsync(&nl, E->nleft_d.p, 8, hipMemcpyDeviceToHost, E->st));
+  CHK(sync(E));
+  for (int64_t k = 0; k < m; ++k) out_rows[k] = r32[(size_t)k];
+  *out_n_left = nl;
+  return BSSCL_OK;
+}
+
+int bsscl_engine_set_profiling(bsscl_engine *E, int32_t on) {
+  if (!E) return set_error(BSSCL_EINVAL, "null engine");
+  HIPCHK(hipSetDevice(E->device));
+  HIPCHK(hipStreamSynchronize(E->st));
+  CHK(prof_collect(E));
+  E->prof = on != 0;
+  if (on) std::memset(E->stats, 0, sizeof(E->stats));
+  return BSSCL_OK;
+}
+
+int bsscl_engine_stats(bsscl_engine *E, double *out, int32_t cap, int32_t *n_out) {
+  if (!E || !out || !n_out) return set_error(BSSCL_EINVAL, "null argument");
+  const int32_t n = std::min<int32_t>(cap, 10);
+  for (int32_t i = 0; i < n; ++i) out[i] = E->stats[i];
+  *n_out = n;
+  return BSSCL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,870 @@
+// HIP kernels of the tree engine, written for gfx950 (wave64, 160 KB LDS).
+//
+// Layouts in HBM
+//   codes     feature-major uint8 [F][ld], ld a multiple of 256, zero padded
+//   ghq       int2 [n]: gradient and hessian of each row in 32-bit fixed
+//             point (g*2^sg, h*2^sh), rebuilt every boosting round
+//   compact   per tree, two ping-pong sets of (codes_c [F_sel][ld_c] uint8,
+//             gh_c int2 [ld_c], rid_c int32 [ld_c]); every node's rows are a
+//             contiguous segment of the set of its depth's parity
+//   pool      per node [F_sel][256 bins][g,h] int64 fixed-point sums
+//
+// Fixed-point sums are exact integer additions, so histograms, splits and
+// trees do not depend on atomic order or on the order of rows.
+#include "kernels.h"
+
+namespace bsscl {
+
+namespace {
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
+
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    T t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Exclusive scan over a block of BLOCK threads; `tmp` holds BLOCK/64 words.
+template <int BLOCK>
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t *tmp,
+                                                    uint32_t &total) {
+  const int wid = (int)(threadIdx.x >> 6);
+  const uint32_t incl = wave_incl_scan<uint32_t>(v);
+  if (lane_id() == 63) tmp[wid] = incl;
+  __syncthreads();
+  uint32_t pre = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < BLOCK / 64; ++w) {
+    uint32_t s = tmp[w];
+    pre += (w < wid) ? s : 0u;
+    tot += s;
+  }
+  __syncthreads();
+  total = tot;
+  return pre + incl - v;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Binning: est:155-226 codes plus est:2144-2189 NaN handling.  A block bins
+// 64 rows x all features: the rows are read row-major (coalesced) into LDS,
+// each code is found by the binary search of the standard strategy (the
+// hybrid strategy returns the same code), and each feature's 64 codes are
+// written as one contiguous run of the feature-major matrix.
+// ---------------------------------------------------------------------------
+constexpr int kBinRows = 64;
+
+// Code of one value: the largest k in [0, nb-1] with e[k] <= v, 0 below
+// e[0], nb-1 at or above e[nb] (est:204-226); NaN handling of est:2159-2177.
+__device__ __forceinline__ uint8_t bin_one(double v, const double *__restrict__ e,
+                                           int32_t nbf, bool nan_feat,
+                                           int32_t has_any_nan) {
+  if (v != v) {
+    if (nan_feat) return 0;
+    if (has_any_nan) v = 0.0;  // placeholder value of est:2160
+  }
+  int32_t c;
+  if (v < e[0]) {
+    c = 0;
+  } else if (v >= e[nbf]) {
+    c = nbf - 1;
+  } else {
+    int32_t lo = 0, hi = nbf - 1;
+    while (lo < hi) {
+      const int32_t mid = (lo + hi) >> 1;
+      if (e[mid + 1] <= v) lo = mid + 1;
+      else hi = mid;
+    }
+    c = lo;
+  }
+  if (nan_feat) c += 1;  // est:2176
+  return (uint8_t)min(c, 255);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_bin(
+    const T *__restrict__ X, int64_t n, int32_t F,
+    const double *__restrict__ edges, int32_t stride,
+    const int32_t *__restrict__ nb, const int32_t *__restrict__ nan_id,
+    int32_t has_any_nan, uint8_t *__restrict__ codes, int64_t ld) {
+  extern __shared__ unsigned char smem[];
+  T *xs = reinterpret_cast<T *>(smem);                        // [64][F]
+  uint8_t *cs = smem + sizeof(T) * (size_t)kBinRows * F;     // [F][64]
+  const int64_t r0 = (int64_t)blockIdx.x * kBinRows;
+  const int rows = (int)min<int64_t>(kBinRows, n - r0);
+  const int tot = rows * F;
+  for (int i = threadIdx.x; i < tot; i += blockDim.x)
+    xs[i] = X[r0 * F + i];
+  __syncthreads();
+  for (int i = threadIdx.x; i < kBinRows * F; i += blockDim.x) {
+    const int f = i / kBinRows, r = i % kBinRows;
+    uint8_t code = 0;
+    if (r < rows)
+      code = bin_one((double)xs[r * F + f], edges + (int64_t)f * stride, nb[f],
+                     nan_id[f] >= 0, has_any_nan);
+    cs[f * kBinRows + r] = code;
+  }
+  __syncthreads();
+  // 16 dwords per feature.
+  for (int i = threadIdx.x; i < F * (kBinRows / 4); i += blockDim.x) {
+    const int f = i / (kBinRows / 4), w = i % (kBinRows / 4);
+    const uint32_t v = *reinterpret_cast<const uint32_t *>(cs + f * kBinRows + 4 * w);
+    *reinterpret_cast<uint32_t *>(codes + (int64_t)f * ld + r0 + 4 * w) = v;
+  }
+}
+
+// One thread per (row, feature) for matrices too wide to stage 64 rows in LDS.
+template <typename T>
+__global__ __launch_bounds__(256) void k_bin_wide(
+    const T *__restrict__ X, int64_t n, int32_t F,
+    const double *__restrict__ edges, int32_t stride,
+    const int32_t *__restrict__ nb, const int32_t *__restrict__ nan_id,
+    int32_t has_any_nan, uint8_t *__restrict__ codes, int64_t ld) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int32_t f = (int32_t)blockIdx.y;
+  if (i >= n) return;
+  codes[(int64_t)f * ld + i] =
+      bin_one((double)X[i * F + f], edges + (int64_t)f * stride, nb[f],
+              nan_id[f] >= 0, has_any_nan);
+}
+
+hipError_t launch_bin(hipStream_t st, const void *X, int is_f64, int64_t n,
+                      int32_t F, const double *edges, int32_t stride,
+                      const int32_t *nb, const int32_t *nan_id,
+                      int32_t has_any_nan, uint8_t *codes, int64_t ld) {
+  if (n <= 0) return hipSuccess;
+  const size_t lds = (is_f64 ? 8 : 4) * (size_t)kBinRows * F + (size_t)kBinRows * F;
+  if (lds > 48 * 1024) {
+    const dim3 grid((unsigned)((n + 255) / 256), (unsigned)F);
+    if (is_f64)
+      hipLaunchKernelGGL(k_bin_wide<double>, grid, dim3(256), 0, st,
+                         (const double *)X, n, F, edges, stride, nb, nan_id,
+                         has_any_nan, codes, ld);
+    else
+      hipLaunchKernelGGL(k_bin_wide<float>, grid, dim3(256), 0, st,
+                         (const float *)X, n, F, edges, stride, nb, nan_id,
+                         has_any_nan, codes, ld);
+    return hipGetLastError();
+  }
+  const unsigned blocks = (unsigned)((n + kBinRows - 1) / kBinRows);
+  if (is_f64)
+    hipLaunchKernelGGL(k_bin<double>, dim3(blocks), dim3(256), lds, st,
+                       (const double *)X, n, F, edges, stride, nb, nan_id,
+                       has_any_nan, codes, ld);
+  else
+    hipLaunchKernelGGL(k_bin<float>, dim3(blocks), dim3(256), lds, st,
+                       (const float *)X, n, F, edges, stride, nb, nan_id,
+                       has_any_nan, codes, ld);
+  return hipGetLastError();
+}
+
+// Row-major uint8/uint16 codes -> feature-major uint8 (values above 255
+// become 255).
+template <typename T>
+__global__ __launch_bounds__(256) void k_load_codes(const T *__restrict__ src,
+                                                    int64_t n, int32_t F,
+                                                    uint8_t *__restrict__ codes,
+                                                    int64_t ld) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  for (int32_t f = 0; f < F; ++f) {
+    uint32_t v = (uint32_t)src[i * F + f];
+    codes[(int64_t)f * ld + i] = (uint8_t)min(v, 255u);
+  }
+}
+
+hipError_t launch_load_codes(hipStream_t st, const void *src, int is_u16,
+                             int64_t n, int32_t F, uint8_t *codes, int64_t ld) {
+  if (n <= 0) return hipSuccess;
+  const unsigned blocks = (unsigned)((n + 255) / 256);
+  if (is_u16)
+    hipLaunchKernelGGL(k_load_codes<uint16_t>, dim3(blocks), dim3(256), 0, st,
+                       (const uint16_t *)src, n, F, codes, ld);
+  else
+    hipLaunchKernelGGL(k_load_codes<uint8_t>, dim3(blocks), dim3(256), 0, st,
+                       (const uint8_t *)src, n, F, codes, ld);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_get_codes(const uint8_t *__restrict__ codes,
+                                                   int64_t ld, int64_t n, int32_t F,
+                                                   uint8_t *__restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  for (int32_t f = 0; f < F; ++f) dst[i * F + f] = codes[(int64_t)f * ld + i];
+}
+
+hipError_t launch_get_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
+                            int64_t n, int32_t F, uint8_t *dst) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_get_codes, dim3((unsigned)((n + 255) / 256)), dim3(256),
+                     0, st, codes, ld, n, F, dst);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Gradients / hessians.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_quantize(const double *__restrict__ g,
+                                                  const double *__restrict__ h,
+                                                  int64_t n, double g_mul,
+                                                  double h_mul,
+                                                  int2 *__restrict__ ghq) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  ghq[i] = make_int2(__double2int_rn(g[i] * g_mul), __double2int_rn(h[i] * h_mul));
+}
+
+hipError_t launch_quantize(hipStream_t st, const double *g, const double *h,
+                           int64_t n, double g_mul, double h_mul, int2 *ghq) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_quantize, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     st, g, h, n, g_mul, h_mul, ghq);
+  return hipGetLastError();
+}
+
+// est:2861 and est:2873-2874: p = 1/(1+exp(-clip(F,-500,500))),
+// g = w*(p-y), h = (w*p)*(1-p), each product rounded separately.
+__device__ __forceinline__ void logistic_gh(double F, double y, double w,
+                                            double &g, double &h) {
+  const double Fc = fmin(fmax(F, -500.0), 500.0);
+  const double p = 1.0 / (1.0 + exp(-Fc));
+  g = __dmul_rn(w, __dsub_rn(p, y));
+  h = __dmul_rn(__dmul_rn(w, p), __dsub_rn(1.0, p));
+}
+
+__global__ __launch_bounds__(256) void k_grad_hess(const double *__restrict__ F,
+                                                   const uint8_t *__restrict__ y,
+                                                   int64_t n, double w0, double w1,
+                                                   double g_mul, double h_mul,
+                                                   int2 *__restrict__ ghq) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int yi = y[i];
+  double g, h;
+  logistic_gh(F[i], (double)yi, yi ? w1 : w0, g, h);
+  ghq[i] = make_int2(__double2int_rn(g * g_mul), __double2int_rn(h * h_mul));
+}
+
+hipError_t launch_grad_hess(hipStream_t st, const double *F, const uint8_t *y,
+                            int64_t n, double w0, double w1, double g_mul,
+                            double h_mul, int2 *ghq) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_grad_hess, dim3((unsigned)((n + 255) / 256)), dim3(256),
+                     0, st, F, y, n, w0, w1, g_mul, h_mul, ghq);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_grad_hess_f64(const double *__restrict__ F,
+                                                       const uint8_t *__restrict__ y,
+                                                       int64_t n, double w0,
+                                                       double w1, double *__restrict__ g,
+                                                       double *__restrict__ h) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int yi = y[i];
+  logistic_gh(F[i], (double)yi, yi ? w1 : w0, g[i], h[i]);
+}
+
+hipError_t launch_grad_hess_f64(hipStream_t st, const double *F,
+                                const uint8_t *y, int64_t n, double w0,
+                                double w1, double *g, double *h) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_grad_hess_f64, dim3((unsigned)((n + 255) / 256)),
+                     dim3(256), 0, st, F, y, n, w0, w1, g, h);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Root gather: the tree's in-bag rows (ascending ids from the sampler, or the
+// caller's order) -> compact feature-major set 0.  One thread fills 4
+// consecutive compact rows, so every store is a dword.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_gather_root(
+    const uint8_t *__restrict__ codes, int64_t ld, const int32_t *__restrict__ feat,
+    int32_t F_sel, const int32_t *__restrict__ rows32,
+    const int64_t *__restrict__ rows64, int64_t m, const int2 *__restrict__ ghq,
+    uint8_t *__restrict__ codes_c, int64_t ld_c, int2 *__restrict__ gh_c,
+    int32_t *__restrict__ rid_c, int64_t pad_to) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t k0 = t * 4;
+  if (k0 >= pad_to) return;
+  int32_t r[4];
+  bool ok[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    ok[k] = (k0 + k) < m;
+    r[k] = ok[k] ? (rows32 ? rows32[k0 + k] : (int32_t)rows64[k0 + k]) : 0;
+    gh_c[k0 + k] = ok[k] ? ghq[r[k]] : make_int2(0, 0);
+    rid_c[k0 + k] = ok[k] ? r[k] : -1;
+  }
+  for (int32_t f = 0; f < F_sel; ++f) {
+    const uint8_t *col = codes + (int64_t)feat[f] * ld;
+    uint32_t w = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      w |= (ok[k] ? (uint32_t)col[r[k]] : 0u) << (8 * k);
+    *reinterpret_cast<uint32_t *>(codes_c + (int64_t)f * ld_c + k0) = w;
+  }
+}
+
+hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
+                              const int32_t *feat, int32_t F_sel,
+                              const int32_t *rows32, const int64_t *rows64,
+                              int64_t m, const int2 *ghq, uint8_t *codes_c,
+                              int64_t ld_c, int2 *gh_c, int32_t *rid_c,
+                              int64_t pad_to) {
+  const int64_t threads = (pad_to + 3) / 4;
+  if (threads <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_gather_root, dim3((unsigned)((threads + 255) / 256)),
+                     dim3(256), 0, st, codes, ld, feat, F_sel, rows32, rows64, m,
+                     ghq, codes_c, ld_c, gh_c, rid_c, pad_to);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Histogram build (est:581-596, est:722-737).
+//
+// A block owns one tile of a node's contiguous rows and a chunk of the
+// selected features.  Its private histogram [nf][256][g,h] int64 lives in
+// LDS (4 KB per feature).  Each thread takes 4 consecutive rows: one 32-byte
+// load of their (g,h), then per feature one dword of 4 packed codes and 8
+// 64-bit LDS adds.  Rows of the dword outside the tile add zero.  The block
+// then adds its non-zero bins into the node's global histogram.
+// ---------------------------------------------------------------------------
+constexpr int kHistBlock = 512;
+
+__global__ __launch_bounds__(kHistBlock) void k_hist(
+    const uint8_t *__restrict__ codes_c, int64_t ld_c,
+    const int2 *__restrict__ gh_c, const HistTask *__restrict__ tasks,
+    const int32_t *__restrict__ hist_node, const NodeSeg *__restrict__ segs,
+    const int32_t *__restrict__ nb_sel, int32_t F_sel, int32_t fchunk,
+    int32_t tile_rows, unsigned long long *__restrict__ pool,
+    int64_t node_stride) {
+  extern __shared__ unsigned long long lh[];
+  const HistTask task = tasks[blockIdx.x];
+  const int32_t node = hist_node[task.ref];
+  if (node < 0) return;
+  const NodeSeg seg = segs[node];
+  if (!seg.valid) return;
+  const int64_t r0 = seg.start + (int64_t)task.tile * tile_rows;
+  const int64_t rend = seg.start + seg.count;
+  if (r0 >= rend) return;
+  const int64_t r1 = min(rend, r0 + (int64_t)tile_rows);
+  const int f0 = (int)blockIdx.y * fchunk;
+  const int nf = min(fchunk, F_sel - f0);
+  if (nf <= 0) return;
+
+  __shared__ int32_t nbm1[256];
+  for (int i = threadIdx.x; i < nf; i += kHistBlock) nbm1[i] = nb_sel[f0 + i] - 1;
+  for (int i = threadIdx.x; i < nf * kHistPerFeat; i += kHistBlock) lh[i] = 0ull;
+  __syncthreads();
+
+  const int64_t d0 = r0 >> 2, d1 = (r1 + 3) >> 2;
+  const uint8_t *cbase = codes_c + (int64_t)f0 * ld_c;
+  for (int64_t d = d0 + threadIdx.x; d < d1; d += kHistBlock) {
+    const int64_t row = d << 2;
+    const int4 *ghp = reinterpret_cast<const int4 *>(gh_c + row);
+    const int4 a = ghp[0], b = ghp[1];
+    long long g[4] = {a.x, a.z, b.x, b.z};
+    long long h[4] = {a.y, a.w, b.y, b.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const bool in = (row + k >= r0) && (row + k < r1);
+      g[k] = in ? g[k] : 0;
+      h[k] = in ? h[k] : 0;
+    }
+    const uint32_t *cp = reinterpret_cast<const uint32_t *>(cbase + row);
+    const int64_t ldw = ld_c >> 2;
+    int f = 0;
+    for (; f + 4 <= nf; f += 4) {
+      uint32_t w[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) w[u] = cp[(int64_t)(f + u) * ldw];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t lim = (uint32_t)nbm1[f + u];
+        unsigned long long *hf = lh + (f + u) * kHistPerFeat;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t bin = min((w[u] >> (8 * k)) & 255u, lim);
+          atomicAdd(hf + 2 * bin, (unsigned long long)g[k]);
+          atomicAdd(hf + 2 * bin + 1, (unsigned long long)h[k]);
+        }
+      }
+    }
+    for (; f < nf; ++f) {
+      const uint32_t w = cp[(int64_t)f * ldw];
+      const uint32_t lim = (uint32_t)nbm1[f];
+      unsigned long long *hf = lh + f * kHistPerFeat;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t bin = min((w >> (8 * k)) & 255u, lim);
+        atomicAdd(hf + 2 * bin, (unsigned long long)g[k]);
+        atomicAdd(hf + 2 * bin + 1, (unsigned long long)h[k]);
+      }
+    }
+  }
+  __syncthreads();
+  unsigned long long *dst = pool + (int64_t)node * node_stride + (int64_t)f0 * kHistPerFeat;
+  for (int i = threadIdx.x; i < nf * kHistPerFeat; i += kHistBlock) {
+    const unsigned long long v = lh[i];
+    if (v) atomicAdd(dst + i, v);
+  }
+}
+
+hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
+                       const int2 *gh_c, const HistTask *tasks,
+                       int32_t n_tasks, const int32_t *hist_node,
+                       const NodeSeg *segs, const int32_t *nb_sel,
+                       int32_t F_sel, int32_t fchunk, int32_t tile_rows,
+                       unsigned long long *pool, int64_t node_stride,
+                       size_t lds_bytes) {
+  if (n_tasks <= 0) return hipSuccess;
+  const unsigned chunks = (unsigned)((F_sel + fchunk - 1) / fchunk);
+  static size_t attr_bytes = 0;
+  if (lds_bytes > attr_bytes) {
+    hipError_t e = hipFuncSetAttribute((const void *)k_hist,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds_bytes);
+    if (e != hipSuccess) return e;
+    attr_bytes = lds_bytes;
+  }
+  hipLaunchKernelGGL(k_hist, dim3((unsigned)n_tasks, chunks), dim3(kHistBlock),
+                     lds_bytes, st, codes_c, ld_c, gh_c, tasks, hist_node, segs,
+                     nb_sel, F_sel, fchunk, tile_rows, pool, node_stride);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Partition (est:662-674, made stable): count, scan, scatter.
+// ---------------------------------------------------------------------------
+constexpr int kPartBlock = 256;
+
+__global__ __launch_bounds__(kPartBlock) void k_part_count(
+    const uint8_t *__restrict__ codes_c, int64_t ld_c,
+    const PartParent *__restrict__ parents, const PartTile *__restrict__ tiles,
+    int32_t *__restrict__ tile_left) {
+  __shared__ uint32_t tmp[kPartBlock / 64];
+  const PartTile t = tiles[blockIdx.x];
+  const PartParent P = parents[t.parent];
+  const int64_t r0 = t.row0, r1 = t.row0 + t.rows;
+  const uint8_t *col = codes_c + (int64_t)P.fpos * ld_c;
+  uint32_t cnt = 0;
+  for (int64_t d = (r0 >> 2) + threadIdx.x; d < ((r1 + 3) >> 2); d += kPartBlock) {
+    const int64_t row = d << 2;
+    const uint32_t w = *reinterpret_cast<const uint32_t *>(col + row);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const bool in = (row + k >= r0) && (row + k < r1);
+      cnt += (in && ((w >> (8 * k)) & 255u) <= (uint32_t)P.bin) ? 1u : 0u;
+    }
+  }
+  uint32_t total;
+  block_excl_scan<kPartBlock>(cnt, tmp, total);
+  if (threadIdx.x == 0) tile_left[blockIdx.x] = (int32_t)total;
+}
+
+hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
+                             int64_t ld_c, const PartParent *parents,
+                             const PartTile *tiles, int32_t n_tiles,
+                             int32_t *tile_left) {
+  if (n_tiles <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_part_count, dim3((unsigned)n_tiles), dim3(kPartBlock), 0,
+                     st, codes_c, ld_c, parents, tiles, tile_left);
+  return hipGetLastError();
+}
+
+// One block per parent: exclusive offsets of its tiles' left counts, the
+// children's segments, whether the split is kept (est:678-683) and which
+// child is the smaller one (est:701-709).
+__global__ __launch_bounds__(kPartBlock) void k_part_scan(
+    const PartParent *__restrict__ parents, const int32_t *__restrict__ tile_begin,
+    const int32_t *__restrict__ tile_left, int64_t *__restrict__ tile_left_off,
+    int64_t *__restrict__ parent_nleft, NodeSeg *__restrict__ segs,
+    int32_t *__restrict__ hist_node, int32_t min_samples_leaf) {
+  __shared__ uint32_t tmp[kPartBlock / 64];
+  const int p = (int)blockIdx.x;
+  const PartParent P = parents[p];
+  const int t0 = tile_begin[p], t1 = tile_begin[p + 1];
+  int64_t carry = 0;
+  for (int base = t0; base < t1; base += kPartBlock) {
+    const int t = base + (int)threadIdx.x;
+    const uint32_t v = (t < t1) ? (uint32_t)tile_left[t] : 0u;
+    uint32_t total;
+    const uint32_t pre = block_excl_scan<kPartBlock>(v, tmp, total);
+    if (t < t1) tile_left_off[t] = carry + pre;
+    carry += total;
+  }
+  if (threadIdx.x != 0) return;
+  parent_nleft[p] = carry;
+  const int64_t nl = carry, nr = P.count - carry;
+  const int32_t ok = (nl >= min_samples_leaf && nr >= min_samples_leaf) ? 1 : 0;
+  const bool left_small = nl <= nr;
+  NodeSeg L, R;
+  L.start = P.start;
+  L.count = nl;
+  L.valid = ok;
+  L.is_small = left_small ? 1 : 0;
+  R.start = P.start + nl;
+  R.count = nr;
+  R.valid = ok;
+  R.is_small = left_small ? 0 : 1;
+  segs[P.left_id] = L;
+  segs[P.right_id] = R;
+  hist_node[p] = ok ? (left_small ? P.left_id : P.right_id) : -1;
+}
+
+hipError_t launch_part_scan(hipStream_t st, const PartParent *parents,
+                            int32_t n_parents, const int32_t *tile_begin,
+                            const int32_t *tile_left, int64_t *tile_left_off,
+                            int64_t *parent_nleft, NodeSeg *segs,
+                            int32_t *hist_node, int32_t min_samples_leaf) {
+  if (n_parents <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_part_scan, dim3((unsigned)n_parents), dim3(kPartBlock), 0,
+                     st, parents, tile_begin, tile_left, tile_left_off,
+                     parent_nleft, segs, hist_node, min_samples_leaf);
+  return hipGetLastError();
+}
+
+// Moves every row of a tile to its child segment in the other buffer set,
+// keeping the input order within each side: a row's rank among the tile's
+// left (right) rows is the block-wide exclusive scan of per-thread counts
+// plus its position inside the thread's 4 rows.
+__global__ __launch_bounds__(kPartBlock) void k_part_scatter(
+    const uint8_t *__restrict__ codes_src, uint8_t *__restrict__ codes_dst,
+    int64_t ld_c, const int2 *__restrict__ gh_src, int2 *__restrict__ gh_dst,
+    const int32_t *__restrict__ rid_src, int32_t *__restrict__ rid_dst,
+    const PartParent *__restrict__ parents, const PartTile *__restrict__ tiles,
+    const int64_t *__restrict__ tile_left_off,
+    const int64_t *__restrict__ parent_nleft, int32_t F_sel) {
+  __shared__ uint32_t tmp[kPartBlock / 64];
+  const PartTile t = tiles[blockIdx.x];
+  const PartParent P = parents[t.parent];
+  const int64_t r0 = t.row0, r1 = t.row0 + t.rows;
+  const int64_t loff = tile_left_off[blockIdx.x];
+  const int64_t nl = parent_nleft[t.parent];
+  // Destinations of this tile's first left / right row.
+  int64_t lbase = P.start + loff;
+  int64_t rbase = P.start + nl + ((r0 - P.start) - loff);
+  const uint8_t *scol = codes_src + (int64_t)P.fpos * ld_c;
+  const int64_t dbeg = r0 >> 2, dend = (r1 + 3) >> 2;
+  for (int64_t pass = dbeg; pass < dend; pass += kPartBlock) {
+    const int64_t d = pass + threadIdx.x;
+    const int64_t row = d << 2;
+    uint32_t lmask = 0, vmask = 0;
+    if (d < dend) {
+      const uint32_t w = *reinterpret_cast<const uint32_t *>(scol + row);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const bool in = (row + k >= r0) && (row + k < r1);
+        vmask |= (in ? 1u : 0u) << k;
+        lmask |= ((in && ((w >> (8 * k)) & 255u) <= (uint32_t)P.bin) ? 1u : 0u) << k;
+      }
+    }
+    const uint32_t lc = __builtin_popcount(lmask);
+    const uint32_t vc = __builtin_popcount(vmask);
+    uint32_t ltot, vtot;
+    const uint32_t lpre = block_excl_scan<kPartBlock>(lc, tmp, ltot);
+    const uint32_t vpre = block_excl_scan<kPartBlock>(vc, tmp, vtot);
+    int64_t dst[4];
+    uint32_t li = 0, ri = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const bool v = (vmask >> k) & 1u;
+      const bool l = (lmask >> k) & 1u;
+      dst[k] = !v ? -1 : (l ? lbase + lpre + li : rbase + (vpre - lpre) + ri);
+      li += l ? 1u : 0u;
+      ri += (v && !l) ? 1u : 0u;
+    }
+    if (vmask) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (dst[k] >= 0) {
+          gh_dst[dst[k]] = gh_src[row + k];
+          rid_dst[dst[k]] = rid_src[row + k];
+        }
+      }
+      for (int32_t f = 0; f < F_sel; ++f) {
+        const uint32_t w = *reinterpret_cast<const uint32_t *>(codes_src + (int64_t)f * ld_c + row);
+        uint8_t *dcol = codes_dst + (int64_t)f * ld_c;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (dst[k] >= 0) dcol[dst[k]] = (uint8_t)(w >> (8 * k));
+      }
+    }
+    lbase += ltot;
+    rbase += vtot - ltot;
+  }
+}
+
+hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
+                               uint8_t *codes_dst, int64_t ld_c,
+                               const int2 *gh_src, int2 *gh_dst,
+                               const int32_t *rid_src, int32_t *rid_dst,
+                               const PartParent *parents,
+                               const PartTile *tiles, int32_t n_tiles,
+                               const int64_t *tile_left_off,
+                               const int64_t *parent_nleft, int32_t F_sel) {
+  if (n_tiles <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_part_scatter, dim3((unsigned)n_tiles), dim3(kPartBlock),
+                     0, st, codes_src, codes_dst, ld_c, gh_src, gh_dst, rid_src,
+                     rid_dst, parents, tiles, tile_left_off, parent_nleft,
+                     F_sel);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Split search (est:598-621, est:775-801).  One wave per (node, feature):
+// lane l holds bins 4l..4l+3; an exact int64 prefix scan gives GL, HL for
+// every bin; the gain is the reference's expression in fp64 without
+// contraction; the wave keeps the largest gain, the lowest bin on ties.
+// A non-small child's histogram is parent minus sibling, stored for its own
+// children.
+// ---------------------------------------------------------------------------
+#pragma clang fp contract(off)
+__global__ __launch_bounds__(256) void k_split(
+    const SplitTask *__restrict__ tasks, int32_t n_tasks,
+    const NodeSeg *__restrict__ segs, unsigned long long *__restrict__ pool,
+    int64_t node_stride, const int32_t *__restrict__ nb_sel, int32_t F_sel,
+    SplitParams P, SplitCand *__restrict__ cand, long long *__restrict__ totals) {
+  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = lane_id();
+  if (gw >= (int64_t)n_tasks * F_sel) return;
+  const int ti = (int)(gw / F_sel), fpos = (int)(gw % F_sel);
+  const SplitTask t = tasks[ti];
+  const NodeSeg s = segs[t.node];
+  if (!s.valid) return;
+  long long *hn = reinterpret_cast<long long *>(pool) + (int64_t)t.node * node_stride +
+                  (int64_t)fpos * kHistPerFeat + lane * 8;
+  long long g[4], h[4];
+  if (t.parent >= 0 && !s.is_small) {
+    const long long *hp = reinterpret_cast<const long long *>(pool) +
+                          (int64_t)t.parent * node_stride + (int64_t)fpos * kHistPerFeat + lane * 8;
+    const long long *hs = reinterpret_cast<const long long *>(pool) +
+                          (int64_t)t.sibling * node_stride + (int64_t)fpos * kHistPerFeat + lane * 8;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      g[k] = hp[2 * k] - hs[2 * k];
+      h[k] = hp[2 * k + 1] - hs[2 * k + 1];
+      hn[2 * k] = g[k];
+      hn[2 * k + 1] = h[k];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      g[k] = hn[2 * k];
+      h[k] = hn[2 * k + 1];
+    }
+  }
+  const long long lg = g[0] + g[1] + g[2] + g[3];
+  const long long lhs = h[0] + h[1] + h[2] + h[3];
+  const long long ig = wave_incl_scan<long long>(lg);
+  const long long ih = wave_incl_scan<long long>(lhs);
+  const long long Gt = __shfl(ig, 63, 64);
+  const long long Ht = __shfl(ih, 63, 64);
+  if (fpos == 0 && lane == 0) {
+    totals[2 * (int64_t)t.node] = Gt;
+    totals[2 * (int64_t)t.node + 1] = Ht;
+  }
+  const double Gtd = (double)Gt * P.g_scale;
+  const double Htd = (double)Ht * P.h_scale;
+  const bool can = s.count >= P.min_samples_leaf && Htd >= P.min_child_weight &&
+                   (t.parent < 0 || t.depth < P.max_depth);
+  const int32_t nb = nb_sel[fpos];
+  double best = -1e9;
+  int32_t bb = -1;
+  if (can && nb >= 2) {
+    const double lam = P.reg_lambda, mcw = P.min_child_weight;
+    const double parent_term = Gtd * Gtd / (Htd + lam);
+    long long GLq = ig - lg, HLq = ih - lhs;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      GLq += g[k];
+      HLq += h[k];
+      const int32_t b = lane * 4 + k;
+      if (b <= nb - 2) {
+        const double GL = (double)GLq * P.g_scale;
+        const double HL = (double)HLq * P.h_scale;
+        const double GR = (double)(Gt - GLq) * P.g_scale;
+        const double HR = (double)(Ht - HLq) * P.h_scale;
+        if (!(HL < mcw || HR < mcw)) {
+          const double gain = (GL * GL / (HL + lam) + GR * GR / (HR + lam)) - parent_term;
+          if (gain > best) {
+            best = gain;
+            bb = b;
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const double og = __shfl_xor(best, o, 64);
+    const int32_t ob = __shfl_xor(bb, o, 64);
+    const bool take = ob >= 0 && (bb < 0 || og > best || (og == best && ob < bb));
+    best = take ? og : best;
+    bb = take ? ob : bb;
+  }
+  if (lane == 0) {
+    SplitCand c;
+    c.gain = best;
+    c.bin = bb;
+    c.pad = 0;
+    cand[(int64_t)t.node * F_sel + fpos] = c;
+  }
+}
+#pragma clang fp contract(on)
+
+hipError_t launch_split(hipStream_t st, const SplitTask *tasks, int32_t n_tasks,
+                        const NodeSeg *segs, unsigned long long *pool,
+                        int64_t node_stride, const int32_t *nb_sel,
+                        int32_t F_sel, SplitParams p, SplitCand *cand,
+                        long long *totals) {
+  const int64_t waves = (int64_t)n_tasks * F_sel;
+  if (waves <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_split, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st,
+                     tasks, n_tasks, segs, pool, node_stride, nb_sel, F_sel, p,
+                     cand, totals);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// F update and training loss (est:2896-2897, est:2905 -> est:2320-2325).
+// ---------------------------------------------------------------------------
+constexpr int kUpdBlock = 256;
+
+int update_F_blocks(int64_t n) {
+  int64_t b = (n + kUpdBlock * 8 - 1) / (kUpdBlock * 8);
+  if (b < 1) b = 1;
+  if (b > 4096) b = 4096;
+  return (int)b;
+}
+
+__device__ __forceinline__ int32_t traverse(const TreeNodeDev *__restrict__ tree,
+                                            const uint8_t *__restrict__ codes,
+                                            int64_t ld, int64_t i) {
+  int32_t node = 0;
+  TreeNodeDev nd = tree[0];
+  while (nd.feature >= 0) {
+    const int32_t c = codes[(int64_t)nd.feature * ld + i];
+    node = (c <= nd.threshold) ? nd.left : nd.right;
+    nd = tree[node];
+  }
+  return node;
+}
+
+#pragma clang fp contract(off)
+__global__ __launch_bounds__(kUpdBlock) void k_update_F(
+    const uint8_t *__restrict__ codes, int64_t ld, int64_t n,
+    const TreeNodeDev *__restrict__ tree, double lr, double *__restrict__ F,
+    const uint8_t *__restrict__ y, double *__restrict__ partials) {
+  __shared__ double red[kUpdBlock / 64];
+  double acc = 0.0;
+  for (int64_t i = (int64_t)blockIdx.x * kUpdBlock + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kUpdBlock) {
+    const int32_t leaf = traverse(tree, codes, ld, i);
+    const double f = __dadd_rn(F[i], __dmul_rn(lr, tree[leaf].value));
+    F[i] = f;
+    const double fc = fmin(fmax(f, -500.0), 500.0);
+    double p = 1.0 / (1.0 + exp(-fc));
+    p = fmin(fmax(p, 1e-15), 1.0 - 1e-15);
+    acc += y[i] ? log(p) : log(1.0 - p);
+  }
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if (lane_id() == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double s = 0.0;
+    for (int w = 0; w < kUpdBlock / 64; ++w) s += red[w];
+    partials[blockIdx.x] = s;
+  }
+}
+#pragma clang fp contract(on)
+
+hipError_t launch_update_F(hipStream_t st, const uint8_t *codes, int64_t ld,
+                           int64_t n, const TreeNodeDev *tree,
+                           int32_t node_count, double lr, double *F,
+                           const uint8_t *y, double *loss_partials,
+                           int32_t n_blocks) {
+  (void)node_count;
+  hipLaunchKernelGGL(k_update_F, dim3((unsigned)n_blocks), dim3(kUpdBlock), 0, st,
+                     codes, ld, n, tree, lr, F, y, loss_partials);
+  return hipGetLastError();
+}
+
+// Fixed-order sum of the per-block partials (deterministic).
+__global__ __launch_bounds__(256) void k_sum_partials(const double *__restrict__ p,
+                                                      int32_t count,
+                                                      double *__restrict__ out) {
+  __shared__ double red[4];
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < count; i += 256) acc += p[i];
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if (lane_id() == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) *out = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+hipError_t launch_sum_partials(hipStream_t st, const double *partials,
+                               int32_t count, double *out) {
+  hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(256), 0, st, partials, count,
+                     out);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Prediction (est:843-861 one tree; est:863-884 ensemble).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_predict_tree(
+    const uint8_t *__restrict__ codes, int64_t ld, int64_t n,
+    const TreeNodeDev *__restrict__ tree, double *__restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = tree[traverse(tree, codes, ld, i)].value;
+}
+
+hipError_t launch_predict_tree(hipStream_t st, const uint8_t *codes,
+                               int64_t ld, int64_t n, const TreeNodeDev *tree,
+                               int32_t node_count, double *out) {
+  (void)node_count;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_predict_tree, dim3((unsigned)((n + 255) / 256)), dim3(256),
+                     0, st, codes, ld, n, tree, out);
+  return hipGetLastError();
+}
+
+#pragma clang fp contract(off)
+__global__ __launch_bounds__(256) void k_predict(
+    const uint8_t *__restrict__ codes, int64_t ld, int64_t n,
+    const TreeNodeDev *__restrict__ nodes, const int32_t *__restrict__ offsets,
+    int32_t n_trees, double lr, double *__restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  double F = 0.0;
+  for (int32_t t = 0; t < n_trees; ++t) {
+    const TreeNodeDev *tree = nodes + offsets[t];
+    F = __dadd_rn(F, __dmul_rn(lr, tree[traverse(tree, codes, ld, i)].value));
+  }
+  out[i] = F;
+}
+#pragma clang fp contract(on)
+
+hipError_t launch_predict(hipStream_t st, const uint8_t *codes, int64_t ld,
+                          int64_t n, const TreeNodeDev *nodes,
+                          const int32_t *offsets, int32_t n_trees, double lr,
+                          double *out) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_predict, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     st, codes, ld, n, nodes, offsets, n_trees, lr, out);
+  return hipGetLastError();
+}
+
+}  // namespace bsscl

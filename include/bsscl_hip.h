@@ -1,0 +1,209 @@
+/*
+ * bsscl_hip.h -- C ABI of the MI355X engine for BSSCL-GBM's histogram path.
+ *
+ * Plain C types only.  Every entry point returns BSSCL_OK (0) or an error
+ * code; bsscl_last_error() gives the calling thread's message for the last
+ * failure.  An engine owns device memory and one HIP stream on one GPU; use
+ * one engine per thread (or serialise calls), and create engines after any
+ * fork(), never before.
+ *
+ * Each entry point names the reference function it replaces
+ * (src/bsscl_gbm/estimator_v1_0_1.py, "est:" below).  The reference has no
+ * FFI: its seam is the Numba functions the estimator calls, with NumPy
+ * arrays.  The arrays here carry the same meaning, shapes and dtypes.
+ */
+#ifndef BSSCL_HIP_H
+#define BSSCL_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BSSCL_OK 0
+#define BSSCL_EINVAL 1   /* bad argument (ValueError in the Python layer) */
+#define BSSCL_ENOMEM 2   /* host or device allocation failed */
+#define BSSCL_EDEVICE 3  /* no GPU, or a HIP runtime call failed */
+#define BSSCL_EINTERNAL 4
+
+typedef struct bsscl_engine bsscl_engine;
+typedef struct bsscl_sampler bsscl_sampler;
+
+/* Message of the calling thread's last failing call ("" if none). */
+const char *bsscl_last_error(void);
+
+/* Number of visible HIP devices (0 without a GPU). */
+int bsscl_device_count(int32_t *out);
+
+/* Engine lifecycle.  No reference counterpart: the reference runs in-process
+ * Numba code with no device state. */
+int bsscl_engine_create(int32_t device, bsscl_engine **out);
+void bsscl_engine_destroy(bsscl_engine *eng);
+
+/*
+ * Binning.  Replaces bin_all_features_hybrid_numba / _standard_numba
+ * (est:155-226) together with the NaN handling of _bin_features
+ * (est:2144-2189): codes are the largest k in [0, nb-1] with e[k] <= v
+ * (0 below e[0], nb-1 at or above e[nb]); when any feature had NaN in
+ * training (nan_bin_id[j] >= 0 for some j), NaN inputs are binned as 0.0 and
+ * NaN-feature codes are shifted by +1 with NaN -> 0.
+ *   X          row-major n x F, float32 (x_is_f64 = 0) or float64
+ *   edges_2d   row-major F x edge_stride float64 (the reference's bin_edges)
+ *   bin_counts int32[F], nan_bin_id int32[F]
+ * The codes stay on the device as matrix `slot` (0 = training, 1 = scoring),
+ * stored feature-major as uint8.  Reference codes above 255 (possible only
+ * with n_bins = 256, for the top bin of a NaN feature) are stored as 255,
+ * which every split and every prediction treats identically.  When codes_out
+ * is not NULL the codes are also copied back row-major (n x F uint8).
+ */
+int bsscl_bin_features(bsscl_engine *eng, int32_t slot, const void *X,
+                       int32_t x_is_f64, int64_t n, int32_t F,
+                       const double *edges_2d, int32_t edge_stride,
+                       const int32_t *bin_counts, const int32_t *nan_bin_id,
+                       uint8_t *codes_out);
+
+/* Upload an already binned matrix: the reference's X_bin, row-major n x F of
+ * uint8 (codes_u16 = 0) or uint16 (codes_u16 = 1). */
+int bsscl_load_codes(bsscl_engine *eng, int32_t slot, const void *codes,
+                     int32_t codes_u16, int64_t n, int32_t F);
+
+/* Copy matrix `slot` back row-major (n x F uint8). */
+int bsscl_get_codes(bsscl_engine *eng, int32_t slot, uint8_t *codes_out);
+
+/*
+ * Tree builder.  Replaces _build_tree_leafwise (est:517-823) and the no-op
+ * post-prune that follows it (est:827-841, est:2452): same arguments, same
+ * 7-tuple.  Runs on training matrix 0.
+ *   grad, hess        float64[n] indexed by row id (n = rows of matrix 0)
+ *   sample_indices    int64[n_samples] row ids of the in-bag rows
+ *   feature_indices   int32[n_selected], ascending
+ *   out_*             arrays of length 2*max_leaves+2 (est:528-537);
+ *                     out_node_count receives node_count
+ * Gradient and hessian sums are accumulated in 64-bit fixed point, so the
+ * tree does not depend on the order of sample_indices.
+ */
+int bsscl_build_tree(bsscl_engine *eng, const double *grad, const double *hess,
+                     const int64_t *sample_indices, int64_t n_samples,
+                     const int32_t *feature_indices, int32_t n_selected,
+                     int32_t max_leaves, int32_t max_depth,
+                     int32_t min_samples_leaf, double min_child_weight,
+                     const int32_t *bin_counts, int32_t max_bins,
+                     double reg_lambda, double gamma, int32_t *out_features,
+                     int64_t *out_thresholds, double *out_values,
+                     int32_t *out_left, int32_t *out_right,
+                     int32_t *out_node_count, double *out_split_gains);
+
+/*
+ * Binary boosting loop state on matrix 0.  Replaces the set-up of
+ * _fit_binary (est:2825-2848): y int64[n] in {0,1}, per-class weights w0/w1
+ * (est:2570-2603), F initialised to base_score (est:2831-2834).
+ */
+int bsscl_boost_begin(bsscl_engine *eng, const int64_t *y, int64_t n,
+                      double w0, double w1, double base_score);
+
+/*
+ * One boosting round of _fit_binary (est:2849-2906): gradients and hessians
+ * from F (est:2861, est:2873-2874), the round's rows and features from the
+ * sampler (est:2886, est:2502-2517), the tree (est:2891), F += lr * tree(X)
+ * over all rows (est:2896-2897) and the training log-loss (est:2905,
+ * est:2320-2325).  Outputs as for bsscl_build_tree, plus out_train_loss.
+ */
+int bsscl_boost_round(bsscl_engine *eng, bsscl_sampler *sampler,
+                      int32_t max_leaves, int32_t max_depth,
+                      int32_t min_samples_leaf, double min_child_weight,
+                      const int32_t *bin_counts, int32_t max_bins,
+                      double reg_lambda, double gamma, double learning_rate,
+                      int32_t *out_features, int64_t *out_thresholds,
+                      double *out_values, int32_t *out_left,
+                      int32_t *out_right, int32_t *out_node_count,
+                      double *out_split_gains, double *out_train_loss);
+
+/* F of the boosting run (float64[n]). */
+int bsscl_boost_get_F(bsscl_engine *eng, double *F_out);
+
+/* Gradients and hessians of the current F (float64[n] each). */
+int bsscl_boost_grad_hess(bsscl_engine *eng, double *grad_out,
+                          double *hess_out);
+
+/*
+ * Ensemble prediction.  Replaces predict_all_trees_jit (est:863-884):
+ * out_F[i] = sum over trees t of learning_rate * value_t(leaf of row i),
+ * accumulated tree by tree from 0.0, on the rows of matrix `slot`.  The tree
+ * arrays are the packed arrays of _pack_tree_list (est:2192-2216).
+ */
+int bsscl_predict(bsscl_engine *eng, int32_t slot, const int16_t *features,
+                  const int64_t *thresholds, const double *values,
+                  const int32_t *left, const int32_t *right,
+                  const int32_t *offsets, int32_t n_trees,
+                  double learning_rate, double *out_F);
+
+/* One tree over the rows of matrix `slot`: predict_batch_jit (est:843-861). */
+int bsscl_predict_tree(bsscl_engine *eng, int32_t slot,
+                       const int32_t *features, const int64_t *thresholds,
+                       const double *values, const int32_t *left,
+                       const int32_t *right, int32_t node_count, double *out);
+
+/*
+ * One node's histogram and best split on matrix 0: the root histogram
+ * (est:581-596) and root split scan (est:598-621) for the given rows.
+ * out_G/out_H: float64[n_selected * 256] (feature-position major, bins past
+ * bin_counts are 0).  out_gain/out_feature/out_bin receive the best split
+ * (out_feature = -1 when none qualifies).  Any output may be NULL.
+ */
+int bsscl_node_split(bsscl_engine *eng, const double *grad, const double *hess,
+                     const int64_t *rows, int64_t m,
+                     const int32_t *feature_indices, int32_t n_selected,
+                     const int32_t *bin_counts, double min_child_weight,
+                     double reg_lambda, double *out_G, double *out_H,
+                     double *out_gain, int32_t *out_feature, int32_t *out_bin);
+
+/*
+ * Partition of a row set by one split on matrix 0: the reference's in-place
+ * two-pointer loop (est:662-674) moves rows with code <= bin to the front.
+ * Here the order is stable: out_rows[0:*out_n_left] are the left rows in
+ * input order, then the right rows in input order.
+ */
+int bsscl_partition(bsscl_engine *eng, const int64_t *rows, int64_t m,
+                    int32_t feature, int32_t bin, int64_t *out_rows,
+                    int64_t *out_n_left);
+
+/* Row/column bagging stream, bit-identical to NumPy RandomState
+ * (est:2502-2517).  key[624]/pos come from RandomState.get_state(). */
+int bsscl_rs_shuffle_i64(uint32_t *key, int32_t *pos, int64_t *data,
+                         int64_t n);
+int bsscl_rs_shuffle_i32(uint32_t *key, int32_t *pos, int32_t *data,
+                         int64_t n);
+int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
+                         int64_t n_sub, int32_t do_rows, int32_t n_features,
+                         int32_t f_sub, int32_t do_feats, int32_t n_rounds,
+                         int32_t lookahead, bsscl_sampler **out);
+/* Next round: ascending in-bag rows (int32[n_sub]) and features
+ * (int32[f_sub]); either output may be NULL. */
+int bsscl_sampler_next(bsscl_sampler *s, int32_t *rows_out,
+                       int32_t *feats_out);
+int bsscl_sampler_state(bsscl_sampler *s, uint32_t *key_out,
+                        int32_t *pos_out);
+void bsscl_sampler_destroy(bsscl_sampler *s);
+
+/*
+ * Timing of the engine's own kernels, taken with HIP events on the engine's
+ * stream while profiling is on.  No reference counterpart (the reference
+ * records only wall times, est:1904).  bsscl_engine_stats fills up to `cap`
+ * doubles in this order:
+ *   [0] histogram launches   [1] histogram ms (sum of launch durations)
+ *   [2] histogram rows x features  [3] histogram algorithmic bytes
+ *   [4] partition launches   [5] partition ms
+ *   [6] split launches       [7] split ms
+ *   [8] trees built          [9] nodes expanded
+ * and returns the number written in *n_out.
+ */
+int bsscl_engine_set_profiling(bsscl_engine *eng, int32_t on);
+int bsscl_engine_stats(bsscl_engine *eng, double *out, int32_t cap,
+                       int32_t *n_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BSSCL_HIP_H */

@@ -1,0 +1,402 @@
+"""CPU restatement of the reference's binary histogram-GBM path.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()``
+and by the ``cpu_baseline`` leg of bench.py, always as the checker or the
+timed baseline.  The product package never imports it.
+
+Host logic follows ``src/bsscl_gbm/estimator_v1_0_1.py`` ("est:" below) with
+the same NumPy calls in the same order; the hot loops call ``oracle.c``
+through ctypes.  ``OracleGBM`` reproduces ``HybridHistGBMNumbaV1_0_1`` for
+``objective='auto'`` with two classes, ``grow_policy='leaf'``,
+``sampling_method='uniform'``, ``boosting_type='gbdt'``, numeric features.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
+_lib = None
+
+
+def build():
+    """Compile oracle.c with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        i32, i64, f64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_double
+        L.oracle_bin_features.argtypes = [P, ctypes.c_int, i64, i32, P, i32, P,
+                                          ctypes.c_int, P]
+        L.oracle_build_tree_leafwise.argtypes = [
+            P, ctypes.c_int, i64, i32, P, P, P, i64, P, i32, i32, i32, i32,
+            f64, P, i32, f64, f64, P, P, P, P, P, P, P, P, P]
+        L.oracle_predict_tree.argtypes = [P, ctypes.c_int, i64, i32, P, P, P, P,
+                                          P, P]
+        L.oracle_predict_all_trees.argtypes = [P, ctypes.c_int, i64, i32, P, P,
+                                               P, P, P, P, i32, f64, P]
+        L.oracle_post_prune.argtypes = [P, P, P, P, f64, i32]
+        for name in ("oracle_bin_features", "oracle_build_tree_leafwise",
+                     "oracle_predict_tree", "oracle_predict_all_trees"):
+            getattr(L, name).restype = ctypes.c_int
+        L.oracle_post_prune.restype = None
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# --------------------------------------------------------------------------
+# Binning (est:2073-2189)
+# --------------------------------------------------------------------------
+
+def build_bin_edges(X, n_bins):
+    """``_build_bin_edges`` without categorical or weighted-quantile branches
+    (est:2073-2141).  Returns (edges_2d, bin_counts, nan_bin_id)."""
+    edges = []
+    F = X.shape[1]
+    bin_counts = np.zeros(F, dtype=np.int32)
+    nan_bin_id = np.full(F, -1, dtype=np.int32)
+    for j in range(F):
+        col = X[:, j]
+        has_nan = np.any(np.isnan(col))
+        if has_nan:
+            nan_bin_id[j] = 0
+            col_clean = col[~np.isnan(col)]
+            if len(col_clean) == 0:
+                edges.append(np.array([0.0, 1.0]))
+                bin_counts[j] = 1
+                continue
+        else:
+            col_clean = col
+        n_unique = len(np.unique(col_clean))
+        max_numeric = n_bins - (1 if has_nan else 0)
+        if n_unique <= max_numeric:
+            e = np.sort(np.unique(col_clean))
+        else:
+            q = np.linspace(0, 1, min(max_numeric + 1, n_unique))
+            e = np.unique(np.percentile(col_clean, q * 100))
+        e = np.append(e, e[-1] + 1e-8)
+        edges.append(e)
+        bin_counts[j] = len(e) - 1 + (1 if has_nan else 0)
+    max_b = int(np.max(bin_counts)) + 1
+    edges_2d = np.zeros((F, max_b), dtype=np.float64)
+    for j, e in enumerate(edges):
+        edges_2d[j, :len(e)] = e
+        edges_2d[j, len(e):] = e[-1]
+    return edges_2d, bin_counts, nan_bin_id
+
+
+def bin_features(X, edges_2d, bin_counts, nan_bin_id, strategy):
+    """``_bin_features`` (est:2144-2189): NaN placeholder 0.0, kernel codes,
+    +1 shift of NaN-feature codes in the code dtype, NaN -> 0."""
+    max_bins = int(np.max(bin_counts))
+    dtype = np.uint8 if max_bins <= 255 else np.uint16
+    has_any_nan = nan_bin_id is not None and np.any(nan_bin_id >= 0)
+    Xs = X
+    nan_mask = None
+    if has_any_nan:
+        nan_mask = np.isnan(X)
+        Xs = X.copy()
+        Xs[nan_mask] = 0.0
+    Xs = np.ascontiguousarray(Xs)
+    if Xs.dtype not in (np.float32, np.float64):
+        Xs = Xs.astype(np.float64)
+    n, F = Xs.shape
+    out16 = np.empty((n, F), dtype=np.uint16)
+    e = np.ascontiguousarray(edges_2d, dtype=np.float64)
+    bc = np.ascontiguousarray(bin_counts, dtype=np.int32)
+    lib().oracle_bin_features(_p(Xs), int(Xs.dtype == np.float64), n, F, _p(e),
+                              e.shape[1], _p(bc), int(strategy == "hybrid"),
+                              _p(out16))
+    codes = out16.astype(dtype)
+    if has_any_nan:
+        for j in range(F):
+            if nan_bin_id[j] >= 0:
+                codes[:, j] += dtype(1)
+                codes[nan_mask[:, j], j] = 0
+    return codes
+
+
+# --------------------------------------------------------------------------
+# Tree builder / prediction wrappers
+# --------------------------------------------------------------------------
+
+def build_tree(X_bin, grad, hess, sample_indices, feature_indices, max_leaves,
+               max_depth, min_samples_leaf, min_child_weight, bin_counts,
+               max_bins, reg_lambda, gamma, trace=False):
+    """``_build_tree_leafwise`` (est:517-823); returns the reference 7-tuple,
+    plus (partition counts per split, number of pops) when ``trace``."""
+    X_bin = np.ascontiguousarray(X_bin)
+    u16 = int(X_bin.dtype == np.uint16)
+    assert X_bin.dtype in (np.uint8, np.uint16)
+    n, F = X_bin.shape
+    grad = np.ascontiguousarray(grad, dtype=np.float64)
+    hess = np.ascontiguousarray(hess, dtype=np.float64)
+    si = np.ascontiguousarray(sample_indices, dtype=np.int64)
+    fi = np.ascontiguousarray(feature_indices, dtype=np.int32)
+    bc = np.ascontiguousarray(bin_counts, dtype=np.int32)
+    M = 2 * max_leaves + 2
+    tf = np.empty(M, np.int32)
+    tt = np.empty(M, np.int64)
+    tv = np.empty(M, np.float64)
+    tl = np.empty(M, np.int32)
+    tr = np.empty(M, np.int32)
+    sg = np.empty(M, np.float64)
+    nc = np.zeros(1, np.int32)
+    tc = np.zeros(2 * max_leaves + 2, np.int64)
+    tp = np.zeros(1, np.int32)
+    rc = lib().oracle_build_tree_leafwise(
+        _p(X_bin), u16, n, F, _p(grad), _p(hess), _p(si), len(si), _p(fi),
+        len(fi), int(max_leaves), int(max_depth), int(min_samples_leaf),
+        float(min_child_weight), _p(bc), int(max_bins), float(reg_lambda),
+        float(gamma), _p(tf), _p(tt), _p(tv), _p(tl), _p(tr), _p(nc), _p(sg),
+        _p(tc), _p(tp))
+    if rc != 0:
+        raise MemoryError("oracle tree builder allocation failed")
+    lib().oracle_post_prune(_p(tf), _p(tl), _p(tr), _p(sg), float(gamma),
+                            int(nc[0]))
+    tree = (tf, tt, tv, tl, tr, int(nc[0]), sg)
+    if trace:
+        n_split = int(np.sum(tf[:nc[0]] >= 0))
+        return tree, tc[:2 * n_split].reshape(-1, 2), int(tp[0])
+    return tree
+
+
+def predict_tree(X_bin, tree):
+    X_bin = np.ascontiguousarray(X_bin)
+    tf, tt, tv, tl, tr, nc, _ = tree
+    n, F = X_bin.shape
+    out = np.empty(n, np.float64)
+    a = [np.ascontiguousarray(x[:nc]) for x in (tf, tt, tv, tl, tr)]
+    lib().oracle_predict_tree(_p(X_bin), int(X_bin.dtype == np.uint16), n, F,
+                              *[_p(x) for x in a], _p(out))
+    return out
+
+
+def pack_trees(trees):
+    """``_pack_tree_list`` (est:2192-2216)."""
+    total = sum(t[5] for t in trees)
+    features = np.empty(total, np.int16)
+    thresholds = np.empty(total, np.int64)
+    values = np.empty(total, np.float64)
+    left = np.empty(total, np.int32)
+    right = np.empty(total, np.int32)
+    offsets = np.empty(len(trees) + 1, np.int32)
+    off = 0
+    for t, (tf, tt, tv, tl, tr, nc, _) in enumerate(trees):
+        offsets[t] = off
+        features[off:off + nc] = tf[:nc]
+        thresholds[off:off + nc] = tt[:nc]
+        values[off:off + nc] = tv[:nc]
+        left[off:off + nc] = tl[:nc]
+        right[off:off + nc] = tr[:nc]
+        off += nc
+    offsets[len(trees)] = off
+    return dict(features=features, thresholds=thresholds, values=values,
+                left=left, right=right, offsets=offsets)
+
+
+def predict_all_trees(X_bin, packed, n_trees, lr):
+    X_bin = np.ascontiguousarray(X_bin)
+    n, F = X_bin.shape
+    out = np.empty(n, np.float64)
+    lib().oracle_predict_all_trees(
+        _p(X_bin), int(X_bin.dtype == np.uint16), n, F,
+        _p(packed["features"]), _p(packed["thresholds"]),
+        _p(packed["values"]), _p(packed["left"]), _p(packed["right"]),
+        _p(packed["offsets"]), int(n_trees), float(lr), _p(out))
+    return out
+
+
+# --------------------------------------------------------------------------
+# Estimator restatement
+# --------------------------------------------------------------------------
+
+class OracleGBM:
+    """Binary-classification restatement of ``HybridHistGBMNumbaV1_0_1``
+    (est:1820-1923 constructor defaults, est:3070-3271 fit,
+    est:3274-3336 predict_proba)."""
+
+    def __init__(self, n_estimators="auto", max_depth="auto",
+                 learning_rate="auto", n_bins="auto", reg_lambda=1.0,
+                 min_samples_leaf=5, min_child_weight="auto", gamma="auto",
+                 subsample="auto", colsample_bytree="auto",
+                 class_weight="balanced_sqrt", max_leaves=31,
+                 binning_strategy="auto", random_state=None):
+        self.binning_strategy_init = binning_strategy
+        self.n_estimators_init = n_estimators
+        self.max_depth_init = max_depth
+        self.learning_rate_init = learning_rate
+        self.n_bins_init = n_bins
+        self.reg_lambda = reg_lambda
+        self.min_samples_leaf = min_samples_leaf
+        self.min_child_weight_init = min_child_weight
+        self.gamma_init = gamma
+        self.subsample_init = subsample
+        self.colsample_init = colsample_bytree
+        self.class_weight = class_weight
+        self.max_leaves = max_leaves
+        self.random_state = random_state
+        self.n_estimators = 100 if n_estimators == "auto" else n_estimators
+        self.max_depth = 5 if max_depth == "auto" else max_depth
+        self.learning_rate = 0.1 if learning_rate == "auto" else learning_rate
+        self.n_bins = 256 if n_bins == "auto" else n_bins
+        self.min_child_weight = 1.0 if min_child_weight == "auto" else min_child_weight
+        self.gamma = 0.0 if gamma == "auto" else gamma
+        self.subsample = 0.8 if subsample == "auto" else subsample
+        self.colsample_bytree = 0.8 if colsample_bytree == "auto" else colsample_bytree
+        self.trees = []
+        self.train_loss_history_ = []
+
+    def _adaptive(self, X):
+        """est:1925-2029 (K = 2)."""
+        n, p = X.shape
+        K = 2
+        if self.binning_strategy_init == "auto":
+            self.binning_strategy = "hybrid" if (n > 20000 or p > 40) else "standard"
+        else:
+            self.binning_strategy = self.binning_strategy_init
+        if self.max_depth_init == "auto":
+            self.max_depth = min(6, max(3, int(np.log2(max(n // 10, 8)))))
+        if self.learning_rate_init == "auto":
+            # The reference computes np.std(X) unconditionally; its value is
+            # only read when n <= 20000.
+            data_std = np.std(X) if n <= 20000 else 0.0
+            if n > 20000:
+                self.learning_rate = 0.08
+            elif data_std > 2.0:
+                self.learning_rate = 0.10
+            elif data_std > 1.5:
+                self.learning_rate = 0.12
+            elif data_std > 1.0:
+                self.learning_rate = 0.15
+            elif data_std > 0.5:
+                self.learning_rate = 0.18
+            else:
+                self.learning_rate = 0.20
+        if self.n_bins_init == "auto":
+            self.n_bins = min(256, p * 8 + 32)
+        if self.n_estimators_init == "auto":
+            self.n_estimators = 150 if K <= 2 else self.n_estimators
+        if self.gamma_init == "auto":
+            self.gamma = 0.0
+        if self.min_child_weight_init == "auto":
+            self.min_child_weight = 3.0 if n > 20000 else (2.0 if n > 5000 else 1.0)
+        if self.subsample_init == "auto":
+            self.subsample = 0.5 if n > 1000000 else (0.75 if n > 20000 else 0.8)
+        if n > 1000000:
+            self.reg_lambda = max(self.reg_lambda, 5.0)
+        if self.colsample_init == "auto":
+            self.colsample_bytree = 0.7 if p > 40 else 0.8
+        self.max_leaves = 63 if n > 10000 else (15 if n < 2000 else 31)
+
+    def _class_weights(self, y):
+        """est:2570-2603 (no scale_pos_weight)."""
+        n = len(y)
+        if self.class_weight not in ("balanced", "balanced_sqrt"):
+            return np.ones(n, dtype=np.float64)
+        w = np.ones(n, dtype=np.float64)
+        for k in range(2):
+            n_k = np.sum(y == k)
+            w_k = n / (2 * max(n_k, 1))
+            if self.class_weight == "balanced_sqrt":
+                w_k = w_k ** 0.35
+            w[y == k] = w_k
+        return w
+
+    def fit(self, X, y, max_rounds=None, round_callback=None):
+        """est:3070-3271 then est:2825-2944.  ``max_rounds`` stops the
+        boosting loop early (used to time a bounded CPU sample);
+        ``round_callback(m, grad, hess, sample_idx, feat_idx, tree)`` sees
+        each round's tree-builder inputs and output."""
+        self.classes_ = np.unique(y)
+        assert len(self.classes_) == 2, "oracle covers binary classification"
+        label_map = {c: i for i, c in enumerate(self.classes_)}
+        y = np.array([label_map[v] for v in y], dtype=np.int64)
+        self.trees = []
+        self.train_loss_history_ = []
+        self.n_features_in_ = X.shape[1]
+        rng = np.random.RandomState(self.random_state)
+        if not np.issubdtype(X.dtype, np.floating) or X.dtype == np.float16:
+            X = X.astype(np.float64)
+        self._adaptive(X)
+        self.bin_edges, self.feature_bin_counts, self._nan_bin_id = \
+            build_bin_edges(X, self.n_bins)
+        self._max_bins = int(np.max(self.feature_bin_counts))
+        X_bin = bin_features(X, self.bin_edges, self.feature_bin_counts,
+                             self._nan_bin_id, self.binning_strategy)
+        self.X_bin_ = X_bin
+
+        n = len(y)
+        F_cnt = X_bin.shape[1]
+        w_init = self._class_weights(y)
+        p0 = np.clip(np.average(y, weights=w_init), 1e-7, 1.0 - 1e-7)
+        self.base_score_ = np.log(p0 / (1.0 - p0))
+        F = np.full(n, self.base_score_)
+        n_sub = max(1, int(n * self.subsample))
+        f_sub = max(1, int(F_cnt * self.colsample_bytree))
+        w = self._class_weights(y)
+        all_rows = np.arange(n, dtype=np.int64)
+        all_feats = np.arange(F_cnt, dtype=np.int32)
+        grad = np.zeros(n, dtype=np.float64)
+        hess = np.zeros(n, dtype=np.float64)
+        rounds = self.n_estimators if max_rounds is None else min(max_rounds, self.n_estimators)
+        import time as _time
+        self.round_times_ = [_time.perf_counter()]
+        for m in range(rounds):
+            p = 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
+            grad[:] = w * (p - y)
+            hess[:] = w * p * (1.0 - p)
+            # est:2502-2517
+            if self.subsample < 1.0:
+                rng.shuffle(all_rows)
+                sample_idx = all_rows[:n_sub].copy()
+            else:
+                sample_idx = all_rows.copy()
+            if self.colsample_bytree < 1.0:
+                rng.shuffle(all_feats)
+                feat_idx = np.sort(all_feats[:f_sub]).copy()
+            else:
+                feat_idx = all_feats.copy()
+            tree = build_tree(X_bin, grad, hess, sample_idx, feat_idx,
+                              self.max_leaves, self.max_depth,
+                              self.min_samples_leaf, self.min_child_weight,
+                              self.feature_bin_counts, self._max_bins,
+                              self.reg_lambda, self.gamma)
+            if round_callback is not None:
+                round_callback(m, grad, hess, sample_idx, feat_idx, tree)
+            self.trees.append(tree)
+            F += self.learning_rate * predict_tree(X_bin, tree)
+            pc = np.clip(1.0 / (1.0 + np.exp(-np.clip(F, -500, 500))), 1e-15, 1 - 1e-15)
+            self.train_loss_history_.append(-np.mean(y * np.log(pc) + (1 - y) * np.log(1 - pc)))
+            self.round_times_.append(_time.perf_counter())
+        self.F_train_ = F
+        self._packed = pack_trees(self.trees)
+        return self
+
+    def predict_proba(self, X):
+        """est:3274-3336."""
+        if not np.issubdtype(X.dtype, np.floating) or X.dtype == np.float16:
+            X = X.astype(np.float64)
+        X_bin = bin_features(X, self.bin_edges, self.feature_bin_counts,
+                             self._nan_bin_id, self.binning_strategy)
+        F = predict_all_trees(X_bin, self._packed, len(self.trees),
+                              self.learning_rate) + self.base_score_
+        proba = 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
+        return np.column_stack([1 - proba, proba])
+
+    def predict(self, X):
+        return self.classes_[(self.predict_proba(X)[:, 1] > 0.5).astype(int)]

@@ -1,0 +1,132 @@
+"""Host-side behaviour of the drop-in estimator and the C ABI library that
+needs no GPU: argument errors (tests/test_fault_injection.py of the
+reference), the parameter surface, the bagging stream, and the library's
+exported symbols."""
+import ctypes
+import os
+import pickle
+import re
+
+import numpy as np
+import pytest
+
+from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+from bsscl_gbm import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_every_header_symbol():
+    header = open(os.path.join(ROOT, "include", "bsscl_hip.h")).read()
+    names = set(re.findall(r"\b(bsscl_[A-Za-z0-9_]+)\s*\(", header))
+    assert len(names) >= 20
+    lib = ctypes.CDLL(_native.library_path())
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, missing
+    # The Python binding declares every exported entry point.
+    assert names == set(_native._SIGS), names ^ set(_native._SIGS)
+
+
+def test_invalid_hyperparameters_raise_value_error():
+    X = np.random.randn(100, 5)
+    y = np.random.randint(0, 2, 100)
+    with pytest.raises(ValueError):
+        HybridHistGBMNumbaV1_0_1(max_depth=-5, verbose=False).fit(X, y)
+    with pytest.raises(ValueError):
+        HybridHistGBMNumbaV1_0_1(learning_rate=-0.1, verbose=False).fit(X, y)
+    with pytest.raises(ValueError):
+        HybridHistGBMNumbaV1_0_1(n_estimators=0, verbose=False).fit(X, y)
+
+
+def test_mismatched_rows_raise_value_error():
+    with pytest.raises(ValueError):
+        HybridHistGBMNumbaV1_0_1(verbose=False).fit(np.random.randn(100, 5),
+                                                    np.random.randint(0, 2, 99))
+
+
+def test_unfitted_predict_raises_value_error():
+    with pytest.raises(ValueError):
+        HybridHistGBMNumbaV1_0_1().predict(np.random.randn(10, 5))
+
+
+@pytest.mark.parametrize("kw", [dict(objective="regression"), dict(grow_policy="level"),
+                                dict(sampling_method="goss"), dict(boosting_type="dart"),
+                                dict(categorical_features=[0]),
+                                dict(monotone_constraints=[1, 0, 0, 0, 0])])
+def test_modes_outside_the_engine_raise(kw):
+    X = np.random.randn(200, 5)
+    y = np.random.randint(0, 2, 200)
+    with pytest.raises(NotImplementedError):
+        HybridHistGBMNumbaV1_0_1(verbose=False, **kw).fit(X, y)
+
+
+def test_multiclass_raises():
+    X = np.random.randn(300, 5)
+    y = np.arange(300) % 3
+    with pytest.raises(NotImplementedError):
+        HybridHistGBMNumbaV1_0_1(verbose=False).fit(X, y)
+
+
+def test_params_surface_and_pickle():
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=7, max_depth=3, random_state=1)
+    p = m.get_params()
+    assert p["n_estimators"] == 7 and p["max_depth"] == 3 and p["random_state"] == 1
+    assert m.set_params(reg_lambda=2.0) is m and m.reg_lambda == 2.0
+    assert "n_estimators=7" in repr(m)
+    m2 = pickle.loads(pickle.dumps(m))
+    assert m2.get_params() == m.get_params()
+
+
+@pytest.mark.parametrize("dtype", [np.int64, np.int32])
+@pytest.mark.parametrize("n", [0, 1, 2, 5, 1000, 65537])
+def test_native_shuffle_matches_randomstate(dtype, n):
+    for seed in (0, 42, 2**32 - 1):
+        rng = np.random.RandomState(seed)
+        rng.randint(0, 10, size=3)
+        a = np.arange(n, dtype=dtype)
+        b = a.copy()
+        key, pos = _native.rs_shuffle(rng.get_state(), b)
+        rng.shuffle(a)
+        st = rng.get_state()
+        np.testing.assert_array_equal(a, b)
+        np.testing.assert_array_equal(st[1], key)
+        assert st[2] == pos
+
+
+@pytest.mark.parametrize("sub,col", [(0.75, 0.8), (1.0, 0.7), (0.5, 1.0), (1.0, 1.0)])
+def test_sampler_stream_matches_reference_calls(sub, col):
+    """The reference's est:2502-2517 call sequence on one RandomState."""
+    n, F, rounds = 20011, 28, 6
+    n_sub, f_sub = max(1, int(n * sub)), max(1, int(F * col))
+    rng = np.random.RandomState(9)
+    s = _native.Sampler(rng.get_state(), n, n_sub if sub < 1 else n, sub < 1, F,
+                        f_sub if col < 1 else F, col < 1, rounds)
+    all_rows = np.arange(n, dtype=np.int64)
+    all_feats = np.arange(F, dtype=np.int32)
+    for _ in range(rounds):
+        if sub < 1:
+            rng.shuffle(all_rows)
+            si = all_rows[:n_sub].copy()
+        else:
+            si = all_rows.copy()
+        if col < 1:
+            rng.shuffle(all_feats)
+            fi = np.sort(all_feats[:f_sub])
+        else:
+            fi = all_feats.copy()
+        r, f = s.next()
+        np.testing.assert_array_equal(r, np.sort(si))
+        np.testing.assert_array_equal(f, fi)
+    key, pos = s.state()
+    st = rng.get_state()
+    np.testing.assert_array_equal(key, st[1])
+    assert pos == st[2]
+    s.close()
+
+
+def test_sampler_rejects_bad_arguments():
+    st = np.random.RandomState(0).get_state()
+    with pytest.raises(ValueError):
+        _native.Sampler(st, 10, 11, True, 3, 2, True, 1)
+    with pytest.raises(ValueError):
+        _native.Sampler(st, 10, 5, False, 3, 2, True, 1)

@@ -1,0 +1,124 @@
+"""The reference's own behaviour tests that apply to the binary path
+(tests/test_bsscl_gbm_v101.py, test_reproducibility.py, test_regression.py,
+test_properties.py, test_serialization.py, test_fuzz.py, test_precision.py
+of the reference), run against the drop-in estimator on the GPU."""
+import pickle
+
+import numpy as np
+import pytest
+from sklearn.datasets import make_classification
+from sklearn.metrics import accuracy_score
+
+from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def bin_data():
+    return make_classification(n_samples=500, n_features=10, n_classes=2, random_state=42)
+
+
+def test_binary_classification(engine, bin_data):
+    X, y = bin_data
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=10, max_depth=3, random_state=42, verbose=False)
+    m.fit(X, y)
+    assert accuracy_score(y, m.predict(X)) > 0.8
+
+
+def test_imbalanced_balanced_sqrt(engine):
+    X, y = make_classification(n_samples=500, n_features=10, n_classes=2,
+                               weights=[0.99, 0.01], random_state=42)
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=50, max_depth=3, class_weight="balanced_sqrt",
+                                 random_state=42, verbose=False).fit(X, y)
+    assert len(m.predict(X)) == len(y)
+
+
+def test_nan_handling(engine, bin_data):
+    X, y = bin_data
+    Xn = X.copy()
+    Xn[0, 0] = np.nan
+    Xn[10, 5] = np.nan
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=10, max_depth=3, verbose=False).fit(Xn, y)
+    assert len(m.predict(Xn)) == len(y)
+    assert (m._nan_bin_id[[0, 5]] == 0).all()
+
+
+def test_early_stopping(engine, bin_data):
+    X, y = bin_data
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=100, max_depth=3, early_stopping_rounds=5,
+                                 verbose=False)
+    m.fit(X, y, eval_set=[(X, y)])
+    assert m.best_iteration_ > 0
+    assert len(m.val_loss_history_) >= m.best_iteration_ + 1
+
+
+def test_scale_pos_weight(engine, bin_data):
+    X, y = bin_data
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=10, max_depth=3, objective="binary",
+                                 scale_pos_weight=3.0, verbose=False).fit(X, y)
+    assert len(m.predict(X)) == len(y)
+
+
+def test_reproducibility_and_checksum(engine):
+    """tests/test_reproducibility.py and tests/test_regression.py."""
+    X = np.random.RandomState(42).randn(100, 5)
+    y = np.random.RandomState(42).randint(0, 2, size=100)
+    ref = None
+    for _ in range(20):
+        m = HybridHistGBMNumbaV1_0_1(n_estimators=5, max_depth=2, random_state=42, verbose=False)
+        m.fit(X, y)
+        p = m.predict_proba(X)
+        if ref is None:
+            ref = p
+        np.testing.assert_array_equal(p, ref)
+    np.testing.assert_allclose(np.sum(ref), 100.0, atol=1e-5)
+
+
+def test_properties(engine, bin_data):
+    X, y = bin_data
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=10, max_depth=3, verbose=False).fit(X, y)
+    p = m.predict_proba(X)
+    assert p.shape == (len(X), 2) and np.all(np.isfinite(p))
+    assert np.all((p >= 0) & (p <= 1))
+    np.testing.assert_allclose(p.sum(1), 1.0)
+    assert set(np.unique(m.predict(X))) <= set(np.unique(y))
+    # Single-row prediction (tests/test_coverage.py:72-86 of the reference).
+    assert m.predict_proba(X[:1]).shape == (1, 2)
+
+
+def test_serialization_roundtrip(engine, bin_data):
+    X, y = bin_data
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=10, max_depth=3, verbose=False).fit(X, y)
+    m2 = pickle.loads(pickle.dumps(m))
+    np.testing.assert_array_equal(m.predict_proba(X), m2.predict_proba(X))
+    import joblib, io
+    buf = io.BytesIO()
+    joblib.dump(m, buf)
+    buf.seek(0)
+    np.testing.assert_array_equal(m.predict(X), joblib.load(buf).predict(X))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16, np.int64, np.float64])
+def test_input_dtypes(engine, dtype, bin_data):
+    X, y = bin_data
+    Xc = (X * 10).astype(dtype)
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=5, max_depth=3, verbose=False).fit(Xc, y)
+    assert m.predict_proba(Xc).shape == (len(y), 2)
+
+
+def test_extreme_values(engine):
+    rng = np.random.RandomState(0)
+    X = rng.randn(300, 4)
+    X[0, 0], X[1, 1], X[2, 2] = 1e308, -1e308, np.inf
+    y = rng.randint(0, 2, 300)
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=5, max_depth=3, verbose=False).fit(X, y)
+    assert np.all(np.isfinite(m.predict_proba(X)))
+
+
+def test_feature_importances(engine, bin_data):
+    X, y = bin_data
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=10, max_depth=3, verbose=False).fit(X, y)
+    assert m.feature_importances_.shape == (10,)
+    np.testing.assert_allclose(m.feature_importances_.sum(), 1.0)
+    assert m.feature_split_counts_.sum() == sum(int((t[0][:t[5]] >= 0).sum()) for t in m.trees)

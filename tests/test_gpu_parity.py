@@ -1,0 +1,224 @@
+"""Parity of the HIP engine with the oracle, through the C ABI.
+
+Bars: bin codes and partitions bit-exact; histogram sums within
+|d| <= 1e-5 * max(|ref|, sum_bin |g|); splits identical except gain ties
+within 1e-7 relative (tests/treecmp.py); predictions within 1e-6.
+"""
+import numpy as np
+import pytest
+
+import treecmp
+from conftest import make_data
+from oracle import model as om
+
+pytestmark = pytest.mark.gpu
+
+HIST_RTOL = 1e-5
+
+
+def _announce(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _binned(X, n_bins, strategy="standard"):
+    e, bc, nid = om.build_bin_edges(X, n_bins)
+    codes = om.bin_features(X, e, bc, nid, strategy)
+    return e, bc, nid, codes
+
+
+@pytest.mark.parametrize("case", ["plain", "nan", "f64", "wide", "special", "nbins256"])
+def test_binning_bit_exact(engine, case):
+    _announce(f"binning {case}")
+    rng = np.random.default_rng(11)
+    n_bins = 255
+    if case == "plain":
+        X, _ = make_data(20000, 7, seed=1)
+    elif case == "nan":
+        X, _ = make_data(20000, 9, seed=2, nan_frac=0.3, nan_cols=[0, 3, 8])
+        X[:, 5] = np.nan
+    elif case == "f64":
+        X, _ = make_data(5000, 5, seed=3, dtype=np.float64, nan_frac=0.05)
+    elif case == "wide":
+        X, _ = make_data(3000, 130, seed=4, nan_frac=0.02)
+    elif case == "special":
+        X, _ = make_data(4000, 6, seed=5)
+        X[:, 1] = np.round(X[:, 1])
+        X[:, 2] = 3.0
+        X[:4, 3] = [np.inf, -np.inf, 1e38, -1e38]
+        X[:, 4] = rng.exponential(1.0, 4000) * (rng.random(4000) < 0.1)
+    else:
+        X, _ = make_data(6000, 4, seed=6, nan_frac=0.1, nan_cols=[1])
+        X[:, 2] = np.round(X[:, 2] * 40)
+        n_bins = 256
+    e, bc, nid, want = _binned(X, n_bins)
+    if bc.max() > 256:
+        pytest.skip("more than 256 bins")
+    got = engine.bin_features(0, X, e, bc, nid, return_codes=True)
+    np.testing.assert_array_equal(got, np.minimum(want.astype(np.int64), 255).astype(np.uint8))
+    # Scoring matrix: values outside the training range and NaN in columns
+    # that had none.
+    Xp = X.copy()
+    Xp[:100, 0] = np.nan
+    Xp[100:200, -1] = 1e30
+    want_p = om.bin_features(Xp, e, bc, nid, "hybrid")
+    got_p = engine.bin_features(1, Xp, e, bc, nid, return_codes=True)
+    np.testing.assert_array_equal(got_p, np.minimum(want_p.astype(np.int64), 255).astype(np.uint8))
+
+
+def test_load_codes_roundtrip(engine):
+    _announce("load_codes")
+    rng = np.random.default_rng(0)
+    codes = rng.integers(0, 256, (3001, 11)).astype(np.uint8)
+    engine.load_codes(0, codes)
+    np.testing.assert_array_equal(engine.get_codes(0, 3001, 11), codes)
+    c16 = rng.integers(0, 300, (777, 3)).astype(np.uint16)
+    engine.load_codes(1, c16)
+    np.testing.assert_array_equal(engine.get_codes(1, 777, 3), np.minimum(c16, 255).astype(np.uint8))
+
+
+def _grad_hess(y, seed, w=(1.0, 1.0)):
+    rng = np.random.default_rng(seed)
+    p = 1 / (1 + np.exp(-rng.standard_normal(len(y))))
+    wt = np.where(y == 1, w[1], w[0])
+    return wt * (p - y), wt * p * (1 - p)
+
+
+@pytest.mark.parametrize("n,F,nan,weights", [
+    (50000, 12, 0.0, (1.0, 1.0)),
+    (200001, 30, 0.05, (0.785, 7.31)),
+    (7000, 70, 0.7, (1.0, 1.0)),
+])
+def test_histogram_and_split(engine, n, F, nan, weights):
+    _announce(f"histogram n={n} F={F} nan={nan}")
+    X, y = make_data(n, F, seed=n % 97, nan_frac=nan, nan_cols=list(range(0, F, 3)))
+    e, bc, nid, codes = _binned(X, 255)
+    engine.load_codes(0, codes)
+    g, h = _grad_hess(y, 1, weights)
+    rng = np.random.default_rng(2)
+    rows = rng.permutation(n)[: int(0.75 * n)].astype(np.int64)
+    feats = np.sort(rng.permutation(F)[: max(1, int(0.8 * F))]).astype(np.int32)
+    G, H, gain, feat, b = engine.node_split(g, h, rows, feats, bc, 3.0, 1.0)
+    absG = np.zeros_like(G)
+    for i, j in enumerate(feats):
+        nb = int(bc[j])
+        c = np.minimum(codes[rows, j].astype(np.int64), nb - 1)
+        Gr = np.bincount(c, weights=g[rows], minlength=256)
+        Hr = np.bincount(c, weights=h[rows], minlength=256)
+        absG[i] = np.bincount(c, weights=np.abs(g[rows]), minlength=256)
+        tolG = HIST_RTOL * np.maximum(np.abs(Gr), absG[i]) + 1e-12
+        tolH = HIST_RTOL * np.abs(Hr) + 1e-12
+        assert np.all(np.abs(G[i] - Gr) <= tolG), f"G feature {j}"
+        assert np.all(np.abs(H[i] - Hr) <= tolH), f"H feature {j}"
+        # Every feature's histogram sums to the node total.
+        assert abs(G[i].sum() - g[rows].sum()) <= 1e-6 * np.abs(g[rows]).sum()
+    # Best split equals the oracle's root split unless the gains tie.
+    tree = om.build_tree(codes, g, h, rows, feats, 2, 1, 0, 3.0, bc, int(bc.max()), 1.0, -1e300)
+    rf, rt = int(tree[0][0]), int(tree[1][0])
+    if (rf, rt) != (feat, b):
+        ga = treecmp.split_gain(codes, g, h, rows, rf, rt, int(bc[rf]), 1.0)
+        gb = treecmp.split_gain(codes, g, h, rows, feat, b, int(bc[feat]), 1.0)
+        assert abs(ga - gb) <= treecmp.GAIN_TIE_RTOL * abs(ga), (rf, rt, feat, b, ga, gb)
+    else:
+        np.testing.assert_allclose(gain, tree[6][0], rtol=1e-7)
+
+
+@pytest.mark.parametrize("m,bin_", [(1, 5), (4097, 100), (123457, 30), (60000, 0), (60000, 254)])
+def test_partition_stable_and_exact(engine, m, bin_):
+    _announce(f"partition m={m} bin={bin_}")
+    rng = np.random.default_rng(m)
+    n, F = max(m * 2, 10), 3
+    codes = rng.integers(0, 256, (n, F)).astype(np.uint8)
+    engine.load_codes(0, codes)
+    rows = rng.permutation(n)[:m].astype(np.int64)
+    out, nl = engine.partition(rows, 1, bin_)
+    left = codes[rows, 1] <= bin_
+    assert nl == int(left.sum())
+    np.testing.assert_array_equal(out[:nl], rows[left])
+    np.testing.assert_array_equal(out[nl:], rows[~left])
+
+
+def _lockstep_case(engine, n, F, seed, n_bins, max_leaves, max_depth, msl, mcw,
+                   lam, nan=0.0, weights=(1.0, 1.0), sub=0.8, col=0.8):
+    X, y = make_data(n, F, seed=seed, nan_frac=nan)
+    e, bc, nid, codes = _binned(X, n_bins, "hybrid")
+    engine.load_codes(0, codes)
+    g, h = _grad_hess(y, seed + 1, weights)
+    rng = np.random.default_rng(seed + 2)
+    rows = rng.permutation(n)[: max(1, int(sub * n))].astype(np.int64)
+    feats = np.sort(rng.permutation(F)[: max(1, int(col * F))]).astype(np.int32)
+    args = (rows, feats, max_leaves, max_depth, msl, mcw, bc, int(bc.max()), lam, 0.0)
+    ref = om.build_tree(codes, g, h, *args)
+    got = engine.build_tree(g, h, *args)
+    return treecmp.compare(ref, got, codes, g, h, rows, bc, lam)
+
+
+@pytest.mark.parametrize("case", [
+    dict(n=10000, F=20, seed=0, n_bins=255, max_leaves=31, max_depth=6, msl=5, mcw=2.0, lam=1.0),
+    dict(n=30000, F=28, seed=1, n_bins=255, max_leaves=63, max_depth=6, msl=5, mcw=3.0, lam=1.0, nan=0.05),
+    dict(n=20000, F=30, seed=2, n_bins=255, max_leaves=63, max_depth=6, msl=5, mcw=3.0, lam=1.0, weights=(0.785, 7.31)),
+    dict(n=8000, F=100, seed=3, n_bins=255, max_leaves=63, max_depth=6, msl=5, mcw=3.0, lam=1.0, col=0.7),
+    dict(n=40000, F=50, seed=4, n_bins=255, max_leaves=63, max_depth=8, msl=5, mcw=3.0, lam=5.0, nan=0.2, col=0.7, sub=0.5),
+    dict(n=3000, F=6, seed=5, n_bins=16, max_leaves=15, max_depth=10, msl=20, mcw=0.0, lam=0.5),
+    dict(n=500, F=10, seed=6, n_bins=112, max_leaves=15, max_depth=3, msl=5, mcw=1.0, lam=1.0),
+    dict(n=2000, F=4, seed=7, n_bins=64, max_leaves=1, max_depth=6, msl=5, mcw=1.0, lam=1.0),
+    dict(n=50, F=3, seed=8, n_bins=8, max_leaves=31, max_depth=6, msl=40, mcw=1.0, lam=1.0),
+])
+def test_build_tree_lockstep(engine, case):
+    _announce(f"lockstep {case}")
+    _lockstep_case(engine, **case)
+
+
+def test_predict_matches_oracle(engine):
+    _announce("predict")
+    X, y = make_data(20000, 12, seed=9, nan_frac=0.05)
+    m = om.OracleGBM(n_estimators=8, max_depth=5, learning_rate=0.1, n_bins=255,
+                     class_weight=None, random_state=3).fit(X, y)
+    Xb = m.X_bin_
+    engine.load_codes(0, Xb)
+    for tree in m.trees[:3]:
+        np.testing.assert_array_equal(engine.predict_tree(0, len(X), tree), om.predict_tree(Xb, tree))
+    F = engine.predict(0, len(X), m._packed, len(m.trees), 0.1)
+    np.testing.assert_allclose(F, om.predict_all_trees(Xb, m._packed, len(m.trees), 0.1), rtol=0, atol=1e-12)
+
+
+def _fit_both(X, y, **params):
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    trees_ref = []
+    ref = om.OracleGBM(**params)
+    est = HybridHistGBMNumbaV1_0_1(verbose=False, **params)
+    est.fit(X, y)
+    ref.fit(X, y)
+    return ref, est
+
+
+@pytest.mark.parametrize("name", ["config1", "nan_imbalanced", "sparse"])
+def test_fit_matches_oracle(engine, name):
+    _announce(f"fit {name}")
+    if name == "config1":
+        rng = np.random.default_rng(0)
+        X = rng.standard_normal((10_000, 20), dtype=np.float32)
+        w = rng.standard_normal(20)
+        y = (rng.random(10_000) < 1 / (1 + np.exp(-(X @ w)))).astype(np.int64)
+        params = dict(n_estimators=10, max_depth=6, learning_rate=0.1, n_bins=255,
+                      class_weight=None, random_state=0)
+    elif name == "nan_imbalanced":
+        X, y = make_data(30000, 30, seed=12, nan_frac=0.05)
+        y = (np.random.default_rng(1).random(30000) < 0.03).astype(np.int64)
+        X[y == 1, :10] += 1.0
+        params = dict(n_estimators=12, max_depth=6, n_bins=255, random_state=0)
+    else:
+        rng = np.random.default_rng(3)
+        X = np.where(rng.random((20000, 40)) < 0.9, 0.0,
+                     rng.exponential(1.0, (20000, 40))).astype(np.float32)
+        y = (X[:, :8].sum(1) + rng.logistic(size=20000) > 3.0).astype(np.int64)
+        params = dict(n_estimators=10, max_depth=6, n_bins=255, random_state=1)
+    ref, est = _fit_both(X, y, **params)
+    assert len(ref.trees) == len(est.trees)
+    for k, (a, b) in enumerate(zip(ref.trees, est.trees)):
+        res = treecmp.compare(a, b)
+        assert res == "equal", f"tree {k}: {res}"
+    np.testing.assert_allclose(est.train_loss_history_, ref.train_loss_history_, rtol=1e-9)
+    np.testing.assert_allclose(est.predict_proba(X), ref.predict_proba(X), rtol=0, atol=1e-6)
+    np.testing.assert_array_equal(est.bin_edges, ref.bin_edges)
+    np.testing.assert_array_equal(est.feature_bin_counts, ref.feature_bin_counts)
+    assert est.base_score_ == ref.base_score_
