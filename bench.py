@@ -208,6 +208,10 @@ def main():
             "split": round(st["split_ms"] / a.steps, 3),
         },
         "nodes_expanded_per_tree": round(st["nodes_expanded"] / max(st["trees"], 1), 2),
+        "host_ms_per_step": {
+            "sampler_wait": round(st.get("sampler_wait_ms", 0.0) / a.steps, 3),
+            "round": round(st.get("round_ms", 0.0) / a.steps, 3),
+        },
     }
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = run_cpu_baseline(a.workload, a.cpu_rounds)

@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -177,6 +178,9 @@ struct bsscl_engine {
   int64_t ld_c = 0;
   DevBuf<int32_t> rows32;
   DevBuf<int64_t> rows64;
+  DevBuf<int32_t> rows_in, sort_tmp;
+  DevBuf<uint8_t> row_flags;  // all zero between rounds
+  int64_t row_flags_n = 0;
   DevBuf<int32_t> feat_d, nb_sel_d;
   DevBuf<unsigned long long> pool;
   int32_t node_cap = 0;
@@ -204,7 +208,7 @@ struct bsscl_engine {
     int kind;  // 0 hist, 1 partition, 2 split
   };
   std::vector<Pending> pending;
-  double stats[10] = {0};
+  double stats[12] = {0};
 };
 
 namespace bsscl {
@@ -1042,24 +1046,47 @@ int bsscl_boost_round(bsscl_engine *E, bsscl_sampler *sampler,
   HIPCHK(launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, gm, hm, E->ghq.p));
   const int32_t *rows = nullptr, *feats_p = nullptr;
   void *token = nullptr;
+  const auto t_wait0 = std::chrono::steady_clock::now();
   CHK(sampler_take(sampler, &rows, &feats_p, &token));
+  if (E->prof)
+    E->stats[10] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_wait0).count();
   TreeOut out{out_features, out_thresholds, out_values, out_left, out_right,
               out_node_count, out_split_gains};
   std::vector<int32_t> feats, nb_sel;
   int rc = validate_tree_args(E, feats_p, fsub, max_leaves, min_samples_leaf,
                               bin_counts, out, feats, nb_sel);
   if (rc == BSSCL_OK && m > X.n) rc = set_error(BSSCL_EINVAL, "boost_round: sampler rows exceed matrix");
+  // The round's sample_idx (shuffled order, pinned host memory) -> device ->
+  // ascending row ids.
+  const int64_t n_pad = sort_rows_flag_bytes(X.n);
   if (rc == BSSCL_OK) rc = E->rows32.ensure((size_t)m);
+  if (rc == BSSCL_OK) rc = E->rows_in.ensure((size_t)m);
+  if (rc == BSSCL_OK) rc = E->sort_tmp.ensure((size_t)(n_pad / 4096 + 1));
+  if (rc == BSSCL_OK && E->row_flags_n != n_pad) {
+    rc = E->row_flags.ensure((size_t)n_pad);
+    if (rc == BSSCL_OK) {
+      hipError_t e = hipMemsetAsync(E->row_flags.p, 0, (size_t)n_pad, E->st);
+      if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("flags: ") + hipGetErrorString(e));
+      else E->row_flags_n = n_pad;
+    }
+  }
   if (rc == BSSCL_OK) {
-    hipError_t e = hipMemcpyAsync(E->rows32.p, rows, (size_t)m * 4, hipMemcpyHostToDevice, E->st);
-    if (e == hipSuccess) e = hipStreamSynchronize(E->st);
+    hipError_t e = hipMemcpyAsync(E->rows_in.p, rows, (size_t)m * 4, hipMemcpyHostToDevice, E->st);
+    if (e == hipSuccess)
+      e = launch_sort_rows(E->st, E->rows_in.p, m, E->row_flags.p, n_pad, E->sort_tmp.p, E->rows32.p);
     if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("row upload: ") + hipGetErrorString(e));
   }
-  sampler_give_back(sampler, token);
-  CHK(rc);
+  if (rc != BSSCL_OK) {
+    (void)hipStreamSynchronize(E->st);
+    sampler_give_back(sampler, token);
+    return rc;
+  }
   TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight,
                 reg_lambda, gamma};
-  CHK(build_tree_core(E, true, m, feats, nb_sel, tp, out));
+  rc = build_tree_core(E, true, m, feats, nb_sel, tp, out);
+  // build_tree_core synchronised the stream, so the pinned rows are free.
+  sampler_give_back(sampler, token);
+  CHK(rc);
   // F += lr * tree(X) over all rows, then the training log-loss.
   CHK(upload_tree(E, out_features, out_thresholds, out_values, out_left,
                   out_right, *out_node_count, X.F));
@@ -1073,6 +1100,8 @@ int bsscl_boost_round(bsscl_engine *E, bsscl_sampler *sampler,
   HIPCHK(hipMemcpyAsync(&s, E->loss_d.p, 8, hipMemcpyDeviceToHost, E->st));
   CHK(sync(E));
   if (out_train_loss) *out_train_loss = -s / (double)X.n;
+  if (E->prof)
+    E->stats[11] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_wait0).count();
   return BSSCL_OK;
 }
 
@@ -1301,7 +1330,7 @@ int bsscl_engine_set_profiling(bsscl_engine *E, int32_t on) {
 
 int bsscl_engine_stats(bsscl_engine *E, double *out, int32_t cap, int32_t *n_out) {
   if (!E || !out || !n_out) return set_error(BSSCL_EINVAL, "null argument");
-  const int32_t n = std::min<int32_t>(cap, 10);
+  const int32_t n = std::min<int32_t>(cap, 12);
   for (int32_t i = 0; i < n; ++i) out[i] = E->stats[i];
   *n_out = n;
   return BSSCL_OK;

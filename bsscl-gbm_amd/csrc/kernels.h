@@ -94,6 +94,10 @@ hipError_t launch_grad_hess(hipStream_t st, const double *F, const uint8_t *y,
 hipError_t launch_grad_hess_f64(hipStream_t st, const double *F,
                                 const uint8_t *y, int64_t n, double w0,
                                 double w1, double *g, double *h);
+hipError_t launch_sort_rows(hipStream_t st, const int32_t *rows, int64_t m,
+                            uint8_t *flags, int64_t n_pad, int32_t *block_tmp,
+                            int32_t *out);
+int64_t sort_rows_flag_bytes(int64_t n);
 hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               const int32_t *feat, int32_t F_sel,
                               const int32_t *rows32, const int64_t *rows64,

@@ -283,6 +283,88 @@ hipError_t launch_grad_hess_f64(hipStream_t st, const double *F,
 }
 
 // ---------------------------------------------------------------------------
+// In-bag rows in ascending order.  The sampler hands over the reference's
+// sample_idx (distinct row ids in shuffled order); a byte flag per row and a
+// stream compaction give the same set in ascending order, so the root gather
+// streams through each feature column.  The write pass clears the flags for
+// the next round.
+// ---------------------------------------------------------------------------
+constexpr int kFlagBlock = 256;
+constexpr int kFlagTile = kFlagBlock * 16;  // flag bytes per block
+
+__global__ __launch_bounds__(256) void k_mark(const int32_t *__restrict__ rows,
+                                              int64_t m, uint8_t *__restrict__ flags) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < m) flags[rows[i]] = 1;
+}
+
+__device__ __forceinline__ uint32_t byte_sum(uint4 v) {
+  // Each byte is 0 or 1: a multiply-by-0x01010101 sums the four bytes of a
+  // word into its top byte.
+  return ((v.x * 0x01010101u) >> 24) + ((v.y * 0x01010101u) >> 24) +
+         ((v.z * 0x01010101u) >> 24) + ((v.w * 0x01010101u) >> 24);
+}
+
+__global__ __launch_bounds__(kFlagBlock) void k_flag_count(const uint8_t *__restrict__ flags,
+                                                           int32_t *__restrict__ block_cnt) {
+  __shared__ uint32_t tmp[kFlagBlock / 64];
+  const uint4 v = reinterpret_cast<const uint4 *>(flags)[(int64_t)blockIdx.x * kFlagBlock + threadIdx.x];
+  uint32_t total;
+  block_excl_scan<kFlagBlock>(byte_sum(v), tmp, total);
+  if (threadIdx.x == 0) block_cnt[blockIdx.x] = (int32_t)total;
+}
+
+__global__ __launch_bounds__(kFlagBlock) void k_block_scan(int32_t *__restrict__ cnt_to_off,
+                                                           int32_t nb) {
+  __shared__ uint32_t tmp[kFlagBlock / 64];
+  uint32_t carry = 0;
+  for (int base = 0; base < nb; base += kFlagBlock) {
+    const int b = base + (int)threadIdx.x;
+    const uint32_t v = b < nb ? (uint32_t)cnt_to_off[b] : 0u;
+    uint32_t total;
+    const uint32_t pre = block_excl_scan<kFlagBlock>(v, tmp, total);
+    if (b < nb) cnt_to_off[b] = (int32_t)(carry + pre);
+    carry += total;
+  }
+}
+
+__global__ __launch_bounds__(kFlagBlock) void k_flag_write(uint8_t *__restrict__ flags,
+                                                           const int32_t *__restrict__ block_off,
+                                                           int32_t *__restrict__ out) {
+  __shared__ uint32_t tmp[kFlagBlock / 64];
+  uint4 *fp = reinterpret_cast<uint4 *>(flags) + (int64_t)blockIdx.x * kFlagBlock + threadIdx.x;
+  const uint4 v = *fp;
+  uint32_t total;
+  uint32_t o = (uint32_t)block_off[blockIdx.x] +
+               block_excl_scan<kFlagBlock>(byte_sum(v), tmp, total);
+  const int64_t base = ((int64_t)blockIdx.x * kFlagBlock + threadIdx.x) * 16;
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      if ((w[q] >> (8 * b)) & 1u) out[o++] = (int32_t)(base + 4 * q + b);
+  if (v.x | v.y | v.z | v.w) *fp = make_uint4(0, 0, 0, 0);
+}
+
+// flags: n_pad bytes (multiple of kFlagTile), zero on entry and on exit.
+hipError_t launch_sort_rows(hipStream_t st, const int32_t *rows, int64_t m,
+                            uint8_t *flags, int64_t n_pad, int32_t *block_tmp,
+                            int32_t *out) {
+  if (m <= 0) return hipSuccess;
+  const unsigned nb = (unsigned)(n_pad / kFlagTile);
+  hipLaunchKernelGGL(k_mark, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, rows, m, flags);
+  hipLaunchKernelGGL(k_flag_count, dim3(nb), dim3(kFlagBlock), 0, st, flags, block_tmp);
+  hipLaunchKernelGGL(k_block_scan, dim3(1), dim3(kFlagBlock), 0, st, block_tmp, (int32_t)nb);
+  hipLaunchKernelGGL(k_flag_write, dim3(nb), dim3(kFlagBlock), 0, st, flags, block_tmp, out);
+  return hipGetLastError();
+}
+
+int64_t sort_rows_flag_bytes(int64_t n) {
+  return (n + kFlagTile - 1) / kFlagTile * kFlagTile;
+}
+
+// ---------------------------------------------------------------------------
 // Root gather: the tree's in-bag rows (ascending ids from the sampler, or the
 // caller's order) -> compact feature-major set 0.  One thread fills 4
 // consecutive compact rows, so every store is a dword.

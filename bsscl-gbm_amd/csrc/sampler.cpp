@@ -7,30 +7,37 @@
 //   rng.shuffle(all_feature_indices); feat_idx = sort(all_feature_indices[:k])
 // (src/bsscl_gbm/estimator_v1_0_1.py:2502-2517, rng created at :3159).  The
 // shuffle is cumulative across rounds and single-threaded in NumPy (44 ms for
-// 1M rows, 0.63 s for 10M on an 8-core Xeon), which would cap the engine's
-// trees/s on the host.  This file restates the same stream:
+// 1M rows on an 8-core Xeon), which would cap the engine's trees/s on the
+// host.  This file restates the same stream:
 //
 //   * MT19937 (Matsumoto & Nishimura 1998): 624-word state, twist with
 //     matrix 0x9908b0df, tempering shifts 11/7/15/18 with masks
-//     0x9d2c5680/0xefc60000; the state and position come from
+//     0x9d2c5680/0xefc60000.  The state and position come from
 //     RandomState.get_state(), so no seeding code is needed here.
 //   * NumPy's bounded integer for the legacy shuffle: smallest all-ones mask
 //     >= max, draw 32-bit words (64-bit when max > 2^32-1, high word first)
 //     until (word & mask) <= max.
 //   * Fisher-Yates from the end: for i = n-1 .. 1, swap a[i] with a[j(i)].
 //
-// The random numbers do not depend on the data, so the swap loop draws them
-// a fixed distance ahead and prefetches a[j] -- the only change from the
-// plain loop, and it leaves the sequence of swaps unchanged.
+// The random numbers never depend on the data, which allows three changes
+// that leave the sequence of swaps unchanged:
+//   * each 624-word block is twisted and tempered at once, and the bounded
+//     draws for a whole range of mask-constant steps run in one branch-free
+//     loop (a rejected word is overwritten by the next one);
+//   * the draws of round r+1 are made on one thread while another thread
+//     applies the swaps of round r;
+//   * the swap loop prefetches a[j] a fixed distance ahead.
 //
-// Rounds are produced by a worker thread up to `lookahead` rounds ahead of
-// the consumer; each round is delivered as the in-bag row ids in ascending
-// order (the tree builder's fixed-point sums do not depend on row order) and
-// the sorted feature subset.
+// Each round is delivered as the reference's sample_idx (the first n_sub
+// entries of the permuted array, in that order) and the sorted feature
+// subset, up to `lookahead` rounds ahead of the consumer.
 #include "bsscl_internal.h"
+
+#include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <condition_variable>
+#include <cstdlib>
 #include <cstring>
 #include <deque>
 #include <mutex>
@@ -47,9 +54,24 @@ constexpr uint32_t kMatrixA = 0x9908b0dfu;
 constexpr uint32_t kUpper = 0x80000000u;
 constexpr uint32_t kLower = 0x7fffffffu;
 
+inline uint32_t temper(uint32_t y) {
+  y ^= y >> 11;
+  y ^= (y << 7) & 0x9d2c5680u;
+  y ^= (y << 15) & 0xefc60000u;
+  y ^= y >> 18;
+  return y;
+}
+
 struct MT {
   uint32_t key[kN];
-  int pos;
+  uint32_t out[kN];  // tempered key[] of the current block
+  int pos;           // next word of the block (NumPy's state position)
+
+  void load(const uint32_t *k, int p) {
+    std::memcpy(key, k, sizeof(key));
+    pos = p;
+    for (int i = 0; i < kN; ++i) out[i] = temper(key[i]);
+  }
 
   void twist() {
     int i = 0;
@@ -63,26 +85,16 @@ struct MT {
     }
     uint32_t y = (key[kN - 1] & kUpper) | (key[0] & kLower);
     key[kN - 1] = key[kM - 1] ^ (y >> 1) ^ ((0u - (y & 1u)) & kMatrixA);
+    for (int k = 0; k < kN; ++k) out[k] = temper(key[k]);
     pos = 0;
   }
 
   inline uint32_t next32() {
     if (pos >= kN) twist();
-    uint32_t y = key[pos++];
-    y ^= y >> 11;
-    y ^= (y << 7) & 0x9d2c5680u;
-    y ^= (y << 15) & 0xefc60000u;
-    y ^= y >> 18;
-    return y;
+    return out[pos++];
   }
 
-  inline uint64_t next64() {
-    uint64_t hi = next32();
-    uint64_t lo = next32();
-    return (hi << 32) | lo;
-  }
-
-  // Uniform integer in [0, max] by masked rejection.
+  // Masked rejection for one bounded draw (any max).
   inline uint64_t interval(uint64_t max) {
     if (max == 0) return 0;
     uint64_t mask = max;
@@ -97,138 +109,274 @@ struct MT {
       while ((v = (next32() & mask)) > max) {
       }
     } else {
-      while ((v = (next64() & mask)) > max) {
-      }
+      do {
+        const uint64_t hi = next32();
+        const uint64_t lo = next32();
+        v = ((hi << 32) | lo) & mask;
+      } while (v > max);
     }
     return v;
+  }
+
+  // Draws for steps i = hi .. 1 of a shuffle (j[i] in [0, i]); hi < 2^32.
+  // Within [2^k, 2^(k+1)-1] the mask is constant; the loop writes every word
+  // to j[i] and moves to the next step only when the word is accepted.
+  void draws(uint64_t hi, uint32_t *j) {
+    uint64_t i = hi;
+    while (i >= 1) {
+      const int k = 63 - __builtin_clzll(i);
+      const uint64_t lo = 1ull << k;
+      const uint32_t mask = (uint32_t)((lo << 1) - 1);
+      while (i >= lo) {
+        if (pos >= kN) twist();
+        const uint32_t *w = out + pos;
+        const int avail = kN - pos;
+        int used = 0;
+        while (used < avail && i >= lo) {
+          const uint32_t v = w[used++] & mask;
+          j[i] = v;
+          i -= (v <= i) ? 1u : 0u;
+        }
+        pos += used;
+      }
+    }
   }
 };
 
 template <typename T>
 void shuffle_inplace(MT &mt, T *a, int64_t n) {
   if (n <= 1) return;
-  constexpr int kAhead = 32;  // power of two
-  uint64_t ring[kAhead];
-  const int64_t first = n - 1;  // steps i = n-1 down to 1
-  const int64_t steps = n - 1;
-  const int64_t pre = std::min<int64_t>(kAhead, steps);
-  for (int64_t s = 0; s < pre; ++s) {
-    uint64_t j = mt.interval((uint64_t)(first - s));
-    ring[s & (kAhead - 1)] = j;
-    __builtin_prefetch(a + j, 1, 1);
-  }
-  for (int64_t s = 0; s < steps; ++s) {
-    const int64_t i = first - s;
-    const uint64_t j = ring[s & (kAhead - 1)];
-    T t = a[j];
-    a[j] = a[i];
-    a[i] = t;
-    const int64_t s2 = s + kAhead;
-    if (s2 < steps) {
-      uint64_t j2 = mt.interval((uint64_t)(first - s2));
-      ring[s2 & (kAhead - 1)] = j2;
-      __builtin_prefetch(a + j2, 1, 1);
+  if ((uint64_t)(n - 1) > 0xffffffffull) {
+    for (int64_t i = n - 1; i >= 1; --i) {
+      const uint64_t j = mt.interval((uint64_t)i);
+      T t = a[j];
+      a[j] = a[i];
+      a[i] = t;
     }
+    return;
+  }
+  std::vector<uint32_t> j((size_t)n);
+  mt.draws((uint64_t)(n - 1), j.data());
+  constexpr int64_t kAhead = 32;
+  for (int64_t i = n - 1; i >= 1; --i) {
+    if (i > kAhead) __builtin_prefetch(a + j[(size_t)(i - kAhead)], 1, 1);
+    const uint32_t ji = j[(size_t)i];
+    T t = a[ji];
+    a[ji] = a[i];
+    a[i] = t;
   }
 }
+
+// Host buffer for a round's rows: pinned when a HIP device is present (the
+// engine copies it to the GPU asynchronously), plain memory otherwise.
+struct HostBuf {
+  int32_t *p = nullptr;
+  size_t n = 0;
+  bool pinned = false;
+  void alloc(size_t count) {
+    if (count <= n && p) return;
+    release();
+    void *q = nullptr;
+    if (hipHostMalloc(&q, count * sizeof(int32_t), hipHostMallocDefault) == hipSuccess) {
+      pinned = true;
+    } else {
+      (void)hipGetLastError();
+      q = std::malloc(count * sizeof(int32_t));
+      pinned = false;
+    }
+    if (!q) throw std::bad_alloc();
+    p = static_cast<int32_t *>(q);
+    n = count;
+  }
+  void release() {
+    if (p) {
+      if (pinned) (void)hipHostFree(p);
+      else std::free(p);
+    }
+    p = nullptr;
+    n = 0;
+  }
+};
 
 }  // namespace
 
 struct Sampler {
-  MT mt;
+  MT mt;  // owned by the draw thread once started
   int64_t n = 0, n_sub = 0;
   int32_t F = 0, f_sub = 0;
   bool do_rows = false, do_feats = false;
   int32_t n_rounds = 0, lookahead = 2;
-  std::vector<int32_t> rows;   // cumulative permutation of 0..n-1
-  std::vector<int32_t> feats;  // cumulative permutation of 0..F-1
-  std::vector<uint64_t> bitmap;
 
-  struct Round {
-    std::vector<int32_t> rows;   // ascending in-bag row ids (n_sub)
-    std::vector<int32_t> feats;  // ascending selected features (f_sub)
+  struct Draws {  // one round's bounded draws
+    std::vector<uint32_t> rows, feats;
   };
-  std::deque<Round> ready;
-  std::vector<Round> pool;
-  int32_t produced = 0, consumed = 0;
-  bool stop = false;
-  std::mutex mu;
-  std::condition_variable cv_prod, cv_cons;
-  std::thread worker;
+  struct Round {
+    HostBuf rows;                // sample_idx, reference order
+    std::vector<int32_t> feats;  // ascending selected features
+  };
 
-  void produce_one(Round &r) {
-    if (do_rows) shuffle_inplace(mt, rows.data(), n);
-    if (do_feats) shuffle_inplace(mt, feats.data(), (int64_t)F);
-    r.rows.resize((size_t)n_sub);
-    r.feats.resize((size_t)f_sub);
-    if (do_rows) {
-      // Ascending order of rows[0:n_sub] through a bitmap: O(n) and sequential
-      // in memory, cheaper than a sort.
-      std::fill(bitmap.begin(), bitmap.end(), 0ull);
-      for (int64_t k = 0; k < n_sub; ++k) {
-        uint32_t v = (uint32_t)rows[(size_t)k];
-        bitmap[v >> 6] |= 1ull << (v & 63);
-      }
-      int64_t o = 0;
-      for (size_t w = 0; w < bitmap.size(); ++w) {
-        uint64_t b = bitmap[w];
-        while (b) {
-          int t = __builtin_ctzll(b);
-          r.rows[(size_t)o++] = (int32_t)(w * 64 + (size_t)t);
-          b &= b - 1;
+  std::deque<Draws> drawn;       // draw thread -> swap thread
+  std::vector<Draws> draw_pool;
+  std::deque<Round> ready;       // swap thread -> consumer
+  std::vector<Round> pool;
+  int32_t n_drawn = 0, produced = 0, consumed = 0;
+  bool stop = false;
+  uint32_t final_key[kN];
+  int final_pos = 0;
+  std::mutex mu;
+  std::condition_variable cv;
+  std::thread draw_thread, swap_thread;
+  std::string error;
+
+  // Cumulative permutations (swap thread only).
+  std::vector<int32_t> rows, feats;
+
+  void run_draws() {
+    try {
+      for (;;) {
+        Draws d;
+        {
+          std::unique_lock<std::mutex> lk(mu);
+          cv.wait(lk, [&] { return stop || (n_drawn < n_rounds && (int32_t)drawn.size() < 2); });
+          if (stop || n_drawn >= n_rounds) return;
+          if (!draw_pool.empty()) {
+            d = std::move(draw_pool.back());
+            draw_pool.pop_back();
+          }
         }
+        if (do_rows) {
+          d.rows.resize((size_t)n);
+          mt.draws((uint64_t)(n - 1), d.rows.data());
+        }
+        if (do_feats && F > 1) {
+          d.feats.resize((size_t)F);
+          mt.draws((uint64_t)(F - 1), d.feats.data());
+        }
+        {
+          std::lock_guard<std::mutex> lk(mu);
+          drawn.push_back(std::move(d));
+          ++n_drawn;
+          if (n_drawn == n_rounds) {
+            std::memcpy(final_key, mt.key, sizeof(final_key));
+            final_pos = mt.pos;
+          }
+        }
+        cv.notify_all();
       }
-    } else {
-      for (int64_t k = 0; k < n_sub; ++k) r.rows[(size_t)k] = (int32_t)k;
+    } catch (...) {
+      std::lock_guard<std::mutex> lk(mu);
+      error = "sampler: draw thread failed";
+      stop = true;
+      cv.notify_all();
     }
-    std::copy(feats.begin(), feats.begin() + f_sub, r.feats.begin());
+  }
+
+  void apply(const Draws &d, Round &r) {
+    if (do_rows) {
+      const uint32_t *j = d.rows.data();
+      int32_t *a = rows.data();
+      constexpr int64_t kAhead = 32;
+      for (int64_t i = n - 1; i >= 1; --i) {
+        if (i > kAhead) __builtin_prefetch(a + j[i - kAhead], 1, 1);
+        const uint32_t ji = j[i];
+        const int32_t t = a[ji];
+        a[ji] = a[i];
+        a[i] = t;
+      }
+    }
+    if (do_feats && F > 1) {
+      const uint32_t *j = d.feats.data();
+      for (int32_t i = F - 1; i >= 1; --i) std::swap(feats[(size_t)i], feats[j[i]]);
+    }
+    r.rows.alloc((size_t)n_sub);
+    std::memcpy(r.rows.p, rows.data(), (size_t)n_sub * sizeof(int32_t));
+    r.feats.assign(feats.begin(), feats.begin() + f_sub);
     std::sort(r.feats.begin(), r.feats.end());
   }
 
-  void run() {
-    for (;;) {
-      Round r;
-      {
-        std::unique_lock<std::mutex> lk(mu);
-        cv_prod.wait(lk, [&] {
-          return stop || (produced < n_rounds &&
-                          (int32_t)ready.size() < lookahead);
-        });
-        if (stop || produced >= n_rounds) return;
-        if (!pool.empty()) {
-          r = std::move(pool.back());
-          pool.pop_back();
+  void run_swaps() {
+    try {
+      for (;;) {
+        Draws d;
+        Round r;
+        {
+          std::unique_lock<std::mutex> lk(mu);
+          cv.wait(lk, [&] {
+            return stop || produced >= n_rounds ||
+                   (!drawn.empty() && (int32_t)ready.size() < lookahead);
+          });
+          if (stop || produced >= n_rounds) return;
+          d = std::move(drawn.front());
+          drawn.pop_front();
+          if (!pool.empty()) {
+            r = std::move(pool.back());
+            pool.pop_back();
+          }
         }
+        cv.notify_all();
+        apply(d, r);
+        {
+          std::lock_guard<std::mutex> lk(mu);
+          ready.push_back(std::move(r));
+          ++produced;
+          draw_pool.push_back(std::move(d));
+        }
+        cv.notify_all();
       }
-      produce_one(r);
-      {
-        std::lock_guard<std::mutex> lk(mu);
-        ready.push_back(std::move(r));
-        ++produced;
-      }
-      cv_cons.notify_all();
+    } catch (...) {
+      std::lock_guard<std::mutex> lk(mu);
+      error = "sampler: swap thread failed (out of memory?)";
+      stop = true;
+      cv.notify_all();
     }
+  }
+
+  // Blocks until the next round is ready; the caller returns it with give().
+  Round *take() {
+    std::unique_lock<std::mutex> lk(mu);
+    if (consumed >= n_rounds) return nullptr;
+    cv.wait(lk, [&] { return stop || !ready.empty(); });
+    if (ready.empty()) return nullptr;
+    Round *r = new Round(std::move(ready.front()));
+    ready.pop_front();
+    ++consumed;
+    lk.unlock();
+    cv.notify_all();
+    return r;
+  }
+
+  void give(Round *r) {
+    {
+      std::lock_guard<std::mutex> lk(mu);
+      pool.push_back(std::move(*r));
+    }
+    delete r;
+    cv.notify_all();
+  }
+
+  ~Sampler() {
+    {
+      std::lock_guard<std::mutex> lk(mu);
+      stop = true;
+    }
+    cv.notify_all();
+    if (draw_thread.joinable()) draw_thread.join();
+    if (swap_thread.joinable()) swap_thread.join();
+    for (auto &r : ready) r.rows.release();
+    for (auto &r : pool) r.rows.release();
   }
 };
 
-}  // namespace bsscl
-
-// Internal: hand the next round to the engine without an extra copy.
-namespace bsscl {
 int sampler_take(bsscl_sampler *hs, const int32_t **rows, const int32_t **feats,
                  void **token) {
   Sampler *s = reinterpret_cast<Sampler *>(hs);
   if (!s) return set_error(BSSCL_EINVAL, "sampler: null sampler");
-  std::unique_lock<std::mutex> lk(s->mu);
-  if (s->consumed >= s->n_rounds)
-    return set_error(BSSCL_EINVAL, "sampler: all rounds consumed");
-  s->cv_cons.wait(lk, [&] { return !s->ready.empty(); });
-  auto *r = new Sampler::Round(std::move(s->ready.front()));
-  s->ready.pop_front();
-  ++s->consumed;
-  lk.unlock();
-  s->cv_prod.notify_all();
-  *rows = r->rows.data();
+  Sampler::Round *r = s->take();
+  if (!r) {
+    std::lock_guard<std::mutex> lk(s->mu);
+    return set_error(BSSCL_EINVAL, s->error.empty() ? "sampler: all rounds consumed" : s->error);
+  }
+  *rows = r->rows.p;
   *feats = r->feats.data();
   *token = r;
   return BSSCL_OK;
@@ -238,11 +386,7 @@ void sampler_give_back(bsscl_sampler *hs, void *token) {
   Sampler *s = reinterpret_cast<Sampler *>(hs);
   auto *r = static_cast<Sampler::Round *>(token);
   if (!s || !r) return;
-  {
-    std::lock_guard<std::mutex> lk(s->mu);
-    s->pool.push_back(std::move(*r));
-  }
-  delete r;
+  s->give(r);
 }
 
 int64_t sampler_n_sub(bsscl_sampler *hs) {
@@ -251,8 +395,8 @@ int64_t sampler_n_sub(bsscl_sampler *hs) {
 int32_t sampler_f_sub(bsscl_sampler *hs) {
   return reinterpret_cast<Sampler *>(hs)->f_sub;
 }
-}  // namespace bsscl
 
+}  // namespace bsscl
 
 using bsscl::Sampler;
 
@@ -263,8 +407,7 @@ int bsscl_rs_shuffle_i64(uint32_t *key, int32_t *pos, int64_t *data,
   if (!key || !pos || (n > 0 && !data) || *pos < 0 || *pos > 624)
     return bsscl::set_error(BSSCL_EINVAL, "rs_shuffle: bad state or buffer");
   bsscl::MT mt;
-  std::memcpy(mt.key, key, sizeof(mt.key));
-  mt.pos = *pos;
+  mt.load(key, *pos);
   bsscl::shuffle_inplace(mt, data, n);
   std::memcpy(key, mt.key, sizeof(mt.key));
   *pos = mt.pos;
@@ -276,8 +419,7 @@ int bsscl_rs_shuffle_i32(uint32_t *key, int32_t *pos, int32_t *data,
   if (!key || !pos || (n > 0 && !data) || *pos < 0 || *pos > 624)
     return bsscl::set_error(BSSCL_EINVAL, "rs_shuffle: bad state or buffer");
   bsscl::MT mt;
-  std::memcpy(mt.key, key, sizeof(mt.key));
-  mt.pos = *pos;
+  mt.load(key, *pos);
   bsscl::shuffle_inplace(mt, data, n);
   std::memcpy(key, mt.key, sizeof(mt.key));
   *pos = mt.pos;
@@ -300,8 +442,7 @@ int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
                             "sampler_create: f_sub must equal F without column bagging");
   Sampler *s = new (std::nothrow) Sampler();
   if (!s) return bsscl::set_error(BSSCL_ENOMEM, "sampler_create: out of memory");
-  std::memcpy(s->mt.key, key, sizeof(s->mt.key));
-  s->mt.pos = pos;
+  s->mt.load(key, pos);
   s->n = n;
   s->n_sub = n_sub;
   s->F = n_features;
@@ -310,13 +451,15 @@ int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
   s->do_feats = do_feats != 0;
   s->n_rounds = n_rounds;
   s->lookahead = lookahead;
+  std::memcpy(s->final_key, key, sizeof(s->final_key));
+  s->final_pos = pos;
   try {
     s->rows.resize((size_t)n);
     for (int64_t i = 0; i < n; ++i) s->rows[(size_t)i] = (int32_t)i;
     s->feats.resize((size_t)n_features);
     for (int32_t j = 0; j < n_features; ++j) s->feats[(size_t)j] = j;
-    s->bitmap.resize((size_t)((n + 63) / 64));
-    s->worker = std::thread([s] { s->run(); });
+    s->draw_thread = std::thread([s] { s->run_draws(); });
+    s->swap_thread = std::thread([s] { s->run_swaps(); });
   } catch (...) {
     delete s;
     return bsscl::set_error(BSSCL_ENOMEM, "sampler_create: allocation failed");
@@ -327,53 +470,33 @@ int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
 
 int bsscl_sampler_next(bsscl_sampler *hs, int32_t *rows_out,
                        int32_t *feats_out) {
+  const int32_t *rows = nullptr, *feats = nullptr;
+  void *token = nullptr;
+  int rc = bsscl::sampler_take(hs, &rows, &feats, &token);
+  if (rc != BSSCL_OK) return rc;
   Sampler *s = reinterpret_cast<Sampler *>(hs);
-  if (!s) return bsscl::set_error(BSSCL_EINVAL, "sampler_next: null sampler");
-  Sampler::Round r;
-  {
-    std::unique_lock<std::mutex> lk(s->mu);
-    if (s->consumed >= s->n_rounds)
-      return bsscl::set_error(BSSCL_EINVAL, "sampler_next: all rounds consumed");
-    s->cv_cons.wait(lk, [&] { return !s->ready.empty(); });
-    r = std::move(s->ready.front());
-    s->ready.pop_front();
-    ++s->consumed;
-  }
-  s->cv_prod.notify_all();
-  if (rows_out) std::memcpy(rows_out, r.rows.data(), r.rows.size() * sizeof(int32_t));
-  if (feats_out) std::memcpy(feats_out, r.feats.data(), r.feats.size() * sizeof(int32_t));
-  {
-    std::lock_guard<std::mutex> lk(s->mu);
-    s->pool.push_back(std::move(r));
-  }
+  if (rows_out) std::memcpy(rows_out, rows, (size_t)s->n_sub * sizeof(int32_t));
+  if (feats_out) std::memcpy(feats_out, feats, (size_t)s->f_sub * sizeof(int32_t));
+  bsscl::sampler_give_back(hs, token);
   return BSSCL_OK;
 }
 
 int bsscl_sampler_state(bsscl_sampler *hs, uint32_t *key_out,
                         int32_t *pos_out) {
-  // State after every produced round (the worker may be ahead of the
-  // consumer); only meaningful once all rounds are produced.
   Sampler *s = reinterpret_cast<Sampler *>(hs);
   if (!s || !key_out || !pos_out)
     return bsscl::set_error(BSSCL_EINVAL, "sampler_state: bad arguments");
   std::unique_lock<std::mutex> lk(s->mu);
-  if (s->produced < s->n_rounds)
-    return bsscl::set_error(BSSCL_EINVAL, "sampler_state: rounds still pending");
-  std::memcpy(key_out, s->mt.key, sizeof(s->mt.key));
-  *pos_out = s->mt.pos;
+  s->cv.wait(lk, [&] { return s->stop || s->n_drawn >= s->n_rounds; });
+  if (s->n_drawn < s->n_rounds)
+    return bsscl::set_error(BSSCL_EINVAL, "sampler_state: sampler stopped early");
+  std::memcpy(key_out, s->final_key, sizeof(s->final_key));
+  *pos_out = s->final_pos;
   return BSSCL_OK;
 }
 
 void bsscl_sampler_destroy(bsscl_sampler *hs) {
-  Sampler *s = reinterpret_cast<Sampler *>(hs);
-  if (!s) return;
-  {
-    std::lock_guard<std::mutex> lk(s->mu);
-    s->stop = true;
-  }
-  s->cv_prod.notify_all();
-  if (s->worker.joinable()) s->worker.join();
-  delete s;
+  delete reinterpret_cast<Sampler *>(hs);
 }
 
 }  // extern "C"

@@ -196,6 +196,8 @@ void bsscl_sampler_destroy(bsscl_sampler *s);
  *   [4] partition launches   [5] partition ms
  *   [6] split launches       [7] split ms
  *   [8] trees built          [9] nodes expanded
+ *   [10] host ms waiting for the bagging sample in bsscl_boost_round
+ *   [11] host ms in bsscl_boost_round (whole rounds)
  * and returns the number written in *n_out.
  */
 int bsscl_engine_set_profiling(bsscl_engine *eng, int32_t on);

@@ -115,7 +115,7 @@ def test_sampler_stream_matches_reference_calls(sub, col):
         else:
             fi = all_feats.copy()
         r, f = s.next()
-        np.testing.assert_array_equal(r, np.sort(si))
+        np.testing.assert_array_equal(r, si)
         np.testing.assert_array_equal(f, fi)
     key, pos = s.state()
     st = rng.get_state()

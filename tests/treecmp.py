@@ -12,8 +12,10 @@ from __future__ import annotations
 import numpy as np
 
 GAIN_TIE_RTOL = 1e-7
-VALUE_RTOL = 1e-7
-VALUE_ATOL = 1e-9
+# Node values are -G/(H+lambda) of fixed-point sums; G of a node can be near
+# zero (the root of the first round), so the bar is absolute plus relative.
+VALUE_RTOL = 1e-6
+VALUE_ATOL = 1e-7
 
 
 def node_rows(X_bin, tree, rows):
@@ -54,10 +56,6 @@ def compare(ref, got, X_bin=None, g=None, h=None, rows=None, bin_counts=None,
             per = node_rows(X_bin, ref, rows)
             r = per.get(node)
             if r is None or rf[node] < 0 or gf[node] < 0:
-                # A leaf-versus-split difference comes from the candidate
-                # order; accept only if the popped gains were tied.
-                if rf[node] >= 0 and gf[node] >= 0:
-                    pass
                 a = rs[node] if rf[node] >= 0 else gs[node]
                 raise AssertionError(f"node {node}: split vs leaf (gain {a})")
             ga = split_gain(X_bin, g, h, r, int(rf[node]), int(rt[node]), int(bin_counts[rf[node]]), lam)
