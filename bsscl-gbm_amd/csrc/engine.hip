@@ -181,19 +181,21 @@ struct bsscl_engine {
   DevBuf<int32_t> rows_in, sort_tmp;
   DevBuf<uint8_t> row_flags;  // all zero between rounds
   int64_t row_flags_n = 0;
-  DevBuf<int32_t> feat_d, nb_sel_d;
   DevBuf<unsigned long long> pool;
   int32_t node_cap = 0;
   int64_t node_stride = 0;  // int64 words per node histogram
   DevBuf<NodeSeg> segs;
   DevBuf<SplitCand> cand;
   DevBuf<long long> totals;
-  DevBuf<PartParent> parents_d;
-  DevBuf<PartTile> tiles_d;
-  DevBuf<int32_t> tile_begin_d, tile_left_d, hist_node_d;
+  DevBuf<int32_t> tile_left_d, hist_node_d;
   DevBuf<int64_t> tile_off_d, nleft_d;
-  DevBuf<HistTask> htasks_d;
-  DevBuf<SplitTask> stasks_d;
+  DevBuf<char> lvl_d;                 // packed per-level inputs
+  const int32_t *nb_sel_d = nullptr;  // bin counts of the selected features
+  DevBuf<int32_t> nb_sel_buf;
+  DevBuf<NodeOut> nodeout_d;          // packed per-level results
+  NodeOut *nodeout_pin = nullptr;     // pinned readback of nodeout_d
+  int32_t nodeout_pin_n = 0;
+  std::vector<NodeOut> nodeout_h;
   DevBuf<TreeNodeDev> tree_d;
   DevBuf<int32_t> offsets_d;
   DevBuf<double> partials_d, loss_d, out_d;
@@ -304,6 +306,19 @@ double fixed_mul(double max_abs) {
   return std::ldexp(1.0, 30 - e);
 }
 
+int ensure_nodeout(bsscl_engine *E, int32_t cap) {
+  CHK(E->nodeout_d.ensure((size_t)cap));
+  if (E->nodeout_pin_n < cap) {
+    if (E->nodeout_pin) (void)hipHostFree(E->nodeout_pin);
+    E->nodeout_pin = nullptr;
+    E->nodeout_pin_n = 0;
+    HIPCHK(hipHostMalloc(reinterpret_cast<void **>(&E->nodeout_pin),
+                         (size_t)cap * sizeof(NodeOut), hipHostMallocDefault));
+    E->nodeout_pin_n = cap;
+  }
+  return BSSCL_OK;
+}
+
 int ensure_nodes(bsscl_engine *E, int32_t need, int32_t F_sel) {
   const int64_t stride = (int64_t)F_sel * kHistPerFeat;
   if (need <= E->node_cap && stride == E->node_stride) return BSSCL_OK;
@@ -333,7 +348,7 @@ int ensure_nodes(bsscl_engine *E, int32_t need, int32_t F_sel) {
     E->cand = cand2;
     E->totals = tot2;
     E->node_cap = cap;
-    return BSSCL_OK;
+    return ensure_nodeout(E, cap);
   }
   CHK(E->pool.ensure((size_t)cap * stride));
   CHK(E->segs.ensure((size_t)cap));
@@ -341,45 +356,74 @@ int ensure_nodes(bsscl_engine *E, int32_t need, int32_t F_sel) {
   CHK(E->totals.ensure((size_t)cap * 2));
   E->node_cap = cap;
   E->node_stride = stride;
+  return ensure_nodeout(E, cap);
+}
+
+// Feature chunk of a histogram block: 4 features (16 KB of LDS) keeps
+// several blocks per CU and limits how often a row's (g,h) is re-read.
+int32_t hist_fchunk(int32_t F_sel) { return F_sel >= 4 ? 4 : (F_sel >= 2 ? 2 : 1); }
+
+// Rows per histogram tile for S rows: enough tiles for about 4 blocks per
+// CU, but never so many that flushed bins (tiles * F_sel * 512 atomics)
+// exceed ~5% of the LDS adds (S * F_sel * 2), i.e. at most S/5120 tiles.
+int32_t hist_tile_rows(bsscl_engine *E, int64_t S, int32_t F_sel) {
+  const int32_t nchunks = (F_sel + hist_fchunk(F_sel) - 1) / hist_fchunk(F_sel);
+  int64_t tiles = std::max<int64_t>(1, (4 * (int64_t)E->n_cu + nchunks - 1) / nchunks);
+  tiles = std::min<int64_t>(tiles, std::max<int64_t>(1, S / 5120));
+  int64_t t = round_up((S + tiles - 1) / tiles, 4096);
+  return (int32_t)std::min<int64_t>(std::max<int64_t>(t, 4096), 1 << 24);
+}
+
+// Packs host arrays into the pinned arena and uploads them with one copy
+// into E->lvl_d; returns device pointers through `offs`.
+struct Pack {
+  std::vector<std::pair<const void *, size_t>> parts;
+  size_t add(const void *p, size_t bytes) {
+    parts.emplace_back(p, bytes);
+    return parts.size() - 1;
+  }
+};
+
+int upload_pack(bsscl_engine *E, const Pack &pk, std::vector<char *> &dev) {
+  size_t total = 0;
+  std::vector<size_t> off(pk.parts.size());
+  for (size_t i = 0; i < pk.parts.size(); ++i) {
+    off[i] = total;
+    total = (total + pk.parts[i].second + 255) & ~size_t(255);
+  }
+  CHK(E->lvl_d.ensure(std::max<size_t>(total, 256)));
+  char *stage = E->pin.take<char>(total);
+  if (!stage) {
+    // Arena too small: synchronise (nothing may still read it) and grow.
+    HIPCHK(hipStreamSynchronize(E->st));
+    E->pin.reset();
+    CHK(E->pin.reserve(2 * total + (1u << 20)));
+    stage = E->pin.take<char>(total);
+    if (!stage) return set_error(BSSCL_EINTERNAL, "pinned staging");
+  }
+  for (size_t i = 0; i < pk.parts.size(); ++i)
+    if (pk.parts[i].second) std::memcpy(stage + off[i], pk.parts[i].first, pk.parts[i].second);
+  HIPCHK(hipMemcpyAsync(E->lvl_d.p, stage, total, hipMemcpyHostToDevice, E->st));
+  dev.resize(pk.parts.size());
+  for (size_t i = 0; i < pk.parts.size(); ++i) dev[i] = E->lvl_d.p + off[i];
   return BSSCL_OK;
 }
 
-// Rows per histogram block: enough blocks to cover the CUs about twice.
-int32_t hist_tile_rows(bsscl_engine *E, int64_t rows) {
-  int64_t t = rows / (2 * (int64_t)E->n_cu);
-  t = round_up(std::max<int64_t>(t, 1), 1024);
-  return (int32_t)std::min<int64_t>(std::max<int64_t>(t, 1024), 1 << 20);
-}
-
-int32_t hist_fchunk(bsscl_engine *E, int32_t F_sel) {
-  // Leave 4 KB for the kernel's static LDS.
-  int32_t by_lds = (int32_t)((E->max_lds - 4096) / (kHistPerFeat * 8));
-  by_lds = std::max<int32_t>(1, std::min<int32_t>(by_lds, 40));
-  // Even chunks: ceil(F_sel / chunks) features each.
-  const int32_t chunks = (F_sel + by_lds - 1) / by_lds;
-  return (F_sel + chunks - 1) / chunks;
-}
-
-int launch_hist_tasks(bsscl_engine *E, int set, const std::vector<HistTask> &tasks,
-                      int32_t F_sel, int32_t tile_rows) {
-  if (tasks.empty()) return BSSCL_OK;
-  CHK(upload(E, E->htasks_d, tasks.data(), tasks.size()));
-  const int32_t fchunk = hist_fchunk(E, F_sel);
+int launch_hist_level(bsscl_engine *E, int set, const HistTask *tasks_d,
+                      int32_t n_tasks, int32_t F_sel, int32_t tile_rows) {
+  if (n_tasks <= 0) return BSSCL_OK;
   hipEvent_t stop;
   CHK(prof_begin(E, 0, &stop));
-  HIPCHK(launch_hist(E->st, E->codes_c[set].p, E->ld_c, E->gh_c[set].p,
-                     E->htasks_d.p, (int32_t)tasks.size(), E->hist_node_d.p,
-                     E->segs.p, E->nb_sel_d.p, F_sel, fchunk, tile_rows,
-                     E->pool.p, E->node_stride,
-                     (size_t)fchunk * kHistPerFeat * 8));
+  HIPCHK(launch_hist(E->st, E->codes_c[set].p, E->ld_c, E->gh_c[set].p, tasks_d,
+                     n_tasks, E->hist_node_d.p, E->segs.p, E->nb_sel_d, F_sel,
+                     hist_fchunk(F_sel), tile_rows, E->pool.p, E->node_stride));
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
 
-int launch_split_tasks(bsscl_engine *E, const std::vector<SplitTask> &tasks,
-                       int32_t F_sel, const TreeParams &tp) {
-  if (tasks.empty()) return BSSCL_OK;
-  CHK(upload(E, E->stasks_d, tasks.data(), tasks.size()));
+int launch_split_level(bsscl_engine *E, const SplitTask *tasks_d, int32_t n_tasks,
+                       int32_t F_sel, const TreeParams &tp, int32_t first) {
+  if (n_tasks <= 0) return BSSCL_OK;
   SplitParams sp;
   sp.min_child_weight = tp.mcw;
   sp.reg_lambda = tp.lam;
@@ -389,54 +433,34 @@ int launch_split_tasks(bsscl_engine *E, const std::vector<SplitTask> &tasks,
   sp.max_depth = tp.max_depth;
   hipEvent_t stop;
   CHK(prof_begin(E, 2, &stop));
-  HIPCHK(launch_split(E->st, E->stasks_d.p, (int32_t)tasks.size(), E->segs.p,
-                      E->pool.p, E->node_stride, E->nb_sel_d.p, F_sel, sp,
-                      E->cand.p, E->totals.p));
+  HIPCHK(launch_split(E->st, tasks_d, n_tasks, E->segs.p, E->pool.p, E->node_stride,
+                      E->nb_sel_d, F_sel, sp, E->cand.p, E->totals.p));
+  HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, first,
+                          n_tasks, E->nodeout_d.p));
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
 
-// Reads back segments, totals and candidates of nodes [a, b) and reduces the
-// candidates over features: the largest gain, the lowest feature position on
-// ties (est:618-621).
-int read_nodes(bsscl_engine *E, int32_t a, int32_t b, int32_t F_sel,
-               std::vector<HNode> &nodes) {
-  const int32_t cnt = b - a;
+// Reads the packed results of nodes [a, a+cnt) (one copy, one sync).
+int read_nodeouts(bsscl_engine *E, int32_t a, int32_t cnt, std::vector<HNode> &nodes) {
   if (cnt <= 0) return BSSCL_OK;
-  // Uploads of this level may still read the staging arena: finish them
-  // before it can be reallocated.
-  HIPCHK(hipStreamSynchronize(E->st));
-  CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, (size_t)cnt * (sizeof(NodeSeg) + 16 + (size_t)F_sel * sizeof(SplitCand)) + 4096)));
-  NodeSeg *sg = E->pin.take<NodeSeg>(cnt);
-  long long *tt = E->pin.take<long long>(2 * (size_t)cnt);
-  SplitCand *cc = E->pin.take<SplitCand>((size_t)cnt * F_sel);
-  if (!sg || !tt || !cc) return set_error(BSSCL_EINTERNAL, "pinned staging too small");
-  HIPCHK(hipMemcpyAsync(sg, E->segs.p + a, cnt * sizeof(NodeSeg), hipMemcpyDeviceToHost, E->st));
-  HIPCHK(hipMemcpyAsync(tt, E->totals.p + 2 * (size_t)a, 2 * cnt * sizeof(long long), hipMemcpyDeviceToHost, E->st));
-  HIPCHK(hipMemcpyAsync(cc, E->cand.p + (size_t)a * F_sel, (size_t)cnt * F_sel * sizeof(SplitCand), hipMemcpyDeviceToHost, E->st));
-  HIPCHK(hipStreamSynchronize(E->st));
+  E->nodeout_h.resize((size_t)cnt);
+  HIPCHK(hipMemcpyAsync(E->nodeout_pin, E->nodeout_d.p, (size_t)cnt * sizeof(NodeOut),
+                        hipMemcpyDeviceToHost, E->st));
+  CHK(sync(E));
+  const NodeOut *o = E->nodeout_pin;
   for (int32_t i = 0; i < cnt; ++i) {
     HNode &nd = nodes[(size_t)(a + i)];
-    nd.start = sg[i].start;
-    nd.count = sg[i].count;
-    nd.valid = sg[i].valid != 0;
+    nd.start = o[i].start;
+    nd.count = o[i].count;
+    nd.valid = o[i].valid != 0;
     if (!nd.valid) continue;
-    nd.Gq = tt[2 * i];
-    nd.Hq = tt[2 * i + 1];
-    nd.fpos = -1;
-    nd.bin = 0;
-    nd.gain = -1e9;
-    for (int32_t f = 0; f < F_sel; ++f) {
-      const SplitCand &c = cc[(size_t)i * F_sel + f];
-      if (c.bin >= 0 && (nd.fpos < 0 || c.gain > nd.gain)) {
-        nd.fpos = f;
-        nd.bin = c.bin;
-        nd.gain = c.gain;
-      }
-    }
+    nd.Gq = o[i].Gq;
+    nd.Hq = o[i].Hq;
+    nd.fpos = o[i].fpos;
+    nd.bin = o[i].bin;
+    nd.gain = o[i].gain;
   }
-  CHK(prof_collect(E));
-  E->pin.reset();
   return BSSCL_OK;
 }
 
@@ -545,57 +569,108 @@ int replay(bsscl_engine *E, const std::vector<HNode> &nodes,
   return BSSCL_OK;
 }
 
-// Builds one tree from the rows already in E->rows32 (rows32 != 0) or
-// E->rows64, with quantized gradients in E->ghq.
-int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
-                    const std::vector<int32_t> &feats,
-                    const std::vector<int32_t> &nb_sel, const TreeParams &tp,
-                    TreeOut &out) {
-  const Matrix &X = E->mat[0];
-  const int32_t F_sel = (int32_t)feats.size();
+// Launches count / scan / scatter for one level: parents' rows in set `src`
+// move to their children's segments in set `dst`.
+int partition_level(bsscl_engine *E, int src, int dst, const PartParent *parents_d,
+                    int32_t n_parents, const int32_t *tile_begin_d,
+                    const PartTile *tiles_d, int32_t n_tiles, int32_t F_sel,
+                    int32_t min_samples_leaf) {
+  CHK(E->tile_left_d.ensure((size_t)n_tiles));
+  CHK(E->tile_off_d.ensure((size_t)n_tiles));
+  CHK(E->nleft_d.ensure((size_t)n_parents));
+  CHK(E->hist_node_d.ensure((size_t)std::max(n_parents, 1)));
+  hipEvent_t stop;
+  CHK(prof_begin(E, 1, &stop));
+  HIPCHK(launch_part_count(E->st, E->codes_c[src].p, E->ld_c, parents_d, tiles_d,
+                           n_tiles, E->tile_left_d.p));
+  HIPCHK(launch_part_scan(E->st, parents_d, n_parents, tile_begin_d, E->tile_left_d.p,
+                          E->tile_off_d.p, E->nleft_d.p, E->segs.p, E->hist_node_d.p,
+                          min_samples_leaf, E->pool.p, E->node_stride));
+  HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p, E->ld_c,
+                             E->gh_c[src].p, E->gh_c[dst].p, E->rid_c[src].p,
+                             E->rid_c[dst].p, parents_d, tiles_d, n_tiles,
+                             E->tile_off_d.p, E->nleft_d.p, F_sel));
+  CHK(prof_end(E, stop));
+  return BSSCL_OK;
+}
+
+void add_part_tiles(const PartParent &P, int32_t parent_index, std::vector<PartTile> &tiles) {
+  const int64_t a = P.start & ~int64_t(3);
+  for (int64_t r = a; r < P.start + P.count; r += kPartTile)
+    tiles.push_back({r, kPartTile, parent_index});
+}
+
+int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel) {
   CHK(sync(E));
-  E->ld_c = round_up(m + 8, 256);
+  E->ld_c = round_up(m + 32, 256);
   for (int s = 0; s < 2; ++s) {
     CHK(E->codes_c[s].ensure((size_t)E->ld_c * F_sel));
     CHK(E->gh_c[s].ensure((size_t)E->ld_c));
     CHK(E->rid_c[s].ensure((size_t)E->ld_c));
   }
-  CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 8u << 20)));
+  CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 16u << 20)));
   CHK(ensure_nodes(E, 256, F_sel));
-  CHK(upload(E, E->feat_d, feats.data(), feats.size()));
-  CHK(upload(E, E->nb_sel_d, nb_sel.data(), nb_sel.size()));
+  CHK(E->hist_node_d.ensure(256));
+  return BSSCL_OK;
+}
 
-  // Root: gather the in-bag rows into set 0.
-  HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, E->feat_d.p, F_sel,
+// Root: gather the in-bag rows into set 0, histogram, split search.  The
+// feature list and the root's tasks go up in one packed copy.
+int build_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_t> &feats,
+               const std::vector<int32_t> &nb_sel, const TreeParams &tp,
+               std::vector<HNode> &nodes) {
+  const Matrix &X = E->mat[0];
+  const int32_t F_sel = (int32_t)feats.size();
+  const int32_t th = hist_tile_rows(E, m, F_sel);
+  std::vector<HistTask> ht;
+  for (int64_t t = 0; t * th < m; ++t) ht.push_back({0, (int32_t)t});
+  const SplitTask st0{0, -1, -1, 0};
+  Pack pk;
+  pk.add(feats.data(), feats.size() * 4);
+  pk.add(nb_sel.data(), nb_sel.size() * 4);
+  pk.add(ht.data(), ht.size() * sizeof(HistTask));
+  pk.add(&st0, sizeof(SplitTask));
+  std::vector<char *> dv;
+  CHK(upload_pack(E, pk, dv));
+  const int32_t *feat_d = reinterpret_cast<const int32_t *>(dv[0]);
+  E->nb_sel_d = reinterpret_cast<const int32_t *>(dv[1]);
+  HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, feat_d, F_sel,
                             use32 ? E->rows32.p : nullptr,
                             use32 ? nullptr : E->rows64.p, m, E->ghq.p,
-                            E->codes_c[0].p, E->ld_c, E->gh_c[0].p,
-                            E->rid_c[0].p, E->ld_c));
-  std::vector<HNode> nodes(1);
-  {
-    NodeSeg rs;
-    rs.start = 0;
-    rs.count = m;
-    rs.valid = 1;
-    rs.is_small = 1;
-    CHK(upload(E, E->segs, &rs, 1));
-    int32_t zero = 0;
-    CHK(E->hist_node_d.ensure(256));
-    HIPCHK(hipMemcpyAsync(E->hist_node_d.p, &zero, sizeof(int32_t), hipMemcpyHostToDevice, E->st));
-    HIPCHK(hipMemsetAsync(E->pool.p, 0, (size_t)E->node_stride * 8, E->st));
-    const int32_t th = hist_tile_rows(E, m);
-    std::vector<HistTask> ht;
-    for (int64_t t = 0; t * th < m; ++t) ht.push_back({0, (int32_t)t});
-    CHK(launch_hist_tasks(E, 0, ht, F_sel, th));
-    if (E->prof) {
-      E->stats[2] += (double)m * F_sel;
-      E->stats[3] += (double)m * (F_sel + 8);
-    }
-    std::vector<SplitTask> stv{{0, -1, -1, 0}};
-    CHK(launch_split_tasks(E, stv, F_sel, tp));
-    CHK(read_nodes(E, 0, 1, F_sel, nodes));
-    nodes[0].e = nodes[0].gain;
+                            E->codes_c[0].p, E->ld_c, E->gh_c[0].p, E->rid_c[0].p,
+                            E->ld_c, E->segs.p, E->hist_node_d.p, E->pool.p,
+                            E->node_stride));
+  CHK(launch_hist_level(E, 0, reinterpret_cast<const HistTask *>(dv[2]),
+                        (int32_t)ht.size(), F_sel, th));
+  if (E->prof) {
+    E->stats[2] += (double)m * F_sel;
+    E->stats[3] += (double)m * (F_sel + 8);
   }
+  CHK(launch_split_level(E, reinterpret_cast<const SplitTask *>(dv[3]), 1, F_sel, tp, 0));
+  nodes.assign(1, HNode());
+  CHK(read_nodeouts(E, 0, 1, nodes));
+  nodes[0].e = nodes[0].gain;
+  return BSSCL_OK;
+}
+
+// Builds one tree from the rows already in E->rows32 (use32) or E->rows64,
+// with quantized gradients in E->ghq.  The level loop keeps nb_sel (uploaded
+// with the root) in the device arena, so the arena for level inputs is
+// separate (lvl2_d) from the root's.
+int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
+                    const std::vector<int32_t> &feats,
+                    const std::vector<int32_t> &nb_sel, const TreeParams &tp,
+                    TreeOut &out, HNode *root_out = nullptr) {
+  const int32_t F_sel = (int32_t)feats.size();
+  CHK(prepare_tree_buffers(E, m, F_sel));
+  std::vector<HNode> nodes;
+  CHK(build_root(E, use32, m, feats, nb_sel, tp, nodes));
+  if (root_out) *root_out = nodes[0];
+  // nb_sel must outlive the root's arena: copy it to its own buffer.
+  CHK(E->nb_sel_buf.ensure((size_t)F_sel));
+  HIPCHK(hipMemcpyAsync(E->nb_sel_buf.p, E->nb_sel_d, (size_t)F_sel * 4,
+                        hipMemcpyDeviceToDevice, E->st));
+  E->nb_sel_d = E->nb_sel_buf.p;
 
   std::vector<int32_t> frontier;
   if (nodes[0].fpos >= 0 && nodes[0].gain > tp.gamma) frontier.push_back(0);
@@ -623,58 +698,47 @@ int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
     parents.clear();
     tiles.clear();
     tile_begin.clear();
+    int64_t ub_rows = 0;
     for (size_t i = 0; i < exp.size(); ++i) {
       HNode &v = nodes[(size_t)exp[i]];
       v.left = first_child + 2 * (int32_t)i;
       v.right = v.left + 1;
       parents.push_back({v.start, v.count, v.fpos, v.bin, v.left, v.right});
       tile_begin.push_back((int32_t)tiles.size());
-      for (int64_t r = 0; r < v.count; r += kPartTile)
-        tiles.push_back({v.start + r, (int32_t)std::min<int64_t>(kPartTile, v.count - r), (int32_t)i});
+      add_part_tiles(parents.back(), (int32_t)i, tiles);
+      ub_rows += v.count / 2;
     }
     tile_begin.push_back((int32_t)tiles.size());
-    const int src = level & 1, dst = src ^ 1;
-    CHK(upload(E, E->parents_d, parents.data(), parents.size()));
-    CHK(upload(E, E->tiles_d, tiles.data(), tiles.size()));
-    CHK(upload(E, E->tile_begin_d, tile_begin.data(), tile_begin.size()));
-    CHK(E->tile_left_d.ensure(tiles.size()));
-    CHK(E->tile_off_d.ensure(tiles.size()));
-    CHK(E->nleft_d.ensure(parents.size()));
-    CHK(E->hist_node_d.ensure(parents.size()));
-    hipEvent_t stop;
-    CHK(prof_begin(E, 1, &stop));
-    HIPCHK(launch_part_count(E->st, E->codes_c[src].p, E->ld_c, E->parents_d.p,
-                             E->tiles_d.p, (int32_t)tiles.size(), E->tile_left_d.p));
-    HIPCHK(launch_part_scan(E->st, E->parents_d.p, (int32_t)parents.size(),
-                            E->tile_begin_d.p, E->tile_left_d.p, E->tile_off_d.p,
-                            E->nleft_d.p, E->segs.p, E->hist_node_d.p,
-                            tp.min_samples_leaf));
-    HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p,
-                               E->ld_c, E->gh_c[src].p, E->gh_c[dst].p,
-                               E->rid_c[src].p, E->rid_c[dst].p,
-                               E->parents_d.p, E->tiles_d.p,
-                               (int32_t)tiles.size(), E->tile_off_d.p,
-                               E->nleft_d.p, F_sel));
-    CHK(prof_end(E, stop));
-    HIPCHK(hipMemsetAsync(E->pool.p + (size_t)first_child * E->node_stride, 0,
-                          (size_t)(end_child - first_child) * E->node_stride * 8, E->st));
-    // Histograms of the smaller children (at most half of each parent).
-    int64_t ub_rows = 0;
-    for (const auto &P : parents) ub_rows += P.count / 2;
-    const int32_t th = hist_tile_rows(E, ub_rows);
+    // Histograms of the smaller children: at most half of each parent.
+    const int32_t th = hist_tile_rows(E, ub_rows, F_sel);
     ht.clear();
     for (size_t i = 0; i < parents.size(); ++i)
       for (int64_t t = 0; t * th < parents[i].count / 2 + 1; ++t)
         ht.push_back({(int32_t)i, (int32_t)t});
-    CHK(launch_hist_tasks(E, dst, ht, F_sel, th));
     stv.clear();
     for (size_t i = 0; i < exp.size(); ++i) {
       const HNode &v = nodes[(size_t)exp[i]];
       stv.push_back({v.left, exp[i], v.right, v.depth + 1});
       stv.push_back({v.right, exp[i], v.left, v.depth + 1});
     }
-    CHK(launch_split_tasks(E, stv, F_sel, tp));
-    CHK(read_nodes(E, first_child, end_child, F_sel, nodes));
+    Pack pk;
+    pk.add(parents.data(), parents.size() * sizeof(PartParent));
+    pk.add(tile_begin.data(), tile_begin.size() * 4);
+    pk.add(tiles.data(), tiles.size() * sizeof(PartTile));
+    pk.add(ht.data(), ht.size() * sizeof(HistTask));
+    pk.add(stv.data(), stv.size() * sizeof(SplitTask));
+    std::vector<char *> dv;
+    CHK(upload_pack(E, pk, dv));
+    const int src = level & 1, dst = src ^ 1;
+    CHK(partition_level(E, src, dst, reinterpret_cast<const PartParent *>(dv[0]),
+                        (int32_t)parents.size(), reinterpret_cast<const int32_t *>(dv[1]),
+                        reinterpret_cast<const PartTile *>(dv[2]), (int32_t)tiles.size(),
+                        F_sel, tp.min_samples_leaf));
+    CHK(launch_hist_level(E, dst, reinterpret_cast<const HistTask *>(dv[3]),
+                          (int32_t)ht.size(), F_sel, th));
+    CHK(launch_split_level(E, reinterpret_cast<const SplitTask *>(dv[4]),
+                           (int32_t)stv.size(), F_sel, tp, first_child));
+    CHK(read_nodeouts(E, first_child, end_child - first_child, nodes));
     frontier.clear();
     for (size_t i = 0; i < exp.size(); ++i) {
       HNode &v = nodes[(size_t)exp[i]];
@@ -846,21 +910,21 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   }
   E->rows32.release();
   E->rows64.release();
-  E->feat_d.release();
-  E->nb_sel_d.release();
+  E->rows_in.release();
+  E->sort_tmp.release();
+  E->row_flags.release();
+  E->nb_sel_buf.release();
+  E->lvl_d.release();
+  E->nodeout_d.release();
+  if (E->nodeout_pin) (void)hipHostFree(E->nodeout_pin);
   E->pool.release();
   E->segs.release();
   E->cand.release();
   E->totals.release();
-  E->parents_d.release();
-  E->tiles_d.release();
-  E->tile_begin_d.release();
   E->tile_left_d.release();
   E->hist_node_d.release();
   E->tile_off_d.release();
   E->nleft_d.release();
-  E->htasks_d.release();
-  E->stasks_d.release();
   E->tree_d.release();
   E->offsets_d.release();
   E->partials_d.release();
@@ -1204,6 +1268,7 @@ int bsscl_node_split(bsscl_engine *E, const double *grad, const double *hess,
   if (m <= 0) return set_error(BSSCL_EINVAL, "node_split: no rows");
   for (int64_t k = 0; k < m; ++k)
     if (rows[k] < 0 || rows[k] >= X.n) return set_error(BSSCL_EINVAL, "node_split: row out of range");
+  if (n_selected <= 0) return set_error(BSSCL_EINVAL, "node_split: no features");
   std::vector<int32_t> feats(feature_indices, feature_indices + n_selected), nb_sel((size_t)n_selected);
   for (int32_t i = 0; i < n_selected; ++i) {
     if (feats[(size_t)i] < 0 || feats[(size_t)i] >= X.F) return set_error(BSSCL_EINVAL, "node_split: feature out of range");
@@ -1214,34 +1279,12 @@ int bsscl_node_split(bsscl_engine *E, const double *grad, const double *hess,
   CHK(load_grad_hess(E, grad, hess, X.n));
   CHK(E->rows64.ensure((size_t)m));
   HIPCHK(hipMemcpyAsync(E->rows64.p, rows, (size_t)m * 8, hipMemcpyHostToDevice, E->st));
-  // A one-node tree build with max_leaves = 1 computes exactly the root
-  // histogram and split; read them back before the replay.
+  // The root of a tree build: histogram and split search of these rows.
   const int32_t F_sel = n_selected;
-  E->ld_c = round_up(m + 8, 256);
-  CHK(E->codes_c[0].ensure((size_t)E->ld_c * F_sel));
-  CHK(E->gh_c[0].ensure((size_t)E->ld_c));
-  CHK(E->rid_c[0].ensure((size_t)E->ld_c));
-  CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 8u << 20)));
-  CHK(ensure_nodes(E, 256, F_sel));
-  CHK(upload(E, E->feat_d, feats.data(), feats.size()));
-  CHK(upload(E, E->nb_sel_d, nb_sel.data(), nb_sel.size()));
-  HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, E->feat_d.p, F_sel, nullptr,
-                            E->rows64.p, m, E->ghq.p, E->codes_c[0].p, E->ld_c,
-                            E->gh_c[0].p, E->rid_c[0].p, E->ld_c));
-  NodeSeg rs{0, m, 1, 1};
-  CHK(upload(E, E->segs, &rs, 1));
-  int32_t zero = 0;
-  CHK(upload(E, E->hist_node_d, &zero, 1));
-  HIPCHK(hipMemsetAsync(E->pool.p, 0, (size_t)E->node_stride * 8, E->st));
-  const int32_t th = hist_tile_rows(E, m);
-  std::vector<HistTask> ht;
-  for (int64_t t = 0; t * th < m; ++t) ht.push_back({0, (int32_t)t});
-  CHK(launch_hist_tasks(E, 0, ht, F_sel, th));
-  TreeParams tp{2, 1, 0, min_child_weight, reg_lambda, 0.0};
-  std::vector<SplitTask> stv{{0, -1, -1, 0}};
-  CHK(launch_split_tasks(E, stv, F_sel, tp));
-  std::vector<HNode> nodes(1);
-  CHK(read_nodes(E, 0, 1, F_sel, nodes));
+  TreeParams tp{1, 1, 0, min_child_weight, reg_lambda, 0.0};
+  CHK(prepare_tree_buffers(E, m, F_sel));
+  std::vector<HNode> nodes;
+  CHK(build_root(E, false, m, feats, nb_sel, tp, nodes));
   if (out_G || out_H) {
     std::vector<long long> h((size_t)E->node_stride);
     HIPCHK(hipMemcpyAsync(h.data(), E->pool.p, (size_t)E->node_stride * 8, hipMemcpyDeviceToHost, E->st));
@@ -1275,39 +1318,29 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
   }
   CHK(E->rows64.ensure((size_t)m));
   HIPCHK(hipMemcpyAsync(E->rows64.p, rows, (size_t)m * 8, hipMemcpyHostToDevice, E->st));
-  E->ld_c = round_up(m + 8, 256);
-  for (int s = 0; s < 2; ++s) {
-    CHK(E->codes_c[s].ensure((size_t)E->ld_c));
-    CHK(E->gh_c[s].ensure((size_t)E->ld_c));
-    CHK(E->rid_c[s].ensure((size_t)E->ld_c));
-  }
-  CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 8u << 20)));
-  CHK(ensure_nodes(E, 256, 1));
+  CHK(prepare_tree_buffers(E, m, 1));
   const int32_t f1 = feature;
-  CHK(upload(E, E->feat_d, &f1, 1));
-  HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, E->feat_d.p, 1, nullptr,
-                            E->rows64.p, m, E->ghq.p, E->codes_c[0].p, E->ld_c,
-                            E->gh_c[0].p, E->rid_c[0].p, E->ld_c));
-  std::vector<PartParent> parents{{0, m, 0, bin, 1, 2}};
+  Pack pk;
+  pk.add(&f1, 4);
+  std::vector<char *> dv;
+  CHK(upload_pack(E, pk, dv));
+  HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, reinterpret_cast<const int32_t *>(dv[0]), 1,
+                            nullptr, E->rows64.p, m, E->ghq.p, E->codes_c[0].p, E->ld_c,
+                            E->gh_c[0].p, E->rid_c[0].p, E->ld_c, E->segs.p,
+                            E->hist_node_d.p, E->pool.p, E->node_stride));
+  const PartParent P{0, m, 0, bin, 1, 2};
   std::vector<PartTile> tiles;
-  for (int64_t r = 0; r < m; r += kPartTile)
-    tiles.push_back({r, (int32_t)std::min<int64_t>(kPartTile, m - r), 0});
-  std::vector<int32_t> tb{0, (int32_t)tiles.size()};
-  CHK(upload(E, E->parents_d, parents.data(), 1));
-  CHK(upload(E, E->tiles_d, tiles.data(), tiles.size()));
-  CHK(upload(E, E->tile_begin_d, tb.data(), 2));
-  CHK(E->tile_left_d.ensure(tiles.size()));
-  CHK(E->tile_off_d.ensure(tiles.size()));
-  CHK(E->nleft_d.ensure(1));
-  CHK(E->hist_node_d.ensure(1));
-  HIPCHK(launch_part_count(E->st, E->codes_c[0].p, E->ld_c, E->parents_d.p, E->tiles_d.p,
-                           (int32_t)tiles.size(), E->tile_left_d.p));
-  HIPCHK(launch_part_scan(E->st, E->parents_d.p, 1, E->tile_begin_d.p, E->tile_left_d.p,
-                          E->tile_off_d.p, E->nleft_d.p, E->segs.p, E->hist_node_d.p, 0));
-  HIPCHK(launch_part_scatter(E->st, E->codes_c[0].p, E->codes_c[1].p, E->ld_c,
-                             E->gh_c[0].p, E->gh_c[1].p, E->rid_c[0].p, E->rid_c[1].p,
-                             E->parents_d.p, E->tiles_d.p, (int32_t)tiles.size(),
-                             E->tile_off_d.p, E->nleft_d.p, 1));
+  add_part_tiles(P, 0, tiles);
+  const int32_t tb[2] = {0, (int32_t)tiles.size()};
+  Pack pk2;
+  pk2.add(&P, sizeof(P));
+  pk2.add(tb, sizeof(tb));
+  pk2.add(tiles.data(), tiles.size() * sizeof(PartTile));
+  CHK(sync(E));
+  CHK(upload_pack(E, pk2, dv));
+  CHK(partition_level(E, 0, 1, reinterpret_cast<const PartParent *>(dv[0]), 1,
+                      reinterpret_cast<const int32_t *>(dv[1]),
+                      reinterpret_cast<const PartTile *>(dv[2]), (int32_t)tiles.size(), 1, 0));
   std::vector<int32_t> r32((size_t)m);
   int64_t nl = 0;
   HIPCHK(hipMemcpyAsync(r32.data(), E->rid_c[1].p, (size_t)m * 4, hipMemcpyDeviceToHost, E->st));

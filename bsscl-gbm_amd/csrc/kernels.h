@@ -28,7 +28,7 @@ struct PartParent {
   int32_t right_id;
 };
 
-// A run of at most kPartTile rows of one parent (host -> device).
+// One partition tile of a parent (host -> device).
 struct PartTile {
   int64_t row0;
   int32_t rows;
@@ -75,7 +75,22 @@ struct TreeNodeDev {
   double value;
 };
 
-constexpr int kPartTile = 4096;  // rows per partition tile
+// A run of kPartTile rows starting at a 4-row boundary (tiles of one parent
+// are consecutive; rows outside the parent's segment are masked).
+constexpr int kPartTile = 1024;
+
+// A node's result after its split search, packed for readback.
+struct NodeOut {
+  int64_t start;
+  int64_t count;
+  long long Gq;
+  long long Hq;
+  double gain;     // best gain (-1e9 when fpos < 0)
+  int32_t fpos;    // best feature position, -1 when none qualifies
+  int32_t bin;
+  int32_t valid;
+  int32_t pad;
+};
 
 // Launchers (kernels.hip).  All are asynchronous on `st`.
 hipError_t launch_bin(hipStream_t st, const void *X, int is_f64, int64_t n,
@@ -103,14 +118,15 @@ hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               const int32_t *rows32, const int64_t *rows64,
                               int64_t m, const int2 *ghq, uint8_t *codes_c,
                               int64_t ld_c, int2 *gh_c, int32_t *rid_c,
-                              int64_t pad_to);
+                              int64_t pad_to, NodeSeg *segs, int32_t *hist_node,
+                              unsigned long long *root_hist, int64_t hist_words);
 hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int2 *gh_c, const HistTask *tasks,
                        int32_t n_tasks, const int32_t *hist_node,
                        const NodeSeg *segs, const int32_t *nb_sel,
                        int32_t F_sel, int32_t fchunk, int32_t tile_rows,
-                       unsigned long long *pool, int64_t node_stride,
-                       size_t lds_bytes);
+                       unsigned long long *pool, int64_t node_stride);
+int hist_blocks(int32_t n_tasks, int32_t nchunks);
 hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
                              int64_t ld_c, const PartParent *parents,
                              const PartTile *tiles, int32_t n_tiles,
@@ -119,7 +135,8 @@ hipError_t launch_part_scan(hipStream_t st, const PartParent *parents,
                             int32_t n_parents, const int32_t *tile_begin,
                             const int32_t *tile_left, int64_t *tile_left_off,
                             int64_t *parent_nleft, NodeSeg *segs,
-                            int32_t *hist_node, int32_t min_samples_leaf);
+                            int32_t *hist_node, int32_t min_samples_leaf,
+                            unsigned long long *pool, int64_t node_stride);
 hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                uint8_t *codes_dst, int64_t ld_c,
                                const int2 *gh_src, int2 *gh_dst,
@@ -133,6 +150,10 @@ hipError_t launch_split(hipStream_t st, const SplitTask *tasks, int32_t n_tasks,
                         int64_t node_stride, const int32_t *nb_sel,
                         int32_t F_sel, SplitParams p, SplitCand *cand,
                         long long *totals);
+hipError_t launch_node_best(hipStream_t st, const NodeSeg *segs,
+                            const long long *totals, const SplitCand *cand,
+                            int32_t F_sel, int32_t first, int32_t count,
+                            NodeOut *out);
 hipError_t launch_update_F(hipStream_t st, const uint8_t *codes, int64_t ld,
                            int64_t n, const TreeNodeDev *tree,
                            int32_t node_count, double lr, double *F,

@@ -374,8 +374,22 @@ __global__ __launch_bounds__(256) void k_gather_root(
     int32_t F_sel, const int32_t *__restrict__ rows32,
     const int64_t *__restrict__ rows64, int64_t m, const int2 *__restrict__ ghq,
     uint8_t *__restrict__ codes_c, int64_t ld_c, int2 *__restrict__ gh_c,
-    int32_t *__restrict__ rid_c, int64_t pad_to) {
+    int32_t *__restrict__ rid_c, int64_t pad_to, NodeSeg *__restrict__ segs,
+    int32_t *__restrict__ hist_node, unsigned long long *__restrict__ root_hist,
+    int64_t hist_words) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
+  // The root's segment, histogram slot and zeroed histogram.
+  for (int64_t i = t; i < hist_words; i += nthreads) root_hist[i] = 0ull;
+  if (t == 0) {
+    NodeSeg r;
+    r.start = 0;
+    r.count = m;
+    r.valid = 1;
+    r.is_small = 1;
+    segs[0] = r;
+    hist_node[0] = 0;
+  }
   const int64_t k0 = t * 4;
   if (k0 >= pad_to) return;
   int32_t r[4];
@@ -402,36 +416,51 @@ hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               const int32_t *rows32, const int64_t *rows64,
                               int64_t m, const int2 *ghq, uint8_t *codes_c,
                               int64_t ld_c, int2 *gh_c, int32_t *rid_c,
-                              int64_t pad_to) {
+                              int64_t pad_to, NodeSeg *segs, int32_t *hist_node,
+                              unsigned long long *root_hist, int64_t hist_words) {
   const int64_t threads = (pad_to + 3) / 4;
   if (threads <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_gather_root, dim3((unsigned)((threads + 255) / 256)),
                      dim3(256), 0, st, codes, ld, feat, F_sel, rows32, rows64, m,
-                     ghq, codes_c, ld_c, gh_c, rid_c, pad_to);
+                     ghq, codes_c, ld_c, gh_c, rid_c, pad_to, segs, hist_node,
+                     root_hist, hist_words);
   return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
 // Histogram build (est:581-596, est:722-737).
 //
-// A block owns one tile of a node's contiguous rows and a chunk of the
-// selected features.  Its private histogram [nf][256][g,h] int64 lives in
-// LDS (4 KB per feature).  Each thread takes 4 consecutive rows: one 32-byte
-// load of their (g,h), then per feature one dword of 4 packed codes and 8
-// 64-bit LDS adds.  Rows of the dword outside the tile add zero.  The block
-// then adds its non-zero bins into the node's global histogram.
+// A work item is one row tile of a node and one chunk of FC selected
+// features.  Its private histogram [FC][256 bins][g,h] int64 lives in LDS
+// (4 KB per feature, so several blocks share a CU).  A thread takes 16
+// consecutive rows: 128 bytes of (g,h), then per feature one 16-byte load of
+// packed codes and 32 64-bit LDS adds.  Rows outside the tile add zero.  The
+// block then adds its non-zero bins into the node's histogram in HBM.
+//
+// Blocks are numbered so that all feature chunks of one row tile get the
+// same blockIdx modulo 8: blocks are dealt to the 8 XCDs round-robin, so
+// the tile's (g,h) rows are fetched from HBM once and then hit that XCD's L2.
+// Splitting features across blocks (rather than rows) keeps the number of
+// flushed bins, rows/tile_rows * F_sel * 512, small.
 // ---------------------------------------------------------------------------
-constexpr int kHistBlock = 512;
+constexpr int kHistBlock = 256;
+constexpr int kHistRows = 16;  // rows per thread per step
 
+template <int FC>
 __global__ __launch_bounds__(kHistBlock) void k_hist(
     const uint8_t *__restrict__ codes_c, int64_t ld_c,
     const int2 *__restrict__ gh_c, const HistTask *__restrict__ tasks,
-    const int32_t *__restrict__ hist_node, const NodeSeg *__restrict__ segs,
-    const int32_t *__restrict__ nb_sel, int32_t F_sel, int32_t fchunk,
-    int32_t tile_rows, unsigned long long *__restrict__ pool,
-    int64_t node_stride) {
-  extern __shared__ unsigned long long lh[];
-  const HistTask task = tasks[blockIdx.x];
+    int32_t n_tasks, const int32_t *__restrict__ hist_node,
+    const NodeSeg *__restrict__ segs, const int32_t *__restrict__ nb_sel,
+    int32_t F_sel, int32_t nchunks, int32_t tile_rows,
+    unsigned long long *__restrict__ pool, int64_t node_stride) {
+  __shared__ unsigned long long lh[FC * kHistPerFeat];
+  const int b = (int)blockIdx.x;
+  const int j = b >> 3;
+  const int chunk = j % nchunks;
+  const int ti = (j / nchunks) * 8 + (b & 7);
+  if (ti >= n_tasks) return;
+  const HistTask task = tasks[ti];
   const int32_t node = hist_node[task.ref];
   if (node < 0) return;
   const NodeSeg seg = segs[node];
@@ -440,57 +469,47 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
   const int64_t rend = seg.start + seg.count;
   if (r0 >= rend) return;
   const int64_t r1 = min(rend, r0 + (int64_t)tile_rows);
-  const int f0 = (int)blockIdx.y * fchunk;
-  const int nf = min(fchunk, F_sel - f0);
-  if (nf <= 0) return;
-
-  __shared__ int32_t nbm1[256];
-  for (int i = threadIdx.x; i < nf; i += kHistBlock) nbm1[i] = nb_sel[f0 + i] - 1;
-  for (int i = threadIdx.x; i < nf * kHistPerFeat; i += kHistBlock) lh[i] = 0ull;
+  const int f0 = chunk * FC;
+  const int nf = min(FC, F_sel - f0);
+  uint32_t lim[FC];
+#pragma unroll
+  for (int u = 0; u < FC; ++u) lim[u] = (u < nf) ? (uint32_t)(nb_sel[f0 + u] - 1) : 0u;
+  for (int i = threadIdx.x; i < FC * kHistPerFeat; i += kHistBlock) lh[i] = 0ull;
   __syncthreads();
 
-  const int64_t d0 = r0 >> 2, d1 = (r1 + 3) >> 2;
-  const uint8_t *cbase = codes_c + (int64_t)f0 * ld_c;
-  for (int64_t d = d0 + threadIdx.x; d < d1; d += kHistBlock) {
-    const int64_t row = d << 2;
-    const int4 *ghp = reinterpret_cast<const int4 *>(gh_c + row);
-    const int4 a = ghp[0], b = ghp[1];
-    long long g[4] = {a.x, a.z, b.x, b.z};
-    long long h[4] = {a.y, a.w, b.y, b.w};
+  const int64_t g0 = r0 >> 4, g1 = (r1 + 15) >> 4;
+  for (int64_t g = g0 + threadIdx.x; g < g1; g += kHistBlock) {
+    const int64_t row = g << 4;
+    const int4 *gp = reinterpret_cast<const int4 *>(gh_c + row);
+    int gq[kHistRows], hq[kHistRows];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int q = 0; q < kHistRows / 2; ++q) {
+      const int4 v = gp[q];
+      gq[2 * q] = v.x;
+      hq[2 * q] = v.y;
+      gq[2 * q + 1] = v.z;
+      hq[2 * q + 1] = v.w;
+    }
+#pragma unroll
+    for (int k = 0; k < kHistRows; ++k) {
       const bool in = (row + k >= r0) && (row + k < r1);
-      g[k] = in ? g[k] : 0;
-      h[k] = in ? h[k] : 0;
+      gq[k] = in ? gq[k] : 0;
+      hq[k] = in ? hq[k] : 0;
     }
-    const uint32_t *cp = reinterpret_cast<const uint32_t *>(cbase + row);
-    const int64_t ldw = ld_c >> 2;
-    int f = 0;
-    for (; f + 4 <= nf; f += 4) {
-      uint32_t w[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) w[u] = cp[(int64_t)(f + u) * ldw];
+    for (int u = 0; u < FC; ++u) {
+      if (u < nf) {
+        const uint4 c = *reinterpret_cast<const uint4 *>(codes_c + (int64_t)(f0 + u) * ld_c + row);
+        const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+        unsigned long long *hf = lh + u * kHistPerFeat;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t lim = (uint32_t)nbm1[f + u];
-        unsigned long long *hf = lh + (f + u) * kHistPerFeat;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint32_t bin = min((w[u] >> (8 * k)) & 255u, lim);
-          atomicAdd(hf + 2 * bin, (unsigned long long)g[k]);
-          atomicAdd(hf + 2 * bin + 1, (unsigned long long)h[k]);
+        for (int k = 0; k < kHistRows; ++k) {
+          const uint32_t bin = min((cw[k >> 2] >> (8 * (k & 3))) & 255u, lim[u]);
+          __hip_atomic_fetch_add(hf + 2 * bin, (unsigned long long)(long long)gq[k],
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          __hip_atomic_fetch_add(hf + 2 * bin + 1, (unsigned long long)(long long)hq[k],
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-      }
-    }
-    for (; f < nf; ++f) {
-      const uint32_t w = cp[(int64_t)f * ldw];
-      const uint32_t lim = (uint32_t)nbm1[f];
-      unsigned long long *hf = lh + f * kHistPerFeat;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t bin = min((w >> (8 * k)) & 255u, lim);
-        atomicAdd(hf + 2 * bin, (unsigned long long)g[k]);
-        atomicAdd(hf + 2 * bin + 1, (unsigned long long)h[k]);
       }
     }
   }
@@ -502,33 +521,46 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
   }
 }
 
+int hist_blocks(int32_t n_tasks, int32_t nchunks) {
+  return ((n_tasks + 7) / 8) * 8 * nchunks;
+}
+
 hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int2 *gh_c, const HistTask *tasks,
                        int32_t n_tasks, const int32_t *hist_node,
                        const NodeSeg *segs, const int32_t *nb_sel,
                        int32_t F_sel, int32_t fchunk, int32_t tile_rows,
-                       unsigned long long *pool, int64_t node_stride,
-                       size_t lds_bytes) {
+                       unsigned long long *pool, int64_t node_stride) {
   if (n_tasks <= 0) return hipSuccess;
-  const unsigned chunks = (unsigned)((F_sel + fchunk - 1) / fchunk);
-  static size_t attr_bytes = 0;
-  if (lds_bytes > attr_bytes) {
-    hipError_t e = hipFuncSetAttribute((const void *)k_hist,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds_bytes);
-    if (e != hipSuccess) return e;
-    attr_bytes = lds_bytes;
+  const int32_t nchunks = (F_sel + fchunk - 1) / fchunk;
+  const dim3 grid((unsigned)hist_blocks(n_tasks, nchunks));
+#define BSSCL_HIST(FC)                                                              \
+  hipLaunchKernelGGL(k_hist<FC>, grid, dim3(kHistBlock), 0, st, codes_c, ld_c, gh_c, \
+                     tasks, n_tasks, hist_node, segs, nb_sel, F_sel, nchunks,       \
+                     tile_rows, pool, node_stride)
+  switch (fchunk) {
+    case 1: BSSCL_HIST(1); break;
+    case 2: BSSCL_HIST(2); break;
+    case 4: BSSCL_HIST(4); break;
+    case 8: BSSCL_HIST(8); break;
+    default: return hipErrorInvalidValue;
   }
-  hipLaunchKernelGGL(k_hist, dim3((unsigned)n_tasks, chunks), dim3(kHistBlock),
-                     lds_bytes, st, codes_c, ld_c, gh_c, tasks, hist_node, segs,
-                     nb_sel, F_sel, fchunk, tile_rows, pool, node_stride);
+#undef BSSCL_HIST
   return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// Partition (est:662-674, made stable): count, scan, scatter.
+// Partition (est:662-674, made stable): count, scan, scatter.  A tile is 256
+// threads x 4 rows = 1024 rows starting at a 4-row boundary; rows of the
+// tile outside the parent's segment are masked.
 // ---------------------------------------------------------------------------
 constexpr int kPartBlock = 256;
+
+__device__ __forceinline__ void tile_rows(const PartTile &t, const PartParent &P,
+                                          int64_t &lo, int64_t &hi) {
+  lo = max(t.row0, P.start);
+  hi = min(t.row0 + (int64_t)kPartTile, P.start + P.count);
+}
 
 __global__ __launch_bounds__(kPartBlock) void k_part_count(
     const uint8_t *__restrict__ codes_c, int64_t ld_c,
@@ -537,17 +569,17 @@ __global__ __launch_bounds__(kPartBlock) void k_part_count(
   __shared__ uint32_t tmp[kPartBlock / 64];
   const PartTile t = tiles[blockIdx.x];
   const PartParent P = parents[t.parent];
-  const int64_t r0 = t.row0, r1 = t.row0 + t.rows;
-  const uint8_t *col = codes_c + (int64_t)P.fpos * ld_c;
+  int64_t lo, hi;
+  tile_rows(t, P, lo, hi);
+  const int64_t row = t.row0 + 4 * (int64_t)threadIdx.x;
+  // A dword wholly past the segment is not read (it may lie past the buffer).
+  const uint32_t w = (row < hi && row + 4 > lo)
+      ? *reinterpret_cast<const uint32_t *>(codes_c + (int64_t)P.fpos * ld_c + row) : 0u;
   uint32_t cnt = 0;
-  for (int64_t d = (r0 >> 2) + threadIdx.x; d < ((r1 + 3) >> 2); d += kPartBlock) {
-    const int64_t row = d << 2;
-    const uint32_t w = *reinterpret_cast<const uint32_t *>(col + row);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const bool in = (row + k >= r0) && (row + k < r1);
-      cnt += (in && ((w >> (8 * k)) & 255u) <= (uint32_t)P.bin) ? 1u : 0u;
-    }
+  for (int k = 0; k < 4; ++k) {
+    const bool in = (row + k >= lo) && (row + k < hi);
+    cnt += (in && ((w >> (8 * k)) & 255u) <= (uint32_t)P.bin) ? 1u : 0u;
   }
   uint32_t total;
   block_excl_scan<kPartBlock>(cnt, tmp, total);
@@ -565,13 +597,14 @@ hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
 }
 
 // One block per parent: exclusive offsets of its tiles' left counts, the
-// children's segments, whether the split is kept (est:678-683) and which
-// child is the smaller one (est:701-709).
+// children's segments, whether the split is kept (est:678-683), which child
+// is the smaller one (est:701-709), and a zeroed histogram for that child.
 __global__ __launch_bounds__(kPartBlock) void k_part_scan(
     const PartParent *__restrict__ parents, const int32_t *__restrict__ tile_begin,
     const int32_t *__restrict__ tile_left, int64_t *__restrict__ tile_left_off,
     int64_t *__restrict__ parent_nleft, NodeSeg *__restrict__ segs,
-    int32_t *__restrict__ hist_node, int32_t min_samples_leaf) {
+    int32_t *__restrict__ hist_node, int32_t min_samples_leaf,
+    unsigned long long *__restrict__ pool, int64_t node_stride) {
   __shared__ uint32_t tmp[kPartBlock / 64];
   const int p = (int)blockIdx.x;
   const PartParent P = parents[p];
@@ -585,41 +618,53 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scan(
     if (t < t1) tile_left_off[t] = carry + pre;
     carry += total;
   }
-  if (threadIdx.x != 0) return;
-  parent_nleft[p] = carry;
   const int64_t nl = carry, nr = P.count - carry;
-  const int32_t ok = (nl >= min_samples_leaf && nr >= min_samples_leaf) ? 1 : 0;
+  const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
   const bool left_small = nl <= nr;
+  const int32_t small_id = left_small ? P.left_id : P.right_id;
+  if (ok) {
+    unsigned long long *h = pool + (int64_t)small_id * node_stride;
+    for (int64_t i = threadIdx.x; i < node_stride; i += kPartBlock) h[i] = 0ull;
+  }
+  if (threadIdx.x != 0) return;
+  parent_nleft[p] = nl;
   NodeSeg L, R;
   L.start = P.start;
   L.count = nl;
-  L.valid = ok;
+  L.valid = ok ? 1 : 0;
   L.is_small = left_small ? 1 : 0;
   R.start = P.start + nl;
   R.count = nr;
-  R.valid = ok;
+  R.valid = ok ? 1 : 0;
   R.is_small = left_small ? 0 : 1;
   segs[P.left_id] = L;
   segs[P.right_id] = R;
-  hist_node[p] = ok ? (left_small ? P.left_id : P.right_id) : -1;
+  hist_node[p] = ok ? small_id : -1;
 }
 
 hipError_t launch_part_scan(hipStream_t st, const PartParent *parents,
                             int32_t n_parents, const int32_t *tile_begin,
                             const int32_t *tile_left, int64_t *tile_left_off,
                             int64_t *parent_nleft, NodeSeg *segs,
-                            int32_t *hist_node, int32_t min_samples_leaf) {
+                            int32_t *hist_node, int32_t min_samples_leaf,
+                            unsigned long long *pool, int64_t node_stride) {
   if (n_parents <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_part_scan, dim3((unsigned)n_parents), dim3(kPartBlock), 0,
                      st, parents, tile_begin, tile_left, tile_left_off,
-                     parent_nleft, segs, hist_node, min_samples_leaf);
+                     parent_nleft, segs, hist_node, min_samples_leaf, pool,
+                     node_stride);
   return hipGetLastError();
 }
 
-// Moves every row of a tile to its child segment in the other buffer set,
-// keeping the input order within each side: a row's rank among the tile's
-// left (right) rows is the block-wide exclusive scan of per-thread counts
-// plus its position inside the thread's 4 rows.
+// Moves a tile's rows to the child segments in the other buffer set, keeping
+// the input order on each side.  A row's rank among the tile's left (right)
+// rows is a block-wide exclusive scan of per-thread counts plus its position
+// among the thread's 4 rows.  Rows are first placed in LDS in output order
+// (left run, then right run), so the global stores are consecutive: codes
+// as whole dwords (bytes only at the two ends of each run), (g,h) and row
+// ids as consecutive elements.
+constexpr int kScatterFeat = 64;  // features staged in LDS at a time
+
 __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
     const uint8_t *__restrict__ codes_src, uint8_t *__restrict__ codes_dst,
     int64_t ld_c, const int2 *__restrict__ gh_src, int2 *__restrict__ gh_dst,
@@ -628,62 +673,103 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
     const int64_t *__restrict__ tile_left_off,
     const int64_t *__restrict__ parent_nleft, int32_t F_sel) {
   __shared__ uint32_t tmp[kPartBlock / 64];
+  __shared__ int2 gh_s[kPartTile];
+  __shared__ int32_t rid_s[kPartTile];
+  __shared__ uint8_t cs[kScatterFeat * kPartTile];
   const PartTile t = tiles[blockIdx.x];
   const PartParent P = parents[t.parent];
-  const int64_t r0 = t.row0, r1 = t.row0 + t.rows;
+  int64_t lo, hi;
+  tile_rows(t, P, lo, hi);
   const int64_t loff = tile_left_off[blockIdx.x];
   const int64_t nl = parent_nleft[t.parent];
-  // Destinations of this tile's first left / right row.
-  int64_t lbase = P.start + loff;
-  int64_t rbase = P.start + nl + ((r0 - P.start) - loff);
-  const uint8_t *scol = codes_src + (int64_t)P.fpos * ld_c;
-  const int64_t dbeg = r0 >> 2, dend = (r1 + 3) >> 2;
-  for (int64_t pass = dbeg; pass < dend; pass += kPartBlock) {
-    const int64_t d = pass + threadIdx.x;
-    const int64_t row = d << 2;
-    uint32_t lmask = 0, vmask = 0;
-    if (d < dend) {
-      const uint32_t w = *reinterpret_cast<const uint32_t *>(scol + row);
+  const int64_t lbase = P.start + loff;
+  const int64_t rbase = P.start + nl + ((lo - P.start) - loff);
+  const int64_t row = t.row0 + 4 * (int64_t)threadIdx.x;
+  const uint32_t w = (row < hi && row + 4 > lo)
+      ? *reinterpret_cast<const uint32_t *>(codes_src + (int64_t)P.fpos * ld_c + row) : 0u;
+  uint32_t lmask = 0, vmask = 0;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const bool in = (row + k >= r0) && (row + k < r1);
-        vmask |= (in ? 1u : 0u) << k;
-        lmask |= ((in && ((w >> (8 * k)) & 255u) <= (uint32_t)P.bin) ? 1u : 0u) << k;
+  for (int k = 0; k < 4; ++k) {
+    const bool in = (row + k >= lo) && (row + k < hi);
+    vmask |= (in ? 1u : 0u) << k;
+    lmask |= ((in && ((w >> (8 * k)) & 255u) <= (uint32_t)P.bin) ? 1u : 0u) << k;
+  }
+  const uint32_t packed = ((uint32_t)__builtin_popcount(vmask) << 16) | (uint32_t)__builtin_popcount(lmask);
+  uint32_t tot;
+  const uint32_t pre = block_excl_scan<kPartBlock>(packed, tmp, tot);
+  const int ltot = (int)(tot & 0xffffu), vtot = (int)(tot >> 16);
+  const int rtot = vtot - ltot;
+  const int lpre = (int)(pre & 0xffffu), rpre = (int)(pre >> 16) - lpre;
+  int sidx[4];
+  int li = 0, ri = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const bool v = (vmask >> k) & 1u, l = (lmask >> k) & 1u;
+    sidx[k] = !v ? -1 : (l ? lpre + li : ltot + rpre + ri);
+    li += l ? 1 : 0;
+    ri += (v && !l) ? 1 : 0;
+  }
+  if (vmask) {
+    const int4 *gp = reinterpret_cast<const int4 *>(gh_src + row);
+    const int4 ga = gp[0], gb = gp[1];
+    const int4 ra = *reinterpret_cast<const int4 *>(rid_src + row);
+    const int2 ghv[4] = {make_int2(ga.x, ga.y), make_int2(ga.z, ga.w),
+                         make_int2(gb.x, gb.y), make_int2(gb.z, gb.w)};
+    const int32_t rv[4] = {ra.x, ra.y, ra.z, ra.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (sidx[k] >= 0) {
+        gh_s[sidx[k]] = ghv[k];
+        rid_s[sidx[k]] = rv[k];
       }
-    }
-    const uint32_t lc = __builtin_popcount(lmask);
-    const uint32_t vc = __builtin_popcount(vmask);
-    uint32_t ltot, vtot;
-    const uint32_t lpre = block_excl_scan<kPartBlock>(lc, tmp, ltot);
-    const uint32_t vpre = block_excl_scan<kPartBlock>(vc, tmp, vtot);
-    int64_t dst[4];
-    uint32_t li = 0, ri = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const bool v = (vmask >> k) & 1u;
-      const bool l = (lmask >> k) & 1u;
-      dst[k] = !v ? -1 : (l ? lbase + lpre + li : rbase + (vpre - lpre) + ri);
-      li += l ? 1u : 0u;
-      ri += (v && !l) ? 1u : 0u;
-    }
+  }
+  // Output dwords of the left run [lbase, lbase+ltot) and the right run.
+  const int64_t lq0 = lbase >> 2, rq0 = rbase >> 2;
+  const int nld = ltot ? (int)(((lbase + ltot + 3) >> 2) - lq0) : 0;
+  const int nrd = rtot ? (int)(((rbase + rtot + 3) >> 2) - rq0) : 0;
+  const int per_f = nld + nrd;
+  for (int f0 = 0; f0 < F_sel; f0 += kScatterFeat) {
+    const int nf = min(kScatterFeat, F_sel - f0);
     if (vmask) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        if (dst[k] >= 0) {
-          gh_dst[dst[k]] = gh_src[row + k];
-          rid_dst[dst[k]] = rid_src[row + k];
-        }
-      }
-      for (int32_t f = 0; f < F_sel; ++f) {
-        const uint32_t w = *reinterpret_cast<const uint32_t *>(codes_src + (int64_t)f * ld_c + row);
-        uint8_t *dcol = codes_dst + (int64_t)f * ld_c;
+      for (int u = 0; u < nf; ++u) {
+        const uint32_t c = *reinterpret_cast<const uint32_t *>(codes_src + (int64_t)(f0 + u) * ld_c + row);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          if (dst[k] >= 0) dcol[dst[k]] = (uint8_t)(w >> (8 * k));
+          if (sidx[k] >= 0) cs[u * kPartTile + sidx[k]] = (uint8_t)(c >> (8 * k));
       }
     }
-    lbase += ltot;
-    rbase += vtot - ltot;
+    __syncthreads();
+    if (f0 == 0) {
+      for (int i = threadIdx.x; i < vtot; i += kPartBlock) {
+        const int64_t d = i < ltot ? lbase + i : rbase + (i - ltot);
+        gh_dst[d] = gh_s[i];
+        rid_dst[d] = rid_s[i];
+      }
+    }
+    for (int i = threadIdx.x; i < nf * per_f; i += kPartBlock) {
+      const int u = i / per_f, r = i - u * per_f;
+      const bool left = r < nld;
+      const int64_t q = left ? lq0 + r : rq0 + (r - nld);
+      const int64_t run0 = left ? lbase : rbase;
+      const int run_len = left ? ltot : rtot;
+      const int soff = left ? 0 : ltot;
+      const int64_t p0 = q << 2;
+      const uint8_t *src = cs + u * kPartTile + soff;
+      uint8_t *dcol = codes_dst + (int64_t)(f0 + u) * ld_c;
+      if (p0 >= run0 && p0 + 4 <= run0 + run_len) {
+        const int o = (int)(p0 - run0);
+        const uint32_t v = (uint32_t)src[o] | ((uint32_t)src[o + 1] << 8) |
+                           ((uint32_t)src[o + 2] << 16) | ((uint32_t)src[o + 3] << 24);
+        *reinterpret_cast<uint32_t *>(dcol + p0) = v;
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int64_t pp = p0 + k;
+          if (pp >= run0 && pp < run0 + run_len) dcol[pp] = src[pp - run0];
+        }
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -815,6 +901,64 @@ hipError_t launch_split(hipStream_t st, const SplitTask *tasks, int32_t n_tasks,
   hipLaunchKernelGGL(k_split, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st,
                      tasks, n_tasks, segs, pool, node_stride, nb_sel, F_sel, p,
                      cand, totals);
+  return hipGetLastError();
+}
+
+// Per node: the best split over features -- the largest gain, the lowest
+// feature position on ties (est:618-621) -- with the node's segment and
+// fixed-point totals, packed for one readback per level.
+__global__ __launch_bounds__(256) void k_node_best(
+    const NodeSeg *__restrict__ segs, const long long *__restrict__ totals,
+    const SplitCand *__restrict__ cand, int32_t F_sel, int32_t first,
+    int32_t count, NodeOut *__restrict__ out) {
+  const int w = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
+  const int lane = lane_id();
+  if (w >= count) return;
+  const int node = first + w;
+  const NodeSeg s = segs[node];
+  double best = 0.0;
+  int32_t bf = -1, bb = 0;
+  if (s.valid) {
+    for (int f = lane; f < F_sel; f += 64) {
+      const SplitCand c = cand[(int64_t)node * F_sel + f];
+      if (c.bin >= 0 && (bf < 0 || c.gain > best)) {
+        best = c.gain;
+        bf = f;
+        bb = c.bin;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const double og = __shfl_xor(best, o, 64);
+    const int32_t of = __shfl_xor(bf, o, 64);
+    const int32_t ob = __shfl_xor(bb, o, 64);
+    const bool take = of >= 0 && (bf < 0 || og > best || (og == best && of < bf));
+    best = take ? og : best;
+    bf = take ? of : bf;
+    bb = take ? ob : bb;
+  }
+  if (lane == 0) {
+    NodeOut o;
+    o.start = s.start;
+    o.count = s.count;
+    o.valid = s.valid;
+    o.Gq = s.valid ? totals[2 * (int64_t)node] : 0;
+    o.Hq = s.valid ? totals[2 * (int64_t)node + 1] : 0;
+    o.gain = bf >= 0 ? best : -1e9;
+    o.fpos = bf;
+    o.bin = bf >= 0 ? bb : 0;
+    out[w] = o;
+  }
+}
+
+hipError_t launch_node_best(hipStream_t st, const NodeSeg *segs,
+                            const long long *totals, const SplitCand *cand,
+                            int32_t F_sel, int32_t first, int32_t count,
+                            NodeOut *out) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_node_best, dim3((unsigned)((count + 3) / 4)), dim3(256), 0,
+                     st, segs, totals, cand, F_sel, first, count, out);
   return hipGetLastError();
 }
 
