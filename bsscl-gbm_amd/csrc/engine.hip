@@ -24,6 +24,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -191,7 +192,9 @@ struct bsscl_engine {
   DevBuf<int64_t> tile_off_d, nleft_d;
   DevBuf<char> lvl_d;                 // packed per-level inputs
   const int32_t *nb_sel_d = nullptr;  // bin counts of the selected features
-  DevBuf<int32_t> nb_sel_buf;
+  const int32_t *hot_sel_d = nullptr; // most frequent bin of each selected feature
+  DevBuf<int32_t> nb_sel_buf;         // [nb_sel | hot_sel] kept for the tree
+  std::vector<int32_t> hot_bin;       // most frequent code per feature of matrix 0
   DevBuf<NodeOut> nodeout_d;          // packed per-level results
   NodeOut *nodeout_pin = nullptr;     // pinned readback of nodeout_d
   int32_t nodeout_pin_n = 0;
@@ -200,6 +203,12 @@ struct bsscl_engine {
   DevBuf<int32_t> offsets_d;
   DevBuf<double> partials_d, loss_d, out_d;
   PinnedArena pin;
+
+  // Histogram launch shape (see hist_fchunk / hist_tile_rows); tunable with
+  // BSSCL_HIST_FC, BSSCL_HIST_BLOCKS_PER_CU and BSSCL_HIST_ROWS_PER_FLUSH.
+  int32_t hist_fc = 4;
+  int32_t hist_blocks_per_cu = 4;
+  int32_t hist_rows_per_flush = 5120;
 
   // Profiling.
   bool prof = false;
@@ -361,15 +370,22 @@ int ensure_nodes(bsscl_engine *E, int32_t need, int32_t F_sel) {
 
 // Feature chunk of a histogram block: 4 features (16 KB of LDS) keeps
 // several blocks per CU and limits how often a row's (g,h) is re-read.
-int32_t hist_fchunk(int32_t F_sel) { return F_sel >= 4 ? 4 : (F_sel >= 2 ? 2 : 1); }
+int32_t hist_fchunk(bsscl_engine *E, int32_t F_sel) {
+  int32_t fc = E->hist_fc;
+  while (fc > 1 && fc > F_sel) fc >>= 1;
+  return fc;
+}
 
-// Rows per histogram tile for S rows: enough tiles for about 4 blocks per
-// CU, but never so many that flushed bins (tiles * F_sel * 512 atomics)
-// exceed ~5% of the LDS adds (S * F_sel * 2), i.e. at most S/5120 tiles.
+// Rows per histogram tile for S rows: enough tiles for about
+// hist_blocks_per_cu blocks per CU, but never so many that flushed bins
+// (tiles * F_sel * 512 atomics) exceed ~5% of the LDS adds (S * F_sel * 2),
+// i.e. at most S/hist_rows_per_flush tiles.
 int32_t hist_tile_rows(bsscl_engine *E, int64_t S, int32_t F_sel) {
-  const int32_t nchunks = (F_sel + hist_fchunk(F_sel) - 1) / hist_fchunk(F_sel);
-  int64_t tiles = std::max<int64_t>(1, (4 * (int64_t)E->n_cu + nchunks - 1) / nchunks);
-  tiles = std::min<int64_t>(tiles, std::max<int64_t>(1, S / 5120));
+  const int32_t fc = hist_fchunk(E, F_sel);
+  const int32_t nchunks = (F_sel + fc - 1) / fc;
+  int64_t tiles = std::max<int64_t>(
+      1, ((int64_t)E->hist_blocks_per_cu * E->n_cu + nchunks - 1) / nchunks);
+  tiles = std::min<int64_t>(tiles, std::max<int64_t>(1, S / E->hist_rows_per_flush));
   int64_t t = round_up((S + tiles - 1) / tiles, 4096);
   return (int32_t)std::min<int64_t>(std::max<int64_t>(t, 4096), 1 << 24);
 }
@@ -415,8 +431,9 @@ int launch_hist_level(bsscl_engine *E, int set, const HistTask *tasks_d,
   hipEvent_t stop;
   CHK(prof_begin(E, 0, &stop));
   HIPCHK(launch_hist(E->st, E->codes_c[set].p, E->ld_c, E->gh_c[set].p, tasks_d,
-                     n_tasks, E->hist_node_d.p, E->segs.p, E->nb_sel_d, F_sel,
-                     hist_fchunk(F_sel), tile_rows, E->pool.p, E->node_stride));
+                     n_tasks, E->hist_node_d.p, E->segs.p, E->nb_sel_d, E->hot_sel_d,
+                     F_sel, hist_fchunk(E, F_sel), tile_rows, E->pool.p,
+                     E->node_stride));
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
@@ -436,7 +453,7 @@ int launch_split_level(bsscl_engine *E, const SplitTask *tasks_d, int32_t n_task
   HIPCHK(launch_split(E->st, tasks_d, n_tasks, E->segs.p, E->pool.p, E->node_stride,
                       E->nb_sel_d, F_sel, sp, E->cand.p, E->totals.p));
   HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, first,
-                          n_tasks, E->nodeout_d.p));
+                          n_tasks, 0, E->nodeout_d.p));
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
@@ -574,7 +591,7 @@ int replay(bsscl_engine *E, const std::vector<HNode> &nodes,
 int partition_level(bsscl_engine *E, int src, int dst, const PartParent *parents_d,
                     int32_t n_parents, const int32_t *tile_begin_d,
                     const PartTile *tiles_d, int32_t n_tiles, int32_t F_sel,
-                    int32_t min_samples_leaf) {
+                    int32_t min_samples_leaf, bool move_rows = true) {
   CHK(E->tile_left_d.ensure((size_t)n_tiles));
   CHK(E->tile_off_d.ensure((size_t)n_tiles));
   CHK(E->nleft_d.ensure((size_t)n_parents));
@@ -585,11 +602,13 @@ int partition_level(bsscl_engine *E, int src, int dst, const PartParent *parents
                            n_tiles, E->tile_left_d.p));
   HIPCHK(launch_part_scan(E->st, parents_d, n_parents, tile_begin_d, E->tile_left_d.p,
                           E->tile_off_d.p, E->nleft_d.p, E->segs.p, E->hist_node_d.p,
-                          min_samples_leaf, E->pool.p, E->node_stride));
-  HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p, E->ld_c,
-                             E->gh_c[src].p, E->gh_c[dst].p, E->rid_c[src].p,
-                             E->rid_c[dst].p, parents_d, tiles_d, n_tiles,
-                             E->tile_off_d.p, E->nleft_d.p, F_sel));
+                          min_samples_leaf, move_rows ? E->pool.p : nullptr,
+                          E->node_stride));
+  if (move_rows)
+    HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p, E->ld_c,
+                               E->gh_c[src].p, E->gh_c[dst].p, E->rid_c[src].p,
+                               E->rid_c[dst].p, parents_d, tiles_d, n_tiles,
+                               E->tile_off_d.p, E->nleft_d.p, F_sel));
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
@@ -600,8 +619,24 @@ void add_part_tiles(const PartParent &P, int32_t parent_index, std::vector<PartT
     tiles.push_back({r, kPartTile, parent_index});
 }
 
+// Histogram launch shape from the environment (read per tree, so a tuning
+// sweep can change it between calls).
+void read_hist_tuning(bsscl_engine *E) {
+  auto env_int = [](const char *name, int32_t lo, int32_t hi, int32_t dflt) {
+    const char *e = std::getenv(name);
+    if (!e) return dflt;
+    const long x = std::strtol(e, nullptr, 10);
+    return (x >= lo && x <= hi) ? (int32_t)x : dflt;
+  };
+  E->hist_fc = env_int("BSSCL_HIST_FC", 1, 8, 4);
+  if (E->hist_fc != 1 && E->hist_fc != 2 && E->hist_fc != 4 && E->hist_fc != 8) E->hist_fc = 4;
+  E->hist_blocks_per_cu = env_int("BSSCL_HIST_BLOCKS_PER_CU", 1, 64, 4);
+  E->hist_rows_per_flush = env_int("BSSCL_HIST_ROWS_PER_FLUSH", 256, 1 << 22, 5120);
+}
+
 int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel) {
   CHK(sync(E));
+  read_hist_tuning(E);
   E->ld_c = round_up(m + 32, 256);
   for (int s = 0; s < 2; ++s) {
     CHK(E->codes_c[s].ensure((size_t)E->ld_c * F_sel));
@@ -625,15 +660,24 @@ int build_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_t
   std::vector<HistTask> ht;
   for (int64_t t = 0; t * th < m; ++t) ht.push_back({0, (int32_t)t});
   const SplitTask st0{0, -1, -1, 0};
+  // Selected features' bin counts followed by their most frequent bins.
+  std::vector<int32_t> nb_hot(2 * (size_t)F_sel);
+  for (int32_t i = 0; i < F_sel; ++i) {
+    nb_hot[(size_t)i] = nb_sel[(size_t)i];
+    const int32_t f = feats[(size_t)i];
+    const int32_t hb = (size_t)f < E->hot_bin.size() ? E->hot_bin[(size_t)f] : -1;
+    nb_hot[(size_t)(F_sel + i)] = hb < 0 ? -1 : std::min(hb, nb_sel[(size_t)i] - 1);
+  }
   Pack pk;
   pk.add(feats.data(), feats.size() * 4);
-  pk.add(nb_sel.data(), nb_sel.size() * 4);
+  pk.add(nb_hot.data(), nb_hot.size() * 4);
   pk.add(ht.data(), ht.size() * sizeof(HistTask));
   pk.add(&st0, sizeof(SplitTask));
   std::vector<char *> dv;
   CHK(upload_pack(E, pk, dv));
   const int32_t *feat_d = reinterpret_cast<const int32_t *>(dv[0]);
   E->nb_sel_d = reinterpret_cast<const int32_t *>(dv[1]);
+  E->hot_sel_d = E->nb_sel_d + F_sel;
   HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, feat_d, F_sel,
                             use32 ? E->rows32.p : nullptr,
                             use32 ? nullptr : E->rows64.p, m, E->ghq.p,
@@ -666,11 +710,12 @@ int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
   std::vector<HNode> nodes;
   CHK(build_root(E, use32, m, feats, nb_sel, tp, nodes));
   if (root_out) *root_out = nodes[0];
-  // nb_sel must outlive the root's arena: copy it to its own buffer.
-  CHK(E->nb_sel_buf.ensure((size_t)F_sel));
-  HIPCHK(hipMemcpyAsync(E->nb_sel_buf.p, E->nb_sel_d, (size_t)F_sel * 4,
+  // nb_sel/hot_sel must outlive the root's arena: copy to their own buffer.
+  CHK(E->nb_sel_buf.ensure(2 * (size_t)F_sel));
+  HIPCHK(hipMemcpyAsync(E->nb_sel_buf.p, E->nb_sel_d, 2 * (size_t)F_sel * 4,
                         hipMemcpyDeviceToDevice, E->st));
   E->nb_sel_d = E->nb_sel_buf.p;
+  E->hot_sel_d = E->nb_sel_buf.p + F_sel;
 
   std::vector<int32_t> frontier;
   if (nodes[0].fpos >= 0 && nodes[0].gain > tp.gamma) frontier.push_back(0);
@@ -709,35 +754,60 @@ int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
       ub_rows += v.count / 2;
     }
     tile_begin.push_back((int32_t)tiles.size());
-    // Histograms of the smaller children: at most half of each parent.
-    const int32_t th = hist_tile_rows(E, ub_rows, F_sel);
-    ht.clear();
-    for (size_t i = 0; i < parents.size(); ++i)
-      for (int64_t t = 0; t * th < parents[i].count / 2 + 1; ++t)
-        ht.push_back({(int32_t)i, (int32_t)t});
-    stv.clear();
-    for (size_t i = 0; i < exp.size(); ++i) {
-      const HNode &v = nodes[(size_t)exp[i]];
-      stv.push_back({v.left, exp[i], v.right, v.depth + 1});
-      stv.push_back({v.right, exp[i], v.left, v.depth + 1});
-    }
-    Pack pk;
-    pk.add(parents.data(), parents.size() * sizeof(PartParent));
-    pk.add(tile_begin.data(), tile_begin.size() * 4);
-    pk.add(tiles.data(), tiles.size() * sizeof(PartTile));
-    pk.add(ht.data(), ht.size() * sizeof(HistTask));
-    pk.add(stv.data(), stv.size() * sizeof(SplitTask));
-    std::vector<char *> dv;
-    CHK(upload_pack(E, pk, dv));
     const int src = level & 1, dst = src ^ 1;
-    CHK(partition_level(E, src, dst, reinterpret_cast<const PartParent *>(dv[0]),
-                        (int32_t)parents.size(), reinterpret_cast<const int32_t *>(dv[1]),
-                        reinterpret_cast<const PartTile *>(dv[2]), (int32_t)tiles.size(),
-                        F_sel, tp.min_samples_leaf));
-    CHK(launch_hist_level(E, dst, reinterpret_cast<const HistTask *>(dv[3]),
-                          (int32_t)ht.size(), F_sel, th));
-    CHK(launch_split_level(E, reinterpret_cast<const SplitTask *>(dv[4]),
-                           (int32_t)stv.size(), F_sel, tp, first_child));
+    // Children at max_depth can never be split (est:775-777): they need
+    // their sizes and totals only, so their rows are not moved and their
+    // histograms are not built.
+    const bool last = nodes[(size_t)exp[0]].depth + 1 >= tp.max_depth;
+    if (last) {
+      std::vector<int32_t> pids(exp.begin(), exp.end());
+      Pack pk;
+      pk.add(parents.data(), parents.size() * sizeof(PartParent));
+      pk.add(tile_begin.data(), tile_begin.size() * 4);
+      pk.add(tiles.data(), tiles.size() * sizeof(PartTile));
+      pk.add(pids.data(), pids.size() * 4);
+      std::vector<char *> dv;
+      CHK(upload_pack(E, pk, dv));
+      const PartParent *pd = reinterpret_cast<const PartParent *>(dv[0]);
+      CHK(partition_level(E, src, dst, pd, (int32_t)parents.size(),
+                          reinterpret_cast<const int32_t *>(dv[1]),
+                          reinterpret_cast<const PartTile *>(dv[2]), (int32_t)tiles.size(),
+                          F_sel, tp.min_samples_leaf, false));
+      HIPCHK(launch_child_totals(E->st, pd, (int32_t)parents.size(),
+                                 reinterpret_cast<const int32_t *>(dv[3]), E->segs.p,
+                                 E->pool.p, E->node_stride, E->totals.p));
+      HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, first_child,
+                              end_child - first_child, 1, E->nodeout_d.p));
+    } else {
+      // Histograms of the smaller children: at most half of each parent.
+      const int32_t th = hist_tile_rows(E, ub_rows, F_sel);
+      ht.clear();
+      for (size_t i = 0; i < parents.size(); ++i)
+        for (int64_t t = 0; t * th < parents[i].count / 2 + 1; ++t)
+          ht.push_back({(int32_t)i, (int32_t)t});
+      stv.clear();
+      for (size_t i = 0; i < exp.size(); ++i) {
+        const HNode &v = nodes[(size_t)exp[i]];
+        stv.push_back({v.left, exp[i], v.right, v.depth + 1});
+        stv.push_back({v.right, exp[i], v.left, v.depth + 1});
+      }
+      Pack pk;
+      pk.add(parents.data(), parents.size() * sizeof(PartParent));
+      pk.add(tile_begin.data(), tile_begin.size() * 4);
+      pk.add(tiles.data(), tiles.size() * sizeof(PartTile));
+      pk.add(ht.data(), ht.size() * sizeof(HistTask));
+      pk.add(stv.data(), stv.size() * sizeof(SplitTask));
+      std::vector<char *> dv;
+      CHK(upload_pack(E, pk, dv));
+      CHK(partition_level(E, src, dst, reinterpret_cast<const PartParent *>(dv[0]),
+                          (int32_t)parents.size(), reinterpret_cast<const int32_t *>(dv[1]),
+                          reinterpret_cast<const PartTile *>(dv[2]), (int32_t)tiles.size(),
+                          F_sel, tp.min_samples_leaf));
+      CHK(launch_hist_level(E, dst, reinterpret_cast<const HistTask *>(dv[3]),
+                            (int32_t)ht.size(), F_sel, th));
+      CHK(launch_split_level(E, reinterpret_cast<const SplitTask *>(dv[4]),
+                             (int32_t)stv.size(), F_sel, tp, first_child));
+    }
     CHK(read_nodeouts(E, first_child, end_child - first_child, nodes));
     frontier.clear();
     for (size_t i = 0; i < exp.size(); ++i) {
@@ -748,7 +818,7 @@ int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
       v.nl = L.count;
       v.nr = R.count;
       v.split_ok = L.valid;
-      if (E->prof && v.split_ok) {
+      if (E->prof && v.split_ok && !last) {
         const int64_t ms = std::min(v.nl, v.nr);
         E->stats[2] += (double)ms * F_sel;
         E->stats[3] += (double)ms * (F_sel + 8);
@@ -821,6 +891,30 @@ int load_grad_hess(bsscl_engine *E, const double *grad, const double *hess,
   return BSSCL_OK;
 }
 
+// Most frequent code of each feature of matrix 0: the histogram kernel sums
+// that bin in registers instead of LDS atomics.
+int find_hot_bins(bsscl_engine *E) {
+  const Matrix &M = E->mat[0];
+  DevBuf<unsigned int> cnt;
+  CHK(cnt.ensure((size_t)M.F * 256));
+  std::vector<unsigned int> h((size_t)M.F * 256);
+  hipError_t e = hipMemsetAsync(cnt.p, 0, (size_t)M.F * 256 * 4, E->st);
+  if (e == hipSuccess) e = launch_code_counts(E->st, M.codes.p, M.ld, M.n, M.F, cnt.p);
+  if (e == hipSuccess) e = hipMemcpyAsync(h.data(), cnt.p, h.size() * 4, hipMemcpyDeviceToHost, E->st);
+  if (e == hipSuccess) e = hipStreamSynchronize(E->st);
+  cnt.release();
+  if (e != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("code counts: ") + hipGetErrorString(e));
+  // Only a bin holding at least 10% of the rows is worth the divergent
+  // register path; -1 (no bin) otherwise.
+  E->hot_bin.assign((size_t)M.F, -1);
+  for (int32_t f = 0; f < M.F; ++f) {
+    const unsigned int *c = h.data() + (size_t)f * 256;
+    const int32_t b = (int32_t)(std::max_element(c, c + 256) - c);
+    if ((double)c[b] >= 0.10 * (double)M.n) E->hot_bin[(size_t)f] = b;
+  }
+  return BSSCL_OK;
+}
+
 int upload_tree(bsscl_engine *E, const int32_t *features,
                 const int64_t *thresholds, const double *values,
                 const int32_t *left, const int32_t *right, int32_t node_count,
@@ -889,6 +983,7 @@ int bsscl_engine_create(int32_t device, bsscl_engine **out) {
     E->n_cu = v;
   if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
     E->max_lds = (size_t)v;
+
   *out = E;
   return BSSCL_OK;
 }
@@ -987,6 +1082,7 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
   ed.release();
   nb.release();
   nid.release();
+  if (slot == 0) CHK(find_hot_bins(E));
   if (codes_out) return bsscl_get_codes(E, slot, codes_out);
   return BSSCL_OK;
 }
@@ -1007,6 +1103,7 @@ int bsscl_load_codes(bsscl_engine *E, int32_t slot, const void *codes,
   if (e == hipSuccess) e = hipStreamSynchronize(E->st);
   tmp.release();
   if (e != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("load_codes: ") + hipGetErrorString(e));
+  if (slot == 0) CHK(find_hot_bins(E));
   return BSSCL_OK;
 }
 

@@ -124,8 +124,9 @@ hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int2 *gh_c, const HistTask *tasks,
                        int32_t n_tasks, const int32_t *hist_node,
                        const NodeSeg *segs, const int32_t *nb_sel,
-                       int32_t F_sel, int32_t fchunk, int32_t tile_rows,
-                       unsigned long long *pool, int64_t node_stride);
+                       const int32_t *hot_sel, int32_t F_sel, int32_t fchunk,
+                       int32_t tile_rows, unsigned long long *pool,
+                       int64_t node_stride);
 int hist_blocks(int32_t n_tasks, int32_t nchunks);
 hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
                              int64_t ld_c, const PartParent *parents,
@@ -153,7 +154,13 @@ hipError_t launch_split(hipStream_t st, const SplitTask *tasks, int32_t n_tasks,
 hipError_t launch_node_best(hipStream_t st, const NodeSeg *segs,
                             const long long *totals, const SplitCand *cand,
                             int32_t F_sel, int32_t first, int32_t count,
-                            NodeOut *out);
+                            int32_t no_split, NodeOut *out);
+hipError_t launch_child_totals(hipStream_t st, const PartParent *parents,
+                               int32_t n_parents, const int32_t *parent_ids,
+                               const NodeSeg *segs, const unsigned long long *pool,
+                               int64_t node_stride, long long *totals);
+hipError_t launch_code_counts(hipStream_t st, const uint8_t *codes, int64_t ld,
+                              int64_t n, int32_t F, unsigned int *counts);
 hipError_t launch_update_F(hipStream_t st, const uint8_t *codes, int64_t ld,
                            int64_t n, const TreeNodeDev *tree,
                            int32_t node_count, double lr, double *F,

@@ -165,6 +165,33 @@ hipError_t launch_bin(hipStream_t st, const void *X, int is_f64, int64_t n,
   return hipGetLastError();
 }
 
+// Per-feature code counts of a matrix (for each feature's most frequent
+// bin).  Block (x, f) counts 64K rows of feature f in LDS.
+constexpr int kCountRows = 1 << 16;
+
+__global__ __launch_bounds__(256) void k_code_counts(const uint8_t *__restrict__ codes,
+                                                     int64_t ld, int64_t n,
+                                                     unsigned int *__restrict__ counts) {
+  __shared__ unsigned int c[256];
+  const int f = (int)blockIdx.y;
+  c[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t r0 = (int64_t)blockIdx.x * kCountRows;
+  const int64_t r1 = min(n, r0 + kCountRows);
+  const uint8_t *col = codes + (int64_t)f * ld;
+  for (int64_t r = r0 + threadIdx.x; r < r1; r += 256) atomicAdd(&c[col[r]], 1u);
+  __syncthreads();
+  if (c[threadIdx.x]) atomicAdd(&counts[f * 256 + threadIdx.x], c[threadIdx.x]);
+}
+
+hipError_t launch_code_counts(hipStream_t st, const uint8_t *codes, int64_t ld,
+                              int64_t n, int32_t F, unsigned int *counts) {
+  if (n <= 0) return hipSuccess;
+  const dim3 grid((unsigned)((n + kCountRows - 1) / kCountRows), (unsigned)F);
+  hipLaunchKernelGGL(k_code_counts, grid, dim3(256), 0, st, codes, ld, n, counts);
+  return hipGetLastError();
+}
+
 // Row-major uint8/uint16 codes -> feature-major uint8 (values above 255
 // become 255).
 template <typename T>
@@ -452,8 +479,9 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
     const int2 *__restrict__ gh_c, const HistTask *__restrict__ tasks,
     int32_t n_tasks, const int32_t *__restrict__ hist_node,
     const NodeSeg *__restrict__ segs, const int32_t *__restrict__ nb_sel,
-    int32_t F_sel, int32_t nchunks, int32_t tile_rows,
-    unsigned long long *__restrict__ pool, int64_t node_stride) {
+    const int32_t *__restrict__ hot_sel, int32_t F_sel, int32_t nchunks,
+    int32_t tile_rows, unsigned long long *__restrict__ pool,
+    int64_t node_stride) {
   __shared__ unsigned long long lh[FC * kHistPerFeat];
   const int b = (int)blockIdx.x;
   const int j = b >> 3;
@@ -471,9 +499,16 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
   const int64_t r1 = min(rend, r0 + (int64_t)tile_rows);
   const int f0 = chunk * FC;
   const int nf = min(FC, F_sel - f0);
-  uint32_t lim[FC];
+  uint32_t lim[FC], hb[FC];
+  long long ag[FC], ah[FC];
 #pragma unroll
-  for (int u = 0; u < FC; ++u) lim[u] = (u < nf) ? (uint32_t)(nb_sel[f0 + u] - 1) : 0u;
+  for (int u = 0; u < FC; ++u) {
+    lim[u] = (u < nf) ? (uint32_t)(nb_sel[f0 + u] - 1) : 0u;
+    // hot_sel < 0 (no frequent bin) becomes 0xffffffff: never matches.
+    hb[u] = (u < nf) ? (uint32_t)hot_sel[f0 + u] : 0xffffffffu;
+    ag[u] = 0;
+    ah[u] = 0;
+  }
   for (int i = threadIdx.x; i < FC * kHistPerFeat; i += kHistBlock) lh[i] = 0ull;
   __syncthreads();
 
@@ -505,12 +540,35 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
 #pragma unroll
         for (int k = 0; k < kHistRows; ++k) {
           const uint32_t bin = min((cw[k >> 2] >> (8 * (k & 3))) & 255u, lim[u]);
-          __hip_atomic_fetch_add(hf + 2 * bin, (unsigned long long)(long long)gq[k],
-                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-          __hip_atomic_fetch_add(hf + 2 * bin + 1, (unsigned long long)(long long)hq[k],
-                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          // The feature's most frequent bin (NaN, zeros) is summed in
+          // registers: same-address LDS atomics within a wave serialise.
+          if (bin == hb[u]) {
+            ag[u] += gq[k];
+            ah[u] += hq[k];
+          } else {
+            __hip_atomic_fetch_add(hf + 2 * bin, (unsigned long long)(long long)gq[k],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_fetch_add(hf + 2 * bin + 1, (unsigned long long)(long long)hq[k],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
         }
       }
+    }
+  }
+  // Hot-bin sums: wave reduction, then one LDS add per wave.
+#pragma unroll
+  for (int u = 0; u < FC; ++u) {
+    long long a = ag[u], c = ah[u];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      a += __shfl_xor(a, o, 64);
+      c += __shfl_xor(c, o, 64);
+    }
+    if (u < nf && hb[u] != 0xffffffffu && lane_id() == 0 && (a | c)) {
+      __hip_atomic_fetch_add(lh + u * kHistPerFeat + 2 * hb[u], (unsigned long long)a,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_fetch_add(lh + u * kHistPerFeat + 2 * hb[u] + 1, (unsigned long long)c,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   }
   __syncthreads();
@@ -529,15 +587,16 @@ hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int2 *gh_c, const HistTask *tasks,
                        int32_t n_tasks, const int32_t *hist_node,
                        const NodeSeg *segs, const int32_t *nb_sel,
-                       int32_t F_sel, int32_t fchunk, int32_t tile_rows,
-                       unsigned long long *pool, int64_t node_stride) {
+                       const int32_t *hot_sel, int32_t F_sel, int32_t fchunk,
+                       int32_t tile_rows, unsigned long long *pool,
+                       int64_t node_stride) {
   if (n_tasks <= 0) return hipSuccess;
   const int32_t nchunks = (F_sel + fchunk - 1) / fchunk;
   const dim3 grid((unsigned)hist_blocks(n_tasks, nchunks));
 #define BSSCL_HIST(FC)                                                              \
   hipLaunchKernelGGL(k_hist<FC>, grid, dim3(kHistBlock), 0, st, codes_c, ld_c, gh_c, \
-                     tasks, n_tasks, hist_node, segs, nb_sel, F_sel, nchunks,       \
-                     tile_rows, pool, node_stride)
+                     tasks, n_tasks, hist_node, segs, nb_sel, hot_sel, F_sel,       \
+                     nchunks, tile_rows, pool, node_stride)
   switch (fchunk) {
     case 1: BSSCL_HIST(1); break;
     case 2: BSSCL_HIST(2); break;
@@ -605,6 +664,7 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scan(
     int64_t *__restrict__ parent_nleft, NodeSeg *__restrict__ segs,
     int32_t *__restrict__ hist_node, int32_t min_samples_leaf,
     unsigned long long *__restrict__ pool, int64_t node_stride) {
+  // pool == nullptr: the children's histograms are not needed.
   __shared__ uint32_t tmp[kPartBlock / 64];
   const int p = (int)blockIdx.x;
   const PartParent P = parents[p];
@@ -622,7 +682,7 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scan(
   const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
   const bool left_small = nl <= nr;
   const int32_t small_id = left_small ? P.left_id : P.right_id;
-  if (ok) {
+  if (ok && pool) {
     unsigned long long *h = pool + (int64_t)small_id * node_stride;
     for (int64_t i = threadIdx.x; i < node_stride; i += kPartBlock) h[i] = 0ull;
   }
@@ -663,7 +723,7 @@ hipError_t launch_part_scan(hipStream_t st, const PartParent *parents,
 // (left run, then right run), so the global stores are consecutive: codes
 // as whole dwords (bytes only at the two ends of each run), (g,h) and row
 // ids as consecutive elements.
-constexpr int kScatterFeat = 64;  // features staged in LDS at a time
+constexpr int kScatterFeat = 16;  // features staged in LDS at a time
 
 __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
     const uint8_t *__restrict__ codes_src, uint8_t *__restrict__ codes_dst,
@@ -675,7 +735,10 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
   __shared__ uint32_t tmp[kPartBlock / 64];
   __shared__ int2 gh_s[kPartTile];
   __shared__ int32_t rid_s[kPartTile];
-  __shared__ uint8_t cs[kScatterFeat * kPartTile];
+  // Staged codes of up to kScatterFeat features, read back as (possibly
+  // unaligned) dwords: 8 bytes of slack past the last feature.
+  __shared__ uint32_t cs32[(kScatterFeat * kPartTile + 8) / 4];
+  uint8_t *cs = reinterpret_cast<uint8_t *>(cs32);
   const PartTile t = tiles[blockIdx.x];
   const PartParent P = parents[t.parent];
   int64_t lo, hi;
@@ -746,26 +809,29 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
         rid_dst[d] = rid_s[i];
       }
     }
-    for (int i = threadIdx.x; i < nf * per_f; i += kPartBlock) {
-      const int u = i / per_f, r = i - u * per_f;
+    for (int r = threadIdx.x; r < per_f; r += kPartBlock) {
       const bool left = r < nld;
       const int64_t q = left ? lq0 + r : rq0 + (r - nld);
       const int64_t run0 = left ? lbase : rbase;
       const int run_len = left ? ltot : rtot;
       const int soff = left ? 0 : ltot;
       const int64_t p0 = q << 2;
-      const uint8_t *src = cs + u * kPartTile + soff;
-      uint8_t *dcol = codes_dst + (int64_t)(f0 + u) * ld_c;
-      if (p0 >= run0 && p0 + 4 <= run0 + run_len) {
-        const int o = (int)(p0 - run0);
-        const uint32_t v = (uint32_t)src[o] | ((uint32_t)src[o + 1] << 8) |
-                           ((uint32_t)src[o + 2] << 16) | ((uint32_t)src[o + 3] << 24);
-        *reinterpret_cast<uint32_t *>(dcol + p0) = v;
-      } else {
+      const bool full = p0 >= run0 && p0 + 4 <= run0 + run_len;
+      for (int u = 0; u < nf; ++u) {
+        uint8_t *dcol = codes_dst + (int64_t)(f0 + u) * ld_c;
+        const int sbase = u * kPartTile + soff;
+        if (full) {
+          // Four staged bytes starting at an arbitrary LDS byte offset.
+          const int a = sbase + (int)(p0 - run0);
+          const uint32_t lo32 = cs32[a >> 2], hi32 = cs32[(a >> 2) + 1];
+          const uint32_t v = __builtin_amdgcn_alignbyte(hi32, lo32, (uint32_t)(a & 3));
+          *reinterpret_cast<uint32_t *>(dcol + p0) = v;
+        } else {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int64_t pp = p0 + k;
-          if (pp >= run0 && pp < run0 + run_len) dcol[pp] = src[pp - run0];
+          for (int k = 0; k < 4; ++k) {
+            const int64_t pp = p0 + k;
+            if (pp >= run0 && pp < run0 + run_len) dcol[pp] = cs[sbase + (int)(pp - run0)];
+          }
         }
       }
     }
@@ -904,13 +970,66 @@ hipError_t launch_split(hipStream_t st, const SplitTask *tasks, int32_t n_tasks,
   return hipGetLastError();
 }
 
+// Children that can never be split (they are at max_depth) need only their
+// gradient/hessian totals: the parent's histogram of the split feature
+// summed up to the split bin (left) and the rest (right).  One wave per
+// parent.
+__global__ __launch_bounds__(256) void k_child_totals(
+    const PartParent *__restrict__ parents, int32_t n_parents,
+    const int32_t *__restrict__ parent_ids, const NodeSeg *__restrict__ segs,
+    const unsigned long long *__restrict__ pool, int64_t node_stride,
+    long long *__restrict__ totals) {
+  const int w = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
+  const int lane = lane_id();
+  if (w >= n_parents) return;
+  const PartParent P = parents[w];
+  if (!segs[P.left_id].valid) return;
+  const long long *h = reinterpret_cast<const long long *>(pool) +
+                       (int64_t)parent_ids[w] * node_stride + (int64_t)P.fpos * kHistPerFeat;
+  long long gl = 0, hl = 0, gt = 0, ht = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int b = lane * 4 + k;
+    const long long g = h[2 * b], hh = h[2 * b + 1];
+    gt += g;
+    ht += hh;
+    if (b <= P.bin) {
+      gl += g;
+      hl += hh;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    gl += __shfl_xor(gl, o, 64);
+    hl += __shfl_xor(hl, o, 64);
+    gt += __shfl_xor(gt, o, 64);
+    ht += __shfl_xor(ht, o, 64);
+  }
+  if (lane == 0) {
+    totals[2 * (int64_t)P.left_id] = gl;
+    totals[2 * (int64_t)P.left_id + 1] = hl;
+    totals[2 * (int64_t)P.right_id] = gt - gl;
+    totals[2 * (int64_t)P.right_id + 1] = ht - hl;
+  }
+}
+
+hipError_t launch_child_totals(hipStream_t st, const PartParent *parents,
+                               int32_t n_parents, const int32_t *parent_ids,
+                               const NodeSeg *segs, const unsigned long long *pool,
+                               int64_t node_stride, long long *totals) {
+  if (n_parents <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_child_totals, dim3((unsigned)((n_parents + 3) / 4)), dim3(256), 0,
+                     st, parents, n_parents, parent_ids, segs, pool, node_stride, totals);
+  return hipGetLastError();
+}
+
 // Per node: the best split over features -- the largest gain, the lowest
 // feature position on ties (est:618-621) -- with the node's segment and
 // fixed-point totals, packed for one readback per level.
 __global__ __launch_bounds__(256) void k_node_best(
     const NodeSeg *__restrict__ segs, const long long *__restrict__ totals,
     const SplitCand *__restrict__ cand, int32_t F_sel, int32_t first,
-    int32_t count, NodeOut *__restrict__ out) {
+    int32_t count, int32_t no_split, NodeOut *__restrict__ out) {
   const int w = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
   const int lane = lane_id();
   if (w >= count) return;
@@ -918,7 +1037,7 @@ __global__ __launch_bounds__(256) void k_node_best(
   const NodeSeg s = segs[node];
   double best = 0.0;
   int32_t bf = -1, bb = 0;
-  if (s.valid) {
+  if (s.valid && !no_split) {
     for (int f = lane; f < F_sel; f += 64) {
       const SplitCand c = cand[(int64_t)node * F_sel + f];
       if (c.bin >= 0 && (bf < 0 || c.gain > best)) {
@@ -955,10 +1074,10 @@ __global__ __launch_bounds__(256) void k_node_best(
 hipError_t launch_node_best(hipStream_t st, const NodeSeg *segs,
                             const long long *totals, const SplitCand *cand,
                             int32_t F_sel, int32_t first, int32_t count,
-                            NodeOut *out) {
+                            int32_t no_split, NodeOut *out) {
   if (count <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_node_best, dim3((unsigned)((count + 3) / 4)), dim3(256), 0,
-                     st, segs, totals, cand, F_sel, first, count, out);
+                     st, segs, totals, cand, F_sel, first, count, no_split, out);
   return hipGetLastError();
 }
 

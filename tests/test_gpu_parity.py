@@ -162,6 +162,9 @@ def _lockstep_case(engine, n, F, seed, n_bins, max_leaves, max_depth, msl, mcw,
     dict(n=500, F=10, seed=6, n_bins=112, max_leaves=15, max_depth=3, msl=5, mcw=1.0, lam=1.0),
     dict(n=2000, F=4, seed=7, n_bins=64, max_leaves=1, max_depth=6, msl=5, mcw=1.0, lam=1.0),
     dict(n=50, F=3, seed=8, n_bins=8, max_leaves=31, max_depth=6, msl=40, mcw=1.0, lam=1.0),
+    dict(n=30000, F=12, seed=9, n_bins=255, max_leaves=63, max_depth=8, msl=5, mcw=1.0, lam=1.0, nan=0.7),
+    dict(n=5000, F=5, seed=10, n_bins=64, max_leaves=31, max_depth=1, msl=5, mcw=1.0, lam=1.0),
+    dict(n=60000, F=30, seed=11, n_bins=255, max_leaves=255, max_depth=12, msl=2, mcw=0.5, lam=1.0, nan=0.05),
 ])
 def test_build_tree_lockstep(engine, case):
     _announce(f"lockstep {case}")
