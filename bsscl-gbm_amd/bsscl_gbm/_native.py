@@ -45,6 +45,7 @@ _SIGS = {
                              _i32, _P],
     "bsscl_sampler_next": [_P, _P, _P],
     "bsscl_sampler_state": [_P, _P, _P],
+    "bsscl_sampler_stats": [_P, _P, _i32, _P],
     "bsscl_sampler_destroy": [_P],
     "bsscl_engine_set_profiling": [_P, _i32],
     "bsscl_engine_stats": [_P, _P, _i32, _P],
@@ -316,6 +317,12 @@ class Sampler:
         pos = np.zeros(1, np.int32)
         check(lib().bsscl_sampler_state(self.handle, ptr(key), ptr(pos)))
         return key, int(pos[0])
+
+    def stats(self):
+        out = np.zeros(3, np.float64)
+        n = np.zeros(1, np.int32)
+        check(lib().bsscl_sampler_stats(self.handle, ptr(out), 3, ptr(n)))
+        return dict(rounds=out[0], draw_ms=out[1], swap_ms=out[2])
 
     def close(self):
         if getattr(self, "_h", None) is not None:

@@ -35,7 +35,10 @@
 
 #include <hip/hip_runtime.h>
 
+#include <sys/mman.h>
+
 #include <algorithm>
+#include <chrono>
 #include <condition_variable>
 #include <cstdlib>
 #include <cstring>
@@ -198,6 +201,27 @@ struct HostBuf {
   }
 };
 
+// Array backed by 2 MB pages where the kernel allows it: the swap loop makes
+// one random access per step into an array of up to 40 MB, and 4 KB pages
+// would add a TLB miss to most of them.
+template <typename T>
+struct BigArray {
+  T *p = nullptr;
+  size_t n = 0;
+  void alloc(size_t count) {
+    const size_t huge = size_t(2) << 20;
+    const size_t bytes = (count * sizeof(T) + huge - 1) / huge * huge;
+    void *q = std::aligned_alloc(huge, bytes);
+    if (!q) throw std::bad_alloc();
+    (void)madvise(q, bytes, MADV_HUGEPAGE);
+    p = static_cast<T *>(q);
+    n = count;
+  }
+  ~BigArray() { std::free(p); }
+  T &operator[](size_t i) { return p[i]; }
+  T *data() { return p; }
+};
+
 }  // namespace
 
 struct Sampler {
@@ -229,7 +253,9 @@ struct Sampler {
   std::string error;
 
   // Cumulative permutations (swap thread only).
-  std::vector<int32_t> rows, feats;
+  BigArray<int32_t> rows;
+  std::vector<int32_t> feats;
+  double draw_ms = 0.0, swap_ms = 0.0;  // time spent in each stage
 
   void run_draws() {
     try {
@@ -244,6 +270,7 @@ struct Sampler {
             draw_pool.pop_back();
           }
         }
+        const auto t0 = std::chrono::steady_clock::now();
         if (do_rows) {
           d.rows.resize((size_t)n);
           mt.draws((uint64_t)(n - 1), d.rows.data());
@@ -252,8 +279,10 @@ struct Sampler {
           d.feats.resize((size_t)F);
           mt.draws((uint64_t)(F - 1), d.feats.data());
         }
+        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         {
           std::lock_guard<std::mutex> lk(mu);
+          draw_ms += ms;
           drawn.push_back(std::move(d));
           ++n_drawn;
           if (n_drawn == n_rounds) {
@@ -271,7 +300,10 @@ struct Sampler {
     }
   }
 
-  void apply(const Draws &d, Round &r) {
+  // Applies one round's swaps and fills r; returns the milliseconds spent in
+  // the swap loops (the round buffer's first allocation is not counted).
+  double apply(const Draws &d, Round &r) {
+    const auto t0 = std::chrono::steady_clock::now();
     if (do_rows) {
       const uint32_t *j = d.rows.data();
       int32_t *a = rows.data();
@@ -288,10 +320,12 @@ struct Sampler {
       const uint32_t *j = d.feats.data();
       for (int32_t i = F - 1; i >= 1; --i) std::swap(feats[(size_t)i], feats[j[i]]);
     }
+    const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     r.rows.alloc((size_t)n_sub);
     std::memcpy(r.rows.p, rows.data(), (size_t)n_sub * sizeof(int32_t));
     r.feats.assign(feats.begin(), feats.begin() + f_sub);
     std::sort(r.feats.begin(), r.feats.end());
+    return ms;
   }
 
   void run_swaps() {
@@ -314,9 +348,10 @@ struct Sampler {
           }
         }
         cv.notify_all();
-        apply(d, r);
+        const double ms = apply(d, r);
         {
           std::lock_guard<std::mutex> lk(mu);
+          swap_ms += ms;
           ready.push_back(std::move(r));
           ++produced;
           draw_pool.push_back(std::move(d));
@@ -454,7 +489,7 @@ int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
   std::memcpy(s->final_key, key, sizeof(s->final_key));
   s->final_pos = pos;
   try {
-    s->rows.resize((size_t)n);
+    s->rows.alloc((size_t)n);
     for (int64_t i = 0; i < n; ++i) s->rows[(size_t)i] = (int32_t)i;
     s->feats.resize((size_t)n_features);
     for (int32_t j = 0; j < n_features; ++j) s->feats[(size_t)j] = j;
@@ -492,6 +527,18 @@ int bsscl_sampler_state(bsscl_sampler *hs, uint32_t *key_out,
     return bsscl::set_error(BSSCL_EINVAL, "sampler_state: sampler stopped early");
   std::memcpy(key_out, s->final_key, sizeof(s->final_key));
   *pos_out = s->final_pos;
+  return BSSCL_OK;
+}
+
+int bsscl_sampler_stats(bsscl_sampler *hs, double *out, int32_t cap,
+                        int32_t *n_out) {
+  Sampler *s = reinterpret_cast<Sampler *>(hs);
+  if (!s || !out || !n_out) return bsscl::set_error(BSSCL_EINVAL, "sampler_stats: bad arguments");
+  std::lock_guard<std::mutex> lk(s->mu);
+  const double v[3] = {(double)s->produced, s->draw_ms, s->swap_ms};
+  const int32_t k = std::min<int32_t>(cap, 3);
+  for (int32_t i = 0; i < k; ++i) out[i] = v[i];
+  *n_out = k;
   return BSSCL_OK;
 }
 

@@ -184,6 +184,10 @@ int bsscl_sampler_next(bsscl_sampler *s, int32_t *rows_out,
                        int32_t *feats_out);
 int bsscl_sampler_state(bsscl_sampler *s, uint32_t *key_out,
                         int32_t *pos_out);
+/* Host time of the sampler's stages (no reference counterpart): [0] rounds
+ * produced, [1] ms drawing bounded integers, [2] ms applying swaps. */
+int bsscl_sampler_stats(bsscl_sampler *s, double *out, int32_t cap,
+                        int32_t *n_out);
 void bsscl_sampler_destroy(bsscl_sampler *s);
 
 /*

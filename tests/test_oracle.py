@@ -1,7 +1,7 @@
 """Pins the oracle (oracle/oracle.c + oracle/model.py) to facts that do not
 come from the oracle itself: closed forms, brute force on small inputs,
-invariants of the reference's algorithm, and the values SURVEY-era analysis
-derived from the reference's parameter rules.  CPU only."""
+invariants of the reference's algorithm, and values derived by hand from
+the reference's parameter rules.  CPU only."""
 import numpy as np
 import pytest
 
