@@ -49,7 +49,8 @@ def build(verbose: bool = False) -> str:
     for src in SOURCES:
         path = os.path.join(CSRC, src)
         obj = os.path.join(OBJ_DIR, src + ".o")
-        lang = [] if src.endswith(".hip") else ["-x", "hip"]
+        # .cpp sources are host code that calls the HIP runtime only.
+        lang = [] if src.endswith(".hip") else ["-x", "hip", "--offload-host-only"]
         cmd = [cc, *flags(), *lang, "-c", path, "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)

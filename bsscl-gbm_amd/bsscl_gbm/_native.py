@@ -41,8 +41,10 @@ _SIGS = {
     "bsscl_partition": [_P, _P, _i64, _i32, _i32, _P, _P],
     "bsscl_rs_shuffle_i64": [_P, _P, _P, _i64],
     "bsscl_rs_shuffle_i32": [_P, _P, _P, _i64],
+    "bsscl_rs_draws": [_P, _P, _P, _i64],
+    "bsscl_fisher_yates_apply": [_P, _P, _i64, _P],
     "bsscl_sampler_create": [_P, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
-                             _i32, _P],
+                             _i32, _i32, _P],
     "bsscl_sampler_next": [_P, _P, _P],
     "bsscl_sampler_state": [_P, _P, _P],
     "bsscl_sampler_stats": [_P, _P, _i32, _P],
@@ -54,6 +56,9 @@ _VOID = {"bsscl_engine_destroy", "bsscl_sampler_destroy"}
 
 _lib = None
 _lock = threading.Lock()
+
+
+DEVICE_ROWS = 1  # BSSCL_SAMPLER_DEVICE_ROWS
 
 
 class EngineError(RuntimeError):
@@ -268,6 +273,16 @@ class Engine:
                                     int(bin_), ptr(out), ptr(nl)))
         return out, int(nl[0])
 
+    def fisher_yates_apply(self, draws, data):
+        """data (int32) permuted by the Fisher-Yates steps i = n-1 .. 1 with
+        draws[n-1-i] = j(i), on the GPU; returns the new array."""
+        a = np.ascontiguousarray(data, dtype=np.int32).copy()
+        d = np.ascontiguousarray(draws, dtype=np.uint32)
+        if len(a) > 1 and len(d) != len(a) - 1:
+            raise ValueError("draws must have len(data) - 1 entries")
+        check(lib().bsscl_fisher_yates_apply(self.handle, ptr(d), len(a), ptr(a)))
+        return a
+
     # -- profiling ------------------------------------------------------------
     def set_profiling(self, on):
         check(lib().bsscl_engine_set_profiling(self.handle, int(bool(on))))
@@ -286,7 +301,7 @@ class Sampler:
     """Row/column bagging stream identical to RandomState.shuffle calls."""
 
     def __init__(self, rng_state, n, n_sub, do_rows, n_features, f_sub,
-                 do_feats, n_rounds, lookahead=3):
+                 do_feats, n_rounds, lookahead=3, device_rows=False):
         name, key, pos = rng_state[0], rng_state[1], rng_state[2]
         if name != "MT19937":
             raise ValueError("RandomState must use MT19937")
@@ -296,6 +311,7 @@ class Sampler:
                                          int(bool(do_rows)), int(n_features),
                                          int(f_sub), int(bool(do_feats)),
                                          int(n_rounds), int(lookahead),
+                                         DEVICE_ROWS if device_rows else 0,
                                          ctypes.byref(h)))
         self._h = h
         self.n_sub, self.f_sub = int(n_sub), int(f_sub)
@@ -319,10 +335,10 @@ class Sampler:
         return key, int(pos[0])
 
     def stats(self):
-        out = np.zeros(3, np.float64)
+        out = np.zeros(4, np.float64)
         n = np.zeros(1, np.int32)
-        check(lib().bsscl_sampler_stats(self.handle, ptr(out), 3, ptr(n)))
-        return dict(rounds=out[0], draw_ms=out[1], swap_ms=out[2])
+        check(lib().bsscl_sampler_stats(self.handle, ptr(out), 4, ptr(n)))
+        return dict(rounds=out[0], draw_ms=out[1], swap_ms=out[2], gen_ms=out[3])
 
     def close(self):
         if getattr(self, "_h", None) is not None:
@@ -334,6 +350,16 @@ class Sampler:
             self.close()
         except Exception:
             pass
+
+
+def rs_draws(rng_state, n):
+    """The bounded draws of RandomState.shuffle of n items: d[n-1-i] = j(i)
+    for i = n-1 .. 1; returns (d, key, pos) with the advanced state."""
+    key = np.ascontiguousarray(rng_state[1], dtype=np.uint32).copy()
+    pos = np.array([rng_state[2]], np.int32)
+    d = np.empty(max(int(n) - 1, 0) + 1, np.uint32)
+    check(lib().bsscl_rs_draws(ptr(key), ptr(pos), ptr(d), int(n)))
+    return d[:max(int(n) - 1, 0)], key, int(pos[0])
 
 
 def rs_shuffle(rng_state, arr):

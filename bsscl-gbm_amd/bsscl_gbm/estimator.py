@@ -446,7 +446,8 @@ class HybridHistGBMNumbaV1_0_1:
         sampler = _native.Sampler(rng.get_state(), n_samples,
                                   n_sub if do_rows else n_samples, do_rows,
                                   n_features, f_sub if do_feats else n_features,
-                                  do_feats, int(self.n_estimators))
+                                  do_feats, int(self.n_estimators),
+                                  device_rows=True)
         best_val_loss = np.inf
         rounds_no_improve = 0
         hook = getattr(self, '_round_hook', None)

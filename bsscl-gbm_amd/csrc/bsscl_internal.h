@@ -13,10 +13,21 @@ namespace bsscl {
 int set_error(int code, const std::string &msg);
 
 // Sampler hand-off used by bsscl_boost_round (sampler.cpp).
-int sampler_take(bsscl_sampler *s, const int32_t **rows, const int32_t **feats,
-                 void **token);
+struct SamplerRound {
+  const uint32_t *draws;  // j(n-1-t) at [t], t < n-1 (row bagging), else null
+  const int32_t *rows;    // sample_idx[n_sub] (host-rows samplers), else null
+  const int32_t *feats;   // f_sub ascending feature indices
+  int32_t round;          // 0-based round number
+};
+struct SamplerShape {
+  int64_t n, n_sub;
+  int32_t f_sub;
+  bool do_rows, device_rows;
+};
+// Blocks until the next round is ready.  The buffers stay valid (and may be
+// read by copies in flight) until sampler_give_back(token).
+int sampler_take(bsscl_sampler *s, SamplerRound *out, void **token);
 void sampler_give_back(bsscl_sampler *s, void *token);
-int64_t sampler_n_sub(bsscl_sampler *s);
-int32_t sampler_f_sub(bsscl_sampler *s);
+SamplerShape sampler_shape(bsscl_sampler *s);
 
 }  // namespace bsscl

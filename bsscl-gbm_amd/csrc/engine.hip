@@ -16,9 +16,15 @@
 // non-increasing order of e(v) = min of the gains on the path from the root
 // to v (the node with the largest gain in the frontier always has the
 // largest e there).  A node v cannot be split if at least max_leaves-1 kept
-// splits u have e(u) > e(v), because all of those come first.  The level
-// loop expands every frontier node not excluded by that count; the replay
+// splits u have e(u) > e(v), because all of those come first.  Each level
+// expands every frontier node not excluded by that count; the replay
 // checks that every node it splits was expanded.
+//
+// The levels run without host round trips: a one-workgroup planner kernel
+// (k_plan) applies that rule on the device and writes the next level's
+// work lists, every level kernel reads its counts from the device plan and
+// is launched with an upper-bound grid, and the node table comes back to
+// the host once per tree for the replay.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -180,25 +186,45 @@ struct bsscl_engine {
   DevBuf<int32_t> rows32;
   DevBuf<int64_t> rows64;
   DevBuf<int32_t> rows_in, sort_tmp;
+  // Row permutation of a device-rows sampler (cumulative over its rounds)
+  // and the Fisher-Yates work arrays.
+  DevBuf<int32_t> perm[2];
+  int perm_cur = 0;
+  const void *perm_sampler = nullptr;
+  int32_t perm_next_round = 0;
+  DevBuf<uint32_t> fy_draws;
+  DevBuf<int32_t> fy_head, fy_next, fy_v;
   DevBuf<uint8_t> row_flags;  // all zero between rounds
   int64_t row_flags_n = 0;
+  // Node-indexed buffers (node_cap nodes) and the level lists the planner
+  // writes (see ensure_nodes / prepare_tree_buffers for their sizes).
   DevBuf<unsigned long long> pool;
-  int32_t node_cap = 0;
-  int64_t node_stride = 0;  // int64 words per node histogram
+  int32_t node_alloc = 0;      // nodes the node-indexed buffers were sized for
+  int32_t node_cap = 0;        // nodes usable at the current histogram width
+  int32_t node_cap_floor = 0;  // raised when a tree needed more nodes
+  int64_t node_stride = 0;     // int64 words per node histogram
   DevBuf<NodeSeg> segs;
   DevBuf<SplitCand> cand;
   DevBuf<long long> totals;
-  DevBuf<int32_t> tile_left_d, hist_node_d;
-  DevBuf<int64_t> tile_off_d, nleft_d;
-  DevBuf<char> lvl_d;                 // packed per-level inputs
+  DevBuf<char> table_d;               // [LevelPlan, padded to 64 B][NodeOut x node_cap]
+  char *table_pin = nullptr;          // pinned readback of table_d
+  size_t table_pin_bytes = 0;
+  LevelPlan *plan_d = nullptr;
+  NodeOut *nodes_d = nullptr;
+  DevBuf<PartParent> parents_d[2];    // by level parity
+  DevBuf<int32_t> tile_begin_d, hist_begin_d, work_flag_d, hist_node_d;
+  DevBuf<double> work_e_d;
+  DevBuf<SplitTask> split_tasks_d;
+  DevBuf<int64_t> nleft_d;
+  int32_t tile_cap = 0, hist_cap = 0;
+  DevBuf<PartTile> tiles_d;
+  DevBuf<int32_t> tile_left_d;
+  DevBuf<int64_t> tile_off_d;
+  DevBuf<HistTask> hist_tasks_d;
+  DevBuf<char> lvl_d;                 // packed inputs of the root (one upload per tree)
   const int32_t *nb_sel_d = nullptr;  // bin counts of the selected features
   const int32_t *hot_sel_d = nullptr; // most frequent bin of each selected feature
-  DevBuf<int32_t> nb_sel_buf;         // [nb_sel | hot_sel] kept for the tree
   std::vector<int32_t> hot_bin;       // most frequent code per feature of matrix 0
-  DevBuf<NodeOut> nodeout_d;          // packed per-level results
-  NodeOut *nodeout_pin = nullptr;     // pinned readback of nodeout_d
-  int32_t nodeout_pin_n = 0;
-  std::vector<NodeOut> nodeout_h;
   DevBuf<TreeNodeDev> tree_d;
   DevBuf<int32_t> offsets_d;
   DevBuf<double> partials_d, loss_d, out_d;
@@ -315,57 +341,57 @@ double fixed_mul(double max_abs) {
   return std::ldexp(1.0, 30 - e);
 }
 
-int ensure_nodeout(bsscl_engine *E, int32_t cap) {
-  CHK(E->nodeout_d.ensure((size_t)cap));
-  if (E->nodeout_pin_n < cap) {
-    if (E->nodeout_pin) (void)hipHostFree(E->nodeout_pin);
-    E->nodeout_pin = nullptr;
-    E->nodeout_pin_n = 0;
-    HIPCHK(hipHostMalloc(reinterpret_cast<void **>(&E->nodeout_pin),
-                         (size_t)cap * sizeof(NodeOut), hipHostMallocDefault));
-    E->nodeout_pin_n = cap;
-  }
-  return BSSCL_OK;
+// Nodes a tree of `levels` levels can hold: the full binary tree when it is
+// small, else room for about 8 * max_leaves (the node table grows if a tree
+// needs more).
+int32_t initial_node_cap(int32_t levels, int32_t max_leaves) {
+  const int64_t full = levels >= 20 ? (int64_t)1 << 21 : ((int64_t)2 << levels) - 1;
+  if (full <= 1023) return (int32_t)full;
+  return (int32_t)std::min<int64_t>(full, std::max<int64_t>(1023, 8 * (int64_t)max_leaves + 3));
 }
 
-int ensure_nodes(bsscl_engine *E, int32_t need, int32_t F_sel) {
+// Node-indexed buffers for `cap` nodes of F_sel features.  Contents do not
+// survive a reallocation (a tree is rebuilt from its root after one).
+int ensure_nodes(bsscl_engine *E, int32_t cap, int32_t F_sel) {
   const int64_t stride = (int64_t)F_sel * kHistPerFeat;
-  if (need <= E->node_cap && stride == E->node_stride) return BSSCL_OK;
-  int32_t cap = std::max<int32_t>(need, std::max<int32_t>(256, E->node_cap));
-  if (stride == E->node_stride && E->node_cap > 0 && need > E->node_cap) {
-    cap = std::max(need, E->node_cap * 2);
-    // Grow while keeping the histograms, segments and results built so far.
-    DevBuf<unsigned long long> pool2;
-    DevBuf<NodeSeg> segs2;
-    DevBuf<SplitCand> cand2;
-    DevBuf<long long> tot2;
-    CHK(pool2.ensure((size_t)cap * stride));
-    CHK(segs2.ensure((size_t)cap));
-    CHK(cand2.ensure((size_t)cap * F_sel));
-    CHK(tot2.ensure((size_t)cap * 2));
-    HIPCHK(hipMemcpyAsync(pool2.p, E->pool.p, (size_t)E->node_cap * stride * 8, hipMemcpyDeviceToDevice, E->st));
-    HIPCHK(hipMemcpyAsync(segs2.p, E->segs.p, (size_t)E->node_cap * sizeof(NodeSeg), hipMemcpyDeviceToDevice, E->st));
-    HIPCHK(hipMemcpyAsync(cand2.p, E->cand.p, (size_t)E->node_cap * F_sel * sizeof(SplitCand), hipMemcpyDeviceToDevice, E->st));
-    HIPCHK(hipMemcpyAsync(tot2.p, E->totals.p, (size_t)E->node_cap * 2 * sizeof(long long), hipMemcpyDeviceToDevice, E->st));
-    HIPCHK(hipStreamSynchronize(E->st));
-    E->pool.release();
-    E->segs.release();
-    E->cand.release();
-    E->totals.release();
-    E->pool = pool2;
-    E->segs = segs2;
-    E->cand = cand2;
-    E->totals = tot2;
-    E->node_cap = cap;
-    return ensure_nodeout(E, cap);
+  if (cap <= E->node_alloc && (size_t)cap * stride <= E->pool.cap &&
+      (size_t)cap * F_sel <= E->cand.cap) {
+    // Usable capacity: what every node-indexed buffer holds at this width.
+    E->node_cap = (int32_t)std::min<int64_t>(
+        E->node_alloc, std::min<int64_t>((int64_t)(E->pool.cap / (size_t)stride),
+                                         (int64_t)(E->cand.cap / (size_t)F_sel)));
+    E->node_stride = stride;
+    return BSSCL_OK;
   }
+  CHK(sync(E));
+  const int32_t pcap = cap / 2 + 2;
   CHK(E->pool.ensure((size_t)cap * stride));
   CHK(E->segs.ensure((size_t)cap));
   CHK(E->cand.ensure((size_t)cap * F_sel));
   CHK(E->totals.ensure((size_t)cap * 2));
+  const size_t tbytes = 64 + (size_t)cap * sizeof(NodeOut);
+  CHK(E->table_d.ensure(tbytes));
+  if (E->table_pin_bytes < tbytes) {
+    if (E->table_pin) (void)hipHostFree(E->table_pin);
+    E->table_pin = nullptr;
+    E->table_pin_bytes = 0;
+    HIPCHK(hipHostMalloc(reinterpret_cast<void **>(&E->table_pin), tbytes, hipHostMallocDefault));
+    E->table_pin_bytes = tbytes;
+  }
+  E->plan_d = reinterpret_cast<LevelPlan *>(E->table_d.p);
+  E->nodes_d = reinterpret_cast<NodeOut *>(E->table_d.p + 64);
+  for (int s = 0; s < 2; ++s) CHK(E->parents_d[s].ensure((size_t)pcap));
+  CHK(E->tile_begin_d.ensure((size_t)pcap + 1));
+  CHK(E->hist_begin_d.ensure((size_t)pcap + 1));
+  CHK(E->hist_node_d.ensure((size_t)pcap));
+  CHK(E->nleft_d.ensure((size_t)pcap));
+  CHK(E->work_flag_d.ensure((size_t)cap));
+  CHK(E->work_e_d.ensure((size_t)cap));
+  CHK(E->split_tasks_d.ensure((size_t)cap));
+  E->node_alloc = cap;
   E->node_cap = cap;
   E->node_stride = stride;
-  return ensure_nodeout(E, cap);
+  return BSSCL_OK;
 }
 
 // Feature chunk of a histogram block: 4 features (16 KB of LDS) keeps
@@ -376,15 +402,21 @@ int32_t hist_fchunk(bsscl_engine *E, int32_t F_sel) {
   return fc;
 }
 
+// Histogram row tiles wanted per level: about hist_blocks_per_cu blocks per
+// CU over all feature chunks.
+int32_t hist_target(bsscl_engine *E, int32_t F_sel) {
+  const int32_t fc = hist_fchunk(E, F_sel);
+  const int32_t nchunks = (F_sel + fc - 1) / fc;
+  return std::max<int32_t>(1, (E->hist_blocks_per_cu * E->n_cu + nchunks - 1) / nchunks);
+}
+
 // Rows per histogram tile for S rows: enough tiles for about
 // hist_blocks_per_cu blocks per CU, but never so many that flushed bins
 // (tiles * F_sel * 512 atomics) exceed ~5% of the LDS adds (S * F_sel * 2),
 // i.e. at most S/hist_rows_per_flush tiles.
+// (k_plan's plan_tile_rows computes the same on the device.)
 int32_t hist_tile_rows(bsscl_engine *E, int64_t S, int32_t F_sel) {
-  const int32_t fc = hist_fchunk(E, F_sel);
-  const int32_t nchunks = (F_sel + fc - 1) / fc;
-  int64_t tiles = std::max<int64_t>(
-      1, ((int64_t)E->hist_blocks_per_cu * E->n_cu + nchunks - 1) / nchunks);
+  int64_t tiles = hist_target(E, F_sel);
   tiles = std::min<int64_t>(tiles, std::max<int64_t>(1, S / E->hist_rows_per_flush));
   int64_t t = round_up((S + tiles - 1) / tiles, 4096);
   return (int32_t)std::min<int64_t>(std::max<int64_t>(t, 4096), 1 << 24);
@@ -422,62 +454,6 @@ int upload_pack(bsscl_engine *E, const Pack &pk, std::vector<char *> &dev) {
   HIPCHK(hipMemcpyAsync(E->lvl_d.p, stage, total, hipMemcpyHostToDevice, E->st));
   dev.resize(pk.parts.size());
   for (size_t i = 0; i < pk.parts.size(); ++i) dev[i] = E->lvl_d.p + off[i];
-  return BSSCL_OK;
-}
-
-int launch_hist_level(bsscl_engine *E, int set, const HistTask *tasks_d,
-                      int32_t n_tasks, int32_t F_sel, int32_t tile_rows) {
-  if (n_tasks <= 0) return BSSCL_OK;
-  hipEvent_t stop;
-  CHK(prof_begin(E, 0, &stop));
-  HIPCHK(launch_hist(E->st, E->codes_c[set].p, E->ld_c, E->gh_c[set].p, tasks_d,
-                     n_tasks, E->hist_node_d.p, E->segs.p, E->nb_sel_d, E->hot_sel_d,
-                     F_sel, hist_fchunk(E, F_sel), tile_rows, E->pool.p,
-                     E->node_stride));
-  CHK(prof_end(E, stop));
-  return BSSCL_OK;
-}
-
-int launch_split_level(bsscl_engine *E, const SplitTask *tasks_d, int32_t n_tasks,
-                       int32_t F_sel, const TreeParams &tp, int32_t first) {
-  if (n_tasks <= 0) return BSSCL_OK;
-  SplitParams sp;
-  sp.min_child_weight = tp.mcw;
-  sp.reg_lambda = tp.lam;
-  sp.g_scale = E->g_scale;
-  sp.h_scale = E->h_scale;
-  sp.min_samples_leaf = tp.min_samples_leaf;
-  sp.max_depth = tp.max_depth;
-  hipEvent_t stop;
-  CHK(prof_begin(E, 2, &stop));
-  HIPCHK(launch_split(E->st, tasks_d, n_tasks, E->segs.p, E->pool.p, E->node_stride,
-                      E->nb_sel_d, F_sel, sp, E->cand.p, E->totals.p));
-  HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, first,
-                          n_tasks, 0, E->nodeout_d.p));
-  CHK(prof_end(E, stop));
-  return BSSCL_OK;
-}
-
-// Reads the packed results of nodes [a, a+cnt) (one copy, one sync).
-int read_nodeouts(bsscl_engine *E, int32_t a, int32_t cnt, std::vector<HNode> &nodes) {
-  if (cnt <= 0) return BSSCL_OK;
-  E->nodeout_h.resize((size_t)cnt);
-  HIPCHK(hipMemcpyAsync(E->nodeout_pin, E->nodeout_d.p, (size_t)cnt * sizeof(NodeOut),
-                        hipMemcpyDeviceToHost, E->st));
-  CHK(sync(E));
-  const NodeOut *o = E->nodeout_pin;
-  for (int32_t i = 0; i < cnt; ++i) {
-    HNode &nd = nodes[(size_t)(a + i)];
-    nd.start = o[i].start;
-    nd.count = o[i].count;
-    nd.valid = o[i].valid != 0;
-    if (!nd.valid) continue;
-    nd.Gq = o[i].Gq;
-    nd.Hq = o[i].Hq;
-    nd.fpos = o[i].fpos;
-    nd.bin = o[i].bin;
-    nd.gain = o[i].gain;
-  }
   return BSSCL_OK;
 }
 
@@ -586,33 +562,6 @@ int replay(bsscl_engine *E, const std::vector<HNode> &nodes,
   return BSSCL_OK;
 }
 
-// Launches count / scan / scatter for one level: parents' rows in set `src`
-// move to their children's segments in set `dst`.
-int partition_level(bsscl_engine *E, int src, int dst, const PartParent *parents_d,
-                    int32_t n_parents, const int32_t *tile_begin_d,
-                    const PartTile *tiles_d, int32_t n_tiles, int32_t F_sel,
-                    int32_t min_samples_leaf, bool move_rows = true) {
-  CHK(E->tile_left_d.ensure((size_t)n_tiles));
-  CHK(E->tile_off_d.ensure((size_t)n_tiles));
-  CHK(E->nleft_d.ensure((size_t)n_parents));
-  CHK(E->hist_node_d.ensure((size_t)std::max(n_parents, 1)));
-  hipEvent_t stop;
-  CHK(prof_begin(E, 1, &stop));
-  HIPCHK(launch_part_count(E->st, E->codes_c[src].p, E->ld_c, parents_d, tiles_d,
-                           n_tiles, E->tile_left_d.p));
-  HIPCHK(launch_part_scan(E->st, parents_d, n_parents, tile_begin_d, E->tile_left_d.p,
-                          E->tile_off_d.p, E->nleft_d.p, E->segs.p, E->hist_node_d.p,
-                          min_samples_leaf, move_rows ? E->pool.p : nullptr,
-                          E->node_stride));
-  if (move_rows)
-    HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p, E->ld_c,
-                               E->gh_c[src].p, E->gh_c[dst].p, E->rid_c[src].p,
-                               E->rid_c[dst].p, parents_d, tiles_d, n_tiles,
-                               E->tile_off_d.p, E->nleft_d.p, F_sel));
-  CHK(prof_end(E, stop));
-  return BSSCL_OK;
-}
-
 void add_part_tiles(const PartParent &P, int32_t parent_index, std::vector<PartTile> &tiles) {
   const int64_t a = P.start & ~int64_t(3);
   for (int64_t r = a; r < P.start + P.count; r += kPartTile)
@@ -634,32 +583,68 @@ void read_hist_tuning(bsscl_engine *E) {
   E->hist_rows_per_flush = env_int("BSSCL_HIST_ROWS_PER_FLUSH", 256, 1 << 22, 5120);
 }
 
-int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel) {
-  CHK(sync(E));
+// Buffers of a tree over m rows: the compact sets, the node table for the
+// tree's levels and the level lists, whose capacities bound what the
+// planner may write (PartTile: m/1024 + 2 per parent; HistTask: the target
+// plus 2 per parent).
+int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t levels,
+                         int32_t max_leaves) {
   read_hist_tuning(E);
-  E->ld_c = round_up(m + 32, 256);
+  const int64_t ld_c = round_up(m + 32, 256);
+  bool grow = false;
+  for (int s = 0; s < 2; ++s)
+    grow = grow || E->codes_c[s].cap < (size_t)ld_c * F_sel || E->gh_c[s].cap < (size_t)ld_c ||
+           E->rid_c[s].cap < (size_t)ld_c;
+  const int32_t cap = std::max(initial_node_cap(levels, max_leaves), E->node_cap_floor);
+  const int64_t tcap = m / kPartTile + (int64_t)cap + 4;
+  const int64_t hcap = (int64_t)hist_target(E, F_sel) + cap + 4;
+  if (tcap > INT32_MAX / 2 || hcap > INT32_MAX / 2)
+    return set_error(BSSCL_EINVAL, "tree too large for the level lists");
+  grow = grow || E->tiles_d.cap < (size_t)tcap || E->hist_tasks_d.cap < (size_t)hcap;
+  if (grow) CHK(sync(E));
+  E->ld_c = ld_c;
   for (int s = 0; s < 2; ++s) {
-    CHK(E->codes_c[s].ensure((size_t)E->ld_c * F_sel));
-    CHK(E->gh_c[s].ensure((size_t)E->ld_c));
-    CHK(E->rid_c[s].ensure((size_t)E->ld_c));
+    CHK(E->codes_c[s].ensure((size_t)ld_c * F_sel));
+    CHK(E->gh_c[s].ensure((size_t)ld_c));
+    CHK(E->rid_c[s].ensure((size_t)ld_c));
   }
+  CHK(E->tiles_d.ensure((size_t)tcap));
+  CHK(E->tile_left_d.ensure((size_t)tcap));
+  CHK(E->tile_off_d.ensure((size_t)tcap));
+  CHK(E->hist_tasks_d.ensure((size_t)hcap));
+  E->tile_cap = (int32_t)tcap;
+  E->hist_cap = (int32_t)hcap;
   CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 16u << 20)));
-  CHK(ensure_nodes(E, 256, F_sel));
-  CHK(E->hist_node_d.ensure(256));
-  return BSSCL_OK;
+  return ensure_nodes(E, cap, F_sel);
 }
 
-// Root: gather the in-bag rows into set 0, histogram, split search.  The
-// feature list and the root's tasks go up in one packed copy.
-int build_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_t> &feats,
-               const std::vector<int32_t> &nb_sel, const TreeParams &tp,
-               std::vector<HNode> &nodes) {
+SplitParams split_params(bsscl_engine *E, const TreeParams &tp) {
+  SplitParams sp;
+  sp.min_child_weight = tp.mcw;
+  sp.reg_lambda = tp.lam;
+  sp.g_scale = E->g_scale;
+  sp.h_scale = E->h_scale;
+  sp.min_samples_leaf = tp.min_samples_leaf;
+  sp.max_depth = tp.max_depth;
+  return sp;
+}
+
+// Root: gather the in-bag rows into set 0, its histogram and split search.
+// The feature list, the root's tasks and its LevelPlan go up in one copy.
+int launch_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_t> &feats,
+                const std::vector<int32_t> &nb_sel, const TreeParams &tp) {
   const Matrix &X = E->mat[0];
   const int32_t F_sel = (int32_t)feats.size();
   const int32_t th = hist_tile_rows(E, m, F_sel);
   std::vector<HistTask> ht;
   for (int64_t t = 0; t * th < m; ++t) ht.push_back({0, (int32_t)t});
   const SplitTask st0{0, -1, -1, 0};
+  LevelPlan rp = {};
+  rp.n_hist = (int32_t)ht.size();
+  rp.n_split = 1;
+  rp.first_child = 0;
+  rp.tile_rows = th;
+  rp.n_nodes = 1;
   // Selected features' bin counts followed by their most frequent bins.
   std::vector<int32_t> nb_hot(2 * (size_t)F_sel);
   for (int32_t i = 0; i < F_sel; ++i) {
@@ -673,9 +658,12 @@ int build_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_t
   pk.add(nb_hot.data(), nb_hot.size() * 4);
   pk.add(ht.data(), ht.size() * sizeof(HistTask));
   pk.add(&st0, sizeof(SplitTask));
+  pk.add(&rp, sizeof(LevelPlan));
   std::vector<char *> dv;
   CHK(upload_pack(E, pk, dv));
+  HIPCHK(hipMemcpyAsync(E->plan_d, dv[4], sizeof(LevelPlan), hipMemcpyDeviceToDevice, E->st));
   const int32_t *feat_d = reinterpret_cast<const int32_t *>(dv[0]);
+  // The root's arena stays untouched until the next tree's upload.
   E->nb_sel_d = reinterpret_cast<const int32_t *>(dv[1]);
   E->hot_sel_d = E->nb_sel_d + F_sel;
   HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, feat_d, F_sel,
@@ -684,158 +672,205 @@ int build_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_t
                             E->codes_c[0].p, E->ld_c, E->gh_c[0].p, E->rid_c[0].p,
                             E->ld_c, E->segs.p, E->hist_node_d.p, E->pool.p,
                             E->node_stride));
-  CHK(launch_hist_level(E, 0, reinterpret_cast<const HistTask *>(dv[2]),
-                        (int32_t)ht.size(), F_sel, th));
-  if (E->prof) {
-    E->stats[2] += (double)m * F_sel;
-    E->stats[3] += (double)m * (F_sel + 8);
-  }
-  CHK(launch_split_level(E, reinterpret_cast<const SplitTask *>(dv[3]), 1, F_sel, tp, 0));
-  nodes.assign(1, HNode());
-  CHK(read_nodeouts(E, 0, 1, nodes));
-  nodes[0].e = nodes[0].gain;
+  hipEvent_t stop;
+  CHK(prof_begin(E, 0, &stop));
+  HIPCHK(launch_hist(E->st, E->codes_c[0].p, E->ld_c, E->gh_c[0].p,
+                     reinterpret_cast<const HistTask *>(dv[2]), E->plan_d, rp.n_hist,
+                     E->hist_node_d.p, E->segs.p, E->nb_sel_d, E->hot_sel_d, F_sel,
+                     hist_fchunk(E, F_sel), E->pool.p, E->node_stride));
+  CHK(prof_end(E, stop));
+  CHK(prof_begin(E, 2, &stop));
+  HIPCHK(launch_split(E->st, reinterpret_cast<const SplitTask *>(dv[3]), E->plan_d, 1,
+                      E->segs.p, E->pool.p, E->node_stride, E->nb_sel_d, F_sel,
+                      split_params(E, tp), E->cand.p, E->totals.p));
+  HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, E->plan_d, 1, 0,
+                          E->nodes_d));
+  CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
 
+// Largest number of parents level `level` can have.
+int32_t level_parents_bound(bsscl_engine *E, int32_t level) {
+  const int64_t full = level >= 30 ? INT32_MAX : (int64_t)1 << level;
+  return (int32_t)std::max<int64_t>(1, std::min<int64_t>(full, (E->node_cap - 1) / 2));
+}
+
+// The planner of level `level` (parents at that depth, rows in set level%2).
+int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParams &tp,
+                      int32_t F_sel) {
+  PlanArgs pa;
+  pa.gamma = tp.gamma;
+  pa.level = level;
+  pa.max_leaves = tp.max_leaves;
+  pa.last = last ? 1 : 0;
+  pa.node_cap = E->node_cap;
+  pa.tile_cap = E->tile_cap;
+  pa.hist_cap = E->hist_cap;
+  pa.hist_target = hist_target(E, F_sel);
+  pa.rows_per_flush = E->hist_rows_per_flush;
+  hipEvent_t stop;
+  CHK(prof_begin(E, 2, &stop));
+  HIPCHK(launch_plan(E->st, E->nodes_d, E->plan_d, E->parents_d[(level + 1) & 1].p,
+                     E->parents_d[level & 1].p, E->tile_begin_d.p, E->hist_begin_d.p,
+                     E->tiles_d.p, E->hist_tasks_d.p, E->split_tasks_d.p,
+                     E->work_flag_d.p, E->work_e_d.p, pa));
+  CHK(prof_end(E, stop));
+  return BSSCL_OK;
+}
+
+// Count / scan / scatter of one level's parents (rows of set src move to
+// their children's segments in set dst).
+int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parents,
+                     const int32_t *tile_begin, const PartTile *tiles, const LevelPlan *plan,
+                     int32_t max_parents, int32_t max_tiles, int32_t F_sel,
+                     int32_t min_samples_leaf, bool move_rows) {
+  hipEvent_t stop;
+  CHK(prof_begin(E, 1, &stop));
+  HIPCHK(launch_part_count(E->st, E->codes_c[src].p, E->ld_c, parents, tiles, plan,
+                           max_tiles, E->tile_left_d.p));
+  HIPCHK(launch_part_scan(E->st, parents, plan, std::min(max_parents, 1024), tile_begin,
+                          E->tile_left_d.p, E->tile_off_d.p, E->nleft_d.p, E->segs.p,
+                          E->hist_node_d.p, min_samples_leaf,
+                          move_rows ? E->pool.p : nullptr, E->node_stride));
+  if (move_rows)
+    HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p, E->ld_c,
+                               E->gh_c[src].p, E->gh_c[dst].p, E->rid_c[src].p,
+                               E->rid_c[dst].p, parents, tiles, plan, max_tiles,
+                               E->tile_off_d.p, E->nleft_d.p, F_sel));
+  CHK(prof_end(E, stop));
+  return BSSCL_OK;
+}
+
+// The kernels of level `level` after its planner.  Grids are upper bounds
+// from the level's depth; the kernels read the planned counts.  Children at
+// max_depth can never be split (est:775-777): they need their sizes and
+// totals only, so their rows are not moved and their histograms not built.
+int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
+                 const TreeParams &tp, int32_t F_sel) {
+  const int src = level & 1, dst = src ^ 1;
+  const PartParent *par = E->parents_d[level & 1].p;
+  const int32_t P = level_parents_bound(E, level);
+  const int32_t T = (int32_t)std::min<int64_t>(E->tile_cap, m / kPartTile + 2 * (int64_t)P + 1);
+  CHK(launch_partition(E, src, dst, par, E->tile_begin_d.p, E->tiles_d.p, E->plan_d, P, T,
+                       F_sel, tp.min_samples_leaf, !last));
+  hipEvent_t stop;
+  if (last) {
+    CHK(prof_begin(E, 2, &stop));
+    HIPCHK(launch_child_totals(E->st, par, E->plan_d, std::min(P, 4096), E->segs.p,
+                               E->pool.p, E->node_stride, E->totals.p));
+    HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, E->plan_d,
+                            std::min(2 * P, 4096), 1, E->nodes_d));
+    CHK(prof_end(E, stop));
+    return BSSCL_OK;
+  }
+  const int32_t H = (int32_t)std::min<int64_t>(E->hist_cap, (int64_t)hist_target(E, F_sel) + 2 * (int64_t)P + 2);
+  CHK(prof_begin(E, 0, &stop));
+  HIPCHK(launch_hist(E->st, E->codes_c[dst].p, E->ld_c, E->gh_c[dst].p, E->hist_tasks_d.p,
+                     E->plan_d, H, E->hist_node_d.p, E->segs.p, E->nb_sel_d, E->hot_sel_d,
+                     F_sel, hist_fchunk(E, F_sel), E->pool.p, E->node_stride));
+  CHK(prof_end(E, stop));
+  CHK(prof_begin(E, 2, &stop));
+  // About 4096 blocks of 4 (node, feature) waves at most; they stride.
+  const int32_t S = std::min(2 * P, std::max(1, 16384 / F_sel));
+  HIPCHK(launch_split(E->st, E->split_tasks_d.p, E->plan_d, S,
+                      E->segs.p, E->pool.p, E->node_stride, E->nb_sel_d, F_sel,
+                      split_params(E, tp), E->cand.p, E->totals.p));
+  HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, E->plan_d,
+                          std::min(2 * P, 4096), 0, E->nodes_d));
+  CHK(prof_end(E, stop));
+  return BSSCL_OK;
+}
+
+// Copies the plan and the first `n` nodes of the node table to the host.
+int read_table(bsscl_engine *E, int32_t n, LevelPlan &plan) {
+  const size_t bytes = 64 + (size_t)std::max(0, std::min(n, E->node_cap)) * sizeof(NodeOut);
+  HIPCHK(hipMemcpyAsync(E->table_pin, E->table_d.p, bytes, hipMemcpyDeviceToHost, E->st));
+  CHK(sync(E));
+  std::memcpy(&plan, E->table_pin, sizeof(LevelPlan));
+  return BSSCL_OK;
+}
+
+constexpr int32_t kLevelsPerCheck = 8;  // levels enqueued between host checks
+
 // Builds one tree from the rows already in E->rows32 (use32) or E->rows64,
-// with quantized gradients in E->ghq.  The level loop keeps nb_sel (uploaded
-// with the root) in the device arena, so the arena for level inputs is
-// separate (lvl2_d) from the root's.
+// with quantized gradients in E->ghq.  All levels are enqueued without host
+// round trips: the planner kernel chooses each level's parents on the
+// device, and the node table comes back once at the end (every
+// kLevelsPerCheck levels the host also checks whether the tree has ended).
 int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
                     const std::vector<int32_t> &feats,
                     const std::vector<int32_t> &nb_sel, const TreeParams &tp,
                     TreeOut &out, HNode *root_out = nullptr) {
   const int32_t F_sel = (int32_t)feats.size();
-  CHK(prepare_tree_buffers(E, m, F_sel));
-  std::vector<HNode> nodes;
-  CHK(build_root(E, use32, m, feats, nb_sel, tp, nodes));
-  if (root_out) *root_out = nodes[0];
-  // nb_sel/hot_sel must outlive the root's arena: copy to their own buffer.
-  CHK(E->nb_sel_buf.ensure(2 * (size_t)F_sel));
-  HIPCHK(hipMemcpyAsync(E->nb_sel_buf.p, E->nb_sel_d, 2 * (size_t)F_sel * 4,
-                        hipMemcpyDeviceToDevice, E->st));
-  E->nb_sel_d = E->nb_sel_buf.p;
-  E->hot_sel_d = E->nb_sel_buf.p + F_sel;
-
-  std::vector<int32_t> frontier;
-  if (nodes[0].fpos >= 0 && nodes[0].gain > tp.gamma) frontier.push_back(0);
-  int level = 0;
-  std::vector<PartParent> parents;
-  std::vector<PartTile> tiles;
-  std::vector<int32_t> tile_begin;
-  std::vector<HistTask> ht;
-  std::vector<SplitTask> stv;
-  std::vector<int32_t> exp;
-  while (!frontier.empty()) {
-    // Nodes that may still be split (see the file comment).
-    exp.clear();
-    for (int32_t v : frontier) {
-      int32_t kept_before = 0;
-      for (const HNode &u : nodes)
-        if (u.expanded && u.split_ok && u.e > nodes[(size_t)v].e) ++kept_before;
-      if (kept_before < tp.max_leaves - 1) exp.push_back(v);
-    }
-    if (exp.empty()) break;
-    const int32_t first_child = (int32_t)nodes.size();
-    const int32_t end_child = first_child + 2 * (int32_t)exp.size();
-    CHK(ensure_nodes(E, end_child, F_sel));
-    nodes.resize((size_t)end_child);
-    parents.clear();
-    tiles.clear();
-    tile_begin.clear();
-    int64_t ub_rows = 0;
-    for (size_t i = 0; i < exp.size(); ++i) {
-      HNode &v = nodes[(size_t)exp[i]];
-      v.left = first_child + 2 * (int32_t)i;
-      v.right = v.left + 1;
-      parents.push_back({v.start, v.count, v.fpos, v.bin, v.left, v.right});
-      tile_begin.push_back((int32_t)tiles.size());
-      add_part_tiles(parents.back(), (int32_t)i, tiles);
-      ub_rows += v.count / 2;
-    }
-    tile_begin.push_back((int32_t)tiles.size());
-    const int src = level & 1, dst = src ^ 1;
-    // Children at max_depth can never be split (est:775-777): they need
-    // their sizes and totals only, so their rows are not moved and their
-    // histograms are not built.
-    const bool last = nodes[(size_t)exp[0]].depth + 1 >= tp.max_depth;
-    if (last) {
-      std::vector<int32_t> pids(exp.begin(), exp.end());
-      Pack pk;
-      pk.add(parents.data(), parents.size() * sizeof(PartParent));
-      pk.add(tile_begin.data(), tile_begin.size() * 4);
-      pk.add(tiles.data(), tiles.size() * sizeof(PartTile));
-      pk.add(pids.data(), pids.size() * 4);
-      std::vector<char *> dv;
-      CHK(upload_pack(E, pk, dv));
-      const PartParent *pd = reinterpret_cast<const PartParent *>(dv[0]);
-      CHK(partition_level(E, src, dst, pd, (int32_t)parents.size(),
-                          reinterpret_cast<const int32_t *>(dv[1]),
-                          reinterpret_cast<const PartTile *>(dv[2]), (int32_t)tiles.size(),
-                          F_sel, tp.min_samples_leaf, false));
-      HIPCHK(launch_child_totals(E->st, pd, (int32_t)parents.size(),
-                                 reinterpret_cast<const int32_t *>(dv[3]), E->segs.p,
-                                 E->pool.p, E->node_stride, E->totals.p));
-      HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, first_child,
-                              end_child - first_child, 1, E->nodeout_d.p));
-    } else {
-      // Histograms of the smaller children: at most half of each parent.
-      const int32_t th = hist_tile_rows(E, ub_rows, F_sel);
-      ht.clear();
-      for (size_t i = 0; i < parents.size(); ++i)
-        for (int64_t t = 0; t * th < parents[i].count / 2 + 1; ++t)
-          ht.push_back({(int32_t)i, (int32_t)t});
-      stv.clear();
-      for (size_t i = 0; i < exp.size(); ++i) {
-        const HNode &v = nodes[(size_t)exp[i]];
-        stv.push_back({v.left, exp[i], v.right, v.depth + 1});
-        stv.push_back({v.right, exp[i], v.left, v.depth + 1});
+  const int32_t levels = std::max(1, tp.max_depth);
+  LevelPlan plan = {};
+  for (;;) {
+    CHK(prepare_tree_buffers(E, m, F_sel, levels, tp.max_leaves));
+    CHK(launch_root(E, use32, m, feats, nb_sel, tp));
+    int32_t run = 0;
+    for (int32_t d = 0; d < levels; ++d) {
+      const bool last = d + 1 >= tp.max_depth;
+      CHK(launch_level_plan(E, d, last, tp, F_sel));
+      if (d > 0 && d % kLevelsPerCheck == 0) {
+        CHK(read_table(E, 0, plan));
+        if (plan.n_parents == 0 || plan.overflow != 0) break;
       }
-      Pack pk;
-      pk.add(parents.data(), parents.size() * sizeof(PartParent));
-      pk.add(tile_begin.data(), tile_begin.size() * 4);
-      pk.add(tiles.data(), tiles.size() * sizeof(PartTile));
-      pk.add(ht.data(), ht.size() * sizeof(HistTask));
-      pk.add(stv.data(), stv.size() * sizeof(SplitTask));
-      std::vector<char *> dv;
-      CHK(upload_pack(E, pk, dv));
-      CHK(partition_level(E, src, dst, reinterpret_cast<const PartParent *>(dv[0]),
-                          (int32_t)parents.size(), reinterpret_cast<const int32_t *>(dv[1]),
-                          reinterpret_cast<const PartTile *>(dv[2]), (int32_t)tiles.size(),
-                          F_sel, tp.min_samples_leaf));
-      CHK(launch_hist_level(E, dst, reinterpret_cast<const HistTask *>(dv[3]),
-                            (int32_t)ht.size(), F_sel, th));
-      CHK(launch_split_level(E, reinterpret_cast<const SplitTask *>(dv[4]),
-                             (int32_t)stv.size(), F_sel, tp, first_child));
+      CHK(launch_level(E, d, last, m, tp, F_sel));
+      run = d + 1;
     }
-    CHK(read_nodeouts(E, first_child, end_child - first_child, nodes));
-    frontier.clear();
-    for (size_t i = 0; i < exp.size(); ++i) {
-      HNode &v = nodes[(size_t)exp[i]];
-      HNode &L = nodes[(size_t)v.left];
-      HNode &R = nodes[(size_t)v.right];
-      v.expanded = true;
-      v.nl = L.count;
-      v.nr = R.count;
-      v.split_ok = L.valid;
-      if (E->prof && v.split_ok && !last) {
+    const int64_t most = run >= 30 ? INT32_MAX : ((int64_t)2 << run) - 1;
+    CHK(read_table(E, (int32_t)std::min<int64_t>(most, E->node_cap), plan));
+    if (plan.overflow < 0) return set_error(BSSCL_EINTERNAL, "tree builder: level list overflow");
+    if (plan.overflow == 0) break;
+    // The node table was too small: grow it and build the tree again.
+    E->node_cap_floor = std::max(plan.overflow, 2 * E->node_cap);
+  }
+  const int32_t n = plan.n_nodes;
+  if (n < 1 || n > E->node_cap) return set_error(BSSCL_EINTERNAL, "tree builder: bad node count");
+  const NodeOut *t = reinterpret_cast<const NodeOut *>(E->table_pin + 64);
+  std::vector<HNode> nodes((size_t)n);
+  std::vector<int32_t> depth((size_t)n, 0);
+  for (int32_t i = 0; i < n; ++i) {
+    HNode &nd = nodes[(size_t)i];
+    const NodeOut &o = t[i];
+    nd.start = o.start;
+    nd.count = o.count;
+    nd.valid = o.valid != 0;
+    nd.Gq = o.Gq;
+    nd.Hq = o.Hq;
+    nd.fpos = o.fpos;
+    nd.bin = o.bin;
+    nd.gain = o.gain;
+    nd.e = o.e;
+    if (o.left >= 0) {
+      if (o.left <= i || o.left + 1 >= n)
+        return set_error(BSSCL_EINTERNAL, "tree builder: bad child link");
+      nd.expanded = true;
+      nd.left = o.left;
+      nd.right = o.left + 1;
+      nd.nl = t[o.left].count;
+      nd.nr = t[o.left + 1].count;
+      nd.split_ok = t[o.left].valid != 0;
+      nodes[(size_t)o.left].parent = nodes[(size_t)o.left + 1].parent = i;
+      depth[(size_t)o.left] = depth[(size_t)o.left + 1] = depth[(size_t)i] + 1;
+    }
+  }
+  if (root_out) *root_out = nodes[0];
+  if (E->prof) {
+    E->stats[2] += (double)m * F_sel;
+    E->stats[3] += (double)m * (F_sel + 8);
+    for (int32_t i = 0; i < n; ++i) {
+      const HNode &v = nodes[(size_t)i];
+      if (!v.expanded) continue;
+      E->stats[9] += 1.0;
+      if (v.split_ok && depth[(size_t)i] + 1 < tp.max_depth) {
         const int64_t ms = std::min(v.nl, v.nr);
         E->stats[2] += (double)ms * F_sel;
         E->stats[3] += (double)ms * (F_sel + 8);
       }
-      for (HNode *c : {&L, &R}) {
-        c->parent = exp[i];
-        c->depth = v.depth + 1;
-        if (!v.split_ok) continue;
-        c->e = std::min(c->gain, v.e);
-        if (c->fpos >= 0 && c->gain > tp.gamma)
-          frontier.push_back((int32_t)(c == &L ? v.left : v.right));
-      }
     }
-    if (E->prof) E->stats[9] += (double)exp.size();
-    ++level;
+    E->stats[8] += 1.0;
   }
-  if (E->prof) E->stats[8] += 1.0;
   return replay(E, nodes, feats, tp, out);
 }
 
@@ -1007,19 +1042,31 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->rows64.release();
   E->rows_in.release();
   E->sort_tmp.release();
+  for (int s = 0; s < 2; ++s) E->perm[s].release();
+  E->fy_draws.release();
+  E->fy_head.release();
+  E->fy_next.release();
+  E->fy_v.release();
   E->row_flags.release();
-  E->nb_sel_buf.release();
   E->lvl_d.release();
-  E->nodeout_d.release();
-  if (E->nodeout_pin) (void)hipHostFree(E->nodeout_pin);
+  E->table_d.release();
+  if (E->table_pin) (void)hipHostFree(E->table_pin);
   E->pool.release();
   E->segs.release();
   E->cand.release();
   E->totals.release();
-  E->tile_left_d.release();
+  for (int s = 0; s < 2; ++s) E->parents_d[s].release();
+  E->tile_begin_d.release();
+  E->hist_begin_d.release();
+  E->work_flag_d.release();
   E->hist_node_d.release();
-  E->tile_off_d.release();
+  E->work_e_d.release();
+  E->split_tasks_d.release();
   E->nleft_d.release();
+  E->tiles_d.release();
+  E->tile_left_d.release();
+  E->tile_off_d.release();
+  E->hist_tasks_d.release();
   E->tree_d.release();
   E->offsets_d.release();
   E->partials_d.release();
@@ -1197,31 +1244,30 @@ int bsscl_boost_round(bsscl_engine *E, bsscl_sampler *sampler,
   (void)max_bins;
   const Matrix &X = E->mat[0];
   HIPCHK(hipSetDevice(E->device));
-  const int64_t m = sampler_n_sub(sampler);
-  const int32_t fsub = sampler_f_sub(sampler);
+  const SamplerShape sh = sampler_shape(sampler);
+  const int64_t m = sh.n_sub;
+  if (sh.n != X.n) return set_error(BSSCL_EINVAL, "boost_round: sampler rows differ from matrix rows");
   // Gradients from the current F: |g| <= max(w0, w1), h <= max(w0, w1)/4.
   const double wmax = std::max(E->w0, E->w1);
   const double gm = fixed_mul(wmax), hm = fixed_mul(0.25 * wmax);
   E->g_scale = 1.0 / gm;
   E->h_scale = 1.0 / hm;
   HIPCHK(launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, gm, hm, E->ghq.p));
-  const int32_t *rows = nullptr, *feats_p = nullptr;
+  SamplerRound sr;
   void *token = nullptr;
   const auto t_wait0 = std::chrono::steady_clock::now();
-  CHK(sampler_take(sampler, &rows, &feats_p, &token));
+  CHK(sampler_take(sampler, &sr, &token));
   if (E->prof)
     E->stats[10] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_wait0).count();
   TreeOut out{out_features, out_thresholds, out_values, out_left, out_right,
               out_node_count, out_split_gains};
   std::vector<int32_t> feats, nb_sel;
-  int rc = validate_tree_args(E, feats_p, fsub, max_leaves, min_samples_leaf,
+  int rc = validate_tree_args(E, sr.feats, sh.f_sub, max_leaves, min_samples_leaf,
                               bin_counts, out, feats, nb_sel);
-  if (rc == BSSCL_OK && m > X.n) rc = set_error(BSSCL_EINVAL, "boost_round: sampler rows exceed matrix");
-  // The round's sample_idx (shuffled order, pinned host memory) -> device ->
-  // ascending row ids.
+  // The round's in-bag rows on the device, ascending: the reference's
+  // sample_idx (a prefix of the cumulative permutation) sorted.
   const int64_t n_pad = sort_rows_flag_bytes(X.n);
   if (rc == BSSCL_OK) rc = E->rows32.ensure((size_t)m);
-  if (rc == BSSCL_OK) rc = E->rows_in.ensure((size_t)m);
   if (rc == BSSCL_OK) rc = E->sort_tmp.ensure((size_t)(n_pad / 4096 + 1));
   if (rc == BSSCL_OK && E->row_flags_n != n_pad) {
     rc = E->row_flags.ensure((size_t)n_pad);
@@ -1232,10 +1278,46 @@ int bsscl_boost_round(bsscl_engine *E, bsscl_sampler *sampler,
     }
   }
   if (rc == BSSCL_OK) {
-    hipError_t e = hipMemcpyAsync(E->rows_in.p, rows, (size_t)m * 4, hipMemcpyHostToDevice, E->st);
-    if (e == hipSuccess)
-      e = launch_sort_rows(E->st, E->rows_in.p, m, E->row_flags.p, n_pad, E->sort_tmp.p, E->rows32.p);
-    if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("row upload: ") + hipGetErrorString(e));
+    hipError_t e = hipSuccess;
+    const int32_t *rows_d = nullptr;
+    if (!sh.do_rows) {
+      e = launch_iota(E->st, E->rows32.p, m);  // every row, in order
+    } else if (sh.device_rows) {
+      // Cumulative permutation: identity before the sampler's first round.
+      if (sr.round == 0) {
+        rc = E->perm[0].ensure((size_t)X.n);
+        if (rc == BSSCL_OK) rc = E->perm[1].ensure((size_t)X.n);
+        if (rc == BSSCL_OK) rc = E->fy_draws.ensure((size_t)X.n);
+        if (rc == BSSCL_OK) rc = E->fy_head.ensure((size_t)X.n);
+        if (rc == BSSCL_OK) rc = E->fy_next.ensure((size_t)X.n);
+        if (rc == BSSCL_OK) rc = E->fy_v.ensure((size_t)X.n);
+        if (rc == BSSCL_OK) {
+          E->perm_cur = 0;
+          E->perm_sampler = sampler;
+          E->perm_next_round = 0;
+          e = launch_iota(E->st, E->perm[0].p, X.n);
+        }
+      } else if (E->perm_sampler != sampler || E->perm_next_round != sr.round) {
+        rc = set_error(BSSCL_EINVAL, "boost_round: the sampler's earlier rounds did not run on this engine");
+      }
+      if (rc == BSSCL_OK && e == hipSuccess && X.n > 1)
+        e = hipMemcpyAsync(E->fy_draws.p, sr.draws, (size_t)(X.n - 1) * 4, hipMemcpyHostToDevice, E->st);
+      if (rc == BSSCL_OK && e == hipSuccess) {
+        const int nxt = E->perm_cur ^ 1;
+        e = launch_fisher_yates(E->st, E->fy_draws.p, X.n, E->perm[E->perm_cur].p,
+                                E->perm[nxt].p, E->fy_head.p, E->fy_next.p, E->fy_v.p);
+        E->perm_cur = nxt;
+        E->perm_next_round = sr.round + 1;
+        rows_d = E->perm[nxt].p;
+      }
+    } else {
+      rc = E->rows_in.ensure((size_t)m);
+      if (rc == BSSCL_OK) e = hipMemcpyAsync(E->rows_in.p, sr.rows, (size_t)m * 4, hipMemcpyHostToDevice, E->st);
+      rows_d = E->rows_in.p;
+    }
+    if (rc == BSSCL_OK && e == hipSuccess && rows_d)
+      e = launch_sort_rows(E->st, rows_d, m, E->row_flags.p, n_pad, E->sort_tmp.p, E->rows32.p);
+    if (rc == BSSCL_OK && e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("rows: ") + hipGetErrorString(e));
   }
   if (rc != BSSCL_OK) {
     (void)hipStreamSynchronize(E->st);
@@ -1379,9 +1461,11 @@ int bsscl_node_split(bsscl_engine *E, const double *grad, const double *hess,
   // The root of a tree build: histogram and split search of these rows.
   const int32_t F_sel = n_selected;
   TreeParams tp{1, 1, 0, min_child_weight, reg_lambda, 0.0};
-  CHK(prepare_tree_buffers(E, m, F_sel));
-  std::vector<HNode> nodes;
-  CHK(build_root(E, false, m, feats, nb_sel, tp, nodes));
+  CHK(prepare_tree_buffers(E, m, F_sel, 1, 2));
+  CHK(launch_root(E, false, m, feats, nb_sel, tp));
+  LevelPlan plan;
+  CHK(read_table(E, 1, plan));
+  const NodeOut root = *reinterpret_cast<const NodeOut *>(E->table_pin + 64);
   if (out_G || out_H) {
     std::vector<long long> h((size_t)E->node_stride);
     HIPCHK(hipMemcpyAsync(h.data(), E->pool.p, (size_t)E->node_stride * 8, hipMemcpyDeviceToHost, E->st));
@@ -1391,9 +1475,9 @@ int bsscl_node_split(bsscl_engine *E, const double *grad, const double *hess,
       if (out_H) out_H[i] = (double)h[(size_t)(2 * i + 1)] * E->h_scale;
     }
   }
-  if (out_gain) *out_gain = nodes[0].fpos >= 0 ? nodes[0].gain : -1e9;
-  if (out_feature) *out_feature = nodes[0].fpos >= 0 ? feats[(size_t)nodes[0].fpos] : -1;
-  if (out_bin) *out_bin = nodes[0].fpos >= 0 ? nodes[0].bin : 0;
+  if (out_gain) *out_gain = root.fpos >= 0 ? root.gain : -1e9;
+  if (out_feature) *out_feature = root.fpos >= 0 ? feats[(size_t)root.fpos] : -1;
+  if (out_bin) *out_bin = root.fpos >= 0 ? root.bin : 0;
   return BSSCL_OK;
 }
 
@@ -1415,7 +1499,7 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
   }
   CHK(E->rows64.ensure((size_t)m));
   HIPCHK(hipMemcpyAsync(E->rows64.p, rows, (size_t)m * 8, hipMemcpyHostToDevice, E->st));
-  CHK(prepare_tree_buffers(E, m, 1));
+  CHK(prepare_tree_buffers(E, m, 1, 1, 2));
   const int32_t f1 = feature;
   Pack pk;
   pk.add(&f1, 4);
@@ -1425,19 +1509,25 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
                             nullptr, E->rows64.p, m, E->ghq.p, E->codes_c[0].p, E->ld_c,
                             E->gh_c[0].p, E->rid_c[0].p, E->ld_c, E->segs.p,
                             E->hist_node_d.p, E->pool.p, E->node_stride));
-  const PartParent P{0, m, 0, bin, 1, 2};
+  const PartParent P{0, m, 0, bin, 1, 2, 0, 0};
   std::vector<PartTile> tiles;
   add_part_tiles(P, 0, tiles);
   const int32_t tb[2] = {0, (int32_t)tiles.size()};
+  LevelPlan lp = {};
+  lp.n_parents = 1;
+  lp.n_tiles = (int32_t)tiles.size();
   Pack pk2;
   pk2.add(&P, sizeof(P));
   pk2.add(tb, sizeof(tb));
   pk2.add(tiles.data(), tiles.size() * sizeof(PartTile));
-  CHK(sync(E));
+  pk2.add(&lp, sizeof(lp));
+  CHK(sync(E));  // the gather has read dv[0]: the arena may be reused
   CHK(upload_pack(E, pk2, dv));
-  CHK(partition_level(E, 0, 1, reinterpret_cast<const PartParent *>(dv[0]), 1,
-                      reinterpret_cast<const int32_t *>(dv[1]),
-                      reinterpret_cast<const PartTile *>(dv[2]), (int32_t)tiles.size(), 1, 0));
+  CHK(launch_partition(E, 0, 1, reinterpret_cast<const PartParent *>(dv[0]),
+                       reinterpret_cast<const int32_t *>(dv[1]),
+                       reinterpret_cast<const PartTile *>(dv[2]),
+                       reinterpret_cast<const LevelPlan *>(dv[3]), 1, (int32_t)tiles.size(),
+                       1, 0, true));
   std::vector<int32_t> r32((size_t)m);
   int64_t nl = 0;
   HIPCHK(hipMemcpyAsync(r32.data(), E->rid_c[1].p, (size_t)m * 4, hipMemcpyDeviceToHost, E->st));
@@ -1446,6 +1536,37 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
   for (int64_t k = 0; k < m; ++k) out_rows[k] = r32[(size_t)k];
   *out_n_left = nl;
   return BSSCL_OK;
+}
+
+int bsscl_fisher_yates_apply(bsscl_engine *E, const uint32_t *draws, int64_t n,
+                             int32_t *data) {
+  if (!E || n < 0 || n > INT32_MAX || (n > 0 && !data) || (n > 1 && !draws))
+    return set_error(BSSCL_EINVAL, "fisher_yates_apply: bad arguments");
+  for (int64_t t = 0; t + 1 < n; ++t)
+    if ((int64_t)draws[t] > n - 1 - t)
+      return set_error(BSSCL_EINVAL, "fisher_yates_apply: draw " + std::to_string(t) +
+                                         " exceeds its step " + std::to_string(n - 1 - t));
+  if (n <= 1) return BSSCL_OK;
+  HIPCHK(hipSetDevice(E->device));
+  DevBuf<int32_t> a, b, head, next, v;
+  DevBuf<uint32_t> d;
+  int rc = BSSCL_OK;
+  for (DevBuf<int32_t> *x : {&a, &b, &head, &next, &v})
+    if (rc == BSSCL_OK) rc = x->ensure((size_t)n);
+  if (rc == BSSCL_OK) rc = d.ensure((size_t)n);
+  hipError_t e = hipSuccess;
+  if (rc == BSSCL_OK) {
+    e = hipMemcpyAsync(a.p, data, (size_t)n * 4, hipMemcpyHostToDevice, E->st);
+    if (e == hipSuccess) e = hipMemcpyAsync(d.p, draws, (size_t)(n - 1) * 4, hipMemcpyHostToDevice, E->st);
+    if (e == hipSuccess) e = launch_fisher_yates(E->st, d.p, n, a.p, b.p, head.p, next.p, v.p);
+    if (e == hipSuccess) e = hipMemcpyAsync(data, b.p, (size_t)n * 4, hipMemcpyDeviceToHost, E->st);
+    if (e == hipSuccess) e = hipStreamSynchronize(E->st);
+    if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("fisher_yates_apply: ") + hipGetErrorString(e));
+  }
+  (void)hipStreamSynchronize(E->st);
+  for (DevBuf<int32_t> *x : {&a, &b, &head, &next, &v}) x->release();
+  d.release();
+  return rc;
 }
 
 int bsscl_engine_set_profiling(bsscl_engine *E, int32_t on) {

@@ -18,7 +18,7 @@ struct NodeSeg {
   int32_t is_small;  // 1 when its histogram is built, 0 when subtracted
 };
 
-// Parent split of one level (host -> device).
+// Parent split of one level.
 struct PartParent {
   int64_t start;
   int64_t count;
@@ -26,6 +26,35 @@ struct PartParent {
   int32_t bin;       // rows with code <= bin go left
   int32_t left_id;   // internal node ids of the children
   int32_t right_id;
+  int32_t node;      // the parent's own id
+  int32_t pad;
+};
+
+// Work counts of one level, written by the planner kernel (or uploaded for
+// the root) and read by every kernel of the level, whose grids are upper
+// bounds.
+struct LevelPlan {
+  int32_t n_parents;    // PartParent entries
+  int32_t n_tiles;      // PartTile entries
+  int32_t n_hist;       // HistTask entries
+  int32_t n_split;      // SplitTask entries = nodes created at this level
+  int32_t first_child;  // id of the first node created at this level
+  int32_t tile_rows;    // rows per HistTask tile
+  int32_t n_nodes;      // nodes in the tree after this level
+  int32_t overflow;     // nodes needed when the node table is too small, else 0
+};
+
+// Planner inputs that do not change within a tree.
+struct PlanArgs {
+  double gamma;
+  int32_t level;          // depth of the nodes that become parents
+  int32_t max_leaves;
+  int32_t last;           // their children are at max_depth
+  int32_t node_cap;       // node table capacity
+  int32_t tile_cap;       // PartTile capacity
+  int32_t hist_cap;       // HistTask capacity
+  int32_t hist_target;    // histogram row tiles wanted per level
+  int32_t rows_per_flush; // fewest rows per histogram tile flush
 };
 
 // One partition tile of a parent (host -> device).
@@ -79,17 +108,19 @@ struct TreeNodeDev {
 // are consecutive; rows outside the parent's segment are masked).
 constexpr int kPartTile = 1024;
 
-// A node's result after its split search, packed for readback.
+// The node table of a tree: a node's split search result (k_node_best),
+// its frontier rank and children (k_plan).  Read back once per tree.
 struct NodeOut {
   int64_t start;
   int64_t count;
   long long Gq;
   long long Hq;
   double gain;     // best gain (-1e9 when fpos < 0)
+  double e;        // smallest best gain on the path from the root
   int32_t fpos;    // best feature position, -1 when none qualifies
   int32_t bin;
-  int32_t valid;
-  int32_t pad;
+  int32_t valid;   // the parent's split was kept
+  int32_t left;    // id of the left child (right = left + 1), -1 if not expanded
 };
 
 // Launchers (kernels.hip).  All are asynchronous on `st`.
@@ -113,6 +144,12 @@ hipError_t launch_sort_rows(hipStream_t st, const int32_t *rows, int64_t m,
                             uint8_t *flags, int64_t n_pad, int32_t *block_tmp,
                             int32_t *out);
 int64_t sort_rows_flag_bytes(int64_t n);
+hipError_t launch_iota(hipStream_t st, int32_t *a, int64_t n);
+// a_new = a_old after the Fisher-Yates steps i = n-1 .. 1 with draws[t] =
+// j(n-1-t) <= n-1-t; head, next and v are int32[n] work arrays.
+hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
+                               const int32_t *a_old, int32_t *a_new, int32_t *head,
+                               int32_t *next, int32_t *v);
 hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               const int32_t *feat, int32_t F_sel,
                               const int32_t *rows32, const int64_t *rows64,
@@ -120,20 +157,24 @@ hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               int64_t ld_c, int2 *gh_c, int32_t *rid_c,
                               int64_t pad_to, NodeSeg *segs, int32_t *hist_node,
                               unsigned long long *root_hist, int64_t hist_words);
+// Level kernels take their work counts from a device LevelPlan; the grid
+// argument (blocks, tasks or parents) is an upper bound, and blocks loop
+// over the work with a grid stride, so any bound >= 1 gives the same result.
 hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int2 *gh_c, const HistTask *tasks,
-                       int32_t n_tasks, const int32_t *hist_node,
-                       const NodeSeg *segs, const int32_t *nb_sel,
-                       const int32_t *hot_sel, int32_t F_sel, int32_t fchunk,
-                       int32_t tile_rows, unsigned long long *pool,
-                       int64_t node_stride);
+                       const LevelPlan *plan, int32_t max_tasks,
+                       const int32_t *hist_node, const NodeSeg *segs,
+                       const int32_t *nb_sel, const int32_t *hot_sel,
+                       int32_t F_sel, int32_t fchunk,
+                       unsigned long long *pool, int64_t node_stride);
 int hist_blocks(int32_t n_tasks, int32_t nchunks);
 hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
                              int64_t ld_c, const PartParent *parents,
-                             const PartTile *tiles, int32_t n_tiles,
-                             int32_t *tile_left);
+                             const PartTile *tiles, const LevelPlan *plan,
+                             int32_t max_tiles, int32_t *tile_left);
 hipError_t launch_part_scan(hipStream_t st, const PartParent *parents,
-                            int32_t n_parents, const int32_t *tile_begin,
+                            const LevelPlan *plan, int32_t max_parents,
+                            const int32_t *tile_begin,
                             const int32_t *tile_left, int64_t *tile_left_off,
                             int64_t *parent_nleft, NodeSeg *segs,
                             int32_t *hist_node, int32_t min_samples_leaf,
@@ -143,22 +184,32 @@ hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                const int2 *gh_src, int2 *gh_dst,
                                const int32_t *rid_src, int32_t *rid_dst,
                                const PartParent *parents,
-                               const PartTile *tiles, int32_t n_tiles,
-                               const int64_t *tile_left_off,
+                               const PartTile *tiles, const LevelPlan *plan,
+                               int32_t max_tiles, const int64_t *tile_left_off,
                                const int64_t *parent_nleft, int32_t F_sel);
-hipError_t launch_split(hipStream_t st, const SplitTask *tasks, int32_t n_tasks,
+hipError_t launch_split(hipStream_t st, const SplitTask *tasks,
+                        const LevelPlan *plan, int32_t max_tasks,
                         const NodeSeg *segs, unsigned long long *pool,
                         int64_t node_stride, const int32_t *nb_sel,
                         int32_t F_sel, SplitParams p, SplitCand *cand,
                         long long *totals);
 hipError_t launch_node_best(hipStream_t st, const NodeSeg *segs,
                             const long long *totals, const SplitCand *cand,
-                            int32_t F_sel, int32_t first, int32_t count,
-                            int32_t no_split, NodeOut *out);
+                            int32_t F_sel, const LevelPlan *plan,
+                            int32_t max_nodes, int32_t no_split, NodeOut *nodes);
 hipError_t launch_child_totals(hipStream_t st, const PartParent *parents,
-                               int32_t n_parents, const int32_t *parent_ids,
+                               const LevelPlan *plan, int32_t max_parents,
                                const NodeSeg *segs, const unsigned long long *pool,
                                int64_t node_stride, long long *totals);
+// One workgroup: picks the level's parents among the nodes created by the
+// previous level and writes their PartParent, PartTile, HistTask and
+// SplitTask lists and the LevelPlan (see k_plan).
+hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
+                       const PartParent *prev_parents, PartParent *parents,
+                       int32_t *tile_begin, int32_t *hist_begin,
+                       PartTile *tiles, HistTask *hist_tasks,
+                       SplitTask *split_tasks, int32_t *work_flag,
+                       double *work_e, PlanArgs a);
 hipError_t launch_code_counts(hipStream_t st, const uint8_t *codes, int64_t ld,
                               int64_t n, int32_t F, unsigned int *counts);
 hipError_t launch_update_F(hipStream_t st, const uint8_t *codes, int64_t ld,

@@ -13,6 +13,8 @@
 // trees do not depend on atomic order or on the order of rows.
 #include "kernels.h"
 
+#include <algorithm>
+
 namespace bsscl {
 
 namespace {
@@ -455,6 +457,174 @@ hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
 }
 
 // ---------------------------------------------------------------------------
+// Fisher-Yates on the device: the swap half of the reference's bagging
+// shuffle (est:2506), given the draws j(i) made on the host.
+//
+// Step i (i = n-1 .. 1, in that order) swaps positions i and j(i) <= i, and
+// position i never changes after step i.  Let the steps that choose
+// position p (j(k) = p, k > p) be s_1 < ... < s_L; they run s_L first.  Then
+// position p holds a_old[p] until step s_L, and after step s_m it holds the
+// value that step s_m brought from position s_m, v(s_m), where
+//   v(k) = the value at position k just before step k
+//        = v(s_1(k)) if any step chose k before, else a_old[k].
+// So a_new[s_m] = v(s_{m+1}) for m < L, a_new[s_L] = a_old[p],
+// a_new[i] = v(i) when j(i) = i, and a_new[0] = v(0).
+//
+// Kernels: every step k with j(k) != k pushes itself on position j(k)'s
+// list (atomic exchange); each list is sorted ascending (head = s_1, links
+// s_m -> s_{m+1}, the last link encodes p as -2 - p); the chains
+// k -> s_1(k) -> ... strictly increase and are followed to their end for
+// v(k); a last pass writes a_new.  Every kernel is O(n) in total for any
+// draws (lists are merge-sorted), and the result is the sequential one.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_iota(int32_t *__restrict__ a, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    a[i] = (int32_t)i;
+}
+
+__global__ __launch_bounds__(256) void k_fill_i32(int32_t *__restrict__ a, int64_t n, int32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    a[i] = v;
+}
+
+// draws[t] = j(n-1-t) for t in [0, n-1).
+__global__ __launch_bounds__(256) void k_fy_push(const uint32_t *__restrict__ draws, int64_t n,
+                                                 int32_t *__restrict__ head,
+                                                 int32_t *__restrict__ next) {
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < n - 1;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t k = (int32_t)(n - 1 - t);
+    const int32_t p = (int32_t)draws[t];
+    if (p != k) next[k] = atomicExch(head + p, k);
+  }
+}
+
+// Ascending sort of the list starting at `h` (links in next[], -1 ends it).
+__device__ int32_t fy_list_sort(int32_t h, int32_t *__restrict__ next) {
+  int64_t L = 0;
+  for (int32_t x = h; x >= 0; x = next[x]) ++L;
+  if (L <= 1) return h;
+  if (L <= 16) {  // insertion into a new list
+    int32_t sorted = -1;
+    for (int32_t x = h; x >= 0;) {
+      const int32_t nx = next[x];
+      if (sorted < 0 || x < sorted) {
+        next[x] = sorted;
+        sorted = x;
+      } else {
+        int32_t y = sorted;
+        while (next[y] >= 0 && next[y] < x) y = next[y];
+        next[x] = next[y];
+        next[y] = x;
+      }
+      x = nx;
+    }
+    return sorted;
+  }
+  for (int64_t width = 1; width < L; width *= 2) {  // bottom-up merge sort
+    int32_t cur = h, new_head = -1, tail = -1;
+    while (cur >= 0) {
+      int32_t a = cur, at = cur;
+      for (int64_t k = 1; k < width && next[at] >= 0; ++k) at = next[at];
+      int32_t b = next[at];
+      next[at] = -1;
+      int32_t rest = -1;
+      if (b >= 0) {
+        int32_t bt = b;
+        for (int64_t k = 1; k < width && next[bt] >= 0; ++k) bt = next[bt];
+        rest = next[bt];
+        next[bt] = -1;
+      }
+      while (a >= 0 || b >= 0) {
+        int32_t take;
+        if (b < 0 || (a >= 0 && a < b)) {
+          take = a;
+          a = next[a];
+        } else {
+          take = b;
+          b = next[b];
+        }
+        if (tail < 0) new_head = take;
+        else next[tail] = take;
+        tail = take;
+      }
+      next[tail] = -1;
+      cur = rest;
+    }
+    h = new_head;
+  }
+  return h;
+}
+
+__global__ __launch_bounds__(256) void k_fy_sort(int32_t *__restrict__ head,
+                                                 int32_t *__restrict__ next, int64_t n) {
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < n;
+       p += (int64_t)gridDim.x * blockDim.x) {
+    int32_t h = head[p];
+    if (h < 0) continue;
+    h = fy_list_sort(h, next);
+    head[p] = h;
+    int32_t x = h;
+    while (next[x] >= 0) x = next[x];
+    next[x] = -2 - (int32_t)p;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_fy_resolve(const int32_t *__restrict__ head,
+                                                    const int32_t *__restrict__ a_old,
+                                                    int32_t *__restrict__ v, int64_t n) {
+  for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < n;
+       k += (int64_t)gridDim.x * blockDim.x) {
+    int32_t x = (int32_t)k;
+    for (int32_t h = head[x]; h >= 0; h = head[x]) x = h;
+    v[k] = a_old[x];
+  }
+}
+
+__global__ __launch_bounds__(256) void k_fy_final(const uint32_t *__restrict__ draws, int64_t n,
+                                                  const int32_t *__restrict__ next,
+                                                  const int32_t *__restrict__ v,
+                                                  const int32_t *__restrict__ a_old,
+                                                  int32_t *__restrict__ a_new) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    int32_t out;
+    if (i == 0 || (int64_t)draws[n - 1 - i] == i) {
+      out = v[i];
+    } else {
+      const int32_t g = next[i];
+      out = g >= 0 ? v[g] : a_old[-2 - g];
+    }
+    a_new[i] = out;
+  }
+}
+
+static unsigned elementwise_blocks(int64_t n) {
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 65536));
+}
+
+hipError_t launch_iota(hipStream_t st, int32_t *a, int64_t n) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_iota, dim3(elementwise_blocks(n)), dim3(256), 0, st, a, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
+                               const int32_t *a_old, int32_t *a_new, int32_t *head,
+                               int32_t *next, int32_t *v) {
+  if (n <= 0) return hipSuccess;
+  const dim3 g(elementwise_blocks(n)), b(256);
+  hipLaunchKernelGGL(k_fill_i32, g, b, 0, st, head, n, -1);
+  if (n > 1) hipLaunchKernelGGL(k_fy_push, g, b, 0, st, draws, n, head, next);
+  hipLaunchKernelGGL(k_fy_sort, g, b, 0, st, head, next, n);
+  hipLaunchKernelGGL(k_fy_resolve, g, b, 0, st, head, a_old, v, n);
+  hipLaunchKernelGGL(k_fy_final, g, b, 0, st, draws, n, next, v, a_old, a_new);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Histogram build (est:581-596, est:722-737).
 //
 // A work item is one row tile of a node and one chunk of FC selected
@@ -474,21 +644,13 @@ constexpr int kHistBlock = 256;
 constexpr int kHistRows = 16;  // rows per thread per step
 
 template <int FC>
-__global__ __launch_bounds__(kHistBlock) void k_hist(
-    const uint8_t *__restrict__ codes_c, int64_t ld_c,
-    const int2 *__restrict__ gh_c, const HistTask *__restrict__ tasks,
-    int32_t n_tasks, const int32_t *__restrict__ hist_node,
-    const NodeSeg *__restrict__ segs, const int32_t *__restrict__ nb_sel,
-    const int32_t *__restrict__ hot_sel, int32_t F_sel, int32_t nchunks,
-    int32_t tile_rows, unsigned long long *__restrict__ pool,
+__device__ __forceinline__ void hist_item(
+    unsigned long long *lh, const uint8_t *__restrict__ codes_c, int64_t ld_c,
+    const int2 *__restrict__ gh_c, const HistTask task, int chunk,
+    const int32_t *__restrict__ hist_node, const NodeSeg *__restrict__ segs,
+    const int32_t *__restrict__ nb_sel, const int32_t *__restrict__ hot_sel,
+    int32_t F_sel, int32_t tile_rows, unsigned long long *__restrict__ pool,
     int64_t node_stride) {
-  __shared__ unsigned long long lh[FC * kHistPerFeat];
-  const int b = (int)blockIdx.x;
-  const int j = b >> 3;
-  const int chunk = j % nchunks;
-  const int ti = (j / nchunks) * 8 + (b & 7);
-  if (ti >= n_tasks) return;
-  const HistTask task = tasks[ti];
   const int32_t node = hist_node[task.ref];
   if (node < 0) return;
   const NodeSeg seg = segs[node];
@@ -577,6 +739,30 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
     const unsigned long long v = lh[i];
     if (v) atomicAdd(dst + i, v);
   }
+  __syncthreads();  // lh is cleared again by the block's next item
+}
+
+template <int FC>
+__global__ __launch_bounds__(kHistBlock) void k_hist(
+    const uint8_t *__restrict__ codes_c, int64_t ld_c,
+    const int2 *__restrict__ gh_c, const HistTask *__restrict__ tasks,
+    const LevelPlan *__restrict__ plan, const int32_t *__restrict__ hist_node,
+    const NodeSeg *__restrict__ segs, const int32_t *__restrict__ nb_sel,
+    const int32_t *__restrict__ hot_sel, int32_t F_sel, int32_t nchunks,
+    unsigned long long *__restrict__ pool, int64_t node_stride) {
+  __shared__ unsigned long long lh[FC * kHistPerFeat];
+  const int32_t n_tasks = plan->n_hist;
+  const int32_t tile_rows = plan->tile_rows;
+  // The grid is a multiple of 8 * nchunks, so every block keeps its XCD
+  // (b & 7) and feature chunk as it strides.
+  for (int b = (int)blockIdx.x;; b += (int)gridDim.x) {
+    const int j = b >> 3;
+    const int ti = (j / nchunks) * 8 + (b & 7);
+    if ((j / nchunks) * 8 >= n_tasks) break;
+    if (ti >= n_tasks) continue;
+    hist_item<FC>(lh, codes_c, ld_c, gh_c, tasks[ti], j % nchunks, hist_node, segs,
+                  nb_sel, hot_sel, F_sel, tile_rows, pool, node_stride);
+  }
 }
 
 int hist_blocks(int32_t n_tasks, int32_t nchunks) {
@@ -585,18 +771,18 @@ int hist_blocks(int32_t n_tasks, int32_t nchunks) {
 
 hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int2 *gh_c, const HistTask *tasks,
-                       int32_t n_tasks, const int32_t *hist_node,
-                       const NodeSeg *segs, const int32_t *nb_sel,
-                       const int32_t *hot_sel, int32_t F_sel, int32_t fchunk,
-                       int32_t tile_rows, unsigned long long *pool,
-                       int64_t node_stride) {
-  if (n_tasks <= 0) return hipSuccess;
+                       const LevelPlan *plan, int32_t max_tasks,
+                       const int32_t *hist_node, const NodeSeg *segs,
+                       const int32_t *nb_sel, const int32_t *hot_sel,
+                       int32_t F_sel, int32_t fchunk,
+                       unsigned long long *pool, int64_t node_stride) {
+  if (max_tasks <= 0) return hipSuccess;
   const int32_t nchunks = (F_sel + fchunk - 1) / fchunk;
-  const dim3 grid((unsigned)hist_blocks(n_tasks, nchunks));
+  const dim3 grid((unsigned)hist_blocks(max_tasks, nchunks));
 #define BSSCL_HIST(FC)                                                              \
   hipLaunchKernelGGL(k_hist<FC>, grid, dim3(kHistBlock), 0, st, codes_c, ld_c, gh_c, \
-                     tasks, n_tasks, hist_node, segs, nb_sel, hot_sel, F_sel,       \
-                     nchunks, tile_rows, pool, node_stride)
+                     tasks, plan, hist_node, segs, nb_sel, hot_sel, F_sel, nchunks, \
+                     pool, node_stride)
   switch (fchunk) {
     case 1: BSSCL_HIST(1); break;
     case 2: BSSCL_HIST(2); break;
@@ -624,34 +810,37 @@ __device__ __forceinline__ void tile_rows(const PartTile &t, const PartParent &P
 __global__ __launch_bounds__(kPartBlock) void k_part_count(
     const uint8_t *__restrict__ codes_c, int64_t ld_c,
     const PartParent *__restrict__ parents, const PartTile *__restrict__ tiles,
-    int32_t *__restrict__ tile_left) {
+    const LevelPlan *__restrict__ plan, int32_t *__restrict__ tile_left) {
   __shared__ uint32_t tmp[kPartBlock / 64];
-  const PartTile t = tiles[blockIdx.x];
-  const PartParent P = parents[t.parent];
-  int64_t lo, hi;
-  tile_rows(t, P, lo, hi);
-  const int64_t row = t.row0 + 4 * (int64_t)threadIdx.x;
-  // A dword wholly past the segment is not read (it may lie past the buffer).
-  const uint32_t w = (row < hi && row + 4 > lo)
-      ? *reinterpret_cast<const uint32_t *>(codes_c + (int64_t)P.fpos * ld_c + row) : 0u;
-  uint32_t cnt = 0;
+  const int32_t n_tiles = plan->n_tiles;
+  for (int32_t ti = (int32_t)blockIdx.x; ti < n_tiles; ti += (int32_t)gridDim.x) {
+    const PartTile t = tiles[ti];
+    const PartParent P = parents[t.parent];
+    int64_t lo, hi;
+    tile_rows(t, P, lo, hi);
+    const int64_t row = t.row0 + 4 * (int64_t)threadIdx.x;
+    // A dword wholly past the segment is not read (it may lie past the buffer).
+    const uint32_t w = (row < hi && row + 4 > lo)
+        ? *reinterpret_cast<const uint32_t *>(codes_c + (int64_t)P.fpos * ld_c + row) : 0u;
+    uint32_t cnt = 0;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const bool in = (row + k >= lo) && (row + k < hi);
-    cnt += (in && ((w >> (8 * k)) & 255u) <= (uint32_t)P.bin) ? 1u : 0u;
+    for (int k = 0; k < 4; ++k) {
+      const bool in = (row + k >= lo) && (row + k < hi);
+      cnt += (in && ((w >> (8 * k)) & 255u) <= (uint32_t)P.bin) ? 1u : 0u;
+    }
+    uint32_t total;
+    block_excl_scan<kPartBlock>(cnt, tmp, total);
+    if (threadIdx.x == 0) tile_left[ti] = (int32_t)total;
   }
-  uint32_t total;
-  block_excl_scan<kPartBlock>(cnt, tmp, total);
-  if (threadIdx.x == 0) tile_left[blockIdx.x] = (int32_t)total;
 }
 
 hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
                              int64_t ld_c, const PartParent *parents,
-                             const PartTile *tiles, int32_t n_tiles,
-                             int32_t *tile_left) {
-  if (n_tiles <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_part_count, dim3((unsigned)n_tiles), dim3(kPartBlock), 0,
-                     st, codes_c, ld_c, parents, tiles, tile_left);
+                             const PartTile *tiles, const LevelPlan *plan,
+                             int32_t max_tiles, int32_t *tile_left) {
+  if (max_tiles <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_part_count, dim3((unsigned)max_tiles), dim3(kPartBlock), 0,
+                     st, codes_c, ld_c, parents, tiles, plan, tile_left);
   return hipGetLastError();
 }
 
@@ -659,58 +848,63 @@ hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
 // children's segments, whether the split is kept (est:678-683), which child
 // is the smaller one (est:701-709), and a zeroed histogram for that child.
 __global__ __launch_bounds__(kPartBlock) void k_part_scan(
-    const PartParent *__restrict__ parents, const int32_t *__restrict__ tile_begin,
+    const PartParent *__restrict__ parents, const LevelPlan *__restrict__ plan,
+    const int32_t *__restrict__ tile_begin,
     const int32_t *__restrict__ tile_left, int64_t *__restrict__ tile_left_off,
     int64_t *__restrict__ parent_nleft, NodeSeg *__restrict__ segs,
     int32_t *__restrict__ hist_node, int32_t min_samples_leaf,
     unsigned long long *__restrict__ pool, int64_t node_stride) {
   // pool == nullptr: the children's histograms are not needed.
   __shared__ uint32_t tmp[kPartBlock / 64];
-  const int p = (int)blockIdx.x;
-  const PartParent P = parents[p];
-  const int t0 = tile_begin[p], t1 = tile_begin[p + 1];
-  int64_t carry = 0;
-  for (int base = t0; base < t1; base += kPartBlock) {
-    const int t = base + (int)threadIdx.x;
-    const uint32_t v = (t < t1) ? (uint32_t)tile_left[t] : 0u;
-    uint32_t total;
-    const uint32_t pre = block_excl_scan<kPartBlock>(v, tmp, total);
-    if (t < t1) tile_left_off[t] = carry + pre;
-    carry += total;
+  const int32_t n_parents = plan->n_parents;
+  for (int p = (int)blockIdx.x; p < n_parents; p += (int)gridDim.x) {
+    const PartParent P = parents[p];
+    const int t0 = tile_begin[p], t1 = tile_begin[p + 1];
+    int64_t carry = 0;
+    for (int base = t0; base < t1; base += kPartBlock) {
+      const int t = base + (int)threadIdx.x;
+      const uint32_t v = (t < t1) ? (uint32_t)tile_left[t] : 0u;
+      uint32_t total;
+      const uint32_t pre = block_excl_scan<kPartBlock>(v, tmp, total);
+      if (t < t1) tile_left_off[t] = carry + pre;
+      carry += total;
+    }
+    const int64_t nl = carry, nr = P.count - carry;
+    const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
+    const bool left_small = nl <= nr;
+    const int32_t small_id = left_small ? P.left_id : P.right_id;
+    if (ok && pool) {
+      unsigned long long *h = pool + (int64_t)small_id * node_stride;
+      for (int64_t i = threadIdx.x; i < node_stride; i += kPartBlock) h[i] = 0ull;
+    }
+    if (threadIdx.x == 0) {
+      parent_nleft[p] = nl;
+      NodeSeg L, R;
+      L.start = P.start;
+      L.count = nl;
+      L.valid = ok ? 1 : 0;
+      L.is_small = left_small ? 1 : 0;
+      R.start = P.start + nl;
+      R.count = nr;
+      R.valid = ok ? 1 : 0;
+      R.is_small = left_small ? 0 : 1;
+      segs[P.left_id] = L;
+      segs[P.right_id] = R;
+      hist_node[p] = ok ? small_id : -1;
+    }
   }
-  const int64_t nl = carry, nr = P.count - carry;
-  const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
-  const bool left_small = nl <= nr;
-  const int32_t small_id = left_small ? P.left_id : P.right_id;
-  if (ok && pool) {
-    unsigned long long *h = pool + (int64_t)small_id * node_stride;
-    for (int64_t i = threadIdx.x; i < node_stride; i += kPartBlock) h[i] = 0ull;
-  }
-  if (threadIdx.x != 0) return;
-  parent_nleft[p] = nl;
-  NodeSeg L, R;
-  L.start = P.start;
-  L.count = nl;
-  L.valid = ok ? 1 : 0;
-  L.is_small = left_small ? 1 : 0;
-  R.start = P.start + nl;
-  R.count = nr;
-  R.valid = ok ? 1 : 0;
-  R.is_small = left_small ? 0 : 1;
-  segs[P.left_id] = L;
-  segs[P.right_id] = R;
-  hist_node[p] = ok ? small_id : -1;
 }
 
 hipError_t launch_part_scan(hipStream_t st, const PartParent *parents,
-                            int32_t n_parents, const int32_t *tile_begin,
+                            const LevelPlan *plan, int32_t max_parents,
+                            const int32_t *tile_begin,
                             const int32_t *tile_left, int64_t *tile_left_off,
                             int64_t *parent_nleft, NodeSeg *segs,
                             int32_t *hist_node, int32_t min_samples_leaf,
                             unsigned long long *pool, int64_t node_stride) {
-  if (n_parents <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_part_scan, dim3((unsigned)n_parents), dim3(kPartBlock), 0,
-                     st, parents, tile_begin, tile_left, tile_left_off,
+  if (max_parents <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_part_scan, dim3((unsigned)max_parents), dim3(kPartBlock), 0,
+                     st, parents, plan, tile_begin, tile_left, tile_left_off,
                      parent_nleft, segs, hist_node, min_samples_leaf, pool,
                      node_stride);
   return hipGetLastError();
@@ -730,7 +924,7 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
     int64_t ld_c, const int2 *__restrict__ gh_src, int2 *__restrict__ gh_dst,
     const int32_t *__restrict__ rid_src, int32_t *__restrict__ rid_dst,
     const PartParent *__restrict__ parents, const PartTile *__restrict__ tiles,
-    const int64_t *__restrict__ tile_left_off,
+    const LevelPlan *__restrict__ plan, const int64_t *__restrict__ tile_left_off,
     const int64_t *__restrict__ parent_nleft, int32_t F_sel) {
   __shared__ uint32_t tmp[kPartBlock / 64];
   __shared__ int2 gh_s[kPartTile];
@@ -739,103 +933,106 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
   // unaligned) dwords: 8 bytes of slack past the last feature.
   __shared__ uint32_t cs32[(kScatterFeat * kPartTile + 8) / 4];
   uint8_t *cs = reinterpret_cast<uint8_t *>(cs32);
-  const PartTile t = tiles[blockIdx.x];
-  const PartParent P = parents[t.parent];
-  int64_t lo, hi;
-  tile_rows(t, P, lo, hi);
-  const int64_t loff = tile_left_off[blockIdx.x];
-  const int64_t nl = parent_nleft[t.parent];
-  const int64_t lbase = P.start + loff;
-  const int64_t rbase = P.start + nl + ((lo - P.start) - loff);
-  const int64_t row = t.row0 + 4 * (int64_t)threadIdx.x;
-  const uint32_t w = (row < hi && row + 4 > lo)
-      ? *reinterpret_cast<const uint32_t *>(codes_src + (int64_t)P.fpos * ld_c + row) : 0u;
-  uint32_t lmask = 0, vmask = 0;
+  const int32_t n_tiles = plan->n_tiles;
+  for (int32_t ti = (int32_t)blockIdx.x; ti < n_tiles; ti += (int32_t)gridDim.x) {
+    const PartTile t = tiles[ti];
+    const PartParent P = parents[t.parent];
+    int64_t lo, hi;
+    tile_rows(t, P, lo, hi);
+    const int64_t loff = tile_left_off[ti];
+    const int64_t nl = parent_nleft[t.parent];
+    const int64_t lbase = P.start + loff;
+    const int64_t rbase = P.start + nl + ((lo - P.start) - loff);
+    const int64_t row = t.row0 + 4 * (int64_t)threadIdx.x;
+    const uint32_t w = (row < hi && row + 4 > lo)
+        ? *reinterpret_cast<const uint32_t *>(codes_src + (int64_t)P.fpos * ld_c + row) : 0u;
+    uint32_t lmask = 0, vmask = 0;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const bool in = (row + k >= lo) && (row + k < hi);
-    vmask |= (in ? 1u : 0u) << k;
-    lmask |= ((in && ((w >> (8 * k)) & 255u) <= (uint32_t)P.bin) ? 1u : 0u) << k;
-  }
-  const uint32_t packed = ((uint32_t)__builtin_popcount(vmask) << 16) | (uint32_t)__builtin_popcount(lmask);
-  uint32_t tot;
-  const uint32_t pre = block_excl_scan<kPartBlock>(packed, tmp, tot);
-  const int ltot = (int)(tot & 0xffffu), vtot = (int)(tot >> 16);
-  const int rtot = vtot - ltot;
-  const int lpre = (int)(pre & 0xffffu), rpre = (int)(pre >> 16) - lpre;
-  int sidx[4];
-  int li = 0, ri = 0;
+    for (int k = 0; k < 4; ++k) {
+      const bool in = (row + k >= lo) && (row + k < hi);
+      vmask |= (in ? 1u : 0u) << k;
+      lmask |= ((in && ((w >> (8 * k)) & 255u) <= (uint32_t)P.bin) ? 1u : 0u) << k;
+    }
+    const uint32_t packed = ((uint32_t)__builtin_popcount(vmask) << 16) | (uint32_t)__builtin_popcount(lmask);
+    uint32_t tot;
+    const uint32_t pre = block_excl_scan<kPartBlock>(packed, tmp, tot);
+    const int ltot = (int)(tot & 0xffffu), vtot = (int)(tot >> 16);
+    const int rtot = vtot - ltot;
+    const int lpre = (int)(pre & 0xffffu), rpre = (int)(pre >> 16) - lpre;
+    int sidx[4];
+    int li = 0, ri = 0;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const bool v = (vmask >> k) & 1u, l = (lmask >> k) & 1u;
-    sidx[k] = !v ? -1 : (l ? lpre + li : ltot + rpre + ri);
-    li += l ? 1 : 0;
-    ri += (v && !l) ? 1 : 0;
-  }
-  if (vmask) {
-    const int4 *gp = reinterpret_cast<const int4 *>(gh_src + row);
-    const int4 ga = gp[0], gb = gp[1];
-    const int4 ra = *reinterpret_cast<const int4 *>(rid_src + row);
-    const int2 ghv[4] = {make_int2(ga.x, ga.y), make_int2(ga.z, ga.w),
-                         make_int2(gb.x, gb.y), make_int2(gb.z, gb.w)};
-    const int32_t rv[4] = {ra.x, ra.y, ra.z, ra.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (sidx[k] >= 0) {
-        gh_s[sidx[k]] = ghv[k];
-        rid_s[sidx[k]] = rv[k];
-      }
-  }
-  // Output dwords of the left run [lbase, lbase+ltot) and the right run.
-  const int64_t lq0 = lbase >> 2, rq0 = rbase >> 2;
-  const int nld = ltot ? (int)(((lbase + ltot + 3) >> 2) - lq0) : 0;
-  const int nrd = rtot ? (int)(((rbase + rtot + 3) >> 2) - rq0) : 0;
-  const int per_f = nld + nrd;
-  for (int f0 = 0; f0 < F_sel; f0 += kScatterFeat) {
-    const int nf = min(kScatterFeat, F_sel - f0);
+    for (int k = 0; k < 4; ++k) {
+      const bool v = (vmask >> k) & 1u, l = (lmask >> k) & 1u;
+      sidx[k] = !v ? -1 : (l ? lpre + li : ltot + rpre + ri);
+      li += l ? 1 : 0;
+      ri += (v && !l) ? 1 : 0;
+    }
     if (vmask) {
-      for (int u = 0; u < nf; ++u) {
-        const uint32_t c = *reinterpret_cast<const uint32_t *>(codes_src + (int64_t)(f0 + u) * ld_c + row);
+      const int4 *gp = reinterpret_cast<const int4 *>(gh_src + row);
+      const int4 ga = gp[0], gb = gp[1];
+      const int4 ra = *reinterpret_cast<const int4 *>(rid_src + row);
+      const int2 ghv[4] = {make_int2(ga.x, ga.y), make_int2(ga.z, ga.w),
+                           make_int2(gb.x, gb.y), make_int2(gb.z, gb.w)};
+      const int32_t rv[4] = {ra.x, ra.y, ra.z, ra.w};
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (sidx[k] >= 0) cs[u * kPartTile + sidx[k]] = (uint8_t)(c >> (8 * k));
-      }
+      for (int k = 0; k < 4; ++k)
+        if (sidx[k] >= 0) {
+          gh_s[sidx[k]] = ghv[k];
+          rid_s[sidx[k]] = rv[k];
+        }
     }
-    __syncthreads();
-    if (f0 == 0) {
-      for (int i = threadIdx.x; i < vtot; i += kPartBlock) {
-        const int64_t d = i < ltot ? lbase + i : rbase + (i - ltot);
-        gh_dst[d] = gh_s[i];
-        rid_dst[d] = rid_s[i];
-      }
-    }
-    for (int r = threadIdx.x; r < per_f; r += kPartBlock) {
-      const bool left = r < nld;
-      const int64_t q = left ? lq0 + r : rq0 + (r - nld);
-      const int64_t run0 = left ? lbase : rbase;
-      const int run_len = left ? ltot : rtot;
-      const int soff = left ? 0 : ltot;
-      const int64_t p0 = q << 2;
-      const bool full = p0 >= run0 && p0 + 4 <= run0 + run_len;
-      for (int u = 0; u < nf; ++u) {
-        uint8_t *dcol = codes_dst + (int64_t)(f0 + u) * ld_c;
-        const int sbase = u * kPartTile + soff;
-        if (full) {
-          // Four staged bytes starting at an arbitrary LDS byte offset.
-          const int a = sbase + (int)(p0 - run0);
-          const uint32_t lo32 = cs32[a >> 2], hi32 = cs32[(a >> 2) + 1];
-          const uint32_t v = __builtin_amdgcn_alignbyte(hi32, lo32, (uint32_t)(a & 3));
-          *reinterpret_cast<uint32_t *>(dcol + p0) = v;
-        } else {
+    // Output dwords of the left run [lbase, lbase+ltot) and the right run.
+    const int64_t lq0 = lbase >> 2, rq0 = rbase >> 2;
+    const int nld = ltot ? (int)(((lbase + ltot + 3) >> 2) - lq0) : 0;
+    const int nrd = rtot ? (int)(((rbase + rtot + 3) >> 2) - rq0) : 0;
+    const int per_f = nld + nrd;
+    for (int f0 = 0; f0 < F_sel; f0 += kScatterFeat) {
+      const int nf = min(kScatterFeat, F_sel - f0);
+      if (vmask) {
+        for (int u = 0; u < nf; ++u) {
+          const uint32_t c = *reinterpret_cast<const uint32_t *>(codes_src + (int64_t)(f0 + u) * ld_c + row);
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const int64_t pp = p0 + k;
-            if (pp >= run0 && pp < run0 + run_len) dcol[pp] = cs[sbase + (int)(pp - run0)];
+          for (int k = 0; k < 4; ++k)
+            if (sidx[k] >= 0) cs[u * kPartTile + sidx[k]] = (uint8_t)(c >> (8 * k));
+        }
+      }
+      __syncthreads();
+      if (f0 == 0) {
+        for (int i = threadIdx.x; i < vtot; i += kPartBlock) {
+          const int64_t d = i < ltot ? lbase + i : rbase + (i - ltot);
+          gh_dst[d] = gh_s[i];
+          rid_dst[d] = rid_s[i];
+        }
+      }
+      for (int r = threadIdx.x; r < per_f; r += kPartBlock) {
+        const bool left = r < nld;
+        const int64_t q = left ? lq0 + r : rq0 + (r - nld);
+        const int64_t run0 = left ? lbase : rbase;
+        const int run_len = left ? ltot : rtot;
+        const int soff = left ? 0 : ltot;
+        const int64_t p0 = q << 2;
+        const bool full = p0 >= run0 && p0 + 4 <= run0 + run_len;
+        for (int u = 0; u < nf; ++u) {
+          uint8_t *dcol = codes_dst + (int64_t)(f0 + u) * ld_c;
+          const int sbase = u * kPartTile + soff;
+          if (full) {
+            // Four staged bytes starting at an arbitrary LDS byte offset.
+            const int a = sbase + (int)(p0 - run0);
+            const uint32_t lo32 = cs32[a >> 2], hi32 = cs32[(a >> 2) + 1];
+            const uint32_t v = __builtin_amdgcn_alignbyte(hi32, lo32, (uint32_t)(a & 3));
+            *reinterpret_cast<uint32_t *>(dcol + p0) = v;
+          } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const int64_t pp = p0 + k;
+              if (pp >= run0 && pp < run0 + run_len) dcol[pp] = cs[sbase + (int)(pp - run0)];
+            }
           }
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
@@ -844,13 +1041,13 @@ hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                const int2 *gh_src, int2 *gh_dst,
                                const int32_t *rid_src, int32_t *rid_dst,
                                const PartParent *parents,
-                               const PartTile *tiles, int32_t n_tiles,
-                               const int64_t *tile_left_off,
+                               const PartTile *tiles, const LevelPlan *plan,
+                               int32_t max_tiles, const int64_t *tile_left_off,
                                const int64_t *parent_nleft, int32_t F_sel) {
-  if (n_tiles <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_part_scatter, dim3((unsigned)n_tiles), dim3(kPartBlock),
+  if (max_tiles <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_part_scatter, dim3((unsigned)max_tiles), dim3(kPartBlock),
                      0, st, codes_src, codes_dst, ld_c, gh_src, gh_dst, rid_src,
-                     rid_dst, parents, tiles, tile_left_off, parent_nleft,
+                     rid_dst, parents, tiles, plan, tile_left_off, parent_nleft,
                      F_sel);
   return hipGetLastError();
 }
@@ -865,107 +1062,110 @@ hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
 // ---------------------------------------------------------------------------
 #pragma clang fp contract(off)
 __global__ __launch_bounds__(256) void k_split(
-    const SplitTask *__restrict__ tasks, int32_t n_tasks,
+    const SplitTask *__restrict__ tasks, const LevelPlan *__restrict__ plan,
     const NodeSeg *__restrict__ segs, unsigned long long *__restrict__ pool,
     int64_t node_stride, const int32_t *__restrict__ nb_sel, int32_t F_sel,
     SplitParams P, SplitCand *__restrict__ cand, long long *__restrict__ totals) {
-  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = lane_id();
-  if (gw >= (int64_t)n_tasks * F_sel) return;
-  const int ti = (int)(gw / F_sel), fpos = (int)(gw % F_sel);
-  const SplitTask t = tasks[ti];
-  const NodeSeg s = segs[t.node];
-  if (!s.valid) return;
-  long long *hn = reinterpret_cast<long long *>(pool) + (int64_t)t.node * node_stride +
-                  (int64_t)fpos * kHistPerFeat + lane * 8;
-  long long g[4], h[4];
-  if (t.parent >= 0 && !s.is_small) {
-    const long long *hp = reinterpret_cast<const long long *>(pool) +
-                          (int64_t)t.parent * node_stride + (int64_t)fpos * kHistPerFeat + lane * 8;
-    const long long *hs = reinterpret_cast<const long long *>(pool) +
-                          (int64_t)t.sibling * node_stride + (int64_t)fpos * kHistPerFeat + lane * 8;
+  const int64_t n_waves = (int64_t)plan->n_split * F_sel;
+  for (int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); gw < n_waves;
+       gw += (int64_t)gridDim.x * 4) {
+    const int ti = (int)(gw / F_sel), fpos = (int)(gw % F_sel);
+    const SplitTask t = tasks[ti];
+    const NodeSeg s = segs[t.node];
+    if (!s.valid) continue;
+    long long *hn = reinterpret_cast<long long *>(pool) + (int64_t)t.node * node_stride +
+                    (int64_t)fpos * kHistPerFeat + lane * 8;
+    long long g[4], h[4];
+    if (t.parent >= 0 && !s.is_small) {
+      const long long *hp = reinterpret_cast<const long long *>(pool) +
+                            (int64_t)t.parent * node_stride + (int64_t)fpos * kHistPerFeat + lane * 8;
+      const long long *hs = reinterpret_cast<const long long *>(pool) +
+                            (int64_t)t.sibling * node_stride + (int64_t)fpos * kHistPerFeat + lane * 8;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      g[k] = hp[2 * k] - hs[2 * k];
-      h[k] = hp[2 * k + 1] - hs[2 * k + 1];
-      hn[2 * k] = g[k];
-      hn[2 * k + 1] = h[k];
+      for (int k = 0; k < 4; ++k) {
+        g[k] = hp[2 * k] - hs[2 * k];
+        h[k] = hp[2 * k + 1] - hs[2 * k + 1];
+        hn[2 * k] = g[k];
+        hn[2 * k + 1] = h[k];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        g[k] = hn[2 * k];
+        h[k] = hn[2 * k + 1];
+      }
     }
-  } else {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      g[k] = hn[2 * k];
-      h[k] = hn[2 * k + 1];
+    const long long lg = g[0] + g[1] + g[2] + g[3];
+    const long long lhs = h[0] + h[1] + h[2] + h[3];
+    const long long ig = wave_incl_scan<long long>(lg);
+    const long long ih = wave_incl_scan<long long>(lhs);
+    const long long Gt = __shfl(ig, 63, 64);
+    const long long Ht = __shfl(ih, 63, 64);
+    if (fpos == 0 && lane == 0) {
+      totals[2 * (int64_t)t.node] = Gt;
+      totals[2 * (int64_t)t.node + 1] = Ht;
     }
-  }
-  const long long lg = g[0] + g[1] + g[2] + g[3];
-  const long long lhs = h[0] + h[1] + h[2] + h[3];
-  const long long ig = wave_incl_scan<long long>(lg);
-  const long long ih = wave_incl_scan<long long>(lhs);
-  const long long Gt = __shfl(ig, 63, 64);
-  const long long Ht = __shfl(ih, 63, 64);
-  if (fpos == 0 && lane == 0) {
-    totals[2 * (int64_t)t.node] = Gt;
-    totals[2 * (int64_t)t.node + 1] = Ht;
-  }
-  const double Gtd = (double)Gt * P.g_scale;
-  const double Htd = (double)Ht * P.h_scale;
-  const bool can = s.count >= P.min_samples_leaf && Htd >= P.min_child_weight &&
-                   (t.parent < 0 || t.depth < P.max_depth);
-  const int32_t nb = nb_sel[fpos];
-  double best = -1e9;
-  int32_t bb = -1;
-  if (can && nb >= 2) {
-    const double lam = P.reg_lambda, mcw = P.min_child_weight;
-    const double parent_term = Gtd * Gtd / (Htd + lam);
-    long long GLq = ig - lg, HLq = ih - lhs;
+    const double Gtd = (double)Gt * P.g_scale;
+    const double Htd = (double)Ht * P.h_scale;
+    const bool can = s.count >= P.min_samples_leaf && Htd >= P.min_child_weight &&
+                     (t.parent < 0 || t.depth < P.max_depth);
+    const int32_t nb = nb_sel[fpos];
+    double best = -1e9;
+    int32_t bb = -1;
+    if (can && nb >= 2) {
+      const double lam = P.reg_lambda, mcw = P.min_child_weight;
+      const double parent_term = Gtd * Gtd / (Htd + lam);
+      long long GLq = ig - lg, HLq = ih - lhs;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      GLq += g[k];
-      HLq += h[k];
-      const int32_t b = lane * 4 + k;
-      if (b <= nb - 2) {
-        const double GL = (double)GLq * P.g_scale;
-        const double HL = (double)HLq * P.h_scale;
-        const double GR = (double)(Gt - GLq) * P.g_scale;
-        const double HR = (double)(Ht - HLq) * P.h_scale;
-        if (!(HL < mcw || HR < mcw)) {
-          const double gain = (GL * GL / (HL + lam) + GR * GR / (HR + lam)) - parent_term;
-          if (gain > best) {
-            best = gain;
-            bb = b;
+      for (int k = 0; k < 4; ++k) {
+        GLq += g[k];
+        HLq += h[k];
+        const int32_t b = lane * 4 + k;
+        if (b <= nb - 2) {
+          const double GL = (double)GLq * P.g_scale;
+          const double HL = (double)HLq * P.h_scale;
+          const double GR = (double)(Gt - GLq) * P.g_scale;
+          const double HR = (double)(Ht - HLq) * P.h_scale;
+          if (!(HL < mcw || HR < mcw)) {
+            const double gain = (GL * GL / (HL + lam) + GR * GR / (HR + lam)) - parent_term;
+            if (gain > best) {
+              best = gain;
+              bb = b;
+            }
           }
         }
       }
     }
-  }
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const double og = __shfl_xor(best, o, 64);
-    const int32_t ob = __shfl_xor(bb, o, 64);
-    const bool take = ob >= 0 && (bb < 0 || og > best || (og == best && ob < bb));
-    best = take ? og : best;
-    bb = take ? ob : bb;
-  }
-  if (lane == 0) {
-    SplitCand c;
-    c.gain = best;
-    c.bin = bb;
-    c.pad = 0;
-    cand[(int64_t)t.node * F_sel + fpos] = c;
+    for (int o = 32; o >= 1; o >>= 1) {
+      const double og = __shfl_xor(best, o, 64);
+      const int32_t ob = __shfl_xor(bb, o, 64);
+      const bool take = ob >= 0 && (bb < 0 || og > best || (og == best && ob < bb));
+      best = take ? og : best;
+      bb = take ? ob : bb;
+    }
+    if (lane == 0) {
+      SplitCand c;
+      c.gain = best;
+      c.bin = bb;
+      c.pad = 0;
+      cand[(int64_t)t.node * F_sel + fpos] = c;
+    }
   }
 }
 #pragma clang fp contract(on)
 
-hipError_t launch_split(hipStream_t st, const SplitTask *tasks, int32_t n_tasks,
+hipError_t launch_split(hipStream_t st, const SplitTask *tasks,
+                        const LevelPlan *plan, int32_t max_tasks,
                         const NodeSeg *segs, unsigned long long *pool,
                         int64_t node_stride, const int32_t *nb_sel,
                         int32_t F_sel, SplitParams p, SplitCand *cand,
                         long long *totals) {
-  const int64_t waves = (int64_t)n_tasks * F_sel;
+  const int64_t waves = (int64_t)max_tasks * F_sel;
   if (waves <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_split, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st,
-                     tasks, n_tasks, segs, pool, node_stride, nb_sel, F_sel, p,
+                     tasks, plan, segs, pool, node_stride, nb_sel, F_sel, p,
                      cand, totals);
   return hipGetLastError();
 }
@@ -975,109 +1175,341 @@ hipError_t launch_split(hipStream_t st, const SplitTask *tasks, int32_t n_tasks,
 // summed up to the split bin (left) and the rest (right).  One wave per
 // parent.
 __global__ __launch_bounds__(256) void k_child_totals(
-    const PartParent *__restrict__ parents, int32_t n_parents,
-    const int32_t *__restrict__ parent_ids, const NodeSeg *__restrict__ segs,
-    const unsigned long long *__restrict__ pool, int64_t node_stride,
-    long long *__restrict__ totals) {
-  const int w = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
+    const PartParent *__restrict__ parents, const LevelPlan *__restrict__ plan,
+    const NodeSeg *__restrict__ segs, const unsigned long long *__restrict__ pool,
+    int64_t node_stride, long long *__restrict__ totals) {
   const int lane = lane_id();
-  if (w >= n_parents) return;
-  const PartParent P = parents[w];
-  if (!segs[P.left_id].valid) return;
-  const long long *h = reinterpret_cast<const long long *>(pool) +
-                       (int64_t)parent_ids[w] * node_stride + (int64_t)P.fpos * kHistPerFeat;
-  long long gl = 0, hl = 0, gt = 0, ht = 0;
+  const int32_t n_parents = plan->n_parents;
+  for (int w = (int)(blockIdx.x * 4 + (threadIdx.x >> 6)); w < n_parents;
+       w += (int)gridDim.x * 4) {
+    const PartParent P = parents[w];
+    if (!segs[P.left_id].valid) continue;
+    const long long *h = reinterpret_cast<const long long *>(pool) +
+                         (int64_t)P.node * node_stride + (int64_t)P.fpos * kHistPerFeat;
+    long long gl = 0, hl = 0, gt = 0, ht = 0;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int b = lane * 4 + k;
-    const long long g = h[2 * b], hh = h[2 * b + 1];
-    gt += g;
-    ht += hh;
-    if (b <= P.bin) {
-      gl += g;
-      hl += hh;
+    for (int k = 0; k < 4; ++k) {
+      const int b = lane * 4 + k;
+      const long long g = h[2 * b], hh = h[2 * b + 1];
+      gt += g;
+      ht += hh;
+      if (b <= P.bin) {
+        gl += g;
+        hl += hh;
+      }
     }
-  }
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    gl += __shfl_xor(gl, o, 64);
-    hl += __shfl_xor(hl, o, 64);
-    gt += __shfl_xor(gt, o, 64);
-    ht += __shfl_xor(ht, o, 64);
-  }
-  if (lane == 0) {
-    totals[2 * (int64_t)P.left_id] = gl;
-    totals[2 * (int64_t)P.left_id + 1] = hl;
-    totals[2 * (int64_t)P.right_id] = gt - gl;
-    totals[2 * (int64_t)P.right_id + 1] = ht - hl;
+    for (int o = 32; o >= 1; o >>= 1) {
+      gl += __shfl_xor(gl, o, 64);
+      hl += __shfl_xor(hl, o, 64);
+      gt += __shfl_xor(gt, o, 64);
+      ht += __shfl_xor(ht, o, 64);
+    }
+    if (lane == 0) {
+      totals[2 * (int64_t)P.left_id] = gl;
+      totals[2 * (int64_t)P.left_id + 1] = hl;
+      totals[2 * (int64_t)P.right_id] = gt - gl;
+      totals[2 * (int64_t)P.right_id + 1] = ht - hl;
+    }
   }
 }
 
 hipError_t launch_child_totals(hipStream_t st, const PartParent *parents,
-                               int32_t n_parents, const int32_t *parent_ids,
+                               const LevelPlan *plan, int32_t max_parents,
                                const NodeSeg *segs, const unsigned long long *pool,
                                int64_t node_stride, long long *totals) {
-  if (n_parents <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_child_totals, dim3((unsigned)((n_parents + 3) / 4)), dim3(256), 0,
-                     st, parents, n_parents, parent_ids, segs, pool, node_stride, totals);
+  if (max_parents <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_child_totals, dim3((unsigned)((max_parents + 3) / 4)), dim3(256), 0,
+                     st, parents, plan, segs, pool, node_stride, totals);
   return hipGetLastError();
 }
 
 // Per node: the best split over features -- the largest gain, the lowest
 // feature position on ties (est:618-621) -- with the node's segment and
-// fixed-point totals, packed for one readback per level.
+// fixed-point totals, into the node table (not yet expanded: left = -1).
 __global__ __launch_bounds__(256) void k_node_best(
     const NodeSeg *__restrict__ segs, const long long *__restrict__ totals,
-    const SplitCand *__restrict__ cand, int32_t F_sel, int32_t first,
-    int32_t count, int32_t no_split, NodeOut *__restrict__ out) {
-  const int w = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
+    const SplitCand *__restrict__ cand, int32_t F_sel,
+    const LevelPlan *__restrict__ plan, int32_t no_split,
+    NodeOut *__restrict__ nodes) {
   const int lane = lane_id();
-  if (w >= count) return;
-  const int node = first + w;
-  const NodeSeg s = segs[node];
-  double best = 0.0;
-  int32_t bf = -1, bb = 0;
-  if (s.valid && !no_split) {
-    for (int f = lane; f < F_sel; f += 64) {
-      const SplitCand c = cand[(int64_t)node * F_sel + f];
-      if (c.bin >= 0 && (bf < 0 || c.gain > best)) {
-        best = c.gain;
-        bf = f;
-        bb = c.bin;
+  const int32_t first = plan->first_child, count = plan->n_split;
+  for (int w = (int)(blockIdx.x * 4 + (threadIdx.x >> 6)); w < count;
+       w += (int)gridDim.x * 4) {
+    const int node = first + w;
+    const NodeSeg s = segs[node];
+    double best = 0.0;
+    int32_t bf = -1, bb = 0;
+    if (s.valid && !no_split) {
+      for (int f = lane; f < F_sel; f += 64) {
+        const SplitCand c = cand[(int64_t)node * F_sel + f];
+        if (c.bin >= 0 && (bf < 0 || c.gain > best)) {
+          best = c.gain;
+          bf = f;
+          bb = c.bin;
+        }
       }
     }
-  }
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const double og = __shfl_xor(best, o, 64);
-    const int32_t of = __shfl_xor(bf, o, 64);
-    const int32_t ob = __shfl_xor(bb, o, 64);
-    const bool take = of >= 0 && (bf < 0 || og > best || (og == best && of < bf));
-    best = take ? og : best;
-    bf = take ? of : bf;
-    bb = take ? ob : bb;
-  }
-  if (lane == 0) {
-    NodeOut o;
-    o.start = s.start;
-    o.count = s.count;
-    o.valid = s.valid;
-    o.Gq = s.valid ? totals[2 * (int64_t)node] : 0;
-    o.Hq = s.valid ? totals[2 * (int64_t)node + 1] : 0;
-    o.gain = bf >= 0 ? best : -1e9;
-    o.fpos = bf;
-    o.bin = bf >= 0 ? bb : 0;
-    out[w] = o;
+    for (int o = 32; o >= 1; o >>= 1) {
+      const double og = __shfl_xor(best, o, 64);
+      const int32_t of = __shfl_xor(bf, o, 64);
+      const int32_t ob = __shfl_xor(bb, o, 64);
+      const bool take = of >= 0 && (bf < 0 || og > best || (og == best && of < bf));
+      best = take ? og : best;
+      bf = take ? of : bf;
+      bb = take ? ob : bb;
+    }
+    if (lane == 0) {
+      NodeOut o;
+      o.start = s.start;
+      o.count = s.count;
+      o.valid = s.valid;
+      o.Gq = s.valid ? totals[2 * (int64_t)node] : 0;
+      o.Hq = s.valid ? totals[2 * (int64_t)node + 1] : 0;
+      o.gain = bf >= 0 ? best : -1e9;
+      o.e = 0.0;
+      o.fpos = bf;
+      o.bin = bf >= 0 ? bb : 0;
+      o.left = -1;
+      nodes[node] = o;
+    }
   }
 }
 
 hipError_t launch_node_best(hipStream_t st, const NodeSeg *segs,
                             const long long *totals, const SplitCand *cand,
-                            int32_t F_sel, int32_t first, int32_t count,
-                            int32_t no_split, NodeOut *out) {
-  if (count <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_node_best, dim3((unsigned)((count + 3) / 4)), dim3(256), 0,
-                     st, segs, totals, cand, F_sel, first, count, no_split, out);
+                            int32_t F_sel, const LevelPlan *plan,
+                            int32_t max_nodes, int32_t no_split, NodeOut *nodes) {
+  if (max_nodes <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_node_best, dim3((unsigned)((max_nodes + 3) / 4)), dim3(256), 0,
+                     st, segs, totals, cand, F_sel, plan, no_split, nodes);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Level planner: est:641-820 grown one depth at a time.  One workgroup.
+//
+// The candidates of level `a.level` are the nodes the previous level created
+// (the root at level 0).  A candidate is expanded when it is valid, has a
+// split whose gain exceeds gamma (est:649-652), and fewer than max_leaves - 1
+// splits kept at earlier levels rank above it.  A node's rank e is the
+// smallest best gain on its root path; the best-first loop pops nodes in
+// non-increasing e order and stops after max_leaves - 1 kept splits, so a
+// node with that many kept splits strictly above it is never popped and its
+// subtree is never needed.  Expanded nodes get consecutive child ids, and the
+// kernel writes the level's PartParent, PartTile, HistTask and SplitTask
+// lists and its LevelPlan.  When the node table is too small the plan
+// records the nodes needed in `overflow` and every later kernel does nothing.
+// ---------------------------------------------------------------------------
+constexpr int kPlanBlock = 1024;
+constexpr int kPlanChunk = 2048;  // ranks of earlier nodes staged in LDS at a time
+
+// Rows per histogram tile for S rows: about hist_target tiles, but no fewer
+// than rows_per_flush rows per tile, a multiple of 4096 rows.
+__device__ __forceinline__ int32_t plan_tile_rows(int64_t S, const PlanArgs &a) {
+  int64_t tiles = max((int64_t)1, (int64_t)a.hist_target);
+  tiles = min(tiles, max((int64_t)1, S / a.rows_per_flush));
+  const int64_t t = ((S + tiles - 1) / tiles + 4095) / 4096 * 4096;
+  return (int32_t)min(max(t, (int64_t)4096), (int64_t)1 << 24);
+}
+
+__global__ __launch_bounds__(kPlanBlock) void k_plan(
+    NodeOut *__restrict__ nodes, LevelPlan *__restrict__ plan,
+    const PartParent *__restrict__ prev_parents, PartParent *__restrict__ parents,
+    int32_t *__restrict__ tile_begin, int32_t *__restrict__ hist_begin,
+    PartTile *__restrict__ tiles, HistTask *__restrict__ hist_tasks,
+    SplitTask *__restrict__ split_tasks, int32_t *__restrict__ work_flag,
+    double *__restrict__ work_e, PlanArgs a) {
+  __shared__ uint32_t stmp[kPlanBlock / 64];
+  __shared__ double ke[kPlanChunk];
+  __shared__ unsigned long long s_rows;
+  const int tid = (int)threadIdx.x;
+  const LevelPlan prev = *plan;
+  if (prev.overflow) return;  // an earlier level ran out of nodes
+  const int32_t first = prev.first_child, nc = prev.n_split, n_prev = prev.n_nodes;
+  if (tid == 0) s_rows = 0ull;
+
+  // Candidates: rank and whether they may be split (est:649-652, 762-801).
+  for (int j = tid; j < nc; j += kPlanBlock) {
+    const int c = first + j;
+    const NodeOut N = nodes[c];
+    double e = 0.0;
+    int32_t f = 0;
+    if (N.valid) {
+      const double pe = a.level == 0 ? N.gain : nodes[prev_parents[j >> 1].node].e;
+      e = pe < N.gain ? pe : N.gain;
+      f = (N.fpos >= 0 && N.gain > a.gamma) ? 1 : 0;
+    }
+    nodes[c].e = e;
+    work_e[j] = e;
+    work_flag[j] = f;
+  }
+  __syncthreads();
+
+  // Kept splits of earlier levels (expanded, children valid) ranked above.
+  for (int jb = 0; jb < nc; jb += kPlanBlock) {
+    const int j = jb + tid;
+    const bool act = j < nc && work_flag[j] != 0;
+    const double ev = act ? work_e[j] : 0.0;
+    int32_t above = 0;
+    for (int kb = 0; kb < first; kb += kPlanChunk) {
+      const int kn = min(kPlanChunk, first - kb);
+      for (int i = tid; i < kn; i += kPlanBlock) {
+        const int32_t l = nodes[kb + i].left;
+        const bool kept = l >= 0 && nodes[l].valid != 0;
+        ke[i] = kept ? nodes[kb + i].e : -INFINITY;
+      }
+      __syncthreads();
+      if (act)
+        for (int i = 0; i < kn; ++i) above += ke[i] > ev ? 1 : 0;
+      __syncthreads();
+    }
+    if (j < nc) work_flag[j] = (act && above < a.max_leaves - 1) ? 1 : 0;
+  }
+  __syncthreads();
+
+  // Expanded candidates in candidate order: work_flag becomes the parent
+  // index, -1 when not expanded.
+  uint32_t carry = 0;
+  for (int jb = 0; jb < nc; jb += kPlanBlock) {
+    const int j = jb + tid;
+    const uint32_t f = (j < nc) ? (uint32_t)work_flag[j] : 0u;
+    uint32_t tot;
+    const uint32_t pre = block_excl_scan<kPlanBlock>(f, stmp, tot);
+    if (j < nc) work_flag[j] = f ? (int32_t)(carry + pre) : -1;
+    carry += tot;
+  }
+  const int32_t n_exp = (int32_t)carry;
+  const int64_t n_new = (int64_t)n_prev + 2 * (int64_t)n_exp;
+  if (n_new > a.node_cap) {
+    if (tid == 0) {
+      LevelPlan q = {};
+      q.first_child = n_prev;
+      q.tile_rows = 4096;
+      q.n_nodes = n_prev;
+      q.overflow = (int32_t)min(n_new, (int64_t)INT32_MAX);
+      *plan = q;
+    }
+    return;
+  }
+
+  // Parents, split tasks and child links; tiles per parent; rows to histogram.
+  unsigned long long rows = 0;
+  for (int j = tid; j < nc; j += kPlanBlock) {
+    const int32_t i = work_flag[j];
+    if (i < 0) continue;
+    const int32_t v = first + j;
+    const int32_t L = n_prev + 2 * i;
+    const NodeOut N = nodes[v];
+    nodes[v].left = L;
+    PartParent P;
+    P.start = N.start;
+    P.count = N.count;
+    P.fpos = N.fpos;
+    P.bin = N.bin;
+    P.left_id = L;
+    P.right_id = L + 1;
+    P.node = v;
+    P.pad = 0;
+    parents[i] = P;
+    if (!a.last) {
+      split_tasks[2 * i] = SplitTask{L, v, L + 1, a.level + 1};
+      split_tasks[2 * i + 1] = SplitTask{L + 1, v, L, a.level + 1};
+    }
+    const int64_t a0 = N.start & ~int64_t(3);
+    tile_begin[i] = (int32_t)((N.start + N.count - a0 + kPartTile - 1) / kPartTile);
+    rows += (unsigned long long)(N.count / 2);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) rows += __shfl_xor(rows, o, 64);
+  if (lane_id() == 0 && rows) atomicAdd(&s_rows, rows);
+  __syncthreads();
+  const int32_t th = plan_tile_rows((int64_t)s_rows, a);
+
+  // Exclusive offsets of each parent's tiles and histogram tasks.
+  uint32_t tcar = 0, hcar = 0;
+  for (int ib = 0; ib < n_exp; ib += kPlanBlock) {
+    const int i = ib + tid;
+    uint32_t nt = 0, nh = 0;
+    if (i < n_exp) {
+      nt = (uint32_t)tile_begin[i];
+      nh = a.last ? 0u : (uint32_t)((parents[i].count / 2 + th) / th);
+    }
+    uint32_t tt, ht;
+    const uint32_t tp = block_excl_scan<kPlanBlock>(nt, stmp, tt);
+    const uint32_t hp = block_excl_scan<kPlanBlock>(nh, stmp, ht);
+    if (i < n_exp) {
+      tile_begin[i] = (int32_t)(tcar + tp);
+      hist_begin[i] = (int32_t)(hcar + hp);
+    }
+    tcar += tt;
+    hcar += ht;
+  }
+  if (tcar > (uint32_t)a.tile_cap || hcar > (uint32_t)a.hist_cap) {
+    // Capacities are sized from proven bounds; reaching this is a bug.
+    if (tid == 0) {
+      LevelPlan q = {};
+      q.first_child = n_prev;
+      q.tile_rows = 4096;
+      q.n_nodes = n_prev;
+      q.overflow = -1;
+      *plan = q;
+    }
+    return;
+  }
+  if (tid == 0) {
+    tile_begin[n_exp] = (int32_t)tcar;
+    hist_begin[n_exp] = (int32_t)hcar;
+  }
+  __syncthreads();
+
+  // Tile and histogram-task lists: item -> its parent by binary search.
+  for (int t = tid; t < (int)tcar; t += kPlanBlock) {
+    int lo = 0, hi = n_exp - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tile_begin[mid] <= t) lo = mid;
+      else hi = mid - 1;
+    }
+    PartTile T;
+    T.row0 = (parents[lo].start & ~int64_t(3)) + (int64_t)(t - tile_begin[lo]) * kPartTile;
+    T.rows = kPartTile;
+    T.parent = lo;
+    tiles[t] = T;
+  }
+  for (int q = tid; q < (int)hcar; q += kPlanBlock) {
+    int lo = 0, hi = n_exp - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (hist_begin[mid] <= q) lo = mid;
+      else hi = mid - 1;
+    }
+    hist_tasks[q] = HistTask{lo, q - hist_begin[lo]};
+  }
+  if (tid == 0) {
+    LevelPlan q;
+    q.n_parents = n_exp;
+    q.n_tiles = (int32_t)tcar;
+    q.n_hist = (int32_t)hcar;
+    q.n_split = 2 * n_exp;
+    q.first_child = n_prev;
+    q.tile_rows = th;
+    q.n_nodes = (int32_t)n_new;
+    q.overflow = 0;
+    *plan = q;
+  }
+}
+
+hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
+                       const PartParent *prev_parents, PartParent *parents,
+                       int32_t *tile_begin, int32_t *hist_begin,
+                       PartTile *tiles, HistTask *hist_tasks,
+                       SplitTask *split_tasks, int32_t *work_flag,
+                       double *work_e, PlanArgs a) {
+  hipLaunchKernelGGL(k_plan, dim3(1), dim3(kPlanBlock), 0, st, nodes, plan,
+                     prev_parents, parents, tile_begin, hist_begin, tiles,
+                     hist_tasks, split_tasks, work_flag, work_e, a);
   return hipGetLastError();
 }
 

@@ -19,30 +19,36 @@
 //     until (word & mask) <= max.
 //   * Fisher-Yates from the end: for i = n-1 .. 1, swap a[i] with a[j(i)].
 //
-// The random numbers never depend on the data, which allows three changes
-// that leave the sequence of swaps unchanged:
-//   * each 624-word block is twisted and tempered at once, and the bounded
-//     draws for a whole range of mask-constant steps run in one branch-free
-//     loop (a rejected word is overwritten by the next one);
-//   * the draws of round r+1 are made on one thread while another thread
-//     applies the swaps of round r;
-//   * the swap loop prefetches a[j] a fixed distance ahead.
+// The random numbers never depend on the data, so the work is split into
+// stages that run on their own threads without changing the sequence:
+//   * a generator thread twists and tempers whole 624-word blocks (AVX-512
+//     when the CPU has it) into a ring of word chunks;
+//   * a draw thread turns words into the bounded draws j(i) of every round.
+//     Within a run of steps with a constant mask, 16 words are classified at
+//     once: a word <= i - 15 is accepted whatever happened to the 15 words
+//     before it (each acceptance lowers i by one), a word > i is rejected
+//     whatever happened, and only a block holding a word in between is
+//     decided one word at a time;
+//   * the swaps: in device-rows mode the draws are handed to the engine,
+//     which applies them on the GPU (bsscl_fisher_yates_apply); otherwise a
+//     swap thread applies them on the host and delivers sample_idx.
 //
-// Each round is delivered as the reference's sample_idx (the first n_sub
-// entries of the permuted array, in that order) and the sorted feature
-// subset, up to `lookahead` rounds ahead of the consumer.
+// Each round is delivered up to `lookahead` rounds ahead of the consumer.
 #include "bsscl_internal.h"
 
 #include <hip/hip_runtime.h>
 
+#include <immintrin.h>
 #include <sys/mman.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <condition_variable>
 #include <cstdlib>
 #include <cstring>
 #include <deque>
+#include <memory>
 #include <mutex>
 #include <thread>
 #include <vector>
@@ -65,6 +71,71 @@ inline uint32_t temper(uint32_t y) {
   return y;
 }
 
+inline uint32_t twist_word(uint32_t a, uint32_t b, uint32_t m) {
+  const uint32_t y = (a & kUpper) | (b & kLower);
+  return m ^ (y >> 1) ^ ((0u - (y & 1u)) & kMatrixA);
+}
+
+// One MT19937 state transition in place (scalar).
+void twist_scalar(uint32_t *key) {
+  int i = 0;
+  for (; i < kN - kM; ++i) key[i] = twist_word(key[i], key[i + 1], key[i + kM]);
+  for (; i < kN - 1; ++i) key[i] = twist_word(key[i], key[i + 1], key[i + kM - kN]);
+  key[kN - 1] = twist_word(key[kN - 1], key[0], key[kM - 1]);
+}
+
+// key[i .. i+15] = twist of (key[i+k], key[i+k+1]) xor key[m+k].
+__attribute__((target("avx512f"))) inline void twist16(uint32_t *key, int i, int m) {
+  const __m512i a = _mm512_loadu_si512(key + i);
+  const __m512i b = _mm512_loadu_si512(key + i + 1);
+  const __m512i c = _mm512_loadu_si512(key + m);
+  const __m512i y = _mm512_or_si512(_mm512_and_si512(a, _mm512_set1_epi32((int)kUpper)),
+                                    _mm512_and_si512(b, _mm512_set1_epi32((int)kLower)));
+  const __mmask16 odd = _mm512_test_epi32_mask(y, _mm512_set1_epi32(1));
+  __m512i r = _mm512_xor_si512(c, _mm512_srli_epi32(y, 1));
+  r = _mm512_mask_xor_epi32(r, odd, r, _mm512_set1_epi32((int)kMatrixA));
+  _mm512_storeu_si512(key + i, r);
+}
+
+// The same transition 16 words at a time.  Words [0, 227) read only old
+// words (i + 1 and i + 397); words [227, 623) read i + 1 (old) and i - 227,
+// which an earlier step of this pass has already written.
+__attribute__((target("avx512f"))) void twist_avx512(uint32_t *key) {
+  int i = 0;
+  for (; i + 16 <= kN - kM; i += 16) twist16(key, i, i + kM);
+  for (; i < kN - kM; ++i) key[i] = twist_word(key[i], key[i + 1], key[i + kM]);
+  for (; i + 16 <= kN - 1; i += 16) twist16(key, i, i + kM - kN);
+  for (; i < kN - 1; ++i) key[i] = twist_word(key[i], key[i + 1], key[i + kM - kN]);
+  key[kN - 1] = twist_word(key[kN - 1], key[0], key[kM - 1]);
+}
+
+__attribute__((target("avx512f"))) void temper_avx512(const uint32_t *key, uint32_t *out) {
+  const __m512i b = _mm512_set1_epi32((int)0x9d2c5680u);
+  const __m512i c = _mm512_set1_epi32((int)0xefc60000u);
+  for (int i = 0; i < kN; i += 16) {  // 624 = 39 * 16
+    __m512i y = _mm512_loadu_si512(key + i);
+    y = _mm512_xor_si512(y, _mm512_srli_epi32(y, 11));
+    y = _mm512_xor_si512(y, _mm512_and_si512(_mm512_slli_epi32(y, 7), b));
+    y = _mm512_xor_si512(y, _mm512_and_si512(_mm512_slli_epi32(y, 15), c));
+    y = _mm512_xor_si512(y, _mm512_srli_epi32(y, 18));
+    _mm512_storeu_si512(out + i, y);
+  }
+}
+
+// AVX-512 paths unless the CPU lacks them or BSSCL_SAMPLER_SCALAR=1.
+bool use_avx512() {
+  static const bool ok = [] {
+    const char *e = std::getenv("BSSCL_SAMPLER_SCALAR");
+    if (e && e[0] == '1') return false;
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512vl") &&
+           __builtin_cpu_supports("avx512bw");
+  }();
+  return ok;
+}
+
+// Scalar MT19937 with NumPy's position convention, for one-shot shuffles
+// and draws (bsscl_rs_*).
 struct MT {
   uint32_t key[kN];
   uint32_t out[kN];  // tempered key[] of the current block
@@ -77,17 +148,7 @@ struct MT {
   }
 
   void twist() {
-    int i = 0;
-    for (; i < kN - kM; ++i) {
-      uint32_t y = (key[i] & kUpper) | (key[i + 1] & kLower);
-      key[i] = key[i + kM] ^ (y >> 1) ^ ((0u - (y & 1u)) & kMatrixA);
-    }
-    for (; i < kN - 1; ++i) {
-      uint32_t y = (key[i] & kUpper) | (key[i + 1] & kLower);
-      key[i] = key[i + kM - kN] ^ (y >> 1) ^ ((0u - (y & 1u)) & kMatrixA);
-    }
-    uint32_t y = (key[kN - 1] & kUpper) | (key[0] & kLower);
-    key[kN - 1] = key[kM - 1] ^ (y >> 1) ^ ((0u - (y & 1u)) & kMatrixA);
+    twist_scalar(key);
     for (int k = 0; k < kN; ++k) out[k] = temper(key[k]);
     pos = 0;
   }
@@ -120,75 +181,38 @@ struct MT {
     }
     return v;
   }
-
-  // Draws for steps i = hi .. 1 of a shuffle (j[i] in [0, i]); hi < 2^32.
-  // Within [2^k, 2^(k+1)-1] the mask is constant; the loop writes every word
-  // to j[i] and moves to the next step only when the word is accepted.
-  void draws(uint64_t hi, uint32_t *j) {
-    uint64_t i = hi;
-    while (i >= 1) {
-      const int k = 63 - __builtin_clzll(i);
-      const uint64_t lo = 1ull << k;
-      const uint32_t mask = (uint32_t)((lo << 1) - 1);
-      while (i >= lo) {
-        if (pos >= kN) twist();
-        const uint32_t *w = out + pos;
-        const int avail = kN - pos;
-        int used = 0;
-        while (used < avail && i >= lo) {
-          const uint32_t v = w[used++] & mask;
-          j[i] = v;
-          i -= (v <= i) ? 1u : 0u;
-        }
-        pos += used;
-      }
-    }
-  }
 };
 
 template <typename T>
 void shuffle_inplace(MT &mt, T *a, int64_t n) {
-  if (n <= 1) return;
-  if ((uint64_t)(n - 1) > 0xffffffffull) {
-    for (int64_t i = n - 1; i >= 1; --i) {
-      const uint64_t j = mt.interval((uint64_t)i);
-      T t = a[j];
-      a[j] = a[i];
-      a[i] = t;
-    }
-    return;
-  }
-  std::vector<uint32_t> j((size_t)n);
-  mt.draws((uint64_t)(n - 1), j.data());
-  constexpr int64_t kAhead = 32;
   for (int64_t i = n - 1; i >= 1; --i) {
-    if (i > kAhead) __builtin_prefetch(a + j[(size_t)(i - kAhead)], 1, 1);
-    const uint32_t ji = j[(size_t)i];
-    T t = a[ji];
-    a[ji] = a[i];
+    const uint64_t j = mt.interval((uint64_t)i);
+    T t = a[j];
+    a[j] = a[i];
     a[i] = t;
   }
 }
 
-// Host buffer for a round's rows: pinned when a HIP device is present (the
-// engine copies it to the GPU asynchronously), plain memory otherwise.
+// Host buffer the engine copies from: pinned when a HIP device is present,
+// plain memory otherwise.
+template <typename T>
 struct HostBuf {
-  int32_t *p = nullptr;
+  T *p = nullptr;
   size_t n = 0;
   bool pinned = false;
   void alloc(size_t count) {
     if (count <= n && p) return;
     release();
     void *q = nullptr;
-    if (hipHostMalloc(&q, count * sizeof(int32_t), hipHostMallocDefault) == hipSuccess) {
+    if (hipHostMalloc(&q, count * sizeof(T), hipHostMallocDefault) == hipSuccess) {
       pinned = true;
     } else {
       (void)hipGetLastError();
-      q = std::malloc(count * sizeof(int32_t));
+      q = std::malloc(count * sizeof(T));
       pinned = false;
     }
     if (!q) throw std::bad_alloc();
-    p = static_cast<int32_t *>(q);
+    p = static_cast<T *>(q);
     n = count;
   }
   void release() {
@@ -199,11 +223,14 @@ struct HostBuf {
     p = nullptr;
     n = 0;
   }
+  HostBuf() = default;
+  HostBuf(const HostBuf &) = delete;
+  HostBuf &operator=(const HostBuf &) = delete;
+  ~HostBuf() { release(); }
 };
 
-// Array backed by 2 MB pages where the kernel allows it: the swap loop makes
-// one random access per step into an array of up to 40 MB, and 4 KB pages
-// would add a TLB miss to most of them.
+// Array backed by 2 MB pages where the kernel allows it: the host swap loop
+// makes one random access per step into an array of up to 40 MB.
 template <typename T>
 struct BigArray {
   T *p = nullptr;
@@ -217,32 +244,226 @@ struct BigArray {
     p = static_cast<T *>(q);
     n = count;
   }
+  BigArray() = default;
+  BigArray(const BigArray &) = delete;
+  BigArray &operator=(const BigArray &) = delete;
   ~BigArray() { std::free(p); }
   T &operator[](size_t i) { return p[i]; }
   T *data() { return p; }
 };
 
+// Backoff of a thread waiting on another stage: spin, then yield, then sleep.
+void wait_pause(int &spins) {
+  if (++spins < 4096) {
+    _mm_pause();
+  } else if (spins < 8192) {
+    std::this_thread::yield();
+  } else {
+    std::this_thread::sleep_for(std::chrono::microseconds(20));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Word generator.  Block b of the stream is the given state (b = 0) or the
+// state after b twists, tempered; chunk c holds blocks [c*B, (c+1)*B).  The
+// consumer releases chunks in order, so a single-producer single-consumer
+// ring of kRing chunks suffices.
+// ---------------------------------------------------------------------------
+constexpr int kChunkBlocks = 128;
+constexpr int64_t kChunkWords = (int64_t)kChunkBlocks * kN;
+constexpr int kRing = 8;
+
+struct WordGen {
+  struct Chunk {
+    std::vector<uint32_t> w;
+    uint32_t key[kN];  // state of the chunk's first block
+  };
+  Chunk ring[kRing];
+  std::atomic<int64_t> head{0};  // chunks produced
+  std::atomic<int64_t> tail{0};  // chunks released by the consumer
+  std::atomic<bool> stop{false};
+  uint32_t key[kN];
+  std::atomic<double> busy_ms{0.0};
+  std::thread th;
+
+  void start(const uint32_t *key0) {
+    std::memcpy(key, key0, sizeof(key));
+    for (auto &c : ring) c.w.resize((size_t)kChunkWords);
+    th = std::thread([this] { run(); });
+  }
+
+  void run() {
+    const bool vec = use_avx512();
+    for (int64_t c = 0;; ++c) {
+      int spins = 0;
+      while (c - tail.load(std::memory_order_acquire) >= kRing) {
+        if (stop.load(std::memory_order_relaxed)) return;
+        wait_pause(spins);
+      }
+      if (stop.load(std::memory_order_relaxed)) return;
+      const auto t0 = std::chrono::steady_clock::now();
+      Chunk &ch = ring[c % kRing];
+      for (int b = 0; b < kChunkBlocks; ++b) {
+        if (c > 0 || b > 0) {
+          if (vec) twist_avx512(key);
+          else twist_scalar(key);
+        }
+        if (b == 0) std::memcpy(ch.key, key, sizeof(key));
+        uint32_t *o = ch.w.data() + (size_t)b * kN;
+        if (vec) {
+          temper_avx512(key, o);
+        } else {
+          for (int k = 0; k < kN; ++k) o[k] = temper(key[k]);
+        }
+      }
+      busy_ms.store(busy_ms.load(std::memory_order_relaxed) +
+                        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count(),
+                    std::memory_order_relaxed);
+      head.store(c + 1, std::memory_order_release);
+    }
+  }
+
+  void finish() {
+    stop.store(true);
+    if (th.joinable()) th.join();
+  }
+};
+
+// The consumer's view of the word stream.
+struct Stream {
+  WordGen *gen = nullptr;
+  const uint32_t *p = nullptr, *end = nullptr, *base = nullptr;
+  int64_t chunk = -1;
+  uint32_t cur_key[kN], prev_key[kN];
+
+  // Moves to chunk `chunk + 1`, releasing the current one; false if stopped.
+  bool next_chunk() {
+    if (chunk >= 0) {
+      std::memcpy(prev_key, cur_key, sizeof(cur_key));
+      gen->tail.store(chunk + 1, std::memory_order_release);
+    }
+    ++chunk;
+    int spins = 0;
+    while (gen->head.load(std::memory_order_acquire) <= chunk) {
+      if (gen->stop.load(std::memory_order_relaxed)) return false;
+      wait_pause(spins);
+    }
+    const WordGen::Chunk &ch = gen->ring[chunk % kRing];
+    std::memcpy(cur_key, ch.key, sizeof(cur_key));
+    base = ch.w.data();
+    p = base;
+    end = base + kChunkWords;
+    return true;
+  }
+
+  int64_t position() const { return chunk * kChunkWords + (p - base); }
+
+  // NumPy state (key, pos) after the words consumed so far, given the
+  // initial state (key0, pos0): the key of the block holding the last
+  // consumed word and the offset just past it (pos = 624 at a block's end).
+  void state(const uint32_t *key0, int pos0, uint32_t *key_out, int *pos_out) const {
+    const int64_t G = position();
+    if (G <= pos0) {
+      std::memcpy(key_out, key0, sizeof(uint32_t) * kN);
+      *pos_out = pos0;
+      return;
+    }
+    const int64_t b = (G - 1) / kN;
+    const int64_t c = b / kChunkBlocks;  // chunk, or chunk - 1 when nothing was read from it
+    uint32_t k[kN];
+    std::memcpy(k, c == chunk ? cur_key : prev_key, sizeof(k));
+    for (int64_t t = c * kChunkBlocks; t < b; ++t) twist_scalar(k);
+    std::memcpy(key_out, k, sizeof(k));
+    *pos_out = (int)(G - b * kN);
+  }
+};
+
+// Bounded draws of the shuffle steps i = hi .. 1: out[hi - i] = j(i).
+// `out` needs 16 words of room past its last entry.  False if stopped.
+bool draw_steps_scalar(Stream &s, uint32_t hi, uint32_t *out) {
+  uint32_t i = hi;
+  while (i >= 1) {
+    const uint32_t lo = 1u << (31 - __builtin_clz(i));
+    const uint32_t mask = lo | (lo - 1);
+    while (i >= lo) {
+      if (s.p == s.end && !s.next_chunk()) return false;
+      const uint32_t *p = s.p, *e = s.end;
+      while (p < e && i >= lo) {
+        const uint32_t v = *p++ & mask;
+        *out = v;  // kept only when accepted
+        const uint32_t a = v <= i ? 1u : 0u;
+        out += a;
+        i -= a;
+      }
+      s.p = p;
+    }
+  }
+  return true;
+}
+
+__attribute__((target("avx512f,avx512vl,avx512bw,popcnt")))
+bool draw_steps_avx512(Stream &s, uint32_t hi, uint32_t *out) {
+  uint32_t i = hi;
+  while (i >= 1) {
+    const uint32_t lo = 1u << (31 - __builtin_clz(i));
+    const uint32_t mask = lo | (lo - 1);
+    const __m512i vm = _mm512_set1_epi32((int)mask);
+    while (i >= lo) {
+      if (s.p == s.end && !s.next_chunk()) return false;
+      const uint32_t *p = s.p, *e = s.end;
+      // 16 words at a time while the mask stays the same for all of them.
+      while (i - lo >= 16 && e - p >= 16) {
+        const __m512i v = _mm512_and_si512(_mm512_loadu_si512(p), vm);
+        const __mmask16 acc = _mm512_cmple_epu32_mask(v, _mm512_set1_epi32((int)i));
+        const __mmask16 amb = _mm512_mask_cmpge_epu32_mask(acc, v, _mm512_set1_epi32((int)(i - 14)));
+        if (amb) break;
+        _mm512_storeu_si512(out, _mm512_maskz_compress_epi32(acc, v));
+        const uint32_t c = (uint32_t)__builtin_popcount((unsigned)acc);
+        out += c;
+        i -= c;
+        p += 16;
+      }
+      // One word: a block with an order-dependent word, the end of a mask
+      // range or the end of a chunk.
+      if (p < e) {
+        const uint32_t v = *p++ & mask;
+        *out = v;
+        const uint32_t a = v <= i ? 1u : 0u;
+        out += a;
+        i -= a;
+      }
+      s.p = p;
+    }
+  }
+  return true;
+}
+
+bool draw_steps(Stream &s, uint32_t hi, uint32_t *out) {
+  if (hi == 0) return true;
+  return use_avx512() ? draw_steps_avx512(s, hi, out) : draw_steps_scalar(s, hi, out);
+}
+
 }  // namespace
 
 struct Sampler {
-  MT mt;  // owned by the draw thread once started
   int64_t n = 0, n_sub = 0;
   int32_t F = 0, f_sub = 0;
-  bool do_rows = false, do_feats = false;
+  bool do_rows = false, do_feats = false, device_rows = false;
   int32_t n_rounds = 0, lookahead = 2;
+  uint32_t key0[kN];
+  int pos0 = 0;
 
-  struct Draws {  // one round's bounded draws
-    std::vector<uint32_t> rows, feats;
-  };
   struct Round {
-    HostBuf rows;                // sample_idx, reference order
+    HostBuf<uint32_t> draws;     // j(i) of steps n-1 .. 1
+    HostBuf<int32_t> rows;       // sample_idx (host mode)
     std::vector<int32_t> feats;  // ascending selected features
+    int32_t index = 0;
   };
 
-  std::deque<Draws> drawn;       // draw thread -> swap thread
-  std::vector<Draws> draw_pool;
-  std::deque<Round> ready;       // swap thread -> consumer
-  std::vector<Round> pool;
+  WordGen gen;
+  std::deque<std::unique_ptr<Round>> drawn;  // draw thread -> swap thread
+  std::deque<std::unique_ptr<Round>> ready;  // -> consumer
+  std::vector<std::unique_ptr<Round>> pool;
   int32_t n_drawn = 0, produced = 0, consumed = 0;
   bool stop = false;
   uint32_t final_key[kN];
@@ -252,117 +473,107 @@ struct Sampler {
   std::thread draw_thread, swap_thread;
   std::string error;
 
-  // Cumulative permutations (swap thread only).
-  BigArray<int32_t> rows;
-  std::vector<int32_t> feats;
-  double draw_ms = 0.0, swap_ms = 0.0;  // time spent in each stage
+  BigArray<int32_t> rows;      // cumulative row permutation (host mode)
+  std::vector<int32_t> feats;  // cumulative feature permutation (draw thread)
+  double draw_ms = 0.0, swap_ms = 0.0;
+
+  void fail(const char *msg) {
+    std::lock_guard<std::mutex> lk(mu);
+    if (error.empty()) error = msg;
+    stop = true;
+    cv.notify_all();
+  }
 
   void run_draws() {
     try {
-      for (;;) {
-        Draws d;
+      Stream st;
+      st.gen = &gen;
+      if (!st.next_chunk()) return;
+      st.p = st.base + pos0;  // block 0 starts at the given position
+      std::vector<uint32_t> jf((size_t)F + 16);
+      for (int32_t r = 0; r < n_rounds; ++r) {
+        std::unique_ptr<Round> R;
         {
           std::unique_lock<std::mutex> lk(mu);
-          cv.wait(lk, [&] { return stop || (n_drawn < n_rounds && (int32_t)drawn.size() < 2); });
-          if (stop || n_drawn >= n_rounds) return;
-          if (!draw_pool.empty()) {
-            d = std::move(draw_pool.back());
-            draw_pool.pop_back();
+          cv.wait(lk, [&] {
+            return stop || (int32_t)(drawn.size() + ready.size()) < lookahead;
+          });
+          if (stop) return;
+          if (!pool.empty()) {
+            R = std::move(pool.back());
+            pool.pop_back();
           }
         }
+        if (!R) R.reset(new Round());
         const auto t0 = std::chrono::steady_clock::now();
         if (do_rows) {
-          d.rows.resize((size_t)n);
-          mt.draws((uint64_t)(n - 1), d.rows.data());
+          R->draws.alloc((size_t)n + 16);
+          if (!draw_steps(st, (uint32_t)(n - 1), R->draws.p)) return;
         }
         if (do_feats && F > 1) {
-          d.feats.resize((size_t)F);
-          mt.draws((uint64_t)(F - 1), d.feats.data());
+          if (!draw_steps(st, (uint32_t)(F - 1), jf.data())) return;
+          for (int32_t t = 0; t < F - 1; ++t) std::swap(feats[(size_t)(F - 1 - t)], feats[jf[(size_t)t]]);
         }
+        R->feats.assign(feats.begin(), feats.begin() + f_sub);
+        std::sort(R->feats.begin(), R->feats.end());
+        R->index = r;
         const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         {
           std::lock_guard<std::mutex> lk(mu);
           draw_ms += ms;
-          drawn.push_back(std::move(d));
-          ++n_drawn;
-          if (n_drawn == n_rounds) {
-            std::memcpy(final_key, mt.key, sizeof(final_key));
-            final_pos = mt.pos;
+          if (device_rows || !do_rows) {
+            ready.push_back(std::move(R));
+            ++produced;
+          } else {
+            drawn.push_back(std::move(R));
           }
+          ++n_drawn;
+          if (n_drawn == n_rounds) st.state(key0, pos0, final_key, &final_pos);
         }
         cv.notify_all();
       }
     } catch (...) {
-      std::lock_guard<std::mutex> lk(mu);
-      error = "sampler: draw thread failed";
-      stop = true;
-      cv.notify_all();
+      fail("sampler: draw thread failed (out of memory?)");
     }
   }
 
-  // Applies one round's swaps and fills r; returns the milliseconds spent in
-  // the swap loops (the round buffer's first allocation is not counted).
-  double apply(const Draws &d, Round &r) {
-    const auto t0 = std::chrono::steady_clock::now();
-    if (do_rows) {
-      const uint32_t *j = d.rows.data();
-      int32_t *a = rows.data();
-      constexpr int64_t kAhead = 32;
-      for (int64_t i = n - 1; i >= 1; --i) {
-        if (i > kAhead) __builtin_prefetch(a + j[i - kAhead], 1, 1);
-        const uint32_t ji = j[i];
-        const int32_t t = a[ji];
-        a[ji] = a[i];
-        a[i] = t;
-      }
-    }
-    if (do_feats && F > 1) {
-      const uint32_t *j = d.feats.data();
-      for (int32_t i = F - 1; i >= 1; --i) std::swap(feats[(size_t)i], feats[j[i]]);
-    }
-    const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    r.rows.alloc((size_t)n_sub);
-    std::memcpy(r.rows.p, rows.data(), (size_t)n_sub * sizeof(int32_t));
-    r.feats.assign(feats.begin(), feats.begin() + f_sub);
-    std::sort(r.feats.begin(), r.feats.end());
-    return ms;
-  }
-
+  // Host mode: Fisher-Yates swaps of each round on the row permutation.
   void run_swaps() {
     try {
       for (;;) {
-        Draws d;
-        Round r;
+        std::unique_ptr<Round> R;
         {
           std::unique_lock<std::mutex> lk(mu);
-          cv.wait(lk, [&] {
-            return stop || produced >= n_rounds ||
-                   (!drawn.empty() && (int32_t)ready.size() < lookahead);
-          });
+          cv.wait(lk, [&] { return stop || produced >= n_rounds || !drawn.empty(); });
           if (stop || produced >= n_rounds) return;
-          d = std::move(drawn.front());
+          R = std::move(drawn.front());
           drawn.pop_front();
-          if (!pool.empty()) {
-            r = std::move(pool.back());
-            pool.pop_back();
-          }
         }
-        cv.notify_all();
-        const double ms = apply(d, r);
+        const auto t0 = std::chrono::steady_clock::now();
+        const uint32_t *j = R->draws.p;
+        int32_t *a = rows.data();
+        constexpr int64_t kAhead = 32;
+        for (int64_t t = 0; t < n - 1; ++t) {
+          if (t + kAhead < n - 1) __builtin_prefetch(a + j[t + kAhead], 1, 1);
+          const int64_t i = n - 1 - t;
+          const uint32_t ji = j[t];
+          const int32_t v = a[ji];
+          a[ji] = a[i];
+          a[i] = v;
+        }
+        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        R->rows.alloc((size_t)n_sub);
+        std::memcpy(R->rows.p, a, (size_t)n_sub * sizeof(int32_t));
         {
           std::lock_guard<std::mutex> lk(mu);
           swap_ms += ms;
-          ready.push_back(std::move(r));
+          ready.push_back(std::move(R));
           ++produced;
-          draw_pool.push_back(std::move(d));
         }
         cv.notify_all();
       }
     } catch (...) {
-      std::lock_guard<std::mutex> lk(mu);
-      error = "sampler: swap thread failed (out of memory?)";
-      stop = true;
-      cv.notify_all();
+      fail("sampler: swap thread failed (out of memory?)");
     }
   }
 
@@ -372,7 +583,7 @@ struct Sampler {
     if (consumed >= n_rounds) return nullptr;
     cv.wait(lk, [&] { return stop || !ready.empty(); });
     if (ready.empty()) return nullptr;
-    Round *r = new Round(std::move(ready.front()));
+    Round *r = ready.front().release();
     ready.pop_front();
     ++consumed;
     lk.unlock();
@@ -383,9 +594,8 @@ struct Sampler {
   void give(Round *r) {
     {
       std::lock_guard<std::mutex> lk(mu);
-      pool.push_back(std::move(*r));
+      pool.emplace_back(r);
     }
-    delete r;
     cv.notify_all();
   }
 
@@ -395,24 +605,25 @@ struct Sampler {
       stop = true;
     }
     cv.notify_all();
+    gen.stop.store(true);
     if (draw_thread.joinable()) draw_thread.join();
     if (swap_thread.joinable()) swap_thread.join();
-    for (auto &r : ready) r.rows.release();
-    for (auto &r : pool) r.rows.release();
+    gen.finish();
   }
 };
 
-int sampler_take(bsscl_sampler *hs, const int32_t **rows, const int32_t **feats,
-                 void **token) {
+int sampler_take(bsscl_sampler *hs, SamplerRound *out, void **token) {
   Sampler *s = reinterpret_cast<Sampler *>(hs);
-  if (!s) return set_error(BSSCL_EINVAL, "sampler: null sampler");
+  if (!s || !out || !token) return set_error(BSSCL_EINVAL, "sampler: null argument");
   Sampler::Round *r = s->take();
   if (!r) {
     std::lock_guard<std::mutex> lk(s->mu);
     return set_error(BSSCL_EINVAL, s->error.empty() ? "sampler: all rounds consumed" : s->error);
   }
-  *rows = r->rows.p;
-  *feats = r->feats.data();
+  out->draws = s->do_rows ? r->draws.p : nullptr;
+  out->rows = (s->do_rows && !s->device_rows) ? r->rows.p : nullptr;
+  out->feats = r->feats.data();
+  out->round = r->index;
   *token = r;
   return BSSCL_OK;
 }
@@ -424,11 +635,15 @@ void sampler_give_back(bsscl_sampler *hs, void *token) {
   s->give(r);
 }
 
-int64_t sampler_n_sub(bsscl_sampler *hs) {
-  return reinterpret_cast<Sampler *>(hs)->n_sub;
-}
-int32_t sampler_f_sub(bsscl_sampler *hs) {
-  return reinterpret_cast<Sampler *>(hs)->f_sub;
+SamplerShape sampler_shape(bsscl_sampler *hs) {
+  const Sampler *s = reinterpret_cast<const Sampler *>(hs);
+  SamplerShape sh;
+  sh.n = s->n;
+  sh.n_sub = s->n_sub;
+  sh.f_sub = s->f_sub;
+  sh.do_rows = s->do_rows;
+  sh.device_rows = s->device_rows;
+  return sh;
 }
 
 }  // namespace bsscl
@@ -461,13 +676,26 @@ int bsscl_rs_shuffle_i32(uint32_t *key, int32_t *pos, int32_t *data,
   return BSSCL_OK;
 }
 
+int bsscl_rs_draws(uint32_t *key, int32_t *pos, uint32_t *draws_out, int64_t n) {
+  if (!key || !pos || (n > 1 && !draws_out) || *pos < 0 || *pos > 624 || n < 0 ||
+      n > INT32_MAX)
+    return bsscl::set_error(BSSCL_EINVAL, "rs_draws: bad state, buffer or length");
+  bsscl::MT mt;
+  mt.load(key, *pos);
+  for (int64_t i = n - 1; i >= 1; --i) draws_out[n - 1 - i] = (uint32_t)mt.interval((uint64_t)i);
+  std::memcpy(key, mt.key, sizeof(mt.key));
+  *pos = mt.pos;
+  return BSSCL_OK;
+}
+
 int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
                          int64_t n_sub, int32_t do_rows, int32_t n_features,
                          int32_t f_sub, int32_t do_feats, int32_t n_rounds,
-                         int32_t lookahead, bsscl_sampler **out) {
+                         int32_t lookahead, int32_t flags, bsscl_sampler **out) {
   if (!key || !out || pos < 0 || pos > 624 || n <= 0 || n > INT32_MAX ||
       n_sub <= 0 || n_sub > n || n_features <= 0 || f_sub <= 0 ||
-      f_sub > n_features || n_rounds < 0 || lookahead < 1)
+      f_sub > n_features || n_rounds < 0 || lookahead < 1 ||
+      (flags & ~BSSCL_SAMPLER_DEVICE_ROWS) != 0)
     return bsscl::set_error(BSSCL_EINVAL, "sampler_create: bad arguments");
   if (!do_rows && n_sub != n)
     return bsscl::set_error(BSSCL_EINVAL,
@@ -477,24 +705,29 @@ int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
                             "sampler_create: f_sub must equal F without column bagging");
   Sampler *s = new (std::nothrow) Sampler();
   if (!s) return bsscl::set_error(BSSCL_ENOMEM, "sampler_create: out of memory");
-  s->mt.load(key, pos);
+  std::memcpy(s->key0, key, sizeof(s->key0));
+  s->pos0 = pos;
   s->n = n;
   s->n_sub = n_sub;
   s->F = n_features;
   s->f_sub = f_sub;
   s->do_rows = do_rows != 0;
   s->do_feats = do_feats != 0;
+  s->device_rows = (flags & BSSCL_SAMPLER_DEVICE_ROWS) != 0;
   s->n_rounds = n_rounds;
   s->lookahead = lookahead;
   std::memcpy(s->final_key, key, sizeof(s->final_key));
   s->final_pos = pos;
   try {
-    s->rows.alloc((size_t)n);
-    for (int64_t i = 0; i < n; ++i) s->rows[(size_t)i] = (int32_t)i;
+    if (s->do_rows && !s->device_rows) {
+      s->rows.alloc((size_t)n);
+      for (int64_t i = 0; i < n; ++i) s->rows[(size_t)i] = (int32_t)i;
+    }
     s->feats.resize((size_t)n_features);
     for (int32_t j = 0; j < n_features; ++j) s->feats[(size_t)j] = j;
+    s->gen.start(key);
     s->draw_thread = std::thread([s] { s->run_draws(); });
-    s->swap_thread = std::thread([s] { s->run_swaps(); });
+    if (s->do_rows && !s->device_rows) s->swap_thread = std::thread([s] { s->run_swaps(); });
   } catch (...) {
     delete s;
     return bsscl::set_error(BSSCL_ENOMEM, "sampler_create: allocation failed");
@@ -505,13 +738,23 @@ int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
 
 int bsscl_sampler_next(bsscl_sampler *hs, int32_t *rows_out,
                        int32_t *feats_out) {
-  const int32_t *rows = nullptr, *feats = nullptr;
-  void *token = nullptr;
-  int rc = bsscl::sampler_take(hs, &rows, &feats, &token);
-  if (rc != BSSCL_OK) return rc;
   Sampler *s = reinterpret_cast<Sampler *>(hs);
-  if (rows_out) std::memcpy(rows_out, rows, (size_t)s->n_sub * sizeof(int32_t));
-  if (feats_out) std::memcpy(feats_out, feats, (size_t)s->f_sub * sizeof(int32_t));
+  if (!s) return bsscl::set_error(BSSCL_EINVAL, "sampler_next: null sampler");
+  if (s->device_rows && s->do_rows)
+    return bsscl::set_error(BSSCL_EINVAL,
+                            "sampler_next: a device-rows sampler's rows exist only on the GPU");
+  bsscl::SamplerRound r;
+  void *token = nullptr;
+  int rc = bsscl::sampler_take(hs, &r, &token);
+  if (rc != BSSCL_OK) return rc;
+  if (rows_out) {
+    if (r.rows) {
+      std::memcpy(rows_out, r.rows, (size_t)s->n_sub * sizeof(int32_t));
+    } else {
+      for (int64_t i = 0; i < s->n_sub; ++i) rows_out[i] = (int32_t)i;
+    }
+  }
+  if (feats_out) std::memcpy(feats_out, r.feats, (size_t)s->f_sub * sizeof(int32_t));
   bsscl::sampler_give_back(hs, token);
   return BSSCL_OK;
 }
@@ -535,8 +778,9 @@ int bsscl_sampler_stats(bsscl_sampler *hs, double *out, int32_t cap,
   Sampler *s = reinterpret_cast<Sampler *>(hs);
   if (!s || !out || !n_out) return bsscl::set_error(BSSCL_EINVAL, "sampler_stats: bad arguments");
   std::lock_guard<std::mutex> lk(s->mu);
-  const double v[3] = {(double)s->produced, s->draw_ms, s->swap_ms};
-  const int32_t k = std::min<int32_t>(cap, 3);
+  const double v[4] = {(double)s->produced, s->draw_ms, s->swap_ms,
+                       s->gen.busy_ms.load(std::memory_order_relaxed)};
+  const int32_t k = std::max<int32_t>(0, std::min<int32_t>(cap, 4));
   for (int32_t i = 0; i < k; ++i) out[i] = v[i];
   *n_out = k;
   return BSSCL_OK;

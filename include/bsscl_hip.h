@@ -169,23 +169,38 @@ int bsscl_partition(bsscl_engine *eng, const int64_t *rows, int64_t m,
                     int64_t *out_n_left);
 
 /* Row/column bagging stream, bit-identical to NumPy RandomState
- * (est:2502-2517).  key[624]/pos come from RandomState.get_state(). */
+ * (est:2502-2517).  key[624]/pos come from RandomState.get_state() and are
+ * updated in place.  rs_shuffle_*: RandomState.shuffle of data[n]. */
 int bsscl_rs_shuffle_i64(uint32_t *key, int32_t *pos, int64_t *data,
                          int64_t n);
 int bsscl_rs_shuffle_i32(uint32_t *key, int32_t *pos, int32_t *data,
                          int64_t n);
+/* The random half of RandomState.shuffle of n items (est:2506): the bounded
+ * draws j(i) of the steps i = n-1 .. 1, draws_out[n-1-i] = j(i). */
+int bsscl_rs_draws(uint32_t *key, int32_t *pos, uint32_t *draws_out, int64_t n);
+/* The swap half of RandomState.shuffle on the GPU (est:2506): data[n] is
+ * permuted in place by the steps i = n-1 .. 1 (swap data[i], data[j(i)])
+ * with draws[n-1-i] = j(i) <= i.  No reference counterpart as a separate
+ * call; bsscl_boost_round uses the same kernels. */
+int bsscl_fisher_yates_apply(bsscl_engine *eng, const uint32_t *draws,
+                             int64_t n, int32_t *data);
+
+/* Sampler flag: the rows are permuted on the GPU by bsscl_boost_round (the
+ * sampler hands it the draws); bsscl_sampler_next then refuses row bagging. */
+#define BSSCL_SAMPLER_DEVICE_ROWS 1
 int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
                          int64_t n_sub, int32_t do_rows, int32_t n_features,
                          int32_t f_sub, int32_t do_feats, int32_t n_rounds,
-                         int32_t lookahead, bsscl_sampler **out);
-/* Next round: ascending in-bag rows (int32[n_sub]) and features
- * (int32[f_sub]); either output may be NULL. */
+                         int32_t lookahead, int32_t flags, bsscl_sampler **out);
+/* Next round: the reference's sample_idx (int32[n_sub], in its order) and
+ * the ascending feature subset (int32[f_sub]); either output may be NULL. */
 int bsscl_sampler_next(bsscl_sampler *s, int32_t *rows_out,
                        int32_t *feats_out);
 int bsscl_sampler_state(bsscl_sampler *s, uint32_t *key_out,
                         int32_t *pos_out);
 /* Host time of the sampler's stages (no reference counterpart): [0] rounds
- * produced, [1] ms drawing bounded integers, [2] ms applying swaps. */
+ * produced, [1] ms drawing bounded integers, [2] ms applying swaps on the
+ * host, [3] ms generating MT19937 words. */
 int bsscl_sampler_stats(bsscl_sampler *s, double *out, int32_t cap,
                         int32_t *n_out);
 void bsscl_sampler_destroy(bsscl_sampler *s);

@@ -152,6 +152,33 @@ def _lockstep_case(engine, n, F, seed, n_bins, max_leaves, max_depth, msl, mcw,
     return treecmp.compare(ref, got, codes, g, h, rows, bc, lam)
 
 
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 64, 1000, 4099])
+def test_fisher_yates_device_adversarial(engine, n):
+    """GPU swaps against the sequential loop for draws no RNG would give:
+    one position chosen by every step, no swaps, a chain through all steps."""
+    from test_sampler import _adversarial_draws
+    import fy_model
+    a0 = np.random.default_rng(n).permutation(n).astype(np.int32)
+    draws = _adversarial_draws(n) if n > 1 else {"empty": np.zeros(0, np.uint32)}
+    for name, d in draws.items():
+        _announce(f"fisher-yates n={n} {name}")
+        np.testing.assert_array_equal(engine.fisher_yates_apply(d, a0),
+                                      fy_model.fisher_yates_sequential(a0, d), err_msg=name)
+
+
+@pytest.mark.parametrize("n", [7, 65_537, 1_000_003])
+def test_fisher_yates_device_equals_numpy_shuffle(engine, n):
+    """The two halves (host draws, GPU swaps) equal RandomState.shuffle."""
+    from bsscl_gbm import _native
+    _announce(f"fisher-yates mt n={n}")
+    rng = np.random.RandomState(n)
+    a = np.arange(n, dtype=np.int32)[::-1].copy()
+    d, _, _ = _native.rs_draws(rng.get_state(), n)
+    got = engine.fisher_yates_apply(d, a)
+    rng.shuffle(a)
+    np.testing.assert_array_equal(got, a)
+
+
 @pytest.mark.parametrize("case", [
     dict(n=10000, F=20, seed=0, n_bins=255, max_leaves=31, max_depth=6, msl=5, mcw=2.0, lam=1.0),
     dict(n=30000, F=28, seed=1, n_bins=255, max_leaves=63, max_depth=6, msl=5, mcw=3.0, lam=1.0, nan=0.05),
