@@ -44,7 +44,7 @@ _SIGS = {
     "bsscl_rs_draws": [_P, _P, _P, _i64],
     "bsscl_fisher_yates_apply": [_P, _P, _i64, _P],
     "bsscl_sampler_create": [_P, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
-                             _i32, _i32, _P],
+                             _i32, _i32, _i32, _P],
     "bsscl_sampler_next": [_P, _P, _P],
     "bsscl_sampler_state": [_P, _P, _P],
     "bsscl_sampler_stats": [_P, _P, _i32, _P],
@@ -284,8 +284,9 @@ class Engine:
         return a
 
     # -- profiling ------------------------------------------------------------
-    def set_profiling(self, on):
-        check(lib().bsscl_engine_set_profiling(self.handle, int(bool(on))))
+    def set_profiling(self, level):
+        """0 off; 1 times the histogram kernel; 2 every kernel group."""
+        check(lib().bsscl_engine_set_profiling(self.handle, int(level)))
 
     def stats(self):
         out = np.zeros(16, np.float64)
@@ -301,7 +302,7 @@ class Sampler:
     """Row/column bagging stream identical to RandomState.shuffle calls."""
 
     def __init__(self, rng_state, n, n_sub, do_rows, n_features, f_sub,
-                 do_feats, n_rounds, lookahead=3, device_rows=False):
+                 do_feats, n_rounds, lookahead=3, device_rows=False, device=0):
         name, key, pos = rng_state[0], rng_state[1], rng_state[2]
         if name != "MT19937":
             raise ValueError("RandomState must use MT19937")
@@ -312,6 +313,7 @@ class Sampler:
                                          int(f_sub), int(bool(do_feats)),
                                          int(n_rounds), int(lookahead),
                                          DEVICE_ROWS if device_rows else 0,
+                                         int(device),
                                          ctypes.byref(h)))
         self._h = h
         self.n_sub, self.f_sub = int(n_sub), int(f_sub)

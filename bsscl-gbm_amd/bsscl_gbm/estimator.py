@@ -447,10 +447,11 @@ class HybridHistGBMNumbaV1_0_1:
                                   n_sub if do_rows else n_samples, do_rows,
                                   n_features, f_sub if do_feats else n_features,
                                   do_feats, int(self.n_estimators),
-                                  device_rows=True)
+                                  device_rows=True, device=eng.device)
         best_val_loss = np.inf
         rounds_no_improve = 0
         hook = getattr(self, '_round_hook', None)
+        self._live_sampler = sampler  # read by profiling hooks during the fit
         try:
             for m in range(self.n_estimators):
                 if hook is not None:
@@ -486,6 +487,7 @@ class HybridHistGBMNumbaV1_0_1:
                             self.trees = self.trees[:self.best_iteration_ + 1]
                             break
         finally:
+            self._live_sampler = None
             sampler.close()
         if hook is not None:
             hook(self.n_estimators, eng)

@@ -5,6 +5,8 @@
 #include <cstdint>
 #include <string>
 
+#include <hip/hip_runtime_api.h>
+
 #include "bsscl_hip.h"
 
 namespace bsscl {
@@ -15,6 +17,8 @@ int set_error(int code, const std::string &msg);
 // Sampler hand-off used by bsscl_boost_round (sampler.cpp).
 struct SamplerRound {
   const uint32_t *draws;  // j(n-1-t) at [t], t < n-1 (row bagging), else null
+  const uint32_t *draws_dev;  // device copy of draws (device-rows samplers)
+  hipEvent_t draws_copied;    // completes when draws_dev is written
   const int32_t *rows;    // sample_idx[n_sub] (host-rows samplers), else null
   const int32_t *feats;   // f_sub ascending feature indices
   int32_t round;          // 0-based round number
@@ -23,6 +27,7 @@ struct SamplerShape {
   int64_t n, n_sub;
   int32_t f_sub;
   bool do_rows, device_rows;
+  int32_t device;
 };
 // Blocks until the next round is ready.  The buffers stay valid (and may be
 // read by copies in flight) until sampler_give_back(token).

@@ -192,7 +192,6 @@ struct bsscl_engine {
   int perm_cur = 0;
   const void *perm_sampler = nullptr;
   int32_t perm_next_round = 0;
-  DevBuf<uint32_t> fy_draws;
   DevBuf<int32_t> fy_head, fy_next, fy_v;
   DevBuf<uint8_t> row_flags;  // all zero between rounds
   int64_t row_flags_n = 0;
@@ -200,7 +199,7 @@ struct bsscl_engine {
   // writes (see ensure_nodes / prepare_tree_buffers for their sizes).
   DevBuf<unsigned long long> pool;
   int32_t node_alloc = 0;      // nodes the node-indexed buffers were sized for
-  int32_t node_cap = 0;        // nodes usable at the current histogram width
+  int32_t node_cap = 0;        // nodes the planner may create in this tree
   int32_t node_cap_floor = 0;  // raised when a tree needed more nodes
   int64_t node_stride = 0;     // int64 words per node histogram
   DevBuf<NodeSeg> segs;
@@ -222,10 +221,14 @@ struct bsscl_engine {
   DevBuf<int64_t> tile_off_d;
   DevBuf<HistTask> hist_tasks_d;
   DevBuf<char> lvl_d;                 // packed inputs of the root (one upload per tree)
+  const int32_t *feat_d = nullptr;    // selected feature indices
   const int32_t *nb_sel_d = nullptr;  // bin counts of the selected features
   const int32_t *hot_sel_d = nullptr; // most frequent bin of each selected feature
   std::vector<int32_t> hot_bin;       // most frequent code per feature of matrix 0
   DevBuf<TreeNodeDev> tree_d;
+  DevBuf<char> round_d;               // RoundHeader + tree arrays of a round
+  char *round_pin = nullptr;          // pinned readback of round_d
+  size_t round_pin_bytes = 0;
   DevBuf<int32_t> offsets_d;
   DevBuf<double> partials_d, loss_d, out_d;
   PinnedArena pin;
@@ -237,7 +240,7 @@ struct bsscl_engine {
   int32_t hist_rows_per_flush = 5120;
 
   // Profiling.
-  bool prof = false;
+  int prof = 0;  // 0 off, 1 histogram kernel timed, 2 every kernel group timed
   std::vector<hipEvent_t> ev_pool;
   size_t ev_used = 0;
   struct Pending {
@@ -265,7 +268,9 @@ int ev_pair(bsscl_engine *E, hipEvent_t &a, hipEvent_t &b) {
 // Starts a timed region of `kind` when profiling; returns the stop event.
 int prof_begin(bsscl_engine *E, int kind, hipEvent_t *stop) {
   *stop = nullptr;
-  if (!E->prof) return BSSCL_OK;
+  // Level 1 times the histogram kernel only; level 2 every kernel group
+  // (each event pair costs a few microseconds of queue time).
+  if (E->prof < (kind == 0 ? 1 : 2)) return BSSCL_OK;
   hipEvent_t a, b;
   CHK(ev_pair(E, a, b));
   HIPCHK(hipEventRecord(a, E->st));
@@ -356,10 +361,8 @@ int ensure_nodes(bsscl_engine *E, int32_t cap, int32_t F_sel) {
   const int64_t stride = (int64_t)F_sel * kHistPerFeat;
   if (cap <= E->node_alloc && (size_t)cap * stride <= E->pool.cap &&
       (size_t)cap * F_sel <= E->cand.cap) {
-    // Usable capacity: what every node-indexed buffer holds at this width.
-    E->node_cap = (int32_t)std::min<int64_t>(
-        E->node_alloc, std::min<int64_t>((int64_t)(E->pool.cap / (size_t)stride),
-                                         (int64_t)(E->cand.cap / (size_t)F_sel)));
+    // Exactly the requested capacity: the level lists are sized from it.
+    E->node_cap = cap;
     E->node_stride = stride;
     return BSSCL_OK;
   }
@@ -595,7 +598,12 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
   for (int s = 0; s < 2; ++s)
     grow = grow || E->codes_c[s].cap < (size_t)ld_c * F_sel || E->gh_c[s].cap < (size_t)ld_c ||
            E->rid_c[s].cap < (size_t)ld_c;
-  const int32_t cap = std::max(initial_node_cap(levels, max_leaves), E->node_cap_floor);
+  int32_t cap = std::max(initial_node_cap(levels, max_leaves), E->node_cap_floor);
+  // Test hook: a small starting node table, to exercise the regrowth path.
+  if (const char *t = std::getenv("BSSCL_TEST_NODE_CAP")) {
+    const long v = std::strtol(t, nullptr, 10);
+    if (v >= 3) cap = std::max<int32_t>((int32_t)std::min<long>(v, cap), E->node_cap_floor);
+  }
   const int64_t tcap = m / kPartTile + (int64_t)cap + 4;
   const int64_t hcap = (int64_t)hist_target(E, F_sel) + cap + 4;
   if (tcap > INT32_MAX / 2 || hcap > INT32_MAX / 2)
@@ -664,6 +672,7 @@ int launch_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_
   HIPCHK(hipMemcpyAsync(E->plan_d, dv[4], sizeof(LevelPlan), hipMemcpyDeviceToDevice, E->st));
   const int32_t *feat_d = reinterpret_cast<const int32_t *>(dv[0]);
   // The root's arena stays untouched until the next tree's upload.
+  E->feat_d = feat_d;
   E->nb_sel_d = reinterpret_cast<const int32_t *>(dv[1]);
   E->hot_sel_d = E->nb_sel_d + F_sel;
   HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, feat_d, F_sel,
@@ -790,13 +799,114 @@ int read_table(bsscl_engine *E, int32_t n, LevelPlan &plan) {
   return BSSCL_OK;
 }
 
+// One boosting round's readback: RoundHeader, then the tree arrays of M
+// entries (features i32, thresholds i64, values f64, left i32, right i32,
+// gains f64), each 8-byte aligned.
+size_t round_out_bytes(int32_t M) {
+  const size_t a4 = ((size_t)M * 4 + 7) & ~size_t(7);
+  return sizeof(RoundHeader) + 3 * a4 + 3 * (size_t)M * 8;
+}
+
+TreeArrays round_arrays(char *base, int32_t M) {
+  const size_t a4 = ((size_t)M * 4 + 7) & ~size_t(7);
+  char *p = base + sizeof(RoundHeader);
+  TreeArrays t;
+  t.features = reinterpret_cast<int32_t *>(p);
+  p += a4;
+  t.thresholds = reinterpret_cast<int64_t *>(p);
+  p += (size_t)M * 8;
+  t.values = reinterpret_cast<double *>(p);
+  p += (size_t)M * 8;
+  t.left = reinterpret_cast<int32_t *>(p);
+  p += a4;
+  t.right = reinterpret_cast<int32_t *>(p);
+  p += a4;
+  t.gains = reinterpret_cast<double *>(p);
+  return t;
+}
+
+int ensure_round_out(bsscl_engine *E, int32_t M) {
+  const size_t bytes = round_out_bytes(M);
+  CHK(E->round_d.ensure(bytes));
+  if (E->round_pin_bytes < bytes) {
+    CHK(sync(E));
+    if (E->round_pin) (void)hipHostFree(E->round_pin);
+    E->round_pin = nullptr;
+    E->round_pin_bytes = 0;
+    HIPCHK(hipHostMalloc(reinterpret_cast<void **>(&E->round_pin), bytes, hipHostMallocDefault));
+    E->round_pin_bytes = bytes;
+  }
+  return BSSCL_OK;
+}
+
+// Device Fisher-Yates work arrays for n items.
+int ensure_fy_work(bsscl_engine *E, int64_t n, FyWork &w) {
+  for (DevBuf<int32_t> *x : {&E->fy_head, &E->fy_next, &E->fy_v}) CHK(x->ensure((size_t)n));
+  w.head = E->fy_head.p;
+  w.next = E->fy_next.p;
+  w.v = E->fy_v.p;
+  return BSSCL_OK;
+}
+
 constexpr int32_t kLevelsPerCheck = 8;  // levels enqueued between host checks
 
+// Enqueues the root and every level of one tree (after
+// prepare_tree_buffers).  All levels are enqueued without host round trips:
+// the planner kernel chooses each level's parents on the device; every
+// kLevelsPerCheck levels the host reads the plan and stops enqueueing once
+// the tree has ended.  *run = levels enqueued.
+int launch_tree(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_t> &feats,
+                const std::vector<int32_t> &nb_sel, const TreeParams &tp, int32_t *run) {
+  const int32_t F_sel = (int32_t)feats.size();
+  const int32_t levels = std::max(1, tp.max_depth);
+  CHK(launch_root(E, use32, m, feats, nb_sel, tp));
+  *run = 0;
+  for (int32_t d = 0; d < levels; ++d) {
+    const bool last = d + 1 >= tp.max_depth;
+    CHK(launch_level_plan(E, d, last, tp, F_sel));
+    if (d > 0 && d % kLevelsPerCheck == 0) {
+      LevelPlan plan;
+      CHK(read_table(E, 0, plan));
+      if (plan.n_parents == 0 || plan.overflow != 0) break;
+    }
+    CHK(launch_level(E, d, last, m, tp, F_sel));
+    *run = d + 1;
+  }
+  return BSSCL_OK;
+}
+
+// Nodes a tree of `run` enqueued levels can have (bounds the readback).
+int32_t table_bound(bsscl_engine *E, int32_t run) {
+  const int64_t most = run >= 30 ? INT32_MAX : ((int64_t)2 << run) - 1;
+  return (int32_t)std::min<int64_t>(most, E->node_cap);
+}
+
+// Profiling counters of one built tree from its node table: histogram
+// rows x features and algorithmic bytes (the root and the smaller child of
+// every kept split above the last level), nodes expanded, trees.
+void tree_stats(bsscl_engine *E, const NodeOut *t, int32_t n, int64_t m, int32_t F_sel,
+                const TreeParams &tp) {
+  std::vector<int32_t> depth((size_t)n, 0);
+  E->stats[2] += (double)m * F_sel;
+  E->stats[3] += (double)m * (F_sel + 8);
+  for (int32_t i = 0; i < n; ++i) {
+    const int32_t l = t[i].left;
+    if (l < 0 || l + 1 >= n) continue;
+    depth[(size_t)l] = depth[(size_t)l + 1] = depth[(size_t)i] + 1;
+    E->stats[9] += 1.0;
+    if (t[l].valid && depth[(size_t)i] + 1 < tp.max_depth) {
+      const int64_t ms = std::min(t[l].count, t[l + 1].count);
+      E->stats[2] += (double)ms * F_sel;
+      E->stats[3] += (double)ms * (F_sel + 8);
+    }
+  }
+  E->stats[8] += 1.0;
+}
+
 // Builds one tree from the rows already in E->rows32 (use32) or E->rows64,
-// with quantized gradients in E->ghq.  All levels are enqueued without host
-// round trips: the planner kernel chooses each level's parents on the
-// device, and the node table comes back once at the end (every
-// kLevelsPerCheck levels the host also checks whether the tree has ended).
+// with quantized gradients in E->ghq, and replays the reference's candidate
+// loop on the host.  The node table comes back once (twice when it had to
+// grow).
 int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
                     const std::vector<int32_t> &feats,
                     const std::vector<int32_t> &nb_sel, const TreeParams &tp,
@@ -806,20 +916,9 @@ int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
   LevelPlan plan = {};
   for (;;) {
     CHK(prepare_tree_buffers(E, m, F_sel, levels, tp.max_leaves));
-    CHK(launch_root(E, use32, m, feats, nb_sel, tp));
     int32_t run = 0;
-    for (int32_t d = 0; d < levels; ++d) {
-      const bool last = d + 1 >= tp.max_depth;
-      CHK(launch_level_plan(E, d, last, tp, F_sel));
-      if (d > 0 && d % kLevelsPerCheck == 0) {
-        CHK(read_table(E, 0, plan));
-        if (plan.n_parents == 0 || plan.overflow != 0) break;
-      }
-      CHK(launch_level(E, d, last, m, tp, F_sel));
-      run = d + 1;
-    }
-    const int64_t most = run >= 30 ? INT32_MAX : ((int64_t)2 << run) - 1;
-    CHK(read_table(E, (int32_t)std::min<int64_t>(most, E->node_cap), plan));
+    CHK(launch_tree(E, use32, m, feats, nb_sel, tp, &run));
+    CHK(read_table(E, table_bound(E, run), plan));
     if (plan.overflow < 0) return set_error(BSSCL_EINTERNAL, "tree builder: level list overflow");
     if (plan.overflow == 0) break;
     // The node table was too small: grow it and build the tree again.
@@ -829,7 +928,6 @@ int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
   if (n < 1 || n > E->node_cap) return set_error(BSSCL_EINTERNAL, "tree builder: bad node count");
   const NodeOut *t = reinterpret_cast<const NodeOut *>(E->table_pin + 64);
   std::vector<HNode> nodes((size_t)n);
-  std::vector<int32_t> depth((size_t)n, 0);
   for (int32_t i = 0; i < n; ++i) {
     HNode &nd = nodes[(size_t)i];
     const NodeOut &o = t[i];
@@ -852,25 +950,10 @@ int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
       nd.nr = t[o.left + 1].count;
       nd.split_ok = t[o.left].valid != 0;
       nodes[(size_t)o.left].parent = nodes[(size_t)o.left + 1].parent = i;
-      depth[(size_t)o.left] = depth[(size_t)o.left + 1] = depth[(size_t)i] + 1;
     }
   }
   if (root_out) *root_out = nodes[0];
-  if (E->prof) {
-    E->stats[2] += (double)m * F_sel;
-    E->stats[3] += (double)m * (F_sel + 8);
-    for (int32_t i = 0; i < n; ++i) {
-      const HNode &v = nodes[(size_t)i];
-      if (!v.expanded) continue;
-      E->stats[9] += 1.0;
-      if (v.split_ok && depth[(size_t)i] + 1 < tp.max_depth) {
-        const int64_t ms = std::min(v.nl, v.nr);
-        E->stats[2] += (double)ms * F_sel;
-        E->stats[3] += (double)ms * (F_sel + 8);
-      }
-    }
-    E->stats[8] += 1.0;
-  }
+  if (E->prof) tree_stats(E, t, n, m, F_sel, tp);
   return replay(E, nodes, feats, tp, out);
 }
 
@@ -1043,10 +1126,10 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->rows_in.release();
   E->sort_tmp.release();
   for (int s = 0; s < 2; ++s) E->perm[s].release();
-  E->fy_draws.release();
   E->fy_head.release();
   E->fy_next.release();
   E->fy_v.release();
+
   E->row_flags.release();
   E->lvl_d.release();
   E->table_d.release();
@@ -1068,6 +1151,8 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->tile_off_d.release();
   E->hist_tasks_d.release();
   E->tree_d.release();
+  E->round_d.release();
+  if (E->round_pin) (void)hipHostFree(E->round_pin);
   E->offsets_d.release();
   E->partials_d.release();
   E->loss_d.release();
@@ -1283,14 +1368,13 @@ int bsscl_boost_round(bsscl_engine *E, bsscl_sampler *sampler,
     if (!sh.do_rows) {
       e = launch_iota(E->st, E->rows32.p, m);  // every row, in order
     } else if (sh.device_rows) {
+      if (sh.device != E->device)
+        rc = set_error(BSSCL_EINVAL, "boost_round: the sampler copies its draws to another GPU");
       // Cumulative permutation: identity before the sampler's first round.
-      if (sr.round == 0) {
+      if (rc != BSSCL_OK) {
+      } else if (sr.round == 0) {
         rc = E->perm[0].ensure((size_t)X.n);
         if (rc == BSSCL_OK) rc = E->perm[1].ensure((size_t)X.n);
-        if (rc == BSSCL_OK) rc = E->fy_draws.ensure((size_t)X.n);
-        if (rc == BSSCL_OK) rc = E->fy_head.ensure((size_t)X.n);
-        if (rc == BSSCL_OK) rc = E->fy_next.ensure((size_t)X.n);
-        if (rc == BSSCL_OK) rc = E->fy_v.ensure((size_t)X.n);
         if (rc == BSSCL_OK) {
           E->perm_cur = 0;
           E->perm_sampler = sampler;
@@ -1300,12 +1384,14 @@ int bsscl_boost_round(bsscl_engine *E, bsscl_sampler *sampler,
       } else if (E->perm_sampler != sampler || E->perm_next_round != sr.round) {
         rc = set_error(BSSCL_EINVAL, "boost_round: the sampler's earlier rounds did not run on this engine");
       }
-      if (rc == BSSCL_OK && e == hipSuccess && X.n > 1)
-        e = hipMemcpyAsync(E->fy_draws.p, sr.draws, (size_t)(X.n - 1) * 4, hipMemcpyHostToDevice, E->st);
+      FyWork w;
+      if (rc == BSSCL_OK) rc = ensure_fy_work(E, X.n, w);
+      // The sampler copied the draws on its own stream.
+      if (rc == BSSCL_OK && e == hipSuccess) e = hipStreamWaitEvent(E->st, sr.draws_copied, 0);
       if (rc == BSSCL_OK && e == hipSuccess) {
         const int nxt = E->perm_cur ^ 1;
-        e = launch_fisher_yates(E->st, E->fy_draws.p, X.n, E->perm[E->perm_cur].p,
-                                E->perm[nxt].p, E->fy_head.p, E->fy_next.p, E->fy_v.p);
+        e = launch_fisher_yates(E->st, sr.draws_dev, X.n, E->perm[E->perm_cur].p,
+                                E->perm[nxt].p, w);
         E->perm_cur = nxt;
         E->perm_next_round = sr.round + 1;
         rows_d = E->perm[nxt].p;
@@ -1326,23 +1412,95 @@ int bsscl_boost_round(bsscl_engine *E, bsscl_sampler *sampler,
   }
   TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight,
                 reg_lambda, gamma};
-  rc = build_tree_core(E, true, m, feats, nb_sel, tp, out);
-  // build_tree_core synchronised the stream, so the pinned rows are free.
+  // The tree, its replay (est:641-820), F += lr * tree(X) and the training
+  // log-loss all run on the device; one readback brings the tree and the
+  // loss.  A tree that needs a larger node table, or more candidate slots
+  // than the device replay holds, is built again by the host-driven path.
+  const int32_t F_sel = (int32_t)feats.size();
+  const int32_t M = 2 * max_leaves + 2;
+  const int nb = update_F_blocks(X.n);
+  int32_t run = 0;
+  // More candidate slots than the device replay holds: host replay only.
+  // (Test hook: BSSCL_TEST_HOST_REPLAY=1 forces the host path.)
+  const char *force_host = std::getenv("BSSCL_TEST_HOST_REPLAY");
+  const bool device_replay = max_leaves + 2 <= kReplaySlots && !(force_host && force_host[0] == '1');
+  if (rc == BSSCL_OK && device_replay)
+    rc = prepare_tree_buffers(E, m, F_sel, std::max(1, max_depth), max_leaves);
+  if (rc == BSSCL_OK) rc = E->partials_d.ensure((size_t)nb);
+  if (rc == BSSCL_OK) rc = E->tree_d.ensure((size_t)M);
+  if (rc == BSSCL_OK) rc = ensure_round_out(E, M);
+  if (rc == BSSCL_OK && device_replay) rc = launch_tree(E, true, m, feats, nb_sel, tp, &run);
+  RoundHeader *hdr = reinterpret_cast<RoundHeader *>(E->round_d.p);
+  const TreeArrays arrays = round_arrays(E->round_d.p, M);
+  if (rc == BSSCL_OK && !device_replay) {
+    rc = sync(E);  // the sampler's buffers must be read before they go back
+  } else if (rc == BSSCL_OK) {
+    ReplayArgs ra;
+    ra.gamma = gamma;
+    ra.reg_lambda = reg_lambda;
+    ra.g_scale = E->g_scale;
+    ra.h_scale = E->h_scale;
+    ra.max_leaves = max_leaves;
+    ra.out_len = M;
+    // (Test hook BSSCL_TEST_REPLAY_GLOBAL: 1 reads the node table from HBM,
+    // 2 keeps the candidate slots in LDS instead of registers.)
+    const char *rg = std::getenv("BSSCL_TEST_REPLAY_GLOBAL");
+    ra.stage_limit = !rg ? (1 << 30) : rg[0] == '1' ? 0 : rg[0] == '2' ? 1023 : (1 << 30);
+    ra.node_cap = E->node_cap;
+    hipError_t e = launch_replay(E->st, E->nodes_d, E->plan_d, E->feat_d, ra, arrays,
+                                 E->tree_d.p, hdr);
+    if (e == hipSuccess)
+      e = launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, &hdr->node_count,
+                          learning_rate, E->F.p, E->y.p, E->partials_d.p, nb);
+    if (e == hipSuccess) e = launch_sum_partials(E->st, E->partials_d.p, nb, &hdr->loss_sum);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(E->round_pin, E->round_d.p, round_out_bytes(M), hipMemcpyDeviceToHost, E->st);
+    const int32_t tb = table_bound(E, run);
+    if (e == hipSuccess && E->prof)
+      e = hipMemcpyAsync(E->table_pin, E->table_d.p, 64 + (size_t)tb * sizeof(NodeOut),
+                         hipMemcpyDeviceToHost, E->st);
+    if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("round: ") + hipGetErrorString(e));
+    if (rc == BSSCL_OK) rc = sync(E);
+    if (rc == BSSCL_OK && E->prof) {
+      const LevelPlan *pl = reinterpret_cast<const LevelPlan *>(E->table_pin);
+      if (pl->overflow == 0 && pl->n_nodes >= 1 && pl->n_nodes <= tb)
+        tree_stats(E, reinterpret_cast<const NodeOut *>(E->table_pin + 64), pl->n_nodes, m, F_sel, tp);
+    }
+  }
+  // The sampler's buffers are no longer read once the stream is idle.
+  if (rc != BSSCL_OK) (void)hipStreamSynchronize(E->st);
   sampler_give_back(sampler, token);
   CHK(rc);
-  // F += lr * tree(X) over all rows, then the training log-loss.
-  CHK(upload_tree(E, out_features, out_thresholds, out_values, out_left,
-                  out_right, *out_node_count, X.F));
-  const int nb = update_F_blocks(X.n);
-  CHK(E->partials_d.ensure((size_t)nb));
-  CHK(E->loss_d.ensure(1));
-  HIPCHK(launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, *out_node_count,
-                         learning_rate, E->F.p, E->y.p, E->partials_d.p, nb));
-  HIPCHK(launch_sum_partials(E->st, E->partials_d.p, nb, E->loss_d.p));
-  double s = 0.0;
-  HIPCHK(hipMemcpyAsync(&s, E->loss_d.p, 8, hipMemcpyDeviceToHost, E->st));
-  CHK(sync(E));
-  if (out_train_loss) *out_train_loss = -s / (double)X.n;
+  RoundHeader h = *reinterpret_cast<const RoundHeader *>(E->round_pin);
+  if (!device_replay) h.status = 4;
+  if (h.status == 0) {
+    const TreeArrays ha = round_arrays(E->round_pin, M);
+    std::memcpy(out_features, ha.features, (size_t)M * 4);
+    std::memcpy(out_thresholds, ha.thresholds, (size_t)M * 8);
+    std::memcpy(out_values, ha.values, (size_t)M * 8);
+    std::memcpy(out_left, ha.left, (size_t)M * 4);
+    std::memcpy(out_right, ha.right, (size_t)M * 4);
+    std::memcpy(out_split_gains, ha.gains, (size_t)M * 8);
+    *out_node_count = h.node_count;
+    if (out_train_loss) *out_train_loss = -h.loss_sum / (double)X.n;
+  } else if (h.status == 1 || h.status == 4) {
+    // F was left alone: build the tree on the host-driven path and apply it.
+    if (h.status == 1) E->node_cap_floor = std::max(h.needed, 2 * E->node_cap);
+    CHK(build_tree_core(E, true, m, feats, nb_sel, tp, out));
+    CHK(upload_tree(E, out_features, out_thresholds, out_values, out_left,
+                    out_right, *out_node_count, X.F));
+    CHK(E->loss_d.ensure(1));
+    HIPCHK(launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, nullptr,
+                           learning_rate, E->F.p, E->y.p, E->partials_d.p, nb));
+    HIPCHK(launch_sum_partials(E->st, E->partials_d.p, nb, E->loss_d.p));
+    double s = 0.0;
+    HIPCHK(hipMemcpyAsync(&s, E->loss_d.p, 8, hipMemcpyDeviceToHost, E->st));
+    CHK(sync(E));
+    if (out_train_loss) *out_train_loss = -s / (double)X.n;
+  } else {
+    return set_error(BSSCL_EINTERNAL, "tree builder: device replay failed (status " +
+                                          std::to_string(h.status) + ")");
+  }
   if (E->prof)
     E->stats[11] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_wait0).count();
   return BSSCL_OK;
@@ -1548,23 +1706,25 @@ int bsscl_fisher_yates_apply(bsscl_engine *E, const uint32_t *draws, int64_t n,
                                          " exceeds its step " + std::to_string(n - 1 - t));
   if (n <= 1) return BSSCL_OK;
   HIPCHK(hipSetDevice(E->device));
-  DevBuf<int32_t> a, b, head, next, v;
+  DevBuf<int32_t> a, b;
   DevBuf<uint32_t> d;
+  FyWork w;
   int rc = BSSCL_OK;
-  for (DevBuf<int32_t> *x : {&a, &b, &head, &next, &v})
+  for (DevBuf<int32_t> *x : {&a, &b})
     if (rc == BSSCL_OK) rc = x->ensure((size_t)n);
   if (rc == BSSCL_OK) rc = d.ensure((size_t)n);
+  if (rc == BSSCL_OK) rc = ensure_fy_work(E, n, w);
   hipError_t e = hipSuccess;
   if (rc == BSSCL_OK) {
     e = hipMemcpyAsync(a.p, data, (size_t)n * 4, hipMemcpyHostToDevice, E->st);
     if (e == hipSuccess) e = hipMemcpyAsync(d.p, draws, (size_t)(n - 1) * 4, hipMemcpyHostToDevice, E->st);
-    if (e == hipSuccess) e = launch_fisher_yates(E->st, d.p, n, a.p, b.p, head.p, next.p, v.p);
+    if (e == hipSuccess) e = launch_fisher_yates(E->st, d.p, n, a.p, b.p, w);
     if (e == hipSuccess) e = hipMemcpyAsync(data, b.p, (size_t)n * 4, hipMemcpyDeviceToHost, E->st);
     if (e == hipSuccess) e = hipStreamSynchronize(E->st);
     if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("fisher_yates_apply: ") + hipGetErrorString(e));
   }
   (void)hipStreamSynchronize(E->st);
-  for (DevBuf<int32_t> *x : {&a, &b, &head, &next, &v}) x->release();
+  for (DevBuf<int32_t> *x : {&a, &b}) x->release();
   d.release();
   return rc;
 }
@@ -1574,7 +1734,7 @@ int bsscl_engine_set_profiling(bsscl_engine *E, int32_t on) {
   HIPCHK(hipSetDevice(E->device));
   HIPCHK(hipStreamSynchronize(E->st));
   CHK(prof_collect(E));
-  E->prof = on != 0;
+  E->prof = std::max(0, std::min(2, (int)on));
   if (on) std::memset(E->stats, 0, sizeof(E->stats));
   return BSSCL_OK;
 }

@@ -123,6 +123,43 @@ struct NodeOut {
   int32_t left;    // id of the left child (right = left + 1), -1 if not expanded
 };
 
+// Result header of one boosting round on the device, read back with the
+// tree arrays in one copy.
+struct RoundHeader {
+  int32_t node_count;  // nodes of the replayed tree, 0 when status != 0
+  int32_t status;      // 0 ok; 1 node table too small (needed nodes in
+                       // `needed`); 2 a popped node was not expanded;
+                       // 3 no free candidate slot; 4 too many leaves for the
+                       // device replay; 5 level lists overflowed
+  int32_t needed;
+  int32_t pad;
+  double loss_sum;     // sum over rows of y log p + (1-y) log(1-p)
+  double pad2[5];
+};
+
+struct ReplayArgs {
+  double gamma;
+  double reg_lambda;
+  double g_scale;
+  double h_scale;
+  int32_t max_leaves;
+  int32_t out_len;     // 2 * max_leaves + 2 entries per output array
+  int32_t stage_limit; // node records are staged in LDS up to this many nodes
+  int32_t node_cap;    // node table capacity of the tree
+};
+
+// Output arrays of the replayed tree (the reference's 7-tuple layout).
+struct TreeArrays {
+  int32_t *features;
+  int64_t *thresholds;
+  double *values;
+  int32_t *left;
+  int32_t *right;
+  double *gains;
+};
+
+constexpr int kReplaySlots = 1024;  // candidate slots the device replay holds
+
 // Launchers (kernels.hip).  All are asynchronous on `st`.
 hipError_t launch_bin(hipStream_t st, const void *X, int is_f64, int64_t n,
                       int32_t F, const double *edges, int32_t stride,
@@ -145,11 +182,14 @@ hipError_t launch_sort_rows(hipStream_t st, const int32_t *rows, int64_t m,
                             int32_t *out);
 int64_t sort_rows_flag_bytes(int64_t n);
 hipError_t launch_iota(hipStream_t st, int32_t *a, int64_t n);
+// Work arrays of the device Fisher-Yates (fisher_yates.hip): int32[n] each.
+struct FyWork {
+  int32_t *head, *next, *v;
+};
 // a_new = a_old after the Fisher-Yates steps i = n-1 .. 1 with draws[t] =
-// j(n-1-t) <= n-1-t; head, next and v are int32[n] work arrays.
+// j(n-1-t) <= n-1-t.
 hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
-                               const int32_t *a_old, int32_t *a_new, int32_t *head,
-                               int32_t *next, int32_t *v);
+                               const int32_t *a_old, int32_t *a_new, const FyWork &w);
 hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               const int32_t *feat, int32_t F_sel,
                               const int32_t *rows32, const int64_t *rows64,
@@ -212,11 +252,19 @@ hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                        double *work_e, PlanArgs a);
 hipError_t launch_code_counts(hipStream_t st, const uint8_t *codes, int64_t ld,
                               int64_t n, int32_t F, unsigned int *counts);
+// F += lr * tree(row) for every row unless *node_count_d == 0 (then F is
+// left alone); per-block partial sums of the training log-likelihood.
 hipError_t launch_update_F(hipStream_t st, const uint8_t *codes, int64_t ld,
                            int64_t n, const TreeNodeDev *tree,
-                           int32_t node_count, double lr, double *F,
+                           const int32_t *node_count_d, double lr, double *F,
                            const uint8_t *y, double *loss_partials,
                            int32_t n_blocks);
+// The reference's best-first candidate loop (est:641-820) over the node
+// table, one wave: writes the tree arrays, its TreeNodeDev form and
+// hdr->node_count / status.
+hipError_t launch_replay(hipStream_t st, const NodeOut *nodes, const LevelPlan *plan,
+                         const int32_t *feats, ReplayArgs a, TreeArrays out,
+                         TreeNodeDev *tree, RoundHeader *hdr);
 hipError_t launch_sum_partials(hipStream_t st, const double *partials,
                                int32_t count, double *out);
 hipError_t launch_predict_tree(hipStream_t st, const uint8_t *codes,

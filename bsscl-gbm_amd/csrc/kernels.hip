@@ -456,149 +456,10 @@ hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
   return hipGetLastError();
 }
 
-// ---------------------------------------------------------------------------
-// Fisher-Yates on the device: the swap half of the reference's bagging
-// shuffle (est:2506), given the draws j(i) made on the host.
-//
-// Step i (i = n-1 .. 1, in that order) swaps positions i and j(i) <= i, and
-// position i never changes after step i.  Let the steps that choose
-// position p (j(k) = p, k > p) be s_1 < ... < s_L; they run s_L first.  Then
-// position p holds a_old[p] until step s_L, and after step s_m it holds the
-// value that step s_m brought from position s_m, v(s_m), where
-//   v(k) = the value at position k just before step k
-//        = v(s_1(k)) if any step chose k before, else a_old[k].
-// So a_new[s_m] = v(s_{m+1}) for m < L, a_new[s_L] = a_old[p],
-// a_new[i] = v(i) when j(i) = i, and a_new[0] = v(0).
-//
-// Kernels: every step k with j(k) != k pushes itself on position j(k)'s
-// list (atomic exchange); each list is sorted ascending (head = s_1, links
-// s_m -> s_{m+1}, the last link encodes p as -2 - p); the chains
-// k -> s_1(k) -> ... strictly increase and are followed to their end for
-// v(k); a last pass writes a_new.  Every kernel is O(n) in total for any
-// draws (lists are merge-sorted), and the result is the sequential one.
-// ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_iota(int32_t *__restrict__ a, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
     a[i] = (int32_t)i;
-}
-
-__global__ __launch_bounds__(256) void k_fill_i32(int32_t *__restrict__ a, int64_t n, int32_t v) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    a[i] = v;
-}
-
-// draws[t] = j(n-1-t) for t in [0, n-1).
-__global__ __launch_bounds__(256) void k_fy_push(const uint32_t *__restrict__ draws, int64_t n,
-                                                 int32_t *__restrict__ head,
-                                                 int32_t *__restrict__ next) {
-  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < n - 1;
-       t += (int64_t)gridDim.x * blockDim.x) {
-    const int32_t k = (int32_t)(n - 1 - t);
-    const int32_t p = (int32_t)draws[t];
-    if (p != k) next[k] = atomicExch(head + p, k);
-  }
-}
-
-// Ascending sort of the list starting at `h` (links in next[], -1 ends it).
-__device__ int32_t fy_list_sort(int32_t h, int32_t *__restrict__ next) {
-  int64_t L = 0;
-  for (int32_t x = h; x >= 0; x = next[x]) ++L;
-  if (L <= 1) return h;
-  if (L <= 16) {  // insertion into a new list
-    int32_t sorted = -1;
-    for (int32_t x = h; x >= 0;) {
-      const int32_t nx = next[x];
-      if (sorted < 0 || x < sorted) {
-        next[x] = sorted;
-        sorted = x;
-      } else {
-        int32_t y = sorted;
-        while (next[y] >= 0 && next[y] < x) y = next[y];
-        next[x] = next[y];
-        next[y] = x;
-      }
-      x = nx;
-    }
-    return sorted;
-  }
-  for (int64_t width = 1; width < L; width *= 2) {  // bottom-up merge sort
-    int32_t cur = h, new_head = -1, tail = -1;
-    while (cur >= 0) {
-      int32_t a = cur, at = cur;
-      for (int64_t k = 1; k < width && next[at] >= 0; ++k) at = next[at];
-      int32_t b = next[at];
-      next[at] = -1;
-      int32_t rest = -1;
-      if (b >= 0) {
-        int32_t bt = b;
-        for (int64_t k = 1; k < width && next[bt] >= 0; ++k) bt = next[bt];
-        rest = next[bt];
-        next[bt] = -1;
-      }
-      while (a >= 0 || b >= 0) {
-        int32_t take;
-        if (b < 0 || (a >= 0 && a < b)) {
-          take = a;
-          a = next[a];
-        } else {
-          take = b;
-          b = next[b];
-        }
-        if (tail < 0) new_head = take;
-        else next[tail] = take;
-        tail = take;
-      }
-      next[tail] = -1;
-      cur = rest;
-    }
-    h = new_head;
-  }
-  return h;
-}
-
-__global__ __launch_bounds__(256) void k_fy_sort(int32_t *__restrict__ head,
-                                                 int32_t *__restrict__ next, int64_t n) {
-  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < n;
-       p += (int64_t)gridDim.x * blockDim.x) {
-    int32_t h = head[p];
-    if (h < 0) continue;
-    h = fy_list_sort(h, next);
-    head[p] = h;
-    int32_t x = h;
-    while (next[x] >= 0) x = next[x];
-    next[x] = -2 - (int32_t)p;
-  }
-}
-
-__global__ __launch_bounds__(256) void k_fy_resolve(const int32_t *__restrict__ head,
-                                                    const int32_t *__restrict__ a_old,
-                                                    int32_t *__restrict__ v, int64_t n) {
-  for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < n;
-       k += (int64_t)gridDim.x * blockDim.x) {
-    int32_t x = (int32_t)k;
-    for (int32_t h = head[x]; h >= 0; h = head[x]) x = h;
-    v[k] = a_old[x];
-  }
-}
-
-__global__ __launch_bounds__(256) void k_fy_final(const uint32_t *__restrict__ draws, int64_t n,
-                                                  const int32_t *__restrict__ next,
-                                                  const int32_t *__restrict__ v,
-                                                  const int32_t *__restrict__ a_old,
-                                                  int32_t *__restrict__ a_new) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    int32_t out;
-    if (i == 0 || (int64_t)draws[n - 1 - i] == i) {
-      out = v[i];
-    } else {
-      const int32_t g = next[i];
-      out = g >= 0 ? v[g] : a_old[-2 - g];
-    }
-    a_new[i] = out;
-  }
 }
 
 static unsigned elementwise_blocks(int64_t n) {
@@ -608,19 +469,6 @@ static unsigned elementwise_blocks(int64_t n) {
 hipError_t launch_iota(hipStream_t st, int32_t *a, int64_t n) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_iota, dim3(elementwise_blocks(n)), dim3(256), 0, st, a, n);
-  return hipGetLastError();
-}
-
-hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
-                               const int32_t *a_old, int32_t *a_new, int32_t *head,
-                               int32_t *next, int32_t *v) {
-  if (n <= 0) return hipSuccess;
-  const dim3 g(elementwise_blocks(n)), b(256);
-  hipLaunchKernelGGL(k_fill_i32, g, b, 0, st, head, n, -1);
-  if (n > 1) hipLaunchKernelGGL(k_fy_push, g, b, 0, st, draws, n, head, next);
-  hipLaunchKernelGGL(k_fy_sort, g, b, 0, st, head, next, n);
-  hipLaunchKernelGGL(k_fy_resolve, g, b, 0, st, head, a_old, v, n);
-  hipLaunchKernelGGL(k_fy_final, g, b, 0, st, draws, n, next, v, a_old, a_new);
   return hipGetLastError();
 }
 
@@ -1541,15 +1389,20 @@ __device__ __forceinline__ int32_t traverse(const TreeNodeDev *__restrict__ tree
 #pragma clang fp contract(off)
 __global__ __launch_bounds__(kUpdBlock) void k_update_F(
     const uint8_t *__restrict__ codes, int64_t ld, int64_t n,
-    const TreeNodeDev *__restrict__ tree, double lr, double *__restrict__ F,
-    const uint8_t *__restrict__ y, double *__restrict__ partials) {
+    const TreeNodeDev *__restrict__ tree, const int32_t *__restrict__ node_count_d,
+    double lr, double *__restrict__ F, const uint8_t *__restrict__ y,
+    double *__restrict__ partials) {
   __shared__ double red[kUpdBlock / 64];
+  const bool apply = !node_count_d || *node_count_d > 0;
   double acc = 0.0;
   for (int64_t i = (int64_t)blockIdx.x * kUpdBlock + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * kUpdBlock) {
-    const int32_t leaf = traverse(tree, codes, ld, i);
-    const double f = __dadd_rn(F[i], __dmul_rn(lr, tree[leaf].value));
-    F[i] = f;
+    double f = F[i];
+    if (apply) {
+      const int32_t leaf = traverse(tree, codes, ld, i);
+      f = __dadd_rn(f, __dmul_rn(lr, tree[leaf].value));
+      F[i] = f;
+    }
     const double fc = fmin(fmax(f, -500.0), 500.0);
     double p = 1.0 / (1.0 + exp(-fc));
     p = fmin(fmax(p, 1e-15), 1.0 - 1e-15);
@@ -1568,12 +1421,11 @@ __global__ __launch_bounds__(kUpdBlock) void k_update_F(
 
 hipError_t launch_update_F(hipStream_t st, const uint8_t *codes, int64_t ld,
                            int64_t n, const TreeNodeDev *tree,
-                           int32_t node_count, double lr, double *F,
+                           const int32_t *node_count_d, double lr, double *F,
                            const uint8_t *y, double *loss_partials,
                            int32_t n_blocks) {
-  (void)node_count;
   hipLaunchKernelGGL(k_update_F, dim3((unsigned)n_blocks), dim3(kUpdBlock), 0, st,
-                     codes, ld, n, tree, lr, F, y, loss_partials);
+                     codes, ld, n, tree, node_count_d, lr, F, y, loss_partials);
   return hipGetLastError();
 }
 
@@ -1594,6 +1446,441 @@ hipError_t launch_sum_partials(hipStream_t st, const double *partials,
                                int32_t count, double *out) {
   hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(256), 0, st, partials, count,
                      out);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Best-first replay (est:641-820) on the device, so a boosting round needs
+// no host round trip between the tree and the F update.  One wave; the
+// candidate slots (max_leaves + 2 of them) live in LDS.  Same steps as the
+// host replay in engine.hip: pop the active slot with the largest gain
+// above gamma (the lowest slot on ties); a node whose split was rejected
+// becomes a leaf; a kept split numbers its children left then right, puts
+// the smaller child in the first free slot and the larger in the next.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double leaf_value(const NodeOut &nd, const ReplayArgs &a) {
+  const double G = (double)nd.Gq * a.g_scale;
+  const double H = (double)nd.Hq * a.h_scale;
+  return -G / (H + a.reg_lambda);
+}
+
+constexpr int kReplayNodes = 1024;            // node records staged in LDS
+constexpr int kReplayOut = 2 * kReplaySlots + 2;  // output nodes of the largest tree
+
+// LDS of k_replay (one wave): node records (gain, leaf value, size, split,
+// first child, kept flag); candidate slots (output id, internal id, gain or
+// -inf when the candidate cannot be split, active flag); the output tree as
+// (internal node, left child or -1) per output node.
+__shared__ double rp_gain[kReplayNodes], rp_val[kReplayNodes];
+__shared__ int32_t rp_count[kReplayNodes], rp_fpos[kReplayNodes], rp_left[kReplayNodes];
+__shared__ uint8_t rp_valid[kReplayNodes], rp_bin[kReplayNodes];
+__shared__ int32_t rs_node[kReplaySlots], rs_int[kReplaySlots];
+__shared__ double rs_gain[kReplaySlots];
+__shared__ uint8_t rs_active[kReplaySlots];
+__shared__ int32_t ro_int[kReplayOut], ro_left[kReplayOut];
+
+// Node fields from the LDS records (kStaged) or from the table in HBM.
+template <bool kStaged> struct ReplayNodes {
+  const NodeOut *nodes;
+  ReplayArgs a;
+  __device__ double gain(int32_t i) const { return kStaged ? rp_gain[i] : nodes[i].gain; }
+  __device__ double val(int32_t i) const { return kStaged ? rp_val[i] : leaf_value(nodes[i], a); }
+  __device__ int64_t count(int32_t i) const { return kStaged ? (int64_t)rp_count[i] : nodes[i].count; }
+  __device__ int32_t fpos(int32_t i) const { return kStaged ? rp_fpos[i] : nodes[i].fpos; }
+  __device__ int32_t bin(int32_t i) const { return kStaged ? (int32_t)rp_bin[i] : nodes[i].bin; }
+  __device__ int32_t left(int32_t i) const { return kStaged ? rp_left[i] : nodes[i].left; }
+  __device__ int32_t valid(int32_t i) const { return kStaged ? (int32_t)rp_valid[i] : nodes[i].valid; }
+};
+
+// Largest value over the wave, returned to every lane: DPP shifts within
+// rows of 16 lanes, then row broadcasts (lane 63 ends with the maximum),
+// then a read of lane 63.  Lanes without a source keep their own value.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ double dpp_max_step(double x) {
+  const int hi = __builtin_amdgcn_update_dpp(__double2hiint(x), __double2hiint(x), kCtrl, kRowMask, 0xf, false);
+  const int lo = __builtin_amdgcn_update_dpp(__double2loint(x), __double2loint(x), kCtrl, kRowMask, 0xf, false);
+  return fmax(x, __hiloint2double(hi, lo));
+}
+
+__device__ __forceinline__ double wave_max_f64(double x) {
+  x = dpp_max_step<0x111, 0xf>(x);  // row_shr:1
+  x = dpp_max_step<0x112, 0xf>(x);  // row_shr:2
+  x = dpp_max_step<0x114, 0xf>(x);  // row_shr:4
+  x = dpp_max_step<0x118, 0xf>(x);  // row_shr:8
+  x = dpp_max_step<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+  x = dpp_max_step<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+  const int hi = __builtin_amdgcn_readlane(__double2hiint(x), 63);
+  const int lo = __builtin_amdgcn_readlane(__double2loint(x), 63);
+  return __hiloint2double(hi, lo);
+}
+
+// Puts internal node v in slot k as output node `id`.
+template <bool kStaged>
+__device__ __forceinline__ void replay_set_slot(const ReplayNodes<kStaged> &N, int32_t k,
+                                                int32_t id, int32_t v) {
+  rs_node[k] = id;
+  rs_int[k] = v;
+  rs_gain[k] = N.fpos(v) >= 0 ? N.gain(v) : -INFINITY;
+  rs_active[k] = 1;
+}
+
+// The candidate loop; returns the node count (0 with *status set on error).
+template <bool kStaged>
+__device__ int32_t replay_loop(const ReplayNodes<kStaged> &N, int32_t C, int32_t *status) {
+  const int lane = (int)threadIdx.x;
+  const ReplayArgs &a = N.a;
+  for (int32_t i = lane; i < C; i += 64) {
+    rs_active[i] = 0;
+    rs_gain[i] = -INFINITY;
+  }
+  __syncthreads();
+  int32_t node_count = 1;
+  if (lane == 0) {
+    ro_int[0] = 0;
+    ro_left[0] = -1;
+  }
+  if (N.fpos(0) < 0) return 1;  // the root is the only leaf (est:575-579, 632-637)
+  if (lane == 0) replay_set_slot(N, 0, 0, 0);
+  __syncthreads();
+  int32_t n_splits = 0;
+  while (n_splits < a.max_leaves - 1) {
+    // The largest gain above gamma, at the lowest slot holding it.
+    double lmax = -INFINITY;
+    for (int32_t i = lane; i < C; i += 64) lmax = fmax(lmax, rs_gain[i]);  // -inf: not a candidate
+    const double best = wave_max_f64(lmax);
+    if (!(best > a.gamma)) break;
+    int32_t ci = -1;
+    for (int32_t base = 0; base < C && ci < 0; base += 64) {
+      const int32_t i = base + lane;
+      const unsigned long long m = __ballot(i < C && rs_gain[i] == best);
+      if (m) ci = base + __builtin_ctzll(m);
+    }
+    const int32_t v = rs_int[ci];
+    const int32_t cur = rs_node[ci];
+    const int32_t l = N.left(v);
+    if (l < 0) {
+      *status = 2;
+      return 0;
+    }
+    if (!N.valid(l)) {  // est:678-683: the node stays a leaf
+      __syncthreads();
+      if (lane == 0) {
+        ro_int[cur] = v;
+        ro_left[cur] = -1;
+        rs_active[ci] = 0;
+        rs_gain[ci] = -INFINITY;
+      }
+      __syncthreads();
+      continue;
+    }
+    const int32_t left_id = node_count, right_id = node_count + 1;
+    node_count += 2;
+    ++n_splits;
+    const bool left_small = N.count(l) <= N.count(l + 1);
+    // The first two free slots other than ci, in slot order.
+    int32_t slot_small = -1, slot_large = -1;
+    for (int32_t base = 0; base < C && slot_large < 0; base += 64) {
+      const int32_t i = base + lane;
+      unsigned long long m = __ballot(i < C && i != ci && !rs_active[i]);
+      while (m && slot_large < 0) {
+        const int32_t k = base + __builtin_ctzll(m);
+        m &= m - 1;
+        if (slot_small < 0) slot_small = k;
+        else slot_large = k;
+      }
+    }
+    if (slot_large < 0) {
+      *status = 3;
+      return 0;
+    }
+    __syncthreads();
+    if (lane == 0) {
+      ro_int[cur] = v;
+      ro_left[cur] = left_id;
+      rs_active[ci] = 0;
+      rs_gain[ci] = -INFINITY;
+      replay_set_slot(N, slot_small, left_small ? left_id : right_id, left_small ? l : l + 1);
+      replay_set_slot(N, slot_large, left_small ? right_id : left_id, left_small ? l + 1 : l);
+    }
+    __syncthreads();
+  }
+  // Candidates left in the slots are leaves.
+  for (int32_t i = lane; i < C; i += 64)
+    if (rs_active[i]) {
+      ro_int[rs_node[i]] = rs_int[i];
+      ro_left[rs_node[i]] = -1;
+    }
+  return node_count;
+}
+
+template <bool kStaged>
+__device__ void replay_write(const ReplayNodes<kStaged> &N, const int32_t *__restrict__ feats,
+                             int32_t node_count, int32_t M, TreeArrays out,
+                             TreeNodeDev *__restrict__ tree) {
+  for (int32_t i = (int32_t)threadIdx.x; i < M; i += 64) {
+    int32_t f = -1, lc = -1, rc = -1;
+    int64_t th = 0;
+    double val = 0.0, g = 0.0;
+    if (i < node_count) {
+      const int32_t v = ro_int[i];
+      val = N.val(v);
+      if (ro_left[i] >= 0) {
+        f = feats[N.fpos(v)];
+        th = N.bin(v);
+        lc = ro_left[i];
+        rc = lc + 1;
+        g = N.gain(v);
+      }
+      TreeNodeDev d;
+      d.feature = f;
+      d.threshold = f >= 0 ? (int32_t)th : 0;
+      d.left = f >= 0 ? lc : 0;
+      d.right = f >= 0 ? rc : 0;
+      d.value = val;
+      tree[i] = d;
+    }
+    out.features[i] = f;
+    out.thresholds[i] = th;
+    out.values[i] = val;
+    out.left[i] = lc;
+    out.right[i] = rc;
+    out.gains[i] = g;
+  }
+}
+
+__global__ __launch_bounds__(64) void k_replay(
+    const NodeOut *__restrict__ nodes, const LevelPlan *__restrict__ plan,
+    const int32_t *__restrict__ feats, ReplayArgs a, TreeArrays out,
+    TreeNodeDev *__restrict__ tree, RoundHeader *__restrict__ hdr) {
+  const int lane = (int)threadIdx.x;
+  const int32_t M = a.out_len;
+  const int32_t C = a.max_leaves + 2;
+  int32_t status = 0, needed = 0;
+  const LevelPlan pl = *plan;
+  if (pl.overflow > 0) {
+    status = 1;
+    needed = pl.overflow;
+  } else if (pl.overflow < 0) {
+    status = 5;
+  } else if (C > kReplaySlots || M > kReplayOut) {
+    status = 4;
+  }
+  int32_t node_count = 0;
+  if (status == 0) {
+    const int32_t n_nodes = pl.n_nodes;
+    if (n_nodes <= min(kReplayNodes, a.stage_limit)) {
+      for (int32_t i = lane; i < n_nodes; i += 64) {
+        const NodeOut nd = nodes[i];
+        rp_gain[i] = nd.gain;
+        rp_val[i] = leaf_value(nd, a);
+        rp_count[i] = (int32_t)nd.count;
+        rp_fpos[i] = nd.fpos;
+        rp_bin[i] = (uint8_t)nd.bin;
+        rp_left[i] = nd.left;
+        rp_valid[i] = (uint8_t)nd.valid;
+      }
+      __syncthreads();
+      const ReplayNodes<true> N{nodes, a};
+      node_count = replay_loop(N, C, &status);
+      __syncthreads();
+      replay_write(N, feats, status == 0 ? node_count : 0, M, out, tree);
+    } else {
+      const ReplayNodes<false> N{nodes, a};
+      node_count = replay_loop(N, C, &status);
+      __syncthreads();
+      replay_write(N, feats, status == 0 ? node_count : 0, M, out, tree);
+    }
+  }
+  if (lane == 0) {
+    hdr->node_count = status == 0 ? node_count : 0;
+    hdr->status = status;
+    hdr->needed = needed;
+  }
+}
+
+// The same loop with the candidate slots in registers (slot k in lane
+// k % 64, register k / 64), for up to kRegSlots slots: a pop is a DPP
+// maximum, a ballot, two lane reads and one LDS read of the popped node's
+// precomputed child facts.
+constexpr int kRegSlotsPerLane = 2;
+constexpr int kRegSlots = 64 * kRegSlotsPerLane;
+
+// Per node v: first child l (or -1), bit 30 = split kept, bit 29 = left
+// child is the smaller; candidate gains of both children (-inf when they
+// cannot be split).
+__shared__ int32_t rq_child[kReplayNodes];
+__shared__ double rq_gl[kReplayNodes], rq_gr[kReplayNodes];
+
+__global__ __launch_bounds__(64) void k_replay_regs(
+    const NodeOut *__restrict__ nodes, const LevelPlan *__restrict__ plan,
+    const int32_t *__restrict__ feats, ReplayArgs a, TreeArrays out,
+    TreeNodeDev *__restrict__ tree, RoundHeader *__restrict__ hdr) {
+  const int lane = (int)threadIdx.x;
+  const int32_t M = a.out_len;
+  const int32_t C = a.max_leaves + 2;
+  int32_t status = 0, needed = 0;
+  const LevelPlan pl = *plan;
+  const int32_t n_nodes = pl.n_nodes;
+  if (pl.overflow > 0) {
+    status = 1;
+    needed = pl.overflow;
+  } else if (pl.overflow < 0) {
+    status = 5;
+  } else if (C > kRegSlots || M > kReplayOut || n_nodes > kReplayNodes) {
+    status = 4;
+  }
+  int32_t node_count = 0;
+  if (status == 0) {
+    for (int32_t i = lane; i < n_nodes; i += 64) {
+      const NodeOut nd = nodes[i];
+      rp_gain[i] = nd.gain;
+      rp_val[i] = leaf_value(nd, a);
+      rp_fpos[i] = nd.fpos;
+      rp_bin[i] = (uint8_t)nd.bin;
+    }
+    __syncthreads();
+    for (int32_t v = lane; v < n_nodes; v += 64) {
+      const int32_t l = nodes[v].left;
+      int32_t c = -1;
+      double gl = -INFINITY, gr = -INFINITY;
+      if (l >= 0) {
+        const NodeOut L = nodes[l], R = nodes[l + 1];
+        c = l | (L.valid ? (1 << 30) : 0) | (L.count <= R.count ? (1 << 29) : 0);
+        gl = rp_fpos[l] >= 0 ? rp_gain[l] : -INFINITY;
+        gr = rp_fpos[l + 1] >= 0 ? rp_gain[l + 1] : -INFINITY;
+      }
+      rq_child[v] = c;
+      rq_gl[v] = gl;
+      rq_gr[v] = gr;
+    }
+    __syncthreads();
+    double g[kRegSlotsPerLane];
+    int32_t sid[kRegSlotsPerLane], sint[kRegSlotsPerLane];
+    bool act[kRegSlotsPerLane];
+#pragma unroll
+    for (int q = 0; q < kRegSlotsPerLane; ++q) {
+      g[q] = -INFINITY;
+      sid[q] = 0;
+      sint[q] = 0;
+      act[q] = false;
+    }
+    node_count = 1;
+    if (lane == 0) {
+      ro_int[0] = 0;
+      ro_left[0] = -1;
+    }
+    if (rp_fpos[0] >= 0) {
+      if (lane == 0) {
+        g[0] = rp_gain[0];
+        act[0] = true;
+      }
+      int32_t n_splits = 0;
+      while (n_splits < a.max_leaves - 1) {
+        double lmax = g[0];
+#pragma unroll
+        for (int q = 1; q < kRegSlotsPerLane; ++q) lmax = fmax(lmax, g[q]);
+        const double best = wave_max_f64(lmax);
+        if (!(best > a.gamma)) break;
+        int32_t ci = -1;
+#pragma unroll
+        for (int q = 0; q < kRegSlotsPerLane; ++q) {
+          const unsigned long long m = __ballot(g[q] == best);
+          if (ci < 0 && m) ci = 64 * q + __builtin_ctzll(m);
+        }
+        const int cq = ci >> 6, cl = ci & 63;
+        int32_t v = 0, cur = 0;
+#pragma unroll
+        for (int q = 0; q < kRegSlotsPerLane; ++q)
+          if (q == cq) {
+            v = __builtin_amdgcn_readlane(sint[q], cl);
+            cur = __builtin_amdgcn_readlane(sid[q], cl);
+          }
+        const int32_t c = rq_child[v];
+        if (c < 0) {
+          status = 2;
+          break;
+        }
+        // The popped slot is free again.
+#pragma unroll
+        for (int q = 0; q < kRegSlotsPerLane; ++q)
+          if (q == cq && lane == cl) {
+            act[q] = false;
+            g[q] = -INFINITY;
+          }
+        if (!(c & (1 << 30))) {  // est:678-683: the node stays a leaf
+          if (lane == 0) {
+            ro_int[cur] = v;
+            ro_left[cur] = -1;
+          }
+          continue;
+        }
+        const int32_t l = c & ((1 << 29) - 1);
+        const bool left_small = (c & (1 << 29)) != 0;
+        const int32_t left_id = node_count, right_id = node_count + 1;
+        node_count += 2;
+        ++n_splits;
+        // The first two free slots other than ci, in slot order.
+        int32_t slot_small = -1, slot_large = -1;
+#pragma unroll
+        for (int q = 0; q < kRegSlotsPerLane; ++q) {
+          const int32_t k = 64 * q + lane;
+          unsigned long long m = __ballot(k < C && k != ci && !act[q]);
+          while (m && slot_large < 0) {
+            const int32_t kk = 64 * q + __builtin_ctzll(m);
+            m &= m - 1;
+            if (slot_small < 0) slot_small = kk;
+            else slot_large = kk;
+          }
+        }
+        if (slot_large < 0) {
+          status = 3;
+          break;
+        }
+        const double gl = rq_gl[v], gr = rq_gr[v];
+#pragma unroll
+        for (int q = 0; q < kRegSlotsPerLane; ++q) {
+          const int32_t k = 64 * q + lane;
+          if (k == slot_small || k == slot_large) {
+            const bool is_left = (k == slot_small) == left_small;
+            act[q] = true;
+            sid[q] = is_left ? left_id : right_id;
+            sint[q] = is_left ? l : l + 1;
+            g[q] = is_left ? gl : gr;
+          }
+        }
+        if (lane == 0) {
+          ro_int[cur] = v;
+          ro_left[cur] = left_id;
+        }
+      }
+      if (status == 0) {
+#pragma unroll
+        for (int q = 0; q < kRegSlotsPerLane; ++q)
+          if (act[q]) {
+            ro_int[sid[q]] = sint[q];
+            ro_left[sid[q]] = -1;
+          }
+      }
+    }
+    __syncthreads();
+    const ReplayNodes<true> N{nodes, a};
+    replay_write(N, feats, status == 0 ? node_count : 0, M, out, tree);
+  }
+  if (lane == 0) {
+    hdr->node_count = status == 0 ? node_count : 0;
+    hdr->status = status;
+    hdr->needed = needed;
+  }
+}
+
+hipError_t launch_replay(hipStream_t st, const NodeOut *nodes, const LevelPlan *plan,
+                         const int32_t *feats, ReplayArgs a, TreeArrays out,
+                         TreeNodeDev *tree, RoundHeader *hdr) {
+  // Register slots for up to 128 candidates when every node fits in LDS.
+  if (a.max_leaves + 2 <= kRegSlots && a.stage_limit >= kReplayNodes && a.node_cap <= kReplayNodes)
+    hipLaunchKernelGGL(k_replay_regs, dim3(1), dim3(64), 0, st, nodes, plan, feats, a, out, tree, hdr);
+  else
+    hipLaunchKernelGGL(k_replay, dim3(1), dim3(64), 0, st, nodes, plan, feats, a, out, tree, hdr);
   return hipGetLastError();
 }
 

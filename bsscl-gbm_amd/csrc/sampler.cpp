@@ -24,11 +24,11 @@
 //   * a generator thread twists and tempers whole 624-word blocks (AVX-512
 //     when the CPU has it) into a ring of word chunks;
 //   * a draw thread turns words into the bounded draws j(i) of every round.
-//     Within a run of steps with a constant mask, 16 words are classified at
-//     once: a word <= i - 15 is accepted whatever happened to the 15 words
-//     before it (each acceptance lowers i by one), a word > i is rejected
-//     whatever happened, and only a block holding a word in between is
-//     decided one word at a time;
+//     Within a run of steps with a constant mask, W = 64 (then 16) words are
+//     classified at once: a word <= i - (W-1) is accepted whatever happened
+//     to the words before it (each acceptance lowers i by one), a word > i
+//     is rejected whatever happened, and only a block holding a word in
+//     between is decided with a narrower window or one word at a time;
 //   * the swaps: in device-rows mode the draws are handed to the engine,
 //     which applies them on the GPU (bsscl_fisher_yates_apply); otherwise a
 //     swap thread applies them on the host and delivers sample_idx.
@@ -411,7 +411,38 @@ bool draw_steps_avx512(Stream &s, uint32_t hi, uint32_t *out) {
     while (i >= lo) {
       if (s.p == s.end && !s.next_chunk()) return false;
       const uint32_t *p = s.p, *e = s.end;
-      // 16 words at a time while the mask stays the same for all of them.
+      // 64 words at a time: word t's threshold is i - (words accepted
+      // before it) >= i - 63, so no word in [i - 62, i] means acceptance is
+      // exactly (word <= i).  The mask stays the same for all of them.
+      while (i - lo >= 64 && e - p >= 64) {
+        const __m512i v0 = _mm512_and_si512(_mm512_loadu_si512(p), vm);
+        const __m512i v1 = _mm512_and_si512(_mm512_loadu_si512(p + 16), vm);
+        const __m512i v2 = _mm512_and_si512(_mm512_loadu_si512(p + 32), vm);
+        const __m512i v3 = _mm512_and_si512(_mm512_loadu_si512(p + 48), vm);
+        const __m512i si = _mm512_set1_epi32((int)i);
+        const __m512i sb = _mm512_set1_epi32((int)(i - 62));
+        const __mmask16 a0 = _mm512_cmple_epu32_mask(v0, si);
+        const __mmask16 a1 = _mm512_cmple_epu32_mask(v1, si);
+        const __mmask16 a2 = _mm512_cmple_epu32_mask(v2, si);
+        const __mmask16 a3 = _mm512_cmple_epu32_mask(v3, si);
+        const __mmask16 amb = _mm512_mask_cmpge_epu32_mask(a0, v0, sb) |
+                              _mm512_mask_cmpge_epu32_mask(a1, v1, sb) |
+                              _mm512_mask_cmpge_epu32_mask(a2, v2, sb) |
+                              _mm512_mask_cmpge_epu32_mask(a3, v3, sb);
+        if (amb) break;
+        const uint32_t c0 = (uint32_t)__builtin_popcount((unsigned)a0);
+        const uint32_t c1 = (uint32_t)__builtin_popcount((unsigned)a1);
+        const uint32_t c2 = (uint32_t)__builtin_popcount((unsigned)a2);
+        const uint32_t c3 = (uint32_t)__builtin_popcount((unsigned)a3);
+        _mm512_storeu_si512(out, _mm512_maskz_compress_epi32(a0, v0));
+        _mm512_storeu_si512(out + c0, _mm512_maskz_compress_epi32(a1, v1));
+        _mm512_storeu_si512(out + c0 + c1, _mm512_maskz_compress_epi32(a2, v2));
+        _mm512_storeu_si512(out + c0 + c1 + c2, _mm512_maskz_compress_epi32(a3, v3));
+        out += c0 + c1 + c2 + c3;
+        i -= c0 + c1 + c2 + c3;
+        p += 64;
+      }
+      // 16 at a time (band [i - 14, i]).
       while (i - lo >= 16 && e - p >= 16) {
         const __m512i v = _mm512_and_si512(_mm512_loadu_si512(p), vm);
         const __mmask16 acc = _mm512_cmple_epu32_mask(v, _mm512_set1_epi32((int)i));
@@ -455,10 +486,14 @@ struct Sampler {
 
   struct Round {
     HostBuf<uint32_t> draws;     // j(i) of steps n-1 .. 1
+    uint32_t *draws_d = nullptr; // device copy (device-rows mode)
+    hipEvent_t copied = nullptr; // recorded after the copy on copy_st
     HostBuf<int32_t> rows;       // sample_idx (host mode)
     std::vector<int32_t> feats;  // ascending selected features
     int32_t index = 0;
   };
+  int32_t device = -1;                // GPU of the device copies
+  hipStream_t copy_st = nullptr;
 
   WordGen gen;
   std::deque<std::unique_ptr<Round>> drawn;  // draw thread -> swap thread
@@ -484,8 +519,51 @@ struct Sampler {
     cv.notify_all();
   }
 
+  // Device-rows mode: the round's draws go to the GPU on the sampler's own
+  // stream, so the copy overlaps the engine's work on the previous round.
+  bool copy_to_device(Round &R) {
+    if (!copy_st) {
+      if (hipSetDevice(device) != hipSuccess ||
+          hipStreamCreateWithFlags(&copy_st, hipStreamNonBlocking) != hipSuccess) {
+        fail("sampler: cannot create the copy stream");
+        return false;
+      }
+    }
+    if (!R.draws_d && hipMalloc(reinterpret_cast<void **>(&R.draws_d), (size_t)n * 4) != hipSuccess) {
+      R.draws_d = nullptr;
+      fail("sampler: hipMalloc of the draws failed");
+      return false;
+    }
+    if (!R.copied && hipEventCreateWithFlags(&R.copied, hipEventDisableTiming) != hipSuccess) {
+      R.copied = nullptr;
+      fail("sampler: hipEventCreate failed");
+      return false;
+    }
+    if (n > 1 && hipMemcpyAsync(R.draws_d, R.draws.p, (size_t)(n - 1) * 4, hipMemcpyHostToDevice,
+                                copy_st) != hipSuccess) {
+      fail("sampler: draws copy failed");
+      return false;
+    }
+    if (hipEventRecord(R.copied, copy_st) != hipSuccess) {
+      fail("sampler: hipEventRecord failed");
+      return false;
+    }
+    return true;
+  }
+
+  void free_device(Round &R) {
+    if (R.draws_d) (void)hipFree(R.draws_d);
+    if (R.copied) (void)hipEventDestroy(R.copied);
+    R.draws_d = nullptr;
+    R.copied = nullptr;
+  }
+
   void run_draws() {
     try {
+      if (device_rows && do_rows && hipSetDevice(device) != hipSuccess) {
+        fail("sampler: hipSetDevice failed");
+        return;
+      }
       Stream st;
       st.gen = &gen;
       if (!st.next_chunk()) return;
@@ -505,11 +583,9 @@ struct Sampler {
           }
         }
         if (!R) R.reset(new Round());
+        if (do_rows) R->draws.alloc((size_t)n + 16);
         const auto t0 = std::chrono::steady_clock::now();
-        if (do_rows) {
-          R->draws.alloc((size_t)n + 16);
-          if (!draw_steps(st, (uint32_t)(n - 1), R->draws.p)) return;
-        }
+        if (do_rows && !draw_steps(st, (uint32_t)(n - 1), R->draws.p)) return;
         if (do_feats && F > 1) {
           if (!draw_steps(st, (uint32_t)(F - 1), jf.data())) return;
           for (int32_t t = 0; t < F - 1; ++t) std::swap(feats[(size_t)(F - 1 - t)], feats[jf[(size_t)t]]);
@@ -518,6 +594,7 @@ struct Sampler {
         std::sort(R->feats.begin(), R->feats.end());
         R->index = r;
         const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        if (device_rows && do_rows && !copy_to_device(*R)) return;
         {
           std::lock_guard<std::mutex> lk(mu);
           draw_ms += ms;
@@ -609,6 +686,13 @@ struct Sampler {
     if (draw_thread.joinable()) draw_thread.join();
     if (swap_thread.joinable()) swap_thread.join();
     gen.finish();
+    if (copy_st) {
+      (void)hipSetDevice(device);
+      (void)hipStreamSynchronize(copy_st);
+      for (auto &r : ready) free_device(*r);
+      for (auto &r : pool) free_device(*r);
+      (void)hipStreamDestroy(copy_st);
+    }
   }
 };
 
@@ -621,6 +705,8 @@ int sampler_take(bsscl_sampler *hs, SamplerRound *out, void **token) {
     return set_error(BSSCL_EINVAL, s->error.empty() ? "sampler: all rounds consumed" : s->error);
   }
   out->draws = s->do_rows ? r->draws.p : nullptr;
+  out->draws_dev = (s->do_rows && s->device_rows) ? r->draws_d : nullptr;
+  out->draws_copied = (s->do_rows && s->device_rows) ? r->copied : nullptr;
   out->rows = (s->do_rows && !s->device_rows) ? r->rows.p : nullptr;
   out->feats = r->feats.data();
   out->round = r->index;
@@ -643,6 +729,7 @@ SamplerShape sampler_shape(bsscl_sampler *hs) {
   sh.f_sub = s->f_sub;
   sh.do_rows = s->do_rows;
   sh.device_rows = s->device_rows;
+  sh.device = s->device;
   return sh;
 }
 
@@ -691,7 +778,8 @@ int bsscl_rs_draws(uint32_t *key, int32_t *pos, uint32_t *draws_out, int64_t n) 
 int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
                          int64_t n_sub, int32_t do_rows, int32_t n_features,
                          int32_t f_sub, int32_t do_feats, int32_t n_rounds,
-                         int32_t lookahead, int32_t flags, bsscl_sampler **out) {
+                         int32_t lookahead, int32_t flags, int32_t device,
+                         bsscl_sampler **out) {
   if (!key || !out || pos < 0 || pos > 624 || n <= 0 || n > INT32_MAX ||
       n_sub <= 0 || n_sub > n || n_features <= 0 || f_sub <= 0 ||
       f_sub > n_features || n_rounds < 0 || lookahead < 1 ||
@@ -714,6 +802,14 @@ int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
   s->do_rows = do_rows != 0;
   s->do_feats = do_feats != 0;
   s->device_rows = (flags & BSSCL_SAMPLER_DEVICE_ROWS) != 0;
+  s->device = device;
+  if (s->device_rows && s->do_rows) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) {
+      delete s;
+      return bsscl::set_error(BSSCL_EINVAL, "sampler_create: device-rows mode needs a valid HIP device");
+    }
+  }
   s->n_rounds = n_rounds;
   s->lookahead = lookahead;
   std::memcpy(s->final_key, key, sizeof(s->final_key));

@@ -185,13 +185,16 @@ int bsscl_rs_draws(uint32_t *key, int32_t *pos, uint32_t *draws_out, int64_t n);
 int bsscl_fisher_yates_apply(bsscl_engine *eng, const uint32_t *draws,
                              int64_t n, int32_t *data);
 
-/* Sampler flag: the rows are permuted on the GPU by bsscl_boost_round (the
- * sampler hands it the draws); bsscl_sampler_next then refuses row bagging. */
+/* Sampler flag: the rows are permuted on GPU `device` by bsscl_boost_round
+ * (the sampler copies each round's draws there on a stream of its own, ahead
+ * of use); bsscl_sampler_next then refuses row bagging.  `device` is
+ * ignored without the flag. */
 #define BSSCL_SAMPLER_DEVICE_ROWS 1
 int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
                          int64_t n_sub, int32_t do_rows, int32_t n_features,
                          int32_t f_sub, int32_t do_feats, int32_t n_rounds,
-                         int32_t lookahead, int32_t flags, bsscl_sampler **out);
+                         int32_t lookahead, int32_t flags, int32_t device,
+                         bsscl_sampler **out);
 /* Next round: the reference's sample_idx (int32[n_sub], in its order) and
  * the ascending feature subset (int32[f_sub]); either output may be NULL. */
 int bsscl_sampler_next(bsscl_sampler *s, int32_t *rows_out,
@@ -207,8 +210,10 @@ void bsscl_sampler_destroy(bsscl_sampler *s);
 
 /*
  * Timing of the engine's own kernels, taken with HIP events on the engine's
- * stream while profiling is on.  No reference counterpart (the reference
- * records only wall times, est:1904).  bsscl_engine_stats fills up to `cap`
+ * stream while profiling is on: level 1 times the histogram kernel only,
+ * level 2 also the partition and split groups (0 turns it off).  No
+ * reference counterpart (the reference records only wall times, est:1904).
+ * bsscl_engine_stats fills up to `cap`
  * doubles in this order:
  *   [0] histogram launches   [1] histogram ms (sum of launch durations)
  *   [2] histogram rows x features  [3] histogram algorithmic bytes

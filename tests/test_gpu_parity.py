@@ -269,3 +269,34 @@ def test_fit_lockstep_and_end_to_end(engine, name):
           f"{'identical' if diverged is None else f'tie at tree {diverged}'}", flush=True)
     if diverged is None:
         np.testing.assert_allclose(est.predict_proba(X), ref.predict_proba(X), rtol=0, atol=1e-6)
+
+
+def test_fit_device_replay_fallbacks_agree(engine, monkeypatch):
+    """The round's device replay, the host replay (forced), and the path that
+    regrows a too-small node table give identical trees and losses."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    X, y, params = _fit_case("nan_imbalanced")
+    params = dict(params, n_estimators=6)
+    fits = {}
+    hooks = ("BSSCL_TEST_HOST_REPLAY", "BSSCL_TEST_NODE_CAP", "BSSCL_TEST_REPLAY_GLOBAL")
+    for mode, env in [("device", {}), ("host", {"BSSCL_TEST_HOST_REPLAY": "1"}),
+                      ("global", {"BSSCL_TEST_REPLAY_GLOBAL": "1"}),
+                      ("lds", {"BSSCL_TEST_REPLAY_GLOBAL": "2"}),
+                      ("regrow", {"BSSCL_TEST_NODE_CAP": "9"})]:
+        _announce(f"fit replay path {mode}")
+        for k in hooks:
+            monkeypatch.delenv(k, raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        fits[mode] = HybridHistGBMNumbaV1_0_1(verbose=False, **params).fit(X, y)
+    for k in hooks:
+        monkeypatch.delenv(k, raising=False)
+    ref = fits["device"]
+    for mode in ("host", "global", "lds", "regrow"):
+        got = fits[mode]
+        assert got.train_loss_history_ == ref.train_loss_history_, mode
+        for a, b in zip(ref.trees, got.trees):
+            nc = a[5]
+            assert nc == b[5], mode
+            for k in (0, 1, 2, 3, 4, 6):
+                np.testing.assert_array_equal(a[k][:nc], b[k][:nc], err_msg=mode)
