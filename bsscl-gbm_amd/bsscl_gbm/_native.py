@@ -50,6 +50,7 @@ _SIGS = {
     "bsscl_sampler_stats": [_P, _P, _i32, _P],
     "bsscl_sampler_destroy": [_P],
     "bsscl_engine_set_profiling": [_P, _i32],
+    "bsscl_boost_set_pipeline": [_P, _i32],
     "bsscl_engine_stats": [_P, _P, _i32, _P],
 }
 _VOID = {"bsscl_engine_destroy", "bsscl_sampler_destroy"}
@@ -284,6 +285,10 @@ class Engine:
         return a
 
     # -- profiling ------------------------------------------------------------
+    def set_pipeline(self, on):
+        """Enqueue each boosting round's successor before returning it."""
+        check(lib().bsscl_boost_set_pipeline(self.handle, int(bool(on))))
+
     def set_profiling(self, level):
         """0 off; 1 times the histogram kernel; 2 every kernel group."""
         check(lib().bsscl_engine_set_profiling(self.handle, int(level)))

@@ -452,6 +452,9 @@ class HybridHistGBMNumbaV1_0_1:
         rounds_no_improve = 0
         hook = getattr(self, '_round_hook', None)
         self._live_sampler = sampler  # read by profiling hooks during the fit
+        # Without an eval set every round runs: the engine may enqueue the
+        # next round while this one is returned.
+        eng.set_pipeline(not n_val and getattr(self, '_pipeline_rounds', True))
         try:
             for m in range(self.n_estimators):
                 if hook is not None:
@@ -487,6 +490,7 @@ class HybridHistGBMNumbaV1_0_1:
                             self.trees = self.trees[:self.best_iteration_ + 1]
                             break
         finally:
+            eng.set_pipeline(False)
             self._live_sampler = None
             sampler.close()
         if hook is not None:

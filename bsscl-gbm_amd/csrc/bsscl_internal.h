@@ -34,5 +34,7 @@ struct SamplerShape {
 int sampler_take(bsscl_sampler *s, SamplerRound *out, void **token);
 void sampler_give_back(bsscl_sampler *s, void *token);
 SamplerShape sampler_shape(bsscl_sampler *s);
+// Rounds not yet taken.
+int32_t sampler_remaining(bsscl_sampler *s);
 
 }  // namespace bsscl

@@ -157,6 +157,34 @@ struct TreeOut {
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
+// Arguments of bsscl_boost_round that a speculatively enqueued round reuses.
+struct RoundArgs {
+  int32_t max_leaves = 0, max_depth = 0, min_samples_leaf = 0;
+  double min_child_weight = 0.0, reg_lambda = 0.0, gamma = 0.0, learning_rate = 0.0;
+  const int32_t *bin_counts = nullptr;
+  bool operator==(const RoundArgs &o) const {
+    return max_leaves == o.max_leaves && max_depth == o.max_depth &&
+           min_samples_leaf == o.min_samples_leaf && min_child_weight == o.min_child_weight &&
+           reg_lambda == o.reg_lambda && gamma == o.gamma && learning_rate == o.learning_rate &&
+           bin_counts == o.bin_counts;
+  }
+};
+
+// A boosting round enqueued on the stream and not yet read back.  Its
+// readback goes to buffer `buf` (two rounds can be in flight).
+struct RoundSlot {
+  bool active = false;
+  bool device_replay = true;
+  bsscl_sampler *sampler = nullptr;
+  void *token = nullptr;
+  RoundArgs args;
+  int32_t M = 0, run = 0, buf = 0;
+  int64_t m = 0;
+  std::vector<int32_t> feats, nb_sel;
+  hipEvent_t done = nullptr;  // after the round's readback copies
+  uint64_t seq = 0;           // tags the round's profiling events
+};
+
 }  // namespace
 }  // namespace bsscl
 
@@ -226,9 +254,16 @@ struct bsscl_engine {
   const int32_t *hot_sel_d = nullptr; // most frequent bin of each selected feature
   std::vector<int32_t> hot_bin;       // most frequent code per feature of matrix 0
   DevBuf<TreeNodeDev> tree_d;
-  DevBuf<char> round_d;               // RoundHeader + tree arrays of a round
-  char *round_pin = nullptr;          // pinned readback of round_d
-  size_t round_pin_bytes = 0;
+  DevBuf<char> round_d[2];            // RoundHeader + tree arrays of a round
+  char *round_pin[2] = {nullptr, nullptr};   // pinned readbacks of round_d
+  size_t round_pin_bytes[2] = {0, 0};
+  char *rtable_pin[2] = {nullptr, nullptr};  // node-table readbacks (profiling)
+  size_t rtable_pin_bytes[2] = {0, 0};
+  RoundSlot rslot[2];
+  int32_t rslot_next = 0;
+  bool pipeline = false;   // enqueue the next round before returning one
+  int32_t ahead = -1;      // slot of a round enqueued ahead, or -1
+  uint64_t round_seq = 0;
   DevBuf<int32_t> offsets_d;
   DevBuf<double> partials_d, loss_d, out_d;
   PinnedArena pin;
@@ -241,11 +276,12 @@ struct bsscl_engine {
 
   // Profiling.
   int prof = 0;  // 0 off, 1 histogram kernel timed, 2 every kernel group timed
-  std::vector<hipEvent_t> ev_pool;
-  size_t ev_used = 0;
+  std::vector<hipEvent_t> ev_pool;  // every timing event (destroyed with the engine)
+  std::vector<hipEvent_t> ev_free;
   struct Pending {
     hipEvent_t a, b;
-    int kind;  // 0 hist, 1 partition, 2 split
+    int kind;      // 0 hist, 1 partition, 2 split
+    uint64_t seq;  // boosting round that recorded them
   };
   std::vector<Pending> pending;
   double stats[12] = {0};
@@ -254,14 +290,18 @@ struct bsscl_engine {
 namespace bsscl {
 namespace {
 
+// Two timing events from the free list (created when it is empty).
 int ev_pair(bsscl_engine *E, hipEvent_t &a, hipEvent_t &b) {
-  while (E->ev_pool.size() < E->ev_used + 2) {
+  while (E->ev_free.size() < 2) {
     hipEvent_t ev;
     HIPCHK(hipEventCreate(&ev));
     E->ev_pool.push_back(ev);
+    E->ev_free.push_back(ev);
   }
-  a = E->ev_pool[E->ev_used++];
-  b = E->ev_pool[E->ev_used++];
+  a = E->ev_free.back();
+  E->ev_free.pop_back();
+  b = E->ev_free.back();
+  E->ev_free.pop_back();
   return BSSCL_OK;
 }
 
@@ -274,7 +314,7 @@ int prof_begin(bsscl_engine *E, int kind, hipEvent_t *stop) {
   hipEvent_t a, b;
   CHK(ev_pair(E, a, b));
   HIPCHK(hipEventRecord(a, E->st));
-  E->pending.push_back({a, b, kind});
+  E->pending.push_back({a, b, kind, E->round_seq});
   *stop = b;
   return BSSCL_OK;
 }
@@ -284,16 +324,23 @@ int prof_end(bsscl_engine *E, hipEvent_t stop) {
   return BSSCL_OK;
 }
 
-// After a stream synchronisation: fold the finished timings into stats.
-int prof_collect(bsscl_engine *E) {
+// Folds finished timings into stats: every pending pair after a stream
+// synchronisation, or those of rounds up to `upto` once they are done.
+int prof_collect(bsscl_engine *E, uint64_t upto = UINT64_MAX) {
+  std::vector<bsscl_engine::Pending> keep;
   for (const auto &p : E->pending) {
+    if (p.seq > upto) {
+      keep.push_back(p);
+      continue;
+    }
     float ms = 0.f;
     HIPCHK(hipEventElapsedTime(&ms, p.a, p.b));
     E->stats[p.kind == 0 ? 0 : (p.kind == 1 ? 4 : 6)] += 1.0;
     E->stats[p.kind == 0 ? 1 : (p.kind == 1 ? 5 : 7)] += (double)ms;
+    E->ev_free.push_back(p.a);
+    E->ev_free.push_back(p.b);
   }
-  E->pending.clear();
-  E->ev_used = 0;
+  E->pending.swap(keep);
   return BSSCL_OK;
 }
 
@@ -825,17 +872,26 @@ TreeArrays round_arrays(char *base, int32_t M) {
   return t;
 }
 
-int ensure_round_out(bsscl_engine *E, int32_t M) {
+int ensure_host_pinned(bsscl_engine *E, char *&p, size_t &have, size_t bytes) {
+  if (have >= bytes) return BSSCL_OK;
+  CHK(sync(E));
+  if (p) (void)hipHostFree(p);
+  p = nullptr;
+  have = 0;
+  HIPCHK(hipHostMalloc(reinterpret_cast<void **>(&p), bytes, hipHostMallocDefault));
+  have = bytes;
+  return BSSCL_OK;
+}
+
+// Readback buffers of round buffer b: the round's header and tree, and the
+// node table (for profiling counters).
+int ensure_round_out(bsscl_engine *E, int b, int32_t M) {
   const size_t bytes = round_out_bytes(M);
-  CHK(E->round_d.ensure(bytes));
-  if (E->round_pin_bytes < bytes) {
-    CHK(sync(E));
-    if (E->round_pin) (void)hipHostFree(E->round_pin);
-    E->round_pin = nullptr;
-    E->round_pin_bytes = 0;
-    HIPCHK(hipHostMalloc(reinterpret_cast<void **>(&E->round_pin), bytes, hipHostMallocDefault));
-    E->round_pin_bytes = bytes;
-  }
+  if (E->round_d[b].cap < bytes) CHK(sync(E));
+  CHK(E->round_d[b].ensure(bytes));
+  CHK(ensure_host_pinned(E, E->round_pin[b], E->round_pin_bytes[b], bytes));
+  CHK(ensure_host_pinned(E, E->rtable_pin[b], E->rtable_pin_bytes[b],
+                         64 + (size_t)E->node_alloc * sizeof(NodeOut)));
   return BSSCL_OK;
 }
 
@@ -854,9 +910,11 @@ constexpr int32_t kLevelsPerCheck = 8;  // levels enqueued between host checks
 // prepare_tree_buffers).  All levels are enqueued without host round trips:
 // the planner kernel chooses each level's parents on the device; every
 // kLevelsPerCheck levels the host reads the plan and stops enqueueing once
-// the tree has ended.  *run = levels enqueued.
+// the tree has ended (unless `checks` is false: then every level is
+// enqueued).  *run = levels enqueued.
 int launch_tree(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_t> &feats,
-                const std::vector<int32_t> &nb_sel, const TreeParams &tp, int32_t *run) {
+                const std::vector<int32_t> &nb_sel, const TreeParams &tp, int32_t *run,
+                bool checks = true) {
   const int32_t F_sel = (int32_t)feats.size();
   const int32_t levels = std::max(1, tp.max_depth);
   CHK(launch_root(E, use32, m, feats, nb_sel, tp));
@@ -864,7 +922,7 @@ int launch_tree(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_
   for (int32_t d = 0; d < levels; ++d) {
     const bool last = d + 1 >= tp.max_depth;
     CHK(launch_level_plan(E, d, last, tp, F_sel));
-    if (d > 0 && d % kLevelsPerCheck == 0) {
+    if (checks && d > 0 && d % kLevelsPerCheck == 0) {
       LevelPlan plan;
       CHK(read_table(E, 0, plan));
       if (plan.n_parents == 0 || plan.overflow != 0) break;
@@ -1064,6 +1122,275 @@ int upload_tree(bsscl_engine *E, const int32_t *features,
 }  // namespace
 }  // namespace bsscl
 
+namespace bsscl {
+namespace {
+
+// Speculative rounds need a device path that cannot fall back: the node
+// table holds the full tree (max_depth <= 9) and the replay's slots hold
+// every candidate.
+bool pipeline_safe(bsscl_engine *E, const RoundArgs &a, bsscl_sampler *sampler) {
+  (void)E;
+  (void)sampler;
+  if (a.max_depth > 9 || a.max_leaves + 2 > kReplaySlots) return false;
+  for (const char *k : {"BSSCL_TEST_HOST_REPLAY", "BSSCL_TEST_NODE_CAP", "BSSCL_TEST_REPLAY_GLOBAL"})
+    if (std::getenv(k)) return false;
+  return true;
+}
+
+// Waits for the round in slot s and returns its sampler buffers; its
+// results are dropped.
+int drain_rounds(bsscl_engine *E, int s) {
+  RoundSlot &r = E->rslot[s];
+  if (!r.active) return BSSCL_OK;
+  const hipError_t e = hipStreamSynchronize(E->st);
+  sampler_give_back(r.sampler, r.token);
+  r.active = false;
+  r.token = nullptr;
+  (void)prof_collect(E);
+  if (e != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("boost_round: ") + hipGetErrorString(e));
+  return BSSCL_OK;
+}
+
+// Enqueues one boosting round: gradients from the current F (est:2868),
+// the sampler's round (est:2886, est:2502-2517), the tree, its replay
+// (est:641-820), F += lr * tree(X) and the training log-loss, and the
+// readback of the tree and the loss into round buffer s.  A tree that needs
+// the host-driven path (a larger node table, more candidate slots than the
+// device replay holds) is finished by finish_round.
+int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, int s) {
+  const Matrix &X = E->mat[0];
+  RoundSlot &R = E->rslot[s];
+  const SamplerShape sh = sampler_shape(sampler);
+  const int64_t m = sh.n_sub;
+  if (sh.n != X.n) return set_error(BSSCL_EINVAL, "boost_round: sampler rows differ from matrix rows");
+  ++E->round_seq;
+  // Gradients from the current F: |g| <= max(w0, w1), h <= max(w0, w1)/4.
+  const double wmax = std::max(E->w0, E->w1);
+  const double gm = fixed_mul(wmax), hm = fixed_mul(0.25 * wmax);
+  E->g_scale = 1.0 / gm;
+  E->h_scale = 1.0 / hm;
+  HIPCHK(launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, gm, hm, E->ghq.p));
+  SamplerRound sr;
+  void *token = nullptr;
+  const auto t_wait0 = std::chrono::steady_clock::now();
+  CHK(sampler_take(sampler, &sr, &token));
+  if (E->prof)
+    E->stats[10] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_wait0).count();
+  R.active = true;
+  R.sampler = sampler;
+  R.token = token;
+  R.args = a;
+  R.m = m;
+  R.buf = s;
+  R.seq = E->round_seq;
+  R.M = 2 * a.max_leaves + 2;
+  R.run = 0;
+  auto fail = [&](int rc) {
+    (void)hipStreamSynchronize(E->st);
+    sampler_give_back(sampler, token);
+    R.active = false;
+    R.token = nullptr;
+    return rc;
+  };
+  TreeOut none{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  (void)none;
+  int rc = BSSCL_OK;
+  {
+    // Feature subset and bin counts (validate_tree_args without outputs).
+    const int32_t f_sub = sh.f_sub;
+    if (a.max_leaves < 1) rc = set_error(BSSCL_EINVAL, "max_leaves must be >= 1");
+    if (rc == BSSCL_OK && !a.bin_counts) rc = set_error(BSSCL_EINVAL, "bin_counts missing");
+    R.feats.assign(sr.feats, sr.feats + f_sub);
+    R.nb_sel.resize((size_t)f_sub);
+    for (int32_t i = 0; rc == BSSCL_OK && i < f_sub; ++i) {
+      const int32_t f = R.feats[(size_t)i];
+      if (f < 0 || f >= X.F) rc = set_error(BSSCL_EINVAL, "feature index out of range");
+      else if (a.bin_counts[f] < 1 || a.bin_counts[f] > kBins)
+        rc = set_error(BSSCL_EINVAL, "bin_counts must be in [1, 256]");
+      else R.nb_sel[(size_t)i] = a.bin_counts[f];
+    }
+  }
+  // The round's in-bag rows on the device, ascending: the reference's
+  // sample_idx (a prefix of the cumulative permutation) sorted.
+  const int64_t n_pad = sort_rows_flag_bytes(X.n);
+  if (rc == BSSCL_OK) rc = E->rows32.ensure((size_t)m);
+  if (rc == BSSCL_OK) rc = E->sort_tmp.ensure((size_t)(n_pad / 4096 + 1));
+  if (rc == BSSCL_OK && E->row_flags_n != n_pad) {
+    rc = E->row_flags.ensure((size_t)n_pad);
+    if (rc == BSSCL_OK) {
+      hipError_t e = hipMemsetAsync(E->row_flags.p, 0, (size_t)n_pad, E->st);
+      if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("flags: ") + hipGetErrorString(e));
+      else E->row_flags_n = n_pad;
+    }
+  }
+  if (rc == BSSCL_OK) {
+    hipError_t e = hipSuccess;
+    const int32_t *rows_d = nullptr;
+    if (!sh.do_rows) {
+      e = launch_iota(E->st, E->rows32.p, m);  // every row, in order
+    } else if (sh.device_rows) {
+      if (sh.device != E->device)
+        rc = set_error(BSSCL_EINVAL, "boost_round: the sampler copies its draws to another GPU");
+      // Cumulative permutation: identity before the sampler's first round.
+      if (rc != BSSCL_OK) {
+      } else if (sr.round == 0) {
+        rc = E->perm[0].ensure((size_t)X.n);
+        if (rc == BSSCL_OK) rc = E->perm[1].ensure((size_t)X.n);
+        if (rc == BSSCL_OK) {
+          E->perm_cur = 0;
+          E->perm_sampler = sampler;
+          E->perm_next_round = 0;
+          e = launch_iota(E->st, E->perm[0].p, X.n);
+        }
+      } else if (E->perm_sampler != sampler || E->perm_next_round != sr.round) {
+        rc = set_error(BSSCL_EINVAL, "boost_round: the sampler's earlier rounds did not run on this engine");
+      }
+      FyWork w;
+      if (rc == BSSCL_OK) rc = ensure_fy_work(E, X.n, w);
+      // The sampler copied the draws on its own stream.
+      if (rc == BSSCL_OK && e == hipSuccess) e = hipStreamWaitEvent(E->st, sr.draws_copied, 0);
+      if (rc == BSSCL_OK && e == hipSuccess) {
+        const int nxt = E->perm_cur ^ 1;
+        e = launch_fisher_yates(E->st, sr.draws_dev, X.n, E->perm[E->perm_cur].p,
+                                E->perm[nxt].p, w);
+        E->perm_cur = nxt;
+        E->perm_next_round = sr.round + 1;
+        rows_d = E->perm[nxt].p;
+      }
+    } else {
+      rc = E->rows_in.ensure((size_t)m);
+      if (rc == BSSCL_OK) e = hipMemcpyAsync(E->rows_in.p, sr.rows, (size_t)m * 4, hipMemcpyHostToDevice, E->st);
+      rows_d = E->rows_in.p;
+    }
+    if (rc == BSSCL_OK && e == hipSuccess && rows_d)
+      e = launch_sort_rows(E->st, rows_d, m, E->row_flags.p, n_pad, E->sort_tmp.p, E->rows32.p);
+    if (rc == BSSCL_OK && e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("rows: ") + hipGetErrorString(e));
+  }
+  if (rc != BSSCL_OK) return fail(rc);
+  const TreeParams tp{a.max_leaves, a.max_depth, a.min_samples_leaf, a.min_child_weight,
+                      a.reg_lambda, a.gamma};
+  const int32_t F_sel = (int32_t)R.feats.size();
+  const int nb = update_F_blocks(X.n);
+  // More candidate slots than the device replay holds: host replay only.
+  // (Test hook: BSSCL_TEST_HOST_REPLAY=1 forces the host path.)
+  const char *force_host = std::getenv("BSSCL_TEST_HOST_REPLAY");
+  R.device_replay = a.max_leaves + 2 <= kReplaySlots && !(force_host && force_host[0] == '1');
+  if (rc == BSSCL_OK) rc = E->partials_d.ensure((size_t)nb);
+  if (rc == BSSCL_OK) rc = E->tree_d.ensure((size_t)R.M);
+  if (rc == BSSCL_OK && R.device_replay)
+    rc = prepare_tree_buffers(E, m, F_sel, std::max(1, a.max_depth), a.max_leaves);
+  if (rc == BSSCL_OK) rc = ensure_round_out(E, s, R.M);
+  if (rc == BSSCL_OK && R.device_replay)
+    rc = launch_tree(E, true, m, R.feats, R.nb_sel, tp, &R.run, !E->pipeline);
+  if (rc == BSSCL_OK && R.device_replay) {
+    RoundHeader *hdr = reinterpret_cast<RoundHeader *>(E->round_d[s].p);
+    ReplayArgs ra;
+    ra.gamma = a.gamma;
+    ra.reg_lambda = a.reg_lambda;
+    ra.g_scale = E->g_scale;
+    ra.h_scale = E->h_scale;
+    ra.max_leaves = a.max_leaves;
+    ra.out_len = R.M;
+    // (Test hook BSSCL_TEST_REPLAY_GLOBAL: 1 reads the node table from HBM,
+    // 2 keeps the candidate slots in LDS instead of registers.)
+    const char *rg = std::getenv("BSSCL_TEST_REPLAY_GLOBAL");
+    ra.stage_limit = !rg ? (1 << 30) : rg[0] == '1' ? 0 : rg[0] == '2' ? 1023 : (1 << 30);
+    ra.node_cap = E->node_cap;
+    hipError_t e = launch_replay(E->st, E->nodes_d, E->plan_d, E->feat_d, ra,
+                                 round_arrays(E->round_d[s].p, R.M), E->tree_d.p, hdr);
+    if (e == hipSuccess)
+      e = launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, &hdr->node_count,
+                          a.learning_rate, E->F.p, E->y.p, E->partials_d.p, nb);
+    if (e == hipSuccess) e = launch_sum_partials(E->st, E->partials_d.p, nb, &hdr->loss_sum);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(E->round_pin[s], E->round_d[s].p, round_out_bytes(R.M),
+                         hipMemcpyDeviceToHost, E->st);
+    if (e == hipSuccess && E->prof)
+      e = hipMemcpyAsync(E->rtable_pin[s], E->table_d.p,
+                         64 + (size_t)table_bound(E, R.run) * sizeof(NodeOut),
+                         hipMemcpyDeviceToHost, E->st);
+    if (e == hipSuccess && !R.done) e = hipEventCreateWithFlags(&R.done, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(R.done, E->st);
+    if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("round: ") + hipGetErrorString(e));
+  }
+  if (rc != BSSCL_OK) return fail(rc);
+  return BSSCL_OK;
+}
+
+// Waits for the round in slot s, returns its sampler buffers and hands its
+// tree and loss to the caller (finishing it on the host-driven path when
+// the device path could not).
+int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
+  const Matrix &X = E->mat[0];
+  RoundSlot &R = E->rslot[s];
+  if (!R.active) return set_error(BSSCL_EINTERNAL, "boost_round: no round in flight");
+  const TreeParams tp{R.args.max_leaves, R.args.max_depth, R.args.min_samples_leaf,
+                      R.args.min_child_weight, R.args.reg_lambda, R.args.gamma};
+  hipError_t e = hipSuccess;
+  if (R.device_replay) {
+    e = hipEventSynchronize(R.done);
+  } else {
+    e = hipStreamSynchronize(E->st);  // the sampler's buffers must be read first
+  }
+  if (e == hipSuccess && E->prof) {
+    const int rc = prof_collect(E, R.seq);
+    if (rc != BSSCL_OK) e = hipErrorUnknown;
+  }
+  sampler_give_back(R.sampler, R.token);
+  R.active = false;
+  R.token = nullptr;
+  if (e != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("boost_round: ") + hipGetErrorString(e));
+  const int32_t M = R.M;
+  RoundHeader h;
+  if (R.device_replay) {
+    h = *reinterpret_cast<const RoundHeader *>(E->round_pin[s]);
+  } else {
+    h = RoundHeader{};
+    h.status = 4;
+  }
+  if (h.status == 0) {
+    if (E->prof) {
+      const LevelPlan *pl = reinterpret_cast<const LevelPlan *>(E->rtable_pin[s]);
+      const int32_t tb = table_bound(E, R.run);
+      if (pl->overflow == 0 && pl->n_nodes >= 1 && pl->n_nodes <= tb)
+        tree_stats(E, reinterpret_cast<const NodeOut *>(E->rtable_pin[s] + 64), pl->n_nodes, R.m,
+                   (int32_t)R.feats.size(), tp);
+    }
+    const TreeArrays ha = round_arrays(E->round_pin[s], M);
+    std::memcpy(out.features, ha.features, (size_t)M * 4);
+    std::memcpy(out.thresholds, ha.thresholds, (size_t)M * 8);
+    std::memcpy(out.values, ha.values, (size_t)M * 8);
+    std::memcpy(out.left, ha.left, (size_t)M * 4);
+    std::memcpy(out.right, ha.right, (size_t)M * 4);
+    std::memcpy(out.gains, ha.gains, (size_t)M * 8);
+    *out.node_count = h.node_count;
+    if (out_train_loss) *out_train_loss = -h.loss_sum / (double)X.n;
+    return BSSCL_OK;
+  }
+  if (h.status != 1 && h.status != 4)
+    return set_error(BSSCL_EINTERNAL, "tree builder: device replay failed (status " +
+                                          std::to_string(h.status) + ")");
+  // F was left alone: build the tree on the host-driven path and apply it.
+  // (Never with a round enqueued behind this one: see pipeline_safe.)
+  if (h.status == 1) E->node_cap_floor = std::max(h.needed, 2 * E->node_cap);
+  CHK(build_tree_core(E, true, R.m, R.feats, R.nb_sel, tp, out));
+  CHK(upload_tree(E, out.features, out.thresholds, out.values, out.left, out.right,
+                  *out.node_count, X.F));
+  const int nb = update_F_blocks(X.n);
+  CHK(E->loss_d.ensure(1));
+  HIPCHK(launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, nullptr,
+                         R.args.learning_rate, E->F.p, E->y.p, E->partials_d.p, nb));
+  HIPCHK(launch_sum_partials(E->st, E->partials_d.p, nb, E->loss_d.p));
+  double sum = 0.0;
+  HIPCHK(hipMemcpyAsync(&sum, E->loss_d.p, 8, hipMemcpyDeviceToHost, E->st));
+  CHK(sync(E));
+  if (out_train_loss) *out_train_loss = -sum / (double)X.n;
+  return BSSCL_OK;
+}
+
+}  // namespace
+}  // namespace bsscl
+
 // ===========================================================================
 // C ABI
 // ===========================================================================
@@ -1110,6 +1437,11 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   if (!E) return;
   (void)hipSetDevice(E->device);
   if (E->st) (void)hipStreamSynchronize(E->st);
+  // A round enqueued ahead hands its sampler buffers back (the sampler
+  // outlives the rounds it feeds).
+  if (E->ahead >= 0 && E->rslot[E->ahead].active)
+    sampler_give_back(E->rslot[E->ahead].sampler, E->rslot[E->ahead].token);
+  E->ahead = -1;
   for (auto &m : E->mat) m.codes.release();
   E->F.release();
   E->y.release();
@@ -1151,8 +1483,12 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->tile_off_d.release();
   E->hist_tasks_d.release();
   E->tree_d.release();
-  E->round_d.release();
-  if (E->round_pin) (void)hipHostFree(E->round_pin);
+  for (int b = 0; b < 2; ++b) {
+    E->round_d[b].release();
+    if (E->round_pin[b]) (void)hipHostFree(E->round_pin[b]);
+    if (E->rtable_pin[b]) (void)hipHostFree(E->rtable_pin[b]);
+    if (E->rslot[b].done) (void)hipEventDestroy(E->rslot[b].done);
+  }
   E->offsets_d.release();
   E->partials_d.release();
   E->loss_d.release();
@@ -1292,6 +1628,11 @@ int bsscl_build_tree(bsscl_engine *E, const double *grad, const double *hess,
 int bsscl_boost_begin(bsscl_engine *E, const int64_t *y, int64_t n, double w0,
                       double w1, double base_score) {
   if (!E || !y) return set_error(BSSCL_EINVAL, "boost_begin: null argument");
+  if (E->ahead >= 0) {
+    const int p = E->ahead;
+    E->ahead = -1;
+    CHK(drain_rounds(E, p));
+  }
   CHK(check_matrix(E, 0));
   if (n != E->mat[0].n) return set_error(BSSCL_EINVAL, "boost_begin: y length differs from matrix rows");
   if (!(w0 > 0.0) || !(w1 > 0.0) || !std::isfinite(w0) || !std::isfinite(w1))
@@ -1327,182 +1668,69 @@ int bsscl_boost_round(bsscl_engine *E, bsscl_sampler *sampler,
   if (!E || !sampler) return set_error(BSSCL_EINVAL, "boost_round: null argument");
   if (!E->boosting) return set_error(BSSCL_EINVAL, "boost_round: call boost_begin first");
   (void)max_bins;
-  const Matrix &X = E->mat[0];
   HIPCHK(hipSetDevice(E->device));
-  const SamplerShape sh = sampler_shape(sampler);
-  const int64_t m = sh.n_sub;
-  if (sh.n != X.n) return set_error(BSSCL_EINVAL, "boost_round: sampler rows differ from matrix rows");
-  // Gradients from the current F: |g| <= max(w0, w1), h <= max(w0, w1)/4.
-  const double wmax = std::max(E->w0, E->w1);
-  const double gm = fixed_mul(wmax), hm = fixed_mul(0.25 * wmax);
-  E->g_scale = 1.0 / gm;
-  E->h_scale = 1.0 / hm;
-  HIPCHK(launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, gm, hm, E->ghq.p));
-  SamplerRound sr;
-  void *token = nullptr;
-  const auto t_wait0 = std::chrono::steady_clock::now();
-  CHK(sampler_take(sampler, &sr, &token));
-  if (E->prof)
-    E->stats[10] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_wait0).count();
+  const auto t0 = std::chrono::steady_clock::now();
+  RoundArgs a;
+  a.max_leaves = max_leaves;
+  a.max_depth = max_depth;
+  a.min_samples_leaf = min_samples_leaf;
+  a.min_child_weight = min_child_weight;
+  a.reg_lambda = reg_lambda;
+  a.gamma = gamma;
+  a.learning_rate = learning_rate;
+  a.bin_counts = bin_counts;
   TreeOut out{out_features, out_thresholds, out_values, out_left, out_right,
               out_node_count, out_split_gains};
-  std::vector<int32_t> feats, nb_sel;
-  int rc = validate_tree_args(E, sr.feats, sh.f_sub, max_leaves, min_samples_leaf,
-                              bin_counts, out, feats, nb_sel);
-  // The round's in-bag rows on the device, ascending: the reference's
-  // sample_idx (a prefix of the cumulative permutation) sorted.
-  const int64_t n_pad = sort_rows_flag_bytes(X.n);
-  if (rc == BSSCL_OK) rc = E->rows32.ensure((size_t)m);
-  if (rc == BSSCL_OK) rc = E->sort_tmp.ensure((size_t)(n_pad / 4096 + 1));
-  if (rc == BSSCL_OK && E->row_flags_n != n_pad) {
-    rc = E->row_flags.ensure((size_t)n_pad);
-    if (rc == BSSCL_OK) {
-      hipError_t e = hipMemsetAsync(E->row_flags.p, 0, (size_t)n_pad, E->st);
-      if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("flags: ") + hipGetErrorString(e));
-      else E->row_flags_n = n_pad;
+  if (!out.features || !out.thresholds || !out.values || !out.left || !out.right ||
+      !out.node_count || !out.gains)
+    return set_error(BSSCL_EINVAL, "boost_round: output arrays missing");
+  int cur = E->ahead;
+  E->ahead = -1;
+  if (cur >= 0) {
+    const RoundSlot &p = E->rslot[cur];
+    if (p.sampler != sampler || !(p.args == a)) {
+      (void)drain_rounds(E, cur);
+      return set_error(BSSCL_EINVAL,
+                       "boost_round: arguments differ from the round enqueued ahead "
+                       "(turn pipelining off to change them between rounds)");
     }
+  } else {
+    cur = E->rslot_next;
+    E->rslot_next ^= 1;
+    CHK(enqueue_round(E, sampler, a, cur));
   }
-  if (rc == BSSCL_OK) {
-    hipError_t e = hipSuccess;
-    const int32_t *rows_d = nullptr;
-    if (!sh.do_rows) {
-      e = launch_iota(E->st, E->rows32.p, m);  // every row, in order
-    } else if (sh.device_rows) {
-      if (sh.device != E->device)
-        rc = set_error(BSSCL_EINVAL, "boost_round: the sampler copies its draws to another GPU");
-      // Cumulative permutation: identity before the sampler's first round.
-      if (rc != BSSCL_OK) {
-      } else if (sr.round == 0) {
-        rc = E->perm[0].ensure((size_t)X.n);
-        if (rc == BSSCL_OK) rc = E->perm[1].ensure((size_t)X.n);
-        if (rc == BSSCL_OK) {
-          E->perm_cur = 0;
-          E->perm_sampler = sampler;
-          E->perm_next_round = 0;
-          e = launch_iota(E->st, E->perm[0].p, X.n);
-        }
-      } else if (E->perm_sampler != sampler || E->perm_next_round != sr.round) {
-        rc = set_error(BSSCL_EINVAL, "boost_round: the sampler's earlier rounds did not run on this engine");
-      }
-      FyWork w;
-      if (rc == BSSCL_OK) rc = ensure_fy_work(E, X.n, w);
-      // The sampler copied the draws on its own stream.
-      if (rc == BSSCL_OK && e == hipSuccess) e = hipStreamWaitEvent(E->st, sr.draws_copied, 0);
-      if (rc == BSSCL_OK && e == hipSuccess) {
-        const int nxt = E->perm_cur ^ 1;
-        e = launch_fisher_yates(E->st, sr.draws_dev, X.n, E->perm[E->perm_cur].p,
-                                E->perm[nxt].p, w);
-        E->perm_cur = nxt;
-        E->perm_next_round = sr.round + 1;
-        rows_d = E->perm[nxt].p;
-      }
-    } else {
-      rc = E->rows_in.ensure((size_t)m);
-      if (rc == BSSCL_OK) e = hipMemcpyAsync(E->rows_in.p, sr.rows, (size_t)m * 4, hipMemcpyHostToDevice, E->st);
-      rows_d = E->rows_in.p;
+  // Enqueue the next round now, so the GPU works on it while this one is
+  // read back and handed to the caller.
+  if (E->pipeline && pipeline_safe(E, a, sampler) && sampler_remaining(sampler) > 0) {
+    const int nxt = E->rslot_next;
+    E->rslot_next ^= 1;
+    const int rc = enqueue_round(E, sampler, a, nxt);
+    if (rc != BSSCL_OK) {
+      (void)drain_rounds(E, cur);
+      return rc;
     }
-    if (rc == BSSCL_OK && e == hipSuccess && rows_d)
-      e = launch_sort_rows(E->st, rows_d, m, E->row_flags.p, n_pad, E->sort_tmp.p, E->rows32.p);
-    if (rc == BSSCL_OK && e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("rows: ") + hipGetErrorString(e));
+    E->ahead = nxt;
   }
+  const int rc = finish_round(E, cur, out, out_train_loss);
   if (rc != BSSCL_OK) {
-    (void)hipStreamSynchronize(E->st);
-    sampler_give_back(sampler, token);
+    if (E->ahead >= 0) (void)drain_rounds(E, E->ahead);
+    E->ahead = -1;
     return rc;
   }
-  TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight,
-                reg_lambda, gamma};
-  // The tree, its replay (est:641-820), F += lr * tree(X) and the training
-  // log-loss all run on the device; one readback brings the tree and the
-  // loss.  A tree that needs a larger node table, or more candidate slots
-  // than the device replay holds, is built again by the host-driven path.
-  const int32_t F_sel = (int32_t)feats.size();
-  const int32_t M = 2 * max_leaves + 2;
-  const int nb = update_F_blocks(X.n);
-  int32_t run = 0;
-  // More candidate slots than the device replay holds: host replay only.
-  // (Test hook: BSSCL_TEST_HOST_REPLAY=1 forces the host path.)
-  const char *force_host = std::getenv("BSSCL_TEST_HOST_REPLAY");
-  const bool device_replay = max_leaves + 2 <= kReplaySlots && !(force_host && force_host[0] == '1');
-  if (rc == BSSCL_OK && device_replay)
-    rc = prepare_tree_buffers(E, m, F_sel, std::max(1, max_depth), max_leaves);
-  if (rc == BSSCL_OK) rc = E->partials_d.ensure((size_t)nb);
-  if (rc == BSSCL_OK) rc = E->tree_d.ensure((size_t)M);
-  if (rc == BSSCL_OK) rc = ensure_round_out(E, M);
-  if (rc == BSSCL_OK && device_replay) rc = launch_tree(E, true, m, feats, nb_sel, tp, &run);
-  RoundHeader *hdr = reinterpret_cast<RoundHeader *>(E->round_d.p);
-  const TreeArrays arrays = round_arrays(E->round_d.p, M);
-  if (rc == BSSCL_OK && !device_replay) {
-    rc = sync(E);  // the sampler's buffers must be read before they go back
-  } else if (rc == BSSCL_OK) {
-    ReplayArgs ra;
-    ra.gamma = gamma;
-    ra.reg_lambda = reg_lambda;
-    ra.g_scale = E->g_scale;
-    ra.h_scale = E->h_scale;
-    ra.max_leaves = max_leaves;
-    ra.out_len = M;
-    // (Test hook BSSCL_TEST_REPLAY_GLOBAL: 1 reads the node table from HBM,
-    // 2 keeps the candidate slots in LDS instead of registers.)
-    const char *rg = std::getenv("BSSCL_TEST_REPLAY_GLOBAL");
-    ra.stage_limit = !rg ? (1 << 30) : rg[0] == '1' ? 0 : rg[0] == '2' ? 1023 : (1 << 30);
-    ra.node_cap = E->node_cap;
-    hipError_t e = launch_replay(E->st, E->nodes_d, E->plan_d, E->feat_d, ra, arrays,
-                                 E->tree_d.p, hdr);
-    if (e == hipSuccess)
-      e = launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, &hdr->node_count,
-                          learning_rate, E->F.p, E->y.p, E->partials_d.p, nb);
-    if (e == hipSuccess) e = launch_sum_partials(E->st, E->partials_d.p, nb, &hdr->loss_sum);
-    if (e == hipSuccess)
-      e = hipMemcpyAsync(E->round_pin, E->round_d.p, round_out_bytes(M), hipMemcpyDeviceToHost, E->st);
-    const int32_t tb = table_bound(E, run);
-    if (e == hipSuccess && E->prof)
-      e = hipMemcpyAsync(E->table_pin, E->table_d.p, 64 + (size_t)tb * sizeof(NodeOut),
-                         hipMemcpyDeviceToHost, E->st);
-    if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("round: ") + hipGetErrorString(e));
-    if (rc == BSSCL_OK) rc = sync(E);
-    if (rc == BSSCL_OK && E->prof) {
-      const LevelPlan *pl = reinterpret_cast<const LevelPlan *>(E->table_pin);
-      if (pl->overflow == 0 && pl->n_nodes >= 1 && pl->n_nodes <= tb)
-        tree_stats(E, reinterpret_cast<const NodeOut *>(E->table_pin + 64), pl->n_nodes, m, F_sel, tp);
-    }
-  }
-  // The sampler's buffers are no longer read once the stream is idle.
-  if (rc != BSSCL_OK) (void)hipStreamSynchronize(E->st);
-  sampler_give_back(sampler, token);
-  CHK(rc);
-  RoundHeader h = *reinterpret_cast<const RoundHeader *>(E->round_pin);
-  if (!device_replay) h.status = 4;
-  if (h.status == 0) {
-    const TreeArrays ha = round_arrays(E->round_pin, M);
-    std::memcpy(out_features, ha.features, (size_t)M * 4);
-    std::memcpy(out_thresholds, ha.thresholds, (size_t)M * 8);
-    std::memcpy(out_values, ha.values, (size_t)M * 8);
-    std::memcpy(out_left, ha.left, (size_t)M * 4);
-    std::memcpy(out_right, ha.right, (size_t)M * 4);
-    std::memcpy(out_split_gains, ha.gains, (size_t)M * 8);
-    *out_node_count = h.node_count;
-    if (out_train_loss) *out_train_loss = -h.loss_sum / (double)X.n;
-  } else if (h.status == 1 || h.status == 4) {
-    // F was left alone: build the tree on the host-driven path and apply it.
-    if (h.status == 1) E->node_cap_floor = std::max(h.needed, 2 * E->node_cap);
-    CHK(build_tree_core(E, true, m, feats, nb_sel, tp, out));
-    CHK(upload_tree(E, out_features, out_thresholds, out_values, out_left,
-                    out_right, *out_node_count, X.F));
-    CHK(E->loss_d.ensure(1));
-    HIPCHK(launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, nullptr,
-                           learning_rate, E->F.p, E->y.p, E->partials_d.p, nb));
-    HIPCHK(launch_sum_partials(E->st, E->partials_d.p, nb, E->loss_d.p));
-    double s = 0.0;
-    HIPCHK(hipMemcpyAsync(&s, E->loss_d.p, 8, hipMemcpyDeviceToHost, E->st));
-    CHK(sync(E));
-    if (out_train_loss) *out_train_loss = -s / (double)X.n;
-  } else {
-    return set_error(BSSCL_EINTERNAL, "tree builder: device replay failed (status " +
-                                          std::to_string(h.status) + ")");
-  }
   if (E->prof)
-    E->stats[11] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_wait0).count();
+    E->stats[11] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  return BSSCL_OK;
+}
+
+int bsscl_boost_set_pipeline(bsscl_engine *E, int32_t on) {
+  if (!E) return set_error(BSSCL_EINVAL, "null engine");
+  HIPCHK(hipSetDevice(E->device));
+  if (!on && E->ahead >= 0) {
+    const int p = E->ahead;
+    E->ahead = -1;
+    CHK(drain_rounds(E, p));
+  }
+  E->pipeline = on != 0;
   return BSSCL_OK;
 }
 

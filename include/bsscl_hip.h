@@ -119,6 +119,17 @@ int bsscl_boost_round(bsscl_engine *eng, bsscl_sampler *sampler,
                       int32_t *out_right, int32_t *out_node_count,
                       double *out_split_gains, double *out_train_loss);
 
+/* Pipelined rounds (no reference counterpart; the reference's loop is
+ * synchronous, est:2825-2906): with `on`, bsscl_boost_round enqueues the
+ * sampler's next round, with the same arguments, before it returns the
+ * current one, so the GPU never waits for the caller.  Every later call
+ * must pass the same arguments until pipelining is turned off; turning it
+ * off (or bsscl_boost_begin) waits for and drops a round enqueued ahead,
+ * whose F update then stays applied.  Trees deeper than 9 levels or with
+ * more than 1022 leaves are not enqueued ahead.  The sampler must outlive a
+ * round enqueued ahead: turn pipelining off before destroying it. */
+int bsscl_boost_set_pipeline(bsscl_engine *eng, int32_t on);
+
 /* F of the boosting run (float64[n]). */
 int bsscl_boost_get_F(bsscl_engine *eng, double *F_out);
 
