@@ -299,7 +299,8 @@ class Engine:
         check(lib().bsscl_engine_stats(self.handle, ptr(out), 16, ptr(n)))
         keys = ["hist_launches", "hist_ms", "hist_row_features", "hist_bytes",
                 "part_launches", "part_ms", "split_launches", "split_ms",
-                "trees", "nodes_expanded", "sampler_wait_ms", "round_ms"]
+                "trees", "nodes_expanded", "sampler_wait_ms", "round_ms",
+                "reduce_launches", "reduce_ms"]
         return dict(zip(keys, out[:int(n[0])].tolist()))
 
 

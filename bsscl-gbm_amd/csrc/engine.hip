@@ -226,6 +226,7 @@ struct bsscl_engine {
   // Node-indexed buffers (node_cap nodes) and the level lists the planner
   // writes (see ensure_nodes / prepare_tree_buffers for their sizes).
   DevBuf<unsigned long long> pool;
+  DevBuf<unsigned long long> part_d;  // per-task partial histograms [task][F_sel][bin][g,h]
   int32_t node_alloc = 0;      // nodes the node-indexed buffers were sized for
   int32_t node_cap = 0;        // nodes the planner may create in this tree
   int32_t node_cap_floor = 0;  // raised when a tree needed more nodes
@@ -268,10 +269,12 @@ struct bsscl_engine {
   DevBuf<double> partials_d, loss_d, out_d;
   PinnedArena pin;
 
-  // Histogram launch shape (see hist_fchunk / hist_tile_rows); tunable with
-  // BSSCL_HIST_FC, BSSCL_HIST_BLOCKS_PER_CU and BSSCL_HIST_ROWS_PER_FLUSH.
-  int32_t hist_fc = 4;
-  int32_t hist_blocks_per_cu = 4;
+  // Histogram launch shape of the current tree (see read_hist_tuning,
+  // hist_fchunk, hist_tile_rows); tunable with BSSCL_HIST_FC,
+  // BSSCL_HIST_BLOCKS_PER_CU and BSSCL_HIST_ROWS_PER_FLUSH.
+  int32_t hist_fc = 1;
+  int32_t hist_copies = 4;
+  int32_t hist_blocks_per_cu = 8;
   int32_t hist_rows_per_flush = 5120;
 
   // Profiling.
@@ -284,7 +287,7 @@ struct bsscl_engine {
     uint64_t seq;  // boosting round that recorded them
   };
   std::vector<Pending> pending;
-  double stats[12] = {0};
+  double stats[14] = {0};
 };
 
 namespace bsscl {
@@ -335,8 +338,9 @@ int prof_collect(bsscl_engine *E, uint64_t upto = UINT64_MAX) {
     }
     float ms = 0.f;
     HIPCHK(hipEventElapsedTime(&ms, p.a, p.b));
-    E->stats[p.kind == 0 ? 0 : (p.kind == 1 ? 4 : 6)] += 1.0;
-    E->stats[p.kind == 0 ? 1 : (p.kind == 1 ? 5 : 7)] += (double)ms;
+    const int slot = p.kind == 0 ? 0 : p.kind == 1 ? 4 : p.kind == 2 ? 6 : 12;
+    E->stats[slot] += 1.0;
+    E->stats[slot + 1] += (double)ms;
     E->ev_free.push_back(p.a);
     E->ev_free.push_back(p.b);
   }
@@ -444,8 +448,7 @@ int ensure_nodes(bsscl_engine *E, int32_t cap, int32_t F_sel) {
   return BSSCL_OK;
 }
 
-// Feature chunk of a histogram block: 4 features (16 KB of LDS) keeps
-// several blocks per CU and limits how often a row's (g,h) is re-read.
+// Feature chunk of a histogram block (hist_fc, at most F_sel).
 int32_t hist_fchunk(bsscl_engine *E, int32_t F_sel) {
   int32_t fc = E->hist_fc;
   while (fc > 1 && fc > F_sel) fc >>= 1;
@@ -618,18 +621,30 @@ void add_part_tiles(const PartParent &P, int32_t parent_index, std::vector<PartT
     tiles.push_back({r, kPartTile, parent_index});
 }
 
-// Histogram launch shape from the environment (read per tree, so a tuning
-// sweep can change it between calls).
-void read_hist_tuning(bsscl_engine *E) {
+// Histogram launch shape of a tree over m rows of F_sel features.  One
+// feature per block gives the most blocks and the least work per block,
+// which suits every level of a tree up to ~64M row-features (measured on
+// MI355X: 1M x 22 root 27.5 us with one feature per block, 33.5 us with
+// four); larger trees use two features per block, which reads each row's
+// (g,h) half as often (5M x 35 root: 165 us, 205 us with one).  The
+// environment overrides the defaults (read per tree, for tuning sweeps).
+void read_hist_tuning(bsscl_engine *E, int64_t m, int32_t F_sel) {
   auto env_int = [](const char *name, int32_t lo, int32_t hi, int32_t dflt) {
     const char *e = std::getenv(name);
     if (!e) return dflt;
     const long x = std::strtol(e, nullptr, 10);
     return (x >= lo && x <= hi) ? (int32_t)x : dflt;
   };
-  E->hist_fc = env_int("BSSCL_HIST_FC", 1, 8, 4);
-  if (E->hist_fc != 1 && E->hist_fc != 2 && E->hist_fc != 4 && E->hist_fc != 8) E->hist_fc = 4;
-  E->hist_blocks_per_cu = env_int("BSSCL_HIST_BLOCKS_PER_CU", 1, 64, 4);
+  const int32_t fc0 = (double)m * F_sel >= 64e6 ? 2 : 1;
+  E->hist_fc = env_int("BSSCL_HIST_FC", 1, 8, fc0);
+  if (E->hist_fc != 1 && E->hist_fc != 2 && E->hist_fc != 4 && E->hist_fc != 8) E->hist_fc = fc0;
+  // Four lane-owned copies of each histogram in LDS (see k_hist): 18.6
+  // instead of 21.7 us per launch at 1M x 28, 72 instead of 85 at 10M x 50.
+  E->hist_copies = env_int("BSSCL_HIST_COPIES", 1, 8, 4);
+  if (E->hist_copies != 1 && E->hist_copies != 4 && E->hist_copies != 8) E->hist_copies = 1;
+  if (E->hist_fc * E->hist_copies > 8) E->hist_copies = 8 / E->hist_fc;
+  if (E->hist_copies == 2) E->hist_copies = 1;
+  E->hist_blocks_per_cu = env_int("BSSCL_HIST_BLOCKS_PER_CU", 1, 64, 8);
   E->hist_rows_per_flush = env_int("BSSCL_HIST_ROWS_PER_FLUSH", 256, 1 << 22, 5120);
 }
 
@@ -639,7 +654,7 @@ void read_hist_tuning(bsscl_engine *E) {
 // plus 2 per parent).
 int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t levels,
                          int32_t max_leaves) {
-  read_hist_tuning(E);
+  read_hist_tuning(E, m, F_sel);
   const int64_t ld_c = round_up(m + 32, 256);
   bool grow = false;
   for (int s = 0; s < 2; ++s)
@@ -655,7 +670,8 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
   const int64_t hcap = (int64_t)hist_target(E, F_sel) + cap + 4;
   if (tcap > INT32_MAX / 2 || hcap > INT32_MAX / 2)
     return set_error(BSSCL_EINVAL, "tree too large for the level lists");
-  grow = grow || E->tiles_d.cap < (size_t)tcap || E->hist_tasks_d.cap < (size_t)hcap;
+  grow = grow || E->tiles_d.cap < (size_t)tcap || E->hist_tasks_d.cap < (size_t)hcap ||
+         E->part_d.cap < (size_t)hcap * F_sel * kHistPerFeat;
   if (grow) CHK(sync(E));
   E->ld_c = ld_c;
   for (int s = 0; s < 2; ++s) {
@@ -667,6 +683,7 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
   CHK(E->tile_left_d.ensure((size_t)tcap));
   CHK(E->tile_off_d.ensure((size_t)tcap));
   CHK(E->hist_tasks_d.ensure((size_t)hcap));
+  CHK(E->part_d.ensure((size_t)hcap * F_sel * kHistPerFeat));
   E->tile_cap = (int32_t)tcap;
   E->hist_cap = (int32_t)hcap;
   CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 16u << 20)));
@@ -695,6 +712,7 @@ int launch_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_
   for (int64_t t = 0; t * th < m; ++t) ht.push_back({0, (int32_t)t});
   const SplitTask st0{0, -1, -1, 0};
   LevelPlan rp = {};
+  rp.n_parents = 1;  // the root's histogram reference, for the reduction
   rp.n_hist = (int32_t)ht.size();
   rp.n_split = 1;
   rp.first_child = 0;
@@ -714,6 +732,8 @@ int launch_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_
   pk.add(ht.data(), ht.size() * sizeof(HistTask));
   pk.add(&st0, sizeof(SplitTask));
   pk.add(&rp, sizeof(LevelPlan));
+  const int32_t root_tasks[2] = {0, rp.n_hist};
+  pk.add(root_tasks, sizeof(root_tasks));
   std::vector<char *> dv;
   CHK(upload_pack(E, pk, dv));
   HIPCHK(hipMemcpyAsync(E->plan_d, dv[4], sizeof(LevelPlan), hipMemcpyDeviceToDevice, E->st));
@@ -726,14 +746,18 @@ int launch_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_
                             use32 ? E->rows32.p : nullptr,
                             use32 ? nullptr : E->rows64.p, m, E->ghq.p,
                             E->codes_c[0].p, E->ld_c, E->gh_c[0].p, E->rid_c[0].p,
-                            E->ld_c, E->segs.p, E->hist_node_d.p, E->pool.p,
-                            E->node_stride));
+                            E->ld_c, E->segs.p, E->hist_node_d.p));
   hipEvent_t stop;
   CHK(prof_begin(E, 0, &stop));
   HIPCHK(launch_hist(E->st, E->codes_c[0].p, E->ld_c, E->gh_c[0].p,
                      reinterpret_cast<const HistTask *>(dv[2]), E->plan_d, rp.n_hist,
                      E->hist_node_d.p, E->segs.p, E->nb_sel_d, E->hot_sel_d, F_sel,
-                     hist_fchunk(E, F_sel), E->pool.p, E->node_stride));
+                     hist_fchunk(E, F_sel), E->hist_copies, E->part_d.p));
+  CHK(prof_end(E, stop));
+  CHK(prof_begin(E, 3, &stop));
+  HIPCHK(launch_hist_reduce(E->st, E->plan_d, 1, reinterpret_cast<const int32_t *>(dv[5]),
+                            E->hist_node_d.p, E->segs.p, E->part_d.p, F_sel, E->pool.p,
+                            E->node_stride));
   CHK(prof_end(E, stop));
   CHK(prof_begin(E, 2, &stop));
   HIPCHK(launch_split(E->st, reinterpret_cast<const SplitTask *>(dv[3]), E->plan_d, 1,
@@ -786,8 +810,7 @@ int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parent
                            max_tiles, E->tile_left_d.p));
   HIPCHK(launch_part_scan(E->st, parents, plan, std::min(max_parents, 1024), tile_begin,
                           E->tile_left_d.p, E->tile_off_d.p, E->nleft_d.p, E->segs.p,
-                          E->hist_node_d.p, min_samples_leaf,
-                          move_rows ? E->pool.p : nullptr, E->node_stride));
+                          E->hist_node_d.p, min_samples_leaf));
   if (move_rows)
     HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p, E->ld_c,
                                E->gh_c[src].p, E->gh_c[dst].p, E->rid_c[src].p,
@@ -823,7 +846,11 @@ int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
   CHK(prof_begin(E, 0, &stop));
   HIPCHK(launch_hist(E->st, E->codes_c[dst].p, E->ld_c, E->gh_c[dst].p, E->hist_tasks_d.p,
                      E->plan_d, H, E->hist_node_d.p, E->segs.p, E->nb_sel_d, E->hot_sel_d,
-                     F_sel, hist_fchunk(E, F_sel), E->pool.p, E->node_stride));
+                     F_sel, hist_fchunk(E, F_sel), E->hist_copies, E->part_d.p));
+  CHK(prof_end(E, stop));
+  CHK(prof_begin(E, 3, &stop));
+  HIPCHK(launch_hist_reduce(E->st, E->plan_d, P, E->hist_begin_d.p, E->hist_node_d.p,
+                            E->segs.p, E->part_d.p, F_sel, E->pool.p, E->node_stride));
   CHK(prof_end(E, stop));
   CHK(prof_begin(E, 2, &stop));
   // About 4096 blocks of 4 (node, feature) waves at most; they stride.
@@ -1467,6 +1494,7 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->table_d.release();
   if (E->table_pin) (void)hipHostFree(E->table_pin);
   E->pool.release();
+  E->part_d.release();
   E->segs.release();
   E->cand.release();
   E->totals.release();
@@ -1894,7 +1922,7 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
   HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, reinterpret_cast<const int32_t *>(dv[0]), 1,
                             nullptr, E->rows64.p, m, E->ghq.p, E->codes_c[0].p, E->ld_c,
                             E->gh_c[0].p, E->rid_c[0].p, E->ld_c, E->segs.p,
-                            E->hist_node_d.p, E->pool.p, E->node_stride));
+                            E->hist_node_d.p));
   const PartParent P{0, m, 0, bin, 1, 2, 0, 0};
   std::vector<PartTile> tiles;
   add_part_tiles(P, 0, tiles);
@@ -1969,7 +1997,7 @@ int bsscl_engine_set_profiling(bsscl_engine *E, int32_t on) {
 
 int bsscl_engine_stats(bsscl_engine *E, double *out, int32_t cap, int32_t *n_out) {
   if (!E || !out || !n_out) return set_error(BSSCL_EINVAL, "null argument");
-  const int32_t n = std::min<int32_t>(cap, 12);
+  const int32_t n = std::min<int32_t>(cap, 14);
   for (int32_t i = 0; i < n; ++i) out[i] = E->stats[i];
   *n_out = n;
   return BSSCL_OK;

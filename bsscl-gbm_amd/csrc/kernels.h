@@ -195,8 +195,7 @@ hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               const int32_t *rows32, const int64_t *rows64,
                               int64_t m, const int2 *ghq, uint8_t *codes_c,
                               int64_t ld_c, int2 *gh_c, int32_t *rid_c,
-                              int64_t pad_to, NodeSeg *segs, int32_t *hist_node,
-                              unsigned long long *root_hist, int64_t hist_words);
+                              int64_t pad_to, NodeSeg *segs, int32_t *hist_node);
 // Level kernels take their work counts from a device LevelPlan; the grid
 // argument (blocks, tasks or parents) is an upper bound, and blocks loop
 // over the work with a grid stride, so any bound >= 1 gives the same result.
@@ -205,8 +204,14 @@ hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const LevelPlan *plan, int32_t max_tasks,
                        const int32_t *hist_node, const NodeSeg *segs,
                        const int32_t *nb_sel, const int32_t *hot_sel,
-                       int32_t F_sel, int32_t fchunk,
-                       unsigned long long *pool, int64_t node_stride);
+                       int32_t F_sel, int32_t fchunk, int32_t copies,
+                       unsigned long long *part);
+// Sums the partials that launch_hist stored for each node with a histogram
+// task (hist_begin: a node's tasks, hist_node: its id) into the pool.
+hipError_t launch_hist_reduce(hipStream_t st, const LevelPlan *plan, int32_t max_refs,
+                              const int32_t *hist_begin, const int32_t *hist_node,
+                              const NodeSeg *segs, const unsigned long long *part,
+                              int32_t F_sel, unsigned long long *pool, int64_t node_stride);
 int hist_blocks(int32_t n_tasks, int32_t nchunks);
 hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
                              int64_t ld_c, const PartParent *parents,
@@ -217,8 +222,7 @@ hipError_t launch_part_scan(hipStream_t st, const PartParent *parents,
                             const int32_t *tile_begin,
                             const int32_t *tile_left, int64_t *tile_left_off,
                             int64_t *parent_nleft, NodeSeg *segs,
-                            int32_t *hist_node, int32_t min_samples_leaf,
-                            unsigned long long *pool, int64_t node_stride);
+                            int32_t *hist_node, int32_t min_samples_leaf);
 hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                uint8_t *codes_dst, int64_t ld_c,
                                const int2 *gh_src, int2 *gh_dst,

@@ -404,12 +404,9 @@ __global__ __launch_bounds__(256) void k_gather_root(
     const int64_t *__restrict__ rows64, int64_t m, const int2 *__restrict__ ghq,
     uint8_t *__restrict__ codes_c, int64_t ld_c, int2 *__restrict__ gh_c,
     int32_t *__restrict__ rid_c, int64_t pad_to, NodeSeg *__restrict__ segs,
-    int32_t *__restrict__ hist_node, unsigned long long *__restrict__ root_hist,
-    int64_t hist_words) {
+    int32_t *__restrict__ hist_node) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
-  // The root's segment, histogram slot and zeroed histogram.
-  for (int64_t i = t; i < hist_words; i += nthreads) root_hist[i] = 0ull;
+  // The root's segment and histogram slot.
   if (t == 0) {
     NodeSeg r;
     r.start = 0;
@@ -445,14 +442,12 @@ hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               const int32_t *rows32, const int64_t *rows64,
                               int64_t m, const int2 *ghq, uint8_t *codes_c,
                               int64_t ld_c, int2 *gh_c, int32_t *rid_c,
-                              int64_t pad_to, NodeSeg *segs, int32_t *hist_node,
-                              unsigned long long *root_hist, int64_t hist_words) {
+                              int64_t pad_to, NodeSeg *segs, int32_t *hist_node) {
   const int64_t threads = (pad_to + 3) / 4;
   if (threads <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_gather_root, dim3((unsigned)((threads + 255) / 256)),
                      dim3(256), 0, st, codes, ld, feat, F_sel, rows32, rows64, m,
-                     ghq, codes_c, ld_c, gh_c, rid_c, pad_to, segs, hist_node,
-                     root_hist, hist_words);
+                     ghq, codes_c, ld_c, gh_c, rid_c, pad_to, segs, hist_node);
   return hipGetLastError();
 }
 
@@ -476,8 +471,17 @@ hipError_t launch_iota(hipStream_t st, int32_t *a, int64_t n) {
 // Histogram build (est:581-596, est:722-737).
 //
 // A work item is one row tile of a node and one chunk of FC selected
-// features.  Its private histogram [FC][256 bins][g,h] int64 lives in LDS
-// (4 KB per feature, so several blocks share a CU).  A thread takes 16
+// features.  Its private histogram [FC][g[256], h[256]] int64 lives in LDS
+// (4 KB per feature, so several blocks share a CU).  Keeping the g and h
+// sums in separate arrays spreads a wave's 64 adds over all LDS banks
+// (interleaved [bin][g,h] pairs use half of them): 2.17 instead of 1.70
+// (g,h) updates per clock per CU on MI355X with uniform random bins.
+//
+// The block stores its histogram, as [bin][g,h], into the task's slot of
+// the partial buffer with plain coalesced stores; k_hist_reduce then sums a
+// node's partials into its histogram.  (Adding every block's bins into the
+// node's histogram with device-scope atomics made one memory-side atomic
+// per bin per block: as many bytes as the codes at 1M rows.)  A thread takes 16
 // consecutive rows: 128 bytes of (g,h), then per feature one 16-byte load of
 // packed codes and 32 64-bit LDS adds.  Rows outside the tile add zero.  The
 // block then adds its non-zero bins into the node's histogram in HBM.
@@ -491,14 +495,17 @@ hipError_t launch_iota(hipStream_t st, int32_t *a, int64_t n) {
 constexpr int kHistBlock = 256;
 constexpr int kHistRows = 16;  // rows per thread per step
 
-template <int FC>
+// With C > 1 copies, lane l adds into copy l % C, stored at bin * C + c:
+// the copies of one bin sit in C consecutive words, so lanes of different
+// copies never meet in an LDS bank whatever their bins (3.13 instead of 2.18
+// (g,h) updates per clock per CU for C = 8 on MI355X).
+template <int FC, int C>
 __device__ __forceinline__ void hist_item(
     unsigned long long *lh, const uint8_t *__restrict__ codes_c, int64_t ld_c,
-    const int2 *__restrict__ gh_c, const HistTask task, int chunk,
+    const int2 *__restrict__ gh_c, const HistTask task, int32_t ti, int chunk,
     const int32_t *__restrict__ hist_node, const NodeSeg *__restrict__ segs,
     const int32_t *__restrict__ nb_sel, const int32_t *__restrict__ hot_sel,
-    int32_t F_sel, int32_t tile_rows, unsigned long long *__restrict__ pool,
-    int64_t node_stride) {
+    int32_t F_sel, int32_t tile_rows, unsigned long long *__restrict__ part) {
   const int32_t node = hist_node[task.ref];
   if (node < 0) return;
   const NodeSeg seg = segs[node];
@@ -519,8 +526,9 @@ __device__ __forceinline__ void hist_item(
     ag[u] = 0;
     ah[u] = 0;
   }
-  for (int i = threadIdx.x; i < FC * kHistPerFeat; i += kHistBlock) lh[i] = 0ull;
+  for (int i = threadIdx.x; i < FC * kHistPerFeat * C; i += kHistBlock) lh[i] = 0ull;
   __syncthreads();
+  const int copy = lane_id() & (C - 1);
 
   const int64_t g0 = r0 >> 4, g1 = (r1 + 15) >> 4;
   for (int64_t g = g0 + threadIdx.x; g < g1; g += kHistBlock) {
@@ -546,7 +554,7 @@ __device__ __forceinline__ void hist_item(
       if (u < nf) {
         const uint4 c = *reinterpret_cast<const uint4 *>(codes_c + (int64_t)(f0 + u) * ld_c + row);
         const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
-        unsigned long long *hf = lh + u * kHistPerFeat;
+        unsigned long long *hf = lh + u * kHistPerFeat * C + copy;
 #pragma unroll
         for (int k = 0; k < kHistRows; ++k) {
           const uint32_t bin = min((cw[k >> 2] >> (8 * (k & 3))) & 255u, lim[u]);
@@ -556,9 +564,9 @@ __device__ __forceinline__ void hist_item(
             ag[u] += gq[k];
             ah[u] += hq[k];
           } else {
-            __hip_atomic_fetch_add(hf + 2 * bin, (unsigned long long)(long long)gq[k],
+            __hip_atomic_fetch_add(hf + bin * C, (unsigned long long)(long long)gq[k],
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            __hip_atomic_fetch_add(hf + 2 * bin + 1, (unsigned long long)(long long)hq[k],
+            __hip_atomic_fetch_add(hf + (kBins + bin) * C, (unsigned long long)(long long)hq[k],
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           }
         }
@@ -575,30 +583,36 @@ __device__ __forceinline__ void hist_item(
       c += __shfl_xor(c, o, 64);
     }
     if (u < nf && hb[u] != 0xffffffffu && lane_id() == 0 && (a | c)) {
-      __hip_atomic_fetch_add(lh + u * kHistPerFeat + 2 * hb[u], (unsigned long long)a,
+      __hip_atomic_fetch_add(lh + u * kHistPerFeat * C + hb[u] * C, (unsigned long long)a,
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      __hip_atomic_fetch_add(lh + u * kHistPerFeat + 2 * hb[u] + 1, (unsigned long long)c,
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_fetch_add(lh + u * kHistPerFeat * C + (kBins + hb[u]) * C,
+                             (unsigned long long)c, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   }
   __syncthreads();
-  unsigned long long *dst = pool + (int64_t)node * node_stride + (int64_t)f0 * kHistPerFeat;
+  // Partial of task ti, features f0 .. f0+nf-1, as [bin][g,h].
+  unsigned long long *dst = part + ((int64_t)ti * F_sel + f0) * kHistPerFeat;
   for (int i = threadIdx.x; i < nf * kHistPerFeat; i += kHistBlock) {
-    const unsigned long long v = lh[i];
-    if (v) atomicAdd(dst + i, v);
+    const int j = i & (kHistPerFeat - 1);
+    const unsigned long long *src = lh + ((i - j) + (j & 1) * kBins + (j >> 1)) * C;
+    unsigned long long v = 0ull;
+#pragma unroll
+    for (int c = 0; c < C; ++c) v += src[c];
+    dst[i] = v;
   }
   __syncthreads();  // lh is cleared again by the block's next item
 }
 
-template <int FC>
+template <int FC, int C>
 __global__ __launch_bounds__(kHistBlock) void k_hist(
     const uint8_t *__restrict__ codes_c, int64_t ld_c,
     const int2 *__restrict__ gh_c, const HistTask *__restrict__ tasks,
     const LevelPlan *__restrict__ plan, const int32_t *__restrict__ hist_node,
     const NodeSeg *__restrict__ segs, const int32_t *__restrict__ nb_sel,
     const int32_t *__restrict__ hot_sel, int32_t F_sel, int32_t nchunks,
-    unsigned long long *__restrict__ pool, int64_t node_stride) {
-  __shared__ unsigned long long lh[FC * kHistPerFeat];
+    unsigned long long *__restrict__ part) {
+  __shared__ unsigned long long lh[FC * kHistPerFeat * C];
   const int32_t n_tasks = plan->n_hist;
   const int32_t tile_rows = plan->tile_rows;
   // The grid is a multiple of 8 * nchunks, so every block keeps its XCD
@@ -608,8 +622,54 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
     const int ti = (j / nchunks) * 8 + (b & 7);
     if ((j / nchunks) * 8 >= n_tasks) break;
     if (ti >= n_tasks) continue;
-    hist_item<FC>(lh, codes_c, ld_c, gh_c, tasks[ti], j % nchunks, hist_node, segs,
-                  nb_sel, hot_sel, F_sel, tile_rows, pool, node_stride);
+    hist_item<FC, C>(lh, codes_c, ld_c, gh_c, tasks[ti], ti, j % nchunks, hist_node, segs,
+                     nb_sel, hot_sel, F_sel, tile_rows, part);
+  }
+}
+
+// Sums each built node's partials (one per task with rows; exact int64, so
+// the order does not matter) into its histogram in the pool.  A block owns
+// 64 consecutive words of one node: its kReduceWaves waves each sum every
+// kReduceWaves-th partial (one coalesced 512-byte load per partial), then
+// the waves' sums are added in LDS.
+constexpr int kReduceWaves = 16;
+
+__global__ __launch_bounds__(64 * kReduceWaves) void k_hist_reduce(
+    const LevelPlan *__restrict__ plan, const int32_t *__restrict__ hist_begin,
+    const int32_t *__restrict__ hist_node, const NodeSeg *__restrict__ segs,
+    const unsigned long long *__restrict__ part, int32_t F_sel,
+    unsigned long long *__restrict__ pool, int64_t node_stride) {
+  __shared__ unsigned long long acc_s[kReduceWaves][64];
+  const int32_t n_refs = plan->n_parents;
+  const int32_t tile_rows = plan->tile_rows;
+  const int32_t words = F_sel * kHistPerFeat;  // a multiple of 64
+  const int32_t groups = words / 64;
+  const int wave = (int)(threadIdx.x >> 6), lane = lane_id();
+  for (int64_t b = blockIdx.x; b < (int64_t)n_refs * groups; b += gridDim.x) {
+    const int32_t p = (int32_t)(b / groups);
+    const int32_t w = (int32_t)(b % groups) * 64 + lane;
+    const int32_t node = hist_node[p];
+    if (node < 0) continue;  // uniform over the block
+    const NodeSeg seg = segs[node];
+    if (!seg.valid) continue;
+    const int32_t t0 = hist_begin[p];
+    const int64_t with_rows = (seg.count + tile_rows - 1) / tile_rows;
+    const int32_t nt = (int32_t)min((int64_t)(hist_begin[p + 1] - t0), with_rows);
+    const unsigned long long *src = part + (int64_t)t0 * words + w;
+    unsigned long long acc = 0ull;
+    int32_t t = wave;
+    for (; t + kReduceWaves < nt; t += 2 * kReduceWaves)
+      acc += src[(int64_t)t * words] + src[(int64_t)(t + kReduceWaves) * words];
+    if (t < nt) acc += src[(int64_t)t * words];
+    acc_s[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+      unsigned long long sum = 0ull;
+#pragma unroll
+      for (int k = 0; k < kReduceWaves; ++k) sum += acc_s[k][lane];
+      pool[(int64_t)node * node_stride + w] = sum;
+    }
+    __syncthreads();
   }
 }
 
@@ -622,23 +682,39 @@ hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const LevelPlan *plan, int32_t max_tasks,
                        const int32_t *hist_node, const NodeSeg *segs,
                        const int32_t *nb_sel, const int32_t *hot_sel,
-                       int32_t F_sel, int32_t fchunk,
-                       unsigned long long *pool, int64_t node_stride) {
+                       int32_t F_sel, int32_t fchunk, int32_t copies,
+                       unsigned long long *part) {
   if (max_tasks <= 0) return hipSuccess;
   const int32_t nchunks = (F_sel + fchunk - 1) / fchunk;
   const dim3 grid((unsigned)hist_blocks(max_tasks, nchunks));
-#define BSSCL_HIST(FC)                                                              \
-  hipLaunchKernelGGL(k_hist<FC>, grid, dim3(kHistBlock), 0, st, codes_c, ld_c, gh_c, \
-                     tasks, plan, hist_node, segs, nb_sel, hot_sel, F_sel, nchunks, \
-                     pool, node_stride)
-  switch (fchunk) {
-    case 1: BSSCL_HIST(1); break;
-    case 2: BSSCL_HIST(2); break;
-    case 4: BSSCL_HIST(4); break;
-    case 8: BSSCL_HIST(8); break;
+#define BSSCL_HIST(FC, C)                                                              \
+  hipLaunchKernelGGL((k_hist<FC, C>), grid, dim3(kHistBlock), 0, st, codes_c, ld_c, gh_c, \
+                     tasks, plan, hist_node, segs, nb_sel, hot_sel, F_sel, nchunks,    \
+                     part)
+  // LDS per block: fchunk * copies * 8 KB (at most 32 KB).
+  switch (fchunk * 16 + copies) {
+    case 1 * 16 + 1: BSSCL_HIST(1, 1); break;
+    case 1 * 16 + 4: BSSCL_HIST(1, 4); break;
+    case 1 * 16 + 8: BSSCL_HIST(1, 8); break;
+    case 2 * 16 + 1: BSSCL_HIST(2, 1); break;
+    case 2 * 16 + 4: BSSCL_HIST(2, 4); break;
+    case 4 * 16 + 1: BSSCL_HIST(4, 1); break;
+    case 8 * 16 + 1: BSSCL_HIST(8, 1); break;
     default: return hipErrorInvalidValue;
   }
 #undef BSSCL_HIST
+  return hipGetLastError();
+}
+
+hipError_t launch_hist_reduce(hipStream_t st, const LevelPlan *plan, int32_t max_refs,
+                              const int32_t *hist_begin, const int32_t *hist_node,
+                              const NodeSeg *segs, const unsigned long long *part,
+                              int32_t F_sel, unsigned long long *pool, int64_t node_stride) {
+  if (max_refs <= 0 || F_sel <= 0) return hipSuccess;
+  const int64_t groups = (int64_t)F_sel * kHistPerFeat / 64;
+  const int64_t blocks = std::min<int64_t>((int64_t)max_refs * groups, 16384);
+  hipLaunchKernelGGL(k_hist_reduce, dim3((unsigned)blocks), dim3(64 * kReduceWaves), 0, st,
+                     plan, hist_begin, hist_node, segs, part, F_sel, pool, node_stride);
   return hipGetLastError();
 }
 
@@ -693,16 +769,14 @@ hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
 }
 
 // One block per parent: exclusive offsets of its tiles' left counts, the
-// children's segments, whether the split is kept (est:678-683), which child
-// is the smaller one (est:701-709), and a zeroed histogram for that child.
+// children's segments, whether the split is kept (est:678-683) and which
+// child is the smaller one (est:701-709), whose histogram is built.
 __global__ __launch_bounds__(kPartBlock) void k_part_scan(
     const PartParent *__restrict__ parents, const LevelPlan *__restrict__ plan,
     const int32_t *__restrict__ tile_begin,
     const int32_t *__restrict__ tile_left, int64_t *__restrict__ tile_left_off,
     int64_t *__restrict__ parent_nleft, NodeSeg *__restrict__ segs,
-    int32_t *__restrict__ hist_node, int32_t min_samples_leaf,
-    unsigned long long *__restrict__ pool, int64_t node_stride) {
-  // pool == nullptr: the children's histograms are not needed.
+    int32_t *__restrict__ hist_node, int32_t min_samples_leaf) {
   __shared__ uint32_t tmp[kPartBlock / 64];
   const int32_t n_parents = plan->n_parents;
   for (int p = (int)blockIdx.x; p < n_parents; p += (int)gridDim.x) {
@@ -721,10 +795,6 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scan(
     const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
     const bool left_small = nl <= nr;
     const int32_t small_id = left_small ? P.left_id : P.right_id;
-    if (ok && pool) {
-      unsigned long long *h = pool + (int64_t)small_id * node_stride;
-      for (int64_t i = threadIdx.x; i < node_stride; i += kPartBlock) h[i] = 0ull;
-    }
     if (threadIdx.x == 0) {
       parent_nleft[p] = nl;
       NodeSeg L, R;
@@ -748,13 +818,11 @@ hipError_t launch_part_scan(hipStream_t st, const PartParent *parents,
                             const int32_t *tile_begin,
                             const int32_t *tile_left, int64_t *tile_left_off,
                             int64_t *parent_nleft, NodeSeg *segs,
-                            int32_t *hist_node, int32_t min_samples_leaf,
-                            unsigned long long *pool, int64_t node_stride) {
+                            int32_t *hist_node, int32_t min_samples_leaf) {
   if (max_parents <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_part_scan, dim3((unsigned)max_parents), dim3(kPartBlock), 0,
                      st, parents, plan, tile_begin, tile_left, tile_left_off,
-                     parent_nleft, segs, hist_node, min_samples_leaf, pool,
-                     node_stride);
+                     parent_nleft, segs, hist_node, min_samples_leaf);
   return hipGetLastError();
 }
 
