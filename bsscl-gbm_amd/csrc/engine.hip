@@ -274,6 +274,9 @@ struct bsscl_engine {
   // BSSCL_HIST_BLOCKS_PER_CU and BSSCL_HIST_ROWS_PER_FLUSH.
   int32_t hist_fc = 1;
   int32_t hist_copies = 4;
+  // Partition tile of the current tree: 256 threads x part_rows rows.
+  int32_t part_rows = 4;
+  int32_t part_tile = 1024;
   int32_t hist_blocks_per_cu = 8;
   int32_t hist_rows_per_flush = 5120;
 
@@ -615,10 +618,11 @@ int replay(bsscl_engine *E, const std::vector<HNode> &nodes,
   return BSSCL_OK;
 }
 
-void add_part_tiles(const PartParent &P, int32_t parent_index, std::vector<PartTile> &tiles) {
-  const int64_t a = P.start & ~int64_t(3);
-  for (int64_t r = a; r < P.start + P.count; r += kPartTile)
-    tiles.push_back({r, kPartTile, parent_index});
+void add_part_tiles(const bsscl_engine *E, const PartParent &P, int32_t parent_index,
+                    std::vector<PartTile> &tiles) {
+  const int64_t a = P.start & ~int64_t(15);
+  for (int64_t r = a; r < P.start + P.count; r += E->part_tile)
+    tiles.push_back({r, E->part_tile, parent_index});
 }
 
 // Histogram launch shape of a tree over m rows of F_sel features.  One
@@ -650,7 +654,7 @@ void read_hist_tuning(bsscl_engine *E, int64_t m, int32_t F_sel) {
 
 // Buffers of a tree over m rows: the compact sets, the node table for the
 // tree's levels and the level lists, whose capacities bound what the
-// planner may write (PartTile: m/1024 + 2 per parent; HistTask: the target
+// planner may write (PartTile: m/kPartTile + 2 per parent; HistTask: the target
 // plus 2 per parent).
 int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t levels,
                          int32_t max_leaves) {
@@ -666,7 +670,13 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
     const long v = std::strtol(t, nullptr, 10);
     if (v >= 3) cap = std::max<int32_t>((int32_t)std::min<long>(v, cap), E->node_cap_floor);
   }
-  const int64_t tcap = m / kPartTile + (int64_t)cap + 4;
+  // Partition tiles: the most rows per thread that still gives about 512
+  // tiles for the root (16-byte loads at 10M rows; 4-byte loads and more
+  // blocks at 1M, where 4096-row tiles left CUs idle).
+  E->part_rows = 16;
+  while (E->part_rows > 4 && m / ((int64_t)kPartThreads * E->part_rows) < 512) E->part_rows >>= 1;
+  E->part_tile = kPartThreads * E->part_rows;
+  const int64_t tcap = m / E->part_tile + (int64_t)cap + 4;
   const int64_t hcap = (int64_t)hist_target(E, F_sel) + cap + 4;
   if (tcap > INT32_MAX / 2 || hcap > INT32_MAX / 2)
     return set_error(BSSCL_EINVAL, "tree too large for the level lists");
@@ -788,6 +798,7 @@ int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParam
   pa.hist_cap = E->hist_cap;
   pa.hist_target = hist_target(E, F_sel);
   pa.rows_per_flush = E->hist_rows_per_flush;
+  pa.part_tile = E->part_tile;
   hipEvent_t stop;
   CHK(prof_begin(E, 2, &stop));
   HIPCHK(launch_plan(E->st, E->nodes_d, E->plan_d, E->parents_d[(level + 1) & 1].p,
@@ -807,7 +818,7 @@ int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parent
   hipEvent_t stop;
   CHK(prof_begin(E, 1, &stop));
   HIPCHK(launch_part_count(E->st, E->codes_c[src].p, E->ld_c, parents, tiles, plan,
-                           max_tiles, E->tile_left_d.p));
+                           max_tiles, E->part_rows, E->tile_left_d.p));
   HIPCHK(launch_part_scan(E->st, parents, plan, std::min(max_parents, 1024), tile_begin,
                           E->tile_left_d.p, E->tile_off_d.p, E->nleft_d.p, E->segs.p,
                           E->hist_node_d.p, min_samples_leaf));
@@ -815,7 +826,7 @@ int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parent
     HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p, E->ld_c,
                                E->gh_c[src].p, E->gh_c[dst].p, E->rid_c[src].p,
                                E->rid_c[dst].p, parents, tiles, plan, max_tiles,
-                               E->tile_off_d.p, E->nleft_d.p, F_sel));
+                               E->part_rows, E->tile_off_d.p, E->nleft_d.p, F_sel));
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
@@ -829,7 +840,7 @@ int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
   const int src = level & 1, dst = src ^ 1;
   const PartParent *par = E->parents_d[level & 1].p;
   const int32_t P = level_parents_bound(E, level);
-  const int32_t T = (int32_t)std::min<int64_t>(E->tile_cap, m / kPartTile + 2 * (int64_t)P + 1);
+  const int32_t T = (int32_t)std::min<int64_t>(E->tile_cap, m / E->part_tile + 2 * (int64_t)P + 1);
   CHK(launch_partition(E, src, dst, par, E->tile_begin_d.p, E->tiles_d.p, E->plan_d, P, T,
                        F_sel, tp.min_samples_leaf, !last));
   hipEvent_t stop;
@@ -1925,7 +1936,7 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
                             E->hist_node_d.p));
   const PartParent P{0, m, 0, bin, 1, 2, 0, 0};
   std::vector<PartTile> tiles;
-  add_part_tiles(P, 0, tiles);
+  add_part_tiles(E, P, 0, tiles);
   const int32_t tb[2] = {0, (int32_t)tiles.size()};
   LevelPlan lp = {};
   lp.n_parents = 1;

@@ -55,6 +55,7 @@ struct PlanArgs {
   int32_t hist_cap;       // HistTask capacity
   int32_t hist_target;    // histogram row tiles wanted per level
   int32_t rows_per_flush; // fewest rows per histogram tile flush
+  int32_t part_tile;      // rows per partition tile
 };
 
 // One partition tile of a parent (host -> device).
@@ -104,9 +105,10 @@ struct TreeNodeDev {
   double value;
 };
 
-// A run of kPartTile rows starting at a 4-row boundary (tiles of one parent
-// are consecutive; rows outside the parent's segment are masked).
-constexpr int kPartTile = 1024;
+// Partition tiles are runs of 256 * R rows (R = 4, 8 or 16 rows per thread,
+// chosen per tree) starting at a 16-row boundary (tiles of one parent are
+// consecutive; rows outside the parent's segment are masked).
+constexpr int kPartThreads = 256;
 
 // The node table of a tree: a node's split search result (k_node_best),
 // its frontier rank and children (k_plan).  Read back once per tree.
@@ -216,7 +218,7 @@ int hist_blocks(int32_t n_tasks, int32_t nchunks);
 hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
                              int64_t ld_c, const PartParent *parents,
                              const PartTile *tiles, const LevelPlan *plan,
-                             int32_t max_tiles, int32_t *tile_left);
+                             int32_t max_tiles, int32_t part_rows, int32_t *tile_left);
 hipError_t launch_part_scan(hipStream_t st, const PartParent *parents,
                             const LevelPlan *plan, int32_t max_parents,
                             const int32_t *tile_begin,
@@ -229,7 +231,8 @@ hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                const int32_t *rid_src, int32_t *rid_dst,
                                const PartParent *parents,
                                const PartTile *tiles, const LevelPlan *plan,
-                               int32_t max_tiles, const int64_t *tile_left_off,
+                               int32_t max_tiles, int32_t part_rows,
+                               const int64_t *tile_left_off,
                                const int64_t *parent_nleft, int32_t F_sel);
 hipError_t launch_split(hipStream_t st, const SplitTask *tasks,
                         const LevelPlan *plan, int32_t max_tasks,

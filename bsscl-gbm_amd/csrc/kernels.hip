@@ -720,17 +720,62 @@ hipError_t launch_hist_reduce(hipStream_t st, const LevelPlan *plan, int32_t max
 
 // ---------------------------------------------------------------------------
 // Partition (est:662-674, made stable): count, scan, scatter.  A tile is 256
-// threads x 4 rows = 1024 rows starting at a 4-row boundary; rows of the
-// tile outside the parent's segment are masked.
+// threads x R rows (R = 4, 8 or 16, chosen per tree: 1024 to 4096 rows)
+// starting at a 16-row boundary; rows of the tile outside the parent's
+// segment are masked.  A thread reads its R rows' codes of a feature as one
+// R-byte load.
 // ---------------------------------------------------------------------------
 constexpr int kPartBlock = 256;
+
+template <int R> struct CodesR;  // R consecutive codes as one load
+template <> struct CodesR<4> { using T = uint32_t; };
+template <> struct CodesR<8> { using T = uint2; };
+template <> struct CodesR<16> { using T = uint4; };
+
+template <int R>
+union CodeWords {
+  typename CodesR<R>::T v;
+  uint32_t w[R / 4];
+};
 
 __device__ __forceinline__ void tile_rows(const PartTile &t, const PartParent &P,
                                           int64_t &lo, int64_t &hi) {
   lo = max(t.row0, P.start);
-  hi = min(t.row0 + (int64_t)kPartTile, P.start + P.count);
+  hi = min(t.row0 + (int64_t)t.rows, P.start + P.count);
 }
 
+// The R codes of rows row .. row+R-1 of one feature column; a group wholly
+// outside [lo, hi) is not read (it may lie past the buffer).
+template <int R>
+__device__ __forceinline__ CodeWords<R> load_codes(const uint8_t *__restrict__ col, int64_t row,
+                                                   int64_t lo, int64_t hi) {
+  CodeWords<R> c;
+  if (row < hi && row + R > lo) {
+    c.v = *reinterpret_cast<const typename CodesR<R>::T *>(col + row);
+  } else {
+#pragma unroll
+    for (int k = 0; k < R / 4; ++k) c.w[k] = 0u;
+  }
+  return c;
+}
+
+// Bit k of the result: row row+k lies in [lo, hi) (valid) and, for lmask,
+// goes left (code <= bin).
+template <int R>
+__device__ __forceinline__ void row_masks(const CodeWords<R> &c, int64_t row, int64_t lo,
+                                          int64_t hi, uint32_t bin, uint32_t &vmask,
+                                          uint32_t &lmask) {
+  vmask = 0u;
+  lmask = 0u;
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const bool in = (row + k >= lo) && (row + k < hi);
+    vmask |= (in ? 1u : 0u) << k;
+    lmask |= ((in && ((c.w[k >> 2] >> (8 * (k & 3))) & 255u) <= bin) ? 1u : 0u) << k;
+  }
+}
+
+template <int R>
 __global__ __launch_bounds__(kPartBlock) void k_part_count(
     const uint8_t *__restrict__ codes_c, int64_t ld_c,
     const PartParent *__restrict__ parents, const PartTile *__restrict__ tiles,
@@ -742,18 +787,12 @@ __global__ __launch_bounds__(kPartBlock) void k_part_count(
     const PartParent P = parents[t.parent];
     int64_t lo, hi;
     tile_rows(t, P, lo, hi);
-    const int64_t row = t.row0 + 4 * (int64_t)threadIdx.x;
-    // A dword wholly past the segment is not read (it may lie past the buffer).
-    const uint32_t w = (row < hi && row + 4 > lo)
-        ? *reinterpret_cast<const uint32_t *>(codes_c + (int64_t)P.fpos * ld_c + row) : 0u;
-    uint32_t cnt = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const bool in = (row + k >= lo) && (row + k < hi);
-      cnt += (in && ((w >> (8 * k)) & 255u) <= (uint32_t)P.bin) ? 1u : 0u;
-    }
+    const int64_t row = t.row0 + (int64_t)R * threadIdx.x;
+    const CodeWords<R> c = load_codes<R>(codes_c + (int64_t)P.fpos * ld_c, row, lo, hi);
+    uint32_t vmask, lmask;
+    row_masks<R>(c, row, lo, hi, (uint32_t)P.bin, vmask, lmask);
     uint32_t total;
-    block_excl_scan<kPartBlock>(cnt, tmp, total);
+    block_excl_scan<kPartBlock>((uint32_t)__builtin_popcount(lmask), tmp, total);
     if (threadIdx.x == 0) tile_left[ti] = (int32_t)total;
   }
 }
@@ -761,10 +800,17 @@ __global__ __launch_bounds__(kPartBlock) void k_part_count(
 hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
                              int64_t ld_c, const PartParent *parents,
                              const PartTile *tiles, const LevelPlan *plan,
-                             int32_t max_tiles, int32_t *tile_left) {
+                             int32_t max_tiles, int32_t part_rows, int32_t *tile_left) {
   if (max_tiles <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_part_count, dim3((unsigned)max_tiles), dim3(kPartBlock), 0,
-                     st, codes_c, ld_c, parents, tiles, plan, tile_left);
+  switch (part_rows) {
+    case 4: hipLaunchKernelGGL(k_part_count<4>, dim3((unsigned)max_tiles), dim3(kPartBlock), 0,
+                               st, codes_c, ld_c, parents, tiles, plan, tile_left); break;
+    case 8: hipLaunchKernelGGL(k_part_count<8>, dim3((unsigned)max_tiles), dim3(kPartBlock), 0,
+                               st, codes_c, ld_c, parents, tiles, plan, tile_left); break;
+    case 16: hipLaunchKernelGGL(k_part_count<16>, dim3((unsigned)max_tiles), dim3(kPartBlock), 0,
+                                st, codes_c, ld_c, parents, tiles, plan, tile_left); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -827,14 +873,18 @@ hipError_t launch_part_scan(hipStream_t st, const PartParent *parents,
 }
 
 // Moves a tile's rows to the child segments in the other buffer set, keeping
-// the input order on each side.  A row's rank among the tile's left (right)
-// rows is a block-wide exclusive scan of per-thread counts plus its position
-// among the thread's 4 rows.  Rows are first placed in LDS in output order
-// (left run, then right run), so the global stores are consecutive: codes
-// as whole dwords (bytes only at the two ends of each run), (g,h) and row
-// ids as consecutive elements.
-constexpr int kScatterFeat = 16;  // features staged in LDS at a time
+// the input order on each side.  A row's slot (left run, then right run) is
+// a block-wide exclusive scan of per-thread counts plus its rank among the
+// thread's 16 rows; inv[slot] is the row it came from.  The output is cut
+// into R-byte chunks aligned in the destination: per feature, the tile's
+// codes go to LDS (one R-byte store per thread) and each chunk is gathered
+// from there and written with one R-byte store (byte stores only for the
+// chunks at the ends of a run, which it shares with the neighbouring
+// tiles).  (g,h) and row ids are gathered through inv and stored as
+// consecutive elements.
+constexpr int kChunkSlots = 2;  // output chunks a thread may own (<= 260 per tile)
 
+template <int R>
 __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
     const uint8_t *__restrict__ codes_src, uint8_t *__restrict__ codes_dst,
     int64_t ld_c, const int2 *__restrict__ gh_src, int2 *__restrict__ gh_dst,
@@ -843,13 +893,11 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
     const LevelPlan *__restrict__ plan, const int64_t *__restrict__ tile_left_off,
     const int64_t *__restrict__ parent_nleft, int32_t F_sel) {
   __shared__ uint32_t tmp[kPartBlock / 64];
-  __shared__ int2 gh_s[kPartTile];
-  __shared__ int32_t rid_s[kPartTile];
-  // Staged codes of up to kScatterFeat features, read back as (possibly
-  // unaligned) dwords: 8 bytes of slack past the last feature.
-  __shared__ uint32_t cs32[(kScatterFeat * kPartTile + 8) / 4];
-  uint8_t *cs = reinterpret_cast<uint8_t *>(cs32);
+  constexpr int kTile = kPartBlock * R;
+  __shared__ uint16_t inv[kTile];
+  __shared__ typename CodesR<R>::T cs[2][kPartBlock];  // one feature's codes, double buffered
   const int32_t n_tiles = plan->n_tiles;
+  const int tid = (int)threadIdx.x;
   for (int32_t ti = (int32_t)blockIdx.x; ti < n_tiles; ti += (int32_t)gridDim.x) {
     const PartTile t = tiles[ti];
     const PartParent P = parents[t.parent];
@@ -859,96 +907,101 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
     const int64_t nl = parent_nleft[t.parent];
     const int64_t lbase = P.start + loff;
     const int64_t rbase = P.start + nl + ((lo - P.start) - loff);
-    const int64_t row = t.row0 + 4 * (int64_t)threadIdx.x;
-    const uint32_t w = (row < hi && row + 4 > lo)
-        ? *reinterpret_cast<const uint32_t *>(codes_src + (int64_t)P.fpos * ld_c + row) : 0u;
-    uint32_t lmask = 0, vmask = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const bool in = (row + k >= lo) && (row + k < hi);
-      vmask |= (in ? 1u : 0u) << k;
-      lmask |= ((in && ((w >> (8 * k)) & 255u) <= (uint32_t)P.bin) ? 1u : 0u) << k;
-    }
-    const uint32_t packed = ((uint32_t)__builtin_popcount(vmask) << 16) | (uint32_t)__builtin_popcount(lmask);
+    const int64_t row = t.row0 + (int64_t)R * tid;
+    const CodeWords<R> sc = load_codes<R>(codes_src + (int64_t)P.fpos * ld_c, row, lo, hi);
+    uint32_t vmask, lmask;
+    row_masks<R>(sc, row, lo, hi, (uint32_t)P.bin, vmask, lmask);
+    const uint32_t packed = ((uint32_t)__builtin_popcount(vmask) << 16) |
+                            (uint32_t)__builtin_popcount(lmask);
     uint32_t tot;
     const uint32_t pre = block_excl_scan<kPartBlock>(packed, tmp, tot);
     const int ltot = (int)(tot & 0xffffu), vtot = (int)(tot >> 16);
     const int rtot = vtot - ltot;
     const int lpre = (int)(pre & 0xffffu), rpre = (int)(pre >> 16) - lpre;
-    int sidx[4];
-    int li = 0, ri = 0;
+    {
+      int li = 0, ri = 0;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const bool v = (vmask >> k) & 1u, l = (lmask >> k) & 1u;
-      sidx[k] = !v ? -1 : (l ? lpre + li : ltot + rpre + ri);
-      li += l ? 1 : 0;
-      ri += (v && !l) ? 1 : 0;
-    }
-    if (vmask) {
-      const int4 *gp = reinterpret_cast<const int4 *>(gh_src + row);
-      const int4 ga = gp[0], gb = gp[1];
-      const int4 ra = *reinterpret_cast<const int4 *>(rid_src + row);
-      const int2 ghv[4] = {make_int2(ga.x, ga.y), make_int2(ga.z, ga.w),
-                           make_int2(gb.x, gb.y), make_int2(gb.z, gb.w)};
-      const int32_t rv[4] = {ra.x, ra.y, ra.z, ra.w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (sidx[k] >= 0) {
-          gh_s[sidx[k]] = ghv[k];
-          rid_s[sidx[k]] = rv[k];
-        }
-    }
-    // Output dwords of the left run [lbase, lbase+ltot) and the right run.
-    const int64_t lq0 = lbase >> 2, rq0 = rbase >> 2;
-    const int nld = ltot ? (int)(((lbase + ltot + 3) >> 2) - lq0) : 0;
-    const int nrd = rtot ? (int)(((rbase + rtot + 3) >> 2) - rq0) : 0;
-    const int per_f = nld + nrd;
-    for (int f0 = 0; f0 < F_sel; f0 += kScatterFeat) {
-      const int nf = min(kScatterFeat, F_sel - f0);
-      if (vmask) {
-        for (int u = 0; u < nf; ++u) {
-          const uint32_t c = *reinterpret_cast<const uint32_t *>(codes_src + (int64_t)(f0 + u) * ld_c + row);
-#pragma unroll
-          for (int k = 0; k < 4; ++k)
-            if (sidx[k] >= 0) cs[u * kPartTile + sidx[k]] = (uint8_t)(c >> (8 * k));
-        }
+      for (int k = 0; k < R; ++k) {
+        const bool v = (vmask >> k) & 1u, l = (lmask >> k) & 1u;
+        if (v) inv[l ? lpre + li : ltot + rpre + ri] = (uint16_t)(R * tid + k);
+        li += l ? 1 : 0;
+        ri += (v && !l) ? 1 : 0;
       }
+    }
+    __syncthreads();
+    // (g,h) and row ids: slot s -> its destination row.
+    for (int sl = tid; sl < vtot; sl += kPartBlock) {
+      const int64_t d = sl < ltot ? lbase + sl : rbase + (sl - ltot);
+      const int64_t r = t.row0 + inv[sl];
+      gh_dst[d] = gh_src[r];
+      rid_dst[d] = rid_src[r];
+    }
+    // Output chunks: the left run's then the right run's aligned R-byte
+    // chunks.  Per owned chunk: its destination row and, per byte, the
+    // tile row it copies (0xffff: outside the run, not written).
+    const int64_t lc0 = lbase & ~int64_t(R - 1), rc0 = rbase & ~int64_t(R - 1);
+    const int nlc = ltot ? (int)((lbase + ltot + R - 1) / R - lbase / R) : 0;
+    const int nrc = rtot ? (int)((rbase + rtot + R - 1) / R - rbase / R) : 0;
+    int64_t cdst[kChunkSlots];
+    uint32_t csrc[kChunkSlots][R / 2];  // R x u16 tile rows
+    bool cfull[kChunkSlots], cown[kChunkSlots];
+#pragma unroll
+    for (int q = 0; q < kChunkSlots; ++q) {
+      const int c = tid + q * kPartBlock;
+      cown[q] = c < nlc + nrc;
+      const bool left = c < nlc;
+      const int64_t c0 = left ? lc0 + R * (int64_t)c : rc0 + R * (int64_t)(c - nlc);
+      const int64_t D = left ? lbase : rbase;
+      const int L = left ? ltot : rtot;
+      const int S = left ? 0 : ltot;
+      cdst[q] = c0;
+      bool full = true;
+#pragma unroll
+      for (int k = 0; k < R; k += 2) {
+        uint32_t pairv = 0u;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int64_t dr = c0 + k + h;
+          const bool in = cown[q] && dr >= D && dr < D + L;
+          full = full && in;
+          const uint32_t src = in ? (uint32_t)inv[S + (int)(dr - D)] : 0xffffu;
+          pairv |= src << (16 * h);
+        }
+        csrc[q][k >> 1] = pairv;
+      }
+      cfull[q] = full;
+    }
+    // Per feature: codes to LDS (double buffered: one barrier per feature),
+    // then the owned chunks gathered from LDS and stored.
+    CodeWords<R> cur = load_codes<R>(codes_src, row, lo, hi);
+    for (int f = 0; f < F_sel; ++f) {
+      cs[f & 1][tid] = cur.v;
+      if (f + 1 < F_sel) cur = load_codes<R>(codes_src + (int64_t)(f + 1) * ld_c, row, lo, hi);
       __syncthreads();
-      if (f0 == 0) {
-        for (int i = threadIdx.x; i < vtot; i += kPartBlock) {
-          const int64_t d = i < ltot ? lbase + i : rbase + (i - ltot);
-          gh_dst[d] = gh_s[i];
-          rid_dst[d] = rid_s[i];
-        }
-      }
-      for (int r = threadIdx.x; r < per_f; r += kPartBlock) {
-        const bool left = r < nld;
-        const int64_t q = left ? lq0 + r : rq0 + (r - nld);
-        const int64_t run0 = left ? lbase : rbase;
-        const int run_len = left ? ltot : rtot;
-        const int soff = left ? 0 : ltot;
-        const int64_t p0 = q << 2;
-        const bool full = p0 >= run0 && p0 + 4 <= run0 + run_len;
-        for (int u = 0; u < nf; ++u) {
-          uint8_t *dcol = codes_dst + (int64_t)(f0 + u) * ld_c;
-          const int sbase = u * kPartTile + soff;
-          if (full) {
-            // Four staged bytes starting at an arbitrary LDS byte offset.
-            const int a = sbase + (int)(p0 - run0);
-            const uint32_t lo32 = cs32[a >> 2], hi32 = cs32[(a >> 2) + 1];
-            const uint32_t v = __builtin_amdgcn_alignbyte(hi32, lo32, (uint32_t)(a & 3));
-            *reinterpret_cast<uint32_t *>(dcol + p0) = v;
-          } else {
+      const uint8_t *tb = reinterpret_cast<const uint8_t *>(cs[f & 1]);
+      uint8_t *dcol = codes_dst + (int64_t)f * ld_c;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              const int64_t pp = p0 + k;
-              if (pp >= run0 && pp < run0 + run_len) dcol[pp] = cs[sbase + (int)(pp - run0)];
-            }
+      for (int q = 0; q < kChunkSlots; ++q) {
+        if (!cown[q]) continue;
+        if (cfull[q]) {
+          CodeWords<R> o;
+#pragma unroll
+          for (int k = 0; k < R / 4; ++k) {
+            const uint32_t s01 = csrc[q][2 * k], s23 = csrc[q][2 * k + 1];
+            o.w[k] = (uint32_t)tb[s01 & 0xffffu] | ((uint32_t)tb[s01 >> 16] << 8) |
+                     ((uint32_t)tb[s23 & 0xffffu] << 16) | ((uint32_t)tb[s23 >> 16] << 24);
+          }
+          *reinterpret_cast<typename CodesR<R>::T *>(dcol + cdst[q]) = o.v;
+        } else {
+#pragma unroll
+          for (int k = 0; k < R; ++k) {
+            const uint32_t sv = (csrc[q][k >> 1] >> (16 * (k & 1))) & 0xffffu;
+            if (sv != 0xffffu) dcol[cdst[q] + k] = tb[sv];
           }
         }
       }
-      __syncthreads();
     }
+    __syncthreads();  // inv and cs are rewritten by the block's next tile
   }
 }
 
@@ -958,13 +1011,21 @@ hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                const int32_t *rid_src, int32_t *rid_dst,
                                const PartParent *parents,
                                const PartTile *tiles, const LevelPlan *plan,
-                               int32_t max_tiles, const int64_t *tile_left_off,
+                               int32_t max_tiles, int32_t part_rows,
+                               const int64_t *tile_left_off,
                                const int64_t *parent_nleft, int32_t F_sel) {
   if (max_tiles <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_part_scatter, dim3((unsigned)max_tiles), dim3(kPartBlock),
-                     0, st, codes_src, codes_dst, ld_c, gh_src, gh_dst, rid_src,
-                     rid_dst, parents, tiles, plan, tile_left_off, parent_nleft,
-                     F_sel);
+#define BSSCL_SCATTER(R)                                                                 \
+  hipLaunchKernelGGL(k_part_scatter<R>, dim3((unsigned)max_tiles), dim3(kPartBlock), 0, st, \
+                     codes_src, codes_dst, ld_c, gh_src, gh_dst, rid_src, rid_dst, parents, \
+                     tiles, plan, tile_left_off, parent_nleft, F_sel)
+  switch (part_rows) {
+    case 4: BSSCL_SCATTER(4); break;
+    case 8: BSSCL_SCATTER(8); break;
+    case 16: BSSCL_SCATTER(16); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef BSSCL_SCATTER
   return hipGetLastError();
 }
 
@@ -1333,8 +1394,8 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
       split_tasks[2 * i] = SplitTask{L, v, L + 1, a.level + 1};
       split_tasks[2 * i + 1] = SplitTask{L + 1, v, L, a.level + 1};
     }
-    const int64_t a0 = N.start & ~int64_t(3);
-    tile_begin[i] = (int32_t)((N.start + N.count - a0 + kPartTile - 1) / kPartTile);
+    const int64_t a0 = N.start & ~int64_t(15);
+    tile_begin[i] = (int32_t)((N.start + N.count - a0 + a.part_tile - 1) / a.part_tile);
     rows += (unsigned long long)(N.count / 2);
   }
 #pragma unroll
@@ -1389,8 +1450,8 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
       else hi = mid - 1;
     }
     PartTile T;
-    T.row0 = (parents[lo].start & ~int64_t(3)) + (int64_t)(t - tile_begin[lo]) * kPartTile;
-    T.rows = kPartTile;
+    T.row0 = (parents[lo].start & ~int64_t(15)) + (int64_t)(t - tile_begin[lo]) * a.part_tile;
+    T.rows = a.part_tile;
     T.parent = lo;
     tiles[t] = T;
   }

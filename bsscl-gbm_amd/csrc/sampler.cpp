@@ -360,9 +360,42 @@ bool draw_steps_scalar(Stream &s, uint32_t hi, uint32_t *out) {
   return true;
 }
 
+// Draws of a long shuffle go through a staging buffer that stays in L1:
+// whole 4 KB blocks of it are written to the destination with
+// non-temporal stores, which need no read-for-ownership of the
+// destination's lines (the destination is read next by the copy engine).
+// Ordinary stores made the draw thread store-bound at 10M rows.
+constexpr int kStageWords = 1024;
+
+struct Staged {
+  alignas(64) uint32_t buf[kStageWords + 128];
+  uint32_t *dst = nullptr;
+
+  __attribute__((target("avx512f"))) uint32_t *flush(uint32_t *o) {
+    for (int k = 0; k < kStageWords; k += 16)
+      _mm512_stream_si512(reinterpret_cast<__m512i *>(dst + k), _mm512_load_si512(buf + k));
+    dst += kStageWords;
+    const ptrdiff_t rest = (o - buf) - kStageWords;
+    std::memmove(buf, buf + kStageWords, (size_t)rest * sizeof(uint32_t));
+    return buf + rest;
+  }
+  void finish(uint32_t *o) {
+    std::memcpy(dst, buf, (size_t)(o - buf) * sizeof(uint32_t));
+    _mm_sfence();
+  }
+};
+
 __attribute__((target("avx512f,avx512vl,avx512bw,popcnt")))
 bool draw_steps_avx512(Stream &s, uint32_t hi, uint32_t *out) {
   uint32_t i = hi;
+  std::unique_ptr<Staged> st;
+  uint32_t *const out0 = out;
+  const bool staged = hi >= 4 * kStageWords && (reinterpret_cast<uintptr_t>(out) & 63) == 0;
+  if (staged) {
+    st.reset(new Staged());
+    st->dst = out0;
+    out = st->buf;
+  }
   while (i >= 1) {
     const uint32_t lo = 1u << (31 - __builtin_clz(i));
     const uint32_t mask = lo | (lo - 1);
@@ -400,6 +433,7 @@ bool draw_steps_avx512(Stream &s, uint32_t hi, uint32_t *out) {
         out += c0 + c1 + c2 + c3;
         i -= c0 + c1 + c2 + c3;
         p += 64;
+        if (staged && out - st->buf >= kStageWords) out = st->flush(out);
       }
       // 16 at a time (band [i - 14, i]).
       while (i - lo >= 16 && e - p >= 16) {
@@ -412,6 +446,7 @@ bool draw_steps_avx512(Stream &s, uint32_t hi, uint32_t *out) {
         out += c;
         i -= c;
         p += 16;
+        if (staged && out - st->buf >= kStageWords) out = st->flush(out);
       }
       // One word: a block with an order-dependent word, the end of a mask
       // range or the end of a chunk.
@@ -421,10 +456,13 @@ bool draw_steps_avx512(Stream &s, uint32_t hi, uint32_t *out) {
         const uint32_t a = v <= i ? 1u : 0u;
         out += a;
         i -= a;
+        if (staged && out - st->buf >= kStageWords) out = st->flush(out);
       }
       s.p = p;
     }
   }
+  if (staged) st->finish(out);
+  (void)out0;
   return true;
 }
 
