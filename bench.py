@@ -29,6 +29,11 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "fit trees/sec at 1M×28 d6 255 bins; histogram-build HBM GB/s vs peak"
 
 
+def _progress(msg):
+    """Progress on stderr; stdout carries only the JSON line."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def _sigmoid(z):
     return 1.0 / (1.0 + np.exp(-z))
 
@@ -96,6 +101,23 @@ def make_workload(name, predict=False):
 BREAKDOWN_ROUNDS = 5
 
 
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload`, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (copy-kernel calibrated), or None
+    when no such summary exists."""
+    import glob
+    import re
+    pat = re.compile(r"^traffic_bytes_per_launch\[%s, %s\]: (\d+)\s*$"
+                     % (re.escape(kernel), re.escape(workload)))
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+        with open(path) as fh:
+            for line in fh:
+                m = pat.match(line)
+                if m:
+                    return int(m.group(1))
+    return None
+
+
 def run_gpu(name, steps, warmup):
     """Fits warmup + steps + BREAKDOWN_ROUNDS rounds.  The timed rounds run
     with the histogram kernel's HIP events only (level 1); the last rounds,
@@ -104,6 +126,7 @@ def run_gpu(name, steps, warmup):
     from bsscl_gbm import HybridHistGBMNumbaV1_0_1
     X, y, params = make_workload(name)
     n, F = X.shape
+    _progress(f"{name}: {n} x {F} generated; fitting")
     marks = {}
 
     def hook(m, eng):
@@ -127,6 +150,7 @@ def run_gpu(name, steps, warmup):
     est.fit(X, y)
     t_fit = time.perf_counter() - t_fit
     del est._round_hook
+    _progress(f"fit done in {t_fit:.1f} s (binning {est.times['binning']:.0f} ms)")
     elapsed = marks["t1"] - marks["t0"]
     st = marks["stats"]
     # Prediction on fresh rows through the fitted trees.
@@ -134,6 +158,7 @@ def run_gpu(name, steps, warmup):
     t = time.perf_counter()
     est.predict_proba(Xp)
     t_pred_total = time.perf_counter() - t
+    _progress(f"predict_proba on {len(Xp)} rows in {t_pred_total:.2f} s")
     s0, s1 = marks["s0"], marks["s1"]
     sampler = {k: (s1[k] - s0[k]) / max(s1["rounds"] - s0["rounds"], 1)
                for k in ("draw_ms", "gen_ms")}
@@ -148,6 +173,7 @@ def run_cpu_baseline(name, rounds):
     the reference is serial) timed on this host for `rounds` rounds."""
     from oracle import model as om
     X, y, params = make_workload(name)
+    _progress(f"cpu baseline: oracle on {name}, {rounds} timed rounds")
     p = dict(params)
     p.pop("verbose")
     m = om.OracleGBM(**p)
@@ -210,7 +236,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("k_hist", a.workload),
             "kernel": "k_hist",
             "launches": int(st["hist_launches"]),
             "avg_launch_us": round(1e3 * st["hist_ms"] / launches, 2),
