@@ -21,7 +21,7 @@ LIB_NAME = "libbsscl_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 OBJ_DIR = os.path.join(ROOT, "_build")
 
-SOURCES = ["kernels.hip", "fisher_yates.hip", "engine.hip", "sampler.cpp"]
+SOURCES = ["kernels.hip", "fisher_yates.hip", "colsort.hip", "engine.hip", "sampler.cpp"]
 ARCH = "gfx950"
 
 

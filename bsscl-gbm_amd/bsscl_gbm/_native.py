@@ -27,6 +27,11 @@ _SIGS = {
     "bsscl_bin_features": [_P, _i32, _P, _i32, _i64, _i32, _P, _i32, _P, _P, _P],
     "bsscl_load_codes": [_P, _i32, _P, _i32, _i64, _i32],
     "bsscl_get_codes": [_P, _i32, _P],
+    "bsscl_stage_features": [_P, _P, _i32, _i64, _i32],
+    "bsscl_sort_columns": [_P, _P, _P],
+    "bsscl_sorted_gather": [_P, _i64, _P, _P, _P],
+    "bsscl_sorted_uniques": [_P, _i32, _i32, _P, _P],
+    "bsscl_release_staged": [_P],
     "bsscl_build_tree": [_P, _P, _P, _P, _i64, _P, _i32, _i32, _i32, _i32, _f64,
                          _P, _i32, _f64, _f64, _P, _P, _P, _P, _P, _P, _P],
     "bsscl_boost_begin": [_P, _P, _i64, _f64, _f64, _f64],
@@ -152,6 +157,49 @@ class Engine:
             ptr(e), e.shape[1], ptr(bc), ptr(ni),
             ptr(out) if out is not None else None))
         return out
+
+    def bin_staged(self, slot, n, F, is_f64, edges_2d, bin_counts, nan_bin_id):
+        """bin_features of the matrix staged by stage_features."""
+        e = np.ascontiguousarray(edges_2d, dtype=np.float64)
+        bc = np.ascontiguousarray(bin_counts, dtype=np.int32)
+        ni = np.ascontiguousarray(nan_bin_id, dtype=np.int32)
+        check(lib().bsscl_bin_features(
+            self.handle, int(slot), None, int(bool(is_f64)), int(n), int(F),
+            ptr(e), e.shape[1], ptr(bc), ptr(ni), None))
+
+    # -- bin edges ------------------------------------------------------------
+    def stage_features(self, X):
+        """Copies X (float32 or float64, n x F) to the device."""
+        X = np.ascontiguousarray(X)
+        if X.dtype not in (np.float32, np.float64):
+            raise ValueError("stage_features needs float32 or float64 X")
+        n, F = X.shape
+        check(lib().bsscl_stage_features(self.handle, ptr(X), int(X.dtype == np.float64), n, F))
+
+    def sort_columns(self, F):
+        """Sorts the staged columns; returns (nan_count, n_unique), int64[F] each."""
+        nan = np.empty(F, np.int64)
+        uniq = np.empty(F, np.int64)
+        check(lib().bsscl_sort_columns(self.handle, ptr(nan), ptr(uniq)))
+        return nan, uniq
+
+    def sorted_gather(self, cols, pos):
+        """Values (float64) at ranks pos of sorted columns cols."""
+        c = np.ascontiguousarray(cols, dtype=np.int32)
+        p = np.ascontiguousarray(pos, dtype=np.int64)
+        out = np.empty(len(p), np.float64)
+        check(lib().bsscl_sorted_gather(self.handle, len(p), ptr(c), ptr(p), ptr(out)))
+        return out
+
+    def sorted_uniques(self, col, max_out):
+        out = np.empty(max(int(max_out), 1), np.float64)
+        cnt = np.zeros(1, np.int32)
+        check(lib().bsscl_sorted_uniques(self.handle, int(col), int(max_out), ptr(out),
+                                         ptr(cnt)))
+        return out[:int(cnt[0])].copy()
+
+    def release_staged(self):
+        check(lib().bsscl_release_staged(self.handle))
 
     def load_codes(self, slot, codes):
         codes = np.ascontiguousarray(codes)

@@ -67,6 +67,38 @@ def _sigmoid(F):
     return 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
 
 
+def _percentile_ranks(m, q100, dtype):
+    """Ranks np.percentile(col, q100) reads from a NaN-free column of m
+    values of `dtype`, and its interpolation weights (NumPy 2.x 'linear'
+    method: q = q100 / dtype(100), virtual index (m - 1) * q, neighbours
+    floor and floor + 1, both clamped to the last value at or beyond it)."""
+    q = np.true_divide(q100, dtype.type(100))
+    vi = (m - 1) * q
+    prev = np.floor(vi)
+    nxt = prev + 1
+    above = vi >= m - 1
+    prev[above] = -1
+    nxt[above] = -1
+    below = vi < 0
+    prev[below] = 0
+    nxt[below] = 0
+    prev = prev.astype(np.intp)
+    nxt = nxt.astype(np.intp)
+    gamma = np.asanyarray(vi - prev, dtype=vi.dtype)
+    return np.where(prev < 0, m - 1, prev), np.where(nxt < 0, m - 1, nxt), gamma
+
+
+def _percentile_lerp(a, b, t):
+    """The interpolation np.percentile applies to the neighbours a, b (arrays
+    of the column's dtype) with weights t: NumPy's own sequence of ufuncs,
+    so the result carries the same roundings."""
+    diff_b_a = np.subtract(b, a)
+    out = np.asanyarray(np.add(a, diff_b_a * t))
+    np.subtract(b, diff_b_a * (1 - t), out=out, where=t >= 0.5,
+                casting='unsafe', dtype=type(out.dtype))
+    return out
+
+
 class HybridHistGBMNumbaV1_0_1:
     """Histogram GBM with the reference's parameters (est:1820-1923)."""
 
@@ -272,7 +304,60 @@ class HybridHistGBMNumbaV1_0_1:
     # ------------------------------------------------------------------
     # est:2073-2141 (numeric features)
     # ------------------------------------------------------------------
-    def _build_bin_edges(self, X, sample_weight=None):
+    def _build_bin_edges(self, X, sample_weight=None, eng=None):
+        """Edges of est:2073-2141.  With `eng` (X staged on its device) the
+        data passes run there: NaN counts, distinct counts, distinct values
+        and the order statistics np.percentile interpolates between; the
+        arithmetic between them is the reference's, on the host."""
+        if eng is None:
+            return self._build_bin_edges_host(X, sample_weight)
+        n, n_features = X.shape
+        nan_count, n_unique = eng.sort_columns(n_features)
+        dtype = X.dtype
+        edges = [None] * n_features
+        bin_counts = np.zeros(n_features, dtype=np.int32)
+        self._nan_bin_id = np.full(n_features, -1, dtype=np.int32)
+        lerp_cols = []  # (feature, m, number of quantiles)
+        for j in range(n_features):
+            has_nan = bool(nan_count[j] > 0)
+            m = n - int(nan_count[j])
+            if has_nan:
+                self._nan_bin_id[j] = 0
+                if m == 0:
+                    edges[j] = np.array([0.0, 1.0])
+                    bin_counts[j] = 1
+                    continue
+            max_numeric_bins = self.n_bins - (1 if has_nan else 0)
+            if n_unique[j] <= max_numeric_bins:
+                e = eng.sorted_uniques(j, int(n_unique[j])).astype(dtype)
+                edges[j] = e
+            else:
+                lerp_cols.append((j, m, min(max_numeric_bins + 1, int(n_unique[j]))))
+        # One gather for every rank the percentiles read.
+        plans, cols, pos = [], [], []
+        for j, m, k in lerp_cols:
+            q = np.linspace(0, 1, k)
+            lo, hi, gamma = _percentile_ranks(m, q * 100, dtype)
+            plans.append((j, len(cols), k, gamma))
+            cols.extend([j] * (2 * k))
+            pos.extend(lo.tolist())
+            pos.extend(hi.tolist())
+        vals = eng.sorted_gather(cols, pos).astype(dtype) if cols else None
+        for j, off, k, gamma in plans:
+            a = vals[off:off + k]
+            b = vals[off + k:off + 2 * k]
+            edges[j] = np.unique(_percentile_lerp(a, b, gamma))
+        for j in range(n_features):
+            if bin_counts[j] == 1 and self._nan_bin_id[j] == 0 and nan_count[j] == n:
+                continue
+            e = np.append(edges[j], edges[j][-1] + 1e-8)
+            edges[j] = e
+            bin_counts[j] = len(e) - 1 + (1 if self._nan_bin_id[j] == 0 else 0)
+        return self._edges_2d(edges, bin_counts)
+
+    def _build_bin_edges_host(self, X, sample_weight=None):
+        """est:2073-2141 with the reference's NumPy calls on the host: the
+        weighted-quantile branch (scale_pos_weight with objective='binary')."""
         edges = []
         n_features = X.shape[1]
         bin_counts = np.zeros(n_features, dtype=np.int32)
@@ -310,6 +395,11 @@ class HybridHistGBMNumbaV1_0_1:
             e = np.append(e, e[-1] + 1e-8)
             edges.append(e)
             bin_counts[j] = len(e) - 1 + (1 if has_nan else 0)
+        return self._edges_2d(edges, bin_counts)
+
+    @staticmethod
+    def _edges_2d(edges, bin_counts):
+        n_features = len(edges)
         max_b = int(np.max(bin_counts)) + 1
         edges_2d = np.zeros((n_features, max_b), dtype=np.float64)
         for j, e in enumerate(edges):
@@ -402,14 +492,29 @@ class HybridHistGBMNumbaV1_0_1:
             sample_weight = np.ones(len(y), dtype=np.float64)
             sample_weight[y == 1] = self.scale_pos_weight
         t0 = time.perf_counter()
-        self.bin_edges, self.feature_bin_counts = self._build_bin_edges(X, sample_weight=sample_weight)
-        self._max_bins = int(np.max(self.feature_bin_counts))
-        if self._max_bins > 256:
-            raise NotImplementedError(
-                f"n_bins={self.n_bins} gives {self._max_bins} bins for some feature; "
-                "the MI355X engine stores uint8 codes (at most 256 bins), use n_bins <= 255")
         eng = _engine(self._device_index())
-        eng.bin_features(0, X, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
+        # Unweighted edges come from the device (X is staged once and binned
+        # from there); the weighted-quantile branch stays on the host.
+        X = np.ascontiguousarray(X)
+        staged = sample_weight is None
+        if staged:
+            eng.stage_features(X)
+        try:
+            self.bin_edges, self.feature_bin_counts = self._build_bin_edges(
+                X, sample_weight=sample_weight, eng=eng if staged else None)
+            self._max_bins = int(np.max(self.feature_bin_counts))
+            if self._max_bins > 256:
+                raise NotImplementedError(
+                    f"n_bins={self.n_bins} gives {self._max_bins} bins for some feature; "
+                    "the MI355X engine stores uint8 codes (at most 256 bins), use n_bins <= 255")
+            if staged:
+                eng.bin_staged(0, X.shape[0], X.shape[1], X.dtype == np.float64, self.bin_edges,
+                               self.feature_bin_counts, self._nan_bin_id)
+            else:
+                eng.bin_features(0, X, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
+        finally:
+            if staged:
+                eng.release_staged()
         self.times['binning'] = (time.perf_counter() - t0) * 1000
         n_val = 0
         if X_val is not None and y_val is not None:

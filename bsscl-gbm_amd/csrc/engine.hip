@@ -269,6 +269,16 @@ struct bsscl_engine {
   DevBuf<double> partials_d, loss_d, out_d;
   PinnedArena pin;
 
+  // Feature matrix staged by bsscl_stage_features (row-major, as given) and
+  // its columns sorted by bsscl_sort_columns (keys [F][col_ld]).
+  DevBuf<unsigned char> xstage;
+  int64_t xs_n = 0;
+  int32_t xs_F = 0, xs_f64 = 0;
+  DevBuf<unsigned char> col_keys;
+  int64_t col_ld = 0;
+  bool cols_sorted = false;
+  std::vector<int64_t> col_m;  // non-NaN values per sorted column
+
   // Histogram launch shape of the current tree (see read_hist_tuning,
   // hist_fchunk, hist_tile_rows); tunable with BSSCL_HIST_FC,
   // BSSCL_HIST_BLOCKS_PER_CU and BSSCL_HIST_ROWS_PER_FLUSH.
@@ -1533,6 +1543,8 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->loss_d.release();
   E->out_d.release();
   E->pin.release();
+  E->xstage.release();
+  E->col_keys.release();
   for (hipEvent_t ev : E->ev_pool) (void)hipEventDestroy(ev);
   if (E->st) (void)hipStreamDestroy(E->st);
   delete E;
@@ -1543,11 +1555,15 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
                        const double *edges_2d, int32_t edge_stride,
                        const int32_t *bin_counts, const int32_t *nan_bin_id,
                        uint8_t *codes_out) {
-  if (!E || !X || !edges_2d || !bin_counts || !nan_bin_id)
+  if (!E || !edges_2d || !bin_counts || !nan_bin_id)
     return set_error(BSSCL_EINVAL, "bin_features: null argument");
   if (slot < 0 || slot > 1) return set_error(BSSCL_EINVAL, "matrix slot must be 0 or 1");
   if (n <= 0 || n > INT32_MAX || F <= 0)
     return set_error(BSSCL_EINVAL, "bin_features: bad shape");
+  const bool staged = (X == nullptr);
+  if (staged && (!E->xstage.p || E->xs_n != n || E->xs_F != F || E->xs_f64 != (x_is_f64 ? 1 : 0)))
+    return set_error(BSSCL_EINVAL,
+                     "bin_features: X is NULL but no staged matrix of this shape and dtype");
   int32_t has_any_nan = 0;
   for (int32_t j = 0; j < F; ++j) {
     if (bin_counts[j] < 1 || bin_counts[j] >= edge_stride)
@@ -1564,33 +1580,188 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
   HIPCHK(hipMemcpyAsync(ed.p, edges_2d, (size_t)F * edge_stride * 8, hipMemcpyHostToDevice, E->st));
   HIPCHK(hipMemcpyAsync(nb.p, bin_counts, (size_t)F * 4, hipMemcpyHostToDevice, E->st));
   HIPCHK(hipMemcpyAsync(nid.p, nan_bin_id, (size_t)F * 4, hipMemcpyHostToDevice, E->st));
-  // Stream X through the device in row chunks of at most 256 MB.
-  const size_t esz = x_is_f64 ? 8 : 4;
-  int64_t chunk = std::max<int64_t>(64, (int64_t)((256u << 20) / (esz * (size_t)F)) / 64 * 64);
-  chunk = std::min<int64_t>(chunk, round_up(n, 64));
-  DevBuf<unsigned char> xd;
-  int rc = xd.ensure((size_t)chunk * F * esz);
-  if (rc != BSSCL_OK) { ed.release(); nb.release(); nid.release(); return rc; }
   Matrix &M = E->mat[slot];
-  for (int64_t r0 = 0; r0 < n; r0 += chunk) {
-    const int64_t rows = std::min(chunk, n - r0);
-    hipError_t e = hipMemcpyAsync(xd.p, (const unsigned char *)X + (size_t)r0 * F * esz,
-                                  (size_t)rows * F * esz, hipMemcpyHostToDevice, E->st);
-    if (e == hipSuccess)
-      e = launch_bin(E->st, xd.p, x_is_f64, rows, F, ed.p, edge_stride, nb.p, nid.p,
-                     has_any_nan, M.codes.p + r0, M.ld);
+  const size_t esz = x_is_f64 ? 8 : 4;
+  if (staged) {
+    hipError_t e = launch_bin(E->st, E->xstage.p, x_is_f64, n, F, ed.p, edge_stride, nb.p,
+                              nid.p, has_any_nan, M.codes.p, M.ld);
     if (e == hipSuccess) e = hipStreamSynchronize(E->st);
-    if (e != hipSuccess) {
-      xd.release(); ed.release(); nb.release(); nid.release();
+    ed.release(); nb.release(); nid.release();
+    if (e != hipSuccess)
       return set_error(BSSCL_EDEVICE, std::string("binning: ") + hipGetErrorString(e));
+  } else {
+    // Stream X through the device in row chunks of at most 256 MB.
+    int64_t chunk = std::max<int64_t>(64, (int64_t)((256u << 20) / (esz * (size_t)F)) / 64 * 64);
+    chunk = std::min<int64_t>(chunk, round_up(n, 64));
+    DevBuf<unsigned char> xd;
+    int rc = xd.ensure((size_t)chunk * F * esz);
+    if (rc != BSSCL_OK) { ed.release(); nb.release(); nid.release(); return rc; }
+    for (int64_t r0 = 0; r0 < n; r0 += chunk) {
+      const int64_t rows = std::min(chunk, n - r0);
+      hipError_t e = hipMemcpyAsync(xd.p, (const unsigned char *)X + (size_t)r0 * F * esz,
+                                    (size_t)rows * F * esz, hipMemcpyHostToDevice, E->st);
+      if (e == hipSuccess)
+        e = launch_bin(E->st, xd.p, x_is_f64, rows, F, ed.p, edge_stride, nb.p, nid.p,
+                       has_any_nan, M.codes.p + r0, M.ld);
+      if (e == hipSuccess) e = hipStreamSynchronize(E->st);
+      if (e != hipSuccess) {
+        xd.release(); ed.release(); nb.release(); nid.release();
+        return set_error(BSSCL_EDEVICE, std::string("binning: ") + hipGetErrorString(e));
+      }
     }
+    xd.release();
+    ed.release();
+    nb.release();
+    nid.release();
   }
-  xd.release();
-  ed.release();
-  nb.release();
-  nid.release();
   if (slot == 0) CHK(find_hot_bins(E));
   if (codes_out) return bsscl_get_codes(E, slot, codes_out);
+  return BSSCL_OK;
+}
+
+int bsscl_stage_features(bsscl_engine *E, const void *X, int32_t x_is_f64, int64_t n,
+                         int32_t F) {
+  if (!E || !X) return set_error(BSSCL_EINVAL, "stage_features: null argument");
+  if (n <= 0 || n > INT32_MAX || F <= 0)
+    return set_error(BSSCL_EINVAL, "stage_features: bad shape");
+  HIPCHK(hipSetDevice(E->device));
+  E->cols_sorted = false;
+  E->col_keys.release();
+  E->col_m.clear();
+  const size_t bytes = (size_t)n * F * (x_is_f64 ? 8 : 4);
+  CHK(E->xstage.ensure(bytes));
+  E->xs_n = 0;
+  HIPCHK(hipMemcpyAsync(E->xstage.p, X, bytes, hipMemcpyHostToDevice, E->st));
+  HIPCHK(hipStreamSynchronize(E->st));
+  E->xs_n = n;
+  E->xs_F = F;
+  E->xs_f64 = x_is_f64 ? 1 : 0;
+  return BSSCL_OK;
+}
+
+int bsscl_sort_columns(bsscl_engine *E, int64_t *nan_count, int64_t *n_unique) {
+  if (!E || !nan_count || !n_unique) return set_error(BSSCL_EINVAL, "sort_columns: null argument");
+  if (!E->xstage.p || E->xs_n <= 0)
+    return set_error(BSSCL_EINVAL, "sort_columns: no staged matrix (call bsscl_stage_features)");
+  HIPCHK(hipSetDevice(E->device));
+  const int64_t n = E->xs_n;
+  const int32_t F = E->xs_F;
+  const int f64 = E->xs_f64;
+  const int64_t ld = col_sort_ld(n, f64);
+  const size_t ksz = f64 ? 8 : 4;
+  E->cols_sorted = false;
+  CHK(E->col_keys.ensure((size_t)F * ld * ksz));
+  DevBuf<unsigned char> tmp;
+  DevBuf<uint32_t> counts, totals;
+  DevBuf<int64_t> m_d;
+  DevBuf<unsigned long long> changes_d;
+  int rc = tmp.ensure((size_t)F * ld * ksz);
+  if (rc == BSSCL_OK) rc = counts.ensure((size_t)col_sort_count_words(n, F, f64));
+  if (rc == BSSCL_OK) rc = totals.ensure((size_t)F * 256);
+  if (rc == BSSCL_OK) rc = m_d.ensure((size_t)F);
+  if (rc == BSSCL_OK) rc = changes_d.ensure((size_t)F);
+  if (rc != BSSCL_OK) return rc;
+  std::vector<int64_t> m(F);
+  std::vector<unsigned long long> changes(F);
+  hipError_t e = launch_col_sort(E->st, E->xstage.p, f64, n, F, E->col_keys.p, tmp.p, ld,
+                                 counts.p, totals.p, m_d.p);
+  if (e == hipSuccess) e = hipMemsetAsync(changes_d.p, 0, (size_t)F * 8, E->st);
+  if (e == hipSuccess)
+    e = launch_col_changes(E->st, E->col_keys.p, f64, ld, F, m_d.p, n, changes_d.p);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(m.data(), m_d.p, (size_t)F * 8, hipMemcpyDeviceToHost, E->st);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(changes.data(), changes_d.p, (size_t)F * 8, hipMemcpyDeviceToHost, E->st);
+  if (e == hipSuccess) e = hipStreamSynchronize(E->st);
+  if (e != hipSuccess)
+    return set_error(BSSCL_EDEVICE, std::string("sort_columns: ") + hipGetErrorString(e));
+  for (int32_t j = 0; j < F; ++j) {
+    if (m[j] < 0 || m[j] > n) return set_error(BSSCL_EINTERNAL, "sort_columns: bad count");
+    nan_count[j] = n - m[j];
+    n_unique[j] = m[j] > 0 ? 1 + (int64_t)changes[j] : 0;
+  }
+  E->col_ld = ld;
+  E->col_m = m;
+  E->cols_sorted = true;
+  return BSSCL_OK;
+}
+
+int bsscl_sorted_gather(bsscl_engine *E, int64_t count, const int32_t *col, const int64_t *pos,
+                        double *out) {
+  if (!E || (count > 0 && (!col || !pos || !out)))
+    return set_error(BSSCL_EINVAL, "sorted_gather: null argument");
+  if (!E->cols_sorted) return set_error(BSSCL_EINVAL, "sorted_gather: columns are not sorted");
+  if (count <= 0) return BSSCL_OK;
+  for (int64_t k = 0; k < count; ++k) {
+    if (col[k] < 0 || col[k] >= E->xs_F || pos[k] < 0 || pos[k] >= E->col_m[col[k]])
+      return set_error(BSSCL_EINVAL, "sorted_gather: position outside the column's values");
+  }
+  HIPCHK(hipSetDevice(E->device));
+  DevBuf<int32_t> c_d;
+  DevBuf<int64_t> p_d;
+  DevBuf<double> o_d;
+  CHK(c_d.ensure((size_t)count));
+  CHK(p_d.ensure((size_t)count));
+  CHK(o_d.ensure((size_t)count));
+  hipError_t e = hipMemcpyAsync(c_d.p, col, (size_t)count * 4, hipMemcpyHostToDevice, E->st);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(p_d.p, pos, (size_t)count * 8, hipMemcpyHostToDevice, E->st);
+  if (e == hipSuccess)
+    e = launch_col_gather(E->st, E->col_keys.p, E->xs_f64, E->col_ld, count, c_d.p, p_d.p, o_d.p);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(out, o_d.p, (size_t)count * 8, hipMemcpyDeviceToHost, E->st);
+  if (e == hipSuccess) e = hipStreamSynchronize(E->st);
+  if (e != hipSuccess)
+    return set_error(BSSCL_EDEVICE, std::string("sorted_gather: ") + hipGetErrorString(e));
+  return BSSCL_OK;
+}
+
+int bsscl_sorted_uniques(bsscl_engine *E, int32_t col, int32_t max_out, double *out,
+                         int32_t *count) {
+  if (!E || !count || (max_out > 0 && !out))
+    return set_error(BSSCL_EINVAL, "sorted_uniques: null argument");
+  if (!E->cols_sorted) return set_error(BSSCL_EINVAL, "sorted_uniques: columns are not sorted");
+  if (col < 0 || col >= E->xs_F) return set_error(BSSCL_EINVAL, "sorted_uniques: bad column");
+  if (max_out < 0) return set_error(BSSCL_EINVAL, "sorted_uniques: max_out < 0");
+  const int64_t m = E->col_m[col];
+  *count = 0;
+  if (m == 0) return BSSCL_OK;
+  HIPCHK(hipSetDevice(E->device));
+  DevBuf<int64_t> p_d;
+  DevBuf<unsigned int> cnt_d;
+  CHK(p_d.ensure((size_t)std::max(max_out, 1)));
+  CHK(cnt_d.ensure(1));
+  unsigned int cnt = 0;
+  hipError_t e = hipMemsetAsync(cnt_d.p, 0, 4, E->st);
+  if (e == hipSuccess)
+    e = launch_col_run_starts(E->st, E->col_keys.p, E->xs_f64, E->col_ld, col, m, max_out,
+                              p_d.p, cnt_d.p);
+  if (e == hipSuccess) e = hipMemcpyAsync(&cnt, cnt_d.p, 4, hipMemcpyDeviceToHost, E->st);
+  if (e == hipSuccess) e = hipStreamSynchronize(E->st);
+  if (e != hipSuccess)
+    return set_error(BSSCL_EDEVICE, std::string("sorted_uniques: ") + hipGetErrorString(e));
+  if ((int64_t)cnt > (int64_t)max_out)
+    return set_error(BSSCL_EINVAL, "sorted_uniques: the column has more than max_out values");
+  std::vector<int64_t> pos(cnt);
+  if (cnt) {
+    HIPCHK(hipMemcpy(pos.data(), p_d.p, (size_t)cnt * 8, hipMemcpyDeviceToHost));
+    std::sort(pos.begin(), pos.end());
+    std::vector<int32_t> cols(cnt, col);
+    CHK(bsscl_sorted_gather(E, cnt, cols.data(), pos.data(), out));
+  }
+  *count = (int32_t)cnt;
+  return BSSCL_OK;
+}
+
+int bsscl_release_staged(bsscl_engine *E) {
+  if (!E) return set_error(BSSCL_EINVAL, "release_staged: null engine");
+  HIPCHK(hipSetDevice(E->device));
+  HIPCHK(hipStreamSynchronize(E->st));
+  E->xstage.release();
+  E->xs_n = 0;
+  E->col_keys.release();
+  E->cols_sorted = false;
+  E->col_m.clear();
   return BSSCL_OK;
 }
 

@@ -284,4 +284,26 @@ hipError_t launch_predict(hipStream_t st, const uint8_t *codes, int64_t ld,
 
 int update_F_blocks(int64_t n);
 
+// Column sort for the bin edges (colsort.hip).  Keys are stored
+// feature-major [F][ld] with ld = col_sort_ld(n, is_f64); counts holds
+// col_sort_count_words(...) words and totals F * 256 words; keys and tmp
+// hold F * ld keys of 4 (float32) or 8 (float64) bytes.  Afterwards keys
+// holds every column sorted (NaNs last) and m[col] its non-NaN count.
+int64_t col_sort_ld(int64_t n, int is_f64);
+int64_t col_sort_count_words(int64_t n, int32_t F, int is_f64);
+hipError_t launch_col_sort(hipStream_t st, const void *X, int is_f64, int64_t n, int32_t F,
+                           void *keys, void *tmp, int64_t ld, uint32_t *counts,
+                           uint32_t *totals, int64_t *m);
+// out[col] += number of adjacent unequal pairs in the first m[col] keys.
+hipError_t launch_col_changes(hipStream_t st, const void *keys, int is_f64, int64_t ld, int32_t F,
+                              const int64_t *m, int64_t max_m, unsigned long long *out);
+// First position of every run of equal keys among the first m keys of
+// column col (unordered, at most max_out stored); *count = number of runs.
+hipError_t launch_col_run_starts(hipStream_t st, const void *keys, int is_f64, int64_t ld,
+                                 int32_t col, int64_t m, int32_t max_out, int64_t *pos,
+                                 unsigned int *count);
+// out[k] = value at position pos[k] of sorted column col[k], as float64.
+hipError_t launch_col_gather(hipStream_t st, const void *keys, int is_f64, int64_t ld,
+                             int64_t count, const int32_t *col, const int64_t *pos, double *out);
+
 }  // namespace bsscl

@@ -51,6 +51,7 @@ void bsscl_engine_destroy(bsscl_engine *eng);
  *   X          row-major n x F, float32 (x_is_f64 = 0) or float64
  *   edges_2d   row-major F x edge_stride float64 (the reference's bin_edges)
  *   bin_counts int32[F], nan_bin_id int32[F]
+ * X may be NULL to bin the matrix staged by bsscl_stage_features (below).
  * The codes stay on the device as matrix `slot` (0 = training, 1 = scoring),
  * stored feature-major as uint8.  Reference codes above 255 (possible only
  * with n_bins = 256, for the top bin of a NaN feature) are stored as 255,
@@ -70,6 +71,41 @@ int bsscl_load_codes(bsscl_engine *eng, int32_t slot, const void *codes,
 
 /* Copy matrix `slot` back row-major (n x F uint8). */
 int bsscl_get_codes(bsscl_engine *eng, int32_t slot, uint8_t *codes_out);
+
+/*
+ * Bin edges on the device.  Replace the data passes of _build_bin_edges
+ * (est:2073-2141): np.isnan (est:2092-2093), np.unique (est:2107, 2111) and
+ * the partition inside np.percentile (est:2126).  The caller keeps the
+ * reference's host arithmetic: the branch on the number of distinct values,
+ * np.linspace, the percentile interpolation between the order statistics
+ * returned here, np.unique of the result and the appended last edge.
+ *
+ * bsscl_stage_features copies X (row-major n x F, float32 or float64) to the
+ * device, where it stays until bsscl_release_staged or the next staging.
+ * bsscl_bin_features with X = NULL then bins the staged matrix (same n, F
+ * and dtype) without a second upload.
+ *
+ * bsscl_sort_columns sorts every staged column on the device with its NaNs
+ * removed and returns, per column, the number of NaNs and the number of
+ * distinct non-NaN values (np.unique semantics: -0.0 and +0.0 are one value,
+ * and it is returned as +0.0).  The sorted columns stay on the device.
+ *
+ * bsscl_sorted_gather returns out[k] = the value of rank pos[k] (0-based,
+ * ascending, NaNs excluded) of column col[k], as float64 (exact for float32
+ * columns); every pos[k] must be below the column's non-NaN count.
+ *
+ * bsscl_sorted_uniques returns the distinct values of column col in
+ * ascending order (the reference's np.unique(col_clean)); fails when there
+ * are more than max_out.
+ */
+int bsscl_stage_features(bsscl_engine *eng, const void *X, int32_t x_is_f64,
+                         int64_t n, int32_t F);
+int bsscl_sort_columns(bsscl_engine *eng, int64_t *nan_count, int64_t *n_unique);
+int bsscl_sorted_gather(bsscl_engine *eng, int64_t count, const int32_t *col,
+                        const int64_t *pos, double *out);
+int bsscl_sorted_uniques(bsscl_engine *eng, int32_t col, int32_t max_out,
+                         double *out, int32_t *count);
+int bsscl_release_staged(bsscl_engine *eng);
 
 /*
  * Tree builder.  Replaces _build_tree_leafwise (est:517-823) and the no-op
