@@ -713,6 +713,124 @@ class HybridHistGBMNumbaV1_0_1:
                 f"max_depth='{self.max_depth_init}', subsample={self.subsample}, "
                 f"colsample_bytree={self.colsample_bytree})")
 
+    # ------------------------------------------------------------------
+    # est:4035-4205: JSON model format
+    # ------------------------------------------------------------------
+    @staticmethod
+    def _tree_to_json(tree):
+        return {
+            'features': np.asarray(tree[0]).tolist(),
+            'thresholds': np.asarray(tree[1]).tolist(),
+            'values': np.asarray(tree[2]).tolist(),
+            'left': np.asarray(tree[3]).tolist(),
+            'right': np.asarray(tree[4]).tolist(),
+            'node_count': int(tree[5]),
+            'split_gains': np.asarray(tree[6]).tolist() if len(tree) > 6 else [],
+        }
+
+    @staticmethod
+    def _tree_from_json(td):
+        # As the reference reads it: thresholds come back as float64 (the
+        # packed arrays convert them to int64 again), and a missing
+        # split_gains list becomes zeros.
+        sg = np.array(td.get('split_gains', [0.0] * td['node_count']), dtype=np.float64)
+        return (np.array(td['features'], dtype=np.int32),
+                np.array(td['thresholds'], dtype=np.float64),
+                np.array(td['values'], dtype=np.float64),
+                np.array(td['left'], dtype=np.int32),
+                np.array(td['right'], dtype=np.int32),
+                td['node_count'],
+                sg)
+
+    def save_model(self, filepath):
+        """Writes the model as JSON in the reference's layout (est:4035-4115)."""
+        import json
+        model_data = {
+            'version': '1.2.2',
+            'params': {},
+            'n_classes_': int(self.n_classes_),
+            'classes_': self.classes_.tolist() if self.classes_ is not None else None,
+            'n_features_in_': int(self.n_features_in_) if self.n_features_in_ is not None else None,
+            'objective': self.objective,
+            '_is_multiclass': self._is_multiclass,
+            'init_score_': float(self.init_score_),
+            'base_score_': float(getattr(self, 'base_score_', 0.0)),
+            'n_trees_fitted_': int(self.n_trees_fitted_),
+            'best_iteration_': int(self.best_iteration_),
+            'train_loss_history_': [float(x) for x in self.train_loss_history_],
+            'val_loss_history_': [float(x) for x in self.val_loss_history_],
+            '_max_bins': int(self._max_bins),
+        }
+        for k, v in self.get_params().items():
+            if callable(v):
+                continue
+            model_data['params'][k] = v
+        if self.bin_edges is not None:
+            model_data['bin_edges'] = self.bin_edges.tolist()
+        if self.feature_bin_counts is not None:
+            model_data['feature_bin_counts'] = self.feature_bin_counts.tolist()
+        if not self._is_multiclass:
+            model_data['trees'] = [self._tree_to_json(t) for t in self.trees]
+        else:
+            model_data['mc_trees'] = [[self._tree_to_json(t) for t in k_trees]
+                                      for k_trees in self.mc_trees]
+        if self.feature_importances_ is not None:
+            model_data['feature_importances_'] = self.feature_importances_.tolist()
+        if self.feature_split_counts_ is not None:
+            model_data['feature_split_counts_'] = self.feature_split_counts_.tolist()
+        model_data['_categorical_set'] = list(self._categorical_set)
+        if self._is_categorical is not None:
+            model_data['_is_categorical'] = self._is_categorical.tolist()
+        with open(filepath, 'w') as f:
+            json.dump(model_data, f)
+
+    @classmethod
+    def load_model(cls, filepath):
+        """Reads a model written by save_model (est:4117-4205).
+
+        As in the reference, the NaN-bin map is not stored: every feature is
+        treated as having had no NaN in training (est:4200-4202), so a model
+        trained on NaN features scores NaN inputs differently after a reload.
+        """
+        import json
+        with open(filepath, 'r') as f:
+            data = json.load(f)
+        model = cls(**data['params'])
+        model.n_classes_ = data['n_classes_']
+        model.classes_ = np.array(data['classes_']) if data['classes_'] is not None else None
+        model.n_features_in_ = data['n_features_in_']
+        model.objective = data['objective']
+        model._is_multiclass = data['_is_multiclass']
+        model.init_score_ = data['init_score_']
+        model.base_score_ = data.get('base_score_', 0.0)
+        model.n_trees_fitted_ = data['n_trees_fitted_']
+        model.best_iteration_ = data['best_iteration_']
+        model.train_loss_history_ = data['train_loss_history_']
+        model.val_loss_history_ = data['val_loss_history_']
+        model._max_bins = data['_max_bins']
+        if 'bin_edges' in data:
+            model.bin_edges = np.array(data['bin_edges'], dtype=np.float64)
+        if 'feature_bin_counts' in data:
+            model.feature_bin_counts = np.array(data['feature_bin_counts'], dtype=np.int32)
+        if 'trees' in data:
+            model.trees = [cls._tree_from_json(td) for td in data['trees']]
+        if 'mc_trees' in data:
+            model.mc_trees = [[cls._tree_from_json(td) for td in class_trees]
+                              for class_trees in data['mc_trees']]
+        if 'feature_importances_' in data:
+            model.feature_importances_ = np.array(data['feature_importances_'])
+        if 'feature_split_counts_' in data:
+            model.feature_split_counts_ = np.array(data['feature_split_counts_'])
+        model._categorical_set = set(data.get('_categorical_set', []))
+        if '_is_categorical' in data and data['_is_categorical'] is not None:
+            model._is_categorical = np.array(data['_is_categorical'], dtype=np.bool_)
+        model.binning_strategy = (model.binning_strategy_init
+                                  if model.binning_strategy_init != 'auto' else 'standard')
+        if model.n_features_in_ is not None:
+            model._nan_bin_id = np.full(model.n_features_in_, -1, dtype=np.int32)
+        model._pack_trees()
+        return model
+
     def warmup(self, n_features=None):
         """The reference compiles its Numba kernels here (est:3807); the HIP
         kernels are compiled ahead of time, so this only opens the device."""
