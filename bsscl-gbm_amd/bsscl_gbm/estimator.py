@@ -12,10 +12,11 @@ resolution, bin edges, class weights, base score, the random stream) is the
 reference's NumPy code path; every per-row loop (binning, gradients, trees,
 F updates, prediction) runs in libbsscl_hip.so.
 
-Covered: binary classification (two classes, objective 'auto' or 'binary'),
-grow_policy='leaf', sampling_method='uniform', boosting_type='gbdt', numeric
-features with NaN, class_weight None/'balanced'/'balanced_sqrt',
-scale_pos_weight, eval_set with early stopping.  Other modes of the
+Covered: binary and multiclass (softmax, K trees per round) classification
+(objective 'auto' or 'binary'), grow_policy='leaf', sampling_method='uniform',
+boosting_type='gbdt', numeric features with NaN, class_weight
+None/'balanced'/'balanced_sqrt', scale_pos_weight, eval_set with early
+stopping, JSON save_model/load_model.  Other modes of the
 reference raise NotImplementedError instead of computing something else.
 """
 from __future__ import annotations
@@ -214,7 +215,7 @@ class HybridHistGBMNumbaV1_0_1:
             unsupported.append("custom_objective")
         if unsupported:
             raise NotImplementedError(
-                "the MI355X engine covers the binary leaf-wise histogram path; "
+                "the MI355X engine covers the leaf-wise histogram path for classification; "
                 "not supported: " + ", ".join(unsupported))
 
     # ------------------------------------------------------------------
@@ -459,11 +460,12 @@ class HybridHistGBMNumbaV1_0_1:
         self.classes_ = np.unique(y)
         self.n_classes_ = len(self.classes_)
         self._is_multiclass = self.n_classes_ > 2
-        if self.n_classes_ != 2:
+        if self.n_classes_ < 2:
             raise NotImplementedError(
-                "the MI355X engine covers binary classification; got "
-                f"{self.n_classes_} classes")
-        y = (y == self.classes_[1]).astype(np.int64)
+                "the MI355X engine needs at least two classes; got "
+                f"{self.n_classes_}")
+        # est:3124-3129: labels become 0 .. K-1.
+        y = np.searchsorted(self.classes_, y).astype(np.int64)
         if y_val is not None:
             y_val = np.asarray(y_val)
             label_map = {c: i for i, c in enumerate(self.classes_)}
@@ -522,7 +524,10 @@ class HybridHistGBMNumbaV1_0_1:
             n_val = X_val.shape[0]
 
         t0_train = time.perf_counter()
-        self._fit_binary(eng, y, n_val, y_val, rng)
+        if self._is_multiclass:
+            self._fit_multiclass(eng, y, n_val, y_val, rng)
+        else:
+            self._fit_binary(eng, y, n_val, y_val, rng)
         self.times['training'] = (time.perf_counter() - t0_train) * 1000
 
         self._pack_trees()
@@ -603,6 +608,117 @@ class HybridHistGBMNumbaV1_0_1:
         self.n_trees_fitted_ = len(self.trees)
 
     # ------------------------------------------------------------------
+    # est:2949-3065 (multiclass softmax) and its helpers est:2327-2341
+    # ------------------------------------------------------------------
+    @staticmethod
+    def _softmax(F):
+        F_shifted = F - F.max(axis=1, keepdims=True)
+        exp_F = np.exp(F_shifted)
+        return exp_F / exp_F.sum(axis=1, keepdims=True)
+
+    @staticmethod
+    def _compute_multiclass_logloss(y_onehot, F):
+        F_shifted = F - F.max(axis=1, keepdims=True)
+        exp_F = np.exp(F_shifted)
+        proba = exp_F / exp_F.sum(axis=1, keepdims=True)
+        proba = np.clip(proba, 1e-15, 1 - 1e-15)
+        return -np.mean(np.sum(y_onehot * np.log(proba), axis=1))
+
+    def _class_weight_vector(self, y):
+        """sample_weight of est:2570-2603 for K classes."""
+        n = len(y)
+        if self.scale_pos_weight is not None and self.objective == 'binary':
+            w = np.ones(n, dtype=np.float64)
+            w[y == 1] = self.scale_pos_weight
+            return w
+        w = np.ones(n, dtype=np.float64)
+        if self.class_weight not in ('balanced', 'balanced_sqrt'):
+            return w
+        K = self.n_classes_
+        for k in range(K):
+            n_k = np.sum(y == k)
+            w_k = n / (K * max(n_k, 1))
+            if self.class_weight == 'balanced_sqrt':
+                w_k = w_k ** 0.35
+            w[y == k] = w_k
+        return w
+
+    def _fit_multiclass(self, eng, y, n_val, y_val, rng):
+        """K trees per round from softmax gradients (est:2949-3065).  The
+        host keeps the reference's NumPy arithmetic on the (n, K) scores;
+        every tree is built and applied to all rows on the device."""
+        n_samples = len(y)
+        n_features = self.n_features_in_
+        K = self.n_classes_
+        y_onehot = np.eye(K, dtype=np.float64)[y]
+        F_train = np.zeros((n_samples, K), dtype=np.float64)
+        F_val = None
+        y_val_onehot = None
+        if n_val:
+            F_val = np.zeros((n_val, K), dtype=np.float64)
+            y_val_onehot = np.eye(K, dtype=np.float64)[y_val]
+        n_sub = max(1, int(n_samples * self.subsample))
+        f_sub = max(1, int(n_features * self.colsample_bytree))
+        do_rows = self.subsample < 1.0
+        do_feats = self.colsample_bytree < 1.0
+        sample_weight = self._class_weight_vector(y)
+        self.mc_trees = [[] for _ in range(K)]
+        best_val_loss = np.inf
+        rounds_no_improve = 0
+        # The reference's rng.shuffle stream (est:2502-2517), one draw per
+        # round shared by the K trees; rows come back in the reference's order.
+        sampler = _native.Sampler(rng.get_state(), n_samples,
+                                  n_sub if do_rows else n_samples, do_rows,
+                                  n_features, f_sub if do_feats else n_features,
+                                  do_feats, int(self.n_estimators), device=eng.device)
+        try:
+            for m in range(self.n_estimators):
+                proba = self._softmax(F_train)
+                sample_idx, feat_idx = sampler.next()
+                grad_all = sample_weight[:, None] * (proba - y_onehot)
+                hess_all = sample_weight[:, None] * proba * (1.0 - proba)
+                for k in range(K):
+                    grad_k = np.ascontiguousarray(grad_all[:, k])
+                    hess_k = np.maximum(np.ascontiguousarray(hess_all[:, k]), 1e-8)
+                    tree = eng.build_tree(grad_k, hess_k, sample_idx, feat_idx,
+                                          self.max_leaves, self.max_depth,
+                                          self.min_samples_leaf, self.min_child_weight,
+                                          self.feature_bin_counts, self._max_bins,
+                                          self.reg_lambda, self.gamma)
+                    self.mc_trees[k].append(tree)
+                    F_train[:, k] += self.learning_rate * eng.predict_tree(0, n_samples, tree)
+                    if F_val is not None:
+                        F_val[:, k] += self.learning_rate * eng.predict_tree(1, n_val, tree)
+                train_loss = self._compute_multiclass_logloss(y_onehot, F_train)
+                self.train_loss_history_.append(train_loss)
+                val_loss = None
+                if F_val is not None:
+                    val_loss = self._compute_multiclass_logloss(y_val_onehot, F_val)
+                    self.val_loss_history_.append(val_loss)
+                if self.verbose and ((m + 1) % 20 == 0 or m == 0):
+                    msg = (f"  ✓ Round {m+1:>3}/{self.n_estimators}  |  {K} trees  |  "
+                           f"train-loss: {train_loss:.6f}")
+                    if val_loss is not None:
+                        msg += f"  |  val-loss: {val_loss:.6f}"
+                    print(msg)
+                if self.early_stopping_rounds is not None and val_loss is not None:
+                    if val_loss < best_val_loss:
+                        best_val_loss = val_loss
+                        self.best_iteration_ = m
+                        rounds_no_improve = 0
+                    else:
+                        rounds_no_improve += 1
+                        if rounds_no_improve >= self.early_stopping_rounds:
+                            if self.verbose:
+                                print(f"\n  ⏹ Early stopping at round {m+1} (best: {self.best_iteration_+1})")
+                            for k in range(K):
+                                self.mc_trees[k] = self.mc_trees[k][:self.best_iteration_ + 1]
+                            break
+        finally:
+            sampler.close()
+        self.n_trees_fitted_ = sum(len(t) for t in self.mc_trees)
+
+    # ------------------------------------------------------------------
     # est:2192-2236, est:2343-2363
     # ------------------------------------------------------------------
     def _pack_tree_list(self, tree_list):
@@ -628,6 +744,10 @@ class HybridHistGBMNumbaV1_0_1:
                 'offsets': offsets}
 
     def _pack_trees(self):
+        if self._is_multiclass:
+            self._mc_packed = [self._pack_tree_list(t) if len(t) > 0 else None
+                               for t in self.mc_trees]
+            return
         packed = self._pack_tree_list(self.trees)
         self._packed_features = packed['features']
         self._packed_thresholds = packed['thresholds']
@@ -639,12 +759,14 @@ class HybridHistGBMNumbaV1_0_1:
     def _compute_feature_importances(self):
         gain_imp = np.zeros(self.n_features_in_, dtype=np.float64)
         split_cnt = np.zeros(self.n_features_in_, dtype=np.int64)
-        for tf, tt, tv, tl, tr, nc, sg in self.trees:
-            for node_idx in range(nc):
-                feat = tf[node_idx]
-                if feat >= 0:
-                    gain_imp[feat] += sg[node_idx]
-                    split_cnt[feat] += 1
+        tree_lists = self.mc_trees if self._is_multiclass else [self.trees]
+        for trees in tree_lists:
+            for tf, tt, tv, tl, tr, nc, sg in trees:
+                for node_idx in range(nc):
+                    feat = tf[node_idx]
+                    if feat >= 0:
+                        gain_imp[feat] += sg[node_idx]
+                        split_cnt[feat] += 1
         total = gain_imp.sum()
         self.feature_importances_ = gain_imp / total if total > 0 else np.zeros(self.n_features_in_)
         self.feature_split_counts_ = split_cnt
@@ -663,6 +785,15 @@ class HybridHistGBMNumbaV1_0_1:
         eng = _engine(self._device_index())
         eng.bin_features(1, X, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
         t0 = time.perf_counter()
+        if self._is_multiclass:
+            # est:3293-3315: per class, sum its trees from 0.0.
+            F = np.zeros((X.shape[0], self.n_classes_), dtype=np.float64)
+            for k in range(self.n_classes_):
+                if self._mc_packed[k] is not None:
+                    F[:, k] = eng.predict(1, X.shape[0], self._mc_packed[k],
+                                          len(self.mc_trees[k]), self.learning_rate)
+            self.times['inference'] = (time.perf_counter() - t0) * 1000
+            return F
         packed = {'features': self._packed_features, 'thresholds': self._packed_thresholds,
                   'values': self._packed_values, 'left': self._packed_left,
                   'right': self._packed_right, 'offsets': self._tree_offsets}
@@ -673,11 +804,15 @@ class HybridHistGBMNumbaV1_0_1:
 
     def predict_proba(self, X):
         F = self._raw_score(X)
+        if self._is_multiclass:
+            return self._softmax(F)
         proba = _sigmoid(F)
         return np.column_stack([1 - proba, proba])
 
     def predict(self, X):
         proba = self.predict_proba(X)
+        if self._is_multiclass:
+            return self.classes_[np.argmax(proba, axis=1)]
         return self.classes_[(proba[:, 1] > 0.5).astype(int)]
 
     # ------------------------------------------------------------------

@@ -262,15 +262,18 @@ class OracleGBM:
         self.train_loss_history_ = []
 
     def _adaptive(self, X):
-        """est:1925-2029 (K = 2)."""
+        """est:1925-2029 (K = number of classes)."""
         n, p = X.shape
-        K = 2
+        K = getattr(self, "n_classes_", 2)
         if self.binning_strategy_init == "auto":
             self.binning_strategy = "hybrid" if (n > 20000 or p > 40) else "standard"
         else:
             self.binning_strategy = self.binning_strategy_init
         if self.max_depth_init == "auto":
-            self.max_depth = min(6, max(3, int(np.log2(max(n // 10, 8)))))
+            if K > 10:
+                self.max_depth = min(8, max(4, int(np.log2(max(n // 8, 8)))))
+            else:
+                self.max_depth = min(6, max(3, int(np.log2(max(n // 10, 8)))))
         if self.learning_rate_init == "auto":
             # The reference computes np.std(X) unconditionally; its value is
             # only read when n <= 20000.
@@ -287,10 +290,21 @@ class OracleGBM:
                 self.learning_rate = 0.18
             else:
                 self.learning_rate = 0.20
+            if K > 10:
+                self.learning_rate *= 0.75
+            elif K > 6:
+                self.learning_rate *= 0.85
         if self.n_bins_init == "auto":
             self.n_bins = min(256, p * 8 + 32)
         if self.n_estimators_init == "auto":
-            self.n_estimators = 150 if K <= 2 else self.n_estimators
+            if K <= 2:
+                self.n_estimators = 150
+            elif K <= 6:
+                self.n_estimators = max(150, min(300, n // 10))
+            elif K <= 15:
+                self.n_estimators = max(200, min(400, n // 8))
+            else:
+                self.n_estimators = max(250, min(500, n // 6))
         if self.gamma_init == "auto":
             self.gamma = 0.0
         if self.min_child_weight_init == "auto":
@@ -306,12 +320,13 @@ class OracleGBM:
     def _class_weights(self, y):
         """est:2570-2603 (no scale_pos_weight)."""
         n = len(y)
+        K = getattr(self, "n_classes_", 2)
         if self.class_weight not in ("balanced", "balanced_sqrt"):
             return np.ones(n, dtype=np.float64)
         w = np.ones(n, dtype=np.float64)
-        for k in range(2):
+        for k in range(K):
             n_k = np.sum(y == k)
-            w_k = n / (2 * max(n_k, 1))
+            w_k = n / (K * max(n_k, 1))
             if self.class_weight == "balanced_sqrt":
                 w_k = w_k ** 0.35
             w[y == k] = w_k
@@ -323,7 +338,9 @@ class OracleGBM:
         ``round_callback(m, grad, hess, sample_idx, feat_idx, tree)`` sees
         each round's tree-builder inputs and output."""
         self.classes_ = np.unique(y)
-        assert len(self.classes_) == 2, "oracle covers binary classification"
+        self.n_classes_ = len(self.classes_)
+        assert self.n_classes_ >= 2, "oracle covers classification with 2+ classes"
+        self._is_multiclass = self.n_classes_ > 2
         label_map = {c: i for i, c in enumerate(self.classes_)}
         y = np.array([label_map[v] for v in y], dtype=np.int64)
         self.trees = []
@@ -340,6 +357,8 @@ class OracleGBM:
                              self._nan_bin_id, self.binning_strategy)
         self.X_bin_ = X_bin
 
+        if self._is_multiclass:
+            return self._fit_multiclass(X_bin, y, rng, max_rounds, round_callback)
         n = len(y)
         F_cnt = X_bin.shape[1]
         w_init = self._class_weights(y)
@@ -387,16 +406,92 @@ class OracleGBM:
         self._packed = pack_trees(self.trees)
         return self
 
+    @staticmethod
+    def _softmax(F):
+        """est:2327-2332."""
+        F_shifted = F - F.max(axis=1, keepdims=True)
+        exp_F = np.exp(F_shifted)
+        return exp_F / exp_F.sum(axis=1, keepdims=True)
+
+    @staticmethod
+    def _multiclass_logloss(y_onehot, F):
+        """est:2334-2341."""
+        F_shifted = F - F.max(axis=1, keepdims=True)
+        exp_F = np.exp(F_shifted)
+        proba = exp_F / exp_F.sum(axis=1, keepdims=True)
+        proba = np.clip(proba, 1e-15, 1 - 1e-15)
+        return -np.mean(np.sum(y_onehot * np.log(proba), axis=1))
+
+    def _fit_multiclass(self, X_bin, y, rng, max_rounds, round_callback):
+        """est:2949-3065 (gbdt, uniform sampling, no eval set): K trees per
+        round from softmax gradients, one bagging draw shared by the K trees.
+        ``round_callback(m, k, grad, hess, sample_idx, feat_idx, tree)``."""
+        n = len(y)
+        F_cnt = X_bin.shape[1]
+        K = self.n_classes_
+        y_onehot = np.eye(K, dtype=np.float64)[y]
+        F_train = np.zeros((n, K), dtype=np.float64)
+        n_sub = max(1, int(n * self.subsample))
+        f_sub = max(1, int(F_cnt * self.colsample_bytree))
+        sample_weight = self._class_weights(y)
+        self.mc_trees = [[] for _ in range(K)]
+        all_rows = np.arange(n, dtype=np.int64)
+        all_feats = np.arange(F_cnt, dtype=np.int32)
+        rounds = self.n_estimators if max_rounds is None else min(max_rounds, self.n_estimators)
+        import time as _time
+        self.round_times_ = [_time.perf_counter()]
+        for m in range(rounds):
+            proba = self._softmax(F_train)
+            if self.subsample < 1.0:
+                rng.shuffle(all_rows)
+                sample_idx = all_rows[:n_sub].copy()
+            else:
+                sample_idx = all_rows.copy()
+            if self.colsample_bytree < 1.0:
+                rng.shuffle(all_feats)
+                feat_idx = np.sort(all_feats[:f_sub]).copy()
+            else:
+                feat_idx = all_feats.copy()
+            grad_all = sample_weight[:, None] * (proba - y_onehot)
+            hess_all = sample_weight[:, None] * proba * (1.0 - proba)
+            for k in range(K):
+                grad_k = np.ascontiguousarray(grad_all[:, k])
+                hess_k = np.maximum(np.ascontiguousarray(hess_all[:, k]), 1e-8)
+                tree = build_tree(X_bin, grad_k, hess_k, sample_idx, feat_idx,
+                                  self.max_leaves, self.max_depth,
+                                  self.min_samples_leaf, self.min_child_weight,
+                                  self.feature_bin_counts, self._max_bins,
+                                  self.reg_lambda, self.gamma)
+                if round_callback is not None:
+                    round_callback(m, k, grad_k, hess_k, sample_idx, feat_idx, tree)
+                self.mc_trees[k].append(tree)
+                F_train[:, k] += self.learning_rate * predict_tree(X_bin, tree)
+            self.train_loss_history_.append(self._multiclass_logloss(y_onehot, F_train))
+            self.round_times_.append(_time.perf_counter())
+        self.F_train_ = F_train
+        self._mc_packed = [pack_trees(t) for t in self.mc_trees]
+        return self
+
     def predict_proba(self, X):
         """est:3274-3336."""
         if not np.issubdtype(X.dtype, np.floating) or X.dtype == np.float16:
             X = X.astype(np.float64)
         X_bin = bin_features(X, self.bin_edges, self.feature_bin_counts,
                              self._nan_bin_id, self.binning_strategy)
+        if self._is_multiclass:
+            F = np.zeros((len(X), self.n_classes_), dtype=np.float64)
+            for k in range(self.n_classes_):
+                F[:, k] = predict_all_trees(X_bin, self._mc_packed[k], len(self.mc_trees[k]),
+                                            self.learning_rate)
+            return self._softmax(F)
         F = predict_all_trees(X_bin, self._packed, len(self.trees),
                               self.learning_rate) + self.base_score_
         proba = 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
         return np.column_stack([1 - proba, proba])
 
     def predict(self, X):
-        return self.classes_[(self.predict_proba(X)[:, 1] > 0.5).astype(int)]
+        """est:3345-3368."""
+        proba = self.predict_proba(X)
+        if self._is_multiclass:
+            return self.classes_[np.argmax(proba, axis=1)]
+        return self.classes_[(proba[:, 1] > 0.5).astype(int)]

@@ -60,9 +60,9 @@ def test_modes_outside_the_engine_raise(kw):
         HybridHistGBMNumbaV1_0_1(verbose=False, **kw).fit(X, y)
 
 
-def test_multiclass_raises():
+def test_single_class_raises():
     X = np.random.randn(300, 5)
-    y = np.arange(300) % 3
+    y = np.zeros(300, dtype=np.int64)
     with pytest.raises(NotImplementedError):
         HybridHistGBMNumbaV1_0_1(verbose=False).fit(X, y)
 
