@@ -883,6 +883,10 @@ hipError_t launch_part_scan(hipStream_t st, const PartParent *parents,
 // tiles).  (g,h) and row ids are gathered through inv and stored as
 // consecutive elements.
 constexpr int kChunkSlots = 2;  // output chunks a thread may own (<= 260 per tile)
+// Features staged in LDS per barrier: more loads in flight for the narrow
+// tiles; one for 16-row tiles, whose registers already limit occupancy.
+template <int R> struct ScatterFeats { static constexpr int value = 4; };
+template <> struct ScatterFeats<16> { static constexpr int value = 1; };
 
 template <int R>
 __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
@@ -895,7 +899,9 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
   __shared__ uint32_t tmp[kPartBlock / 64];
   constexpr int kTile = kPartBlock * R;
   __shared__ uint16_t inv[kTile];
-  __shared__ typename CodesR<R>::T cs[2][kPartBlock];  // one feature's codes, double buffered
+  constexpr int kScatterFeats = ScatterFeats<R>::value;
+  // kScatterFeats features' codes per batch, double buffered.
+  __shared__ typename CodesR<R>::T cs[2][kScatterFeats][kPartBlock];
   const int32_t n_tiles = plan->n_tiles;
   const int tid = (int)threadIdx.x;
   for (int32_t ti = (int32_t)blockIdx.x; ti < n_tiles; ti += (int32_t)gridDim.x) {
@@ -971,32 +977,45 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
       }
       cfull[q] = full;
     }
-    // Per feature: codes to LDS (double buffered: one barrier per feature),
+    // Per batch of kScatterFeats features: codes to LDS (double buffered:
+    // one barrier per batch, the next batch's loads in flight meanwhile),
     // then the owned chunks gathered from LDS and stored.
-    CodeWords<R> cur = load_codes<R>(codes_src, row, lo, hi);
-    for (int f = 0; f < F_sel; ++f) {
-      cs[f & 1][tid] = cur.v;
-      if (f + 1 < F_sel) cur = load_codes<R>(codes_src + (int64_t)(f + 1) * ld_c, row, lo, hi);
+    CodeWords<R> cur[kScatterFeats];
+#pragma unroll
+    for (int u = 0; u < kScatterFeats; ++u)
+      if (u < F_sel) cur[u] = load_codes<R>(codes_src + (int64_t)u * ld_c, row, lo, hi);
+    for (int f0 = 0, b = 0; f0 < F_sel; f0 += kScatterFeats, b ^= 1) {
+#pragma unroll
+      for (int u = 0; u < kScatterFeats; ++u)
+        if (f0 + u < F_sel) cs[b][u][tid] = cur[u].v;
+#pragma unroll
+      for (int u = 0; u < kScatterFeats; ++u)
+        if (f0 + kScatterFeats + u < F_sel)
+          cur[u] = load_codes<R>(codes_src + (int64_t)(f0 + kScatterFeats + u) * ld_c, row, lo, hi);
       __syncthreads();
-      const uint8_t *tb = reinterpret_cast<const uint8_t *>(cs[f & 1]);
-      uint8_t *dcol = codes_dst + (int64_t)f * ld_c;
 #pragma unroll
-      for (int q = 0; q < kChunkSlots; ++q) {
-        if (!cown[q]) continue;
-        if (cfull[q]) {
-          CodeWords<R> o;
+      for (int u = 0; u < kScatterFeats; ++u) {
+        if (f0 + u >= F_sel) break;
+        const uint8_t *tb = reinterpret_cast<const uint8_t *>(cs[b][u]);
+        uint8_t *dcol = codes_dst + (int64_t)(f0 + u) * ld_c;
 #pragma unroll
-          for (int k = 0; k < R / 4; ++k) {
-            const uint32_t s01 = csrc[q][2 * k], s23 = csrc[q][2 * k + 1];
-            o.w[k] = (uint32_t)tb[s01 & 0xffffu] | ((uint32_t)tb[s01 >> 16] << 8) |
-                     ((uint32_t)tb[s23 & 0xffffu] << 16) | ((uint32_t)tb[s23 >> 16] << 24);
-          }
-          *reinterpret_cast<typename CodesR<R>::T *>(dcol + cdst[q]) = o.v;
-        } else {
+        for (int q = 0; q < kChunkSlots; ++q) {
+          if (!cown[q]) continue;
+          if (cfull[q]) {
+            CodeWords<R> o;
 #pragma unroll
-          for (int k = 0; k < R; ++k) {
-            const uint32_t sv = (csrc[q][k >> 1] >> (16 * (k & 1))) & 0xffffu;
-            if (sv != 0xffffu) dcol[cdst[q] + k] = tb[sv];
+            for (int k = 0; k < R / 4; ++k) {
+              const uint32_t s01 = csrc[q][2 * k], s23 = csrc[q][2 * k + 1];
+              o.w[k] = (uint32_t)tb[s01 & 0xffffu] | ((uint32_t)tb[s01 >> 16] << 8) |
+                       ((uint32_t)tb[s23 & 0xffffu] << 16) | ((uint32_t)tb[s23 >> 16] << 24);
+            }
+            *reinterpret_cast<typename CodesR<R>::T *>(dcol + cdst[q]) = o.v;
+          } else {
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+              const uint32_t sv = (csrc[q][k >> 1] >> (16 * (k & 1))) & 0xffffu;
+              if (sv != 0xffffu) dcol[cdst[q] + k] = tb[sv];
+            }
           }
         }
       }

@@ -23,7 +23,10 @@
 // stages that run on their own threads without changing the sequence:
 //   * a draw thread twists and tempers whole 624-word blocks (AVX-512 when
 //     the CPU has it), a chunk at a time, and turns the words into the
-//     bounded draws j(i) of every round.
+//     bounded draws j(i) of every round.  For long shuffles it only counts:
+//     it decides which words are accepted, without storing draws, and hands
+//     each chunk's part of the round (the chunk's state, first word, step)
+//     to worker threads, which regenerate the chunk and write its draws.
 //     Within a run of steps with a constant mask, W = 64 (then 16) words are
 //     classified at once: a word <= i - (W-1) is accepted whatever happened
 //     to the words before it (each acceptance lowers i by one), a word > i
@@ -466,6 +469,178 @@ bool draw_steps_avx512(Stream &s, uint32_t hi, uint32_t *out) {
   return true;
 }
 
+// ---------------------------------------------------------------------------
+// Parallel draws.  Which words a shuffle accepts is a strictly sequential
+// question (word t is tested against i, which counts the words accepted
+// before it), but answering it needs no stores: a counting pass walks the
+// stream with the same tests as draw_steps_avx512 and, at the first word it
+// reads in each chunk, records a segment (the chunk's first-block state, the
+// word offset, the current i).  Worker threads then regenerate each
+// segment's chunk from that state and write its draws, out[hi - i], with
+// masked stores, so segments never touch each other's entries.
+// ---------------------------------------------------------------------------
+struct Segment {
+  uint32_t key[kN];  // state of the chunk's first block (before tempering)
+  int32_t w0;        // first word of the segment, offset in the chunk
+  uint32_t i0;       // the step that word is tested for
+  void *round;       // the round whose draws it writes
+};
+
+// The tempered words of the chunk whose first block has state key0.
+__attribute__((target("avx512f"))) void gen_chunk(const uint32_t *key0, uint32_t *out) {
+  alignas(64) uint32_t k[kN];
+  std::memcpy(k, key0, sizeof(k));
+  for (int b = 0; b < kChunkBlocks; ++b, out += kN) {
+    if (b > 0) twist_avx512(k);
+    temper_avx512(k, out);
+  }
+}
+
+// Counting pass of the draws of steps hi .. 1 (the acceptance tests of
+// draw_steps_avx512, without stores); emit(key, w0, i) opens a segment at
+// the first word read from each chunk.  False if the stream stops.
+template <class Emit>
+__attribute__((target("avx512f,avx512vl,avx512bw,popcnt")))
+bool count_steps_avx512(Stream &s, uint32_t hi, Emit &&emit) {
+  uint32_t i = hi;
+  int64_t open_chunk = -1;
+  while (i >= 1) {
+    const uint32_t lo = 1u << (31 - __builtin_clz(i));
+    const uint32_t mask = lo | (lo - 1);
+    const __m512i vm = _mm512_set1_epi32((int)mask);
+    while (i >= lo) {
+      if (s.p == s.end && !s.next_chunk()) return false;
+      if (s.chunk != open_chunk) {
+        emit(s.cur_key, (int32_t)(s.p - s.base), i);
+        open_chunk = s.chunk;
+      }
+      const uint32_t *p = s.p, *e = s.end;
+      // 256 words against one threshold pair (band [i - 254, i]): the
+      // counter i, which the next block's tests depend on, is updated once
+      // per 256 words instead of once per 64.
+      while (i - lo >= 256 && e - p >= 256) {
+        const __m512i si = _mm512_set1_epi32((int)i);
+        const __m512i sb = _mm512_set1_epi32((int)(i - 254));
+        __mmask16 amb = 0;
+        uint32_t acc = 0;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const __m512i v = _mm512_and_si512(_mm512_loadu_si512(p + 16 * q), vm);
+          const __mmask16 a = _mm512_cmple_epu32_mask(v, si);
+          amb |= _mm512_mask_cmpge_epu32_mask(a, v, sb);
+          acc += (uint32_t)__builtin_popcount((unsigned)a);
+        }
+        if (amb) break;
+        i -= acc;
+        p += 256;
+      }
+      while (i - lo >= 64 && e - p >= 64) {
+        const __m512i si = _mm512_set1_epi32((int)i);
+        const __m512i sb = _mm512_set1_epi32((int)(i - 62));
+        const __m512i v0 = _mm512_and_si512(_mm512_loadu_si512(p), vm);
+        const __m512i v1 = _mm512_and_si512(_mm512_loadu_si512(p + 16), vm);
+        const __m512i v2 = _mm512_and_si512(_mm512_loadu_si512(p + 32), vm);
+        const __m512i v3 = _mm512_and_si512(_mm512_loadu_si512(p + 48), vm);
+        const __mmask16 a0 = _mm512_cmple_epu32_mask(v0, si);
+        const __mmask16 a1 = _mm512_cmple_epu32_mask(v1, si);
+        const __mmask16 a2 = _mm512_cmple_epu32_mask(v2, si);
+        const __mmask16 a3 = _mm512_cmple_epu32_mask(v3, si);
+        const __mmask16 amb = _mm512_mask_cmpge_epu32_mask(a0, v0, sb) |
+                              _mm512_mask_cmpge_epu32_mask(a1, v1, sb) |
+                              _mm512_mask_cmpge_epu32_mask(a2, v2, sb) |
+                              _mm512_mask_cmpge_epu32_mask(a3, v3, sb);
+        if (amb) break;
+        const uint64_t all = (uint64_t)a0 | ((uint64_t)a1 << 16) | ((uint64_t)a2 << 32) |
+                             ((uint64_t)a3 << 48);
+        i -= (uint32_t)__builtin_popcountll(all);
+        p += 64;
+        if (i - lo >= 256 && e - p >= 256) break;  // back to the wide blocks
+      }
+      while (i - lo >= 16 && e - p >= 16) {
+        const __m512i v = _mm512_and_si512(_mm512_loadu_si512(p), vm);
+        const __mmask16 acc = _mm512_cmple_epu32_mask(v, _mm512_set1_epi32((int)i));
+        const __mmask16 amb = _mm512_mask_cmpge_epu32_mask(acc, v, _mm512_set1_epi32((int)(i - 14)));
+        if (amb) break;
+        i -= (uint32_t)__builtin_popcount((unsigned)acc);
+        p += 16;
+      }
+      if (p < e) {
+        const uint32_t v = *p++ & mask;
+        i -= v <= i ? 1u : 0u;
+      }
+      s.p = p;
+    }
+  }
+  return true;
+}
+
+// A segment's draws: from word w0 of the chunk `words` at step i0 to the
+// chunk's end or step 1, written to out[hi - i].  Same tests as the
+// counting pass; only accepted lanes are stored.
+__attribute__((target("avx512f,avx512vl,avx512bw,popcnt")))
+void write_segment_avx512(const uint32_t *words, int32_t w0, uint32_t i0, uint32_t hi,
+                          uint32_t *draws) {
+  const uint32_t *p = words + w0, *const e = words + kChunkWords;
+  uint32_t i = i0;
+  uint32_t *out = draws + (hi - i0);
+  while (i >= 1 && p < e) {
+    const uint32_t lo = 1u << (31 - __builtin_clz(i));
+    const uint32_t mask = lo | (lo - 1);
+    const __m512i vm = _mm512_set1_epi32((int)mask);
+    while (i >= lo && p < e) {
+      while (i - lo >= 64 && e - p >= 64) {
+        const __m512i si = _mm512_set1_epi32((int)i);
+        const __m512i sb = _mm512_set1_epi32((int)(i - 62));
+        const __m512i v0 = _mm512_and_si512(_mm512_loadu_si512(p), vm);
+        const __m512i v1 = _mm512_and_si512(_mm512_loadu_si512(p + 16), vm);
+        const __m512i v2 = _mm512_and_si512(_mm512_loadu_si512(p + 32), vm);
+        const __m512i v3 = _mm512_and_si512(_mm512_loadu_si512(p + 48), vm);
+        const __mmask16 a0 = _mm512_cmple_epu32_mask(v0, si);
+        const __mmask16 a1 = _mm512_cmple_epu32_mask(v1, si);
+        const __mmask16 a2 = _mm512_cmple_epu32_mask(v2, si);
+        const __mmask16 a3 = _mm512_cmple_epu32_mask(v3, si);
+        const __mmask16 amb = _mm512_mask_cmpge_epu32_mask(a0, v0, sb) |
+                              _mm512_mask_cmpge_epu32_mask(a1, v1, sb) |
+                              _mm512_mask_cmpge_epu32_mask(a2, v2, sb) |
+                              _mm512_mask_cmpge_epu32_mask(a3, v3, sb);
+        if (amb) break;
+        const uint32_t c0 = (uint32_t)__builtin_popcount((unsigned)a0);
+        const uint32_t c1 = (uint32_t)__builtin_popcount((unsigned)a1);
+        const uint32_t c2 = (uint32_t)__builtin_popcount((unsigned)a2);
+        const uint32_t c3 = (uint32_t)__builtin_popcount((unsigned)a3);
+        _mm512_mask_storeu_epi32(out, (__mmask16)((1u << c0) - 1u), _mm512_maskz_compress_epi32(a0, v0));
+        out += c0;
+        _mm512_mask_storeu_epi32(out, (__mmask16)((1u << c1) - 1u), _mm512_maskz_compress_epi32(a1, v1));
+        out += c1;
+        _mm512_mask_storeu_epi32(out, (__mmask16)((1u << c2) - 1u), _mm512_maskz_compress_epi32(a2, v2));
+        out += c2;
+        _mm512_mask_storeu_epi32(out, (__mmask16)((1u << c3) - 1u), _mm512_maskz_compress_epi32(a3, v3));
+        out += c3;
+        i -= c0 + c1 + c2 + c3;
+        p += 64;
+      }
+      while (i - lo >= 16 && e - p >= 16) {
+        const __m512i v = _mm512_and_si512(_mm512_loadu_si512(p), vm);
+        const __mmask16 acc = _mm512_cmple_epu32_mask(v, _mm512_set1_epi32((int)i));
+        const __mmask16 amb = _mm512_mask_cmpge_epu32_mask(acc, v, _mm512_set1_epi32((int)(i - 14)));
+        if (amb) break;
+        const uint32_t c = (uint32_t)__builtin_popcount((unsigned)acc);
+        _mm512_mask_storeu_epi32(out, (__mmask16)((1u << c) - 1u), _mm512_maskz_compress_epi32(acc, v));
+        out += c;
+        i -= c;
+        p += 16;
+      }
+      if (p < e) {
+        const uint32_t v = *p++ & mask;
+        if (v <= i) {
+          *out++ = v;
+          --i;
+        }
+      }
+    }
+  }
+}
+
 bool draw_steps(Stream &s, uint32_t hi, uint32_t *out) {
   if (hi == 0) return true;
   return use_avx512() ? draw_steps_avx512(s, hi, out) : draw_steps_scalar(s, hi, out);
@@ -488,14 +663,24 @@ struct Sampler {
     HostBuf<int32_t> rows;       // sample_idx (host mode)
     std::vector<int32_t> feats;  // ascending selected features
     int32_t index = 0;
+    std::atomic<int32_t> pending{0};  // segments still being written, +1 while counting
+    bool done = false;                // draws complete (and copied): deliverable
   };
   int32_t device = -1;                // GPU of the device copies
   hipStream_t copy_st = nullptr;
 
   std::atomic<bool> halt{false};     // makes the draw thread's stream stop
   std::atomic<double> gen_ms{0.0};   // word generation (inside draw_ms)
+  std::deque<std::unique_ptr<Round>> inflight;  // counted, draws being written (in order)
   std::deque<std::unique_ptr<Round>> drawn;  // draw thread -> swap thread
   std::deque<std::unique_ptr<Round>> ready;  // -> consumer
+  // Parallel draws (rounds of at least kParallelSteps steps with AVX-512):
+  // segments from the counting pass, written by the worker threads.
+  std::deque<Segment> segs;
+  std::condition_variable seg_cv;
+  int32_t idle_workers = 0;  // workers asleep on seg_cv
+  std::vector<std::thread> workers;
+  bool parallel = false;
   std::vector<std::unique_ptr<Round>> pool;
   int32_t n_drawn = 0, produced = 0, consumed = 0;
   bool stop = false;
@@ -511,10 +696,13 @@ struct Sampler {
   double draw_ms = 0.0, swap_ms = 0.0;
 
   void fail(const char *msg) {
-    std::lock_guard<std::mutex> lk(mu);
-    if (error.empty()) error = msg;
-    stop = true;
+    {
+      std::lock_guard<std::mutex> lk(mu);
+      if (error.empty()) error = msg;
+      stop = true;
+    }
     cv.notify_all();
+    seg_cv.notify_all();
   }
 
   // Device-rows mode: the round's draws go to the GPU on the sampler's own
@@ -556,6 +744,63 @@ struct Sampler {
     R.copied = nullptr;
   }
 
+  // The round's draws are complete: copy them to the device (device-rows
+  // mode), then hand every complete round at the head of `inflight` on, in
+  // round order.
+  void finalize(Round *R) {
+    if (device_rows && do_rows && !copy_to_device(*R)) return;
+    {
+      std::lock_guard<std::mutex> lk(mu);
+      R->done = true;
+      while (!inflight.empty() && inflight.front()->done) {
+        std::unique_ptr<Round> q = std::move(inflight.front());
+        inflight.pop_front();
+        if (device_rows || !do_rows) {
+          ready.push_back(std::move(q));
+          ++produced;
+        } else {
+          drawn.push_back(std::move(q));
+        }
+      }
+    }
+    cv.notify_all();
+  }
+
+  void release(Round *R) {
+    if (R->pending.fetch_sub(1, std::memory_order_acq_rel) == 1) finalize(R);
+  }
+
+  void run_worker() {
+    (void)pthread_setname_np(pthread_self(), "bsscl-drawseg");
+    try {
+      if (device_rows && do_rows && hipSetDevice(device) != hipSuccess) {
+        fail("sampler: hipSetDevice failed");
+        return;
+      }
+      std::vector<uint32_t> words((size_t)kChunkWords + 16);
+      for (;;) {
+        Segment sg;
+        {
+          std::unique_lock<std::mutex> lk(mu);
+          if (!stop && segs.empty()) {
+            ++idle_workers;
+            seg_cv.wait(lk, [&] { return stop || !segs.empty(); });
+            --idle_workers;
+          }
+          if (stop) return;
+          sg = segs.front();
+          segs.pop_front();
+        }
+        Round *R = static_cast<Round *>(sg.round);
+        gen_chunk(sg.key, words.data());
+        write_segment_avx512(words.data(), sg.w0, sg.i0, (uint32_t)(n - 1), R->draws.p);
+        release(R);
+      }
+    } catch (...) {
+      fail("sampler: draw worker failed (out of memory?)");
+    }
+  }
+
   void run_draws() {
     (void)pthread_setname_np(pthread_self(), "bsscl-draw");
     try {
@@ -571,7 +816,8 @@ struct Sampler {
         {
           std::unique_lock<std::mutex> lk(mu);
           cv.wait(lk, [&] {
-            return stop || (int32_t)(drawn.size() + ready.size()) < lookahead;
+            return stop ||
+                   (int32_t)(inflight.size() + drawn.size() + ready.size()) < lookahead;
           });
           if (stop) return;
           if (!pool.empty()) {
@@ -581,30 +827,55 @@ struct Sampler {
         }
         if (!R) R.reset(new Round());
         if (do_rows) R->draws.alloc((size_t)n + 16);
+        R->done = false;
+        R->pending.store(1, std::memory_order_relaxed);  // this thread's share
+        Round *Rp = R.get();
+        {
+          std::lock_guard<std::mutex> lk(mu);
+          inflight.push_back(std::move(R));
+        }
         const auto t0 = std::chrono::steady_clock::now();
-        if (do_rows && !draw_steps(st, (uint32_t)(n - 1), R->draws.p)) return;
+        if (do_rows && parallel) {
+          auto emit = [&](const uint32_t *key, int32_t w0, uint32_t i) {
+            Segment sg;
+            std::memcpy(sg.key, key, sizeof(sg.key));
+            sg.w0 = w0;
+            sg.i0 = i;
+            sg.round = Rp;
+            Rp->pending.fetch_add(1, std::memory_order_relaxed);
+            // A sleeping worker is woken once four segments wait (waking
+            // costs a system call; a worker drains the queue before it
+            // sleeps again).
+            bool wake;
+            {
+              std::lock_guard<std::mutex> lk(mu);
+              segs.push_back(sg);
+              wake = idle_workers > 0 && segs.size() >= 4;
+            }
+            if (wake) seg_cv.notify_one();
+          };
+          const bool ok = count_steps_avx512(st, (uint32_t)(n - 1), emit);
+          seg_cv.notify_all();  // the round's last segments
+          if (!ok) return;
+        } else if (do_rows && !draw_steps(st, (uint32_t)(n - 1), Rp->draws.p)) {
+          return;
+        }
         if (do_feats && F > 1) {
           if (!draw_steps(st, (uint32_t)(F - 1), jf.data())) return;
           for (int32_t t = 0; t < F - 1; ++t) std::swap(feats[(size_t)(F - 1 - t)], feats[jf[(size_t)t]]);
         }
-        R->feats.assign(feats.begin(), feats.begin() + f_sub);
-        std::sort(R->feats.begin(), R->feats.end());
-        R->index = r;
+        Rp->feats.assign(feats.begin(), feats.begin() + f_sub);
+        std::sort(Rp->feats.begin(), Rp->feats.end());
+        Rp->index = r;
         const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-        if (device_rows && do_rows && !copy_to_device(*R)) return;
         {
           std::lock_guard<std::mutex> lk(mu);
           draw_ms += ms;
-          if (device_rows || !do_rows) {
-            ready.push_back(std::move(R));
-            ++produced;
-          } else {
-            drawn.push_back(std::move(R));
-          }
           ++n_drawn;
           if (n_drawn == n_rounds) st.state(key0, pos0, final_key, &final_pos);
         }
         cv.notify_all();
+        release(Rp);
       }
     } catch (...) {
       fail("sampler: draw thread failed (out of memory?)");
@@ -679,14 +950,18 @@ struct Sampler {
       stop = true;
     }
     cv.notify_all();
+    seg_cv.notify_all();
     halt.store(true);
     if (draw_thread.joinable()) draw_thread.join();
+    for (auto &w : workers)
+      if (w.joinable()) w.join();
     if (swap_thread.joinable()) swap_thread.join();
     if (copy_st) {
       (void)hipSetDevice(device);
       (void)hipStreamSynchronize(copy_st);
       for (auto &r : ready) free_device(*r);
       for (auto &r : pool) free_device(*r);
+      for (auto &r : inflight) free_device(*r);
       (void)hipStreamDestroy(copy_st);
     }
   }
@@ -823,6 +1098,14 @@ int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
     }
     s->feats.resize((size_t)n_features);
     for (int32_t j = 0; j < n_features; ++j) s->feats[(size_t)j] = j;
+    // Rounds of at least four chunks of steps split their draws over
+    // worker threads (AVX-512 only; the scalar path stays sequential).
+    s->parallel = s->do_rows && bsscl::use_avx512() && n - 1 >= 4 * bsscl::kChunkWords;
+    if (s->parallel) {
+      const unsigned hw = std::max(2u, std::thread::hardware_concurrency());
+      const int nw = (int)std::min(4u, hw / 2);
+      for (int w = 0; w < nw; ++w) s->workers.emplace_back([s] { s->run_worker(); });
+    }
     s->draw_thread = std::thread([s] { s->run_draws(); });
     if (s->do_rows && !s->device_rows) s->swap_thread = std::thread([s] { s->run_swaps(); });
   } catch (...) {

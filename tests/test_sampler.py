@@ -59,6 +59,29 @@ def test_sampler_starting_positions_and_final_state(doubles):
     s.close()
 
 
+@pytest.mark.parametrize("doubles", [0, 7, 312])
+def test_parallel_draws_match_numpy_over_mask_ranges(doubles):
+    """Rounds long enough for the counting pass and the draw workers (about
+    100 chunks of words each, crossing the masks 2^21-1 .. 1), against
+    RandomState.shuffle, and the state after them."""
+    n, F, rounds = 2_000_003, 5, 3
+    rng = _state_after(23, doubles)
+    s = _native.Sampler(rng.get_state(), n, n - 1, True, F, 3, True, rounds)
+    rows = np.arange(n, dtype=np.int64)
+    feats = np.arange(F, dtype=np.int32)
+    for _ in range(rounds):
+        rng.shuffle(rows)
+        rng.shuffle(feats)
+        r, f = s.next()
+        np.testing.assert_array_equal(r, rows[:n - 1])
+        np.testing.assert_array_equal(f, np.sort(feats[:3]))
+    key, pos = s.state()
+    st = rng.get_state()
+    np.testing.assert_array_equal(key, st[1])
+    assert pos == st[2]
+    s.close()
+
+
 def test_sampler_scalar_path_matches():
     """The same stream with the AVX-512 draws switched off (the switch is
     read once per process, so this runs in a child)."""
