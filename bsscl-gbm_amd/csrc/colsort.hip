@@ -375,6 +375,27 @@ hipError_t launch_col_sort(hipStream_t st, const void *X, int is_f64, int64_t n,
   return col_sort_impl<float, uint32_t>(st, X, n, F, keys, tmp, ld, counts, totals, m);
 }
 
+int64_t sort_u64_ld(int64_t n) { return col_sort_ld(n, 1); }
+
+int64_t sort_u64_count_words(int64_t n) { return col_sort_count_words(n, 1, 1); }
+
+hipError_t launch_sort_u64(hipStream_t st, uint64_t *keys, uint64_t *tmp, int64_t ld,
+                           int lo_bit, int hi_bit, uint32_t *counts, uint32_t *totals,
+                           uint64_t **result) {
+  const int32_t n_tiles = (int32_t)(ld / tile_keys<uint64_t>());
+  const dim3 tiles((unsigned)n_tiles, 1u);
+  for (int shift = lo_bit; shift < hi_bit; shift += 8) {
+    hipLaunchKernelGGL((k_rs_count<uint64_t>), tiles, dim3(kSortThreads), 0, st, keys, ld,
+                       n_tiles, shift, counts);
+    hipLaunchKernelGGL(k_rs_scan, dim3(kRadix, 1u), dim3(256), 0, st, counts, n_tiles, totals);
+    hipLaunchKernelGGL((k_rs_scatter<uint64_t>), tiles, dim3(kSortThreads), 0, st, keys, tmp,
+                       ld, n_tiles, shift, counts, totals);
+    std::swap(keys, tmp);
+  }
+  *result = keys;
+  return hipGetLastError();
+}
+
 hipError_t launch_col_changes(hipStream_t st, const void *keys, int is_f64, int64_t ld, int32_t F,
                               const int64_t *m, int64_t max_m, unsigned long long *out) {
   if (F <= 0 || max_m <= 1) return hipSuccess;

@@ -210,6 +210,7 @@ struct bsscl_engine {
   DevBuf<uint8_t> codes_c[2];
   DevBuf<int2> gh_c[2];
   DevBuf<int32_t> rid_c[2];
+  bool track_rid = false;  // carry row ids through the partition (bsscl_partition)
   int64_t ld_c = 0;
   DevBuf<int32_t> rows32;
   DevBuf<int64_t> rows64;
@@ -221,6 +222,8 @@ struct bsscl_engine {
   const void *perm_sampler = nullptr;
   int32_t perm_next_round = 0;
   DevBuf<int32_t> fy_head, fy_next, fy_v;
+  DevBuf<uint64_t> fy_keys[2];       // sorted Fisher-Yates form (long shuffles)
+  DevBuf<uint32_t> fy_counts, fy_totals;
   DevBuf<uint8_t> row_flags;  // all zero between rounds
   int64_t row_flags_n = 0;
   // Node-indexed buffers (node_cap nodes) and the level lists the planner
@@ -765,14 +768,16 @@ int launch_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_
   HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, feat_d, F_sel,
                             use32 ? E->rows32.p : nullptr,
                             use32 ? nullptr : E->rows64.p, m, E->ghq.p,
-                            E->codes_c[0].p, E->ld_c, E->gh_c[0].p, E->rid_c[0].p,
+                            E->codes_c[0].p, E->ld_c, E->gh_c[0].p,
+                            E->track_rid ? E->rid_c[0].p : nullptr,
                             E->ld_c, E->segs.p, E->hist_node_d.p));
   hipEvent_t stop;
   CHK(prof_begin(E, 0, &stop));
   HIPCHK(launch_hist(E->st, E->codes_c[0].p, E->ld_c, E->gh_c[0].p,
                      reinterpret_cast<const HistTask *>(dv[2]), E->plan_d, rp.n_hist,
-                     E->hist_node_d.p, E->segs.p, E->nb_sel_d, E->hot_sel_d, F_sel,
-                     hist_fchunk(E, F_sel), E->hist_copies, E->part_d.p));
+                     E->hist_node_d.p, reinterpret_cast<const int32_t *>(dv[5]), E->segs.p,
+                     E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel), E->hist_copies,
+                     E->part_d.p, E->pool.p, E->node_stride));
   CHK(prof_end(E, stop));
   CHK(prof_begin(E, 3, &stop));
   HIPCHK(launch_hist_reduce(E->st, E->plan_d, 1, reinterpret_cast<const int32_t *>(dv[5]),
@@ -834,8 +839,10 @@ int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parent
                           E->hist_node_d.p, min_samples_leaf));
   if (move_rows)
     HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p, E->ld_c,
-                               E->gh_c[src].p, E->gh_c[dst].p, E->rid_c[src].p,
-                               E->rid_c[dst].p, parents, tiles, plan, max_tiles,
+                               E->gh_c[src].p, E->gh_c[dst].p,
+                               E->track_rid ? E->rid_c[src].p : nullptr,
+                               E->track_rid ? E->rid_c[dst].p : nullptr, parents, tiles,
+                               plan, max_tiles,
                                E->part_rows, E->tile_off_d.p, E->nleft_d.p, F_sel));
   CHK(prof_end(E, stop));
   return BSSCL_OK;
@@ -866,8 +873,9 @@ int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
   const int32_t H = (int32_t)std::min<int64_t>(E->hist_cap, (int64_t)hist_target(E, F_sel) + 2 * (int64_t)P + 2);
   CHK(prof_begin(E, 0, &stop));
   HIPCHK(launch_hist(E->st, E->codes_c[dst].p, E->ld_c, E->gh_c[dst].p, E->hist_tasks_d.p,
-                     E->plan_d, H, E->hist_node_d.p, E->segs.p, E->nb_sel_d, E->hot_sel_d,
-                     F_sel, hist_fchunk(E, F_sel), E->hist_copies, E->part_d.p));
+                     E->plan_d, H, E->hist_node_d.p, E->hist_begin_d.p, E->segs.p,
+                     E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel), E->hist_copies,
+                     E->part_d.p, E->pool.p, E->node_stride));
   CHK(prof_end(E, stop));
   CHK(prof_begin(E, 3, &stop));
   HIPCHK(launch_hist_reduce(E->st, E->plan_d, P, E->hist_begin_d.p, E->hist_node_d.p,
@@ -944,11 +952,31 @@ int ensure_round_out(bsscl_engine *E, int b, int32_t M) {
 }
 
 // Device Fisher-Yates work arrays for n items.
+// Shuffles of at least this many positions build their step lists by
+// sorting (position, step) keys; shorter ones use per-position linked
+// lists.  (Test hook: BSSCL_FY_SORTED=1 or 0 forces one form.)
+constexpr int64_t kFySortedMin = 1 << 16;
+
 int ensure_fy_work(bsscl_engine *E, int64_t n, FyWork &w) {
   for (DevBuf<int32_t> *x : {&E->fy_head, &E->fy_next, &E->fy_v}) CHK(x->ensure((size_t)n));
   w.head = E->fy_head.p;
   w.next = E->fy_next.p;
   w.v = E->fy_v.p;
+  const char *force = std::getenv("BSSCL_FY_SORTED");
+  const bool sorted = force && (force[0] == '0' || force[0] == '1') ? force[0] == '1'
+                                                                    : n >= kFySortedMin;
+  w.keys = w.keys_tmp = nullptr;
+  w.counts = w.totals = nullptr;
+  if (sorted && n > 1) {
+    const size_t ld = (size_t)sort_u64_ld(n - 1);
+    for (auto &k : E->fy_keys) CHK(k.ensure(ld));
+    CHK(E->fy_counts.ensure((size_t)sort_u64_count_words(n - 1)));
+    CHK(E->fy_totals.ensure(256));
+    w.keys = E->fy_keys[0].p;
+    w.keys_tmp = E->fy_keys[1].p;
+    w.counts = E->fy_counts.p;
+    w.totals = E->fy_totals.p;
+  }
   return BSSCL_OK;
 }
 
@@ -1509,6 +1537,9 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->fy_head.release();
   E->fy_next.release();
   E->fy_v.release();
+  for (auto &k : E->fy_keys) k.release();
+  E->fy_counts.release();
+  E->fy_totals.release();
 
   E->row_flags.release();
   E->lvl_d.release();
@@ -2105,6 +2136,7 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
                             nullptr, E->rows64.p, m, E->ghq.p, E->codes_c[0].p, E->ld_c,
                             E->gh_c[0].p, E->rid_c[0].p, E->ld_c, E->segs.p,
                             E->hist_node_d.p));
+  E->track_rid = true;  // this call reads the moved row ids back
   const PartParent P{0, m, 0, bin, 1, 2, 0, 0};
   std::vector<PartTile> tiles;
   add_part_tiles(E, P, 0, tiles);
@@ -2124,6 +2156,7 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
                        reinterpret_cast<const PartTile *>(dv[2]),
                        reinterpret_cast<const LevelPlan *>(dv[3]), 1, (int32_t)tiles.size(),
                        1, 0, true));
+  E->track_rid = false;
   std::vector<int32_t> r32((size_t)m);
   int64_t nl = 0;
   HIPCHK(hipMemcpyAsync(r32.data(), E->rid_c[1].p, (size_t)m * 4, hipMemcpyDeviceToHost, E->st));

@@ -187,12 +187,90 @@ __global__ __launch_bounds__(256) void k_fy_final(const uint32_t *__restrict__ d
   }
 }
 
+// ---------------------------------------------------------------------------
+// Sorted form of the same lists.  Step k (1 <= k < n, j(k) != k) becomes the
+// key (j(k) << 32) | k; a stable sort by the high word puts each position's
+// steps together in ascending order.  The first step of a run is head[p];
+// the successor of step k in its position's list is the next key of the run.
+// ---------------------------------------------------------------------------
+constexpr uint64_t kFyNoKey = ~0ull;
+
+__global__ __launch_bounds__(256) void k_fy_keys(const uint32_t *__restrict__ draws, int64_t n,
+                                                 int64_t ld, uint64_t *__restrict__ keys) {
+  for (int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; s < ld;
+       s += (int64_t)gridDim.x * blockDim.x) {
+    uint64_t key = kFyNoKey;
+    if (s < n - 1) {
+      const int64_t k = s + 1;
+      const uint32_t p = draws[n - 1 - k];
+      if ((int64_t)p != k) key = ((uint64_t)p << 32) | (uint64_t)k;
+    }
+    keys[s] = key;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_fy_links(const uint64_t *__restrict__ keys, int64_t ld,
+                                                  int32_t *__restrict__ head) {
+  for (int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; s < ld;
+       s += (int64_t)gridDim.x * blockDim.x) {
+    const uint64_t key = keys[s];
+    if (key == kFyNoKey) continue;
+    const uint32_t p = (uint32_t)(key >> 32);
+    if (s == 0 || (uint32_t)(keys[s - 1] >> 32) != p) head[p] = (int32_t)(key & 0xffffffffu);
+  }
+}
+
+// a_new[k] for every step k with j(k) != k, in sorted order.
+__global__ __launch_bounds__(256) void k_fy_final_sorted(const uint64_t *__restrict__ keys,
+                                                         int64_t ld,
+                                                         const int32_t *__restrict__ v,
+                                                         const int32_t *__restrict__ a_old,
+                                                         int32_t *__restrict__ a_new) {
+  for (int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; s < ld;
+       s += (int64_t)gridDim.x * blockDim.x) {
+    const uint64_t key = keys[s];
+    if (key == kFyNoKey) continue;
+    const uint32_t p = (uint32_t)(key >> 32);
+    const int32_t k = (int32_t)(key & 0xffffffffu);
+    const uint64_t nk = s + 1 < ld ? keys[s + 1] : kFyNoKey;
+    const bool has_next = nk != kFyNoKey && (uint32_t)(nk >> 32) == p;
+    a_new[k] = has_next ? v[(int32_t)(nk & 0xffffffffu)] : a_old[p];
+  }
+}
+
+// a_new[k] for position 0 and every step with j(k) == k.
+__global__ __launch_bounds__(256) void k_fy_final_self(const uint32_t *__restrict__ draws,
+                                                       int64_t n, const int32_t *__restrict__ v,
+                                                       int32_t *__restrict__ a_new) {
+  for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < n;
+       k += (int64_t)gridDim.x * blockDim.x) {
+    if (k == 0 || (int64_t)draws[n - 1 - k] == k) a_new[k] = v[k];
+  }
+}
+
 }  // namespace
 
 hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
                                const int32_t *a_old, int32_t *a_new, const FyWork &w) {
   if (n <= 0) return hipSuccess;
   const dim3 g(blocks_for(n)), b(256);
+  if (w.keys && n > 1) {
+    const int64_t ld = sort_u64_ld(n - 1);
+    int bits = 0;
+    while (bits < 32 && ((uint64_t)(n - 1) >> bits) != 0) ++bits;  // positions < 2^bits
+    const dim3 gk(blocks_for(ld));
+    hipLaunchKernelGGL(k_fill_neg, g, b, 0, st, w.head, n);
+    hipLaunchKernelGGL(k_fy_keys, gk, b, 0, st, draws, n, ld, w.keys);
+    uint64_t *sorted = nullptr;
+    hipError_t e = launch_sort_u64(st, w.keys, w.keys_tmp, ld, 32, 32 + (bits + 7) / 8 * 8,
+                                   w.counts, w.totals, &sorted);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_fy_links, gk, b, 0, st, sorted, ld, w.head);
+    hipLaunchKernelGGL(k_fy_resolve, g, b, 0, st, w.head, a_old, w.v, n);
+    hipLaunchKernelGGL(k_fy_final_sorted, gk, b, 0, st, sorted, ld, w.v, a_old, a_new);
+    hipLaunchKernelGGL(k_fy_final_self, g, b, 0, st, draws, n, w.v, a_new);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(k_fill_neg, g, b, 0, st, w.head, n);
   if (n > 1) hipLaunchKernelGGL(k_fy_push, g, b, 0, st, draws, n, w.head, w.next);
   hipLaunchKernelGGL(k_fy_sort, g, b, 0, st, w.head, w.next, n);

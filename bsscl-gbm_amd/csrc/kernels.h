@@ -187,6 +187,11 @@ hipError_t launch_iota(hipStream_t st, int32_t *a, int64_t n);
 // Work arrays of the device Fisher-Yates (fisher_yates.hip): int32[n] each.
 struct FyWork {
   int32_t *head, *next, *v;
+  // Sorted form (used when keys is set): (position, step) keys, their sort
+  // buffer and counts (sort_u64_ld(n - 1) keys, sort_u64_count_words(n - 1)
+  // and 256 words).
+  uint64_t *keys = nullptr, *keys_tmp = nullptr;
+  uint32_t *counts = nullptr, *totals = nullptr;
 };
 // a_new = a_old after the Fisher-Yates steps i = n-1 .. 1 with draws[t] =
 // j(n-1-t) <= n-1-t.
@@ -204,10 +209,12 @@ hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
 hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int2 *gh_c, const HistTask *tasks,
                        const LevelPlan *plan, int32_t max_tasks,
-                       const int32_t *hist_node, const NodeSeg *segs,
+                       const int32_t *hist_node, const int32_t *hist_begin,
+                       const NodeSeg *segs,
                        const int32_t *nb_sel, const int32_t *hot_sel,
                        int32_t F_sel, int32_t fchunk, int32_t copies,
-                       unsigned long long *part);
+                       unsigned long long *part, unsigned long long *pool,
+                       int64_t node_stride);
 // Sums the partials that launch_hist stored for each node with a histogram
 // task (hist_begin: a node's tasks, hist_node: its id) into the pool.
 hipError_t launch_hist_reduce(hipStream_t st, const LevelPlan *plan, int32_t max_refs,
@@ -303,6 +310,13 @@ hipError_t launch_col_run_starts(hipStream_t st, const void *keys, int is_f64, i
                                  int32_t col, int64_t m, int32_t max_out, int64_t *pos,
                                  unsigned int *count);
 // out[k] = value at position pos[k] of sorted column col[k], as float64.
+// Stable LSD sort of one padded column of ld 64-bit keys by bits
+// [lo_bit, hi_bit) (8-bit digits); *result is the buffer holding it.
+int64_t sort_u64_ld(int64_t n);
+int64_t sort_u64_count_words(int64_t n);
+hipError_t launch_sort_u64(hipStream_t st, uint64_t *keys, uint64_t *tmp, int64_t ld,
+                           int lo_bit, int hi_bit, uint32_t *counts, uint32_t *totals,
+                           uint64_t **result);
 hipError_t launch_col_gather(hipStream_t st, const void *keys, int is_f64, int64_t ld,
                              int64_t count, const int32_t *col, const int64_t *pos, double *out);
 

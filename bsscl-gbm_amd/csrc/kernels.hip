@@ -396,7 +396,8 @@ int64_t sort_rows_flag_bytes(int64_t n) {
 // ---------------------------------------------------------------------------
 // Root gather: the tree's in-bag rows (ascending ids from the sampler, or the
 // caller's order) -> compact feature-major set 0.  One thread fills 4
-// consecutive compact rows, so every store is a dword.
+// consecutive compact rows, so every store is a dword.  Row ids are kept
+// (rid_c) only when a caller reads the partition back.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_gather_root(
     const uint8_t *__restrict__ codes, int64_t ld, const int32_t *__restrict__ feat,
@@ -425,7 +426,7 @@ __global__ __launch_bounds__(256) void k_gather_root(
     ok[k] = (k0 + k) < m;
     r[k] = ok[k] ? (rows32 ? rows32[k0 + k] : (int32_t)rows64[k0 + k]) : 0;
     gh_c[k0 + k] = ok[k] ? ghq[r[k]] : make_int2(0, 0);
-    rid_c[k0 + k] = ok[k] ? r[k] : -1;
+    if (rid_c) rid_c[k0 + k] = ok[k] ? r[k] : -1;
   }
   for (int32_t f = 0; f < F_sel; ++f) {
     const uint8_t *col = codes + (int64_t)feat[f] * ld;
@@ -499,13 +500,24 @@ constexpr int kHistRows = 16;  // rows per thread per step
 // the copies of one bin sit in C consecutive words, so lanes of different
 // copies never meet in an LDS bank whatever their bins (3.13 instead of 2.18
 // (g,h) updates per clock per CU for C = 8 on MI355X).
+// Tasks of histogram reference p that hold rows: at most the planned tasks,
+// and none past the node's last row.
+__device__ __forceinline__ int32_t hist_tasks_with_rows(const int32_t *__restrict__ hist_begin,
+                                                        int32_t p, int64_t count,
+                                                        int32_t tile_rows) {
+  const int64_t with_rows = (count + tile_rows - 1) / tile_rows;
+  return (int32_t)min((int64_t)(hist_begin[p + 1] - hist_begin[p]), with_rows);
+}
+
 template <int FC, int C>
 __device__ __forceinline__ void hist_item(
     unsigned long long *lh, const uint8_t *__restrict__ codes_c, int64_t ld_c,
     const int2 *__restrict__ gh_c, const HistTask task, int32_t ti, int chunk,
-    const int32_t *__restrict__ hist_node, const NodeSeg *__restrict__ segs,
+    const int32_t *__restrict__ hist_node, const int32_t *__restrict__ hist_begin,
+    const NodeSeg *__restrict__ segs,
     const int32_t *__restrict__ nb_sel, const int32_t *__restrict__ hot_sel,
-    int32_t F_sel, int32_t tile_rows, unsigned long long *__restrict__ part) {
+    int32_t F_sel, int32_t tile_rows, unsigned long long *__restrict__ part,
+    unsigned long long *__restrict__ pool, int64_t node_stride) {
   const int32_t node = hist_node[task.ref];
   if (node < 0) return;
   const NodeSeg seg = segs[node];
@@ -591,8 +603,13 @@ __device__ __forceinline__ void hist_item(
     }
   }
   __syncthreads();
-  // Partial of task ti, features f0 .. f0+nf-1, as [bin][g,h].
-  unsigned long long *dst = part + ((int64_t)ti * F_sel + f0) * kHistPerFeat;
+  // Partial of task ti, features f0 .. f0+nf-1, as [bin][g,h]; a node built
+  // by this one task gets it as its histogram directly (k_hist_reduce skips
+  // such nodes).
+  unsigned long long *dst =
+      hist_tasks_with_rows(hist_begin, task.ref, seg.count, tile_rows) == 1
+          ? pool + (int64_t)node * node_stride + (int64_t)f0 * kHistPerFeat
+          : part + ((int64_t)ti * F_sel + f0) * kHistPerFeat;
   for (int i = threadIdx.x; i < nf * kHistPerFeat; i += kHistBlock) {
     const int j = i & (kHistPerFeat - 1);
     const unsigned long long *src = lh + ((i - j) + (j & 1) * kBins + (j >> 1)) * C;
@@ -609,9 +626,11 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
     const uint8_t *__restrict__ codes_c, int64_t ld_c,
     const int2 *__restrict__ gh_c, const HistTask *__restrict__ tasks,
     const LevelPlan *__restrict__ plan, const int32_t *__restrict__ hist_node,
+    const int32_t *__restrict__ hist_begin,
     const NodeSeg *__restrict__ segs, const int32_t *__restrict__ nb_sel,
     const int32_t *__restrict__ hot_sel, int32_t F_sel, int32_t nchunks,
-    unsigned long long *__restrict__ part) {
+    unsigned long long *__restrict__ part, unsigned long long *__restrict__ pool,
+    int64_t node_stride) {
   __shared__ unsigned long long lh[FC * kHistPerFeat * C];
   const int32_t n_tasks = plan->n_hist;
   const int32_t tile_rows = plan->tile_rows;
@@ -622,13 +641,15 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
     const int ti = (j / nchunks) * 8 + (b & 7);
     if ((j / nchunks) * 8 >= n_tasks) break;
     if (ti >= n_tasks) continue;
-    hist_item<FC, C>(lh, codes_c, ld_c, gh_c, tasks[ti], ti, j % nchunks, hist_node, segs,
-                     nb_sel, hot_sel, F_sel, tile_rows, part);
+    hist_item<FC, C>(lh, codes_c, ld_c, gh_c, tasks[ti], ti, j % nchunks, hist_node,
+                     hist_begin, segs, nb_sel, hot_sel, F_sel, tile_rows, part, pool,
+                     node_stride);
   }
 }
 
 // Sums each built node's partials (one per task with rows; exact int64, so
-// the order does not matter) into its histogram in the pool.  A block owns
+// the order does not matter) into its histogram in the pool; a node with a
+// single task was written there by k_hist.  A block owns
 // 64 consecutive words of one node: its kReduceWaves waves each sum every
 // kReduceWaves-th partial (one coalesced 512-byte load per partial), then
 // the waves' sums are added in LDS.
@@ -653,8 +674,8 @@ __global__ __launch_bounds__(64 * kReduceWaves) void k_hist_reduce(
     const NodeSeg seg = segs[node];
     if (!seg.valid) continue;
     const int32_t t0 = hist_begin[p];
-    const int64_t with_rows = (seg.count + tile_rows - 1) / tile_rows;
-    const int32_t nt = (int32_t)min((int64_t)(hist_begin[p + 1] - t0), with_rows);
+    const int32_t nt = hist_tasks_with_rows(hist_begin, p, seg.count, tile_rows);
+    if (nt == 1) continue;  // k_hist wrote it
     const unsigned long long *src = part + (int64_t)t0 * words + w;
     unsigned long long acc = 0ull;
     int32_t t = wave;
@@ -680,17 +701,19 @@ int hist_blocks(int32_t n_tasks, int32_t nchunks) {
 hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int2 *gh_c, const HistTask *tasks,
                        const LevelPlan *plan, int32_t max_tasks,
-                       const int32_t *hist_node, const NodeSeg *segs,
+                       const int32_t *hist_node, const int32_t *hist_begin,
+                       const NodeSeg *segs,
                        const int32_t *nb_sel, const int32_t *hot_sel,
                        int32_t F_sel, int32_t fchunk, int32_t copies,
-                       unsigned long long *part) {
+                       unsigned long long *part, unsigned long long *pool,
+                       int64_t node_stride) {
   if (max_tasks <= 0) return hipSuccess;
   const int32_t nchunks = (F_sel + fchunk - 1) / fchunk;
   const dim3 grid((unsigned)hist_blocks(max_tasks, nchunks));
 #define BSSCL_HIST(FC, C)                                                              \
   hipLaunchKernelGGL((k_hist<FC, C>), grid, dim3(kHistBlock), 0, st, codes_c, ld_c, gh_c, \
-                     tasks, plan, hist_node, segs, nb_sel, hot_sel, F_sel, nchunks,    \
-                     part)
+                     tasks, plan, hist_node, hist_begin, segs, nb_sel, hot_sel, F_sel, \
+                     nchunks, part, pool, node_stride)
   // LDS per block: fchunk * copies * 8 KB (at most 32 KB).
   switch (fchunk * 16 + copies) {
     case 1 * 16 + 1: BSSCL_HIST(1, 1); break;
@@ -940,7 +963,7 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
       const int64_t d = sl < ltot ? lbase + sl : rbase + (sl - ltot);
       const int64_t r = t.row0 + inv[sl];
       gh_dst[d] = gh_src[r];
-      rid_dst[d] = rid_src[r];
+      if (rid_dst) rid_dst[d] = rid_src[r];
     }
     // Output chunks: the left run's then the right run's aligned R-byte
     // chunks.  Per owned chunk: its destination row and, per byte, the

@@ -60,3 +60,45 @@ def fisher_yates_lists(a_old, draws):
     res = np.where(g >= 0, v[np.maximum(g, 0)], np.asarray(a_old)[np.maximum(-2 - g, 0)])
     out[1:] = np.where(ji == i, v[1:], res)
     return out
+
+
+def fisher_yates_sorted_keys(a_old, draws):
+    """The sorted form of the device kernels (k_fy_keys, k_fy_links,
+    k_fy_final_sorted, k_fy_final_self in fisher_yates.hip): step k with
+    j(k) != k becomes the key (j(k) << 32) | k, steps with j(k) == k the
+    largest key; a stable sort on the high word; run starts give head[];
+    each key's successor in its run gives a_new[k]."""
+    a_old = np.asarray(a_old)
+    n = len(a_old)
+    if n <= 1:
+        return np.array(a_old, copy=True)
+    NO = np.uint64(0xFFFFFFFFFFFFFFFF)
+    k = np.arange(1, n, dtype=np.uint64)
+    p = np.asarray(draws, dtype=np.uint64)[n - 1 - np.arange(1, n)]
+    keys = np.where(p != k, (p << np.uint64(32)) | k, NO)
+    keys = keys[np.argsort(keys >> np.uint64(32), kind="stable")]
+    valid = keys != NO
+    hi = (keys >> np.uint64(32)).astype(np.int64)
+    lo = (keys & np.uint64(0xFFFFFFFF)).astype(np.int64)
+    head = np.full(n, -1, np.int64)
+    start = valid.copy()
+    start[1:] &= hi[1:] != hi[:-1]
+    head[hi[start]] = lo[start]
+    root = np.arange(n)
+    while True:
+        h = head[root]
+        moved = h >= 0
+        if not moved.any():
+            break
+        root = np.where(moved, h, root)
+    v = a_old[root]
+    out = np.full(n, -12345, dtype=a_old.dtype)
+    nxt_same = np.zeros(len(keys), bool)
+    nxt_same[:-1] = valid[1:] & (hi[1:] == hi[:-1])
+    succ = np.full(len(keys), -1, np.int64)
+    succ[:-1] = np.where(nxt_same[:-1], lo[1:], -1)
+    idx = np.nonzero(valid)[0]
+    out[lo[idx]] = np.where(succ[idx] >= 0, v[np.maximum(succ[idx], 0)], a_old[hi[idx]])
+    self_k = np.nonzero(np.concatenate([[True], p == k]))[0]
+    out[self_k] = v[self_k]
+    return out

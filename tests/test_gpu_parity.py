@@ -153,24 +153,29 @@ def _lockstep_case(engine, n, F, seed, n_bins, max_leaves, max_depth, msl, mcw,
 
 
 @pytest.mark.parametrize("n", [1, 2, 3, 5, 64, 1000, 4099])
-def test_fisher_yates_device_adversarial(engine, n):
-    """GPU swaps against the sequential loop for draws no RNG would give:
-    one position chosen by every step, no swaps, a chain through all steps."""
+@pytest.mark.parametrize("form", ["lists", "sorted"])
+def test_fisher_yates_device_adversarial(engine, n, form, monkeypatch):
+    """GPU swaps (per-position lists, or the sorted (position, step) form)
+    against the sequential loop for draws no RNG would give: one position
+    chosen by every step, no swaps, a chain through all steps."""
     from test_sampler import _adversarial_draws
     import fy_model
+    monkeypatch.setenv("BSSCL_FY_SORTED", "1" if form == "sorted" else "0")
     a0 = np.random.default_rng(n).permutation(n).astype(np.int32)
     draws = _adversarial_draws(n) if n > 1 else {"empty": np.zeros(0, np.uint32)}
     for name, d in draws.items():
-        _announce(f"fisher-yates n={n} {name}")
+        _announce(f"fisher-yates n={n} {form} {name}")
         np.testing.assert_array_equal(engine.fisher_yates_apply(d, a0),
                                       fy_model.fisher_yates_sequential(a0, d), err_msg=name)
 
 
 @pytest.mark.parametrize("n", [7, 65_537, 1_000_003])
-def test_fisher_yates_device_equals_numpy_shuffle(engine, n):
+@pytest.mark.parametrize("form", ["lists", "sorted"])
+def test_fisher_yates_device_equals_numpy_shuffle(engine, n, form, monkeypatch):
     """The two halves (host draws, GPU swaps) equal RandomState.shuffle."""
     from bsscl_gbm import _native
-    _announce(f"fisher-yates mt n={n}")
+    monkeypatch.setenv("BSSCL_FY_SORTED", "1" if form == "sorted" else "0")
+    _announce(f"fisher-yates mt n={n} {form}")
     rng = np.random.RandomState(n)
     a = np.arange(n, dtype=np.int32)[::-1].copy()
     d, _, _ = _native.rs_draws(rng.get_state(), n)

@@ -137,6 +137,15 @@ def _adversarial_draws(n):
     }
 
 
+@pytest.mark.parametrize("n", [2, 3, 5, 64, 257, 1000, 4099])
+def test_fisher_yates_sorted_key_form_equals_sequential(n):
+    """The sorted (position, step) key form of the device kernels."""
+    a0 = np.random.default_rng(2).permutation(n).astype(np.int32)
+    for name, d in _adversarial_draws(n).items():
+        np.testing.assert_array_equal(fy_model.fisher_yates_sorted_keys(a0, d),
+                                      fy_model.fisher_yates_sequential(a0, d), err_msg=name)
+
+
 @pytest.mark.parametrize("n", [1, 2, 3, 5, 64, 1000, 4099])
 def test_fisher_yates_list_form_equals_sequential(n):
     a0 = np.random.default_rng(1).permutation(n).astype(np.int32)
