@@ -143,6 +143,7 @@ def run_gpu(name, steps, warmup):
             marks["breakdown"] = eng.stats()
             eng.set_profiling(0)
 
+    full_params = dict(params)
     params = dict(params, n_estimators=warmup + steps + BREAKDOWN_ROUNDS)
     est = HybridHistGBMNumbaV1_0_1(**params)
     est._round_hook = hook
@@ -159,12 +160,23 @@ def run_gpu(name, steps, warmup):
     est.predict_proba(Xp)
     t_pred_total = time.perf_counter() - t
     _progress(f"predict_proba on {len(Xp)} rows in {t_pred_total:.2f} s")
+    # A complete fit with the workload's own n_estimators: bin edges,
+    # binning and every boosting round, from host float32 X.
+    full = HybridHistGBMNumbaV1_0_1(**full_params)
+    t = time.perf_counter()
+    full.fit(X, y)
+    t_full = time.perf_counter() - t
+    fit_full = dict(n_estimators=int(full.n_trees_fitted_), seconds=round(t_full, 4),
+                    trees_per_s=round(full.n_trees_fitted_ / t_full, 2),
+                    binning_ms=round(full.times["binning"], 1),
+                    training_ms=round(full.times["training"], 1))
+    _progress(f"full fit: {fit_full}")
     s0, s1 = marks["s0"], marks["s1"]
     sampler = {k: (s1[k] - s0[k]) / max(s1["rounds"] - s0["rounds"], 1)
                for k in ("draw_ms", "gen_ms")}
     return dict(est=est, n=n, F=F, elapsed=elapsed, stats=st, t_fit=t_fit,
                 breakdown=marks["breakdown"], sampler=sampler,
-                t_pred_total=t_pred_total, pred_rows=len(Xp),
+                t_pred_total=t_pred_total, pred_rows=len(Xp), fit_full=fit_full,
                 t_pred_dev=est.times["inference"] / 1e3, params=params)
 
 
@@ -250,6 +262,7 @@ def main():
             "partition": round(bd["part_ms"] / BREAKDOWN_ROUNDS, 3),
             "split": round(bd["split_ms"] / BREAKDOWN_ROUNDS, 3),
         },
+        "fit_end_to_end": r["fit_full"],
         "nodes_expanded_per_tree": round(st["nodes_expanded"] / max(st["trees"], 1), 2),
         "host_ms_per_step": {
             "sampler_wait": round(st.get("sampler_wait_ms", 0.0) / a.steps, 3),

@@ -272,11 +272,13 @@ __global__ __launch_bounds__(64) void k_col_valid(const KT *__restrict__ keys, i
   m[col] = lo;
 }
 
-// Number of i in [1, m_col) with key[i] != key[i-1], added to out[col].
+// Number of i in [1, m_col) with key[i] != key[i-1], added to out[col]:
+// one atomic per block (a few dozen blocks per column).
 template <typename KT>
 __global__ __launch_bounds__(256) void k_col_changes(const KT *__restrict__ keys, int64_t ld,
                                                      const int64_t *__restrict__ m,
                                                      unsigned long long *__restrict__ out) {
+  __shared__ unsigned long long wsum[4];
   const int32_t col = (int32_t)blockIdx.y;
   const int64_t mc = m[col];
   const KT *k = keys + (int64_t)col * ld;
@@ -286,7 +288,12 @@ __global__ __launch_bounds__(256) void k_col_changes(const KT *__restrict__ keys
     c += (k[i] != k[i - 1]) ? 1ull : 0ull;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
-  if ((threadIdx.x & 63) == 0 && c) atomicAdd(out + col, c);
+  if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned long long t = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    if (t) atomicAdd(out + col, t);
+  }
 }
 
 // Positions of the first key of every run of equal keys in [0, m); at most
@@ -399,7 +406,7 @@ hipError_t launch_sort_u64(hipStream_t st, uint64_t *keys, uint64_t *tmp, int64_
 hipError_t launch_col_changes(hipStream_t st, const void *keys, int is_f64, int64_t ld, int32_t F,
                               const int64_t *m, int64_t max_m, unsigned long long *out) {
   if (F <= 0 || max_m <= 1) return hipSuccess;
-  const dim3 grid(grid_1d(max_m, 1024), (unsigned)F);
+  const dim3 grid(grid_1d(max_m, 64), (unsigned)F);
   if (is_f64)
     hipLaunchKernelGGL(k_col_changes<uint64_t>, grid, dim3(256), 0, st,
                        static_cast<const uint64_t *>(keys), ld, m, out);

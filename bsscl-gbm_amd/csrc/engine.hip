@@ -788,8 +788,7 @@ int launch_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_
   HIPCHK(launch_split(E->st, reinterpret_cast<const SplitTask *>(dv[3]), E->plan_d, 1,
                       E->segs.p, E->pool.p, E->node_stride, E->nb_sel_d, F_sel,
                       split_params(E, tp), E->cand.p, E->totals.p));
-  HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, E->plan_d, 1, 0,
-                          E->nodes_d));
+  // The root's table record is written by the level-0 planner.
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
@@ -819,7 +818,8 @@ int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParam
   HIPCHK(launch_plan(E->st, E->nodes_d, E->plan_d, E->parents_d[(level + 1) & 1].p,
                      E->parents_d[level & 1].p, E->tile_begin_d.p, E->hist_begin_d.p,
                      E->tiles_d.p, E->hist_tasks_d.p, E->split_tasks_d.p,
-                     E->work_flag_d.p, E->work_e_d.p, pa));
+                     E->work_flag_d.p, E->work_e_d.p, E->segs.p, E->totals.p, E->cand.p,
+                     F_sel, pa));
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
@@ -887,8 +887,7 @@ int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
   HIPCHK(launch_split(E->st, E->split_tasks_d.p, E->plan_d, S,
                       E->segs.p, E->pool.p, E->node_stride, E->nb_sel_d, F_sel,
                       split_params(E, tp), E->cand.p, E->totals.p));
-  HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, E->plan_d,
-                          std::min(2 * P, 4096), 0, E->nodes_d));
+  // The new nodes' table records are written by the next level's planner.
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
@@ -955,7 +954,7 @@ int ensure_round_out(bsscl_engine *E, int b, int32_t M) {
 // Shuffles of at least this many positions build their step lists by
 // sorting (position, step) keys; shorter ones use per-position linked
 // lists.  (Test hook: BSSCL_FY_SORTED=1 or 0 forces one form.)
-constexpr int64_t kFySortedMin = 1 << 16;
+constexpr int64_t kFySortedMin = 1 << 21;
 
 int ensure_fy_work(bsscl_engine *E, int64_t n, FyWork &w) {
   for (DevBuf<int32_t> *x : {&E->fy_head, &E->fy_next, &E->fy_v}) CHK(x->ensure((size_t)n));
@@ -2090,9 +2089,13 @@ int bsscl_node_split(bsscl_engine *E, const double *grad, const double *hess,
   TreeParams tp{1, 1, 0, min_child_weight, reg_lambda, 0.0};
   CHK(prepare_tree_buffers(E, m, F_sel, 1, 2));
   CHK(launch_root(E, false, m, feats, nb_sel, tp));
+  // No planner follows this root: write its table record here.
+  HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, E->plan_d, 1, 0,
+                          E->nodes_d));
   LevelPlan plan;
   CHK(read_table(E, 1, plan));
   const NodeOut root = *reinterpret_cast<const NodeOut *>(E->table_pin + 64);
+  if (root.fpos >= F_sel) return set_error(BSSCL_EINTERNAL, "node_split: bad split record");
   if (out_G || out_H) {
     std::vector<long long> h((size_t)E->node_stride);
     HIPCHK(hipMemcpyAsync(h.data(), E->pool.p, (size_t)E->node_stride * 8, hipMemcpyDeviceToHost, E->st));

@@ -263,7 +263,8 @@ hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                        int32_t *tile_begin, int32_t *hist_begin,
                        PartTile *tiles, HistTask *hist_tasks,
                        SplitTask *split_tasks, int32_t *work_flag,
-                       double *work_e, PlanArgs a);
+                       double *work_e, const NodeSeg *segs, const long long *totals,
+                       const SplitCand *cand, int32_t F_sel, PlanArgs a);
 hipError_t launch_code_counts(hipStream_t st, const uint8_t *codes, int64_t ld,
                               int64_t n, int32_t F, unsigned int *counts);
 // F += lr * tree(row) for every row unless *node_count_d == 0 (then F is

@@ -1243,9 +1243,42 @@ hipError_t launch_child_totals(hipStream_t st, const PartParent *parents,
   return hipGetLastError();
 }
 
-// Per node: the best split over features -- the largest gain, the lowest
-// feature position on ties (est:618-621) -- with the node's segment and
-// fixed-point totals, into the node table (not yet expanded: left = -1).
+// A node's table record: its segment, fixed-point totals and best split
+// over the features -- the largest gain, the lowest feature position on
+// ties (est:618-621) -- not yet expanded (left = -1).  One thread.
+__device__ __forceinline__ NodeOut node_record(int32_t node, const NodeSeg *__restrict__ segs,
+                                               const long long *__restrict__ totals,
+                                               const SplitCand *__restrict__ cand,
+                                               int32_t F_sel) {
+  const NodeSeg s = segs[node];
+  double best = 0.0;
+  int32_t bf = -1, bb = 0;
+  if (s.valid) {
+    for (int32_t f = 0; f < F_sel; ++f) {
+      const SplitCand c = cand[(int64_t)node * F_sel + f];
+      if (c.bin >= 0 && (bf < 0 || c.gain > best)) {
+        best = c.gain;
+        bf = f;
+        bb = c.bin;
+      }
+    }
+  }
+  NodeOut o;
+  o.start = s.start;
+  o.count = s.count;
+  o.valid = s.valid;
+  o.Gq = s.valid ? totals[2 * (int64_t)node] : 0;
+  o.Hq = s.valid ? totals[2 * (int64_t)node + 1] : 0;
+  o.gain = bf >= 0 ? best : -1e9;
+  o.e = 0.0;
+  o.fpos = bf;
+  o.bin = bf >= 0 ? bb : 0;
+  o.left = -1;
+  return o;
+}
+
+// Per node: node_record with one wave over the features (the last level,
+// whose children have no planner after them).
 __global__ __launch_bounds__(256) void k_node_best(
     const NodeSeg *__restrict__ segs, const long long *__restrict__ totals,
     const SplitCand *__restrict__ cand, int32_t F_sel,
@@ -1339,7 +1372,9 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
     int32_t *__restrict__ tile_begin, int32_t *__restrict__ hist_begin,
     PartTile *__restrict__ tiles, HistTask *__restrict__ hist_tasks,
     SplitTask *__restrict__ split_tasks, int32_t *__restrict__ work_flag,
-    double *__restrict__ work_e, PlanArgs a) {
+    double *__restrict__ work_e, const NodeSeg *__restrict__ segs,
+    const long long *__restrict__ totals, const SplitCand *__restrict__ cand, int32_t F_sel,
+    PlanArgs a) {
   __shared__ uint32_t stmp[kPlanBlock / 64];
   __shared__ double ke[kPlanChunk];
   __shared__ unsigned long long s_rows;
@@ -1349,10 +1384,11 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
   const int32_t first = prev.first_child, nc = prev.n_split, n_prev = prev.n_nodes;
   if (tid == 0) s_rows = 0ull;
 
-  // Candidates: rank and whether they may be split (est:649-652, 762-801).
+  // Candidates: their table records (best split over the features), rank
+  // and whether they may be split (est:649-652, 762-801).
   for (int j = tid; j < nc; j += kPlanBlock) {
     const int c = first + j;
-    const NodeOut N = nodes[c];
+    NodeOut N = node_record(c, segs, totals, cand, F_sel);
     double e = 0.0;
     int32_t f = 0;
     if (N.valid) {
@@ -1360,7 +1396,8 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
       e = pe < N.gain ? pe : N.gain;
       f = (N.fpos >= 0 && N.gain > a.gamma) ? 1 : 0;
     }
-    nodes[c].e = e;
+    N.e = e;
+    nodes[c] = N;
     work_e[j] = e;
     work_flag[j] = f;
   }
@@ -1525,10 +1562,12 @@ hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                        int32_t *tile_begin, int32_t *hist_begin,
                        PartTile *tiles, HistTask *hist_tasks,
                        SplitTask *split_tasks, int32_t *work_flag,
-                       double *work_e, PlanArgs a) {
+                       double *work_e, const NodeSeg *segs, const long long *totals,
+                       const SplitCand *cand, int32_t F_sel, PlanArgs a) {
   hipLaunchKernelGGL(k_plan, dim3(1), dim3(kPlanBlock), 0, st, nodes, plan,
                      prev_parents, parents, tile_begin, hist_begin, tiles,
-                     hist_tasks, split_tasks, work_flag, work_e, a);
+                     hist_tasks, split_tasks, work_flag, work_e, segs, totals, cand, F_sel,
+                     a);
   return hipGetLastError();
 }
 
