@@ -545,41 +545,67 @@ __device__ __forceinline__ void hist_item(
   const int64_t g0 = r0 >> 4, g1 = (r1 + 15) >> 4;
   for (int64_t g = g0 + threadIdx.x; g < g1; g += kHistBlock) {
     const int64_t row = g << 4;
+    // Every load of the step first: (g,h) of the 16 rows, then each
+    // feature's 16 codes.
     const int4 *gp = reinterpret_cast<const int4 *>(gh_c + row);
+    int4 ghv[kHistRows / 2];
+#pragma unroll
+    for (int q = 0; q < kHistRows / 2; ++q) ghv[q] = gp[q];
+    uint4 cv[FC];
+#pragma unroll
+    for (int u = 0; u < FC; ++u)
+      if (u < nf) cv[u] = *reinterpret_cast<const uint4 *>(codes_c + (int64_t)(f0 + u) * ld_c + row);
+    // Rows [klo, khi) of the group lie in the tile: all 16 except at a
+    // node's first and last groups.  Rows outside add zero.
+    const int klo = (int)max((int64_t)0, min((int64_t)kHistRows, r0 - row));
+    const int khi = (int)max((int64_t)0, min((int64_t)kHistRows, r1 - row));
     int gq[kHistRows], hq[kHistRows];
 #pragma unroll
     for (int q = 0; q < kHistRows / 2; ++q) {
-      const int4 v = gp[q];
-      gq[2 * q] = v.x;
-      hq[2 * q] = v.y;
-      gq[2 * q + 1] = v.z;
-      hq[2 * q + 1] = v.w;
+      gq[2 * q] = ghv[q].x;
+      hq[2 * q] = ghv[q].y;
+      gq[2 * q + 1] = ghv[q].z;
+      hq[2 * q + 1] = ghv[q].w;
     }
+    if (klo != 0 || khi != kHistRows) {
 #pragma unroll
-    for (int k = 0; k < kHistRows; ++k) {
-      const bool in = (row + k >= r0) && (row + k < r1);
-      gq[k] = in ? gq[k] : 0;
-      hq[k] = in ? hq[k] : 0;
+      for (int k = 0; k < kHistRows; ++k) {
+        const bool in = k >= klo && k < khi;
+        gq[k] = in ? gq[k] : 0;
+        hq[k] = in ? hq[k] : 0;
+      }
     }
 #pragma unroll
     for (int u = 0; u < FC; ++u) {
       if (u < nf) {
-        const uint4 c = *reinterpret_cast<const uint4 *>(codes_c + (int64_t)(f0 + u) * ld_c + row);
-        const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+        const uint32_t cw[4] = {cv[u].x, cv[u].y, cv[u].z, cv[u].w};
         unsigned long long *hf = lh + u * kHistPerFeat * C + copy;
+        if (hb[u] == 0xffffffffu) {
+          // No frequent bin (the same for the whole block): every row is
+          // one pair of LDS adds, without a branch.
 #pragma unroll
-        for (int k = 0; k < kHistRows; ++k) {
-          const uint32_t bin = min((cw[k >> 2] >> (8 * (k & 3))) & 255u, lim[u]);
-          // The feature's most frequent bin (NaN, zeros) is summed in
-          // registers: same-address LDS atomics within a wave serialise.
-          if (bin == hb[u]) {
-            ag[u] += gq[k];
-            ah[u] += hq[k];
-          } else {
+          for (int k = 0; k < kHistRows; ++k) {
+            const uint32_t bin = min((cw[k >> 2] >> (8 * (k & 3))) & 255u, lim[u]);
             __hip_atomic_fetch_add(hf + bin * C, (unsigned long long)(long long)gq[k],
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             __hip_atomic_fetch_add(hf + (kBins + bin) * C, (unsigned long long)(long long)hq[k],
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < kHistRows; ++k) {
+            const uint32_t bin = min((cw[k >> 2] >> (8 * (k & 3))) & 255u, lim[u]);
+            // The feature's most frequent bin (NaN, zeros) is summed in
+            // registers: same-address LDS atomics within a wave serialise.
+            if (bin == hb[u]) {
+              ag[u] += gq[k];
+              ah[u] += hq[k];
+            } else {
+              __hip_atomic_fetch_add(hf + bin * C, (unsigned long long)(long long)gq[k],
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+              __hip_atomic_fetch_add(hf + (kBins + bin) * C, (unsigned long long)(long long)hq[k],
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
           }
         }
       }

@@ -3,6 +3,8 @@
 // u64), with 256 and 16 distinct bins per block.  Each block owns a 4-feature
 // histogram in LDS; bins come from 8 independent xorshift streams.
 // Build: hipcc --offload-arch=gfx950 -O3 -munsafe-fp-atomics -o lds_atomics lds_atomics.hip
+#include <hip/hip_runtime.h>
+
 #include <cstdio>
 #include <cstdint>
 #define CHECK(x) do { hipError_t e=(x); if(e!=hipSuccess){printf("err %s line %d\n", hipGetErrorString(e), __LINE__); return 1;} } while(0)
