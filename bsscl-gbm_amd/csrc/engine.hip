@@ -193,6 +193,11 @@ using namespace bsscl;
 struct bsscl_engine {
   int32_t device = 0;
   hipStream_t st = nullptr;
+  // A boosting round's in-bag rows (Fisher-Yates, sort) are made on their
+  // own stream, so the next round's rows are ready while this round's tree
+  // is built; the tree stream waits on rows_ready of its slot.
+  hipStream_t st_rows = nullptr;
+  hipEvent_t rows_ready[2] = {nullptr, nullptr};
   int32_t n_cu = 256;
   size_t max_lds = 64 * 1024;
   Matrix mat[2];
@@ -212,7 +217,7 @@ struct bsscl_engine {
   DevBuf<int32_t> rid_c[2];
   bool track_rid = false;  // carry row ids through the partition (bsscl_partition)
   int64_t ld_c = 0;
-  DevBuf<int32_t> rows32;
+  DevBuf<int32_t> round_rows[2];  // in-bag rows of round slot s, ascending
   DevBuf<int64_t> rows64;
   DevBuf<int32_t> rows_in, sort_tmp;
   // Row permutation of a device-rows sampler (cumulative over its rounds)
@@ -726,7 +731,8 @@ SplitParams split_params(bsscl_engine *E, const TreeParams &tp) {
 
 // Root: gather the in-bag rows into set 0, its histogram and split search.
 // The feature list, the root's tasks and its LevelPlan go up in one copy.
-int launch_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_t> &feats,
+int launch_root(bsscl_engine *E, const int32_t *rows32, int64_t m,
+                const std::vector<int32_t> &feats,
                 const std::vector<int32_t> &nb_sel, const TreeParams &tp) {
   const Matrix &X = E->mat[0];
   const int32_t F_sel = (int32_t)feats.size();
@@ -766,8 +772,7 @@ int launch_root(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_
   E->nb_sel_d = reinterpret_cast<const int32_t *>(dv[1]);
   E->hot_sel_d = E->nb_sel_d + F_sel;
   HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, feat_d, F_sel,
-                            use32 ? E->rows32.p : nullptr,
-                            use32 ? nullptr : E->rows64.p, m, E->ghq.p,
+                            rows32, rows32 ? nullptr : E->rows64.p, m, E->ghq.p,
                             E->codes_c[0].p, E->ld_c, E->gh_c[0].p,
                             E->track_rid ? E->rid_c[0].p : nullptr,
                             E->ld_c, E->segs.p, E->hist_node_d.p));
@@ -987,12 +992,13 @@ constexpr int32_t kLevelsPerCheck = 8;  // levels enqueued between host checks
 // kLevelsPerCheck levels the host reads the plan and stops enqueueing once
 // the tree has ended (unless `checks` is false: then every level is
 // enqueued).  *run = levels enqueued.
-int launch_tree(bsscl_engine *E, bool use32, int64_t m, const std::vector<int32_t> &feats,
+int launch_tree(bsscl_engine *E, const int32_t *rows32, int64_t m,
+                const std::vector<int32_t> &feats,
                 const std::vector<int32_t> &nb_sel, const TreeParams &tp, int32_t *run,
                 bool checks = true) {
   const int32_t F_sel = (int32_t)feats.size();
   const int32_t levels = std::max(1, tp.max_depth);
-  CHK(launch_root(E, use32, m, feats, nb_sel, tp));
+  CHK(launch_root(E, rows32, m, feats, nb_sel, tp));
   *run = 0;
   for (int32_t d = 0; d < levels; ++d) {
     const bool last = d + 1 >= tp.max_depth;
@@ -1036,11 +1042,12 @@ void tree_stats(bsscl_engine *E, const NodeOut *t, int32_t n, int64_t m, int32_t
   E->stats[8] += 1.0;
 }
 
-// Builds one tree from the rows already in E->rows32 (use32) or E->rows64,
+// Builds one tree from the rows already in rows32 (device, int32) or, when
+// rows32 is null, E->rows64,
 // with quantized gradients in E->ghq, and replays the reference's candidate
 // loop on the host.  The node table comes back once (twice when it had to
 // grow).
-int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
+int build_tree_core(bsscl_engine *E, const int32_t *rows32, int64_t m,
                     const std::vector<int32_t> &feats,
                     const std::vector<int32_t> &nb_sel, const TreeParams &tp,
                     TreeOut &out, HNode *root_out = nullptr) {
@@ -1050,7 +1057,7 @@ int build_tree_core(bsscl_engine *E, bool use32, int64_t m,
   for (;;) {
     CHK(prepare_tree_buffers(E, m, F_sel, levels, tp.max_leaves));
     int32_t run = 0;
-    CHK(launch_tree(E, use32, m, feats, nb_sel, tp, &run));
+    CHK(launch_tree(E, rows32, m, feats, nb_sel, tp, &run));
     CHK(read_table(E, table_bound(E, run), plan));
     if (plan.overflow < 0) return set_error(BSSCL_EINTERNAL, "tree builder: level list overflow");
     if (plan.overflow == 0) break;
@@ -1217,7 +1224,9 @@ bool pipeline_safe(bsscl_engine *E, const RoundArgs &a, bsscl_sampler *sampler) 
 int drain_rounds(bsscl_engine *E, int s) {
   RoundSlot &r = E->rslot[s];
   if (!r.active) return BSSCL_OK;
-  const hipError_t e = hipStreamSynchronize(E->st);
+  hipError_t e = hipStreamSynchronize(E->st_rows);
+  const hipError_t e2 = hipStreamSynchronize(E->st);
+  if (e == hipSuccess) e = e2;
   sampler_give_back(r.sampler, r.token);
   r.active = false;
   r.token = nullptr;
@@ -1261,6 +1270,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   R.M = 2 * a.max_leaves + 2;
   R.run = 0;
   auto fail = [&](int rc) {
+    (void)hipStreamSynchronize(E->st_rows);
     (void)hipStreamSynchronize(E->st);
     sampler_give_back(sampler, token);
     R.active = false;
@@ -1286,14 +1296,19 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     }
   }
   // The round's in-bag rows on the device, ascending: the reference's
-  // sample_idx (a prefix of the cumulative permutation) sorted.
+  // sample_idx (a prefix of the cumulative permutation) sorted.  Made on
+  // the rows stream; only that stream touches the permutation, the
+  // Fisher-Yates arrays, the row flags and round_rows[s] until rows_ready[s].
+  // (round_rows[s] was last read by the tree of the round before the
+  // previous one, which finish_round has waited for.)
   const int64_t n_pad = sort_rows_flag_bytes(X.n);
-  if (rc == BSSCL_OK) rc = E->rows32.ensure((size_t)m);
+  hipStream_t rs = E->st_rows;
+  if (rc == BSSCL_OK) rc = E->round_rows[s].ensure((size_t)m);
   if (rc == BSSCL_OK) rc = E->sort_tmp.ensure((size_t)(n_pad / 4096 + 1));
   if (rc == BSSCL_OK && E->row_flags_n != n_pad) {
     rc = E->row_flags.ensure((size_t)n_pad);
     if (rc == BSSCL_OK) {
-      hipError_t e = hipMemsetAsync(E->row_flags.p, 0, (size_t)n_pad, E->st);
+      hipError_t e = hipMemsetAsync(E->row_flags.p, 0, (size_t)n_pad, rs);
       if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("flags: ") + hipGetErrorString(e));
       else E->row_flags_n = n_pad;
     }
@@ -1302,7 +1317,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     hipError_t e = hipSuccess;
     const int32_t *rows_d = nullptr;
     if (!sh.do_rows) {
-      e = launch_iota(E->st, E->rows32.p, m);  // every row, in order
+      e = launch_iota(rs, E->round_rows[s].p, m);  // every row, in order
     } else if (sh.device_rows) {
       if (sh.device != E->device)
         rc = set_error(BSSCL_EINVAL, "boost_round: the sampler copies its draws to another GPU");
@@ -1315,7 +1330,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
           E->perm_cur = 0;
           E->perm_sampler = sampler;
           E->perm_next_round = 0;
-          e = launch_iota(E->st, E->perm[0].p, X.n);
+          e = launch_iota(rs, E->perm[0].p, X.n);
         }
       } else if (E->perm_sampler != sampler || E->perm_next_round != sr.round) {
         rc = set_error(BSSCL_EINVAL, "boost_round: the sampler's earlier rounds did not run on this engine");
@@ -1323,10 +1338,10 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
       FyWork w;
       if (rc == BSSCL_OK) rc = ensure_fy_work(E, X.n, w);
       // The sampler copied the draws on its own stream.
-      if (rc == BSSCL_OK && e == hipSuccess) e = hipStreamWaitEvent(E->st, sr.draws_copied, 0);
+      if (rc == BSSCL_OK && e == hipSuccess) e = hipStreamWaitEvent(rs, sr.draws_copied, 0);
       if (rc == BSSCL_OK && e == hipSuccess) {
         const int nxt = E->perm_cur ^ 1;
-        e = launch_fisher_yates(E->st, sr.draws_dev, X.n, E->perm[E->perm_cur].p,
+        e = launch_fisher_yates(rs, sr.draws_dev, X.n, E->perm[E->perm_cur].p,
                                 E->perm[nxt].p, w);
         E->perm_cur = nxt;
         E->perm_next_round = sr.round + 1;
@@ -1334,11 +1349,16 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
       }
     } else {
       rc = E->rows_in.ensure((size_t)m);
-      if (rc == BSSCL_OK) e = hipMemcpyAsync(E->rows_in.p, sr.rows, (size_t)m * 4, hipMemcpyHostToDevice, E->st);
+      if (rc == BSSCL_OK) e = hipMemcpyAsync(E->rows_in.p, sr.rows, (size_t)m * 4, hipMemcpyHostToDevice, rs);
       rows_d = E->rows_in.p;
     }
     if (rc == BSSCL_OK && e == hipSuccess && rows_d)
-      e = launch_sort_rows(E->st, rows_d, m, E->row_flags.p, n_pad, E->sort_tmp.p, E->rows32.p);
+      e = launch_sort_rows(rs, rows_d, m, E->row_flags.p, n_pad, E->sort_tmp.p,
+                           E->round_rows[s].p);
+    if (rc == BSSCL_OK && e == hipSuccess && !E->rows_ready[s])
+      e = hipEventCreateWithFlags(&E->rows_ready[s], hipEventDisableTiming);
+    if (rc == BSSCL_OK && e == hipSuccess) e = hipEventRecord(E->rows_ready[s], rs);
+    if (rc == BSSCL_OK && e == hipSuccess) e = hipStreamWaitEvent(E->st, E->rows_ready[s], 0);
     if (rc == BSSCL_OK && e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("rows: ") + hipGetErrorString(e));
   }
   if (rc != BSSCL_OK) return fail(rc);
@@ -1356,7 +1376,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     rc = prepare_tree_buffers(E, m, F_sel, std::max(1, a.max_depth), a.max_leaves);
   if (rc == BSSCL_OK) rc = ensure_round_out(E, s, R.M);
   if (rc == BSSCL_OK && R.device_replay)
-    rc = launch_tree(E, true, m, R.feats, R.nb_sel, tp, &R.run, !E->pipeline);
+    rc = launch_tree(E, E->round_rows[s].p, m, R.feats, R.nb_sel, tp, &R.run, !E->pipeline);
   if (rc == BSSCL_OK && R.device_replay) {
     RoundHeader *hdr = reinterpret_cast<RoundHeader *>(E->round_d[s].p);
     ReplayArgs ra;
@@ -1448,7 +1468,7 @@ int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
   // F was left alone: build the tree on the host-driven path and apply it.
   // (Never with a round enqueued behind this one: see pipeline_safe.)
   if (h.status == 1) E->node_cap_floor = std::max(h.needed, 2 * E->node_cap);
-  CHK(build_tree_core(E, true, R.m, R.feats, R.nb_sel, tp, out));
+  CHK(build_tree_core(E, E->round_rows[s].p, R.m, R.feats, R.nb_sel, tp, out));
   CHK(upload_tree(E, out.features, out.thresholds, out.values, out.left, out.right,
                   *out.node_count, X.F));
   const int nb = update_F_blocks(X.n);
@@ -1494,7 +1514,9 @@ int bsscl_engine_create(int32_t device, bsscl_engine **out) {
   if (!E) return set_error(BSSCL_ENOMEM, "engine allocation failed");
   E->device = device;
   hipError_t e = hipStreamCreateWithFlags(&E->st, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&E->st_rows, hipStreamNonBlocking);
   if (e != hipSuccess) {
+    if (E->st) (void)hipStreamDestroy(E->st);
     delete E;
     return set_error(BSSCL_EDEVICE, std::string("hipStreamCreate: ") + hipGetErrorString(e));
   }
@@ -1511,6 +1533,7 @@ int bsscl_engine_create(int32_t device, bsscl_engine **out) {
 void bsscl_engine_destroy(bsscl_engine *E) {
   if (!E) return;
   (void)hipSetDevice(E->device);
+  if (E->st_rows) (void)hipStreamSynchronize(E->st_rows);
   if (E->st) (void)hipStreamSynchronize(E->st);
   // A round enqueued ahead hands its sampler buffers back (the sampler
   // outlives the rounds it feeds).
@@ -1528,7 +1551,7 @@ void bsscl_engine_destroy(bsscl_engine *E) {
     E->gh_c[s].release();
     E->rid_c[s].release();
   }
-  E->rows32.release();
+  for (auto &r : E->round_rows) r.release();
   E->rows64.release();
   E->rows_in.release();
   E->sort_tmp.release();
@@ -1576,6 +1599,9 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->xstage.release();
   E->col_keys.release();
   for (hipEvent_t ev : E->ev_pool) (void)hipEventDestroy(ev);
+  for (hipEvent_t ev : E->rows_ready)
+    if (ev) (void)hipEventDestroy(ev);
+  if (E->st_rows) (void)hipStreamDestroy(E->st_rows);
   if (E->st) (void)hipStreamDestroy(E->st);
   delete E;
 }
@@ -1862,7 +1888,7 @@ int bsscl_build_tree(bsscl_engine *E, const double *grad, const double *hess,
                         hipMemcpyHostToDevice, E->st));
   TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight,
                 reg_lambda, gamma};
-  return build_tree_core(E, false, n_samples, feats, nb_sel, tp, out);
+  return build_tree_core(E, nullptr, n_samples, feats, nb_sel, tp, out);
 }
 
 int bsscl_boost_begin(bsscl_engine *E, const int64_t *y, int64_t n, double w0,
@@ -2088,7 +2114,7 @@ int bsscl_node_split(bsscl_engine *E, const double *grad, const double *hess,
   const int32_t F_sel = n_selected;
   TreeParams tp{1, 1, 0, min_child_weight, reg_lambda, 0.0};
   CHK(prepare_tree_buffers(E, m, F_sel, 1, 2));
-  CHK(launch_root(E, false, m, feats, nb_sel, tp));
+  CHK(launch_root(E, nullptr, m, feats, nb_sel, tp));
   // No planner follows this root: write its table record here.
   HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, E->plan_d, 1, 0,
                           E->nodes_d));
@@ -2180,6 +2206,7 @@ int bsscl_fisher_yates_apply(bsscl_engine *E, const uint32_t *draws, int64_t n,
                                          " exceeds its step " + std::to_string(n - 1 - t));
   if (n <= 1) return BSSCL_OK;
   HIPCHK(hipSetDevice(E->device));
+  HIPCHK(hipStreamSynchronize(E->st_rows));  // the work arrays are shared with the rounds
   DevBuf<int32_t> a, b;
   DevBuf<uint32_t> d;
   FyWork w;
