@@ -391,10 +391,11 @@ class Sampler:
         return key, int(pos[0])
 
     def stats(self):
-        out = np.zeros(4, np.float64)
+        out = np.zeros(6, np.float64)
         n = np.zeros(1, np.int32)
-        check(lib().bsscl_sampler_stats(self.handle, ptr(out), 4, ptr(n)))
-        return dict(rounds=out[0], draw_ms=out[1], swap_ms=out[2], gen_ms=out[3])
+        check(lib().bsscl_sampler_stats(self.handle, ptr(out), 6, ptr(n)))
+        return dict(rounds=out[0], draw_ms=out[1], swap_ms=out[2], gen_ms=out[3],
+                    spec_chunks=out[4], seq_chunks=out[5])
 
     def close(self):
         if getattr(self, "_h", None) is not None:

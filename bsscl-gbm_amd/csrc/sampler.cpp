@@ -48,6 +48,7 @@
 #include <algorithm>
 #include <atomic>
 #include <chrono>
+#include <cmath>
 #include <condition_variable>
 #include <cstdlib>
 #include <cstring>
@@ -276,6 +277,7 @@ struct Stream {
   const std::atomic<bool> *halt = nullptr;
   std::atomic<double> *gen_ms = nullptr;  // time spent generating
   bool vec = false;
+  bool key_is_next = true;  // key[] is the next chunk's first block (else: its predecessor)
 
   // Positions the stream at word pos0 of the state key0.
   bool start(const uint32_t *key0, int pos0, const std::atomic<bool> *h, std::atomic<double> *ms) {
@@ -284,8 +286,24 @@ struct Stream {
     halt = h;
     gen_ms = ms;
     vec = use_avx512();
+    key_is_next = true;
     if (!next_chunk()) return false;
     p = base + pos0;  // block 0 starts at the given position
+    return true;
+  }
+
+  // Positions the stream at word `off` of chunk c, whose first block has
+  // state key_c.
+  bool seek(int64_t c, int64_t off, const uint32_t *key_c, const std::atomic<bool> *h) {
+    std::memcpy(key, key_c, sizeof(key));
+    buf.resize((size_t)kChunkWords);
+    halt = h;
+    gen_ms = nullptr;
+    vec = use_avx512();
+    chunk = c - 1;
+    key_is_next = true;
+    if (!next_chunk()) return false;
+    p = base + off;
     return true;
   }
 
@@ -297,7 +315,7 @@ struct Stream {
     const auto t0 = std::chrono::steady_clock::now();
     uint32_t *o = buf.data();
     for (int b = 0; b < kChunkBlocks; ++b, o += kN) {
-      if (chunk > 0 || b > 0) {
+      if (b > 0 || !key_is_next) {
         if (vec) twist_avx512(key);
         else twist_scalar(key);
       }
@@ -308,6 +326,7 @@ struct Stream {
         for (int k = 0; k < kN; ++k) o[k] = temper(key[k]);
       }
     }
+    key_is_next = false;
     if (gen_ms)
       gen_ms->store(gen_ms->load(std::memory_order_relaxed) +
                         std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count(),
@@ -470,14 +489,27 @@ bool draw_steps_avx512(Stream &s, uint32_t hi, uint32_t *out) {
 }
 
 // ---------------------------------------------------------------------------
-// Parallel draws.  Which words a shuffle accepts is a strictly sequential
-// question (word t is tested against i, which counts the words accepted
-// before it), but answering it needs no stores: a counting pass walks the
-// stream with the same tests as draw_steps_avx512 and, at the first word it
-// reads in each chunk, records a segment (the chunk's first-block state, the
-// word offset, the current i).  Worker threads then regenerate each
-// segment's chunk from that state and write its draws, out[hi - i], with
-// masked stores, so segments never touch each other's entries.
+// Parallel draws.  Which words a shuffle accepts is a sequential question
+// (word t is tested against the step i, which counts the words accepted
+// before it), but its dependence on the step a chunk of words starts at is
+// simple.  Run two copies of the test from entry steps e and e + 1 over the
+// same words: a word v <= e is accepted by both, v > e + 1 by neither, and
+// v = e + 1 is accepted by the upper one only, after which both sit at e
+// and stay together.  So the trajectories of a whole window of entries
+// [lo, hi] (one mask range) always occupy an interval [a, b] of steps: a word
+// v <= a moves it down by one, v > b leaves it, and a < v <= b merges the
+// trajectories at v - 1 and v (b drops by one).  A chunk's transfer function
+// over its window is therefore the exit of the lowest entry plus the list of
+// merges, which worker threads compute for every chunk of a round at once,
+// each around the step the chunk is expected to start at.  The draw thread
+// then walks the chunks in order with the true entry step, which maps
+// through a chunk in O(merges); a chunk whose entry falls outside its window,
+// whose window crosses a mask range, or that holds the round's last steps is
+// counted word by word.  Each chunk becomes a segment (the chunk's first-
+// block state, the first word, the entry step) whose draws, out[hi - i],
+// worker threads write with masked stores, so segments never touch each
+// other's entries.  The chunks' first-block states come from a twister
+// thread that runs ahead of the stream.
 // ---------------------------------------------------------------------------
 struct Segment {
   uint32_t key[kN];  // state of the chunk's first block (before tempering)
@@ -496,44 +528,139 @@ __attribute__((target("avx512f"))) void gen_chunk(const uint32_t *key0, uint32_t
   }
 }
 
-// Counting pass of the draws of steps hi .. 1 (the acceptance tests of
-// draw_steps_avx512, without stores); emit(key, w0, i) opens a segment at
-// the first word read from each chunk.  False if the stream stops.
-template <class Emit>
+// Windows never reach below this step (a transfer function must not hold
+// the round's end, where the words go on to the feature shuffle).
+constexpr uint32_t kSpecMin = 4096;
+constexpr int32_t kMaxMerges = 4096;
+
+// Transfer function of one chunk over the entry window [lo, hi]: entry e
+// leaves the chunk at a_exit + g(e), g(e) = (e - lo) lowered by one for
+// every merge m (in order) below it.
+struct ChunkFn {
+  std::atomic<int32_t> state{0};  // 0 pending, 1 ready, 2 not available (count word by word)
+  uint32_t lo = 0, hi = 0, a_exit = 0;
+  int32_t nm = 0;
+  std::vector<uint32_t> m;  // lower group of each merge, in order
+};
+
+inline uint32_t chunk_exit(const ChunkFn &f, uint32_t e) {
+  uint32_t g = e - f.lo;
+  for (int32_t t = 0; t < f.nm; ++t) g -= g > f.m[t] ? 1u : 0u;
+  return f.a_exit + g;
+}
+
+// The transfer function of a whole chunk of words over [lo, hi]; false if
+// the window crosses a mask range, comes within kSpecMin of the round's end
+// or merges more than kMaxMerges times.
 __attribute__((target("avx512f,avx512vl,avx512bw,popcnt")))
-bool count_steps_avx512(Stream &s, uint32_t hi, Emit &&emit) {
-  uint32_t i = hi;
-  int64_t open_chunk = -1;
-  while (i >= 1) {
+bool spec_chunk_avx512(const uint32_t *words, uint32_t lo, uint32_t hi, ChunkFn &f) {
+  uint32_t a = lo, b = hi;
+  int32_t nm = 0;
+  f.m.clear();
+  const uint32_t *p = words, *const e = words + kChunkWords;
+  while (p < e) {
+    if (a < kSpecMin) return false;
+    const int k = 31 - __builtin_clz(a);
+    if (31 - __builtin_clz(b) != k) return false;
+    const uint32_t lo_pow = 1u << k;
+    const uint32_t mask = lo_pow | (lo_pow - 1);
+    const __m512i vm = _mm512_set1_epi32((int)mask);
+    // 64 words with none in (a - 63, b]: each is accepted by every
+    // trajectory (v <= a - 63 <= the lowest one's step) or by none (v > b).
+    while (a - lo_pow >= 64 && e - p >= 64) {
+      const __m512i sa = _mm512_set1_epi32((int)(a - 63));
+      const __m512i sb = _mm512_set1_epi32((int)b);
+      const __m512i v0 = _mm512_and_si512(_mm512_loadu_si512(p), vm);
+      const __m512i v1 = _mm512_and_si512(_mm512_loadu_si512(p + 16), vm);
+      const __m512i v2 = _mm512_and_si512(_mm512_loadu_si512(p + 32), vm);
+      const __m512i v3 = _mm512_and_si512(_mm512_loadu_si512(p + 48), vm);
+      const __mmask16 amb =
+          _mm512_mask_cmple_epu32_mask(_mm512_cmpgt_epu32_mask(v0, sa), v0, sb) |
+          _mm512_mask_cmple_epu32_mask(_mm512_cmpgt_epu32_mask(v1, sa), v1, sb) |
+          _mm512_mask_cmple_epu32_mask(_mm512_cmpgt_epu32_mask(v2, sa), v2, sb) |
+          _mm512_mask_cmple_epu32_mask(_mm512_cmpgt_epu32_mask(v3, sa), v3, sb);
+      if (amb) break;
+      const uint64_t all = (uint64_t)_mm512_cmple_epu32_mask(v0, sa) |
+                           ((uint64_t)_mm512_cmple_epu32_mask(v1, sa) << 16) |
+                           ((uint64_t)_mm512_cmple_epu32_mask(v2, sa) << 32) |
+                           ((uint64_t)_mm512_cmple_epu32_mask(v3, sa) << 48);
+      const uint32_t c = (uint32_t)__builtin_popcountll(all);
+      a -= c;
+      b -= c;
+      p += 64;
+    }
+    while (a - lo_pow >= 16 && e - p >= 16) {
+      const __m512i sa = _mm512_set1_epi32((int)(a - 15));
+      const __m512i v = _mm512_and_si512(_mm512_loadu_si512(p), vm);
+      const __mmask16 amb = _mm512_mask_cmple_epu32_mask(_mm512_cmpgt_epu32_mask(v, sa), v,
+                                                         _mm512_set1_epi32((int)b));
+      if (amb) break;
+      const uint32_t c = (uint32_t)__builtin_popcount((unsigned)_mm512_cmple_epu32_mask(v, sa));
+      a -= c;
+      b -= c;
+      p += 16;
+    }
+    if (p < e) {
+      const uint32_t v = *p++ & mask;
+      if (v <= a) {
+        --a;
+        --b;
+      } else if (v <= b) {
+        if (nm == kMaxMerges) return false;
+        f.m.push_back(v - 1 - a);
+        ++nm;
+        --b;
+      }
+    }
+  }
+  f.lo = lo;
+  f.hi = hi;
+  f.a_exit = a;
+  f.nm = nm;
+  return true;
+}
+
+// Expected step after o words of a shuffle that starts at step n - 1: step
+// s takes (mask + 1) / (s + 1) words on average, so within one mask range
+// (all-ones mask M - 1) the step after w words from step i is about
+// (i + 1) exp(-w / M) - 1.
+double expected_step(int64_t n, double o) {
+  double i = (double)(n - 1);
+  while (i >= 1.0) {
+    const int k = 63 - __builtin_clzll((uint64_t)i);
+    const double lo = std::ldexp(1.0, k), M = 2.0 * lo;
+    const double wr = M * std::log((i + 1.0) / lo);  // words to leave the range
+    if (o <= wr) return (i + 1.0) * std::exp(-o / M) - 1.0;
+    o -= wr;
+    i = lo - 1.0;
+  }
+  return 0.0;
+}
+
+// Expected words of a shuffle of n entries (steps n - 1 .. 1).
+double expected_words(int64_t n) {
+  double i = (double)(n - 1), w = 0.0;
+  while (i >= 1.0) {
+    const int k = 63 - __builtin_clzll((uint64_t)i);
+    const double lo = std::ldexp(1.0, k);
+    w += 2.0 * lo * std::log((i + 1.0) / lo);
+    i = lo - 1.0;
+  }
+  return w;
+}
+
+// Counting form of write_segment_avx512: from word w0 at step i0 to the
+// chunk's end or the round's last step; returns the offset just past the
+// last word read and the step reached (0 when the round ended).
+__attribute__((target("avx512f,avx512vl,avx512bw,popcnt")))
+int64_t count_segment_avx512(const uint32_t *words, int64_t w0, uint32_t i0, uint32_t &i_out) {
+  const uint32_t *p = words + w0, *const e = words + kChunkWords;
+  uint32_t i = i0;
+  while (i >= 1 && p < e) {
     const uint32_t lo = 1u << (31 - __builtin_clz(i));
     const uint32_t mask = lo | (lo - 1);
     const __m512i vm = _mm512_set1_epi32((int)mask);
-    while (i >= lo) {
-      if (s.p == s.end && !s.next_chunk()) return false;
-      if (s.chunk != open_chunk) {
-        emit(s.cur_key, (int32_t)(s.p - s.base), i);
-        open_chunk = s.chunk;
-      }
-      const uint32_t *p = s.p, *e = s.end;
-      // 256 words against one threshold pair (band [i - 254, i]): the
-      // counter i, which the next block's tests depend on, is updated once
-      // per 256 words instead of once per 64.
-      while (i - lo >= 256 && e - p >= 256) {
-        const __m512i si = _mm512_set1_epi32((int)i);
-        const __m512i sb = _mm512_set1_epi32((int)(i - 254));
-        __mmask16 amb = 0;
-        uint32_t acc = 0;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const __m512i v = _mm512_and_si512(_mm512_loadu_si512(p + 16 * q), vm);
-          const __mmask16 a = _mm512_cmple_epu32_mask(v, si);
-          amb |= _mm512_mask_cmpge_epu32_mask(a, v, sb);
-          acc += (uint32_t)__builtin_popcount((unsigned)a);
-        }
-        if (amb) break;
-        i -= acc;
-        p += 256;
-      }
+    while (i >= lo && p < e) {
       while (i - lo >= 64 && e - p >= 64) {
         const __m512i si = _mm512_set1_epi32((int)i);
         const __m512i sb = _mm512_set1_epi32((int)(i - 62));
@@ -554,7 +681,6 @@ bool count_steps_avx512(Stream &s, uint32_t hi, Emit &&emit) {
                              ((uint64_t)a3 << 48);
         i -= (uint32_t)__builtin_popcountll(all);
         p += 64;
-        if (i - lo >= 256 && e - p >= 256) break;  // back to the wide blocks
       }
       while (i - lo >= 16 && e - p >= 16) {
         const __m512i v = _mm512_and_si512(_mm512_loadu_si512(p), vm);
@@ -568,10 +694,10 @@ bool count_steps_avx512(Stream &s, uint32_t hi, Emit &&emit) {
         const uint32_t v = *p++ & mask;
         i -= v <= i ? 1u : 0u;
       }
-      s.p = p;
     }
   }
-  return true;
+  i_out = i;
+  return p - words;
 }
 
 // A segment's draws: from word w0 of the chunk `words` at step i0 to the
@@ -674,13 +800,34 @@ struct Sampler {
   std::deque<std::unique_ptr<Round>> inflight;  // counted, draws being written (in order)
   std::deque<std::unique_ptr<Round>> drawn;  // draw thread -> swap thread
   std::deque<std::unique_ptr<Round>> ready;  // -> consumer
-  // Parallel draws (rounds of at least kParallelSteps steps with AVX-512):
-  // segments from the counting pass, written by the worker threads.
+  // Parallel draws (rounds of at least four chunks of steps, AVX-512):
+  // chunk transfer functions and segments, both done by the worker threads.
+  struct CountTask {
+    int64_t chunk;
+    uint32_t lo, hi;
+    ChunkFn *out;
+  };
+  std::deque<CountTask> ctasks;
+  int32_t count_running = 0;  // count tasks being worked on
   std::deque<Segment> segs;
   std::condition_variable seg_cv;
   int32_t idle_workers = 0;  // workers asleep on seg_cv
   std::vector<std::thread> workers;
   bool parallel = false;
+  double window_scale = 1.0;  // entry windows: scale * (2.5 sqrt(words) + 64)
+  std::unique_ptr<ChunkFn[]> fns;
+  int64_t fns_cap = 0;
+  // First-block states of the chunks [produced - cap, produced), made by the
+  // twister thread, which stays fewer than ring_lead <= cap chunks ahead of
+  // ring_floor (the draw thread's chunk).
+  static constexpr int64_t kRingChunks = 4096;
+  int64_t ring_lead = kRingChunks;
+  std::vector<uint32_t> ring;
+  std::atomic<int64_t> ring_produced{0};
+  std::atomic<int64_t> ring_floor{0};
+  std::mutex ring_mu;
+  std::condition_variable ring_cv;
+  std::thread twister;
   std::vector<std::unique_ptr<Round>> pool;
   int32_t n_drawn = 0, produced = 0, consumed = 0;
   bool stop = false;
@@ -694,6 +841,7 @@ struct Sampler {
   BigArray<int32_t> rows;      // cumulative row permutation (host mode)
   std::vector<int32_t> feats;  // cumulative feature permutation (draw thread)
   double draw_ms = 0.0, swap_ms = 0.0;
+  int64_t spec_chunks = 0, seq_chunks = 0;  // parallel form: chunks by transfer function / word by word
 
   void fail(const char *msg) {
     {
@@ -701,8 +849,10 @@ struct Sampler {
       if (error.empty()) error = msg;
       stop = true;
     }
+    halt.store(true);
     cv.notify_all();
     seg_cv.notify_all();
+    ring_cv.notify_all();
   }
 
   // Device-rows mode: the round's draws go to the GPU on the sampler's own
@@ -780,16 +930,34 @@ struct Sampler {
       std::vector<uint32_t> words((size_t)kChunkWords + 16);
       for (;;) {
         Segment sg;
+        CountTask ct{-1, 0, 0, nullptr};
         {
           std::unique_lock<std::mutex> lk(mu);
-          if (!stop && segs.empty()) {
+          if (!stop && segs.empty() && ctasks.empty()) {
             ++idle_workers;
-            seg_cv.wait(lk, [&] { return stop || !segs.empty(); });
+            seg_cv.wait(lk, [&] { return stop || !segs.empty() || !ctasks.empty(); });
             --idle_workers;
           }
           if (stop) return;
-          sg = segs.front();
-          segs.pop_front();
+          if (!ctasks.empty()) {  // transfer functions first: the draw thread waits on them
+            ct = ctasks.front();
+            ctasks.pop_front();
+            ++count_running;
+          } else {
+            sg = segs.front();
+            segs.pop_front();
+          }
+        }
+        if (ct.out) {
+          bool ok = wait_key(ct.chunk);
+          if (ok) {
+            gen_chunk(ring_key(ct.chunk), words.data());
+            ok = spec_chunk_avx512(words.data(), ct.lo, ct.hi, *ct.out);
+          }
+          ct.out->state.store(ok ? 1 : 2, std::memory_order_release);
+          std::lock_guard<std::mutex> lk(mu);
+          --count_running;
+          continue;
         }
         Round *R = static_cast<Round *>(sg.round);
         gen_chunk(sg.key, words.data());
@@ -801,11 +969,260 @@ struct Sampler {
     }
   }
 
+  const uint32_t *ring_key(int64_t c) const {
+    return ring.data() + (size_t)(c % kRingChunks) * kN;
+  }
+
+  // Waits until chunk c's first-block state exists; false if stopping.
+  bool wait_key(int64_t c) {
+    for (int spin = 0; ring_produced.load(std::memory_order_acquire) <= c; ++spin) {
+      if (halt.load(std::memory_order_relaxed)) return false;
+      if (spin < 4096) {
+        _mm_pause();
+      } else {
+        std::unique_lock<std::mutex> lk(ring_mu);
+        ring_cv.wait_for(lk, std::chrono::microseconds(200), [&] {
+          return halt.load(std::memory_order_relaxed) ||
+                 ring_produced.load(std::memory_order_acquire) > c;
+        });
+      }
+    }
+    return true;
+  }
+
+  void set_floor(int64_t c) {
+    if (ring_floor.load(std::memory_order_relaxed) >= c) return;
+    ring_floor.store(c, std::memory_order_release);
+    ring_cv.notify_all();
+  }
+
+  // Twists the stream ahead of its readers, chunk after chunk (the states
+  // do not depend on how the words are used).
+  void run_twister() {
+    (void)pthread_setname_np(pthread_self(), "bsscl-twist");
+    alignas(64) uint32_t k[kN];
+    std::memcpy(k, key0, sizeof(k));
+    for (int64_t c = 0;; ++c) {
+      if (c > 0) {
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int b = 0; b < kChunkBlocks; ++b) twist_avx512(k);
+        gen_ms.store(gen_ms.load(std::memory_order_relaxed) +
+                         std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count(),
+                     std::memory_order_relaxed);
+      }
+      if (c >= ring_floor.load(std::memory_order_acquire) + ring_lead) {
+        std::unique_lock<std::mutex> lk(ring_mu);
+        ring_cv.wait(lk, [&] {
+          return halt.load(std::memory_order_relaxed) ||
+                 c < ring_floor.load(std::memory_order_acquire) + ring_lead;
+        });
+      }
+      if (halt.load(std::memory_order_relaxed)) return;
+      std::memcpy(ring.data() + (size_t)(c % kRingChunks) * kN, k, sizeof(k));
+      ring_produced.store(c + 1, std::memory_order_release);
+      ring_cv.notify_all();
+    }
+  }
+
+  // Waits for a transfer function; 0 if the sampler stops.
+  int32_t wait_fn(const ChunkFn &f) {
+    for (int spin = 0;; ++spin) {
+      const int32_t st = f.state.load(std::memory_order_acquire);
+      if (st != 0) return st;
+      if (halt.load(std::memory_order_relaxed)) return 0;
+      if (spin < 4096) _mm_pause();
+      else std::this_thread::yield();
+    }
+  }
+
+  // The row steps of one round from global word G, as segments for the
+  // workers (emit); returns the global word after the round's last step, or
+  // -1 if the sampler stops.
+  template <class Emit>
+  int64_t resolve_round(int64_t G, Emit &&emit, std::vector<uint32_t> &words) {
+    const int64_t c0 = G / kChunkWords;
+    // Transfer functions of the chunks after the first, each around its
+    // expected entry step, while the window stays above kSpecMin.
+    int64_t nt = 0;
+    {
+      std::vector<CountTask> tl;
+      for (int64_t c = c0 + 1;; ++c) {
+        const double o = (double)(c * kChunkWords - G);
+        const double e = expected_step(n, o);
+        const double h = window_scale * (2.5 * std::sqrt(o) + 64.0);
+        if (e - h < (double)kSpecMin) break;
+        const double hi = std::min(e + h, (double)(n - 1));
+        tl.push_back({c, (uint32_t)(e - h), (uint32_t)hi, nullptr});
+      }
+      nt = (int64_t)tl.size();
+      if (nt > fns_cap) {
+        fns.reset(new ChunkFn[(size_t)nt]);
+        fns_cap = nt;
+      }
+      for (int64_t t = 0; t < nt; ++t) {
+        fns[(size_t)t].state.store(0, std::memory_order_relaxed);
+        tl[(size_t)t].out = &fns[(size_t)t];
+      }
+      if (nt) {
+        {
+          std::lock_guard<std::mutex> lk(mu);
+          for (const CountTask &t : tl) ctasks.push_back(t);
+        }
+        seg_cv.notify_all();
+      }
+    }
+    uint32_t i = (uint32_t)(n - 1);
+    int64_t c = c0, w = G - c0 * kChunkWords, end = -1, n_spec = 0, n_seq = 0;
+    while (end < 0) {
+      set_floor(c - 1);  // (the state of the word before a chunk's first stays readable)
+      if (!wait_key(c)) break;
+      const int64_t t = c - c0 - 1;
+      if (t >= 0 && t < nt) {
+        const ChunkFn &f = fns[(size_t)t];
+        const int32_t st = wait_fn(f);
+        if (st == 0) break;
+        if (st == 1 && f.lo <= i && i <= f.hi) {
+          ++n_spec;
+          emit(ring_key(c), 0, i);
+          i = chunk_exit(f, i);
+          ++c;
+          w = 0;
+          continue;
+        }
+      }
+      // Word by word: the round's first and last chunks, and any chunk
+      // whose transfer function does not cover the entry step.
+      ++n_seq;
+      gen_chunk(ring_key(c), words.data());
+      emit(ring_key(c), (int32_t)w, i);
+      uint32_t i2 = 0;
+      const int64_t pe = count_segment_avx512(words.data(), w, i, i2);
+      i = i2;
+      if (i == 0) end = c * kChunkWords + pe;
+      ++c;
+      w = 0;
+    }
+    // Transfer functions past the round's end are not needed.
+    {
+      std::unique_lock<std::mutex> lk(mu);
+      spec_chunks += n_spec;
+      seq_chunks += n_seq;
+      ctasks.clear();
+      while (count_running > 0 && !stop) {
+        lk.unlock();
+        std::this_thread::yield();
+        lk.lock();
+      }
+    }
+    return end;
+  }
+
+  // NumPy state after the words before global position G.
+  void state_at(int64_t G, uint32_t *key_out, int *pos_out) {
+    if (G <= pos0) {
+      std::memcpy(key_out, key0, sizeof(uint32_t) * kN);
+      *pos_out = pos0;
+      return;
+    }
+    const int64_t b = (G - 1) / kN;
+    const int64_t c = b / kChunkBlocks;
+    alignas(64) uint32_t k[kN];
+    if (!wait_key(c)) return;
+    std::memcpy(k, ring_key(c), sizeof(k));
+    for (int64_t t = c * kChunkBlocks; t < b; ++t) twist_scalar(k);
+    std::memcpy(key_out, k, sizeof(k));
+    *pos_out = (int)(G - b * kN);
+  }
+
+  // Draw loop of the parallel form.
+  void run_draws_parallel() {
+    std::vector<uint32_t> jf((size_t)F + 16);
+    std::vector<uint32_t> words((size_t)kChunkWords + 16);
+    int64_t G = pos0;  // global position of the next word
+    for (int32_t r = 0; r < n_rounds; ++r) {
+      std::unique_ptr<Round> R;
+      {
+        std::unique_lock<std::mutex> lk(mu);
+        cv.wait(lk, [&] {
+          return stop || (int32_t)(inflight.size() + drawn.size() + ready.size()) < lookahead;
+        });
+        if (stop) return;
+        if (!pool.empty()) {
+          R = std::move(pool.back());
+          pool.pop_back();
+        }
+      }
+      if (!R) R.reset(new Round());
+      R->draws.alloc((size_t)n + 16);
+      R->done = false;
+      R->pending.store(1, std::memory_order_relaxed);  // this thread's share
+      Round *Rp = R.get();
+      {
+        std::lock_guard<std::mutex> lk(mu);
+        inflight.push_back(std::move(R));
+      }
+      const auto t0 = std::chrono::steady_clock::now();
+      auto emit = [&](const uint32_t *key, int32_t w0, uint32_t i) {
+        Segment sg;
+        std::memcpy(sg.key, key, sizeof(sg.key));
+        sg.w0 = w0;
+        sg.i0 = i;
+        sg.round = Rp;
+        Rp->pending.fetch_add(1, std::memory_order_relaxed);
+        // A sleeping worker is woken once four segments wait (waking costs
+        // a system call; a worker drains the queue before it sleeps again).
+        bool wake;
+        {
+          std::lock_guard<std::mutex> lk(mu);
+          segs.push_back(sg);
+          wake = idle_workers > 0 && segs.size() >= 4;
+        }
+        if (wake) seg_cv.notify_one();
+      };
+      const int64_t end = resolve_round(G, emit, words);
+      seg_cv.notify_all();  // the round's last segments
+      if (end < 0) return;
+      G = end;
+      if (do_feats && F > 1) {
+        Stream fs;
+        const int64_t c = G / kChunkWords;
+        if (!wait_key(c) || !fs.seek(c, G - c * kChunkWords, ring_key(c), &halt)) return;
+        if (!draw_steps(fs, (uint32_t)(F - 1), jf.data())) return;
+        for (int32_t t = 0; t < F - 1; ++t) std::swap(feats[(size_t)(F - 1 - t)], feats[jf[(size_t)t]]);
+        G = fs.position();
+      }
+      Rp->feats.assign(feats.begin(), feats.begin() + f_sub);
+      std::sort(Rp->feats.begin(), Rp->feats.end());
+      Rp->index = r;
+      const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+      uint32_t fk[kN];
+      std::memcpy(fk, key0, sizeof(fk));
+      int fp = pos0;
+      const bool last = r + 1 == n_rounds;
+      if (last) state_at(G, fk, &fp);
+      {
+        std::lock_guard<std::mutex> lk(mu);
+        draw_ms += ms;
+        ++n_drawn;
+        if (last) {
+          std::memcpy(final_key, fk, sizeof(fk));
+          final_pos = fp;
+        }
+      }
+      cv.notify_all();
+      release(Rp);
+    }
+  }
+
   void run_draws() {
     (void)pthread_setname_np(pthread_self(), "bsscl-draw");
     try {
       if (device_rows && do_rows && hipSetDevice(device) != hipSuccess) {
         fail("sampler: hipSetDevice failed");
+        return;
+      }
+      if (do_rows && parallel) {
+        run_draws_parallel();
         return;
       }
       Stream st;
@@ -835,29 +1252,7 @@ struct Sampler {
           inflight.push_back(std::move(R));
         }
         const auto t0 = std::chrono::steady_clock::now();
-        if (do_rows && parallel) {
-          auto emit = [&](const uint32_t *key, int32_t w0, uint32_t i) {
-            Segment sg;
-            std::memcpy(sg.key, key, sizeof(sg.key));
-            sg.w0 = w0;
-            sg.i0 = i;
-            sg.round = Rp;
-            Rp->pending.fetch_add(1, std::memory_order_relaxed);
-            // A sleeping worker is woken once four segments wait (waking
-            // costs a system call; a worker drains the queue before it
-            // sleeps again).
-            bool wake;
-            {
-              std::lock_guard<std::mutex> lk(mu);
-              segs.push_back(sg);
-              wake = idle_workers > 0 && segs.size() >= 4;
-            }
-            if (wake) seg_cv.notify_one();
-          };
-          const bool ok = count_steps_avx512(st, (uint32_t)(n - 1), emit);
-          seg_cv.notify_all();  // the round's last segments
-          if (!ok) return;
-        } else if (do_rows && !draw_steps(st, (uint32_t)(n - 1), Rp->draws.p)) {
+        if (do_rows && !draw_steps(st, (uint32_t)(n - 1), Rp->draws.p)) {
           return;
         }
         if (do_feats && F > 1) {
@@ -952,7 +1347,9 @@ struct Sampler {
     cv.notify_all();
     seg_cv.notify_all();
     halt.store(true);
+    ring_cv.notify_all();
     if (draw_thread.joinable()) draw_thread.join();
+    if (twister.joinable()) twister.join();
     for (auto &w : workers)
       if (w.joinable()) w.join();
     if (swap_thread.joinable()) swap_thread.join();
@@ -1102,9 +1499,18 @@ int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
     // worker threads (AVX-512 only; the scalar path stays sequential).
     s->parallel = s->do_rows && bsscl::use_avx512() && n - 1 >= 4 * bsscl::kChunkWords;
     if (s->parallel) {
+      // (Test hook: BSSCL_SAMPLER_WINDOW scales the entry windows; 0 makes
+      // almost every chunk miss its window and be counted word by word.)
+      const char *ws = std::getenv("BSSCL_SAMPLER_WINDOW");
+      if (ws && ws[0]) s->window_scale = std::max(0.0, std::atof(ws));
+      s->ring.resize((size_t)Sampler::kRingChunks * bsscl::kN);
+      // The twister stays about three rounds of words ahead.
+      const double rc = bsscl::expected_words(n) / (double)bsscl::kChunkWords;
+      s->ring_lead = std::min<int64_t>(Sampler::kRingChunks, (int64_t)(3.0 * rc) + 64);
       const unsigned hw = std::max(2u, std::thread::hardware_concurrency());
-      const int nw = (int)std::min(4u, hw / 2);
+      const int nw = (int)std::max(2u, std::min(6u, hw / 2));
       for (int w = 0; w < nw; ++w) s->workers.emplace_back([s] { s->run_worker(); });
+      s->twister = std::thread([s] { s->run_twister(); });
     }
     s->draw_thread = std::thread([s] { s->run_draws(); });
     if (s->do_rows && !s->device_rows) s->swap_thread = std::thread([s] { s->run_swaps(); });
@@ -1158,9 +1564,10 @@ int bsscl_sampler_stats(bsscl_sampler *hs, double *out, int32_t cap,
   Sampler *s = reinterpret_cast<Sampler *>(hs);
   if (!s || !out || !n_out) return bsscl::set_error(BSSCL_EINVAL, "sampler_stats: bad arguments");
   std::lock_guard<std::mutex> lk(s->mu);
-  const double v[4] = {(double)s->produced, s->draw_ms, s->swap_ms,
-                       s->gen_ms.load(std::memory_order_relaxed)};
-  const int32_t k = std::max<int32_t>(0, std::min<int32_t>(cap, 4));
+  const double v[6] = {(double)s->produced, s->draw_ms, s->swap_ms,
+                       s->gen_ms.load(std::memory_order_relaxed), (double)s->spec_chunks,
+                       (double)s->seq_chunks};
+  const int32_t k = std::max<int32_t>(0, std::min<int32_t>(cap, 6));
   for (int32_t i = 0; i < k; ++i) out[i] = v[i];
   *n_out = k;
   return BSSCL_OK;

@@ -250,7 +250,9 @@ int bsscl_sampler_state(bsscl_sampler *s, uint32_t *key_out,
                         int32_t *pos_out);
 /* Host time of the sampler's stages (no reference counterpart): [0] rounds
  * produced, [1] ms drawing bounded integers, [2] ms applying swaps on the
- * host, [3] ms generating MT19937 words. */
+ * host, [3] ms generating MT19937 words (twisting, in the parallel form),
+ * [4] chunks of words mapped through a transfer function and [5] chunks
+ * counted word by word (parallel form; 0 otherwise). */
 int bsscl_sampler_stats(bsscl_sampler *s, double *out, int32_t cap,
                         int32_t *n_out);
 void bsscl_sampler_destroy(bsscl_sampler *s);

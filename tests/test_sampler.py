@@ -82,6 +82,38 @@ def test_parallel_draws_match_numpy_over_mask_ranges(doubles):
     s.close()
 
 
+@pytest.mark.parametrize("window", ["1", "0", "6"])
+def test_parallel_transfer_functions_and_word_by_word_chunks(monkeypatch, window):
+    """The chunk transfer functions of the parallel form (default entry
+    windows; windows of width 0, so nearly every chunk is counted word by
+    word; windows six times wider, with many merges per chunk) give the
+    stream of RandomState.shuffle exactly."""
+    monkeypatch.setenv("BSSCL_SAMPLER_WINDOW", window)
+    n, F, rounds = 1_500_007, 7, 3
+    rng = _state_after(31, 5)
+    s = _native.Sampler(rng.get_state(), n, n // 3, True, F, 4, True, rounds)
+    rows = np.arange(n, dtype=np.int64)
+    feats = np.arange(F, dtype=np.int32)
+    for _ in range(rounds):
+        rng.shuffle(rows)
+        rng.shuffle(feats)
+        r, f = s.next()
+        np.testing.assert_array_equal(r, rows[:n // 3])
+        np.testing.assert_array_equal(f, np.sort(feats[:4]))
+    key, pos = s.state()
+    st = rng.get_state()
+    np.testing.assert_array_equal(key, st[1])
+    assert pos == st[2]
+    stats = s.stats()
+    s.close()
+    chunks = stats["spec_chunks"] + stats["seq_chunks"]
+    assert chunks >= rounds * 100
+    if window == "0":
+        assert stats["seq_chunks"] > 0.9 * chunks
+    else:
+        assert stats["spec_chunks"] > 0.7 * chunks
+
+
 def test_sampler_scalar_path_matches():
     """The same stream with the AVX-512 draws switched off (the switch is
     read once per process, so this runs in a child)."""
