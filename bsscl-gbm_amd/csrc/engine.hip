@@ -250,6 +250,10 @@ struct bsscl_engine {
   DevBuf<PartParent> parents_d[2];    // by level parity
   DevBuf<int32_t> tile_begin_d, hist_begin_d, work_flag_d, hist_node_d;
   DevBuf<double> work_e_d;
+  // Planner in LDS (trees of at most kPlanLdsMaxNodes nodes): ranks of kept
+  // splits per node and of each level's parents (by level parity).
+  bool plan_lds = false;
+  DevBuf<double> kept_e_d, parent_e_d[2];
   DevBuf<SplitTask> split_tasks_d;
   DevBuf<int64_t> nleft_d;
   int32_t tile_cap = 0, hist_cap = 0;
@@ -462,6 +466,8 @@ int ensure_nodes(bsscl_engine *E, int32_t cap, int32_t F_sel) {
   CHK(E->nleft_d.ensure((size_t)pcap));
   CHK(E->work_flag_d.ensure((size_t)cap));
   CHK(E->work_e_d.ensure((size_t)cap));
+  CHK(E->kept_e_d.ensure((size_t)cap));
+  for (int s = 0; s < 2; ++s) CHK(E->parent_e_d[s].ensure((size_t)pcap));
   CHK(E->split_tasks_d.ensure((size_t)cap));
   E->node_alloc = cap;
   E->node_cap = cap;
@@ -715,7 +721,13 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
   E->tile_cap = (int32_t)tcap;
   E->hist_cap = (int32_t)hcap;
   CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 16u << 20)));
-  return ensure_nodes(E, cap, F_sel);
+  CHK(ensure_nodes(E, cap, F_sel));
+  // One planner for the whole tree (the LDS planner's per-node ranks are
+  // written by its own earlier levels).  Test hook: BSSCL_TEST_PLAN_GLOBAL=1
+  // keeps the general planner.
+  const char *pg = std::getenv("BSSCL_TEST_PLAN_GLOBAL");
+  E->plan_lds = E->node_cap <= kPlanLdsMaxNodes && !(pg && pg[0] == '1');
+  return BSSCL_OK;
 }
 
 SplitParams split_params(bsscl_engine *E, const TreeParams &tp) {
@@ -820,11 +832,19 @@ int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParam
   pa.part_tile = E->part_tile;
   hipEvent_t stop;
   CHK(prof_begin(E, 2, &stop));
-  HIPCHK(launch_plan(E->st, E->nodes_d, E->plan_d, E->parents_d[(level + 1) & 1].p,
-                     E->parents_d[level & 1].p, E->tile_begin_d.p, E->hist_begin_d.p,
-                     E->tiles_d.p, E->hist_tasks_d.p, E->split_tasks_d.p,
-                     E->work_flag_d.p, E->work_e_d.p, E->segs.p, E->totals.p, E->cand.p,
-                     F_sel, pa));
+  if (E->plan_lds)
+    HIPCHK(launch_plan_lds(E->st, E->nodes_d, E->plan_d, E->parents_d[(level + 1) & 1].p,
+                           E->parents_d[level & 1].p, E->tile_begin_d.p, E->hist_begin_d.p,
+                           E->tiles_d.p, E->hist_tasks_d.p, E->split_tasks_d.p, E->segs.p,
+                           E->totals.p, E->cand.p, E->kept_e_d.p,
+                           E->parent_e_d[(level + 1) & 1].p, E->parent_e_d[level & 1].p,
+                           F_sel, pa));
+  else
+    HIPCHK(launch_plan(E->st, E->nodes_d, E->plan_d, E->parents_d[(level + 1) & 1].p,
+                       E->parents_d[level & 1].p, E->tile_begin_d.p, E->hist_begin_d.p,
+                       E->tiles_d.p, E->hist_tasks_d.p, E->split_tasks_d.p,
+                       E->work_flag_d.p, E->work_e_d.p, E->segs.p, E->totals.p, E->cand.p,
+                       F_sel, pa));
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
@@ -1576,6 +1596,8 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->tile_begin_d.release();
   E->hist_begin_d.release();
   E->work_flag_d.release();
+  E->kept_e_d.release();
+  for (auto &b : E->parent_e_d) b.release();
   E->hist_node_d.release();
   E->work_e_d.release();
   E->split_tasks_d.release();

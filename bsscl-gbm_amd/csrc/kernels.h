@@ -265,6 +265,17 @@ hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                        SplitTask *split_tasks, int32_t *work_flag,
                        double *work_e, const NodeSeg *segs, const long long *totals,
                        const SplitCand *cand, int32_t F_sel, PlanArgs a);
+// k_plan with its intermediates in LDS, for trees of at most 513 nodes; keeps
+// kept_e (node ranks of kept splits, per node) and parent_e (ranks of a
+// level's parents, by level parity) for the levels after it.
+hipError_t launch_plan_lds(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
+                           const PartParent *prev_parents, PartParent *parents,
+                           int32_t *tile_begin, int32_t *hist_begin, PartTile *tiles,
+                           HistTask *hist_tasks, SplitTask *split_tasks, const NodeSeg *segs,
+                           const long long *totals, const SplitCand *cand, double *kept_e,
+                           const double *prev_parent_e, double *parent_e, int32_t F_sel,
+                           PlanArgs a);
+constexpr int32_t kPlanLdsMaxNodes = 513;
 hipError_t launch_code_counts(hipStream_t st, const uint8_t *codes, int64_t ld,
                               int64_t n, int32_t F, unsigned int *counts);
 // F += lr * tree(row) for every row unless *node_count_d == 0 (then F is

@@ -1583,6 +1583,308 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
   }
 }
 
+// The same planner with every intermediate in LDS, for trees of at most
+// kPlanLdsC + 1 nodes.  The reference's rule and outputs are those of
+// k_plan; what changes is where the inputs come from, so that the kernel
+// waits on global memory twice (the plan, then all its inputs at once)
+// instead of once per phase:
+//   * kept_e[u] is the rank e(u) of node u when u is a kept split (expanded,
+//     children valid), -inf otherwise.  A level writes it for its candidates
+//     that are not expanded and for the previous level's parents, whose
+//     children are this level's candidates;
+//   * parent_e[i] is the rank of this level's parent i, read by the next
+//     level as prev_parent_e;
+//   * the best split of a candidate over its features is a wave reduction,
+//     four candidates per wave at a time.
+constexpr int kPlanLdsC = 512;
+
+__global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
+    NodeOut *__restrict__ nodes, LevelPlan *__restrict__ plan,
+    const PartParent *__restrict__ prev_parents, PartParent *__restrict__ parents,
+    int32_t *__restrict__ tile_begin, int32_t *__restrict__ hist_begin,
+    PartTile *__restrict__ tiles, HistTask *__restrict__ hist_tasks,
+    SplitTask *__restrict__ split_tasks, const NodeSeg *__restrict__ segs,
+    const long long *__restrict__ totals, const SplitCand *__restrict__ cand,
+    double *__restrict__ kept_e, const double *__restrict__ prev_parent_e,
+    double *__restrict__ parent_e, int32_t F_sel, PlanArgs a) {
+  __shared__ uint32_t stmp[kPlanBlock / 64];
+  __shared__ double s_ke[kPlanLdsC + 1];
+  __shared__ int64_t s_start[kPlanLdsC], s_count[kPlanLdsC];
+  __shared__ long long s_gq[kPlanLdsC], s_hq[kPlanLdsC];
+  __shared__ double s_gain[kPlanLdsC], s_e[kPlanLdsC];
+  __shared__ int32_t s_fpos[kPlanLdsC], s_bin[kPlanLdsC], s_valid[kPlanLdsC];
+  __shared__ int32_t s_flag[kPlanLdsC];
+  __shared__ int32_t s_pj[kPlanLdsC / 2 + 1];  // candidate of each parent
+  __shared__ int32_t s_tb[kPlanLdsC / 2 + 1], s_hb[kPlanLdsC / 2 + 1];
+  __shared__ unsigned long long s_rows;
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const LevelPlan prev = *plan;
+  if (prev.overflow) return;
+  const int32_t first = prev.first_child, nc = prev.n_split, n_prev = prev.n_nodes;
+  const int32_t n_pp = a.level == 0 ? 0 : nc / 2;  // the previous level's parents
+  if (nc > kPlanLdsC || first > kPlanLdsC + 1) {
+    // The host selects this kernel only for trees that fit; reaching this is a bug.
+    if (tid == 0) {
+      LevelPlan q = {};
+      q.first_child = n_prev;
+      q.tile_rows = 4096;
+      q.n_nodes = n_prev;
+      q.overflow = -1;
+      *plan = q;
+    }
+    return;
+  }
+  if (tid == 0) s_rows = 0ull;
+
+  // Every input at once: earlier ranks, the previous parents' ids and ranks,
+  // and the candidates' segments, totals and split candidates.
+  for (int u = tid; u < first; u += kPlanBlock) s_ke[u] = kept_e[u];
+  int32_t pnode = -1;
+  double pe = 0.0;
+  if (tid < n_pp) {
+    pnode = prev_parents[tid].node;
+    pe = prev_parent_e[tid];
+  }
+  for (int jb = wave * 4; jb < nc; jb += (kPlanBlock / 64) * 4) {
+    NodeSeg sg[4];
+    long long gq[4], hq[4];
+    double ppe[4];
+    SplitCand cf[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = min(jb + q, nc - 1);
+      const int64_t c = first + j;
+      sg[q] = segs[c];
+      gq[q] = totals[2 * c];
+      hq[q] = totals[2 * c + 1];
+      ppe[q] = a.level == 0 ? 0.0 : prev_parent_e[j >> 1];
+      cf[q] = lane < F_sel ? cand[c * F_sel + lane] : SplitCand{0.0, -1, 0};
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = jb + q;
+      const int64_t c = first + min(j, nc - 1);
+      // Best over the features: largest gain, lowest position on ties.
+      double best = 0.0;
+      int32_t bf = -1, bb = 0;
+      if (cf[q].bin >= 0) {
+        best = cf[q].gain;
+        bf = lane;
+        bb = cf[q].bin;
+      }
+      for (int f = lane + 64; f < F_sel; f += 64) {
+        const SplitCand x = cand[c * F_sel + f];
+        if (x.bin >= 0 && (bf < 0 || x.gain > best)) {
+          best = x.gain;
+          bf = f;
+          bb = x.bin;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const double og = __shfl_xor(best, o, 64);
+        const int32_t of = __shfl_xor(bf, o, 64);
+        const int32_t ob = __shfl_xor(bb, o, 64);
+        const bool take = of >= 0 && (bf < 0 || og > best || (og == best && of < bf));
+        best = take ? og : best;
+        bf = take ? of : bf;
+        bb = take ? ob : bb;
+      }
+      if (lane == 0 && j < nc) {
+        const bool valid = sg[q].valid != 0;
+        if (!valid) bf = -1;
+        const double gain = bf >= 0 ? best : -1e9;
+        double e = 0.0;
+        int32_t fl = 0;
+        if (valid) {
+          const double pv = a.level == 0 ? gain : ppe[q];
+          e = pv < gain ? pv : gain;
+          fl = (bf >= 0 && gain > a.gamma) ? 1 : 0;
+        }
+        s_start[j] = sg[q].start;
+        s_count[j] = sg[q].count;
+        s_gq[j] = valid ? gq[q] : 0;
+        s_hq[j] = valid ? hq[q] : 0;
+        s_gain[j] = gain;
+        s_e[j] = e;
+        s_fpos[j] = bf;
+        s_bin[j] = bf >= 0 ? bb : 0;
+        s_valid[j] = sg[q].valid;
+        s_flag[j] = fl;
+      }
+    }
+  }
+  __syncthreads();
+
+  // The previous level's parents are kept splits when their children (this
+  // level's candidates 2i, 2i+1) are valid.
+  if (tid < n_pp) {
+    const double kv = s_valid[2 * tid] ? pe : -INFINITY;
+    s_ke[pnode] = kv;
+    kept_e[pnode] = kv;
+  }
+  __syncthreads();
+
+  // Expanded: valid, a split above gamma, and fewer than max_leaves - 1 kept
+  // splits ranked above it.
+  int32_t fl = 0;
+  if (tid < nc && s_flag[tid]) {
+    const double ev = s_e[tid];
+    int32_t above = 0;
+    for (int u = 0; u < first; ++u) above += s_ke[u] > ev ? 1 : 0;
+    fl = above < a.max_leaves - 1 ? 1 : 0;
+  }
+  uint32_t n_exp_u;
+  const uint32_t pidx = block_excl_scan<kPlanBlock>((uint32_t)fl, stmp, n_exp_u);
+  const int32_t n_exp = (int32_t)n_exp_u;
+  const int64_t n_new = (int64_t)n_prev + 2 * (int64_t)n_exp;
+  if (n_new > a.node_cap) {
+    if (tid == 0) {
+      LevelPlan q = {};
+      q.first_child = n_prev;
+      q.tile_rows = 4096;
+      q.n_nodes = n_prev;
+      q.overflow = (int32_t)min(n_new, (int64_t)INT32_MAX);
+      *plan = q;
+    }
+    return;
+  }
+
+  // Records, parents, split tasks, ranks; tiles per parent; rows to build.
+  unsigned long long rows = 0;
+  if (tid < nc) {
+    const int32_t v = first + tid;
+    const int32_t L = fl ? n_prev + 2 * (int32_t)pidx : -1;
+    NodeOut N;
+    N.start = s_start[tid];
+    N.count = s_count[tid];
+    N.Gq = s_gq[tid];
+    N.Hq = s_hq[tid];
+    N.gain = s_gain[tid];
+    N.e = s_e[tid];
+    N.fpos = s_fpos[tid];
+    N.bin = s_bin[tid];
+    N.valid = s_valid[tid];
+    N.left = L;
+    nodes[v] = N;
+    if (!fl) {
+      kept_e[v] = -INFINITY;
+    } else {
+      const int32_t i = (int32_t)pidx;
+      PartParent P;
+      P.start = N.start;
+      P.count = N.count;
+      P.fpos = N.fpos;
+      P.bin = N.bin;
+      P.left_id = L;
+      P.right_id = L + 1;
+      P.node = v;
+      P.pad = 0;
+      parents[i] = P;
+      parent_e[i] = N.e;
+      if (!a.last) {
+        split_tasks[2 * i] = SplitTask{L, v, L + 1, a.level + 1};
+        split_tasks[2 * i + 1] = SplitTask{L + 1, v, L, a.level + 1};
+      }
+      const int64_t a0 = N.start & ~int64_t(15);
+      s_tb[i] = (int32_t)((N.start + N.count - a0 + a.part_tile - 1) / a.part_tile);
+      s_pj[i] = tid;
+      rows = (unsigned long long)(N.count / 2);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) rows += __shfl_xor(rows, o, 64);
+  if (lane == 0 && rows) atomicAdd(&s_rows, rows);
+  __syncthreads();
+  const int32_t th = plan_tile_rows((int64_t)s_rows, a);
+
+  // Exclusive offsets of each parent's tiles and histogram tasks.
+  uint32_t nt = 0, nh = 0;
+  if (tid < n_exp) {
+    nt = (uint32_t)s_tb[tid];
+    nh = a.last ? 0u : (uint32_t)((s_count[s_pj[tid]] / 2 + th) / th);
+  }
+  uint32_t tcar, hcar;
+  const uint32_t tp = block_excl_scan<kPlanBlock>(nt, stmp, tcar);
+  const uint32_t hp = block_excl_scan<kPlanBlock>(nh, stmp, hcar);
+  if (tcar > (uint32_t)a.tile_cap || hcar > (uint32_t)a.hist_cap) {
+    // Capacities are sized from proven bounds; reaching this is a bug.
+    if (tid == 0) {
+      LevelPlan q = {};
+      q.first_child = n_prev;
+      q.tile_rows = 4096;
+      q.n_nodes = n_prev;
+      q.overflow = -1;
+      *plan = q;
+    }
+    return;
+  }
+  __syncthreads();  // s_tb is rewritten below
+  if (tid < n_exp) {
+    s_tb[tid] = (int32_t)tp;
+    s_hb[tid] = (int32_t)hp;
+    tile_begin[tid] = (int32_t)tp;
+    hist_begin[tid] = (int32_t)hp;
+  }
+  if (tid == 0) {
+    s_tb[n_exp] = (int32_t)tcar;
+    s_hb[n_exp] = (int32_t)hcar;
+    tile_begin[n_exp] = (int32_t)tcar;
+    hist_begin[n_exp] = (int32_t)hcar;
+  }
+  __syncthreads();
+
+  // Tile and histogram-task lists: item -> its parent by binary search.
+  for (int t = tid; t < (int)tcar; t += kPlanBlock) {
+    int lo = 0, hi = n_exp - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_tb[mid] <= t) lo = mid;
+      else hi = mid - 1;
+    }
+    PartTile T;
+    T.row0 = (s_start[s_pj[lo]] & ~int64_t(15)) + (int64_t)(t - s_tb[lo]) * a.part_tile;
+    T.rows = a.part_tile;
+    T.parent = lo;
+    tiles[t] = T;
+  }
+  for (int q = tid; q < (int)hcar; q += kPlanBlock) {
+    int lo = 0, hi = n_exp - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_hb[mid] <= q) lo = mid;
+      else hi = mid - 1;
+    }
+    hist_tasks[q] = HistTask{lo, q - s_hb[lo]};
+  }
+  if (tid == 0) {
+    LevelPlan q;
+    q.n_parents = n_exp;
+    q.n_tiles = (int32_t)tcar;
+    q.n_hist = (int32_t)hcar;
+    q.n_split = 2 * n_exp;
+    q.first_child = n_prev;
+    q.tile_rows = th;
+    q.n_nodes = (int32_t)n_new;
+    q.overflow = 0;
+    *plan = q;
+  }
+}
+
+hipError_t launch_plan_lds(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
+                           const PartParent *prev_parents, PartParent *parents,
+                           int32_t *tile_begin, int32_t *hist_begin, PartTile *tiles,
+                           HistTask *hist_tasks, SplitTask *split_tasks, const NodeSeg *segs,
+                           const long long *totals, const SplitCand *cand, double *kept_e,
+                           const double *prev_parent_e, double *parent_e, int32_t F_sel,
+                           PlanArgs a) {
+  hipLaunchKernelGGL(k_plan_lds, dim3(1), dim3(kPlanBlock), 0, st, nodes, plan, prev_parents,
+                     parents, tile_begin, hist_begin, tiles, hist_tasks, split_tasks, segs,
+                     totals, cand, kept_e, prev_parent_e, parent_e, F_sel, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                        const PartParent *prev_parents, PartParent *parents,
                        int32_t *tile_begin, int32_t *hist_begin,

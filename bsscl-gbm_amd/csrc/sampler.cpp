@@ -23,15 +23,18 @@
 // stages that run on their own threads without changing the sequence:
 //   * a draw thread twists and tempers whole 624-word blocks (AVX-512 when
 //     the CPU has it), a chunk at a time, and turns the words into the
-//     bounded draws j(i) of every round.  For long shuffles it only counts:
-//     it decides which words are accepted, without storing draws, and hands
-//     each chunk's part of the round (the chunk's state, first word, step)
-//     to worker threads, which regenerate the chunk and write its draws.
-//     Within a run of steps with a constant mask, W = 64 (then 16) words are
-//     classified at once: a word <= i - (W-1) is accepted whatever happened
-//     to the words before it (each acceptance lowers i by one), a word > i
-//     is rejected whatever happened, and only a block holding a word in
-//     between is decided with a narrower window or one word at a time;
+//     bounded draws j(i) of every round.  Within a run of steps with a
+//     constant mask, W = 64 (then 16) words are classified at once: a word
+//     <= i - (W-1) is accepted whatever happened to the words before it
+//     (each acceptance lowers i by one), a word > i is rejected whatever
+//     happened, and only a block holding a word in between is decided with
+//     a narrower window or one word at a time;
+//   * long shuffles are counted in parallel instead: a twister thread makes
+//     each chunk's first-block state ahead of time, worker threads compute
+//     every chunk's transfer function (entry step -> exit step) over a
+//     window of likely entry steps, the draw thread maps the true entry
+//     step through the chunks in order, and worker threads regenerate each
+//     chunk and write its draws (see "Parallel draws" below);
 //   * the swaps: in device-rows mode the draws are handed to the engine,
 //     which applies them on the GPU (bsscl_fisher_yates_apply); otherwise a
 //     swap thread applies them on the host and delivers sample_idx.

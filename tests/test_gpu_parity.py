@@ -278,17 +278,19 @@ def test_fit_lockstep_and_end_to_end(engine, name):
 
 def test_fit_device_replay_fallbacks_agree(engine, monkeypatch):
     """The round's device replay (pipelined and not), the host replay
-    (forced), and the path that regrows a too-small node table give
-    identical trees and losses."""
+    (forced), the path that regrows a too-small node table, and the general
+    planner in place of the LDS one give identical trees and losses."""
     from bsscl_gbm import HybridHistGBMNumbaV1_0_1
     X, y, params = _fit_case("nan_imbalanced")
     params = dict(params, n_estimators=6)
     fits = {}
-    hooks = ("BSSCL_TEST_HOST_REPLAY", "BSSCL_TEST_NODE_CAP", "BSSCL_TEST_REPLAY_GLOBAL")
+    hooks = ("BSSCL_TEST_HOST_REPLAY", "BSSCL_TEST_NODE_CAP", "BSSCL_TEST_REPLAY_GLOBAL",
+             "BSSCL_TEST_PLAN_GLOBAL")
     for mode, env in [("device", {}), ("sync", {}), ("host", {"BSSCL_TEST_HOST_REPLAY": "1"}),
                       ("global", {"BSSCL_TEST_REPLAY_GLOBAL": "1"}),
                       ("lds", {"BSSCL_TEST_REPLAY_GLOBAL": "2"}),
-                      ("regrow", {"BSSCL_TEST_NODE_CAP": "9"})]:
+                      ("regrow", {"BSSCL_TEST_NODE_CAP": "9"}),
+                      ("plan_global", {"BSSCL_TEST_PLAN_GLOBAL": "1"})]:
         _announce(f"fit replay path {mode}")
         for k in hooks:
             monkeypatch.delenv(k, raising=False)
@@ -300,7 +302,7 @@ def test_fit_device_replay_fallbacks_agree(engine, monkeypatch):
     for k in hooks:
         monkeypatch.delenv(k, raising=False)
     ref = fits["device"]
-    for mode in ("sync", "host", "global", "lds", "regrow"):
+    for mode in ("sync", "host", "global", "lds", "regrow", "plan_global"):
         got = fits[mode]
         assert got.train_loss_history_ == ref.train_loss_history_, mode
         for a, b in zip(ref.trees, got.trees):
