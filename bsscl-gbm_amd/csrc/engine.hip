@@ -714,7 +714,7 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
     CHK(E->rid_c[s].ensure((size_t)ld_c));
   }
   CHK(E->tiles_d.ensure((size_t)tcap));
-  CHK(E->tile_left_d.ensure((size_t)tcap));
+  CHK(E->tile_left_d.ensure((size_t)tcap + 4));  // 16-byte reads past the last tile
   CHK(E->tile_off_d.ensure((size_t)tcap));
   CHK(E->hist_tasks_d.ensure((size_t)hcap));
   CHK(E->part_d.ensure((size_t)hcap * F_sel * kHistPerFeat));
@@ -859,16 +859,18 @@ int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parent
   CHK(prof_begin(E, 1, &stop));
   HIPCHK(launch_part_count(E->st, E->codes_c[src].p, E->ld_c, parents, tiles, plan,
                            max_tiles, E->part_rows, E->tile_left_d.p));
-  HIPCHK(launch_part_scan(E->st, parents, plan, std::min(max_parents, 1024), tile_begin,
-                          E->tile_left_d.p, E->tile_off_d.p, E->nleft_d.p, E->segs.p,
-                          E->hist_node_d.p, min_samples_leaf));
-  if (move_rows)
+  if (move_rows)  // the scatter does each parent's scan itself
     HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p, E->ld_c,
                                E->gh_c[src].p, E->gh_c[dst].p,
                                E->track_rid ? E->rid_c[src].p : nullptr,
                                E->track_rid ? E->rid_c[dst].p : nullptr, parents, tiles,
-                               plan, max_tiles,
-                               E->part_rows, E->tile_off_d.p, E->nleft_d.p, F_sel));
+                               plan, max_tiles, E->part_rows, tile_begin, E->tile_left_d.p,
+                               E->nleft_d.p, E->segs.p, E->hist_node_d.p, min_samples_leaf,
+                               F_sel));
+  else
+    HIPCHK(launch_part_scan(E->st, parents, plan, std::min(max_parents, 1024), tile_begin,
+                            E->tile_left_d.p, E->tile_off_d.p, E->nleft_d.p, E->segs.p,
+                            E->hist_node_d.p, min_samples_leaf));
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }

@@ -239,8 +239,9 @@ hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                const PartParent *parents,
                                const PartTile *tiles, const LevelPlan *plan,
                                int32_t max_tiles, int32_t part_rows,
-                               const int64_t *tile_left_off,
-                               const int64_t *parent_nleft, int32_t F_sel);
+                               const int32_t *tile_begin, const int32_t *tile_left,
+                               int64_t *parent_nleft, NodeSeg *segs, int32_t *hist_node,
+                               int32_t min_samples_leaf, int32_t F_sel);
 hipError_t launch_split(hipStream_t st, const SplitTask *tasks,
                         const LevelPlan *plan, int32_t max_tasks,
                         const NodeSeg *segs, unsigned long long *pool,

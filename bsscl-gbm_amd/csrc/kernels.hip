@@ -936,16 +936,24 @@ constexpr int kChunkSlots = 2;  // output chunks a thread may own (<= 260 per ti
 // tiles; one for 16-row tiles, whose registers already limit occupancy.
 template <int R> struct ScatterFeats { static constexpr int value = 4; };
 template <> struct ScatterFeats<16> { static constexpr int value = 1; };
+// Waves per SIMD the register budget must allow (the occupancy each tile
+// shape had before the parents' scan moved into this kernel).
+template <int R> struct ScatterWaves { static constexpr int value = 5; };
+template <> struct ScatterWaves<4> { static constexpr int value = 7; };
 
 template <int R>
-__global__ __launch_bounds__(kPartBlock) void k_part_scatter(
+__global__ __launch_bounds__(kPartBlock) __attribute__((amdgpu_waves_per_eu(ScatterWaves<R>::value)))
+void k_part_scatter(
     const uint8_t *__restrict__ codes_src, uint8_t *__restrict__ codes_dst,
     int64_t ld_c, const int2 *__restrict__ gh_src, int2 *__restrict__ gh_dst,
     const int32_t *__restrict__ rid_src, int32_t *__restrict__ rid_dst,
     const PartParent *__restrict__ parents, const PartTile *__restrict__ tiles,
-    const LevelPlan *__restrict__ plan, const int64_t *__restrict__ tile_left_off,
-    const int64_t *__restrict__ parent_nleft, int32_t F_sel) {
+    const LevelPlan *__restrict__ plan, const int32_t *__restrict__ tile_begin,
+    const int32_t *__restrict__ tile_left, int64_t *__restrict__ parent_nleft,
+    NodeSeg *__restrict__ segs, int32_t *__restrict__ hist_node, int32_t min_samples_leaf,
+    int32_t F_sel) {
   __shared__ uint32_t tmp[kPartBlock / 64];
+  __shared__ unsigned long long red[kPartBlock / 64];
   constexpr int kTile = kPartBlock * R;
   __shared__ uint16_t inv[kTile];
   constexpr int kScatterFeats = ScatterFeats<R>::value;
@@ -958,18 +966,64 @@ __global__ __launch_bounds__(kPartBlock) void k_part_scatter(
     const PartParent P = parents[t.parent];
     int64_t lo, hi;
     tile_rows(t, P, lo, hi);
-    const int64_t loff = tile_left_off[ti];
-    const int64_t nl = parent_nleft[t.parent];
-    const int64_t lbase = P.start + loff;
-    const int64_t rbase = P.start + nl + ((lo - P.start) - loff);
     const int64_t row = t.row0 + (int64_t)R * tid;
     const CodeWords<R> sc = load_codes<R>(codes_src + (int64_t)P.fpos * ld_c, row, lo, hi);
+    // Left rows of the parent before this tile (high word) and in all its
+    // tiles (low word), from k_part_count's per-tile counts: the parent's
+    // scan, done by each of its tiles.
+    // (16-byte loads of four counts, two per thread in flight: one wait
+    // covers 2048 tiles; tile_left has room for the aligned overrun.)
+    const int32_t tb0 = tile_begin[t.parent], tb1 = tile_begin[t.parent + 1];
+    unsigned long long acc = 0ull;
+    for (int k0 = (tb0 & ~3) + 4 * tid; k0 < tb1; k0 += 8 * kPartBlock) {
+      const int k1 = k0 + 4 * kPartBlock;
+      const uint4 a = *reinterpret_cast<const uint4 *>(tile_left + k0);
+      const uint4 b = k1 < tb1 ? *reinterpret_cast<const uint4 *>(tile_left + k1)
+                               : make_uint4(0u, 0u, 0u, 0u);
+      const uint32_t va[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int k = (u < 4 ? k0 : k1) + (u & 3);
+        const unsigned long long v = (k >= tb0 && k < tb1) ? (unsigned long long)va[u] : 0ull;
+        acc += v + (k < ti ? v << 32 : 0ull);
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane_id() == 0) red[tid >> 6] = acc;
     uint32_t vmask, lmask;
     row_masks<R>(sc, row, lo, hi, (uint32_t)P.bin, vmask, lmask);
     const uint32_t packed = ((uint32_t)__builtin_popcount(vmask) << 16) |
                             (uint32_t)__builtin_popcount(lmask);
     uint32_t tot;
-    const uint32_t pre = block_excl_scan<kPartBlock>(packed, tmp, tot);
+    const uint32_t pre = block_excl_scan<kPartBlock>(packed, tmp, tot);  // (its barriers publish red)
+    unsigned long long psum = 0ull;
+#pragma unroll
+    for (int w = 0; w < kPartBlock / 64; ++w) psum += red[w];
+    const int64_t loff = (int64_t)(psum >> 32), nl = (int64_t)(psum & 0xffffffffull);
+    const int64_t lbase = P.start + loff;
+    const int64_t rbase = P.start + nl + ((lo - P.start) - loff);
+    if (ti == tb0 && tid == 0) {
+      // The children's segments, whether the split is kept (est:678-683)
+      // and which child is the smaller one (est:701-709), whose histogram
+      // is built.
+      const int64_t nr = P.count - nl;
+      const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
+      const bool left_small = nl <= nr;
+      parent_nleft[t.parent] = nl;
+      NodeSeg Ls, Rs;
+      Ls.start = P.start;
+      Ls.count = nl;
+      Ls.valid = ok ? 1 : 0;
+      Ls.is_small = left_small ? 1 : 0;
+      Rs.start = P.start + nl;
+      Rs.count = nr;
+      Rs.valid = ok ? 1 : 0;
+      Rs.is_small = left_small ? 0 : 1;
+      segs[P.left_id] = Ls;
+      segs[P.right_id] = Rs;
+      hist_node[t.parent] = ok ? (left_small ? P.left_id : P.right_id) : -1;
+    }
     const int ltot = (int)(tot & 0xffffu), vtot = (int)(tot >> 16);
     const int rtot = vtot - ltot;
     const int lpre = (int)(pre & 0xffffu), rpre = (int)(pre >> 16) - lpre;
@@ -1080,13 +1134,15 @@ hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                const PartParent *parents,
                                const PartTile *tiles, const LevelPlan *plan,
                                int32_t max_tiles, int32_t part_rows,
-                               const int64_t *tile_left_off,
-                               const int64_t *parent_nleft, int32_t F_sel) {
+                               const int32_t *tile_begin, const int32_t *tile_left,
+                               int64_t *parent_nleft, NodeSeg *segs, int32_t *hist_node,
+                               int32_t min_samples_leaf, int32_t F_sel) {
   if (max_tiles <= 0) return hipSuccess;
 #define BSSCL_SCATTER(R)                                                                 \
   hipLaunchKernelGGL(k_part_scatter<R>, dim3((unsigned)max_tiles), dim3(kPartBlock), 0, st, \
                      codes_src, codes_dst, ld_c, gh_src, gh_dst, rid_src, rid_dst, parents, \
-                     tiles, plan, tile_left_off, parent_nleft, F_sel)
+                     tiles, plan, tile_begin, tile_left, parent_nleft, segs, hist_node,   \
+                     min_samples_leaf, F_sel)
   switch (part_rows) {
     case 4: BSSCL_SCATTER(4); break;
     case 8: BSSCL_SCATTER(8); break;
@@ -1500,7 +1556,8 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
       split_tasks[2 * i + 1] = SplitTask{L + 1, v, L, a.level + 1};
     }
     const int64_t a0 = N.start & ~int64_t(15);
-    tile_begin[i] = (int32_t)((N.start + N.count - a0 + a.part_tile - 1) / a.part_tile);
+    // At least one tile: a parent's first tile writes its children's segments.
+    tile_begin[i] = (int32_t)max((int64_t)1, (N.start + N.count - a0 + a.part_tile - 1) / a.part_tile);
     rows += (unsigned long long)(N.count / 2);
   }
 #pragma unroll
@@ -1788,7 +1845,8 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
         split_tasks[2 * i + 1] = SplitTask{L + 1, v, L, a.level + 1};
       }
       const int64_t a0 = N.start & ~int64_t(15);
-      s_tb[i] = (int32_t)((N.start + N.count - a0 + a.part_tile - 1) / a.part_tile);
+      // At least one tile: a parent's first tile writes its children's segments.
+      s_tb[i] = (int32_t)max((int64_t)1, (N.start + N.count - a0 + a.part_tile - 1) / a.part_tile);
       s_pj[i] = tid;
       rows = (unsigned long long)(N.count / 2);
     }
