@@ -212,9 +212,16 @@ struct bsscl_engine {
   double g_scale = 1.0, h_scale = 1.0;  // fixed point -> value
 
   // Tree workspace.
-  DevBuf<uint8_t> codes_c[2];
-  DevBuf<int2> gh_c[2];
-  DevBuf<int32_t> rid_c[2];
+  // Compact row sets: a tree uses sets set_base and set_base + 1 (levels
+  // alternate); a boosting round in slot s uses base 2s, so the next round's
+  // root codes are gathered while this round's tree still reads its own.
+  DevBuf<uint8_t> codes_c[4];
+  DevBuf<int2> gh_c[4];
+  DevBuf<int32_t> rid_c[2];  // with set_base 0 only
+  int32_t set_base = 0;
+  DevBuf<int32_t> feat_slot_d[2];          // a round's selected features (rows stream)
+  int32_t *feat_pin[2] = {nullptr, nullptr};
+  int32_t feat_pin_n[2] = {0, 0};
   bool track_rid = false;  // carry row ids through the partition (bsscl_partition)
   int64_t ld_c = 0;
   DevBuf<int32_t> round_rows[2];  // in-bag rows of round slot s, ascending
@@ -374,6 +381,7 @@ int prof_collect(bsscl_engine *E, uint64_t upto = UINT64_MAX) {
 }
 
 int sync(bsscl_engine *E) {
+  HIPCHK(hipStreamSynchronize(E->st_rows));
   HIPCHK(hipStreamSynchronize(E->st));
   CHK(prof_collect(E));
   E->pin.reset();
@@ -685,9 +693,10 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
   read_hist_tuning(E, m, F_sel);
   const int64_t ld_c = round_up(m + 32, 256);
   bool grow = false;
+  const int b = E->set_base;
   for (int s = 0; s < 2; ++s)
-    grow = grow || E->codes_c[s].cap < (size_t)ld_c * F_sel || E->gh_c[s].cap < (size_t)ld_c ||
-           E->rid_c[s].cap < (size_t)ld_c;
+    grow = grow || E->codes_c[b + s].cap < (size_t)ld_c * F_sel ||
+           E->gh_c[b + s].cap < (size_t)ld_c || (b == 0 && E->rid_c[s].cap < (size_t)ld_c);
   int32_t cap = std::max(initial_node_cap(levels, max_leaves), E->node_cap_floor);
   // Test hook: a small starting node table, to exercise the regrowth path.
   if (const char *t = std::getenv("BSSCL_TEST_NODE_CAP")) {
@@ -709,9 +718,9 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
   if (grow) CHK(sync(E));
   E->ld_c = ld_c;
   for (int s = 0; s < 2; ++s) {
-    CHK(E->codes_c[s].ensure((size_t)ld_c * F_sel));
-    CHK(E->gh_c[s].ensure((size_t)ld_c));
-    CHK(E->rid_c[s].ensure((size_t)ld_c));
+    CHK(E->codes_c[b + s].ensure((size_t)ld_c * F_sel));
+    CHK(E->gh_c[b + s].ensure((size_t)ld_c));
+    if (b == 0) CHK(E->rid_c[s].ensure((size_t)ld_c));
   }
   CHK(E->tiles_d.ensure((size_t)tcap));
   CHK(E->tile_left_d.ensure((size_t)tcap + 4));  // 16-byte reads past the last tile
@@ -745,7 +754,8 @@ SplitParams split_params(bsscl_engine *E, const TreeParams &tp) {
 // The feature list, the root's tasks and its LevelPlan go up in one copy.
 int launch_root(bsscl_engine *E, const int32_t *rows32, int64_t m,
                 const std::vector<int32_t> &feats,
-                const std::vector<int32_t> &nb_sel, const TreeParams &tp) {
+                const std::vector<int32_t> &nb_sel, const TreeParams &tp, bool gathered) {
+  const int b = E->set_base;
   const Matrix &X = E->mat[0];
   const int32_t F_sel = (int32_t)feats.size();
   const int32_t th = hist_tile_rows(E, m, F_sel);
@@ -783,14 +793,17 @@ int launch_root(bsscl_engine *E, const int32_t *rows32, int64_t m,
   E->feat_d = feat_d;
   E->nb_sel_d = reinterpret_cast<const int32_t *>(dv[1]);
   E->hot_sel_d = E->nb_sel_d + F_sel;
-  HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, feat_d, F_sel,
-                            rows32, rows32 ? nullptr : E->rows64.p, m, E->ghq.p,
-                            E->codes_c[0].p, E->ld_c, E->gh_c[0].p,
-                            E->track_rid ? E->rid_c[0].p : nullptr,
-                            E->ld_c, E->segs.p, E->hist_node_d.p));
+  // (A boosting round's root rows are already in set b: launch_gather_codes
+  // and launch_gather_gh.)
+  if (!gathered)
+    HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, feat_d, F_sel,
+                              rows32, rows32 ? nullptr : E->rows64.p, m, E->ghq.p,
+                              E->codes_c[b].p, E->ld_c, E->gh_c[b].p,
+                              E->track_rid && b == 0 ? E->rid_c[0].p : nullptr,
+                              E->ld_c, E->segs.p, E->hist_node_d.p));
   hipEvent_t stop;
   CHK(prof_begin(E, 0, &stop));
-  HIPCHK(launch_hist(E->st, E->codes_c[0].p, E->ld_c, E->gh_c[0].p,
+  HIPCHK(launch_hist(E->st, E->codes_c[b].p, E->ld_c, E->gh_c[b].p,
                      reinterpret_cast<const HistTask *>(dv[2]), E->plan_d, rp.n_hist,
                      E->hist_node_d.p, reinterpret_cast<const int32_t *>(dv[5]), E->segs.p,
                      E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel), E->hist_copies,
@@ -862,8 +875,8 @@ int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parent
   if (move_rows)  // the scatter does each parent's scan itself
     HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p, E->ld_c,
                                E->gh_c[src].p, E->gh_c[dst].p,
-                               E->track_rid ? E->rid_c[src].p : nullptr,
-                               E->track_rid ? E->rid_c[dst].p : nullptr, parents, tiles,
+                               E->track_rid ? E->rid_c[src & 1].p : nullptr,
+                               E->track_rid ? E->rid_c[dst & 1].p : nullptr, parents, tiles,
                                plan, max_tiles, E->part_rows, tile_begin, E->tile_left_d.p,
                                E->nleft_d.p, E->segs.p, E->hist_node_d.p, min_samples_leaf,
                                F_sel));
@@ -881,7 +894,7 @@ int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parent
 // totals only, so their rows are not moved and their histograms not built.
 int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
                  const TreeParams &tp, int32_t F_sel) {
-  const int src = level & 1, dst = src ^ 1;
+  const int src = E->set_base + (level & 1), dst = E->set_base + ((level & 1) ^ 1);
   const PartParent *par = E->parents_d[level & 1].p;
   const int32_t P = level_parents_bound(E, level);
   const int32_t T = (int32_t)std::min<int64_t>(E->tile_cap, m / E->part_tile + 2 * (int64_t)P + 1);
@@ -1017,10 +1030,10 @@ constexpr int32_t kLevelsPerCheck = 8;  // levels enqueued between host checks
 int launch_tree(bsscl_engine *E, const int32_t *rows32, int64_t m,
                 const std::vector<int32_t> &feats,
                 const std::vector<int32_t> &nb_sel, const TreeParams &tp, int32_t *run,
-                bool checks = true) {
+                bool checks = true, bool gathered = false) {
   const int32_t F_sel = (int32_t)feats.size();
   const int32_t levels = std::max(1, tp.max_depth);
-  CHK(launch_root(E, rows32, m, feats, nb_sel, tp));
+  CHK(launch_root(E, rows32, m, feats, nb_sel, tp, gathered));
   *run = 0;
   for (int32_t d = 0; d < levels; ++d) {
     const bool last = d + 1 >= tp.max_depth;
@@ -1275,7 +1288,6 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   const double gm = fixed_mul(wmax), hm = fixed_mul(0.25 * wmax);
   E->g_scale = 1.0 / gm;
   E->h_scale = 1.0 / hm;
-  HIPCHK(launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, gm, hm, E->ghq.p));
   SamplerRound sr;
   void *token = nullptr;
   const auto t_wait0 = std::chrono::steady_clock::now();
@@ -1317,6 +1329,28 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
       else R.nb_sel[(size_t)i] = a.bin_counts[f];
     }
   }
+  const TreeParams tp{a.max_leaves, a.max_depth, a.min_samples_leaf, a.min_child_weight,
+                      a.reg_lambda, a.gamma};
+  const int32_t F_sel = (int32_t)R.feats.size();
+  const int nb = update_F_blocks(X.n);
+  // More candidate slots than the device replay holds: host replay only.
+  // (Test hook: BSSCL_TEST_HOST_REPLAY=1 forces the host path.)
+  const char *force_host = std::getenv("BSSCL_TEST_HOST_REPLAY");
+  R.device_replay = a.max_leaves + 2 <= kReplaySlots && !(force_host && force_host[0] == '1');
+  // The tree's compact row sets: 2s and 2s + 1.
+  E->set_base = 2 * s;
+  if (rc == BSSCL_OK && R.device_replay)
+    rc = prepare_tree_buffers(E, m, F_sel, std::max(1, a.max_depth), a.max_leaves);
+  if (rc == BSSCL_OK && R.device_replay && E->feat_pin_n[s] < F_sel) {
+    if (E->feat_pin[s]) (void)hipHostFree(E->feat_pin[s]);
+    E->feat_pin[s] = nullptr;
+    E->feat_pin_n[s] = 0;
+    hipError_t e = hipHostMalloc(reinterpret_cast<void **>(&E->feat_pin[s]),
+                                 (size_t)std::max(F_sel, 1) * 4, hipHostMallocDefault);
+    if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("feature list: ") + hipGetErrorString(e));
+    else E->feat_pin_n[s] = std::max(F_sel, 1);
+  }
+  if (rc == BSSCL_OK && R.device_replay) rc = E->feat_slot_d[s].ensure((size_t)std::max(F_sel, 1));
   // The round's in-bag rows on the device, ascending: the reference's
   // sample_idx (a prefix of the cumulative permutation) sorted.  Made on
   // the rows stream; only that stream touches the permutation, the
@@ -1377,6 +1411,17 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     if (rc == BSSCL_OK && e == hipSuccess && rows_d)
       e = launch_sort_rows(rs, rows_d, m, E->row_flags.p, n_pad, E->sort_tmp.p,
                            E->round_rows[s].p);
+    // The root's codes too (sets 2s, 2s + 1 were last read by the tree of
+    // the round before the previous one).  feat_pin[s] was last copied by
+    // that round's rows stream.
+    if (rc == BSSCL_OK && e == hipSuccess && R.device_replay) {
+      std::memcpy(E->feat_pin[s], R.feats.data(), (size_t)F_sel * 4);
+      e = hipMemcpyAsync(E->feat_slot_d[s].p, E->feat_pin[s], (size_t)F_sel * 4,
+                         hipMemcpyHostToDevice, rs);
+      if (e == hipSuccess)
+        e = launch_gather_codes(rs, X.codes.p, X.ld, E->feat_slot_d[s].p, F_sel,
+                                E->round_rows[s].p, m, E->codes_c[2 * s].p, E->ld_c, E->ld_c);
+    }
     if (rc == BSSCL_OK && e == hipSuccess && !E->rows_ready[s])
       e = hipEventCreateWithFlags(&E->rows_ready[s], hipEventDisableTiming);
     if (rc == BSSCL_OK && e == hipSuccess) e = hipEventRecord(E->rows_ready[s], rs);
@@ -1384,21 +1429,24 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     if (rc == BSSCL_OK && e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("rows: ") + hipGetErrorString(e));
   }
   if (rc != BSSCL_OK) return fail(rc);
-  const TreeParams tp{a.max_leaves, a.max_depth, a.min_samples_leaf, a.min_child_weight,
-                      a.reg_lambda, a.gamma};
-  const int32_t F_sel = (int32_t)R.feats.size();
-  const int nb = update_F_blocks(X.n);
-  // More candidate slots than the device replay holds: host replay only.
-  // (Test hook: BSSCL_TEST_HOST_REPLAY=1 forces the host path.)
-  const char *force_host = std::getenv("BSSCL_TEST_HOST_REPLAY");
-  R.device_replay = a.max_leaves + 2 <= kReplaySlots && !(force_host && force_host[0] == '1');
+  // Gradients from the current F (est:2868): for the in-bag rows, straight
+  // into the root's set, on the device path; for every row otherwise (the
+  // host-driven path gathers them).
+  {
+    hipError_t e = R.device_replay
+                       ? launch_gather_gh(E->st, E->F.p, E->y.p, E->round_rows[s].p, m, E->w0,
+                                          E->w1, gm, hm, E->gh_c[2 * s].p, E->ld_c, E->segs.p,
+                                          E->hist_node_d.p)
+                       : launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, gm, hm,
+                                          E->ghq.p);
+    if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("gradients: ") + hipGetErrorString(e));
+  }
   if (rc == BSSCL_OK) rc = E->partials_d.ensure((size_t)nb);
   if (rc == BSSCL_OK) rc = E->tree_d.ensure((size_t)R.M);
-  if (rc == BSSCL_OK && R.device_replay)
-    rc = prepare_tree_buffers(E, m, F_sel, std::max(1, a.max_depth), a.max_leaves);
   if (rc == BSSCL_OK) rc = ensure_round_out(E, s, R.M);
   if (rc == BSSCL_OK && R.device_replay)
-    rc = launch_tree(E, E->round_rows[s].p, m, R.feats, R.nb_sel, tp, &R.run, !E->pipeline);
+    rc = launch_tree(E, E->round_rows[s].p, m, R.feats, R.nb_sel, tp, &R.run, !E->pipeline,
+                     true);
   if (rc == BSSCL_OK && R.device_replay) {
     RoundHeader *hdr = reinterpret_cast<RoundHeader *>(E->round_d[s].p);
     ReplayArgs ra;
@@ -1490,6 +1538,14 @@ int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
   // F was left alone: build the tree on the host-driven path and apply it.
   // (Never with a round enqueued behind this one: see pipeline_safe.)
   if (h.status == 1) E->node_cap_floor = std::max(h.needed, 2 * E->node_cap);
+  {
+    // Gradients of every row from the unchanged F (the device path gathered
+    // only the in-bag rows').
+    const double wmax = std::max(E->w0, E->w1);
+    HIPCHK(launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, fixed_mul(wmax),
+                            fixed_mul(0.25 * wmax), E->ghq.p));
+  }
+  E->set_base = 2 * s;
   CHK(build_tree_core(E, E->round_rows[s].p, R.m, R.feats, R.nb_sel, tp, out));
   CHK(upload_tree(E, out.features, out.thresholds, out.values, out.left, out.right,
                   *out.node_count, X.F));
@@ -1568,10 +1624,14 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->ghq.release();
   E->g64.release();
   E->h64.release();
-  for (int s = 0; s < 2; ++s) {
+  for (int s = 0; s < 4; ++s) {
     E->codes_c[s].release();
     E->gh_c[s].release();
+  }
+  for (int s = 0; s < 2; ++s) {
     E->rid_c[s].release();
+    E->feat_slot_d[s].release();
+    if (E->feat_pin[s]) (void)hipHostFree(E->feat_pin[s]);
   }
   for (auto &r : E->round_rows) r.release();
   E->rows64.release();
@@ -1912,6 +1972,7 @@ int bsscl_build_tree(bsscl_engine *E, const double *grad, const double *hess,
                         hipMemcpyHostToDevice, E->st));
   TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight,
                 reg_lambda, gamma};
+  E->set_base = 0;
   return build_tree_core(E, nullptr, n_samples, feats, nb_sel, tp, out);
 }
 
@@ -2137,8 +2198,9 @@ int bsscl_node_split(bsscl_engine *E, const double *grad, const double *hess,
   // The root of a tree build: histogram and split search of these rows.
   const int32_t F_sel = n_selected;
   TreeParams tp{1, 1, 0, min_child_weight, reg_lambda, 0.0};
+  E->set_base = 0;
   CHK(prepare_tree_buffers(E, m, F_sel, 1, 2));
-  CHK(launch_root(E, nullptr, m, feats, nb_sel, tp));
+  CHK(launch_root(E, nullptr, m, feats, nb_sel, tp, false));
   // No planner follows this root: write its table record here.
   HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, E->plan_d, 1, 0,
                           E->nodes_d));
@@ -2179,6 +2241,7 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
   }
   CHK(E->rows64.ensure((size_t)m));
   HIPCHK(hipMemcpyAsync(E->rows64.p, rows, (size_t)m * 8, hipMemcpyHostToDevice, E->st));
+  E->set_base = 0;
   CHK(prepare_tree_buffers(E, m, 1, 1, 2));
   const int32_t f1 = feature;
   Pack pk;

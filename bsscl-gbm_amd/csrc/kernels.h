@@ -203,6 +203,15 @@ hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               int64_t m, const int2 *ghq, uint8_t *codes_c,
                               int64_t ld_c, int2 *gh_c, int32_t *rid_c,
                               int64_t pad_to, NodeSeg *segs, int32_t *hist_node);
+// Root gather in two parts for a boosting round: the codes (when the rows are
+// known) and the fixed-point (g, h) with the root segment (when F is).
+hipError_t launch_gather_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
+                               const int32_t *feat, int32_t F_sel, const int32_t *rows32,
+                               int64_t m, uint8_t *codes_c, int64_t ld_c, int64_t pad_to);
+hipError_t launch_gather_gh(hipStream_t st, const double *F, const uint8_t *y,
+                            const int32_t *rows32, int64_t m, double w0, double w1,
+                            double g_mul, double h_mul, int2 *gh_c, int64_t pad_to,
+                            NodeSeg *segs, int32_t *hist_node);
 // Level kernels take their work counts from a device LevelPlan; the grid
 // argument (blocks, tasks or parents) is an upper bound, and blocks loop
 // over the work with a grid stride, so any bound >= 1 gives the same result.

@@ -438,6 +438,80 @@ __global__ __launch_bounds__(256) void k_gather_root(
   }
 }
 
+// The in-bag rows' codes alone, for a round whose rows are known before its
+// gradients (the codes are gathered while the previous tree is built).
+__global__ __launch_bounds__(256) void k_gather_codes(
+    const uint8_t *__restrict__ codes, int64_t ld, const int32_t *__restrict__ feat,
+    int32_t F_sel, const int32_t *__restrict__ rows32, int64_t m,
+    uint8_t *__restrict__ codes_c, int64_t ld_c, int64_t pad_to) {
+  const int64_t k0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (k0 >= pad_to) return;
+  int32_t r[4];
+  bool ok[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    ok[k] = (k0 + k) < m;
+    r[k] = ok[k] ? rows32[k0 + k] : 0;
+  }
+  for (int32_t f = 0; f < F_sel; ++f) {
+    const uint8_t *col = codes + (int64_t)feat[f] * ld;
+    uint32_t w = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      w |= (ok[k] ? (uint32_t)col[r[k]] : 0u) << (8 * k);
+    *reinterpret_cast<uint32_t *>(codes_c + (int64_t)f * ld_c + k0) = w;
+  }
+}
+
+// The in-bag rows' fixed-point (g, h) straight from F and y (k_grad_hess's
+// arithmetic, for these rows only), and the root's segment.
+__global__ __launch_bounds__(256) void k_gather_gh(
+    const double *__restrict__ F, const uint8_t *__restrict__ y,
+    const int32_t *__restrict__ rows32, int64_t m, double w0, double w1, double g_mul,
+    double h_mul, int2 *__restrict__ gh_c, int64_t pad_to, NodeSeg *__restrict__ segs,
+    int32_t *__restrict__ hist_node) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k == 0) {
+    NodeSeg r;
+    r.start = 0;
+    r.count = m;
+    r.valid = 1;
+    r.is_small = 1;
+    segs[0] = r;
+    hist_node[0] = 0;
+  }
+  if (k >= pad_to) return;
+  int2 q = make_int2(0, 0);
+  if (k < m) {
+    const int32_t i = rows32[k];
+    const int yi = y[i];
+    double g, h;
+    logistic_gh(F[i], (double)yi, yi ? w1 : w0, g, h);
+    q = make_int2(__double2int_rn(g * g_mul), __double2int_rn(h * h_mul));
+  }
+  gh_c[k] = q;
+}
+
+hipError_t launch_gather_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
+                               const int32_t *feat, int32_t F_sel, const int32_t *rows32,
+                               int64_t m, uint8_t *codes_c, int64_t ld_c, int64_t pad_to) {
+  const int64_t threads = (pad_to + 3) / 4;
+  if (threads <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_gather_codes, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     st, codes, ld, feat, F_sel, rows32, m, codes_c, ld_c, pad_to);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_gh(hipStream_t st, const double *F, const uint8_t *y,
+                            const int32_t *rows32, int64_t m, double w0, double w1,
+                            double g_mul, double h_mul, int2 *gh_c, int64_t pad_to,
+                            NodeSeg *segs, int32_t *hist_node) {
+  if (pad_to <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_gather_gh, dim3((unsigned)((pad_to + 255) / 256)), dim3(256), 0, st,
+                     F, y, rows32, m, w0, w1, g_mul, h_mul, gh_c, pad_to, segs, hist_node);
+  return hipGetLastError();
+}
+
 hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               const int32_t *feat, int32_t F_sel,
                               const int32_t *rows32, const int64_t *rows64,
