@@ -2286,18 +2286,19 @@ __device__ int32_t replay_loop(const ReplayNodes<kStaged> &N, int32_t C, int32_t
 template <bool kStaged>
 __device__ void replay_write(const ReplayNodes<kStaged> &N, const int32_t *__restrict__ feats,
                              int32_t node_count, int32_t M, TreeArrays out,
-                             TreeNodeDev *__restrict__ tree) {
-  for (int32_t i = (int32_t)threadIdx.x; i < M; i += 64) {
+                             TreeNodeDev *__restrict__ tree, const int32_t *o_int = ro_int,
+                             const int32_t *o_left = ro_left, int32_t stride = 64) {
+  for (int32_t i = (int32_t)threadIdx.x; i < M; i += stride) {
     int32_t f = -1, lc = -1, rc = -1;
     int64_t th = 0;
     double val = 0.0, g = 0.0;
     if (i < node_count) {
-      const int32_t v = ro_int[i];
+      const int32_t v = o_int[i];
       val = N.val(v);
-      if (ro_left[i] >= 0) {
+      if (o_left[i] >= 0) {
         f = feats[N.fpos(v)];
         th = N.bin(v);
-        lc = ro_left[i];
+        lc = o_left[i];
         rc = lc + 1;
         g = N.gain(v);
       }
@@ -2368,175 +2369,341 @@ __global__ __launch_bounds__(64) void k_replay(
   }
 }
 
-// The same loop with the candidate slots in registers (slot k in lane
-// k % 64, register k / 64), for up to kRegSlots slots: a pop is a DPP
-// maximum, a ballot, two lane reads and one LDS read of the popped node's
-// precomputed child facts.
+// Trees of up to kRegSlots candidate slots and kReplayNodes nodes: one
+// workgroup.  Best-first search with distinct keys pops nodes in a fixed
+// order.  Let a candidate be a node whose ancestors are all kept splits with
+// key > gamma and whose own key G (best gain, -inf without a split) is
+// > gamma; give each candidate the vector whose component d is the smallest
+// key on its path below depth d (+inf past its depth).  For two candidates,
+// the node on the other's path comes first (its vector is larger at the
+// ancestor's depth); otherwise the paths below their deepest common
+// ancestor hold distinct keys, the one whose smallest such key is larger is
+// popped first (every node of the other path that is popped first had the
+// largest key of the frontier while an unpopped node of this path waited
+// there with a larger one -- impossible), and the vectors first differ
+// exactly there.  So the kernel ranks the candidates by their vectors (keys
+// replaced by their ranks, 11 bits per depth), and the loop's stop rules
+// become a cut of that order: after max_leaves - 1 kept splits; every
+// candidate before it is popped (a candidate whose level loop did not expand
+// it is the replay's failure, status 2).  Output ids follow from the number
+// of kept splits before each one.  Candidates with equal keys (the slot
+// order breaks those ties) or deeper trees run the slot loop below in
+// wave 0.
 constexpr int kRegSlotsPerLane = 2;
 constexpr int kRegSlots = 64 * kRegSlotsPerLane;
+constexpr int kTreeBlock = 1024;
+constexpr int kTreeMaxDepth = 10;  // components of a node's vector (11 bits each)
+constexpr uint32_t kCodeInf = 2047;
+constexpr int32_t kKept = 1 << 30, kLeftSmall = 1 << 29, kChildMask = (1 << 29) - 1;
 
-// Per node v: first child l (or -1), bit 30 = split kept, bit 29 = left
-// child is the smaller; candidate gains of both children (-inf when they
-// cannot be split).
-__shared__ int32_t rq_child[kReplayNodes];
-__shared__ double rq_gl[kReplayNodes], rq_gr[kReplayNodes];
+__shared__ int32_t rq_child[kReplayNodes];  // first child | kept | left smaller, or -1
+__shared__ double rt_G[kReplayNodes];
+__shared__ int16_t rt_parent[kReplayNodes], rt_code[kReplayNodes], rt_at[kReplayNodes];
+__shared__ int16_t rt_kk[kReplayNodes];  // kept splits popped before a popped kept split, else -1
+__shared__ uint8_t rt_pc[kReplayNodes], rt_depth[kReplayNodes];
+// Staging of the child facts, then the candidates' keys, then their vectors.
+__shared__ __align__(16) unsigned long long rt_raw[2 * kReplayNodes];
+__shared__ int32_t rt_int[2 * kRegSlots + 2], rt_left[2 * kRegSlots + 2];
+__shared__ int32_t rt_flags[4];  // [0] slot loop needed, [1] candidates, [2] status, [3] nodes
 
-__global__ __launch_bounds__(64) void k_replay_regs(
+// The slot loop (one wave): candidate slot k in lane k % 64, register
+// k / 64; a pop is a DPP maximum, a ballot and two lane reads.
+__device__ int32_t replay_slot_loop(int32_t C, const ReplayArgs &a, int32_t &status) {
+  const int lane = lane_id();
+  double g[kRegSlotsPerLane];
+  int32_t sid[kRegSlotsPerLane], sint[kRegSlotsPerLane];
+  bool act[kRegSlotsPerLane];
+#pragma unroll
+  for (int q = 0; q < kRegSlotsPerLane; ++q) {
+    g[q] = -INFINITY;
+    sid[q] = 0;
+    sint[q] = 0;
+    act[q] = false;
+  }
+  int32_t node_count = 1;
+  if (lane == 0) {
+    rt_int[0] = 0;
+    rt_left[0] = -1;
+  }
+  if (rp_fpos[0] < 0) return node_count;
+  if (lane == 0) {
+    g[0] = rp_gain[0];
+    act[0] = true;
+  }
+  int32_t n_splits = 0;
+  while (n_splits < a.max_leaves - 1) {
+    double lmax = g[0];
+#pragma unroll
+    for (int q = 1; q < kRegSlotsPerLane; ++q) lmax = fmax(lmax, g[q]);
+    const double best = wave_max_f64(lmax);
+    if (!(best > a.gamma)) break;
+    int32_t ci = -1;
+#pragma unroll
+    for (int q = 0; q < kRegSlotsPerLane; ++q) {
+      const unsigned long long m = __ballot(g[q] == best);
+      if (ci < 0 && m) ci = 64 * q + __builtin_ctzll(m);
+    }
+    const int cq = ci >> 6, cl = ci & 63;
+    int32_t v = 0, cur = 0;
+#pragma unroll
+    for (int q = 0; q < kRegSlotsPerLane; ++q)
+      if (q == cq) {
+        v = __builtin_amdgcn_readlane(sint[q], cl);
+        cur = __builtin_amdgcn_readlane(sid[q], cl);
+      }
+    const int32_t c = rq_child[v];
+    if (c < 0) {
+      status = 2;
+      break;
+    }
+    // The popped slot is free again.
+#pragma unroll
+    for (int q = 0; q < kRegSlotsPerLane; ++q)
+      if (q == cq && lane == cl) {
+        act[q] = false;
+        g[q] = -INFINITY;
+      }
+    if (!(c & kKept)) {  // est:678-683: the node stays a leaf
+      if (lane == 0) {
+        rt_int[cur] = v;
+        rt_left[cur] = -1;
+      }
+      continue;
+    }
+    const int32_t l = c & kChildMask;
+    const bool left_small = (c & kLeftSmall) != 0;
+    const int32_t left_id = node_count, right_id = node_count + 1;
+    node_count += 2;
+    ++n_splits;
+    // The first two free slots other than ci, in slot order.
+    int32_t slot_small = -1, slot_large = -1;
+#pragma unroll
+    for (int q = 0; q < kRegSlotsPerLane; ++q) {
+      const int32_t k = 64 * q + lane;
+      unsigned long long m = __ballot(k < C && k != ci && !act[q]);
+      while (m && slot_large < 0) {
+        const int32_t kk = 64 * q + __builtin_ctzll(m);
+        m &= m - 1;
+        if (slot_small < 0) slot_small = kk;
+        else slot_large = kk;
+      }
+    }
+    if (slot_large < 0) {
+      status = 3;
+      break;
+    }
+    const double gl = rt_G[l], gr = rt_G[l + 1];
+#pragma unroll
+    for (int q = 0; q < kRegSlotsPerLane; ++q) {
+      const int32_t k = 64 * q + lane;
+      if (k == slot_small || k == slot_large) {
+        const bool is_left = (k == slot_small) == left_small;
+        act[q] = true;
+        sid[q] = is_left ? left_id : right_id;
+        sint[q] = is_left ? l : l + 1;
+        g[q] = is_left ? gl : gr;
+      }
+    }
+    if (lane == 0) {
+      rt_int[cur] = v;
+      rt_left[cur] = left_id;
+    }
+  }
+  if (status == 0) {
+#pragma unroll
+    for (int q = 0; q < kRegSlotsPerLane; ++q)
+      if (act[q]) {
+        rt_int[sid[q]] = sint[q];
+        rt_left[sid[q]] = -1;
+      }
+  }
+  return node_count;
+}
+
+__global__ __launch_bounds__(kTreeBlock) void k_replay_tree(
     const NodeOut *__restrict__ nodes, const LevelPlan *__restrict__ plan,
     const int32_t *__restrict__ feats, ReplayArgs a, TreeArrays out,
     TreeNodeDev *__restrict__ tree, RoundHeader *__restrict__ hdr) {
-  const int lane = (int)threadIdx.x;
+  __shared__ uint32_t stmp[kTreeBlock / 64];
+  const int tid = (int)threadIdx.x, wave = tid >> 6;
   const int32_t M = a.out_len;
   const int32_t C = a.max_leaves + 2;
   int32_t status = 0, needed = 0;
   const LevelPlan pl = *plan;
-  const int32_t n_nodes = pl.n_nodes;
+  const int32_t n = pl.n_nodes;
   if (pl.overflow > 0) {
     status = 1;
     needed = pl.overflow;
   } else if (pl.overflow < 0) {
     status = 5;
-  } else if (C > kRegSlots || M > kReplayOut || n_nodes > kReplayNodes) {
+  } else if (C > kRegSlots || M > 2 * kRegSlots + 2 || n > kReplayNodes || n < 1) {
     status = 4;
   }
   int32_t node_count = 0;
-  if (status == 0) {
-    for (int32_t i = lane; i < n_nodes; i += 64) {
+  if (status == 0) {  // (uniform)
+    int32_t *cnt = reinterpret_cast<int32_t *>(rt_raw);
+    int32_t *lft = cnt + kReplayNodes;
+    uint8_t *vld = reinterpret_cast<uint8_t *>(lft + kReplayNodes);
+    for (int32_t i = tid; i < n; i += kTreeBlock) {
       const NodeOut nd = nodes[i];
       rp_gain[i] = nd.gain;
       rp_val[i] = leaf_value(nd, a);
       rp_fpos[i] = nd.fpos;
       rp_bin[i] = (uint8_t)nd.bin;
+      rt_G[i] = nd.fpos >= 0 ? nd.gain : -INFINITY;
+      cnt[i] = (int32_t)nd.count;
+      lft[i] = nd.left;
+      vld[i] = (uint8_t)nd.valid;
+      rt_parent[i] = -1;
+      rt_kk[i] = -1;
     }
+    if (tid < 4) rt_flags[tid] = 0;
     __syncthreads();
-    for (int32_t v = lane; v < n_nodes; v += 64) {
-      const int32_t l = nodes[v].left;
+    for (int32_t v = tid; v < n; v += kTreeBlock) {
+      const int32_t l = lft[v];
       int32_t c = -1;
-      double gl = -INFINITY, gr = -INFINITY;
       if (l >= 0) {
-        const NodeOut L = nodes[l], R = nodes[l + 1];
-        c = l | (L.valid ? (1 << 30) : 0) | (L.count <= R.count ? (1 << 29) : 0);
-        gl = rp_fpos[l] >= 0 ? rp_gain[l] : -INFINITY;
-        gr = rp_fpos[l + 1] >= 0 ? rp_gain[l + 1] : -INFINITY;
+        c = l | (vld[l] ? kKept : 0) | (cnt[l] <= cnt[l + 1] ? kLeftSmall : 0);
+        rt_parent[l] = (int16_t)v;
+        rt_parent[l + 1] = (int16_t)v;
       }
       rq_child[v] = c;
-      rq_gl[v] = gl;
-      rq_gr[v] = gr;
     }
     __syncthreads();
-    double g[kRegSlotsPerLane];
-    int32_t sid[kRegSlotsPerLane], sint[kRegSlotsPerLane];
-    bool act[kRegSlotsPerLane];
-#pragma unroll
-    for (int q = 0; q < kRegSlotsPerLane; ++q) {
-      g[q] = -INFINITY;
-      sid[q] = 0;
-      sint[q] = 0;
-      act[q] = false;
-    }
-    node_count = 1;
-    if (lane == 0) {
-      ro_int[0] = 0;
-      ro_left[0] = -1;
-    }
-    if (rp_fpos[0] >= 0) {
-      if (lane == 0) {
-        g[0] = rp_gain[0];
-        act[0] = true;
-      }
-      int32_t n_splits = 0;
-      while (n_splits < a.max_leaves - 1) {
-        double lmax = g[0];
-#pragma unroll
-        for (int q = 1; q < kRegSlotsPerLane; ++q) lmax = fmax(lmax, g[q]);
-        const double best = wave_max_f64(lmax);
-        if (!(best > a.gamma)) break;
-        int32_t ci = -1;
-#pragma unroll
-        for (int q = 0; q < kRegSlotsPerLane; ++q) {
-          const unsigned long long m = __ballot(g[q] == best);
-          if (ci < 0 && m) ci = 64 * q + __builtin_ctzll(m);
-        }
-        const int cq = ci >> 6, cl = ci & 63;
-        int32_t v = 0, cur = 0;
-#pragma unroll
-        for (int q = 0; q < kRegSlotsPerLane; ++q)
-          if (q == cq) {
-            v = __builtin_amdgcn_readlane(sint[q], cl);
-            cur = __builtin_amdgcn_readlane(sid[q], cl);
-          }
-        const int32_t c = rq_child[v];
-        if (c < 0) {
-          status = 2;
+    // Candidates and depths (each node walks to the root).
+    double *gc = reinterpret_cast<double *>(rt_raw);  // key of a candidate, NaN otherwise
+    for (int32_t v = tid; v < n; v += kTreeBlock) {
+      bool pc = rt_G[v] > a.gamma;
+      int32_t d = 0, u = v;
+      while (u != 0 && d <= kTreeMaxDepth) {
+        const int32_t p = rt_parent[u];
+        if (p < 0) {
+          pc = false;
           break;
         }
-        // The popped slot is free again.
+        pc = pc && (rq_child[p] & kKept) && rt_G[p] > a.gamma;
+        u = p;
+        ++d;
+      }
+      if (d > kTreeMaxDepth) rt_flags[0] = 1;
+      rt_pc[v] = pc ? 1 : 0;
+      rt_depth[v] = (uint8_t)min(d, 255);
+      gc[v] = pc ? rt_G[v] : __longlong_as_double(0x7ff8000000000000ll);
+    }
+    __syncthreads();
+    // Key ranks among the candidates; equal keys need the slot loop.
+    for (int32_t v = tid; v < n; v += kTreeBlock) {
+      if (!rt_pc[v]) continue;
+      const double gv = gc[v];
+      int32_t lt = 0, eq = 0;
+      int32_t u = 0;
+      for (; u + 4 <= n; u += 4) {
+        const double g0 = gc[u], g1 = gc[u + 1], g2 = gc[u + 2], g3 = gc[u + 3];
+        lt += (g0 < gv) + (g1 < gv) + (g2 < gv) + (g3 < gv);
+        eq += (g0 == gv) + (g1 == gv) + (g2 == gv) + (g3 == gv);
+      }
+      for (; u < n; ++u) {
+        lt += gc[u] < gv;
+        eq += gc[u] == gv;
+      }
+      rt_code[v] = (int16_t)lt;
+      if (eq > 1) rt_flags[0] = 1;
+      atomicAdd(&rt_flags[1], 1);
+    }
+    __syncthreads();
+    const bool slots = rt_flags[0] != 0;
+    if (!slots) {
+      // Vectors: component d (depth d + 1 and below) in 11 bits, d = 0 in
+      // the top bits of hi; 0 for nodes that are not candidates.
+      unsigned long long *key = rt_raw;
+      for (int32_t v = tid; v < n; v += kTreeBlock) {
+        unsigned long long hi = 0, lo = 0;
+        if (rt_pc[v]) {
+          uint32_t comp[kTreeMaxDepth];
 #pragma unroll
-        for (int q = 0; q < kRegSlotsPerLane; ++q)
-          if (q == cq && lane == cl) {
-            act[q] = false;
-            g[q] = -INFINITY;
-          }
-        if (!(c & (1 << 30))) {  // est:678-683: the node stays a leaf
-          if (lane == 0) {
-            ro_int[cur] = v;
-            ro_left[cur] = -1;
-          }
-          continue;
-        }
-        const int32_t l = c & ((1 << 29) - 1);
-        const bool left_small = (c & (1 << 29)) != 0;
-        const int32_t left_id = node_count, right_id = node_count + 1;
-        node_count += 2;
-        ++n_splits;
-        // The first two free slots other than ci, in slot order.
-        int32_t slot_small = -1, slot_large = -1;
+          for (int d = 0; d < kTreeMaxDepth; ++d) comp[d] = kCodeInf;
+          uint32_t mn = kCodeInf;
+          int32_t u = v;
+          for (int d = (int)rt_depth[v] - 1; d >= 0; --d) {
+            mn = min(mn, (uint32_t)rt_code[u]);
 #pragma unroll
-        for (int q = 0; q < kRegSlotsPerLane; ++q) {
-          const int32_t k = 64 * q + lane;
-          unsigned long long m = __ballot(k < C && k != ci && !act[q]);
-          while (m && slot_large < 0) {
-            const int32_t kk = 64 * q + __builtin_ctzll(m);
-            m &= m - 1;
-            if (slot_small < 0) slot_small = kk;
-            else slot_large = kk;
+            for (int q = 0; q < kTreeMaxDepth; ++q)
+              if (q == d) comp[q] = mn;
+            u = rt_parent[u];
           }
-        }
-        if (slot_large < 0) {
-          status = 3;
-          break;
-        }
-        const double gl = rq_gl[v], gr = rq_gr[v];
 #pragma unroll
-        for (int q = 0; q < kRegSlotsPerLane; ++q) {
-          const int32_t k = 64 * q + lane;
-          if (k == slot_small || k == slot_large) {
-            const bool is_left = (k == slot_small) == left_small;
-            act[q] = true;
-            sid[q] = is_left ? left_id : right_id;
-            sint[q] = is_left ? l : l + 1;
-            g[q] = is_left ? gl : gr;
+          for (int d = 0; d < 5; ++d) {
+            hi |= (unsigned long long)comp[d] << (44 - 11 * d);
+            lo |= (unsigned long long)comp[d + 5] << (44 - 11 * d);
           }
         }
-        if (lane == 0) {
-          ro_int[cur] = v;
-          ro_left[cur] = left_id;
+        key[2 * v] = hi;
+        key[2 * v + 1] = lo;
+      }
+      __syncthreads();
+      for (int32_t v = tid; v < n; v += kTreeBlock) {
+        if (!rt_pc[v]) continue;
+        const unsigned long long kh = key[2 * v], kl = key[2 * v + 1];
+        int32_t r = 0;
+        for (int32_t u = 0; u < n; ++u) {
+          const unsigned long long uh = key[2 * u], ul = key[2 * u + 1];
+          r += (uh > kh || (uh == kh && ul > kl)) ? 1 : 0;
+        }
+        rt_at[r] = (int16_t)v;
+      }
+      __syncthreads();
+      // The cut: a candidate is popped while fewer than max_leaves - 1
+      // kept splits came before it.
+      const int32_t npc = rt_flags[1];
+      int32_t v = -1, c = -1;
+      if (tid < npc) {
+        v = rt_at[tid];
+        c = rq_child[v];
+      }
+      const uint32_t ks = (v >= 0 && c >= 0 && (c & kKept)) ? 1u : 0u;
+      uint32_t ktot;
+      const uint32_t kb = block_excl_scan<kTreeBlock>(ks, stmp, ktot);
+      const bool popped = v >= 0 && (int32_t)kb < a.max_leaves - 1;
+      if (popped && c < 0) rt_flags[2] = 2;
+      if (popped && ks) rt_kk[v] = (int16_t)kb;
+      __syncthreads();
+      const int32_t K = min((int32_t)ktot, a.max_leaves - 1);
+      node_count = 1 + 2 * K;
+      if (rt_flags[2] == 0) {
+        if (tid == 0) {
+          rt_int[0] = 0;
+          rt_left[0] = rt_kk[0] >= 0 ? 1 + 2 * rt_kk[0] : -1;
+        }
+        for (int32_t u = tid; u < n; u += kTreeBlock) {
+          const int32_t k = rt_kk[u];
+          if (k < 0) continue;
+          const int32_t l = rq_child[u] & kChildMask, lid = 1 + 2 * k;
+          rt_int[lid] = l;
+          rt_left[lid] = rt_kk[l] >= 0 ? 1 + 2 * rt_kk[l] : -1;
+          rt_int[lid + 1] = l + 1;
+          rt_left[lid + 1] = rt_kk[l + 1] >= 0 ? 1 + 2 * rt_kk[l + 1] : -1;
         }
       }
-      if (status == 0) {
-#pragma unroll
-        for (int q = 0; q < kRegSlotsPerLane; ++q)
-          if (act[q]) {
-            ro_int[sid[q]] = sint[q];
-            ro_left[sid[q]] = -1;
-          }
+      status = rt_flags[2];
+    } else {
+      if (wave == 0) {
+        int32_t st = 0;
+        const int32_t nc = replay_slot_loop(C, a, st);
+        if (lane_id() == 0) {
+          rt_flags[2] = st;
+          rt_flags[3] = nc;
+        }
       }
+      __syncthreads();
+      status = rt_flags[2];
+      node_count = rt_flags[3];
     }
     __syncthreads();
     const ReplayNodes<true> N{nodes, a};
-    replay_write(N, feats, status == 0 ? node_count : 0, M, out, tree);
+    replay_write(N, feats, status == 0 ? node_count : 0, M, out, tree, rt_int, rt_left,
+                 kTreeBlock);
   }
-  if (lane == 0) {
+  if (tid == 0) {
     hdr->node_count = status == 0 ? node_count : 0;
     hdr->status = status;
     hdr->needed = needed;
@@ -2546,9 +2713,10 @@ __global__ __launch_bounds__(64) void k_replay_regs(
 hipError_t launch_replay(hipStream_t st, const NodeOut *nodes, const LevelPlan *plan,
                          const int32_t *feats, ReplayArgs a, TreeArrays out,
                          TreeNodeDev *tree, RoundHeader *hdr) {
-  // Register slots for up to 128 candidates when every node fits in LDS.
+  // Up to 128 candidate slots when every node fits in LDS: the order form.
   if (a.max_leaves + 2 <= kRegSlots && a.stage_limit >= kReplayNodes && a.node_cap <= kReplayNodes)
-    hipLaunchKernelGGL(k_replay_regs, dim3(1), dim3(64), 0, st, nodes, plan, feats, a, out, tree, hdr);
+    hipLaunchKernelGGL(k_replay_tree, dim3(1), dim3(kTreeBlock), 0, st, nodes, plan, feats, a,
+                       out, tree, hdr);
   else
     hipLaunchKernelGGL(k_replay, dim3(1), dim3(64), 0, st, nodes, plan, feats, a, out, tree, hdr);
   return hipGetLastError();
