@@ -118,7 +118,7 @@ def measured_traffic(kernel, workload):
     return None
 
 
-def run_gpu(name, steps, warmup):
+def run_gpu(name, steps, warmup, rounds_only=False):
     """Fits warmup + steps + BREAKDOWN_ROUNDS rounds.  The timed rounds run
     with the histogram kernel's HIP events only (level 1); the last rounds,
     after the timed region, time every kernel group (level 2) for the
@@ -154,30 +154,33 @@ def run_gpu(name, steps, warmup):
     _progress(f"fit done in {t_fit:.1f} s (binning {est.times['binning']:.0f} ms)")
     elapsed = marks["t1"] - marks["t0"]
     st = marks["stats"]
-    # Prediction on fresh rows through the fitted trees.
-    Xp, _, _ = make_workload(name, predict=True)
-    t = time.perf_counter()
-    est.predict_proba(Xp)
-    t_pred_total = time.perf_counter() - t
-    _progress(f"predict_proba on {len(Xp)} rows in {t_pred_total:.2f} s")
-    # A complete fit with the workload's own n_estimators: bin edges,
-    # binning and every boosting round, from host float32 X.
-    full = HybridHistGBMNumbaV1_0_1(**full_params)
-    t = time.perf_counter()
-    full.fit(X, y)
-    t_full = time.perf_counter() - t
-    fit_full = dict(n_estimators=int(full.n_trees_fitted_), seconds=round(t_full, 4),
-                    trees_per_s=round(full.n_trees_fitted_ / t_full, 2),
-                    binning_ms=round(full.times["binning"], 1),
-                    training_ms=round(full.times["training"], 1))
-    _progress(f"full fit: {fit_full}")
+    t_pred_total, pred_rows, fit_full = None, 0, None
+    if not rounds_only:
+        # Prediction on fresh rows through the fitted trees.
+        Xp, _, _ = make_workload(name, predict=True)
+        t = time.perf_counter()
+        est.predict_proba(Xp)
+        t_pred_total = time.perf_counter() - t
+        pred_rows = len(Xp)
+        _progress(f"predict_proba on {len(Xp)} rows in {t_pred_total:.2f} s")
+        # A complete fit with the workload's own n_estimators: bin edges,
+        # binning and every boosting round, from host float32 X.
+        full = HybridHistGBMNumbaV1_0_1(**full_params)
+        t = time.perf_counter()
+        full.fit(X, y)
+        t_full = time.perf_counter() - t
+        fit_full = dict(n_estimators=int(full.n_trees_fitted_), seconds=round(t_full, 4),
+                        trees_per_s=round(full.n_trees_fitted_ / t_full, 2),
+                        binning_ms=round(full.times["binning"], 1),
+                        training_ms=round(full.times["training"], 1))
+        _progress(f"full fit: {fit_full}")
     s0, s1 = marks["s0"], marks["s1"]
     sampler = {k: (s1[k] - s0[k]) / max(s1["rounds"] - s0["rounds"], 1)
                for k in ("draw_ms", "gen_ms")}
     return dict(est=est, n=n, F=F, elapsed=elapsed, stats=st, t_fit=t_fit,
                 breakdown=marks["breakdown"], sampler=sampler,
-                t_pred_total=t_pred_total, pred_rows=len(Xp), fit_full=fit_full,
-                t_pred_dev=est.times["inference"] / 1e3, params=params)
+                t_pred_total=t_pred_total, pred_rows=pred_rows, fit_full=fit_full,
+                t_pred_dev=est.times.get("inference", 0.0) / 1e3, params=params)
 
 
 def run_cpu_baseline(name, rounds):
@@ -209,12 +212,14 @@ def main():
     ap.add_argument("--workload", default="dense_1m")
     ap.add_argument("--cpu-rounds", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--rounds-only", action="store_true",
+                    help="skip the prediction and the end-to-end fit (profiler runs)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(json.dumps({"error": "this engine runs on one GPU; --gpus must be 1 "
                                    "(row sharding across GPUs is not built)"}))
         sys.exit(2)
-    r = run_gpu(a.workload, a.steps, a.warmup)
+    r = run_gpu(a.workload, a.steps, a.warmup, a.rounds_only)
     st = r["stats"]
     bd = r["breakdown"]
     trees_per_s = a.steps / r["elapsed"]
@@ -255,8 +260,10 @@ def main():
             "bytes_per_launch": round(st["hist_bytes"] / launches),
         },
         "hist_rows_x_features_per_s": round(st["hist_row_features"] / hist_s) if hist_s > 0 else None,
-        "predict_rows_per_s": round(r["pred_rows"] / r["t_pred_dev"]) if r["t_pred_dev"] > 0 else None,
-        "predict_rows_per_s_end_to_end": round(r["pred_rows"] / r["t_pred_total"]),
+        "predict_rows_per_s": (round(r["pred_rows"] / r["t_pred_dev"])
+                               if r["pred_rows"] and r["t_pred_dev"] > 0 else None),
+        "predict_rows_per_s_end_to_end": (round(r["pred_rows"] / r["t_pred_total"])
+                                          if r["pred_rows"] else None),
         "kernel_ms_per_step": {  # every group timed, rounds after the timed region
             "hist": round(bd["hist_ms"] / BREAKDOWN_ROUNDS, 3),
             "partition": round(bd["part_ms"] / BREAKDOWN_ROUNDS, 3),
