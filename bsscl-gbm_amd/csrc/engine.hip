@@ -1464,7 +1464,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     hipError_t e = launch_replay(E->st, E->nodes_d, E->plan_d, E->feat_d, ra,
                                  round_arrays(E->round_d[s].p, R.M), E->tree_d.p, hdr);
     if (e == hipSuccess)
-      e = launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, &hdr->node_count,
+      e = launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, R.M, &hdr->node_count,
                           a.learning_rate, E->F.p, E->y.p, E->partials_d.p, nb);
     if (e == hipSuccess) e = launch_sum_partials(E->st, E->partials_d.p, nb, &hdr->loss_sum);
     if (e == hipSuccess)
@@ -1551,7 +1551,7 @@ int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
                   *out.node_count, X.F));
   const int nb = update_F_blocks(X.n);
   CHK(E->loss_d.ensure(1));
-  HIPCHK(launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, nullptr,
+  HIPCHK(launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, *out.node_count, nullptr,
                          R.args.learning_rate, E->F.p, E->y.p, E->partials_d.p, nb));
   HIPCHK(launch_sum_partials(E->st, E->partials_d.p, nb, E->loss_d.p));
   double sum = 0.0;

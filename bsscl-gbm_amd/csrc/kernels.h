@@ -291,7 +291,7 @@ hipError_t launch_code_counts(hipStream_t st, const uint8_t *codes, int64_t ld,
 // F += lr * tree(row) for every row unless *node_count_d == 0 (then F is
 // left alone); per-block partial sums of the training log-likelihood.
 hipError_t launch_update_F(hipStream_t st, const uint8_t *codes, int64_t ld,
-                           int64_t n, const TreeNodeDev *tree,
+                           int64_t n, const TreeNodeDev *tree, int32_t tree_len,
                            const int32_t *node_count_d, double lr, double *F,
                            const uint8_t *y, double *loss_partials,
                            int32_t n_blocks);

@@ -2037,7 +2037,7 @@ hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
 constexpr int kUpdBlock = 256;
 
 int update_F_blocks(int64_t n) {
-  int64_t b = (n + kUpdBlock * 8 - 1) / (kUpdBlock * 8);
+  int64_t b = (n + kUpdBlock * 16 - 1) / (kUpdBlock * 16);
   if (b < 1) b = 1;
   if (b > 4096) b = 4096;
   return (int)b;
@@ -2056,27 +2056,81 @@ __device__ __forceinline__ int32_t traverse(const TreeNodeDev *__restrict__ tree
   return node;
 }
 
+// F += lr * tree(x) for every row (est:2896-2897) and the log-loss of the
+// new F (est:2320-2325, est:2905), partial sums per block.  The tree sits in
+// LDS (up to kUpdTreeLds nodes) and each thread walks four rows at once, so
+// four chains of dependent code loads are in flight per thread.
+constexpr int kUpdTreeLds = 1024;
+constexpr int kUpdRows = 4;
+
 #pragma clang fp contract(off)
+__device__ __forceinline__ double row_loss(double f, uint8_t yi) {
+  const double fc = fmin(fmax(f, -500.0), 500.0);
+  double p = 1.0 / (1.0 + exp(-fc));
+  p = fmin(fmax(p, 1e-15), 1.0 - 1e-15);
+  return yi ? log(p) : log(1.0 - p);
+}
+
 __global__ __launch_bounds__(kUpdBlock) void k_update_F(
     const uint8_t *__restrict__ codes, int64_t ld, int64_t n,
-    const TreeNodeDev *__restrict__ tree, const int32_t *__restrict__ node_count_d,
-    double lr, double *__restrict__ F, const uint8_t *__restrict__ y,
-    double *__restrict__ partials) {
+    const TreeNodeDev *__restrict__ tree, int32_t tree_len,
+    const int32_t *__restrict__ node_count_d, double lr, double *__restrict__ F,
+    const uint8_t *__restrict__ y, double *__restrict__ partials) {
   __shared__ double red[kUpdBlock / 64];
+  __shared__ TreeNodeDev st[kUpdTreeLds];
   const bool apply = !node_count_d || *node_count_d > 0;
+  const bool lds = tree_len <= kUpdTreeLds;
+  if (apply && lds)
+    for (int32_t k = (int32_t)threadIdx.x; k < tree_len; k += kUpdBlock) st[k] = tree[k];
+  __syncthreads();
+  const TreeNodeDev *tr = lds ? st : tree;
   double acc = 0.0;
-  for (int64_t i = (int64_t)blockIdx.x * kUpdBlock + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * kUpdBlock) {
-    double f = F[i];
-    if (apply) {
-      const int32_t leaf = traverse(tree, codes, ld, i);
-      f = __dadd_rn(f, __dmul_rn(lr, tree[leaf].value));
-      F[i] = f;
+  const int64_t step = (int64_t)gridDim.x * kUpdBlock * kUpdRows;
+  for (int64_t base = (int64_t)blockIdx.x * kUpdBlock * kUpdRows + threadIdx.x; base < n;
+       base += step) {
+    int64_t i[kUpdRows];
+    bool in[kUpdRows];
+    double f[kUpdRows];
+#pragma unroll
+    for (int r = 0; r < kUpdRows; ++r) {
+      i[r] = base + (int64_t)r * kUpdBlock;
+      in[r] = i[r] < n;
+      f[r] = in[r] ? F[i[r]] : 0.0;
     }
-    const double fc = fmin(fmax(f, -500.0), 500.0);
-    double p = 1.0 / (1.0 + exp(-fc));
-    p = fmin(fmax(p, 1e-15), 1.0 - 1e-15);
-    acc += y[i] ? log(p) : log(1.0 - p);
+    if (apply) {
+      TreeNodeDev nd[kUpdRows];
+      int32_t node[kUpdRows];
+#pragma unroll
+      for (int r = 0; r < kUpdRows; ++r) {
+        node[r] = 0;
+        nd[r] = tr[0];
+      }
+      bool more = true;
+      while (more) {
+        int32_t c[kUpdRows];
+#pragma unroll
+        for (int r = 0; r < kUpdRows; ++r)
+          c[r] = (in[r] && nd[r].feature >= 0) ? codes[(int64_t)nd[r].feature * ld + i[r]] : 0;
+        more = false;
+#pragma unroll
+        for (int r = 0; r < kUpdRows; ++r) {
+          if (in[r] && nd[r].feature >= 0) {
+            node[r] = (c[r] <= nd[r].threshold) ? nd[r].left : nd[r].right;
+            nd[r] = tr[node[r]];
+            more = more || nd[r].feature >= 0;
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < kUpdRows; ++r)
+        if (in[r]) {
+          f[r] = __dadd_rn(f[r], __dmul_rn(lr, nd[r].value));
+          F[i[r]] = f[r];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kUpdRows; ++r)
+      if (in[r]) acc += row_loss(f[r], y[i[r]]);
   }
   for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
   if (lane_id() == 0) red[threadIdx.x >> 6] = acc;
@@ -2090,12 +2144,12 @@ __global__ __launch_bounds__(kUpdBlock) void k_update_F(
 #pragma clang fp contract(on)
 
 hipError_t launch_update_F(hipStream_t st, const uint8_t *codes, int64_t ld,
-                           int64_t n, const TreeNodeDev *tree,
+                           int64_t n, const TreeNodeDev *tree, int32_t tree_len,
                            const int32_t *node_count_d, double lr, double *F,
                            const uint8_t *y, double *loss_partials,
                            int32_t n_blocks) {
   hipLaunchKernelGGL(k_update_F, dim3((unsigned)n_blocks), dim3(kUpdBlock), 0, st,
-                     codes, ld, n, tree, node_count_d, lr, F, y, loss_partials);
+                     codes, ld, n, tree, tree_len, node_count_d, lr, F, y, loss_partials);
   return hipGetLastError();
 }
 
