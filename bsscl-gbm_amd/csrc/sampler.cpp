@@ -1140,6 +1140,8 @@ struct Sampler {
   // Draw loop of the parallel form.
   void run_draws_parallel() {
     std::vector<uint32_t> jf((size_t)F + 16);
+    std::vector<Segment> sbatch;
+    sbatch.reserve(8);
     std::vector<uint32_t> words((size_t)kChunkWords + 16);
     int64_t G = pos0;  // global position of the next word
     for (int32_t r = 0; r < n_rounds; ++r) {
@@ -1165,25 +1167,32 @@ struct Sampler {
         inflight.push_back(std::move(R));
       }
       const auto t0 = std::chrono::steady_clock::now();
+      // Segments go to the workers eight at a time: one lock and at most
+      // one wake-up (a system call) per batch.
+      auto publish = [&] {
+        if (sbatch.empty()) return;
+        bool wake;
+        {
+          std::lock_guard<std::mutex> lk(mu);
+          for (const Segment &sg : sbatch) segs.push_back(sg);
+          wake = idle_workers > 0;
+        }
+        sbatch.clear();
+        if (wake) seg_cv.notify_all();
+      };
       auto emit = [&](const uint32_t *key, int32_t w0, uint32_t i) {
-        Segment sg;
+        sbatch.emplace_back();
+        Segment &sg = sbatch.back();
         std::memcpy(sg.key, key, sizeof(sg.key));
         sg.w0 = w0;
         sg.i0 = i;
         sg.round = Rp;
         Rp->pending.fetch_add(1, std::memory_order_relaxed);
-        // A sleeping worker is woken once four segments wait (waking costs
-        // a system call; a worker drains the queue before it sleeps again).
-        bool wake;
-        {
-          std::lock_guard<std::mutex> lk(mu);
-          segs.push_back(sg);
-          wake = idle_workers > 0 && segs.size() >= 4;
-        }
-        if (wake) seg_cv.notify_one();
+        if (sbatch.size() >= 8) publish();
       };
       const int64_t end = resolve_round(G, emit, words);
-      seg_cv.notify_all();  // the round's last segments
+      publish();  // the round's last segments
+      seg_cv.notify_all();
       if (end < 0) return;
       G = end;
       if (do_feats && F > 1) {
@@ -1511,7 +1520,7 @@ int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
       const double rc = bsscl::expected_words(n) / (double)bsscl::kChunkWords;
       s->ring_lead = std::min<int64_t>(Sampler::kRingChunks, (int64_t)(3.0 * rc) + 64);
       const unsigned hw = std::max(2u, std::thread::hardware_concurrency());
-      const int nw = (int)std::max(2u, std::min(6u, hw / 2));
+      const int nw = (int)std::max(2u, std::min(8u, hw / 2));
       for (int w = 0; w < nw; ++w) s->workers.emplace_back([s] { s->run_worker(); });
       s->twister = std::thread([s] { s->run_twister(); });
     }
