@@ -274,6 +274,8 @@ def main():
         "host_ms_per_step": {
             "sampler_wait": round(st.get("sampler_wait_ms", 0.0) / a.steps, 3),
             "round": round(st.get("round_ms", 0.0) / a.steps, 3),
+            "enqueue": round(st.get("enqueue_ms", 0.0) / a.steps, 3),
+            "finish_wait": round(st.get("finish_ms", 0.0) / a.steps, 3),
             "sampler_draw": round(r["sampler"]["draw_ms"], 3),
             "sampler_gen": round(r["sampler"]["gen_ms"], 3),
         },

@@ -348,7 +348,7 @@ class Engine:
         keys = ["hist_launches", "hist_ms", "hist_row_features", "hist_bytes",
                 "part_launches", "part_ms", "split_launches", "split_ms",
                 "trees", "nodes_expanded", "sampler_wait_ms", "round_ms",
-                "reduce_launches", "reduce_ms"]
+                "reduce_launches", "reduce_ms", "enqueue_ms", "finish_ms"]
         return dict(zip(keys, out[:int(n[0])].tolist()))
 
 

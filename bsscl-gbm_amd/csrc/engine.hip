@@ -319,7 +319,7 @@ struct bsscl_engine {
     uint64_t seq;  // boosting round that recorded them
   };
   std::vector<Pending> pending;
-  double stats[14] = {0};
+  double stats[16] = {0};
 };
 
 namespace bsscl {
@@ -2055,14 +2055,20 @@ int bsscl_boost_round(bsscl_engine *E, bsscl_sampler *sampler,
   if (E->pipeline && pipeline_safe(E, a, sampler) && sampler_remaining(sampler) > 0) {
     const int nxt = E->rslot_next;
     E->rslot_next ^= 1;
+    const auto te = std::chrono::steady_clock::now();
     const int rc = enqueue_round(E, sampler, a, nxt);
+    if (E->prof)
+      E->stats[14] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - te).count();
     if (rc != BSSCL_OK) {
       (void)drain_rounds(E, cur);
       return rc;
     }
     E->ahead = nxt;
   }
+  const auto tf = std::chrono::steady_clock::now();
   const int rc = finish_round(E, cur, out, out_train_loss);
+  if (E->prof)
+    E->stats[15] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - tf).count();
   if (rc != BSSCL_OK) {
     if (E->ahead >= 0) (void)drain_rounds(E, E->ahead);
     E->ahead = -1;
@@ -2329,7 +2335,7 @@ int bsscl_engine_set_profiling(bsscl_engine *E, int32_t on) {
 
 int bsscl_engine_stats(bsscl_engine *E, double *out, int32_t cap, int32_t *n_out) {
   if (!E || !out || !n_out) return set_error(BSSCL_EINVAL, "null argument");
-  const int32_t n = std::min<int32_t>(cap, 14);
+  const int32_t n = std::min<int32_t>(cap, 16);
   for (int32_t i = 0; i < n; ++i) out[i] = E->stats[i];
   *n_out = n;
   return BSSCL_OK;

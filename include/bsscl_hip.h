@@ -271,6 +271,8 @@ void bsscl_sampler_destroy(bsscl_sampler *s);
  *   [8] trees built          [9] nodes expanded
  *   [10] host ms waiting for the bagging sample in bsscl_boost_round
  *   [11] host ms in bsscl_boost_round (whole rounds)
+ *   [12] histogram-reduction launches  [13] histogram-reduction ms
+ *   [14] host ms enqueueing rounds     [15] host ms waiting for a round's results
  * and returns the number written in *n_out.
  */
 int bsscl_engine_set_profiling(bsscl_engine *eng, int32_t on);
