@@ -266,7 +266,6 @@ struct bsscl_engine {
   int32_t tile_cap = 0, hist_cap = 0;
   DevBuf<PartTile> tiles_d;
   DevBuf<int32_t> tile_left_d;
-  DevBuf<int64_t> tile_off_d;
   DevBuf<HistTask> hist_tasks_d;
   DevBuf<char> lvl_d;                 // packed inputs of the root (one upload per tree)
   const int32_t *feat_d = nullptr;    // selected feature indices
@@ -724,7 +723,6 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
   }
   CHK(E->tiles_d.ensure((size_t)tcap));
   CHK(E->tile_left_d.ensure((size_t)tcap + 4));  // 16-byte reads past the last tile
-  CHK(E->tile_off_d.ensure((size_t)tcap));
   CHK(E->hist_tasks_d.ensure((size_t)hcap));
   CHK(E->part_d.ensure((size_t)hcap * F_sel * kHistPerFeat));
   E->tile_cap = (int32_t)tcap;
@@ -880,10 +878,7 @@ int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parent
                                plan, max_tiles, E->part_rows, tile_begin, E->tile_left_d.p,
                                E->nleft_d.p, E->segs.p, E->hist_node_d.p, min_samples_leaf,
                                F_sel));
-  else
-    HIPCHK(launch_part_scan(E->st, parents, plan, std::min(max_parents, 1024), tile_begin,
-                            E->tile_left_d.p, E->tile_off_d.p, E->nleft_d.p, E->segs.p,
-                            E->hist_node_d.p, min_samples_leaf));
+  // (Without rows to move -- the last level -- k_last_level does the scan.)
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
@@ -903,10 +898,10 @@ int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
   hipEvent_t stop;
   if (last) {
     CHK(prof_begin(E, 2, &stop));
-    HIPCHK(launch_child_totals(E->st, par, E->plan_d, std::min(P, 4096), E->segs.p,
-                               E->pool.p, E->node_stride, E->totals.p));
-    HIPCHK(launch_node_best(E->st, E->segs.p, E->totals.p, E->cand.p, F_sel, E->plan_d,
-                            std::min(2 * P, 4096), 1, E->nodes_d));
+    HIPCHK(launch_last_level(E->st, par, E->plan_d, std::min(P, 4096), E->tile_begin_d.p,
+                             E->tile_left_d.p, E->nleft_d.p, E->segs.p, E->hist_node_d.p,
+                             tp.min_samples_leaf, E->pool.p, E->node_stride, E->totals.p,
+                             E->nodes_d));
     CHK(prof_end(E, stop));
     return BSSCL_OK;
   }
@@ -1666,7 +1661,6 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->nleft_d.release();
   E->tiles_d.release();
   E->tile_left_d.release();
-  E->tile_off_d.release();
   E->hist_tasks_d.release();
   E->tree_d.release();
   for (int b = 0; b < 2; ++b) {

@@ -235,12 +235,6 @@ hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
                              int64_t ld_c, const PartParent *parents,
                              const PartTile *tiles, const LevelPlan *plan,
                              int32_t max_tiles, int32_t part_rows, int32_t *tile_left);
-hipError_t launch_part_scan(hipStream_t st, const PartParent *parents,
-                            const LevelPlan *plan, int32_t max_parents,
-                            const int32_t *tile_begin,
-                            const int32_t *tile_left, int64_t *tile_left_off,
-                            int64_t *parent_nleft, NodeSeg *segs,
-                            int32_t *hist_node, int32_t min_samples_leaf);
 hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                uint8_t *codes_dst, int64_t ld_c,
                                const int2 *gh_src, int2 *gh_dst,
@@ -261,10 +255,14 @@ hipError_t launch_node_best(hipStream_t st, const NodeSeg *segs,
                             const long long *totals, const SplitCand *cand,
                             int32_t F_sel, const LevelPlan *plan,
                             int32_t max_nodes, int32_t no_split, NodeOut *nodes);
-hipError_t launch_child_totals(hipStream_t st, const PartParent *parents,
-                               const LevelPlan *plan, int32_t max_parents,
-                               const NodeSeg *segs, const unsigned long long *pool,
-                               int64_t node_stride, long long *totals);
+// The last level after its partition count: each parent's scan, its
+// children's totals and table records, one wave per parent.
+hipError_t launch_last_level(hipStream_t st, const PartParent *parents, const LevelPlan *plan,
+                             int32_t max_parents, const int32_t *tile_begin,
+                             const int32_t *tile_left, int64_t *parent_nleft, NodeSeg *segs,
+                             int32_t *hist_node, int32_t min_samples_leaf,
+                             const unsigned long long *pool, int64_t node_stride,
+                             long long *totals, NodeOut *nodes);
 // One workgroup: picks the level's parents among the nodes created by the
 // previous level and writes their PartParent, PartTile, HistTask and
 // SplitTask lists and the LevelPlan (see k_plan).

@@ -937,64 +937,6 @@ hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
   return hipGetLastError();
 }
 
-// One block per parent: exclusive offsets of its tiles' left counts, the
-// children's segments, whether the split is kept (est:678-683) and which
-// child is the smaller one (est:701-709), whose histogram is built.
-__global__ __launch_bounds__(kPartBlock) void k_part_scan(
-    const PartParent *__restrict__ parents, const LevelPlan *__restrict__ plan,
-    const int32_t *__restrict__ tile_begin,
-    const int32_t *__restrict__ tile_left, int64_t *__restrict__ tile_left_off,
-    int64_t *__restrict__ parent_nleft, NodeSeg *__restrict__ segs,
-    int32_t *__restrict__ hist_node, int32_t min_samples_leaf) {
-  __shared__ uint32_t tmp[kPartBlock / 64];
-  const int32_t n_parents = plan->n_parents;
-  for (int p = (int)blockIdx.x; p < n_parents; p += (int)gridDim.x) {
-    const PartParent P = parents[p];
-    const int t0 = tile_begin[p], t1 = tile_begin[p + 1];
-    int64_t carry = 0;
-    for (int base = t0; base < t1; base += kPartBlock) {
-      const int t = base + (int)threadIdx.x;
-      const uint32_t v = (t < t1) ? (uint32_t)tile_left[t] : 0u;
-      uint32_t total;
-      const uint32_t pre = block_excl_scan<kPartBlock>(v, tmp, total);
-      if (t < t1) tile_left_off[t] = carry + pre;
-      carry += total;
-    }
-    const int64_t nl = carry, nr = P.count - carry;
-    const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
-    const bool left_small = nl <= nr;
-    const int32_t small_id = left_small ? P.left_id : P.right_id;
-    if (threadIdx.x == 0) {
-      parent_nleft[p] = nl;
-      NodeSeg L, R;
-      L.start = P.start;
-      L.count = nl;
-      L.valid = ok ? 1 : 0;
-      L.is_small = left_small ? 1 : 0;
-      R.start = P.start + nl;
-      R.count = nr;
-      R.valid = ok ? 1 : 0;
-      R.is_small = left_small ? 0 : 1;
-      segs[P.left_id] = L;
-      segs[P.right_id] = R;
-      hist_node[p] = ok ? small_id : -1;
-    }
-  }
-}
-
-hipError_t launch_part_scan(hipStream_t st, const PartParent *parents,
-                            const LevelPlan *plan, int32_t max_parents,
-                            const int32_t *tile_begin,
-                            const int32_t *tile_left, int64_t *tile_left_off,
-                            int64_t *parent_nleft, NodeSeg *segs,
-                            int32_t *hist_node, int32_t min_samples_leaf) {
-  if (max_parents <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_part_scan, dim3((unsigned)max_parents), dim3(kPartBlock), 0,
-                     st, parents, plan, tile_begin, tile_left, tile_left_off,
-                     parent_nleft, segs, hist_node, min_samples_leaf);
-  return hipGetLastError();
-}
-
 // Moves a tile's rows to the child segments in the other buffer set, keeping
 // the input order on each side.  A row's slot (left run, then right run) is
 // a block-wide exclusive scan of per-thread counts plus its rank among the
@@ -1345,20 +1287,27 @@ hipError_t launch_split(hipStream_t st, const SplitTask *tasks,
   return hipGetLastError();
 }
 
-// Children that can never be split (they are at max_depth) need only their
-// gradient/hessian totals: the parent's histogram of the split feature
-// summed up to the split bin (left) and the rest (right).  One wave per
-// parent.
-__global__ __launch_bounds__(256) void k_child_totals(
+// The last level (its children are at max_depth, est:775-777): one wave per
+// parent does the parent's scan of its tiles' left counts (the children's
+// segments, whether the split is kept, est:678-683), the children's totals
+// from the parent's histogram of the split feature, and the children's
+// table records (no split).  Replaces scan, child totals and record kernels.
+__global__ __launch_bounds__(256) void k_last_level(
     const PartParent *__restrict__ parents, const LevelPlan *__restrict__ plan,
-    const NodeSeg *__restrict__ segs, const unsigned long long *__restrict__ pool,
-    int64_t node_stride, long long *__restrict__ totals) {
+    const int32_t *__restrict__ tile_begin, const int32_t *__restrict__ tile_left,
+    int64_t *__restrict__ parent_nleft, NodeSeg *__restrict__ segs,
+    int32_t *__restrict__ hist_node, int32_t min_samples_leaf,
+    const unsigned long long *__restrict__ pool, int64_t node_stride,
+    long long *__restrict__ totals, NodeOut *__restrict__ nodes) {
   const int lane = lane_id();
   const int32_t n_parents = plan->n_parents;
   for (int w = (int)(blockIdx.x * 4 + (threadIdx.x >> 6)); w < n_parents;
        w += (int)gridDim.x * 4) {
     const PartParent P = parents[w];
-    if (!segs[P.left_id].valid) continue;
+    const int32_t t0 = tile_begin[w], t1 = tile_begin[w + 1];
+    long long nl = 0;
+    for (int32_t t = t0 + lane; t < t1; t += 64) nl += tile_left[t];
+    // The parent's histogram of its split feature: totals of bins <= bin.
     const long long *h = reinterpret_cast<const long long *>(pool) +
                          (int64_t)P.node * node_stride + (int64_t)P.fpos * kHistPerFeat;
     long long gl = 0, hl = 0, gt = 0, ht = 0;
@@ -1375,29 +1324,69 @@ __global__ __launch_bounds__(256) void k_child_totals(
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
+      nl += __shfl_xor(nl, o, 64);
       gl += __shfl_xor(gl, o, 64);
       hl += __shfl_xor(hl, o, 64);
       gt += __shfl_xor(gt, o, 64);
       ht += __shfl_xor(ht, o, 64);
     }
     if (lane == 0) {
-      totals[2 * (int64_t)P.left_id] = gl;
-      totals[2 * (int64_t)P.left_id + 1] = hl;
-      totals[2 * (int64_t)P.right_id] = gt - gl;
-      totals[2 * (int64_t)P.right_id + 1] = ht - hl;
+      const long long nr = P.count - nl;
+      const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
+      const bool left_small = nl <= nr;
+      parent_nleft[w] = nl;
+      NodeSeg Ls, Rs;
+      Ls.start = P.start;
+      Ls.count = nl;
+      Ls.valid = ok ? 1 : 0;
+      Ls.is_small = left_small ? 1 : 0;
+      Rs.start = P.start + nl;
+      Rs.count = nr;
+      Rs.valid = ok ? 1 : 0;
+      Rs.is_small = left_small ? 0 : 1;
+      segs[P.left_id] = Ls;
+      segs[P.right_id] = Rs;
+      hist_node[w] = ok ? (left_small ? P.left_id : P.right_id) : -1;
+      if (ok) {
+        totals[2 * (int64_t)P.left_id] = gl;
+        totals[2 * (int64_t)P.left_id + 1] = hl;
+        totals[2 * (int64_t)P.right_id] = gt - gl;
+        totals[2 * (int64_t)P.right_id + 1] = ht - hl;
+      }
+      NodeOut o;
+      o.gain = -1e9;
+      o.e = 0.0;
+      o.fpos = -1;
+      o.bin = 0;
+      o.valid = ok ? 1 : 0;
+      o.left = -1;
+      o.start = Ls.start;
+      o.count = nl;
+      o.Gq = ok ? gl : 0;
+      o.Hq = ok ? hl : 0;
+      nodes[P.left_id] = o;
+      o.start = Rs.start;
+      o.count = nr;
+      o.Gq = ok ? gt - gl : 0;
+      o.Hq = ok ? ht - hl : 0;
+      nodes[P.right_id] = o;
     }
   }
 }
 
-hipError_t launch_child_totals(hipStream_t st, const PartParent *parents,
-                               const LevelPlan *plan, int32_t max_parents,
-                               const NodeSeg *segs, const unsigned long long *pool,
-                               int64_t node_stride, long long *totals) {
+hipError_t launch_last_level(hipStream_t st, const PartParent *parents, const LevelPlan *plan,
+                             int32_t max_parents, const int32_t *tile_begin,
+                             const int32_t *tile_left, int64_t *parent_nleft, NodeSeg *segs,
+                             int32_t *hist_node, int32_t min_samples_leaf,
+                             const unsigned long long *pool, int64_t node_stride,
+                             long long *totals, NodeOut *nodes) {
   if (max_parents <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_child_totals, dim3((unsigned)((max_parents + 3) / 4)), dim3(256), 0,
-                     st, parents, plan, segs, pool, node_stride, totals);
+  hipLaunchKernelGGL(k_last_level, dim3((unsigned)((max_parents + 3) / 4)), dim3(256), 0, st,
+                     parents, plan, tile_begin, tile_left, parent_nleft, segs, hist_node,
+                     min_samples_leaf, pool, node_stride, totals, nodes);
   return hipGetLastError();
 }
+
 
 // A node's table record: its segment, fixed-point totals and best split
 // over the features -- the largest gain, the lowest feature position on
