@@ -219,9 +219,11 @@ struct bsscl_engine {
   DevBuf<int2> gh_c[4];
   DevBuf<int32_t> rid_c[2];  // with set_base 0 only
   int32_t set_base = 0;
-  DevBuf<int32_t> feat_slot_d[2];          // a round's selected features (rows stream)
-  int32_t *feat_pin[2] = {nullptr, nullptr};
-  int32_t feat_pin_n[2] = {0, 0};
+  // A boosting round's root inputs (RootPack), uploaded by the rows stream
+  // into the slot's own arena.
+  DevBuf<char> root_d[2];
+  char *root_pin[2] = {nullptr, nullptr};
+  size_t root_pin_n[2] = {0, 0};
   bool track_rid = false;  // carry row ids through the partition (bsscl_partition)
   int64_t ld_c = 0;
   DevBuf<int32_t> round_rows[2];  // in-bag rows of round slot s, ascending
@@ -519,13 +521,25 @@ struct Pack {
   }
 };
 
-int upload_pack(bsscl_engine *E, const Pack &pk, std::vector<char *> &dev) {
+// Byte offsets of the pack's parts (256-byte aligned); returns the total.
+size_t pack_layout(const Pack &pk, std::vector<size_t> &off) {
   size_t total = 0;
-  std::vector<size_t> off(pk.parts.size());
+  off.resize(pk.parts.size());
   for (size_t i = 0; i < pk.parts.size(); ++i) {
     off[i] = total;
     total = (total + pk.parts[i].second + 255) & ~size_t(255);
   }
+  return total;
+}
+
+void pack_copy(const Pack &pk, const std::vector<size_t> &off, char *stage) {
+  for (size_t i = 0; i < pk.parts.size(); ++i)
+    if (pk.parts[i].second) std::memcpy(stage + off[i], pk.parts[i].first, pk.parts[i].second);
+}
+
+int upload_pack(bsscl_engine *E, const Pack &pk, std::vector<char *> &dev) {
+  std::vector<size_t> off;
+  const size_t total = pack_layout(pk, off);
   CHK(E->lvl_d.ensure(std::max<size_t>(total, 256)));
   char *stage = E->pin.take<char>(total);
   if (!stage) {
@@ -536,8 +550,7 @@ int upload_pack(bsscl_engine *E, const Pack &pk, std::vector<char *> &dev) {
     stage = E->pin.take<char>(total);
     if (!stage) return set_error(BSSCL_EINTERNAL, "pinned staging");
   }
-  for (size_t i = 0; i < pk.parts.size(); ++i)
-    if (pk.parts[i].second) std::memcpy(stage + off[i], pk.parts[i].first, pk.parts[i].second);
+  pack_copy(pk, off, stage);
   HIPCHK(hipMemcpyAsync(E->lvl_d.p, stage, total, hipMemcpyHostToDevice, E->st));
   dev.resize(pk.parts.size());
   for (size_t i = 0; i < pk.parts.size(); ++i) dev[i] = E->lvl_d.p + off[i];
@@ -748,48 +761,87 @@ SplitParams split_params(bsscl_engine *E, const TreeParams &tp) {
   return sp;
 }
 
+// The root's inputs as one upload: the selected features, their bin counts
+// followed by their most frequent bins, the root's histogram tasks, its
+// split task, its LevelPlan and its task range (parts kPack*, in order).
+enum { kPackFeat = 0, kPackNbHot, kPackHist, kPackSplit, kPackPlan, kPackTasks };
+struct RootPack {
+  std::vector<HistTask> ht;
+  std::vector<int32_t> nb_hot;
+  SplitTask st0{0, -1, -1, 0};
+  LevelPlan rp = {};
+  int32_t root_tasks[2] = {0, 0};
+  Pack pk;  // points into the members above: a RootPack is not copied
+  RootPack() = default;
+  RootPack(const RootPack &) = delete;
+  RootPack &operator=(const RootPack &) = delete;
+};
+
+void build_root_pack(bsscl_engine *E, int64_t m, const std::vector<int32_t> &feats,
+                     const std::vector<int32_t> &nb_sel, RootPack &R) {
+  const int32_t F_sel = (int32_t)feats.size();
+  const int32_t th = hist_tile_rows(E, m, F_sel);
+  R.ht.clear();
+  for (int64_t t = 0; t * th < m; ++t) R.ht.push_back({0, (int32_t)t});
+  R.rp = LevelPlan{};
+  R.rp.n_parents = 1;  // the root's histogram reference, for the reduction
+  R.rp.n_hist = (int32_t)R.ht.size();
+  R.rp.n_split = 1;
+  R.rp.first_child = 0;
+  R.rp.tile_rows = th;
+  R.rp.n_nodes = 1;
+  R.nb_hot.assign(2 * (size_t)F_sel, 0);
+  for (int32_t i = 0; i < F_sel; ++i) {
+    R.nb_hot[(size_t)i] = nb_sel[(size_t)i];
+    const int32_t f = feats[(size_t)i];
+    const int32_t hb = (size_t)f < E->hot_bin.size() ? E->hot_bin[(size_t)f] : -1;
+    R.nb_hot[(size_t)(F_sel + i)] = hb < 0 ? -1 : std::min(hb, nb_sel[(size_t)i] - 1);
+  }
+  R.root_tasks[0] = 0;
+  R.root_tasks[1] = R.rp.n_hist;
+  R.pk = Pack{};
+  R.pk.add(feats.data(), feats.size() * 4);
+  R.pk.add(R.nb_hot.data(), R.nb_hot.size() * 4);
+  R.pk.add(R.ht.data(), R.ht.size() * sizeof(HistTask));
+  R.pk.add(&R.st0, sizeof(SplitTask));
+  R.pk.add(&R.rp, sizeof(LevelPlan));
+  R.pk.add(R.root_tasks, sizeof(R.root_tasks));
+}
+
+// A root pack already on the device (a boosting round's, uploaded by the
+// rows stream; its plan installed by k_gather_gh).
+struct PreRoot {
+  int32_t n_hist = 0;
+  std::vector<char *> dev;
+};
+
 // Root: gather the in-bag rows into set 0, its histogram and split search.
-// The feature list, the root's tasks and its LevelPlan go up in one copy.
+// The root's pack goes up in one copy, unless `pre` holds it already.
 int launch_root(bsscl_engine *E, const int32_t *rows32, int64_t m,
                 const std::vector<int32_t> &feats,
-                const std::vector<int32_t> &nb_sel, const TreeParams &tp, bool gathered) {
+                const std::vector<int32_t> &nb_sel, const TreeParams &tp, bool gathered,
+                const PreRoot *pre = nullptr) {
   const int b = E->set_base;
   const Matrix &X = E->mat[0];
   const int32_t F_sel = (int32_t)feats.size();
-  const int32_t th = hist_tile_rows(E, m, F_sel);
-  std::vector<HistTask> ht;
-  for (int64_t t = 0; t * th < m; ++t) ht.push_back({0, (int32_t)t});
-  const SplitTask st0{0, -1, -1, 0};
-  LevelPlan rp = {};
-  rp.n_parents = 1;  // the root's histogram reference, for the reduction
-  rp.n_hist = (int32_t)ht.size();
-  rp.n_split = 1;
-  rp.first_child = 0;
-  rp.tile_rows = th;
-  rp.n_nodes = 1;
-  // Selected features' bin counts followed by their most frequent bins.
-  std::vector<int32_t> nb_hot(2 * (size_t)F_sel);
-  for (int32_t i = 0; i < F_sel; ++i) {
-    nb_hot[(size_t)i] = nb_sel[(size_t)i];
-    const int32_t f = feats[(size_t)i];
-    const int32_t hb = (size_t)f < E->hot_bin.size() ? E->hot_bin[(size_t)f] : -1;
-    nb_hot[(size_t)(F_sel + i)] = hb < 0 ? -1 : std::min(hb, nb_sel[(size_t)i] - 1);
-  }
-  Pack pk;
-  pk.add(feats.data(), feats.size() * 4);
-  pk.add(nb_hot.data(), nb_hot.size() * 4);
-  pk.add(ht.data(), ht.size() * sizeof(HistTask));
-  pk.add(&st0, sizeof(SplitTask));
-  pk.add(&rp, sizeof(LevelPlan));
-  const int32_t root_tasks[2] = {0, rp.n_hist};
-  pk.add(root_tasks, sizeof(root_tasks));
   std::vector<char *> dv;
-  CHK(upload_pack(E, pk, dv));
-  HIPCHK(hipMemcpyAsync(E->plan_d, dv[4], sizeof(LevelPlan), hipMemcpyDeviceToDevice, E->st));
-  const int32_t *feat_d = reinterpret_cast<const int32_t *>(dv[0]);
-  // The root's arena stays untouched until the next tree's upload.
+  int32_t n_hist = 0;
+  if (pre) {
+    dv = pre->dev;
+    n_hist = pre->n_hist;
+  } else {
+    RootPack R;
+    build_root_pack(E, m, feats, nb_sel, R);
+    CHK(upload_pack(E, R.pk, dv));
+    HIPCHK(hipMemcpyAsync(E->plan_d, dv[kPackPlan], sizeof(LevelPlan), hipMemcpyDeviceToDevice,
+                          E->st));
+    n_hist = R.rp.n_hist;
+  }
+  const int32_t *feat_d = reinterpret_cast<const int32_t *>(dv[kPackFeat]);
+  // The root's arena stays untouched until the next tree's upload (a
+  // round's: until its slot's next round).
   E->feat_d = feat_d;
-  E->nb_sel_d = reinterpret_cast<const int32_t *>(dv[1]);
+  E->nb_sel_d = reinterpret_cast<const int32_t *>(dv[kPackNbHot]);
   E->hot_sel_d = E->nb_sel_d + F_sel;
   // (A boosting round's root rows are already in set b: launch_gather_codes
   // and launch_gather_gh.)
@@ -802,18 +854,18 @@ int launch_root(bsscl_engine *E, const int32_t *rows32, int64_t m,
   hipEvent_t stop;
   CHK(prof_begin(E, 0, &stop));
   HIPCHK(launch_hist(E->st, E->codes_c[b].p, E->ld_c, E->gh_c[b].p,
-                     reinterpret_cast<const HistTask *>(dv[2]), E->plan_d, rp.n_hist,
-                     E->hist_node_d.p, reinterpret_cast<const int32_t *>(dv[5]), E->segs.p,
+                     reinterpret_cast<const HistTask *>(dv[kPackHist]), E->plan_d, n_hist,
+                     E->hist_node_d.p, reinterpret_cast<const int32_t *>(dv[kPackTasks]), E->segs.p,
                      E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel), E->hist_copies,
                      E->part_d.p, E->pool.p, E->node_stride));
   CHK(prof_end(E, stop));
   CHK(prof_begin(E, 3, &stop));
-  HIPCHK(launch_hist_reduce(E->st, E->plan_d, 1, reinterpret_cast<const int32_t *>(dv[5]),
+  HIPCHK(launch_hist_reduce(E->st, E->plan_d, 1, reinterpret_cast<const int32_t *>(dv[kPackTasks]),
                             E->hist_node_d.p, E->segs.p, E->part_d.p, F_sel, E->pool.p,
                             E->node_stride));
   CHK(prof_end(E, stop));
   CHK(prof_begin(E, 2, &stop));
-  HIPCHK(launch_split(E->st, reinterpret_cast<const SplitTask *>(dv[3]), E->plan_d, 1,
+  HIPCHK(launch_split(E->st, reinterpret_cast<const SplitTask *>(dv[kPackSplit]), E->plan_d, 1,
                       E->segs.p, E->pool.p, E->node_stride, E->nb_sel_d, F_sel,
                       split_params(E, tp), E->cand.p, E->totals.p));
   // The root's table record is written by the level-0 planner.
@@ -1025,10 +1077,10 @@ constexpr int32_t kLevelsPerCheck = 8;  // levels enqueued between host checks
 int launch_tree(bsscl_engine *E, const int32_t *rows32, int64_t m,
                 const std::vector<int32_t> &feats,
                 const std::vector<int32_t> &nb_sel, const TreeParams &tp, int32_t *run,
-                bool checks = true, bool gathered = false) {
+                bool checks = true, bool gathered = false, const PreRoot *pre = nullptr) {
   const int32_t F_sel = (int32_t)feats.size();
   const int32_t levels = std::max(1, tp.max_depth);
-  CHK(launch_root(E, rows32, m, feats, nb_sel, tp, gathered));
+  CHK(launch_root(E, rows32, m, feats, nb_sel, tp, gathered, pre));
   *run = 0;
   for (int32_t d = 0; d < levels; ++d) {
     const bool last = d + 1 >= tp.max_depth;
@@ -1336,16 +1388,32 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   E->set_base = 2 * s;
   if (rc == BSSCL_OK && R.device_replay)
     rc = prepare_tree_buffers(E, m, F_sel, std::max(1, a.max_depth), a.max_leaves);
-  if (rc == BSSCL_OK && R.device_replay && E->feat_pin_n[s] < F_sel) {
-    if (E->feat_pin[s]) (void)hipHostFree(E->feat_pin[s]);
-    E->feat_pin[s] = nullptr;
-    E->feat_pin_n[s] = 0;
-    hipError_t e = hipHostMalloc(reinterpret_cast<void **>(&E->feat_pin[s]),
-                                 (size_t)std::max(F_sel, 1) * 4, hipHostMallocDefault);
-    if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("feature list: ") + hipGetErrorString(e));
-    else E->feat_pin_n[s] = std::max(F_sel, 1);
+  // The root's pack, for the rows stream to upload into the slot's arena
+  // (root_pin[s] and root_d[s] were last used by the round before the
+  // previous one, which finish_round has waited for).
+  RootPack rpk;
+  std::vector<size_t> rpk_off;
+  size_t total = 0;
+  PreRoot pre;
+  if (rc == BSSCL_OK && R.device_replay) {
+    build_root_pack(E, m, R.feats, R.nb_sel, rpk);
+    total = pack_layout(rpk.pk, rpk_off);
+    if (E->root_pin_n[s] < total) {
+      if (E->root_pin[s]) (void)hipHostFree(E->root_pin[s]);
+      E->root_pin[s] = nullptr;
+      E->root_pin_n[s] = 0;
+      hipError_t e = hipHostMalloc(reinterpret_cast<void **>(&E->root_pin[s]), 2 * total,
+                                   hipHostMallocDefault);
+      if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("root pack: ") + hipGetErrorString(e));
+      else E->root_pin_n[s] = 2 * total;
+    }
+    if (rc == BSSCL_OK) rc = E->root_d[s].ensure(total);
+    if (rc == BSSCL_OK) {
+      pre.n_hist = rpk.rp.n_hist;
+      pre.dev.resize(rpk_off.size());
+      for (size_t i = 0; i < rpk_off.size(); ++i) pre.dev[i] = E->root_d[s].p + rpk_off[i];
+    }
   }
-  if (rc == BSSCL_OK && R.device_replay) rc = E->feat_slot_d[s].ensure((size_t)std::max(F_sel, 1));
   // The round's in-bag rows on the device, ascending: the reference's
   // sample_idx (a prefix of the cumulative permutation) sorted.  Made on
   // the rows stream; only that stream touches the permutation, the
@@ -1406,15 +1474,14 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     if (rc == BSSCL_OK && e == hipSuccess && rows_d)
       e = launch_sort_rows(rs, rows_d, m, E->row_flags.p, n_pad, E->sort_tmp.p,
                            E->round_rows[s].p);
-    // The root's codes too (sets 2s, 2s + 1 were last read by the tree of
-    // the round before the previous one).  feat_pin[s] was last copied by
-    // that round's rows stream.
+    // The root's pack, then its codes (sets 2s, 2s + 1 were last read by
+    // the tree of the round before the previous one).
     if (rc == BSSCL_OK && e == hipSuccess && R.device_replay) {
-      std::memcpy(E->feat_pin[s], R.feats.data(), (size_t)F_sel * 4);
-      e = hipMemcpyAsync(E->feat_slot_d[s].p, E->feat_pin[s], (size_t)F_sel * 4,
-                         hipMemcpyHostToDevice, rs);
+      pack_copy(rpk.pk, rpk_off, E->root_pin[s]);
+      e = hipMemcpyAsync(E->root_d[s].p, E->root_pin[s], total, hipMemcpyHostToDevice, rs);
       if (e == hipSuccess)
-        e = launch_gather_codes(rs, X.codes.p, X.ld, E->feat_slot_d[s].p, F_sel,
+        e = launch_gather_codes(rs, X.codes.p, X.ld,
+                                reinterpret_cast<const int32_t *>(pre.dev[kPackFeat]), F_sel,
                                 E->round_rows[s].p, m, E->codes_c[2 * s].p, E->ld_c, E->ld_c);
     }
     if (rc == BSSCL_OK && e == hipSuccess && !E->rows_ready[s])
@@ -1431,7 +1498,9 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     hipError_t e = R.device_replay
                        ? launch_gather_gh(E->st, E->F.p, E->y.p, E->round_rows[s].p, m, E->w0,
                                           E->w1, gm, hm, E->gh_c[2 * s].p, E->ld_c, E->segs.p,
-                                          E->hist_node_d.p)
+                                          E->hist_node_d.p,
+                                          reinterpret_cast<const LevelPlan *>(pre.dev[kPackPlan]),
+                                          E->plan_d)
                        : launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, gm, hm,
                                           E->ghq.p);
     if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("gradients: ") + hipGetErrorString(e));
@@ -1441,7 +1510,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   if (rc == BSSCL_OK) rc = ensure_round_out(E, s, R.M);
   if (rc == BSSCL_OK && R.device_replay)
     rc = launch_tree(E, E->round_rows[s].p, m, R.feats, R.nb_sel, tp, &R.run, !E->pipeline,
-                     true);
+                     true, &pre);
   if (rc == BSSCL_OK && R.device_replay) {
     RoundHeader *hdr = reinterpret_cast<RoundHeader *>(E->round_d[s].p);
     ReplayArgs ra;
@@ -1589,6 +1658,7 @@ int bsscl_engine_create(int32_t device, bsscl_engine **out) {
   hipError_t e = hipStreamCreateWithFlags(&E->st, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&E->st_rows, hipStreamNonBlocking);
   if (e != hipSuccess) {
+    if (E->st_rows) (void)hipStreamDestroy(E->st_rows);
     if (E->st) (void)hipStreamDestroy(E->st);
     delete E;
     return set_error(BSSCL_EDEVICE, std::string("hipStreamCreate: ") + hipGetErrorString(e));
@@ -1625,8 +1695,8 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   }
   for (int s = 0; s < 2; ++s) {
     E->rid_c[s].release();
-    E->feat_slot_d[s].release();
-    if (E->feat_pin[s]) (void)hipHostFree(E->feat_pin[s]);
+    E->root_d[s].release();
+    if (E->root_pin[s]) (void)hipHostFree(E->root_pin[s]);
   }
   for (auto &r : E->round_rows) r.release();
   E->rows64.release();

@@ -211,7 +211,9 @@ hipError_t launch_gather_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
 hipError_t launch_gather_gh(hipStream_t st, const double *F, const uint8_t *y,
                             const int32_t *rows32, int64_t m, double w0, double w1,
                             double g_mul, double h_mul, int2 *gh_c, int64_t pad_to,
-                            NodeSeg *segs, int32_t *hist_node);
+                            NodeSeg *segs, int32_t *hist_node,
+                            const LevelPlan *plan_src = nullptr,
+                            LevelPlan *plan_dst = nullptr);
 // Level kernels take their work counts from a device LevelPlan; the grid
 // argument (blocks, tasks or parents) is an upper bound, and blocks loop
 // over the work with a grid stride, so any bound >= 1 gives the same result.

@@ -469,9 +469,11 @@ __global__ __launch_bounds__(256) void k_gather_gh(
     const double *__restrict__ F, const uint8_t *__restrict__ y,
     const int32_t *__restrict__ rows32, int64_t m, double w0, double w1, double g_mul,
     double h_mul, int2 *__restrict__ gh_c, int64_t pad_to, NodeSeg *__restrict__ segs,
-    int32_t *__restrict__ hist_node) {
+    int32_t *__restrict__ hist_node, const LevelPlan *__restrict__ plan_src,
+    LevelPlan *__restrict__ plan_dst) {
   const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (k == 0) {
+    if (plan_src) *plan_dst = *plan_src;
     NodeSeg r;
     r.start = 0;
     r.count = m;
@@ -505,10 +507,12 @@ hipError_t launch_gather_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
 hipError_t launch_gather_gh(hipStream_t st, const double *F, const uint8_t *y,
                             const int32_t *rows32, int64_t m, double w0, double w1,
                             double g_mul, double h_mul, int2 *gh_c, int64_t pad_to,
-                            NodeSeg *segs, int32_t *hist_node) {
+                            NodeSeg *segs, int32_t *hist_node, const LevelPlan *plan_src,
+                            LevelPlan *plan_dst) {
   if (pad_to <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_gather_gh, dim3((unsigned)((pad_to + 255) / 256)), dim3(256), 0, st,
-                     F, y, rows32, m, w0, w1, g_mul, h_mul, gh_c, pad_to, segs, hist_node);
+                     F, y, rows32, m, w0, w1, g_mul, h_mul, gh_c, pad_to, segs, hist_node,
+                     plan_src, plan_dst);
   return hipGetLastError();
 }
 
