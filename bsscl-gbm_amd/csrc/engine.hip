@@ -1027,8 +1027,33 @@ int ensure_host_pinned(bsscl_engine *E, char *&p, size_t &have, size_t bytes) {
 
 // Readback buffers of round buffer b: the round's header and tree, and the
 // node table (for profiling counters).
-int ensure_round_out(bsscl_engine *E, int b, int32_t M) {
-  const size_t bytes = round_out_bytes(M);
+// The sum k_sum_partials forms, in its order: 256 strided sums, each wave's
+// xor butterfly, then the four waves' sums pairwise (so a round summed here
+// gives the bits of one summed on the device).
+double sum_partials_host(const double *p, int32_t count) {
+  double lane[256];
+  for (int t = 0; t < 256; ++t) {
+    double acc = 0.0;
+    for (int32_t i = t; i < count; i += 256) acc += p[i];
+    lane[t] = acc;
+  }
+  double red[4];
+  for (int w = 0; w < 4; ++w) {
+    double a[64], b[64];
+    for (int l = 0; l < 64; ++l) a[l] = lane[64 * w + l];
+    for (int o = 32; o >= 1; o >>= 1) {
+      for (int l = 0; l < 64; ++l) b[l] = a[l] + a[l ^ o];
+      std::memcpy(a, b, sizeof(a));
+    }
+    red[w] = a[0];
+  }
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// A round's readback: the round_out_bytes(M) of the tree, then the F
+// update's per-block losses (`partials` doubles).
+int ensure_round_out(bsscl_engine *E, int b, int32_t M, int32_t partials) {
+  const size_t bytes = round_out_bytes(M) + (size_t)partials * 8;
   if (E->round_d[b].cap < bytes) CHK(sync(E));
   CHK(E->round_d[b].ensure(bytes));
   CHK(ensure_host_pinned(E, E->round_pin[b], E->round_pin_bytes[b], bytes));
@@ -1507,7 +1532,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   }
   if (rc == BSSCL_OK) rc = E->partials_d.ensure((size_t)nb);
   if (rc == BSSCL_OK) rc = E->tree_d.ensure((size_t)R.M);
-  if (rc == BSSCL_OK) rc = ensure_round_out(E, s, R.M);
+  if (rc == BSSCL_OK) rc = ensure_round_out(E, s, R.M, nb);
   if (rc == BSSCL_OK && R.device_replay)
     rc = launch_tree(E, E->round_rows[s].p, m, R.feats, R.nb_sel, tp, &R.run, !E->pipeline,
                      true, &pre);
@@ -1527,13 +1552,15 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     ra.node_cap = E->node_cap;
     hipError_t e = launch_replay(E->st, E->nodes_d, E->plan_d, E->feat_d, ra,
                                  round_arrays(E->round_d[s].p, R.M), E->tree_d.p, hdr);
+    // The per-block losses follow the tree; the host sums them
+    // (sum_partials_host).
     if (e == hipSuccess)
       e = launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, R.M, &hdr->node_count,
-                          a.learning_rate, E->F.p, E->y.p, E->partials_d.p, nb);
-    if (e == hipSuccess) e = launch_sum_partials(E->st, E->partials_d.p, nb, &hdr->loss_sum);
+                          a.learning_rate, E->F.p, E->y.p,
+                          reinterpret_cast<double *>(E->round_d[s].p + round_out_bytes(R.M)), nb);
     if (e == hipSuccess)
-      e = hipMemcpyAsync(E->round_pin[s], E->round_d[s].p, round_out_bytes(R.M),
-                         hipMemcpyDeviceToHost, E->st);
+      e = hipMemcpyAsync(E->round_pin[s], E->round_d[s].p,
+                         round_out_bytes(R.M) + (size_t)nb * 8, hipMemcpyDeviceToHost, E->st);
     if (e == hipSuccess && E->prof)
       e = hipMemcpyAsync(E->rtable_pin[s], E->table_d.p,
                          64 + (size_t)table_bound(E, R.run) * sizeof(NodeOut),
@@ -1593,7 +1620,11 @@ int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
     std::memcpy(out.right, ha.right, (size_t)M * 4);
     std::memcpy(out.gains, ha.gains, (size_t)M * 8);
     *out.node_count = h.node_count;
-    if (out_train_loss) *out_train_loss = -h.loss_sum / (double)X.n;
+    if (out_train_loss) {
+      const double *parts =
+          reinterpret_cast<const double *>(E->round_pin[s] + round_out_bytes(R.M));
+      *out_train_loss = -sum_partials_host(parts, update_F_blocks(X.n)) / (double)X.n;
+    }
     return BSSCL_OK;
   }
   if (h.status != 1 && h.status != 4)

@@ -2028,11 +2028,14 @@ hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
 // F update and training loss (est:2896-2897, est:2905 -> est:2320-2325).
 // ---------------------------------------------------------------------------
 constexpr int kUpdBlock = 256;
+constexpr int kUpdRows = 4;  // rows a thread walks at once
 
+// One pass of kUpdRows rows per thread where the grid allows (every row's
+// chain of code loads in flight at once), at most 8192 blocks.
 int update_F_blocks(int64_t n) {
-  int64_t b = (n + kUpdBlock * 16 - 1) / (kUpdBlock * 16);
+  int64_t b = (n + kUpdBlock * kUpdRows - 1) / (kUpdBlock * kUpdRows);
   if (b < 1) b = 1;
-  if (b > 4096) b = 4096;
+  if (b > 8192) b = 8192;
   return (int)b;
 }
 
@@ -2054,7 +2057,6 @@ __device__ __forceinline__ int32_t traverse(const TreeNodeDev *__restrict__ tree
 // LDS (up to kUpdTreeLds nodes) and each thread walks four rows at once, so
 // four chains of dependent code loads are in flight per thread.
 constexpr int kUpdTreeLds = 1024;
-constexpr int kUpdRows = 4;
 
 #pragma clang fp contract(off)
 __device__ __forceinline__ double row_loss(double f, uint8_t yi) {
