@@ -944,22 +944,36 @@ hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
 // Moves a tile's rows to the child segments in the other buffer set, keeping
 // the input order on each side.  A row's slot (left run, then right run) is
 // a block-wide exclusive scan of per-thread counts plus its rank among the
-// thread's 16 rows; inv[slot] is the row it came from.  The output is cut
-// into R-byte chunks aligned in the destination: per feature, the tile's
-// codes go to LDS (one R-byte store per thread) and each chunk is gathered
-// from there and written with one R-byte store (byte stores only for the
-// chunks at the ends of a run, which it shares with the neighbouring
-// tiles).  (g,h) and row ids are gathered through inv and stored as
-// consecutive elements.
+// thread's R rows; inv[slot] is the row it came from.  The output is cut
+// into R-byte chunks aligned in the destination.  Features move four at a
+// time: each tile row's four codes go to LDS as one 32-bit word (a 4x4 byte
+// transpose of the thread's loads), and each output chunk reads its R
+// source rows' words and transposes them back into one R-byte store per
+// feature (byte stores only for the chunks at the ends of a run, which it
+// shares with the neighbouring tiles).  (g,h) and row ids are gathered
+// through inv and stored as consecutive elements.
 constexpr int kChunkSlots = 2;  // output chunks a thread may own (<= 260 per tile)
-// Features staged in LDS per barrier: more loads in flight for the narrow
-// tiles; one for 16-row tiles, whose registers already limit occupancy.
-template <int R> struct ScatterFeats { static constexpr int value = 4; };
-template <> struct ScatterFeats<16> { static constexpr int value = 1; };
-// Waves per SIMD the register budget must allow (the occupancy each tile
-// shape had before the parents' scan moved into this kernel).
-template <int R> struct ScatterWaves { static constexpr int value = 5; };
-template <> struct ScatterWaves<4> { static constexpr int value = 7; };
+constexpr int kQuad = 4;        // features per LDS pass (one 32-bit word per row)
+
+// 4x4 byte transpose: byte j of r_i is byte i of w_j.
+__device__ __forceinline__ void transpose4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                           uint32_t &r0, uint32_t &r1, uint32_t &r2,
+                                           uint32_t &r3) {
+  const uint32_t lo01 = (w0 & 0x00ff00ffu) | ((w1 & 0x00ff00ffu) << 8);  // w0.0 w1.0 w0.2 w1.2
+  const uint32_t hi01 = ((w0 >> 8) & 0x00ff00ffu) | (w1 & 0xff00ff00u);  // w0.1 w1.1 w0.3 w1.3
+  const uint32_t lo23 = (w2 & 0x00ff00ffu) | ((w3 & 0x00ff00ffu) << 8);
+  const uint32_t hi23 = ((w2 >> 8) & 0x00ff00ffu) | (w3 & 0xff00ff00u);
+  r0 = (lo01 & 0xffffu) | (lo23 << 16);
+  r1 = (hi01 & 0xffffu) | (hi23 << 16);
+  r2 = (lo01 >> 16) | (lo23 & 0xffff0000u);
+  r3 = (hi01 >> 16) | (hi23 & 0xffff0000u);
+}
+// Waves per SIMD the register budget must allow.  16-row tiles move one
+// feature per barrier through LDS bytes instead of four through words: the
+// word transposes of 16 rows need more registers than that occupancy allows.
+template <int R> struct ScatterWaves { static constexpr int value = 4; };
+template <> struct ScatterWaves<4> { static constexpr int value = 5; };
+template <> struct ScatterWaves<16> { static constexpr int value = 5; };
 
 template <int R>
 __global__ __launch_bounds__(kPartBlock) __attribute__((amdgpu_waves_per_eu(ScatterWaves<R>::value)))
@@ -976,9 +990,11 @@ void k_part_scatter(
   __shared__ unsigned long long red[kPartBlock / 64];
   constexpr int kTile = kPartBlock * R;
   __shared__ uint16_t inv[kTile];
-  constexpr int kScatterFeats = ScatterFeats<R>::value;
-  // kScatterFeats features' codes per batch, double buffered.
-  __shared__ typename CodesR<R>::T cs[2][kScatterFeats][kPartBlock];
+  constexpr bool kQuads = R < 16;
+  // Four features' codes per tile row (16-row tiles: one feature's codes per
+  // thread), double buffered.
+  __shared__ __align__(16) uint32_t rows4[2][kQuads ? kTile : 1];
+  __shared__ typename CodesR<R>::T cs[2][kQuads ? 1 : kPartBlock];
   const int32_t n_tiles = plan->n_tiles;
   const int tid = (int)threadIdx.x;
   for (int32_t ti = (int32_t)blockIdx.x; ti < n_tiles; ti += (int32_t)gridDim.x) {
@@ -1100,27 +1116,18 @@ void k_part_scatter(
       }
       cfull[q] = full;
     }
-    // Per batch of kScatterFeats features: codes to LDS (double buffered:
-    // one barrier per batch, the next batch's loads in flight meanwhile),
-    // then the owned chunks gathered from LDS and stored.
-    CodeWords<R> cur[kScatterFeats];
-#pragma unroll
-    for (int u = 0; u < kScatterFeats; ++u)
-      if (u < F_sel) cur[u] = load_codes<R>(codes_src + (int64_t)u * ld_c, row, lo, hi);
-    for (int f0 = 0, b = 0; f0 < F_sel; f0 += kScatterFeats, b ^= 1) {
-#pragma unroll
-      for (int u = 0; u < kScatterFeats; ++u)
-        if (f0 + u < F_sel) cs[b][u][tid] = cur[u].v;
-#pragma unroll
-      for (int u = 0; u < kScatterFeats; ++u)
-        if (f0 + kScatterFeats + u < F_sel)
-          cur[u] = load_codes<R>(codes_src + (int64_t)(f0 + kScatterFeats + u) * ld_c, row, lo, hi);
-      __syncthreads();
-#pragma unroll
-      for (int u = 0; u < kScatterFeats; ++u) {
-        if (f0 + u >= F_sel) break;
-        const uint8_t *tb = reinterpret_cast<const uint8_t *>(cs[b][u]);
-        uint8_t *dcol = codes_dst + (int64_t)(f0 + u) * ld_c;
+    // Codes, double buffered in LDS (one barrier per batch, the next batch's
+    // loads in flight meanwhile), then the owned chunks gathered and stored:
+    // 16-row tiles one feature per batch as bytes, narrower tiles four
+    // features per batch as one word of four codes per tile row.
+    if constexpr (!kQuads) {
+      CodeWords<R> c1 = load_codes<R>(codes_src, row, lo, hi);
+      for (int f = 0, b = 0; f < F_sel; ++f, b ^= 1) {
+        cs[b][tid] = c1.v;
+        if (f + 1 < F_sel) c1 = load_codes<R>(codes_src + (int64_t)(f + 1) * ld_c, row, lo, hi);
+        __syncthreads();
+        const uint8_t *tb = reinterpret_cast<const uint8_t *>(cs[b]);
+        uint8_t *dcol = codes_dst + (int64_t)f * ld_c;
 #pragma unroll
         for (int q = 0; q < kChunkSlots; ++q) {
           if (!cown[q]) continue;
@@ -1142,8 +1149,67 @@ void k_part_scatter(
           }
         }
       }
+    } else {
+      CodeWords<R> cur[kQuad];
+#pragma unroll
+      for (int u = 0; u < kQuad; ++u) {
+        if (u < F_sel) {
+          cur[u] = load_codes<R>(codes_src + (int64_t)u * ld_c, row, lo, hi);
+        } else {
+#pragma unroll
+          for (int k = 0; k < R / 4; ++k) cur[u].w[k] = 0u;
+        }
+      }
+      for (int f0 = 0, b = 0; f0 < F_sel; f0 += kQuad, b ^= 1) {
+#pragma unroll
+        for (int g = 0; g < R / 4; ++g) {
+          uint4 r;
+          transpose4(cur[0].w[g], cur[1].w[g], cur[2].w[g], cur[3].w[g], r.x, r.y, r.z, r.w);
+          *reinterpret_cast<uint4 *>(&rows4[b][R * tid + 4 * g]) = r;
+        }
+#pragma unroll
+        for (int u = 0; u < kQuad; ++u) {
+          if (f0 + kQuad + u < F_sel) {
+            cur[u] = load_codes<R>(codes_src + (int64_t)(f0 + kQuad + u) * ld_c, row, lo, hi);
+          } else {
+#pragma unroll
+            for (int k = 0; k < R / 4; ++k) cur[u].w[k] = 0u;
+          }
+        }
+        __syncthreads();
+        const int nf = min(kQuad, F_sel - f0);
+#pragma unroll
+        for (int q = 0; q < kChunkSlots; ++q) {
+          if (!cown[q]) continue;
+          CodeWords<R> o[kQuad];
+#pragma unroll
+          for (int g = 0; g < R / 4; ++g) {
+            uint32_t sw[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint32_t sv = (csrc[q][(4 * g + j) >> 1] >> (16 * ((4 * g + j) & 1))) & 0xffffu;
+              sw[j] = rows4[b][sv < (uint32_t)kTile ? sv : 0u];
+            }
+            transpose4(sw[0], sw[1], sw[2], sw[3], o[0].w[g], o[1].w[g], o[2].w[g], o[3].w[g]);
+          }
+#pragma unroll
+          for (int u = 0; u < kQuad; ++u) {
+            if (u >= nf) break;
+            uint8_t *dcol = codes_dst + (int64_t)(f0 + u) * ld_c;
+            if (cfull[q]) {
+              *reinterpret_cast<typename CodesR<R>::T *>(dcol + cdst[q]) = o[u].v;
+            } else {
+#pragma unroll
+              for (int k = 0; k < R; ++k) {
+                const uint32_t sv = (csrc[q][k >> 1] >> (16 * (k & 1))) & 0xffffu;
+                if (sv != 0xffffu) dcol[cdst[q] + k] = (uint8_t)(o[u].w[k >> 2] >> (8 * (k & 3)));
+              }
+            }
+          }
+        }
+      }
     }
-    __syncthreads();  // inv and cs are rewritten by the block's next tile
+    __syncthreads();  // inv and rows4 are rewritten by the block's next tile
   }
 }
 
