@@ -757,7 +757,7 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
 // 64 consecutive words of one node: its kReduceWaves waves each sum every
 // kReduceWaves-th partial (one coalesced 512-byte load per partial), then
 // the waves' sums are added in LDS.
-constexpr int kReduceWaves = 16;
+constexpr int kReduceWaves = 4;
 
 __global__ __launch_bounds__(64 * kReduceWaves) void k_hist_reduce(
     const LevelPlan *__restrict__ plan, const int32_t *__restrict__ hist_begin,
