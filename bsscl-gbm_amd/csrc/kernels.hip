@@ -464,7 +464,8 @@ __global__ __launch_bounds__(256) void k_gather_codes(
 }
 
 // The in-bag rows' fixed-point (g, h) straight from F and y (k_grad_hess's
-// arithmetic, for these rows only), and the root's segment.
+// arithmetic, for these rows only), the root's segment and, when plan_src is
+// given, the root's LevelPlan (copied to plan_dst).
 __global__ __launch_bounds__(256) void k_gather_gh(
     const double *__restrict__ F, const uint8_t *__restrict__ y,
     const int32_t *__restrict__ rows32, int64_t m, double w0, double w1, double g_mul,
