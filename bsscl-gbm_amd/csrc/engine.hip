@@ -1066,7 +1066,7 @@ int ensure_round_out(bsscl_engine *E, int b, int32_t M, int32_t partials) {
 // Shuffles of at least this many positions build their step lists by
 // sorting (position, step) keys; shorter ones use per-position linked
 // lists.  (Test hook: BSSCL_FY_SORTED=1 or 0 forces one form.)
-constexpr int64_t kFySortedMin = 1 << 19;
+constexpr int64_t kFySortedMin = 1 << 18;
 
 int ensure_fy_work(bsscl_engine *E, int64_t n, FyWork &w) {
   for (DevBuf<int32_t> *x : {&E->fy_head, &E->fy_next, &E->fy_v}) CHK(x->ensure((size_t)n));
