@@ -207,7 +207,7 @@ struct bsscl_engine {
   DevBuf<double> F;
   DevBuf<uint8_t> y;
   double w0 = 1.0, w1 = 1.0;
-  DevBuf<int2> ghq;
+  DevBuf<GH> ghq;
   DevBuf<double> g64, h64;
   double g_scale = 1.0, h_scale = 1.0;  // fixed point -> value
 
@@ -216,7 +216,7 @@ struct bsscl_engine {
   // alternate); a boosting round in slot s uses base 2s, so the next round's
   // root codes are gathered while this round's tree still reads its own.
   DevBuf<uint8_t> codes_c[4];
-  DevBuf<int2> gh_c[4];
+  DevBuf<GH> gh_c[4];
   DevBuf<int32_t> rid_c[2];  // with set_base 0 only
   int32_t set_base = 0;
   // A boosting round's root inputs (RootPack), uploaded by the rows stream
@@ -422,13 +422,19 @@ int alloc_matrix(bsscl_engine *E, int32_t slot, int64_t n, int32_t F) {
   return BSSCL_OK;
 }
 
-// Exponent s with max_abs * 2^s <= 2^30, so per-row fixed-point values fit
-// in int32 and a sum of up to 2^33 rows fits in int64.
-double fixed_mul(double max_abs) {
-  if (!(max_abs > 0.0) || !std::isfinite(max_abs)) return std::ldexp(1.0, 30);
+// Scale 2^s of the 64-bit fixed-point values of a tree whose sums run over at
+// most `rows` rows: every row's |v| * 2^s < 2^B with B = 62 - ceil(log2(rows)),
+// so any such sum (and the difference of two nested ones) fits in int64.
+// The widest exponent the sums allow: a bin of many tiny, equal hessians
+// (confident rows late in a fit) then keeps its relative precision.
+double fixed_mul(double max_abs, int64_t rows) {
+  int lg = 1;
+  while (lg < 62 && (int64_t(1) << lg) < rows) ++lg;
+  const int B = 62 - lg;
+  if (!(max_abs > 0.0) || !std::isfinite(max_abs)) return std::ldexp(1.0, B);
   int e;
   std::frexp(max_abs, &e);  // max_abs < 2^e
-  return std::ldexp(1.0, 30 - e);
+  return std::ldexp(1.0, B - e);
 }
 
 // Nodes a tree of `levels` levels can hold: the full binary tree when it is
@@ -669,13 +675,13 @@ void add_part_tiles(const bsscl_engine *E, const PartParent &P, int32_t parent_i
     tiles.push_back({r, E->part_tile, parent_index});
 }
 
-// Histogram launch shape of a tree over m rows of F_sel features.  One
-// feature per block gives the most blocks and the least work per block,
-// which suits every level of a tree up to ~64M row-features (measured on
-// MI355X: 1M x 22 root 27.5 us with one feature per block, 33.5 us with
-// four); larger trees use two features per block, which reads each row's
-// (g,h) half as often (5M x 35 root: 165 us, 205 us with one).  The
-// environment overrides the defaults (read per tree, for tuning sweeps).
+// Histogram launch shape of a tree over m rows of F_sel features.  A block
+// reads its rows' 16-byte (g,h) once per feature chunk, so wider
+// chunks read them less often but hold more LDS.  Measured on MI355X (whole
+// rounds): 1M x 22, two features per block 2080 trees/s against 2009 with
+// one and 1939 with four; 5M x 35, four features per block 336 trees/s
+// against 324 with two.  The environment overrides the defaults (read per
+// tree, for tuning sweeps).
 void read_hist_tuning(bsscl_engine *E, int64_t m, int32_t F_sel) {
   auto env_int = [](const char *name, int32_t lo, int32_t hi, int32_t dflt) {
     const char *e = std::getenv(name);
@@ -683,7 +689,7 @@ void read_hist_tuning(bsscl_engine *E, int64_t m, int32_t F_sel) {
     const long x = std::strtol(e, nullptr, 10);
     return (x >= lo && x <= hi) ? (int32_t)x : dflt;
   };
-  const int32_t fc0 = (double)m * F_sel >= 64e6 ? 2 : 1;
+  const int32_t fc0 = (double)m * F_sel >= 64e6 ? 4 : 2;
   E->hist_fc = env_int("BSSCL_HIST_FC", 1, 8, fc0);
   if (E->hist_fc != 1 && E->hist_fc != 2 && E->hist_fc != 4 && E->hist_fc != 8) E->hist_fc = fc0;
   // Four lane-owned copies of each histogram in LDS (see k_hist): 18.6
@@ -1235,7 +1241,7 @@ int validate_tree_args(bsscl_engine *E, const int32_t *feature_indices,
 // Uploads host gradients/hessians and quantizes them with scales from their
 // largest magnitudes.
 int load_grad_hess(bsscl_engine *E, const double *grad, const double *hess,
-                   int64_t n) {
+                   int64_t n, int64_t rows_summed) {
   double gmax = 0.0, hmax = 0.0;
   for (int64_t i = 0; i < n; ++i) {
     const double a = std::fabs(grad[i]), b = std::fabs(hess[i]);
@@ -1244,7 +1250,7 @@ int load_grad_hess(bsscl_engine *E, const double *grad, const double *hess,
     gmax = std::max(gmax, a);
     hmax = std::max(hmax, b);
   }
-  const double gm = fixed_mul(gmax), hm = fixed_mul(hmax);
+  const double gm = fixed_mul(gmax, rows_summed), hm = fixed_mul(hmax, rows_summed);
   E->g_scale = 1.0 / gm;
   E->h_scale = 1.0 / hm;
   CHK(E->g64.ensure((size_t)n));
@@ -1357,7 +1363,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   ++E->round_seq;
   // Gradients from the current F: |g| <= max(w0, w1), h <= max(w0, w1)/4.
   const double wmax = std::max(E->w0, E->w1);
-  const double gm = fixed_mul(wmax), hm = fixed_mul(0.25 * wmax);
+  const double gm = fixed_mul(wmax, m), hm = fixed_mul(0.25 * wmax, m);
   E->g_scale = 1.0 / gm;
   E->h_scale = 1.0 / hm;
   SamplerRound sr;
@@ -1637,8 +1643,8 @@ int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
     // Gradients of every row from the unchanged F (the device path gathered
     // only the in-bag rows').
     const double wmax = std::max(E->w0, E->w1);
-    HIPCHK(launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, fixed_mul(wmax),
-                            fixed_mul(0.25 * wmax), E->ghq.p));
+    HIPCHK(launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, fixed_mul(wmax, R.m),
+                            fixed_mul(0.25 * wmax, R.m), E->ghq.p));
   }
   E->set_base = 2 * s;
   CHK(build_tree_core(E, E->round_rows[s].p, R.m, R.feats, R.nb_sel, tp, out));
@@ -2061,7 +2067,7 @@ int bsscl_build_tree(bsscl_engine *E, const double *grad, const double *hess,
   CHK(validate_tree_args(E, feature_indices, n_selected, max_leaves,
                          min_samples_leaf, bin_counts, out, feats, nb_sel));
   HIPCHK(hipSetDevice(E->device));
-  CHK(load_grad_hess(E, grad, hess, X.n));
+  CHK(load_grad_hess(E, grad, hess, X.n, n_samples));
   CHK(E->rows64.ensure((size_t)n_samples));
   HIPCHK(hipMemcpyAsync(E->rows64.p, sample_indices, (size_t)n_samples * 8,
                         hipMemcpyHostToDevice, E->st));
@@ -2293,7 +2299,7 @@ int bsscl_node_split(bsscl_engine *E, const double *grad, const double *hess,
     if (nb_sel[(size_t)i] < 1 || nb_sel[(size_t)i] > kBins) return set_error(BSSCL_EINVAL, "node_split: bad bin count");
   }
   HIPCHK(hipSetDevice(E->device));
-  CHK(load_grad_hess(E, grad, hess, X.n));
+  CHK(load_grad_hess(E, grad, hess, X.n, m));
   CHK(E->rows64.ensure((size_t)m));
   HIPCHK(hipMemcpyAsync(E->rows64.p, rows, (size_t)m * 8, hipMemcpyHostToDevice, E->st));
   // The root of a tree build: histogram and split search of these rows.
@@ -2338,7 +2344,7 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
   HIPCHK(hipSetDevice(E->device));
   if (!E->ghq.p || E->ghq.cap < (size_t)X.n) {
     CHK(E->ghq.ensure((size_t)X.n));
-    HIPCHK(hipMemsetAsync(E->ghq.p, 0, (size_t)X.n * sizeof(int2), E->st));
+    HIPCHK(hipMemsetAsync(E->ghq.p, 0, (size_t)X.n * sizeof(GH), E->st));
   }
   CHK(E->rows64.ensure((size_t)m));
   HIPCHK(hipMemcpyAsync(E->rows64.p, rows, (size_t)m * 8, hipMemcpyHostToDevice, E->st));

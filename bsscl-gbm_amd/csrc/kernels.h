@@ -10,6 +10,11 @@ namespace bsscl {
 constexpr int kBins = 256;          // histogram bins per feature (uint8 codes)
 constexpr int kHistPerFeat = 512;   // int64 words per feature: [bin][g,h]
 
+// Fixed-point gradient and hessian of one row: (g * 2^sg, h * 2^sh) as
+// int64, with the exponents chosen so that a sum over all rows of a tree
+// fits in int64.
+using GH = longlong2;
+
 // A node's row segment in the compact buffers of its depth (buffer = depth%2).
 struct NodeSeg {
   int64_t start;
@@ -172,10 +177,10 @@ hipError_t launch_load_codes(hipStream_t st, const void *src, int is_u16,
 hipError_t launch_get_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
                             int64_t n, int32_t F, uint8_t *dst);
 hipError_t launch_quantize(hipStream_t st, const double *g, const double *h,
-                           int64_t n, double g_mul, double h_mul, int2 *ghq);
+                           int64_t n, double g_mul, double h_mul, GH *ghq);
 hipError_t launch_grad_hess(hipStream_t st, const double *F, const uint8_t *y,
                             int64_t n, double w0, double w1, double g_mul,
-                            double h_mul, int2 *ghq);
+                            double h_mul, GH *ghq);
 hipError_t launch_grad_hess_f64(hipStream_t st, const double *F,
                                 const uint8_t *y, int64_t n, double w0,
                                 double w1, double *g, double *h);
@@ -200,8 +205,8 @@ hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
 hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               const int32_t *feat, int32_t F_sel,
                               const int32_t *rows32, const int64_t *rows64,
-                              int64_t m, const int2 *ghq, uint8_t *codes_c,
-                              int64_t ld_c, int2 *gh_c, int32_t *rid_c,
+                              int64_t m, const GH *ghq, uint8_t *codes_c,
+                              int64_t ld_c, GH *gh_c, int32_t *rid_c,
                               int64_t pad_to, NodeSeg *segs, int32_t *hist_node);
 // Root gather in two parts for a boosting round: the codes (when the rows are
 // known) and the fixed-point (g, h) with the root segment (when F is).
@@ -210,7 +215,7 @@ hipError_t launch_gather_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
                                int64_t m, uint8_t *codes_c, int64_t ld_c, int64_t pad_to);
 hipError_t launch_gather_gh(hipStream_t st, const double *F, const uint8_t *y,
                             const int32_t *rows32, int64_t m, double w0, double w1,
-                            double g_mul, double h_mul, int2 *gh_c, int64_t pad_to,
+                            double g_mul, double h_mul, GH *gh_c, int64_t pad_to,
                             NodeSeg *segs, int32_t *hist_node,
                             const LevelPlan *plan_src = nullptr,
                             LevelPlan *plan_dst = nullptr);
@@ -218,7 +223,7 @@ hipError_t launch_gather_gh(hipStream_t st, const double *F, const uint8_t *y,
 // argument (blocks, tasks or parents) is an upper bound, and blocks loop
 // over the work with a grid stride, so any bound >= 1 gives the same result.
 hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
-                       const int2 *gh_c, const HistTask *tasks,
+                       const GH *gh_c, const HistTask *tasks,
                        const LevelPlan *plan, int32_t max_tasks,
                        const int32_t *hist_node, const int32_t *hist_begin,
                        const NodeSeg *segs,
@@ -239,7 +244,7 @@ hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
                              int32_t max_tiles, int32_t part_rows, int32_t *tile_left);
 hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                uint8_t *codes_dst, int64_t ld_c,
-                               const int2 *gh_src, int2 *gh_dst,
+                               const GH *gh_src, GH *gh_dst,
                                const int32_t *rid_src, int32_t *rid_dst,
                                const PartParent *parents,
                                const PartTile *tiles, const LevelPlan *plan,

@@ -2,10 +2,10 @@
 //
 // Layouts in HBM
 //   codes     feature-major uint8 [F][ld], ld a multiple of 256, zero padded
-//   ghq       int2 [n]: gradient and hessian of each row in 32-bit fixed
+//   ghq       GH [n]: gradient and hessian of each row in 64-bit fixed
 //             point (g*2^sg, h*2^sh), rebuilt every boosting round
 //   compact   per tree, two ping-pong sets of (codes_c [F_sel][ld_c] uint8,
-//             gh_c int2 [ld_c], rid_c int32 [ld_c]); every node's rows are a
+//             gh_c GH [ld_c], rid_c int32 [ld_c]); every node's rows are a
 //             contiguous segment of the set of its depth's parity
 //   pool      per node [F_sel][256 bins][g,h] int64 fixed-point sums
 //
@@ -245,14 +245,14 @@ __global__ __launch_bounds__(256) void k_quantize(const double *__restrict__ g,
                                                   const double *__restrict__ h,
                                                   int64_t n, double g_mul,
                                                   double h_mul,
-                                                  int2 *__restrict__ ghq) {
+                                                  GH *__restrict__ ghq) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  ghq[i] = make_int2(__double2int_rn(g[i] * g_mul), __double2int_rn(h[i] * h_mul));
+  ghq[i] = make_longlong2(__double2ll_rn(g[i] * g_mul), __double2ll_rn(h[i] * h_mul));
 }
 
 hipError_t launch_quantize(hipStream_t st, const double *g, const double *h,
-                           int64_t n, double g_mul, double h_mul, int2 *ghq) {
+                           int64_t n, double g_mul, double h_mul, GH *ghq) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_quantize, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                      st, g, h, n, g_mul, h_mul, ghq);
@@ -273,18 +273,18 @@ __global__ __launch_bounds__(256) void k_grad_hess(const double *__restrict__ F,
                                                    const uint8_t *__restrict__ y,
                                                    int64_t n, double w0, double w1,
                                                    double g_mul, double h_mul,
-                                                   int2 *__restrict__ ghq) {
+                                                   GH *__restrict__ ghq) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int yi = y[i];
   double g, h;
   logistic_gh(F[i], (double)yi, yi ? w1 : w0, g, h);
-  ghq[i] = make_int2(__double2int_rn(g * g_mul), __double2int_rn(h * h_mul));
+  ghq[i] = make_longlong2(__double2ll_rn(g * g_mul), __double2ll_rn(h * h_mul));
 }
 
 hipError_t launch_grad_hess(hipStream_t st, const double *F, const uint8_t *y,
                             int64_t n, double w0, double w1, double g_mul,
-                            double h_mul, int2 *ghq) {
+                            double h_mul, GH *ghq) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_grad_hess, dim3((unsigned)((n + 255) / 256)), dim3(256),
                      0, st, F, y, n, w0, w1, g_mul, h_mul, ghq);
@@ -402,8 +402,8 @@ int64_t sort_rows_flag_bytes(int64_t n) {
 __global__ __launch_bounds__(256) void k_gather_root(
     const uint8_t *__restrict__ codes, int64_t ld, const int32_t *__restrict__ feat,
     int32_t F_sel, const int32_t *__restrict__ rows32,
-    const int64_t *__restrict__ rows64, int64_t m, const int2 *__restrict__ ghq,
-    uint8_t *__restrict__ codes_c, int64_t ld_c, int2 *__restrict__ gh_c,
+    const int64_t *__restrict__ rows64, int64_t m, const GH *__restrict__ ghq,
+    uint8_t *__restrict__ codes_c, int64_t ld_c, GH *__restrict__ gh_c,
     int32_t *__restrict__ rid_c, int64_t pad_to, NodeSeg *__restrict__ segs,
     int32_t *__restrict__ hist_node) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -425,7 +425,7 @@ __global__ __launch_bounds__(256) void k_gather_root(
   for (int k = 0; k < 4; ++k) {
     ok[k] = (k0 + k) < m;
     r[k] = ok[k] ? (rows32 ? rows32[k0 + k] : (int32_t)rows64[k0 + k]) : 0;
-    gh_c[k0 + k] = ok[k] ? ghq[r[k]] : make_int2(0, 0);
+    gh_c[k0 + k] = ok[k] ? ghq[r[k]] : make_longlong2(0, 0);
     if (rid_c) rid_c[k0 + k] = ok[k] ? r[k] : -1;
   }
   for (int32_t f = 0; f < F_sel; ++f) {
@@ -469,7 +469,7 @@ __global__ __launch_bounds__(256) void k_gather_codes(
 __global__ __launch_bounds__(256) void k_gather_gh(
     const double *__restrict__ F, const uint8_t *__restrict__ y,
     const int32_t *__restrict__ rows32, int64_t m, double w0, double w1, double g_mul,
-    double h_mul, int2 *__restrict__ gh_c, int64_t pad_to, NodeSeg *__restrict__ segs,
+    double h_mul, GH *__restrict__ gh_c, int64_t pad_to, NodeSeg *__restrict__ segs,
     int32_t *__restrict__ hist_node, const LevelPlan *__restrict__ plan_src,
     LevelPlan *__restrict__ plan_dst) {
   const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -484,13 +484,13 @@ __global__ __launch_bounds__(256) void k_gather_gh(
     hist_node[0] = 0;
   }
   if (k >= pad_to) return;
-  int2 q = make_int2(0, 0);
+  GH q = make_longlong2(0, 0);
   if (k < m) {
     const int32_t i = rows32[k];
     const int yi = y[i];
     double g, h;
     logistic_gh(F[i], (double)yi, yi ? w1 : w0, g, h);
-    q = make_int2(__double2int_rn(g * g_mul), __double2int_rn(h * h_mul));
+    q = make_longlong2(__double2ll_rn(g * g_mul), __double2ll_rn(h * h_mul));
   }
   gh_c[k] = q;
 }
@@ -507,7 +507,7 @@ hipError_t launch_gather_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
 
 hipError_t launch_gather_gh(hipStream_t st, const double *F, const uint8_t *y,
                             const int32_t *rows32, int64_t m, double w0, double w1,
-                            double g_mul, double h_mul, int2 *gh_c, int64_t pad_to,
+                            double g_mul, double h_mul, GH *gh_c, int64_t pad_to,
                             NodeSeg *segs, int32_t *hist_node, const LevelPlan *plan_src,
                             LevelPlan *plan_dst) {
   if (pad_to <= 0) return hipSuccess;
@@ -520,8 +520,8 @@ hipError_t launch_gather_gh(hipStream_t st, const double *F, const uint8_t *y,
 hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               const int32_t *feat, int32_t F_sel,
                               const int32_t *rows32, const int64_t *rows64,
-                              int64_t m, const int2 *ghq, uint8_t *codes_c,
-                              int64_t ld_c, int2 *gh_c, int32_t *rid_c,
+                              int64_t m, const GH *ghq, uint8_t *codes_c,
+                              int64_t ld_c, GH *gh_c, int32_t *rid_c,
                               int64_t pad_to, NodeSeg *segs, int32_t *hist_node) {
   const int64_t threads = (pad_to + 3) / 4;
   if (threads <= 0) return hipSuccess;
@@ -591,7 +591,7 @@ __device__ __forceinline__ int32_t hist_tasks_with_rows(const int32_t *__restric
 template <int FC, int C>
 __device__ __forceinline__ void hist_item(
     unsigned long long *lh, const uint8_t *__restrict__ codes_c, int64_t ld_c,
-    const int2 *__restrict__ gh_c, const HistTask task, int32_t ti, int chunk,
+    const GH *__restrict__ gh_c, const HistTask task, int32_t ti, int chunk,
     const int32_t *__restrict__ hist_node, const int32_t *__restrict__ hist_begin,
     const NodeSeg *__restrict__ segs,
     const int32_t *__restrict__ nb_sel, const int32_t *__restrict__ hot_sel,
@@ -626,10 +626,13 @@ __device__ __forceinline__ void hist_item(
     const int64_t row = g << 4;
     // Every load of the step first: (g,h) of the 16 rows, then each
     // feature's 16 codes.
-    const int4 *gp = reinterpret_cast<const int4 *>(gh_c + row);
-    int4 ghv[kHistRows / 2];
+    long long gq[kHistRows], hq[kHistRows];
 #pragma unroll
-    for (int q = 0; q < kHistRows / 2; ++q) ghv[q] = gp[q];
+    for (int q = 0; q < kHistRows; ++q) {
+      const GH v = gh_c[row + q];
+      gq[q] = v.x;
+      hq[q] = v.y;
+    }
     uint4 cv[FC];
 #pragma unroll
     for (int u = 0; u < FC; ++u)
@@ -638,14 +641,6 @@ __device__ __forceinline__ void hist_item(
     // node's first and last groups.  Rows outside add zero.
     const int klo = (int)max((int64_t)0, min((int64_t)kHistRows, r0 - row));
     const int khi = (int)max((int64_t)0, min((int64_t)kHistRows, r1 - row));
-    int gq[kHistRows], hq[kHistRows];
-#pragma unroll
-    for (int q = 0; q < kHistRows / 2; ++q) {
-      gq[2 * q] = ghv[q].x;
-      hq[2 * q] = ghv[q].y;
-      gq[2 * q + 1] = ghv[q].z;
-      hq[2 * q + 1] = ghv[q].w;
-    }
     if (klo != 0 || khi != kHistRows) {
 #pragma unroll
       for (int k = 0; k < kHistRows; ++k) {
@@ -665,9 +660,9 @@ __device__ __forceinline__ void hist_item(
 #pragma unroll
           for (int k = 0; k < kHistRows; ++k) {
             const uint32_t bin = min((cw[k >> 2] >> (8 * (k & 3))) & 255u, lim[u]);
-            __hip_atomic_fetch_add(hf + bin * C, (unsigned long long)(long long)gq[k],
+            __hip_atomic_fetch_add(hf + bin * C, (unsigned long long)gq[k],
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            __hip_atomic_fetch_add(hf + (kBins + bin) * C, (unsigned long long)(long long)hq[k],
+            __hip_atomic_fetch_add(hf + (kBins + bin) * C, (unsigned long long)hq[k],
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           }
         } else {
@@ -680,9 +675,9 @@ __device__ __forceinline__ void hist_item(
               ag[u] += gq[k];
               ah[u] += hq[k];
             } else {
-              __hip_atomic_fetch_add(hf + bin * C, (unsigned long long)(long long)gq[k],
+              __hip_atomic_fetch_add(hf + bin * C, (unsigned long long)gq[k],
                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-              __hip_atomic_fetch_add(hf + (kBins + bin) * C, (unsigned long long)(long long)hq[k],
+              __hip_atomic_fetch_add(hf + (kBins + bin) * C, (unsigned long long)hq[k],
                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
           }
@@ -729,7 +724,7 @@ __device__ __forceinline__ void hist_item(
 template <int FC, int C>
 __global__ __launch_bounds__(kHistBlock) void k_hist(
     const uint8_t *__restrict__ codes_c, int64_t ld_c,
-    const int2 *__restrict__ gh_c, const HistTask *__restrict__ tasks,
+    const GH *__restrict__ gh_c, const HistTask *__restrict__ tasks,
     const LevelPlan *__restrict__ plan, const int32_t *__restrict__ hist_node,
     const int32_t *__restrict__ hist_begin,
     const NodeSeg *__restrict__ segs, const int32_t *__restrict__ nb_sel,
@@ -804,7 +799,7 @@ int hist_blocks(int32_t n_tasks, int32_t nchunks) {
 }
 
 hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
-                       const int2 *gh_c, const HistTask *tasks,
+                       const GH *gh_c, const HistTask *tasks,
                        const LevelPlan *plan, int32_t max_tasks,
                        const int32_t *hist_node, const int32_t *hist_begin,
                        const NodeSeg *segs,
@@ -980,7 +975,7 @@ template <int R>
 __global__ __launch_bounds__(kPartBlock) __attribute__((amdgpu_waves_per_eu(ScatterWaves<R>::value)))
 void k_part_scatter(
     const uint8_t *__restrict__ codes_src, uint8_t *__restrict__ codes_dst,
-    int64_t ld_c, const int2 *__restrict__ gh_src, int2 *__restrict__ gh_dst,
+    int64_t ld_c, const GH *__restrict__ gh_src, GH *__restrict__ gh_dst,
     const int32_t *__restrict__ rid_src, int32_t *__restrict__ rid_dst,
     const PartParent *__restrict__ parents, const PartTile *__restrict__ tiles,
     const LevelPlan *__restrict__ plan, const int32_t *__restrict__ tile_begin,
@@ -1216,7 +1211,7 @@ void k_part_scatter(
 
 hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                uint8_t *codes_dst, int64_t ld_c,
-                               const int2 *gh_src, int2 *gh_dst,
+                               const GH *gh_src, GH *gh_dst,
                                const int32_t *rid_src, int32_t *rid_dst,
                                const PartParent *parents,
                                const PartTile *tiles, const LevelPlan *plan,

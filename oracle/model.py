@@ -40,7 +40,7 @@ def lib():
                                           ctypes.c_int, P]
         L.oracle_build_tree_leafwise.argtypes = [
             P, ctypes.c_int, i64, i32, P, P, P, i64, P, i32, i32, i32, i32,
-            f64, P, i32, f64, f64, P, P, P, P, P, P, P, P, P]
+            f64, P, i32, f64, f64, P, P, P, P, P, P, P, P, P, P, P, P]
         L.oracle_predict_tree.argtypes = [P, ctypes.c_int, i64, i32, P, P, P, P,
                                           P, P]
         L.oracle_predict_all_trees.argtypes = [P, ctypes.c_int, i64, i32, P, P,
@@ -62,35 +62,47 @@ def _p(a):
 # Binning (est:2073-2189)
 # --------------------------------------------------------------------------
 
-def build_bin_edges(X, n_bins):
+def _column_edges(col, n_bins):
+    """One feature of ``_build_bin_edges`` (est:2092-2133): (edges, count,
+    has_nan)."""
+    has_nan = np.any(np.isnan(col))
+    if has_nan:
+        col_clean = col[~np.isnan(col)]
+        if len(col_clean) == 0:
+            return np.array([0.0, 1.0]), 1, True
+    else:
+        col_clean = col
+    n_unique = len(np.unique(col_clean))
+    max_numeric = n_bins - (1 if has_nan else 0)
+    if n_unique <= max_numeric:
+        e = np.sort(np.unique(col_clean))
+    else:
+        q = np.linspace(0, 1, min(max_numeric + 1, n_unique))
+        e = np.unique(np.percentile(col_clean, q * 100))
+    e = np.append(e, e[-1] + 1e-8)
+    return e, len(e) - 1 + (1 if has_nan else 0), has_nan
+
+
+def build_bin_edges(X, n_bins, threads=1):
     """``_build_bin_edges`` without categorical or weighted-quantile branches
-    (est:2073-2141).  Returns (edges_2d, bin_counts, nan_bin_id)."""
-    edges = []
+    (est:2073-2141).  Returns (edges_2d, bin_counts, nan_bin_id).  With
+    ``threads`` > 1 the columns are processed concurrently (each column's
+    NumPy calls are unchanged, so the result is the same)."""
     F = X.shape[1]
     bin_counts = np.zeros(F, dtype=np.int32)
     nan_bin_id = np.full(F, -1, dtype=np.int32)
-    for j in range(F):
-        col = X[:, j]
-        has_nan = np.any(np.isnan(col))
+    if threads > 1:
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(threads) as pool:
+            per = list(pool.map(lambda j: _column_edges(X[:, j], n_bins), range(F)))
+    else:
+        per = [_column_edges(X[:, j], n_bins) for j in range(F)]
+    edges = []
+    for j, (e, count, has_nan) in enumerate(per):
+        edges.append(e)
+        bin_counts[j] = count
         if has_nan:
             nan_bin_id[j] = 0
-            col_clean = col[~np.isnan(col)]
-            if len(col_clean) == 0:
-                edges.append(np.array([0.0, 1.0]))
-                bin_counts[j] = 1
-                continue
-        else:
-            col_clean = col
-        n_unique = len(np.unique(col_clean))
-        max_numeric = n_bins - (1 if has_nan else 0)
-        if n_unique <= max_numeric:
-            e = np.sort(np.unique(col_clean))
-        else:
-            q = np.linspace(0, 1, min(max_numeric + 1, n_unique))
-            e = np.unique(np.percentile(col_clean, q * 100))
-        e = np.append(e, e[-1] + 1e-8)
-        edges.append(e)
-        bin_counts[j] = len(e) - 1 + (1 if has_nan else 0)
     max_b = int(np.max(bin_counts)) + 1
     edges_2d = np.zeros((F, max_b), dtype=np.float64)
     for j, e in enumerate(edges):
@@ -136,9 +148,19 @@ def bin_features(X, edges_2d, bin_counts, nan_bin_id, strategy):
 
 def build_tree(X_bin, grad, hess, sample_indices, feature_indices, max_leaves,
                max_depth, min_samples_leaf, min_child_weight, bin_counts,
-               max_bins, reg_lambda, gamma, trace=False):
+               max_bins, reg_lambda, gamma, trace=False, forced=None,
+               forced_pops=None):
     """``_build_tree_leafwise`` (est:517-823); returns the reference 7-tuple,
-    plus (partition counts per split, number of pops) when ``trace``."""
+    plus (partition counts per split, number of pops) when ``trace``.
+
+    ``forced`` ({node id: (feature, bin)}) replaces the argmax of those
+    nodes' split searches by the given candidate (with the gain this builder
+    computes for it); a tie-following comparison uses it to adopt the other
+    builder's choice at a certified gain tie.  ``forced_pops`` ({split
+    index s: node id}) makes the pop that would make split s take that node
+    instead of the max-gain candidate (the other builder's order where two
+    nodes' gains tie).  ValueError when a forced split or pop is not a
+    candidate."""
     X_bin = np.ascontiguousarray(X_bin)
     u16 = int(X_bin.dtype == np.uint16)
     assert X_bin.dtype in (np.uint8, np.uint16)
@@ -158,12 +180,27 @@ def build_tree(X_bin, grad, hess, sample_indices, feature_indices, max_leaves,
     nc = np.zeros(1, np.int32)
     tc = np.zeros(2 * max_leaves + 2, np.int64)
     tp = np.zeros(1, np.int32)
+    ff = fb = None
+    if forced:
+        ff = np.full(M, -1, np.int32)
+        fb = np.zeros(M, np.int32)
+        for node, (f, b) in forced.items():
+            ff[int(node)] = int(f)
+            fb[int(node)] = int(b)
+    fp = None
+    if forced_pops:
+        fp = np.full(max(1, max_leaves), -1, np.int32)
+        for k, node in forced_pops.items():
+            fp[int(k)] = int(node)
     rc = lib().oracle_build_tree_leafwise(
         _p(X_bin), u16, n, F, _p(grad), _p(hess), _p(si), len(si), _p(fi),
         len(fi), int(max_leaves), int(max_depth), int(min_samples_leaf),
         float(min_child_weight), _p(bc), int(max_bins), float(reg_lambda),
         float(gamma), _p(tf), _p(tt), _p(tv), _p(tl), _p(tr), _p(nc), _p(sg),
-        _p(tc), _p(tp))
+        _p(tc), _p(tp), None if ff is None else _p(ff), None if fb is None else _p(fb),
+        None if fp is None else _p(fp))
+    if rc == 2:
+        raise ValueError(f"forced split or pop is not a candidate: {forced} {forced_pops}")
     if rc != 0:
         raise MemoryError("oracle tree builder allocation failed")
     lib().oracle_post_prune(_p(tf), _p(tl), _p(tr), _p(sg), float(gamma),
@@ -222,6 +259,30 @@ def predict_all_trees(X_bin, packed, n_trees, lr):
 
 
 # --------------------------------------------------------------------------
+# Binary logistic loss (est:2861, 2873-2874, 2320-2325, 3335)
+# --------------------------------------------------------------------------
+
+def binary_proba(F):
+    """p = 1 / (1 + exp(-clip(F, -500, 500))) (est:2861, est:3335)."""
+    return 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
+
+
+def binary_grad_hess(F, y, w, grad, hess):
+    """grad = w (p - y), hess = w p (1 - p) into the given buffers
+    (est:2861, 2873-2874)."""
+    p = binary_proba(F)
+    grad[:] = w * (p - y)
+    hess[:] = w * p * (1.0 - p)
+
+
+def binary_logloss(y, F):
+    """``_compute_logloss`` (est:2320-2325): unweighted mean of the log-loss
+    of p clipped to [1e-15, 1 - 1e-15]."""
+    pc = np.clip(binary_proba(F), 1e-15, 1 - 1e-15)
+    return -np.mean(y * np.log(pc) + (1 - y) * np.log(1 - pc))
+
+
+# --------------------------------------------------------------------------
 # Estimator restatement
 # --------------------------------------------------------------------------
 
@@ -235,7 +296,7 @@ class OracleGBM:
                  min_samples_leaf=5, min_child_weight="auto", gamma="auto",
                  subsample="auto", colsample_bytree="auto",
                  class_weight="balanced_sqrt", max_leaves=31,
-                 binning_strategy="auto", random_state=None):
+                 binning_strategy="auto", random_state=None, edge_threads=1):
         self.binning_strategy_init = binning_strategy
         self.n_estimators_init = n_estimators
         self.max_depth_init = max_depth
@@ -250,6 +311,7 @@ class OracleGBM:
         self.class_weight = class_weight
         self.max_leaves = max_leaves
         self.random_state = random_state
+        self.edge_threads = edge_threads  # columns of the edge pass run concurrently
         self.n_estimators = 100 if n_estimators == "auto" else n_estimators
         self.max_depth = 5 if max_depth == "auto" else max_depth
         self.learning_rate = 0.1 if learning_rate == "auto" else learning_rate
@@ -332,11 +394,16 @@ class OracleGBM:
             w[y == k] = w_k
         return w
 
-    def fit(self, X, y, max_rounds=None, round_callback=None):
+    def fit(self, X, y, max_rounds=None, round_callback=None, tree_hook=None):
         """est:3070-3271 then est:2825-2944.  ``max_rounds`` stops the
         boosting loop early (used to time a bounded CPU sample);
         ``round_callback(m, grad, hess, sample_idx, feat_idx, tree)`` sees
-        each round's tree-builder inputs and output."""
+        each round's tree-builder inputs and output.  ``tree_hook`` (same
+        arguments; with the class index after ``m`` for multiclass) returns
+        the tree the round keeps: a
+        tie-following comparison returns this builder's tree rebuilt with
+        the other builder's choices at certified gain ties, so the two fits
+        stay on one trajectory."""
         self.classes_ = np.unique(y)
         self.n_classes_ = len(self.classes_)
         assert self.n_classes_ >= 2, "oracle covers classification with 2+ classes"
@@ -351,14 +418,14 @@ class OracleGBM:
             X = X.astype(np.float64)
         self._adaptive(X)
         self.bin_edges, self.feature_bin_counts, self._nan_bin_id = \
-            build_bin_edges(X, self.n_bins)
+            build_bin_edges(X, self.n_bins, threads=self.edge_threads)
         self._max_bins = int(np.max(self.feature_bin_counts))
         X_bin = bin_features(X, self.bin_edges, self.feature_bin_counts,
                              self._nan_bin_id, self.binning_strategy)
         self.X_bin_ = X_bin
 
         if self._is_multiclass:
-            return self._fit_multiclass(X_bin, y, rng, max_rounds, round_callback)
+            return self._fit_multiclass(X_bin, y, rng, max_rounds, round_callback, tree_hook)
         n = len(y)
         F_cnt = X_bin.shape[1]
         w_init = self._class_weights(y)
@@ -376,9 +443,7 @@ class OracleGBM:
         import time as _time
         self.round_times_ = [_time.perf_counter()]
         for m in range(rounds):
-            p = 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
-            grad[:] = w * (p - y)
-            hess[:] = w * p * (1.0 - p)
+            binary_grad_hess(F, y, w, grad, hess)
             # est:2502-2517
             if self.subsample < 1.0:
                 rng.shuffle(all_rows)
@@ -395,12 +460,13 @@ class OracleGBM:
                               self.min_samples_leaf, self.min_child_weight,
                               self.feature_bin_counts, self._max_bins,
                               self.reg_lambda, self.gamma)
+            if tree_hook is not None:
+                tree = tree_hook(m, grad, hess, sample_idx, feat_idx, tree)
             if round_callback is not None:
                 round_callback(m, grad, hess, sample_idx, feat_idx, tree)
             self.trees.append(tree)
             F += self.learning_rate * predict_tree(X_bin, tree)
-            pc = np.clip(1.0 / (1.0 + np.exp(-np.clip(F, -500, 500))), 1e-15, 1 - 1e-15)
-            self.train_loss_history_.append(-np.mean(y * np.log(pc) + (1 - y) * np.log(1 - pc)))
+            self.train_loss_history_.append(binary_logloss(y, F))
             self.round_times_.append(_time.perf_counter())
         self.F_train_ = F
         self._packed = pack_trees(self.trees)
@@ -422,10 +488,11 @@ class OracleGBM:
         proba = np.clip(proba, 1e-15, 1 - 1e-15)
         return -np.mean(np.sum(y_onehot * np.log(proba), axis=1))
 
-    def _fit_multiclass(self, X_bin, y, rng, max_rounds, round_callback):
+    def _fit_multiclass(self, X_bin, y, rng, max_rounds, round_callback, tree_hook=None):
         """est:2949-3065 (gbdt, uniform sampling, no eval set): K trees per
         round from softmax gradients, one bagging draw shared by the K trees.
-        ``round_callback(m, k, grad, hess, sample_idx, feat_idx, tree)``."""
+        ``round_callback(m, k, grad, hess, sample_idx, feat_idx, tree)``;
+        ``tree_hook`` (same arguments) returns the tree the round keeps."""
         n = len(y)
         F_cnt = X_bin.shape[1]
         K = self.n_classes_
@@ -462,6 +529,8 @@ class OracleGBM:
                                   self.min_samples_leaf, self.min_child_weight,
                                   self.feature_bin_counts, self._max_bins,
                                   self.reg_lambda, self.gamma)
+                if tree_hook is not None:
+                    tree = tree_hook(m, k, grad_k, hess_k, sample_idx, feat_idx, tree)
                 if round_callback is not None:
                     round_callback(m, k, grad_k, hess_k, sample_idx, feat_idx, tree)
                 self.mc_trees[k].append(tree)
@@ -486,7 +555,7 @@ class OracleGBM:
             return self._softmax(F)
         F = predict_all_trees(X_bin, self._packed, len(self.trees),
                               self.learning_rate) + self.base_score_
-        proba = 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
+        proba = binary_proba(F)
         return np.column_stack([1 - proba, proba])
 
     def predict(self, X):

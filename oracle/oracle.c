@@ -25,6 +25,7 @@
 
 #define ORACLE_OK 0
 #define ORACLE_EALLOC 1
+#define ORACLE_EFORCE 2
 
 /* ------------------------------------------------------------------------ */
 /* Binning kernels                                                           */
@@ -153,12 +154,13 @@ static void build_hist(const void *xb, int u16, int32_t p, const double *grad,
 static void best_split(const double *hG, const double *hH, int64_t slot_stride,
                        int32_t max_bins, int32_t slot, const int32_t *feats,
                        int32_t n_sel, const int32_t *bin_counts, double mcw,
-                       double lam, double *out_gain, int32_t *out_feat,
-                       int32_t *out_bin)
+                       double lam, int32_t force_feat, int32_t force_bin,
+                       double *out_gain, int32_t *out_feat, int32_t *out_bin)
 {
     double best_gain = -1e9;
     int32_t best_feat = -1, best_bin = 0;
     int32_t jj;
+    int forced_found = 0;
     for (jj = 0; jj < n_sel; ++jj) {
         int32_t j = feats[jj];
         int32_t nb = bin_counts[j];
@@ -180,12 +182,26 @@ static void best_split(const double *hG, const double *hH, int64_t slot_stride,
             if (HL < mcw || HR < mcw) continue;
             gain = (GL * GL / (HL + lam) + GR * GR / (HR + lam)) -
                    Gt * Gt / (Ht + lam);
-            if (gain > best_gain) {
+            if (force_feat >= 0) {
+                if (j == force_feat && b == force_bin) {
+                    best_gain = gain;
+                    best_feat = j;
+                    best_bin = b;
+                    forced_found = 1;
+                }
+            } else if (gain > best_gain) {
                 best_gain = gain;
                 best_feat = j;
                 best_bin = b;
             }
         }
+    }
+    if (force_feat >= 0 && !forced_found) {
+        /* The forced split is not a candidate of this node (feature not
+         * selected, bin out of range or a min_child_weight violation). */
+        best_gain = -1e9;
+        best_feat = -2;
+        best_bin = 0;
     }
     *out_gain = best_gain;
     *out_feat = best_feat;
@@ -200,6 +216,21 @@ static void best_split(const double *hG, const double *hH, int64_t slot_stride,
  * partition counts (n_left, n_right) are appended to trace_counts[2*s..] and
  * the number of splits attempted (including min_samples_leaf rejections) is
  * written to *trace_pops.  Tests use it to check partitions.
+ *
+ * Optional forced splits (may be NULL; arrays of 2*max_leaves+2 indexed by
+ * node id, -1 = not forced): the split search of node v returns
+ * (force_feat[v], force_bin[v]) with the gain this builder computes for it,
+ * in place of the argmax.  Tests use it to follow the other builder's choice
+ * at a certified gain tie, so comparison can go on below that node.  A
+ * forced split that is not a candidate of its node fails the call with
+ * ORACLE_EFORCE.
+ *
+ * Optional forced pops (may be NULL; max_leaves entries indexed by the
+ * number of splits done, -1 = not forced): the pop that would make split s
+ * takes the active candidate of node force_pop[s] in place of the max-gain
+ * one (est:645-653), once.  Tests use it to follow the other builder's order
+ * where two nodes' gains tie.  A forced node that is not an active candidate
+ * with a split fails the call with ORACLE_EFORCE.
  */
 int oracle_build_tree_leafwise(
     const void *X_bin, int xbin_u16, int64_t n_rows, int32_t p,
@@ -209,7 +240,9 @@ int oracle_build_tree_leafwise(
     double mcw, const int32_t *bin_counts, int32_t max_bins, double lam,
     double gamma, int32_t *tf, int64_t *tt, double *tv, int32_t *tl,
     int32_t *tr, int32_t *node_count_out, double *sg,
-    int64_t *trace_counts, int32_t *trace_pops)
+    int64_t *trace_counts, int32_t *trace_pops,
+    const int32_t *force_feat, const int32_t *force_bin,
+    const int32_t *force_pop)
 {
     const int32_t max_nodes = max_leaves * 2 + 2;
     const int32_t MAX_C = max_leaves + 2;
@@ -227,6 +260,8 @@ int oracle_build_tree_leafwise(
     double g_root = 0.0, h_root = 0.0, root_val;
     double r_gain;
     int32_t r_feat, r_bin;
+    int rc = ORACLE_OK;
+    int32_t pop_forced_at = -1;
     (void)n_rows;
 
     for (i = 0; i < max_nodes; ++i) {
@@ -279,7 +314,12 @@ int oracle_build_tree_leafwise(
     build_hist(X_bin, xbin_u16, p, grad, hess, indices, 0, n_samples, feats,
                n_sel, bin_counts, hG, hH, slot_stride, max_bins, 0);
     best_split(hG, hH, slot_stride, max_bins, 0, feats, n_sel, bin_counts, mcw,
-               lam, &r_gain, &r_feat, &r_bin);
+               lam, force_feat ? force_feat[root_id] : -1,
+               force_bin ? force_bin[root_id] : 0, &r_gain, &r_feat, &r_bin);
+    if (r_feat == -2) {
+        rc = ORACLE_EFORCE;
+        goto done;
+    }
     c_node[0] = root_id;
     c_start[0] = 0;
     c_end[0] = n_samples;
@@ -304,10 +344,23 @@ int oracle_build_tree_leafwise(
         int32_t small_id, large_id, left_id, right_id;
         int32_t slot_small = -1, slot_large = -1, si, pass;
 
-        for (ci = 0; ci < MAX_C; ++ci) {
-            if (c_active[ci] && c_feat[ci] >= 0 && c_gain[ci] > best_gain) {
-                best_gain = c_gain[ci];
-                best_ci = ci;
+        if (force_pop && force_pop[n_splits_done] >= 0 &&
+            pop_forced_at != n_splits_done) {
+            pop_forced_at = n_splits_done;
+            for (ci = 0; ci < MAX_C; ++ci) {
+                if (c_active[ci] && c_node[ci] == force_pop[n_splits_done]) break;
+            }
+            if (ci == MAX_C || c_feat[ci] < 0 || !(c_gain[ci] > gamma)) {
+                rc = ORACLE_EFORCE;
+                goto done;
+            }
+            best_ci = ci;
+        } else {
+            for (ci = 0; ci < MAX_C; ++ci) {
+                if (c_active[ci] && c_feat[ci] >= 0 && c_gain[ci] > best_gain) {
+                    best_gain = c_gain[ci];
+                    best_ci = ci;
+                }
             }
         }
         if (best_ci < 0) break;
@@ -420,7 +473,14 @@ int oracle_build_tree_leafwise(
             can_split = (cn >= min_samples_leaf && hc >= mcw && new_depth < max_depth);
             if (can_split) {
                 best_split(hG, hH, slot_stride, max_bins, slot, feats, n_sel,
-                           bin_counts, mcw, lam, &cb_gain, &cb_feat, &cb_bin);
+                           bin_counts, mcw, lam,
+                           force_feat ? force_feat[cid] : -1,
+                           force_bin ? force_bin[cid] : 0,
+                           &cb_gain, &cb_feat, &cb_bin);
+                if (cb_feat == -2) {
+                    rc = ORACLE_EFORCE;
+                    goto done;
+                }
             }
             c_node[slot] = cid;
             c_start[slot] = cs;
@@ -448,7 +508,7 @@ done:
     free(indices); free(hG); free(hH); free(c_node); free(c_depth);
     free(c_feat); free(c_bin); free(c_start); free(c_end); free(c_gain);
     free(c_val); free(c_active);
-    return ORACLE_OK;
+    return rc;
 }
 
 /* Post-prune (est:827-841), restated for completeness; after leaf-wise growth

@@ -1,69 +1,100 @@
-"""Parity at the benchmark workloads' full sizes (bench.py:make_workload):
-1,000,000 x 28 (depth 6, 255 bins) and 10,000,000 x 50 (depth 8, 10
-columns 70% NaN), where the oracle still finishes a tree in seconds.
+"""Parity at the benchmark workloads' full sizes (bench.py:make_workload).
 
-* 1M x 28: the oracle's first rounds of the workload's fit, every tree
-  rebuilt by the engine from the oracle's gradients, rows and features
-  (identical, or a certified gain tie: tests/treecmp.py); the estimator's
-  own fit of the same rounds, which must give the oracle's losses (rtol
-  1e-9) and trees, and predict_proba within 1e-6.
-* 10M x 50: the estimator bins the matrix on the device (its codes are the
-  oracle's codes: test_gpu_parity.py::test_binning_bit_exact pins the
-  binning); one tree of the workload's shape from 5,000,000 rows and 35
-  features, engine against the oracle's tree builder on those codes.
+* dense_1m (1,000,000 x 28, 5% NaN, depth 6): the first 10 rounds of the
+  workload's fit.
+* imbalanced (284,807 x 30, 0.17% positives, balanced_sqrt) and sparse_hd
+  (100,000 x 100, 90% zeros, balanced_sqrt): the complete fits, 200 and 300
+  trees.
+* stress_10m (10,000,000 x 50, 10 columns 70% NaN, depth 8): bin edges and
+  codes of all 10M rows against the oracle's; the first two rounds of the
+  workload's fit; one depth-8 tree from 5M rows x 35 features; and the
+  500-tree fit scored on a fresh 10M-row batch, checked on its first 1M rows
+  (codes bit-exact, raw scores within 1e-12, predict_proba within 1e-6).
+
+Every fit compares each round in lockstep and end to end with the oracle,
+following certified gain ties (tests/fitcmp.py), then every round's loss
+and predict_proba.
 """
 import numpy as np
 import pytest
 
 import bench
+import fitcmp
 import treecmp
 from oracle import model as om
 from test_gpu_parity import _grad_hess
 
 pytestmark = pytest.mark.gpu
 
+_CACHE = {}
 
-def test_dense_1m_rounds_lockstep_and_fit(engine):
+
+def _workload(name, predict=False):
+    key = (name, predict)
+    if key not in _CACHE:
+        if name == "stress_10m":
+            _CACHE.clear()  # keep at most one 10M matrix in memory
+        _CACHE[key] = bench.make_workload(name, predict=predict)
+    return _CACHE[key]
+
+
+def _fit_and_follow(engine, name, n_estimators=None, eval_rows=200_000):
     from bsscl_gbm import HybridHistGBMNumbaV1_0_1
-    print("[case] dense_1m full size, 3 rounds", flush=True)
-    X, y, params = bench.make_workload("dense_1m")
-    params = dict(params, n_estimators=3)
-    rounds = []
-    ref = om.OracleGBM(**{k: v for k, v in params.items() if k != "verbose"})
-    ref.fit(X, y, round_callback=lambda m, g, h, si, fi, t: rounds.append((g.copy(), h.copy(), si, fi, t)))
-    Xb, bc = ref.X_bin_, ref.feature_bin_counts
-    engine.load_codes(0, Xb)
-    ties = 0
-    for g, h, si, fi, tree in rounds:
-        got = engine.build_tree(g, h, si, fi, ref.max_leaves, ref.max_depth,
-                                ref.min_samples_leaf, ref.min_child_weight, bc,
-                                ref._max_bins, ref.reg_lambda, ref.gamma)
-        ties += treecmp.compare(tree, got, Xb, g, h, si, bc, ref.reg_lambda) == "tie"
+    X, y, params = _workload(name)
+    if n_estimators is not None:
+        params = dict(params, n_estimators=n_estimators)
+    print(f"[case] {name} full size, {params['n_estimators']} rounds", flush=True)
     est = HybridHistGBMNumbaV1_0_1(**params).fit(X, y)
-    np.testing.assert_array_equal(est.bin_edges, ref.bin_edges)
-    diverged = None
-    for k in range(len(rounds)):
-        g, h, si, _, _ = rounds[k]
-        if treecmp.compare(ref.trees[k], est.trees[k], Xb, g, h, si, bc, ref.reg_lambda) == "tie":
-            diverged = k
-            break
-        np.testing.assert_allclose(est.train_loss_history_[k], ref.train_loss_history_[k],
-                                   rtol=1e-9)
-    print(f"[result] dense_1m: lockstep ties {ties}/{len(rounds)}, end-to-end "
-          f"{'identical' if diverged is None else f'tie at tree {diverged}'}", flush=True)
-    if diverged is None:
-        np.testing.assert_allclose(est.predict_proba(X[:200_000]), ref.predict_proba(X[:200_000]),
-                                   rtol=0, atol=1e-6)
+    ref, rep = fitcmp.follow_fit(engine, est, X, y, params)
+    print(rep.line(name), flush=True)
+    assert rep.rounds == params["n_estimators"]
+    fitcmp.assert_fit_equal(ref, est, X[:eval_rows])
+    return est, ref
+
+
+def test_dense_1m_rounds(engine):
+    _fit_and_follow(engine, "dense_1m", n_estimators=10)
+
+
+@pytest.mark.parametrize("name", ["imbalanced", "sparse_hd"])
+def test_workload_full_fit(engine, name):
+    est, ref = _fit_and_follow(engine, name)
+    if name == "imbalanced":
+        w0, w1 = est._class_weight_pair(_workload(name)[1])
+        print(f"[result] imbalanced class weights w0={w0:.6f} w1={w1:.6f}", flush=True)
+        assert abs(w1 - 7.31) < 0.01 and abs(w0 - 0.785) < 0.01
+    Xp, _, _ = bench.make_workload(name, predict=True)
+    np.testing.assert_allclose(est.predict_proba(Xp), ref.predict_proba(Xp), rtol=0, atol=1e-6)
+
+
+def test_stress_10m_binning(engine):
+    """Edges and codes of the whole 10M x 50 matrix equal the oracle's."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    from bsscl_gbm import estimator as est_mod
+    print("[case] stress_10m binning, 10M x 50", flush=True)
+    X, y, params = _workload("stress_10m")
+    est = HybridHistGBMNumbaV1_0_1(**dict(params, n_estimators=1)).fit(X, y)
+    e, bc, nid = om.build_bin_edges(X, 255, threads=16)
+    np.testing.assert_array_equal(est.bin_edges, e)
+    np.testing.assert_array_equal(est.feature_bin_counts, bc)
+    np.testing.assert_array_equal(est._nan_bin_id, nid)
+    want = om.bin_features(X, e, bc, nid, "hybrid")
+    got = est_mod._engine(0).get_codes(0, *X.shape)
+    np.testing.assert_array_equal(got, want)
+    print(f"[result] stress_10m binning: edges and {got.size} codes identical", flush=True)
+
+
+def test_stress_10m_rounds(engine):
+    _fit_and_follow(engine, "stress_10m", n_estimators=2, eval_rows=500_000)
 
 
 def test_stress_10m_tree(engine):
     from bsscl_gbm import HybridHistGBMNumbaV1_0_1
     from bsscl_gbm import estimator as est_mod
     print("[case] stress_10m full size, one tree from 5M rows x 35 features", flush=True)
-    X, y, params = bench.make_workload("stress_10m")
+    X, y, params = _workload("stress_10m")
     n, F = X.shape
     est = HybridHistGBMNumbaV1_0_1(**dict(params, n_estimators=1)).fit(X, y)
-    del X
     eng = est_mod._engine(0)  # the estimator's engine holds the codes in slot 0
     codes = eng.get_codes(0, n, F)
     bc = np.asarray(est.feature_bin_counts)
@@ -73,8 +104,42 @@ def test_stress_10m_tree(engine):
     feats = np.sort(rng.permutation(F)[:35]).astype(np.int32)
     args = (rows, feats, est.max_leaves, est.max_depth, est.min_samples_leaf,
             est.min_child_weight, bc, int(bc.max()), est.reg_lambda, 0.0)
-    ref = om.build_tree(codes, g, h, *args)
     got = eng.build_tree(g, h, *args)
-    verdict = treecmp.compare(ref, got, codes, g, h, rows, bc, est.reg_lambda)
-    print(f"[result] stress_10m tree: {verdict}, {got[5]} nodes", flush=True)
+    out = treecmp.follow(got, codes, g, h, *args)
+    print(f"[result] stress_10m tree: {got[5]} nodes, ties {out.ties}", flush=True)
     assert got[5] > 100
+
+
+def test_stress_10m_inference(engine):
+    """The workload's 500-tree fit, then predict_proba of a fresh 10M-row
+    batch (default_rng(5)), checked on its first 1M rows."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    from bsscl_gbm import estimator as est_mod
+    X, y, params = _workload("stress_10m")
+    print(f"[case] stress_10m inference: {params['n_estimators']}-tree fit", flush=True)
+    est = HybridHistGBMNumbaV1_0_1(**params).fit(X, y)
+    assert len(est.trees) == 500
+    Xp, _, _ = _workload("stress_10m", predict=True)
+    n, F = Xp.shape
+    p = est.predict_proba(Xp)
+    assert p.shape == (n, 2) and np.all(np.isfinite(p))
+    eng = est_mod._engine(0)
+    k = 1_000_000
+    codes = eng.get_codes(1, n, F)[:k]
+    want = om.bin_features(Xp[:k], est.bin_edges, est.feature_bin_counts, est._nan_bin_id,
+                           "hybrid")
+    # A NaN feature's value above its training maximum gets the reference
+    # code bin_counts = 256 (uint16 codes, est:2163-2166); every threshold
+    # there is <= 254, so the engine stores it as 255.
+    assert want.max() <= 256
+    np.testing.assert_array_equal(codes, np.minimum(want, 255))
+    packed = {"features": est._packed_features, "thresholds": est._packed_thresholds,
+              "values": est._packed_values, "left": est._packed_left,
+              "right": est._packed_right, "offsets": est._tree_offsets}
+    F_dev = eng.predict(1, n, packed, len(est.trees), est.learning_rate)
+    F_ref = om.predict_all_trees(want, packed, len(est.trees), est.learning_rate)
+    np.testing.assert_allclose(F_dev[:k], F_ref, rtol=0, atol=1e-12)
+    p_ref = 1.0 / (1.0 + np.exp(-np.clip(F_ref + est.base_score_, -500, 500)))
+    np.testing.assert_allclose(p[:k, 1], p_ref, rtol=0, atol=1e-6)
+    print(f"[result] stress_10m inference: 500 trees over {n} rows; first {k} rows: codes "
+          f"identical, max |dF| {np.max(np.abs(F_dev[:k] - F_ref)):.3g}", flush=True)

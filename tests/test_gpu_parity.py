@@ -2,11 +2,14 @@
 
 Bars: bin codes and partitions bit-exact; histogram sums within
 |d| <= 1e-5 * max(|ref|, sum_bin |g|); splits identical except gain ties
-within 1e-7 relative (tests/treecmp.py); predictions within 1e-6.
+within 1e-7 relative, which are followed to the end of the tree
+(tests/treecmp.py); every training loss within 1e-9 relative and
+predict_proba within 1e-6 (tests/fitcmp.py).
 """
 import numpy as np
 import pytest
 
+import fitcmp
 import treecmp
 from conftest import make_data
 from oracle import model as om
@@ -122,8 +125,11 @@ def test_histogram_and_split(engine, n, F, nan, weights):
         np.testing.assert_allclose(gain, tree[6][0], rtol=1e-7)
 
 
-@pytest.mark.parametrize("m,bin_", [(1, 5), (4097, 100), (123457, 30), (60000, 0), (60000, 254)])
+@pytest.mark.parametrize("m,bin_", [(1, 5), (4097, 100), (123457, 30), (60000, 0), (60000, 254),
+                                    (1_200_001, 77), (2_097_151, 200)])
 def test_partition_stable_and_exact(engine, m, bin_):
+    """Sizes from 1 row to 2,097,151 cover the 1024-, 2048- and 4096-row
+    partition tiles (chosen by the in-bag row count)."""
     _announce(f"partition m={m} bin={bin_}")
     rng = np.random.default_rng(m)
     n, F = max(m * 2, 10), 3
@@ -147,9 +153,10 @@ def _lockstep_case(engine, n, F, seed, n_bins, max_leaves, max_depth, msl, mcw,
     rows = rng.permutation(n)[: max(1, int(sub * n))].astype(np.int64)
     feats = np.sort(rng.permutation(F)[: max(1, int(col * F))]).astype(np.int32)
     args = (rows, feats, max_leaves, max_depth, msl, mcw, bc, int(bc.max()), lam, 0.0)
-    ref = om.build_tree(codes, g, h, *args)
     got = engine.build_tree(g, h, *args)
-    return treecmp.compare(ref, got, codes, g, h, rows, bc, lam)
+    out = treecmp.follow(got, codes, g, h, *args)
+    print(f"[result] lockstep n={n} F={F} seed={seed}: {got[5]} nodes, ties {out.ties}", flush=True)
+    return out
 
 
 @pytest.mark.parametrize("n", [1, 2, 3, 5, 64, 1000, 4099])
@@ -197,6 +204,9 @@ def test_fisher_yates_device_equals_numpy_shuffle(engine, n, form, monkeypatch):
     dict(n=30000, F=12, seed=9, n_bins=255, max_leaves=63, max_depth=8, msl=5, mcw=1.0, lam=1.0, nan=0.7),
     dict(n=5000, F=5, seed=10, n_bins=64, max_leaves=31, max_depth=1, msl=5, mcw=1.0, lam=1.0),
     dict(n=60000, F=30, seed=11, n_bins=255, max_leaves=255, max_depth=12, msl=2, mcw=0.5, lam=1.0, nan=0.05),
+    # 1.5M in-bag rows: the 2048-row partition tiles.
+    dict(n=2_000_000, F=8, seed=12, n_bins=255, max_leaves=63, max_depth=6, msl=5, mcw=3.0, lam=1.0,
+         nan=0.05, sub=0.75, col=1.0),
 ])
 def test_build_tree_lockstep(engine, case):
     _announce(f"lockstep {case}")
@@ -241,39 +251,18 @@ def _fit_case(name):
 @pytest.mark.parametrize("name", ["config1", "nan_imbalanced", "sparse"])
 def test_fit_lockstep_and_end_to_end(engine, name):
     """Every round of the oracle's fit, rebuilt by the engine from the same
-    gradients, rows and features, gives the same tree or a certified gain
-    tie.  The estimator's own fit then matches the oracle's trees up to the
-    first certified tie and, without one, predict_proba within 1e-6."""
+    gradients, rows and features (lockstep), and the estimator's own tree of
+    that round (end to end) equal the oracle's tree, following certified
+    gain ties (tests/fitcmp.py).  Then every round's training loss and
+    predict_proba match."""
     from bsscl_gbm import HybridHistGBMNumbaV1_0_1
     _announce(f"fit {name}")
     X, y, params = _fit_case(name)
-    rounds = []
-    ref = om.OracleGBM(**params)
-    ref.fit(X, y, round_callback=lambda m, g, h, si, fi, t: rounds.append((g.copy(), h.copy(), si, fi, t)))
-    Xb, bc = ref.X_bin_, ref.feature_bin_counts
-    engine.load_codes(0, Xb)
-    ties = 0
-    for g, h, si, fi, tree in rounds:
-        got = engine.build_tree(g, h, si, fi, ref.max_leaves, ref.max_depth,
-                                ref.min_samples_leaf, ref.min_child_weight, bc,
-                                ref._max_bins, ref.reg_lambda, ref.gamma)
-        ties += treecmp.compare(tree, got, Xb, g, h, si, bc, ref.reg_lambda) == "tie"
     est = HybridHistGBMNumbaV1_0_1(verbose=False, **params).fit(X, y)
-    np.testing.assert_array_equal(est.bin_edges, ref.bin_edges)
-    np.testing.assert_array_equal(est.feature_bin_counts, ref.feature_bin_counts)
-    assert est.base_score_ == ref.base_score_
-    assert len(ref.trees) == len(est.trees)
-    diverged = None
-    for k, (a, b) in enumerate(zip(ref.trees, est.trees)):
-        g, h, si, fi, _ = rounds[k]
-        if treecmp.compare(a, b, Xb, g, h, si, bc, ref.reg_lambda) == "tie":
-            diverged = k
-            break
-        np.testing.assert_allclose(est.train_loss_history_[k], ref.train_loss_history_[k], rtol=1e-9)
-    print(f"[result] {name}: lockstep ties {ties}/{len(rounds)}, end-to-end "
-          f"{'identical' if diverged is None else f'tie at tree {diverged}'}", flush=True)
-    if diverged is None:
-        np.testing.assert_allclose(est.predict_proba(X), ref.predict_proba(X), rtol=0, atol=1e-6)
+    ref, rep = fitcmp.follow_fit(engine, est, X, y, params)
+    print(rep.line(name), flush=True)
+    assert rep.rounds == params["n_estimators"]
+    fitcmp.assert_fit_equal(ref, est, X)
 
 
 def test_fit_device_replay_fallbacks_agree(engine, monkeypatch):

@@ -6,13 +6,14 @@ trees by the independent traversal; the K trees of a round share one
 bagging draw, which equals a fresh RandomState's shuffle stream; softmax
 gradients sum to zero over the classes of a row; the K-dependent parameter
 rules give hand-derived values.  GPU tests rebuild every oracle tree on the
-engine from the same inputs (identical or a certified gain tie) and compare
-the estimator's own fit and predict_proba with the oracle's.
+engine from the same inputs and compare the estimator's own trees, losses
+and predict_proba with the oracle's, following certified gain ties
+(tests/fitcmp.py).
 """
 import numpy as np
 import pytest
 
-import treecmp
+import fitcmp
 from oracle import model as om
 
 
@@ -96,35 +97,13 @@ def test_multiclass_lockstep_and_end_to_end(engine, K, n, nan):
     print(f"[case] multiclass K={K} n={n} nan={nan}", flush=True)
     X, y = _mc_data(n, 9, K, seed=K, nan_frac=nan)
     params = dict(n_estimators=4, max_depth=5, n_bins=255, random_state=5)
-    rounds = []
-    ref = om.OracleGBM(**params).fit(
-        X, y, round_callback=lambda m, k, g, h, si, fi, t: rounds.append((g.copy(), h.copy(), si, fi, t)))
-    Xb, bc = ref.X_bin_, ref.feature_bin_counts
-    engine.load_codes(0, Xb)
-    ties = 0
-    for g, h, si, fi, tree in rounds:
-        got = engine.build_tree(g, h, si, fi, ref.max_leaves, ref.max_depth,
-                                ref.min_samples_leaf, ref.min_child_weight, bc,
-                                ref._max_bins, ref.reg_lambda, ref.gamma)
-        ties += treecmp.compare(tree, got, Xb, g, h, si, bc, ref.reg_lambda) == "tie"
     est = HybridHistGBMNumbaV1_0_1(verbose=False, **params).fit(X, y)
-    np.testing.assert_array_equal(est.classes_, ref.classes_)
+    np.testing.assert_array_equal(est.classes_, np.unique(y))
     assert est._is_multiclass and len(est.mc_trees) == K
-    diverged = None
-    for m in range(params["n_estimators"]):
-        for k in range(K):
-            g, h, si, fi, _ = rounds[m * K + k]
-            if treecmp.compare(ref.mc_trees[k][m], est.mc_trees[k][m], Xb, g, h, si, bc,
-                               ref.reg_lambda) == "tie":
-                diverged = (m, k)
-                break
-        if diverged:
-            break
-        np.testing.assert_allclose(est.train_loss_history_[m], ref.train_loss_history_[m],
-                                   rtol=1e-9)
-    print(f"[result] multiclass K={K}: lockstep ties {ties}/{len(rounds)}, end-to-end "
-          f"{'identical' if diverged is None else f'tie at round/class {diverged}'}", flush=True)
-    if diverged is None:
-        Xp, _ = _mc_data(3000, 9, K, seed=100 + K, nan_frac=nan)
-        np.testing.assert_allclose(est.predict_proba(Xp), ref.predict_proba(Xp), rtol=0, atol=1e-6)
-        np.testing.assert_array_equal(est.predict(Xp), ref.predict(Xp))
+    ref, rep = fitcmp.follow_fit(engine, est, X, y, params)
+    print(rep.line(f"multiclass K={K}"), flush=True)
+    assert rep.rounds == params["n_estimators"]
+    assert len(rep.end_to_end_ties) == K * params["n_estimators"]
+    Xp, _ = _mc_data(3000, 9, K, seed=100 + K, nan_frac=nan)
+    fitcmp.assert_fit_equal(ref, est, Xp)
+    np.testing.assert_array_equal(est.predict(Xp), ref.predict(Xp))
