@@ -41,6 +41,7 @@ _SIGS = {
     "bsscl_boost_grad_hess": [_P, _P, _P],
     "bsscl_predict": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _P],
     "bsscl_predict_tree": [_P, _i32, _P, _P, _P, _P, _P, _i32, _P],
+    "bsscl_predict_noalloc": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _P],
     "bsscl_node_split": [_P, _P, _P, _P, _i64, _P, _i32, _P, _f64, _f64, _P, _P,
                          _P, _P, _P],
     "bsscl_partition": [_P, _P, _i64, _i32, _i32, _P, _P],
@@ -282,6 +283,19 @@ class Engine:
                                   ptr(l), ptr(r), ptr(o), int(n_trees),
                                   float(learning_rate), ptr(out)))
         return out
+
+    def predict_noalloc(self, slot, packed, n_trees, learning_rate, out_dev_ptr):
+        """bsscl_predict_noalloc: F of matrix `slot` into the device buffer at
+        address out_dev_ptr (float64, one value per row)."""
+        f = np.ascontiguousarray(packed["features"], np.int16)
+        t = np.ascontiguousarray(packed["thresholds"], np.int64)
+        v = np.ascontiguousarray(packed["values"], np.float64)
+        l = np.ascontiguousarray(packed["left"], np.int32)
+        r = np.ascontiguousarray(packed["right"], np.int32)
+        o = np.ascontiguousarray(packed["offsets"], np.int32)
+        check(lib().bsscl_predict_noalloc(self.handle, int(slot), ptr(f), ptr(t), ptr(v),
+                                          ptr(l), ptr(r), ptr(o), int(n_trees),
+                                          float(learning_rate), ctypes.c_void_p(int(out_dev_ptr))))
 
     def predict_tree(self, slot, n, tree):
         tf, tt, tv, tl, tr, nc, _ = tree

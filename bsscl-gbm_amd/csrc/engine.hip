@@ -32,6 +32,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -190,9 +191,58 @@ struct RoundSlot {
 
 using namespace bsscl;
 
+// ---------------------------------------------------------------------------
+// Fixed device scratch of bsscl_predict_noalloc: one call's packed tree
+// arrays and their traversal form, so that call allocates nothing.  Each GPU
+// holds its own copy of the array at its own address, looked up once per
+// device with that device current (scratch_for_device) and kept; host code
+// passes only those addresses to copies and kernels, never the symbol.
+// Calls on one GPU share its copy: overlapping calls race.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int32_t kNoAllocMaxNodes = 1 << 17;   // nodes of all trees of a call
+constexpr int32_t kNoAllocMaxTrees = 1 << 14;
+constexpr size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+constexpr size_t kScrNodes = 0;
+constexpr size_t kScrFeat = kScrNodes + align256(sizeof(TreeNodeDev) * kNoAllocMaxNodes);
+constexpr size_t kScrThr = kScrFeat + align256(sizeof(int16_t) * kNoAllocMaxNodes);
+constexpr size_t kScrVal = kScrThr + align256(sizeof(int64_t) * kNoAllocMaxNodes);
+constexpr size_t kScrLeft = kScrVal + align256(sizeof(double) * kNoAllocMaxNodes);
+constexpr size_t kScrRight = kScrLeft + align256(sizeof(int32_t) * kNoAllocMaxNodes);
+constexpr size_t kScrOffs = kScrRight + align256(sizeof(int32_t) * kNoAllocMaxNodes);
+constexpr size_t kScratchBytes = kScrOffs + align256(sizeof(int32_t) * (kNoAllocMaxTrees + 1));
+static_assert(kScratchBytes <= (7u << 20), "noalloc scratch stays under 7 MiB");
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+unsigned char *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on `device`, which must be current.
+int scratch_for_device(int device, unsigned char **out) {
+  if (device < 0 || device >= kMaxDevices)
+    return set_error(BSSCL_EDEVICE, "device index beyond the scratch table");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(BSSCL_EDEVICE, std::string("hipGetSymbolAddress(scratch): ") +
+                                          hipGetErrorString(e));
+    g_scratch_ptr[device] = static_cast<unsigned char *>(p);
+  }
+  *out = g_scratch_ptr[device];
+  return BSSCL_OK;
+}
+}  // namespace
+
 struct bsscl_engine {
   int32_t device = 0;
   hipStream_t st = nullptr;
+  unsigned char *scratch_p = nullptr;  // this device's copy of `scratch`
   // A boosting round's in-bag rows (Fisher-Yates, sort) are made on their
   // own stream, so the next round's rows are ready while this round's tree
   // is built; the tree stream waits on rows_ready of its slot.
@@ -1705,6 +1755,11 @@ int bsscl_engine_create(int32_t device, bsscl_engine **out) {
     E->n_cu = v;
   if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
     E->max_lds = (size_t)v;
+  if (scratch_for_device(device, &E->scratch_p) != BSSCL_OK) {
+    const std::string msg = bsscl_last_error();
+    bsscl_engine_destroy(E);
+    return set_error(BSSCL_EDEVICE, msg);
+  }
 
   *out = E;
   return BSSCL_OK;
@@ -2258,6 +2313,72 @@ int bsscl_predict(bsscl_engine *E, int32_t slot, const int16_t *features,
                         n_trees, learning_rate, E->out_d.p));
   HIPCHK(hipMemcpyAsync(out_F, E->out_d.p, (size_t)M.n * 8, hipMemcpyDeviceToHost, E->st));
   CHK(sync(E));
+  return BSSCL_OK;
+}
+
+int bsscl_predict_noalloc(bsscl_engine *E, int32_t slot, const int16_t *features,
+                          const int64_t *thresholds, const double *values,
+                          const int32_t *left, const int32_t *right,
+                          const int32_t *offsets, int32_t n_trees,
+                          double learning_rate, double *out_F_dev) {
+  if (!E || !out_F_dev ||
+      (n_trees > 0 && (!features || !thresholds || !values || !left || !right || !offsets)))
+    return set_error(BSSCL_EINVAL, "predict_noalloc: null argument");
+  CHK(check_matrix(E, slot));
+  if (n_trees < 0) return set_error(BSSCL_EINVAL, "predict_noalloc: negative tree count");
+  if (n_trees > kNoAllocMaxTrees)
+    return set_error(BSSCL_EINVAL, "predict_noalloc: " + std::to_string(n_trees) +
+                                       " trees exceed the fixed scratch (at most " +
+                                       std::to_string(kNoAllocMaxTrees) + ")");
+  const Matrix &M = E->mat[slot];
+  const int32_t total = n_trees > 0 ? offsets[n_trees] : 0;
+  if (n_trees > 0 && offsets[0] != 0) return set_error(BSSCL_EINVAL, "predict_noalloc: bad offsets");
+  if (total > kNoAllocMaxNodes)
+    return set_error(BSSCL_EINVAL, "predict_noalloc: " + std::to_string(total) +
+                                       " nodes exceed the fixed scratch (at most " +
+                                       std::to_string(kNoAllocMaxNodes) + ")");
+  // The same checks as bsscl_predict: every traversal stays in its tree.
+  for (int32_t t = 0; t < n_trees; ++t) {
+    const int32_t a = offsets[t], b = offsets[t + 1];
+    if (a < 0 || b <= a || b > total) return set_error(BSSCL_EINVAL, "predict_noalloc: bad offsets");
+    for (int32_t i = a; i < b; ++i) {
+      if (features[i] < 0) continue;
+      const int32_t l = left[i], r = right[i];
+      if (features[i] >= M.F || l < 0 || r < 0 || l >= b - a || r >= b - a || l <= i - a ||
+          r <= i - a)
+        return set_error(BSSCL_EINVAL, "predict_noalloc: malformed tree " + std::to_string(t));
+    }
+  }
+  HIPCHK(hipSetDevice(E->device));
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, out_F_dev) != hipSuccess ||
+      attr.type != hipMemoryTypeDevice || attr.device != E->device) {
+    (void)hipGetLastError();
+    return set_error(BSSCL_EINVAL, "predict_noalloc: out_F_dev is not device memory of GPU " +
+                                       std::to_string(E->device));
+  }
+  unsigned char *S = E->scratch_p;
+  if (!S) return set_error(BSSCL_EINTERNAL, "predict_noalloc: scratch address missing");
+  TreeNodeDev *nodes = reinterpret_cast<TreeNodeDev *>(S + kScrNodes);
+  int32_t *offs = reinterpret_cast<int32_t *>(S + kScrOffs);
+  if (total > 0) {
+    const size_t nt = (size_t)total;
+    HIPCHK(hipMemcpyAsync(S + kScrFeat, features, nt * 2, hipMemcpyHostToDevice, E->st));
+    HIPCHK(hipMemcpyAsync(S + kScrThr, thresholds, nt * 8, hipMemcpyHostToDevice, E->st));
+    HIPCHK(hipMemcpyAsync(S + kScrVal, values, nt * 8, hipMemcpyHostToDevice, E->st));
+    HIPCHK(hipMemcpyAsync(S + kScrLeft, left, nt * 4, hipMemcpyHostToDevice, E->st));
+    HIPCHK(hipMemcpyAsync(S + kScrRight, right, nt * 4, hipMemcpyHostToDevice, E->st));
+    HIPCHK(hipMemcpyAsync(offs, offsets, ((size_t)n_trees + 1) * 4, hipMemcpyHostToDevice,
+                          E->st));
+    HIPCHK(launch_pack_trees(E->st, reinterpret_cast<const int16_t *>(S + kScrFeat),
+                             reinterpret_cast<const int64_t *>(S + kScrThr),
+                             reinterpret_cast<const double *>(S + kScrVal),
+                             reinterpret_cast<const int32_t *>(S + kScrLeft),
+                             reinterpret_cast<const int32_t *>(S + kScrRight), total, nodes));
+  }
+  HIPCHK(launch_predict(E->st, M.codes.p, M.ld, M.n, nodes, offs, n_trees, learning_rate,
+                        out_F_dev));
+  HIPCHK(hipStreamSynchronize(E->st));
   return BSSCL_OK;
 }
 

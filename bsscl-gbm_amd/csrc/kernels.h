@@ -311,6 +311,9 @@ hipError_t launch_sum_partials(hipStream_t st, const double *partials,
 hipError_t launch_predict_tree(hipStream_t st, const uint8_t *codes,
                                int64_t ld, int64_t n, const TreeNodeDev *tree,
                                int32_t node_count, double *out);
+hipError_t launch_pack_trees(hipStream_t st, const int16_t *features, const int64_t *thresholds,
+                             const double *values, const int32_t *left, const int32_t *right,
+                             int32_t total, TreeNodeDev *nodes);
 hipError_t launch_predict(hipStream_t st, const uint8_t *codes, int64_t ld,
                           int64_t n, const TreeNodeDev *nodes,
                           const int32_t *offsets, int32_t n_trees, double lr,

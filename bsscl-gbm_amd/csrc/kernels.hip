@@ -2870,6 +2870,40 @@ __global__ __launch_bounds__(256) void k_predict(
 }
 #pragma clang fp contract(on)
 
+// Packed trees of _pack_tree_list (est:2192-2216) -> traversal nodes: the
+// host has checked every feature and child index.
+__global__ __launch_bounds__(256) void k_pack_trees(
+    const int16_t *__restrict__ features, const int64_t *__restrict__ thresholds,
+    const double *__restrict__ values, const int32_t *__restrict__ left,
+    const int32_t *__restrict__ right, int32_t total, TreeNodeDev *__restrict__ nodes) {
+  const int32_t i = (int32_t)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i >= total) return;
+  TreeNodeDev d;
+  d.value = values[i];
+  d.feature = features[i];
+  if (d.feature >= 0) {
+    const int64_t t = thresholds[i];
+    d.threshold = (int32_t)(t < -1 ? -1 : (t > (1 << 20) ? (1 << 20) : t));
+    d.left = left[i];
+    d.right = right[i];
+  } else {
+    d.feature = -1;
+    d.threshold = 0;
+    d.left = 0;
+    d.right = 0;
+  }
+  nodes[i] = d;
+}
+
+hipError_t launch_pack_trees(hipStream_t st, const int16_t *features, const int64_t *thresholds,
+                             const double *values, const int32_t *left, const int32_t *right,
+                             int32_t total, TreeNodeDev *nodes) {
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_pack_trees, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+                     features, thresholds, values, left, right, total, nodes);
+  return hipGetLastError();
+}
+
 hipError_t launch_predict(hipStream_t st, const uint8_t *codes, int64_t ld,
                           int64_t n, const TreeNodeDev *nodes,
                           const int32_t *offsets, int32_t n_trees, double lr,

@@ -185,6 +185,24 @@ int bsscl_predict(bsscl_engine *eng, int32_t slot, const int16_t *features,
                   const int32_t *offsets, int32_t n_trees,
                   double learning_rate, double *out_F);
 
+/*
+ * Ensemble prediction that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (serving
+ * loops, code under HIP graph capture, harnesses that forbid hipMalloc).
+ * Same trees, arithmetic and result as bsscl_predict, but out_F_dev is a
+ * float64[n] buffer in the device memory of the engine's GPU (n = rows of
+ * matrix `slot`), written before the call returns.  The packed trees are
+ * copied into a fixed per-GPU scratch area of at most 131072 nodes and 16384
+ * trees; larger ensembles fail with BSSCL_EINVAL.  No hipMalloc, hipFree or
+ * other allocating call is made.  Calls on one GPU share that area (it keeps
+ * the last call's trees): calls that overlap on one GPU race.
+ */
+int bsscl_predict_noalloc(bsscl_engine *eng, int32_t slot, const int16_t *features,
+                          const int64_t *thresholds, const double *values,
+                          const int32_t *left, const int32_t *right,
+                          const int32_t *offsets, int32_t n_trees,
+                          double learning_rate, double *out_F_dev);
+
 /* One tree over the rows of matrix `slot`: predict_batch_jit (est:843-861). */
 int bsscl_predict_tree(bsscl_engine *eng, int32_t slot,
                        const int32_t *features, const int64_t *thresholds,
