@@ -27,6 +27,7 @@ _SIGS = {
     "bsscl_bin_features": [_P, _i32, _P, _i32, _i64, _i32, _P, _i32, _P, _P, _P],
     "bsscl_load_codes": [_P, _i32, _P, _i32, _i64, _i32],
     "bsscl_get_codes": [_P, _i32, _P],
+    "bsscl_get_codes_u16": [_P, _i32, _P],
     "bsscl_stage_features": [_P, _P, _i32, _i64, _i32],
     "bsscl_sort_columns": [_P, _P, _P],
     "bsscl_sorted_gather": [_P, _i64, _P, _P, _P],
@@ -210,9 +211,12 @@ class Engine:
         check(lib().bsscl_load_codes(self.handle, int(slot), ptr(codes),
                                      int(codes.dtype == np.uint16), n, F))
 
-    def get_codes(self, slot, n, F):
-        out = np.empty((n, F), np.uint8)
-        check(lib().bsscl_get_codes(self.handle, int(slot), ptr(out)))
+    def get_codes(self, slot, n, F, u16=False):
+        """Row-major codes of matrix `slot`: uint8 min(code, 255), or with
+        u16 the reference's uint16 codes (est:2163-2166)."""
+        out = np.empty((n, F), np.uint16 if u16 else np.uint8)
+        fn = lib().bsscl_get_codes_u16 if u16 else lib().bsscl_get_codes
+        check(fn(self.handle, int(slot), ptr(out)))
         return out
 
     # -- trees --------------------------------------------------------------

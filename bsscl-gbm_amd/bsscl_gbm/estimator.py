@@ -505,10 +505,10 @@ class HybridHistGBMNumbaV1_0_1:
             self.bin_edges, self.feature_bin_counts = self._build_bin_edges(
                 X, sample_weight=sample_weight, eng=eng if staged else None)
             self._max_bins = int(np.max(self.feature_bin_counts))
-            if self._max_bins > 256:
+            if self._max_bins > 257:
                 raise NotImplementedError(
                     f"n_bins={self.n_bins} gives {self._max_bins} bins for some feature; "
-                    "the MI355X engine stores uint8 codes (at most 256 bins), use n_bins <= 255")
+                    "the MI355X engine holds at most 257 bins per feature (n_bins <= 256)")
             if staged:
                 eng.bin_staged(0, X.shape[0], X.shape[1], X.dtype == np.float64, self.bin_edges,
                                self.feature_bin_counts, self._nan_bin_id)

@@ -128,6 +128,12 @@ struct Matrix {
   DevBuf<uint8_t> codes;
   int64_t n = 0, ld = 0;
   int32_t F = 0;
+  // Top columns: column F + j holds (code >= 256) of feature j, and column j
+  // min(code, 255).  Present when some feature has 257 bins (n_bins = 256,
+  // est:1963-1964), whose codes the reference keeps as uint16
+  // (est:2163-2166, 2179-2182).
+  int32_t top = 0;
+  int32_t cols() const { return top ? 2 * F : F; }
 };
 
 struct HNode {
@@ -461,14 +467,58 @@ int check_matrix(bsscl_engine *E, int32_t slot) {
   return BSSCL_OK;
 }
 
-int alloc_matrix(bsscl_engine *E, int32_t slot, int64_t n, int32_t F) {
+int alloc_matrix(bsscl_engine *E, int32_t slot, int64_t n, int32_t F, int32_t top = 0) {
   Matrix &M = E->mat[slot];
   const int64_t ld = round_up(n + 8, 256);
-  CHK(M.codes.ensure((size_t)ld * (size_t)F));
-  HIPCHK(hipMemsetAsync(M.codes.p, 0, (size_t)ld * (size_t)F, E->st));
+  const size_t bytes = (size_t)ld * (size_t)F * (top ? 2 : 1);
+  CHK(M.codes.ensure(bytes));
+  HIPCHK(hipMemsetAsync(M.codes.p, 0, bytes, E->st));
   M.n = n;
   M.ld = ld;
   M.F = F;
+  M.top = top;
+  return BSSCL_OK;
+}
+
+// Gives matrix `slot` (all codes <= 255) zero top columns.
+int ensure_top_columns(bsscl_engine *E, int32_t slot) {
+  Matrix &M = E->mat[slot];
+  if (M.top) return BSSCL_OK;
+  const size_t half = (size_t)M.ld * (size_t)M.F;
+  DevBuf<uint8_t> wide;
+  CHK(wide.ensure(2 * half));
+  HIPCHK(hipMemcpyAsync(wide.p, M.codes.p, half, hipMemcpyDeviceToDevice, E->st));
+  HIPCHK(hipMemsetAsync(wide.p + half, 0, half, E->st));
+  HIPCHK(hipStreamSynchronize(E->st));
+  std::swap(M.codes, wide);
+  wide.release();
+  M.top = 1;
+  return BSSCL_OK;
+}
+
+// Engine columns of a tree's selected features (ascending feature ids, each
+// with bin count nb in [1, 257]): the feature's code column and, right after
+// it for a 257-bin feature, its top column F + j with 2 bins.  The
+// reference's candidate (j, 255) -- codes <= 255 go left -- is the top
+// column's candidate (F + j, 0); it follows (j, 0..254) exactly as bin 255
+// follows bins 0..254 in est:611-621, so the argmax and its strict-'>'
+// tie-breaks pick the same split.
+int expand_features(const Matrix &X, const std::vector<int32_t> &feats,
+                    const std::vector<int32_t> &nb, std::vector<int32_t> &cols,
+                    std::vector<int32_t> &nb_cols) {
+  cols.clear();
+  nb_cols.clear();
+  for (size_t i = 0; i < feats.size(); ++i) {
+    cols.push_back(feats[i]);
+    nb_cols.push_back(std::min(nb[i], kBins));
+    if (nb[i] > kBins) {
+      if (!X.top)
+        return set_error(BSSCL_EINVAL, "feature " + std::to_string(feats[i]) +
+                                           " has 257 bins but the matrix has no codes above 255");
+      cols.push_back(X.F + feats[i]);
+      nb_cols.push_back(2);
+    }
+  }
   return BSSCL_OK;
 }
 
@@ -1281,11 +1331,36 @@ int validate_tree_args(bsscl_engine *E, const int32_t *feature_indices,
     if (i > 0 && f <= feats[(size_t)i - 1])
       return set_error(BSSCL_EINVAL, "feature_indices must be strictly ascending");
     const int32_t nb = bin_counts[f];
-    if (nb < 1 || nb > kBins)
-      return set_error(BSSCL_EINVAL, "bin_counts must be in [1, 256]");
+    if (nb < 1 || nb > kBins + 1)
+      return set_error(BSSCL_EINVAL, "bin_counts must be in [1, 257]");
     nb_sel[(size_t)i] = nb;
+    if (nb > kBins) CHK(ensure_top_columns(E, 0));
   }
+  std::vector<int32_t> cols, nb_cols;
+  CHK(expand_features(X, feats, nb_sel, cols, nb_cols));
+  feats.swap(cols);
+  nb_sel.swap(nb_cols);
   return BSSCL_OK;
+}
+
+// Tree arrays from engine columns to the reference's features: a split on a
+// top column (F + j, 0) is the split (j, 255).
+void tree_to_reference(const Matrix &X, const TreeOut &out) {
+  const int32_t n = *out.node_count;
+  for (int32_t i = 0; i < n; ++i) {
+    if (out.features[i] >= X.F) {
+      out.features[i] -= X.F;
+      out.thresholds[i] += 255;
+    }
+  }
+}
+
+// A reference split (j, t) as the engine traverses it on matrix X.
+inline void split_to_engine(const Matrix &X, int32_t &feature, int64_t &threshold) {
+  if (X.top && feature >= 0 && threshold >= 255) {
+    feature += X.F;
+    threshold -= 255;
+  }
 }
 
 // Uploads host gradients/hessians and quantizes them with scales from their
@@ -1316,19 +1391,20 @@ int load_grad_hess(bsscl_engine *E, const double *grad, const double *hess,
 // that bin in registers instead of LDS atomics.
 int find_hot_bins(bsscl_engine *E) {
   const Matrix &M = E->mat[0];
+  const int32_t C = M.cols();
   DevBuf<unsigned int> cnt;
-  CHK(cnt.ensure((size_t)M.F * 256));
-  std::vector<unsigned int> h((size_t)M.F * 256);
-  hipError_t e = hipMemsetAsync(cnt.p, 0, (size_t)M.F * 256 * 4, E->st);
-  if (e == hipSuccess) e = launch_code_counts(E->st, M.codes.p, M.ld, M.n, M.F, cnt.p);
+  CHK(cnt.ensure((size_t)C * 256));
+  std::vector<unsigned int> h((size_t)C * 256);
+  hipError_t e = hipMemsetAsync(cnt.p, 0, (size_t)C * 256 * 4, E->st);
+  if (e == hipSuccess) e = launch_code_counts(E->st, M.codes.p, M.ld, M.n, C, cnt.p);
   if (e == hipSuccess) e = hipMemcpyAsync(h.data(), cnt.p, h.size() * 4, hipMemcpyDeviceToHost, E->st);
   if (e == hipSuccess) e = hipStreamSynchronize(E->st);
   cnt.release();
   if (e != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("code counts: ") + hipGetErrorString(e));
   // Only a bin holding at least 10% of the rows is worth the divergent
   // register path; -1 (no bin) otherwise.
-  E->hot_bin.assign((size_t)M.F, -1);
-  for (int32_t f = 0; f < M.F; ++f) {
+  E->hot_bin.assign((size_t)C, -1);
+  for (int32_t f = 0; f < C; ++f) {
     const unsigned int *c = h.data() + (size_t)f * 256;
     const int32_t b = (int32_t)(std::max_element(c, c + 256) - c);
     if ((double)c[b] >= 0.10 * (double)M.n) E->hot_bin[(size_t)f] = b;
@@ -1447,15 +1523,16 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     const int32_t f_sub = sh.f_sub;
     if (a.max_leaves < 1) rc = set_error(BSSCL_EINVAL, "max_leaves must be >= 1");
     if (rc == BSSCL_OK && !a.bin_counts) rc = set_error(BSSCL_EINVAL, "bin_counts missing");
-    R.feats.assign(sr.feats, sr.feats + f_sub);
-    R.nb_sel.resize((size_t)f_sub);
+    std::vector<int32_t> feats(sr.feats, sr.feats + f_sub), nb((size_t)f_sub);
     for (int32_t i = 0; rc == BSSCL_OK && i < f_sub; ++i) {
-      const int32_t f = R.feats[(size_t)i];
+      const int32_t f = feats[(size_t)i];
       if (f < 0 || f >= X.F) rc = set_error(BSSCL_EINVAL, "feature index out of range");
-      else if (a.bin_counts[f] < 1 || a.bin_counts[f] > kBins)
-        rc = set_error(BSSCL_EINVAL, "bin_counts must be in [1, 256]");
-      else R.nb_sel[(size_t)i] = a.bin_counts[f];
+      else if (a.bin_counts[f] < 1 || a.bin_counts[f] > kBins + 1)
+        rc = set_error(BSSCL_EINVAL, "bin_counts must be in [1, 257]");
+      else nb[(size_t)i] = a.bin_counts[f];
     }
+    // Engine columns: a 257-bin feature adds its top column.
+    if (rc == BSSCL_OK) rc = expand_features(X, feats, nb, R.feats, R.nb_sel);
   }
   const TreeParams tp{a.max_leaves, a.max_depth, a.min_samples_leaf, a.min_child_weight,
                       a.reg_lambda, a.gamma};
@@ -1676,6 +1753,7 @@ int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
     std::memcpy(out.right, ha.right, (size_t)M * 4);
     std::memcpy(out.gains, ha.gains, (size_t)M * 8);
     *out.node_count = h.node_count;
+    tree_to_reference(X, out);
     if (out_train_loss) {
       const double *parts =
           reinterpret_cast<const double *>(E->round_pin[s] + round_out_bytes(R.M));
@@ -1699,7 +1777,8 @@ int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
   E->set_base = 2 * s;
   CHK(build_tree_core(E, E->round_rows[s].p, R.m, R.feats, R.nb_sel, tp, out));
   CHK(upload_tree(E, out.features, out.thresholds, out.values, out.left, out.right,
-                  *out.node_count, X.F));
+                  *out.node_count, X.cols()));
+  tree_to_reference(X, out);
   const int nb = update_F_blocks(X.n);
   CHK(E->loss_d.ensure(1));
   HIPCHK(launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, *out.node_count, nullptr,
@@ -1860,14 +1939,17 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
   if (staged && (!E->xstage.p || E->xs_n != n || E->xs_F != F || E->xs_f64 != (x_is_f64 ? 1 : 0)))
     return set_error(BSSCL_EINVAL,
                      "bin_features: X is NULL but no staged matrix of this shape and dtype");
-  int32_t has_any_nan = 0;
+  int32_t has_any_nan = 0, top = 0;
   for (int32_t j = 0; j < F; ++j) {
     if (bin_counts[j] < 1 || bin_counts[j] >= edge_stride)
       return set_error(BSSCL_EINVAL, "bin_features: bin_counts must be in [1, edge_stride)");
+    if (bin_counts[j] > kBins + 1)
+      return set_error(BSSCL_EINVAL, "bin_features: more than 257 bins (n_bins > 256)");
+    if (bin_counts[j] > kBins) top = 1;
     if (nan_bin_id[j] >= 0) has_any_nan = 1;
   }
   HIPCHK(hipSetDevice(E->device));
-  CHK(alloc_matrix(E, slot, n, F));
+  CHK(alloc_matrix(E, slot, n, F, top));
   DevBuf<double> ed;
   DevBuf<int32_t> nb, nid;
   CHK(ed.ensure((size_t)F * edge_stride));
@@ -1880,7 +1962,7 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
   const size_t esz = x_is_f64 ? 8 : 4;
   if (staged) {
     hipError_t e = launch_bin(E->st, E->xstage.p, x_is_f64, n, F, ed.p, edge_stride, nb.p,
-                              nid.p, has_any_nan, M.codes.p, M.ld);
+                              nid.p, has_any_nan, M.codes.p, M.ld, top);
     if (e == hipSuccess) e = hipStreamSynchronize(E->st);
     ed.release(); nb.release(); nid.release();
     if (e != hipSuccess)
@@ -1898,7 +1980,7 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
                                     (size_t)rows * F * esz, hipMemcpyHostToDevice, E->st);
       if (e == hipSuccess)
         e = launch_bin(E->st, xd.p, x_is_f64, rows, F, ed.p, edge_stride, nb.p, nid.p,
-                       has_any_nan, M.codes.p + r0, M.ld);
+                       has_any_nan, M.codes.p + r0, M.ld, top);
       if (e == hipSuccess) e = hipStreamSynchronize(E->st);
       if (e != hipSuccess) {
         xd.release(); ed.release(); nb.release(); nid.release();
@@ -2067,13 +2149,19 @@ int bsscl_load_codes(bsscl_engine *E, int32_t slot, const void *codes,
   if (slot < 0 || slot > 1) return set_error(BSSCL_EINVAL, "matrix slot must be 0 or 1");
   if (n <= 0 || n > INT32_MAX || F <= 0) return set_error(BSSCL_EINVAL, "load_codes: bad shape");
   HIPCHK(hipSetDevice(E->device));
-  CHK(alloc_matrix(E, slot, n, F));
+  int32_t top = 0;
+  if (codes_u16) {
+    const uint16_t *c16 = static_cast<const uint16_t *>(codes);
+    for (int64_t k = 0; k < n * F && !top; ++k) top = c16[k] > 255;
+  }
+  CHK(alloc_matrix(E, slot, n, F, top));
   const size_t bytes = (size_t)n * F * (codes_u16 ? 2 : 1);
   DevBuf<unsigned char> tmp;
   CHK(tmp.ensure(bytes));
   hipError_t e = hipMemcpyAsync(tmp.p, codes, bytes, hipMemcpyHostToDevice, E->st);
   if (e == hipSuccess)
-    e = launch_load_codes(E->st, tmp.p, codes_u16, n, F, E->mat[slot].codes.p, E->mat[slot].ld);
+    e = launch_load_codes(E->st, tmp.p, codes_u16, n, F, E->mat[slot].codes.p, E->mat[slot].ld,
+                          top);
   if (e == hipSuccess) e = hipStreamSynchronize(E->st);
   tmp.release();
   if (e != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("load_codes: ") + hipGetErrorString(e));
@@ -2081,20 +2169,30 @@ int bsscl_load_codes(bsscl_engine *E, int32_t slot, const void *codes,
   return BSSCL_OK;
 }
 
-int bsscl_get_codes(bsscl_engine *E, int32_t slot, uint8_t *codes_out) {
+namespace {
+int get_codes(bsscl_engine *E, int32_t slot, void *codes_out, int as_u16) {
   if (!E || !codes_out) return set_error(BSSCL_EINVAL, "get_codes: null argument");
   CHK(check_matrix(E, slot));
   HIPCHK(hipSetDevice(E->device));
   const Matrix &M = E->mat[slot];
+  const size_t bytes = (size_t)M.n * M.F * (as_u16 ? 2 : 1);
   DevBuf<uint8_t> tmp;
-  CHK(tmp.ensure((size_t)M.n * M.F));
-  hipError_t e = launch_get_codes(E->st, M.codes.p, M.ld, M.n, M.F, tmp.p);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(codes_out, tmp.p, (size_t)M.n * M.F, hipMemcpyDeviceToHost, E->st);
+  CHK(tmp.ensure(bytes));
+  hipError_t e = launch_get_codes(E->st, M.codes.p, M.ld, M.n, M.F, M.top, tmp.p, as_u16);
+  if (e == hipSuccess) e = hipMemcpyAsync(codes_out, tmp.p, bytes, hipMemcpyDeviceToHost, E->st);
   if (e == hipSuccess) e = hipStreamSynchronize(E->st);
   tmp.release();
   if (e != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("get_codes: ") + hipGetErrorString(e));
   return BSSCL_OK;
+}
+}  // namespace
+
+int bsscl_get_codes(bsscl_engine *E, int32_t slot, uint8_t *codes_out) {
+  return get_codes(E, slot, codes_out, 0);
+}
+
+int bsscl_get_codes_u16(bsscl_engine *E, int32_t slot, uint16_t *codes_out) {
+  return get_codes(E, slot, codes_out, 1);
 }
 
 int bsscl_build_tree(bsscl_engine *E, const double *grad, const double *hess,
@@ -2119,9 +2217,9 @@ int bsscl_build_tree(bsscl_engine *E, const double *grad, const double *hess,
   TreeOut out{out_features, out_thresholds, out_values, out_left, out_right,
               out_node_count, out_split_gains};
   std::vector<int32_t> feats, nb_sel;
+  HIPCHK(hipSetDevice(E->device));
   CHK(validate_tree_args(E, feature_indices, n_selected, max_leaves,
                          min_samples_leaf, bin_counts, out, feats, nb_sel));
-  HIPCHK(hipSetDevice(E->device));
   CHK(load_grad_hess(E, grad, hess, X.n, n_samples));
   CHK(E->rows64.ensure((size_t)n_samples));
   HIPCHK(hipMemcpyAsync(E->rows64.p, sample_indices, (size_t)n_samples * 8,
@@ -2129,7 +2227,9 @@ int bsscl_build_tree(bsscl_engine *E, const double *grad, const double *hess,
   TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight,
                 reg_lambda, gamma};
   E->set_base = 0;
-  return build_tree_core(E, nullptr, n_samples, feats, nb_sel, tp, out);
+  CHK(build_tree_core(E, nullptr, n_samples, feats, nb_sel, tp, out));
+  tree_to_reference(X, out);
+  return BSSCL_OK;
 }
 
 int bsscl_boost_begin(bsscl_engine *E, const int64_t *y, int64_t n, double w0,
@@ -2294,7 +2394,9 @@ int bsscl_predict(bsscl_engine *E, int32_t slot, const int16_t *features,
         const int32_t l = left[i], r = right[i];
         if (d.feature >= M.F || l < 0 || r < 0 || l >= b - a || r >= b - a || l <= i - a || r <= i - a)
           return set_error(BSSCL_EINVAL, "predict: malformed tree " + std::to_string(t));
-        d.threshold = (int32_t)std::max<int64_t>(-1, std::min<int64_t>(thresholds[i], 1 << 20));
+        int64_t thr = thresholds[i];
+        split_to_engine(M, d.feature, thr);
+        d.threshold = (int32_t)std::max<int64_t>(-1, std::min<int64_t>(thr, 1 << 20));
         d.left = l;
         d.right = r;
       } else {
@@ -2374,7 +2476,8 @@ int bsscl_predict_noalloc(bsscl_engine *E, int32_t slot, const int16_t *features
                              reinterpret_cast<const int64_t *>(S + kScrThr),
                              reinterpret_cast<const double *>(S + kScrVal),
                              reinterpret_cast<const int32_t *>(S + kScrLeft),
-                             reinterpret_cast<const int32_t *>(S + kScrRight), total, nodes));
+                             reinterpret_cast<const int32_t *>(S + kScrRight), total,
+                             M.top ? M.F : 0, nodes));
   }
   HIPCHK(launch_predict(E->st, M.codes.p, M.ld, M.n, nodes, offs, n_trees, learning_rate,
                         out_F_dev));
@@ -2391,7 +2494,14 @@ int bsscl_predict_tree(bsscl_engine *E, int32_t slot, const int32_t *features,
   CHK(check_matrix(E, slot));
   HIPCHK(hipSetDevice(E->device));
   const Matrix &M = E->mat[slot];
-  CHK(upload_tree(E, features, thresholds, values, left, right, node_count, M.F));
+  if (node_count <= 0) return set_error(BSSCL_EINVAL, "empty tree");
+  std::vector<int32_t> f(features, features + node_count);
+  std::vector<int64_t> t(thresholds, thresholds + node_count);
+  for (int32_t i = 0; i < node_count; ++i) {
+    if (f[(size_t)i] >= M.F) return set_error(BSSCL_EINVAL, "malformed tree node " + std::to_string(i));
+    split_to_engine(M, f[(size_t)i], t[(size_t)i]);
+  }
+  CHK(upload_tree(E, f.data(), t.data(), values, left, right, node_count, M.cols()));
   CHK(E->out_d.ensure((size_t)M.n));
   HIPCHK(launch_predict_tree(E->st, M.codes.p, M.ld, M.n, E->tree_d.p, node_count, E->out_d.p));
   HIPCHK(hipMemcpyAsync(out, E->out_d.p, (size_t)M.n * 8, hipMemcpyDeviceToHost, E->st));
@@ -2460,6 +2570,9 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
   const Matrix &X = E->mat[0];
   if (m <= 0) return set_error(BSSCL_EINVAL, "partition: no rows");
   if (feature < 0 || feature >= X.F) return set_error(BSSCL_EINVAL, "partition: feature out of range");
+  int64_t bin64 = bin;
+  split_to_engine(X, feature, bin64);
+  bin = (int32_t)bin64;
   for (int64_t k = 0; k < m; ++k)
     if (rows[k] < 0 || rows[k] >= X.n) return set_error(BSSCL_EINVAL, "partition: row out of range");
   HIPCHK(hipSetDevice(E->device));

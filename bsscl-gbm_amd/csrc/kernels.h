@@ -171,11 +171,11 @@ constexpr int kReplaySlots = 1024;  // candidate slots the device replay holds
 hipError_t launch_bin(hipStream_t st, const void *X, int is_f64, int64_t n,
                       int32_t F, const double *edges, int32_t stride,
                       const int32_t *nb, const int32_t *nan_id,
-                      int32_t has_any_nan, uint8_t *codes, int64_t ld);
+                      int32_t has_any_nan, uint8_t *codes, int64_t ld, int32_t top);
 hipError_t launch_load_codes(hipStream_t st, const void *src, int is_u16,
-                             int64_t n, int32_t F, uint8_t *codes, int64_t ld);
+                             int64_t n, int32_t F, uint8_t *codes, int64_t ld, int32_t top);
 hipError_t launch_get_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
-                            int64_t n, int32_t F, uint8_t *dst);
+                            int64_t n, int32_t F, int32_t top, void *dst, int as_u16);
 hipError_t launch_quantize(hipStream_t st, const double *g, const double *h,
                            int64_t n, double g_mul, double h_mul, GH *ghq);
 hipError_t launch_grad_hess(hipStream_t st, const double *F, const uint8_t *y,
@@ -313,7 +313,7 @@ hipError_t launch_predict_tree(hipStream_t st, const uint8_t *codes,
                                int32_t node_count, double *out);
 hipError_t launch_pack_trees(hipStream_t st, const int16_t *features, const int64_t *thresholds,
                              const double *values, const int32_t *left, const int32_t *right,
-                             int32_t total, TreeNodeDev *nodes);
+                             int32_t total, int32_t top_F, TreeNodeDev *nodes);
 hipError_t launch_predict(hipStream_t st, const uint8_t *codes, int64_t ld,
                           int64_t n, const TreeNodeDev *nodes,
                           const int32_t *offsets, int32_t n_trees, double lr,

@@ -65,7 +65,9 @@ constexpr int kBinRows = 64;
 
 // Code of one value: the largest k in [0, nb-1] with e[k] <= v, 0 below
 // e[0], nb-1 at or above e[nb] (est:204-226); NaN handling of est:2159-2177.
-__device__ __forceinline__ uint8_t bin_one(double v, const double *__restrict__ e,
+// The matrix stores min(code, 255) in the feature's column and, when it has
+// top columns (some feature has 257 bins), code >= 256 in column F + f.
+__device__ __forceinline__ int32_t bin_one(double v, const double *__restrict__ e,
                                            int32_t nbf, bool nan_feat,
                                            int32_t has_any_nan) {
   if (v != v) {
@@ -87,7 +89,7 @@ __device__ __forceinline__ uint8_t bin_one(double v, const double *__restrict__ 
     c = lo;
   }
   if (nan_feat) c += 1;  // est:2176
-  return (uint8_t)min(c, 255);
+  return c;
 }
 
 template <typename T>
@@ -95,27 +97,29 @@ __global__ __launch_bounds__(256) void k_bin(
     const T *__restrict__ X, int64_t n, int32_t F,
     const double *__restrict__ edges, int32_t stride,
     const int32_t *__restrict__ nb, const int32_t *__restrict__ nan_id,
-    int32_t has_any_nan, uint8_t *__restrict__ codes, int64_t ld) {
+    int32_t has_any_nan, uint8_t *__restrict__ codes, int64_t ld, int32_t top) {
   extern __shared__ unsigned char smem[];
   T *xs = reinterpret_cast<T *>(smem);                        // [64][F]
-  uint8_t *cs = smem + sizeof(T) * (size_t)kBinRows * F;     // [F][64]
+  uint8_t *cs = smem + sizeof(T) * (size_t)kBinRows * F;     // [F (+F top)][64]
   const int64_t r0 = (int64_t)blockIdx.x * kBinRows;
   const int rows = (int)min<int64_t>(kBinRows, n - r0);
   const int tot = rows * F;
+  const int cols = top ? 2 * F : F;
   for (int i = threadIdx.x; i < tot; i += blockDim.x)
     xs[i] = X[r0 * F + i];
   __syncthreads();
   for (int i = threadIdx.x; i < kBinRows * F; i += blockDim.x) {
     const int f = i / kBinRows, r = i % kBinRows;
-    uint8_t code = 0;
+    int32_t code = 0;
     if (r < rows)
       code = bin_one((double)xs[r * F + f], edges + (int64_t)f * stride, nb[f],
                      nan_id[f] >= 0, has_any_nan);
-    cs[f * kBinRows + r] = code;
+    cs[f * kBinRows + r] = (uint8_t)min(code, 255);
+    if (top) cs[(F + f) * kBinRows + r] = code >= 256 ? 1 : 0;
   }
   __syncthreads();
-  // 16 dwords per feature.
-  for (int i = threadIdx.x; i < F * (kBinRows / 4); i += blockDim.x) {
+  // 16 dwords per column.
+  for (int i = threadIdx.x; i < cols * (kBinRows / 4); i += blockDim.x) {
     const int f = i / (kBinRows / 4), w = i % (kBinRows / 4);
     const uint32_t v = *reinterpret_cast<const uint32_t *>(cs + f * kBinRows + 4 * w);
     *reinterpret_cast<uint32_t *>(codes + (int64_t)f * ld + r0 + 4 * w) = v;
@@ -128,42 +132,44 @@ __global__ __launch_bounds__(256) void k_bin_wide(
     const T *__restrict__ X, int64_t n, int32_t F,
     const double *__restrict__ edges, int32_t stride,
     const int32_t *__restrict__ nb, const int32_t *__restrict__ nan_id,
-    int32_t has_any_nan, uint8_t *__restrict__ codes, int64_t ld) {
+    int32_t has_any_nan, uint8_t *__restrict__ codes, int64_t ld, int32_t top) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int32_t f = (int32_t)blockIdx.y;
   if (i >= n) return;
-  codes[(int64_t)f * ld + i] =
-      bin_one((double)X[i * F + f], edges + (int64_t)f * stride, nb[f],
-              nan_id[f] >= 0, has_any_nan);
+  const int32_t code = bin_one((double)X[i * F + f], edges + (int64_t)f * stride, nb[f],
+                               nan_id[f] >= 0, has_any_nan);
+  codes[(int64_t)f * ld + i] = (uint8_t)min(code, 255);
+  if (top) codes[(int64_t)(F + f) * ld + i] = code >= 256 ? 1 : 0;
 }
 
 hipError_t launch_bin(hipStream_t st, const void *X, int is_f64, int64_t n,
                       int32_t F, const double *edges, int32_t stride,
                       const int32_t *nb, const int32_t *nan_id,
-                      int32_t has_any_nan, uint8_t *codes, int64_t ld) {
+                      int32_t has_any_nan, uint8_t *codes, int64_t ld, int32_t top) {
   if (n <= 0) return hipSuccess;
-  const size_t lds = (is_f64 ? 8 : 4) * (size_t)kBinRows * F + (size_t)kBinRows * F;
+  const size_t lds = (is_f64 ? 8 : 4) * (size_t)kBinRows * F +
+                     (size_t)kBinRows * F * (top ? 2 : 1);
   if (lds > 48 * 1024) {
     const dim3 grid((unsigned)((n + 255) / 256), (unsigned)F);
     if (is_f64)
       hipLaunchKernelGGL(k_bin_wide<double>, grid, dim3(256), 0, st,
                          (const double *)X, n, F, edges, stride, nb, nan_id,
-                         has_any_nan, codes, ld);
+                         has_any_nan, codes, ld, top);
     else
       hipLaunchKernelGGL(k_bin_wide<float>, grid, dim3(256), 0, st,
                          (const float *)X, n, F, edges, stride, nb, nan_id,
-                         has_any_nan, codes, ld);
+                         has_any_nan, codes, ld, top);
     return hipGetLastError();
   }
   const unsigned blocks = (unsigned)((n + kBinRows - 1) / kBinRows);
   if (is_f64)
     hipLaunchKernelGGL(k_bin<double>, dim3(blocks), dim3(256), lds, st,
                        (const double *)X, n, F, edges, stride, nb, nan_id,
-                       has_any_nan, codes, ld);
+                       has_any_nan, codes, ld, top);
   else
     hipLaunchKernelGGL(k_bin<float>, dim3(blocks), dim3(256), lds, st,
                        (const float *)X, n, F, edges, stride, nb, nan_id,
-                       has_any_nan, codes, ld);
+                       has_any_nan, codes, ld, top);
   return hipGetLastError();
 }
 
@@ -194,47 +200,60 @@ hipError_t launch_code_counts(hipStream_t st, const uint8_t *codes, int64_t ld,
   return hipGetLastError();
 }
 
-// Row-major uint8/uint16 codes -> feature-major uint8 (values above 255
-// become 255).
+// Row-major uint8/uint16 codes -> feature-major uint8: min(code, 255), and
+// code >= 256 in the top column F + f when the matrix has top columns.
 template <typename T>
 __global__ __launch_bounds__(256) void k_load_codes(const T *__restrict__ src,
                                                     int64_t n, int32_t F,
                                                     uint8_t *__restrict__ codes,
-                                                    int64_t ld) {
+                                                    int64_t ld, int32_t top) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   for (int32_t f = 0; f < F; ++f) {
     uint32_t v = (uint32_t)src[i * F + f];
     codes[(int64_t)f * ld + i] = (uint8_t)min(v, 255u);
+    if (top) codes[(int64_t)(F + f) * ld + i] = v >= 256u ? 1 : 0;
   }
 }
 
 hipError_t launch_load_codes(hipStream_t st, const void *src, int is_u16,
-                             int64_t n, int32_t F, uint8_t *codes, int64_t ld) {
+                             int64_t n, int32_t F, uint8_t *codes, int64_t ld, int32_t top) {
   if (n <= 0) return hipSuccess;
   const unsigned blocks = (unsigned)((n + 255) / 256);
   if (is_u16)
     hipLaunchKernelGGL(k_load_codes<uint16_t>, dim3(blocks), dim3(256), 0, st,
-                       (const uint16_t *)src, n, F, codes, ld);
+                       (const uint16_t *)src, n, F, codes, ld, top);
   else
     hipLaunchKernelGGL(k_load_codes<uint8_t>, dim3(blocks), dim3(256), 0, st,
-                       (const uint8_t *)src, n, F, codes, ld);
+                       (const uint8_t *)src, n, F, codes, ld, top);
   return hipGetLastError();
 }
 
+// Feature-major matrix -> row-major codes: uint8 min(code, 255), or uint16
+// min(code, 255) + top flag (256 for every code >= 256).
+template <typename T>
 __global__ __launch_bounds__(256) void k_get_codes(const uint8_t *__restrict__ codes,
                                                    int64_t ld, int64_t n, int32_t F,
-                                                   uint8_t *__restrict__ dst) {
+                                                   int32_t top, T *__restrict__ dst) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  for (int32_t f = 0; f < F; ++f) dst[i * F + f] = codes[(int64_t)f * ld + i];
+  for (int32_t f = 0; f < F; ++f) {
+    uint32_t v = codes[(int64_t)f * ld + i];
+    if (top) v += codes[(int64_t)(F + f) * ld + i];
+    dst[i * F + f] = (T)v;
+  }
 }
 
 hipError_t launch_get_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
-                            int64_t n, int32_t F, uint8_t *dst) {
+                            int64_t n, int32_t F, int32_t top, void *dst, int as_u16) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_get_codes, dim3((unsigned)((n + 255) / 256)), dim3(256),
-                     0, st, codes, ld, n, F, dst);
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (as_u16)
+    hipLaunchKernelGGL(k_get_codes<uint16_t>, grid, dim3(256), 0, st, codes, ld, n, F, top,
+                       (uint16_t *)dst);
+  else
+    hipLaunchKernelGGL(k_get_codes<uint8_t>, grid, dim3(256), 0, st, codes, ld, n, F, 0,
+                       (uint8_t *)dst);
   return hipGetLastError();
 }
 
@@ -2875,7 +2894,8 @@ __global__ __launch_bounds__(256) void k_predict(
 __global__ __launch_bounds__(256) void k_pack_trees(
     const int16_t *__restrict__ features, const int64_t *__restrict__ thresholds,
     const double *__restrict__ values, const int32_t *__restrict__ left,
-    const int32_t *__restrict__ right, int32_t total, TreeNodeDev *__restrict__ nodes) {
+    const int32_t *__restrict__ right, int32_t total, int32_t top_F,
+    TreeNodeDev *__restrict__ nodes) {
   const int32_t i = (int32_t)(blockIdx.x * blockDim.x + threadIdx.x);
   if (i >= total) return;
   TreeNodeDev d;
@@ -2884,6 +2904,12 @@ __global__ __launch_bounds__(256) void k_pack_trees(
   if (d.feature >= 0) {
     const int64_t t = thresholds[i];
     d.threshold = (int32_t)(t < -1 ? -1 : (t > (1 << 20) ? (1 << 20) : t));
+    if (top_F > 0 && d.threshold >= 255) {
+      // code <= 255 is "top flag <= 0" (est's split at bin 255 of a 257-bin
+      // feature).
+      d.feature += top_F;
+      d.threshold -= 255;
+    }
     d.left = left[i];
     d.right = right[i];
   } else {
@@ -2897,10 +2923,10 @@ __global__ __launch_bounds__(256) void k_pack_trees(
 
 hipError_t launch_pack_trees(hipStream_t st, const int16_t *features, const int64_t *thresholds,
                              const double *values, const int32_t *left, const int32_t *right,
-                             int32_t total, TreeNodeDev *nodes) {
+                             int32_t total, int32_t top_F, TreeNodeDev *nodes) {
   if (total <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_pack_trees, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
-                     features, thresholds, values, left, right, total, nodes);
+                     features, thresholds, values, left, right, total, top_F, nodes);
   return hipGetLastError();
 }
 

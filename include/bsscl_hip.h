@@ -53,10 +53,16 @@ void bsscl_engine_destroy(bsscl_engine *eng);
  *   bin_counts int32[F], nan_bin_id int32[F]
  * X may be NULL to bin the matrix staged by bsscl_stage_features (below).
  * The codes stay on the device as matrix `slot` (0 = training, 1 = scoring),
- * stored feature-major as uint8.  Reference codes above 255 (possible only
- * with n_bins = 256, for the top bin of a NaN feature) are stored as 255,
- * which every split and every prediction treats identically.  When codes_out
- * is not NULL the codes are also copied back row-major (n x F uint8).
+ * stored feature-major as uint8 min(code, 255).  Bin counts go up to 257
+ * (n_bins = 256, the reference's 'auto' value for p >= 28, est:1963-1964,
+ * whose codes it keeps as uint16, est:2163-2166); when any feature has 257
+ * bins the matrix also holds, per feature, whether its code is >= 256, and
+ * every split and prediction sees the reference's codes.  Otherwise a code
+ * above 255 (a scoring value above the training range of a 256-bin NaN
+ * feature) is stored as 255, which every threshold (<= 254) treats
+ * identically.  When codes_out is not NULL the codes are also copied back
+ * row-major (n x F uint8, min(code, 255)).  More than 257 bins (n_bins > 256)
+ * fail with BSSCL_EINVAL.
  */
 int bsscl_bin_features(bsscl_engine *eng, int32_t slot, const void *X,
                        int32_t x_is_f64, int64_t n, int32_t F,
@@ -69,8 +75,13 @@ int bsscl_bin_features(bsscl_engine *eng, int32_t slot, const void *X,
 int bsscl_load_codes(bsscl_engine *eng, int32_t slot, const void *codes,
                      int32_t codes_u16, int64_t n, int32_t F);
 
-/* Copy matrix `slot` back row-major (n x F uint8). */
+/* Copy matrix `slot` back row-major: n x F uint8 min(code, 255), or (_u16)
+ * n x F uint16 codes as the reference stores them when _max_bins > 255
+ * (est:2163-2166).  A code above every bin of its feature (a scoring value
+ * above a NaN feature's training range) reads back as 256 when the matrix
+ * holds 257-bin features and as 255 otherwise. */
 int bsscl_get_codes(bsscl_engine *eng, int32_t slot, uint8_t *codes_out);
+int bsscl_get_codes_u16(bsscl_engine *eng, int32_t slot, uint16_t *codes_out);
 
 /*
  * Bin edges on the device.  Replace the data passes of _build_bin_edges
@@ -213,7 +224,7 @@ int bsscl_predict_tree(bsscl_engine *eng, int32_t slot,
  * One node's histogram and best split on matrix 0: the root histogram
  * (est:581-596) and root split scan (est:598-621) for the given rows.
  * out_G/out_H: float64[n_selected * 256] (feature-position major, bins past
- * bin_counts are 0).  out_gain/out_feature/out_bin receive the best split
+ * bin_counts are 0); bin counts up to 256.  out_gain/out_feature/out_bin receive the best split
  * (out_feature = -1 when none qualifies).  Any output may be NULL.
  */
 int bsscl_node_split(bsscl_engine *eng, const double *grad, const double *hess,

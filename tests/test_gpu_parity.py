@@ -54,10 +54,13 @@ def test_binning_bit_exact(engine, case):
         X[:, 2] = np.round(X[:, 2] * 40)
         n_bins = 256
     e, bc, nid, want = _binned(X, n_bins)
-    if bc.max() > 256:
-        pytest.skip("more than 256 bins")
+    if case == "nbins256":
+        # n_bins = 256: continuous columns get 257 bins and uint16 codes.
+        assert bc.max() == 257 and want.dtype == np.uint16 and want.max() == 256
     got = engine.bin_features(0, X, e, bc, nid, return_codes=True)
     np.testing.assert_array_equal(got, np.minimum(want.astype(np.int64), 255).astype(np.uint8))
+    if want.dtype == np.uint16:
+        np.testing.assert_array_equal(engine.get_codes(0, *X.shape, u16=True), want)
     # Scoring matrix: values outside the training range and NaN in columns
     # that had none.
     Xp = X.copy()
@@ -66,6 +69,31 @@ def test_binning_bit_exact(engine, case):
     want_p = om.bin_features(Xp, e, bc, nid, "hybrid")
     got_p = engine.bin_features(1, Xp, e, bc, nid, return_codes=True)
     np.testing.assert_array_equal(got_p, np.minimum(want_p.astype(np.int64), 255).astype(np.uint8))
+    if want_p.dtype == np.uint16:
+        # A code above every bin of its feature (a value above the training
+        # range of a NaN feature) reads back as 256 when the matrix holds
+        # 257-bin features and as 255 otherwise; no split tells them apart.
+        cap = 256 if bc.max() > 256 else 255
+        np.testing.assert_array_equal(engine.get_codes(1, *Xp.shape, u16=True),
+                                      np.minimum(want_p, cap))
+
+
+@pytest.mark.parametrize("m,bin_", [(50_001, 255), (50_001, 254), (3000, 256)])
+def test_partition_top_bin(engine, m, bin_):
+    """257-bin codes (uint16): the split at bin 255 sends code 256 right."""
+    _announce(f"partition 257 bins m={m} bin={bin_}")
+    rng = np.random.default_rng(m + bin_)
+    n = 2 * m
+    codes = rng.integers(0, 257, (n, 3)).astype(np.uint16)
+    codes[rng.random(n) < 0.2, 1] = 256
+    engine.load_codes(0, codes)
+    np.testing.assert_array_equal(engine.get_codes(0, n, 3, u16=True), codes)
+    rows = rng.permutation(n)[:m].astype(np.int64)
+    out, nl = engine.partition(rows, 1, bin_)
+    left = codes[rows, 1] <= bin_
+    assert nl == int(left.sum())
+    np.testing.assert_array_equal(out[:nl], rows[left])
+    np.testing.assert_array_equal(out[nl:], rows[~left])
 
 
 def test_load_codes_roundtrip(engine):
@@ -204,6 +232,10 @@ def test_fisher_yates_device_equals_numpy_shuffle(engine, n, form, monkeypatch):
     dict(n=30000, F=12, seed=9, n_bins=255, max_leaves=63, max_depth=8, msl=5, mcw=1.0, lam=1.0, nan=0.7),
     dict(n=5000, F=5, seed=10, n_bins=64, max_leaves=31, max_depth=1, msl=5, mcw=1.0, lam=1.0),
     dict(n=60000, F=30, seed=11, n_bins=255, max_leaves=255, max_depth=12, msl=2, mcw=0.5, lam=1.0, nan=0.05),
+    # n_bins = 256: 257-bin features (uint16 codes, est:2163-2166).
+    dict(n=40000, F=30, seed=13, n_bins=256, max_leaves=63, max_depth=6, msl=5, mcw=3.0, lam=1.0),
+    dict(n=30000, F=28, seed=14, n_bins=256, max_leaves=63, max_depth=8, msl=5, mcw=1.0, lam=1.0,
+         nan=0.1, col=0.8),
     # 1.5M in-bag rows: the 2048-row partition tiles.
     dict(n=2_000_000, F=8, seed=12, n_bins=255, max_leaves=63, max_depth=6, msl=5, mcw=3.0, lam=1.0,
          nan=0.05, sub=0.75, col=1.0),
@@ -227,6 +259,24 @@ def test_predict_matches_oracle(engine):
 
 
 def _fit_case(name):
+    if name == "defaults_28":
+        # Every parameter at the reference's default: n_bins='auto' resolves
+        # to 256 at p = 28 (est:1963-1964), so the continuous columns get 257
+        # bins.
+        X, y = make_data(30000, 28, seed=15, nan_frac=0.05, nan_cols=list(range(0, 28, 4)))
+        return X, y, dict(random_state=0)
+    if name == "top_bin_28":
+        # Defaults again, and in two columns 60 rows sit exactly at the
+        # column's maximum (code 256 of 257) and are all positive: the split
+        # at bin 255 (code 256 goes right) is the best one there.
+        rng = np.random.default_rng(16)
+        X = rng.standard_normal((20000, 28)).astype(np.float32)
+        y = (rng.random(20000) < 0.05).astype(np.int64)
+        for j in (3, 11):
+            idx = rng.choice(20000, 60, replace=False)
+            X[idx, j] = X[:, j].max()
+            y[idx] = 1
+        return X, y, dict(n_estimators=40, random_state=0)
     if name == "config1":
         rng = np.random.default_rng(0)
         X = rng.standard_normal((10_000, 20), dtype=np.float32)
@@ -248,7 +298,8 @@ def _fit_case(name):
     return X, y, params
 
 
-@pytest.mark.parametrize("name", ["config1", "nan_imbalanced", "sparse"])
+@pytest.mark.parametrize("name", ["config1", "nan_imbalanced", "sparse", "defaults_28",
+                                  "top_bin_28"])
 def test_fit_lockstep_and_end_to_end(engine, name):
     """Every round of the oracle's fit, rebuilt by the engine from the same
     gradients, rows and features (lockstep), and the estimator's own tree of
@@ -261,8 +312,18 @@ def test_fit_lockstep_and_end_to_end(engine, name):
     est = HybridHistGBMNumbaV1_0_1(verbose=False, **params).fit(X, y)
     ref, rep = fitcmp.follow_fit(engine, est, X, y, params)
     print(rep.line(name), flush=True)
-    assert rep.rounds == params["n_estimators"]
+    assert rep.rounds == ref.n_estimators == len(est.trees)
     fitcmp.assert_fit_equal(ref, est, X)
+    if name in ("defaults_28", "top_bin_28"):
+        from bsscl_gbm import estimator as est_mod
+        assert est.n_bins == 256 and est._max_bins == 257
+        got = est_mod._engine(0).get_codes(0, *X.shape, u16=True)
+        np.testing.assert_array_equal(got, ref.X_bin_)
+        splits = [(f, t) for tr in est.trees for f, t in zip(tr[0][:tr[5]], tr[1][:tr[5]]) if f >= 0]
+        at255 = sum(t == 255 for _, t in splits)
+        print(f"[result] {name}: {at255} splits at bin 255 of {len(splits)}", flush=True)
+        if name == "top_bin_28":
+            assert at255 > 0
 
 
 def test_fit_device_replay_fallbacks_agree(engine, monkeypatch):
