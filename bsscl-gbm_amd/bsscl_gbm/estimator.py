@@ -22,6 +22,7 @@ reference raise NotImplementedError instead of computing something else.
 from __future__ import annotations
 
 import os
+import threading
 import time
 
 import numpy as np
@@ -31,17 +32,24 @@ from . import _native
 __all__ = ["HybridHistGBMNumbaV1_0_1"]
 
 _ENGINES: dict = {}
+_ENGINES_LOCK = threading.Lock()
 
 
 def _engine(device: int) -> _native.Engine:
-    """Per-process engine cache; a forked child creates its own."""
+    """Per-process engine cache; a forked child creates its own.  Every
+    estimator of the process shares the device's engine, whose matrices and
+    boosting state one operation at a time may use: callers hold
+    ``eng.lock`` (re-entrant) for a whole fit or prediction, so estimators
+    may be fitted and used from several threads."""
     key = (os.getpid(), int(device))
-    eng = _ENGINES.get(key)
-    if eng is None:
-        for k in [k for k in _ENGINES if k[0] != os.getpid()]:
-            _ENGINES.pop(k)._h = None  # the parent's handle is not ours to free
-        eng = _native.Engine(device)
-        _ENGINES[key] = eng
+    with _ENGINES_LOCK:
+        eng = _ENGINES.get(key)
+        if eng is None:
+            for k in [k for k in _ENGINES if k[0] != os.getpid()]:
+                _ENGINES.pop(k)._h = None  # the parent's handle is not ours to free
+            eng = _native.Engine(device)
+            eng.lock = threading.RLock()
+            _ENGINES[key] = eng
     return eng
 
 
@@ -493,42 +501,43 @@ class HybridHistGBMNumbaV1_0_1:
         if self.scale_pos_weight is not None and self.objective in ('binary', 'binary_focal'):
             sample_weight = np.ones(len(y), dtype=np.float64)
             sample_weight[y == 1] = self.scale_pos_weight
-        t0 = time.perf_counter()
         eng = _engine(self._device_index())
-        # Unweighted edges come from the device (X is staged once and binned
-        # from there); the weighted-quantile branch stays on the host.
-        X = np.ascontiguousarray(X)
-        staged = sample_weight is None
-        if staged:
-            eng.stage_features(X)
-        try:
-            self.bin_edges, self.feature_bin_counts = self._build_bin_edges(
-                X, sample_weight=sample_weight, eng=eng if staged else None)
-            self._max_bins = int(np.max(self.feature_bin_counts))
-            if self._max_bins > 257:
-                raise NotImplementedError(
-                    f"n_bins={self.n_bins} gives {self._max_bins} bins for some feature; "
-                    "the MI355X engine holds at most 257 bins per feature (n_bins <= 256)")
+        with eng.lock:
+            t0 = time.perf_counter()
+            # Unweighted edges come from the device (X is staged once and binned
+            # from there); the weighted-quantile branch stays on the host.
+            X = np.ascontiguousarray(X)
+            staged = sample_weight is None
             if staged:
-                eng.bin_staged(0, X.shape[0], X.shape[1], X.dtype == np.float64, self.bin_edges,
-                               self.feature_bin_counts, self._nan_bin_id)
-            else:
-                eng.bin_features(0, X, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
-        finally:
-            if staged:
-                eng.release_staged()
-        self.times['binning'] = (time.perf_counter() - t0) * 1000
-        n_val = 0
-        if X_val is not None and y_val is not None:
-            eng.bin_features(1, X_val, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
-            n_val = X_val.shape[0]
+                eng.stage_features(X)
+            try:
+                self.bin_edges, self.feature_bin_counts = self._build_bin_edges(
+                    X, sample_weight=sample_weight, eng=eng if staged else None)
+                self._max_bins = int(np.max(self.feature_bin_counts))
+                if self._max_bins > 257:
+                    raise NotImplementedError(
+                        f"n_bins={self.n_bins} gives {self._max_bins} bins for some feature; "
+                        "the MI355X engine holds at most 257 bins per feature (n_bins <= 256)")
+                if staged:
+                    eng.bin_staged(0, X.shape[0], X.shape[1], X.dtype == np.float64, self.bin_edges,
+                                   self.feature_bin_counts, self._nan_bin_id)
+                else:
+                    eng.bin_features(0, X, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
+            finally:
+                if staged:
+                    eng.release_staged()
+            self.times['binning'] = (time.perf_counter() - t0) * 1000
+            n_val = 0
+            if X_val is not None and y_val is not None:
+                eng.bin_features(1, X_val, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
+                n_val = X_val.shape[0]
 
-        t0_train = time.perf_counter()
-        if self._is_multiclass:
-            self._fit_multiclass(eng, y, n_val, y_val, rng)
-        else:
-            self._fit_binary(eng, y, n_val, y_val, rng)
-        self.times['training'] = (time.perf_counter() - t0_train) * 1000
+            t0_train = time.perf_counter()
+            if self._is_multiclass:
+                self._fit_multiclass(eng, y, n_val, y_val, rng)
+            else:
+                self._fit_binary(eng, y, n_val, y_val, rng)
+            self.times['training'] = (time.perf_counter() - t0_train) * 1000
 
         self._pack_trees()
         self._compute_feature_importances()
@@ -783,23 +792,24 @@ class HybridHistGBMNumbaV1_0_1:
         if X.ndim != 2 or X.shape[1] != self.n_features_in_:
             raise ValueError(f"X must have {self.n_features_in_} features")
         eng = _engine(self._device_index())
-        eng.bin_features(1, X, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
-        t0 = time.perf_counter()
-        if self._is_multiclass:
-            # est:3293-3315: per class, sum its trees from 0.0.
-            F = np.zeros((X.shape[0], self.n_classes_), dtype=np.float64)
-            for k in range(self.n_classes_):
-                if self._mc_packed[k] is not None:
-                    F[:, k] = eng.predict(1, X.shape[0], self._mc_packed[k],
-                                          len(self.mc_trees[k]), self.learning_rate)
+        with eng.lock:  # matrix slot 1 holds this call's codes until it returns
+            eng.bin_features(1, X, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
+            t0 = time.perf_counter()
+            if self._is_multiclass:
+                # est:3293-3315: per class, sum its trees from 0.0.
+                F = np.zeros((X.shape[0], self.n_classes_), dtype=np.float64)
+                for k in range(self.n_classes_):
+                    if self._mc_packed[k] is not None:
+                        F[:, k] = eng.predict(1, X.shape[0], self._mc_packed[k],
+                                              len(self.mc_trees[k]), self.learning_rate)
+                self.times['inference'] = (time.perf_counter() - t0) * 1000
+                return F
+            packed = {'features': self._packed_features, 'thresholds': self._packed_thresholds,
+                      'values': self._packed_values, 'left': self._packed_left,
+                      'right': self._packed_right, 'offsets': self._tree_offsets}
+            F = eng.predict(1, X.shape[0], packed, len(self.trees),
+                            self.learning_rate) + getattr(self, 'base_score_', 0.0)
             self.times['inference'] = (time.perf_counter() - t0) * 1000
-            return F
-        packed = {'features': self._packed_features, 'thresholds': self._packed_thresholds,
-                  'values': self._packed_values, 'left': self._packed_left,
-                  'right': self._packed_right, 'offsets': self._tree_offsets}
-        F = eng.predict(1, X.shape[0], packed, len(self.trees),
-                        self.learning_rate) + getattr(self, 'base_score_', 0.0)
-        self.times['inference'] = (time.perf_counter() - t0) * 1000
         return F
 
     def predict_proba(self, X):

@@ -852,9 +852,18 @@ struct Sampler {
       if (error.empty()) error = msg;
       stop = true;
     }
-    halt.store(true);
+    set_halt();
     cv.notify_all();
     seg_cv.notify_all();
+  }
+
+  // halt and ring_floor change under ring_mu, so the twister cannot miss
+  // the wake-up between its predicate check and its wait.
+  void set_halt() {
+    {
+      std::lock_guard<std::mutex> lk(ring_mu);
+      halt.store(true);
+    }
     ring_cv.notify_all();
   }
 
@@ -995,7 +1004,10 @@ struct Sampler {
 
   void set_floor(int64_t c) {
     if (ring_floor.load(std::memory_order_relaxed) >= c) return;
-    ring_floor.store(c, std::memory_order_release);
+    {
+      std::lock_guard<std::mutex> lk(ring_mu);
+      ring_floor.store(c, std::memory_order_release);
+    }
     ring_cv.notify_all();
   }
 
@@ -1358,8 +1370,7 @@ struct Sampler {
     }
     cv.notify_all();
     seg_cv.notify_all();
-    halt.store(true);
-    ring_cv.notify_all();
+    set_halt();
     if (draw_thread.joinable()) draw_thread.join();
     if (twister.joinable()) twister.join();
     for (auto &w : workers)

@@ -10,6 +10,7 @@ from sklearn.datasets import make_classification
 from sklearn.metrics import accuracy_score
 
 from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+from conftest import make_data
 
 pytestmark = pytest.mark.gpu
 
@@ -122,3 +123,42 @@ def test_feature_importances(engine, bin_data):
     assert m.feature_importances_.shape == (10,)
     np.testing.assert_allclose(m.feature_importances_.sum(), 1.0)
     assert m.feature_split_counts_.sum() == sum(int((t[0][:t[5]] >= 0).sum()) for t in m.trees)
+
+
+def test_threads_fit_and_predict_concurrently():
+    """Estimators share the device's engine; fits and predictions from two
+    threads at once give what they give one after the other."""
+    import threading
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    data = [make_data(20000, 10, seed=s, nan_frac=0.05) for s in (41, 42)]
+    params = [dict(n_estimators=15, max_depth=5, random_state=0, verbose=False),
+              dict(n_estimators=12, max_depth=4, n_bins=100, random_state=3, verbose=False)]
+    seq = [HybridHistGBMNumbaV1_0_1(**p).fit(X, y) for p, (X, y) in zip(params, data)]
+    want = [m.predict_proba(X) for m, (X, _) in zip(seq, data)]
+    for rep in range(3):
+        out, errors = [None, None], []
+
+        def work(i):
+            try:
+                X, y = data[i]
+                m = HybridHistGBMNumbaV1_0_1(**params[i]).fit(X, y)
+                out[i] = (m, m.predict_proba(X), seq[1 - i].predict_proba(data[1 - i][0]))
+            except Exception as e:  # noqa: BLE001 - reported below
+                errors.append(e)
+
+        threads = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        assert not errors, errors
+        for i in range(2):
+            m, p, p_other = out[i]
+            assert m.train_loss_history_ == seq[i].train_loss_history_, (rep, i)
+            for a, b in zip(m.trees, seq[i].trees):
+                nc = a[5]
+                assert nc == b[5]
+                np.testing.assert_array_equal(a[0][:nc], b[0][:nc])
+                np.testing.assert_array_equal(a[1][:nc], b[1][:nc])
+            np.testing.assert_array_equal(p, want[i])
+            np.testing.assert_array_equal(p_other, want[1 - i])
