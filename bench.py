@@ -7,8 +7,11 @@ round ends with a stream synchronisation, so wall-clock time over the K
 rounds is the device time including host work.
 
 Prints one JSON line with the fit rate (trees/s), the histogram kernel's
-roofline (algorithmic bytes per launch over its average HIP-event duration,
-against 8 TB/s HBM) and the oracle's CPU rate on a bounded sample.
+roofline (algorithmic bytes per launch over its average execution time,
+from events recorded by each launch's own dispatch, against 8 TB/s HBM),
+prediction through the workload's full ensemble with its own roofline, a
+rounds-only block for the 10M x 50 workload and the oracle's CPU rate on a
+bounded sample.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -102,9 +105,9 @@ BREAKDOWN_ROUNDS = 5
 
 
 def measured_traffic(kernel, workload):
-    """HBM bytes per launch of `kernel` on `workload`, from the committed
-    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (copy-kernel calibrated), or None
-    when no such summary exists."""
+    """HBM bytes per launch of `kernel` on `workload` and the file they come
+    from: the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary (copy-kernel
+    calibrated), or (None, None) when no such summary exists."""
     import glob
     import re
     pat = re.compile(r"^traffic_bytes_per_launch\[%s, %s\]: (\d+)\s*$"
@@ -114,8 +117,8 @@ def measured_traffic(kernel, workload):
             for line in fh:
                 m = pat.match(line)
                 if m:
-                    return int(m.group(1))
-    return None
+                    return int(m.group(1)), os.path.relpath(path, ROOT)
+    return None, None
 
 
 def run_gpu(name, steps, warmup, rounds_only=False):
@@ -154,15 +157,8 @@ def run_gpu(name, steps, warmup, rounds_only=False):
     _progress(f"fit done in {t_fit:.1f} s (binning {est.times['binning']:.0f} ms)")
     elapsed = marks["t1"] - marks["t0"]
     st = marks["stats"]
-    t_pred_total, pred_rows, fit_full = None, 0, None
+    predict, fit_full = None, None
     if not rounds_only:
-        # Prediction on fresh rows through the fitted trees.
-        Xp, _, _ = make_workload(name, predict=True)
-        t = time.perf_counter()
-        est.predict_proba(Xp)
-        t_pred_total = time.perf_counter() - t
-        pred_rows = len(Xp)
-        _progress(f"predict_proba on {len(Xp)} rows in {t_pred_total:.2f} s")
         # A complete fit with the workload's own n_estimators: bin edges,
         # binning and every boosting round, from host float32 X.
         full = HybridHistGBMNumbaV1_0_1(**full_params)
@@ -174,13 +170,80 @@ def run_gpu(name, steps, warmup, rounds_only=False):
                         binning_ms=round(full.times["binning"], 1),
                         training_ms=round(full.times["training"], 1))
         _progress(f"full fit: {fit_full}")
+        predict = run_predict(full, name)
     s0, s1 = marks["s0"], marks["s1"]
     sampler = {k: (s1[k] - s0[k]) / max(s1["rounds"] - s0["rounds"], 1)
                for k in ("draw_ms", "gen_ms")}
     return dict(est=est, n=n, F=F, elapsed=elapsed, stats=st, t_fit=t_fit,
-                breakdown=marks["breakdown"], sampler=sampler,
-                t_pred_total=t_pred_total, pred_rows=pred_rows, fit_full=fit_full,
-                t_pred_dev=est.times.get("inference", 0.0) / 1e3, params=params)
+                breakdown=marks["breakdown"], sampler=sampler, predict=predict,
+                fit_full=fit_full, params=params)
+
+
+def run_predict(model, name, repeats=3):
+    """predict_proba of a fresh batch of the workload through the model's
+    whole ensemble: rows/s end to end (host float32 in, probabilities out)
+    and per k_predict launch (kernel execution time), with the kernel's
+    roofline over the algorithmic bytes n * (F + 16) of device-resident
+    codes (one code byte per feature, 8 B of output and 8 B of F per row)."""
+    from bsscl_gbm import estimator as est_mod
+    Xp, _, _ = make_workload(name, predict=True)
+    n, F = Xp.shape
+    eng = est_mod._engine(0)
+    model.predict_proba(Xp)  # warm-up
+    eng.set_profiling(1)
+    t = time.perf_counter()
+    for _ in range(repeats):
+        model.predict_proba(Xp)
+    t_total = (time.perf_counter() - t) / repeats
+    st = eng.stats()
+    eng.set_profiling(0)
+    launches = max(st["predict_launches"], 1.0)
+    kernel_s = st["predict_ms"] / 1e3 / launches
+    bytes_ = n * (F + 16)
+    achieved = bytes_ / kernel_s / 1e9
+    _progress(f"predict: {n} rows x {len(model.trees)} trees, kernel {1e3 * kernel_s:.2f} ms, "
+              f"end to end {1e3 * t_total:.1f} ms")
+    return {
+        "rows": n, "trees": len(model.trees),
+        "rows_per_s": round(n / kernel_s),
+        "rows_per_s_end_to_end": round(n / t_total),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "k_predict",
+                     "avg_launch_us": round(1e6 * kernel_s, 1), "bytes_per_launch": bytes_},
+    }
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def hist_roofline(st, workload):
+    hist_s = st["hist_ms"] / 1e3
+    achieved = st["hist_bytes"] / hist_s / 1e9 if hist_s > 0 else 0.0
+    launches = max(st["hist_launches"], 1.0)
+    traffic, source = measured_traffic("k_hist", workload)
+    return {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": traffic,
+        "traffic_source": source,
+        "kernel": "k_hist",
+        "timing": "kernel execution, events recorded by each launch's own dispatch",
+        "launches": int(st["hist_launches"]),
+        "avg_launch_us": round(1e3 * st["hist_ms"] / launches, 2),
+        "bytes_per_launch": round(st["hist_bytes"] / launches),
+    }
 
 
 def run_cpu_baseline(name, rounds):
@@ -199,7 +262,7 @@ def run_cpu_baseline(name, rounds):
     if omp and omp.isdigit():
         cores = min(cores, int(omp))
     return dict(value=float(len(t) / t.sum()), unit="trees/s", cores=cores,
-                kind="port",
+                cpu_model=cpu_model(), kind="port",
                 sample=f"rounds 2-{rounds + 1} of the same {name} fit "
                        f"({X.shape[0]}x{X.shape[1]}), oracle/oracle.c via OracleGBM")
 
@@ -214,6 +277,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--rounds-only", action="store_true",
                     help="skip the prediction and the end-to-end fit (profiler runs)")
+    ap.add_argument("--also", default="stress_10m",
+                    help="workload of the extra rounds-only block ('' for none)")
+    ap.add_argument("--also-steps", type=int, default=10)
     a = ap.parse_args()
     if a.gpus != 1:
         print(json.dumps({"error": "this engine runs on one GPU; --gpus must be 1 "
@@ -224,8 +290,6 @@ def main():
     bd = r["breakdown"]
     trees_per_s = a.steps / r["elapsed"]
     hist_s = st["hist_ms"] / 1e3
-    achieved = st["hist_bytes"] / hist_s / 1e9 if hist_s > 0 else 0.0
-    launches = max(st["hist_launches"], 1.0)
     line = {
         "metric": METRIC,
         "value": round(trees_per_s, 3),
@@ -247,23 +311,9 @@ def main():
             "subsample": r["est"].subsample, "colsample_bytree": r["est"].colsample_bytree,
             "parallelism": "single GPU",
         },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic("k_hist", a.workload),
-            "kernel": "k_hist",
-            "launches": int(st["hist_launches"]),
-            "avg_launch_us": round(1e3 * st["hist_ms"] / launches, 2),
-            "bytes_per_launch": round(st["hist_bytes"] / launches),
-        },
+        "roofline": hist_roofline(st, a.workload),
         "hist_rows_x_features_per_s": round(st["hist_row_features"] / hist_s) if hist_s > 0 else None,
-        "predict_rows_per_s": (round(r["pred_rows"] / r["t_pred_dev"])
-                               if r["pred_rows"] and r["t_pred_dev"] > 0 else None),
-        "predict_rows_per_s_end_to_end": (round(r["pred_rows"] / r["t_pred_total"])
-                                          if r["pred_rows"] else None),
+        "predict": r["predict"],
         "kernel_ms_per_step": {  # every group timed, rounds after the timed region
             "hist": round(bd["hist_ms"] / BREAKDOWN_ROUNDS, 3),
             "partition": round(bd["part_ms"] / BREAKDOWN_ROUNDS, 3),
@@ -280,6 +330,23 @@ def main():
             "sampler_gen": round(r["sampler"]["gen_ms"], 3),
         },
     }
+    if a.also and a.also != a.workload:
+        r2 = run_gpu(a.also, a.also_steps, a.warmup, rounds_only=True)
+        st2 = r2["stats"]
+        line[a.also] = {
+            "trees_per_s": round(a.also_steps / r2["elapsed"], 3),
+            "ms_per_step": round(1e3 * r2["elapsed"] / a.also_steps, 3),
+            "steps": a.also_steps,
+            "config": {"rows": r2["n"], "features": r2["F"],
+                       "max_depth": r2["params"]["max_depth"],
+                       "max_leaves": int(r2["est"].max_leaves),
+                       "subsample": r2["est"].subsample,
+                       "colsample_bytree": r2["est"].colsample_bytree},
+            "roofline": hist_roofline(st2, a.also),
+            "kernel_ms_per_step": {k: round(r2["breakdown"][f"{k}_ms"] / BREAKDOWN_ROUNDS, 3)
+                                   for k in ("hist", "part", "split")},
+        }
+        del r2
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = run_cpu_baseline(a.workload, a.cpu_rounds)
     print(json.dumps(line), flush=True)

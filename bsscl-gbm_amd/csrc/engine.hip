@@ -376,7 +376,7 @@ struct bsscl_engine {
     uint64_t seq;  // boosting round that recorded them
   };
   std::vector<Pending> pending;
-  double stats[16] = {0};
+  double stats[18] = {0};
 };
 
 namespace bsscl {
@@ -411,6 +411,21 @@ int prof_begin(bsscl_engine *E, int kind, hipEvent_t *stop) {
   return BSSCL_OK;
 }
 
+// The start/stop events of one timed kernel of `kind` (0 histogram, 4
+// prediction), recorded by that kernel's own dispatch
+// (hipExtLaunchKernelGGL), so the time is the kernel's execution alone;
+// null events when not profiling.
+int prof_kernel(bsscl_engine *E, int kind, hipEvent_t *start, hipEvent_t *stop) {
+  *start = *stop = nullptr;
+  if (E->prof < 1) return BSSCL_OK;
+  hipEvent_t a, b;
+  CHK(ev_pair(E, a, b));
+  E->pending.push_back({a, b, kind, E->round_seq});
+  *start = a;
+  *stop = b;
+  return BSSCL_OK;
+}
+
 int prof_end(bsscl_engine *E, hipEvent_t stop) {
   if (stop) HIPCHK(hipEventRecord(stop, E->st));
   return BSSCL_OK;
@@ -427,7 +442,7 @@ int prof_collect(bsscl_engine *E, uint64_t upto = UINT64_MAX) {
     }
     float ms = 0.f;
     HIPCHK(hipEventElapsedTime(&ms, p.a, p.b));
-    const int slot = p.kind == 0 ? 0 : p.kind == 1 ? 4 : p.kind == 2 ? 6 : 12;
+    const int slot = p.kind == 0 ? 0 : p.kind == 1 ? 4 : p.kind == 2 ? 6 : p.kind == 4 ? 16 : 12;
     E->stats[slot] += 1.0;
     E->stats[slot + 1] += (double)ms;
     E->ev_free.push_back(p.a);
@@ -957,14 +972,13 @@ int launch_root(bsscl_engine *E, const int32_t *rows32, int64_t m,
                               E->codes_c[b].p, E->ld_c, E->gh_c[b].p,
                               E->track_rid && b == 0 ? E->rid_c[0].p : nullptr,
                               E->ld_c, E->segs.p, E->hist_node_d.p));
-  hipEvent_t stop;
-  CHK(prof_begin(E, 0, &stop));
+  hipEvent_t start, stop;
+  CHK(prof_kernel(E, 0, &start, &stop));
   HIPCHK(launch_hist(E->st, E->codes_c[b].p, E->ld_c, E->gh_c[b].p,
                      reinterpret_cast<const HistTask *>(dv[kPackHist]), E->plan_d, n_hist,
                      E->hist_node_d.p, reinterpret_cast<const int32_t *>(dv[kPackTasks]), E->segs.p,
                      E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel), E->hist_copies,
-                     E->part_d.p, E->pool.p, E->node_stride));
-  CHK(prof_end(E, stop));
+                     E->part_d.p, E->pool.p, E->node_stride, start, stop));
   CHK(prof_begin(E, 3, &stop));
   HIPCHK(launch_hist_reduce(E->st, E->plan_d, 1, reinterpret_cast<const int32_t *>(dv[kPackTasks]),
                             E->hist_node_d.p, E->segs.p, E->part_d.p, F_sel, E->pool.p,
@@ -1064,12 +1078,14 @@ int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
     return BSSCL_OK;
   }
   const int32_t H = (int32_t)std::min<int64_t>(E->hist_cap, (int64_t)hist_target(E, F_sel) + 2 * (int64_t)P + 2);
-  CHK(prof_begin(E, 0, &stop));
-  HIPCHK(launch_hist(E->st, E->codes_c[dst].p, E->ld_c, E->gh_c[dst].p, E->hist_tasks_d.p,
-                     E->plan_d, H, E->hist_node_d.p, E->hist_begin_d.p, E->segs.p,
-                     E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel), E->hist_copies,
-                     E->part_d.p, E->pool.p, E->node_stride));
-  CHK(prof_end(E, stop));
+  {
+    hipEvent_t start, kstop;
+    CHK(prof_kernel(E, 0, &start, &kstop));
+    HIPCHK(launch_hist(E->st, E->codes_c[dst].p, E->ld_c, E->gh_c[dst].p, E->hist_tasks_d.p,
+                       E->plan_d, H, E->hist_node_d.p, E->hist_begin_d.p, E->segs.p,
+                       E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel), E->hist_copies,
+                       E->part_d.p, E->pool.p, E->node_stride, start, kstop));
+  }
   CHK(prof_begin(E, 3, &stop));
   HIPCHK(launch_hist_reduce(E->st, E->plan_d, P, E->hist_begin_d.p, E->hist_node_d.p,
                             E->segs.p, E->part_d.p, F_sel, E->pool.p, E->node_stride));
@@ -2411,8 +2427,10 @@ int bsscl_predict(bsscl_engine *E, int32_t slot, const int16_t *features,
   CHK(upload(E, E->tree_d, nodes.data(), nodes.size()));
   CHK(upload(E, E->offsets_d, offs.data(), offs.size()));
   CHK(E->out_d.ensure((size_t)M.n));
+  hipEvent_t start, stop;
+  CHK(prof_kernel(E, 4, &start, &stop));
   HIPCHK(launch_predict(E->st, M.codes.p, M.ld, M.n, E->tree_d.p, E->offsets_d.p,
-                        n_trees, learning_rate, E->out_d.p));
+                        n_trees, learning_rate, E->out_d.p, start, stop));
   HIPCHK(hipMemcpyAsync(out_F, E->out_d.p, (size_t)M.n * 8, hipMemcpyDeviceToHost, E->st));
   CHK(sync(E));
   return BSSCL_OK;
@@ -2670,7 +2688,7 @@ int bsscl_engine_set_profiling(bsscl_engine *E, int32_t on) {
 
 int bsscl_engine_stats(bsscl_engine *E, double *out, int32_t cap, int32_t *n_out) {
   if (!E || !out || !n_out) return set_error(BSSCL_EINVAL, "null argument");
-  const int32_t n = std::min<int32_t>(cap, 16);
+  const int32_t n = std::min<int32_t>(cap, 18);
   for (int32_t i = 0; i < n; ++i) out[i] = E->stats[i];
   *n_out = n;
   return BSSCL_OK;

@@ -230,7 +230,8 @@ hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int32_t *nb_sel, const int32_t *hot_sel,
                        int32_t F_sel, int32_t fchunk, int32_t copies,
                        unsigned long long *part, unsigned long long *pool,
-                       int64_t node_stride);
+                       int64_t node_stride, hipEvent_t ev_start = nullptr,
+                       hipEvent_t ev_stop = nullptr);
 // Sums the partials that launch_hist stored for each node with a histogram
 // task (hist_begin: a node's tasks, hist_node: its id) into the pool.
 hipError_t launch_hist_reduce(hipStream_t st, const LevelPlan *plan, int32_t max_refs,
@@ -317,7 +318,8 @@ hipError_t launch_pack_trees(hipStream_t st, const int16_t *features, const int6
 hipError_t launch_predict(hipStream_t st, const uint8_t *codes, int64_t ld,
                           int64_t n, const TreeNodeDev *nodes,
                           const int32_t *offsets, int32_t n_trees, double lr,
-                          double *out);
+                          double *out, hipEvent_t ev_start = nullptr,
+                          hipEvent_t ev_stop = nullptr);
 
 int update_F_blocks(int64_t n);
 

@@ -13,6 +13,8 @@
 // trees do not depend on atomic order or on the order of rows.
 #include "kernels.h"
 
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 
 namespace bsscl {
@@ -825,12 +827,13 @@ hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int32_t *nb_sel, const int32_t *hot_sel,
                        int32_t F_sel, int32_t fchunk, int32_t copies,
                        unsigned long long *part, unsigned long long *pool,
-                       int64_t node_stride) {
+                       int64_t node_stride, hipEvent_t ev_start, hipEvent_t ev_stop) {
   if (max_tasks <= 0) return hipSuccess;
   const int32_t nchunks = (F_sel + fchunk - 1) / fchunk;
   const dim3 grid((unsigned)hist_blocks(max_tasks, nchunks));
 #define BSSCL_HIST(FC, C)                                                              \
-  hipLaunchKernelGGL((k_hist<FC, C>), grid, dim3(kHistBlock), 0, st, codes_c, ld_c, gh_c, \
+  hipExtLaunchKernelGGL((k_hist<FC, C>), grid, dim3(kHistBlock), 0, st, ev_start, ev_stop, 0, \
+                        codes_c, ld_c, gh_c, \
                      tasks, plan, hist_node, hist_begin, segs, nb_sel, hot_sel, F_sel, \
                      nchunks, part, pool, node_stride)
   // LDS per block: fchunk * copies * 8 KB (at most 32 KB).
@@ -2933,10 +2936,10 @@ hipError_t launch_pack_trees(hipStream_t st, const int16_t *features, const int6
 hipError_t launch_predict(hipStream_t st, const uint8_t *codes, int64_t ld,
                           int64_t n, const TreeNodeDev *nodes,
                           const int32_t *offsets, int32_t n_trees, double lr,
-                          double *out) {
+                          double *out, hipEvent_t ev_start, hipEvent_t ev_stop) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_predict, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                     st, codes, ld, n, nodes, offsets, n_trees, lr, out);
+  hipExtLaunchKernelGGL(k_predict, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                        ev_start, ev_stop, 0, codes, ld, n, nodes, offsets, n_trees, lr, out);
   return hipGetLastError();
 }
 

@@ -288,11 +288,10 @@ void bsscl_sampler_destroy(bsscl_sampler *s);
 
 /*
  * Timing of the engine's own kernels, taken with HIP events on the engine's
- * stream while profiling is on: level 1 times the histogram kernel only,
- * level 2 also the partition and split groups (0 turns it off).  No
- * reference counterpart (the reference records only wall times, est:1904).
- * bsscl_engine_stats fills up to `cap`
- * doubles in this order:
+ * stream while profiling is on: level 1 times the histogram and prediction
+ * kernels only, level 2 also the partition and split groups (0 turns it
+ * off).  No reference counterpart (the reference records only wall times,
+ * est:1904).  bsscl_engine_stats fills up to `cap` doubles in this order:
  *   [0] histogram launches   [1] histogram ms (sum of launch durations)
  *   [2] histogram rows x features  [3] histogram algorithmic bytes
  *   [4] partition launches   [5] partition ms
@@ -302,7 +301,10 @@ void bsscl_sampler_destroy(bsscl_sampler *s);
  *   [11] host ms in bsscl_boost_round (whole rounds)
  *   [12] histogram-reduction launches  [13] histogram-reduction ms
  *   [14] host ms enqueueing rounds     [15] host ms waiting for a round's results
- * and returns the number written in *n_out.
+ *   [16] prediction launches (bsscl_predict)  [17] prediction ms
+ * and returns the number written in *n_out.  Histogram and prediction times
+ * are each kernel's execution, from events recorded by its own dispatch;
+ * the other groups are bracketed by event pairs on the stream.
  */
 int bsscl_engine_set_profiling(bsscl_engine *eng, int32_t on);
 int bsscl_engine_stats(bsscl_engine *eng, double *out, int32_t cap,
