@@ -28,6 +28,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <chrono>
 #include <cmath>
 #include <cstdlib>
@@ -216,7 +217,8 @@ constexpr size_t kScrVal = kScrThr + align256(sizeof(int64_t) * kNoAllocMaxNodes
 constexpr size_t kScrLeft = kScrVal + align256(sizeof(double) * kNoAllocMaxNodes);
 constexpr size_t kScrRight = kScrLeft + align256(sizeof(int32_t) * kNoAllocMaxNodes);
 constexpr size_t kScrOffs = kScrRight + align256(sizeof(int32_t) * kNoAllocMaxNodes);
-constexpr size_t kScratchBytes = kScrOffs + align256(sizeof(int32_t) * (kNoAllocMaxTrees + 1));
+constexpr size_t kScrChunks = kScrOffs + align256(sizeof(int32_t) * (kNoAllocMaxTrees + 1));
+constexpr size_t kScratchBytes = kScrChunks + align256(sizeof(int32_t) * (kNoAllocMaxTrees + 1));
 static_assert(kScratchBytes <= (7u << 20), "noalloc scratch stays under 7 MiB");
 constexpr int kMaxDevices = 64;
 }  // namespace
@@ -2399,6 +2401,7 @@ int bsscl_predict(bsscl_engine *E, int32_t slot, const int16_t *features,
   const Matrix &M = E->mat[slot];
   const int32_t total = n_trees > 0 ? offsets[n_trees] : 0;
   std::vector<TreeNodeDev> nodes((size_t)std::max(total, 1));
+  bool adjacent = true;  // every right child is its left child + 1
   for (int32_t t = 0; t < n_trees; ++t) {
     const int32_t a = offsets[t], b = offsets[t + 1];
     if (a < 0 || b <= a || b > total) return set_error(BSSCL_EINVAL, "predict: bad offsets");
@@ -2410,6 +2413,7 @@ int bsscl_predict(bsscl_engine *E, int32_t slot, const int16_t *features,
         const int32_t l = left[i], r = right[i];
         if (d.feature >= M.F || l < 0 || r < 0 || l >= b - a || r >= b - a || l <= i - a || r <= i - a)
           return set_error(BSSCL_EINVAL, "predict: malformed tree " + std::to_string(t));
+        adjacent = adjacent && r == l + 1;
         int64_t thr = thresholds[i];
         split_to_engine(M, d.feature, thr);
         d.threshold = (int32_t)std::max<int64_t>(-1, std::min<int64_t>(thr, 1 << 20));
@@ -2423,14 +2427,27 @@ int bsscl_predict(bsscl_engine *E, int32_t slot, const int16_t *features,
     }
   }
   CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 8u << 20)));
+  // The offsets, then (for the LDS-staged kernel) the runs of whole trees it
+  // stages at a time.
+  int32_t max_nodes = 0;
+  for (int32_t t = 0; t < n_trees; ++t) max_nodes = std::max(max_nodes, offsets[t + 1] - offsets[t]);
+  // (Test hook BSSCL_TEST_PREDICT_GLOBAL=1: every row walks the trees in HBM.)
+  const bool staged = n_trees > 0 && predict_staged_ok(M.cols(), max_nodes, adjacent) &&
+                      !std::getenv("BSSCL_TEST_PREDICT_GLOBAL");
   std::vector<int32_t> offs(offsets, offsets + n_trees + 1);
+  int32_t n_chunks = 0;
+  if (staged) {
+    offs.resize(2 * ((size_t)n_trees + 1));
+    n_chunks = predict_chunks(offsets, n_trees, offs.data() + n_trees + 1);
+  }
   CHK(upload(E, E->tree_d, nodes.data(), nodes.size()));
   CHK(upload(E, E->offsets_d, offs.data(), offs.size()));
   CHK(E->out_d.ensure((size_t)M.n));
   hipEvent_t start, stop;
   CHK(prof_kernel(E, 4, &start, &stop));
-  HIPCHK(launch_predict(E->st, M.codes.p, M.ld, M.n, E->tree_d.p, E->offsets_d.p,
-                        n_trees, learning_rate, E->out_d.p, start, stop));
+  HIPCHK(launch_predict(E->st, M.codes.p, M.ld, M.n, M.cols(), E->tree_d.p, E->offsets_d.p,
+                        n_trees, staged ? E->offsets_d.p + n_trees + 1 : nullptr, n_chunks,
+                        learning_rate, E->out_d.p, start, stop));
   HIPCHK(hipMemcpyAsync(out_F, E->out_d.p, (size_t)M.n * 8, hipMemcpyDeviceToHost, E->st));
   CHK(sync(E));
   return BSSCL_OK;
@@ -2458,6 +2475,7 @@ int bsscl_predict_noalloc(bsscl_engine *E, int32_t slot, const int16_t *features
                                        " nodes exceed the fixed scratch (at most " +
                                        std::to_string(kNoAllocMaxNodes) + ")");
   // The same checks as bsscl_predict: every traversal stays in its tree.
+  bool adjacent = true;  // every right child is its left child + 1
   for (int32_t t = 0; t < n_trees; ++t) {
     const int32_t a = offsets[t], b = offsets[t + 1];
     if (a < 0 || b <= a || b > total) return set_error(BSSCL_EINVAL, "predict_noalloc: bad offsets");
@@ -2467,6 +2485,7 @@ int bsscl_predict_noalloc(bsscl_engine *E, int32_t slot, const int16_t *features
       if (features[i] >= M.F || l < 0 || r < 0 || l >= b - a || r >= b - a || l <= i - a ||
           r <= i - a)
         return set_error(BSSCL_EINVAL, "predict_noalloc: malformed tree " + std::to_string(t));
+      adjacent = adjacent && r == l + 1;
     }
   }
   HIPCHK(hipSetDevice(E->device));
@@ -2497,8 +2516,26 @@ int bsscl_predict_noalloc(bsscl_engine *E, int32_t slot, const int16_t *features
                              reinterpret_cast<const int32_t *>(S + kScrRight), total,
                              M.top ? M.F : 0, nodes));
   }
-  HIPCHK(launch_predict(E->st, M.codes.p, M.ld, M.n, nodes, offs, n_trees, learning_rate,
-                        out_F_dev));
+  // The LDS-staged kernel's runs of whole trees (host list on the stack; the
+  // copy has finished when the call returns).
+  int32_t max_nodes = 0;
+  for (int32_t t = 0; t < n_trees; ++t) max_nodes = std::max(max_nodes, offsets[t + 1] - offsets[t]);
+  const bool staged = n_trees > 0 && predict_staged_ok(M.cols(), max_nodes, adjacent) &&
+                      !std::getenv("BSSCL_TEST_PREDICT_GLOBAL");
+  int32_t n_chunks = 0;
+  int32_t *chunks_d = reinterpret_cast<int32_t *>(S + kScrChunks);
+  if (staged) {
+    std::array<int32_t, kNoAllocMaxTrees + 1> chunks;
+    n_chunks = predict_chunks(offsets, n_trees, chunks.data());
+    HIPCHK(hipMemcpyAsync(chunks_d, chunks.data(), ((size_t)n_chunks + 1) * 4,
+                          hipMemcpyHostToDevice, E->st));
+    HIPCHK(launch_predict(E->st, M.codes.p, M.ld, M.n, M.cols(), nodes, offs, n_trees, chunks_d,
+                          n_chunks, learning_rate, out_F_dev));
+    HIPCHK(hipStreamSynchronize(E->st));
+    return BSSCL_OK;
+  }
+  HIPCHK(launch_predict(E->st, M.codes.p, M.ld, M.n, M.cols(), nodes, offs, n_trees, nullptr, 0,
+                        learning_rate, out_F_dev));
   HIPCHK(hipStreamSynchronize(E->st));
   return BSSCL_OK;
 }

@@ -315,11 +315,21 @@ hipError_t launch_predict_tree(hipStream_t st, const uint8_t *codes,
 hipError_t launch_pack_trees(hipStream_t st, const int16_t *features, const int64_t *thresholds,
                              const double *values, const int32_t *left, const int32_t *right,
                              int32_t total, int32_t top_F, TreeNodeDev *nodes);
+// Ensemble prediction.  With `chunks` (predict_chunks' list of n_chunks
+// runs of whole trees; only when predict_staged_ok) the rows' codes and the
+// trees are staged in LDS; otherwise each row walks the trees in HBM.
+int32_t predict_chunk_nodes();
+// (right_follows_left: every split node's right child is its left child + 1.)
+bool predict_staged_ok(int32_t n_cols, int32_t max_tree_nodes, bool right_follows_left);
+// Greedy runs of whole trees of at most predict_chunk_nodes() nodes: writes
+// the first tree of each run and n_trees after the last (n_trees + 1 entries
+// at most); returns the number of runs.
+int32_t predict_chunks(const int32_t *offsets, int32_t n_trees, int32_t *chunks);
 hipError_t launch_predict(hipStream_t st, const uint8_t *codes, int64_t ld,
-                          int64_t n, const TreeNodeDev *nodes,
-                          const int32_t *offsets, int32_t n_trees, double lr,
-                          double *out, hipEvent_t ev_start = nullptr,
-                          hipEvent_t ev_stop = nullptr);
+                          int64_t n, int32_t n_cols, const TreeNodeDev *nodes,
+                          const int32_t *offsets, int32_t n_trees, const int32_t *chunks,
+                          int32_t n_chunks, double lr, double *out,
+                          hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 
 int update_F_blocks(int64_t n);
 

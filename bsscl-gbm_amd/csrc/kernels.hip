@@ -2933,13 +2933,156 @@ hipError_t launch_pack_trees(hipStream_t st, const int16_t *features, const int6
   return hipGetLastError();
 }
 
+// Ensemble prediction with the rows' codes and the trees staged in LDS.
+// A block takes kPredRows rows (two per thread, two independent walks in
+// flight): it loads their codes of every column once (16-byte loads, all
+// independent), then walks the trees a chunk at a time.  A chunk is a run of
+// whole trees of at most kPredChunk nodes (the host's list, predict_chunks),
+// copied into LDS as one 32-bit word per node plus the values.  Per row the
+// trees are added in order from 0.0, lr * value and the add rounded
+// separately, so the result is bit-identical to k_predict's.
+//
+// Node word: bits 0-8 threshold + 1 (go left when code < it; thresholds
+// clamped to [-1, 255]), bits 9-15 column (127 for a leaf), bits 16-31 the
+// left child's index in the chunk; the right child is the next node, as the
+// builder numbers them (est:686-687; the host checks every tree).
+constexpr int kPredRows = 512;
+constexpr int kPredChunk = 1024;
+constexpr int kPredMaxCols = 64;   // staged columns (7 bits, 127 marks a leaf)
+constexpr uint32_t kPredLeaf = 127u;
+
+int32_t predict_chunk_nodes() { return kPredChunk; }
+
+bool predict_staged_ok(int32_t n_cols, int32_t max_tree_nodes, bool right_follows_left) {
+  return right_follows_left && n_cols > 0 && n_cols <= kPredMaxCols &&
+         max_tree_nodes <= kPredChunk;
+}
+
+int32_t predict_chunks(const int32_t *offsets, int32_t n_trees, int32_t *chunks) {
+  int32_t nc = 0;
+  int32_t t0 = 0;
+  while (t0 < n_trees) {
+    int32_t t1 = t0 + 1;
+    while (t1 < n_trees && offsets[t1 + 1] - offsets[t0] <= kPredChunk) ++t1;
+    chunks[nc++] = t0;
+    t0 = t1;
+  }
+  chunks[nc] = n_trees;
+  return nc;
+}
+
+#pragma clang fp contract(off)
+__global__ __launch_bounds__(256) void k_predict_staged(
+    const uint8_t *__restrict__ codes, int64_t ld, int64_t n, int32_t n_cols,
+    const TreeNodeDev *__restrict__ nodes, const int32_t *__restrict__ offsets,
+    const int32_t *__restrict__ chunks, int32_t n_chunks, double lr, double *__restrict__ out) {
+  extern __shared__ uint4 sc4[];  // codes [n_cols][kPredRows]
+  __shared__ uint32_t wn[kPredChunk];
+  __shared__ double wv[kPredChunk];
+  __shared__ int32_t wt[kPredChunk];  // each staged tree's first node
+  const int tid = (int)threadIdx.x;
+  const int64_t row0 = (int64_t)blockIdx.x * kPredRows;
+  constexpr int kChunksPerCol = kPredRows / 16;
+  // Chunks past ld (the last column's padding) are never read: rows there
+  // are >= n.
+  for (int k = tid; k < n_cols * kChunksPerCol; k += 256) {
+    const int c = k / kChunksPerCol, ch = k % kChunksPerCol;
+    const int64_t r = row0 + 16 * ch;
+    if (r < ld) sc4[k] = *reinterpret_cast<const uint4 *>(codes + (int64_t)c * ld + r);
+  }
+  const uint8_t *sc0 = reinterpret_cast<const uint8_t *>(sc4) + tid;
+  const uint8_t *sc1 = sc0 + 256;
+  const bool in0 = row0 + tid < n, in1 = row0 + tid + 256 < n;
+  double F0 = 0.0, F1 = 0.0;
+  // Chunk c + 1's nodes and tree starts are loaded into registers while
+  // chunk c is walked (kPredChunk / 256 nodes and tree starts per thread).
+  constexpr int kPer = kPredChunk / 256;
+  TreeNodeDev pn[kPer];
+  int32_t pt[kPer];
+  int32_t t0 = 0, t1 = 0, base = 0, cnt = 0;
+  auto prefetch = [&](int32_t c) {
+    t0 = chunks[c];
+    t1 = chunks[c + 1];
+    base = offsets[t0];
+    cnt = offsets[t1] - base;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int k = tid + 256 * q;
+      if (k < cnt) pn[q] = nodes[base + k];
+      if (k < t1 - t0) pt[q] = offsets[t0 + k] - base;
+    }
+  };
+  if (n_chunks > 0) prefetch(0);
+  for (int32_t c = 0; c < n_chunks; ++c) {
+    const int32_t nt = t1 - t0, nn = cnt;
+    __syncthreads();  // the previous chunk's walks are done
+#pragma unroll
+    for (int q = 0; q < kPer; ++q)
+      if (tid + 256 * q < nt) wt[tid + 256 * q] = pt[q];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int k = tid + 256 * q;
+      if (k >= nn) continue;
+      const TreeNodeDev d = pn[q];
+      // The node's tree starts at the last wt <= k (binary search).
+      int lo = 0, hi = nt - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (wt[mid] <= k) lo = mid;
+        else hi = mid - 1;
+      }
+      const uint32_t col = d.feature >= 0 ? (uint32_t)d.feature : kPredLeaf;
+      const uint32_t thr1 = (uint32_t)(min(max(d.threshold, -1), 255) + 1);
+      const uint32_t left = d.feature >= 0 ? (uint32_t)(wt[lo] + d.left) : 0u;
+      wn[k] = thr1 | (col << 9) | (left << 16);
+      wv[k] = d.value;
+    }
+    __syncthreads();
+    if (c + 1 < n_chunks) prefetch(c + 1);
+    for (int32_t t = 0; t < nt; ++t) {
+      int32_t n0 = wt[t], n1 = n0;
+      uint32_t w0 = wn[n0], w1 = w0;
+      bool a0 = in0 && ((w0 >> 9) & 127u) != kPredLeaf;
+      bool a1 = in1 && ((w1 >> 9) & 127u) != kPredLeaf;
+      while (a0 || a1) {
+        if (a0) {
+          const uint32_t code = sc0[((w0 >> 9) & 127u) * kPredRows];
+          n0 = (int32_t)(w0 >> 16) + (code < (w0 & 511u) ? 0 : 1);
+          w0 = wn[n0];
+          a0 = ((w0 >> 9) & 127u) != kPredLeaf;
+        }
+        if (a1) {
+          const uint32_t code = sc1[((w1 >> 9) & 127u) * kPredRows];
+          n1 = (int32_t)(w1 >> 16) + (code < (w1 & 511u) ? 0 : 1);
+          w1 = wn[n1];
+          a1 = ((w1 >> 9) & 127u) != kPredLeaf;
+        }
+      }
+      F0 = __dadd_rn(F0, __dmul_rn(lr, wv[n0]));
+      F1 = __dadd_rn(F1, __dmul_rn(lr, wv[n1]));
+    }
+  }
+  if (in0) out[row0 + tid] = F0;
+  if (in1) out[row0 + tid + 256] = F1;
+}
+#pragma clang fp contract(on)
+
 hipError_t launch_predict(hipStream_t st, const uint8_t *codes, int64_t ld,
-                          int64_t n, const TreeNodeDev *nodes,
-                          const int32_t *offsets, int32_t n_trees, double lr,
-                          double *out, hipEvent_t ev_start, hipEvent_t ev_stop) {
+                          int64_t n, int32_t n_cols, const TreeNodeDev *nodes,
+                          const int32_t *offsets, int32_t n_trees, const int32_t *chunks,
+                          int32_t n_chunks, double lr, double *out, hipEvent_t ev_start,
+                          hipEvent_t ev_stop) {
   if (n <= 0) return hipSuccess;
-  hipExtLaunchKernelGGL(k_predict, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                        ev_start, ev_stop, 0, codes, ld, n, nodes, offsets, n_trees, lr, out);
+  if (chunks) {
+    const size_t lds = (size_t)n_cols * kPredRows;
+    hipExtLaunchKernelGGL(k_predict_staged, dim3((unsigned)((n + kPredRows - 1) / kPredRows)),
+                          dim3(256), lds, st, ev_start, ev_stop, 0, codes, ld, n, n_cols, nodes,
+                          offsets, chunks, n_chunks, lr, out);
+  } else {
+    hipExtLaunchKernelGGL(k_predict, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                          ev_start, ev_stop, 0, codes, ld, n, nodes, offsets, n_trees, lr, out);
+  }
   return hipGetLastError();
 }
 

@@ -258,6 +258,47 @@ def test_predict_matches_oracle(engine):
     np.testing.assert_allclose(F, om.predict_all_trees(Xb, m._packed, len(m.trees), 0.1), rtol=0, atol=1e-12)
 
 
+def _swap_first_children(packed, t):
+    """Tree t of a packed model with nodes 1 and 2 exchanged: the root's right
+    child then precedes its left child (same tree, other numbering)."""
+    p = {k: np.array(v, copy=True) for k, v in packed.items()}
+    a = int(p["offsets"][t])
+    i1, i2 = a + 1, a + 2
+    for k in ("features", "thresholds", "values", "left", "right"):
+        p[k][[i1, i2]] = p[k][[i2, i1]]
+    for k in ("left", "right"):
+        seg = p[k][a:int(p["offsets"][t + 1])]
+        one, two = seg == 1, seg == 2
+        seg[one], seg[two] = 2, 1
+    return p
+
+
+def test_predict_kernels_agree(engine, monkeypatch):
+    """The LDS-staged ensemble kernel (several tree runs per block) and the
+    HBM walk give bit-identical F; a tree numbered with the right child first
+    takes the HBM walk and still predicts the oracle's F (est:863-884)."""
+    _announce("predict kernels")
+    X, y = make_data(30000, 24, seed=21, nan_frac=0.05)
+    m = om.OracleGBM(n_estimators=60, max_depth=6, learning_rate=0.1, n_bins=255,
+                     class_weight=None, random_state=4).fit(X, y)
+    Xb = m.X_bin_
+    engine.load_codes(0, Xb)
+    n_t = len(m.trees)
+    assert int(m._packed["offsets"][n_t]) > 2048  # several runs of whole trees
+    want = om.predict_all_trees(Xb, m._packed, n_t, 0.1)
+    staged = engine.predict(0, len(X), m._packed, n_t, 0.1)
+    monkeypatch.setenv("BSSCL_TEST_PREDICT_GLOBAL", "1")
+    walked = engine.predict(0, len(X), m._packed, n_t, 0.1)
+    monkeypatch.delenv("BSSCL_TEST_PREDICT_GLOBAL")
+    np.testing.assert_array_equal(staged, walked)
+    np.testing.assert_allclose(staged, want, rtol=0, atol=1e-12)
+    swapped = _swap_first_children(m._packed, 5)
+    assert swapped["right"][int(swapped["offsets"][5])] + 1 == swapped["left"][int(swapped["offsets"][5])]
+    np.testing.assert_array_equal(engine.predict(0, len(X), swapped, n_t, 0.1), staged)
+    print(f"[result] predict kernels: {n_t} trees, {int(m._packed['offsets'][n_t])} nodes over "
+          f"{len(X)} rows: staged == HBM walk == renumbered tree", flush=True)
+
+
 def _fit_case(name):
     if name == "defaults_28":
         # Every parameter at the reference's default: n_bins='auto' resolves
