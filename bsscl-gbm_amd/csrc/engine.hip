@@ -321,7 +321,6 @@ struct bsscl_engine {
   // splits per node and of each level's parents (by level parity).
   bool plan_lds = false;
   DevBuf<double> kept_e_d, parent_e_d[2];
-  DevBuf<SplitTask> split_tasks_d;
   DevBuf<int64_t> nleft_d;
   int32_t tile_cap = 0, hist_cap = 0;
   DevBuf<PartTile> tiles_d;
@@ -600,7 +599,6 @@ int ensure_nodes(bsscl_engine *E, int32_t cap, int32_t F_sel) {
   CHK(E->work_e_d.ensure((size_t)cap));
   CHK(E->kept_e_d.ensure((size_t)cap));
   for (int s = 0; s < 2; ++s) CHK(E->parent_e_d[s].ensure((size_t)pcap));
-  CHK(E->split_tasks_d.ensure((size_t)cap));
   E->node_alloc = cap;
   E->node_cap = cap;
   E->node_stride = stride;
@@ -886,12 +884,11 @@ SplitParams split_params(bsscl_engine *E, const TreeParams &tp) {
 
 // The root's inputs as one upload: the selected features, their bin counts
 // followed by their most frequent bins, the root's histogram tasks, its
-// split task, its LevelPlan and its task range (parts kPack*, in order).
-enum { kPackFeat = 0, kPackNbHot, kPackHist, kPackSplit, kPackPlan, kPackTasks };
+// LevelPlan and its task range (parts kPack*, in order).
+enum { kPackFeat = 0, kPackNbHot, kPackHist, kPackPlan, kPackTasks };
 struct RootPack {
   std::vector<HistTask> ht;
   std::vector<int32_t> nb_hot;
-  SplitTask st0{0, -1, -1, 0};
   LevelPlan rp = {};
   int32_t root_tasks[2] = {0, 0};
   Pack pk;  // points into the members above: a RootPack is not copied
@@ -926,7 +923,6 @@ void build_root_pack(bsscl_engine *E, int64_t m, const std::vector<int32_t> &fea
   R.pk.add(feats.data(), feats.size() * 4);
   R.pk.add(R.nb_hot.data(), R.nb_hot.size() * 4);
   R.pk.add(R.ht.data(), R.ht.size() * sizeof(HistTask));
-  R.pk.add(&R.st0, sizeof(SplitTask));
   R.pk.add(&R.rp, sizeof(LevelPlan));
   R.pk.add(R.root_tasks, sizeof(R.root_tasks));
 }
@@ -981,15 +977,11 @@ int launch_root(bsscl_engine *E, const int32_t *rows32, int64_t m,
                      E->hist_node_d.p, reinterpret_cast<const int32_t *>(dv[kPackTasks]), E->segs.p,
                      E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel), E->hist_copies,
                      E->part_d.p, E->pool.p, E->node_stride, start, stop));
-  CHK(prof_begin(E, 3, &stop));
-  HIPCHK(launch_hist_reduce(E->st, E->plan_d, 1, reinterpret_cast<const int32_t *>(dv[kPackTasks]),
-                            E->hist_node_d.p, E->segs.p, E->part_d.p, F_sel, E->pool.p,
-                            E->node_stride));
-  CHK(prof_end(E, stop));
   CHK(prof_begin(E, 2, &stop));
-  HIPCHK(launch_split(E->st, reinterpret_cast<const SplitTask *>(dv[kPackSplit]), E->plan_d, 1,
-                      E->segs.p, E->pool.p, E->node_stride, E->nb_sel_d, F_sel,
-                      split_params(E, tp), E->cand.p, E->totals.p));
+  HIPCHK(launch_reduce_split(E->st, E->plan_d, 1, nullptr,
+                             reinterpret_cast<const int32_t *>(dv[kPackTasks]), E->hist_node_d.p,
+                             E->segs.p, E->part_d.p, E->pool.p, E->node_stride, E->nb_sel_d,
+                             F_sel, 0, split_params(E, tp), E->cand.p, E->totals.p));
   // The root's table record is written by the level-0 planner.
   CHK(prof_end(E, stop));
   return BSSCL_OK;
@@ -1020,14 +1012,14 @@ int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParam
   if (E->plan_lds)
     HIPCHK(launch_plan_lds(E->st, E->nodes_d, E->plan_d, E->parents_d[(level + 1) & 1].p,
                            E->parents_d[level & 1].p, E->tile_begin_d.p, E->hist_begin_d.p,
-                           E->tiles_d.p, E->hist_tasks_d.p, E->split_tasks_d.p, E->segs.p,
+                           E->tiles_d.p, E->hist_tasks_d.p, E->segs.p,
                            E->totals.p, E->cand.p, E->kept_e_d.p,
                            E->parent_e_d[(level + 1) & 1].p, E->parent_e_d[level & 1].p,
                            F_sel, pa));
   else
     HIPCHK(launch_plan(E->st, E->nodes_d, E->plan_d, E->parents_d[(level + 1) & 1].p,
                        E->parents_d[level & 1].p, E->tile_begin_d.p, E->hist_begin_d.p,
-                       E->tiles_d.p, E->hist_tasks_d.p, E->split_tasks_d.p,
+                       E->tiles_d.p, E->hist_tasks_d.p,
                        E->work_flag_d.p, E->work_e_d.p, E->segs.p, E->totals.p, E->cand.p,
                        F_sel, pa));
   CHK(prof_end(E, stop));
@@ -1088,16 +1080,10 @@ int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
                        E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel), E->hist_copies,
                        E->part_d.p, E->pool.p, E->node_stride, start, kstop));
   }
-  CHK(prof_begin(E, 3, &stop));
-  HIPCHK(launch_hist_reduce(E->st, E->plan_d, P, E->hist_begin_d.p, E->hist_node_d.p,
-                            E->segs.p, E->part_d.p, F_sel, E->pool.p, E->node_stride));
-  CHK(prof_end(E, stop));
   CHK(prof_begin(E, 2, &stop));
-  // About 4096 blocks of 4 (node, feature) waves at most; they stride.
-  const int32_t S = std::min(2 * P, std::max(1, 16384 / F_sel));
-  HIPCHK(launch_split(E->st, E->split_tasks_d.p, E->plan_d, S,
-                      E->segs.p, E->pool.p, E->node_stride, E->nb_sel_d, F_sel,
-                      split_params(E, tp), E->cand.p, E->totals.p));
+  HIPCHK(launch_reduce_split(E->st, E->plan_d, P, par, E->hist_begin_d.p, E->hist_node_d.p,
+                             E->segs.p, E->part_d.p, E->pool.p, E->node_stride, E->nb_sel_d,
+                             F_sel, level + 1, split_params(E, tp), E->cand.p, E->totals.p));
   // The new nodes' table records are written by the next level's planner.
   CHK(prof_end(E, stop));
   return BSSCL_OK;
@@ -1916,7 +1902,6 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   for (auto &b : E->parent_e_d) b.release();
   E->hist_node_d.release();
   E->work_e_d.release();
-  E->split_tasks_d.release();
   E->nleft_d.release();
   E->tiles_d.release();
   E->tile_left_d.release();

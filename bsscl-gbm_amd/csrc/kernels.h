@@ -42,7 +42,7 @@ struct LevelPlan {
   int32_t n_parents;    // PartParent entries
   int32_t n_tiles;      // PartTile entries
   int32_t n_hist;       // HistTask entries
-  int32_t n_split;      // SplitTask entries = nodes created at this level
+  int32_t n_split;      // nodes created at this level (the next level's candidates)
   int32_t first_child;  // id of the first node created at this level
   int32_t tile_rows;    // rows per HistTask tile
   int32_t n_nodes;      // nodes in the tree after this level
@@ -78,13 +78,6 @@ struct HistTask {
 
 // One node whose split is searched.  parent < 0: its own histogram is read;
 // otherwise a non-small node's histogram is parent minus sibling.
-struct SplitTask {
-  int32_t node;
-  int32_t parent;
-  int32_t sibling;
-  int32_t depth;
-};
-
 // Best split of one (node, feature): bin < 0 when no bin qualifies.
 struct SplitCand {
   double gain;
@@ -234,10 +227,6 @@ hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        hipEvent_t ev_stop = nullptr);
 // Sums the partials that launch_hist stored for each node with a histogram
 // task (hist_begin: a node's tasks, hist_node: its id) into the pool.
-hipError_t launch_hist_reduce(hipStream_t st, const LevelPlan *plan, int32_t max_refs,
-                              const int32_t *hist_begin, const int32_t *hist_node,
-                              const NodeSeg *segs, const unsigned long long *part,
-                              int32_t F_sel, unsigned long long *pool, int64_t node_stride);
 int hist_blocks(int32_t n_tasks, int32_t nchunks);
 hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
                              int64_t ld_c, const PartParent *parents,
@@ -253,12 +242,15 @@ hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                const int32_t *tile_begin, const int32_t *tile_left,
                                int64_t *parent_nleft, NodeSeg *segs, int32_t *hist_node,
                                int32_t min_samples_leaf, int32_t F_sel);
-hipError_t launch_split(hipStream_t st, const SplitTask *tasks,
-                        const LevelPlan *plan, int32_t max_tasks,
-                        const NodeSeg *segs, unsigned long long *pool,
-                        int64_t node_stride, const int32_t *nb_sel,
-                        int32_t F_sel, SplitParams p, SplitCand *cand,
-                        long long *totals);
+// Histogram reduction and split search of one level (parents == nullptr:
+// the root, node 0, whose tasks hist_begin[0] .. hist_begin[1] built it).
+hipError_t launch_reduce_split(hipStream_t st, const LevelPlan *plan, int32_t max_parents,
+                               const PartParent *parents, const int32_t *hist_begin,
+                               const int32_t *hist_node, const NodeSeg *segs,
+                               const unsigned long long *part, unsigned long long *pool,
+                               int64_t node_stride, const int32_t *nb_sel, int32_t F_sel,
+                               int32_t child_depth, SplitParams p, SplitCand *cand,
+                               long long *totals);
 hipError_t launch_node_best(hipStream_t st, const NodeSeg *segs,
                             const long long *totals, const SplitCand *cand,
                             int32_t F_sel, const LevelPlan *plan,
@@ -272,13 +264,13 @@ hipError_t launch_last_level(hipStream_t st, const PartParent *parents, const Le
                              const unsigned long long *pool, int64_t node_stride,
                              long long *totals, NodeOut *nodes);
 // One workgroup: picks the level's parents among the nodes created by the
-// previous level and writes their PartParent, PartTile, HistTask and
-// SplitTask lists and the LevelPlan (see k_plan).
+// previous level and writes their PartParent, PartTile and HistTask lists
+// and the LevelPlan (see k_plan).
 hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                        const PartParent *prev_parents, PartParent *parents,
                        int32_t *tile_begin, int32_t *hist_begin,
                        PartTile *tiles, HistTask *hist_tasks,
-                       SplitTask *split_tasks, int32_t *work_flag,
+                       int32_t *work_flag,
                        double *work_e, const NodeSeg *segs, const long long *totals,
                        const SplitCand *cand, int32_t F_sel, PlanArgs a);
 // k_plan with its intermediates in LDS, for trees of at most 513 nodes; keeps
@@ -287,7 +279,7 @@ hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
 hipError_t launch_plan_lds(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                            const PartParent *prev_parents, PartParent *parents,
                            int32_t *tile_begin, int32_t *hist_begin, PartTile *tiles,
-                           HistTask *hist_tasks, SplitTask *split_tasks, const NodeSeg *segs,
+                           HistTask *hist_tasks, const NodeSeg *segs,
                            const long long *totals, const SplitCand *cand, double *kept_e,
                            const double *prev_parent_e, double *parent_e, int32_t F_sel,
                            PlanArgs a);

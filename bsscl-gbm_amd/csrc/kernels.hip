@@ -579,7 +579,7 @@ hipError_t launch_iota(hipStream_t st, int32_t *a, int64_t n) {
 // (g,h) updates per clock per CU on MI355X with uniform random bins.
 //
 // The block stores its histogram, as [bin][g,h], into the task's slot of
-// the partial buffer with plain coalesced stores; k_hist_reduce then sums a
+// the partial buffer with plain coalesced stores; k_reduce_split then sums a
 // node's partials into its histogram.  (Adding every block's bins into the
 // node's histogram with device-scope atomics made one memory-side atomic
 // per bin per block: as many bytes as the codes at 1M rows.)  A thread takes 16
@@ -725,7 +725,7 @@ __device__ __forceinline__ void hist_item(
   }
   __syncthreads();
   // Partial of task ti, features f0 .. f0+nf-1, as [bin][g,h]; a node built
-  // by this one task gets it as its histogram directly (k_hist_reduce skips
+  // by this one task gets it as its histogram directly (k_reduce_split reads
   // such nodes).
   unsigned long long *dst =
       hist_tasks_with_rows(hist_begin, task.ref, seg.count, tile_rows) == 1
@@ -768,53 +768,6 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
   }
 }
 
-// Sums each built node's partials (one per task with rows; exact int64, so
-// the order does not matter) into its histogram in the pool; a node with a
-// single task was written there by k_hist.  A block owns
-// 64 consecutive words of one node: its kReduceWaves waves each sum every
-// kReduceWaves-th partial (one coalesced 512-byte load per partial), then
-// the waves' sums are added in LDS.
-constexpr int kReduceWaves = 4;
-
-__global__ __launch_bounds__(64 * kReduceWaves) void k_hist_reduce(
-    const LevelPlan *__restrict__ plan, const int32_t *__restrict__ hist_begin,
-    const int32_t *__restrict__ hist_node, const NodeSeg *__restrict__ segs,
-    const unsigned long long *__restrict__ part, int32_t F_sel,
-    unsigned long long *__restrict__ pool, int64_t node_stride) {
-  __shared__ unsigned long long acc_s[kReduceWaves][64];
-  const int32_t n_refs = plan->n_parents;
-  const int32_t tile_rows = plan->tile_rows;
-  const int32_t words = F_sel * kHistPerFeat;  // a multiple of 64
-  const int32_t groups = words / 64;
-  const int wave = (int)(threadIdx.x >> 6), lane = lane_id();
-  for (int64_t b = blockIdx.x; b < (int64_t)n_refs * groups; b += gridDim.x) {
-    const int32_t p = (int32_t)(b / groups);
-    const int32_t w = (int32_t)(b % groups) * 64 + lane;
-    const int32_t node = hist_node[p];
-    if (node < 0) continue;  // uniform over the block
-    const NodeSeg seg = segs[node];
-    if (!seg.valid) continue;
-    const int32_t t0 = hist_begin[p];
-    const int32_t nt = hist_tasks_with_rows(hist_begin, p, seg.count, tile_rows);
-    if (nt == 1) continue;  // k_hist wrote it
-    const unsigned long long *src = part + (int64_t)t0 * words + w;
-    unsigned long long acc = 0ull;
-    int32_t t = wave;
-    for (; t + kReduceWaves < nt; t += 2 * kReduceWaves)
-      acc += src[(int64_t)t * words] + src[(int64_t)(t + kReduceWaves) * words];
-    if (t < nt) acc += src[(int64_t)t * words];
-    acc_s[wave][lane] = acc;
-    __syncthreads();
-    if (wave == 0) {
-      unsigned long long sum = 0ull;
-#pragma unroll
-      for (int k = 0; k < kReduceWaves; ++k) sum += acc_s[k][lane];
-      pool[(int64_t)node * node_stride + w] = sum;
-    }
-    __syncthreads();
-  }
-}
-
 int hist_blocks(int32_t n_tasks, int32_t nchunks) {
   return ((n_tasks + 7) / 8) * 8 * nchunks;
 }
@@ -848,18 +801,6 @@ hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
     default: return hipErrorInvalidValue;
   }
 #undef BSSCL_HIST
-  return hipGetLastError();
-}
-
-hipError_t launch_hist_reduce(hipStream_t st, const LevelPlan *plan, int32_t max_refs,
-                              const int32_t *hist_begin, const int32_t *hist_node,
-                              const NodeSeg *segs, const unsigned long long *part,
-                              int32_t F_sel, unsigned long long *pool, int64_t node_stride) {
-  if (max_refs <= 0 || F_sel <= 0) return hipSuccess;
-  const int64_t groups = (int64_t)F_sel * kHistPerFeat / 64;
-  const int64_t blocks = std::min<int64_t>((int64_t)max_refs * groups, 16384);
-  hipLaunchKernelGGL(k_hist_reduce, dim3((unsigned)blocks), dim3(64 * kReduceWaves), 0, st,
-                     plan, hist_begin, hist_node, segs, part, F_sel, pool, node_stride);
   return hipGetLastError();
 }
 
@@ -1262,116 +1203,203 @@ hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
 // lane l holds bins 4l..4l+3; an exact int64 prefix scan gives GL, HL for
 // every bin; the gain is the reference's expression in fp64 without
 // contraction; the wave keeps the largest gain, the lowest bin on ties.
-// A non-small child's histogram is parent minus sibling, stored for its own
-// children.
 // ---------------------------------------------------------------------------
 #pragma clang fp contract(off)
-__global__ __launch_bounds__(256) void k_split(
-    const SplitTask *__restrict__ tasks, const LevelPlan *__restrict__ plan,
-    const NodeSeg *__restrict__ segs, unsigned long long *__restrict__ pool,
-    int64_t node_stride, const int32_t *__restrict__ nb_sel, int32_t F_sel,
-    SplitParams P, SplitCand *__restrict__ cand, long long *__restrict__ totals) {
+// Histogram reduction and split search of one level in one launch.  A block
+// of eight waves owns one (parent, feature): the waves sum every eighth of the
+// small child's per-task partials (or read its histogram from the pool when
+// one task wrote it there), the eight sums meet in LDS, then wave 0 stores
+// the small child's histogram and searches it, and wave 1 stores the larger
+// child's (parent minus small) and searches that.  The root is a level of
+// one parent-less node.
+__device__ __forceinline__ void split_search(const long long (&g)[4], const long long (&h)[4],
+                                             int32_t node, const NodeSeg &s, bool depth_ok,
+                                             int32_t fpos, int32_t nb, const SplitParams &P,
+                                             int32_t F_sel, SplitCand *__restrict__ cand,
+                                             long long *__restrict__ totals) {
   const int lane = lane_id();
-  const int64_t n_waves = (int64_t)plan->n_split * F_sel;
-  for (int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); gw < n_waves;
-       gw += (int64_t)gridDim.x * 4) {
-    const int ti = (int)(gw / F_sel), fpos = (int)(gw % F_sel);
-    const SplitTask t = tasks[ti];
-    const NodeSeg s = segs[t.node];
-    if (!s.valid) continue;
-    long long *hn = reinterpret_cast<long long *>(pool) + (int64_t)t.node * node_stride +
-                    (int64_t)fpos * kHistPerFeat + lane * 8;
-    long long g[4], h[4];
-    if (t.parent >= 0 && !s.is_small) {
-      const long long *hp = reinterpret_cast<const long long *>(pool) +
-                            (int64_t)t.parent * node_stride + (int64_t)fpos * kHistPerFeat + lane * 8;
-      const long long *hs = reinterpret_cast<const long long *>(pool) +
-                            (int64_t)t.sibling * node_stride + (int64_t)fpos * kHistPerFeat + lane * 8;
+  const long long lg = g[0] + g[1] + g[2] + g[3];
+  const long long lhs = h[0] + h[1] + h[2] + h[3];
+  const long long ig = wave_incl_scan<long long>(lg);
+  const long long ih = wave_incl_scan<long long>(lhs);
+  const long long Gt = __shfl(ig, 63, 64);
+  const long long Ht = __shfl(ih, 63, 64);
+  if (fpos == 0 && lane == 0) {
+    totals[2 * (int64_t)node] = Gt;
+    totals[2 * (int64_t)node + 1] = Ht;
+  }
+  const double Gtd = (double)Gt * P.g_scale;
+  const double Htd = (double)Ht * P.h_scale;
+  const bool can = s.count >= P.min_samples_leaf && Htd >= P.min_child_weight && depth_ok;
+  double best = -1e9;
+  int32_t bb = -1;
+  if (can && nb >= 2) {
+    const double lam = P.reg_lambda, mcw = P.min_child_weight;
+    const double parent_term = Gtd * Gtd / (Htd + lam);
+    long long GLq = ig - lg, HLq = ih - lhs;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        g[k] = hp[2 * k] - hs[2 * k];
-        h[k] = hp[2 * k + 1] - hs[2 * k + 1];
-        hn[2 * k] = g[k];
-        hn[2 * k + 1] = h[k];
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        g[k] = hn[2 * k];
-        h[k] = hn[2 * k + 1];
-      }
-    }
-    const long long lg = g[0] + g[1] + g[2] + g[3];
-    const long long lhs = h[0] + h[1] + h[2] + h[3];
-    const long long ig = wave_incl_scan<long long>(lg);
-    const long long ih = wave_incl_scan<long long>(lhs);
-    const long long Gt = __shfl(ig, 63, 64);
-    const long long Ht = __shfl(ih, 63, 64);
-    if (fpos == 0 && lane == 0) {
-      totals[2 * (int64_t)t.node] = Gt;
-      totals[2 * (int64_t)t.node + 1] = Ht;
-    }
-    const double Gtd = (double)Gt * P.g_scale;
-    const double Htd = (double)Ht * P.h_scale;
-    const bool can = s.count >= P.min_samples_leaf && Htd >= P.min_child_weight &&
-                     (t.parent < 0 || t.depth < P.max_depth);
-    const int32_t nb = nb_sel[fpos];
-    double best = -1e9;
-    int32_t bb = -1;
-    if (can && nb >= 2) {
-      const double lam = P.reg_lambda, mcw = P.min_child_weight;
-      const double parent_term = Gtd * Gtd / (Htd + lam);
-      long long GLq = ig - lg, HLq = ih - lhs;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        GLq += g[k];
-        HLq += h[k];
-        const int32_t b = lane * 4 + k;
-        if (b <= nb - 2) {
-          const double GL = (double)GLq * P.g_scale;
-          const double HL = (double)HLq * P.h_scale;
-          const double GR = (double)(Gt - GLq) * P.g_scale;
-          const double HR = (double)(Ht - HLq) * P.h_scale;
-          if (!(HL < mcw || HR < mcw)) {
-            const double gain = (GL * GL / (HL + lam) + GR * GR / (HR + lam)) - parent_term;
-            if (gain > best) {
-              best = gain;
-              bb = b;
-            }
+    for (int k = 0; k < 4; ++k) {
+      GLq += g[k];
+      HLq += h[k];
+      const int32_t b = lane * 4 + k;
+      if (b <= nb - 2) {
+        const double GL = (double)GLq * P.g_scale;
+        const double HL = (double)HLq * P.h_scale;
+        const double GR = (double)(Gt - GLq) * P.g_scale;
+        const double HR = (double)(Ht - HLq) * P.h_scale;
+        if (!(HL < mcw || HR < mcw)) {
+          const double gain = (GL * GL / (HL + lam) + GR * GR / (HR + lam)) - parent_term;
+          if (gain > best) {
+            best = gain;
+            bb = b;
           }
         }
       }
     }
+  }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const double og = __shfl_xor(best, o, 64);
-      const int32_t ob = __shfl_xor(bb, o, 64);
-      const bool take = ob >= 0 && (bb < 0 || og > best || (og == best && ob < bb));
-      best = take ? og : best;
-      bb = take ? ob : bb;
-    }
-    if (lane == 0) {
-      SplitCand c;
-      c.gain = best;
-      c.bin = bb;
-      c.pad = 0;
-      cand[(int64_t)t.node * F_sel + fpos] = c;
-    }
+  for (int o = 32; o >= 1; o >>= 1) {
+    const double og = __shfl_xor(best, o, 64);
+    const int32_t ob = __shfl_xor(bb, o, 64);
+    const bool take = ob >= 0 && (bb < 0 || og > best || (og == best && ob < bb));
+    best = take ? og : best;
+    bb = take ? ob : bb;
+  }
+  if (lane == 0) {
+    SplitCand c;
+    c.gain = best;
+    c.bin = bb;
+    c.pad = 0;
+    cand[(int64_t)node * F_sel + fpos] = c;
   }
 }
+
+constexpr int kRsWaves = 8;  // waves of a reduce-split block
+
+__global__ __launch_bounds__(64 * kRsWaves) void k_reduce_split(
+    const LevelPlan *__restrict__ plan, const PartParent *__restrict__ parents,
+    const int32_t *__restrict__ hist_begin, const int32_t *__restrict__ hist_node,
+    const NodeSeg *__restrict__ segs, const unsigned long long *__restrict__ part,
+    unsigned long long *__restrict__ pool, int64_t node_stride,
+    const int32_t *__restrict__ nb_sel, int32_t F_sel, int32_t child_depth, SplitParams P,
+    SplitCand *__restrict__ cand, long long *__restrict__ totals) {
+  __shared__ long long red[kRsWaves][kHistPerFeat];
+  const int lane = lane_id(), wave = (int)(threadIdx.x >> 6);
+  // The root's block (parents == nullptr) has one node and no sibling.
+  const int32_t n_par = parents ? plan->n_parents : 1;
+  const int32_t tile_rows = plan->tile_rows;
+  const int64_t n_items = (int64_t)n_par * F_sel;
+  for (int64_t it = blockIdx.x; it < n_items; it += gridDim.x) {
+    const int32_t p = (int32_t)(it / F_sel), fpos = (int32_t)(it % F_sel);
+    const int32_t small = parents ? hist_node[p] : 0;
+    if (small < 0) continue;  // split not kept: no children (uniform)
+    const NodeSeg ss = segs[small];
+    const int32_t nt = hist_tasks_with_rows(hist_begin, p, ss.count, tile_rows);
+    const int64_t woff = (int64_t)fpos * kHistPerFeat + lane * 8;
+    unsigned long long *hs = pool + (int64_t)small * node_stride + woff;
+    long long g[4] = {0, 0, 0, 0}, h[4] = {0, 0, 0, 0};
+    if (nt == 1) {
+      if (wave == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          g[k] = (long long)hs[2 * k];
+          h[k] = (long long)hs[2 * k + 1];
+        }
+      }
+    } else {
+      const unsigned long long *src =
+          part + ((int64_t)hist_begin[p] * F_sel) * kHistPerFeat + woff;
+      const int64_t tstride = (int64_t)F_sel * kHistPerFeat;
+      int32_t t = wave;
+      for (; t + kRsWaves < nt; t += 2 * kRsWaves) {
+        const longlong2 *a = reinterpret_cast<const longlong2 *>(src + (int64_t)t * tstride);
+        const longlong2 *b =
+            reinterpret_cast<const longlong2 *>(src + (int64_t)(t + kRsWaves) * tstride);
+        longlong2 va[4], vb[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          va[k] = a[k];
+          vb[k] = b[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          g[k] += va[k].x + vb[k].x;
+          h[k] += va[k].y + vb[k].y;
+        }
+      }
+      if (t < nt) {
+        const longlong2 *a = reinterpret_cast<const longlong2 *>(src + (int64_t)t * tstride);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const longlong2 v = a[k];
+          g[k] += v.x;
+          h[k] += v.y;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      red[wave][lane * 8 + 2 * k] = g[k];
+      red[wave][lane * 8 + 2 * k + 1] = h[k];
+    }
+    __syncthreads();
+    if (wave < 2 && (wave == 0 || parents)) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        g[k] = 0;
+        h[k] = 0;
+#pragma unroll
+        for (int w = 0; w < kRsWaves; ++w) {
+          g[k] += red[w][lane * 8 + 2 * k];
+          h[k] += red[w][lane * 8 + 2 * k + 1];
+        }
+      }
+      int32_t node = small;
+      NodeSeg s = ss;
+      if (wave == 0) {
+        if (nt != 1) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            hs[2 * k] = (unsigned long long)g[k];
+            hs[2 * k + 1] = (unsigned long long)h[k];
+          }
+        }
+      } else {
+        // The larger child: parent minus small.
+        const PartParent pp = parents[p];
+        node = pp.left_id == small ? pp.right_id : pp.left_id;
+        s = segs[node];
+        const unsigned long long *hp = pool + (int64_t)pp.node * node_stride + woff;
+        unsigned long long *hl = pool + (int64_t)node * node_stride + woff;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          g[k] = (long long)hp[2 * k] - g[k];
+          h[k] = (long long)hp[2 * k + 1] - h[k];
+          hl[2 * k] = (unsigned long long)g[k];
+          hl[2 * k + 1] = (unsigned long long)h[k];
+        }
+      }
+      split_search(g, h, node, s, !parents || child_depth < P.max_depth, fpos, nb_sel[fpos], P,
+                   F_sel, cand, totals);
+    }
+    __syncthreads();  // red is rewritten by the block's next item
+  }
+}
+
 #pragma clang fp contract(on)
 
-hipError_t launch_split(hipStream_t st, const SplitTask *tasks,
-                        const LevelPlan *plan, int32_t max_tasks,
-                        const NodeSeg *segs, unsigned long long *pool,
-                        int64_t node_stride, const int32_t *nb_sel,
-                        int32_t F_sel, SplitParams p, SplitCand *cand,
-                        long long *totals) {
-  const int64_t waves = (int64_t)max_tasks * F_sel;
-  if (waves <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_split, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st,
-                     tasks, plan, segs, pool, node_stride, nb_sel, F_sel, p,
-                     cand, totals);
+hipError_t launch_reduce_split(hipStream_t st, const LevelPlan *plan, int32_t max_parents,
+                               const PartParent *parents, const int32_t *hist_begin,
+                               const int32_t *hist_node, const NodeSeg *segs,
+                               const unsigned long long *part, unsigned long long *pool,
+                               int64_t node_stride, const int32_t *nb_sel, int32_t F_sel,
+                               int32_t child_depth, SplitParams p, SplitCand *cand,
+                               long long *totals) {
+  const int64_t items = (int64_t)max_parents * F_sel;
+  if (items <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_reduce_split, dim3((unsigned)std::min<int64_t>(items, 16384)),
+                     dim3(64 * kRsWaves), 0, st, plan, parents, hist_begin, hist_node, segs, part, pool, node_stride,
+                     nb_sel, F_sel, child_depth, p, cand, totals);
   return hipGetLastError();
 }
 
@@ -1583,8 +1611,8 @@ hipError_t launch_node_best(hipStream_t st, const NodeSeg *segs,
 // non-increasing e order and stops after max_leaves - 1 kept splits, so a
 // node with that many kept splits strictly above it is never popped and its
 // subtree is never needed.  Expanded nodes get consecutive child ids, and the
-// kernel writes the level's PartParent, PartTile, HistTask and SplitTask
-// lists and its LevelPlan.  When the node table is too small the plan
+// kernel writes the level's PartParent, PartTile and HistTask lists and its
+// LevelPlan.  When the node table is too small the plan
 // records the nodes needed in `overflow` and every later kernel does nothing.
 // ---------------------------------------------------------------------------
 constexpr int kPlanBlock = 1024;
@@ -1604,7 +1632,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
     const PartParent *__restrict__ prev_parents, PartParent *__restrict__ parents,
     int32_t *__restrict__ tile_begin, int32_t *__restrict__ hist_begin,
     PartTile *__restrict__ tiles, HistTask *__restrict__ hist_tasks,
-    SplitTask *__restrict__ split_tasks, int32_t *__restrict__ work_flag,
+    int32_t *__restrict__ work_flag,
     double *__restrict__ work_e, const NodeSeg *__restrict__ segs,
     const long long *__restrict__ totals, const SplitCand *__restrict__ cand, int32_t F_sel,
     PlanArgs a) {
@@ -1683,7 +1711,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
     return;
   }
 
-  // Parents, split tasks and child links; tiles per parent; rows to histogram.
+  // Parents and child links; tiles per parent; rows to histogram.
   unsigned long long rows = 0;
   for (int j = tid; j < nc; j += kPlanBlock) {
     const int32_t i = work_flag[j];
@@ -1702,10 +1730,6 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
     P.node = v;
     P.pad = 0;
     parents[i] = P;
-    if (!a.last) {
-      split_tasks[2 * i] = SplitTask{L, v, L + 1, a.level + 1};
-      split_tasks[2 * i + 1] = SplitTask{L + 1, v, L, a.level + 1};
-    }
     const int64_t a0 = N.start & ~int64_t(15);
     // At least one tile: a parent's first tile writes its children's segments.
     tile_begin[i] = (int32_t)max((int64_t)1, (N.start + N.count - a0 + a.part_tile - 1) / a.part_tile);
@@ -1811,7 +1835,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     const PartParent *__restrict__ prev_parents, PartParent *__restrict__ parents,
     int32_t *__restrict__ tile_begin, int32_t *__restrict__ hist_begin,
     PartTile *__restrict__ tiles, HistTask *__restrict__ hist_tasks,
-    SplitTask *__restrict__ split_tasks, const NodeSeg *__restrict__ segs,
+    const NodeSeg *__restrict__ segs,
     const long long *__restrict__ totals, const SplitCand *__restrict__ cand,
     double *__restrict__ kept_e, const double *__restrict__ prev_parent_e,
     double *__restrict__ parent_e, int32_t F_sel, PlanArgs a) {
@@ -1959,7 +1983,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     return;
   }
 
-  // Records, parents, split tasks, ranks; tiles per parent; rows to build.
+  // Records, parents, ranks; tiles per parent; rows to build.
   unsigned long long rows = 0;
   if (tid < nc) {
     const int32_t v = first + tid;
@@ -1991,10 +2015,6 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       P.pad = 0;
       parents[i] = P;
       parent_e[i] = N.e;
-      if (!a.last) {
-        split_tasks[2 * i] = SplitTask{L, v, L + 1, a.level + 1};
-        split_tasks[2 * i + 1] = SplitTask{L + 1, v, L, a.level + 1};
-      }
       const int64_t a0 = N.start & ~int64_t(15);
       // At least one tile: a parent's first tile writes its children's segments.
       s_tb[i] = (int32_t)max((int64_t)1, (N.start + N.count - a0 + a.part_tile - 1) / a.part_tile);
@@ -2084,12 +2104,12 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
 hipError_t launch_plan_lds(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                            const PartParent *prev_parents, PartParent *parents,
                            int32_t *tile_begin, int32_t *hist_begin, PartTile *tiles,
-                           HistTask *hist_tasks, SplitTask *split_tasks, const NodeSeg *segs,
+                           HistTask *hist_tasks, const NodeSeg *segs,
                            const long long *totals, const SplitCand *cand, double *kept_e,
                            const double *prev_parent_e, double *parent_e, int32_t F_sel,
                            PlanArgs a) {
   hipLaunchKernelGGL(k_plan_lds, dim3(1), dim3(kPlanBlock), 0, st, nodes, plan, prev_parents,
-                     parents, tile_begin, hist_begin, tiles, hist_tasks, split_tasks, segs,
+                     parents, tile_begin, hist_begin, tiles, hist_tasks, segs,
                      totals, cand, kept_e, prev_parent_e, parent_e, F_sel, a);
   return hipGetLastError();
 }
@@ -2098,12 +2118,12 @@ hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                        const PartParent *prev_parents, PartParent *parents,
                        int32_t *tile_begin, int32_t *hist_begin,
                        PartTile *tiles, HistTask *hist_tasks,
-                       SplitTask *split_tasks, int32_t *work_flag,
+                       int32_t *work_flag,
                        double *work_e, const NodeSeg *segs, const long long *totals,
                        const SplitCand *cand, int32_t F_sel, PlanArgs a) {
   hipLaunchKernelGGL(k_plan, dim3(1), dim3(kPlanBlock), 0, st, nodes, plan,
                      prev_parents, parents, tile_begin, hist_begin, tiles,
-                     hist_tasks, split_tasks, work_flag, work_e, segs, totals, cand, F_sel,
+                     hist_tasks, work_flag, work_e, segs, totals, cand, F_sel,
                      a);
   return hipGetLastError();
 }
