@@ -8,7 +8,8 @@ rounds is the device time including host work.
 
 Prints one JSON line with the fit rate (trees/s), the histogram kernel's
 roofline (algorithmic bytes per launch over its average execution time,
-from events recorded by each launch's own dispatch, against 8 TB/s HBM),
+from the first block's start to the last block's end as the kernel stamps
+them, against 8 TB/s HBM),
 prediction through the workload's full ensemble with its own roofline, a
 rounds-only block for the 10M x 50 workload and the oracle's CPU rate on a
 bounded sample.
@@ -123,8 +124,9 @@ def measured_traffic(kernel, workload):
 
 def run_gpu(name, steps, warmup, rounds_only=False):
     """Fits warmup + steps + BREAKDOWN_ROUNDS rounds.  The timed rounds run
-    with the histogram kernel's HIP events only (level 1); the last rounds,
-    after the timed region, time every kernel group (level 2) for the
+    with the histogram kernel's own clock stamps only (level 1: no event
+    packets between the tree's kernels); the last rounds, after the timed
+    region, time every kernel group with HIP events (level 2) for the
     per-kernel breakdown."""
     from bsscl_gbm import HybridHistGBMNumbaV1_0_1
     X, y, params = make_workload(name)
@@ -239,7 +241,9 @@ def hist_roofline(st, workload):
         "traffic": traffic,
         "traffic_source": source,
         "kernel": "k_hist",
-        "timing": "kernel execution, events recorded by each launch's own dispatch",
+        "timing": "kernel execution: first block's start to last block's end, stamped by "
+                  "the kernel on the device's constant-rate clock (no event packets in the "
+                  "timed rounds)",
         "launches": int(st["hist_launches"]),
         "avg_launch_us": round(1e3 * st["hist_ms"] / launches, 2),
         "bytes_per_launch": round(st["hist_bytes"] / launches),

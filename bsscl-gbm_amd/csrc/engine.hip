@@ -377,6 +377,14 @@ struct bsscl_engine {
     uint64_t seq;  // boosting round that recorded them
   };
   std::vector<Pending> pending;
+  // Histogram launches timed by the kernel itself: slot k holds the first
+  // block's start and the last block's end on the device's constant-rate
+  // clock (no event packets between the tree's kernels, which would each
+  // hold the queue for several microseconds).
+  DevBuf<unsigned long long> ktime_d;
+  size_t ktime_used = 0;                                   // words
+  std::vector<std::pair<size_t, size_t>> ktime_launches;  // (first word, blocks)
+  double wall_khz = 0.0;
   double stats[18] = {0};
 };
 
@@ -412,18 +420,56 @@ int prof_begin(bsscl_engine *E, int kind, hipEvent_t *stop) {
   return BSSCL_OK;
 }
 
-// The start/stop events of one timed kernel of `kind` (0 histogram, 4
-// prediction), recorded by that kernel's own dispatch
-// (hipExtLaunchKernelGGL), so the time is the kernel's execution alone;
-// null events when not profiling.
+// The start/stop events of one timed kernel of `kind` (4 prediction),
+// recorded by that kernel's own dispatch (hipExtLaunchKernelGGL), so the
+// time is the kernel's execution alone; null events when not profiling.
+// (Histogram launches are timed by the kernel itself: prof_slot.)
 int prof_kernel(bsscl_engine *E, int kind, hipEvent_t *start, hipEvent_t *stop) {
   *start = *stop = nullptr;
   if (E->prof < 1) return BSSCL_OK;
+  if (kind == 0) return BSSCL_OK;  // histograms: prof_slot
   hipEvent_t a, b;
   CHK(ev_pair(E, a, b));
   E->pending.push_back({a, b, kind, E->round_seq});
   *start = a;
   *stop = b;
+  return BSSCL_OK;
+}
+
+// Per-block (start, end) pairs of one histogram launch of `blocks` blocks
+// when profiling (null otherwise, or when this profiling run's space is
+// used up).
+constexpr size_t kTimeWords = (size_t)1 << 22;  // 32 MB of pairs
+
+unsigned long long *prof_slot(bsscl_engine *E, int64_t blocks) {
+  if (E->prof < 1 || blocks <= 0) return nullptr;
+  if (!E->ktime_d.p && E->ktime_d.ensure(kTimeWords) != BSSCL_OK) return nullptr;
+  if (E->ktime_used + 2 * (size_t)blocks > kTimeWords) return nullptr;
+  unsigned long long *p = E->ktime_d.p + E->ktime_used;
+  E->ktime_launches.push_back({E->ktime_used, (size_t)blocks});
+  E->ktime_used += 2 * (size_t)blocks;
+  return p;
+}
+
+// Folds the recorded launches into the histogram timings (after a
+// synchronisation): each launch from its first block's start to its last
+// block's end.
+int prof_slots_collect(bsscl_engine *E) {
+  if (E->ktime_launches.empty()) return BSSCL_OK;
+  std::vector<unsigned long long> t(E->ktime_used);
+  HIPCHK(hipMemcpy(t.data(), E->ktime_d.p, t.size() * 8, hipMemcpyDeviceToHost));
+  for (const auto &L : E->ktime_launches) {
+    unsigned long long a = ~0ull, b = 0ull;
+    for (size_t k = 0; k < L.second; ++k) {
+      a = std::min(a, t[L.first + 2 * k]);
+      b = std::max(b, t[L.first + 2 * k + 1]);
+    }
+    if (b < a) continue;
+    E->stats[0] += 1.0;
+    E->stats[1] += (double)(b - a) / E->wall_khz;  // ms
+  }
+  E->ktime_launches.clear();
+  E->ktime_used = 0;
   return BSSCL_OK;
 }
 
@@ -610,6 +656,12 @@ int32_t hist_fchunk(bsscl_engine *E, int32_t F_sel) {
   int32_t fc = E->hist_fc;
   while (fc > 1 && fc > F_sel) fc >>= 1;
   return fc;
+}
+
+// Blocks of a histogram launch for up to max_tasks tasks.
+int64_t hist_grid(bsscl_engine *E, int32_t max_tasks, int32_t F_sel) {
+  const int32_t fc = hist_fchunk(E, F_sel);
+  return max_tasks > 0 ? hist_blocks(max_tasks, (F_sel + fc - 1) / fc) : 0;
 }
 
 // Histogram row tiles wanted per level: about hist_blocks_per_cu blocks per
@@ -970,13 +1022,13 @@ int launch_root(bsscl_engine *E, const int32_t *rows32, int64_t m,
                               E->codes_c[b].p, E->ld_c, E->gh_c[b].p,
                               E->track_rid && b == 0 ? E->rid_c[0].p : nullptr,
                               E->ld_c, E->segs.p, E->hist_node_d.p));
-  hipEvent_t start, stop;
-  CHK(prof_kernel(E, 0, &start, &stop));
+  hipEvent_t stop;
   HIPCHK(launch_hist(E->st, E->codes_c[b].p, E->ld_c, E->gh_c[b].p,
                      reinterpret_cast<const HistTask *>(dv[kPackHist]), E->plan_d, n_hist,
                      E->hist_node_d.p, reinterpret_cast<const int32_t *>(dv[kPackTasks]), E->segs.p,
                      E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel), E->hist_copies,
-                     E->part_d.p, E->pool.p, E->node_stride, start, stop));
+                     E->part_d.p, E->pool.p, E->node_stride,
+                     prof_slot(E, hist_grid(E, n_hist, F_sel))));
   CHK(prof_begin(E, 2, &stop));
   HIPCHK(launch_reduce_split(E->st, E->plan_d, 1, nullptr,
                              reinterpret_cast<const int32_t *>(dv[kPackTasks]), E->hist_node_d.p,
@@ -1073,12 +1125,11 @@ int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
   }
   const int32_t H = (int32_t)std::min<int64_t>(E->hist_cap, (int64_t)hist_target(E, F_sel) + 2 * (int64_t)P + 2);
   {
-    hipEvent_t start, kstop;
-    CHK(prof_kernel(E, 0, &start, &kstop));
     HIPCHK(launch_hist(E->st, E->codes_c[dst].p, E->ld_c, E->gh_c[dst].p, E->hist_tasks_d.p,
                        E->plan_d, H, E->hist_node_d.p, E->hist_begin_d.p, E->segs.p,
                        E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel), E->hist_copies,
-                       E->part_d.p, E->pool.p, E->node_stride, start, kstop));
+                       E->part_d.p, E->pool.p, E->node_stride,
+                       prof_slot(E, hist_grid(E, H, F_sel))));
   }
   CHK(prof_begin(E, 2, &stop));
   HIPCHK(launch_reduce_split(E->st, E->plan_d, P, par, E->hist_begin_d.p, E->hist_node_d.p,
@@ -1838,6 +1889,10 @@ int bsscl_engine_create(int32_t device, bsscl_engine **out) {
     E->n_cu = v;
   if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
     E->max_lds = (size_t)v;
+  // The rate of the clock kernels read with wall_clock64 (kHz).
+  E->wall_khz = 100000.0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeWallClockRate, device) == hipSuccess && v > 0)
+    E->wall_khz = (double)v;
   if (scratch_for_device(device, &E->scratch_p) != BSSCL_OK) {
     const std::string msg = bsscl_last_error();
     bsscl_engine_destroy(E);
@@ -1915,6 +1970,7 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   }
   E->offsets_d.release();
   E->partials_d.release();
+  E->ktime_d.release();
   E->loss_d.release();
   E->out_d.release();
   E->pin.release();
@@ -2703,13 +2759,22 @@ int bsscl_engine_set_profiling(bsscl_engine *E, int32_t on) {
   HIPCHK(hipSetDevice(E->device));
   HIPCHK(hipStreamSynchronize(E->st));
   CHK(prof_collect(E));
+  if (on) {
+    std::memset(E->stats, 0, sizeof(E->stats));
+    E->ktime_launches.clear();
+    E->ktime_used = 0;
+  }
   E->prof = std::max(0, std::min(2, (int)on));
-  if (on) std::memset(E->stats, 0, sizeof(E->stats));
   return BSSCL_OK;
 }
 
 int bsscl_engine_stats(bsscl_engine *E, double *out, int32_t cap, int32_t *n_out) {
   if (!E || !out || !n_out) return set_error(BSSCL_EINVAL, "null argument");
+  if (!E->ktime_launches.empty()) {
+    HIPCHK(hipSetDevice(E->device));
+    HIPCHK(hipStreamSynchronize(E->st));
+    CHK(prof_slots_collect(E));
+  }
   const int32_t n = std::min<int32_t>(cap, 18);
   for (int32_t i = 0; i < n; ++i) out[i] = E->stats[i];
   *n_out = n;

@@ -223,8 +223,7 @@ hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int32_t *nb_sel, const int32_t *hot_sel,
                        int32_t F_sel, int32_t fchunk, int32_t copies,
                        unsigned long long *part, unsigned long long *pool,
-                       int64_t node_stride, hipEvent_t ev_start = nullptr,
-                       hipEvent_t ev_stop = nullptr);
+                       int64_t node_stride, unsigned long long *ktime = nullptr);
 // Sums the partials that launch_hist stored for each node with a histogram
 // task (hist_begin: a node's tasks, hist_node: its id) into the pool.
 int hist_blocks(int32_t n_tasks, int32_t nchunks);

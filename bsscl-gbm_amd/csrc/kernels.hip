@@ -751,10 +751,14 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
     const NodeSeg *__restrict__ segs, const int32_t *__restrict__ nb_sel,
     const int32_t *__restrict__ hot_sel, int32_t F_sel, int32_t nchunks,
     unsigned long long *__restrict__ part, unsigned long long *__restrict__ pool,
-    int64_t node_stride) {
+    int64_t node_stride, unsigned long long *__restrict__ ktime) {
   __shared__ unsigned long long lh[FC * kHistPerFeat * C];
   const int32_t n_tasks = plan->n_hist;
   const int32_t tile_rows = plan->tile_rows;
+  // Optional timing: each block's start and end on the constant-rate clock,
+  // one plain store each into its own pair (the launch's time is the first
+  // start to the last end).
+  if (ktime && threadIdx.x == 0) ktime[2 * blockIdx.x] = (unsigned long long)wall_clock64();
   // The grid is a multiple of 8 * nchunks, so every block keeps its XCD
   // (b & 7) and feature chunk as it strides.
   for (int b = (int)blockIdx.x;; b += (int)gridDim.x) {
@@ -765,6 +769,10 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
     hist_item<FC, C>(lh, codes_c, ld_c, gh_c, tasks[ti], ti, j % nchunks, hist_node,
                      hist_begin, segs, nb_sel, hot_sel, F_sel, tile_rows, part, pool,
                      node_stride);
+  }
+  if (ktime) {
+    __syncthreads();  // every wave's stores issued
+    if (threadIdx.x == 0) ktime[2 * blockIdx.x + 1] = (unsigned long long)wall_clock64();
   }
 }
 
@@ -780,15 +788,14 @@ hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int32_t *nb_sel, const int32_t *hot_sel,
                        int32_t F_sel, int32_t fchunk, int32_t copies,
                        unsigned long long *part, unsigned long long *pool,
-                       int64_t node_stride, hipEvent_t ev_start, hipEvent_t ev_stop) {
+                       int64_t node_stride, unsigned long long *ktime) {
   if (max_tasks <= 0) return hipSuccess;
   const int32_t nchunks = (F_sel + fchunk - 1) / fchunk;
   const dim3 grid((unsigned)hist_blocks(max_tasks, nchunks));
-#define BSSCL_HIST(FC, C)                                                              \
-  hipExtLaunchKernelGGL((k_hist<FC, C>), grid, dim3(kHistBlock), 0, st, ev_start, ev_stop, 0, \
-                        codes_c, ld_c, gh_c, \
-                     tasks, plan, hist_node, hist_begin, segs, nb_sel, hot_sel, F_sel, \
-                     nchunks, part, pool, node_stride)
+#define BSSCL_HIST(FC, C)                                                                  \
+  hipLaunchKernelGGL((k_hist<FC, C>), grid, dim3(kHistBlock), 0, st, codes_c, ld_c, gh_c, tasks, \
+                     plan, hist_node, hist_begin, segs, nb_sel, hot_sel, F_sel, nchunks, part,  \
+                     pool, node_stride, ktime)
   // LDS per block: fchunk * copies * 8 KB (at most 32 KB).
   switch (fchunk * 16 + copies) {
     case 1 * 16 + 1: BSSCL_HIST(1, 1); break;
