@@ -1877,21 +1877,25 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
   if (tid == 0) s_rows = 0ull;
 
   // Every input at once: earlier ranks, the previous parents' ids and ranks,
-  // and the candidates' segments, totals and split candidates.
-  for (int u = tid; u < first; u += kPlanBlock) s_ke[u] = kept_e[u];
+  // and the candidates' segments, totals and split candidates (four per
+  // wave and pass: one pass for up to 64 candidates).  The earlier ranks go
+  // through registers so that their LDS stores wait after every load is
+  // issued.  (first <= kPlanLdsC + 1 <= kPlanBlock: one per thread.)
+  const double ke0 = tid < first ? kept_e[tid] : 0.0;
   int32_t pnode = -1;
   double pe = 0.0;
   if (tid < n_pp) {
     pnode = prev_parents[tid].node;
     pe = prev_parent_e[tid];
   }
-  for (int jb = wave * 4; jb < nc; jb += (kPlanBlock / 64) * 4) {
-    NodeSeg sg[4];
-    long long gq[4], hq[4];
-    double ppe[4];
-    SplitCand cf[4];
+  constexpr int kPer = 4;  // candidates per wave and pass
+  for (int jb = wave * kPer; jb < nc; jb += (kPlanBlock / 64) * kPer) {
+    NodeSeg sg[kPer];
+    long long gq[kPer], hq[kPer];
+    double ppe[kPer];
+    SplitCand cf[kPer];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kPer; ++q) {
       const int j = min(jb + q, nc - 1);
       const int64_t c = first + j;
       sg[q] = segs[c];
@@ -1900,8 +1904,9 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       ppe[q] = a.level == 0 ? 0.0 : prev_parent_e[j >> 1];
       cf[q] = lane < F_sel ? cand[c * F_sel + lane] : SplitCand{0.0, -1, 0};
     }
+    if (jb == wave * kPer && tid < first) s_ke[tid] = ke0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kPer; ++q) {
       const int j = jb + q;
       const int64_t c = first + min(j, nc - 1);
       // Best over the features: largest gain, lowest position on ties.
@@ -1954,6 +1959,8 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       }
     }
   }
+  // (Waves that took no candidate store their earlier ranks here.)
+  if (wave * kPer >= nc && tid < first) s_ke[tid] = ke0;
   __syncthreads();
 
   // The previous level's parents are kept splits when their children (this
@@ -2757,10 +2764,17 @@ __global__ __launch_bounds__(kTreeBlock) void k_replay_tree(
       const double gv = gc[v];
       int32_t lt = 0, eq = 0;
       int32_t u = 0;
-      for (; u + 4 <= n; u += 4) {
-        const double g0 = gc[u], g1 = gc[u + 1], g2 = gc[u + 2], g3 = gc[u + 3];
-        lt += (g0 < gv) + (g1 < gv) + (g2 < gv) + (g3 < gv);
-        eq += (g0 == gv) + (g1 == gv) + (g2 == gv) + (g3 == gv);
+      // Eight keys per step in four 16-byte LDS reads, all in flight at once.
+      const double2 *gc2 = reinterpret_cast<const double2 *>(gc);
+      for (; u + 8 <= n; u += 8) {
+        double2 q[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = gc2[(u >> 1) + j];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          lt += (q[j].x < gv) + (q[j].y < gv);
+          eq += (q[j].x == gv) + (q[j].y == gv);
+        }
       }
       for (; u < n; ++u) {
         lt += gc[u] < gv;
@@ -2805,7 +2819,18 @@ __global__ __launch_bounds__(kTreeBlock) void k_replay_tree(
         if (!rt_pc[v]) continue;
         const unsigned long long kh = key[2 * v], kl = key[2 * v + 1];
         int32_t r = 0;
-        for (int32_t u = 0; u < n; ++u) {
+        int32_t u = 0;
+        // Eight (hi, lo) vectors per step, one 16-byte LDS read each, all in
+        // flight at once.
+        const ulonglong2 *key2 = reinterpret_cast<const ulonglong2 *>(key);
+        for (; u + 8 <= n; u += 8) {
+          ulonglong2 q[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) q[j] = key2[u + j];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) r += (q[j].x > kh || (q[j].x == kh && q[j].y > kl)) ? 1 : 0;
+        }
+        for (; u < n; ++u) {
           const unsigned long long uh = key[2 * u], ul = key[2 * u + 1];
           r += (uh > kh || (uh == kh && ul > kl)) ? 1 : 0;
         }
