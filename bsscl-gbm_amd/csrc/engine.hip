@@ -365,7 +365,8 @@ struct bsscl_engine {
   int32_t part_rows = 4;
   int32_t part_tile = 1024;
   int32_t hist_blocks_per_cu = 8;
-  int32_t hist_rows_per_flush = 5120;
+  int32_t hist_rows_per_flush = 5120;        // the root's tiles
+  int32_t hist_rows_per_flush_level = 2560;  // the planned levels' tiles
 
   // Profiling.
   int prof = 0;  // 0 off, 1 histogram kernel timed, 2 every kernel group timed
@@ -676,7 +677,8 @@ int32_t hist_target(bsscl_engine *E, int32_t F_sel) {
 // hist_blocks_per_cu blocks per CU, but never so many that flushed bins
 // (tiles * F_sel * 512 atomics) exceed ~5% of the LDS adds (S * F_sel * 2),
 // i.e. at most S/hist_rows_per_flush tiles.
-// (k_plan's plan_tile_rows computes the same on the device.)
+// (plan_tile_rows computes the same on the device for the planned levels,
+// with hist_rows_per_flush_level.)
 int32_t hist_tile_rows(bsscl_engine *E, int64_t S, int32_t F_sel) {
   int64_t tiles = hist_target(E, F_sel);
   tiles = std::min<int64_t>(tiles, std::max<int64_t>(1, S / E->hist_rows_per_flush));
@@ -867,6 +869,12 @@ void read_hist_tuning(bsscl_engine *E, int64_t m, int32_t F_sel) {
   if (E->hist_copies == 2) E->hist_copies = 1;
   E->hist_blocks_per_cu = env_int("BSSCL_HIST_BLOCKS_PER_CU", 1, 64, 8);
   E->hist_rows_per_flush = env_int("BSSCL_HIST_ROWS_PER_FLUSH", 256, 1 << 22, 5120);
+  // Below the root, smaller tiles (more blocks for the smaller levels, more
+  // partials to sum): 1M x 28, 2560 rows took the five planned levels'
+  // histograms and reductions from 120 to 114 us per round; the root keeps
+  // 5120 (42 against 45 us).
+  E->hist_rows_per_flush_level =
+      env_int("BSSCL_HIST_ROWS_PER_FLUSH_LEVEL", 256, 1 << 22, 2560);
 }
 
 // Buffers of a tree over m rows: the compact sets, the node table for the
@@ -1057,7 +1065,7 @@ int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParam
   pa.tile_cap = E->tile_cap;
   pa.hist_cap = E->hist_cap;
   pa.hist_target = hist_target(E, F_sel);
-  pa.rows_per_flush = E->hist_rows_per_flush;
+  pa.rows_per_flush = E->hist_rows_per_flush_level;
   pa.part_tile = E->part_tile;
   hipEvent_t stop;
   CHK(prof_begin(E, 2, &stop));
