@@ -315,6 +315,10 @@ struct bsscl_engine {
   LevelPlan *plan_d = nullptr;
   NodeOut *nodes_d = nullptr;
   DevBuf<PartParent> parents_d[2];    // by level parity
+  DevBuf<PartGroup> groups_d;         // a grouped level's partition groups
+  // Rows move every second level (in-place and grouped levels alternate;
+  // with the LDS planner) instead of at every level.
+  bool pair_levels = false;
   DevBuf<int32_t> tile_begin_d, hist_begin_d, work_flag_d, hist_node_d;
   DevBuf<double> work_e_d;
   // Planner in LDS (trees of at most kPlanLdsMaxNodes nodes): ranks of kept
@@ -324,7 +328,7 @@ struct bsscl_engine {
   DevBuf<int64_t> nleft_d;
   int32_t tile_cap = 0, hist_cap = 0;
   DevBuf<PartTile> tiles_d;
-  DevBuf<int32_t> tile_left_d;
+  DevBuf<int32_t> tile_cnt_d;         // per partition tile: its rows of the four runs
   DevBuf<HistTask> hist_tasks_d;
   DevBuf<char> lvl_d;                 // packed inputs of the root (one upload per tree)
   const int32_t *feat_d = nullptr;    // selected feature indices
@@ -361,6 +365,10 @@ struct bsscl_engine {
   // BSSCL_HIST_BLOCKS_PER_CU and BSSCL_HIST_ROWS_PER_FLUSH.
   int32_t hist_fc = 1;
   int32_t hist_copies = 4;
+  // The same for the in-place levels' histograms (BSSCL_HIST_SPAN_FC,
+  // BSSCL_HIST_SPAN_COPIES).
+  int32_t hist_fc_span = 1;
+  int32_t hist_copies_span = 1;
   // Partition tile of the current tree: 256 threads x part_rows rows.
   int32_t part_rows = 4;
   int32_t part_tile = 1024;
@@ -638,6 +646,7 @@ int ensure_nodes(bsscl_engine *E, int32_t cap, int32_t F_sel) {
   E->plan_d = reinterpret_cast<LevelPlan *>(E->table_d.p);
   E->nodes_d = reinterpret_cast<NodeOut *>(E->table_d.p + 64);
   for (int s = 0; s < 2; ++s) CHK(E->parents_d[s].ensure((size_t)pcap));
+  CHK(E->groups_d.ensure((size_t)pcap));
   CHK(E->tile_begin_d.ensure((size_t)pcap + 1));
   CHK(E->hist_begin_d.ensure((size_t)pcap + 1));
   CHK(E->hist_node_d.ensure((size_t)pcap));
@@ -652,23 +661,24 @@ int ensure_nodes(bsscl_engine *E, int32_t cap, int32_t F_sel) {
   return BSSCL_OK;
 }
 
-// Feature chunk of a histogram block (hist_fc, at most F_sel).
-int32_t hist_fchunk(bsscl_engine *E, int32_t F_sel) {
-  int32_t fc = E->hist_fc;
+// Feature chunk of a histogram block (hist_fc, or hist_fc_span for an
+// in-place level, at most F_sel).
+int32_t hist_fchunk(bsscl_engine *E, int32_t F_sel, bool span = false) {
+  int32_t fc = span ? E->hist_fc_span : E->hist_fc;
   while (fc > 1 && fc > F_sel) fc >>= 1;
   return fc;
 }
 
 // Blocks of a histogram launch for up to max_tasks tasks.
-int64_t hist_grid(bsscl_engine *E, int32_t max_tasks, int32_t F_sel) {
-  const int32_t fc = hist_fchunk(E, F_sel);
+int64_t hist_grid(bsscl_engine *E, int32_t max_tasks, int32_t F_sel, bool span = false) {
+  const int32_t fc = hist_fchunk(E, F_sel, span);
   return max_tasks > 0 ? hist_blocks(max_tasks, (F_sel + fc - 1) / fc) : 0;
 }
 
 // Histogram row tiles wanted per level: about hist_blocks_per_cu blocks per
 // CU over all feature chunks.
-int32_t hist_target(bsscl_engine *E, int32_t F_sel) {
-  const int32_t fc = hist_fchunk(E, F_sel);
+int32_t hist_target(bsscl_engine *E, int32_t F_sel, bool span = false) {
+  const int32_t fc = hist_fchunk(E, F_sel, span);
   const int32_t nchunks = (F_sel + fc - 1) / fc;
   return std::max<int32_t>(1, (E->hist_blocks_per_cu * E->n_cu + nchunks - 1) / nchunks);
 }
@@ -867,6 +877,18 @@ void read_hist_tuning(bsscl_engine *E, int64_t m, int32_t F_sel) {
   if (E->hist_copies != 1 && E->hist_copies != 4 && E->hist_copies != 8) E->hist_copies = 1;
   if (E->hist_fc * E->hist_copies > 8) E->hist_copies = 8 / E->hist_fc;
   if (E->hist_copies == 2) E->hist_copies = 1;
+  E->hist_fc_span = env_int("BSSCL_HIST_SPAN_FC", 1, 8, E->hist_fc);
+  if (E->hist_fc_span != 1 && E->hist_fc_span != 2 && E->hist_fc_span != 4 &&
+      E->hist_fc_span != 8)
+    E->hist_fc_span = E->hist_fc;
+  // In place one copy: the listed rows' LDS adds come from scattered lanes,
+  // and the smaller block leaves room for more waves (1M x 28: 2330 trees/s
+  // against 1780-2180 with four copies; 10M x 50: 364 with four features).
+  E->hist_copies_span = env_int("BSSCL_HIST_SPAN_COPIES", 1, 8, 1);
+  if (E->hist_copies_span != 1 && E->hist_copies_span != 4 && E->hist_copies_span != 8)
+    E->hist_copies_span = 1;
+  if (E->hist_fc_span * E->hist_copies_span > 8) E->hist_copies_span = 8 / E->hist_fc_span;
+  if (E->hist_copies_span == 2) E->hist_copies_span = 1;
   E->hist_blocks_per_cu = env_int("BSSCL_HIST_BLOCKS_PER_CU", 1, 64, 8);
   E->hist_rows_per_flush = env_int("BSSCL_HIST_ROWS_PER_FLUSH", 256, 1 << 22, 5120);
   // Below the root, smaller tiles (more blocks for the smaller levels, more
@@ -903,7 +925,8 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
   while (E->part_rows > 4 && m / ((int64_t)kPartThreads * E->part_rows) < 512) E->part_rows >>= 1;
   E->part_tile = kPartThreads * E->part_rows;
   const int64_t tcap = m / E->part_tile + (int64_t)cap + 4;
-  const int64_t hcap = (int64_t)hist_target(E, F_sel) + cap + 4;
+  const int64_t hcap =
+      (int64_t)std::max(hist_target(E, F_sel), hist_target(E, F_sel, true)) + cap + 4;
   if (tcap > INT32_MAX / 2 || hcap > INT32_MAX / 2)
     return set_error(BSSCL_EINVAL, "tree too large for the level lists");
   grow = grow || E->tiles_d.cap < (size_t)tcap || E->hist_tasks_d.cap < (size_t)hcap ||
@@ -916,7 +939,7 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
     if (b == 0) CHK(E->rid_c[s].ensure((size_t)ld_c));
   }
   CHK(E->tiles_d.ensure((size_t)tcap));
-  CHK(E->tile_left_d.ensure((size_t)tcap + 4));  // 16-byte reads past the last tile
+  CHK(E->tile_cnt_d.ensure(4 * (size_t)tcap + 8));  // a 16-byte read past the last tile
   CHK(E->hist_tasks_d.ensure((size_t)hcap));
   CHK(E->part_d.ensure((size_t)hcap * F_sel * kHistPerFeat));
   E->tile_cap = (int32_t)tcap;
@@ -1035,7 +1058,7 @@ int launch_root(bsscl_engine *E, const int32_t *rows32, int64_t m,
                      reinterpret_cast<const HistTask *>(dv[kPackHist]), E->plan_d, n_hist,
                      E->hist_node_d.p, reinterpret_cast<const int32_t *>(dv[kPackTasks]), E->segs.p,
                      E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel), E->hist_copies,
-                     E->part_d.p, E->pool.p, E->node_stride,
+                     E->part_d.p, E->pool.p, E->node_stride, nullptr,
                      prof_slot(E, hist_grid(E, n_hist, F_sel))));
   CHK(prof_begin(E, 2, &stop));
   HIPCHK(launch_reduce_split(E->st, E->plan_d, 1, nullptr,
@@ -1053,7 +1076,22 @@ int32_t level_parents_bound(bsscl_engine *E, int32_t level) {
   return (int32_t)std::max<int64_t>(1, std::min<int64_t>(full, (E->node_cap - 1) / 2));
 }
 
-// The planner of level `level` (parents at that depth, rows in set level%2).
+// How level `level` (parents at that depth) treats its rows: with paired
+// levels, in place at even depths and grouped at odd ones, so that rows
+// move once every two levels; otherwise every level moves them.
+int32_t level_mode(const bsscl_engine *E, int32_t level) {
+  if (!E->pair_levels) return kLevelMove;
+  return (level & 1) ? kLevelGrouped : kLevelInPlace;
+}
+
+// The set holding the rows of level `level`'s parents (their own segments;
+// a grouped level's: its grandparents'); a moving level writes the other
+// set of the tree's pair.
+int level_src(const bsscl_engine *E, int32_t level) {
+  return E->set_base + (E->pair_levels ? ((level >> 1) & 1) : (level & 1));
+}
+
+// The planner of level `level`.
 int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParams &tp,
                       int32_t F_sel) {
   PlanArgs pa;
@@ -1064,47 +1102,54 @@ int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParam
   pa.node_cap = E->node_cap;
   pa.tile_cap = E->tile_cap;
   pa.hist_cap = E->hist_cap;
-  pa.hist_target = hist_target(E, F_sel);
+  pa.hist_target = hist_target(E, F_sel, level_mode(E, level) == kLevelInPlace);
   pa.rows_per_flush = E->hist_rows_per_flush_level;
   pa.part_tile = E->part_tile;
+  pa.mode = level_mode(E, level);
   hipEvent_t stop;
   CHK(prof_begin(E, 2, &stop));
   if (E->plan_lds)
     HIPCHK(launch_plan_lds(E->st, E->nodes_d, E->plan_d, E->parents_d[(level + 1) & 1].p,
-                           E->parents_d[level & 1].p, E->tile_begin_d.p, E->hist_begin_d.p,
-                           E->tiles_d.p, E->hist_tasks_d.p, E->segs.p,
+                           E->parents_d[level & 1].p, E->groups_d.p, E->tile_begin_d.p,
+                           E->hist_begin_d.p, E->tiles_d.p, E->hist_tasks_d.p, E->segs.p,
                            E->totals.p, E->cand.p, E->kept_e_d.p,
                            E->parent_e_d[(level + 1) & 1].p, E->parent_e_d[level & 1].p,
                            F_sel, pa));
-  else
+  else if (pa.mode == kLevelMove)
     HIPCHK(launch_plan(E->st, E->nodes_d, E->plan_d, E->parents_d[(level + 1) & 1].p,
                        E->parents_d[level & 1].p, E->tile_begin_d.p, E->hist_begin_d.p,
                        E->tiles_d.p, E->hist_tasks_d.p,
                        E->work_flag_d.p, E->work_e_d.p, E->segs.p, E->totals.p, E->cand.p,
                        F_sel, pa));
+  else
+    return set_error(BSSCL_EINTERNAL, "paired levels need the LDS planner");
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
 
-// Count / scan / scatter of one level's parents (rows of set src move to
-// their children's segments in set dst).
+// Count of one level's groups (groups == nullptr: one per parent), then
+// the scatter of their rows from set src to their children's segments in
+// set dst (move_rows), or the children's sizes only (sizes: an in-place
+// level).  (The last level moves nothing: k_last_level takes the sizes.)
 int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parents,
-                     const int32_t *tile_begin, const PartTile *tiles, const LevelPlan *plan,
-                     int32_t max_parents, int32_t max_tiles, int32_t F_sel,
-                     int32_t min_samples_leaf, bool move_rows) {
+                     const PartGroup *groups, const int32_t *tile_begin, const PartTile *tiles,
+                     const LevelPlan *plan, int32_t max_parents, int32_t max_tiles,
+                     int32_t F_sel, int32_t min_samples_leaf, bool move_rows, bool sizes) {
   hipEvent_t stop;
   CHK(prof_begin(E, 1, &stop));
-  HIPCHK(launch_part_count(E->st, E->codes_c[src].p, E->ld_c, parents, tiles, plan,
-                           max_tiles, E->part_rows, E->tile_left_d.p));
-  if (move_rows)  // the scatter does each parent's scan itself
+  HIPCHK(launch_part_count(E->st, E->codes_c[src].p, E->ld_c, parents, groups, tiles, plan,
+                           max_tiles, E->part_rows, E->tile_cnt_d.p));
+  if (move_rows)  // the scatter does each group's scan itself
     HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p, E->ld_c,
                                E->gh_c[src].p, E->gh_c[dst].p,
                                E->track_rid ? E->rid_c[src & 1].p : nullptr,
-                               E->track_rid ? E->rid_c[dst & 1].p : nullptr, parents, tiles,
-                               plan, max_tiles, E->part_rows, tile_begin, E->tile_left_d.p,
-                               E->nleft_d.p, E->segs.p, E->hist_node_d.p, min_samples_leaf,
-                               F_sel));
-  // (Without rows to move -- the last level -- k_last_level does the scan.)
+                               E->track_rid ? E->rid_c[dst & 1].p : nullptr, parents, groups,
+                               tiles, plan, max_tiles, E->part_rows, tile_begin,
+                               E->tile_cnt_d.p, E->nleft_d.p, E->segs.p, E->hist_node_d.p,
+                               min_samples_leaf, F_sel));
+  else if (sizes)
+    HIPCHK(launch_part_sizes(E->st, parents, plan, max_parents, tile_begin, E->tile_cnt_d.p,
+                             E->nleft_d.p, E->segs.p, E->hist_node_d.p, min_samples_leaf));
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
@@ -1115,34 +1160,42 @@ int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parent
 // totals only, so their rows are not moved and their histograms not built.
 int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
                  const TreeParams &tp, int32_t F_sel) {
-  const int src = E->set_base + (level & 1), dst = E->set_base + ((level & 1) ^ 1);
+  const int32_t mode = level_mode(E, level);
+  const int src = level_src(E, level);
+  const int dst = E->set_base + ((src - E->set_base) ^ 1);
   const PartParent *par = E->parents_d[level & 1].p;
+  const PartGroup *grp = mode == kLevelGrouped ? E->groups_d.p : nullptr;
+  const bool in_place = mode == kLevelInPlace;
   const int32_t P = level_parents_bound(E, level);
   const int32_t T = (int32_t)std::min<int64_t>(E->tile_cap, m / E->part_tile + 2 * (int64_t)P + 1);
-  CHK(launch_partition(E, src, dst, par, E->tile_begin_d.p, E->tiles_d.p, E->plan_d, P, T,
-                       F_sel, tp.min_samples_leaf, !last));
+  CHK(launch_partition(E, src, dst, par, grp, E->tile_begin_d.p, E->tiles_d.p, E->plan_d, P, T,
+                       F_sel, tp.min_samples_leaf, !last && !in_place, !last && in_place));
   hipEvent_t stop;
   if (last) {
     CHK(prof_begin(E, 2, &stop));
-    HIPCHK(launch_last_level(E->st, par, E->plan_d, std::min(P, 4096), E->tile_begin_d.p,
-                             E->tile_left_d.p, E->nleft_d.p, E->segs.p, E->hist_node_d.p,
-                             tp.min_samples_leaf, E->pool.p, E->node_stride, E->totals.p,
-                             E->nodes_d));
+    HIPCHK(launch_last_level(E->st, par, grp ? 1 : 0, E->plan_d, std::min(P, 4096),
+                             E->tile_begin_d.p, E->tile_cnt_d.p, E->nleft_d.p, E->segs.p,
+                             E->hist_node_d.p, tp.min_samples_leaf, E->pool.p, E->node_stride,
+                             E->totals.p, E->nodes_d));
     CHK(prof_end(E, stop));
     return BSSCL_OK;
   }
-  const int32_t H = (int32_t)std::min<int64_t>(E->hist_cap, (int64_t)hist_target(E, F_sel) + 2 * (int64_t)P + 2);
-  {
-    HIPCHK(launch_hist(E->st, E->codes_c[dst].p, E->ld_c, E->gh_c[dst].p, E->hist_tasks_d.p,
-                       E->plan_d, H, E->hist_node_d.p, E->hist_begin_d.p, E->segs.p,
-                       E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel), E->hist_copies,
-                       E->part_d.p, E->pool.p, E->node_stride,
-                       prof_slot(E, hist_grid(E, H, F_sel))));
-  }
+  const int32_t H = (int32_t)std::min<int64_t>(
+      E->hist_cap, (int64_t)hist_target(E, F_sel, in_place) + 2 * (int64_t)P + 2);
+  // In place, the smaller children's rows are read from their parents'
+  // segments in src.
+  const int hs = in_place ? src : dst;
+  HIPCHK(launch_hist(E->st, E->codes_c[hs].p, E->ld_c, E->gh_c[hs].p, E->hist_tasks_d.p,
+                     E->plan_d, H, E->hist_node_d.p, E->hist_begin_d.p, E->segs.p,
+                     E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel, in_place),
+                     in_place ? E->hist_copies_span : E->hist_copies, E->part_d.p, E->pool.p,
+                     E->node_stride, in_place ? par : nullptr,
+                     prof_slot(E, hist_grid(E, H, F_sel, in_place))));
   CHK(prof_begin(E, 2, &stop));
   HIPCHK(launch_reduce_split(E->st, E->plan_d, P, par, E->hist_begin_d.p, E->hist_node_d.p,
                              E->segs.p, E->part_d.p, E->pool.p, E->node_stride, E->nb_sel_d,
-                             F_sel, level + 1, split_params(E, tp), E->cand.p, E->totals.p));
+                             F_sel, level + 1, split_params(E, tp), E->cand.p, E->totals.p,
+                             in_place ? 1 : 0));
   // The new nodes' table records are written by the next level's planner.
   CHK(prof_end(E, stop));
   return BSSCL_OK;
@@ -1274,6 +1327,9 @@ int launch_tree(bsscl_engine *E, const int32_t *rows32, int64_t m,
                 bool checks = true, bool gathered = false, const PreRoot *pre = nullptr) {
   const int32_t F_sel = (int32_t)feats.size();
   const int32_t levels = std::max(1, tp.max_depth);
+  // (Test hook: BSSCL_TEST_PAIR_LEVELS=0 moves the rows at every level.)
+  const char *pl = std::getenv("BSSCL_TEST_PAIR_LEVELS");
+  E->pair_levels = E->plan_lds && !(pl && pl[0] == '0');
   CHK(launch_root(E, rows32, m, feats, nb_sel, tp, gathered, pre));
   *run = 0;
   for (int32_t d = 0; d < levels; ++d) {
@@ -1958,6 +2014,7 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->cand.release();
   E->totals.release();
   for (int s = 0; s < 2; ++s) E->parents_d[s].release();
+  E->groups_d.release();
   E->tile_begin_d.release();
   E->hist_begin_d.release();
   E->work_flag_d.release();
@@ -1967,7 +2024,7 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->work_e_d.release();
   E->nleft_d.release();
   E->tiles_d.release();
-  E->tile_left_d.release();
+  E->tile_cnt_d.release();
   E->hist_tasks_d.release();
   E->tree_d.release();
   for (int b = 0; b < 2; ++b) {
@@ -2712,11 +2769,11 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
   pk2.add(&lp, sizeof(lp));
   CHK(sync(E));  // the gather has read dv[0]: the arena may be reused
   CHK(upload_pack(E, pk2, dv));
-  CHK(launch_partition(E, 0, 1, reinterpret_cast<const PartParent *>(dv[0]),
+  CHK(launch_partition(E, 0, 1, reinterpret_cast<const PartParent *>(dv[0]), nullptr,
                        reinterpret_cast<const int32_t *>(dv[1]),
                        reinterpret_cast<const PartTile *>(dv[2]),
                        reinterpret_cast<const LevelPlan *>(dv[3]), 1, (int32_t)tiles.size(),
-                       1, 0, true));
+                       1, 0, true, false));
   E->track_rid = false;
   std::vector<int32_t> r32((size_t)m);
   int64_t nl = 0;

@@ -32,7 +32,24 @@ struct PartParent {
   int32_t left_id;   // internal node ids of the children
   int32_t right_id;
   int32_t node;      // the parent's own id
-  int32_t pad;
+  int32_t gslot;     // 2 * its PartGroup + its side (levels with groups only)
+};
+
+// A partition group: the rows [start, start + count) of the source set,
+// sent first by an optional split (fpos >= 0: code <= bin is side 0, else
+// side 1; fpos < 0: every row is on side 0) to the parent par[side], then
+// by that parent's own split to its left or right child.  The rows of a
+// side whose par is -1 are not moved.  A level whose parents' rows lie in
+// their own segments has no groups: group i is parent i.  A level whose
+// parents are the children of the previous level's parents, still in their
+// parent's segment, has one group per such grandparent.  Each tile counts
+// its rows of the four runs 2 * side + (right child ? 1 : 0).
+struct PartGroup {
+  int64_t start;
+  int64_t count;
+  int32_t fpos;
+  int32_t bin;
+  int32_t par[2];
 };
 
 // Work counts of one level, written by the planner kernel (or uploaded for
@@ -61,13 +78,28 @@ struct PlanArgs {
   int32_t hist_target;    // histogram row tiles wanted per level
   int32_t rows_per_flush; // fewest rows per histogram tile flush
   int32_t part_tile;      // rows per partition tile
+  int32_t mode;           // kLevelMove, kLevelInPlace or kLevelGrouped
 };
 
-// One partition tile of a parent (host -> device).
+// How a level treats its rows:
+//   kLevelMove: the parents' rows move to their children's segments in the
+//     other set (one group per parent), and the smaller children's
+//     histograms read them there;
+//   kLevelInPlace: the rows stay in the parents' segments; the children get
+//     the segments the move would give them, and the smaller child's
+//     histogram reads its parent's segment, taking the rows that go its way;
+//   kLevelGrouped: the parents are the children of an in-place level; their
+//     rows move from the grandparents' segments (one group per grandparent)
+//     straight to their children's segments in the other set.
+constexpr int32_t kLevelMove = 0;
+constexpr int32_t kLevelInPlace = 1;
+constexpr int32_t kLevelGrouped = 2;
+
+// One partition tile of a group (host -> device).
 struct PartTile {
   int64_t row0;
   int32_t rows;
-  int32_t parent;    // index into the level's PartParent array
+  int32_t parent;    // its PartGroup (the PartParent of that index without groups)
 };
 
 // One histogram work item: `tile`-th block of rows of node hist_node[ref].
@@ -215,6 +247,9 @@ hipError_t launch_gather_gh(hipStream_t st, const double *F, const uint8_t *y,
 // Level kernels take their work counts from a device LevelPlan; the grid
 // argument (blocks, tasks or parents) is an upper bound, and blocks loop
 // over the work with a grid stride, so any bound >= 1 gives the same result.
+// With `span` (an in-place level's parents), a task's rows are a tile of
+// its parent's segment and only the rows its split sends to the smaller
+// child (hist_node) are added.
 hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const GH *gh_c, const HistTask *tasks,
                        const LevelPlan *plan, int32_t max_tasks,
@@ -223,42 +258,56 @@ hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int32_t *nb_sel, const int32_t *hot_sel,
                        int32_t F_sel, int32_t fchunk, int32_t copies,
                        unsigned long long *part, unsigned long long *pool,
-                       int64_t node_stride, unsigned long long *ktime = nullptr);
-// Sums the partials that launch_hist stored for each node with a histogram
-// task (hist_begin: a node's tasks, hist_node: its id) into the pool.
+                       int64_t node_stride, const PartParent *span = nullptr,
+                       unsigned long long *ktime = nullptr);
 int hist_blocks(int32_t n_tasks, int32_t nchunks);
+// Per tile, its rows of each of the four runs (tile_cnt[4 * tile + run]).
+// groups == nullptr: group i is parent i.
 hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
-                             int64_t ld_c, const PartParent *parents,
+                             int64_t ld_c, const PartParent *parents, const PartGroup *groups,
                              const PartTile *tiles, const LevelPlan *plan,
-                             int32_t max_tiles, int32_t part_rows, int32_t *tile_left);
+                             int32_t max_tiles, int32_t part_rows, int32_t *tile_cnt);
+// Moves the rows of every group to its parents' children's segments in the
+// other set; each group's first tile writes the children's segments.
 hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                uint8_t *codes_dst, int64_t ld_c,
                                const GH *gh_src, GH *gh_dst,
                                const int32_t *rid_src, int32_t *rid_dst,
-                               const PartParent *parents,
+                               const PartParent *parents, const PartGroup *groups,
                                const PartTile *tiles, const LevelPlan *plan,
                                int32_t max_tiles, int32_t part_rows,
-                               const int32_t *tile_begin, const int32_t *tile_left,
+                               const int32_t *tile_begin, const int32_t *tile_cnt,
                                int64_t *parent_nleft, NodeSeg *segs, int32_t *hist_node,
                                int32_t min_samples_leaf, int32_t F_sel);
+// An in-place level after its count: each parent's children's segments (as
+// a move would place them), whether the split is kept and which child is
+// smaller, one wave per parent.
+hipError_t launch_part_sizes(hipStream_t st, const PartParent *parents, const LevelPlan *plan,
+                             int32_t max_parents, const int32_t *tile_begin,
+                             const int32_t *tile_cnt, int64_t *parent_nleft, NodeSeg *segs,
+                             int32_t *hist_node, int32_t min_samples_leaf);
 // Histogram reduction and split search of one level (parents == nullptr:
 // the root, node 0, whose tasks hist_begin[0] .. hist_begin[1] built it).
+// span_parents: the tasks of parent p tiled its own segment (an in-place
+// level), not its smaller child's.
 hipError_t launch_reduce_split(hipStream_t st, const LevelPlan *plan, int32_t max_parents,
                                const PartParent *parents, const int32_t *hist_begin,
                                const int32_t *hist_node, const NodeSeg *segs,
                                const unsigned long long *part, unsigned long long *pool,
                                int64_t node_stride, const int32_t *nb_sel, int32_t F_sel,
                                int32_t child_depth, SplitParams p, SplitCand *cand,
-                               long long *totals);
+                               long long *totals, int32_t span_parents = 0);
 hipError_t launch_node_best(hipStream_t st, const NodeSeg *segs,
                             const long long *totals, const SplitCand *cand,
                             int32_t F_sel, const LevelPlan *plan,
                             int32_t max_nodes, int32_t no_split, NodeOut *nodes);
 // The last level after its partition count: each parent's scan, its
-// children's totals and table records, one wave per parent.
-hipError_t launch_last_level(hipStream_t st, const PartParent *parents, const LevelPlan *plan,
+// children's totals and table records, one wave per parent (grouped: the
+// parent's counts are its side's runs in its group's tiles).
+hipError_t launch_last_level(hipStream_t st, const PartParent *parents, int32_t grouped,
+                             const LevelPlan *plan,
                              int32_t max_parents, const int32_t *tile_begin,
-                             const int32_t *tile_left, int64_t *parent_nleft, NodeSeg *segs,
+                             const int32_t *tile_cnt, int64_t *parent_nleft, NodeSeg *segs,
                              int32_t *hist_node, int32_t min_samples_leaf,
                              const unsigned long long *pool, int64_t node_stride,
                              long long *totals, NodeOut *nodes);
@@ -274,9 +323,12 @@ hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                        const SplitCand *cand, int32_t F_sel, PlanArgs a);
 // k_plan with its intermediates in LDS, for trees of at most 513 nodes; keeps
 // kept_e (node ranks of kept splits, per node) and parent_e (ranks of a
-// level's parents, by level parity) for the levels after it.
+// level's parents, by level parity) for the levels after it.  Plans any
+// level mode (a.mode); a grouped level also writes its PartGroup list.
+// (k_plan plans kLevelMove levels only.)
 hipError_t launch_plan_lds(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                            const PartParent *prev_parents, PartParent *parents,
+                           PartGroup *groups,
                            int32_t *tile_begin, int32_t *hist_begin, PartTile *tiles,
                            HistTask *hist_tasks, const NodeSeg *segs,
                            const long long *totals, const SplitCand *cand, double *kept_e,

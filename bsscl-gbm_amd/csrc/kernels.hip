@@ -35,18 +35,17 @@ __device__ __forceinline__ T wave_incl_scan(T v) {
 }
 
 // Exclusive scan over a block of BLOCK threads; `tmp` holds BLOCK/64 words.
-template <int BLOCK>
-__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t *tmp,
-                                                    uint32_t &total) {
+template <int BLOCK, typename T>
+__device__ __forceinline__ T block_excl_scan(T v, T *tmp, T &total) {
   const int wid = (int)(threadIdx.x >> 6);
-  const uint32_t incl = wave_incl_scan<uint32_t>(v);
+  const T incl = wave_incl_scan<T>(v);
   if (lane_id() == 63) tmp[wid] = incl;
   __syncthreads();
-  uint32_t pre = 0, tot = 0;
+  T pre = 0, tot = 0;
 #pragma unroll
   for (int w = 0; w < BLOCK / 64; ++w) {
-    uint32_t s = tmp[w];
-    pre += (w < wid) ? s : 0u;
+    T s = tmp[w];
+    pre += (w < wid) ? s : T(0);
     tot += s;
   }
   __syncthreads();
@@ -609,21 +608,169 @@ __device__ __forceinline__ int32_t hist_tasks_with_rows(const int32_t *__restric
   return (int32_t)min((int64_t)(hist_begin[p + 1] - hist_begin[p]), with_rows);
 }
 
+// In place (an in-place level's task: a tile of its parent's segment, of
+// which only the rows going to the smaller child are added).  Each wave
+// takes 64 x kSpanRows rows at a time: every lane loads its rows' codes of
+// the split feature and of the block's features (one load per feature, as
+// the compact path), stores each row's codes as one word per four features
+// in the wave's part of LDS, and the wave lists the rows to add (a prefix
+// sum over its lanes).  The lanes then take the listed rows in turn, with
+// one (g,h) load each, so that every LDS add has all lanes active whatever
+// share of the rows is added.  A wave reads only what it wrote itself, and
+// a wave's LDS operations complete in issue order, so no barrier is needed
+// between its steps.
+constexpr int kSpanRows = 8;
+constexpr int kSpanWave = 64 * kSpanRows;        // rows per wave and step
+constexpr int kSpanStep = kHistBlock * kSpanRows;  // rows per block and step
+
 template <int FC, int C>
+__device__ __forceinline__ void hist_rows_span(
+    unsigned long long *lh, uint32_t *stage, uint16_t *mlist, uint32_t *stmp,
+    const uint8_t *__restrict__ codes_c, int64_t ld_c, const GH *__restrict__ gh_c, int f0,
+    int nf, const uint32_t (&lim)[FC], const uint32_t (&hb)[FC], long long (&ag)[FC],
+    long long (&ah)[FC], int64_t r0, int64_t r1, const uint8_t *__restrict__ scol,
+    uint32_t sbin, bool sright) {
+  (void)stmp;
+  constexpr int kW = (FC + 3) / 4;  // LDS words per row
+  const int lane = lane_id(), wave = (int)(threadIdx.x >> 6);
+  const int copy = lane & (C - 1);
+  uint32_t *wst = stage + wave * kSpanWave;  // this wave's rows: word q at q * kSpanStep
+  uint16_t *wl = mlist + wave * kSpanWave;
+  // The wave's groups of kSpanRows rows: every fourth run of 64 groups.  The
+  // codes of the wave's next step are loaded before this step's listed rows
+  // are added.
+  const int64_t g0 = r0 / kSpanRows, g1 = (r1 + kSpanRows - 1) / kSpanRows;
+  uint2 nsv = make_uint2(0u, 0u), ncv[FC];
+  auto load_step = [&](int64_t gb) {
+    const int64_t g = gb + lane;
+    if (g < g1) {
+      const int64_t row = g * kSpanRows;
+      nsv = *reinterpret_cast<const uint2 *>(scol + row);
+#pragma unroll
+      for (int u = 0; u < FC; ++u)
+        ncv[u] = u < nf ? *reinterpret_cast<const uint2 *>(codes_c + (int64_t)(f0 + u) * ld_c + row)
+                        : make_uint2(0u, 0u);
+    }
+  };
+  load_step(g0 + (int64_t)wave * 64);
+  for (int64_t gb = g0 + (int64_t)wave * 64; gb < g1; gb += (int64_t)kHistBlock) {
+    const int64_t g = gb + lane;
+    const int64_t row = g * kSpanRows;
+    uint32_t mem = 0u;
+    if (g < g1) {
+      const uint2 sv = nsv;
+      uint2 cv[FC];
+#pragma unroll
+      for (int u = 0; u < FC; ++u) cv[u] = ncv[u];
+      const uint32_t sw[2] = {sv.x, sv.y};
+#pragma unroll
+      for (int k = 0; k < kSpanRows; ++k) {
+        const bool right = ((sw[k >> 2] >> (8 * (k & 3))) & 255u) > sbin;
+        const bool in = row + k >= r0 && row + k < r1;
+        mem |= ((in && right == sright) ? 1u : 0u) << k;
+      }
+#pragma unroll
+      for (int q = 0; q < kW; ++q) {
+        uint32_t w[kSpanRows];
+#pragma unroll
+        for (int k = 0; k < kSpanRows; ++k) {
+          w[k] = 0u;
+#pragma unroll
+          for (int u = 4 * q; u < FC && u < 4 * q + 4; ++u) {
+            const uint32_t cw = (k < 4) ? cv[u].x : cv[u].y;
+            w[k] |= ((cw >> (8 * (k & 3))) & 255u) << (8 * (u - 4 * q));
+          }
+        }
+        uint4 *sp = reinterpret_cast<uint4 *>(wst + q * kSpanStep + kSpanRows * lane);
+        sp[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        sp[1] = make_uint4(w[4], w[5], w[6], w[7]);
+      }
+    }
+    if (gb + kHistBlock < g1) load_step(gb + kHistBlock);
+    const uint32_t cnt = (uint32_t)__builtin_popcount(mem);
+    const uint32_t incl = wave_incl_scan<uint32_t>(cnt);
+    const int nm = (int)__shfl(incl, 63, 64);
+    uint32_t at = incl - cnt;
+#pragma unroll
+    for (int k = 0; k < kSpanRows; ++k)
+      if ((mem >> k) & 1u) wl[at++] = (uint16_t)(kSpanRows * lane + k);
+    __builtin_amdgcn_wave_barrier();
+    // The listed rows, four per lane in flight.
+    const int64_t base = gb * kSpanRows;
+    for (int j0 = lane; j0 < nm; j0 += 4 * 64) {
+      long long gq[4], hq[4];
+      uint32_t ww[4][kW];
+      bool ok[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = j0 + e * 64;
+        ok[e] = j < nm;
+        const int rl = ok[e] ? (int)wl[j] : 0;
+        const GH v = ok[e] ? gh_c[base + rl] : GH{0, 0};
+        gq[e] = v.x;
+        hq[e] = v.y;
+#pragma unroll
+        for (int q = 0; q < kW; ++q) ww[e][q] = wst[q * kSpanStep + rl];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (!ok[e]) continue;
+#pragma unroll
+        for (int u = 0; u < FC; ++u) {
+          if (u >= nf) break;
+          unsigned long long *hf = lh + u * kHistPerFeat * C + copy;
+          const uint32_t bin = min((ww[e][u >> 2] >> (8 * (u & 3))) & 255u, lim[u]);
+          // The feature's most frequent bin is summed in registers.
+          if (bin == hb[u]) {
+            ag[u] += gq[e];
+            ah[u] += hq[e];
+          } else {
+            __hip_atomic_fetch_add(hf + bin * C, (unsigned long long)gq[e], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_fetch_add(hf + (kBins + bin) * C, (unsigned long long)hq[e],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // (the next step's stores follow these reads)
+  }
+}
+
+// SPAN: the task tiles the segment of parent span[task.ref] and adds the
+// rows whose code of the parent's split feature sends them to the smaller
+// child hist_node[task.ref] (hist_rows_span).
+template <int FC, int C, bool SPAN>
 __device__ __forceinline__ void hist_item(
-    unsigned long long *lh, const uint8_t *__restrict__ codes_c, int64_t ld_c,
+    unsigned long long *lh, uint32_t *stage, uint16_t *mlist, uint32_t *stmp,
+    const uint8_t *__restrict__ codes_c, int64_t ld_c,
     const GH *__restrict__ gh_c, const HistTask task, int32_t ti, int chunk,
     const int32_t *__restrict__ hist_node, const int32_t *__restrict__ hist_begin,
-    const NodeSeg *__restrict__ segs,
+    const NodeSeg *__restrict__ segs, const PartParent *__restrict__ span,
     const int32_t *__restrict__ nb_sel, const int32_t *__restrict__ hot_sel,
     int32_t F_sel, int32_t tile_rows, unsigned long long *__restrict__ part,
     unsigned long long *__restrict__ pool, int64_t node_stride) {
   const int32_t node = hist_node[task.ref];
   if (node < 0) return;
-  const NodeSeg seg = segs[node];
-  if (!seg.valid) return;
-  const int64_t r0 = seg.start + (int64_t)task.tile * tile_rows;
-  const int64_t rend = seg.start + seg.count;
+  int64_t s0, sn;  // the rows the tasks of this reference tile
+  const uint8_t *scol = nullptr;
+  uint32_t sbin = 0u;
+  bool sright = false;
+  if constexpr (SPAN) {
+    const PartParent P = span[task.ref];
+    s0 = P.start;
+    sn = P.count;
+    scol = codes_c + (int64_t)P.fpos * ld_c;
+    sbin = (uint32_t)P.bin;
+    sright = node != P.left_id;
+  } else {
+    const NodeSeg seg = segs[node];
+    if (!seg.valid) return;
+    s0 = seg.start;
+    sn = seg.count;
+  }
+  const int64_t r0 = s0 + (int64_t)task.tile * tile_rows;
+  const int64_t rend = s0 + sn;
   if (r0 >= rend) return;
   const int64_t r1 = min(rend, r0 + (int64_t)tile_rows);
   const int f0 = chunk * FC;
@@ -642,6 +789,10 @@ __device__ __forceinline__ void hist_item(
   __syncthreads();
   const int copy = lane_id() & (C - 1);
 
+  if constexpr (SPAN) {
+    hist_rows_span<FC, C>(lh, stage, mlist, stmp, codes_c, ld_c, gh_c, f0, nf, lim, hb, ag, ah,
+                          r0, r1, scol, sbin, sright);
+  } else {
   const int64_t g0 = r0 >> 4, g1 = (r1 + 15) >> 4;
   for (int64_t g = g0 + threadIdx.x; g < g1; g += kHistBlock) {
     const int64_t row = g << 4;
@@ -706,6 +857,7 @@ __device__ __forceinline__ void hist_item(
       }
     }
   }
+  }
   // Hot-bin sums: wave reduction, then one LDS add per wave.
 #pragma unroll
   for (int u = 0; u < FC; ++u) {
@@ -728,7 +880,7 @@ __device__ __forceinline__ void hist_item(
   // by this one task gets it as its histogram directly (k_reduce_split reads
   // such nodes).
   unsigned long long *dst =
-      hist_tasks_with_rows(hist_begin, task.ref, seg.count, tile_rows) == 1
+      hist_tasks_with_rows(hist_begin, task.ref, sn, tile_rows) == 1
           ? pool + (int64_t)node * node_stride + (int64_t)f0 * kHistPerFeat
           : part + ((int64_t)ti * F_sel + f0) * kHistPerFeat;
   for (int i = threadIdx.x; i < nf * kHistPerFeat; i += kHistBlock) {
@@ -742,17 +894,23 @@ __device__ __forceinline__ void hist_item(
   __syncthreads();  // lh is cleared again by the block's next item
 }
 
-template <int FC, int C>
+template <int FC, int C, bool SPAN>
 __global__ __launch_bounds__(kHistBlock) void k_hist(
     const uint8_t *__restrict__ codes_c, int64_t ld_c,
     const GH *__restrict__ gh_c, const HistTask *__restrict__ tasks,
     const LevelPlan *__restrict__ plan, const int32_t *__restrict__ hist_node,
     const int32_t *__restrict__ hist_begin,
-    const NodeSeg *__restrict__ segs, const int32_t *__restrict__ nb_sel,
+    const NodeSeg *__restrict__ segs, const PartParent *__restrict__ span,
+    const int32_t *__restrict__ nb_sel,
     const int32_t *__restrict__ hot_sel, int32_t F_sel, int32_t nchunks,
     unsigned long long *__restrict__ part, unsigned long long *__restrict__ pool,
     int64_t node_stride, unsigned long long *__restrict__ ktime) {
   __shared__ unsigned long long lh[FC * kHistPerFeat * C];
+  // In place: each step's codes (one word per four features and row) and
+  // listed rows.
+  __shared__ __align__(16) uint32_t stage[SPAN ? (FC + 3) / 4 : 1][SPAN ? kSpanStep : 1];
+  __shared__ uint16_t mlist[SPAN ? kSpanStep : 1];
+  __shared__ uint32_t stmp[kHistBlock / 64];
   const int32_t n_tasks = plan->n_hist;
   const int32_t tile_rows = plan->tile_rows;
   // Optional timing: each block's start and end on the constant-rate clock,
@@ -766,9 +924,9 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
     const int ti = (j / nchunks) * 8 + (b & 7);
     if ((j / nchunks) * 8 >= n_tasks) break;
     if (ti >= n_tasks) continue;
-    hist_item<FC, C>(lh, codes_c, ld_c, gh_c, tasks[ti], ti, j % nchunks, hist_node,
-                     hist_begin, segs, nb_sel, hot_sel, F_sel, tile_rows, part, pool,
-                     node_stride);
+    hist_item<FC, C, SPAN>(lh, &stage[0][0], mlist, stmp, codes_c, ld_c, gh_c, tasks[ti], ti, j % nchunks, hist_node,
+                           hist_begin, segs, span, nb_sel, hot_sel, F_sel, tile_rows, part,
+                           pool, node_stride);
   }
   if (ktime) {
     __syncthreads();  // every wave's stores issued
@@ -788,14 +946,20 @@ hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const int32_t *nb_sel, const int32_t *hot_sel,
                        int32_t F_sel, int32_t fchunk, int32_t copies,
                        unsigned long long *part, unsigned long long *pool,
-                       int64_t node_stride, unsigned long long *ktime) {
+                       int64_t node_stride, const PartParent *span,
+                       unsigned long long *ktime) {
   if (max_tasks <= 0) return hipSuccess;
   const int32_t nchunks = (F_sel + fchunk - 1) / fchunk;
   const dim3 grid((unsigned)hist_blocks(max_tasks, nchunks));
-#define BSSCL_HIST(FC, C)                                                                  \
-  hipLaunchKernelGGL((k_hist<FC, C>), grid, dim3(kHistBlock), 0, st, codes_c, ld_c, gh_c, tasks, \
-                     plan, hist_node, hist_begin, segs, nb_sel, hot_sel, F_sel, nchunks, part,  \
-                     pool, node_stride, ktime)
+#define BSSCL_HIST(FC, C)                                                                    \
+  if (span)                                                                                  \
+    hipLaunchKernelGGL((k_hist<FC, C, true>), grid, dim3(kHistBlock), 0, st, codes_c, ld_c, gh_c, \
+                       tasks, plan, hist_node, hist_begin, segs, span, nb_sel, hot_sel, F_sel,  \
+                       nchunks, part, pool, node_stride, ktime);                              \
+  else                                                                                       \
+    hipLaunchKernelGGL((k_hist<FC, C, false>), grid, dim3(kHistBlock), 0, st, codes_c, ld_c,   \
+                       gh_c, tasks, plan, hist_node, hist_begin, segs, span, nb_sel, hot_sel,  \
+                       F_sel, nchunks, part, pool, node_stride, ktime)
   // LDS per block: fchunk * copies * 8 KB (at most 32 KB).
   switch (fchunk * 16 + copies) {
     case 1 * 16 + 1: BSSCL_HIST(1, 1); break;
@@ -814,9 +978,11 @@ hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
 // ---------------------------------------------------------------------------
 // Partition (est:662-674, made stable): count, scan, scatter.  A tile is 256
 // threads x R rows (R = 4, 8 or 16, chosen per tree: 1024 to 4096 rows)
-// starting at a 16-row boundary; rows of the tile outside the parent's
+// starting at a 16-row boundary; rows of the tile outside its group's
 // segment are masked.  A thread reads its R rows' codes of a feature as one
-// R-byte load.
+// R-byte load.  A group (PartGroup) sends each row by up to two splits to
+// one of four runs, 2 * side + (right child ? 1 : 0), so one pass can move
+// rows down two tree levels; each run keeps the input order.
 // ---------------------------------------------------------------------------
 constexpr int kPartBlock = 256;
 
@@ -831,10 +997,12 @@ union CodeWords {
   uint32_t w[R / 4];
 };
 
-__device__ __forceinline__ void tile_rows(const PartTile &t, const PartParent &P,
-                                          int64_t &lo, int64_t &hi) {
-  lo = max(t.row0, P.start);
-  hi = min(t.row0 + (int64_t)t.rows, P.start + P.count);
+template <int R>
+__device__ __forceinline__ CodeWords<R> zero_codes() {
+  CodeWords<R> c;
+#pragma unroll
+  for (int k = 0; k < R / 4; ++k) c.w[k] = 0u;
+  return c;
 }
 
 // The R codes of rows row .. row+R-1 of one feature column; a group wholly
@@ -846,79 +1014,232 @@ __device__ __forceinline__ CodeWords<R> load_codes(const uint8_t *__restrict__ c
   if (row < hi && row + R > lo) {
     c.v = *reinterpret_cast<const typename CodesR<R>::T *>(col + row);
   } else {
-#pragma unroll
-    for (int k = 0; k < R / 4; ++k) c.w[k] = 0u;
+    c = zero_codes<R>();
   }
   return c;
 }
 
-// Bit k of the result: row row+k lies in [lo, hi) (valid) and, for lmask,
-// goes left (code <= bin).
+// Tile t's group: groups[g], or (without groups) parent g as the only side.
+__device__ __forceinline__ PartGroup tile_group(const PartGroup *__restrict__ groups,
+                                                const PartParent *__restrict__ parents,
+                                                int32_t g) {
+  if (groups) return groups[g];
+  const PartParent P = parents[g];
+  PartGroup G;
+  G.start = P.start;
+  G.count = P.count;
+  G.fpos = -1;
+  G.bin = 0;
+  G.par[0] = g;
+  G.par[1] = -1;
+  return G;
+}
+
+// A tile's routing: its group's rows of the tile [lo, hi), the side
+// parents' splits and the codes each split reads for this thread's rows.
 template <int R>
-__device__ __forceinline__ void row_masks(const CodeWords<R> &c, int64_t row, int64_t lo,
-                                          int64_t hi, uint32_t bin, uint32_t &vmask,
-                                          uint32_t &lmask) {
-  vmask = 0u;
-  lmask = 0u;
+struct Route {
+  int64_t lo, hi;
+  CodeWords<R> c0, ca, cb;  // the group's split, side 0's and side 1's
+  uint32_t bin_a, bin_b;
+};
+
+template <int R>
+__device__ __forceinline__ Route<R> route_load(const uint8_t *__restrict__ codes_c, int64_t ld_c,
+                                               const PartTile &t, const PartGroup &G,
+                                               const PartParent &Pa, const PartParent &Pb,
+                                               int64_t row) {
+  Route<R> q;
+  q.lo = max(t.row0, G.start);
+  q.hi = min(t.row0 + (int64_t)t.rows, G.start + G.count);
+  q.bin_a = (uint32_t)Pa.bin;
+  q.bin_b = (uint32_t)Pb.bin;
+  q.c0 = G.fpos >= 0 ? load_codes<R>(codes_c + (int64_t)G.fpos * ld_c, row, q.lo, q.hi)
+                     : zero_codes<R>();
+  q.ca = G.par[0] >= 0 ? load_codes<R>(codes_c + (int64_t)Pa.fpos * ld_c, row, q.lo, q.hi)
+                       : zero_codes<R>();
+  q.cb = G.par[1] >= 0 ? load_codes<R>(codes_c + (int64_t)Pb.fpos * ld_c, row, q.lo, q.hi)
+                       : zero_codes<R>();
+  return q;
+}
+
+// Bit k of run[r]: row row+k lies in the tile's part of the group and goes
+// to run r (side 1 when the group's split sends it right, then right when
+// its side's parent's split does: code > bin).  Rows of a side without a
+// parent are in no run.
+template <int R>
+__device__ __forceinline__ void route_masks(const Route<R> &q, const PartGroup &G, int64_t row,
+                                            uint32_t (&run)[4]) {
+  const bool has_a = G.par[0] >= 0, has_b = G.par[1] >= 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) run[r] = 0u;
 #pragma unroll
   for (int k = 0; k < R; ++k) {
-    const bool in = (row + k >= lo) && (row + k < hi);
-    vmask |= (in ? 1u : 0u) << k;
-    lmask |= ((in && ((c.w[k >> 2] >> (8 * (k & 3))) & 255u) <= bin) ? 1u : 0u) << k;
+    const int sh = 8 * (k & 3);
+    const bool in = (row + k >= q.lo) && (row + k < q.hi);
+    const bool side = G.fpos >= 0 && ((q.c0.w[k >> 2] >> sh) & 255u) > (uint32_t)G.bin;
+    const bool right = side ? ((q.cb.w[k >> 2] >> sh) & 255u) > q.bin_b
+                            : ((q.ca.w[k >> 2] >> sh) & 255u) > q.bin_a;
+    const uint32_t bit = ((in && (side ? has_b : has_a)) ? 1u : 0u) << k;
+    run[0] |= (!side && !right) ? bit : 0u;
+    run[1] |= (!side && right) ? bit : 0u;
+    run[2] |= (side && !right) ? bit : 0u;
+    run[3] |= (side && right) ? bit : 0u;
   }
+}
+
+// The side parents of a group (start 0 and no split when a side has none).
+__device__ __forceinline__ void group_parents(const PartGroup &G,
+                                              const PartParent *__restrict__ parents,
+                                              PartParent &Pa, PartParent &Pb) {
+  const PartParent none{0, 0, 0, 0, -1, -1, -1, 0};
+  Pa = G.par[0] >= 0 ? parents[G.par[0]] : none;
+  Pb = G.par[1] >= 0 ? parents[G.par[1]] : none;
 }
 
 template <int R>
 __global__ __launch_bounds__(kPartBlock) void k_part_count(
     const uint8_t *__restrict__ codes_c, int64_t ld_c,
-    const PartParent *__restrict__ parents, const PartTile *__restrict__ tiles,
-    const LevelPlan *__restrict__ plan, int32_t *__restrict__ tile_left) {
-  __shared__ uint32_t tmp[kPartBlock / 64];
+    const PartParent *__restrict__ parents, const PartGroup *__restrict__ groups,
+    const PartTile *__restrict__ tiles, const LevelPlan *__restrict__ plan,
+    int32_t *__restrict__ tile_cnt) {
+  __shared__ uint2 red[kPartBlock / 64];
   const int32_t n_tiles = plan->n_tiles;
   for (int32_t ti = (int32_t)blockIdx.x; ti < n_tiles; ti += (int32_t)gridDim.x) {
     const PartTile t = tiles[ti];
-    const PartParent P = parents[t.parent];
-    int64_t lo, hi;
-    tile_rows(t, P, lo, hi);
+    const PartGroup G = tile_group(groups, parents, t.parent);
+    PartParent Pa, Pb;
+    group_parents(G, parents, Pa, Pb);
     const int64_t row = t.row0 + (int64_t)R * threadIdx.x;
-    const CodeWords<R> c = load_codes<R>(codes_c + (int64_t)P.fpos * ld_c, row, lo, hi);
-    uint32_t vmask, lmask;
-    row_masks<R>(c, row, lo, hi, (uint32_t)P.bin, vmask, lmask);
-    uint32_t total;
-    block_excl_scan<kPartBlock>((uint32_t)__builtin_popcount(lmask), tmp, total);
-    if (threadIdx.x == 0) tile_left[ti] = (int32_t)total;
+    const Route<R> rt = route_load<R>(codes_c, ld_c, t, G, Pa, Pb, row);
+    uint32_t run[4];
+    route_masks<R>(rt, G, row, run);
+    // Four counts as 16-bit fields (a tile has at most 4096 rows).
+    uint32_t a = (uint32_t)__builtin_popcount(run[0]) | ((uint32_t)__builtin_popcount(run[1]) << 16);
+    uint32_t b = (uint32_t)__builtin_popcount(run[2]) | ((uint32_t)__builtin_popcount(run[3]) << 16);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      a += __shfl_xor(a, o, 64);
+      b += __shfl_xor(b, o, 64);
+    }
+    if (lane_id() == 0) red[threadIdx.x >> 6] = make_uint2(a, b);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t sa = 0u, sb = 0u;
+#pragma unroll
+      for (int w = 0; w < kPartBlock / 64; ++w) {
+        sa += red[w].x;
+        sb += red[w].y;
+      }
+      *reinterpret_cast<uint4 *>(tile_cnt + 4 * (int64_t)ti) =
+          make_uint4(sa & 0xffffu, sa >> 16, sb & 0xffffu, sb >> 16);
+    }
+    __syncthreads();  // red is rewritten by the block's next tile
   }
 }
 
 hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
-                             int64_t ld_c, const PartParent *parents,
+                             int64_t ld_c, const PartParent *parents, const PartGroup *groups,
                              const PartTile *tiles, const LevelPlan *plan,
-                             int32_t max_tiles, int32_t part_rows, int32_t *tile_left) {
+                             int32_t max_tiles, int32_t part_rows, int32_t *tile_cnt) {
   if (max_tiles <= 0) return hipSuccess;
+#define BSSCL_COUNT(R)                                                                 \
+  hipLaunchKernelGGL(k_part_count<R>, dim3((unsigned)max_tiles), dim3(kPartBlock), 0, st, \
+                     codes_c, ld_c, parents, groups, tiles, plan, tile_cnt)
   switch (part_rows) {
-    case 4: hipLaunchKernelGGL(k_part_count<4>, dim3((unsigned)max_tiles), dim3(kPartBlock), 0,
-                               st, codes_c, ld_c, parents, tiles, plan, tile_left); break;
-    case 8: hipLaunchKernelGGL(k_part_count<8>, dim3((unsigned)max_tiles), dim3(kPartBlock), 0,
-                               st, codes_c, ld_c, parents, tiles, plan, tile_left); break;
-    case 16: hipLaunchKernelGGL(k_part_count<16>, dim3((unsigned)max_tiles), dim3(kPartBlock), 0,
-                                st, codes_c, ld_c, parents, tiles, plan, tile_left); break;
+    case 4: BSSCL_COUNT(4); break;
+    case 8: BSSCL_COUNT(8); break;
+    case 16: BSSCL_COUNT(16); break;
     default: return hipErrorInvalidValue;
   }
+#undef BSSCL_COUNT
   return hipGetLastError();
 }
 
-// Moves a tile's rows to the child segments in the other buffer set, keeping
-// the input order on each side.  A row's slot (left run, then right run) is
-// a block-wide exclusive scan of per-thread counts plus its rank among the
-// thread's R rows; inv[slot] is the row it came from.  The output is cut
-// into R-byte chunks aligned in the destination.  Features move four at a
-// time: each tile row's four codes go to LDS as one 32-bit word (a 4x4 byte
-// transpose of the thread's loads), and each output chunk reads its R
-// source rows' words and transposes them back into one R-byte store per
-// feature (byte stores only for the chunks at the ends of a run, which it
-// shares with the neighbouring tiles).  (g,h) and row ids are gathered
-// through inv and stored as consecutive elements.
-constexpr int kChunkSlots = 2;  // output chunks a thread may own (<= 260 per tile)
+// The children of parent p, whose split sends nl of its rows left and nr
+// right: their segments (left first, from the parent's start), whether the
+// split is kept (est:678-683) and which child is the smaller one
+// (est:701-709), whose histogram is built.
+__device__ __forceinline__ void write_children(const PartParent &P, int32_t p, int64_t nl,
+                                               int64_t nr, int32_t min_samples_leaf,
+                                               int64_t *__restrict__ parent_nleft,
+                                               NodeSeg *__restrict__ segs,
+                                               int32_t *__restrict__ hist_node) {
+  const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
+  const bool left_small = nl <= nr;
+  parent_nleft[p] = nl;
+  NodeSeg Ls, Rs;
+  Ls.start = P.start;
+  Ls.count = nl;
+  Ls.valid = ok ? 1 : 0;
+  Ls.is_small = left_small ? 1 : 0;
+  Rs.start = P.start + nl;
+  Rs.count = nr;
+  Rs.valid = ok ? 1 : 0;
+  Rs.is_small = left_small ? 0 : 1;
+  segs[P.left_id] = Ls;
+  segs[P.right_id] = Rs;
+  hist_node[p] = ok ? (left_small ? P.left_id : P.right_id) : -1;
+}
+
+// A side's rows over its group's tiles [t0, t1): runs 2*side (left) and
+// 2*side + 1 (right), summed by one wave (every lane gets the sums).
+__device__ __forceinline__ void wave_side_counts(const int32_t *__restrict__ tile_cnt, int32_t t0,
+                                                 int32_t t1, int side, long long &nl,
+                                                 long long &nr) {
+  nl = 0;
+  nr = 0;
+  for (int32_t t = t0 + lane_id(); t < t1; t += 64) {
+    const int2 v = *reinterpret_cast<const int2 *>(tile_cnt + 4 * (int64_t)t + 2 * side);
+    nl += v.x;
+    nr += v.y;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    nl += __shfl_xor(nl, o, 64);
+    nr += __shfl_xor(nr, o, 64);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_part_sizes(
+    const PartParent *__restrict__ parents, const LevelPlan *__restrict__ plan,
+    const int32_t *__restrict__ tile_begin, const int32_t *__restrict__ tile_cnt,
+    int64_t *__restrict__ parent_nleft, NodeSeg *__restrict__ segs,
+    int32_t *__restrict__ hist_node, int32_t min_samples_leaf) {
+  const int32_t n_parents = plan->n_parents;
+  for (int w = (int)(blockIdx.x * 4 + (threadIdx.x >> 6)); w < n_parents;
+       w += (int)gridDim.x * 4) {
+    const PartParent P = parents[w];
+    long long nl, nr;
+    wave_side_counts(tile_cnt, tile_begin[w], tile_begin[w + 1], 0, nl, nr);
+    if (lane_id() == 0) write_children(P, w, nl, nr, min_samples_leaf, parent_nleft, segs, hist_node);
+  }
+}
+
+hipError_t launch_part_sizes(hipStream_t st, const PartParent *parents, const LevelPlan *plan,
+                             int32_t max_parents, const int32_t *tile_begin,
+                             const int32_t *tile_cnt, int64_t *parent_nleft, NodeSeg *segs,
+                             int32_t *hist_node, int32_t min_samples_leaf) {
+  if (max_parents <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_part_sizes, dim3((unsigned)((max_parents + 3) / 4)), dim3(256), 0, st,
+                     parents, plan, tile_begin, tile_cnt, parent_nleft, segs, hist_node,
+                     min_samples_leaf);
+  return hipGetLastError();
+}
+
+// Moves a tile's rows to their runs' segments in the other buffer set,
+// keeping the input order within each run.  A row's slot (the tile's rows
+// of run 0, then run 1, 2, 3) is a block-wide exclusive scan of per-thread
+// counts plus its rank among the thread's R rows; inv[slot] is the row it
+// came from.  The output is cut into R-byte chunks aligned in the
+// destination.  Features move four at a time: each tile row's four codes go
+// to LDS as one 32-bit word (a 4x4 byte transpose of the thread's loads),
+// and each output chunk reads its R source rows' words and transposes them
+// back into one R-byte store per feature (byte stores only for the chunks
+// at the ends of a run, which it shares with the neighbouring tiles).
+// (g,h) and row ids are gathered through inv and stored as consecutive
+// elements.
+constexpr int kChunkSlots = 2;  // output chunks a thread may own (<= 264 per tile)
 constexpr int kQuad = 4;        // features per LDS pass (one 32-bit word per row)
 
 // 4x4 byte transpose: byte j of r_i is byte i of w_j.
@@ -934,12 +1255,18 @@ __device__ __forceinline__ void transpose4(uint32_t w0, uint32_t w1, uint32_t w2
   r2 = (lo01 >> 16) | (lo23 & 0xffff0000u);
   r3 = (hi01 >> 16) | (hi23 & 0xffff0000u);
 }
-// Waves per SIMD the register budget must allow.  16-row tiles move one
-// feature per barrier through LDS bytes instead of four through words: the
-// word transposes of 16 rows need more registers than that occupancy allows.
+// Waves per SIMD the register budget must allow (4: 128 VGPRs, which the
+// four-run routing needs without spilling).  16-row tiles move one feature
+// per barrier through LDS bytes instead of four through words: the word
+// transposes of 16 rows need more registers than that.
 template <int R> struct ScatterWaves { static constexpr int value = 4; };
-template <> struct ScatterWaves<4> { static constexpr int value = 5; };
-template <> struct ScatterWaves<16> { static constexpr int value = 5; };
+
+// One of four values by a run index r in 0..3, as selects of values (an
+// array indexed by r would live in scratch memory).
+template <typename T>
+__device__ __forceinline__ T sel4(int r, T a, T b, T c, T d) {
+  return r == 0 ? a : r == 1 ? b : r == 2 ? c : d;
+}
 
 template <int R>
 __global__ __launch_bounds__(kPartBlock) __attribute__((amdgpu_waves_per_eu(ScatterWaves<R>::value)))
@@ -947,13 +1274,14 @@ void k_part_scatter(
     const uint8_t *__restrict__ codes_src, uint8_t *__restrict__ codes_dst,
     int64_t ld_c, const GH *__restrict__ gh_src, GH *__restrict__ gh_dst,
     const int32_t *__restrict__ rid_src, int32_t *__restrict__ rid_dst,
-    const PartParent *__restrict__ parents, const PartTile *__restrict__ tiles,
+    const PartParent *__restrict__ parents, const PartGroup *__restrict__ groups,
+    const PartTile *__restrict__ tiles,
     const LevelPlan *__restrict__ plan, const int32_t *__restrict__ tile_begin,
-    const int32_t *__restrict__ tile_left, int64_t *__restrict__ parent_nleft,
+    const int32_t *__restrict__ tile_cnt, int64_t *__restrict__ parent_nleft,
     NodeSeg *__restrict__ segs, int32_t *__restrict__ hist_node, int32_t min_samples_leaf,
     int32_t F_sel) {
-  __shared__ uint32_t tmp[kPartBlock / 64];
-  __shared__ unsigned long long red[kPartBlock / 64];
+  __shared__ unsigned long long tmp[kPartBlock / 64];
+  __shared__ unsigned long long red[kPartBlock / 64][4];
   constexpr int kTile = kPartBlock * R;
   __shared__ uint16_t inv[kTile];
   constexpr bool kQuads = R < 16;
@@ -965,106 +1293,127 @@ void k_part_scatter(
   const int tid = (int)threadIdx.x;
   for (int32_t ti = (int32_t)blockIdx.x; ti < n_tiles; ti += (int32_t)gridDim.x) {
     const PartTile t = tiles[ti];
-    const PartParent P = parents[t.parent];
-    int64_t lo, hi;
-    tile_rows(t, P, lo, hi);
+    const PartGroup G = tile_group(groups, parents, t.parent);
+    PartParent Pa, Pb;
+    group_parents(G, parents, Pa, Pb);
     const int64_t row = t.row0 + (int64_t)R * tid;
-    const CodeWords<R> sc = load_codes<R>(codes_src + (int64_t)P.fpos * ld_c, row, lo, hi);
-    // Left rows of the parent before this tile (high word) and in all its
-    // tiles (low word), from k_part_count's per-tile counts: the parent's
-    // scan, done by each of its tiles.
-    // (16-byte loads of four counts, two per thread in flight: one wait
-    // covers 2048 tiles; tile_left has room for the aligned overrun.)
+    const Route<R> rt = route_load<R>(codes_src, ld_c, t, G, Pa, Pb, row);
+    const int64_t lo = rt.lo, hi = rt.hi;
+    // (The masks first: the routing codes are not held through the scan.)
+    uint32_t run[4];
+    route_masks<R>(rt, G, row, run);
+    // The group's scan of its tiles' run counts, done by each of its tiles:
+    // per run, the rows of the tiles before this one (high word) and of all
+    // of them (low word).  (One 16-byte load per tile, two per thread in
+    // flight.)
     const int32_t tb0 = tile_begin[t.parent], tb1 = tile_begin[t.parent + 1];
-    unsigned long long acc = 0ull;
-    for (int k0 = (tb0 & ~3) + 4 * tid; k0 < tb1; k0 += 8 * kPartBlock) {
-      const int k1 = k0 + 4 * kPartBlock;
-      const uint4 a = *reinterpret_cast<const uint4 *>(tile_left + k0);
-      const uint4 b = k1 < tb1 ? *reinterpret_cast<const uint4 *>(tile_left + k1)
+    unsigned long long acc[4] = {0ull, 0ull, 0ull, 0ull};
+    for (int k0 = tb0 + tid; k0 < tb1; k0 += 2 * kPartBlock) {
+      const int k1 = k0 + kPartBlock;
+      const uint4 a = *reinterpret_cast<const uint4 *>(tile_cnt + 4 * (int64_t)k0);
+      const uint4 b = k1 < tb1 ? *reinterpret_cast<const uint4 *>(tile_cnt + 4 * (int64_t)k1)
                                : make_uint4(0u, 0u, 0u, 0u);
-      const uint32_t va[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      const uint32_t va[4] = {a.x, a.y, a.z, a.w}, vb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int k = (u < 4 ? k0 : k1) + (u & 3);
-        const unsigned long long v = (k >= tb0 && k < tb1) ? (unsigned long long)va[u] : 0ull;
-        acc += v + (k < ti ? v << 32 : 0ull);
+      for (int r = 0; r < 4; ++r) {
+        const unsigned long long x = va[r], y = vb[r];
+        acc[r] += x + y + (k0 < ti ? x << 32 : 0ull) + (k1 < ti ? y << 32 : 0ull);
       }
     }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (lane_id() == 0) red[tid >> 6] = acc;
-    uint32_t vmask, lmask;
-    row_masks<R>(sc, row, lo, hi, (uint32_t)P.bin, vmask, lmask);
-    const uint32_t packed = ((uint32_t)__builtin_popcount(vmask) << 16) |
-                            (uint32_t)__builtin_popcount(lmask);
-    uint32_t tot;
-    const uint32_t pre = block_excl_scan<kPartBlock>(packed, tmp, tot);  // (its barriers publish red)
-    unsigned long long psum = 0ull;
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int w = 0; w < kPartBlock / 64; ++w) psum += red[w];
-    const int64_t loff = (int64_t)(psum >> 32), nl = (int64_t)(psum & 0xffffffffull);
-    const int64_t lbase = P.start + loff;
-    const int64_t rbase = P.start + nl + ((lo - P.start) - loff);
-    if (ti == tb0 && tid == 0) {
-      // The children's segments, whether the split is kept (est:678-683)
-      // and which child is the smaller one (est:701-709), whose histogram
-      // is built.
-      const int64_t nr = P.count - nl;
-      const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
-      const bool left_small = nl <= nr;
-      parent_nleft[t.parent] = nl;
-      NodeSeg Ls, Rs;
-      Ls.start = P.start;
-      Ls.count = nl;
-      Ls.valid = ok ? 1 : 0;
-      Ls.is_small = left_small ? 1 : 0;
-      Rs.start = P.start + nl;
-      Rs.count = nr;
-      Rs.valid = ok ? 1 : 0;
-      Rs.is_small = left_small ? 0 : 1;
-      segs[P.left_id] = Ls;
-      segs[P.right_id] = Rs;
-      hist_node[t.parent] = ok ? (left_small ? P.left_id : P.right_id) : -1;
+      for (int o = 32; o >= 1; o >>= 1) acc[r] += __shfl_xor(acc[r], o, 64);
+    if (lane_id() == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[tid >> 6][r] = acc[r];
     }
-    const int ltot = (int)(tot & 0xffffu), vtot = (int)(tot >> 16);
-    const int rtot = vtot - ltot;
-    const int lpre = (int)(pre & 0xffffu), rpre = (int)(pre >> 16) - lpre;
+    // This thread's counts as four 16-bit fields (a tile has at most 4096 rows).
+    const unsigned long long packed = (unsigned long long)__builtin_popcount(run[0]) |
+                                      ((unsigned long long)__builtin_popcount(run[1]) << 16) |
+                                      ((unsigned long long)__builtin_popcount(run[2]) << 32) |
+                                      ((unsigned long long)__builtin_popcount(run[3]) << 48);
+    unsigned long long tot;
+    const unsigned long long pre =
+        block_excl_scan<kPartBlock>(packed, tmp, tot);  // (its barriers publish red)
+    int64_t gpre[4], gtot[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      unsigned long long s = 0ull;
+#pragma unroll
+      for (int w = 0; w < kPartBlock / 64; ++w) s += red[w][r];
+      gpre[r] = (int64_t)(s >> 32);
+      gtot[r] = (int64_t)(s & 0xffffffffull);
+    }
+    // Destination of each run's first row of this tile: side 0's parent's
+    // left child, its right child, then side 1's.
+    const int64_t base[4] = {Pa.start + gpre[0], Pa.start + gtot[0] + gpre[1],
+                             Pb.start + gpre[2], Pb.start + gtot[2] + gpre[3]};
+    if (ti == tb0 && tid == 0) {
+      if (G.par[0] >= 0)
+        write_children(Pa, G.par[0], gtot[0], gtot[1], min_samples_leaf, parent_nleft, segs,
+                       hist_node);
+      if (G.par[1] >= 0)
+        write_children(Pb, G.par[1], gtot[2], gtot[3], min_samples_leaf, parent_nleft, segs,
+                       hist_node);
+    }
+    int len[4], off[4], tpre[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      len[r] = (int)((tot >> (16 * r)) & 0xffffull);
+      tpre[r] = (int)((pre >> (16 * r)) & 0xffffull);
+    }
+    off[0] = 0;
+    off[1] = len[0];
+    off[2] = off[1] + len[1];
+    off[3] = off[2] + len[2];
+    const int vtot = off[3] + len[3];
     {
-      int li = 0, ri = 0;
+      int rk[4] = {0, 0, 0, 0};
 #pragma unroll
       for (int k = 0; k < R; ++k) {
-        const bool v = (vmask >> k) & 1u, l = (lmask >> k) & 1u;
-        if (v) inv[l ? lpre + li : ltot + rpre + ri] = (uint16_t)(R * tid + k);
-        li += l ? 1 : 0;
-        ri += (v && !l) ? 1 : 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if ((run[r] >> k) & 1u) {
+            inv[off[r] + tpre[r] + rk[r]] = (uint16_t)(R * tid + k);
+            ++rk[r];
+          }
+        }
       }
     }
     __syncthreads();
-    // (g,h) and row ids: slot s -> its destination row.
+    // (g,h) and row ids: slot s -> its destination row.  (An empty run's
+    // offset equals the next one's, so the count below skips it.)
     for (int sl = tid; sl < vtot; sl += kPartBlock) {
-      const int64_t d = sl < ltot ? lbase + sl : rbase + (sl - ltot);
-      const int64_t r = t.row0 + inv[sl];
-      gh_dst[d] = gh_src[r];
-      if (rid_dst) rid_dst[d] = rid_src[r];
+      const int r = (sl >= off[1] ? 1 : 0) + (sl >= off[2] ? 1 : 0) + (sl >= off[3] ? 1 : 0);
+      const int64_t d = sel4(r, base[0], base[1], base[2], base[3]) +
+                        (sl - sel4(r, off[0], off[1], off[2], off[3]));
+      const int64_t src = t.row0 + inv[sl];
+      gh_dst[d] = gh_src[src];
+      if (rid_dst) rid_dst[d] = rid_src[src];
     }
-    // Output chunks: the left run's then the right run's aligned R-byte
-    // chunks.  Per owned chunk: its destination row and, per byte, the
-    // tile row it copies (0xffff: outside the run, not written).
-    const int64_t lc0 = lbase & ~int64_t(R - 1), rc0 = rbase & ~int64_t(R - 1);
-    const int nlc = ltot ? (int)((lbase + ltot + R - 1) / R - lbase / R) : 0;
-    const int nrc = rtot ? (int)((rbase + rtot + R - 1) / R - rbase / R) : 0;
+    // Output chunks: each run's aligned R-byte chunks, runs in order.  Per
+    // owned chunk: its destination row and, per byte, the tile row it
+    // copies (0xffff: outside the run, not written).
+    int cum[4], n_chunks = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      cum[r] = n_chunks;
+      n_chunks += len[r] ? (int)((base[r] + len[r] + R - 1) / R - base[r] / R) : 0;
+    }
     int64_t cdst[kChunkSlots];
     uint32_t csrc[kChunkSlots][R / 2];  // R x u16 tile rows
     bool cfull[kChunkSlots], cown[kChunkSlots];
 #pragma unroll
     for (int q = 0; q < kChunkSlots; ++q) {
       const int c = tid + q * kPartBlock;
-      cown[q] = c < nlc + nrc;
-      const bool left = c < nlc;
-      const int64_t c0 = left ? lc0 + R * (int64_t)c : rc0 + R * (int64_t)(c - nlc);
-      const int64_t D = left ? lbase : rbase;
-      const int L = left ? ltot : rtot;
-      const int S = left ? 0 : ltot;
+      cown[q] = c < n_chunks;
+      const int r = (c >= cum[1] ? 1 : 0) + (c >= cum[2] ? 1 : 0) + (c >= cum[3] ? 1 : 0);
+      const int64_t D = sel4(r, base[0], base[1], base[2], base[3]);
+      const int L = sel4(r, len[0], len[1], len[2], len[3]);
+      const int S = sel4(r, off[0], off[1], off[2], off[3]);
+      const int64_t c0 =
+          (D & ~int64_t(R - 1)) + R * (int64_t)(c - sel4(r, cum[0], cum[1], cum[2], cum[3]));
       cdst[q] = c0;
       bool full = true;
 #pragma unroll
@@ -1183,17 +1532,18 @@ hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                uint8_t *codes_dst, int64_t ld_c,
                                const GH *gh_src, GH *gh_dst,
                                const int32_t *rid_src, int32_t *rid_dst,
-                               const PartParent *parents,
+                               const PartParent *parents, const PartGroup *groups,
                                const PartTile *tiles, const LevelPlan *plan,
                                int32_t max_tiles, int32_t part_rows,
-                               const int32_t *tile_begin, const int32_t *tile_left,
+                               const int32_t *tile_begin, const int32_t *tile_cnt,
                                int64_t *parent_nleft, NodeSeg *segs, int32_t *hist_node,
                                int32_t min_samples_leaf, int32_t F_sel) {
   if (max_tiles <= 0) return hipSuccess;
 #define BSSCL_SCATTER(R)                                                                 \
   hipLaunchKernelGGL(k_part_scatter<R>, dim3((unsigned)max_tiles), dim3(kPartBlock), 0, st, \
                      codes_src, codes_dst, ld_c, gh_src, gh_dst, rid_src, rid_dst, parents, \
-                     tiles, plan, tile_begin, tile_left, parent_nleft, segs, hist_node,   \
+                     groups, tiles, plan, tile_begin, tile_cnt, parent_nleft, segs,       \
+                     hist_node,                                                           \
                      min_samples_leaf, F_sel)
   switch (part_rows) {
     case 4: BSSCL_SCATTER(4); break;
@@ -1204,6 +1554,7 @@ hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
 #undef BSSCL_SCATTER
   return hipGetLastError();
 }
+
 
 // ---------------------------------------------------------------------------
 // Split search (est:598-621, est:775-801).  One wave per (node, feature):
@@ -1289,7 +1640,7 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_reduce_split(
     const NodeSeg *__restrict__ segs, const unsigned long long *__restrict__ part,
     unsigned long long *__restrict__ pool, int64_t node_stride,
     const int32_t *__restrict__ nb_sel, int32_t F_sel, int32_t child_depth, SplitParams P,
-    SplitCand *__restrict__ cand, long long *__restrict__ totals) {
+    SplitCand *__restrict__ cand, long long *__restrict__ totals, int32_t span_parents) {
   __shared__ long long red[kRsWaves][kHistPerFeat];
   const int lane = lane_id(), wave = (int)(threadIdx.x >> 6);
   // The root's block (parents == nullptr) has one node and no sibling.
@@ -1301,7 +1652,9 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_reduce_split(
     const int32_t small = parents ? hist_node[p] : 0;
     if (small < 0) continue;  // split not kept: no children (uniform)
     const NodeSeg ss = segs[small];
-    const int32_t nt = hist_tasks_with_rows(hist_begin, p, ss.count, tile_rows);
+    // (An in-place level's tasks tiled the parent's segment.)
+    const int32_t nt = hist_tasks_with_rows(hist_begin, p,
+                                            span_parents ? parents[p].count : ss.count, tile_rows);
     const int64_t woff = (int64_t)fpos * kHistPerFeat + lane * 8;
     unsigned long long *hs = pool + (int64_t)small * node_stride + woff;
     long long g[4] = {0, 0, 0, 0}, h[4] = {0, 0, 0, 0};
@@ -1401,23 +1754,23 @@ hipError_t launch_reduce_split(hipStream_t st, const LevelPlan *plan, int32_t ma
                                const unsigned long long *part, unsigned long long *pool,
                                int64_t node_stride, const int32_t *nb_sel, int32_t F_sel,
                                int32_t child_depth, SplitParams p, SplitCand *cand,
-                               long long *totals) {
+                               long long *totals, int32_t span_parents) {
   const int64_t items = (int64_t)max_parents * F_sel;
   if (items <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_reduce_split, dim3((unsigned)std::min<int64_t>(items, 16384)),
                      dim3(64 * kRsWaves), 0, st, plan, parents, hist_begin, hist_node, segs, part, pool, node_stride,
-                     nb_sel, F_sel, child_depth, p, cand, totals);
+                     nb_sel, F_sel, child_depth, p, cand, totals, span_parents);
   return hipGetLastError();
 }
 
 // The last level (its children are at max_depth, est:775-777): one wave per
-// parent does the parent's scan of its tiles' left counts (the children's
+// parent sums its side's runs over its group's tiles (the children's
 // segments, whether the split is kept, est:678-683), the children's totals
 // from the parent's histogram of the split feature, and the children's
 // table records (no split).  Replaces scan, child totals and record kernels.
 __global__ __launch_bounds__(256) void k_last_level(
-    const PartParent *__restrict__ parents, const LevelPlan *__restrict__ plan,
-    const int32_t *__restrict__ tile_begin, const int32_t *__restrict__ tile_left,
+    const PartParent *__restrict__ parents, int32_t grouped, const LevelPlan *__restrict__ plan,
+    const int32_t *__restrict__ tile_begin, const int32_t *__restrict__ tile_cnt,
     int64_t *__restrict__ parent_nleft, NodeSeg *__restrict__ segs,
     int32_t *__restrict__ hist_node, int32_t min_samples_leaf,
     const unsigned long long *__restrict__ pool, int64_t node_stride,
@@ -1427,9 +1780,9 @@ __global__ __launch_bounds__(256) void k_last_level(
   for (int w = (int)(blockIdx.x * 4 + (threadIdx.x >> 6)); w < n_parents;
        w += (int)gridDim.x * 4) {
     const PartParent P = parents[w];
-    const int32_t t0 = tile_begin[w], t1 = tile_begin[w + 1];
-    long long nl = 0;
-    for (int32_t t = t0 + lane; t < t1; t += 64) nl += tile_left[t];
+    const int32_t gs = grouped ? P.gslot : 2 * w;
+    long long nl, nr;
+    wave_side_counts(tile_cnt, tile_begin[gs >> 1], tile_begin[(gs >> 1) + 1], gs & 1, nl, nr);
     // The parent's histogram of its split feature: totals of bins <= bin.
     const long long *h = reinterpret_cast<const long long *>(pool) +
                          (int64_t)P.node * node_stride + (int64_t)P.fpos * kHistPerFeat;
@@ -1447,29 +1800,14 @@ __global__ __launch_bounds__(256) void k_last_level(
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
-      nl += __shfl_xor(nl, o, 64);
       gl += __shfl_xor(gl, o, 64);
       hl += __shfl_xor(hl, o, 64);
       gt += __shfl_xor(gt, o, 64);
       ht += __shfl_xor(ht, o, 64);
     }
     if (lane == 0) {
-      const long long nr = P.count - nl;
+      write_children(P, w, nl, nr, min_samples_leaf, parent_nleft, segs, hist_node);
       const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
-      const bool left_small = nl <= nr;
-      parent_nleft[w] = nl;
-      NodeSeg Ls, Rs;
-      Ls.start = P.start;
-      Ls.count = nl;
-      Ls.valid = ok ? 1 : 0;
-      Ls.is_small = left_small ? 1 : 0;
-      Rs.start = P.start + nl;
-      Rs.count = nr;
-      Rs.valid = ok ? 1 : 0;
-      Rs.is_small = left_small ? 0 : 1;
-      segs[P.left_id] = Ls;
-      segs[P.right_id] = Rs;
-      hist_node[w] = ok ? (left_small ? P.left_id : P.right_id) : -1;
       if (ok) {
         totals[2 * (int64_t)P.left_id] = gl;
         totals[2 * (int64_t)P.left_id + 1] = hl;
@@ -1483,12 +1821,12 @@ __global__ __launch_bounds__(256) void k_last_level(
       o.bin = 0;
       o.valid = ok ? 1 : 0;
       o.left = -1;
-      o.start = Ls.start;
+      o.start = P.start;
       o.count = nl;
       o.Gq = ok ? gl : 0;
       o.Hq = ok ? hl : 0;
       nodes[P.left_id] = o;
-      o.start = Rs.start;
+      o.start = P.start + nl;
       o.count = nr;
       o.Gq = ok ? gt - gl : 0;
       o.Hq = ok ? ht - hl : 0;
@@ -1497,15 +1835,16 @@ __global__ __launch_bounds__(256) void k_last_level(
   }
 }
 
-hipError_t launch_last_level(hipStream_t st, const PartParent *parents, const LevelPlan *plan,
+hipError_t launch_last_level(hipStream_t st, const PartParent *parents, int32_t grouped,
+                             const LevelPlan *plan,
                              int32_t max_parents, const int32_t *tile_begin,
-                             const int32_t *tile_left, int64_t *parent_nleft, NodeSeg *segs,
+                             const int32_t *tile_cnt, int64_t *parent_nleft, NodeSeg *segs,
                              int32_t *hist_node, int32_t min_samples_leaf,
                              const unsigned long long *pool, int64_t node_stride,
                              long long *totals, NodeOut *nodes) {
   if (max_parents <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_last_level, dim3((unsigned)((max_parents + 3) / 4)), dim3(256), 0, st,
-                     parents, plan, tile_begin, tile_left, parent_nleft, segs, hist_node,
+                     parents, grouped, plan, tile_begin, tile_cnt, parent_nleft, segs, hist_node,
                      min_samples_leaf, pool, node_stride, totals, nodes);
   return hipGetLastError();
 }
@@ -1735,7 +2074,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
     P.left_id = L;
     P.right_id = L + 1;
     P.node = v;
-    P.pad = 0;
+    P.gslot = 2 * i;
     parents[i] = P;
     const int64_t a0 = N.start & ~int64_t(15);
     // At least one tile: a parent's first tile writes its children's segments.
@@ -1840,6 +2179,7 @@ constexpr int kPlanLdsC = 512;
 __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     NodeOut *__restrict__ nodes, LevelPlan *__restrict__ plan,
     const PartParent *__restrict__ prev_parents, PartParent *__restrict__ parents,
+    PartGroup *__restrict__ groups,
     int32_t *__restrict__ tile_begin, int32_t *__restrict__ hist_begin,
     PartTile *__restrict__ tiles, HistTask *__restrict__ hist_tasks,
     const NodeSeg *__restrict__ segs,
@@ -1855,6 +2195,11 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
   __shared__ int32_t s_flag[kPlanLdsC];
   __shared__ int32_t s_pj[kPlanLdsC / 2 + 1];  // candidate of each parent
   __shared__ int32_t s_tb[kPlanLdsC / 2 + 1], s_hb[kPlanLdsC / 2 + 1];
+  // Grouped levels: each candidate's parent index (-1: not expanded), each
+  // previous parent's group (-1: none) and each group's first tile row.
+  __shared__ int32_t s_pidx[kPlanLdsC], s_gi[kPlanLdsC / 2 + 1];
+  __shared__ int64_t s_gs[kPlanLdsC / 2 + 1];
+  __shared__ uint32_t s_tcar;
   __shared__ unsigned long long s_rows;
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -1882,12 +2227,13 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
   // through registers so that their LDS stores wait after every load is
   // issued.  (first <= kPlanLdsC + 1 <= kPlanBlock: one per thread.)
   const double ke0 = tid < first ? kept_e[tid] : 0.0;
-  int32_t pnode = -1;
+  PartParent pq{0, 0, 0, 0, -1, -1, -1, 0};  // previous parent tid (a grouped level's grandparent)
   double pe = 0.0;
   if (tid < n_pp) {
-    pnode = prev_parents[tid].node;
+    pq = prev_parents[tid];
     pe = prev_parent_e[tid];
   }
+  const int32_t pnode = pq.node;
   constexpr int kPer = 4;  // candidates per wave and pass
   for (int jb = wave * kPer; jb < nc; jb += (kPlanBlock / 64) * kPer) {
     NodeSeg sg[kPer];
@@ -1997,6 +2343,48 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     return;
   }
 
+  // A grouped level's groups: the previous parents with an expanded child,
+  // each with its tiles over the previous parent's segment.
+  if (a.mode == kLevelGrouped) {
+    if (tid < nc) s_pidx[tid] = fl ? (int32_t)pidx : -1;
+    __syncthreads();
+    int32_t pl = -1, pr = -1;
+    uint32_t ge = 0u, gt = 0u;
+    if (tid < n_pp) {
+      pl = s_pidx[2 * tid];
+      pr = s_pidx[2 * tid + 1];
+      ge = (pl >= 0 || pr >= 0) ? 1u : 0u;
+      const int64_t a0 = pq.start & ~int64_t(15);
+      gt = ge ? (uint32_t)max((int64_t)1, (pq.start + pq.count - a0 + a.part_tile - 1) / a.part_tile)
+              : 0u;
+    }
+    uint32_t n_groups, tcar_g;
+    const uint32_t gidx = block_excl_scan<kPlanBlock>(ge, stmp, n_groups);
+    const uint32_t toff = block_excl_scan<kPlanBlock>(gt, stmp, tcar_g);
+    if (tid < n_pp) {
+      s_gi[tid] = ge ? (int32_t)gidx : -1;
+      if (ge) {
+        PartGroup G;
+        G.start = pq.start;
+        G.count = pq.count;
+        G.fpos = pq.fpos;
+        G.bin = pq.bin;
+        G.par[0] = pl;
+        G.par[1] = pr;
+        groups[gidx] = G;
+        s_tb[gidx] = (int32_t)toff;
+        s_gs[gidx] = pq.start & ~int64_t(15);
+        tile_begin[gidx] = (int32_t)toff;
+      }
+    }
+    if (tid == 0) {
+      s_tb[n_groups] = (int32_t)tcar_g;
+      tile_begin[n_groups] = (int32_t)tcar_g;
+      s_tcar = n_groups;  // (the group count, until the tile scan below)
+    }
+    __syncthreads();
+  }
+
   // Records, parents, ranks; tiles per parent; rows to build.
   unsigned long long rows = 0;
   if (tid < nc) {
@@ -2026,31 +2414,43 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       P.left_id = L;
       P.right_id = L + 1;
       P.node = v;
-      P.pad = 0;
+      P.gslot = a.mode == kLevelGrouped ? 2 * s_gi[tid >> 1] + (tid & 1) : 2 * i;
       parents[i] = P;
       parent_e[i] = N.e;
-      const int64_t a0 = N.start & ~int64_t(15);
-      // At least one tile: a parent's first tile writes its children's segments.
-      s_tb[i] = (int32_t)max((int64_t)1, (N.start + N.count - a0 + a.part_tile - 1) / a.part_tile);
+      if (a.mode != kLevelGrouped) {
+        const int64_t a0 = N.start & ~int64_t(15);
+        // At least one tile: a parent's first tile writes its children's segments.
+        s_tb[i] = (int32_t)max((int64_t)1, (N.start + N.count - a0 + a.part_tile - 1) / a.part_tile);
+      }
       s_pj[i] = tid;
-      rows = (unsigned long long)(N.count / 2);
+      rows = (unsigned long long)(N.count / 2);  // at most the smaller child's
     }
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) rows += __shfl_xor(rows, o, 64);
   if (lane == 0 && rows) atomicAdd(&s_rows, rows);
   __syncthreads();
-  const int32_t th = plan_tile_rows((int64_t)s_rows, a);
+  // Rows per histogram task: sized for the smaller children's rows; in
+  // place a task tiles twice as many of its parent's rows, of which it adds
+  // those of the smaller child (at most half).
+  const int32_t th = plan_tile_rows((int64_t)s_rows, a) * (a.mode == kLevelInPlace ? 2 : 1);
 
-  // Exclusive offsets of each parent's tiles and histogram tasks.
+  // Exclusive offsets of each parent's tiles (a grouped level: its groups'
+  // tiles, already laid out) and histogram tasks.
+  const bool grouped = a.mode == kLevelGrouped;
   uint32_t nt = 0, nh = 0;
   if (tid < n_exp) {
-    nt = (uint32_t)s_tb[tid];
-    nh = a.last ? 0u : (uint32_t)((s_count[s_pj[tid]] / 2 + th) / th);
+    nt = grouped ? 0u : (uint32_t)s_tb[tid];
+    const int64_t cnt = s_count[s_pj[tid]];
+    nh = a.last ? 0u
+                : a.mode == kLevelInPlace ? (uint32_t)max((int64_t)1, (cnt + th - 1) / th)
+                                          : (uint32_t)((cnt / 2 + th) / th);
   }
   uint32_t tcar, hcar;
+  const int32_t n_groups = grouped ? (int32_t)s_tcar : n_exp;
   const uint32_t tp = block_excl_scan<kPlanBlock>(nt, stmp, tcar);
   const uint32_t hp = block_excl_scan<kPlanBlock>(nh, stmp, hcar);
+  if (grouped) tcar = (uint32_t)s_tb[n_groups];
   if (tcar > (uint32_t)a.tile_cap || hcar > (uint32_t)a.hist_cap) {
     // Capacities are sized from proven bounds; reaching this is a bug.
     if (tid == 0) {
@@ -2065,29 +2465,35 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
   }
   __syncthreads();  // s_tb is rewritten below
   if (tid < n_exp) {
-    s_tb[tid] = (int32_t)tp;
+    if (!grouped) {
+      s_tb[tid] = (int32_t)tp;
+      tile_begin[tid] = (int32_t)tp;
+      s_gs[tid] = s_start[s_pj[tid]] & ~int64_t(15);
+    }
     s_hb[tid] = (int32_t)hp;
-    tile_begin[tid] = (int32_t)tp;
     hist_begin[tid] = (int32_t)hp;
   }
   if (tid == 0) {
-    s_tb[n_exp] = (int32_t)tcar;
+    if (!grouped) {
+      s_tb[n_exp] = (int32_t)tcar;
+      tile_begin[n_exp] = (int32_t)tcar;
+    }
     s_hb[n_exp] = (int32_t)hcar;
-    tile_begin[n_exp] = (int32_t)tcar;
     hist_begin[n_exp] = (int32_t)hcar;
   }
   __syncthreads();
 
-  // Tile and histogram-task lists: item -> its parent by binary search.
+  // Tile and histogram-task lists: item -> its group (parent) by binary
+  // search.
   for (int t = tid; t < (int)tcar; t += kPlanBlock) {
-    int lo = 0, hi = n_exp - 1;
+    int lo = 0, hi = n_groups - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       if (s_tb[mid] <= t) lo = mid;
       else hi = mid - 1;
     }
     PartTile T;
-    T.row0 = (s_start[s_pj[lo]] & ~int64_t(15)) + (int64_t)(t - s_tb[lo]) * a.part_tile;
+    T.row0 = s_gs[lo] + (int64_t)(t - s_tb[lo]) * a.part_tile;
     T.rows = a.part_tile;
     T.parent = lo;
     tiles[t] = T;
@@ -2117,13 +2523,14 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
 
 hipError_t launch_plan_lds(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                            const PartParent *prev_parents, PartParent *parents,
+                           PartGroup *groups,
                            int32_t *tile_begin, int32_t *hist_begin, PartTile *tiles,
                            HistTask *hist_tasks, const NodeSeg *segs,
                            const long long *totals, const SplitCand *cand, double *kept_e,
                            const double *prev_parent_e, double *parent_e, int32_t F_sel,
                            PlanArgs a) {
   hipLaunchKernelGGL(k_plan_lds, dim3(1), dim3(kPlanBlock), 0, st, nodes, plan, prev_parents,
-                     parents, tile_begin, hist_begin, tiles, hist_tasks, segs,
+                     parents, groups, tile_begin, hist_begin, tiles, hist_tasks, segs,
                      totals, cand, kept_e, prev_parent_e, parent_e, F_sel, a);
   return hipGetLastError();
 }

@@ -245,6 +245,20 @@ def test_build_tree_lockstep(engine, case):
     _lockstep_case(engine, **case)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", [
+    dict(n=40000, F=50, seed=4, n_bins=255, max_leaves=63, max_depth=8, msl=5, mcw=3.0, lam=5.0, nan=0.2, col=0.7, sub=0.5),
+    dict(n=3000, F=6, seed=5, n_bins=16, max_leaves=15, max_depth=10, msl=20, mcw=0.0, lam=0.5),
+    dict(n=60000, F=30, seed=11, n_bins=255, max_leaves=255, max_depth=12, msl=2, mcw=0.5, lam=1.0, nan=0.05),
+])
+def test_build_tree_lockstep_moving_every_level(engine, case, monkeypatch):
+    """The builder that moves the rows at every level (instead of every
+    second level, the default) builds the oracle's trees too."""
+    _announce(f"lockstep, rows moved every level {case}")
+    monkeypatch.setenv("BSSCL_TEST_PAIR_LEVELS", "0")
+    _lockstep_case(engine, **case)
+
+
 def test_predict_matches_oracle(engine):
     _announce("predict")
     X, y = make_data(20000, 12, seed=9, nan_frac=0.05)
@@ -369,19 +383,21 @@ def test_fit_lockstep_and_end_to_end(engine, name):
 
 def test_fit_device_replay_fallbacks_agree(engine, monkeypatch):
     """The round's device replay (pipelined and not), the host replay
-    (forced), the path that regrows a too-small node table, and the general
-    planner in place of the LDS one give identical trees and losses."""
+    (forced), the path that regrows a too-small node table, the general
+    planner in place of the LDS one, and rows moved at every level instead of
+    every second one give identical trees and losses."""
     from bsscl_gbm import HybridHistGBMNumbaV1_0_1
     X, y, params = _fit_case("nan_imbalanced")
     params = dict(params, n_estimators=6)
     fits = {}
     hooks = ("BSSCL_TEST_HOST_REPLAY", "BSSCL_TEST_NODE_CAP", "BSSCL_TEST_REPLAY_GLOBAL",
-             "BSSCL_TEST_PLAN_GLOBAL")
+             "BSSCL_TEST_PLAN_GLOBAL", "BSSCL_TEST_PAIR_LEVELS")
     for mode, env in [("device", {}), ("sync", {}), ("host", {"BSSCL_TEST_HOST_REPLAY": "1"}),
                       ("global", {"BSSCL_TEST_REPLAY_GLOBAL": "1"}),
                       ("lds", {"BSSCL_TEST_REPLAY_GLOBAL": "2"}),
                       ("regrow", {"BSSCL_TEST_NODE_CAP": "9"}),
-                      ("plan_global", {"BSSCL_TEST_PLAN_GLOBAL": "1"})]:
+                      ("plan_global", {"BSSCL_TEST_PLAN_GLOBAL": "1"}),
+                      ("every_level", {"BSSCL_TEST_PAIR_LEVELS": "0"})]:
         _announce(f"fit replay path {mode}")
         for k in hooks:
             monkeypatch.delenv(k, raising=False)
@@ -393,7 +409,7 @@ def test_fit_device_replay_fallbacks_agree(engine, monkeypatch):
     for k in hooks:
         monkeypatch.delenv(k, raising=False)
     ref = fits["device"]
-    for mode in ("sync", "host", "global", "lds", "regrow", "plan_global"):
+    for mode in ("sync", "host", "global", "lds", "regrow", "plan_global", "every_level"):
         got = fits[mode]
         assert got.train_loss_history_ == ref.train_loss_history_, mode
         for a, b in zip(ref.trees, got.trees):
