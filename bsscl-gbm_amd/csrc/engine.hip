@@ -1129,12 +1129,13 @@ int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParam
 
 // Count of one level's groups (groups == nullptr: one per parent), then
 // the scatter of their rows from set src to their children's segments in
-// set dst (move_rows), or the children's sizes only (sizes: an in-place
-// level).  (The last level moves nothing: k_last_level takes the sizes.)
+// set dst (move_rows).  (A level that moves nothing takes the children's
+// sizes from the counts in its next kernel: the in-place histogram, or
+// k_last_level.)
 int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parents,
                      const PartGroup *groups, const int32_t *tile_begin, const PartTile *tiles,
-                     const LevelPlan *plan, int32_t max_parents, int32_t max_tiles,
-                     int32_t F_sel, int32_t min_samples_leaf, bool move_rows, bool sizes) {
+                     const LevelPlan *plan, int32_t max_tiles, int32_t F_sel,
+                     int32_t min_samples_leaf, bool move_rows) {
   hipEvent_t stop;
   CHK(prof_begin(E, 1, &stop));
   HIPCHK(launch_part_count(E->st, E->codes_c[src].p, E->ld_c, parents, groups, tiles, plan,
@@ -1147,9 +1148,6 @@ int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parent
                                tiles, plan, max_tiles, E->part_rows, tile_begin,
                                E->tile_cnt_d.p, E->nleft_d.p, E->segs.p, E->hist_node_d.p,
                                min_samples_leaf, F_sel));
-  else if (sizes)
-    HIPCHK(launch_part_sizes(E->st, parents, plan, max_parents, tile_begin, E->tile_cnt_d.p,
-                             E->nleft_d.p, E->segs.p, E->hist_node_d.p, min_samples_leaf));
   CHK(prof_end(E, stop));
   return BSSCL_OK;
 }
@@ -1168,8 +1166,8 @@ int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
   const bool in_place = mode == kLevelInPlace;
   const int32_t P = level_parents_bound(E, level);
   const int32_t T = (int32_t)std::min<int64_t>(E->tile_cap, m / E->part_tile + 2 * (int64_t)P + 1);
-  CHK(launch_partition(E, src, dst, par, grp, E->tile_begin_d.p, E->tiles_d.p, E->plan_d, P, T,
-                       F_sel, tp.min_samples_leaf, !last && !in_place, !last && in_place));
+  CHK(launch_partition(E, src, dst, par, grp, E->tile_begin_d.p, E->tiles_d.p, E->plan_d, T,
+                       F_sel, tp.min_samples_leaf, !last && !in_place));
   hipEvent_t stop;
   if (last) {
     CHK(prof_begin(E, 2, &stop));
@@ -1183,13 +1181,15 @@ int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
   const int32_t H = (int32_t)std::min<int64_t>(
       E->hist_cap, (int64_t)hist_target(E, F_sel, in_place) + 2 * (int64_t)P + 2);
   // In place, the smaller children's rows are read from their parents'
-  // segments in src.
+  // segments in src, and the histogram launch takes the children's sizes.
   const int hs = in_place ? src : dst;
+  const SpanLevel span{par, E->tile_begin_d.p, E->tile_cnt_d.p, E->nleft_d.p,
+                       tp.min_samples_leaf};
   HIPCHK(launch_hist(E->st, E->codes_c[hs].p, E->ld_c, E->gh_c[hs].p, E->hist_tasks_d.p,
                      E->plan_d, H, E->hist_node_d.p, E->hist_begin_d.p, E->segs.p,
                      E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel, in_place),
                      in_place ? E->hist_copies_span : E->hist_copies, E->part_d.p, E->pool.p,
-                     E->node_stride, in_place ? par : nullptr,
+                     E->node_stride, in_place ? &span : nullptr,
                      prof_slot(E, hist_grid(E, H, F_sel, in_place))));
   CHK(prof_begin(E, 2, &stop));
   HIPCHK(launch_reduce_split(E->st, E->plan_d, P, par, E->hist_begin_d.p, E->hist_node_d.p,
@@ -2772,8 +2772,8 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
   CHK(launch_partition(E, 0, 1, reinterpret_cast<const PartParent *>(dv[0]), nullptr,
                        reinterpret_cast<const int32_t *>(dv[1]),
                        reinterpret_cast<const PartTile *>(dv[2]),
-                       reinterpret_cast<const LevelPlan *>(dv[3]), 1, (int32_t)tiles.size(),
-                       1, 0, true, false));
+                       reinterpret_cast<const LevelPlan *>(dv[3]), (int32_t)tiles.size(),
+                       1, 0, true));
   E->track_rid = false;
   std::vector<int32_t> r32((size_t)m);
   int64_t nl = 0;

@@ -247,18 +247,28 @@ hipError_t launch_gather_gh(hipStream_t st, const double *F, const uint8_t *y,
 // Level kernels take their work counts from a device LevelPlan; the grid
 // argument (blocks, tasks or parents) is an upper bound, and blocks loop
 // over the work with a grid stride, so any bound >= 1 gives the same result.
-// With `span` (an in-place level's parents), a task's rows are a tile of
-// its parent's segment and only the rows its split sends to the smaller
-// child (hist_node) are added.
+// An in-place level's histogram inputs (see launch_hist).
+struct SpanLevel {
+  const PartParent *parents;  // the level's parents; task.ref indexes them
+  const int32_t *tile_begin;  // each parent's partition tiles
+  const int32_t *tile_cnt;    // their run counts (k_part_count)
+  int64_t *parent_nleft;      // written: each parent's left rows
+  int32_t min_samples_leaf;
+};
+// With `span` (an in-place level), a task's rows are a tile of its parent's
+// segment: the task finds the children's sizes from the tile counts, its
+// parent's first task writes the children's segments, whether the split is
+// kept and the smaller child (segs, hist_node, parent_nleft), and only the
+// rows the split sends to the smaller child are added.
 hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const GH *gh_c, const HistTask *tasks,
                        const LevelPlan *plan, int32_t max_tasks,
-                       const int32_t *hist_node, const int32_t *hist_begin,
-                       const NodeSeg *segs,
+                       int32_t *hist_node, const int32_t *hist_begin,
+                       NodeSeg *segs,
                        const int32_t *nb_sel, const int32_t *hot_sel,
                        int32_t F_sel, int32_t fchunk, int32_t copies,
                        unsigned long long *part, unsigned long long *pool,
-                       int64_t node_stride, const PartParent *span = nullptr,
+                       int64_t node_stride, const SpanLevel *span = nullptr,
                        unsigned long long *ktime = nullptr);
 int hist_blocks(int32_t n_tasks, int32_t nchunks);
 // Per tile, its rows of each of the four runs (tile_cnt[4 * tile + run]).
@@ -279,13 +289,6 @@ hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                const int32_t *tile_begin, const int32_t *tile_cnt,
                                int64_t *parent_nleft, NodeSeg *segs, int32_t *hist_node,
                                int32_t min_samples_leaf, int32_t F_sel);
-// An in-place level after its count: each parent's children's segments (as
-// a move would place them), whether the split is kept and which child is
-// smaller, one wave per parent.
-hipError_t launch_part_sizes(hipStream_t st, const PartParent *parents, const LevelPlan *plan,
-                             int32_t max_parents, const int32_t *tile_begin,
-                             const int32_t *tile_cnt, int64_t *parent_nleft, NodeSeg *segs,
-                             int32_t *hist_node, int32_t min_samples_leaf);
 // Histogram reduction and split search of one level (parents == nullptr:
 // the root, node 0, whose tasks hist_begin[0] .. hist_begin[1] built it).
 // span_parents: the tasks of parent p tiled its own segment (an in-place

@@ -599,6 +599,54 @@ constexpr int kHistRows = 16;  // rows per thread per step
 // the copies of one bin sit in C consecutive words, so lanes of different
 // copies never meet in an LDS bank whatever their bins (3.13 instead of 2.18
 // (g,h) updates per clock per CU for C = 8 on MI355X).
+// Sums over tiles t = t_first, t_first + stride, ... < t1 of the two
+// adjacent counts cnt[4t], cnt[4t + 1], eight loads in flight per pass.
+__device__ __forceinline__ void strided_side_counts(const int32_t *__restrict__ cnt,
+                                                    int32_t t_first, int32_t t1, int32_t stride,
+                                                    long long &a, long long &b) {
+  a = 0;
+  b = 0;
+  for (int32_t t = t_first; t < t1; t += 8 * stride) {
+    int2 v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int32_t te = t + e * stride;
+      v[e] = te < t1 ? *reinterpret_cast<const int2 *>(cnt + 4 * (int64_t)te) : make_int2(0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a += v[e].x;
+      b += v[e].y;
+    }
+  }
+}
+
+// The children of parent p, whose split sends nl of its rows left and nr
+// right: their segments (left first, from the parent's start), whether the
+// split is kept (est:678-683) and which child is the smaller one
+// (est:701-709), whose histogram is built.
+__device__ __forceinline__ void write_children(const PartParent &P, int32_t p, int64_t nl,
+                                               int64_t nr, int32_t min_samples_leaf,
+                                               int64_t *__restrict__ parent_nleft,
+                                               NodeSeg *__restrict__ segs,
+                                               int32_t *__restrict__ hist_node) {
+  const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
+  const bool left_small = nl <= nr;
+  parent_nleft[p] = nl;
+  NodeSeg Ls, Rs;
+  Ls.start = P.start;
+  Ls.count = nl;
+  Ls.valid = ok ? 1 : 0;
+  Ls.is_small = left_small ? 1 : 0;
+  Rs.start = P.start + nl;
+  Rs.count = nr;
+  Rs.valid = ok ? 1 : 0;
+  Rs.is_small = left_small ? 0 : 1;
+  segs[P.left_id] = Ls;
+  segs[P.right_id] = Rs;
+  hist_node[p] = ok ? (left_small ? P.left_id : P.right_id) : -1;
+}
+
 // Tasks of histogram reference p that hold rows: at most the planned tasks,
 // and none past the node's last row.
 __device__ __forceinline__ int32_t hist_tasks_with_rows(const int32_t *__restrict__ hist_begin,
@@ -623,45 +671,54 @@ constexpr int kSpanRows = 8;
 constexpr int kSpanWave = 64 * kSpanRows;        // rows per wave and step
 constexpr int kSpanStep = kHistBlock * kSpanRows;  // rows per block and step
 
+// A lane's codes of one step: the split feature's and the block's features'
+// for its kSpanRows rows (group g of the tile's groups g < g1).
+template <int FC>
+struct SpanCodes {
+  uint2 sv;
+  uint2 cv[FC];
+};
+
+template <int FC>
+__device__ __forceinline__ void span_load(SpanCodes<FC> &L, const uint8_t *__restrict__ codes_c,
+                                          int64_t ld_c, const uint8_t *__restrict__ scol, int f0,
+                                          int nf, int64_t g, int64_t g1) {
+  if (g < g1) {
+    const int64_t row = g * kSpanRows;
+    L.sv = *reinterpret_cast<const uint2 *>(scol + row);
+#pragma unroll
+    for (int u = 0; u < FC; ++u)
+      L.cv[u] = u < nf ? *reinterpret_cast<const uint2 *>(codes_c + (int64_t)(f0 + u) * ld_c + row)
+                       : make_uint2(0u, 0u);
+  }
+}
+
+// The wave's groups of kSpanRows rows are every fourth run of 64 groups of
+// the tile, from group r0 / kSpanRows + 64 * wave, whose codes the caller
+// has loaded into L; the codes of the wave's next step are loaded before
+// this step's listed rows are added.
 template <int FC, int C>
 __device__ __forceinline__ void hist_rows_span(
-    unsigned long long *lh, uint32_t *stage, uint16_t *mlist, uint32_t *stmp,
+    unsigned long long *lh, uint32_t *stage, uint16_t *mlist,
     const uint8_t *__restrict__ codes_c, int64_t ld_c, const GH *__restrict__ gh_c, int f0,
     int nf, const uint32_t (&lim)[FC], const uint32_t (&hb)[FC], long long (&ag)[FC],
     long long (&ah)[FC], int64_t r0, int64_t r1, const uint8_t *__restrict__ scol,
-    uint32_t sbin, bool sright) {
-  (void)stmp;
+    uint32_t sbin, bool sright, SpanCodes<FC> &L) {
   constexpr int kW = (FC + 3) / 4;  // LDS words per row
   const int lane = lane_id(), wave = (int)(threadIdx.x >> 6);
   const int copy = lane & (C - 1);
   uint32_t *wst = stage + wave * kSpanWave;  // this wave's rows: word q at q * kSpanStep
   uint16_t *wl = mlist + wave * kSpanWave;
-  // The wave's groups of kSpanRows rows: every fourth run of 64 groups.  The
-  // codes of the wave's next step are loaded before this step's listed rows
-  // are added.
   const int64_t g0 = r0 / kSpanRows, g1 = (r1 + kSpanRows - 1) / kSpanRows;
-  uint2 nsv = make_uint2(0u, 0u), ncv[FC];
-  auto load_step = [&](int64_t gb) {
-    const int64_t g = gb + lane;
-    if (g < g1) {
-      const int64_t row = g * kSpanRows;
-      nsv = *reinterpret_cast<const uint2 *>(scol + row);
-#pragma unroll
-      for (int u = 0; u < FC; ++u)
-        ncv[u] = u < nf ? *reinterpret_cast<const uint2 *>(codes_c + (int64_t)(f0 + u) * ld_c + row)
-                        : make_uint2(0u, 0u);
-    }
-  };
-  load_step(g0 + (int64_t)wave * 64);
   for (int64_t gb = g0 + (int64_t)wave * 64; gb < g1; gb += (int64_t)kHistBlock) {
     const int64_t g = gb + lane;
     const int64_t row = g * kSpanRows;
     uint32_t mem = 0u;
     if (g < g1) {
-      const uint2 sv = nsv;
+      const uint2 sv = L.sv;
       uint2 cv[FC];
 #pragma unroll
-      for (int u = 0; u < FC; ++u) cv[u] = ncv[u];
+      for (int u = 0; u < FC; ++u) cv[u] = L.cv[u];
       const uint32_t sw[2] = {sv.x, sv.y};
 #pragma unroll
       for (int k = 0; k < kSpanRows; ++k) {
@@ -686,7 +743,7 @@ __device__ __forceinline__ void hist_rows_span(
         sp[1] = make_uint4(w[4], w[5], w[6], w[7]);
       }
     }
-    if (gb + kHistBlock < g1) load_step(gb + kHistBlock);
+    if (gb + kHistBlock < g1) span_load<FC>(L, codes_c, ld_c, scol, f0, nf, gb + kHistBlock + lane, g1);
     const uint32_t cnt = (uint32_t)__builtin_popcount(mem);
     const uint32_t incl = wave_incl_scan<uint32_t>(cnt);
     const int nm = (int)__shfl(incl, 63, 64);
@@ -742,28 +799,28 @@ __device__ __forceinline__ void hist_rows_span(
 // child hist_node[task.ref] (hist_rows_span).
 template <int FC, int C, bool SPAN>
 __device__ __forceinline__ void hist_item(
-    unsigned long long *lh, uint32_t *stage, uint16_t *mlist, uint32_t *stmp,
+    unsigned long long *lh, uint32_t *stage, uint16_t *mlist,
     const uint8_t *__restrict__ codes_c, int64_t ld_c,
     const GH *__restrict__ gh_c, const HistTask task, int32_t ti, int chunk,
-    const int32_t *__restrict__ hist_node, const int32_t *__restrict__ hist_begin,
-    const NodeSeg *__restrict__ segs, const PartParent *__restrict__ span,
+    int32_t *__restrict__ hist_node, const int32_t *__restrict__ hist_begin,
+    NodeSeg *__restrict__ segs, const SpanLevel &span, long long (*sred)[kHistBlock / 64],
     const int32_t *__restrict__ nb_sel, const int32_t *__restrict__ hot_sel,
     int32_t F_sel, int32_t tile_rows, unsigned long long *__restrict__ part,
     unsigned long long *__restrict__ pool, int64_t node_stride) {
-  const int32_t node = hist_node[task.ref];
-  if (node < 0) return;
+  int32_t node = -1;
   int64_t s0, sn;  // the rows the tasks of this reference tile
   const uint8_t *scol = nullptr;
   uint32_t sbin = 0u;
-  bool sright = false;
+  PartParent P;
   if constexpr (SPAN) {
-    const PartParent P = span[task.ref];
+    P = span.parents[task.ref];
     s0 = P.start;
     sn = P.count;
     scol = codes_c + (int64_t)P.fpos * ld_c;
     sbin = (uint32_t)P.bin;
-    sright = node != P.left_id;
   } else {
+    node = hist_node[task.ref];
+    if (node < 0) return;
     const NodeSeg seg = segs[node];
     if (!seg.valid) return;
     s0 = seg.start;
@@ -771,10 +828,31 @@ __device__ __forceinline__ void hist_item(
   }
   const int64_t r0 = s0 + (int64_t)task.tile * tile_rows;
   const int64_t rend = s0 + sn;
-  if (r0 >= rend) return;
+  if (r0 >= rend) return;  // (never a parent's first task: it writes the children)
   const int64_t r1 = min(rend, r0 + (int64_t)tile_rows);
   const int f0 = chunk * FC;
   const int nf = min(FC, F_sel - f0);
+  // In place: the first step's codes, then the children's sizes (the
+  // parent's tiles' counts of runs 0, left, and 1, right), both in flight
+  // together; every block of the parent sums them.
+  SpanCodes<FC> L;
+  if constexpr (SPAN) {
+    span_load<FC>(L, codes_c, ld_c, scol, f0, nf,
+                  r0 / kSpanRows + 64 * (int64_t)(threadIdx.x >> 6) + lane_id(),
+                  (r1 + kSpanRows - 1) / kSpanRows);
+    const int32_t t0 = span.tile_begin[task.ref], t1 = span.tile_begin[task.ref + 1];
+    long long nl, nr;
+    strided_side_counts(span.tile_cnt, t0 + (int32_t)threadIdx.x, t1, kHistBlock, nl, nr);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      nl += __shfl_xor(nl, o, 64);
+      nr += __shfl_xor(nr, o, 64);
+    }
+    if (lane_id() == 0) {
+      sred[0][threadIdx.x >> 6] = nl;
+      sred[1][threadIdx.x >> 6] = nr;
+    }
+  }
   uint32_t lim[FC], hb[FC];
   long long ag[FC], ah[FC];
 #pragma unroll
@@ -787,11 +865,31 @@ __device__ __forceinline__ void hist_item(
   }
   for (int i = threadIdx.x; i < FC * kHistPerFeat * C; i += kHistBlock) lh[i] = 0ull;
   __syncthreads();
+  bool sright = false;
+  if constexpr (SPAN) {
+    long long nl = 0, nr = 0;
+#pragma unroll
+    for (int w = 0; w < kHistBlock / 64; ++w) {
+      nl += sred[0][w];
+      nr += sred[1][w];
+    }
+    // The parent's first block writes the children's segments, whether the
+    // split is kept and the smaller child (as k_last_level does).
+    if (task.tile == 0 && chunk == 0 && threadIdx.x == 0)
+      write_children(P, task.ref, nl, nr, span.min_samples_leaf, span.parent_nleft, segs,
+                     hist_node);
+    if (nl < span.min_samples_leaf || nr < span.min_samples_leaf) {  // split not kept
+      __syncthreads();  // sred is rewritten by the block's next item
+      return;
+    }
+    node = nl <= nr ? P.left_id : P.right_id;
+    sright = node != P.left_id;
+  }
   const int copy = lane_id() & (C - 1);
 
   if constexpr (SPAN) {
-    hist_rows_span<FC, C>(lh, stage, mlist, stmp, codes_c, ld_c, gh_c, f0, nf, lim, hb, ag, ah,
-                          r0, r1, scol, sbin, sright);
+    hist_rows_span<FC, C>(lh, stage, mlist, codes_c, ld_c, gh_c, f0, nf, lim, hb, ag, ah, r0, r1,
+                          scol, sbin, sright, L);
   } else {
   const int64_t g0 = r0 >> 4, g1 = (r1 + 15) >> 4;
   for (int64_t g = g0 + threadIdx.x; g < g1; g += kHistBlock) {
@@ -894,13 +992,14 @@ __device__ __forceinline__ void hist_item(
   __syncthreads();  // lh is cleared again by the block's next item
 }
 
+// (In place, five waves per SIMD: the listed rows' loads need the waves.)
 template <int FC, int C, bool SPAN>
-__global__ __launch_bounds__(kHistBlock) void k_hist(
+__global__ __launch_bounds__(kHistBlock) __attribute__((amdgpu_waves_per_eu(SPAN ? 5 : 1)))
+void k_hist(
     const uint8_t *__restrict__ codes_c, int64_t ld_c,
     const GH *__restrict__ gh_c, const HistTask *__restrict__ tasks,
-    const LevelPlan *__restrict__ plan, const int32_t *__restrict__ hist_node,
-    const int32_t *__restrict__ hist_begin,
-    const NodeSeg *__restrict__ segs, const PartParent *__restrict__ span,
+    const LevelPlan *__restrict__ plan, int32_t *__restrict__ hist_node,
+    const int32_t *__restrict__ hist_begin, NodeSeg *__restrict__ segs, SpanLevel span,
     const int32_t *__restrict__ nb_sel,
     const int32_t *__restrict__ hot_sel, int32_t F_sel, int32_t nchunks,
     unsigned long long *__restrict__ part, unsigned long long *__restrict__ pool,
@@ -910,7 +1009,7 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
   // listed rows.
   __shared__ __align__(16) uint32_t stage[SPAN ? (FC + 3) / 4 : 1][SPAN ? kSpanStep : 1];
   __shared__ uint16_t mlist[SPAN ? kSpanStep : 1];
-  __shared__ uint32_t stmp[kHistBlock / 64];
+  __shared__ long long sred[2][kHistBlock / 64];
   const int32_t n_tasks = plan->n_hist;
   const int32_t tile_rows = plan->tile_rows;
   // Optional timing: each block's start and end on the constant-rate clock,
@@ -924,9 +1023,9 @@ __global__ __launch_bounds__(kHistBlock) void k_hist(
     const int ti = (j / nchunks) * 8 + (b & 7);
     if ((j / nchunks) * 8 >= n_tasks) break;
     if (ti >= n_tasks) continue;
-    hist_item<FC, C, SPAN>(lh, &stage[0][0], mlist, stmp, codes_c, ld_c, gh_c, tasks[ti], ti, j % nchunks, hist_node,
-                           hist_begin, segs, span, nb_sel, hot_sel, F_sel, tile_rows, part,
-                           pool, node_stride);
+    hist_item<FC, C, SPAN>(lh, &stage[0][0], mlist, codes_c, ld_c, gh_c, tasks[ti], ti,
+                           j % nchunks, hist_node, hist_begin, segs, span, sred, nb_sel, hot_sel,
+                           F_sel, tile_rows, part, pool, node_stride);
   }
   if (ktime) {
     __syncthreads();  // every wave's stores issued
@@ -941,24 +1040,25 @@ int hist_blocks(int32_t n_tasks, int32_t nchunks) {
 hipError_t launch_hist(hipStream_t st, const uint8_t *codes_c, int64_t ld_c,
                        const GH *gh_c, const HistTask *tasks,
                        const LevelPlan *plan, int32_t max_tasks,
-                       const int32_t *hist_node, const int32_t *hist_begin,
-                       const NodeSeg *segs,
+                       int32_t *hist_node, const int32_t *hist_begin,
+                       NodeSeg *segs,
                        const int32_t *nb_sel, const int32_t *hot_sel,
                        int32_t F_sel, int32_t fchunk, int32_t copies,
                        unsigned long long *part, unsigned long long *pool,
-                       int64_t node_stride, const PartParent *span,
+                       int64_t node_stride, const SpanLevel *span,
                        unsigned long long *ktime) {
   if (max_tasks <= 0) return hipSuccess;
+  const SpanLevel sp = span ? *span : SpanLevel{};
   const int32_t nchunks = (F_sel + fchunk - 1) / fchunk;
   const dim3 grid((unsigned)hist_blocks(max_tasks, nchunks));
 #define BSSCL_HIST(FC, C)                                                                    \
   if (span)                                                                                  \
     hipLaunchKernelGGL((k_hist<FC, C, true>), grid, dim3(kHistBlock), 0, st, codes_c, ld_c, gh_c, \
-                       tasks, plan, hist_node, hist_begin, segs, span, nb_sel, hot_sel, F_sel,  \
+                       tasks, plan, hist_node, hist_begin, segs, sp, nb_sel, hot_sel, F_sel,    \
                        nchunks, part, pool, node_stride, ktime);                              \
   else                                                                                       \
     hipLaunchKernelGGL((k_hist<FC, C, false>), grid, dim3(kHistBlock), 0, st, codes_c, ld_c,   \
-                       gh_c, tasks, plan, hist_node, hist_begin, segs, span, nb_sel, hot_sel,  \
+                       gh_c, tasks, plan, hist_node, hist_begin, segs, sp, nb_sel, hot_sel,    \
                        F_sel, nchunks, part, pool, node_stride, ktime)
   // LDS per block: fchunk * copies * 8 KB (at most 32 KB).
   switch (fchunk * 16 + copies) {
@@ -1156,75 +1256,17 @@ hipError_t launch_part_count(hipStream_t st, const uint8_t *codes_c,
   return hipGetLastError();
 }
 
-// The children of parent p, whose split sends nl of its rows left and nr
-// right: their segments (left first, from the parent's start), whether the
-// split is kept (est:678-683) and which child is the smaller one
-// (est:701-709), whose histogram is built.
-__device__ __forceinline__ void write_children(const PartParent &P, int32_t p, int64_t nl,
-                                               int64_t nr, int32_t min_samples_leaf,
-                                               int64_t *__restrict__ parent_nleft,
-                                               NodeSeg *__restrict__ segs,
-                                               int32_t *__restrict__ hist_node) {
-  const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
-  const bool left_small = nl <= nr;
-  parent_nleft[p] = nl;
-  NodeSeg Ls, Rs;
-  Ls.start = P.start;
-  Ls.count = nl;
-  Ls.valid = ok ? 1 : 0;
-  Ls.is_small = left_small ? 1 : 0;
-  Rs.start = P.start + nl;
-  Rs.count = nr;
-  Rs.valid = ok ? 1 : 0;
-  Rs.is_small = left_small ? 0 : 1;
-  segs[P.left_id] = Ls;
-  segs[P.right_id] = Rs;
-  hist_node[p] = ok ? (left_small ? P.left_id : P.right_id) : -1;
-}
-
 // A side's rows over its group's tiles [t0, t1): runs 2*side (left) and
 // 2*side + 1 (right), summed by one wave (every lane gets the sums).
 __device__ __forceinline__ void wave_side_counts(const int32_t *__restrict__ tile_cnt, int32_t t0,
                                                  int32_t t1, int side, long long &nl,
                                                  long long &nr) {
-  nl = 0;
-  nr = 0;
-  for (int32_t t = t0 + lane_id(); t < t1; t += 64) {
-    const int2 v = *reinterpret_cast<const int2 *>(tile_cnt + 4 * (int64_t)t + 2 * side);
-    nl += v.x;
-    nr += v.y;
-  }
+  strided_side_counts(tile_cnt + 2 * side, t0 + lane_id(), t1, 64, nl, nr);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
     nl += __shfl_xor(nl, o, 64);
     nr += __shfl_xor(nr, o, 64);
   }
-}
-
-__global__ __launch_bounds__(256) void k_part_sizes(
-    const PartParent *__restrict__ parents, const LevelPlan *__restrict__ plan,
-    const int32_t *__restrict__ tile_begin, const int32_t *__restrict__ tile_cnt,
-    int64_t *__restrict__ parent_nleft, NodeSeg *__restrict__ segs,
-    int32_t *__restrict__ hist_node, int32_t min_samples_leaf) {
-  const int32_t n_parents = plan->n_parents;
-  for (int w = (int)(blockIdx.x * 4 + (threadIdx.x >> 6)); w < n_parents;
-       w += (int)gridDim.x * 4) {
-    const PartParent P = parents[w];
-    long long nl, nr;
-    wave_side_counts(tile_cnt, tile_begin[w], tile_begin[w + 1], 0, nl, nr);
-    if (lane_id() == 0) write_children(P, w, nl, nr, min_samples_leaf, parent_nleft, segs, hist_node);
-  }
-}
-
-hipError_t launch_part_sizes(hipStream_t st, const PartParent *parents, const LevelPlan *plan,
-                             int32_t max_parents, const int32_t *tile_begin,
-                             const int32_t *tile_cnt, int64_t *parent_nleft, NodeSeg *segs,
-                             int32_t *hist_node, int32_t min_samples_leaf) {
-  if (max_parents <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_part_sizes, dim3((unsigned)((max_parents + 3) / 4)), dim3(256), 0, st,
-                     parents, plan, tile_begin, tile_cnt, parent_nleft, segs, hist_node,
-                     min_samples_leaf);
-  return hipGetLastError();
 }
 
 // Moves a tile's rows to their runs' segments in the other buffer set,
