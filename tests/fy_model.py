@@ -67,7 +67,8 @@ def fisher_yates_sorted_keys(a_old, draws):
     k_fy_final_sorted, k_fy_final_self in fisher_yates.hip): step k with
     j(k) != k becomes the key (j(k) << 32) | k, steps with j(k) == k the
     largest key; a stable sort on the high word; run starts give head[];
-    each key's successor in its run gives a_new[k]."""
+    each key's successor in its run gives a_new[k], with v resolved only at
+    the successors and the self steps."""
     a_old = np.asarray(a_old)
     n = len(a_old)
     if n <= 1:
@@ -84,21 +85,29 @@ def fisher_yates_sorted_keys(a_old, draws):
     start = valid.copy()
     start[1:] &= hi[1:] != hi[:-1]
     head[hi[start]] = lo[start]
-    root = np.arange(n)
-    while True:
-        h = head[root]
-        moved = h >= 0
-        if not moved.any():
-            break
-        root = np.where(moved, h, root)
-    v = a_old[root]
+
+    def value(x):
+        """v(x): a_old at the end of each x's chain x -> head[x] -> ...,
+        resolved only for the positions asked (as k_fy_final_* do)."""
+        root = np.array(x, dtype=np.int64, copy=True)
+        while True:
+            h = head[root]
+            moved = h >= 0
+            if not moved.any():
+                break
+            root = np.where(moved, h, root)
+        return a_old[root]
+
     out = np.full(n, -12345, dtype=a_old.dtype)
     nxt_same = np.zeros(len(keys), bool)
     nxt_same[:-1] = valid[1:] & (hi[1:] == hi[:-1])
     succ = np.full(len(keys), -1, np.int64)
     succ[:-1] = np.where(nxt_same[:-1], lo[1:], -1)
     idx = np.nonzero(valid)[0]
-    out[lo[idx]] = np.where(succ[idx] >= 0, v[np.maximum(succ[idx], 0)], a_old[hi[idx]])
+    has = succ[idx] >= 0
+    res = a_old[hi[idx]].copy()
+    res[has] = value(succ[idx][has])
+    out[lo[idx]] = res
     self_k = np.nonzero(np.concatenate([[True], p == k]))[0]
-    out[self_k] = v[self_k]
+    out[self_k] = value(self_k)
     return out
