@@ -19,8 +19,12 @@
 //
 // Sort.  Least-significant-digit radix sort with 8-bit digits: 4 passes for
 // float32 columns, 8 for float64.  Each pass is
-//   k_rs_count   per tile (4096 keys of one column): digit counts,
-//   k_rs_scan    per (column, digit): exclusive prefix over the tiles,
+//   k_rs_count   per tile (4096 keys of one column): digit counts, stored
+//                tile-major (one coalesced 1 KB row per tile),
+//   k_rs_scan_tiles  per group of 32 tiles: each tile's exclusive prefix
+//                within the group (in place) and the group's totals,
+//   k_rs_scan_groups per column: each group's exclusive prefix and each
+//                digit's start,
 //   k_rs_scatter per tile: each key's stable rank among the tile's keys of
 //                its digit, the tile regrouped by digit in LDS, then written
 //                out run by run (consecutive threads, consecutive addresses).
@@ -144,7 +148,7 @@ __global__ __launch_bounds__(256) void k_col_pad(KT *__restrict__ keys, int64_t 
   if (i < ld) keys[(int64_t)blockIdx.y * ld + i] = (KT)~(KT)0;
 }
 
-// Digit counts of one tile: counts[(col * 256 + d) * n_tiles + tile].
+// Digit counts of one tile: counts[(col * n_tiles + tile) * 256 + d].
 template <typename KT>
 __global__ __launch_bounds__(kSortThreads) void k_rs_count(const KT *__restrict__ keys, int64_t ld,
                                                            int32_t n_tiles, int32_t shift,
@@ -166,29 +170,60 @@ __global__ __launch_bounds__(kSortThreads) void k_rs_count(const KT *__restrict_
   uint32_t s = 0;
 #pragma unroll
   for (int k = 0; k < kSortWaves; ++k) s += cnt[k][t];
-  counts[((int64_t)col * kRadix + t) * n_tiles + tile] = s;
+  counts[((int64_t)col * n_tiles + tile) * kRadix + t] = s;
 }
 
-// Exclusive prefix over the tiles of one (column, digit), in place; the
-// digit's total goes to totals[col * 256 + d].
-__global__ __launch_bounds__(256) void k_rs_scan(uint32_t *__restrict__ counts, int32_t n_tiles,
-                                                 uint32_t *__restrict__ totals) {
-  __shared__ uint32_t tmp[4];
-  __shared__ uint32_t chunk_total;
-  const int64_t row = (int64_t)blockIdx.y * kRadix + blockIdx.x;
-  uint32_t *c = counts + row * n_tiles;
-  uint32_t carry = 0;
-  for (int32_t base = 0; base < n_tiles; base += 256) {
-    const int32_t i = base + (int32_t)threadIdx.x;
-    const uint32_t v = (i < n_tiles) ? c[i] : 0u;
-    const uint32_t ex = block_excl_256(v, tmp);
-    if (i < n_tiles) c[i] = carry + ex;
-    if (threadIdx.x == 255) chunk_total = ex + v;
-    __syncthreads();
-    carry += chunk_total;
-    __syncthreads();
+// Tiles per group of the two-level prefix over the tiles.
+constexpr int kScanGroup = 32;
+
+__host__ __device__ constexpr int32_t scan_groups(int32_t n_tiles) {
+  return (n_tiles + kScanGroup - 1) / kScanGroup;
+}
+
+// One group of kScanGroup tiles of one column, one thread per digit: each
+// tile's count becomes the exclusive prefix of the group's earlier tiles (in
+// place), and the group's total goes to gsum[(col * n_groups + g) * 256 + d].
+__global__ __launch_bounds__(256) void k_rs_scan_tiles(uint32_t *__restrict__ counts,
+                                                       int32_t n_tiles, int32_t n_groups,
+                                                       uint32_t *__restrict__ gsum) {
+  const int d = (int)threadIdx.x;
+  const int32_t g = (int32_t)blockIdx.x, col = (int32_t)blockIdx.y;
+  const int32_t t0 = g * kScanGroup;
+  uint32_t *c = counts + ((int64_t)col * n_tiles + t0) * kRadix + d;
+  uint32_t v[kScanGroup];
+#pragma unroll
+  for (int i = 0; i < kScanGroup; ++i) v[i] = t0 + i < n_tiles ? c[(int64_t)i * kRadix] : 0u;
+  uint32_t run = 0;
+#pragma unroll
+  for (int i = 0; i < kScanGroup; ++i) {
+    if (t0 + i < n_tiles) c[(int64_t)i * kRadix] = run;
+    run += v[i];
   }
-  if (threadIdx.x == 0) totals[row] = carry;
+  gsum[((int64_t)col * n_groups + g) * kRadix + d] = run;
+}
+
+// One column, one thread per digit: each group's total becomes the
+// exclusive prefix of the earlier groups (in place), and each digit's start
+// in the output (the keys of all smaller digits) goes to starts[col * 256 + d].
+__global__ __launch_bounds__(256) void k_rs_scan_groups(uint32_t *__restrict__ gsum,
+                                                        int32_t n_groups,
+                                                        uint32_t *__restrict__ starts) {
+  __shared__ uint32_t tmp[4];
+  const int d = (int)threadIdx.x;
+  const int32_t col = (int32_t)blockIdx.x;
+  uint32_t *gs = gsum + (int64_t)col * n_groups * kRadix + d;
+  uint32_t run = 0;
+  for (int32_t g0 = 0; g0 < n_groups; g0 += 8) {
+    uint32_t v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = g0 + e < n_groups ? gs[(int64_t)(g0 + e) * kRadix] : 0u;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (g0 + e < n_groups) gs[(int64_t)(g0 + e) * kRadix] = run;
+      run += v[e];
+    }
+  }
+  starts[(int64_t)col * kRadix + d] = block_excl_256(run, tmp);
 }
 
 // One stable counting-sort pass of one tile by the digit at `shift`.
@@ -197,7 +232,8 @@ __global__ __launch_bounds__(kSortThreads) void k_rs_scatter(const KT *__restric
                                                              KT *__restrict__ out, int64_t ld,
                                                              int32_t n_tiles, int32_t shift,
                                                              const uint32_t *__restrict__ offs,
-                                                             const uint32_t *__restrict__ totals) {
+                                                             const uint32_t *__restrict__ gpre,
+                                                             const uint32_t *__restrict__ starts) {
   constexpr int kItems = SortTile<KT>::kItems;
   constexpr int kTile = tile_keys<KT>();
   __shared__ KT tk[kTile];
@@ -210,9 +246,12 @@ __global__ __launch_bounds__(kSortThreads) void k_rs_scatter(const KT *__restric
   KT key[kItems];
 #pragma unroll
   for (int i = 0; i < kItems; ++i) key[i] = src[i * kSortThreads + t];
-  // Start of digit t's run for this tile in the output column.
-  const uint32_t dbase = block_excl_256(totals[(int64_t)col * kRadix + t], tmp);
-  gbase[t] = dbase + offs[((int64_t)col * kRadix + t) * n_tiles + tile];
+  // Start of digit t's run for this tile in the output column: the digit's
+  // start, its keys in the earlier groups and in the group's earlier tiles.
+  const int32_t n_groups = scan_groups(n_tiles);
+  gbase[t] = starts[(int64_t)col * kRadix + t] +
+             gpre[((int64_t)col * n_groups + tile / kScanGroup) * kRadix + t] +
+             offs[((int64_t)col * n_tiles + tile) * kRadix + t];
   running[t] = 0;
   for (int k = 0; k < kSortWaves; ++k) wcnt[k][t] = 0;
   __syncthreads();
@@ -345,14 +384,18 @@ hipError_t col_sort_impl(hipStream_t st, const void *Xv, int64_t n, int32_t F, v
     hipLaunchKernelGGL((k_col_pad<KT>), dim3((unsigned)((ld - n + 255) / 256), (unsigned)F),
                        dim3(256), 0, st, keys, n, ld);
   const int32_t n_tiles = (int32_t)(ld / tile_keys<KT>());
+  const int32_t n_groups = scan_groups(n_tiles);
+  uint32_t *gsum = counts + (int64_t)F * n_tiles * kRadix;  // after the counts
   const dim3 tiles((unsigned)n_tiles, (unsigned)F);
   for (int shift = 0; shift < (int)(8 * sizeof(KT)); shift += 8) {
     hipLaunchKernelGGL((k_rs_count<KT>), tiles, dim3(kSortThreads), 0, st, keys, ld, n_tiles,
                        shift, counts);
-    hipLaunchKernelGGL(k_rs_scan, dim3(kRadix, (unsigned)F), dim3(256), 0, st, counts, n_tiles,
+    hipLaunchKernelGGL(k_rs_scan_tiles, dim3((unsigned)n_groups, (unsigned)F), dim3(256), 0, st,
+                       counts, n_tiles, n_groups, gsum);
+    hipLaunchKernelGGL(k_rs_scan_groups, dim3((unsigned)F), dim3(256), 0, st, gsum, n_groups,
                        totals);
     hipLaunchKernelGGL((k_rs_scatter<KT>), tiles, dim3(kSortThreads), 0, st, keys, tmp, ld,
-                       n_tiles, shift, counts, totals);
+                       n_tiles, shift, counts, gsum, totals);
     std::swap(keys, tmp);
   }
   // An even number of passes leaves the sorted keys in keys_v.
@@ -370,7 +413,9 @@ int64_t col_sort_ld(int64_t n, int is_f64) {
 
 int64_t col_sort_count_words(int64_t n, int32_t F, int is_f64) {
   const int64_t tile = is_f64 ? tile_keys<uint64_t>() : tile_keys<uint32_t>();
-  return (int64_t)F * kRadix * (col_sort_ld(n, is_f64) / tile);
+  const int64_t n_tiles = col_sort_ld(n, is_f64) / tile;
+  // The tiles' counts, then the groups' prefixes.
+  return (int64_t)F * kRadix * (n_tiles + scan_groups((int32_t)n_tiles));
 }
 
 hipError_t launch_col_sort(hipStream_t st, const void *X, int is_f64, int64_t n, int32_t F,
@@ -390,13 +435,17 @@ hipError_t launch_sort_u64(hipStream_t st, uint64_t *keys, uint64_t *tmp, int64_
                            int lo_bit, int hi_bit, uint32_t *counts, uint32_t *totals,
                            uint64_t **result) {
   const int32_t n_tiles = (int32_t)(ld / tile_keys<uint64_t>());
+  const int32_t n_groups = scan_groups(n_tiles);
+  uint32_t *gsum = counts + (int64_t)n_tiles * kRadix;  // after the counts
   const dim3 tiles((unsigned)n_tiles, 1u);
   for (int shift = lo_bit; shift < hi_bit; shift += 8) {
     hipLaunchKernelGGL((k_rs_count<uint64_t>), tiles, dim3(kSortThreads), 0, st, keys, ld,
                        n_tiles, shift, counts);
-    hipLaunchKernelGGL(k_rs_scan, dim3(kRadix, 1u), dim3(256), 0, st, counts, n_tiles, totals);
+    hipLaunchKernelGGL(k_rs_scan_tiles, dim3((unsigned)n_groups, 1u), dim3(256), 0, st, counts,
+                       n_tiles, n_groups, gsum);
+    hipLaunchKernelGGL(k_rs_scan_groups, dim3(1u), dim3(256), 0, st, gsum, n_groups, totals);
     hipLaunchKernelGGL((k_rs_scatter<uint64_t>), tiles, dim3(kSortThreads), 0, st, keys, tmp,
-                       ld, n_tiles, shift, counts, totals);
+                       ld, n_tiles, shift, counts, gsum, totals);
     std::swap(keys, tmp);
   }
   *result = keys;

@@ -44,10 +44,14 @@ __global__ __launch_bounds__(256) void k_fy_push(const uint32_t *__restrict__ dr
   }
 }
 
+// a[0, n) = -1 with 16-byte stores (a is 16-byte aligned).
 __global__ __launch_bounds__(256) void k_fill_neg(int32_t *__restrict__ a, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+  const int64_t n4 = n >> 2;
+  int4 *a4 = reinterpret_cast<int4 *>(a);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
        i += (int64_t)gridDim.x * blockDim.x)
-    a[i] = -1;
+    a4[i] = make_int4(-1, -1, -1, -1);
+  if (blockIdx.x == 0 && (int64_t)threadIdx.x < (n & 3)) a[(n4 << 2) + threadIdx.x] = -1;
 }
 
 // Ascending merge sort of the list starting at `h` (links in next[], -1
@@ -272,7 +276,7 @@ hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
     int bits = 0;
     while (bits < 32 && ((uint64_t)(n - 1) >> bits) != 0) ++bits;  // positions < 2^bits
     const dim3 gk(blocks_for(ld));
-    hipLaunchKernelGGL(k_fill_neg, g, b, 0, st, w.head, n);
+    hipLaunchKernelGGL(k_fill_neg, dim3(blocks_for((n + 3) / 4)), b, 0, st, w.head, n);
     hipLaunchKernelGGL(k_fy_keys, gk, b, 0, st, draws, n, ld, w.keys);
     uint64_t *sorted = nullptr;
     hipError_t e = launch_sort_u64(st, w.keys, w.keys_tmp, ld, 32, 32 + (bits + 7) / 8 * 8,
@@ -283,7 +287,7 @@ hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
     hipLaunchKernelGGL(k_fy_final_self, g, b, 0, st, draws, n, w.head, a_old, a_new);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL(k_fill_neg, g, b, 0, st, w.head, n);
+  hipLaunchKernelGGL(k_fill_neg, dim3(blocks_for((n + 3) / 4)), b, 0, st, w.head, n);
   if (n > 1) hipLaunchKernelGGL(k_fy_push, g, b, 0, st, draws, n, w.head, w.next);
   hipLaunchKernelGGL(k_fy_sort, g, b, 0, st, w.head, w.next, n);
   hipLaunchKernelGGL(k_fy_resolve, g, b, 0, st, w.head, a_old, w.v, n);
