@@ -283,7 +283,7 @@ def main():
                     help="skip the prediction and the end-to-end fit (profiler runs)")
     ap.add_argument("--also", default="stress_10m",
                     help="workload of the extra rounds-only block ('' for none)")
-    ap.add_argument("--also-steps", type=int, default=10)
+    ap.add_argument("--also-steps", type=int, default=30)
     a = ap.parse_args()
     if a.gpus != 1:
         print(json.dumps({"error": "this engine runs on one GPU; --gpus must be 1 "

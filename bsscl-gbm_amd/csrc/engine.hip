@@ -373,7 +373,7 @@ struct bsscl_engine {
   int32_t part_rows = 4;
   int32_t part_tile = 1024;
   int32_t hist_blocks_per_cu = 8;
-  int32_t hist_rows_per_flush = 5120;        // the root's tiles
+  int32_t hist_rows_per_flush = 10240;       // the root's tiles
   int32_t hist_rows_per_flush_level = 2560;  // the planned levels' tiles
 
   // Profiling.
@@ -890,11 +890,13 @@ void read_hist_tuning(bsscl_engine *E, int64_t m, int32_t F_sel) {
   if (E->hist_fc_span * E->hist_copies_span > 8) E->hist_copies_span = 8 / E->hist_fc_span;
   if (E->hist_copies_span == 2) E->hist_copies_span = 1;
   E->hist_blocks_per_cu = env_int("BSSCL_HIST_BLOCKS_PER_CU", 1, 64, 8);
-  E->hist_rows_per_flush = env_int("BSSCL_HIST_ROWS_PER_FLUSH", 256, 1 << 22, 5120);
+  // The root: at least 10240 rows per tile (1M x 28, 73 tiles and half the
+  // partials of 5120-row tiles: 2440 -> 2480 trees/s; at 10M x 50 the block
+  // target decides, 227 tiles either way).
+  E->hist_rows_per_flush = env_int("BSSCL_HIST_ROWS_PER_FLUSH", 256, 1 << 22, 10240);
   // Below the root, smaller tiles (more blocks for the smaller levels, more
   // partials to sum): 1M x 28, 2560 rows took the five planned levels'
-  // histograms and reductions from 120 to 114 us per round; the root keeps
-  // 5120 (42 against 45 us).
+  // histograms and reductions from 120 to 114 us per round.
   E->hist_rows_per_flush_level =
       env_int("BSSCL_HIST_ROWS_PER_FLUSH_LEVEL", 256, 1 << 22, 2560);
 }
