@@ -12,6 +12,7 @@
 // Fixed-point sums are exact integer additions, so histograms, splits and
 // trees do not depend on atomic order or on the order of rows.
 #include "kernels.h"
+#include "wave.h"
 
 #include <hip/hip_ext.h>
 
@@ -23,15 +24,11 @@ namespace {
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
 
-template <typename T>
-__device__ __forceinline__ T wave_incl_scan(T v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    T t = __shfl_up(v, o, 64);
-    if (lane >= o) v += t;
-  }
-  return v;
+// a / b for a >= 0, b > 0 in 32-bit arithmetic when both fit (row counts
+// do); the 64-bit division is a long software sequence.
+__device__ __forceinline__ int64_t div_pos(int64_t a, int64_t b) {
+  if ((((uint64_t)a | (uint64_t)b) >> 32) == 0) return (int64_t)((uint32_t)a / (uint32_t)b);
+  return a / b;
 }
 
 // Exclusive scan over a block of BLOCK threads; `tmp` holds BLOCK/64 words.
@@ -652,7 +649,7 @@ __device__ __forceinline__ void write_children(const PartParent &P, int32_t p, i
 __device__ __forceinline__ int32_t hist_tasks_with_rows(const int32_t *__restrict__ hist_begin,
                                                         int32_t p, int64_t count,
                                                         int32_t tile_rows) {
-  const int64_t with_rows = (count + tile_rows - 1) / tile_rows;
+  const int64_t with_rows = div_pos(count + tile_rows - 1, tile_rows);
   return (int32_t)min((int64_t)(hist_begin[p + 1] - hist_begin[p]), with_rows);
 }
 
@@ -746,7 +743,7 @@ __device__ __forceinline__ void hist_rows_span(
     if (gb + kHistBlock < g1) span_load<FC>(L, codes_c, ld_c, scol, f0, nf, gb + kHistBlock + lane, g1);
     const uint32_t cnt = (uint32_t)__builtin_popcount(mem);
     const uint32_t incl = wave_incl_scan<uint32_t>(cnt);
-    const int nm = (int)__shfl(incl, 63, 64);
+    const int nm = (int)wave_lane(incl, 63);
     uint32_t at = incl - cnt;
 #pragma unroll
     for (int k = 0; k < kSpanRows; ++k)
@@ -843,11 +840,8 @@ __device__ __forceinline__ void hist_item(
     const int32_t t0 = span.tile_begin[task.ref], t1 = span.tile_begin[task.ref + 1];
     long long nl, nr;
     strided_side_counts(span.tile_cnt, t0 + (int32_t)threadIdx.x, t1, kHistBlock, nl, nr);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      nl += __shfl_xor(nl, o, 64);
-      nr += __shfl_xor(nr, o, 64);
-    }
+    nl = wave_sum(nl);
+    nr = wave_sum(nr);
     if (lane_id() == 0) {
       sred[0][threadIdx.x >> 6] = nl;
       sred[1][threadIdx.x >> 6] = nr;
@@ -959,12 +953,7 @@ __device__ __forceinline__ void hist_item(
   // Hot-bin sums: wave reduction, then one LDS add per wave.
 #pragma unroll
   for (int u = 0; u < FC; ++u) {
-    long long a = ag[u], c = ah[u];
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      a += __shfl_xor(a, o, 64);
-      c += __shfl_xor(c, o, 64);
-    }
+    const long long a = wave_sum(ag[u]), c = wave_sum(ah[u]);
     if (u < nf && hb[u] != 0xffffffffu && lane_id() == 0 && (a | c)) {
       __hip_atomic_fetch_add(lh + u * kHistPerFeat * C + hb[u] * C, (unsigned long long)a,
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1215,13 +1204,10 @@ __global__ __launch_bounds__(kPartBlock) void k_part_count(
     uint32_t run[4];
     route_masks<R>(rt, G, row, run);
     // Four counts as 16-bit fields (a tile has at most 4096 rows).
-    uint32_t a = (uint32_t)__builtin_popcount(run[0]) | ((uint32_t)__builtin_popcount(run[1]) << 16);
-    uint32_t b = (uint32_t)__builtin_popcount(run[2]) | ((uint32_t)__builtin_popcount(run[3]) << 16);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      a += __shfl_xor(a, o, 64);
-      b += __shfl_xor(b, o, 64);
-    }
+    const uint32_t a = wave_sum((uint32_t)__builtin_popcount(run[0]) |
+                                ((uint32_t)__builtin_popcount(run[1]) << 16));
+    const uint32_t b = wave_sum((uint32_t)__builtin_popcount(run[2]) |
+                                ((uint32_t)__builtin_popcount(run[3]) << 16));
     if (lane_id() == 0) red[threadIdx.x >> 6] = make_uint2(a, b);
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -1262,11 +1248,8 @@ __device__ __forceinline__ void wave_side_counts(const int32_t *__restrict__ til
                                                  int32_t t1, int side, long long &nl,
                                                  long long &nr) {
   strided_side_counts(tile_cnt + 2 * side, t0 + lane_id(), t1, 64, nl, nr);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    nl += __shfl_xor(nl, o, 64);
-    nr += __shfl_xor(nr, o, 64);
-  }
+  nl = wave_sum(nl);
+  nr = wave_sum(nr);
 }
 
 // Moves a tile's rows to their runs' segments in the other buffer set,
@@ -1363,9 +1346,7 @@ void k_part_scatter(
       }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) acc[r] += __shfl_xor(acc[r], o, 64);
+    for (int r = 0; r < 4; ++r) acc[r] = wave_sum(acc[r]);
     if (lane_id() == 0) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) red[tid >> 6][r] = acc[r];
@@ -1622,8 +1603,8 @@ __device__ __forceinline__ void split_search(const long long (&g)[4], const long
   const long long lhs = h[0] + h[1] + h[2] + h[3];
   const long long ig = wave_incl_scan<long long>(lg);
   const long long ih = wave_incl_scan<long long>(lhs);
-  const long long Gt = __shfl(ig, 63, 64);
-  const long long Ht = __shfl(ih, 63, 64);
+  const long long Gt = wave_lane(ig, 63);
+  const long long Ht = wave_lane(ih, 63);
   if (fpos == 0 && lane == 0) {
     totals[2 * (int64_t)node] = Gt;
     totals[2 * (int64_t)node + 1] = Ht;
@@ -1657,14 +1638,8 @@ __device__ __forceinline__ void split_search(const long long (&g)[4], const long
       }
     }
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const double og = __shfl_xor(best, o, 64);
-    const int32_t ob = __shfl_xor(bb, o, 64);
-    const bool take = ob >= 0 && (bb < 0 || og > best || (og == best && ob < bb));
-    best = take ? og : best;
-    bb = take ? ob : bb;
-  }
+  int32_t unused = 0;
+  wave_argmax(best, bb, unused);
   if (lane == 0) {
     SplitCand c;
     c.gain = best;
@@ -1690,7 +1665,7 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_reduce_split(
   const int32_t tile_rows = plan->tile_rows;
   const int64_t n_items = (int64_t)n_par * F_sel;
   for (int64_t it = blockIdx.x; it < n_items; it += gridDim.x) {
-    const int32_t p = (int32_t)(it / F_sel), fpos = (int32_t)(it % F_sel);
+    const int32_t p = (int32_t)div_pos(it, F_sel), fpos = (int32_t)(it - (int64_t)p * F_sel);
     const int32_t small = parents ? hist_node[p] : 0;
     if (small < 0) continue;  // split not kept: no children (uniform)
     const NodeSeg ss = segs[small];
@@ -1840,13 +1815,10 @@ __global__ __launch_bounds__(256) void k_last_level(
         hl += hh;
       }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      gl += __shfl_xor(gl, o, 64);
-      hl += __shfl_xor(hl, o, 64);
-      gt += __shfl_xor(gt, o, 64);
-      ht += __shfl_xor(ht, o, 64);
-    }
+    gl = wave_sum(gl);
+    hl = wave_sum(hl);
+    gt = wave_sum(gt);
+    ht = wave_sum(ht);
     if (lane == 0) {
       write_children(P, w, nl, nr, min_samples_leaf, parent_nleft, segs, hist_node);
       const bool ok = nl >= min_samples_leaf && nr >= min_samples_leaf;
@@ -1951,16 +1923,7 @@ __global__ __launch_bounds__(256) void k_node_best(
         }
       }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const double og = __shfl_xor(best, o, 64);
-      const int32_t of = __shfl_xor(bf, o, 64);
-      const int32_t ob = __shfl_xor(bb, o, 64);
-      const bool take = of >= 0 && (bf < 0 || og > best || (og == best && of < bf));
-      best = take ? og : best;
-      bf = take ? of : bf;
-      bb = take ? ob : bb;
-    }
+    wave_argmax(best, bf, bb);
     if (lane == 0) {
       NodeOut o;
       o.start = s.start;
@@ -2010,8 +1973,8 @@ constexpr int kPlanChunk = 2048;  // ranks of earlier nodes staged in LDS at a t
 // than rows_per_flush rows per tile, a multiple of 4096 rows.
 __device__ __forceinline__ int32_t plan_tile_rows(int64_t S, const PlanArgs &a) {
   int64_t tiles = max((int64_t)1, (int64_t)a.hist_target);
-  tiles = min(tiles, max((int64_t)1, S / a.rows_per_flush));
-  const int64_t t = ((S + tiles - 1) / tiles + 4095) / 4096 * 4096;
+  tiles = min(tiles, max((int64_t)1, div_pos(S, a.rows_per_flush)));
+  const int64_t t = (div_pos(S + tiles - 1, tiles) + 4095) / 4096 * 4096;
   return (int32_t)min(max(t, (int64_t)4096), (int64_t)1 << 24);
 }
 
@@ -2120,11 +2083,10 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
     parents[i] = P;
     const int64_t a0 = N.start & ~int64_t(15);
     // At least one tile: a parent's first tile writes its children's segments.
-    tile_begin[i] = (int32_t)max((int64_t)1, (N.start + N.count - a0 + a.part_tile - 1) / a.part_tile);
+    tile_begin[i] = (int32_t)max((int64_t)1, div_pos(N.start + N.count - a0 + a.part_tile - 1, a.part_tile));
     rows += (unsigned long long)(N.count / 2);
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) rows += __shfl_xor(rows, o, 64);
+  rows = wave_sum(rows);
   if (lane_id() == 0 && rows) atomicAdd(&s_rows, rows);
   __syncthreads();
   const int32_t th = plan_tile_rows((int64_t)s_rows, a);
@@ -2136,7 +2098,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
     uint32_t nt = 0, nh = 0;
     if (i < n_exp) {
       nt = (uint32_t)tile_begin[i];
-      nh = a.last ? 0u : (uint32_t)((parents[i].count / 2 + th) / th);
+      nh = a.last ? 0u : (uint32_t)div_pos(parents[i].count / 2 + th, th);
     }
     uint32_t tt, ht;
     const uint32_t tp = block_excl_scan<kPlanBlock>(nt, stmp, tt);
@@ -2313,16 +2275,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
           bb = x.bin;
         }
       }
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) {
-        const double og = __shfl_xor(best, o, 64);
-        const int32_t of = __shfl_xor(bf, o, 64);
-        const int32_t ob = __shfl_xor(bb, o, 64);
-        const bool take = of >= 0 && (bf < 0 || og > best || (og == best && of < bf));
-        best = take ? og : best;
-        bf = take ? of : bf;
-        bb = take ? ob : bb;
-      }
+      wave_argmax(best, bf, bb);
       if (lane == 0 && j < nc) {
         const bool valid = sg[q].valid != 0;
         if (!valid) bf = -1;
@@ -2397,7 +2350,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       pr = s_pidx[2 * tid + 1];
       ge = (pl >= 0 || pr >= 0) ? 1u : 0u;
       const int64_t a0 = pq.start & ~int64_t(15);
-      gt = ge ? (uint32_t)max((int64_t)1, (pq.start + pq.count - a0 + a.part_tile - 1) / a.part_tile)
+      gt = ge ? (uint32_t)max((int64_t)1, div_pos(pq.start + pq.count - a0 + a.part_tile - 1, a.part_tile))
               : 0u;
     }
     uint32_t n_groups, tcar_g;
@@ -2462,14 +2415,13 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       if (a.mode != kLevelGrouped) {
         const int64_t a0 = N.start & ~int64_t(15);
         // At least one tile: a parent's first tile writes its children's segments.
-        s_tb[i] = (int32_t)max((int64_t)1, (N.start + N.count - a0 + a.part_tile - 1) / a.part_tile);
+        s_tb[i] = (int32_t)max((int64_t)1, div_pos(N.start + N.count - a0 + a.part_tile - 1, a.part_tile));
       }
       s_pj[i] = tid;
       rows = (unsigned long long)(N.count / 2);  // at most the smaller child's
     }
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) rows += __shfl_xor(rows, o, 64);
+  rows = wave_sum(rows);
   if (lane == 0 && rows) atomicAdd(&s_rows, rows);
   __syncthreads();
   // Rows per histogram task: sized for the smaller children's rows; in
@@ -2485,8 +2437,8 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     nt = grouped ? 0u : (uint32_t)s_tb[tid];
     const int64_t cnt = s_count[s_pj[tid]];
     nh = a.last ? 0u
-                : a.mode == kLevelInPlace ? (uint32_t)max((int64_t)1, (cnt + th - 1) / th)
-                                          : (uint32_t)((cnt / 2 + th) / th);
+                : a.mode == kLevelInPlace ? (uint32_t)max((int64_t)1, div_pos(cnt + th - 1, th))
+                                          : (uint32_t)div_pos(cnt / 2 + th, th);
   }
   uint32_t tcar, hcar;
   const int32_t n_groups = grouped ? (int32_t)s_tcar : n_exp;
