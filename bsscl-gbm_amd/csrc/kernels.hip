@@ -2180,6 +2180,41 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
 //     four candidates per wave at a time.
 constexpr int kPlanLdsC = 512;
 
+// A candidate's planner record in LDS (est:649-652, 762-801): its best
+// split over the features (bf < 0: none), its rank e (the smaller of its
+// parent's rank `ppe` and its gain; the root's is its gain) and whether it
+// may be split.
+__device__ __forceinline__ void plan_record(
+    int j, const NodeSeg &sg, long long gq, long long hq, double ppe, double best, int32_t bf,
+    int32_t bb, const PlanArgs &a, int64_t *s_start, int64_t *s_count, long long *s_gq,
+    long long *s_hq, double *s_gain, double *s_e, int32_t *s_fpos, int32_t *s_bin,
+    int32_t *s_valid, int32_t *s_flag) {
+  const bool valid = sg.valid != 0;
+  if (!valid) bf = -1;
+  const double gain = bf >= 0 ? best : -1e9;
+  double e = 0.0;
+  int32_t fl = 0;
+  if (valid) {
+    const double pv = a.level == 0 ? gain : ppe;
+    e = pv < gain ? pv : gain;
+    fl = (bf >= 0 && gain > a.gamma) ? 1 : 0;
+  }
+  s_start[j] = sg.start;
+  s_count[j] = sg.count;
+  s_gq[j] = valid ? gq : 0;
+  s_hq[j] = valid ? hq : 0;
+  s_gain[j] = gain;
+  s_e[j] = e;
+  s_fpos[j] = bf;
+  s_bin[j] = bf >= 0 ? bb : 0;
+  s_valid[j] = sg.valid;
+  s_flag[j] = fl;
+}
+
+// Candidates x features staged in LDS by k_plan_lds (levels of up to 64
+// candidates over up to 64 features; larger ones use a wave per candidate).
+constexpr int kStageC = 64, kStageF = 64;
+
 __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     NodeOut *__restrict__ nodes, LevelPlan *__restrict__ plan,
     const PartParent *__restrict__ prev_parents, PartParent *__restrict__ parents,
@@ -2191,6 +2226,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     double *__restrict__ kept_e, const double *__restrict__ prev_parent_e,
     double *__restrict__ parent_e, int32_t F_sel, PlanArgs a) {
   __shared__ uint32_t stmp[kPlanBlock / 64];
+  __shared__ unsigned long long stmp64[kPlanBlock / 64];
   __shared__ double s_ke[kPlanLdsC + 1];
   __shared__ int64_t s_start[kPlanLdsC], s_count[kPlanLdsC];
   __shared__ long long s_gq[kPlanLdsC], s_hq[kPlanLdsC];
@@ -2205,6 +2241,8 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
   __shared__ int64_t s_gs[kPlanLdsC / 2 + 1];
   __shared__ uint32_t s_tcar;
   __shared__ unsigned long long s_rows;
+  __shared__ double s_cg[kStageF * kStageC];   // staged gains [feature][candidate]
+  __shared__ int16_t s_cb[kStageF * kStageC];  // staged bins (-1: no split)
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const LevelPlan prev = *plan;
@@ -2226,10 +2264,9 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
   if (tid == 0) s_rows = 0ull;
 
   // Every input at once: earlier ranks, the previous parents' ids and ranks,
-  // and the candidates' segments, totals and split candidates (four per
-  // wave and pass: one pass for up to 64 candidates).  The earlier ranks go
-  // through registers so that their LDS stores wait after every load is
-  // issued.  (first <= kPlanLdsC + 1 <= kPlanBlock: one per thread.)
+  // and the candidates' segments, totals and split candidates.  The earlier
+  // ranks go through registers so that their LDS stores wait after every
+  // load is issued.  (first <= kPlanLdsC + 1 <= kPlanBlock: one per thread.)
   const double ke0 = tid < first ? kept_e[tid] : 0.0;
   PartParent pq{0, 0, 0, 0, -1, -1, -1, 0};  // previous parent tid (a grouped level's grandparent)
   double pe = 0.0;
@@ -2238,70 +2275,113 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     pe = prev_parent_e[tid];
   }
   const int32_t pnode = pq.node;
-  constexpr int kPer = 4;  // candidates per wave and pass
-  for (int jb = wave * kPer; jb < nc; jb += (kPlanBlock / 64) * kPer) {
-    NodeSeg sg[kPer];
-    long long gq[kPer], hq[kPer];
-    double ppe[kPer];
-    SplitCand cf[kPer];
+  if (nc <= kStageC && F_sel <= kStageF) {
+    // Staged: the level's split candidates (nc x F_sel consecutive records)
+    // in one coalesced pass of the whole block, transposed into LDS; then
+    // one lane per candidate takes the best over its features in order
+    // (largest gain, lowest position on ties: the first of equal gains).
+    const int32_t E = nc * F_sel;
+    SplitCand cv[kStageC * kStageF / kPlanBlock];
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-      const int j = min(jb + q, nc - 1);
-      const int64_t c = first + j;
-      sg[q] = segs[c];
-      gq[q] = totals[2 * c];
-      hq[q] = totals[2 * c + 1];
-      ppe[q] = a.level == 0 ? 0.0 : prev_parent_e[j >> 1];
-      cf[q] = lane < F_sel ? cand[c * F_sel + lane] : SplitCand{0.0, -1, 0};
+    for (int k = 0; k < kStageC * kStageF / kPlanBlock; ++k) {
+      const int32_t e = tid + k * kPlanBlock;
+      cv[k] = e < E ? cand[(int64_t)first * F_sel + e] : SplitCand{0.0, -1, 0};
     }
-    if (jb == wave * kPer && tid < first) s_ke[tid] = ke0;
+    NodeSeg sg{0, 0, 0, 0};
+    long long gq = 0, hq = 0;
+    double ppe = 0.0;
+    if (tid < nc) {
+      const int64_t c = first + tid;
+      sg = segs[c];
+      gq = totals[2 * c];
+      hq = totals[2 * c + 1];
+      ppe = a.level == 0 ? 0.0 : prev_parent_e[tid >> 1];
+    }
+    if (tid < first) s_ke[tid] = ke0;
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-      const int j = jb + q;
-      const int64_t c = first + min(j, nc - 1);
-      // Best over the features: largest gain, lowest position on ties.
+    for (int k = 0; k < kStageC * kStageF / kPlanBlock; ++k) {
+      const int32_t e = tid + k * kPlanBlock;
+      if (e < E) {
+        const int32_t j = e / F_sel, f = e - j * F_sel;
+        s_cg[f * kStageC + j] = cv[k].gain;
+        s_cb[f * kStageC + j] = (int16_t)cv[k].bin;
+      }
+    }
+    __syncthreads();
+    if (tid < nc) {
       double best = 0.0;
       int32_t bf = -1, bb = 0;
-      if (cf[q].bin >= 0) {
-        best = cf[q].gain;
-        bf = lane;
-        bb = cf[q].bin;
-      }
-      for (int f = lane + 64; f < F_sel; f += 64) {
-        const SplitCand x = cand[c * F_sel + f];
-        if (x.bin >= 0 && (bf < 0 || x.gain > best)) {
-          best = x.gain;
-          bf = f;
-          bb = x.bin;
+      // Eight features' reads in flight, then their comparisons in order.
+      for (int32_t f0 = 0; f0 < F_sel; f0 += 8) {
+        double g[8];
+        int32_t b[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int32_t f = min(f0 + u, kStageF - 1);
+          g[u] = s_cg[f * kStageC + tid];
+          b[u] = s_cb[f * kStageC + tid];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (f0 + u < F_sel && b[u] >= 0 && (bf < 0 || g[u] > best)) {
+            best = g[u];
+            bf = f0 + u;
+            bb = b[u];
+          }
         }
       }
-      wave_argmax(best, bf, bb);
-      if (lane == 0 && j < nc) {
-        const bool valid = sg[q].valid != 0;
-        if (!valid) bf = -1;
-        const double gain = bf >= 0 ? best : -1e9;
-        double e = 0.0;
-        int32_t fl = 0;
-        if (valid) {
-          const double pv = a.level == 0 ? gain : ppe[q];
-          e = pv < gain ? pv : gain;
-          fl = (bf >= 0 && gain > a.gamma) ? 1 : 0;
+      plan_record(tid, sg, gq, hq, ppe, best, bf, bb, a, s_start, s_count, s_gq, s_hq, s_gain,
+                  s_e, s_fpos, s_bin, s_valid, s_flag);
+    }
+  } else {
+    // Four candidates per wave and pass, one lane per feature (one pass for
+    // up to 64 candidates).
+    constexpr int kPer = 4;
+    for (int jb = wave * kPer; jb < nc; jb += (kPlanBlock / 64) * kPer) {
+      NodeSeg sg[kPer];
+      long long gq[kPer], hq[kPer];
+      double ppe[kPer];
+      SplitCand cf[kPer];
+#pragma unroll
+      for (int q = 0; q < kPer; ++q) {
+        const int j = min(jb + q, nc - 1);
+        const int64_t c = first + j;
+        sg[q] = segs[c];
+        gq[q] = totals[2 * c];
+        hq[q] = totals[2 * c + 1];
+        ppe[q] = a.level == 0 ? 0.0 : prev_parent_e[j >> 1];
+        cf[q] = lane < F_sel ? cand[c * F_sel + lane] : SplitCand{0.0, -1, 0};
+      }
+      if (jb == wave * kPer && tid < first) s_ke[tid] = ke0;
+#pragma unroll
+      for (int q = 0; q < kPer; ++q) {
+        const int j = jb + q;
+        const int64_t c = first + min(j, nc - 1);
+        // Best over the features: largest gain, lowest position on ties.
+        double best = 0.0;
+        int32_t bf = -1, bb = 0;
+        if (cf[q].bin >= 0) {
+          best = cf[q].gain;
+          bf = lane;
+          bb = cf[q].bin;
         }
-        s_start[j] = sg[q].start;
-        s_count[j] = sg[q].count;
-        s_gq[j] = valid ? gq[q] : 0;
-        s_hq[j] = valid ? hq[q] : 0;
-        s_gain[j] = gain;
-        s_e[j] = e;
-        s_fpos[j] = bf;
-        s_bin[j] = bf >= 0 ? bb : 0;
-        s_valid[j] = sg[q].valid;
-        s_flag[j] = fl;
+        for (int f = lane + 64; f < F_sel; f += 64) {
+          const SplitCand x = cand[c * F_sel + f];
+          if (x.bin >= 0 && (bf < 0 || x.gain > best)) {
+            best = x.gain;
+            bf = f;
+            bb = x.bin;
+          }
+        }
+        wave_argmax(best, bf, bb);
+        if (lane == 0 && j < nc)
+          plan_record(j, sg[q], gq[q], hq[q], ppe[q], best, bf, bb, a, s_start, s_count, s_gq,
+                      s_hq, s_gain, s_e, s_fpos, s_bin, s_valid, s_flag);
       }
     }
+    // (Waves that took no candidate store their earlier ranks here.)
+    if (wave * kPer >= nc && tid < first) s_ke[tid] = ke0;
   }
-  // (Waves that took no candidate store their earlier ranks here.)
-  if (wave * kPer >= nc && tid < first) s_ke[tid] = ke0;
   __syncthreads();
 
   // The previous level's parents are kept splits when their children (this
@@ -2353,9 +2433,12 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       gt = ge ? (uint32_t)max((int64_t)1, div_pos(pq.start + pq.count - a0 + a.part_tile - 1, a.part_tile))
               : 0u;
     }
-    uint32_t n_groups, tcar_g;
-    const uint32_t gidx = block_excl_scan<kPlanBlock>(ge, stmp, n_groups);
-    const uint32_t toff = block_excl_scan<kPlanBlock>(gt, stmp, tcar_g);
+    // Both scans in one: groups in the low word, tiles in the high word.
+    unsigned long long gtot;
+    const unsigned long long gpre =
+        block_excl_scan<kPlanBlock>(((unsigned long long)gt << 32) | ge, stmp64, gtot);
+    const uint32_t gidx = (uint32_t)gpre, toff = (uint32_t)(gpre >> 32);
+    const uint32_t n_groups = (uint32_t)gtot, tcar_g = (uint32_t)(gtot >> 32);
     if (tid < n_pp) {
       s_gi[tid] = ge ? (int32_t)gidx : -1;
       if (ge) {
@@ -2440,10 +2523,14 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
                 : a.mode == kLevelInPlace ? (uint32_t)max((int64_t)1, div_pos(cnt + th - 1, th))
                                           : (uint32_t)div_pos(cnt / 2 + th, th);
   }
-  uint32_t tcar, hcar;
   const int32_t n_groups = grouped ? (int32_t)s_tcar : n_exp;
-  const uint32_t tp = block_excl_scan<kPlanBlock>(nt, stmp, tcar);
-  const uint32_t hp = block_excl_scan<kPlanBlock>(nh, stmp, hcar);
+  // Both scans in one: tiles in the low word, histogram tasks in the high.
+  unsigned long long thtot;
+  const unsigned long long thpre =
+      block_excl_scan<kPlanBlock>(((unsigned long long)nh << 32) | nt, stmp64, thtot);
+  const uint32_t tp = (uint32_t)thpre, hp = (uint32_t)(thpre >> 32);
+  uint32_t tcar = (uint32_t)thtot;
+  const uint32_t hcar = (uint32_t)(thtot >> 32);
   if (grouped) tcar = (uint32_t)s_tb[n_groups];
   if (tcar > (uint32_t)a.tile_cap || hcar > (uint32_t)a.hist_cap) {
     // Capacities are sized from proven bounds; reaching this is a bug.
