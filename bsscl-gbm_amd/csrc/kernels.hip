@@ -1660,19 +1660,53 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_reduce_split(
     SplitCand *__restrict__ cand, long long *__restrict__ totals, int32_t span_parents) {
   __shared__ long long red[kRsWaves][kHistPerFeat];
   const int lane = lane_id(), wave = (int)(threadIdx.x >> 6);
-  // The root's block (parents == nullptr) has one node and no sibling.
+  // An item's records: its parent's split, smaller child and task range.
+  // The first item's are loaded with the plan (its parent index is below
+  // the launch's parent bound, so the reads stay in the level lists even
+  // when the level has fewer parents); the root's block (parents ==
+  // nullptr) has one node and no sibling.
+  struct Item {
+    int32_t small, hb0, hb1;
+    PartParent pp;
+  };
+  const auto records = [&](int32_t p) {
+    Item r;
+    r.small = parents ? hist_node[p] : 0;
+    r.pp = parents ? parents[p] : PartParent{0, 0, 0, 0, -1, -1, -1, 0};
+    r.hb0 = hist_begin[p];
+    r.hb1 = hist_begin[p + 1];
+    return r;
+  };
+  const int64_t it0 = blockIdx.x;
+  Item cur = records((int32_t)div_pos(it0, F_sel));
   const int32_t n_par = parents ? plan->n_parents : 1;
   const int32_t tile_rows = plan->tile_rows;
   const int64_t n_items = (int64_t)n_par * F_sel;
-  for (int64_t it = blockIdx.x; it < n_items; it += gridDim.x) {
+  for (int64_t it = it0; it < n_items; it += gridDim.x) {
     const int32_t p = (int32_t)div_pos(it, F_sel), fpos = (int32_t)(it - (int64_t)p * F_sel);
-    const int32_t small = parents ? hist_node[p] : 0;
+    if (it != it0) cur = records(p);
+    const int32_t small = cur.small;
     if (small < 0) continue;  // split not kept: no children (uniform)
+    const PartParent &pp = cur.pp;
+    const int32_t large = parents ? (pp.left_id == small ? pp.right_id : pp.left_id) : small;
+    // Both children's segments and (wave 1) the parent's histogram, in
+    // flight with the partials below.
     const NodeSeg ss = segs[small];
-    // (An in-place level's tasks tiled the parent's segment.)
-    const int32_t nt = hist_tasks_with_rows(hist_begin, p,
-                                            span_parents ? parents[p].count : ss.count, tile_rows);
+    const NodeSeg sl = segs[large];
     const int64_t woff = (int64_t)fpos * kHistPerFeat + lane * 8;
+    long long pg[4] = {0, 0, 0, 0}, ph[4] = {0, 0, 0, 0};
+    if (wave == 1 && parents) {
+      const unsigned long long *hp = pool + (int64_t)pp.node * node_stride + woff;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        pg[k] = (long long)hp[2 * k];
+        ph[k] = (long long)hp[2 * k + 1];
+      }
+    }
+    // (An in-place level's tasks tiled the parent's segment.)
+    const int64_t rows_tiled = span_parents ? pp.count : ss.count;
+    const int32_t nt = (int32_t)min((int64_t)(cur.hb1 - cur.hb0),
+                                    div_pos(rows_tiled + tile_rows - 1, tile_rows));
     unsigned long long *hs = pool + (int64_t)small * node_stride + woff;
     long long g[4] = {0, 0, 0, 0}, h[4] = {0, 0, 0, 0};
     if (nt == 1) {
@@ -1685,7 +1719,7 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_reduce_split(
       }
     } else {
       const unsigned long long *src =
-          part + ((int64_t)hist_begin[p] * F_sel) * kHistPerFeat + woff;
+          part + ((int64_t)cur.hb0 * F_sel) * kHistPerFeat + woff;
       const int64_t tstride = (int64_t)F_sel * kHistPerFeat;
       int32_t t = wave;
       for (; t + kRsWaves < nt; t += 2 * kRsWaves) {
@@ -1743,15 +1777,13 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_reduce_split(
         }
       } else {
         // The larger child: parent minus small.
-        const PartParent pp = parents[p];
-        node = pp.left_id == small ? pp.right_id : pp.left_id;
-        s = segs[node];
-        const unsigned long long *hp = pool + (int64_t)pp.node * node_stride + woff;
+        node = large;
+        s = sl;
         unsigned long long *hl = pool + (int64_t)node * node_stride + woff;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          g[k] = (long long)hp[2 * k] - g[k];
-          h[k] = (long long)hp[2 * k + 1] - h[k];
+          g[k] = pg[k] - g[k];
+          h[k] = ph[k] - h[k];
           hl[2 * k] = (unsigned long long)g[k];
           hl[2 * k + 1] = (unsigned long long)h[k];
         }

@@ -62,9 +62,23 @@ def _p(a):
 # Binning (est:2073-2189)
 # --------------------------------------------------------------------------
 
-def _column_edges(col, n_bins):
+def weighted_quantiles(values, weights, q):
+    """est:2114-2124: the quantiles q of ``values`` under ``weights``.  Each
+    sorted value sits at the midpoint of its weight's share of the total,
+    (cumsum(w) - w/2) / sum(w), and q is interpolated linearly between those
+    positions (clamped to the end values outside them)."""
+    sorter = np.argsort(values)
+    v = values[sorter]
+    w = weights[sorter]
+    pos = (np.cumsum(w) - 0.5 * w) / np.sum(w)
+    return np.interp(q, pos, v)
+
+
+def _column_edges(col, n_bins, weights=None):
     """One feature of ``_build_bin_edges`` (est:2092-2133): (edges, count,
-    has_nan)."""
+    has_nan).  ``weights`` (the rows' sample weights) selects the weighted
+    quantiles of est:2114-2124 for the edges of a column with more distinct
+    values than bins."""
     has_nan = np.any(np.isnan(col))
     if has_nan:
         col_clean = col[~np.isnan(col)]
@@ -78,14 +92,19 @@ def _column_edges(col, n_bins):
         e = np.sort(np.unique(col_clean))
     else:
         q = np.linspace(0, 1, min(max_numeric + 1, n_unique))
-        e = np.unique(np.percentile(col_clean, q * 100))
+        if weights is not None:
+            w_clean = weights[~np.isnan(col)] if has_nan else weights
+            e = np.unique(weighted_quantiles(col_clean, w_clean, q))
+        else:
+            e = np.unique(np.percentile(col_clean, q * 100))
     e = np.append(e, e[-1] + 1e-8)
     return e, len(e) - 1 + (1 if has_nan else 0), has_nan
 
 
-def build_bin_edges(X, n_bins, threads=1):
-    """``_build_bin_edges`` without categorical or weighted-quantile branches
-    (est:2073-2141).  Returns (edges_2d, bin_counts, nan_bin_id).  With
+def build_bin_edges(X, n_bins, threads=1, sample_weight=None):
+    """``_build_bin_edges`` without the categorical branch (est:2073-2141).
+    Returns (edges_2d, bin_counts, nan_bin_id).  ``sample_weight`` selects
+    the weighted-quantile branch (est:2114-2124, scale_pos_weight).  With
     ``threads`` > 1 the columns are processed concurrently (each column's
     NumPy calls are unchanged, so the result is the same)."""
     F = X.shape[1]
@@ -94,9 +113,9 @@ def build_bin_edges(X, n_bins, threads=1):
     if threads > 1:
         from concurrent.futures import ThreadPoolExecutor
         with ThreadPoolExecutor(threads) as pool:
-            per = list(pool.map(lambda j: _column_edges(X[:, j], n_bins), range(F)))
+            per = list(pool.map(lambda j: _column_edges(X[:, j], n_bins, sample_weight), range(F)))
     else:
-        per = [_column_edges(X[:, j], n_bins) for j in range(F)]
+        per = [_column_edges(X[:, j], n_bins, sample_weight) for j in range(F)]
     edges = []
     for j, (e, count, has_nan) in enumerate(per):
         edges.append(e)
@@ -296,7 +315,8 @@ class OracleGBM:
                  min_samples_leaf=5, min_child_weight="auto", gamma="auto",
                  subsample="auto", colsample_bytree="auto",
                  class_weight="balanced_sqrt", max_leaves=31,
-                 binning_strategy="auto", random_state=None, edge_threads=1):
+                 binning_strategy="auto", random_state=None, edge_threads=1,
+                 scale_pos_weight=None, objective="auto"):
         self.binning_strategy_init = binning_strategy
         self.n_estimators_init = n_estimators
         self.max_depth_init = max_depth
@@ -309,6 +329,8 @@ class OracleGBM:
         self.subsample_init = subsample
         self.colsample_init = colsample_bytree
         self.class_weight = class_weight
+        self.scale_pos_weight = scale_pos_weight
+        self.objective = objective  # 'auto' or 'binary' (the reference never resolves 'auto')
         self.max_leaves = max_leaves
         self.random_state = random_state
         self.edge_threads = edge_threads  # columns of the edge pass run concurrently
@@ -380,9 +402,15 @@ class OracleGBM:
         self.max_leaves = 63 if n > 10000 else (15 if n < 2000 else 31)
 
     def _class_weights(self, y):
-        """est:2570-2603 (no scale_pos_weight)."""
+        """est:2570-2603: scale_pos_weight with objective='binary' replaces
+        the class weights by 1 for class 0 and scale_pos_weight for class 1
+        (with the default objective 'auto' the reference ignores it)."""
         n = len(y)
         K = getattr(self, "n_classes_", 2)
+        if self.scale_pos_weight is not None and self.objective == "binary":
+            w = np.ones(n, dtype=np.float64)
+            w[y == 1] = self.scale_pos_weight
+            return w
         if self.class_weight not in ("balanced", "balanced_sqrt"):
             return np.ones(n, dtype=np.float64)
         w = np.ones(n, dtype=np.float64)
@@ -417,8 +445,12 @@ class OracleGBM:
         if not np.issubdtype(X.dtype, np.floating) or X.dtype == np.float16:
             X = X.astype(np.float64)
         self._adaptive(X)
+        edge_w = None  # est:3211-3215: scale_pos_weight weights the edges' quantiles
+        if self.scale_pos_weight is not None and self.objective == "binary":
+            edge_w = np.ones(len(y), dtype=np.float64)
+            edge_w[y == 1] = self.scale_pos_weight
         self.bin_edges, self.feature_bin_counts, self._nan_bin_id = \
-            build_bin_edges(X, self.n_bins, threads=self.edge_threads)
+            build_bin_edges(X, self.n_bins, threads=self.edge_threads, sample_weight=edge_w)
         self._max_bins = int(np.max(self.feature_bin_counts))
         X_bin = bin_features(X, self.bin_edges, self.feature_bin_counts,
                              self._nan_bin_id, self.binning_strategy)

@@ -339,6 +339,15 @@ def _fit_case(name):
         y = (rng.random(10_000) < 1 / (1 + np.exp(-(X @ w)))).astype(np.int64)
         params = dict(n_estimators=10, max_depth=6, learning_rate=0.1, n_bins=255,
                       class_weight=None, random_state=0)
+    elif name == "scale_pos_weight":
+        # scale_pos_weight with objective='binary' (est:2570-2576): class
+        # weights 1 and 6, edges from weighted quantiles (est:2114-2124, host
+        # branch), 4% positives.
+        X, y = make_data(25000, 16, seed=17, nan_frac=0.05, nan_cols=[2, 9])
+        y = (np.random.default_rng(7).random(25000) < 0.04).astype(np.int64)
+        X[y == 1, :6] += 0.8
+        params = dict(n_estimators=12, max_depth=6, n_bins=255, scale_pos_weight=6.0,
+                      objective="binary", random_state=0)
     elif name == "nan_imbalanced":
         X, y = make_data(30000, 30, seed=12, nan_frac=0.05)
         y = (np.random.default_rng(1).random(30000) < 0.03).astype(np.int64)
@@ -354,7 +363,7 @@ def _fit_case(name):
 
 
 @pytest.mark.parametrize("name", ["config1", "nan_imbalanced", "sparse", "defaults_28",
-                                  "top_bin_28"])
+                                  "top_bin_28", "scale_pos_weight"])
 def test_fit_lockstep_and_end_to_end(engine, name):
     """Every round of the oracle's fit, rebuilt by the engine from the same
     gradients, rows and features (lockstep), and the estimator's own tree of

@@ -259,3 +259,65 @@ class _Shape:
 
     def __init__(self, n, p):
         self.shape = (n, p)
+
+
+# --------------------------------------------------------------------------
+# scale_pos_weight: weighted-quantile edges (est:2114-2124), class weights
+# (est:2570-2576).
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [7, 100, 5001])
+def test_weighted_quantiles_equal_weights_are_hazen(n):
+    """With equal weights every value sits at position (k + 1/2) / n, which
+    is the Hazen plotting position (Hyndman & Fan type 5): NumPy's
+    percentile(method='hazen') computes the same quantiles independently.
+    Unequal positions (a dropped -w/2, another divisor) fail this; the
+    default linear percentile differs from it."""
+    rng = np.random.default_rng(n)
+    v = rng.standard_normal(n)
+    q = np.linspace(0, 1, 33)
+    got = om.weighted_quantiles(v, np.full(n, 2.5), q)
+    np.testing.assert_allclose(got, np.percentile(v, q * 100, method="hazen"), rtol=0, atol=1e-14)
+    assert not np.allclose(got, np.percentile(v, q * 100))
+
+
+def test_weighted_quantiles_two_values_closed_form():
+    """Values a < b with weights wa, wb sit at wa/2/W and (wa + wb/2)/W; q
+    between them interpolates linearly, q outside takes the end value."""
+    a, b, wa, wb = -1.0, 3.0, 1.0, 5.0
+    W = wa + wb
+    pa, pb = 0.5 * wa / W, (wa + 0.5 * wb) / W
+    q = np.array([0.0, pa, 0.3, 0.5, pb, 1.0])
+    want = np.where(q <= pa, a, np.where(q >= pb, b, a + (b - a) * (q - pa) / (pb - pa)))
+    got = om.weighted_quantiles(np.array([b, a]), np.array([wb, wa]), q)
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-15)
+
+
+def test_scale_pos_weight_class_weights():
+    y = np.array([0] * 90 + [1] * 10)
+    m = om.OracleGBM(scale_pos_weight=4.0, class_weight="balanced_sqrt", objective="binary")
+    w = m._class_weights(y)
+    assert (w[:90] == 1.0).all() and (w[90:] == 4.0).all()
+    # With the default objective ('auto') the reference ignores scale_pos_weight
+    # (est:2572): the class weights stay balanced_sqrt.
+    w_auto = om.OracleGBM(scale_pos_weight=4.0, class_weight="balanced_sqrt")._class_weights(y)
+    np.testing.assert_allclose(w_auto[-1], (100 / (2 * 10)) ** 0.35)
+
+
+def test_estimator_weighted_edges_match_oracle():
+    """The estimator's host branch for scale_pos_weight (est:2114-2124) gives
+    the oracle's edges and bin counts, with NaN columns and few-valued
+    columns mixed in."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    X, y = make_data(6000, 9, seed=21, nan_frac=0.1, nan_cols=[1, 4], dtype=np.float64)
+    X[:, 7] = np.round(X[:, 7])  # few distinct values: the sorted-uniques branch
+    sw = np.ones(len(y))
+    sw[y == 1] = 3.5
+    est = HybridHistGBMNumbaV1_0_1(n_bins=64, verbose=False)
+    e_est, c_est = est._build_bin_edges_host(X, sample_weight=sw)
+    e_ref, c_ref, nan_ref = om.build_bin_edges(X, 64, sample_weight=sw)
+    np.testing.assert_array_equal(c_est, c_ref)
+    np.testing.assert_array_equal(e_est, e_ref)
+    np.testing.assert_array_equal(est._nan_bin_id, nan_ref)
+    e_unw, _, _ = om.build_bin_edges(X, 64)
+    assert not np.array_equal(e_unw, e_ref)  # the weights move the edges
