@@ -2246,6 +2246,9 @@ __device__ __forceinline__ void plan_record(
 // Candidates x features staged in LDS by k_plan_lds (levels of up to 64
 // candidates over up to 64 features; larger ones use a wave per candidate).
 constexpr int kStageC = 64, kStageF = 64;
+// Its fast path also needs at most this many nodes before the level's
+// candidates (every level of a tree of up to 63 leaves).
+constexpr int kFastFirst = 128;
 
 __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     NodeOut *__restrict__ nodes, LevelPlan *__restrict__ plan,
@@ -2275,6 +2278,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
   __shared__ unsigned long long s_rows;
   __shared__ double s_cg[kStageF * kStageC];   // staged gains [feature][candidate]
   __shared__ int16_t s_cb[kStageF * kStageC];  // staged bins (-1: no split)
+  __shared__ int32_t s_fast[8];                // fast path: wave 0's results
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const LevelPlan prev = *plan;
@@ -2289,6 +2293,307 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       q.tile_rows = 4096;
       q.n_nodes = n_prev;
       q.overflow = -1;
+      *plan = q;
+    }
+    return;
+  }
+  const bool grouped = a.mode == kLevelGrouped;
+  if (nc <= kStageC && first <= kFastFirst && F_sel <= kStageF) {
+    // Fast path: one candidate per lane of wave 0, which takes every
+    // decision below with wave operations and no block barrier; the other
+    // waves stage the split candidates and write the tile and task lists.
+    const int32_t E = nc * F_sel;
+    SplitCand cv[kStageC * kStageF / kPlanBlock];
+#pragma unroll
+    for (int k = 0; k < kStageC * kStageF / kPlanBlock; ++k) {
+      const int32_t e = tid + k * kPlanBlock;
+      cv[k] = e < E ? cand[(int64_t)first * F_sel + e] : SplitCand{0.0, -1, 0};
+    }
+    const int j = lane;  // wave 0: candidate j, previous parent j, earlier nodes j, j + 64
+    NodeSeg sg{0, 0, 0, 0};
+    long long gq = 0, hq = 0;
+    double ppe = 0.0, pe = 0.0, ke_a = 0.0, ke_b = 0.0;
+    PartParent pq{0, 0, 0, 0, -1, -1, -1, 0};
+    if (wave == 0) {
+      if (j < nc) {
+        const int64_t c = first + j;
+        sg = segs[c];
+        gq = totals[2 * c];
+        hq = totals[2 * c + 1];
+        ppe = a.level == 0 ? 0.0 : prev_parent_e[j >> 1];
+      }
+      if (j < n_pp) {
+        pq = prev_parents[j];
+        pe = prev_parent_e[j];
+      }
+      if (j < first) ke_a = kept_e[j];
+      if (j + 64 < first) ke_b = kept_e[j + 64];
+    }
+#pragma unroll
+    for (int k = 0; k < kStageC * kStageF / kPlanBlock; ++k) {
+      const int32_t e = tid + k * kPlanBlock;
+      if (e < E) {
+        const int32_t jj = e / F_sel, f = e - jj * F_sel;
+        s_cg[f * kStageC + jj] = cv[k].gain;
+        s_cb[f * kStageC + jj] = (int16_t)cv[k].bin;
+      }
+    }
+    if (wave == 0) {
+      if (j < first) s_ke[j] = ke_a;
+      if (j + 64 < first) s_ke[j + 64] = ke_b;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      // Best split over the features (largest gain, first position of equal
+      // gains), then the candidate's rank and whether it may be split
+      // (est:649-652, 762-801).
+      const bool is_cand = j < nc;
+      double best = 0.0;
+      int32_t bf = -1, bb = 0;
+      if (is_cand) {
+        for (int32_t f0 = 0; f0 < F_sel; f0 += 8) {
+          double g[8];
+          int32_t b[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int32_t f = min(f0 + u, kStageF - 1);
+            g[u] = s_cg[f * kStageC + j];
+            b[u] = s_cb[f * kStageC + j];
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            if (f0 + u < F_sel && b[u] >= 0 && (bf < 0 || g[u] > best)) {
+              best = g[u];
+              bf = f0 + u;
+              bb = b[u];
+            }
+          }
+        }
+      }
+      const bool valid = is_cand && sg.valid != 0;
+      if (!valid) bf = -1;
+      const double gain = bf >= 0 ? best : -1e9;
+      double e = 0.0;
+      int32_t cand_ok = 0;
+      if (valid) {
+        const double pv = a.level == 0 ? gain : ppe;
+        e = pv < gain ? pv : gain;
+        cand_ok = (bf >= 0 && gain > a.gamma) ? 1 : 0;
+      }
+      // The previous level's parents are kept splits when their children
+      // (this level's candidates 2j, 2j + 1) are valid.
+      const int32_t v2 = __shfl(valid ? 1 : 0, min(2 * j, 63), 64);
+      if (j < n_pp) {
+        const double kv = v2 ? pe : -INFINITY;
+        s_ke[pq.node] = kv;
+        kept_e[pq.node] = kv;
+      }
+      __builtin_amdgcn_wave_barrier();
+      // Expanded: fewer than max_leaves - 1 kept splits ranked above.
+      int32_t fl = 0;
+      if (cand_ok) {
+        int32_t above = 0;
+        for (int32_t u0 = 0; u0 < first; u0 += 8) {
+          double k8[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) k8[q] = s_ke[u0 + q];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) above += (u0 + q < first && k8[q] > e) ? 1 : 0;
+        }
+        fl = above < a.max_leaves - 1 ? 1 : 0;
+      }
+      const uint32_t fincl = wave_incl_scan<uint32_t>((uint32_t)fl);
+      const uint32_t pidx = fincl - (uint32_t)fl;
+      const int32_t n_exp = (int32_t)wave_lane(fincl, 63);
+      const int64_t n_new = (int64_t)n_prev + 2 * (int64_t)n_exp;
+      int32_t status = n_new > a.node_cap ? 1 : 0;
+      int32_t n_groups = n_exp;
+      uint32_t tcar = 0, hcar = 0;
+      int32_t th = 0;
+      if (status == 0) {
+        // A grouped level's groups: the previous parents with an expanded
+        // child, each with its tiles over the previous parent's segment.
+        int32_t gi = -1;
+        if (grouped) {
+          const int32_t pid_or = fl ? (int32_t)pidx : -1;
+          const int32_t pl = __shfl(pid_or, min(2 * j, 63), 64);
+          const int32_t pr = __shfl(pid_or, min(2 * j + 1, 63), 64);
+          const bool ge = j < n_pp && (pl >= 0 || pr >= 0);
+          const int64_t a0 = pq.start & ~int64_t(15);
+          const uint32_t gt =
+              ge ? (uint32_t)max((int64_t)1,
+                                 div_pos(pq.start + pq.count - a0 + a.part_tile - 1, a.part_tile))
+                 : 0u;
+          // Groups in the low word, tiles in the high word.
+          const unsigned long long gv = ((unsigned long long)gt << 32) | (ge ? 1ull : 0ull);
+          const unsigned long long gincl = wave_incl_scan<unsigned long long>(gv);
+          const unsigned long long gpre = gincl - gv, gtot = wave_lane(gincl, 63);
+          const uint32_t gidx = (uint32_t)gpre, toff = (uint32_t)(gpre >> 32);
+          n_groups = (int32_t)(uint32_t)gtot;
+          const uint32_t tcar_g = (uint32_t)(gtot >> 32);
+          if (ge) {
+            PartGroup G;
+            G.start = pq.start;
+            G.count = pq.count;
+            G.fpos = pq.fpos;
+            G.bin = pq.bin;
+            G.par[0] = pl;
+            G.par[1] = pr;
+            groups[gidx] = G;
+            s_tb[gidx] = (int32_t)toff;
+            s_gs[gidx] = a0;
+            tile_begin[gidx] = (int32_t)toff;
+            gi = (int32_t)gidx;
+          }
+          if (j == 0) {
+            s_tb[n_groups] = (int32_t)tcar_g;
+            tile_begin[n_groups] = (int32_t)tcar_g;
+          }
+          tcar = tcar_g;
+        }
+        // Records, parents, ranks; tiles per parent; rows to build.
+        const int32_t gi_j = __shfl(gi, j >> 1, 64);
+        unsigned long long rows = 0;
+        if (is_cand) {
+          const int32_t v = first + j;
+          const int32_t L = fl ? n_prev + 2 * (int32_t)pidx : -1;
+          NodeOut N;
+          N.start = sg.start;
+          N.count = sg.count;
+          N.Gq = valid ? gq : 0;
+          N.Hq = valid ? hq : 0;
+          N.gain = gain;
+          N.e = e;
+          N.fpos = bf;
+          N.bin = bf >= 0 ? bb : 0;
+          N.valid = sg.valid;
+          N.left = L;
+          nodes[v] = N;
+          if (!fl) {
+            kept_e[v] = -INFINITY;
+          } else {
+            const int32_t i = (int32_t)pidx;
+            PartParent P;
+            P.start = N.start;
+            P.count = N.count;
+            P.fpos = N.fpos;
+            P.bin = N.bin;
+            P.left_id = L;
+            P.right_id = L + 1;
+            P.node = v;
+            P.gslot = grouped ? 2 * gi_j + (j & 1) : 2 * i;
+            parents[i] = P;
+            parent_e[i] = N.e;
+            if (!grouped) {
+              const int64_t a0 = N.start & ~int64_t(15);
+              // At least one tile: a parent's first tile writes its children's segments.
+              s_tb[i] = (int32_t)max((int64_t)1,
+                                     div_pos(N.start + N.count - a0 + a.part_tile - 1, a.part_tile));
+              s_gs[i] = a0;
+            }
+            s_count[i] = N.count;
+            rows = (unsigned long long)(N.count / 2);  // at most the smaller child's
+          }
+        }
+        rows = wave_sum(rows);
+        __builtin_amdgcn_wave_barrier();
+        // Rows per histogram task: sized for the smaller children's rows;
+        // in place a task tiles twice as many of its parent's rows, of which
+        // it adds those of the smaller child (at most half).
+        th = plan_tile_rows((int64_t)rows, a) * (a.mode == kLevelInPlace ? 2 : 1);
+        uint32_t nt = 0, nh = 0;
+        if (j < n_exp) {
+          nt = grouped ? 0u : (uint32_t)s_tb[j];
+          const int64_t cnt = s_count[j];
+          nh = a.last ? 0u
+                      : a.mode == kLevelInPlace ? (uint32_t)max((int64_t)1, div_pos(cnt + th - 1, th))
+                                                : (uint32_t)div_pos(cnt / 2 + th, th);
+        }
+        // Tiles in the low word, histogram tasks in the high word.
+        const unsigned long long tv = ((unsigned long long)nh << 32) | nt;
+        const unsigned long long tincl = wave_incl_scan<unsigned long long>(tv);
+        const unsigned long long tpre = tincl - tv, ttot = wave_lane(tincl, 63);
+        if (!grouped) tcar = (uint32_t)ttot;
+        hcar = (uint32_t)(ttot >> 32);
+        if (tcar > (uint32_t)a.tile_cap || hcar > (uint32_t)a.hist_cap) {
+          status = 2;  // capacities are sized from proven bounds; reaching this is a bug
+        } else {
+          if (j < n_exp) {
+            if (!grouped) {
+              s_tb[j] = (int32_t)(uint32_t)tpre;
+              tile_begin[j] = (int32_t)(uint32_t)tpre;
+            }
+            s_hb[j] = (int32_t)(uint32_t)(tpre >> 32);
+            hist_begin[j] = (int32_t)(uint32_t)(tpre >> 32);
+          }
+          if (j == 0) {
+            if (!grouped) {
+              s_tb[n_exp] = (int32_t)tcar;
+              tile_begin[n_exp] = (int32_t)tcar;
+            }
+            s_hb[n_exp] = (int32_t)hcar;
+            hist_begin[n_exp] = (int32_t)hcar;
+          }
+        }
+      }
+      if (j == 0) {
+        s_fast[0] = status;
+        s_fast[1] = n_exp;
+        s_fast[2] = n_groups;
+        s_fast[3] = (int32_t)tcar;
+        s_fast[4] = (int32_t)hcar;
+        s_fast[5] = th;
+        s_fast[6] = (int32_t)min(n_new, (int64_t)INT32_MAX);
+      }
+    }
+    __syncthreads();
+    const int32_t status = s_fast[0], n_exp = s_fast[1], n_groups = s_fast[2];
+    const int32_t tcar = s_fast[3], hcar = s_fast[4];
+    if (status != 0) {
+      if (tid == 0) {
+        LevelPlan q = {};
+        q.first_child = n_prev;
+        q.tile_rows = 4096;
+        q.n_nodes = n_prev;
+        q.overflow = status == 1 ? s_fast[6] : -1;
+        *plan = q;
+      }
+      return;
+    }
+    // Tile and histogram-task lists: item -> its group (parent) by binary
+    // search.
+    for (int t = tid; t < tcar; t += kPlanBlock) {
+      int lo = 0, hi = n_groups - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_tb[mid] <= t) lo = mid;
+        else hi = mid - 1;
+      }
+      PartTile T;
+      T.row0 = s_gs[lo] + (int64_t)(t - s_tb[lo]) * a.part_tile;
+      T.rows = a.part_tile;
+      T.parent = lo;
+      tiles[t] = T;
+    }
+    for (int q = tid; q < hcar; q += kPlanBlock) {
+      int lo = 0, hi = n_exp - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_hb[mid] <= q) lo = mid;
+        else hi = mid - 1;
+      }
+      hist_tasks[q] = HistTask{lo, q - s_hb[lo]};
+    }
+    if (tid == 0) {
+      LevelPlan q;
+      q.n_parents = n_exp;
+      q.n_tiles = tcar;
+      q.n_hist = hcar;
+      q.n_split = 2 * n_exp;
+      q.first_child = n_prev;
+      q.tile_rows = s_fast[5];
+      q.n_nodes = (int32_t)((int64_t)n_prev + 2 * (int64_t)n_exp);
+      q.overflow = 0;
       *plan = q;
     }
     return;
@@ -2546,7 +2851,6 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
 
   // Exclusive offsets of each parent's tiles (a grouped level: its groups'
   // tiles, already laid out) and histogram tasks.
-  const bool grouped = a.mode == kLevelGrouped;
   uint32_t nt = 0, nh = 0;
   if (tid < n_exp) {
     nt = grouped ? 0u : (uint32_t)s_tb[tid];
