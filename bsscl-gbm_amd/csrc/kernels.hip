@@ -2279,6 +2279,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
   __shared__ double s_cg[kStageF * kStageC];   // staged gains [feature][candidate]
   __shared__ int16_t s_cb[kStageF * kStageC];  // staged bins (-1: no split)
   __shared__ int32_t s_fast[8];                // fast path: wave 0's results
+  __shared__ int32_t s_cpf[(kPlanBlock / 64) * kStageC];  // fast path: each wave's best feature
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const LevelPlan prev = *plan;
@@ -2302,12 +2303,14 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     // Fast path: one candidate per lane of wave 0, which takes every
     // decision below with wave operations and no block barrier; the other
     // waves stage the split candidates and write the tile and task lists.
-    const int32_t E = nc * F_sel;
-    SplitCand cv[kStageC * kStageF / kPlanBlock];
+    // Wave w takes features 4w .. 4w + 3 of candidate `lane` (F_sel <= 64).
+    constexpr int kFw = kStageF / (kPlanBlock / 64);
+    SplitCand cv[kFw];
 #pragma unroll
-    for (int k = 0; k < kStageC * kStageF / kPlanBlock; ++k) {
-      const int32_t e = tid + k * kPlanBlock;
-      cv[k] = e < E ? cand[(int64_t)first * F_sel + e] : SplitCand{0.0, -1, 0};
+    for (int u = 0; u < kFw; ++u) {
+      const int32_t f = wave * kFw + u;
+      cv[u] = (lane < nc && f < F_sel) ? cand[(int64_t)(first + lane) * F_sel + f]
+                                       : SplitCand{0.0, -1, 0};
     }
     const int j = lane;  // wave 0: candidate j, previous parent j, earlier nodes j, j + 64
     NodeSeg sg{0, 0, 0, 0};
@@ -2329,14 +2332,22 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       if (j < first) ke_a = kept_e[j];
       if (j + 64 < first) ke_b = kept_e[j + 64];
     }
+    {
+      // This wave's best over its features (largest gain, first position of
+      // equal gains), for the merge below.
+      double pb = 0.0;
+      int32_t pf = -1, pbin = 0;
 #pragma unroll
-    for (int k = 0; k < kStageC * kStageF / kPlanBlock; ++k) {
-      const int32_t e = tid + k * kPlanBlock;
-      if (e < E) {
-        const int32_t jj = e / F_sel, f = e - jj * F_sel;
-        s_cg[f * kStageC + jj] = cv[k].gain;
-        s_cb[f * kStageC + jj] = (int16_t)cv[k].bin;
+      for (int u = 0; u < kFw; ++u) {
+        if (cv[u].bin >= 0 && (pf < 0 || cv[u].gain > pb)) {
+          pb = cv[u].gain;
+          pf = wave * kFw + u;
+          pbin = cv[u].bin;
+        }
       }
+      s_cg[wave * kStageC + lane] = pb;
+      s_cpf[wave * kStageC + lane] = pf;
+      s_cb[wave * kStageC + lane] = (int16_t)pbin;
     }
     if (wave == 0) {
       if (j < first) s_ke[j] = ke_a;
@@ -2344,29 +2355,27 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     }
     __syncthreads();
     if (wave == 0) {
-      // Best split over the features (largest gain, first position of equal
-      // gains), then the candidate's rank and whether it may be split
-      // (est:649-652, 762-801).
+      // Best split over the features: the waves' bests in feature order
+      // (largest gain, first position of equal gains), then the candidate's
+      // rank and whether it may be split (est:649-652, 762-801).
       const bool is_cand = j < nc;
       double best = 0.0;
       int32_t bf = -1, bb = 0;
       if (is_cand) {
-        for (int32_t f0 = 0; f0 < F_sel; f0 += 8) {
-          double g[8];
-          int32_t b[8];
+        double g[kPlanBlock / 64];
+        int32_t f[kPlanBlock / 64], b[kPlanBlock / 64];
 #pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            const int32_t f = min(f0 + u, kStageF - 1);
-            g[u] = s_cg[f * kStageC + j];
-            b[u] = s_cb[f * kStageC + j];
-          }
+        for (int w = 0; w < kPlanBlock / 64; ++w) {
+          g[w] = s_cg[w * kStageC + j];
+          f[w] = s_cpf[w * kStageC + j];
+          b[w] = s_cb[w * kStageC + j];
+        }
 #pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            if (f0 + u < F_sel && b[u] >= 0 && (bf < 0 || g[u] > best)) {
-              best = g[u];
-              bf = f0 + u;
-              bb = b[u];
-            }
+        for (int w = 0; w < kPlanBlock / 64; ++w) {
+          if (f[w] >= 0 && (bf < 0 || g[w] > best)) {
+            best = g[w];
+            bf = f[w];
+            bb = b[w];
           }
         }
       }
