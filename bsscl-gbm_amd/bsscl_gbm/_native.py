@@ -40,6 +40,12 @@ _SIGS = {
                           _f64, _P, _P, _P, _P, _P, _P, _P, _P],
     "bsscl_boost_get_F": [_P, _P],
     "bsscl_boost_grad_hess": [_P, _P, _P],
+    "bsscl_mc_begin": [_P, _P, _i64, _i32, _P],
+    "bsscl_mc_round": [_P, _P, _i64],
+    "bsscl_mc_build_tree": [_P, _i32, _P, _i32, _i32, _i32, _i32, _f64, _P, _i32, _f64,
+                            _f64, _f64, _P, _P, _P, _P, _P, _P, _P],
+    "bsscl_mc_loss": [_P, _P],
+    "bsscl_mc_get_scores": [_P, _P],
     "bsscl_predict": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _P],
     "bsscl_predict_tree": [_P, _i32, _P, _P, _P, _P, _P, _i32, _P],
     "bsscl_predict_noalloc": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _P],
@@ -67,6 +73,7 @@ _lock = threading.Lock()
 
 
 DEVICE_ROWS = 1  # BSSCL_SAMPLER_DEVICE_ROWS
+MC_DEVICE_MAX_CLASSES = 16  # bsscl_mc_begin's limit
 
 
 class EngineError(RuntimeError):
@@ -244,6 +251,41 @@ class Engine:
             float(gamma), ptr(tf), ptr(tt), ptr(tv), ptr(tl), ptr(tr), ptr(nc),
             ptr(sg)))
         return (tf, tt, tv, tl, tr, int(nc[0]), sg)
+
+    # Multiclass rounds with the scores on the device (include/bsscl_hip.h).
+    def mc_begin(self, y, n_classes, sample_weight):
+        y = np.ascontiguousarray(y, np.int64)
+        w = np.ascontiguousarray(sample_weight, np.float64)
+        check(lib().bsscl_mc_begin(self.handle, ptr(y), len(y), int(n_classes), ptr(w)))
+        self._mc = (len(y), int(n_classes))
+
+    def mc_round(self, sample_indices):
+        si = np.ascontiguousarray(sample_indices, np.int64)
+        check(lib().bsscl_mc_round(self.handle, ptr(si), len(si)))
+
+    def mc_build_tree(self, k, feature_indices, max_leaves, max_depth, min_samples_leaf,
+                      min_child_weight, bin_counts, max_bins, reg_lambda, gamma,
+                      learning_rate):
+        fi = np.ascontiguousarray(feature_indices, np.int32)
+        bc = np.ascontiguousarray(bin_counts, np.int32)
+        tf, tt, tv, tl, tr, nc, sg = self._tree_out(max_leaves)
+        check(lib().bsscl_mc_build_tree(
+            self.handle, int(k), ptr(fi), len(fi), int(max_leaves), int(max_depth),
+            int(min_samples_leaf), float(min_child_weight), ptr(bc), int(max_bins),
+            float(reg_lambda), float(gamma), float(learning_rate), ptr(tf), ptr(tt),
+            ptr(tv), ptr(tl), ptr(tr), ptr(nc), ptr(sg)))
+        return (tf, tt, tv, tl, tr, int(nc[0]), sg)
+
+    def mc_loss(self):
+        out = np.zeros(1, np.float64)
+        check(lib().bsscl_mc_loss(self.handle, ptr(out)))
+        return float(out[0])
+
+    def mc_scores(self):
+        n, K = self._mc
+        out = np.empty((K, n), np.float64)
+        check(lib().bsscl_mc_get_scores(self.handle, ptr(out)))
+        return out.T.copy()
 
     def boost_begin(self, y, w0, w1, base_score):
         y = np.ascontiguousarray(y, np.int64)

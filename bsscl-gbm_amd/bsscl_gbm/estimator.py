@@ -659,8 +659,9 @@ class HybridHistGBMNumbaV1_0_1:
         n_samples = len(y)
         n_features = self.n_features_in_
         K = self.n_classes_
-        y_onehot = np.eye(K, dtype=np.float64)[y]
-        F_train = np.zeros((n_samples, K), dtype=np.float64)
+        on_device = K <= _native.MC_DEVICE_MAX_CLASSES
+        y_onehot = None if on_device else np.eye(K, dtype=np.float64)[y]
+        F_train = None if on_device else np.zeros((n_samples, K), dtype=np.float64)
         F_val = None
         y_val_onehot = None
         if n_val:
@@ -680,25 +681,44 @@ class HybridHistGBMNumbaV1_0_1:
                                   n_sub if do_rows else n_samples, do_rows,
                                   n_features, f_sub if do_feats else n_features,
                                   do_feats, int(self.n_estimators), device=eng.device)
+        # Up to MC_DEVICE_MAX_CLASSES classes the scores, gradients, score
+        # updates and loss stay on the device (the engine's multiclass
+        # rounds); more classes keep the (n, K) arithmetic on the host.
+        if on_device:
+            eng.mc_begin(y, K, sample_weight)
         try:
             for m in range(self.n_estimators):
-                proba = self._softmax(F_train)
-                sample_idx, feat_idx = sampler.next()
-                grad_all = sample_weight[:, None] * (proba - y_onehot)
-                hess_all = sample_weight[:, None] * proba * (1.0 - proba)
-                for k in range(K):
-                    grad_k = np.ascontiguousarray(grad_all[:, k])
-                    hess_k = np.maximum(np.ascontiguousarray(hess_all[:, k]), 1e-8)
-                    tree = eng.build_tree(grad_k, hess_k, sample_idx, feat_idx,
-                                          self.max_leaves, self.max_depth,
-                                          self.min_samples_leaf, self.min_child_weight,
-                                          self.feature_bin_counts, self._max_bins,
-                                          self.reg_lambda, self.gamma)
-                    self.mc_trees[k].append(tree)
-                    F_train[:, k] += self.learning_rate * eng.predict_tree(0, n_samples, tree)
-                    if F_val is not None:
-                        F_val[:, k] += self.learning_rate * eng.predict_tree(1, n_val, tree)
-                train_loss = self._compute_multiclass_logloss(y_onehot, F_train)
+                if on_device:
+                    sample_idx, feat_idx = sampler.next()
+                    eng.mc_round(sample_idx)
+                    for k in range(K):
+                        tree = eng.mc_build_tree(k, feat_idx, self.max_leaves, self.max_depth,
+                                                 self.min_samples_leaf, self.min_child_weight,
+                                                 self.feature_bin_counts, self._max_bins,
+                                                 self.reg_lambda, self.gamma,
+                                                 self.learning_rate)
+                        self.mc_trees[k].append(tree)
+                        if F_val is not None:
+                            F_val[:, k] += self.learning_rate * eng.predict_tree(1, n_val, tree)
+                    train_loss = eng.mc_loss()
+                else:
+                    proba = self._softmax(F_train)
+                    sample_idx, feat_idx = sampler.next()
+                    grad_all = sample_weight[:, None] * (proba - y_onehot)
+                    hess_all = sample_weight[:, None] * proba * (1.0 - proba)
+                    for k in range(K):
+                        grad_k = np.ascontiguousarray(grad_all[:, k])
+                        hess_k = np.maximum(np.ascontiguousarray(hess_all[:, k]), 1e-8)
+                        tree = eng.build_tree(grad_k, hess_k, sample_idx, feat_idx,
+                                              self.max_leaves, self.max_depth,
+                                              self.min_samples_leaf, self.min_child_weight,
+                                              self.feature_bin_counts, self._max_bins,
+                                              self.reg_lambda, self.gamma)
+                        self.mc_trees[k].append(tree)
+                        F_train[:, k] += self.learning_rate * eng.predict_tree(0, n_samples, tree)
+                        if F_val is not None:
+                            F_val[:, k] += self.learning_rate * eng.predict_tree(1, n_val, tree)
+                    train_loss = self._compute_multiclass_logloss(y_onehot, F_train)
                 self.train_loss_history_.append(train_loss)
                 val_loss = None
                 if F_val is not None:

@@ -269,6 +269,15 @@ struct bsscl_engine {
   DevBuf<double> g64, h64;
   double g_scale = 1.0, h_scale = 1.0;  // fixed point -> value
 
+  // Multiclass run on matrix 0: scores, gradients and hessians [K][n], the
+  // rows' class and weight, each class's largest |g| and h of the round.
+  int32_t mc_K = 0;
+  int64_t mc_m = 0;  // the round's in-bag rows (rows64)
+  DevBuf<double> mc_F, mc_G, mc_H, mc_w, mc_part;
+  DevBuf<int32_t> mc_y;
+  DevBuf<unsigned long long> mc_max;
+  std::vector<double> mc_gm, mc_hm;  // fixed-point multipliers per class
+
   // Tree workspace.
   // Compact row sets: a tree uses sets set_base and set_base + 1 (levels
   // alternate); a boosting round in slot s uses base 2s, so the next round's
@@ -2470,6 +2479,140 @@ int bsscl_boost_set_pipeline(bsscl_engine *E, int32_t on) {
     CHK(drain_rounds(E, p));
   }
   E->pipeline = on != 0;
+  return BSSCL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Multiclass rounds (est:2949-3065) with the scores on the device.
+// ---------------------------------------------------------------------------
+int bsscl_mc_begin(bsscl_engine *E, const int64_t *y, int64_t n, int32_t n_classes,
+                   const double *sample_weight) {
+  if (!E || !y || !sample_weight) return set_error(BSSCL_EINVAL, "mc_begin: null argument");
+  CHK(check_matrix(E, 0));
+  if (n != E->mat[0].n) return set_error(BSSCL_EINVAL, "mc_begin: y length differs from matrix rows");
+  if (n_classes < 2 || n_classes > kMcMaxK)
+    return set_error(BSSCL_EINVAL, "mc_begin: between 2 and " + std::to_string(kMcMaxK) + " classes");
+  std::vector<int32_t> yi((size_t)n);
+  for (int64_t i = 0; i < n; ++i) {
+    if (y[i] < 0 || y[i] >= n_classes) return set_error(BSSCL_EINVAL, "mc_begin: label out of range");
+    if (!(sample_weight[i] > 0.0) || !std::isfinite(sample_weight[i]))
+      return set_error(BSSCL_EINVAL, "mc_begin: sample weights must be positive");
+    yi[(size_t)i] = (int32_t)y[i];
+  }
+  HIPCHK(hipSetDevice(E->device));
+  const size_t nk = (size_t)n * (size_t)n_classes;
+  CHK(E->mc_F.ensure(nk));
+  CHK(E->mc_G.ensure(nk));
+  CHK(E->mc_H.ensure(nk));
+  CHK(E->mc_w.ensure((size_t)n));
+  CHK(E->mc_y.ensure((size_t)n));
+  CHK(E->mc_max.ensure(2 * (size_t)kMcMaxK));
+  CHK(E->mc_part.ensure((size_t)mc_loss_blocks(n)));
+  CHK(E->ghq.ensure((size_t)n));
+  HIPCHK(hipMemcpyAsync(E->mc_y.p, yi.data(), (size_t)n * 4, hipMemcpyHostToDevice, E->st));
+  HIPCHK(hipMemcpyAsync(E->mc_w.p, sample_weight, (size_t)n * 8, hipMemcpyHostToDevice, E->st));
+  HIPCHK(hipMemsetAsync(E->mc_F.p, 0, nk * 8, E->st));  // the reference starts from 0 (est:2950)
+  HIPCHK(hipStreamSynchronize(E->st));
+  E->mc_K = n_classes;
+  E->mc_m = 0;
+  return BSSCL_OK;
+}
+
+int bsscl_mc_round(bsscl_engine *E, const int64_t *sample_indices, int64_t n_samples) {
+  if (!E || !sample_indices) return set_error(BSSCL_EINVAL, "mc_round: null argument");
+  if (E->mc_K < 2) return set_error(BSSCL_EINVAL, "mc_round: no multiclass run");
+  CHK(check_matrix(E, 0));
+  const int64_t n = E->mat[0].n;
+  if (n_samples <= 0) return set_error(BSSCL_EINVAL, "mc_round: no samples");
+  for (int64_t k = 0; k < n_samples; ++k)
+    if (sample_indices[k] < 0 || sample_indices[k] >= n)
+      return set_error(BSSCL_EINVAL, "mc_round: sample index out of range");
+  HIPCHK(hipSetDevice(E->device));
+  const int32_t K = E->mc_K;
+  CHK(E->rows64.ensure((size_t)n_samples));
+  HIPCHK(hipMemcpyAsync(E->rows64.p, sample_indices, (size_t)n_samples * 8,
+                        hipMemcpyHostToDevice, E->st));
+  HIPCHK(hipMemsetAsync(E->mc_max.p, 0, 2 * (size_t)K * 8, E->st));
+  HIPCHK(launch_mc_grad_hess(E->st, E->mc_F.p, E->mc_y.p, E->mc_w.p, n, K, E->mc_G.p, E->mc_H.p,
+                             E->mc_max.p));
+  unsigned long long mx[2 * kMcMaxK];
+  HIPCHK(hipMemcpyAsync(mx, E->mc_max.p, 2 * (size_t)K * 8, hipMemcpyDeviceToHost, E->st));
+  HIPCHK(hipStreamSynchronize(E->st));
+  E->mc_gm.assign((size_t)K, 0.0);
+  E->mc_hm.assign((size_t)K, 0.0);
+  for (int32_t k = 0; k < K; ++k) {
+    double gmax, hmax;
+    std::memcpy(&gmax, &mx[2 * k], 8);
+    std::memcpy(&hmax, &mx[2 * k + 1], 8);
+    if (!std::isfinite(gmax) || !std::isfinite(hmax))
+      return set_error(BSSCL_EINVAL, "mc_round: gradients are not finite");
+    // The scale load_grad_hess would take from the same arrays.
+    E->mc_gm[(size_t)k] = fixed_mul(gmax, n_samples);
+    E->mc_hm[(size_t)k] = fixed_mul(hmax, n_samples);
+  }
+  E->mc_m = n_samples;
+  return BSSCL_OK;
+}
+
+int bsscl_mc_build_tree(bsscl_engine *E, int32_t k, const int32_t *feature_indices,
+                        int32_t n_selected, int32_t max_leaves, int32_t max_depth,
+                        int32_t min_samples_leaf, double min_child_weight,
+                        const int32_t *bin_counts, int32_t max_bins, double reg_lambda,
+                        double gamma, double learning_rate, int32_t *out_features,
+                        int64_t *out_thresholds, double *out_values, int32_t *out_left,
+                        int32_t *out_right, int32_t *out_node_count, double *out_split_gains) {
+  if (!E) return set_error(BSSCL_EINVAL, "mc_build_tree: null argument");
+  if (E->mc_K < 2 || E->mc_m <= 0) return set_error(BSSCL_EINVAL, "mc_build_tree: no round");
+  if (k < 0 || k >= E->mc_K) return set_error(BSSCL_EINVAL, "mc_build_tree: class out of range");
+  CHK(check_matrix(E, 0));
+  (void)max_bins;
+  const Matrix &X = E->mat[0];
+  const int64_t n = X.n;
+  TreeOut out{out_features, out_thresholds, out_values, out_left, out_right,
+              out_node_count, out_split_gains};
+  std::vector<int32_t> feats, nb_sel;
+  HIPCHK(hipSetDevice(E->device));
+  CHK(validate_tree_args(E, feature_indices, n_selected, max_leaves,
+                         min_samples_leaf, bin_counts, out, feats, nb_sel));
+  const double gm = E->mc_gm[(size_t)k], hm = E->mc_hm[(size_t)k];
+  E->g_scale = 1.0 / gm;
+  E->h_scale = 1.0 / hm;
+  HIPCHK(launch_quantize(E->st, E->mc_G.p + (size_t)k * n, E->mc_H.p + (size_t)k * n, n, gm, hm,
+                         E->ghq.p));
+  TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight, reg_lambda, gamma};
+  E->set_base = 0;
+  CHK(build_tree_core(E, nullptr, E->mc_m, feats, nb_sel, tp, out));
+  // F[:, k] += lr * tree(X) (est:2977), with the tree in the engine's columns.
+  CHK(upload_tree(E, out.features, out.thresholds, out.values, out.left, out.right,
+                  *out.node_count, X.cols()));
+  HIPCHK(launch_mc_apply(E->st, X.codes.p, X.ld, n, E->tree_d.p, learning_rate,
+                         E->mc_F.p + (size_t)k * n));
+  tree_to_reference(X, out);
+  return BSSCL_OK;
+}
+
+int bsscl_mc_loss(bsscl_engine *E, double *out_loss) {
+  if (!E || !out_loss) return set_error(BSSCL_EINVAL, "mc_loss: null argument");
+  if (E->mc_K < 2) return set_error(BSSCL_EINVAL, "mc_loss: no multiclass run");
+  HIPCHK(hipSetDevice(E->device));
+  const int64_t n = E->mat[0].n, nb = mc_loss_blocks(n);
+  HIPCHK(launch_mc_loss(E->st, E->mc_F.p, E->mc_y.p, n, E->mc_K, E->mc_part.p));
+  std::vector<double> part((size_t)nb);
+  HIPCHK(hipMemcpyAsync(part.data(), E->mc_part.p, (size_t)nb * 8, hipMemcpyDeviceToHost, E->st));
+  HIPCHK(hipStreamSynchronize(E->st));
+  double acc = 0.0;
+  for (double v : part) acc += v;
+  *out_loss = -(acc / (double)n);
+  return BSSCL_OK;
+}
+
+int bsscl_mc_get_scores(bsscl_engine *E, double *out) {
+  if (!E || !out) return set_error(BSSCL_EINVAL, "mc_get_scores: null argument");
+  if (E->mc_K < 2) return set_error(BSSCL_EINVAL, "mc_get_scores: no multiclass run");
+  HIPCHK(hipSetDevice(E->device));
+  const size_t nk = (size_t)E->mat[0].n * (size_t)E->mc_K;
+  HIPCHK(hipMemcpyAsync(out, E->mc_F.p, nk * 8, hipMemcpyDeviceToHost, E->st));
+  HIPCHK(hipStreamSynchronize(E->st));
   return BSSCL_OK;
 }
 

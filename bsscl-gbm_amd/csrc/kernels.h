@@ -355,6 +355,17 @@ hipError_t launch_replay(hipStream_t st, const NodeOut *nodes, const LevelPlan *
                          TreeNodeDev *tree, RoundHeader *hdr);
 hipError_t launch_sum_partials(hipStream_t st, const double *partials,
                                int32_t count, double *out);
+// Multiclass rounds: scores, gradients and hessians as [K][n] float64, for
+// 2 <= K <= kMcMaxK classes.
+constexpr int kMcMaxK = 16;
+hipError_t launch_mc_grad_hess(hipStream_t st, const double *F, const int32_t *y, const double *w,
+                               int64_t n, int32_t K, double *G, double *H,
+                               unsigned long long *mx);
+hipError_t launch_mc_apply(hipStream_t st, const uint8_t *codes, int64_t ld, int64_t n,
+                           const TreeNodeDev *tree, double lr, double *Fk);
+int64_t mc_loss_blocks(int64_t n);
+hipError_t launch_mc_loss(hipStream_t st, const double *F, const int32_t *y, int64_t n,
+                          int32_t K, double *partials);
 hipError_t launch_predict_tree(hipStream_t st, const uint8_t *codes,
                                int64_t ld, int64_t n, const TreeNodeDev *tree,
                                int32_t node_count, double *out);

@@ -3971,4 +3971,157 @@ hipError_t launch_predict(hipStream_t st, const uint8_t *codes, int64_t ld,
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Multiclass rounds (est:2949-3065).  Scores F are [K][n] float64, class k's
+// gradients G[k][i] and hessians H[k][i] likewise.  A row's softmax follows
+// the reference's NumPy order: F - max over the classes, exp, the sum over
+// the classes in class order, then one division per class.
+// ---------------------------------------------------------------------------
+#pragma clang fp contract(off)
+namespace {
+
+// Order-preserving bits of a non-negative double.
+__device__ __forceinline__ unsigned long long nonneg_bits(double v) {
+  return (unsigned long long)__double_as_longlong(v);
+}
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const unsigned long long t = __shfl_xor(v, o, 64);
+    v = t > v ? t : v;
+  }
+  return v;
+}
+
+}  // namespace
+
+// grad_all = w * (p - onehot), hess_all = w * p * (1 - p) floored at 1e-8
+// (est:2966-2972); mx[2k], mx[2k + 1] collect the largest |g| and h of class
+// k over the rows (the fixed-point scale of its tree).
+__global__ __launch_bounds__(256) void k_mc_grad_hess(
+    const double *__restrict__ F, const int32_t *__restrict__ y, const double *__restrict__ w,
+    int64_t n, int32_t K, double *__restrict__ G, double *__restrict__ H,
+    unsigned long long *__restrict__ mx) {
+  __shared__ unsigned long long red[2 * kMcMaxK][256 / 64];
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const bool in = i < n;
+  double e[kMcMaxK];
+  double fmaxv = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kMcMaxK; ++k) {
+    e[k] = (in && k < K) ? F[(int64_t)k * n + i] : 0.0;
+    if (k < K) fmaxv = fmax(fmaxv, e[k]);
+  }
+  double sum = 0.0;
+#pragma unroll
+  for (int k = 0; k < kMcMaxK; ++k) {
+    if (k < K) {
+      e[k] = exp(__dsub_rn(e[k], fmaxv));
+      sum = __dadd_rn(sum, e[k]);
+    }
+  }
+  const double wi = in ? w[i] : 0.0;
+  const int32_t yi = in ? y[i] : -1;
+#pragma unroll
+  for (int k = 0; k < kMcMaxK; ++k) {
+    if (k >= K) continue;  // (uniform)
+    const double p = __ddiv_rn(e[k], sum);
+    const double g = __dmul_rn(wi, __dsub_rn(p, yi == k ? 1.0 : 0.0));
+    const double h = fmax(__dmul_rn(__dmul_rn(wi, p), __dsub_rn(1.0, p)), 1e-8);
+    if (in) {
+      G[(int64_t)k * n + i] = g;
+      H[(int64_t)k * n + i] = h;
+    }
+    const unsigned long long gm = wave_max_u64(in ? nonneg_bits(fabs(g)) : 0ull);
+    const unsigned long long hm = wave_max_u64(in ? nonneg_bits(h) : 0ull);
+    if ((threadIdx.x & 63) == 0) {
+      red[2 * k][threadIdx.x >> 6] = gm;
+      red[2 * k + 1][threadIdx.x >> 6] = hm;
+    }
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < 2 * K) {
+    unsigned long long m = 0ull;
+#pragma unroll
+    for (int q = 0; q < 256 / 64; ++q) m = red[threadIdx.x][q] > m ? red[threadIdx.x][q] : m;
+    atomicMax(mx + threadIdx.x, m);
+  }
+}
+
+// F[i] += lr * tree(x_i) for one class's scores (est:2977).
+__global__ __launch_bounds__(256) void k_mc_apply(const uint8_t *__restrict__ codes, int64_t ld,
+                                                  int64_t n, const TreeNodeDev *__restrict__ tree,
+                                                  double lr, double *__restrict__ Fk) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  Fk[i] = __dadd_rn(Fk[i], __dmul_rn(lr, tree[traverse(tree, codes, ld, i)].value));
+}
+
+// Per block: the sum of log(clip(softmax(F_i))[y_i], 1e-15, 1 - 1e-15)
+// over its rows (est:2320-2325's multiclass form, est:2982).
+__global__ __launch_bounds__(256) void k_mc_loss(const double *__restrict__ F,
+                                                 const int32_t *__restrict__ y, int64_t n,
+                                                 int32_t K, double *__restrict__ partials) {
+  __shared__ double red[256 / 64];
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  double v = 0.0;
+  if (i < n) {
+    double e[kMcMaxK];
+    double fmaxv = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kMcMaxK; ++k) {
+      e[k] = k < K ? F[(int64_t)k * n + i] : 0.0;
+      if (k < K) fmaxv = fmax(fmaxv, e[k]);
+    }
+    double sum = 0.0, ey = 0.0;
+    const int32_t yi = y[i];
+#pragma unroll
+    for (int k = 0; k < kMcMaxK; ++k) {
+      if (k < K) {
+        e[k] = exp(__dsub_rn(e[k], fmaxv));
+        sum = __dadd_rn(sum, e[k]);
+        if (k == yi) ey = e[k];
+      }
+    }
+    const double p = fmin(fmax(__ddiv_rn(ey, sum), 1e-15), 1.0 - 1e-15);
+    v = log(p);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) partials[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+#pragma clang fp contract(on)
+
+hipError_t launch_mc_grad_hess(hipStream_t st, const double *F, const int32_t *y, const double *w,
+                               int64_t n, int32_t K, double *G, double *H,
+                               unsigned long long *mx) {
+  if (n <= 0) return hipSuccess;
+  if (K < 2 || K > kMcMaxK) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_mc_grad_hess, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, F, y,
+                     w, n, K, G, H, mx);
+  return hipGetLastError();
+}
+
+hipError_t launch_mc_apply(hipStream_t st, const uint8_t *codes, int64_t ld, int64_t n,
+                           const TreeNodeDev *tree, double lr, double *Fk) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_mc_apply, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, codes, ld,
+                     n, tree, lr, Fk);
+  return hipGetLastError();
+}
+
+int64_t mc_loss_blocks(int64_t n) { return (n + 255) / 256; }
+
+hipError_t launch_mc_loss(hipStream_t st, const double *F, const int32_t *y, int64_t n,
+                          int32_t K, double *partials) {
+  if (n <= 0) return hipSuccess;
+  if (K < 2 || K > kMcMaxK) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_mc_loss, dim3((unsigned)mc_loss_blocks(n)), dim3(256), 0, st, F, y, n, K,
+                     partials);
+  return hipGetLastError();
+}
+
 }  // namespace bsscl

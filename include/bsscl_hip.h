@@ -185,6 +185,38 @@ int bsscl_boost_grad_hess(bsscl_engine *eng, double *grad_out,
                           double *hess_out);
 
 /*
+ * Multiclass rounds with the scores on the device.  Replace the NumPy
+ * arithmetic of the reference's multiclass loop (est:2949-3065): the (n, K)
+ * score matrix starting at 0 (est:2950), each round's softmax gradients and
+ * hessians from the scores at the round's start (est:2962-2972, hessians
+ * floored at 1e-8), each class's tree (the _build_tree_leafwise seam on those
+ * gradients, est:2973-2976) and its score update F[:, k] += lr * tree (est:2977),
+ * and the round's multiclass log-loss (est:2982).  Runs on training matrix 0.
+ *   mc_begin       y int64[n] in [0, n_classes), sample_weight float64[n] > 0,
+ *                  2 <= n_classes <= 16
+ *   mc_round       the round's in-bag rows (int64[n_samples], shared by its
+ *                  K trees); computes every class's gradients and hessians
+ *   mc_build_tree  class k's tree from the round's rows and the features
+ *                  (arguments and outputs as bsscl_build_tree), then adds
+ *                  learning_rate * tree to class k's scores
+ *   mc_loss        -mean log(clip(softmax(F)[y], 1e-15, 1 - 1e-15))
+ *   mc_get_scores  F as float64[n_classes * n], class by class (row i of
+ *                  class k at k * n + i)
+ */
+int bsscl_mc_begin(bsscl_engine *eng, const int64_t *y, int64_t n, int32_t n_classes,
+                   const double *sample_weight);
+int bsscl_mc_round(bsscl_engine *eng, const int64_t *sample_indices, int64_t n_samples);
+int bsscl_mc_build_tree(bsscl_engine *eng, int32_t k, const int32_t *feature_indices,
+                        int32_t n_selected, int32_t max_leaves, int32_t max_depth,
+                        int32_t min_samples_leaf, double min_child_weight,
+                        const int32_t *bin_counts, int32_t max_bins, double reg_lambda,
+                        double gamma, double learning_rate, int32_t *out_features,
+                        int64_t *out_thresholds, double *out_values, int32_t *out_left,
+                        int32_t *out_right, int32_t *out_node_count, double *out_split_gains);
+int bsscl_mc_loss(bsscl_engine *eng, double *out_loss);
+int bsscl_mc_get_scores(bsscl_engine *eng, double *out);
+
+/*
  * Ensemble prediction.  Replaces predict_all_trees_jit (est:863-884):
  * out_F[i] = sum over trees t of learning_rate * value_t(leaf of row i),
  * accumulated tree by tree from 0.0, on the rows of matrix `slot`.  The tree

@@ -107,3 +107,21 @@ def test_multiclass_lockstep_and_end_to_end(engine, K, n, nan):
     Xp, _ = _mc_data(3000, 9, K, seed=100 + K, nan_frac=nan)
     fitcmp.assert_fit_equal(ref, est, Xp)
     np.testing.assert_array_equal(est.predict(Xp), ref.predict(Xp))
+
+
+@pytest.mark.gpu
+def test_multiclass_host_path_matches_oracle(engine, monkeypatch):
+    """More classes than the device rounds take keep the (n, K) arithmetic
+    on the host (est:2949-3065 in NumPy, each tree through the builder seam);
+    forced here for K = 3, that path too follows the oracle."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1, _native
+    print("[case] multiclass host path K=3", flush=True)
+    monkeypatch.setattr(_native, "MC_DEVICE_MAX_CLASSES", 0)
+    X, y = _mc_data(6000, 9, 3, seed=3)
+    params = dict(n_estimators=4, max_depth=5, n_bins=255, random_state=5)
+    est = HybridHistGBMNumbaV1_0_1(verbose=False, **params).fit(X, y)
+    ref, rep = fitcmp.follow_fit(engine, est, X, y, params)
+    print(rep.line("multiclass host path K=3"), flush=True)
+    assert rep.rounds == params["n_estimators"]
+    Xp, _ = _mc_data(3000, 9, 3, seed=103)
+    fitcmp.assert_fit_equal(ref, est, Xp)
