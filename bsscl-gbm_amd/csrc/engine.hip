@@ -183,6 +183,7 @@ struct RoundArgs {
 struct RoundSlot {
   bool active = false;
   bool device_replay = true;
+  bool table_readback = false;  // the node table comes back for tree_stats
   bsscl_sampler *sampler = nullptr;
   void *token = nullptr;
   RoundArgs args;
@@ -1366,23 +1367,30 @@ int32_t table_bound(bsscl_engine *E, int32_t run) {
 // Profiling counters of one built tree from its node table: histogram
 // rows x features and algorithmic bytes (the root and the smaller child of
 // every kept split above the last level), nodes expanded, trees.
+// `small_rows` sums the smaller child's rows over those splits, `expanded`
+// counts the nodes with children.
+void tree_stats_add(bsscl_engine *E, int64_t m, int32_t F_sel, int64_t small_rows,
+                    int32_t expanded) {
+  E->stats[2] += (double)(m + small_rows) * F_sel;
+  E->stats[3] += (double)(m + small_rows) * (F_sel + 8);
+  E->stats[9] += (double)expanded;
+  E->stats[8] += 1.0;
+}
+
 void tree_stats(bsscl_engine *E, const NodeOut *t, int32_t n, int64_t m, int32_t F_sel,
                 const TreeParams &tp) {
   std::vector<int32_t> depth((size_t)n, 0);
-  E->stats[2] += (double)m * F_sel;
-  E->stats[3] += (double)m * (F_sel + 8);
+  int64_t small_rows = 0;
+  int32_t expanded = 0;
   for (int32_t i = 0; i < n; ++i) {
     const int32_t l = t[i].left;
     if (l < 0 || l + 1 >= n) continue;
     depth[(size_t)l] = depth[(size_t)l + 1] = depth[(size_t)i] + 1;
-    E->stats[9] += 1.0;
-    if (t[l].valid && depth[(size_t)i] + 1 < tp.max_depth) {
-      const int64_t ms = std::min(t[l].count, t[l + 1].count);
-      E->stats[2] += (double)ms * F_sel;
-      E->stats[3] += (double)ms * (F_sel + 8);
-    }
+    ++expanded;
+    if (t[l].valid && depth[(size_t)i] + 1 < tp.max_depth)
+      small_rows += std::min(t[l].count, t[l + 1].count);
   }
-  E->stats[8] += 1.0;
+  tree_stats_add(E, m, F_sel, small_rows, expanded);
 }
 
 // Builds one tree from the rows already in rows32 (device, int32) or, when
@@ -1672,6 +1680,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   // (Test hook: BSSCL_TEST_HOST_REPLAY=1 forces the host path.)
   const char *force_host = std::getenv("BSSCL_TEST_HOST_REPLAY");
   R.device_replay = a.max_leaves + 2 <= kReplaySlots && !(force_host && force_host[0] == '1');
+  R.table_readback = false;
   // The tree's compact row sets: 2s and 2s + 1.
   E->set_base = 2 * s;
   if (rc == BSSCL_OK && R.device_replay)
@@ -1813,6 +1822,9 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     const char *rg = std::getenv("BSSCL_TEST_REPLAY_GLOBAL");
     ra.stage_limit = !rg ? (1 << 30) : rg[0] == '1' ? 0 : rg[0] == '2' ? 1023 : (1 << 30);
     ra.node_cap = E->node_cap;
+    ra.max_depth = a.max_depth;
+    ra.pad = 0;
+    R.table_readback = E->prof && !replay_counts_nodes(ra);
     hipError_t e = launch_replay(E->st, E->nodes_d, E->plan_d, E->feat_d, ra,
                                  round_arrays(E->round_d[s].p, R.M), E->tree_d.p, hdr);
     // The per-block losses follow the tree; the host sums them
@@ -1824,7 +1836,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     if (e == hipSuccess)
       e = hipMemcpyAsync(E->round_pin[s], E->round_d[s].p,
                          round_out_bytes(R.M) + (size_t)nb * 8, hipMemcpyDeviceToHost, E->st);
-    if (e == hipSuccess && E->prof)
+    if (e == hipSuccess && R.table_readback)
       e = hipMemcpyAsync(E->rtable_pin[s], E->table_d.p,
                          64 + (size_t)table_bound(E, R.run) * sizeof(NodeOut),
                          hipMemcpyDeviceToHost, E->st);
@@ -1868,7 +1880,9 @@ int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
     h.status = 4;
   }
   if (h.status == 0) {
-    if (E->prof) {
+    if (E->prof && h.expanded >= 0) {
+      tree_stats_add(E, R.m, (int32_t)R.feats.size(), h.hist_rows, h.expanded);
+    } else if (R.table_readback) {
       const LevelPlan *pl = reinterpret_cast<const LevelPlan *>(E->rtable_pin[s]);
       const int32_t tb = table_bound(E, R.run);
       if (pl->overflow == 0 && pl->n_nodes >= 1 && pl->n_nodes <= tb)

@@ -164,9 +164,15 @@ struct RoundHeader {
                        // 3 no free candidate slot; 4 too many leaves for the
                        // device replay; 5 level lists overflowed
   int32_t needed;
-  int32_t pad;
+  // Profiling counts of the node table, from the in-LDS replay
+  // (k_replay_tree): nodes with children, and the rows of the smaller child
+  // of every kept split whose children are above max_depth (the rows the
+  // level loop histogrammed besides the root's).  expanded is -1 when the
+  // replay did not count them (k_replay).
+  int32_t expanded;
   double loss_sum;     // sum over rows of y log p + (1-y) log(1-p)
-  double pad2[5];
+  int64_t hist_rows;
+  double pad2[4];
 };
 
 struct ReplayArgs {
@@ -178,6 +184,8 @@ struct ReplayArgs {
   int32_t out_len;     // 2 * max_leaves + 2 entries per output array
   int32_t stage_limit; // node records are staged in LDS up to this many nodes
   int32_t node_cap;    // node table capacity of the tree
+  int32_t max_depth;   // for the profiling counts in RoundHeader
+  int32_t pad;
 };
 
 // Output arrays of the replayed tree (the reference's 7-tuple layout).
@@ -353,6 +361,9 @@ hipError_t launch_update_F(hipStream_t st, const uint8_t *codes, int64_t ld,
 hipError_t launch_replay(hipStream_t st, const NodeOut *nodes, const LevelPlan *plan,
                          const int32_t *feats, ReplayArgs a, TreeArrays out,
                          TreeNodeDev *tree, RoundHeader *hdr);
+// Whether launch_replay takes the in-LDS form, which also fills
+// hdr->expanded and hdr->hist_rows.
+bool replay_counts_nodes(const ReplayArgs &a);
 hipError_t launch_sum_partials(hipStream_t st, const double *partials,
                                int32_t count, double *out);
 // Multiclass rounds: scores, gradients and hessians as [K][n] float64, for

@@ -3366,6 +3366,8 @@ __global__ __launch_bounds__(64) void k_replay(
     hdr->node_count = status == 0 ? node_count : 0;
     hdr->status = status;
     hdr->needed = needed;
+    hdr->expanded = -1;
+    hdr->hist_rows = 0;
   }
 }
 
@@ -3525,6 +3527,9 @@ __global__ __launch_bounds__(kTreeBlock) void k_replay_tree(
     const int32_t *__restrict__ feats, ReplayArgs a, TreeArrays out,
     TreeNodeDev *__restrict__ tree, RoundHeader *__restrict__ hdr) {
   __shared__ uint32_t stmp[kTreeBlock / 64];
+  __shared__ long long s_hist_rows[kTreeBlock / 64];
+  __shared__ int32_t s_expanded[kTreeBlock / 64];
+  static_assert(kReplayNodes <= kTreeBlock, "one node per thread");
   const int tid = (int)threadIdx.x, wave = tid >> 6;
   const int32_t M = a.out_len;
   const int32_t C = a.max_leaves + 2;
@@ -3559,10 +3564,16 @@ __global__ __launch_bounds__(kTreeBlock) void k_replay_tree(
     }
     if (tid < 4) rt_flags[tid] = 0;
     __syncthreads();
+    // Profiling counts (one node per thread): the smaller child's rows of a
+    // kept split, added below when the children are above max_depth.
+    long long small_rows = -1;
+    int32_t expanded = 0;
     for (int32_t v = tid; v < n; v += kTreeBlock) {
       const int32_t l = lft[v];
       int32_t c = -1;
       if (l >= 0) {
+        expanded = 1;
+        if (vld[l]) small_rows = min(cnt[l], cnt[l + 1]);
         c = l | (vld[l] ? kKept : 0) | (cnt[l] <= cnt[l + 1] ? kLeftSmall : 0);
         rt_parent[l] = (int16_t)v;
         rt_parent[l + 1] = (int16_t)v;
@@ -3589,6 +3600,21 @@ __global__ __launch_bounds__(kTreeBlock) void k_replay_tree(
       rt_pc[v] = pc ? 1 : 0;
       rt_depth[v] = (uint8_t)min(d, 255);
       gc[v] = pc ? rt_G[v] : __longlong_as_double(0x7ff8000000000000ll);
+      // The full depth for the counts (parents have lower ids: the walk ends).
+      int32_t depth = d;
+      while (depth > kTreeMaxDepth && u != 0 && rt_parent[u] >= 0) {
+        u = rt_parent[u];
+        ++depth;
+      }
+      if (depth + 1 >= a.max_depth) small_rows = -1;
+    }
+    {
+      const long long hr = wave_sum(small_rows > 0 ? small_rows : 0ll);
+      const int32_t ex = wave_sum(expanded);
+      if ((tid & 63) == 0) {
+        s_hist_rows[wave] = hr;
+        s_expanded[wave] = ex;
+      }
     }
     __syncthreads();
     // Key ranks among the candidates; equal keys need the slot loop.
@@ -3725,14 +3751,29 @@ __global__ __launch_bounds__(kTreeBlock) void k_replay_tree(
     hdr->node_count = status == 0 ? node_count : 0;
     hdr->status = status;
     hdr->needed = needed;
+    long long hr = 0;
+    int32_t ex = 0;
+    if (status == 0) {
+      for (int w = 0; w < kTreeBlock / 64; ++w) {
+        hr += s_hist_rows[w];
+        ex += s_expanded[w];
+      }
+    }
+    hdr->expanded = status == 0 ? ex : -1;
+    hdr->hist_rows = hr;
   }
+}
+
+bool replay_counts_nodes(const ReplayArgs &a) {
+  return a.max_leaves + 2 <= kRegSlots && a.stage_limit >= kReplayNodes &&
+         a.node_cap <= kReplayNodes;
 }
 
 hipError_t launch_replay(hipStream_t st, const NodeOut *nodes, const LevelPlan *plan,
                          const int32_t *feats, ReplayArgs a, TreeArrays out,
                          TreeNodeDev *tree, RoundHeader *hdr) {
   // Up to 128 candidate slots when every node fits in LDS: the order form.
-  if (a.max_leaves + 2 <= kRegSlots && a.stage_limit >= kReplayNodes && a.node_cap <= kReplayNodes)
+  if (replay_counts_nodes(a))
     hipLaunchKernelGGL(k_replay_tree, dim3(1), dim3(kTreeBlock), 0, st, nodes, plan, feats, a,
                        out, tree, hdr);
   else

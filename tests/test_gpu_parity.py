@@ -390,6 +390,38 @@ def test_fit_lockstep_and_end_to_end(engine, name):
             assert at255 > 0
 
 
+def test_profiling_counts_agree(engine, monkeypatch):
+    """The node-table counts behind the histogram roofline (rows x features
+    histogrammed, bytes, nodes expanded), taken by the in-LDS replay kernel,
+    equal those the host takes from the node table read back after the
+    other replay form, and include every round's root."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    from bsscl_gbm import estimator as est_mod
+    X, y, params = _fit_case("nan_imbalanced")
+    params = dict(params, n_estimators=6)
+    eng = est_mod._engine(0)
+    got = {}
+    for mode, env in [("lds", {}), ("table", {"BSSCL_TEST_REPLAY_GLOBAL": "1"})]:
+        _announce(f"profiling counts, replay {mode}")
+        monkeypatch.delenv("BSSCL_TEST_REPLAY_GLOBAL", raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        est = HybridHistGBMNumbaV1_0_1(verbose=False, **params)
+        eng.set_profiling(1)
+        try:
+            est.fit(X, y)
+            st = eng.stats()
+        finally:
+            eng.set_profiling(0)
+        got[mode] = {k: st[k] for k in ("hist_row_features", "hist_bytes", "nodes_expanded",
+                                        "trees")}
+    monkeypatch.delenv("BSSCL_TEST_REPLAY_GLOBAL", raising=False)
+    print(f"[result] profiling counts {got['lds']}", flush=True)
+    assert got["lds"] == got["table"]
+    assert got["lds"]["trees"] == 6
+    assert got["lds"]["hist_row_features"] > 0 and got["lds"]["nodes_expanded"] >= 6
+
+
 def test_fit_device_replay_fallbacks_agree(engine, monkeypatch):
     """The round's device replay (pipelined and not), the host replay
     (forced), the path that regrows a too-small node table, the general
