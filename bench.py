@@ -123,33 +123,42 @@ def measured_traffic(kernel, workload):
 
 
 def run_gpu(name, steps, warmup, rounds_only=False):
-    """Fits warmup + steps + BREAKDOWN_ROUNDS rounds.  The timed rounds run
-    with the histogram kernel's own clock stamps only (level 1: no event
-    packets between the tree's kernels); the last rounds, after the timed
-    region, time every kernel group with HIP events (level 2) for the
-    per-kernel breakdown."""
+    """Fits warmup + 2 * steps + BREAKDOWN_ROUNDS rounds.  The timed rounds
+    run as the library runs by default: unprofiled, each round's rows-stream
+    kernels replayed from a captured HIP graph.  The next `steps` rounds of the same
+    fit run at profiling level 1, where the histogram kernel stamps each
+    block's start and end on the device's constant-rate clock (no event
+    packets between the tree's kernels; the kernels are launched one by
+    one), for the kernel's timing; the last rounds time every kernel group
+    with HIP events (level 2) for the per-kernel breakdown.  Host times
+    (enqueue, waits) are kept at every level and taken over the timed
+    rounds."""
     from bsscl_gbm import HybridHistGBMNumbaV1_0_1
     X, y, params = make_workload(name)
     n, F = X.shape
     _progress(f"{name}: {n} x {F} generated; fitting")
     marks = {}
+    prof0 = warmup + steps
 
     def hook(m, eng):
         if m == warmup:
-            eng.set_profiling(1)
             marks["s0"] = est._live_sampler.stats()
+            marks["host0"] = eng.stats()
             marks["t0"] = time.perf_counter()
-        if m == warmup + steps:
+        if m == prof0:
             marks["t1"] = time.perf_counter()
-            marks["stats"] = eng.stats()
+            marks["host1"] = eng.stats()
             marks["s1"] = est._live_sampler.stats()
+            eng.set_profiling(1)
+        if m == prof0 + steps:
+            marks["stats"] = eng.stats()
             eng.set_profiling(2)
-        if m == warmup + steps + BREAKDOWN_ROUNDS:
+        if m == prof0 + steps + BREAKDOWN_ROUNDS:
             marks["breakdown"] = eng.stats()
             eng.set_profiling(0)
 
     full_params = dict(params)
-    params = dict(params, n_estimators=warmup + steps + BREAKDOWN_ROUNDS)
+    params = dict(params, n_estimators=warmup + 2 * steps + BREAKDOWN_ROUNDS)
     est = HybridHistGBMNumbaV1_0_1(**params)
     est._round_hook = hook
     t_fit = time.perf_counter()
@@ -159,6 +168,7 @@ def run_gpu(name, steps, warmup, rounds_only=False):
     _progress(f"fit done in {t_fit:.1f} s (binning {est.times['binning']:.0f} ms)")
     elapsed = marks["t1"] - marks["t0"]
     st = marks["stats"]
+    host = {k: marks["host1"][k] - marks["host0"][k] for k in marks["host1"]}
     predict, fit_full = None, None
     if not rounds_only:
         # A complete fit with the workload's own n_estimators: bin edges,
@@ -177,7 +187,7 @@ def run_gpu(name, steps, warmup, rounds_only=False):
     sampler = {k: (s1[k] - s0[k]) / max(s1["rounds"] - s0["rounds"], 1)
                for k in ("draw_ms", "gen_ms")}
     return dict(est=est, n=n, F=F, elapsed=elapsed, stats=st, t_fit=t_fit,
-                breakdown=marks["breakdown"], sampler=sampler, predict=predict,
+                breakdown=marks["breakdown"], sampler=sampler, predict=predict, host=host,
                 fit_full=fit_full, params=params)
 
 
@@ -242,8 +252,9 @@ def hist_roofline(st, workload):
         "traffic_source": source,
         "kernel": "k_hist",
         "timing": "kernel execution: first block's start to last block's end, stamped by "
-                  "the kernel on the device's constant-rate clock (no event packets in the "
-                  "timed rounds)",
+                  "the kernel on the device's constant-rate clock, over as many rounds as "
+                  "the timed region, right after it in the same fit (profiling level 1: no "
+                  "event packets; the timed rounds themselves run unprofiled)",
         "launches": int(st["hist_launches"]),
         "avg_launch_us": round(1e3 * st["hist_ms"] / launches, 2),
         "bytes_per_launch": round(st["hist_bytes"] / launches),
@@ -325,11 +336,13 @@ def main():
         },
         "fit_end_to_end": r["fit_full"],
         "nodes_expanded_per_tree": round(st["nodes_expanded"] / max(st["trees"], 1), 2),
+        "timed_rounds_as_graphs": {"rows": int(r["host"]["rows_graph_rounds"]),
+                                   "tree": int(r["host"]["tree_graph_rounds"])},
         "host_ms_per_step": {
-            "sampler_wait": round(st.get("sampler_wait_ms", 0.0) / a.steps, 3),
-            "round": round(st.get("round_ms", 0.0) / a.steps, 3),
-            "enqueue": round(st.get("enqueue_ms", 0.0) / a.steps, 3),
-            "finish_wait": round(st.get("finish_ms", 0.0) / a.steps, 3),
+            "sampler_wait": round(r["host"]["sampler_wait_ms"] / a.steps, 3),
+            "round": round(r["host"]["round_ms"] / a.steps, 3),
+            "enqueue": round(r["host"]["enqueue_ms"] / a.steps, 3),
+            "finish_wait": round(r["host"]["finish_ms"] / a.steps, 3),
             "sampler_draw": round(r["sampler"]["draw_ms"], 3),
             "sampler_gen": round(r["sampler"]["gen_ms"], 3),
         },
@@ -341,6 +354,8 @@ def main():
             "trees_per_s": round(a.also_steps / r2["elapsed"], 3),
             "ms_per_step": round(1e3 * r2["elapsed"] / a.also_steps, 3),
             "steps": a.also_steps,
+            "timed_rounds_as_graphs": {"rows": int(r2["host"]["rows_graph_rounds"]),
+                                       "tree": int(r2["host"]["tree_graph_rounds"])},
             "config": {"rows": r2["n"], "features": r2["F"],
                        "max_depth": r2["params"]["max_depth"],
                        "max_leaves": int(r2["est"].max_leaves),

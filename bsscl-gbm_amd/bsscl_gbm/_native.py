@@ -402,14 +402,15 @@ class Engine:
         check(lib().bsscl_engine_set_profiling(self.handle, int(level)))
 
     def stats(self):
-        out = np.zeros(18, np.float64)
+        out = np.zeros(21, np.float64)
         n = np.zeros(1, np.int32)
-        check(lib().bsscl_engine_stats(self.handle, ptr(out), 18, ptr(n)))
+        check(lib().bsscl_engine_stats(self.handle, ptr(out), 21, ptr(n)))
         keys = ["hist_launches", "hist_ms", "hist_row_features", "hist_bytes",
                 "part_launches", "part_ms", "split_launches", "split_ms",
                 "trees", "nodes_expanded", "sampler_wait_ms", "round_ms",
                 "reduce_launches", "reduce_ms", "enqueue_ms", "finish_ms",
-                "predict_launches", "predict_ms"]
+                "predict_launches", "predict_ms", "rows_graph_rounds", "tree_graph_rounds",
+                "graph_captures"]
         return dict(zip(keys, out[:int(n[0])].tolist()))
 
 

@@ -29,6 +29,7 @@
 
 #include <algorithm>
 #include <array>
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstdlib>
@@ -67,12 +68,18 @@ namespace {
     if (rc_ != BSSCL_OK) return rc_; \
   } while (0)
 
+// Counts device allocations and frees made through DevBuf.  A captured
+// round (RoundGraph) holds the addresses of the buffers it uses, so it is
+// replayed only while this count is the one it was captured at.
+std::atomic<uint64_t> g_alloc_gen{0};
+
 template <typename T>
 struct DevBuf {
   T *p = nullptr;
   size_t cap = 0;
   int ensure(size_t count) {
     if (count <= cap && p) return BSSCL_OK;
+    g_alloc_gen.fetch_add(1, std::memory_order_relaxed);
     if (p) (void)hipFree(p);
     p = nullptr;
     cap = 0;
@@ -86,7 +93,10 @@ struct DevBuf {
     return BSSCL_OK;
   }
   void release() {
-    if (p) (void)hipFree(p);
+    if (p) {
+      g_alloc_gen.fetch_add(1, std::memory_order_relaxed);
+      (void)hipFree(p);
+    }
     p = nullptr;
     cap = 0;
   }
@@ -192,6 +202,19 @@ struct RoundSlot {
   std::vector<int32_t> feats, nb_sel;
   hipEvent_t done = nullptr;  // after the round's readback copies
   uint64_t seq = 0;           // tags the round's profiling events
+};
+
+// A captured launch sequence of one stream of a boosting round (a HIP
+// graph), replayed for every later round whose key matches: the key holds
+// every host value the launches take (sizes, parameters, slot, device
+// addresses through the allocation count).  Rows graphs: Fisher-Yates, the
+// in-bag sort and the root's code gather.  Tree graphs: gradients, root,
+// levels, replay and F update, while profiling is off (the histogram
+// launches' timing stamps and the event pairs take per-round addresses).
+struct RoundGraph {
+  std::vector<uint64_t> key;
+  hipGraphExec_t exec = nullptr;
+  int32_t run = 0;  // tree graphs: levels enqueued
 };
 
 }  // namespace
@@ -353,6 +376,12 @@ struct bsscl_engine {
   size_t rtable_pin_bytes[2] = {0, 0};
   RoundSlot rslot[2];
   int32_t rslot_next = 0;
+  // Captured rounds by slot (off with BSSCL_GRAPHS=0, and after a capture
+  // that failed); the first boosting round of an engine runs uncaptured.
+  RoundGraph rows_graph[2], tree_graph[2];
+  bool graphs = true;
+  bool launched_round = false;
+  DevBuf<const void *> draws_ref_d;  // per slot: the round's draws address
   bool pipeline = false;   // enqueue the next round before returning one
   int32_t ahead = -1;      // slot of a round enqueued ahead, or -1
   uint64_t round_seq = 0;
@@ -404,7 +433,7 @@ struct bsscl_engine {
   size_t ktime_used = 0;                                   // words
   std::vector<std::pair<size_t, size_t>> ktime_launches;  // (first word, blocks)
   double wall_khz = 0.0;
-  double stats[18] = {0};
+  double stats[21] = {0};
 };
 
 namespace bsscl {
@@ -1612,6 +1641,74 @@ int drain_rounds(bsscl_engine *E, int s) {
   return BSSCL_OK;
 }
 
+void release_graph(RoundGraph &g) {
+  if (g.exec) (void)hipGraphExecDestroy(g.exec);
+  g = RoundGraph{};
+}
+
+template <typename T>
+void key_add(std::vector<uint64_t> &k, T v) {
+  static_assert(sizeof(T) <= 8, "scalar");
+  uint64_t u = 0;
+  std::memcpy(&u, &v, sizeof(T));
+  k.push_back(u);
+}
+
+// Which of a round's launch sequences run as captured graphs: the rows
+// stream's by default; BSSCL_GRAPHS=1 adds the tree stream's, =0 turns both
+// off.  On one MI355X at 1M x 28 rows graphs left the GPU time per round as
+// it was and took 0.05-0.09 ms of host time off each round's enqueue; tree
+// graphs took another 0.07-0.1 ms off but made the GPU round about 2%
+// longer (the same kernels, dispatched from a graph), so they are for hosts
+// whose enqueue paces the rounds.
+bool graphs_wanted(bool tree) {
+  const char *v = std::getenv("BSSCL_GRAPHS");
+  if (v && v[0] == '0') return false;
+  return !tree || (v && v[0] == '1');
+}
+
+// Enqueues `launches` (a function returning an engine status) on stream st:
+// through g's graph when its key is `key`, else captured into a new graph
+// for `key` and launched, or run directly while the engine has not yet run
+// a round, or graphs are off.  A capture that fails turns graphs off and
+// runs the launches directly.  Sets *replayed when the launches ran as a
+// graph.
+template <typename F>
+int run_graph(bsscl_engine *E, RoundGraph &g, const std::vector<uint64_t> &key, hipStream_t st,
+              bool tree, F &&launches, bool *replayed) {
+  *replayed = false;
+  if (!E->graphs || !E->launched_round || !graphs_wanted(tree)) return launches();
+  if (g.exec && g.key == key) {
+    HIPCHK(hipGraphLaunch(g.exec, st));
+    *replayed = true;
+    return BSSCL_OK;
+  }
+  // (The slot's previous round has finished: its graph is idle.)
+  release_graph(g);
+  hipGraph_t graph = nullptr;
+  hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+  int rc = BSSCL_OK;
+  if (e == hipSuccess) {
+    rc = launches();
+    const hipError_t e2 = hipStreamEndCapture(st, &graph);
+    if (e2 != hipSuccess) e = e2;
+  }
+  if (rc == BSSCL_OK && e == hipSuccess && graph)
+    e = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+  if (graph) (void)hipGraphDestroy(graph);
+  if (rc != BSSCL_OK || e != hipSuccess || !g.exec) {
+    (void)hipGetLastError();
+    release_graph(g);
+    E->graphs = false;
+    return launches();  // captured, not run: run them now
+  }
+  g.key = key;
+  E->stats[20] += 1.0;
+  HIPCHK(hipGraphLaunch(g.exec, st));
+  *replayed = true;
+  return BSSCL_OK;
+}
+
 // Enqueues one boosting round: gradients from the current F (est:2868),
 // the sampler's round (est:2886, est:2502-2517), the tree, its replay
 // (est:641-820), F += lr * tree(X) and the training log-loss, and the
@@ -1634,8 +1731,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   void *token = nullptr;
   const auto t_wait0 = std::chrono::steady_clock::now();
   CHK(sampler_take(sampler, &sr, &token));
-  if (E->prof)
-    E->stats[10] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_wait0).count();
+  E->stats[10] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_wait0).count();
   R.active = true;
   R.sampler = sampler;
   R.token = token;
@@ -1732,6 +1828,8 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   if (rc == BSSCL_OK) {
     hipError_t e = hipSuccess;
     const int32_t *rows_d = nullptr;
+    FyWork w;
+    bool fy = false;  // this round's Fisher-Yates steps run on the device
     if (!sh.do_rows) {
       e = launch_iota(rs, E->round_rows[s].p, m);  // every row, in order
     } else if (sh.device_rows) {
@@ -1751,35 +1849,69 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
       } else if (E->perm_sampler != sampler || E->perm_next_round != sr.round) {
         rc = set_error(BSSCL_EINVAL, "boost_round: the sampler's earlier rounds did not run on this engine");
       }
-      FyWork w;
       if (rc == BSSCL_OK) rc = ensure_fy_work(E, X.n, w);
       // The sampler copied the draws on its own stream.
       if (rc == BSSCL_OK && e == hipSuccess) e = hipStreamWaitEvent(rs, sr.draws_copied, 0);
       if (rc == BSSCL_OK && e == hipSuccess) {
-        const int nxt = E->perm_cur ^ 1;
-        e = launch_fisher_yates(rs, sr.draws_dev, X.n, E->perm[E->perm_cur].p,
-                                E->perm[nxt].p, w);
-        E->perm_cur = nxt;
-        E->perm_next_round = sr.round + 1;
-        rows_d = E->perm[nxt].p;
+        fy = true;
+        rows_d = E->perm[E->perm_cur ^ 1].p;
       }
     } else {
       rc = E->rows_in.ensure((size_t)m);
       if (rc == BSSCL_OK) e = hipMemcpyAsync(E->rows_in.p, sr.rows, (size_t)m * 4, hipMemcpyHostToDevice, rs);
       rows_d = E->rows_in.p;
     }
-    if (rc == BSSCL_OK && e == hipSuccess && rows_d)
-      e = launch_sort_rows(rs, rows_d, m, E->row_flags.p, n_pad, E->sort_tmp.p,
-                           E->round_rows[s].p);
-    // The root's pack, then its codes (sets 2s, 2s + 1 were last read by
+    // The root's pack (root_d[s], like sets 2s and 2s + 1, was last read by
     // the tree of the round before the previous one).
     if (rc == BSSCL_OK && e == hipSuccess && R.device_replay) {
       pack_copy(rpk.pk, rpk_off, E->root_pin[s]);
       e = hipMemcpyAsync(E->root_d[s].p, E->root_pin[s], total, hipMemcpyHostToDevice, rs);
-      if (e == hipSuccess)
-        e = launch_gather_codes(rs, X.codes.p, X.ld,
-                                reinterpret_cast<const int32_t *>(pre.dev[kPackFeat]), F_sel,
-                                E->round_rows[s].p, m, E->codes_c[2 * s].p, E->ld_c, E->ld_c);
+    }
+    // Device rows after the sampler's first round go through the slot's
+    // rows graph; the draws' address reaches it through draws_ref_d[s].
+    const bool rows_graph = fy && sr.round > 0 && R.device_replay && E->prof <= 1;
+    if (rc == BSSCL_OK && e == hipSuccess && rows_graph) {
+      rc = E->draws_ref_d.ensure(2);
+      if (rc == BSSCL_OK) {
+        e = launch_store_ptr(rs, E->draws_ref_d.p + s, sr.draws_dev);
+        w.draws_ref = reinterpret_cast<const uint32_t *const *>(E->draws_ref_d.p + s);
+      }
+    }
+    const int cur = E->perm_cur;
+    auto rows_launches = [&]() -> int {
+      hipError_t e2 = hipSuccess;
+      if (fy)
+        e2 = launch_fisher_yates(rs, w.draws_ref ? nullptr : sr.draws_dev, X.n, E->perm[cur].p,
+                                 E->perm[cur ^ 1].p, w);
+      if (e2 == hipSuccess && rows_d)
+        e2 = launch_sort_rows(rs, rows_d, m, E->row_flags.p, n_pad, E->sort_tmp.p,
+                              E->round_rows[s].p);
+      if (e2 == hipSuccess && R.device_replay)
+        e2 = launch_gather_codes(rs, X.codes.p, X.ld,
+                                 reinterpret_cast<const int32_t *>(pre.dev[kPackFeat]), F_sel,
+                                 E->round_rows[s].p, m, E->codes_c[2 * s].p, E->ld_c, E->ld_c);
+      if (e2 != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("rows: ") + hipGetErrorString(e2));
+      return BSSCL_OK;
+    };
+    if (rc == BSSCL_OK && e == hipSuccess) {
+      if (rows_graph) {
+        std::vector<uint64_t> key;
+        key_add(key, g_alloc_gen.load(std::memory_order_relaxed));
+        for (int64_t v : {(int64_t)s, X.n, X.ld, m, (int64_t)cur, n_pad, (int64_t)F_sel, E->ld_c})
+          key_add(key, v);
+        for (const void *ptr : {(const void *)X.codes.p, (const void *)pre.dev[kPackFeat],
+                                (const void *)w.keys, (const void *)rows_d})
+          key_add(key, ptr);
+        bool replayed = false;
+        rc = run_graph(E, E->rows_graph[s], key, rs, false, rows_launches, &replayed);
+        if (rc == BSSCL_OK && replayed) E->stats[18] += 1.0;
+      } else {
+        rc = rows_launches();
+      }
+    }
+    if (rc == BSSCL_OK && e == hipSuccess && fy) {
+      E->perm_cur = cur ^ 1;
+      E->perm_next_round = sr.round + 1;
     }
     if (rc == BSSCL_OK && e == hipSuccess && !E->rows_ready[s])
       e = hipEventCreateWithFlags(&E->rows_ready[s], hipEventDisableTiming);
@@ -1788,26 +1920,16 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     if (rc == BSSCL_OK && e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("rows: ") + hipGetErrorString(e));
   }
   if (rc != BSSCL_OK) return fail(rc);
-  // Gradients from the current F (est:2868): for the in-bag rows, straight
-  // into the root's set, on the device path; for every row otherwise (the
-  // host-driven path gathers them).
-  {
-    hipError_t e = R.device_replay
-                       ? launch_gather_gh(E->st, E->F.p, E->y.p, E->round_rows[s].p, m, E->w0,
-                                          E->w1, gm, hm, E->gh_c[2 * s].p, E->ld_c, E->segs.p,
-                                          E->hist_node_d.p,
-                                          reinterpret_cast<const LevelPlan *>(pre.dev[kPackPlan]),
-                                          E->plan_d)
-                       : launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, gm, hm,
-                                          E->ghq.p);
-    if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("gradients: ") + hipGetErrorString(e));
-  }
   if (rc == BSSCL_OK) rc = E->partials_d.ensure((size_t)nb);
   if (rc == BSSCL_OK) rc = E->tree_d.ensure((size_t)R.M);
   if (rc == BSSCL_OK) rc = ensure_round_out(E, s, R.M, nb);
-  if (rc == BSSCL_OK && R.device_replay)
-    rc = launch_tree(E, E->round_rows[s].p, m, R.feats, R.nb_sel, tp, &R.run, !E->pipeline,
-                     true, &pre);
+  // Gradients from the current F (est:2868): for every row on the
+  // host-driven path, which gathers them itself.
+  if (rc == BSSCL_OK && !R.device_replay) {
+    const hipError_t e = launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, gm, hm,
+                                          E->ghq.p);
+    if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("gradients: ") + hipGetErrorString(e));
+  }
   if (rc == BSSCL_OK && R.device_replay) {
     RoundHeader *hdr = reinterpret_cast<RoundHeader *>(E->round_d[s].p);
     ReplayArgs ra;
@@ -1825,26 +1947,85 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     ra.max_depth = a.max_depth;
     ra.pad = 0;
     R.table_readback = E->prof && !replay_counts_nodes(ra);
-    hipError_t e = launch_replay(E->st, E->nodes_d, E->plan_d, E->feat_d, ra,
-                                 round_arrays(E->round_d[s].p, R.M), E->tree_d.p, hdr);
-    // The per-block losses follow the tree; the host sums them
-    // (sum_partials_host).
-    if (e == hipSuccess)
-      e = launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, R.M, &hdr->node_count,
-                          a.learning_rate, E->F.p, E->y.p,
-                          reinterpret_cast<double *>(E->round_d[s].p + round_out_bytes(R.M)), nb);
-    if (e == hipSuccess)
-      e = hipMemcpyAsync(E->round_pin[s], E->round_d[s].p,
-                         round_out_bytes(R.M) + (size_t)nb * 8, hipMemcpyDeviceToHost, E->st);
+    char *const partials = E->round_d[s].p + round_out_bytes(R.M);
+    const bool checks = !E->pipeline;
+    // Gradients of the in-bag rows straight into the root's set, the tree,
+    // its replay, then F += lr * tree(X) with the per-block losses, which the
+    // host sums (sum_partials_host).
+    auto tree_launches = [&]() -> int {
+      hipError_t e = launch_gather_gh(E->st, E->F.p, E->y.p, E->round_rows[s].p, m, E->w0,
+                                      E->w1, gm, hm, E->gh_c[2 * s].p, E->ld_c, E->segs.p,
+                                      E->hist_node_d.p,
+                                      reinterpret_cast<const LevelPlan *>(pre.dev[kPackPlan]),
+                                      E->plan_d);
+      if (e != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("gradients: ") + hipGetErrorString(e));
+      CHK(launch_tree(E, E->round_rows[s].p, m, R.feats, R.nb_sel, tp, &R.run, checks, true, &pre));
+      e = launch_replay(E->st, E->nodes_d, E->plan_d, E->feat_d, ra,
+                        round_arrays(E->round_d[s].p, R.M), E->tree_d.p, hdr);
+      if (e == hipSuccess)
+        e = launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, R.M, &hdr->node_count,
+                            a.learning_rate, E->F.p, E->y.p, reinterpret_cast<double *>(partials),
+                            nb);
+      // The round's readback (tree arrays and losses) into pinned memory,
+      // inside the graph: an operation enqueued after a graph waits for
+      // the graph's completion, which costs microseconds per round.
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(E->round_pin[s], E->round_d[s].p, round_out_bytes(R.M) + (size_t)nb * 8,
+                           hipMemcpyDeviceToHost, E->st);
+      if (e != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("round: ") + hipGetErrorString(e));
+      return BSSCL_OK;
+    };
+    // A tree graph needs every level enqueued without a host check, and
+    // profiling off.
+    const bool tree_graph =
+        E->prof == 0 && (!checks || std::max(1, a.max_depth) <= kLevelsPerCheck);
+    if (tree_graph) {
+      const char *pl = std::getenv("BSSCL_TEST_PAIR_LEVELS");
+      const bool pair = E->plan_lds && !(pl && pl[0] == '0');
+      std::vector<uint64_t> key;
+      key_add(key, g_alloc_gen.load(std::memory_order_relaxed));
+      for (int64_t v : {(int64_t)s, X.n, X.ld, m, (int64_t)F_sel, (int64_t)R.M, (int64_t)nb,
+                        (int64_t)E->prof, (int64_t)checks, (int64_t)pair, (int64_t)E->plan_lds,
+                        (int64_t)E->track_rid, (int64_t)E->node_cap, (int64_t)E->tile_cap,
+                        (int64_t)E->hist_cap, E->ld_c, E->node_stride, (int64_t)E->part_rows,
+                        (int64_t)pre.n_hist, (int64_t)ra.stage_limit,
+                        (int64_t)E->hist_fc, (int64_t)E->hist_copies, (int64_t)E->hist_fc_span,
+                        (int64_t)E->hist_copies_span, (int64_t)E->hist_blocks_per_cu,
+                        (int64_t)E->hist_rows_per_flush, (int64_t)E->hist_rows_per_flush_level,
+                        (int64_t)tp.max_leaves, (int64_t)tp.max_depth,
+                        (int64_t)tp.min_samples_leaf})
+        key_add(key, v);
+      for (double v : {tp.mcw, tp.lam, tp.gamma, a.learning_rate, gm, hm, E->w0, E->w1})
+        key_add(key, v);
+      // (round_pin is host memory: its address is not covered by the
+      // allocation count.)
+      for (const void *ptr : {(const void *)X.codes.p, (const void *)pre.dev[kPackFeat],
+                              (const void *)pre.dev[kPackNbHot], (const void *)pre.dev[kPackHist],
+                              (const void *)pre.dev[kPackPlan], (const void *)pre.dev[kPackTasks],
+                              (const void *)E->round_pin[s]})
+        key_add(key, ptr);
+      bool replayed = false;
+      RoundGraph &g = E->tree_graph[s];
+      rc = run_graph(E, g, key, E->st, true, tree_launches, &replayed);
+      if (rc == BSSCL_OK && replayed) {
+        E->stats[19] += 1.0;
+        if (R.run > 0) g.run = R.run;  // captured in this round
+        else R.run = g.run;
+      }
+    } else {
+      rc = tree_launches();
+    }
+    hipError_t e = rc == BSSCL_OK ? hipSuccess : hipErrorUnknown;
     if (e == hipSuccess && R.table_readback)
       e = hipMemcpyAsync(E->rtable_pin[s], E->table_d.p,
                          64 + (size_t)table_bound(E, R.run) * sizeof(NodeOut),
                          hipMemcpyDeviceToHost, E->st);
     if (e == hipSuccess && !R.done) e = hipEventCreateWithFlags(&R.done, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventRecord(R.done, E->st);
-    if (e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("round: ") + hipGetErrorString(e));
+    if (rc == BSSCL_OK && e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("round: ") + hipGetErrorString(e));
   }
   if (rc != BSSCL_OK) return fail(rc);
+  E->launched_round = true;
   return BSSCL_OK;
 }
 
@@ -2002,6 +2183,10 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   if (E->ahead >= 0 && E->rslot[E->ahead].active)
     sampler_give_back(E->rslot[E->ahead].sampler, E->rslot[E->ahead].token);
   E->ahead = -1;
+  for (int b = 0; b < 2; ++b) {
+    release_graph(E->rows_graph[b]);
+    release_graph(E->tree_graph[b]);
+  }
   for (auto &m : E->mat) m.codes.release();
   E->F.release();
   E->y.release();
@@ -2462,8 +2647,7 @@ int bsscl_boost_round(bsscl_engine *E, bsscl_sampler *sampler,
     E->rslot_next ^= 1;
     const auto te = std::chrono::steady_clock::now();
     const int rc = enqueue_round(E, sampler, a, nxt);
-    if (E->prof)
-      E->stats[14] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - te).count();
+    E->stats[14] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - te).count();
     if (rc != BSSCL_OK) {
       (void)drain_rounds(E, cur);
       return rc;
@@ -2472,15 +2656,13 @@ int bsscl_boost_round(bsscl_engine *E, bsscl_sampler *sampler,
   }
   const auto tf = std::chrono::steady_clock::now();
   const int rc = finish_round(E, cur, out, out_train_loss);
-  if (E->prof)
-    E->stats[15] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - tf).count();
+  E->stats[15] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - tf).count();
   if (rc != BSSCL_OK) {
     if (E->ahead >= 0) (void)drain_rounds(E, E->ahead);
     E->ahead = -1;
     return rc;
   }
-  if (E->prof)
-    E->stats[11] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  E->stats[11] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
   return BSSCL_OK;
 }
 
@@ -2999,7 +3181,7 @@ int bsscl_engine_stats(bsscl_engine *E, double *out, int32_t cap, int32_t *n_out
     HIPCHK(hipStreamSynchronize(E->st));
     CHK(prof_slots_collect(E));
   }
-  const int32_t n = std::min<int32_t>(cap, 18);
+  const int32_t n = std::min<int32_t>(cap, 21);
   for (int32_t i = 0; i < n; ++i) out[i] = E->stats[i];
   *n_out = n;
   return BSSCL_OK;

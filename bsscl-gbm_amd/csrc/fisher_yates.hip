@@ -40,9 +40,11 @@ unsigned blocks_for(int64_t n) {
   return (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, kRowsStreamBlocks));
 }
 
-__global__ __launch_bounds__(256) void k_fy_push(const uint32_t *__restrict__ draws, int64_t n,
+__global__ __launch_bounds__(256) void k_fy_push(const uint32_t *__restrict__ draws,
+                                                 const uint32_t *const *draws_ref, int64_t n,
                                                  int32_t *__restrict__ head,
                                                  int32_t *__restrict__ next) {
+  if (draws_ref) draws = *draws_ref;
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < n - 1;
        t += (int64_t)gridDim.x * blockDim.x) {
     const int32_t k = (int32_t)(n - 1 - t);
@@ -180,11 +182,13 @@ __global__ __launch_bounds__(256) void k_fy_resolve(const int32_t *__restrict__ 
   }
 }
 
-__global__ __launch_bounds__(256) void k_fy_final(const uint32_t *__restrict__ draws, int64_t n,
+__global__ __launch_bounds__(256) void k_fy_final(const uint32_t *__restrict__ draws,
+                                                  const uint32_t *const *draws_ref, int64_t n,
                                                   const int32_t *__restrict__ next,
                                                   const int32_t *__restrict__ v,
                                                   const int32_t *__restrict__ a_old,
                                                   int32_t *__restrict__ a_new) {
+  if (draws_ref) draws = *draws_ref;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
     int32_t out;
@@ -206,8 +210,10 @@ __global__ __launch_bounds__(256) void k_fy_final(const uint32_t *__restrict__ d
 // ---------------------------------------------------------------------------
 constexpr uint64_t kFyNoKey = ~0ull;
 
-__global__ __launch_bounds__(256) void k_fy_keys(const uint32_t *__restrict__ draws, int64_t n,
+__global__ __launch_bounds__(256) void k_fy_keys(const uint32_t *__restrict__ draws,
+                                                 const uint32_t *const *draws_ref, int64_t n,
                                                  int64_t ld, uint64_t *__restrict__ keys) {
+  if (draws_ref) draws = *draws_ref;
   for (int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; s < ld;
        s += (int64_t)gridDim.x * blockDim.x) {
     uint64_t key = kFyNoKey;
@@ -262,10 +268,12 @@ __global__ __launch_bounds__(256) void k_fy_final_sorted(const uint64_t *__restr
 
 // a_new[k] = v(k) for position 0 and every step with j(k) == k.
 __global__ __launch_bounds__(256) void k_fy_final_self(const uint32_t *__restrict__ draws,
+                                                       const uint32_t *const *draws_ref,
                                                        int64_t n,
                                                        const int32_t *__restrict__ head,
                                                        const int32_t *__restrict__ a_old,
                                                        int32_t *__restrict__ a_new) {
+  if (draws_ref) draws = *draws_ref;
   for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < n;
        k += (int64_t)gridDim.x * blockDim.x) {
     if (k == 0 || (int64_t)draws[n - 1 - k] == k) a_new[k] = fy_value(head, a_old, (int32_t)k);
@@ -273,6 +281,15 @@ __global__ __launch_bounds__(256) void k_fy_final_self(const uint32_t *__restric
 }
 
 }  // namespace
+
+namespace {
+__global__ void k_store_ptr(const void **cell, const void *value) { *cell = value; }
+}  // namespace
+
+hipError_t launch_store_ptr(hipStream_t st, const void **cell, const void *value) {
+  hipLaunchKernelGGL(k_store_ptr, dim3(1), dim3(1), 0, st, cell, value);
+  return hipGetLastError();
+}
 
 hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
                                const int32_t *a_old, int32_t *a_new, const FyWork &w) {
@@ -284,21 +301,22 @@ hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
     while (bits < 32 && ((uint64_t)(n - 1) >> bits) != 0) ++bits;  // positions < 2^bits
     const dim3 gk(blocks_for(ld));
     hipLaunchKernelGGL(k_fill_neg, dim3(blocks_for((n + 3) / 4)), b, 0, st, w.head, n);
-    hipLaunchKernelGGL(k_fy_keys, gk, b, 0, st, draws, n, ld, w.keys);
+    hipLaunchKernelGGL(k_fy_keys, gk, b, 0, st, draws, w.draws_ref, n, ld, w.keys);
     uint64_t *sorted = nullptr;
     hipError_t e = launch_sort_u64(st, w.keys, w.keys_tmp, ld, 32, 32 + (bits + 7) / 8 * 8,
                                    w.counts, w.totals, &sorted);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_fy_links, gk, b, 0, st, sorted, ld, w.head);
     hipLaunchKernelGGL(k_fy_final_sorted, gk, b, 0, st, sorted, ld, w.head, a_old, a_new);
-    hipLaunchKernelGGL(k_fy_final_self, g, b, 0, st, draws, n, w.head, a_old, a_new);
+    hipLaunchKernelGGL(k_fy_final_self, g, b, 0, st, draws, w.draws_ref, n, w.head, a_old,
+                       a_new);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(k_fill_neg, dim3(blocks_for((n + 3) / 4)), b, 0, st, w.head, n);
-  if (n > 1) hipLaunchKernelGGL(k_fy_push, g, b, 0, st, draws, n, w.head, w.next);
+  if (n > 1) hipLaunchKernelGGL(k_fy_push, g, b, 0, st, draws, w.draws_ref, n, w.head, w.next);
   hipLaunchKernelGGL(k_fy_sort, g, b, 0, st, w.head, w.next, n);
   hipLaunchKernelGGL(k_fy_resolve, g, b, 0, st, w.head, a_old, w.v, n);
-  hipLaunchKernelGGL(k_fy_final, g, b, 0, st, draws, n, w.next, w.v, a_old, a_new);
+  hipLaunchKernelGGL(k_fy_final, g, b, 0, st, draws, w.draws_ref, n, w.next, w.v, a_old, a_new);
   return hipGetLastError();
 }
 

@@ -319,11 +319,11 @@ int bsscl_sampler_stats(bsscl_sampler *s, double *out, int32_t cap,
 void bsscl_sampler_destroy(bsscl_sampler *s);
 
 /*
- * Timing of the engine's own kernels, taken with HIP events on the engine's
- * stream while profiling is on: level 1 times the histogram and prediction
- * kernels only, level 2 also the partition and split groups (0 turns it
- * off).  No reference counterpart (the reference records only wall times,
- * est:1904).  bsscl_engine_stats fills up to `cap` doubles in this order:
+ * Timing of the engine's own kernels while profiling is on: level 1 times
+ * the histogram and prediction kernels only, level 2 also the partition and
+ * split groups (0 turns it off).  No reference counterpart (the reference
+ * records only wall times, est:1904).  bsscl_engine_stats fills up to `cap`
+ * doubles in this order:
  *   [0] histogram launches   [1] histogram ms (sum of launch durations)
  *   [2] histogram rows x features  [3] histogram algorithmic bytes
  *   [4] partition launches   [5] partition ms
@@ -334,9 +334,21 @@ void bsscl_sampler_destroy(bsscl_sampler *s);
  *   [12] histogram-reduction launches  [13] histogram-reduction ms
  *   [14] host ms enqueueing rounds     [15] host ms waiting for a round's results
  *   [16] prediction launches (bsscl_predict)  [17] prediction ms
- * and returns the number written in *n_out.  Histogram and prediction times
- * are each kernel's execution, from events recorded by its own dispatch;
- * the other groups are bracketed by event pairs on the stream.
+ *   [18] boosting rounds whose rows-stream kernels (bagging, in-bag sort,
+ *        root gather) ran as a captured HIP graph
+ *   [19] boosting rounds whose tree kernels ran as a captured HIP graph
+ *   [20] graphs captured
+ * and returns the number written in *n_out.  A histogram launch's time runs
+ * from its first block's start to its last block's end, stamped by the
+ * kernel on the device's constant-rate clock; prediction times come from
+ * events recorded by the kernel's own dispatch; the other groups are
+ * bracketed by event pairs on the stream.  The host times [10], [11], [14],
+ * [15] and the counters [18]-[20] are kept at every level (0 included);
+ * set_profiling with a level of 1 or 2 clears every entry.  The rows-stream
+ * sequence runs as a graph by default, the tree sequence with
+ * BSSCL_GRAPHS=1 in the environment and only while profiling is off (its
+ * stamps and event pairs take per-round addresses); BSSCL_GRAPHS=0 launches
+ * every kernel one by one.
  */
 int bsscl_engine_set_profiling(bsscl_engine *eng, int32_t on);
 int bsscl_engine_stats(bsscl_engine *eng, double *out, int32_t cap,

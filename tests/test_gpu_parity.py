@@ -390,6 +390,72 @@ def test_fit_lockstep_and_end_to_end(engine, name):
             assert at255 > 0
 
 
+def test_fit_graph_rounds_match_direct_launches(engine, monkeypatch):
+    """Boosting rounds replayed from captured HIP graphs give the trees and
+    losses of rounds whose kernels are launched one by one: the rows
+    stream's graph (Fisher-Yates, in-bag sort, code gather; the default) and
+    the tree stream's (gradients, levels, replay, F update and the readback;
+    BSSCL_GRAPHS=1).  Rows and features are bagged, so each round's draws
+    reach the rows graph through its device-side address.  Graphs are
+    replayed within a fit and across fits, pipelined and not.  At profiling
+    level 1 the tree kernels are launched one by one (their timing stamps
+    take per-round addresses) and every histogram launch is timed."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    from bsscl_gbm import estimator as est_mod
+    X, y = make_data(60000, 24, seed=21, nan_frac=0.03)
+    params = dict(n_estimators=14, max_depth=6, n_bins=255, subsample=0.7,
+                  colsample_bytree=0.8, random_state=3)
+    eng = est_mod._engine(0)
+
+    def fit(graphs, prof=0, pipeline=True):
+        _announce(f"fit BSSCL_GRAPHS={graphs} prof={prof} pipeline={pipeline}")
+        if graphs is None:
+            monkeypatch.delenv("BSSCL_GRAPHS", raising=False)
+        else:
+            monkeypatch.setenv("BSSCL_GRAPHS", graphs)
+        est = HybridHistGBMNumbaV1_0_1(verbose=False, **params)
+        est._pipeline_rounds = pipeline
+        eng.set_profiling(prof)
+        try:
+            st0 = eng.stats()
+            est.fit(X, y)
+            st = eng.stats()
+        finally:
+            eng.set_profiling(0)
+        d = {k: st[k] - (st0[k] if prof == 0 else 0.0) for k in st}
+        print(f"[result] BSSCL_GRAPHS={graphs} prof={prof} pipeline={pipeline}: rows graph "
+              f"rounds {d['rows_graph_rounds']:.0f}, tree graph rounds "
+              f"{d['tree_graph_rounds']:.0f}, captures {d['graph_captures']:.0f}, "
+              f"histogram launches {d['hist_launches']:.0f}", flush=True)
+        return est, d
+
+    n = params["n_estimators"]
+    ref, d0 = fit("0")
+    assert d0["rows_graph_rounds"] == d0["tree_graph_rounds"] == 0
+    _, dp0 = fit("0", prof=1)
+    # (A fit's first round starts the permutation, outside the rows graph.)
+    for graphs, prof, pipeline, rows_min, tree_min in (
+            (None, 0, True, n - 1, 0), ("1", 0, True, n - 1, n), ("1", 0, True, n - 1, n),
+            ("1", 1, True, n - 1, 0), ("1", 0, False, n - 1, n)):
+        got, d = fit(graphs, prof, pipeline)
+        mode = (graphs, prof, pipeline)
+        assert d["rows_graph_rounds"] >= rows_min, mode
+        assert d["tree_graph_rounds"] >= tree_min, mode
+        if tree_min == 0:
+            assert d["tree_graph_rounds"] == 0, mode
+        if prof == 1:
+            assert d["hist_launches"] == dp0["hist_launches"] > 0, mode
+            assert d["hist_ms"] > 0
+        assert got.train_loss_history_ == ref.train_loss_history_, mode
+        assert len(got.trees) == len(ref.trees) == n
+        for a, b in zip(ref.trees, got.trees):
+            nc = a[5]
+            assert nc == b[5], mode
+            for k in (0, 1, 2, 3, 4, 6):
+                np.testing.assert_array_equal(a[k][:nc], b[k][:nc], err_msg=str(mode))
+    monkeypatch.delenv("BSSCL_GRAPHS", raising=False)
+
+
 def test_profiling_counts_agree(engine, monkeypatch):
     """The node-table counts behind the histogram roofline (rows x features
     histogrammed, bytes, nodes expanded), taken by the in-LDS replay kernel,
