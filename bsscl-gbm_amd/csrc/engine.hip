@@ -381,7 +381,6 @@ struct bsscl_engine {
   RoundGraph rows_graph[2], tree_graph[2];
   bool graphs = true;
   bool launched_round = false;
-  DevBuf<const void *> draws_ref_d;  // per slot: the round's draws address
   bool pipeline = false;   // enqueue the next round before returning one
   int32_t ahead = -1;      // slot of a round enqueued ahead, or -1
   uint64_t round_seq = 0;
@@ -1008,13 +1007,16 @@ SplitParams split_params(bsscl_engine *E, const TreeParams &tp) {
 
 // The root's inputs as one upload: the selected features, their bin counts
 // followed by their most frequent bins, the root's histogram tasks, its
-// LevelPlan and its task range (parts kPack*, in order).
-enum { kPackFeat = 0, kPackNbHot, kPackHist, kPackPlan, kPackTasks };
+// LevelPlan, its task range and, for a boosting round, the address of the
+// round's bagging draws, which the Fisher-Yates kernels read from there
+// (parts kPack*, in order).
+enum { kPackFeat = 0, kPackNbHot, kPackHist, kPackPlan, kPackTasks, kPackDraws };
 struct RootPack {
   std::vector<HistTask> ht;
   std::vector<int32_t> nb_hot;
   LevelPlan rp = {};
   int32_t root_tasks[2] = {0, 0};
+  const void *draws = nullptr;
   Pack pk;  // points into the members above: a RootPack is not copied
   RootPack() = default;
   RootPack(const RootPack &) = delete;
@@ -1049,6 +1051,7 @@ void build_root_pack(bsscl_engine *E, int64_t m, const std::vector<int32_t> &fea
   R.pk.add(R.ht.data(), R.ht.size() * sizeof(HistTask));
   R.pk.add(&R.rp, sizeof(LevelPlan));
   R.pk.add(R.root_tasks, sizeof(R.root_tasks));
+  R.pk.add(&R.draws, sizeof(R.draws));
 }
 
 // A root pack already on the device (a boosting round's, uploaded by the
@@ -1864,19 +1867,15 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     // The root's pack (root_d[s], like sets 2s and 2s + 1, was last read by
     // the tree of the round before the previous one).
     if (rc == BSSCL_OK && e == hipSuccess && R.device_replay) {
+      rpk.draws = fy ? static_cast<const void *>(sr.draws_dev) : nullptr;
       pack_copy(rpk.pk, rpk_off, E->root_pin[s]);
       e = hipMemcpyAsync(E->root_d[s].p, E->root_pin[s], total, hipMemcpyHostToDevice, rs);
     }
     // Device rows after the sampler's first round go through the slot's
-    // rows graph; the draws' address reaches it through draws_ref_d[s].
+    // rows graph; the draws' address reaches it in the root's pack.
     const bool rows_graph = fy && sr.round > 0 && R.device_replay && E->prof <= 1;
-    if (rc == BSSCL_OK && e == hipSuccess && rows_graph) {
-      rc = E->draws_ref_d.ensure(2);
-      if (rc == BSSCL_OK) {
-        e = launch_store_ptr(rs, E->draws_ref_d.p + s, sr.draws_dev);
-        w.draws_ref = reinterpret_cast<const uint32_t *const *>(E->draws_ref_d.p + s);
-      }
-    }
+    if (rows_graph)
+      w.draws_ref = reinterpret_cast<const uint32_t *const *>(pre.dev[kPackDraws]);
     const int cur = E->perm_cur;
     auto rows_launches = [&]() -> int {
       hipError_t e2 = hipSuccess;
@@ -1900,7 +1899,8 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
         for (int64_t v : {(int64_t)s, X.n, X.ld, m, (int64_t)cur, n_pad, (int64_t)F_sel, E->ld_c})
           key_add(key, v);
         for (const void *ptr : {(const void *)X.codes.p, (const void *)pre.dev[kPackFeat],
-                                (const void *)w.keys, (const void *)rows_d})
+                                (const void *)pre.dev[kPackDraws], (const void *)w.keys,
+                                (const void *)rows_d})
           key_add(key, ptr);
         bool replayed = false;
         rc = run_graph(E, E->rows_graph[s], key, rs, false, rows_launches, &replayed);

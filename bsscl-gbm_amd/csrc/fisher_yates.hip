@@ -282,15 +282,6 @@ __global__ __launch_bounds__(256) void k_fy_final_self(const uint32_t *__restric
 
 }  // namespace
 
-namespace {
-__global__ void k_store_ptr(const void **cell, const void *value) { *cell = value; }
-}  // namespace
-
-hipError_t launch_store_ptr(hipStream_t st, const void **cell, const void *value) {
-  hipLaunchKernelGGL(k_store_ptr, dim3(1), dim3(1), 0, st, cell, value);
-  return hipGetLastError();
-}
-
 hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
                                const int32_t *a_old, int32_t *a_new, const FyWork &w) {
   if (n <= 0) return hipSuccess;

@@ -232,15 +232,14 @@ struct FyWork {
   uint32_t *counts = nullptr, *totals = nullptr;
   // When set, the kernels read the draws' address from this device word
   // instead of taking `draws`, so that one captured launch sequence serves
-  // every round's draws buffer (launch_store_ptr writes it).
+  // every round's draws buffer (the word is uploaded with the round's root
+  // pack).
   const uint32_t *const *draws_ref = nullptr;
 };
 // a_new = a_old after the Fisher-Yates steps i = n-1 .. 1 with draws[t] =
 // j(n-1-t) <= n-1-t.
 hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
                                const int32_t *a_old, int32_t *a_new, const FyWork &w);
-// *cell = value (one thread).
-hipError_t launch_store_ptr(hipStream_t st, const void **cell, const void *value);
 
 hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               const int32_t *feat, int32_t F_sel,
