@@ -626,19 +626,29 @@ bool spec_chunk_avx512(const uint32_t *words, uint32_t lo, uint32_t hi, ChunkFn 
 // Expected step after o words of a shuffle that starts at step n - 1: step
 // s takes (mask + 1) / (s + 1) words on average, so within one mask range
 // (all-ones mask M - 1) the step after w words from step i is about
-// (i + 1) exp(-w / M) - 1.
-double expected_step(int64_t n, double o) {
-  double i = (double)(n - 1);
-  while (i >= 1.0) {
+// (i + 1) exp(-w / M) - 1, and the range is left after M ln((i + 1) / lo)
+// words (lo = M / 2).  at() takes increasing offsets, so a round's chunks
+// walk the mask ranges once.
+struct ExpectedSteps {
+  double i, o0 = 0.0, M = 0.0, wr = 0.0;  // range entered at offset o0 with step i
+  explicit ExpectedSteps(int64_t n) : i((double)(n - 1)) { enter(); }
+  void enter() {
+    if (i < 1.0) return;
     const int k = 63 - __builtin_clzll((uint64_t)i);
-    const double lo = std::ldexp(1.0, k), M = 2.0 * lo;
-    const double wr = M * std::log((i + 1.0) / lo);  // words to leave the range
-    if (o <= wr) return (i + 1.0) * std::exp(-o / M) - 1.0;
-    o -= wr;
-    i = lo - 1.0;
+    const double lo = std::ldexp(1.0, k);
+    M = 2.0 * lo;
+    wr = M * std::log((i + 1.0) / lo);
   }
-  return 0.0;
-}
+  double at(double o) {  // o must not decrease between calls
+    while (i >= 1.0) {
+      if (o - o0 <= wr) return (i + 1.0) * std::exp(-(o - o0) / M) - 1.0;
+      o0 += wr;
+      i = std::ldexp(1.0, 63 - __builtin_clzll((uint64_t)i)) - 1.0;
+      enter();
+    }
+    return 0.0;
+  }
+};
 
 // Expected words of a shuffle of n entries (steps n - 1 .. 1).
 double expected_words(int64_t n) {
@@ -1002,8 +1012,12 @@ struct Sampler {
     return true;
   }
 
+  // The floor moves in steps of kFloorStep chunks: each move takes ring_mu
+  // and wakes the twister, and a floor that lags only holds the twister
+  // back (ring_lead is at least 64 chunks).
+  static constexpr int64_t kFloorStep = 16;
   void set_floor(int64_t c) {
-    if (ring_floor.load(std::memory_order_relaxed) >= c) return;
+    if (ring_floor.load(std::memory_order_relaxed) + kFloorStep > c) return;
     {
       std::lock_guard<std::mutex> lk(ring_mu);
       ring_floor.store(c, std::memory_order_release);
@@ -1039,6 +1053,7 @@ struct Sampler {
     }
   }
 
+  static constexpr size_t kSegBatch = 16;
   // Waits for a transfer function; 0 if the sampler stops.
   int32_t wait_fn(const ChunkFn &f) {
     for (int spin = 0;; ++spin) {
@@ -1061,9 +1076,10 @@ struct Sampler {
     int64_t nt = 0;
     {
       std::vector<CountTask> tl;
+      ExpectedSteps es(n);
       for (int64_t c = c0 + 1;; ++c) {
         const double o = (double)(c * kChunkWords - G);
-        const double e = expected_step(n, o);
+        const double e = es.at(o);
         const double h = window_scale * (2.5 * std::sqrt(o) + 64.0);
         if (e - h < (double)kSpecMin) break;
         const double hi = std::min(e + h, (double)(n - 1));
@@ -1153,7 +1169,7 @@ struct Sampler {
   void run_draws_parallel() {
     std::vector<uint32_t> jf((size_t)F + 16);
     std::vector<Segment> sbatch;
-    sbatch.reserve(8);
+    sbatch.reserve(kSegBatch);
     std::vector<uint32_t> words((size_t)kChunkWords + 16);
     int64_t G = pos0;  // global position of the next word
     for (int32_t r = 0; r < n_rounds; ++r) {
@@ -1179,8 +1195,8 @@ struct Sampler {
         inflight.push_back(std::move(R));
       }
       const auto t0 = std::chrono::steady_clock::now();
-      // Segments go to the workers eight at a time: one lock and at most
-      // one wake-up (a system call) per batch.
+      // Segments go to the workers kSegBatch at a time: one lock and at
+      // most one wake-up (a system call) per batch.
       auto publish = [&] {
         if (sbatch.empty()) return;
         bool wake;
@@ -1200,7 +1216,7 @@ struct Sampler {
         sg.i0 = i;
         sg.round = Rp;
         Rp->pending.fetch_add(1, std::memory_order_relaxed);
-        if (sbatch.size() >= 8) publish();
+        if (sbatch.size() >= kSegBatch) publish();
       };
       const int64_t end = resolve_round(G, emit, words);
       publish();  // the round's last segments
@@ -1531,7 +1547,10 @@ int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
       const double rc = bsscl::expected_words(n) / (double)bsscl::kChunkWords;
       s->ring_lead = std::min<int64_t>(Sampler::kRingChunks, (int64_t)(3.0 * rc) + 64);
       const unsigned hw = std::max(2u, std::thread::hardware_concurrency());
-      const int nw = (int)std::max(2u, std::min(8u, hw / 2));
+      int nw = (int)std::max(2u, std::min(8u, hw / 2));
+      // (Test hook: BSSCL_SAMPLER_WORKERS sets the worker count, 1-32.)
+      if (const char *wv = std::getenv("BSSCL_SAMPLER_WORKERS"))
+        nw = std::max(1, std::min(32, std::atoi(wv)));
       for (int w = 0; w < nw; ++w) s->workers.emplace_back([s] { s->run_worker(); });
       s->twister = std::thread([s] { s->run_twister(); });
     }
