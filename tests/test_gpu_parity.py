@@ -456,6 +456,42 @@ def test_fit_graph_rounds_match_direct_launches(engine, monkeypatch):
     monkeypatch.delenv("BSSCL_GRAPHS", raising=False)
 
 
+def test_graph_rounds_after_buffers_grow(engine, monkeypatch):
+    """Fits of different sizes in turn (the second grows the engine's
+    buffers, so graphs captured before hold stale addresses and must be
+    captured again; the third returns to the first size with the larger
+    buffers) give with BSSCL_GRAPHS=1 the trees and losses of fits whose
+    kernels are launched one by one."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    from bsscl_gbm import estimator as est_mod
+    eng = est_mod._engine(0)
+    cases = [make_data(30000, 12, seed=41, nan_frac=0.02), make_data(90000, 20, seed=42),
+             make_data(30000, 12, seed=41, nan_frac=0.02)]
+    params = dict(n_estimators=8, max_depth=5, n_bins=255, subsample=0.8,
+                  colsample_bytree=0.9, random_state=5)
+    fits = {}
+    for graphs in ("0", "1"):
+        monkeypatch.setenv("BSSCL_GRAPHS", graphs)
+        for j, (X, y) in enumerate(cases):
+            _announce(f"fit {j} ({X.shape[0]} x {X.shape[1]}) BSSCL_GRAPHS={graphs}")
+            st0 = eng.stats()
+            fits[graphs, j] = HybridHistGBMNumbaV1_0_1(verbose=False, **params).fit(X, y)
+            st = eng.stats()
+            if graphs == "1":
+                assert st["tree_graph_rounds"] - st0["tree_graph_rounds"] >= params["n_estimators"]
+    monkeypatch.delenv("BSSCL_GRAPHS", raising=False)
+    for j in range(len(cases)):
+        ref, got = fits["0", j], fits["1", j]
+        assert got.train_loss_history_ == ref.train_loss_history_, j
+        for a, b in zip(ref.trees, got.trees):
+            nc = a[5]
+            assert nc == b[5], j
+            for k in (0, 1, 2, 3, 4, 6):
+                np.testing.assert_array_equal(a[k][:nc], b[k][:nc], err_msg=str(j))
+    print(f"[result] graphs after buffer growth: {len(cases)} fits equal to direct launches",
+          flush=True)
+
+
 def test_profiling_counts_agree(engine, monkeypatch):
     """The node-table counts behind the histogram roofline (rows x features
     histogrammed, bytes, nodes expanded), taken by the in-LDS replay kernel,
