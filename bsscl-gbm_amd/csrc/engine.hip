@@ -1359,6 +1359,13 @@ int ensure_fy_work(bsscl_engine *E, int64_t n, FyWork &w) {
 
 constexpr int32_t kLevelsPerCheck = 8;  // levels enqueued between host checks
 
+// Whether a tree moves its rows every second level (with the LDS planner).
+// (Test hook: BSSCL_TEST_PAIR_LEVELS=0 moves the rows at every level.)
+bool want_pair_levels(const bsscl_engine *E) {
+  const char *pl = std::getenv("BSSCL_TEST_PAIR_LEVELS");
+  return E->plan_lds && !(pl && pl[0] == '0');
+}
+
 // Enqueues the root and every level of one tree (after
 // prepare_tree_buffers).  All levels are enqueued without host round trips:
 // the planner kernel chooses each level's parents on the device; every
@@ -1371,9 +1378,7 @@ int launch_tree(bsscl_engine *E, const int32_t *rows32, int64_t m,
                 bool checks = true, bool gathered = false, const PreRoot *pre = nullptr) {
   const int32_t F_sel = (int32_t)feats.size();
   const int32_t levels = std::max(1, tp.max_depth);
-  // (Test hook: BSSCL_TEST_PAIR_LEVELS=0 moves the rows at every level.)
-  const char *pl = std::getenv("BSSCL_TEST_PAIR_LEVELS");
-  E->pair_levels = E->plan_lds && !(pl && pl[0] == '0');
+  E->pair_levels = want_pair_levels(E);
   CHK(launch_root(E, rows32, m, feats, nb_sel, tp, gathered, pre));
   *run = 0;
   for (int32_t d = 0; d < levels; ++d) {
@@ -1980,8 +1985,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     const bool tree_graph =
         E->prof == 0 && (!checks || std::max(1, a.max_depth) <= kLevelsPerCheck);
     if (tree_graph) {
-      const char *pl = std::getenv("BSSCL_TEST_PAIR_LEVELS");
-      const bool pair = E->plan_lds && !(pl && pl[0] == '0');
+      const bool pair = want_pair_levels(E);
       std::vector<uint64_t> key;
       key_add(key, g_alloc_gen.load(std::memory_order_relaxed));
       for (int64_t v : {(int64_t)s, X.n, X.ld, m, (int64_t)F_sel, (int64_t)R.M, (int64_t)nb,
