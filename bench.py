@@ -285,8 +285,8 @@ def run_cpu_baseline(name, rounds):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="dense_1m")
     ap.add_argument("--cpu-rounds", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -294,7 +294,7 @@ def main():
                     help="skip the prediction and the end-to-end fit (profiler runs)")
     ap.add_argument("--also", default="stress_10m",
                     help="workload of the extra rounds-only block ('' for none)")
-    ap.add_argument("--also-steps", type=int, default=30)
+    ap.add_argument("--also-steps", type=int, default=60)
     a = ap.parse_args()
     if a.gpus != 1:
         print(json.dumps({"error": "this engine runs on one GPU; --gpus must be 1 "
