@@ -9,10 +9,13 @@ rounds is the device time including host work.
 Prints one JSON line with the fit rate (trees/s), the histogram kernel's
 roofline (algorithmic bytes per launch over its average execution time,
 from the first block's start to the last block's end as the kernel stamps
-them, against 8 TB/s HBM),
-prediction through the workload's full ensemble with its own roofline, a
-rounds-only block for the 10M x 50 workload and the oracle's CPU rate on a
-bounded sample.
+them, against 8 TB/s HBM), a complete fit with the workload's own
+n_estimators (training-only and end-to-end trees/s), prediction through
+that ensemble with its own roofline, and the oracle's CPU rates on a
+bounded sample (fit trees/s, histogram rows x features/s, predict rows/s).
+The same block is repeated for the 10M x 50 depth-8 workload: its
+steady-state rounds, its 500-tree fit, predict_proba of a fresh 10M-row
+batch through those 500 trees, and the oracle's first rounds at 10M.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -169,7 +172,7 @@ def run_gpu(name, steps, warmup, rounds_only=False):
     elapsed = marks["t1"] - marks["t0"]
     st = marks["stats"]
     host = {k: marks["host1"][k] - marks["host0"][k] for k in marks["host1"]}
-    predict, fit_full = None, None
+    predict, fit_full, full, Xp_sample = None, None, None, None
     if not rounds_only:
         # A complete fit with the workload's own n_estimators: bin edges,
         # binning and every boosting round, from host float32 X.
@@ -181,14 +184,20 @@ def run_gpu(name, steps, warmup, rounds_only=False):
                         trees_per_s=round(full.n_trees_fitted_ / t_full, 2),
                         binning_ms=round(full.times["binning"], 1),
                         training_ms=round(full.times["training"], 1))
+        fit_full["training_trees_per_s"] = round(
+            full.n_trees_fitted_ / (full.times["training"] / 1e3), 2)
         _progress(f"full fit: {fit_full}")
-        predict = run_predict(full, name)
+        predict, Xp_sample = run_predict(full, name)
     s0, s1 = marks["s0"], marks["s1"]
     sampler = {k: (s1[k] - s0[k]) / max(s1["rounds"] - s0["rounds"], 1)
                for k in ("draw_ms", "gen_ms")}
     return dict(est=est, n=n, F=F, elapsed=elapsed, stats=st, t_fit=t_fit,
                 breakdown=marks["breakdown"], sampler=sampler, predict=predict, host=host,
-                fit_full=fit_full, params=params)
+                fit_full=fit_full, params=params, model=full, Xp_sample=Xp_sample,
+                data=(X, y, full_params))
+
+
+CPU_PREDICT_ROWS = 200_000
 
 
 def run_predict(model, name, repeats=3):
@@ -196,7 +205,9 @@ def run_predict(model, name, repeats=3):
     whole ensemble: rows/s end to end (host float32 in, probabilities out)
     and per k_predict launch (kernel execution time), with the kernel's
     roofline over the algorithmic bytes n * (F + 16) of device-resident
-    codes (one code byte per feature, 8 B of output and 8 B of F per row)."""
+    codes (one code byte per feature, 8 B of output and 8 B of F per row).
+    Returns the line's entry and the batch's first CPU_PREDICT_ROWS rows
+    (the CPU baseline's predict sample)."""
     from bsscl_gbm import estimator as est_mod
     Xp, _, _ = make_workload(name, predict=True)
     n, F = Xp.shape
@@ -215,6 +226,8 @@ def run_predict(model, name, repeats=3):
     achieved = bytes_ / kernel_s / 1e9
     _progress(f"predict: {n} rows x {len(model.trees)} trees, kernel {1e3 * kernel_s:.2f} ms, "
               f"end to end {1e3 * t_total:.1f} ms")
+    sample = np.ascontiguousarray(Xp[:CPU_PREDICT_ROWS])
+    del Xp
     return {
         "rows": n, "trees": len(model.trees),
         "rows_per_s": round(n / kernel_s),
@@ -223,7 +236,7 @@ def run_predict(model, name, repeats=3):
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": None, "kernel": "k_predict",
                      "avg_launch_us": round(1e6 * kernel_s, 1), "bytes_per_launch": bytes_},
-    }
+    }, sample
 
 
 def cpu_model():
@@ -261,25 +274,63 @@ def hist_roofline(st, workload):
     }
 
 
-def run_cpu_baseline(name, rounds):
-    """The oracle (C/OpenMP restatement of the reference path, serial where
-    the reference is serial) timed on this host for `rounds` rounds."""
-    from oracle import model as om
-    X, y, params = make_workload(name)
-    _progress(f"cpu baseline: oracle on {name}, {rounds} timed rounds")
-    p = dict(params)
-    p.pop("verbose")
-    m = om.OracleGBM(**p)
-    m.fit(X, y, max_rounds=rounds + 1)
-    t = np.diff(m.round_times_)[1:]  # first round excluded (page-in)
+def cpu_cores():
     cores = len(os.sched_getaffinity(0))
     omp = os.environ.get("OMP_NUM_THREADS")
     if omp and omp.isdigit():
         cores = min(cores, int(omp))
-    return dict(value=float(len(t) / t.sum()), unit="trees/s", cores=cores,
-                cpu_model=cpu_model(), kind="port",
-                sample=f"rounds 2-{rounds + 1} of the same {name} fit "
-                       f"({X.shape[0]}x{X.shape[1]}), oracle/oracle.c via OracleGBM")
+    return cores
+
+
+def run_cpu_baseline(name, rounds, data=None, model=None, Xp_sample=None):
+    """The oracle (C/OpenMP restatement of the reference path, serial where
+    the reference is serial) on this host: `rounds` rounds of the workload's
+    fit after an untimed first round (training trees/s, and the histogram
+    phase's rows x features/s over the same rounds), the time from fit() to
+    the first round (bin edges and codes), and the traversal of the GPU
+    model's whole ensemble over the first rows of the fresh predict batch
+    (predict rows/s; the trees equal the oracle's up to certified ties)."""
+    from oracle import model as om
+    X, y, params = data if data is not None else make_workload(name)
+    cores = cpu_cores()
+    _progress(f"cpu baseline: oracle on {name}, {rounds} timed rounds, {cores} threads")
+    p = dict(params)
+    p.pop("verbose", None)
+    m = om.OracleGBM(edge_threads=cores, **p)
+
+    def first_round_done(r, *_):
+        if r == 0:
+            om.hist_stats(reset=True)
+
+    t0 = time.perf_counter()
+    m.fit(X, y, max_rounds=rounds + 1, round_callback=first_round_done)
+    binning_s = m.round_times_[0] - t0
+    t = np.diff(m.round_times_)[1:]  # first round excluded (page-in)
+    hist_s, hist_rf = om.hist_stats()
+    out = dict(value=float(len(t) / t.sum()), unit="trees/s", cores=cores,
+               cpu_model=cpu_model(), kind="port",
+               sample=f"rounds 2-{rounds + 1} of the same {name} fit "
+                      f"({X.shape[0]}x{X.shape[1]}), oracle/oracle.c via OracleGBM",
+               binning_ms=round(1e3 * binning_s, 1),
+               hist_rows_x_features_per_s=round(hist_rf / hist_s) if hist_s > 0 else None)
+    if model is not None and Xp_sample is not None:
+        k = Xp_sample.shape[0]
+        t = time.perf_counter()
+        codes = om.bin_features(Xp_sample, model.bin_edges, model.feature_bin_counts,
+                                model._nan_bin_id, model.binning_strategy)
+        t_bin = time.perf_counter() - t
+        packed = {"features": model._packed_features, "thresholds": model._packed_thresholds,
+                  "values": model._packed_values, "left": model._packed_left,
+                  "right": model._packed_right, "offsets": model._tree_offsets}
+        t = time.perf_counter()
+        om.predict_all_trees(codes, packed, len(model.trees), model.learning_rate)
+        t_walk = time.perf_counter() - t
+        out["predict_rows_per_s"] = round(k / t_walk)
+        out["predict_rows_per_s_end_to_end"] = round(k / (t_walk + t_bin))
+        out["predict_sample"] = (f"first {k} rows of the fresh batch through the GPU fit's "
+                                 f"{len(model.trees)} trees, oracle_predict_all_trees "
+                                 f"(end to end adds oracle_bin_features)")
+    return out
 
 
 def main():
@@ -289,6 +340,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="dense_1m")
     ap.add_argument("--cpu-rounds", type=int, default=4)
+    ap.add_argument("--also-cpu-rounds", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--rounds-only", action="store_true",
                     help="skip the prediction and the end-to-end fit (profiler runs)")
@@ -347,8 +399,12 @@ def main():
             "sampler_gen": round(r["sampler"]["gen_ms"], 3),
         },
     }
+    if not a.no_cpu_baseline:
+        line["cpu_baseline"] = run_cpu_baseline(a.workload, a.cpu_rounds, data=r["data"],
+                                                model=r["model"], Xp_sample=r["Xp_sample"])
+    del r
     if a.also and a.also != a.workload:
-        r2 = run_gpu(a.also, a.also_steps, a.warmup, rounds_only=True)
+        r2 = run_gpu(a.also, a.also_steps, a.warmup, rounds_only=a.rounds_only)
         st2 = r2["stats"]
         line[a.also] = {
             "trees_per_s": round(a.also_steps / r2["elapsed"], 3),
@@ -364,10 +420,14 @@ def main():
             "roofline": hist_roofline(st2, a.also),
             "kernel_ms_per_step": {k: round(r2["breakdown"][f"{k}_ms"] / BREAKDOWN_ROUNDS, 3)
                                    for k in ("hist", "part", "split")},
+            "fit_end_to_end": r2["fit_full"],
+            "predict": r2["predict"],
         }
+        if not a.no_cpu_baseline:
+            line[a.also]["cpu_baseline"] = run_cpu_baseline(
+                a.also, a.also_cpu_rounds, data=r2["data"], model=r2["model"],
+                Xp_sample=r2["Xp_sample"])
         del r2
-    if not a.no_cpu_baseline:
-        line["cpu_baseline"] = run_cpu_baseline(a.workload, a.cpu_rounds)
     print(json.dumps(line), flush=True)
 
 

@@ -46,6 +46,7 @@ _SIGS = {
                             _f64, _f64, _P, _P, _P, _P, _P, _P, _P],
     "bsscl_mc_loss": [_P, _P],
     "bsscl_mc_get_scores": [_P, _P],
+    "bsscl_mc_get_grad_hess": [_P, _P, _P],
     "bsscl_predict": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _P],
     "bsscl_predict_tree": [_P, _i32, _P, _P, _P, _P, _P, _i32, _P],
     "bsscl_predict_noalloc": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _P],
@@ -286,6 +287,14 @@ class Engine:
         out = np.empty((K, n), np.float64)
         check(lib().bsscl_mc_get_scores(self.handle, ptr(out)))
         return out.T.copy()
+
+    def mc_grad_hess(self):
+        """The last mc_round's gradients and hessians, each (n, K)."""
+        n, K = self._mc
+        g = np.empty((K, n), np.float64)
+        h = np.empty((K, n), np.float64)
+        check(lib().bsscl_mc_get_grad_hess(self.handle, ptr(g), ptr(h)))
+        return g.T.copy(), h.T.copy()
 
     def boost_begin(self, y, w0, w1, base_score):
         y = np.ascontiguousarray(y, np.int64)

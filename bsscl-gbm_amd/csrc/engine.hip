@@ -2711,7 +2711,7 @@ int bsscl_mc_begin(bsscl_engine *E, const int64_t *y, int64_t n, int32_t n_class
   CHK(E->ghq.ensure((size_t)n));
   HIPCHK(hipMemcpyAsync(E->mc_y.p, yi.data(), (size_t)n * 4, hipMemcpyHostToDevice, E->st));
   HIPCHK(hipMemcpyAsync(E->mc_w.p, sample_weight, (size_t)n * 8, hipMemcpyHostToDevice, E->st));
-  HIPCHK(hipMemsetAsync(E->mc_F.p, 0, nk * 8, E->st));  // the reference starts from 0 (est:2950)
+  HIPCHK(hipMemsetAsync(E->mc_F.p, 0, nk * 8, E->st));  // the reference starts from 0 (est:2958)
   HIPCHK(hipStreamSynchronize(E->st));
   E->mc_K = n_classes;
   E->mc_m = 0;
@@ -2782,7 +2782,7 @@ int bsscl_mc_build_tree(bsscl_engine *E, int32_t k, const int32_t *feature_indic
   TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight, reg_lambda, gamma};
   E->set_base = 0;
   CHK(build_tree_core(E, nullptr, E->mc_m, feats, nb_sel, tp, out));
-  // F[:, k] += lr * tree(X) (est:2977), with the tree in the engine's columns.
+  // F[:, k] += lr * tree(X) (est:3029), with the tree in the engine's columns.
   CHK(upload_tree(E, out.features, out.thresholds, out.values, out.left, out.right,
                   *out.node_count, X.cols()));
   HIPCHK(launch_mc_apply(E->st, X.codes.p, X.ld, n, E->tree_d.p, learning_rate,
@@ -2812,6 +2812,17 @@ int bsscl_mc_get_scores(bsscl_engine *E, double *out) {
   HIPCHK(hipSetDevice(E->device));
   const size_t nk = (size_t)E->mat[0].n * (size_t)E->mc_K;
   HIPCHK(hipMemcpyAsync(out, E->mc_F.p, nk * 8, hipMemcpyDeviceToHost, E->st));
+  HIPCHK(hipStreamSynchronize(E->st));
+  return BSSCL_OK;
+}
+
+int bsscl_mc_get_grad_hess(bsscl_engine *E, double *grad_out, double *hess_out) {
+  if (!E || !grad_out || !hess_out) return set_error(BSSCL_EINVAL, "mc_get_grad_hess: null argument");
+  if (E->mc_K < 2 || E->mc_m <= 0) return set_error(BSSCL_EINVAL, "mc_get_grad_hess: no round");
+  HIPCHK(hipSetDevice(E->device));
+  const size_t nk = (size_t)E->mat[0].n * (size_t)E->mc_K;
+  HIPCHK(hipMemcpyAsync(grad_out, E->mc_G.p, nk * 8, hipMemcpyDeviceToHost, E->st));
+  HIPCHK(hipMemcpyAsync(hess_out, E->mc_H.p, nk * 8, hipMemcpyDeviceToHost, E->st));
   HIPCHK(hipStreamSynchronize(E->st));
   return BSSCL_OK;
 }

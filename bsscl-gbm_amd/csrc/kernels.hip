@@ -4016,10 +4016,39 @@ hipError_t launch_predict(hipStream_t st, const uint8_t *codes, int64_t ld,
 // Multiclass rounds (est:2949-3065).  Scores F are [K][n] float64, class k's
 // gradients G[k][i] and hessians H[k][i] likewise.  A row's softmax follows
 // the reference's NumPy order: F - max over the classes, exp, the sum over
-// the classes in class order, then one division per class.
+// the classes in the order NumPy's sum(axis=1) adds a contiguous row (below),
+// then one division per class.
 // ---------------------------------------------------------------------------
 #pragma clang fp contract(off)
 namespace {
+
+// Sum of e[0..K-1] in the order of NumPy's pairwise summation of a
+// contiguous run of K <= 16 doubles: below 8 terms one running sum in index
+// order; from 8 on, eight partial sums r[j] = e[j] (+ e[j + 8] when a second
+// whole block of eight exists, K = 16), combined as
+// ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7)), then the terms left
+// after the whole blocks added one by one in index order.
+__device__ __forceinline__ double numpy_row_sum(const double (&e)[kMcMaxK], int K) {
+  static_assert(kMcMaxK == 16, "the block structure below covers at most two blocks of eight");
+  if (K < 8) {
+    double s = e[0];
+#pragma unroll
+    for (int k = 1; k < 8; ++k)
+      if (k < K) s = __dadd_rn(s, e[k]);
+    return s;
+  }
+  double r[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = K == 16 ? __dadd_rn(e[j], e[j + 8]) : e[j];
+  double s = __dadd_rn(__dadd_rn(__dadd_rn(r[0], r[1]), __dadd_rn(r[2], r[3])),
+                       __dadd_rn(__dadd_rn(r[4], r[5]), __dadd_rn(r[6], r[7])));
+  if (K < 16) {
+#pragma unroll
+    for (int k = 8; k < 16; ++k)
+      if (k < K) s = __dadd_rn(s, e[k]);
+  }
+  return s;
+}
 
 // Order-preserving bits of a non-negative double.
 __device__ __forceinline__ unsigned long long nonneg_bits(double v) {
@@ -4038,7 +4067,8 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
 }  // namespace
 
 // grad_all = w * (p - onehot), hess_all = w * p * (1 - p) floored at 1e-8
-// (est:2966-2972); mx[2k], mx[2k + 1] collect the largest |g| and h of class
+// (softmax est:2327-2332 called at est:2996, gradients est:3013-3014, floor
+// est:3019); mx[2k], mx[2k + 1] collect the largest |g| and h of class
 // k over the rows (the fixed-point scale of its tree).
 __global__ __launch_bounds__(256) void k_mc_grad_hess(
     const double *__restrict__ F, const int32_t *__restrict__ y, const double *__restrict__ w,
@@ -4054,14 +4084,10 @@ __global__ __launch_bounds__(256) void k_mc_grad_hess(
     e[k] = (in && k < K) ? F[(int64_t)k * n + i] : 0.0;
     if (k < K) fmaxv = fmax(fmaxv, e[k]);
   }
-  double sum = 0.0;
 #pragma unroll
-  for (int k = 0; k < kMcMaxK; ++k) {
-    if (k < K) {
-      e[k] = exp(__dsub_rn(e[k], fmaxv));
-      sum = __dadd_rn(sum, e[k]);
-    }
-  }
+  for (int k = 0; k < kMcMaxK; ++k)
+    if (k < K) e[k] = exp(__dsub_rn(e[k], fmaxv));
+  const double sum = numpy_row_sum(e, K);
   const double wi = in ? w[i] : 0.0;
   const int32_t yi = in ? y[i] : -1;
 #pragma unroll
@@ -4090,7 +4116,7 @@ __global__ __launch_bounds__(256) void k_mc_grad_hess(
   }
 }
 
-// F[i] += lr * tree(x_i) for one class's scores (est:2977).
+// F[i] += lr * tree(x_i) for one class's scores (est:3029).
 __global__ __launch_bounds__(256) void k_mc_apply(const uint8_t *__restrict__ codes, int64_t ld,
                                                   int64_t n, const TreeNodeDev *__restrict__ tree,
                                                   double lr, double *__restrict__ Fk) {
@@ -4100,7 +4126,7 @@ __global__ __launch_bounds__(256) void k_mc_apply(const uint8_t *__restrict__ co
 }
 
 // Per block: the sum of log(clip(softmax(F_i))[y_i], 1e-15, 1 - 1e-15)
-// over its rows (est:2320-2325's multiclass form, est:2982).
+// over its rows (est:2335-2341, called at est:3035).
 __global__ __launch_bounds__(256) void k_mc_loss(const double *__restrict__ F,
                                                  const int32_t *__restrict__ y, int64_t n,
                                                  int32_t K, double *__restrict__ partials) {
@@ -4115,16 +4141,16 @@ __global__ __launch_bounds__(256) void k_mc_loss(const double *__restrict__ F,
       e[k] = k < K ? F[(int64_t)k * n + i] : 0.0;
       if (k < K) fmaxv = fmax(fmaxv, e[k]);
     }
-    double sum = 0.0, ey = 0.0;
+    double ey = 0.0;
     const int32_t yi = y[i];
 #pragma unroll
     for (int k = 0; k < kMcMaxK; ++k) {
       if (k < K) {
         e[k] = exp(__dsub_rn(e[k], fmaxv));
-        sum = __dadd_rn(sum, e[k]);
         if (k == yi) ey = e[k];
       }
     }
+    const double sum = numpy_row_sum(e, K);
     const double p = fmin(fmax(__ddiv_rn(ey, sum), 1e-15), 1.0 - 1e-15);
     v = log(p);
   }

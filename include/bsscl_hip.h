@@ -187,11 +187,11 @@ int bsscl_boost_grad_hess(bsscl_engine *eng, double *grad_out,
 /*
  * Multiclass rounds with the scores on the device.  Replace the NumPy
  * arithmetic of the reference's multiclass loop (est:2949-3065): the (n, K)
- * score matrix starting at 0 (est:2950), each round's softmax gradients and
- * hessians from the scores at the round's start (est:2962-2972, hessians
+ * score matrix starting at 0 (est:2958), each round's softmax gradients and
+ * hessians from the scores at the round's start (est:2996, 3013-3014, hessians
  * floored at 1e-8), each class's tree (the _build_tree_leafwise seam on those
- * gradients, est:2973-2976) and its score update F[:, k] += lr * tree (est:2977),
- * and the round's multiclass log-loss (est:2982).  Runs on training matrix 0.
+ * gradients, est:3016-3026) and its score update F[:, k] += lr * tree (est:3029),
+ * and the round's multiclass log-loss (est:3035).  Runs on training matrix 0.
  *   mc_begin       y int64[n] in [0, n_classes), sample_weight float64[n] > 0,
  *                  2 <= n_classes <= 16
  *   mc_round       the round's in-bag rows (int64[n_samples], shared by its
@@ -202,6 +202,9 @@ int bsscl_boost_grad_hess(bsscl_engine *eng, double *grad_out,
  *   mc_loss        -mean log(clip(softmax(F)[y], 1e-15, 1 - 1e-15))
  *   mc_get_scores  F as float64[n_classes * n], class by class (row i of
  *                  class k at k * n + i)
+ *   mc_get_grad_hess  the last mc_round's gradients and hessians (est:3013-3014,
+ *                  hessians after the 1e-8 floor of est:3019), float64[n_classes * n]
+ *                  each, laid out as mc_get_scores
  */
 int bsscl_mc_begin(bsscl_engine *eng, const int64_t *y, int64_t n, int32_t n_classes,
                    const double *sample_weight);
@@ -215,6 +218,7 @@ int bsscl_mc_build_tree(bsscl_engine *eng, int32_t k, const int32_t *feature_ind
                         int32_t *out_right, int32_t *out_node_count, double *out_split_gains);
 int bsscl_mc_loss(bsscl_engine *eng, double *out_loss);
 int bsscl_mc_get_scores(bsscl_engine *eng, double *out);
+int bsscl_mc_get_grad_hess(bsscl_engine *eng, double *grad_out, double *hess_out);
 
 /*
  * Ensemble prediction.  Replaces predict_all_trees_jit (est:863-884):

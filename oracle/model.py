@@ -46,12 +46,23 @@ def lib():
         L.oracle_predict_all_trees.argtypes = [P, ctypes.c_int, i64, i32, P, P,
                                                P, P, P, P, i32, f64, P]
         L.oracle_post_prune.argtypes = [P, P, P, P, f64, i32]
+        L.oracle_hist_stats.argtypes = [P, P, ctypes.c_int]
+        L.oracle_hist_stats.restype = None
         for name in ("oracle_bin_features", "oracle_build_tree_leafwise",
                      "oracle_predict_tree", "oracle_predict_all_trees"):
             getattr(L, name).restype = ctypes.c_int
         L.oracle_post_prune.restype = None
         _lib = L
     return _lib
+
+
+def hist_stats(reset=False):
+    """(seconds, row x feature updates) the builder's histogram phase took
+    since the last reset (the CPU baseline's histogram rate)."""
+    sec = ctypes.c_double()
+    rf = ctypes.c_int64()
+    lib().oracle_hist_stats(ctypes.byref(sec), ctypes.byref(rf), int(bool(reset)))
+    return sec.value, rf.value
 
 
 def _p(a):
@@ -292,6 +303,14 @@ def binary_grad_hess(F, y, w, grad, hess):
     p = binary_proba(F)
     grad[:] = w * (p - y)
     hess[:] = w * p * (1.0 - p)
+
+
+def multiclass_grad_hess(proba, y_onehot, sample_weight):
+    """Softmax gradients and hessians of every class, (n, K) each:
+    est:3013-3014, and the hessian floor of est:3019 applied to every class."""
+    grad_all = sample_weight[:, None] * (proba - y_onehot)
+    hess_all = sample_weight[:, None] * proba * (1.0 - proba)
+    return grad_all, np.maximum(hess_all, 1e-8)
 
 
 def binary_logloss(y, F):
@@ -551,11 +570,10 @@ class OracleGBM:
                 feat_idx = np.sort(all_feats[:f_sub]).copy()
             else:
                 feat_idx = all_feats.copy()
-            grad_all = sample_weight[:, None] * (proba - y_onehot)
-            hess_all = sample_weight[:, None] * proba * (1.0 - proba)
+            grad_all, hess_all = multiclass_grad_hess(proba, y_onehot, sample_weight)
             for k in range(K):
                 grad_k = np.ascontiguousarray(grad_all[:, k])
-                hess_k = np.maximum(np.ascontiguousarray(hess_all[:, k]), 1e-8)
+                hess_k = np.ascontiguousarray(hess_all[:, k])
                 tree = build_tree(X_bin, grad_k, hess_k, sample_idx, feat_idx,
                                   self.max_leaves, self.max_depth,
                                   self.min_samples_leaf, self.min_child_weight,

@@ -19,6 +19,7 @@
  * Build: oracle/Makefile -> oracle/_build/liboracle.so
  */
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -116,6 +117,23 @@ static inline int32_t xbin_at(const void *xb, int u16, int64_t row, int32_t p,
                : (int32_t)((const uint8_t *)xb)[row * p + j];
 }
 
+/* Wall time spent in build_hist and the (row, feature) updates it made,
+ * since the last oracle_hist_stats(..., reset=1): the CPU baseline's
+ * histogram rows x features per second.  Updated by the calling thread
+ * only (build_hist parallelises inside). */
+static double g_hist_seconds = 0.0;
+static int64_t g_hist_row_features = 0;
+
+void oracle_hist_stats(double *seconds, int64_t *row_features, int reset)
+{
+    if (seconds) *seconds = g_hist_seconds;
+    if (row_features) *row_features = g_hist_row_features;
+    if (reset) {
+        g_hist_seconds = 0.0;
+        g_hist_row_features = 0;
+    }
+}
+
 /* Histogram of rows indices[start:end) for the selected features into slot
  * `slot` (est:581-596 root, est:722-737 smaller child). */
 static void build_hist(const void *xb, int u16, int32_t p, const double *grad,
@@ -126,6 +144,7 @@ static void build_hist(const void *xb, int u16, int32_t p, const double *grad,
                        int32_t max_bins, int32_t slot)
 {
     int32_t jj;
+    const double t0 = omp_get_wtime();
 #pragma omp parallel for schedule(dynamic, 1)
     for (jj = 0; jj < n_sel; ++jj) {
         int32_t j = feats[jj];
@@ -146,6 +165,8 @@ static void build_hist(const void *xb, int u16, int32_t p, const double *grad,
             H[bv] += hess[ii];
         }
     }
+    g_hist_seconds += omp_get_wtime() - t0;
+    g_hist_row_features += (end - start) * (int64_t)n_sel;
 }
 
 /* Best split scan over the selected features of one slot (est:598-621 root,

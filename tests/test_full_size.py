@@ -1,14 +1,14 @@
 """Parity at the benchmark workloads' full sizes (bench.py:make_workload).
 
-* dense_1m (1,000,000 x 28, 5% NaN, depth 6): the first 10 rounds of the
-  workload's fit.
+* dense_1m (1,000,000 x 28, 5% NaN, depth 6): the workload's complete
+  100-round fit.
 * imbalanced (284,807 x 30, 0.17% positives, balanced_sqrt) and sparse_hd
   (100,000 x 100, 90% zeros, balanced_sqrt): the complete fits, 200 and 300
   trees.
 * stress_10m (10,000,000 x 50, 10 columns 70% NaN, depth 8): bin edges and
-  codes of all 10M rows against the oracle's; the first two rounds of the
+  codes of all 10M rows against the oracle's; the first ten rounds of the
   workload's fit; one depth-8 tree from 5M rows x 35 features; and the
-  500-tree fit scored on a fresh 10M-row batch, checked on its first 1M rows
+  500-tree fit scored on a fresh 10M-row batch, checked on all 10M rows
   (codes bit-exact, raw scores within 1e-12, predict_proba within 1e-6).
 
 Every fit compares each round in lockstep and end to end with the oracle,
@@ -52,8 +52,8 @@ def _fit_and_follow(engine, name, n_estimators=None, eval_rows=200_000):
     return est, ref
 
 
-def test_dense_1m_rounds(engine):
-    _fit_and_follow(engine, "dense_1m", n_estimators=10)
+def test_dense_1m_full_fit(engine):
+    _fit_and_follow(engine, "dense_1m")
 
 
 @pytest.mark.parametrize("name", ["imbalanced", "sparse_hd"])
@@ -85,7 +85,7 @@ def test_stress_10m_binning(engine):
 
 
 def test_stress_10m_rounds(engine):
-    _fit_and_follow(engine, "stress_10m", n_estimators=2, eval_rows=500_000)
+    _fit_and_follow(engine, "stress_10m", n_estimators=10, eval_rows=500_000)
 
 
 def test_stress_10m_tree(engine):
@@ -112,7 +112,7 @@ def test_stress_10m_tree(engine):
 
 def test_stress_10m_inference(engine):
     """The workload's 500-tree fit, then predict_proba of a fresh 10M-row
-    batch (default_rng(5)), checked on its first 1M rows."""
+    batch (default_rng(5)), checked on every row."""
     from bsscl_gbm import HybridHistGBMNumbaV1_0_1
     from bsscl_gbm import estimator as est_mod
     X, y, params = _workload("stress_10m")
@@ -124,9 +124,9 @@ def test_stress_10m_inference(engine):
     p = est.predict_proba(Xp)
     assert p.shape == (n, 2) and np.all(np.isfinite(p))
     eng = est_mod._engine(0)
-    k = 1_000_000
-    codes = eng.get_codes(1, n, F)[:k]
-    want = om.bin_features(Xp[:k], est.bin_edges, est.feature_bin_counts, est._nan_bin_id,
+    k = n
+    codes = eng.get_codes(1, n, F)
+    want = om.bin_features(Xp, est.bin_edges, est.feature_bin_counts, est._nan_bin_id,
                            "hybrid")
     # A NaN feature's value above its training maximum gets the reference
     # code bin_counts = 256 (uint16 codes, est:2163-2166); every threshold
@@ -141,5 +141,5 @@ def test_stress_10m_inference(engine):
     np.testing.assert_allclose(F_dev[:k], F_ref, rtol=0, atol=1e-12)
     p_ref = 1.0 / (1.0 + np.exp(-np.clip(F_ref + est.base_score_, -500, 500)))
     np.testing.assert_allclose(p[:k, 1], p_ref, rtol=0, atol=1e-6)
-    print(f"[result] stress_10m inference: 500 trees over {n} rows; first {k} rows: codes "
+    print(f"[result] stress_10m inference: 500 trees over {n} rows; all {k} rows: codes "
           f"identical, max |dF| {np.max(np.abs(F_dev[:k] - F_ref)):.3g}", flush=True)

@@ -348,6 +348,16 @@ def _fit_case(name):
         X[y == 1, :6] += 0.8
         params = dict(n_estimators=12, max_depth=6, n_bins=255, scale_pos_weight=6.0,
                       objective="binary", random_state=0)
+    elif name == "confident_400":
+        # A long fit on separable data (12% positives, balanced_sqrt): the
+        # late rounds' gradients and hessians of most rows are far below
+        # the class weight that scales the fixed-point values, and a small
+        # min_child_weight lets the trees keep splitting those rows.
+        rng = np.random.default_rng(0)
+        X = rng.standard_normal((30000, 8)).astype(np.float32)
+        y = ((X[:, 0] + 0.5 * X[:, 1]) > 1.3).astype(np.int64)
+        params = dict(n_estimators=400, max_depth=6, learning_rate=1.0, n_bins=255,
+                      min_child_weight=1e-3, class_weight="balanced_sqrt", random_state=0)
     elif name == "nan_imbalanced":
         X, y = make_data(30000, 30, seed=12, nan_frac=0.05)
         y = (np.random.default_rng(1).random(30000) < 0.03).astype(np.int64)
@@ -363,7 +373,7 @@ def _fit_case(name):
 
 
 @pytest.mark.parametrize("name", ["config1", "nan_imbalanced", "sparse", "defaults_28",
-                                  "top_bin_28", "scale_pos_weight"])
+                                  "top_bin_28", "scale_pos_weight", "confident_400"])
 def test_fit_lockstep_and_end_to_end(engine, name):
     """Every round of the oracle's fit, rebuilt by the engine from the same
     gradients, rows and features (lockstep), and the estimator's own tree of
@@ -378,6 +388,10 @@ def test_fit_lockstep_and_end_to_end(engine, name):
     print(rep.line(name), flush=True)
     assert rep.rounds == ref.n_estimators == len(est.trees)
     fitcmp.assert_fit_equal(ref, est, X)
+    if name == "confident_400":
+        print(f"[result] confident_400: final training loss {est.train_loss_history_[-1]:.3g}",
+              flush=True)
+        assert est.train_loss_history_[-1] < 1e-4
     if name in ("defaults_28", "top_bin_28"):
         from bsscl_gbm import estimator as est_mod
         assert est.n_bins == 256 and est._max_bins == 257

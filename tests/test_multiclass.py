@@ -1,17 +1,24 @@
 """Multiclass softmax boosting (est:2949-3065; predict est:3293-3315).
 
 CPU tests pin the oracle's multiclass loop by checks that do not restate
-it: the recorded training loss equals the loss recomputed from the fitted
-trees by the independent traversal; the K trees of a round share one
-bagging draw, which equals a fresh RandomState's shuffle stream; softmax
-gradients sum to zero over the classes of a row; the K-dependent parameter
-rules give hand-derived values.  GPU tests rebuild every oracle tree on the
-engine from the same inputs and compare the estimator's own trees, losses
-and predict_proba with the oracle's, following certified gain ties
-(tests/fitcmp.py).
+it: every round's gradients and hessians equal central finite differences
+of the weighted softmax cross-entropy sum_i w_i (logsumexp(F_i) - F_i[y_i])
+(scipy's logsumexp) in each class's score, at the scores rebuilt by the
+independent traversal, under balanced_sqrt weights, and the hessian floor
+of 1e-8 holds exactly where w p (1 - p) falls below it; the recorded
+training loss equals the loss recomputed from the fitted trees; the K trees
+of a round share one bagging draw, which equals a fresh RandomState's
+shuffle stream; the K-dependent parameter rules give hand-derived values;
+NumPy's row sum over the classes adds in the pairwise order the device
+kernels restate.  GPU tests rebuild every oracle tree on the engine from the
+same inputs and compare the estimator's own trees, losses and predict_proba
+with the oracle's, following certified gain ties (tests/fitcmp.py), up to
+16 classes, and compare the device's gradients and hessians with NumPy's on
+the device's own scores.
 """
 import numpy as np
 import pytest
+from scipy.special import logsumexp
 
 import fitcmp
 from oracle import model as om
@@ -25,7 +32,7 @@ def _mc_data(n, F, K, seed, nan_frac=0.0):
     y = np.argmax(logits, axis=1)
     if nan_frac:
         X[rng.random((n, F)) < nan_frac] = np.nan
-    labels = np.array([3, 7, 11, 20, 21, 40, 41, 50, 60, 70, 80, 90])[:K]
+    labels = np.array([3, 7, 11, 20, 21, 40, 41, 50, 60, 70, 80, 90, 91, 95, 99, 120])[:K]
     return X, labels[y]
 
 
@@ -75,6 +82,112 @@ def test_oracle_multiclass_rounds_share_one_bagging_draw():
         assert min(seen[4 * m + k][3].min() for k in range(4)) >= 1e-8
 
 
+def _weighted_ce(F, yi, w):
+    """Per-row weighted softmax cross-entropy w_i (logsumexp(F_i) - F_i[y_i])."""
+    return w * (logsumexp(F, axis=1) - F[np.arange(len(yi)), yi])
+
+
+def _fd_grad_hess(F, yi, w, eps1=1e-5, eps2=1e-3):
+    """Central differences of the per-row loss in each class's score."""
+    n, K = F.shape
+    G, H = np.empty((n, K)), np.empty((n, K))
+    base = _weighted_ce(F, yi, w)
+    for k in range(K):
+        d1, d2 = np.zeros(K), np.zeros(K)
+        d1[k], d2[k] = eps1, eps2
+        G[:, k] = (_weighted_ce(F + d1, yi, w) - _weighted_ce(F - d1, yi, w)) / (2 * eps1)
+        H[:, k] = (_weighted_ce(F + d2, yi, w) - 2 * base + _weighted_ce(F - d2, yi, w)) / eps2 ** 2
+    return G, H
+
+
+def _balanced_sqrt(yi, K):
+    n = len(yi)
+    counts = np.bincount(yi, minlength=K)
+    return (n / (K * np.maximum(counts, 1)))[yi] ** 0.35
+
+
+@pytest.mark.parametrize("K", [3, 5])
+def test_oracle_multiclass_grad_hess_are_loss_derivatives(K):
+    """Every round's (g, h) of every class, as handed to the tree builder,
+    against finite differences of the weighted softmax loss at the scores
+    rebuilt from the fitted trees (balanced_sqrt weights on unequal classes,
+    so a missing weight on either fails)."""
+    X, y = _mc_data(2400, 6, K, seed=30 + K)
+    seen = {}
+    m = om.OracleGBM(n_estimators=4, max_depth=4, learning_rate=0.6, n_bins=64,
+                     class_weight="balanced_sqrt", random_state=4)
+    m.fit(X, y, round_callback=lambda r, k, g, h, si, fi, t: seen.__setitem__((r, k),
+                                                                             (g.copy(), h.copy())))
+    yi = np.searchsorted(m.classes_, y)
+    w = _balanced_sqrt(yi, K)
+    assert np.ptp(w) > 0.05  # the weights differ between classes
+    F = np.zeros((len(y), K))
+    for r in range(4):
+        G, H = _fd_grad_hess(F, yi, w)
+        for k in range(K):
+            g, h = seen[(r, k)]
+            np.testing.assert_allclose(g, G[:, k], rtol=0, atol=1e-8 * w.max(),
+                                       err_msg=f"g round {r} class {k}")
+            np.testing.assert_allclose(h, np.maximum(H[:, k], 1e-8), rtol=0,
+                                       atol=1e-6 * w.max(), err_msg=f"h round {r} class {k}")
+        for k in range(K):  # the scores after round r, by the independent walk
+            packed = om.pack_trees([m.mc_trees[k][r]])
+            F[:, k] += om.predict_all_trees(m.X_bin_, packed, 1, m.learning_rate)
+
+
+def test_oracle_multiclass_hessian_floor():
+    """Confident rows: w p (1 - p) below 1e-8 is floored to exactly 1e-8
+    (est:3019), elsewhere the hessian is the loss's second derivative."""
+    rng = np.random.default_rng(7)
+    n, K = 4000, 4
+    yi = rng.integers(0, K, n)
+    w = _balanced_sqrt(yi, K)
+    F = rng.standard_normal((n, K))
+    F[: n // 2] *= 25.0  # margins of tens: p of the losing classes ~ e^-50
+    e = np.exp(F - F.max(axis=1, keepdims=True))
+    proba = e / e.sum(axis=1, keepdims=True)
+    G, H = om.multiclass_grad_hess(proba, np.eye(K)[yi], w)
+    raw = w[:, None] * proba * (1.0 - proba)
+    floored = raw < 1e-8
+    assert floored.sum() > n // 4 and (~floored).sum() > n
+    assert np.all(H[floored] == 1e-8)
+    Gfd, Hfd = _fd_grad_hess(F, yi, w)
+    np.testing.assert_allclose(G, Gfd, rtol=0, atol=1e-7 * w.max())
+    np.testing.assert_allclose(H[~floored], Hfd[~floored], rtol=0, atol=1e-5 * w.max())
+
+
+def _numpy_row_sum_order(e):
+    """The order the device kernels add a row's K <= 16 class terms in:
+    one running sum below 8 terms; else eight partial sums over whole blocks
+    of eight, combined pairwise, then the remaining terms in order."""
+    K = len(e)
+    if K < 8:
+        s = e[0]
+        for j in range(1, K):
+            s = s + e[j]
+        return s
+    r = [e[j] + e[j + 8] if K == 16 else e[j] for j in range(8)]
+    s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]))
+    for j in range(8, K if K < 16 else 8):
+        s = s + e[j]
+    return s
+
+
+def test_numpy_row_sum_is_pairwise_from_eight_classes():
+    rng = np.random.default_rng(8)
+    for K in range(2, 17):
+        F = 3.0 * rng.standard_normal((3000, K))
+        e = np.exp(F - F.max(axis=1, keepdims=True))
+        want = e.sum(axis=1, keepdims=True)[:, 0]
+        got = np.array([_numpy_row_sum_order(row) for row in e])
+        np.testing.assert_array_equal(got, want, err_msg=f"K={K}")
+        if K >= 8:  # the class-order sum differs somewhere
+            seq = np.zeros(len(e))
+            for k in range(K):
+                seq = seq + e[:, k]
+            assert np.any(seq != want), K
+
+
 def test_oracle_multiclass_adaptive_parameters():
     """est:1925-2029 for K = 7 and K = 12 on 2000 rows (hand-derived)."""
     for K, depth, lr, n_est in [(7, 6, 0.20 * 0.85, 250), (12, 7, 0.20 * 0.75, 250)]:
@@ -91,7 +204,8 @@ def test_oracle_multiclass_adaptive_parameters():
 # GPU
 # ---------------------------------------------------------------------------
 @pytest.mark.gpu
-@pytest.mark.parametrize("K,n,nan", [(3, 6000, 0.0), (7, 12000, 0.1)])
+@pytest.mark.parametrize("K,n,nan", [(3, 6000, 0.0), (7, 12000, 0.1), (12, 16000, 0.05),
+                                     (16, 20000, 0.0)])
 def test_multiclass_lockstep_and_end_to_end(engine, K, n, nan):
     from bsscl_gbm import HybridHistGBMNumbaV1_0_1
     print(f"[case] multiclass K={K} n={n} nan={nan}", flush=True)
@@ -125,3 +239,40 @@ def test_multiclass_host_path_matches_oracle(engine, monkeypatch):
     assert rep.rounds == params["n_estimators"]
     Xp, _ = _mc_data(3000, 9, 3, seed=103)
     fitcmp.assert_fit_equal(ref, est, Xp)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K", [3, 8, 12, 16])
+def test_multiclass_device_grad_hess_equal_numpy(engine, K):
+    """The device's softmax gradients and hessians against the reference's
+    NumPy expressions (est:2327-2332, 3013-3014, 3019) on the device's own
+    scores after two rounds: within 4 ulp everywhere; NumPy's and the
+    device's exp may round differently, so the share of bit-identical values
+    is printed and must stay high."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    from bsscl_gbm import estimator as est_mod
+    print(f"[case] multiclass device grad/hess K={K}", flush=True)
+    X, y = _mc_data(20000, 9, K, seed=40 + K)
+    params = dict(n_estimators=2, max_depth=5, n_bins=255, random_state=5,
+                  class_weight="balanced_sqrt", learning_rate=0.7)
+    est = HybridHistGBMNumbaV1_0_1(verbose=False, **params).fit(X, y)
+    eng = est_mod._engine(0)
+    yi = np.searchsorted(est.classes_, y)
+    n = len(y)
+    w = _balanced_sqrt(yi, K)
+    eng.mc_round(np.arange(n, dtype=np.int64))  # gradients at the fitted scores
+    g_dev, h_dev = eng.mc_grad_hess()
+    F = eng.mc_scores()
+    assert np.ptp(F) > 0.5
+    F_shifted = F - F.max(axis=1, keepdims=True)
+    exp_F = np.exp(F_shifted)
+    proba = exp_F / exp_F.sum(axis=1, keepdims=True)
+    g_np, h_np = om.multiclass_grad_hess(proba, np.eye(K)[yi], w)
+    for name, a, b in (("grad", g_dev, g_np), ("hess", h_dev, h_np)):
+        ulp = np.spacing(np.maximum(np.abs(a), np.abs(b)))
+        worst = float(np.max(np.abs(a - b) / ulp))
+        same = float(np.mean(a == b))
+        print(f"[result] multiclass K={K} {name}: {100 * same:.3f}% bit-identical, "
+              f"max {worst:.1f} ulp", flush=True)
+        assert worst <= 4.0, (name, worst)
+        assert same >= 0.9, (name, same)
