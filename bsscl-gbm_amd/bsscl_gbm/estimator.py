@@ -426,9 +426,10 @@ class HybridHistGBMNumbaV1_0_1:
         if self.class_weight not in ('balanced', 'balanced_sqrt'):
             return 1.0, 1.0
         n = len(y)
+        n1 = int(np.count_nonzero(y))  # y holds 0 and 1
         w = []
         for k in range(2):
-            n_k = np.sum(y == k)
+            n_k = n1 if k == 1 else n - n1
             w_k = n / (2 * max(n_k, 1))
             if self.class_weight == 'balanced_sqrt':
                 w_k = w_k ** 0.35
@@ -503,42 +504,14 @@ class HybridHistGBMNumbaV1_0_1:
             sample_weight[y == 1] = self.scale_pos_weight
         eng = _engine(self._device_index())
         with eng.lock:
-            t0 = time.perf_counter()
-            # Unweighted edges come from the device (X is staged once and binned
-            # from there); the weighted-quantile branch stays on the host.
-            X = np.ascontiguousarray(X)
-            staged = sample_weight is None
-            if staged:
-                eng.stage_features(X)
+            # The bagging stream (est:2502-2517) starts drawing now, so that its
+            # first rounds are ready when the boosting loop begins: the draws
+            # run on host threads while the device bins X.
+            sampler = self._make_sampler(eng, rng, len(y))
             try:
-                self.bin_edges, self.feature_bin_counts = self._build_bin_edges(
-                    X, sample_weight=sample_weight, eng=eng if staged else None)
-                self._max_bins = int(np.max(self.feature_bin_counts))
-                if self._max_bins > 257:
-                    raise NotImplementedError(
-                        f"n_bins={self.n_bins} gives {self._max_bins} bins for some feature; "
-                        "the MI355X engine holds at most 257 bins per feature (n_bins <= 256)")
-                if staged:
-                    eng.bin_staged(0, X.shape[0], X.shape[1], X.dtype == np.float64, self.bin_edges,
-                                   self.feature_bin_counts, self._nan_bin_id)
-                else:
-                    eng.bin_features(0, X, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
+                self._fit_locked(eng, X, y, X_val, y_val, sample_weight, sampler)
             finally:
-                if staged:
-                    eng.release_staged()
-            self.times['binning'] = (time.perf_counter() - t0) * 1000
-            n_val = 0
-            if X_val is not None and y_val is not None:
-                eng.bin_features(1, X_val, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
-                n_val = X_val.shape[0]
-
-            t0_train = time.perf_counter()
-            if self._is_multiclass:
-                self._fit_multiclass(eng, y, n_val, y_val, rng)
-            else:
-                self._fit_binary(eng, y, n_val, y_val, rng)
-            self.times['training'] = (time.perf_counter() - t0_train) * 1000
-
+                sampler.close()
         self._pack_trees()
         self._compute_feature_importances()
         if self.verbose:
@@ -548,7 +521,61 @@ class HybridHistGBMNumbaV1_0_1:
             print(f"    Total:    {self.times['binning'] + self.times['training']:.2f} ms")
         return self
 
-    def _fit_binary(self, eng, y, n_val, y_val, rng):
+    def _make_sampler(self, eng, rng, n_samples):
+        """The native RandomState.shuffle stream for this fit's rounds: rows
+        and features per round (est:2502-2517), from rng's current state.
+        Binary fits hand the draws to the device (the engine applies the
+        swaps); multiclass fits take the rows back on the host."""
+        n_features = self.n_features_in_
+        n_sub = max(1, int(n_samples * self.subsample))
+        f_sub = max(1, int(n_features * self.colsample_bytree))
+        do_rows = self.subsample < 1.0
+        do_feats = self.colsample_bytree < 1.0
+        return _native.Sampler(rng.get_state(), n_samples,
+                               n_sub if do_rows else n_samples, do_rows,
+                               n_features, f_sub if do_feats else n_features,
+                               do_feats, int(self.n_estimators),
+                               device_rows=not self._is_multiclass, device=eng.device)
+
+    def _fit_locked(self, eng, X, y, X_val, y_val, sample_weight, sampler):
+        """Binning and the boosting loop, with the engine's lock held."""
+        t0 = time.perf_counter()
+        # Unweighted edges come from the device (X is staged once and binned
+        # from there); the weighted-quantile branch stays on the host.
+        X = np.ascontiguousarray(X)
+        staged = sample_weight is None
+        if staged:
+            eng.stage_features(X)
+        try:
+            self.bin_edges, self.feature_bin_counts = self._build_bin_edges(
+                X, sample_weight=sample_weight, eng=eng if staged else None)
+            self._max_bins = int(np.max(self.feature_bin_counts))
+            if self._max_bins > 257:
+                raise NotImplementedError(
+                    f"n_bins={self.n_bins} gives {self._max_bins} bins for some feature; "
+                    "the MI355X engine holds at most 257 bins per feature (n_bins <= 256)")
+            if staged:
+                eng.bin_staged(0, X.shape[0], X.shape[1], X.dtype == np.float64, self.bin_edges,
+                               self.feature_bin_counts, self._nan_bin_id)
+            else:
+                eng.bin_features(0, X, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
+        finally:
+            if staged:
+                eng.release_staged()
+        self.times['binning'] = (time.perf_counter() - t0) * 1000
+        n_val = 0
+        if X_val is not None and y_val is not None:
+            eng.bin_features(1, X_val, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
+            n_val = X_val.shape[0]
+
+        t0_train = time.perf_counter()
+        if self._is_multiclass:
+            self._fit_multiclass(eng, y, n_val, y_val, sampler)
+        else:
+            self._fit_binary(eng, y, n_val, y_val, sampler)
+        self.times['training'] = (time.perf_counter() - t0_train) * 1000
+
+    def _fit_binary(self, eng, y, n_val, y_val, sampler):
         n_samples = len(y)
         n_features = self.n_features_in_
         w0, w1 = self._class_weight_pair(y)
@@ -557,16 +584,7 @@ class HybridHistGBMNumbaV1_0_1:
         p0 = np.clip(weighted_mean, 1e-7, 1.0 - 1e-7)
         self.base_score_ = np.log(p0 / (1.0 - p0))
         F_val = np.full(n_val, self.base_score_) if n_val else None
-        n_sub = max(1, int(n_samples * self.subsample))
-        f_sub = max(1, int(n_features * self.colsample_bytree))
-        do_rows = self.subsample < 1.0
-        do_feats = self.colsample_bytree < 1.0
         eng.boost_begin(y, w0, w1, self.base_score_)
-        sampler = _native.Sampler(rng.get_state(), n_samples,
-                                  n_sub if do_rows else n_samples, do_rows,
-                                  n_features, f_sub if do_feats else n_features,
-                                  do_feats, int(self.n_estimators),
-                                  device_rows=True, device=eng.device)
         best_val_loss = np.inf
         rounds_no_improve = 0
         hook = getattr(self, '_round_hook', None)
@@ -611,7 +629,6 @@ class HybridHistGBMNumbaV1_0_1:
         finally:
             eng.set_pipeline(False)
             self._live_sampler = None
-            sampler.close()
         if hook is not None:
             hook(self.n_estimators, eng)
         self.n_trees_fitted_ = len(self.trees)
@@ -652,7 +669,7 @@ class HybridHistGBMNumbaV1_0_1:
             w[y == k] = w_k
         return w
 
-    def _fit_multiclass(self, eng, y, n_val, y_val, rng):
+    def _fit_multiclass(self, eng, y, n_val, y_val, sampler):
         """K trees per round from softmax gradients (est:2949-3065).  The
         host keeps the reference's NumPy arithmetic on the (n, K) scores;
         every tree is built and applied to all rows on the device."""
@@ -667,84 +684,74 @@ class HybridHistGBMNumbaV1_0_1:
         if n_val:
             F_val = np.zeros((n_val, K), dtype=np.float64)
             y_val_onehot = np.eye(K, dtype=np.float64)[y_val]
-        n_sub = max(1, int(n_samples * self.subsample))
-        f_sub = max(1, int(n_features * self.colsample_bytree))
-        do_rows = self.subsample < 1.0
-        do_feats = self.colsample_bytree < 1.0
         sample_weight = self._class_weight_vector(y)
         self.mc_trees = [[] for _ in range(K)]
         best_val_loss = np.inf
         rounds_no_improve = 0
         # The reference's rng.shuffle stream (est:2502-2517), one draw per
-        # round shared by the K trees; rows come back in the reference's order.
-        sampler = _native.Sampler(rng.get_state(), n_samples,
-                                  n_sub if do_rows else n_samples, do_rows,
-                                  n_features, f_sub if do_feats else n_features,
-                                  do_feats, int(self.n_estimators), device=eng.device)
+        # round shared by the K trees (the sampler made by fit); rows come
+        # back in the reference's order.
         # Up to MC_DEVICE_MAX_CLASSES classes the scores, gradients, score
         # updates and loss stay on the device (the engine's multiclass
         # rounds); more classes keep the (n, K) arithmetic on the host.
         if on_device:
             eng.mc_begin(y, K, sample_weight)
-        try:
-            for m in range(self.n_estimators):
-                if on_device:
-                    sample_idx, feat_idx = sampler.next()
-                    eng.mc_round(sample_idx)
-                    for k in range(K):
-                        tree = eng.mc_build_tree(k, feat_idx, self.max_leaves, self.max_depth,
-                                                 self.min_samples_leaf, self.min_child_weight,
-                                                 self.feature_bin_counts, self._max_bins,
-                                                 self.reg_lambda, self.gamma,
-                                                 self.learning_rate)
-                        self.mc_trees[k].append(tree)
-                        if F_val is not None:
-                            F_val[:, k] += self.learning_rate * eng.predict_tree(1, n_val, tree)
-                    train_loss = eng.mc_loss()
+        for m in range(self.n_estimators):
+            if on_device:
+                sample_idx, feat_idx = sampler.next()
+                eng.mc_round(sample_idx)
+                for k in range(K):
+                    tree = eng.mc_build_tree(k, feat_idx, self.max_leaves, self.max_depth,
+                                             self.min_samples_leaf, self.min_child_weight,
+                                             self.feature_bin_counts, self._max_bins,
+                                             self.reg_lambda, self.gamma,
+                                             self.learning_rate)
+                    self.mc_trees[k].append(tree)
+                    if F_val is not None:
+                        F_val[:, k] += self.learning_rate * eng.predict_tree(1, n_val, tree)
+                train_loss = eng.mc_loss()
+            else:
+                proba = self._softmax(F_train)
+                sample_idx, feat_idx = sampler.next()
+                grad_all = sample_weight[:, None] * (proba - y_onehot)
+                hess_all = sample_weight[:, None] * proba * (1.0 - proba)
+                for k in range(K):
+                    grad_k = np.ascontiguousarray(grad_all[:, k])
+                    hess_k = np.maximum(np.ascontiguousarray(hess_all[:, k]), 1e-8)
+                    tree = eng.build_tree(grad_k, hess_k, sample_idx, feat_idx,
+                                          self.max_leaves, self.max_depth,
+                                          self.min_samples_leaf, self.min_child_weight,
+                                          self.feature_bin_counts, self._max_bins,
+                                          self.reg_lambda, self.gamma)
+                    self.mc_trees[k].append(tree)
+                    F_train[:, k] += self.learning_rate * eng.predict_tree(0, n_samples, tree)
+                    if F_val is not None:
+                        F_val[:, k] += self.learning_rate * eng.predict_tree(1, n_val, tree)
+                train_loss = self._compute_multiclass_logloss(y_onehot, F_train)
+            self.train_loss_history_.append(train_loss)
+            val_loss = None
+            if F_val is not None:
+                val_loss = self._compute_multiclass_logloss(y_val_onehot, F_val)
+                self.val_loss_history_.append(val_loss)
+            if self.verbose and ((m + 1) % 20 == 0 or m == 0):
+                msg = (f"  ✓ Round {m+1:>3}/{self.n_estimators}  |  {K} trees  |  "
+                       f"train-loss: {train_loss:.6f}")
+                if val_loss is not None:
+                    msg += f"  |  val-loss: {val_loss:.6f}"
+                print(msg)
+            if self.early_stopping_rounds is not None and val_loss is not None:
+                if val_loss < best_val_loss:
+                    best_val_loss = val_loss
+                    self.best_iteration_ = m
+                    rounds_no_improve = 0
                 else:
-                    proba = self._softmax(F_train)
-                    sample_idx, feat_idx = sampler.next()
-                    grad_all = sample_weight[:, None] * (proba - y_onehot)
-                    hess_all = sample_weight[:, None] * proba * (1.0 - proba)
-                    for k in range(K):
-                        grad_k = np.ascontiguousarray(grad_all[:, k])
-                        hess_k = np.maximum(np.ascontiguousarray(hess_all[:, k]), 1e-8)
-                        tree = eng.build_tree(grad_k, hess_k, sample_idx, feat_idx,
-                                              self.max_leaves, self.max_depth,
-                                              self.min_samples_leaf, self.min_child_weight,
-                                              self.feature_bin_counts, self._max_bins,
-                                              self.reg_lambda, self.gamma)
-                        self.mc_trees[k].append(tree)
-                        F_train[:, k] += self.learning_rate * eng.predict_tree(0, n_samples, tree)
-                        if F_val is not None:
-                            F_val[:, k] += self.learning_rate * eng.predict_tree(1, n_val, tree)
-                    train_loss = self._compute_multiclass_logloss(y_onehot, F_train)
-                self.train_loss_history_.append(train_loss)
-                val_loss = None
-                if F_val is not None:
-                    val_loss = self._compute_multiclass_logloss(y_val_onehot, F_val)
-                    self.val_loss_history_.append(val_loss)
-                if self.verbose and ((m + 1) % 20 == 0 or m == 0):
-                    msg = (f"  ✓ Round {m+1:>3}/{self.n_estimators}  |  {K} trees  |  "
-                           f"train-loss: {train_loss:.6f}")
-                    if val_loss is not None:
-                        msg += f"  |  val-loss: {val_loss:.6f}"
-                    print(msg)
-                if self.early_stopping_rounds is not None and val_loss is not None:
-                    if val_loss < best_val_loss:
-                        best_val_loss = val_loss
-                        self.best_iteration_ = m
-                        rounds_no_improve = 0
-                    else:
-                        rounds_no_improve += 1
-                        if rounds_no_improve >= self.early_stopping_rounds:
-                            if self.verbose:
-                                print(f"\n  ⏹ Early stopping at round {m+1} (best: {self.best_iteration_+1})")
-                            for k in range(K):
-                                self.mc_trees[k] = self.mc_trees[k][:self.best_iteration_ + 1]
-                            break
-        finally:
-            sampler.close()
+                    rounds_no_improve += 1
+                    if rounds_no_improve >= self.early_stopping_rounds:
+                        if self.verbose:
+                            print(f"\n  ⏹ Early stopping at round {m+1} (best: {self.best_iteration_+1})")
+                        for k in range(K):
+                            self.mc_trees[k] = self.mc_trees[k][:self.best_iteration_ + 1]
+                        break
         self.n_trees_fitted_ = sum(len(t) for t in self.mc_trees)
 
     # ------------------------------------------------------------------

@@ -292,6 +292,7 @@ struct bsscl_engine {
   DevBuf<GH> ghq;
   DevBuf<double> g64, h64;
   double g_scale = 1.0, h_scale = 1.0;  // fixed point -> value
+  double h_bound = 0.0;  // no hessian of the current tree's rows exceeds this
 
   // Multiclass run on matrix 0: scores, gradients and hessians [K][n], the
   // rows' class and weight, each class's largest |g| and h of the round.
@@ -301,6 +302,7 @@ struct bsscl_engine {
   DevBuf<int32_t> mc_y;
   DevBuf<unsigned long long> mc_max;
   std::vector<double> mc_gm, mc_hm;  // fixed-point multipliers per class
+  std::vector<double> mc_hmax;       // largest hessian per class
 
   // Tree workspace.
   // Compact row sets: a tree uses sets set_base and set_base + 1 (levels
@@ -1135,6 +1137,20 @@ int level_src(const bsscl_engine *E, int32_t level) {
   return E->set_base + (E->pair_levels ? ((level >> 1) & 1) : (level & 1));
 }
 
+// Whether every split a node can take is kept when popped (est:678-683):
+// a split has H >= min_child_weight on each side (est:614-615), so with no
+// row's hessian above h_bound each side holds at least mcw / h_bound rows.
+// The margin covers the rounding of the hessians (a few ulps of w p (1 - p))
+// and of their fixed-point values (below 2^-30 of h_bound).
+// (Test hook: BSSCL_TEST_ALL_KEPT=0 plans as if a split could be refused.)
+bool splits_always_kept(const bsscl_engine *E, const TreeParams &tp) {
+  const char *t = std::getenv("BSSCL_TEST_ALL_KEPT");
+  if (t && t[0] == '0') return false;
+  if (tp.min_samples_leaf <= 0) return true;
+  if (!(tp.mcw > 0.0) || !(E->h_bound > 0.0) || !std::isfinite(E->h_bound)) return false;
+  return tp.mcw >= (double)tp.min_samples_leaf * E->h_bound * (1.0 + 1e-9);
+}
+
 // The planner of level `level`.
 int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParams &tp,
                       int32_t F_sel) {
@@ -1150,6 +1166,7 @@ int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParam
   pa.rows_per_flush = E->hist_rows_per_flush_level;
   pa.part_tile = E->part_tile;
   pa.mode = level_mode(E, level);
+  pa.all_kept = splits_always_kept(E, tp) ? 1 : 0;
   hipEvent_t stop;
   CHK(prof_begin(E, 2, &stop));
   if (E->plan_lds)
@@ -1553,6 +1570,7 @@ int load_grad_hess(bsscl_engine *E, const double *grad, const double *hess,
   const double gm = fixed_mul(gmax, rows_summed), hm = fixed_mul(hmax, rows_summed);
   E->g_scale = 1.0 / gm;
   E->h_scale = 1.0 / hm;
+  E->h_bound = hmax;
   CHK(E->g64.ensure((size_t)n));
   CHK(E->h64.ensure((size_t)n));
   CHK(E->ghq.ensure((size_t)n));
@@ -1735,6 +1753,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   const double gm = fixed_mul(wmax, m), hm = fixed_mul(0.25 * wmax, m);
   E->g_scale = 1.0 / gm;
   E->h_scale = 1.0 / hm;
+  E->h_bound = 0.25 * wmax;
   SamplerRound sr;
   void *token = nullptr;
   const auto t_wait0 = std::chrono::steady_clock::now();
@@ -2584,16 +2603,17 @@ int bsscl_boost_begin(bsscl_engine *E, const int64_t *y, int64_t n, double w0,
     return set_error(BSSCL_EINVAL, "boost_begin: class weights must be positive");
   HIPCHK(hipSetDevice(E->device));
   std::vector<uint8_t> yb((size_t)n);
+  uint64_t bad = 0;  // any label outside {0, 1} (one branch-free pass)
   for (int64_t i = 0; i < n; ++i) {
-    if (y[i] != 0 && y[i] != 1) return set_error(BSSCL_EINVAL, "boost_begin: labels must be 0 or 1");
+    bad |= (uint64_t)y[i] >> 1;
     yb[(size_t)i] = (uint8_t)y[i];
   }
+  if (bad) return set_error(BSSCL_EINVAL, "boost_begin: labels must be 0 or 1");
   CHK(E->y.ensure((size_t)n));
   CHK(E->F.ensure((size_t)n));
   CHK(E->ghq.ensure((size_t)n));
   HIPCHK(hipMemcpyAsync(E->y.p, yb.data(), (size_t)n, hipMemcpyHostToDevice, E->st));
-  std::vector<double> f0((size_t)n, base_score);
-  HIPCHK(hipMemcpyAsync(E->F.p, f0.data(), (size_t)n * 8, hipMemcpyHostToDevice, E->st));
+  HIPCHK(launch_fill_f64(E->st, E->F.p, n, base_score));  // F starts at base_score (est:2834)
   HIPCHK(hipStreamSynchronize(E->st));
   E->w0 = w0;
   E->w1 = w1;
@@ -2740,6 +2760,7 @@ int bsscl_mc_round(bsscl_engine *E, const int64_t *sample_indices, int64_t n_sam
   HIPCHK(hipStreamSynchronize(E->st));
   E->mc_gm.assign((size_t)K, 0.0);
   E->mc_hm.assign((size_t)K, 0.0);
+  E->mc_hmax.assign((size_t)K, 0.0);
   for (int32_t k = 0; k < K; ++k) {
     double gmax, hmax;
     std::memcpy(&gmax, &mx[2 * k], 8);
@@ -2749,6 +2770,7 @@ int bsscl_mc_round(bsscl_engine *E, const int64_t *sample_indices, int64_t n_sam
     // The scale load_grad_hess would take from the same arrays.
     E->mc_gm[(size_t)k] = fixed_mul(gmax, n_samples);
     E->mc_hm[(size_t)k] = fixed_mul(hmax, n_samples);
+    E->mc_hmax[(size_t)k] = hmax;
   }
   E->mc_m = n_samples;
   return BSSCL_OK;
@@ -2777,6 +2799,7 @@ int bsscl_mc_build_tree(bsscl_engine *E, int32_t k, const int32_t *feature_indic
   const double gm = E->mc_gm[(size_t)k], hm = E->mc_hm[(size_t)k];
   E->g_scale = 1.0 / gm;
   E->h_scale = 1.0 / hm;
+  E->h_bound = E->mc_hmax[(size_t)k];
   HIPCHK(launch_quantize(E->st, E->mc_G.p + (size_t)k * n, E->mc_H.p + (size_t)k * n, n, gm, hm,
                          E->ghq.p));
   TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight, reg_lambda, gamma};

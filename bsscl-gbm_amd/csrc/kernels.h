@@ -79,6 +79,12 @@ struct PlanArgs {
   int32_t rows_per_flush; // fewest rows per histogram tile flush
   int32_t part_tile;      // rows per partition tile
   int32_t mode;           // kLevelMove, kLevelInPlace or kLevelGrouped
+  // Every split a candidate can take is kept when popped: a split needs
+  // H >= min_child_weight on both sides and no row's hessian exceeds
+  // min_child_weight / min_samples_leaf, so both children have at least
+  // min_samples_leaf rows (est:614-615, 678-683).  Then the level's other
+  // candidates with a split count as kept splits ranked above a candidate.
+  int32_t all_kept;
 };
 
 // How a level treats its rows:
@@ -222,6 +228,8 @@ hipError_t launch_sort_rows(hipStream_t st, const int32_t *rows, int64_t m,
                             int32_t *out);
 int64_t sort_rows_flag_bytes(int64_t n);
 hipError_t launch_iota(hipStream_t st, int32_t *a, int64_t n);
+// a[0, n) = v.
+hipError_t launch_fill_f64(hipStream_t st, double *a, int64_t n, double v);
 // Work arrays of the device Fisher-Yates (fisher_yates.hip): int32[n] each.
 struct FyWork {
   int32_t *head, *next, *v;

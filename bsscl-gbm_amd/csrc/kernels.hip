@@ -564,6 +564,18 @@ hipError_t launch_iota(hipStream_t st, int32_t *a, int64_t n) {
   return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void k_fill_f64(double *__restrict__ a, int64_t n, double v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    a[i] = v;
+}
+
+hipError_t launch_fill_f64(hipStream_t st, double *a, int64_t n, double v) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fill_f64, dim3(elementwise_blocks(n)), dim3(256), 0, st, a, n, v);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Histogram build (est:581-596, est:722-737).
 //
@@ -2397,6 +2409,9 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
         s_ke[pq.node] = kv;
         kept_e[pq.node] = kv;
       }
+      // With every split kept (a.all_kept), the level's candidates with a
+      // split are kept splits too: their ranks, for the count below.
+      if (a.all_kept && is_cand) s_e[j] = cand_ok ? e : -INFINITY;
       __builtin_amdgcn_wave_barrier();
       // Expanded: fewer than max_leaves - 1 kept splits ranked above.
       int32_t fl = 0;
@@ -2409,6 +2424,8 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
 #pragma unroll
           for (int q = 0; q < 8; ++q) above += (u0 + q < first && k8[q] > e) ? 1 : 0;
         }
+        if (a.all_kept)
+          for (int32_t q = 0; q < nc; ++q) above += (q != j && s_e[q] > e) ? 1 : 0;
         fl = above < a.max_leaves - 1 ? 1 : 0;
       }
       const uint32_t fincl = wave_incl_scan<uint32_t>((uint32_t)fl);
@@ -2741,11 +2758,15 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
 
   // Expanded: valid, a split above gamma, and fewer than max_leaves - 1 kept
   // splits ranked above it.
+  // With every split kept (a.all_kept), the level's other candidates with a
+  // split count as well.
   int32_t fl = 0;
   if (tid < nc && s_flag[tid]) {
     const double ev = s_e[tid];
     int32_t above = 0;
     for (int u = 0; u < first; ++u) above += s_ke[u] > ev ? 1 : 0;
+    if (a.all_kept)
+      for (int u = 0; u < nc; ++u) above += (u != tid && s_flag[u] && s_e[u] > ev) ? 1 : 0;
     fl = above < a.max_leaves - 1 ? 1 : 0;
   }
   uint32_t n_exp_u;

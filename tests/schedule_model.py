@@ -4,7 +4,10 @@ The engine builds a tree level by level -- every node of a depth at once --
 and then replays the reference's best-first candidate loop
 (src/bsscl_gbm/estimator_v1_0_1.py:641-820) on the computed nodes.  A node is
 expanded unless at least max_leaves-1 kept splits u have e(u) > e(v), where
-e is the smallest gain on the path from the root.  This model implements
+e is the smallest gain on the path from the root.  When every split is
+known to be kept (``all_kept``: min_child_weight >= min_samples_leaf times
+the largest hessian), the level's other candidates count as kept splits too.
+This model implements
 that schedule with plain fp64 NumPy so tests can check, on the CPU, that it
 yields the same trees as the sequential builder of the oracle.
 """
@@ -39,7 +42,7 @@ def _best_split(X_bin, g, h, rows, feats, bin_counts, mcw, lam):
 
 
 def build(X_bin, grad, hess, rows, feats, max_leaves, max_depth, msl, mcw,
-          bin_counts, lam, gamma, stats=None):
+          bin_counts, lam, gamma, stats=None, all_kept=False):
     rows = np.asarray(rows, np.int64)
     nodes = []
 
@@ -62,6 +65,8 @@ def build(X_bin, grad, hess, rows, feats, max_leaves, max_depth, msl, mcw,
         exp = []
         for v in frontier:
             kept = sum(1 for u in nodes if u["expanded"] and u["ok"] and u["e"] > nodes[v]["e"])
+            if all_kept:
+                kept += sum(1 for u in frontier if u != v and nodes[u]["e"] > nodes[v]["e"])
             if kept < max_leaves - 1:
                 exp.append(v)
         if not exp:

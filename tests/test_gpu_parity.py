@@ -506,6 +506,48 @@ def test_graph_rounds_after_buffers_grow(engine, monkeypatch):
           flush=True)
 
 
+def test_fit_planner_counts_same_level_splits(engine, monkeypatch):
+    """With min_child_weight >= min_samples_leaf * (largest hessian), every
+    split a node can take is kept (est:614-615, 678-683), so the level
+    planner also counts the level's other candidates as kept splits ranked
+    above a candidate.  A depth-8 fit with 63 leaves then expands far fewer
+    nodes, and its trees and losses equal those of the planner that counts
+    earlier levels only (BSSCL_TEST_ALL_KEPT=0) and the oracle's."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    from bsscl_gbm import estimator as est_mod
+    X, y = make_data(80000, 24, seed=31, nan_frac=0.02)
+    params = dict(n_estimators=8, max_depth=8, n_bins=255, random_state=2, class_weight=None)
+    eng = est_mod._engine(0)
+    fits, expanded = {}, {}
+    for mode in ("1", "0"):
+        _announce(f"planner counting same-level splits: BSSCL_TEST_ALL_KEPT={mode}")
+        monkeypatch.setenv("BSSCL_TEST_ALL_KEPT", mode)
+        est = HybridHistGBMNumbaV1_0_1(verbose=False, **params)
+        eng.set_profiling(1)
+        try:
+            est.fit(X, y)
+            st = eng.stats()
+        finally:
+            eng.set_profiling(0)
+        fits[mode] = est
+        expanded[mode] = st["nodes_expanded"] / max(st["trees"], 1)
+    monkeypatch.delenv("BSSCL_TEST_ALL_KEPT", raising=False)
+    print(f"[result] nodes expanded per tree: {expanded['1']:.1f} counting the level's "
+          f"splits, {expanded['0']:.1f} without", flush=True)
+    a_fit, b_fit = fits["1"], fits["0"]
+    assert a_fit.min_child_weight >= a_fit.min_samples_leaf * 0.25
+    assert expanded["1"] < expanded["0"]
+    assert a_fit.train_loss_history_ == b_fit.train_loss_history_
+    for a, b in zip(a_fit.trees, b_fit.trees):
+        nc = a[5]
+        assert nc == b[5]
+        for k in (0, 1, 2, 3, 4, 6):
+            np.testing.assert_array_equal(a[k][:nc], b[k][:nc])
+    ref, rep = fitcmp.follow_fit(engine, a_fit, X, y, params)
+    print(rep.line("planner counting same-level splits"), flush=True)
+    fitcmp.assert_fit_equal(ref, a_fit, X)
+
+
 def test_profiling_counts_agree(engine, monkeypatch):
     """The node-table counts behind the histogram roofline (rows x features
     histogrammed, bytes, nodes expanded), taken by the in-LDS replay kernel,

@@ -204,6 +204,41 @@ def test_tree_matches_level_schedule(trial):
     np.testing.assert_allclose(ref[2][:k], got[2][:k], rtol=1e-9, atol=1e-12)
 
 
+@pytest.mark.parametrize("trial", range(24))
+def test_tree_matches_level_schedule_counting_level_splits(trial):
+    """With min_child_weight >= min_samples_leaf * max hessian every split
+    is kept (est:614-615, 678-683); the schedule that then also counts the
+    level's other candidates as kept splits gives the sequential builder's
+    tree, and never expands more nodes than the schedule without them."""
+    rng = np.random.default_rng(500 + trial)
+    n = int(rng.integers(2000, 12000))
+    F = int(rng.integers(3, 12))
+    X, y = make_data(n, F, seed=50 + trial, nan_frac=0.1 if trial % 2 else 0.0)
+    e, bc, nid = om.build_bin_edges(X, 255)
+    Xb = om.bin_features(X, e, bc, nid, "standard")
+    p = 1 / (1 + np.exp(-0.5 * rng.standard_normal(n)))
+    w = np.where(y == 1, float(rng.choice([1.0, 1.4])), 1.0)
+    g, h = w * (p - y), w * p * (1 - p)
+    rows = rng.permutation(n)[: int(n * 0.75)].astype(np.int64)
+    fs = np.sort(rng.permutation(F)[: max(1, int(F * 0.8))]).astype(np.int32)
+    ml = int(rng.choice([7, 15, 31, 63]))
+    md = int(rng.choice([5, 6, 8, 10]))
+    msl = int(rng.choice([1, 5, 10]))
+    mcw = msl * float(h.max()) * float(rng.choice([1.0 + 1e-9, 1.5, 3.0]))
+    lam = float(rng.choice([1.0, 5.0]))
+    ref = om.build_tree(Xb, g, h, rows, fs, ml, md, msl, mcw, bc, int(bc.max()), lam, 0.0)
+    st0, st1 = {}, {}
+    plain = sm.build(Xb, g, h, rows, fs, ml, md, msl, mcw, bc, lam, 0.0, stats=st0)
+    got = sm.build(Xb, g, h, rows, fs, ml, md, msl, mcw, bc, lam, 0.0, stats=st1, all_kept=True)
+    assert st1["expanded"] <= st0["expanded"]
+    for tree in (plain, got):
+        assert ref[5] == tree[5]
+        k = ref[5]
+        for i in (0, 1, 3, 4):
+            np.testing.assert_array_equal(ref[i][:k], tree[i][:k])
+        np.testing.assert_allclose(ref[2][:k], tree[2][:k], rtol=1e-9, atol=1e-12)
+
+
 def test_predict_brute_force():
     X, y = make_data(2000, 6, seed=4)
     m = om.OracleGBM(n_estimators=5, max_depth=4, learning_rate=0.1, n_bins=64,
@@ -321,3 +356,31 @@ def test_estimator_weighted_edges_match_oracle():
     np.testing.assert_array_equal(est._nan_bin_id, nan_ref)
     e_unw, _, _ = om.build_bin_edges(X, 64)
     assert not np.array_equal(e_unw, e_ref)  # the weights move the edges
+
+
+def test_counting_level_splits_needs_kept_splits():
+    """The condition matters: with min_child_weight = 0 and a large
+    min_samples_leaf, splits are refused (est:678-683), and a schedule that
+    counted the level's other candidates anyway misses a node the sequential
+    builder pops within a few hundred random trees."""
+    for trial in range(400):
+        rng = np.random.default_rng(900 + trial)
+        n = int(rng.integers(300, 3000))
+        F = int(rng.integers(2, 8))
+        X, y = make_data(n, F, seed=trial)
+        e, bc, nid = om.build_bin_edges(X, 255)
+        Xb = om.bin_features(X, e, bc, nid, "standard")
+        p = 1 / (1 + np.exp(-0.5 * rng.standard_normal(n)))
+        g, h = p - y, p * (1 - p)
+        rows = rng.permutation(n)[: int(n * 0.75)].astype(np.int64)
+        fs = np.arange(F, dtype=np.int32)
+        ml = int(rng.choice([3, 5, 7, 15]))
+        msl = int(rng.choice([100, 200, 400]))
+        ref = om.build_tree(Xb, g, h, rows, fs, ml, 8, msl, 0.0, bc, int(bc.max()), 1.0, 0.0)
+        try:
+            got = sm.build(Xb, g, h, rows, fs, ml, 8, msl, 0.0, bc, 1.0, 0.0, all_kept=True)
+        except AssertionError:
+            return  # popped a node the schedule did not expand
+        if got[5] != ref[5] or not np.array_equal(got[0][:ref[5]], ref[0][:ref[5]]):
+            return
+    raise AssertionError("no refused split changed the schedule")
