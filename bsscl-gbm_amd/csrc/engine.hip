@@ -364,6 +364,10 @@ struct bsscl_engine {
   int32_t tile_cap = 0, hist_cap = 0;
   DevBuf<PartTile> tiles_d;
   DevBuf<int32_t> tile_cnt_d;         // per partition tile: its rows of the four runs
+  // {first candidate, candidates} of the next level, by level parity: the
+  // planner of level d writes slot (d + 1) & 1 for level d + 1's counting
+  // blocks (which cannot read the plan that level's planner rewrites).
+  DevBuf<int32_t> level_args_d;
   DevBuf<HistTask> hist_tasks_d;
   DevBuf<char> lvl_d;                 // packed inputs of the root (one upload per tree)
   const int32_t *feat_d = nullptr;    // selected feature indices
@@ -966,7 +970,9 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
   E->part_rows = 16;
   while (E->part_rows > 4 && m / ((int64_t)kPartThreads * E->part_rows) < 512) E->part_rows >>= 1;
   E->part_tile = kPartThreads * E->part_rows;
-  const int64_t tcap = m / E->part_tile + (int64_t)cap + 4;
+  // (A level counts the tiles of every candidate or previous parent: at most
+  // m / part_tile plus two partial tiles per candidate.)
+  const int64_t tcap = m / E->part_tile + 2 * (int64_t)cap + 4;
   const int64_t hcap =
       (int64_t)std::max(hist_target(E, F_sel), hist_target(E, F_sel, true)) + cap + 4;
   if (tcap > INT32_MAX / 2 || hcap > INT32_MAX / 2)
@@ -982,6 +988,7 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
   }
   CHK(E->tiles_d.ensure((size_t)tcap));
   CHK(E->tile_cnt_d.ensure(4 * (size_t)tcap + 8));  // a 16-byte read past the last tile
+  CHK(E->level_args_d.ensure(4));
   CHK(E->hist_tasks_d.ensure((size_t)hcap));
   CHK(E->part_d.ensure((size_t)hcap * F_sel * kHistPerFeat));
   E->tile_cap = (int32_t)tcap;
@@ -1151,9 +1158,24 @@ bool splits_always_kept(const bsscl_engine *E, const TreeParams &tp) {
   return tp.mcw >= (double)tp.min_samples_leaf * E->h_bound * (1.0 + 1e-9);
 }
 
+// Whether level `level`'s partition tiles are counted by its planner
+// launch (in-place and grouped levels, with the LDS planner) rather than by
+// k_part_count after it.
+bool count_fused(const bsscl_engine *E, int32_t level) {
+  return E->plan_lds && level_mode(E, level) != kLevelMove;
+}
+
+// Most partition tiles level `level` can count over m rows: m / part_tile
+// plus two partial tiles per candidate (at most 2^level of them).
+int64_t count_tiles_bound(const bsscl_engine *E, int32_t level, int64_t m) {
+  const int64_t items = std::min<int64_t>(level >= 30 ? INT32_MAX : (int64_t)1 << level,
+                                          (int64_t)E->node_cap);
+  return std::min<int64_t>(E->tile_cap, m / E->part_tile + 2 * items + 2);
+}
+
 // The planner of level `level`.
 int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParams &tp,
-                      int32_t F_sel) {
+                      int32_t F_sel, int64_t m) {
   PlanArgs pa;
   pa.gamma = tp.gamma;
   pa.level = level;
@@ -1167,15 +1189,25 @@ int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParam
   pa.part_tile = E->part_tile;
   pa.mode = level_mode(E, level);
   pa.all_kept = splits_always_kept(E, tp) ? 1 : 0;
+  pa.part_rows = E->part_rows;
+  pa.fused_count = count_fused(E, level) ? 1 : 0;
   hipEvent_t stop;
   CHK(prof_begin(E, 2, &stop));
-  if (E->plan_lds)
+  if (E->plan_lds) {
+    // The counting blocks read the level's rows where its parents hold them.
+    const int src = level_src(E, level);
+    const int64_t tiles = count_tiles_bound(E, level, m);
+    const int32_t cblocks =
+        (int32_t)std::max<int64_t>(1, (tiles + kCountTilesPerBlock - 1) / kCountTilesPerBlock);
     HIPCHK(launch_plan_lds(E->st, E->nodes_d, E->plan_d, E->parents_d[(level + 1) & 1].p,
                            E->parents_d[level & 1].p, E->groups_d.p, E->tile_begin_d.p,
                            E->hist_begin_d.p, E->tiles_d.p, E->hist_tasks_d.p, E->segs.p,
                            E->totals.p, E->cand.p, E->kept_e_d.p,
                            E->parent_e_d[(level + 1) & 1].p, E->parent_e_d[level & 1].p,
-                           F_sel, pa));
+                           F_sel, pa, E->codes_c[src].p, E->ld_c, E->tile_cnt_d.p,
+                           E->level_args_d.p + 2 * (level & 1),
+                           E->level_args_d.p + 2 * ((level + 1) & 1), cblocks));
+  }
   else if (pa.mode == kLevelMove)
     HIPCHK(launch_plan(E->st, E->nodes_d, E->plan_d, E->parents_d[(level + 1) & 1].p,
                        E->parents_d[level & 1].p, E->tile_begin_d.p, E->hist_begin_d.p,
@@ -1196,11 +1228,13 @@ int launch_level_plan(bsscl_engine *E, int32_t level, bool last, const TreeParam
 int launch_partition(bsscl_engine *E, int src, int dst, const PartParent *parents,
                      const PartGroup *groups, const int32_t *tile_begin, const PartTile *tiles,
                      const LevelPlan *plan, int32_t max_tiles, int32_t F_sel,
-                     int32_t min_samples_leaf, bool move_rows) {
+                     int32_t min_samples_leaf, bool move_rows, bool counted = false) {
+  if (counted && !move_rows) return BSSCL_OK;
   hipEvent_t stop;
   CHK(prof_begin(E, 1, &stop));
-  HIPCHK(launch_part_count(E->st, E->codes_c[src].p, E->ld_c, parents, groups, tiles, plan,
-                           max_tiles, E->part_rows, E->tile_cnt_d.p));
+  if (!counted)  // (counted: the planner launch has counted the tiles)
+    HIPCHK(launch_part_count(E->st, E->codes_c[src].p, E->ld_c, parents, groups, tiles, plan,
+                             max_tiles, E->part_rows, E->tile_cnt_d.p));
   if (move_rows)  // the scatter does each group's scan itself
     HIPCHK(launch_part_scatter(E->st, E->codes_c[src].p, E->codes_c[dst].p, E->ld_c,
                                E->gh_c[src].p, E->gh_c[dst].p,
@@ -1228,7 +1262,7 @@ int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
   const int32_t P = level_parents_bound(E, level);
   const int32_t T = (int32_t)std::min<int64_t>(E->tile_cap, m / E->part_tile + 2 * (int64_t)P + 1);
   CHK(launch_partition(E, src, dst, par, grp, E->tile_begin_d.p, E->tiles_d.p, E->plan_d, T,
-                       F_sel, tp.min_samples_leaf, !last && !in_place));
+                       F_sel, tp.min_samples_leaf, !last && !in_place, count_fused(E, level)));
   hipEvent_t stop;
   if (last) {
     CHK(prof_begin(E, 2, &stop));
@@ -1244,8 +1278,7 @@ int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
   // In place, the smaller children's rows are read from their parents'
   // segments in src, and the histogram launch takes the children's sizes.
   const int hs = in_place ? src : dst;
-  const SpanLevel span{par, E->tile_begin_d.p, E->tile_cnt_d.p, E->nleft_d.p,
-                       tp.min_samples_leaf};
+  const SpanLevel span{par, E->tile_cnt_d.p, E->nleft_d.p, tp.min_samples_leaf};
   HIPCHK(launch_hist(E->st, E->codes_c[hs].p, E->ld_c, E->gh_c[hs].p, E->hist_tasks_d.p,
                      E->plan_d, H, E->hist_node_d.p, E->hist_begin_d.p, E->segs.p,
                      E->nb_sel_d, E->hot_sel_d, F_sel, hist_fchunk(E, F_sel, in_place),
@@ -1400,7 +1433,7 @@ int launch_tree(bsscl_engine *E, const int32_t *rows32, int64_t m,
   *run = 0;
   for (int32_t d = 0; d < levels; ++d) {
     const bool last = d + 1 >= tp.max_depth;
-    CHK(launch_level_plan(E, d, last, tp, F_sel));
+    CHK(launch_level_plan(E, d, last, tp, F_sel, m));
     if (checks && d > 0 && d % kLevelsPerCheck == 0) {
       LevelPlan plan;
       CHK(read_table(E, 0, plan));
@@ -2145,6 +2178,28 @@ int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
 // ===========================================================================
 // C ABI
 // ===========================================================================
+namespace bsscl {
+
+hipStream_t copy_stream(int device) {
+  static std::mutex mu;
+  static std::vector<hipStream_t> streams;
+  std::lock_guard<std::mutex> lk(mu);
+  if (device < 0) return nullptr;
+  if ((size_t)device >= streams.size()) streams.resize((size_t)device + 1, nullptr);
+  hipStream_t &s = streams[(size_t)device];
+  if (!s) {
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    if (hipSetDevice(device) != hipSuccess ||
+        hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess)
+      s = nullptr;
+    (void)hipSetDevice(cur);
+  }
+  return s;
+}
+
+}  // namespace bsscl
+
 extern "C" {
 
 const char *bsscl_last_error(void) { return g_last_error.c_str(); }
@@ -2176,6 +2231,12 @@ int bsscl_engine_create(int32_t device, bsscl_engine **out) {
     if (E->st) (void)hipStreamDestroy(E->st);
     delete E;
     return set_error(BSSCL_EDEVICE, std::string("hipStreamCreate: ") + hipGetErrorString(e));
+  }
+  if (!copy_stream(device)) {
+    (void)hipStreamDestroy(E->st_rows);
+    (void)hipStreamDestroy(E->st);
+    delete E;
+    return set_error(BSSCL_EDEVICE, "hipStreamCreate of the draws' copy stream failed");
   }
   int v = 0;
   if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && v > 0)
@@ -3134,9 +3195,10 @@ int bsscl_partition(bsscl_engine *E, const int64_t *rows, int64_t m,
                             E->gh_c[0].p, E->rid_c[0].p, E->ld_c, E->segs.p,
                             E->hist_node_d.p));
   E->track_rid = true;  // this call reads the moved row ids back
-  const PartParent P{0, m, 0, bin, 1, 2, 0, 0};
+  PartParent P{0, m, 0, bin, 1, 2, 0, 0, 0, 0};
   std::vector<PartTile> tiles;
   add_part_tiles(E, P, 0, tiles);
+  P.tile1 = (int32_t)tiles.size();
   const int32_t tb[2] = {0, (int32_t)tiles.size()};
   LevelPlan lp = {};
   lp.n_parents = 1;

@@ -33,6 +33,9 @@ struct PartParent {
   int32_t right_id;
   int32_t node;      // the parent's own id
   int32_t gslot;     // 2 * its PartGroup + its side (levels with groups only)
+  // The partition tiles [tile0, tile1) that count this parent's rows (runs
+  // 2 * side and 2 * side + 1 of each, side = gslot & 1 with groups, else 0).
+  int32_t tile0, tile1;
 };
 
 // A partition group: the rows [start, start + count) of the source set,
@@ -85,6 +88,10 @@ struct PlanArgs {
   // min_samples_leaf rows (est:614-615, 678-683).  Then the level's other
   // candidates with a split count as kept splits ranked above a candidate.
   int32_t all_kept;
+  int32_t part_rows;      // rows per thread of a partition tile (4, 8 or 16)
+  // In place and grouped levels: blocks 1.. of the planner launch count the
+  // level's partition tiles (plan_count_role) while block 0 plans.
+  int32_t fused_count;
 };
 
 // How a level treats its rows:
@@ -272,8 +279,7 @@ hipError_t launch_gather_gh(hipStream_t st, const double *F, const uint8_t *y,
 // An in-place level's histogram inputs (see launch_hist).
 struct SpanLevel {
   const PartParent *parents;  // the level's parents; task.ref indexes them
-  const int32_t *tile_begin;  // each parent's partition tiles
-  const int32_t *tile_cnt;    // their run counts (k_part_count)
+  const int32_t *tile_cnt;    // their tiles' run counts (PartParent::tile0, tile1)
   int64_t *parent_nleft;      // written: each parent's left rows
   int32_t min_samples_leaf;
 };
@@ -350,7 +356,13 @@ hipError_t launch_plan(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
 // kept_e (node ranks of kept splits, per node) and parent_e (ranks of a
 // level's parents, by level parity) for the levels after it.  Plans any
 // level mode (a.mode); a grouped level also writes its PartGroup list.
-// (k_plan plans kLevelMove levels only.)
+// (k_plan plans kLevelMove levels only.)  With a.fused_count (in-place and
+// grouped levels) the launch has 1 + count_blocks blocks: blocks 1.. count
+// the level's partition tiles into tile_cnt (codes of set codes_c), as
+// k_part_count would for every candidate, while block 0 plans.  level_in
+// holds {first candidate, candidates} of this level (written by the
+// previous level's planner; unused at level 0, whose only candidate is the
+// root) and the planner writes the next level's into level_out.
 hipError_t launch_plan_lds(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                            const PartParent *prev_parents, PartParent *parents,
                            PartGroup *groups,
@@ -358,7 +370,13 @@ hipError_t launch_plan_lds(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                            HistTask *hist_tasks, const NodeSeg *segs,
                            const long long *totals, const SplitCand *cand, double *kept_e,
                            const double *prev_parent_e, double *parent_e, int32_t F_sel,
-                           PlanArgs a);
+                           PlanArgs a, const uint8_t *codes_c, int64_t ld_c,
+                           int32_t *tile_cnt, const int32_t *level_in, int32_t *level_out,
+                           int32_t count_blocks);
+// Partition tiles of a level's count: each of `items` rows segments (in
+// place: the candidates; grouped: the previous level's parents), from its
+// start rounded down to 16, in tiles of part_tile rows, at least one.
+constexpr int kCountTilesPerBlock = 4;  // tiles a counting block of the planner launch takes
 constexpr int32_t kPlanLdsMaxNodes = 513;
 hipError_t launch_code_counts(hipStream_t st, const uint8_t *codes, int64_t ld,
                               int64_t n, int32_t F, unsigned int *counts);

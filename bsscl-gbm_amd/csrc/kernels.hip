@@ -849,7 +849,7 @@ __device__ __forceinline__ void hist_item(
     span_load<FC>(L, codes_c, ld_c, scol, f0, nf,
                   r0 / kSpanRows + 64 * (int64_t)(threadIdx.x >> 6) + lane_id(),
                   (r1 + kSpanRows - 1) / kSpanRows);
-    const int32_t t0 = span.tile_begin[task.ref], t1 = span.tile_begin[task.ref + 1];
+    const int32_t t0 = P.tile0, t1 = P.tile1;
     long long nl, nr;
     strided_side_counts(span.tile_cnt, t0 + (int32_t)threadIdx.x, t1, kHistBlock, nl, nr);
     nl = wave_sum(nl);
@@ -1193,7 +1193,7 @@ __device__ __forceinline__ void route_masks(const Route<R> &q, const PartGroup &
 __device__ __forceinline__ void group_parents(const PartGroup &G,
                                               const PartParent *__restrict__ parents,
                                               PartParent &Pa, PartParent &Pb) {
-  const PartParent none{0, 0, 0, 0, -1, -1, -1, 0};
+  const PartParent none{0, 0, 0, 0, -1, -1, -1, 0, 0, 0};
   Pa = G.par[0] >= 0 ? parents[G.par[0]] : none;
   Pb = G.par[1] >= 0 ? parents[G.par[1]] : none;
 }
@@ -1331,6 +1331,7 @@ void k_part_scatter(
   for (int32_t ti = (int32_t)blockIdx.x; ti < n_tiles; ti += (int32_t)gridDim.x) {
     const PartTile t = tiles[ti];
     const PartGroup G = tile_group(groups, parents, t.parent);
+    if (G.par[0] < 0 && G.par[1] < 0) continue;  // a group with no expanded side: rows stay
     PartParent Pa, Pb;
     group_parents(G, parents, Pa, Pb);
     const int64_t row = t.row0 + (int64_t)R * tid;
@@ -1684,7 +1685,7 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_reduce_split(
   const auto records = [&](int32_t p) {
     Item r;
     r.small = parents ? hist_node[p] : 0;
-    r.pp = parents ? parents[p] : PartParent{0, 0, 0, 0, -1, -1, -1, 0};
+    r.pp = parents ? parents[p] : PartParent{0, 0, 0, 0, -1, -1, -1, 0, 0, 0};
     r.hb0 = hist_begin[p];
     r.hb1 = hist_begin[p + 1];
     return r;
@@ -1841,9 +1842,8 @@ __global__ __launch_bounds__(256) void k_last_level(
   for (int w = (int)(blockIdx.x * 4 + (threadIdx.x >> 6)); w < n_parents;
        w += (int)gridDim.x * 4) {
     const PartParent P = parents[w];
-    const int32_t gs = grouped ? P.gslot : 2 * w;
     long long nl, nr;
-    wave_side_counts(tile_cnt, tile_begin[gs >> 1], tile_begin[(gs >> 1) + 1], gs & 1, nl, nr);
+    wave_side_counts(tile_cnt, P.tile0, P.tile1, grouped ? (P.gslot & 1) : 0, nl, nr);
     // The parent's histogram of its split feature: totals of bins <= bin.
     const long long *h = reinterpret_cast<const long long *>(pool) +
                          (int64_t)P.node * node_stride + (int64_t)P.fpos * kHistPerFeat;
@@ -2171,6 +2171,10 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan(
     hist_begin[n_exp] = (int32_t)hcar;
   }
   __syncthreads();
+  for (int i = tid; i < n_exp; i += kPlanBlock) {  // each parent's own tiles
+    parents[i].tile0 = tile_begin[i];
+    parents[i].tile1 = tile_begin[i + 1];
+  }
 
   // Tile and histogram-task lists: item -> its parent by binary search.
   for (int t = tid; t < (int)tcar; t += kPlanBlock) {
@@ -2262,6 +2266,161 @@ constexpr int kStageC = 64, kStageF = 64;
 // candidates (every level of a tree of up to 63 leaves).
 constexpr int kFastFirst = 128;
 
+// The next level's {first candidate, candidates}, for its counting blocks.
+__device__ __forceinline__ void plan_next_level(int32_t *level_out, int32_t first, int32_t nc) {
+  if (level_out) {
+    level_out[0] = first;
+    level_out[1] = nc;
+  }
+}
+
+// Tiles of one item of a level's count: its rows [start, start + count)
+// from start rounded down to 16, part_tile rows a tile, at least one (a
+// parent's first tile writes its children's segments); none when off.
+__device__ __forceinline__ uint32_t count_item_tiles(int64_t start, int64_t count, bool on,
+                                                     int32_t part_tile) {
+  if (!on) return 0u;
+  const int64_t a0 = start & ~int64_t(15);
+  return (uint32_t)max((int64_t)1, div_pos(start + count - a0 + part_tile - 1, part_tile));
+}
+
+// A candidate's best split over its features, as the planner takes it
+// (est:618-621: the largest gain, the first position of equal gains), by
+// one wave (wave-uniform `exists`); fpos -1 when there is none.
+__device__ __forceinline__ void wave_best_split(const SplitCand *__restrict__ cand, int64_t c,
+                                                int32_t F_sel, bool exists, int32_t &fpos,
+                                                int32_t &bin) {
+  double best = 0.0;
+  int32_t bf = -1, bb = 0;
+  if (exists) {
+    for (int32_t f = lane_id(); f < F_sel; f += 64) {
+      const SplitCand x = cand[c * F_sel + f];
+      if (x.bin >= 0 && (bf < 0 || x.gain > best)) {
+        best = x.gain;
+        bf = f;
+        bb = x.bin;
+      }
+    }
+  }
+  wave_argmax(best, bf, bb);
+  fpos = bf;
+  bin = bb;
+}
+
+// The counting role of an in-place or grouped level's planner launch
+// (blocks 1..): the level's partition tiles over every candidate (in place)
+// or every previous parent (grouped), from count_item_tiles in item order as
+// block 0 lays them out, each routed by its candidates' best splits whether
+// or not block 0 expands them, and each tile's four run counts written as
+// k_part_count writes them.  The level's kernels read the counts of the
+// expanded parents' tiles only (PartParent::tile0, tile1).  Each quarter of
+// the block (256 threads, R rows each) takes one tile at a time.
+template <int R>
+__device__ void plan_count_role(const uint8_t *__restrict__ codes_c, int64_t ld_c,
+                                const NodeSeg *__restrict__ segs,
+                                const SplitCand *__restrict__ cand, int32_t F_sel,
+                                const PartParent *__restrict__ prev_parents, int32_t first,
+                                int32_t nc, bool grouped, const PlanArgs &a,
+                                int32_t *__restrict__ tile_cnt, uint32_t *stmp, uint32_t *s_ctb,
+                                int32_t (*s_cbest)[2][2], uint2 (*s_cred)[4]) {
+  static_assert(kPlanBlock == kCountTilesPerBlock * kPartBlock, "a quarter per tile");
+  const int tid = (int)threadIdx.x;
+  const int n_items = grouped ? nc / 2 : nc;
+  uint32_t nt = 0u;
+  if (tid < n_items) {
+    if (grouped) {
+      const PartParent pp = prev_parents[tid];
+      nt = count_item_tiles(pp.start, pp.count, true, a.part_tile);
+    } else {
+      const NodeSeg sg = segs[first + tid];
+      nt = count_item_tiles(sg.start, sg.count, sg.valid != 0, a.part_tile);
+    }
+  }
+  uint32_t total;
+  const uint32_t pre = block_excl_scan<kPlanBlock>(nt, stmp, total);
+  if (tid < kPlanLdsC) s_ctb[tid] = pre;
+  if (tid == 0) s_ctb[kPlanLdsC] = total;
+  __syncthreads();
+  if (total > (uint32_t)a.tile_cap) return;  // block 0 reports the level as broken
+  const int q = tid / kPartBlock, r = tid % kPartBlock, w = (tid >> 6) & 3;
+  const int64_t stride = (int64_t)(gridDim.x - 1) * kCountTilesPerBlock;
+  for (int64_t base = (int64_t)(blockIdx.x - 1) * kCountTilesPerBlock; base < (int64_t)total;
+       base += stride) {
+    const int64_t t = base + q;
+    const bool act = t < (int64_t)total;
+    int item = 0;
+    if (act) {
+      int lo = 0, hi = n_items - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if ((int64_t)s_ctb[mid] <= t) lo = mid;
+        else hi = mid - 1;
+      }
+      item = lo;
+    }
+    // The best split of each side's candidate: wave 0 of the quarter for
+    // side 0 (in place: the candidate itself), wave 1 for side 1.
+    if (act && (w == 0 || (grouped && w == 1))) {
+      const int32_t j = grouped ? 2 * item + w : item;
+      const bool exists = segs[first + j].valid != 0;
+      int32_t fp, bn;
+      wave_best_split(cand, (int64_t)first + j, F_sel, exists, fp, bn);
+      if (lane_id() == 0) {
+        s_cbest[q][w][0] = fp;
+        s_cbest[q][w][1] = bn;
+      }
+    }
+    __syncthreads();
+    uint32_t run[4] = {0u, 0u, 0u, 0u};
+    if (act) {
+      PartGroup G;
+      if (grouped) {
+        const PartParent pp = prev_parents[item];
+        G.start = pp.start;
+        G.count = pp.count;
+        G.fpos = pp.fpos;
+        G.bin = pp.bin;
+      } else {
+        const NodeSeg sg = segs[first + item];
+        G.start = sg.start;
+        G.count = sg.count;
+        G.fpos = -1;
+        G.bin = 0;
+      }
+      const int32_t fa = s_cbest[q][0][0], fb = grouped ? s_cbest[q][1][0] : -1;
+      G.par[0] = fa >= 0 ? 0 : -1;
+      G.par[1] = fb >= 0 ? 1 : -1;
+      PartParent Pa{0, 0, fa, s_cbest[q][0][1], -1, -1, -1, 0, 0, 0};
+      PartParent Pb{0, 0, fb, grouped ? s_cbest[q][1][1] : 0, -1, -1, -1, 0, 0, 0};
+      PartTile T;
+      T.row0 = (G.start & ~int64_t(15)) + (t - (int64_t)s_ctb[item]) * a.part_tile;
+      T.rows = a.part_tile;
+      T.parent = item;
+      const int64_t row = T.row0 + (int64_t)R * r;
+      const Route<R> rt = route_load<R>(codes_c, ld_c, T, G, Pa, Pb, row);
+      route_masks<R>(rt, G, row, run);
+    }
+    // Four counts as 16-bit fields (a tile has at most 4096 rows).
+    const uint32_t ca = wave_sum((uint32_t)__builtin_popcount(run[0]) |
+                                 ((uint32_t)__builtin_popcount(run[1]) << 16));
+    const uint32_t cb = wave_sum((uint32_t)__builtin_popcount(run[2]) |
+                                 ((uint32_t)__builtin_popcount(run[3]) << 16));
+    if (lane_id() == 0) s_cred[q][w] = make_uint2(ca, cb);
+    __syncthreads();
+    if (act && r == 0) {
+      uint32_t sa = 0u, sb = 0u;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        sa += s_cred[q][k].x;
+        sb += s_cred[q][k].y;
+      }
+      *reinterpret_cast<uint4 *>(tile_cnt + 4 * t) =
+          make_uint4(sa & 0xffffu, sa >> 16, sb & 0xffffu, sb >> 16);
+    }
+    __syncthreads();  // s_cbest and s_cred are rewritten by the next tiles
+  }
+}
+
 __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     NodeOut *__restrict__ nodes, LevelPlan *__restrict__ plan,
     const PartParent *__restrict__ prev_parents, PartParent *__restrict__ parents,
@@ -2271,9 +2430,11 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     const NodeSeg *__restrict__ segs,
     const long long *__restrict__ totals, const SplitCand *__restrict__ cand,
     double *__restrict__ kept_e, const double *__restrict__ prev_parent_e,
-    double *__restrict__ parent_e, int32_t F_sel, PlanArgs a) {
+    double *__restrict__ parent_e, int32_t F_sel, PlanArgs a,
+    const uint8_t *__restrict__ codes_c, int64_t ld_c, int32_t *__restrict__ tile_cnt,
+    const int32_t *__restrict__ level_in, int32_t *__restrict__ level_out) {
   __shared__ uint32_t stmp[kPlanBlock / 64];
-  __shared__ unsigned long long stmp64[kPlanBlock / 64];
+  __shared__ uint32_t s_ctb[kPlanLdsC + 1];  // each count item's first tile (and the total)
   __shared__ double s_ke[kPlanLdsC + 1];
   __shared__ int64_t s_start[kPlanLdsC], s_count[kPlanLdsC];
   __shared__ long long s_gq[kPlanLdsC], s_hq[kPlanLdsC];
@@ -2282,9 +2443,9 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
   __shared__ int32_t s_flag[kPlanLdsC];
   __shared__ int32_t s_pj[kPlanLdsC / 2 + 1];  // candidate of each parent
   __shared__ int32_t s_tb[kPlanLdsC / 2 + 1], s_hb[kPlanLdsC / 2 + 1];
-  // Grouped levels: each candidate's parent index (-1: not expanded), each
-  // previous parent's group (-1: none) and each group's first tile row.
-  __shared__ int32_t s_pidx[kPlanLdsC], s_gi[kPlanLdsC / 2 + 1];
+  // Grouped levels: each candidate's parent index (-1: not expanded); each
+  // group's (parent's) first tile row.
+  __shared__ int32_t s_pidx[kPlanLdsC];
   __shared__ int64_t s_gs[kPlanLdsC / 2 + 1];
   __shared__ uint32_t s_tcar;
   __shared__ unsigned long long s_rows;
@@ -2292,10 +2453,41 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
   __shared__ int16_t s_cb[kStageF * kStageC];  // staged bins (-1: no split)
   __shared__ int32_t s_fast[8];                // fast path: wave 0's results
   __shared__ int32_t s_cpf[(kPlanBlock / 64) * kStageC];  // fast path: each wave's best feature
+  // Counting blocks: each tile's candidates' best splits and its waves' counts.
+  __shared__ int32_t s_cbest[kCountTilesPerBlock][2][2];
+  __shared__ uint2 s_cred[kCountTilesPerBlock][4];
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
+  if (blockIdx.x > 0) {
+    // Counting blocks (a.fused_count): this level's candidates come from the
+    // previous level's planner (the root alone at level 0), not from *plan,
+    // which block 0 rewrites meanwhile.
+    const int32_t c_first = a.level == 0 ? 0 : level_in[0];
+    const int32_t c_nc = a.level == 0 ? 1 : level_in[1];
+    if (a.fused_count && c_nc > 0 && c_nc <= kPlanLdsC) {
+      const bool g = a.mode == kLevelGrouped;
+      switch (a.part_rows) {
+        case 4:
+          plan_count_role<4>(codes_c, ld_c, segs, cand, F_sel, prev_parents, c_first, c_nc, g, a,
+                             tile_cnt, stmp, s_ctb, s_cbest, s_cred);
+          break;
+        case 8:
+          plan_count_role<8>(codes_c, ld_c, segs, cand, F_sel, prev_parents, c_first, c_nc, g, a,
+                             tile_cnt, stmp, s_ctb, s_cbest, s_cred);
+          break;
+        default:
+          plan_count_role<16>(codes_c, ld_c, segs, cand, F_sel, prev_parents, c_first, c_nc, g,
+                              a, tile_cnt, stmp, s_ctb, s_cbest, s_cred);
+          break;
+      }
+    }
+    return;
+  }
   const LevelPlan prev = *plan;
-  if (prev.overflow) return;
+  if (prev.overflow) {
+    if (tid == 0) plan_next_level(level_out, prev.n_nodes, 0);
+    return;
+  }
   const int32_t first = prev.first_child, nc = prev.n_split, n_prev = prev.n_nodes;
   const int32_t n_pp = a.level == 0 ? 0 : nc / 2;  // the previous level's parents
   if (nc > kPlanLdsC || first > kPlanLdsC + 1) {
@@ -2307,6 +2499,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       q.n_nodes = n_prev;
       q.overflow = -1;
       *plan = q;
+      plan_next_level(level_out, n_prev, 0);
     }
     return;
   }
@@ -2328,7 +2521,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     NodeSeg sg{0, 0, 0, 0};
     long long gq = 0, hq = 0;
     double ppe = 0.0, pe = 0.0, ke_a = 0.0, ke_b = 0.0;
-    PartParent pq{0, 0, 0, 0, -1, -1, -1, 0};
+    PartParent pq{0, 0, 0, 0, -1, -1, -1, 0, 0, 0};
     if (wave == 0) {
       if (j < nc) {
         const int64_t c = first + j;
@@ -2437,27 +2630,27 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       uint32_t tcar = 0, hcar = 0;
       int32_t th = 0;
       if (status == 0) {
-        // A grouped level's groups: the previous parents with an expanded
-        // child, each with its tiles over the previous parent's segment.
-        int32_t gi = -1;
+        // Partition tiles, each lane's item in order: in place every
+        // candidate and grouped every previous parent (counted by the
+        // launch's other blocks, plan_count_role, whether or not a side is
+        // expanded); moving, the expanded parents (k_part_count).
+        uint32_t ntc = 0u;
+        if (a.mode == kLevelInPlace)
+          ntc = is_cand ? count_item_tiles(sg.start, sg.count, sg.valid != 0, a.part_tile) : 0u;
+        else if (grouped)
+          ntc = j < n_pp ? count_item_tiles(pq.start, pq.count, true, a.part_tile) : 0u;
+        else
+          ntc = fl ? count_item_tiles(sg.start, sg.count, true, a.part_tile) : 0u;
+        const uint32_t cincl = wave_incl_scan<uint32_t>(ntc);
+        const uint32_t cpre = cincl - ntc;
+        tcar = wave_lane(cincl, 63);
+        // A grouped level's groups: every previous parent, par -1 for a side
+        // that is not expanded (its rows stay), tiles over its segment.
         if (grouped) {
           const int32_t pid_or = fl ? (int32_t)pidx : -1;
           const int32_t pl = __shfl(pid_or, min(2 * j, 63), 64);
           const int32_t pr = __shfl(pid_or, min(2 * j + 1, 63), 64);
-          const bool ge = j < n_pp && (pl >= 0 || pr >= 0);
-          const int64_t a0 = pq.start & ~int64_t(15);
-          const uint32_t gt =
-              ge ? (uint32_t)max((int64_t)1,
-                                 div_pos(pq.start + pq.count - a0 + a.part_tile - 1, a.part_tile))
-                 : 0u;
-          // Groups in the low word, tiles in the high word.
-          const unsigned long long gv = ((unsigned long long)gt << 32) | (ge ? 1ull : 0ull);
-          const unsigned long long gincl = wave_incl_scan<unsigned long long>(gv);
-          const unsigned long long gpre = gincl - gv, gtot = wave_lane(gincl, 63);
-          const uint32_t gidx = (uint32_t)gpre, toff = (uint32_t)(gpre >> 32);
-          n_groups = (int32_t)(uint32_t)gtot;
-          const uint32_t tcar_g = (uint32_t)(gtot >> 32);
-          if (ge) {
+          if (j < n_pp) {
             PartGroup G;
             G.start = pq.start;
             G.count = pq.count;
@@ -2465,20 +2658,22 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
             G.bin = pq.bin;
             G.par[0] = pl;
             G.par[1] = pr;
-            groups[gidx] = G;
-            s_tb[gidx] = (int32_t)toff;
-            s_gs[gidx] = a0;
-            tile_begin[gidx] = (int32_t)toff;
-            gi = (int32_t)gidx;
+            groups[j] = G;
+            s_tb[j] = (int32_t)cpre;
+            s_gs[j] = pq.start & ~int64_t(15);
+            tile_begin[j] = (int32_t)cpre;
           }
           if (j == 0) {
-            s_tb[n_groups] = (int32_t)tcar_g;
-            tile_begin[n_groups] = (int32_t)tcar_g;
+            s_tb[n_pp] = (int32_t)tcar;
+            tile_begin[n_pp] = (int32_t)tcar;
           }
-          tcar = tcar_g;
+          n_groups = n_pp;
         }
-        // Records, parents, ranks; tiles per parent; rows to build.
-        const int32_t gi_j = __shfl(gi, j >> 1, 64);
+        // The tiles that count a candidate's rows: its own, or grouped its
+        // previous parent's (j >> 1).
+        const uint32_t g0 = __shfl(cpre, j >> 1, 64), g1 = __shfl(cpre + ntc, j >> 1, 64);
+        const uint32_t t0 = grouped ? g0 : cpre, t1 = grouped ? g1 : cpre + ntc;
+        // Records, parents, ranks; rows to build.
         unsigned long long rows = 0;
         if (is_cand) {
           const int32_t v = first + j;
@@ -2507,19 +2702,23 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
             P.left_id = L;
             P.right_id = L + 1;
             P.node = v;
-            P.gslot = grouped ? 2 * gi_j + (j & 1) : 2 * i;
+            P.gslot = grouped ? j : 2 * i;  // grouped: 2 * group (j >> 1) + side
+            P.tile0 = (int32_t)t0;
+            P.tile1 = (int32_t)t1;
             parents[i] = P;
             parent_e[i] = N.e;
-            if (!grouped) {
-              const int64_t a0 = N.start & ~int64_t(15);
-              // At least one tile: a parent's first tile writes its children's segments.
-              s_tb[i] = (int32_t)max((int64_t)1,
-                                     div_pos(N.start + N.count - a0 + a.part_tile - 1, a.part_tile));
-              s_gs[i] = a0;
+            if (a.mode == kLevelMove) {
+              s_tb[i] = (int32_t)cpre;
+              s_gs[i] = N.start & ~int64_t(15);
+              tile_begin[i] = (int32_t)cpre;
             }
             s_count[i] = N.count;
             rows = (unsigned long long)(N.count / 2);  // at most the smaller child's
           }
+        }
+        if (a.mode == kLevelMove && j == 0) {
+          s_tb[n_exp] = (int32_t)tcar;
+          tile_begin[n_exp] = (int32_t)tcar;
         }
         rows = wave_sum(rows);
         __builtin_amdgcn_wave_barrier();
@@ -2527,36 +2726,24 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
         // in place a task tiles twice as many of its parent's rows, of which
         // it adds those of the smaller child (at most half).
         th = plan_tile_rows((int64_t)rows, a) * (a.mode == kLevelInPlace ? 2 : 1);
-        uint32_t nt = 0, nh = 0;
+        uint32_t nh = 0;
         if (j < n_exp) {
-          nt = grouped ? 0u : (uint32_t)s_tb[j];
           const int64_t cnt = s_count[j];
           nh = a.last ? 0u
                       : a.mode == kLevelInPlace ? (uint32_t)max((int64_t)1, div_pos(cnt + th - 1, th))
                                                 : (uint32_t)div_pos(cnt / 2 + th, th);
         }
-        // Tiles in the low word, histogram tasks in the high word.
-        const unsigned long long tv = ((unsigned long long)nh << 32) | nt;
-        const unsigned long long tincl = wave_incl_scan<unsigned long long>(tv);
-        const unsigned long long tpre = tincl - tv, ttot = wave_lane(tincl, 63);
-        if (!grouped) tcar = (uint32_t)ttot;
-        hcar = (uint32_t)(ttot >> 32);
+        const uint32_t hincl = wave_incl_scan<uint32_t>(nh);
+        const uint32_t hpre = hincl - nh;
+        hcar = wave_lane(hincl, 63);
         if (tcar > (uint32_t)a.tile_cap || hcar > (uint32_t)a.hist_cap) {
           status = 2;  // capacities are sized from proven bounds; reaching this is a bug
         } else {
           if (j < n_exp) {
-            if (!grouped) {
-              s_tb[j] = (int32_t)(uint32_t)tpre;
-              tile_begin[j] = (int32_t)(uint32_t)tpre;
-            }
-            s_hb[j] = (int32_t)(uint32_t)(tpre >> 32);
-            hist_begin[j] = (int32_t)(uint32_t)(tpre >> 32);
+            s_hb[j] = (int32_t)hpre;
+            hist_begin[j] = (int32_t)hpre;
           }
           if (j == 0) {
-            if (!grouped) {
-              s_tb[n_exp] = (int32_t)tcar;
-              tile_begin[n_exp] = (int32_t)tcar;
-            }
             s_hb[n_exp] = (int32_t)hcar;
             hist_begin[n_exp] = (int32_t)hcar;
           }
@@ -2583,12 +2770,15 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
         q.n_nodes = n_prev;
         q.overflow = status == 1 ? s_fast[6] : -1;
         *plan = q;
+        plan_next_level(level_out, n_prev, 0);
       }
       return;
     }
     // Tile and histogram-task lists: item -> its group (parent) by binary
-    // search.
-    for (int t = tid; t < tcar; t += kPlanBlock) {
+    // search.  (In place the counting blocks tile the candidates themselves:
+    // no tile list.)
+    const int32_t listed = a.mode == kLevelInPlace ? 0 : tcar;
+    for (int t = tid; t < listed; t += kPlanBlock) {
       int lo = 0, hi = n_groups - 1;
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -2621,6 +2811,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       q.n_nodes = (int32_t)((int64_t)n_prev + 2 * (int64_t)n_exp);
       q.overflow = 0;
       *plan = q;
+      plan_next_level(level_out, n_prev, 2 * n_exp);
     }
     return;
   }
@@ -2631,7 +2822,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
   // ranks go through registers so that their LDS stores wait after every
   // load is issued.  (first <= kPlanLdsC + 1 <= kPlanBlock: one per thread.)
   const double ke0 = tid < first ? kept_e[tid] : 0.0;
-  PartParent pq{0, 0, 0, 0, -1, -1, -1, 0};  // previous parent tid (a grouped level's grandparent)
+  PartParent pq{0, 0, 0, 0, -1, -1, -1, 0, 0, 0};  // previous parent tid (a grouped level's grandparent)
   double pe = 0.0;
   if (tid < n_pp) {
     pq = prev_parents[tid];
@@ -2781,56 +2972,59 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       q.n_nodes = n_prev;
       q.overflow = (int32_t)min(n_new, (int64_t)INT32_MAX);
       *plan = q;
+      plan_next_level(level_out, n_prev, 0);
     }
     return;
   }
 
-  // A grouped level's groups: the previous parents with an expanded child,
-  // each with its tiles over the previous parent's segment.
-  if (a.mode == kLevelGrouped) {
-    if (tid < nc) s_pidx[tid] = fl ? (int32_t)pidx : -1;
-    __syncthreads();
-    int32_t pl = -1, pr = -1;
-    uint32_t ge = 0u, gt = 0u;
-    if (tid < n_pp) {
-      pl = s_pidx[2 * tid];
-      pr = s_pidx[2 * tid + 1];
-      ge = (pl >= 0 || pr >= 0) ? 1u : 0u;
-      const int64_t a0 = pq.start & ~int64_t(15);
-      gt = ge ? (uint32_t)max((int64_t)1, div_pos(pq.start + pq.count - a0 + a.part_tile - 1, a.part_tile))
-              : 0u;
+  // Partition tiles, one item per thread in order (as the fast path): in
+  // place every candidate and grouped every previous parent (counted by the
+  // launch's other blocks, plan_count_role), moving the expanded parents
+  // (k_part_count).  Item i's tiles are [s_ctb[i], s_ctb[i + 1]).
+  {
+    uint32_t ntc = 0u;
+    if (a.mode == kLevelInPlace) {
+      if (tid < nc) ntc = count_item_tiles(s_start[tid], s_count[tid], s_valid[tid] != 0, a.part_tile);
+    } else if (grouped) {
+      if (tid < n_pp) ntc = count_item_tiles(pq.start, pq.count, true, a.part_tile);
+    } else if (fl) {
+      ntc = count_item_tiles(s_start[tid], s_count[tid], true, a.part_tile);
     }
-    // Both scans in one: groups in the low word, tiles in the high word.
-    unsigned long long gtot;
-    const unsigned long long gpre =
-        block_excl_scan<kPlanBlock>(((unsigned long long)gt << 32) | ge, stmp64, gtot);
-    const uint32_t gidx = (uint32_t)gpre, toff = (uint32_t)(gpre >> 32);
-    const uint32_t n_groups = (uint32_t)gtot, tcar_g = (uint32_t)(gtot >> 32);
-    if (tid < n_pp) {
-      s_gi[tid] = ge ? (int32_t)gidx : -1;
-      if (ge) {
-        PartGroup G;
-        G.start = pq.start;
-        G.count = pq.count;
-        G.fpos = pq.fpos;
-        G.bin = pq.bin;
-        G.par[0] = pl;
-        G.par[1] = pr;
-        groups[gidx] = G;
-        s_tb[gidx] = (int32_t)toff;
-        s_gs[gidx] = pq.start & ~int64_t(15);
-        tile_begin[gidx] = (int32_t)toff;
-      }
-    }
+    uint32_t ctot;
+    const uint32_t cpre = block_excl_scan<kPlanBlock>(ntc, stmp, ctot);
+    if (tid < kPlanLdsC) s_ctb[tid] = cpre;
     if (tid == 0) {
-      s_tb[n_groups] = (int32_t)tcar_g;
-      tile_begin[n_groups] = (int32_t)tcar_g;
-      s_tcar = n_groups;  // (the group count, until the tile scan below)
+      s_ctb[kPlanLdsC] = ctot;
+      s_tcar = ctot;
     }
     __syncthreads();
   }
 
-  // Records, parents, ranks; tiles per parent; rows to build.
+  // A grouped level's groups: every previous parent, par -1 for a side
+  // that is not expanded (its rows stay), tiles over its segment.
+  if (grouped) {
+    if (tid < nc) s_pidx[tid] = fl ? (int32_t)pidx : -1;
+    __syncthreads();
+    if (tid < n_pp) {
+      PartGroup G;
+      G.start = pq.start;
+      G.count = pq.count;
+      G.fpos = pq.fpos;
+      G.bin = pq.bin;
+      G.par[0] = s_pidx[2 * tid];
+      G.par[1] = s_pidx[2 * tid + 1];
+      groups[tid] = G;
+      s_tb[tid] = (int32_t)s_ctb[tid];
+      s_gs[tid] = pq.start & ~int64_t(15);
+      tile_begin[tid] = (int32_t)s_ctb[tid];
+    }
+    if (tid == 0) {
+      s_tb[n_pp] = (int32_t)s_ctb[n_pp];
+      tile_begin[n_pp] = (int32_t)s_ctb[n_pp];
+    }
+  }
+
+  // Records, parents, ranks; rows to build.
   unsigned long long rows = 0;
   if (tid < nc) {
     const int32_t v = first + tid;
@@ -2859,17 +3053,24 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       P.left_id = L;
       P.right_id = L + 1;
       P.node = v;
-      P.gslot = a.mode == kLevelGrouped ? 2 * s_gi[tid >> 1] + (tid & 1) : 2 * i;
+      P.gslot = grouped ? tid : 2 * i;  // grouped: 2 * group (tid >> 1) + side
+      const int32_t it = grouped ? (tid >> 1) : tid;  // the item counting its rows
+      P.tile0 = (int32_t)s_ctb[it];
+      P.tile1 = (int32_t)s_ctb[it + 1];
       parents[i] = P;
       parent_e[i] = N.e;
-      if (a.mode != kLevelGrouped) {
-        const int64_t a0 = N.start & ~int64_t(15);
-        // At least one tile: a parent's first tile writes its children's segments.
-        s_tb[i] = (int32_t)max((int64_t)1, div_pos(N.start + N.count - a0 + a.part_tile - 1, a.part_tile));
+      if (a.mode == kLevelMove) {
+        s_tb[i] = (int32_t)s_ctb[tid];
+        s_gs[i] = N.start & ~int64_t(15);
+        tile_begin[i] = (int32_t)s_ctb[tid];
       }
       s_pj[i] = tid;
       rows = (unsigned long long)(N.count / 2);  // at most the smaller child's
     }
+  }
+  if (a.mode == kLevelMove && tid == 0) {
+    s_tb[n_exp] = (int32_t)s_tcar;
+    tile_begin[n_exp] = (int32_t)s_tcar;
   }
   rows = wave_sum(rows);
   if (lane == 0 && rows) atomicAdd(&s_rows, rows);
@@ -2879,25 +3080,17 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
   // those of the smaller child (at most half).
   const int32_t th = plan_tile_rows((int64_t)s_rows, a) * (a.mode == kLevelInPlace ? 2 : 1);
 
-  // Exclusive offsets of each parent's tiles (a grouped level: its groups'
-  // tiles, already laid out) and histogram tasks.
-  uint32_t nt = 0, nh = 0;
+  // Exclusive offsets of each parent's histogram tasks.
+  uint32_t nh = 0;
   if (tid < n_exp) {
-    nt = grouped ? 0u : (uint32_t)s_tb[tid];
     const int64_t cnt = s_count[s_pj[tid]];
     nh = a.last ? 0u
                 : a.mode == kLevelInPlace ? (uint32_t)max((int64_t)1, div_pos(cnt + th - 1, th))
                                           : (uint32_t)div_pos(cnt / 2 + th, th);
   }
-  const int32_t n_groups = grouped ? (int32_t)s_tcar : n_exp;
-  // Both scans in one: tiles in the low word, histogram tasks in the high.
-  unsigned long long thtot;
-  const unsigned long long thpre =
-      block_excl_scan<kPlanBlock>(((unsigned long long)nh << 32) | nt, stmp64, thtot);
-  const uint32_t tp = (uint32_t)thpre, hp = (uint32_t)(thpre >> 32);
-  uint32_t tcar = (uint32_t)thtot;
-  const uint32_t hcar = (uint32_t)(thtot >> 32);
-  if (grouped) tcar = (uint32_t)s_tb[n_groups];
+  uint32_t hcar;
+  const uint32_t hp = block_excl_scan<kPlanBlock>(nh, stmp, hcar);
+  const uint32_t tcar = s_tcar;
   if (tcar > (uint32_t)a.tile_cap || hcar > (uint32_t)a.hist_cap) {
     // Capacities are sized from proven bounds; reaching this is a bug.
     if (tid == 0) {
@@ -2907,32 +3100,26 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
       q.n_nodes = n_prev;
       q.overflow = -1;
       *plan = q;
+      plan_next_level(level_out, n_prev, 0);
     }
     return;
   }
-  __syncthreads();  // s_tb is rewritten below
   if (tid < n_exp) {
-    if (!grouped) {
-      s_tb[tid] = (int32_t)tp;
-      tile_begin[tid] = (int32_t)tp;
-      s_gs[tid] = s_start[s_pj[tid]] & ~int64_t(15);
-    }
     s_hb[tid] = (int32_t)hp;
     hist_begin[tid] = (int32_t)hp;
   }
   if (tid == 0) {
-    if (!grouped) {
-      s_tb[n_exp] = (int32_t)tcar;
-      tile_begin[n_exp] = (int32_t)tcar;
-    }
     s_hb[n_exp] = (int32_t)hcar;
     hist_begin[n_exp] = (int32_t)hcar;
   }
   __syncthreads();
 
   // Tile and histogram-task lists: item -> its group (parent) by binary
-  // search.
-  for (int t = tid; t < (int)tcar; t += kPlanBlock) {
+  // search.  (In place the counting blocks tile the candidates themselves:
+  // no tile list.)
+  const int32_t n_groups = grouped ? n_pp : n_exp;
+  const int32_t listed = a.mode == kLevelInPlace ? 0 : (int32_t)tcar;
+  for (int t = tid; t < listed; t += kPlanBlock) {
     int lo = 0, hi = n_groups - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -2965,6 +3152,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_lds(
     q.n_nodes = (int32_t)n_new;
     q.overflow = 0;
     *plan = q;
+    plan_next_level(level_out, n_prev, 2 * n_exp);
   }
 }
 
@@ -2975,10 +3163,16 @@ hipError_t launch_plan_lds(hipStream_t st, NodeOut *nodes, LevelPlan *plan,
                            HistTask *hist_tasks, const NodeSeg *segs,
                            const long long *totals, const SplitCand *cand, double *kept_e,
                            const double *prev_parent_e, double *parent_e, int32_t F_sel,
-                           PlanArgs a) {
-  hipLaunchKernelGGL(k_plan_lds, dim3(1), dim3(kPlanBlock), 0, st, nodes, plan, prev_parents,
+                           PlanArgs a, const uint8_t *codes_c, int64_t ld_c,
+                           int32_t *tile_cnt, const int32_t *level_in, int32_t *level_out,
+                           int32_t count_blocks) {
+  if (a.fused_count && (a.part_rows != 4 && a.part_rows != 8 && a.part_rows != 16))
+    return hipErrorInvalidValue;
+  const unsigned grid = 1u + (a.fused_count ? (unsigned)std::max(1, count_blocks) : 0u);
+  hipLaunchKernelGGL(k_plan_lds, dim3(grid), dim3(kPlanBlock), 0, st, nodes, plan, prev_parents,
                      parents, groups, tile_begin, hist_begin, tiles, hist_tasks, segs,
-                     totals, cand, kept_e, prev_parent_e, parent_e, F_sel, a);
+                     totals, cand, kept_e, prev_parent_e, parent_e, F_sel, a, codes_c, ld_c,
+                     tile_cnt, level_in, level_out);
   return hipGetLastError();
 }
 

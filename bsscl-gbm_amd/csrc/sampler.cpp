@@ -804,9 +804,16 @@ struct Sampler {
     int32_t index = 0;
     std::atomic<int32_t> pending{0};  // segments still being written, +1 while counting
     bool done = false;                // draws complete (and copied): deliverable
+    bool on_device = false;           // draws_d holds this round's draws
   };
   int32_t device = -1;                // GPU of the device copies
-  hipStream_t copy_st = nullptr;
+  hipStream_t copy_st = nullptr;      // the process's copy stream (copy_stream)
+  // Device-rows mode: rounds finished before the first take keep their
+  // draws on the host, and the first take copies them; later rounds are
+  // copied as soon as they are drawn.  A sampler made before its fit bins X
+  // then draws its first rounds meanwhile, and allocates its device buffers
+  // after the engine's.
+  std::atomic<bool> device_go{false};
 
   std::atomic<bool> halt{false};     // makes the draw thread's stream stop
   std::atomic<double> gen_ms{0.0};   // word generation (inside draw_ms)
@@ -880,12 +887,9 @@ struct Sampler {
   // Device-rows mode: the round's draws go to the GPU on the sampler's own
   // stream, so the copy overlaps the engine's work on the previous round.
   bool copy_to_device(Round &R) {
-    if (!copy_st) {
-      if (hipSetDevice(device) != hipSuccess ||
-          hipStreamCreateWithFlags(&copy_st, hipStreamNonBlocking) != hipSuccess) {
-        fail("sampler: cannot create the copy stream");
-        return false;
-      }
+    if (!copy_st || hipSetDevice(device) != hipSuccess) {
+      fail("sampler: no copy stream");
+      return false;
     }
     if (!R.draws_d && hipMalloc(reinterpret_cast<void **>(&R.draws_d), (size_t)n * 4) != hipSuccess) {
       R.draws_d = nullptr;
@@ -906,6 +910,7 @@ struct Sampler {
       fail("sampler: hipEventRecord failed");
       return false;
     }
+    R.on_device = true;
     return true;
   }
 
@@ -920,7 +925,9 @@ struct Sampler {
   // mode), then hand every complete round at the head of `inflight` on, in
   // round order.
   void finalize(Round *R) {
-    if (device_rows && do_rows && !copy_to_device(*R)) return;
+    if (device_rows && do_rows && device_go.load(std::memory_order_acquire) &&
+        !copy_to_device(*R))
+      return;
     {
       std::lock_guard<std::mutex> lk(mu);
       R->done = true;
@@ -1188,6 +1195,7 @@ struct Sampler {
       if (!R) R.reset(new Round());
       R->draws.alloc((size_t)n + 16);
       R->done = false;
+      R->on_device = false;
       R->pending.store(1, std::memory_order_relaxed);  // this thread's share
       Round *Rp = R.get();
       {
@@ -1285,6 +1293,7 @@ struct Sampler {
         if (!R) R.reset(new Round());
         if (do_rows) R->draws.alloc((size_t)n + 16);
         R->done = false;
+        R->on_device = false;
         R->pending.store(1, std::memory_order_relaxed);  // this thread's share
         Round *Rp = R.get();
         {
@@ -1398,7 +1407,7 @@ struct Sampler {
       for (auto &r : ready) free_device(*r);
       for (auto &r : pool) free_device(*r);
       for (auto &r : inflight) free_device(*r);
-      (void)hipStreamDestroy(copy_st);
+      // (copy_st is the process's copy stream: it stays.)
     }
   }
 };
@@ -1406,10 +1415,17 @@ struct Sampler {
 int sampler_take(bsscl_sampler *hs, SamplerRound *out, void **token) {
   Sampler *s = reinterpret_cast<Sampler *>(hs);
   if (!s || !out || !token) return set_error(BSSCL_EINVAL, "sampler: null argument");
+  if (s->device_rows && s->do_rows) s->device_go.store(true, std::memory_order_release);
   Sampler::Round *r = s->take();
   if (!r) {
     std::lock_guard<std::mutex> lk(s->mu);
     return set_error(BSSCL_EINVAL, s->error.empty() ? "sampler: all rounds consumed" : s->error);
+  }
+  // A round drawn before the first take is copied by the taker.
+  if (s->device_rows && s->do_rows && !r->on_device && !s->copy_to_device(*r)) {
+    s->give(r);
+    std::lock_guard<std::mutex> lk(s->mu);
+    return set_error(BSSCL_EDEVICE, s->error.empty() ? "sampler: draws copy failed" : s->error);
   }
   out->draws = s->do_rows ? r->draws.p : nullptr;
   out->draws_dev = (s->do_rows && s->device_rows) ? r->draws_d : nullptr;
@@ -1521,6 +1537,11 @@ int bsscl_sampler_create(const uint32_t *key, int32_t pos, int64_t n,
     if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) {
       delete s;
       return bsscl::set_error(BSSCL_EINVAL, "sampler_create: device-rows mode needs a valid HIP device");
+    }
+    s->copy_st = bsscl::copy_stream(device);
+    if (!s->copy_st) {
+      delete s;
+      return bsscl::set_error(BSSCL_EDEVICE, "sampler_create: no copy stream");
     }
   }
   s->n_rounds = n_rounds;
