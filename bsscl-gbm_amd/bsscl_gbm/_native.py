@@ -40,6 +40,7 @@ _SIGS = {
                           _f64, _P, _P, _P, _P, _P, _P, _P, _P],
     "bsscl_boost_get_F": [_P, _P],
     "bsscl_boost_grad_hess": [_P, _P, _P],
+    "bsscl_boost_grad_hess_max": [_P, _P],
     "bsscl_mc_begin": [_P, _P, _i64, _i32, _P],
     "bsscl_mc_round": [_P, _P, _i64],
     "bsscl_mc_build_tree": [_P, _i32, _P, _i32, _i32, _i32, _i32, _f64, _P, _i32, _f64,
@@ -325,6 +326,13 @@ class Engine:
         h = np.empty(n, np.float64)
         check(lib().bsscl_boost_grad_hess(self.handle, ptr(g), ptr(h)))
         return g, h
+
+    def boost_grad_hess_max(self):
+        """(max |g|, max h) of the current F as the device holds them for the
+        next round's fixed-point scale."""
+        out = np.empty(2, np.float64)
+        check(lib().bsscl_boost_grad_hess_max(self.handle, ptr(out)))
+        return float(out[0]), float(out[1])
 
     def predict(self, slot, n, packed, n_trees, learning_rate):
         out = np.empty(n, np.float64)

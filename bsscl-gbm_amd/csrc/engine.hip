@@ -293,6 +293,16 @@ struct bsscl_engine {
   DevBuf<double> g64, h64;
   double g_scale = 1.0, h_scale = 1.0;  // fixed point -> value
   double h_bound = 0.0;  // no hessian of the current tree's rows exceeds this
+  // The largest |g| and h over all rows of the current F, as k_update_F
+  // leaves them: two slots of [max |g|, max h].  gh_slot holds the current
+  // F's; the update that makes the next F raises the other slot and clears
+  // this one.  A boosting round on the device path scales its tree's fixed
+  // point from them (gh_ok; BSSCL_TEST_BOUND_SCALE=1 keeps the bound
+  // max(w0, w1) instead).
+  DevBuf<unsigned long long> ghmax_d;
+  int32_t gh_slot = 0;
+  bool gh_ok = false;
+  DevScale round_dev{nullptr, 0, 0};  // the tree being enqueued (split_params)
 
   // Multiclass run on matrix 0: scores, gradients and hessians [K][n], the
   // rows' class and weight, each class's largest |g| and h of the round.
@@ -642,10 +652,14 @@ int expand_features(const Matrix &X, const std::vector<int32_t> &feats,
 // so any such sum (and the difference of two nested ones) fits in int64.
 // The widest exponent the sums allow: a bin of many tiny, equal hessians
 // (confident rows late in a fit) then keeps its relative precision.
-double fixed_mul(double max_abs, int64_t rows) {
+int32_t fixed_bits(int64_t rows) {
   int lg = 1;
   while (lg < 62 && (int64_t(1) << lg) < rows) ++lg;
-  const int B = 62 - lg;
+  return 62 - lg;
+}
+
+double fixed_mul(double max_abs, int64_t rows) {
+  const int B = fixed_bits(rows);
   if (!(max_abs > 0.0) || !std::isfinite(max_abs)) return std::ldexp(1.0, B);
   int e;
   std::frexp(max_abs, &e);  // max_abs < 2^e
@@ -1011,6 +1025,7 @@ SplitParams split_params(bsscl_engine *E, const TreeParams &tp) {
   sp.h_scale = E->h_scale;
   sp.min_samples_leaf = tp.min_samples_leaf;
   sp.max_depth = tp.max_depth;
+  sp.dev = E->round_dev;
   return sp;
 }
 
@@ -1768,6 +1783,31 @@ int run_graph(bsscl_engine *E, RoundGraph &g, const std::vector<uint64_t> &key, 
   return BSSCL_OK;
 }
 
+// The fixed-point multipliers of a boosting tree over m rows on the
+// host-driven path, from the largest |g| and h of the current F as the
+// device holds them (read back; the host-driven path waits for the stream
+// anyway), so the path quantises as the device path does; from the bound
+// max(w0, w1) when the device holds none or BSSCL_TEST_BOUND_SCALE=1.  Sets
+// the engine's scales to match.
+int host_round_scales(bsscl_engine *E, int64_t m, double &gm, double &hm) {
+  const double wmax = std::max(E->w0, E->w1);
+  double gmax = wmax, hmax = 0.25 * wmax;
+  const char *bound_env = std::getenv("BSSCL_TEST_BOUND_SCALE");
+  if (E->gh_ok && !(bound_env && bound_env[0] == '1')) {
+    unsigned long long bits[2];
+    HIPCHK(hipMemcpyAsync(bits, E->ghmax_d.p + 2 * E->gh_slot, sizeof(bits),
+                          hipMemcpyDeviceToHost, E->st));
+    HIPCHK(hipStreamSynchronize(E->st));
+    std::memcpy(&gmax, &bits[0], 8);
+    std::memcpy(&hmax, &bits[1], 8);
+  }
+  gm = fixed_mul(gmax, m);
+  hm = fixed_mul(hmax, m);
+  E->g_scale = 1.0 / gm;
+  E->h_scale = 1.0 / hm;
+  return BSSCL_OK;
+}
+
 // Enqueues one boosting round: gradients from the current F (est:2868),
 // the sampler's round (est:2886, est:2502-2517), the tree, its replay
 // (est:641-820), F += lr * tree(X) and the training log-loss, and the
@@ -1782,8 +1822,10 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   if (sh.n != X.n) return set_error(BSSCL_EINVAL, "boost_round: sampler rows differ from matrix rows");
   ++E->round_seq;
   // Gradients from the current F: |g| <= max(w0, w1), h <= max(w0, w1)/4.
+  // (The device path scales from the maxima themselves, see dev_scale; the
+  // host-driven path reads them back, host_round_scales.)
   const double wmax = std::max(E->w0, E->w1);
-  const double gm = fixed_mul(wmax, m), hm = fixed_mul(0.25 * wmax, m);
+  double gm = fixed_mul(wmax, m), hm = fixed_mul(0.25 * wmax, m);
   E->g_scale = 1.0 / gm;
   E->h_scale = 1.0 / hm;
   E->h_bound = 0.25 * wmax;
@@ -1804,6 +1846,8 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   auto fail = [&](int rc) {
     (void)hipStreamSynchronize(E->st_rows);
     (void)hipStreamSynchronize(E->st);
+    E->gh_ok = false;  // the device maxima may be out of step with gh_slot
+    E->round_dev = DevScale{nullptr, 0, 0};
     sampler_give_back(sampler, token);
     R.active = false;
     R.token = nullptr;
@@ -1982,6 +2026,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   if (rc == BSSCL_OK) rc = ensure_round_out(E, s, R.M, nb);
   // Gradients from the current F (est:2868): for every row on the
   // host-driven path, which gathers them itself.
+  if (rc == BSSCL_OK && !R.device_replay) rc = host_round_scales(E, m, gm, hm);
   if (rc == BSSCL_OK && !R.device_replay) {
     const hipError_t e = launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, gm, hm,
                                           E->ghq.p);
@@ -2003,6 +2048,19 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     ra.node_cap = E->node_cap;
     ra.max_depth = a.max_depth;
     ra.pad = 0;
+    // The tree's fixed point from the largest |g| and h of the current F
+    // (every row's; the in-bag rows are among them), which the previous
+    // F update or boost_begin left on the device.
+    const char *bound_env = std::getenv("BSSCL_TEST_BOUND_SCALE");
+    const bool dev_scale = E->gh_ok && !(bound_env && bound_env[0] == '1');
+    DevScale dv{nullptr, 0, 0};
+    unsigned long long *gh_next = nullptr, *gh_cur = nullptr;
+    if (E->gh_ok) {
+      gh_cur = E->ghmax_d.p + 2 * E->gh_slot;
+      gh_next = E->ghmax_d.p + 2 * (E->gh_slot ^ 1);
+    }
+    if (dev_scale) dv = DevScale{gh_cur, fixed_bits(m), 0};
+    ra.dev = dv;
     R.table_readback = E->prof && !replay_counts_nodes(ra);
     char *const partials = E->round_d[s].p + round_out_bytes(R.M);
     const bool checks = !E->pipeline;
@@ -2011,18 +2069,22 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     // host sums (sum_partials_host).
     auto tree_launches = [&]() -> int {
       hipError_t e = launch_gather_gh(E->st, E->F.p, E->y.p, E->round_rows[s].p, m, E->w0,
-                                      E->w1, gm, hm, E->gh_c[2 * s].p, E->ld_c, E->segs.p,
+                                      E->w1, gm, hm, dv, E->gh_c[2 * s].p, E->ld_c, E->segs.p,
                                       E->hist_node_d.p,
                                       reinterpret_cast<const LevelPlan *>(pre.dev[kPackPlan]),
                                       E->plan_d);
       if (e != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("gradients: ") + hipGetErrorString(e));
-      CHK(launch_tree(E, E->round_rows[s].p, m, R.feats, R.nb_sel, tp, &R.run, checks, true, &pre));
+      E->round_dev = dv;
+      const int trc = launch_tree(E, E->round_rows[s].p, m, R.feats, R.nb_sel, tp, &R.run,
+                                  checks, true, &pre);
+      E->round_dev = DevScale{nullptr, 0, 0};
+      CHK(trc);
       e = launch_replay(E->st, E->nodes_d, E->plan_d, E->feat_d, ra,
                         round_arrays(E->round_d[s].p, R.M), E->tree_d.p, hdr);
       if (e == hipSuccess)
         e = launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, R.M, &hdr->node_count,
                             a.learning_rate, E->F.p, E->y.p, reinterpret_cast<double *>(partials),
-                            nb);
+                            nb, E->w0, E->w1, gh_next, gh_cur);
       // The round's readback (tree arrays and losses) into pinned memory,
       // inside the graph: an operation enqueued after a graph waits for
       // the graph's completion, which costs microseconds per round.
@@ -2053,6 +2115,8 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
         key_add(key, v);
       for (double v : {tp.mcw, tp.lam, tp.gamma, a.learning_rate, gm, hm, E->w0, E->w1})
         key_add(key, v);
+      for (int64_t v : {(int64_t)E->gh_ok, (int64_t)dev_scale, (int64_t)E->gh_slot})
+        key_add(key, v);
       // (round_pin is host memory: its address is not covered by the
       // allocation count.)
       for (const void *ptr : {(const void *)X.codes.p, (const void *)pre.dev[kPackFeat],
@@ -2079,6 +2143,8 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     if (e == hipSuccess && !R.done) e = hipEventCreateWithFlags(&R.done, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventRecord(R.done, E->st);
     if (rc == BSSCL_OK && e != hipSuccess) rc = set_error(BSSCL_EDEVICE, std::string("round: ") + hipGetErrorString(e));
+    // The F update raised the other slot.
+    if (rc == BSSCL_OK && E->gh_ok) E->gh_slot ^= 1;
   }
   if (rc != BSSCL_OK) return fail(rc);
   E->launched_round = true;
@@ -2150,10 +2216,10 @@ int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
   if (h.status == 1) E->node_cap_floor = std::max(h.needed, 2 * E->node_cap);
   {
     // Gradients of every row from the unchanged F (the device path gathered
-    // only the in-bag rows').
-    const double wmax = std::max(E->w0, E->w1);
-    HIPCHK(launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, fixed_mul(wmax, R.m),
-                            fixed_mul(0.25 * wmax, R.m), E->ghq.p));
+    // only the in-bag rows'), with the scales the device path used.
+    double gm = 0.0, hm = 0.0;
+    CHK(host_round_scales(E, R.m, gm, hm));
+    HIPCHK(launch_grad_hess(E->st, E->F.p, E->y.p, X.n, E->w0, E->w1, gm, hm, E->ghq.p));
   }
   E->set_base = 2 * s;
   CHK(build_tree_core(E, E->round_rows[s].p, R.m, R.feats, R.nb_sel, tp, out));
@@ -2162,8 +2228,19 @@ int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
   tree_to_reference(X, out);
   const int nb = update_F_blocks(X.n);
   CHK(E->loss_d.ensure(1));
-  HIPCHK(launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p, *out.node_count, nullptr,
-                         R.args.learning_rate, E->F.p, E->y.p, E->partials_d.p, nb));
+  {
+    unsigned long long *gh_cur = E->gh_ok ? E->ghmax_d.p + 2 * E->gh_slot : nullptr;
+    unsigned long long *gh_next = E->gh_ok ? E->ghmax_d.p + 2 * (E->gh_slot ^ 1) : nullptr;
+    const hipError_t e2 = launch_update_F(E->st, X.codes.p, X.ld, X.n, E->tree_d.p,
+                                          *out.node_count, nullptr, R.args.learning_rate,
+                                          E->F.p, E->y.p, E->partials_d.p, nb, E->w0, E->w1,
+                                          gh_next, gh_cur);
+    if (e2 != hipSuccess) {
+      E->gh_ok = false;
+      return set_error(BSSCL_EDEVICE, std::string("F update: ") + hipGetErrorString(e2));
+    }
+    if (E->gh_ok) E->gh_slot ^= 1;
+  }
   HIPCHK(launch_sum_partials(E->st, E->partials_d.p, nb, E->loss_d.p));
   double sum = 0.0;
   HIPCHK(hipMemcpyAsync(&sum, E->loss_d.p, 8, hipMemcpyDeviceToHost, E->st));
@@ -2273,6 +2350,7 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   }
   for (auto &m : E->mat) m.codes.release();
   E->F.release();
+  E->ghmax_d.release();
   E->y.release();
   E->ghq.release();
   E->g64.release();
@@ -2675,7 +2753,18 @@ int bsscl_boost_begin(bsscl_engine *E, const int64_t *y, int64_t n, double w0,
   CHK(E->ghq.ensure((size_t)n));
   HIPCHK(hipMemcpyAsync(E->y.p, yb.data(), (size_t)n, hipMemcpyHostToDevice, E->st));
   HIPCHK(launch_fill_f64(E->st, E->F.p, n, base_score));  // F starts at base_score (est:2834)
+  // The largest |g| and h of the starting F into slot 0 (an F update with
+  // no tree).
+  E->gh_ok = false;
+  const int nb = update_F_blocks(n);
+  CHK(E->ghmax_d.ensure(4));
+  CHK(E->partials_d.ensure((size_t)nb));
+  HIPCHK(hipMemsetAsync(E->ghmax_d.p, 0, 4 * sizeof(unsigned long long), E->st));
+  HIPCHK(launch_update_F(E->st, E->mat[0].codes.p, E->mat[0].ld, n, nullptr, 0, nullptr, 0.0,
+                         E->F.p, E->y.p, E->partials_d.p, nb, w0, w1, E->ghmax_d.p, nullptr));
   HIPCHK(hipStreamSynchronize(E->st));
+  E->gh_slot = 0;
+  E->gh_ok = true;
   E->w0 = w0;
   E->w1 = w1;
   E->boosting = true;
@@ -2917,6 +3006,19 @@ int bsscl_boost_get_F(bsscl_engine *E, double *F_out) {
   HIPCHK(hipSetDevice(E->device));
   HIPCHK(hipMemcpyAsync(F_out, E->F.p, (size_t)E->mat[0].n * 8, hipMemcpyDeviceToHost, E->st));
   HIPCHK(hipStreamSynchronize(E->st));
+  return BSSCL_OK;
+}
+
+int bsscl_boost_grad_hess_max(bsscl_engine *E, double *out) {
+  if (!E || !out) return set_error(BSSCL_EINVAL, "boost_grad_hess_max: null argument");
+  if (!E->boosting) return set_error(BSSCL_EINVAL, "boost_grad_hess_max: no boosting run");
+  if (!E->gh_ok) return set_error(BSSCL_EINVAL, "boost_grad_hess_max: no maxima on the device");
+  HIPCHK(hipSetDevice(E->device));
+  unsigned long long bits[2];
+  HIPCHK(hipMemcpyAsync(bits, E->ghmax_d.p + 2 * E->gh_slot, sizeof(bits), hipMemcpyDeviceToHost,
+                        E->st));
+  HIPCHK(hipStreamSynchronize(E->st));
+  std::memcpy(out, bits, sizeof(bits));
   return BSSCL_OK;
 }
 

@@ -130,6 +130,17 @@ struct SplitCand {
   int32_t pad;
 };
 
+// The largest |g| and h of a boosting round's rows, held on the device as
+// the bit patterns of non-negative doubles (which order as unsigned
+// integers), and the bits a row's fixed-point value may use
+// (62 - ceil(log2(rows summed))).  A kernel given `max` takes its scales
+// from them (dev_fixed_mul); with max == nullptr it uses the host's.
+struct DevScale {
+  const unsigned long long *max;  // [max |g|, max h] or nullptr
+  int32_t bits;
+  int32_t pad;
+};
+
 struct SplitParams {
   double min_child_weight;
   double reg_lambda;
@@ -137,6 +148,7 @@ struct SplitParams {
   double h_scale;      // 2^-sh: fixed point -> hessian
   int32_t min_samples_leaf;
   int32_t max_depth;
+  DevScale dev;
 };
 
 // A tree in device form for traversal (node_count entries).
@@ -193,6 +205,7 @@ struct ReplayArgs {
   double reg_lambda;
   double g_scale;
   double h_scale;
+  DevScale dev;        // device-held scales (SplitParams::dev)
   int32_t max_leaves;
   int32_t out_len;     // 2 * max_leaves + 2 entries per output array
   int32_t stage_limit; // node records are staged in LDS up to this many nodes
@@ -269,8 +282,8 @@ hipError_t launch_gather_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
                                int64_t m, uint8_t *codes_c, int64_t ld_c, int64_t pad_to);
 hipError_t launch_gather_gh(hipStream_t st, const double *F, const uint8_t *y,
                             const int32_t *rows32, int64_t m, double w0, double w1,
-                            double g_mul, double h_mul, GH *gh_c, int64_t pad_to,
-                            NodeSeg *segs, int32_t *hist_node,
+                            double g_mul, double h_mul, DevScale dev, GH *gh_c,
+                            int64_t pad_to, NodeSeg *segs, int32_t *hist_node,
                             const LevelPlan *plan_src = nullptr,
                             LevelPlan *plan_dst = nullptr);
 // Level kernels take their work counts from a device LevelPlan; the grid
@@ -382,11 +395,17 @@ hipError_t launch_code_counts(hipStream_t st, const uint8_t *codes, int64_t ld,
                               int64_t n, int32_t F, unsigned int *counts);
 // F += lr * tree(row) for every row unless *node_count_d == 0 (then F is
 // left alone); per-block partial sums of the training log-likelihood.
+// gh_max_out (optional): raised to the largest |g| and h (logistic_gh with
+// weights w0, w1) of the updated F over all rows, one atomic max per block
+// that exceeds it; gh_max_clear (optional) is set to zero by block 0.
+// tree_len == 0 leaves F unchanged.
 hipError_t launch_update_F(hipStream_t st, const uint8_t *codes, int64_t ld,
                            int64_t n, const TreeNodeDev *tree, int32_t tree_len,
                            const int32_t *node_count_d, double lr, double *F,
                            const uint8_t *y, double *loss_partials,
-                           int32_t n_blocks);
+                           int32_t n_blocks, double w0 = 1.0, double w1 = 1.0,
+                           unsigned long long *gh_max_out = nullptr,
+                           unsigned long long *gh_max_clear = nullptr);
 // The reference's best-first candidate loop (est:641-820) over the node
 // table, one wave: writes the tree arrays, its TreeNodeDev form and
 // hdr->node_count / status.

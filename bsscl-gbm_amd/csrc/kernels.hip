@@ -286,6 +286,24 @@ __device__ __forceinline__ void logistic_gh(double F, double y, double w,
   h = __dmul_rn(__dmul_rn(w, p), __dsub_rn(1.0, p));
 }
 
+// engine.hip::fixed_mul from a maximum held on the device (DevScale):
+// 2^(bits - e) with max < 2^e, or 2^bits when the maximum is not positive.
+// frexp and ldexp are exact, so the result equals the host's for the same
+// maximum.
+__device__ __forceinline__ double dev_fixed_mul(unsigned long long max_bits, int32_t bits) {
+  const double mx = __longlong_as_double((long long)max_bits);
+  if (!(mx > 0.0) || !isfinite(mx)) return ldexp(1.0, bits);
+  int e;
+  (void)frexp(mx, &e);
+  return ldexp(1.0, bits - e);
+}
+
+// The fixed point -> value scales 1 / dev_fixed_mul of both maxima.
+__device__ __forceinline__ void dev_scales(const DevScale &d, double &g_scale, double &h_scale) {
+  g_scale = 1.0 / dev_fixed_mul(d.max[0], d.bits);
+  h_scale = 1.0 / dev_fixed_mul(d.max[1], d.bits);
+}
+
 __global__ __launch_bounds__(256) void k_grad_hess(const double *__restrict__ F,
                                                    const uint8_t *__restrict__ y,
                                                    int64_t n, double w0, double w1,
@@ -486,10 +504,14 @@ __global__ __launch_bounds__(256) void k_gather_codes(
 __global__ __launch_bounds__(256) void k_gather_gh(
     const double *__restrict__ F, const uint8_t *__restrict__ y,
     const int32_t *__restrict__ rows32, int64_t m, double w0, double w1, double g_mul,
-    double h_mul, GH *__restrict__ gh_c, int64_t pad_to, NodeSeg *__restrict__ segs,
-    int32_t *__restrict__ hist_node, const LevelPlan *__restrict__ plan_src,
-    LevelPlan *__restrict__ plan_dst) {
+    double h_mul, DevScale dev, GH *__restrict__ gh_c, int64_t pad_to,
+    NodeSeg *__restrict__ segs, int32_t *__restrict__ hist_node,
+    const LevelPlan *__restrict__ plan_src, LevelPlan *__restrict__ plan_dst) {
   const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (dev.max) {
+    g_mul = dev_fixed_mul(dev.max[0], dev.bits);
+    h_mul = dev_fixed_mul(dev.max[1], dev.bits);
+  }
   if (k == 0) {
     if (plan_src) *plan_dst = *plan_src;
     NodeSeg r;
@@ -524,13 +546,13 @@ hipError_t launch_gather_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
 
 hipError_t launch_gather_gh(hipStream_t st, const double *F, const uint8_t *y,
                             const int32_t *rows32, int64_t m, double w0, double w1,
-                            double g_mul, double h_mul, GH *gh_c, int64_t pad_to,
-                            NodeSeg *segs, int32_t *hist_node, const LevelPlan *plan_src,
-                            LevelPlan *plan_dst) {
+                            double g_mul, double h_mul, DevScale dev, GH *gh_c,
+                            int64_t pad_to, NodeSeg *segs, int32_t *hist_node,
+                            const LevelPlan *plan_src, LevelPlan *plan_dst) {
   if (pad_to <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_gather_gh, dim3((unsigned)((pad_to + 255) / 256)), dim3(256), 0, st,
-                     F, y, rows32, m, w0, w1, g_mul, h_mul, gh_c, pad_to, segs, hist_node,
-                     plan_src, plan_dst);
+                     F, y, rows32, m, w0, w1, g_mul, h_mul, dev, gh_c, pad_to, segs,
+                     hist_node, plan_src, plan_dst);
   return hipGetLastError();
 }
 
@@ -1673,6 +1695,7 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_reduce_split(
     SplitCand *__restrict__ cand, long long *__restrict__ totals, int32_t span_parents) {
   __shared__ long long red[kRsWaves][kHistPerFeat];
   const int lane = lane_id(), wave = (int)(threadIdx.x >> 6);
+  if (P.dev.max) dev_scales(P.dev, P.g_scale, P.h_scale);
   // An item's records: its parent's split, smaller child and task range.
   // The first item's are loaded with the plan (its parent index is below
   // the launch's parent bound, so the reads stay in the level lists even
@@ -3232,20 +3255,59 @@ __device__ __forceinline__ double row_loss(double f, uint8_t yi) {
   return yi ? log(p) : log(1.0 - p);
 }
 
+// row_loss, and the row's gradient and hessian of the next round from the
+// same p (logistic_gh's expressions: the next round's k_gather_gh computes
+// the same values from the same F).
+__device__ __forceinline__ double row_loss_gh(double f, uint8_t yi, double w, double &g,
+                                              double &h) {
+  const double fc = fmin(fmax(f, -500.0), 500.0);
+  const double p = 1.0 / (1.0 + exp(-fc));
+  g = __dmul_rn(w, __dsub_rn(p, (double)yi));
+  h = __dmul_rn(__dmul_rn(w, p), __dsub_rn(1.0, p));
+  const double pc = fmin(fmax(p, 1e-15), 1.0 - 1e-15);
+  return yi ? log(pc) : log(1.0 - pc);
+}
+
+// Raises out[0], out[1] to the block's largest |g| and h (bit patterns of
+// non-negative doubles order as unsigned integers).  A block whose maxima
+// do not exceed what it reads issues no atomic.
+__device__ __forceinline__ void block_gh_max(double gm, double hm, unsigned long long *out) {
+  __shared__ double s_mx[kUpdBlock / 64][2];
+  for (int o = 32; o >= 1; o >>= 1) {
+    gm = fmax(gm, __shfl_xor(gm, o, 64));
+    hm = fmax(hm, __shfl_xor(hm, o, 64));
+  }
+  if (lane_id() == 0) {
+    s_mx[threadIdx.x >> 6][0] = gm;
+    s_mx[threadIdx.x >> 6][1] = hm;
+  }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    double v = 0.0;
+    for (int w = 0; w < kUpdBlock / 64; ++w) v = fmax(v, s_mx[w][threadIdx.x]);
+    const unsigned long long bits = (unsigned long long)__double_as_longlong(v);
+    unsigned long long *dst = out + threadIdx.x;
+    if (bits > __hip_atomic_load(dst, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      (void)__hip_atomic_fetch_max(dst, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 __global__ __launch_bounds__(kUpdBlock) void k_update_F(
     const uint8_t *__restrict__ codes, int64_t ld, int64_t n,
     const TreeNodeDev *__restrict__ tree, int32_t tree_len,
     const int32_t *__restrict__ node_count_d, double lr, double *__restrict__ F,
-    const uint8_t *__restrict__ y, double *__restrict__ partials) {
+    const uint8_t *__restrict__ y, double *__restrict__ partials, double w0, double w1,
+    unsigned long long *__restrict__ gh_max_out, unsigned long long *__restrict__ gh_max_clear) {
   __shared__ double red[kUpdBlock / 64];
   __shared__ TreeNodeDev st[kUpdTreeLds];
-  const bool apply = !node_count_d || *node_count_d > 0;
+  if (gh_max_clear && blockIdx.x == 0 && threadIdx.x < 2) gh_max_clear[threadIdx.x] = 0ull;
+  const bool apply = tree_len > 0 && (!node_count_d || *node_count_d > 0);
   const bool lds = tree_len <= kUpdTreeLds;
   if (apply && lds)
     for (int32_t k = (int32_t)threadIdx.x; k < tree_len; k += kUpdBlock) st[k] = tree[k];
   __syncthreads();
   const TreeNodeDev *tr = lds ? st : tree;
-  double acc = 0.0;
+  double acc = 0.0, gm = 0.0, hm = 0.0;
   const int64_t step = (int64_t)gridDim.x * kUpdBlock * kUpdRows;
   for (int64_t base = (int64_t)blockIdx.x * kUpdBlock * kUpdRows + threadIdx.x; base < n;
        base += step) {
@@ -3289,9 +3351,21 @@ __global__ __launch_bounds__(kUpdBlock) void k_update_F(
           F[i[r]] = f[r];
         }
     }
+    if (gh_max_out) {
 #pragma unroll
-    for (int r = 0; r < kUpdRows; ++r)
-      if (in[r]) acc += row_loss(f[r], y[i[r]]);
+      for (int r = 0; r < kUpdRows; ++r)
+        if (in[r]) {
+          const uint8_t yi = y[i[r]];
+          double g, h;
+          acc += row_loss_gh(f[r], yi, yi ? w1 : w0, g, h);
+          gm = fmax(gm, fabs(g));
+          hm = fmax(hm, h);
+        }
+    } else {
+#pragma unroll
+      for (int r = 0; r < kUpdRows; ++r)
+        if (in[r]) acc += row_loss(f[r], y[i[r]]);
+    }
   }
   for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
   if (lane_id() == 0) red[threadIdx.x >> 6] = acc;
@@ -3301,6 +3375,7 @@ __global__ __launch_bounds__(kUpdBlock) void k_update_F(
     for (int w = 0; w < kUpdBlock / 64; ++w) s += red[w];
     partials[blockIdx.x] = s;
   }
+  if (gh_max_out) block_gh_max(gm, hm, gh_max_out);
 }
 #pragma clang fp contract(on)
 
@@ -3308,9 +3383,12 @@ hipError_t launch_update_F(hipStream_t st, const uint8_t *codes, int64_t ld,
                            int64_t n, const TreeNodeDev *tree, int32_t tree_len,
                            const int32_t *node_count_d, double lr, double *F,
                            const uint8_t *y, double *loss_partials,
-                           int32_t n_blocks) {
+                           int32_t n_blocks, double w0, double w1,
+                           unsigned long long *gh_max_out,
+                           unsigned long long *gh_max_clear) {
   hipLaunchKernelGGL(k_update_F, dim3((unsigned)n_blocks), dim3(kUpdBlock), 0, st,
-                     codes, ld, n, tree, tree_len, node_count_d, lr, F, y, loss_partials);
+                     codes, ld, n, tree, tree_len, node_count_d, lr, F, y, loss_partials,
+                     w0, w1, gh_max_out, gh_max_clear);
   return hipGetLastError();
 }
 
@@ -3539,6 +3617,7 @@ __global__ __launch_bounds__(64) void k_replay(
     const int32_t *__restrict__ feats, ReplayArgs a, TreeArrays out,
     TreeNodeDev *__restrict__ tree, RoundHeader *__restrict__ hdr) {
   const int lane = (int)threadIdx.x;
+  if (a.dev.max) dev_scales(a.dev, a.g_scale, a.h_scale);
   const int32_t M = a.out_len;
   const int32_t C = a.max_leaves + 2;
   int32_t status = 0, needed = 0;
@@ -3746,6 +3825,7 @@ __global__ __launch_bounds__(kTreeBlock) void k_replay_tree(
   __shared__ int32_t s_expanded[kTreeBlock / 64];
   static_assert(kReplayNodes <= kTreeBlock, "one node per thread");
   const int tid = (int)threadIdx.x, wave = tid >> 6;
+  if (a.dev.max) dev_scales(a.dev, a.g_scale, a.h_scale);
   const int32_t M = a.out_len;
   const int32_t C = a.max_leaves + 2;
   int32_t status = 0, needed = 0;

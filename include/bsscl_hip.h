@@ -184,6 +184,14 @@ int bsscl_boost_get_F(bsscl_engine *eng, double *F_out);
 int bsscl_boost_grad_hess(bsscl_engine *eng, double *grad_out,
                           double *hess_out);
 
+/* The largest |g| and h over all rows of the current F (out[0], out[1]),
+ * as the device holds them for the next round's fixed-point scale (no
+ * reference counterpart: the reference sums float64 gradients, est:581-596).
+ * A round on the device path scales its tree's int64 gradients by
+ * 2^(62 - ceil(log2 m) - e) with max |g| < 2^e (hessians likewise), so any
+ * sum over its m rows fits in int64.  Waits for the engine's stream. */
+int bsscl_boost_grad_hess_max(bsscl_engine *eng, double *out);
+
 /*
  * Multiclass rounds with the scores on the device.  Replace the NumPy
  * arithmetic of the reference's multiclass loop (est:2949-3065): the (n, K)

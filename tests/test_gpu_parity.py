@@ -404,6 +404,46 @@ def test_fit_lockstep_and_end_to_end(engine, name):
             assert at255 > 0
 
 
+def test_fit_fixed_point_scale_from_device_maxima(engine, monkeypatch):
+    """A boosting round scales its tree's int64 gradients and hessians from
+    the largest |g| and h of the current F, which the previous F update (or
+    boost_begin) leaves on the device.  Those maxima equal NumPy's over the
+    device's float64 gradients of the same F, at the start and after the
+    fit.  On the confident fit, where late rounds' hessians are far below
+    the class-weight bound, the device-scaled fit follows the oracle with no
+    more certified ties than the bound-scaled one (BSSCL_TEST_BOUND_SCALE=1)."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    from bsscl_gbm import estimator as est_mod
+    _announce("fit confident_400 (160 rounds): device maxima against the bound")
+    X, y, params = _fit_case("confident_400")
+    params = dict(params, n_estimators=160)
+    eng = est_mod._engine(0)
+    n = len(y)
+    ties = {}
+    for mode in ("bound", "device"):
+        if mode == "bound":
+            monkeypatch.setenv("BSSCL_TEST_BOUND_SCALE", "1")
+        else:
+            monkeypatch.delenv("BSSCL_TEST_BOUND_SCALE", raising=False)
+        est = HybridHistGBMNumbaV1_0_1(verbose=False, **params).fit(X, y)
+        # After the fit the engine still holds the run's F and its maxima.
+        g, h = eng.boost_grad_hess(n)
+        gmax, hmax = eng.boost_grad_hess_max()
+        assert gmax == np.max(np.abs(g)) and hmax == np.max(h)
+        w0, w1 = est._class_weight_pair(y)
+        print(f"[result] confident fit after 160 rounds: max |g| {gmax:.3g}, max h {hmax:.3g} "
+              f"(bound: {max(w0, w1):.3g}, {0.25 * max(w0, w1):.3g})", flush=True)
+        ref, rep = fitcmp.follow_fit(engine, est, X, y, params, lockstep=False)
+        fitcmp.assert_fit_equal(ref, est, X)
+        ties[mode] = sum(rep.end_to_end_ties)
+        print(rep.line(f"confident_160 {mode}-scaled"), flush=True)
+    assert ties["device"] <= ties["bound"]
+    # The starting F's maxima (boost_begin), against NumPy's.
+    eng.boost_begin(y, 1.0, 3.0, 0.25)
+    g, h = eng.boost_grad_hess(n)
+    assert eng.boost_grad_hess_max() == (np.max(np.abs(g)), np.max(h))
+
+
 def test_fit_graph_rounds_match_direct_launches(engine, monkeypatch):
     """Boosting rounds replayed from captured HIP graphs give the trees and
     losses of rounds whose kernels are launched one by one: the rows
