@@ -550,10 +550,11 @@ class HybridHistGBMNumbaV1_0_1:
             self.bin_edges, self.feature_bin_counts = self._build_bin_edges(
                 X, sample_weight=sample_weight, eng=eng if staged else None)
             self._max_bins = int(np.max(self.feature_bin_counts))
-            if self._max_bins > 257:
-                raise NotImplementedError(
+            if self._max_bins > 65536:
+                # The reference's codes are uint16 above 255 bins (est:2163-2166).
+                raise ValueError(
                     f"n_bins={self.n_bins} gives {self._max_bins} bins for some feature; "
-                    "the MI355X engine holds at most 257 bins per feature (n_bins <= 256)")
+                    "codes are uint16, so at most 65536 bins per feature")
             if staged:
                 eng.bin_staged(0, X.shape[0], X.shape[1], X.dtype == np.float64, self.bin_edges,
                                self.feature_bin_counts, self._nan_bin_id)

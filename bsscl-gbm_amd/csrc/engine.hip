@@ -139,12 +139,13 @@ struct Matrix {
   DevBuf<uint8_t> codes;
   int64_t n = 0, ld = 0;
   int32_t F = 0;
-  // Top columns: column F + j holds (code >= 256) of feature j, and column j
-  // min(code, 255).  Present when some feature has 257 bins (n_bins = 256,
-  // est:1963-1964), whose codes the reference keeps as uint16
+  // Code tiers (kernels.h): column t * F + j holds clamp(code - 255 t, 0,
+  // 255) of feature j.  More than one when some feature has more than 256
+  // bins (n_bins = 256 with 257 bins is the reference's 'auto' value from 28
+  // features on, est:1963-1964), whose codes the reference keeps as uint16
   // (est:2163-2166, 2179-2182).
-  int32_t top = 0;
-  int32_t cols() const { return top ? 2 * F : F; }
+  int32_t tiers = 1;
+  int32_t cols() const { return tiers * F; }
 };
 
 struct HNode {
@@ -592,56 +593,59 @@ int check_matrix(bsscl_engine *E, int32_t slot) {
   return BSSCL_OK;
 }
 
-int alloc_matrix(bsscl_engine *E, int32_t slot, int64_t n, int32_t F, int32_t top = 0) {
+int alloc_matrix(bsscl_engine *E, int32_t slot, int64_t n, int32_t F, int32_t tiers = 1) {
   Matrix &M = E->mat[slot];
   const int64_t ld = round_up(n + 8, 256);
-  const size_t bytes = (size_t)ld * (size_t)F * (top ? 2 : 1);
+  const size_t bytes = (size_t)ld * (size_t)F * (size_t)tiers;
   CHK(M.codes.ensure(bytes));
   HIPCHK(hipMemsetAsync(M.codes.p, 0, bytes, E->st));
   M.n = n;
   M.ld = ld;
   M.F = F;
-  M.top = top;
+  M.tiers = tiers;
   return BSSCL_OK;
 }
 
-// Gives matrix `slot` (all codes <= 255) zero top columns.
-int ensure_top_columns(bsscl_engine *E, int32_t slot) {
+// Gives matrix `slot` at least `tiers` code tiers.  Its codes are held
+// exactly by the tiers it has (codes <= 255 * M.tiers), so the added tiers
+// are zero.
+int ensure_tiers(bsscl_engine *E, int32_t slot, int32_t tiers) {
   Matrix &M = E->mat[slot];
-  if (M.top) return BSSCL_OK;
-  const size_t half = (size_t)M.ld * (size_t)M.F;
+  if (M.tiers >= tiers) return BSSCL_OK;
+  const size_t have = (size_t)M.ld * (size_t)M.F * (size_t)M.tiers;
+  const size_t want = (size_t)M.ld * (size_t)M.F * (size_t)tiers;
   DevBuf<uint8_t> wide;
-  CHK(wide.ensure(2 * half));
-  HIPCHK(hipMemcpyAsync(wide.p, M.codes.p, half, hipMemcpyDeviceToDevice, E->st));
-  HIPCHK(hipMemsetAsync(wide.p + half, 0, half, E->st));
+  CHK(wide.ensure(want));
+  HIPCHK(hipMemcpyAsync(wide.p, M.codes.p, have, hipMemcpyDeviceToDevice, E->st));
+  HIPCHK(hipMemsetAsync(wide.p + have, 0, want - have, E->st));
   HIPCHK(hipStreamSynchronize(E->st));
   std::swap(M.codes, wide);
   wide.release();
-  M.top = 1;
+  M.tiers = tiers;
   return BSSCL_OK;
 }
 
 // Engine columns of a tree's selected features (ascending feature ids, each
-// with bin count nb in [1, 257]): the feature's code column and, right after
-// it for a 257-bin feature, its top column F + j with 2 bins.  The
-// reference's candidate (j, 255) -- codes <= 255 go left -- is the top
-// column's candidate (F + j, 0); it follows (j, 0..254) exactly as bin 255
-// follows bins 0..254 in est:611-621, so the argmax and its strict-'>'
-// tie-breaks pick the same split.
+// with bin count nb in [1, kMaxBinCount]): the feature's tier-0 column and,
+// right after it for a feature of more than 256 bins, its tiers 1 .. k - 1
+// (k = tiers_for_bins(nb)), tier t with min(256, nb - 255 t) bins.  The
+// reference's candidates (j, 255 t + b) are tier t's candidates (t F + j, b),
+// listed in the reference's order (est:611-621), so the argmax and its
+// strict-'>' tie-breaks pick the same split.
 int expand_features(const Matrix &X, const std::vector<int32_t> &feats,
                     const std::vector<int32_t> &nb, std::vector<int32_t> &cols,
                     std::vector<int32_t> &nb_cols) {
   cols.clear();
   nb_cols.clear();
   for (size_t i = 0; i < feats.size(); ++i) {
-    cols.push_back(feats[i]);
-    nb_cols.push_back(std::min(nb[i], kBins));
-    if (nb[i] > kBins) {
-      if (!X.top)
-        return set_error(BSSCL_EINVAL, "feature " + std::to_string(feats[i]) +
-                                           " has 257 bins but the matrix has no codes above 255");
-      cols.push_back(X.F + feats[i]);
-      nb_cols.push_back(2);
+    const int32_t k = tiers_for_bins(nb[i]);
+    if (k > X.tiers)
+      return set_error(BSSCL_EINVAL, "feature " + std::to_string(feats[i]) + " has " +
+                                         std::to_string(nb[i]) +
+                                         " bins but the matrix holds smaller codes");
+    for (int32_t t = 0; t < k; ++t) {
+      cols.push_back(t * X.F + feats[i]);
+      nb_cols.push_back(std::min(kBins, nb[i] - 255 * t));
     }
   }
   return BSSCL_OK;
@@ -1571,10 +1575,10 @@ int validate_tree_args(bsscl_engine *E, const int32_t *feature_indices,
     if (i > 0 && f <= feats[(size_t)i - 1])
       return set_error(BSSCL_EINVAL, "feature_indices must be strictly ascending");
     const int32_t nb = bin_counts[f];
-    if (nb < 1 || nb > kBins + 1)
-      return set_error(BSSCL_EINVAL, "bin_counts must be in [1, 257]");
+    if (nb < 1 || nb > kMaxBinCount)
+      return set_error(BSSCL_EINVAL, "bin_counts must be in [1, 65536]");
     nb_sel[(size_t)i] = nb;
-    if (nb > kBins) CHK(ensure_top_columns(E, 0));
+    CHK(ensure_tiers(E, 0, tiers_for_bins(nb)));
   }
   std::vector<int32_t> cols, nb_cols;
   CHK(expand_features(X, feats, nb_sel, cols, nb_cols));
@@ -1583,23 +1587,27 @@ int validate_tree_args(bsscl_engine *E, const int32_t *feature_indices,
   return BSSCL_OK;
 }
 
-// Tree arrays from engine columns to the reference's features: a split on a
-// top column (F + j, 0) is the split (j, 255).
+// Tree arrays from engine columns to the reference's features: a split on
+// tier t, (t F + j, b), is the split (j, 255 t + b).
 void tree_to_reference(const Matrix &X, const TreeOut &out) {
   const int32_t n = *out.node_count;
   for (int32_t i = 0; i < n; ++i) {
     if (out.features[i] >= X.F) {
-      out.features[i] -= X.F;
-      out.thresholds[i] += 255;
+      const int32_t t = out.features[i] / X.F;
+      out.features[i] -= t * X.F;
+      out.thresholds[i] += 255 * (int64_t)t;
     }
   }
 }
 
-// A reference split (j, t) as the engine traverses it on matrix X.
+// A reference split (j, c) as the engine traverses it on matrix X: tier
+// t = c / 255 at b = c - 255 t (a threshold above the last tier's range
+// sends every row left, as b = 255 does).
 inline void split_to_engine(const Matrix &X, int32_t &feature, int64_t &threshold) {
-  if (X.top && feature >= 0 && threshold >= 255) {
-    feature += X.F;
-    threshold -= 255;
+  if (X.tiers > 1 && feature >= 0 && threshold >= 255) {
+    const int32_t t = (int32_t)std::min<int64_t>(threshold / 255, X.tiers - 1);
+    feature += t * X.F;
+    threshold = std::min<int64_t>(threshold - 255 * (int64_t)t, 255);
   }
 }
 
@@ -1865,11 +1873,11 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     for (int32_t i = 0; rc == BSSCL_OK && i < f_sub; ++i) {
       const int32_t f = feats[(size_t)i];
       if (f < 0 || f >= X.F) rc = set_error(BSSCL_EINVAL, "feature index out of range");
-      else if (a.bin_counts[f] < 1 || a.bin_counts[f] > kBins + 1)
-        rc = set_error(BSSCL_EINVAL, "bin_counts must be in [1, 257]");
+      else if (a.bin_counts[f] < 1 || a.bin_counts[f] > kMaxBinCount)
+        rc = set_error(BSSCL_EINVAL, "bin_counts must be in [1, 65536]");
       else nb[(size_t)i] = a.bin_counts[f];
     }
-    // Engine columns: a 257-bin feature adds its top column.
+    // Engine columns: a feature of more than 256 bins adds its code tiers.
     if (rc == BSSCL_OK) rc = expand_features(X, feats, nb, R.feats, R.nb_sel);
   }
   const TreeParams tp{a.max_leaves, a.max_depth, a.min_samples_leaf, a.min_child_weight,
@@ -2435,17 +2443,18 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
   if (staged && (!E->xstage.p || E->xs_n != n || E->xs_F != F || E->xs_f64 != (x_is_f64 ? 1 : 0)))
     return set_error(BSSCL_EINVAL,
                      "bin_features: X is NULL but no staged matrix of this shape and dtype");
-  int32_t has_any_nan = 0, top = 0;
+  int32_t has_any_nan = 0, tiers = 1;
   for (int32_t j = 0; j < F; ++j) {
     if (bin_counts[j] < 1 || bin_counts[j] >= edge_stride)
       return set_error(BSSCL_EINVAL, "bin_features: bin_counts must be in [1, edge_stride)");
-    if (bin_counts[j] > kBins + 1)
-      return set_error(BSSCL_EINVAL, "bin_features: more than 257 bins (n_bins > 256)");
-    if (bin_counts[j] > kBins) top = 1;
+    if (bin_counts[j] > kMaxBinCount)
+      return set_error(BSSCL_EINVAL, "bin_features: more than 65536 bins");
+    // Training codes are at most nb - 1, which these tiers hold exactly.
+    tiers = std::max(tiers, tiers_for_bins(bin_counts[j]));
     if (nan_bin_id[j] >= 0) has_any_nan = 1;
   }
   HIPCHK(hipSetDevice(E->device));
-  CHK(alloc_matrix(E, slot, n, F, top));
+  CHK(alloc_matrix(E, slot, n, F, tiers));
   DevBuf<double> ed;
   DevBuf<int32_t> nb, nid;
   CHK(ed.ensure((size_t)F * edge_stride));
@@ -2458,7 +2467,7 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
   const size_t esz = x_is_f64 ? 8 : 4;
   if (staged) {
     hipError_t e = launch_bin(E->st, E->xstage.p, x_is_f64, n, F, ed.p, edge_stride, nb.p,
-                              nid.p, has_any_nan, M.codes.p, M.ld, top);
+                              nid.p, has_any_nan, M.codes.p, M.ld, tiers);
     if (e == hipSuccess) e = hipStreamSynchronize(E->st);
     ed.release(); nb.release(); nid.release();
     if (e != hipSuccess)
@@ -2476,7 +2485,7 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
                                     (size_t)rows * F * esz, hipMemcpyHostToDevice, E->st);
       if (e == hipSuccess)
         e = launch_bin(E->st, xd.p, x_is_f64, rows, F, ed.p, edge_stride, nb.p, nid.p,
-                       has_any_nan, M.codes.p + r0, M.ld, top);
+                       has_any_nan, M.codes.p + r0, M.ld, tiers);
       if (e == hipSuccess) e = hipStreamSynchronize(E->st);
       if (e != hipSuccess) {
         xd.release(); ed.release(); nb.release(); nid.release();
@@ -2645,19 +2654,21 @@ int bsscl_load_codes(bsscl_engine *E, int32_t slot, const void *codes,
   if (slot < 0 || slot > 1) return set_error(BSSCL_EINVAL, "matrix slot must be 0 or 1");
   if (n <= 0 || n > INT32_MAX || F <= 0) return set_error(BSSCL_EINVAL, "load_codes: bad shape");
   HIPCHK(hipSetDevice(E->device));
-  int32_t top = 0;
+  int32_t tiers = 1;
   if (codes_u16) {
     const uint16_t *c16 = static_cast<const uint16_t *>(codes);
-    for (int64_t k = 0; k < n * F && !top; ++k) top = c16[k] > 255;
+    uint16_t cmax = 0;
+    for (int64_t k = 0; k < n * F; ++k) cmax = std::max(cmax, c16[k]);
+    tiers = tiers_for_code(cmax);
   }
-  CHK(alloc_matrix(E, slot, n, F, top));
+  CHK(alloc_matrix(E, slot, n, F, tiers));
   const size_t bytes = (size_t)n * F * (codes_u16 ? 2 : 1);
   DevBuf<unsigned char> tmp;
   CHK(tmp.ensure(bytes));
   hipError_t e = hipMemcpyAsync(tmp.p, codes, bytes, hipMemcpyHostToDevice, E->st);
   if (e == hipSuccess)
     e = launch_load_codes(E->st, tmp.p, codes_u16, n, F, E->mat[slot].codes.p, E->mat[slot].ld,
-                          top);
+                          tiers);
   if (e == hipSuccess) e = hipStreamSynchronize(E->st);
   tmp.release();
   if (e != hipSuccess) return set_error(BSSCL_EDEVICE, std::string("load_codes: ") + hipGetErrorString(e));
@@ -2674,7 +2685,7 @@ int get_codes(bsscl_engine *E, int32_t slot, void *codes_out, int as_u16) {
   const size_t bytes = (size_t)M.n * M.F * (as_u16 ? 2 : 1);
   DevBuf<uint8_t> tmp;
   CHK(tmp.ensure(bytes));
-  hipError_t e = launch_get_codes(E->st, M.codes.p, M.ld, M.n, M.F, M.top, tmp.p, as_u16);
+  hipError_t e = launch_get_codes(E->st, M.codes.p, M.ld, M.n, M.F, M.tiers, tmp.p, as_u16);
   if (e == hipSuccess) e = hipMemcpyAsync(codes_out, tmp.p, bytes, hipMemcpyDeviceToHost, E->st);
   if (e == hipSuccess) e = hipStreamSynchronize(E->st);
   tmp.release();
@@ -3162,7 +3173,7 @@ int bsscl_predict_noalloc(bsscl_engine *E, int32_t slot, const int16_t *features
                              reinterpret_cast<const double *>(S + kScrVal),
                              reinterpret_cast<const int32_t *>(S + kScrLeft),
                              reinterpret_cast<const int32_t *>(S + kScrRight), total,
-                             M.top ? M.F : 0, nodes));
+                             M.F, M.tiers, nodes));
   }
   // The LDS-staged kernel's runs of whole trees (host list on the stack; the
   // copy has finished when the call returns).

@@ -10,6 +10,20 @@ namespace bsscl {
 constexpr int kBins = 256;          // histogram bins per feature (uint8 codes)
 constexpr int kHistPerFeat = 512;   // int64 words per feature: [bin][g,h]
 
+// Codes above 255 (the reference keeps uint16 codes when a feature has more
+// than 255 bins, est:2163-2166) are held in tiers of uint8 columns: column
+// t * F + j of feature j holds clamp(code - 255 t, 0, 255), so tier 0 is
+// min(code, 255).  The reference's split "code <= 255 t + b" (0 <= b <= 254)
+// is "tier t <= b", tier t's cumulative histogram up to bin b is the
+// feature's up to 255 t + b, and the tiers of a row add up to its code (up to
+// 255 T for T tiers).
+constexpr int32_t kMaxBinCount = 65536;  // uint16 codes
+constexpr int32_t kMaxTiers = 257;       // tiers_for_bins(kMaxBinCount)
+// Tiers a feature of nb bins splits on (thresholds 0 .. nb - 2).
+inline int32_t tiers_for_bins(int32_t nb) { return nb <= kBins ? 1 : (nb - 2) / 255 + 1; }
+// Tiers that hold code c exactly.
+inline int32_t tiers_for_code(int32_t c) { return c <= 255 ? 1 : (c + 254) / 255; }
+
 // Fixed-point gradient and hessian of one row: (g * 2^sg, h * 2^sh) as
 // int64, with the exponents chosen so that a sum over all rows of a tree
 // fits in int64.
@@ -230,11 +244,11 @@ constexpr int kReplaySlots = 1024;  // candidate slots the device replay holds
 hipError_t launch_bin(hipStream_t st, const void *X, int is_f64, int64_t n,
                       int32_t F, const double *edges, int32_t stride,
                       const int32_t *nb, const int32_t *nan_id,
-                      int32_t has_any_nan, uint8_t *codes, int64_t ld, int32_t top);
+                      int32_t has_any_nan, uint8_t *codes, int64_t ld, int32_t tiers);
 hipError_t launch_load_codes(hipStream_t st, const void *src, int is_u16,
-                             int64_t n, int32_t F, uint8_t *codes, int64_t ld, int32_t top);
+                             int64_t n, int32_t F, uint8_t *codes, int64_t ld, int32_t tiers);
 hipError_t launch_get_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
-                            int64_t n, int32_t F, int32_t top, void *dst, int as_u16);
+                            int64_t n, int32_t F, int32_t tiers, void *dst, int as_u16);
 hipError_t launch_quantize(hipStream_t st, const double *g, const double *h,
                            int64_t n, double g_mul, double h_mul, GH *ghq);
 hipError_t launch_grad_hess(hipStream_t st, const double *F, const uint8_t *y,
@@ -433,7 +447,7 @@ hipError_t launch_predict_tree(hipStream_t st, const uint8_t *codes,
                                int32_t node_count, double *out);
 hipError_t launch_pack_trees(hipStream_t st, const int16_t *features, const int64_t *thresholds,
                              const double *values, const int32_t *left, const int32_t *right,
-                             int32_t total, int32_t top_F, TreeNodeDev *nodes);
+                             int32_t total, int32_t F, int32_t tiers, TreeNodeDev *nodes);
 // Ensemble prediction.  With `chunks` (predict_chunks' list of n_chunks
 // runs of whole trees; only when predict_staged_ok) the rows' codes and the
 // trees are staged in LDS; otherwise each row walks the trees in HBM.

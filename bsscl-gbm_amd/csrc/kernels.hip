@@ -63,8 +63,7 @@ constexpr int kBinRows = 64;
 
 // Code of one value: the largest k in [0, nb-1] with e[k] <= v, 0 below
 // e[0], nb-1 at or above e[nb] (est:204-226); NaN handling of est:2159-2177.
-// The matrix stores min(code, 255) in the feature's column and, when it has
-// top columns (some feature has 257 bins), code >= 256 in column F + f.
+// The matrix stores the code's tiers (tier_code) in columns t * F + f.
 __device__ __forceinline__ int32_t bin_one(double v, const double *__restrict__ e,
                                            int32_t nbf, bool nan_feat,
                                            int32_t has_any_nan) {
@@ -90,19 +89,24 @@ __device__ __forceinline__ int32_t bin_one(double v, const double *__restrict__ 
   return c;
 }
 
+// Tier t of a code (t = 0: min(code, 255); kernels.h).
+__device__ __forceinline__ uint8_t tier_code(int32_t code, int32_t t) {
+  return (uint8_t)min(max(code - 255 * t, 0), 255);
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_bin(
     const T *__restrict__ X, int64_t n, int32_t F,
     const double *__restrict__ edges, int32_t stride,
     const int32_t *__restrict__ nb, const int32_t *__restrict__ nan_id,
-    int32_t has_any_nan, uint8_t *__restrict__ codes, int64_t ld, int32_t top) {
+    int32_t has_any_nan, uint8_t *__restrict__ codes, int64_t ld, int32_t tiers) {
   extern __shared__ unsigned char smem[];
   T *xs = reinterpret_cast<T *>(smem);                        // [64][F]
-  uint8_t *cs = smem + sizeof(T) * (size_t)kBinRows * F;     // [F (+F top)][64]
+  uint8_t *cs = smem + sizeof(T) * (size_t)kBinRows * F;     // [tiers * F][64]
   const int64_t r0 = (int64_t)blockIdx.x * kBinRows;
   const int rows = (int)min<int64_t>(kBinRows, n - r0);
   const int tot = rows * F;
-  const int cols = top ? 2 * F : F;
+  const int cols = tiers * F;
   for (int i = threadIdx.x; i < tot; i += blockDim.x)
     xs[i] = X[r0 * F + i];
   __syncthreads();
@@ -112,8 +116,7 @@ __global__ __launch_bounds__(256) void k_bin(
     if (r < rows)
       code = bin_one((double)xs[r * F + f], edges + (int64_t)f * stride, nb[f],
                      nan_id[f] >= 0, has_any_nan);
-    cs[f * kBinRows + r] = (uint8_t)min(code, 255);
-    if (top) cs[(F + f) * kBinRows + r] = code >= 256 ? 1 : 0;
+    for (int32_t t = 0; t < tiers; ++t) cs[(t * F + f) * kBinRows + r] = tier_code(code, t);
   }
   __syncthreads();
   // 16 dwords per column.
@@ -130,44 +133,43 @@ __global__ __launch_bounds__(256) void k_bin_wide(
     const T *__restrict__ X, int64_t n, int32_t F,
     const double *__restrict__ edges, int32_t stride,
     const int32_t *__restrict__ nb, const int32_t *__restrict__ nan_id,
-    int32_t has_any_nan, uint8_t *__restrict__ codes, int64_t ld, int32_t top) {
+    int32_t has_any_nan, uint8_t *__restrict__ codes, int64_t ld, int32_t tiers) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int32_t f = (int32_t)blockIdx.y;
   if (i >= n) return;
   const int32_t code = bin_one((double)X[i * F + f], edges + (int64_t)f * stride, nb[f],
                                nan_id[f] >= 0, has_any_nan);
-  codes[(int64_t)f * ld + i] = (uint8_t)min(code, 255);
-  if (top) codes[(int64_t)(F + f) * ld + i] = code >= 256 ? 1 : 0;
+  for (int32_t t = 0; t < tiers; ++t) codes[(int64_t)(t * F + f) * ld + i] = tier_code(code, t);
 }
 
 hipError_t launch_bin(hipStream_t st, const void *X, int is_f64, int64_t n,
                       int32_t F, const double *edges, int32_t stride,
                       const int32_t *nb, const int32_t *nan_id,
-                      int32_t has_any_nan, uint8_t *codes, int64_t ld, int32_t top) {
+                      int32_t has_any_nan, uint8_t *codes, int64_t ld, int32_t tiers) {
   if (n <= 0) return hipSuccess;
   const size_t lds = (is_f64 ? 8 : 4) * (size_t)kBinRows * F +
-                     (size_t)kBinRows * F * (top ? 2 : 1);
+                     (size_t)kBinRows * F * (size_t)tiers;
   if (lds > 48 * 1024) {
     const dim3 grid((unsigned)((n + 255) / 256), (unsigned)F);
     if (is_f64)
       hipLaunchKernelGGL(k_bin_wide<double>, grid, dim3(256), 0, st,
                          (const double *)X, n, F, edges, stride, nb, nan_id,
-                         has_any_nan, codes, ld, top);
+                         has_any_nan, codes, ld, tiers);
     else
       hipLaunchKernelGGL(k_bin_wide<float>, grid, dim3(256), 0, st,
                          (const float *)X, n, F, edges, stride, nb, nan_id,
-                         has_any_nan, codes, ld, top);
+                         has_any_nan, codes, ld, tiers);
     return hipGetLastError();
   }
   const unsigned blocks = (unsigned)((n + kBinRows - 1) / kBinRows);
   if (is_f64)
     hipLaunchKernelGGL(k_bin<double>, dim3(blocks), dim3(256), lds, st,
                        (const double *)X, n, F, edges, stride, nb, nan_id,
-                       has_any_nan, codes, ld, top);
+                       has_any_nan, codes, ld, tiers);
   else
     hipLaunchKernelGGL(k_bin<float>, dim3(blocks), dim3(256), lds, st,
                        (const float *)X, n, F, edges, stride, nb, nan_id,
-                       has_any_nan, codes, ld, top);
+                       has_any_nan, codes, ld, tiers);
   return hipGetLastError();
 }
 
@@ -198,59 +200,57 @@ hipError_t launch_code_counts(hipStream_t st, const uint8_t *codes, int64_t ld,
   return hipGetLastError();
 }
 
-// Row-major uint8/uint16 codes -> feature-major uint8: min(code, 255), and
-// code >= 256 in the top column F + f when the matrix has top columns.
+// Row-major uint8/uint16 codes -> feature-major tiers (tier_code).
 template <typename T>
 __global__ __launch_bounds__(256) void k_load_codes(const T *__restrict__ src,
                                                     int64_t n, int32_t F,
                                                     uint8_t *__restrict__ codes,
-                                                    int64_t ld, int32_t top) {
+                                                    int64_t ld, int32_t tiers) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   for (int32_t f = 0; f < F; ++f) {
-    uint32_t v = (uint32_t)src[i * F + f];
-    codes[(int64_t)f * ld + i] = (uint8_t)min(v, 255u);
-    if (top) codes[(int64_t)(F + f) * ld + i] = v >= 256u ? 1 : 0;
+    const int32_t v = (int32_t)src[i * F + f];
+    for (int32_t t = 0; t < tiers; ++t) codes[(int64_t)(t * F + f) * ld + i] = tier_code(v, t);
   }
 }
 
 hipError_t launch_load_codes(hipStream_t st, const void *src, int is_u16,
-                             int64_t n, int32_t F, uint8_t *codes, int64_t ld, int32_t top) {
+                             int64_t n, int32_t F, uint8_t *codes, int64_t ld, int32_t tiers) {
   if (n <= 0) return hipSuccess;
   const unsigned blocks = (unsigned)((n + 255) / 256);
   if (is_u16)
     hipLaunchKernelGGL(k_load_codes<uint16_t>, dim3(blocks), dim3(256), 0, st,
-                       (const uint16_t *)src, n, F, codes, ld, top);
+                       (const uint16_t *)src, n, F, codes, ld, tiers);
   else
     hipLaunchKernelGGL(k_load_codes<uint8_t>, dim3(blocks), dim3(256), 0, st,
-                       (const uint8_t *)src, n, F, codes, ld, top);
+                       (const uint8_t *)src, n, F, codes, ld, tiers);
   return hipGetLastError();
 }
 
-// Feature-major matrix -> row-major codes: uint8 min(code, 255), or uint16
-// min(code, 255) + top flag (256 for every code >= 256).
+// Feature-major matrix -> row-major codes: uint8 min(code, 255) (tier 0), or
+// uint16 the sum of the tiers (the code, up to 255 * tiers).
 template <typename T>
 __global__ __launch_bounds__(256) void k_get_codes(const uint8_t *__restrict__ codes,
                                                    int64_t ld, int64_t n, int32_t F,
-                                                   int32_t top, T *__restrict__ dst) {
+                                                   int32_t tiers, T *__restrict__ dst) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   for (int32_t f = 0; f < F; ++f) {
-    uint32_t v = codes[(int64_t)f * ld + i];
-    if (top) v += codes[(int64_t)(F + f) * ld + i];
+    uint32_t v = 0;
+    for (int32_t t = 0; t < tiers; ++t) v += codes[(int64_t)(t * F + f) * ld + i];
     dst[i * F + f] = (T)v;
   }
 }
 
 hipError_t launch_get_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
-                            int64_t n, int32_t F, int32_t top, void *dst, int as_u16) {
+                            int64_t n, int32_t F, int32_t tiers, void *dst, int as_u16) {
   if (n <= 0) return hipSuccess;
   const dim3 grid((unsigned)((n + 255) / 256));
   if (as_u16)
-    hipLaunchKernelGGL(k_get_codes<uint16_t>, grid, dim3(256), 0, st, codes, ld, n, F, top,
+    hipLaunchKernelGGL(k_get_codes<uint16_t>, grid, dim3(256), 0, st, codes, ld, n, F, tiers,
                        (uint16_t *)dst);
   else
-    hipLaunchKernelGGL(k_get_codes<uint8_t>, grid, dim3(256), 0, st, codes, ld, n, F, 0,
+    hipLaunchKernelGGL(k_get_codes<uint8_t>, grid, dim3(256), 0, st, codes, ld, n, F, 1,
                        (uint8_t *)dst);
   return hipGetLastError();
 }
@@ -4118,7 +4118,7 @@ __global__ __launch_bounds__(256) void k_predict(
 __global__ __launch_bounds__(256) void k_pack_trees(
     const int16_t *__restrict__ features, const int64_t *__restrict__ thresholds,
     const double *__restrict__ values, const int32_t *__restrict__ left,
-    const int32_t *__restrict__ right, int32_t total, int32_t top_F,
+    const int32_t *__restrict__ right, int32_t total, int32_t F, int32_t tiers,
     TreeNodeDev *__restrict__ nodes) {
   const int32_t i = (int32_t)(blockIdx.x * blockDim.x + threadIdx.x);
   if (i >= total) return;
@@ -4128,11 +4128,12 @@ __global__ __launch_bounds__(256) void k_pack_trees(
   if (d.feature >= 0) {
     const int64_t t = thresholds[i];
     d.threshold = (int32_t)(t < -1 ? -1 : (t > (1 << 20) ? (1 << 20) : t));
-    if (top_F > 0 && d.threshold >= 255) {
-      // code <= 255 is "top flag <= 0" (est's split at bin 255 of a 257-bin
-      // feature).
-      d.feature += top_F;
-      d.threshold -= 255;
+    if (tiers > 1 && d.threshold >= 255) {
+      // "code <= 255 k + b" is "tier k <= b" (kernels.h); a threshold above
+      // the last tier's range sends every row left, as b = 255 does.
+      const int32_t k = min(d.threshold / 255, tiers - 1);
+      d.feature += k * F;
+      d.threshold = min(d.threshold - 255 * k, 255);
     }
     d.left = left[i];
     d.right = right[i];
@@ -4147,10 +4148,10 @@ __global__ __launch_bounds__(256) void k_pack_trees(
 
 hipError_t launch_pack_trees(hipStream_t st, const int16_t *features, const int64_t *thresholds,
                              const double *values, const int32_t *left, const int32_t *right,
-                             int32_t total, int32_t top_F, TreeNodeDev *nodes) {
+                             int32_t total, int32_t F, int32_t tiers, TreeNodeDev *nodes) {
   if (total <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_pack_trees, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
-                     features, thresholds, values, left, right, total, top_F, nodes);
+                     features, thresholds, values, left, right, total, F, tiers, nodes);
   return hipGetLastError();
 }
 

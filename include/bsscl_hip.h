@@ -53,16 +53,16 @@ void bsscl_engine_destroy(bsscl_engine *eng);
  *   bin_counts int32[F], nan_bin_id int32[F]
  * X may be NULL to bin the matrix staged by bsscl_stage_features (below).
  * The codes stay on the device as matrix `slot` (0 = training, 1 = scoring),
- * stored feature-major as uint8 min(code, 255).  Bin counts go up to 257
- * (n_bins = 256, the reference's 'auto' value for p >= 28, est:1963-1964,
- * whose codes it keeps as uint16, est:2163-2166); when any feature has 257
- * bins the matrix also holds, per feature, whether its code is >= 256, and
- * every split and prediction sees the reference's codes.  Otherwise a code
- * above 255 (a scoring value above the training range of a 256-bin NaN
- * feature) is stored as 255, which every threshold (<= 254) treats
- * identically.  When codes_out is not NULL the codes are also copied back
- * row-major (n x F uint8, min(code, 255)).  More than 257 bins (n_bins > 256)
- * fail with BSSCL_EINVAL.
+ * stored feature-major as uint8 tiers: T tiers when the largest bin count nb
+ * needs them (T = 1 up to 256 bins, else (nb - 2) / 255 + 1), tier t of a
+ * code holding clamp(code - 255 t, 0, 255).  Bin counts go up to 65536: the
+ * reference keeps codes as uint16 above 255 bins (est:2163-2166), and
+ * n_bins = 256, its 'auto' value for p >= 28 (est:1963-1964), already gives
+ * 257.  Every split and prediction sees the reference's codes; a code above
+ * 255 T (a scoring value above the training range of a NaN feature) is held
+ * as 255 T, which every threshold (<= nb - 2) treats identically.  When
+ * codes_out is not NULL the codes are also copied back row-major (n x F
+ * uint8, min(code, 255)).  More than 65536 bins fail with BSSCL_EINVAL.
  */
 int bsscl_bin_features(bsscl_engine *eng, int32_t slot, const void *X,
                        int32_t x_is_f64, int64_t n, int32_t F,
@@ -77,9 +77,8 @@ int bsscl_load_codes(bsscl_engine *eng, int32_t slot, const void *codes,
 
 /* Copy matrix `slot` back row-major: n x F uint8 min(code, 255), or (_u16)
  * n x F uint16 codes as the reference stores them when _max_bins > 255
- * (est:2163-2166).  A code above every bin of its feature (a scoring value
- * above a NaN feature's training range) reads back as 256 when the matrix
- * holds 257-bin features and as 255 otherwise. */
+ * (est:2163-2166).  A code above 255 T (T tiers, bsscl_bin_features) reads
+ * back as 255 T. */
 int bsscl_get_codes(bsscl_engine *eng, int32_t slot, uint8_t *codes_out);
 int bsscl_get_codes_u16(bsscl_engine *eng, int32_t slot, uint16_t *codes_out);
 

@@ -29,7 +29,15 @@ def _binned(X, n_bins, strategy="standard"):
     return e, bc, nid, codes
 
 
-@pytest.mark.parametrize("case", ["plain", "nan", "f64", "wide", "special", "nbins256"])
+def _tier_cap(bc):
+    """Largest code a matrix binned with bin counts bc reads back exactly:
+    255 per code tier, one tier per 255 thresholds past the first 255."""
+    nb = int(np.max(bc))
+    return 255 * (1 if nb <= 256 else (nb - 2) // 255 + 1)
+
+
+@pytest.mark.parametrize("case", ["plain", "nan", "f64", "wide", "special", "nbins256",
+                                  "nbins300", "nbins1000"])
 def test_binning_bit_exact(engine, case):
     _announce(f"binning {case}")
     rng = np.random.default_rng(11)
@@ -49,14 +57,21 @@ def test_binning_bit_exact(engine, case):
         X[:, 2] = 3.0
         X[:4, 3] = [np.inf, -np.inf, 1e38, -1e38]
         X[:, 4] = rng.exponential(1.0, 4000) * (rng.random(4000) < 0.1)
-    else:
+    elif case == "nbins256":
         X, _ = make_data(6000, 4, seed=6, nan_frac=0.1, nan_cols=[1])
         X[:, 2] = np.round(X[:, 2] * 40)
         n_bins = 256
+    else:
+        # More than 256 bins: codes in two and in four 8-bit tiers.
+        X, _ = make_data(12000, 5, seed=7, nan_frac=0.1, nan_cols=[0, 3])
+        X[:, 2] = np.round(X[:, 2] * 40)
+        n_bins = 300 if case == "nbins300" else 1000
     e, bc, nid, want = _binned(X, n_bins)
     if case == "nbins256":
         # n_bins = 256: continuous columns get 257 bins and uint16 codes.
         assert bc.max() == 257 and want.dtype == np.uint16 and want.max() == 256
+    if case in ("nbins300", "nbins1000"):
+        assert want.dtype == np.uint16 and want.max() == n_bins
     got = engine.bin_features(0, X, e, bc, nid, return_codes=True)
     np.testing.assert_array_equal(got, np.minimum(want.astype(np.int64), 255).astype(np.uint8))
     if want.dtype == np.uint16:
@@ -71,11 +86,10 @@ def test_binning_bit_exact(engine, case):
     np.testing.assert_array_equal(got_p, np.minimum(want_p.astype(np.int64), 255).astype(np.uint8))
     if want_p.dtype == np.uint16:
         # A code above every bin of its feature (a value above the training
-        # range of a NaN feature) reads back as 256 when the matrix holds
-        # 257-bin features and as 255 otherwise; no split tells them apart.
-        cap = 256 if bc.max() > 256 else 255
+        # range of a NaN feature) reads back capped at the tiers' range; no
+        # split tells the two apart.
         np.testing.assert_array_equal(engine.get_codes(1, *Xp.shape, u16=True),
-                                      np.minimum(want_p, cap))
+                                      np.minimum(want_p, _tier_cap(bc)))
 
 
 @pytest.mark.parametrize("m,bin_", [(50_001, 255), (50_001, 254), (3000, 256)])
@@ -86,6 +100,26 @@ def test_partition_top_bin(engine, m, bin_):
     n = 2 * m
     codes = rng.integers(0, 257, (n, 3)).astype(np.uint16)
     codes[rng.random(n) < 0.2, 1] = 256
+    engine.load_codes(0, codes)
+    np.testing.assert_array_equal(engine.get_codes(0, n, 3, u16=True), codes)
+    rows = rng.permutation(n)[:m].astype(np.int64)
+    out, nl = engine.partition(rows, 1, bin_)
+    left = codes[rows, 1] <= bin_
+    assert nl == int(left.sum())
+    np.testing.assert_array_equal(out[:nl], rows[left])
+    np.testing.assert_array_equal(out[nl:], rows[~left])
+
+
+@pytest.mark.parametrize("bin_", [254, 255, 300, 509, 510, 764, 765, 999])
+def test_partition_code_tiers(engine, bin_):
+    """Codes up to 1000 (uint16, four tiers): the split at any bin sends
+    exactly the rows with code <= bin left, in order."""
+    _announce(f"partition code tiers bin={bin_}")
+    rng = np.random.default_rng(bin_)
+    m = 70_001
+    n = 2 * m
+    codes = rng.integers(0, 1001, (n, 3)).astype(np.uint16)
+    codes[rng.random(n) < 0.1, 1] = 1000
     engine.load_codes(0, codes)
     np.testing.assert_array_equal(engine.get_codes(0, n, 3, u16=True), codes)
     rows = rng.permutation(n)[:m].astype(np.int64)
@@ -332,6 +366,13 @@ def _fit_case(name):
             X[idx, j] = X[:, j].max()
             y[idx] = 1
         return X, y, dict(n_estimators=40, random_state=0)
+    if name in ("nbins_600", "nbins_2000"):
+        # More than 256 bins per feature (uint16 codes, est:2163-2166): two
+        # or more 8-bit code tiers per feature, with bagging and NaN columns.
+        X, y = make_data(40000, 10, seed=18, nan_frac=0.05, nan_cols=[1, 6])
+        nb = 600 if name == "nbins_600" else 2000
+        return X, y, dict(n_estimators=12, max_depth=6, n_bins=nb, subsample=0.8,
+                          colsample_bytree=0.8, random_state=0)
     if name == "config1":
         rng = np.random.default_rng(0)
         X = rng.standard_normal((10_000, 20), dtype=np.float32)
@@ -373,7 +414,8 @@ def _fit_case(name):
 
 
 @pytest.mark.parametrize("name", ["config1", "nan_imbalanced", "sparse", "defaults_28",
-                                  "top_bin_28", "scale_pos_weight", "confident_400"])
+                                  "top_bin_28", "scale_pos_weight", "confident_400",
+                                  "nbins_600", "nbins_2000"])
 def test_fit_lockstep_and_end_to_end(engine, name):
     """Every round of the oracle's fit, rebuilt by the engine from the same
     gradients, rows and features (lockstep), and the estimator's own tree of
@@ -392,6 +434,15 @@ def test_fit_lockstep_and_end_to_end(engine, name):
         print(f"[result] confident_400: final training loss {est.train_loss_history_[-1]:.3g}",
               flush=True)
         assert est.train_loss_history_[-1] < 1e-4
+    if name in ("nbins_600", "nbins_2000"):
+        from bsscl_gbm import estimator as est_mod
+        got = est_mod._engine(0).get_codes(0, *X.shape, u16=True)
+        np.testing.assert_array_equal(got, ref.X_bin_)
+        splits = [t for tr in est.trees for f, t in zip(tr[0][:tr[5]], tr[1][:tr[5]]) if f >= 0]
+        past = sum(t > 255 for t in splits)
+        print(f"[result] {name}: {est._max_bins} bins, {past} of {len(splits)} splits past "
+              f"bin 255", flush=True)
+        assert past > 0
     if name in ("defaults_28", "top_bin_28"):
         from bsscl_gbm import estimator as est_mod
         assert est.n_bins == 256 and est._max_bins == 257

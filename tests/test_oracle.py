@@ -48,7 +48,7 @@ def test_binning_matches_closed_form(strategy, seed):
     X[:, 4] = np.nan                           # all-NaN column
     X[:5, 5] = [np.inf, -np.inf, 1e30, -1e30, 0.0]
     X[:, 6] = rng.exponential(1.0, n) * (rng.random(n) < 0.1)  # mostly zero
-    for n_bins in (16, 255, 256):
+    for n_bins in (16, 255, 256, 300, 1000):
         e, bc, nid = om.build_bin_edges(X, n_bins)
         codes = om.bin_features(X, e, bc, nid, strategy)
         want = closed_form_codes(X, e, bc, nid)
@@ -136,13 +136,15 @@ def brute_best_split(X_bin, g, h, rows, feats, bc, mcw, lam):
     return best
 
 
-@pytest.mark.parametrize("seed", [0, 1])
-def test_tree_invariants_and_brute_force_splits(seed):
+@pytest.mark.parametrize("seed,n_bins", [(0, 32), (1, 32), (2, 600)])
+def test_tree_invariants_and_brute_force_splits(seed, n_bins):
+    """n_bins = 600 gives uint16 codes and splits past bin 255."""
     rng = np.random.default_rng(seed)
     n, F = 1500, 5
     X, y = make_data(n, F, seed=seed, nan_frac=0.05)
-    e, bc, nid = om.build_bin_edges(X, 32)
+    e, bc, nid = om.build_bin_edges(X, n_bins)
     Xb = om.bin_features(X, e, bc, nid, "standard")
+    assert (Xb.dtype == np.uint16) == (n_bins > 255)
     p = 1 / (1 + np.exp(-rng.standard_normal(n)))
     g, h = p - y, p * (1 - p)
     rows = rng.permutation(n)[:1200].astype(np.int64)
@@ -151,6 +153,8 @@ def test_tree_invariants_and_brute_force_splits(seed):
     tree, counts, pops = om.build_tree(Xb, g, h, rows, feats, ml, md, msl, mcw, bc,
                                        int(bc.max()), lam, 0.0, trace=True)
     tf, tt, tv, tl, tr, nc, sg = tree
+    if n_bins > 256:
+        assert np.any(tt[:nc][tf[:nc] >= 0] > 255)
     per = _node_rows(Xb, tree, rows)
     assert set(per) == set(range(nc))
     n_leaves = int(np.sum(tf[:nc] < 0))
