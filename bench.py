@@ -16,6 +16,9 @@ bounded sample (fit trees/s, histogram rows x features/s, predict rows/s).
 The same block is repeated for the 10M x 50 depth-8 workload: its
 steady-state rounds, its 500-tree fit, predict_proba of a fresh 10M-row
 batch through those 500 trees, and the oracle's first rounds at 10M.
+The smaller benchmark shapes (10,000 x 20, 284,807 x 30 imbalanced,
+100,000 x 100 sparse) follow as complete fits and predictions under
+`workloads`, each with the oracle's rates.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -333,6 +336,38 @@ def run_cpu_baseline(name, rounds, data=None, model=None, Xp_sample=None):
     return out
 
 
+def run_fit_workload(name, cpu_rounds, cpu):
+    """A smaller benchmark shape's complete fit (the workload's own
+    n_estimators, from host float32, after one untimed fit of the same data)
+    and predict_proba of its fresh batch, with the oracle's rates on this
+    host when `cpu`."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    X, y, params = make_workload(name)
+    _progress(f"{name}: {X.shape[0]} x {X.shape[1]}, complete fit")
+    HybridHistGBMNumbaV1_0_1(**params).fit(X, y)
+    est = HybridHistGBMNumbaV1_0_1(**params)
+    t = time.perf_counter()
+    est.fit(X, y)
+    t = time.perf_counter() - t
+    n_trees = int(est.n_trees_fitted_)
+    out = {
+        "config": {"rows": X.shape[0], "features": X.shape[1],
+                   "n_estimators": n_trees, "max_depth": params["max_depth"],
+                   "class_weight": params.get("class_weight", est.class_weight),
+                   "subsample": est.subsample, "colsample_bytree": est.colsample_bytree},
+        "fit_end_to_end": {
+            "seconds": round(t, 4), "trees_per_s": round(n_trees / t, 2),
+            "binning_ms": round(est.times["binning"], 1),
+            "training_ms": round(est.times["training"], 1),
+            "training_trees_per_s": round(n_trees / (est.times["training"] / 1e3), 2)},
+    }
+    out["predict"], sample = run_predict(est, name)
+    if cpu:
+        out["cpu_baseline"] = run_cpu_baseline(name, cpu_rounds, data=(X, y, params),
+                                               model=est, Xp_sample=sample)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -347,6 +382,10 @@ def main():
     ap.add_argument("--also", default="stress_10m",
                     help="workload of the extra rounds-only block ('' for none)")
     ap.add_argument("--also-steps", type=int, default=60)
+    ap.add_argument("--fits", default="cpu_plumbing,imbalanced,sparse_hd",
+                    help="smaller workloads timed as complete fits and predictions "
+                         "('' for none)")
+    ap.add_argument("--fits-cpu-rounds", type=int, default=3)
     a = ap.parse_args()
     if a.gpus != 1:
         print(json.dumps({"error": "this engine runs on one GPU; --gpus must be 1 "
@@ -420,6 +459,12 @@ def main():
             "roofline": hist_roofline(st2, a.also),
             "kernel_ms_per_step": {k: round(r2["breakdown"][f"{k}_ms"] / BREAKDOWN_ROUNDS, 3)
                                    for k in ("hist", "part", "split")},
+            "host_ms_per_step": {
+                "enqueue": round(r2["host"]["enqueue_ms"] / a.also_steps, 3),
+                "finish_wait": round(r2["host"]["finish_ms"] / a.also_steps, 3),
+                "sampler_wait": round(r2["host"]["sampler_wait_ms"] / a.also_steps, 3),
+                "sampler_draw": round(r2["sampler"]["draw_ms"], 3),
+            },
             "fit_end_to_end": r2["fit_full"],
             "predict": r2["predict"],
         }
@@ -428,6 +473,10 @@ def main():
                 a.also, a.also_cpu_rounds, data=r2["data"], model=r2["model"],
                 Xp_sample=r2["Xp_sample"])
         del r2
+    if a.fits and not a.rounds_only:
+        line["workloads"] = {
+            w: run_fit_workload(w, a.fits_cpu_rounds, not a.no_cpu_baseline)
+            for w in a.fits.split(",") if w and w not in (a.workload, a.also)}
     print(json.dumps(line), flush=True)
 
 

@@ -148,10 +148,24 @@ __global__ __launch_bounds__(256) void k_col_pad(KT *__restrict__ keys, int64_t 
   if (i < ld) keys[(int64_t)blockIdx.y * ld + i] = (KT)~(KT)0;
 }
 
-// Digit counts of one tile: counts[(col * n_tiles + tile) * 256 + d].
+// Key sources of a pass: the keys of the previous pass in memory, or (the
+// first pass of the Fisher-Yates sort) keys made from the draws.  in(col, s)
+// is key s of column col.
 template <typename KT>
-__global__ __launch_bounds__(kSortThreads) void k_rs_count(const KT *__restrict__ keys, int64_t ld,
-                                                           int32_t n_tiles, int32_t shift,
+struct KeysIn {
+  const KT *keys;
+  int64_t ld;
+  __device__ void prepare() {}
+  __device__ KT operator()(int32_t col, int64_t s) const { return keys[(int64_t)col * ld + s]; }
+};
+
+}  // namespace
+
+namespace {
+
+// Digit counts of one tile: counts[(col * n_tiles + tile) * 256 + d].
+template <typename KT, typename In>
+__global__ __launch_bounds__(kSortThreads) void k_rs_count(In in, int32_t n_tiles, int32_t shift,
                                                            uint32_t *__restrict__ counts) {
   constexpr int kItems = SortTile<KT>::kItems;
   __shared__ uint32_t cnt[kSortWaves][kRadix];
@@ -159,10 +173,11 @@ __global__ __launch_bounds__(kSortThreads) void k_rs_count(const KT *__restrict_
   const int32_t tile = (int32_t)blockIdx.x, col = (int32_t)blockIdx.y;
   for (int k = 0; k < kSortWaves; ++k) cnt[k][t] = 0;
   __syncthreads();
-  const KT *src = keys + (int64_t)col * ld + (int64_t)tile * tile_keys<KT>();
+  in.prepare();
+  const int64_t s0 = (int64_t)tile * tile_keys<KT>();
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
-    const uint32_t d = (uint32_t)(src[i * kSortThreads + t] >> shift) & 255u;
+    const uint32_t d = (uint32_t)(in(col, s0 + i * kSortThreads + t) >> shift) & 255u;
     const uint64_t m = match_digit(d);
     if (lanes_below(m) == 0) cnt[w][d] += (uint32_t)__popcll(m);
   }
@@ -227,10 +242,10 @@ __global__ __launch_bounds__(256) void k_rs_scan_groups(uint32_t *__restrict__ g
 }
 
 // One stable counting-sort pass of one tile by the digit at `shift`.
-template <typename KT>
-__global__ __launch_bounds__(kSortThreads) void k_rs_scatter(const KT *__restrict__ in,
-                                                             KT *__restrict__ out, int64_t ld,
-                                                             int32_t n_tiles, int32_t shift,
+template <typename KT, typename In>
+__global__ __launch_bounds__(kSortThreads) void k_rs_scatter(In in, KT *__restrict__ out,
+                                                             int64_t ld, int32_t n_tiles,
+                                                             int32_t shift,
                                                              const uint32_t *__restrict__ offs,
                                                              const uint32_t *__restrict__ gpre,
                                                              const uint32_t *__restrict__ starts) {
@@ -242,10 +257,11 @@ __global__ __launch_bounds__(kSortThreads) void k_rs_scatter(const KT *__restric
   __shared__ uint32_t tmp[4];
   const int t = (int)threadIdx.x, w = t >> 6;
   const int32_t tile = (int32_t)blockIdx.x, col = (int32_t)blockIdx.y;
-  const KT *src = in + (int64_t)col * ld + (int64_t)tile * kTile;
+  in.prepare();
+  const int64_t s0 = (int64_t)tile * kTile;
   KT key[kItems];
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) key[i] = src[i * kSortThreads + t];
+  for (int i = 0; i < kItems; ++i) key[i] = in(col, s0 + i * kSortThreads + t);
   // Start of digit t's run for this tile in the output column: the digit's
   // start, its keys in the earlier groups and in the group's earlier tiles.
   const int32_t n_groups = scan_groups(n_tiles);
@@ -388,14 +404,14 @@ hipError_t col_sort_impl(hipStream_t st, const void *Xv, int64_t n, int32_t F, v
   uint32_t *gsum = counts + (int64_t)F * n_tiles * kRadix;  // after the counts
   const dim3 tiles((unsigned)n_tiles, (unsigned)F);
   for (int shift = 0; shift < (int)(8 * sizeof(KT)); shift += 8) {
-    hipLaunchKernelGGL((k_rs_count<KT>), tiles, dim3(kSortThreads), 0, st, keys, ld, n_tiles,
-                       shift, counts);
+    hipLaunchKernelGGL((k_rs_count<KT, KeysIn<KT>>), tiles, dim3(kSortThreads), 0, st,
+                       KeysIn<KT>{keys, ld}, n_tiles, shift, counts);
     hipLaunchKernelGGL(k_rs_scan_tiles, dim3((unsigned)n_groups, (unsigned)F), dim3(256), 0, st,
                        counts, n_tiles, n_groups, gsum);
     hipLaunchKernelGGL(k_rs_scan_groups, dim3((unsigned)F), dim3(256), 0, st, gsum, n_groups,
                        totals);
-    hipLaunchKernelGGL((k_rs_scatter<KT>), tiles, dim3(kSortThreads), 0, st, keys, tmp, ld,
-                       n_tiles, shift, counts, gsum, totals);
+    hipLaunchKernelGGL((k_rs_scatter<KT, KeysIn<KT>>), tiles, dim3(kSortThreads), 0, st,
+                       KeysIn<KT>{keys, ld}, tmp, ld, n_tiles, shift, counts, gsum, totals);
     std::swap(keys, tmp);
   }
   // An even number of passes leaves the sorted keys in keys_v.
@@ -431,25 +447,66 @@ int64_t sort_u64_ld(int64_t n) { return col_sort_ld(n, 1); }
 
 int64_t sort_u64_count_words(int64_t n) { return col_sort_count_words(n, 1, 1); }
 
-hipError_t launch_sort_u64(hipStream_t st, uint64_t *keys, uint64_t *tmp, int64_t ld,
+namespace {
+
+// Passes over bits [lo_bit, hi_bit) in 8-bit digits, the first one reading
+// its keys from `first` (the keys buffer, or keys made on the fly), the
+// others from the previous pass's output; `keys` and `tmp` alternate as
+// outputs, starting with `keys`.
+template <typename In>
+hipError_t sort_u64_passes(hipStream_t st, In first, uint64_t *keys, uint64_t *tmp, int64_t ld,
                            int lo_bit, int hi_bit, uint32_t *counts, uint32_t *totals,
                            uint64_t **result) {
   const int32_t n_tiles = (int32_t)(ld / tile_keys<uint64_t>());
   const int32_t n_groups = scan_groups(n_tiles);
   uint32_t *gsum = counts + (int64_t)n_tiles * kRadix;  // after the counts
   const dim3 tiles((unsigned)n_tiles, 1u);
+  const uint64_t *src = nullptr;
+  uint64_t *dst = keys, *other = tmp;
   for (int shift = lo_bit; shift < hi_bit; shift += 8) {
-    hipLaunchKernelGGL((k_rs_count<uint64_t>), tiles, dim3(kSortThreads), 0, st, keys, ld,
-                       n_tiles, shift, counts);
+    if (!src) {
+      hipLaunchKernelGGL((k_rs_count<uint64_t, In>), tiles, dim3(kSortThreads), 0, st, first,
+                         n_tiles, shift, counts);
+    } else {
+      hipLaunchKernelGGL((k_rs_count<uint64_t, KeysIn<uint64_t>>), tiles, dim3(kSortThreads), 0,
+                         st, KeysIn<uint64_t>{src, ld}, n_tiles, shift, counts);
+    }
     hipLaunchKernelGGL(k_rs_scan_tiles, dim3((unsigned)n_groups, 1u), dim3(256), 0, st, counts,
                        n_tiles, n_groups, gsum);
     hipLaunchKernelGGL(k_rs_scan_groups, dim3(1u), dim3(256), 0, st, gsum, n_groups, totals);
-    hipLaunchKernelGGL((k_rs_scatter<uint64_t>), tiles, dim3(kSortThreads), 0, st, keys, tmp,
-                       ld, n_tiles, shift, counts, gsum, totals);
-    std::swap(keys, tmp);
+    if (!src) {
+      hipLaunchKernelGGL((k_rs_scatter<uint64_t, In>), tiles, dim3(kSortThreads), 0, st, first,
+                         dst, ld, n_tiles, shift, counts, gsum, totals);
+    } else {
+      hipLaunchKernelGGL((k_rs_scatter<uint64_t, KeysIn<uint64_t>>), tiles, dim3(kSortThreads),
+                         0, st, KeysIn<uint64_t>{src, ld}, dst, ld, n_tiles, shift, counts, gsum,
+                         totals);
+    }
+    src = dst;
+    std::swap(dst, other);
   }
-  *result = keys;
+  *result = const_cast<uint64_t *>(src);
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_sort_u64(hipStream_t st, uint64_t *keys, uint64_t *tmp, int64_t ld,
+                           int lo_bit, int hi_bit, uint32_t *counts, uint32_t *totals,
+                           uint64_t **result) {
+  // The first pass reads `keys` and writes `tmp`.
+  if (lo_bit >= hi_bit) {
+    *result = keys;
+    return hipSuccess;
+  }
+  return sort_u64_passes(st, KeysIn<uint64_t>{keys, ld}, tmp, keys, ld, lo_bit, hi_bit, counts,
+                         totals, result);
+}
+
+hipError_t launch_sort_fy_keys(hipStream_t st, FyKeysIn first, uint64_t *keys, uint64_t *tmp,
+                               int64_t ld, int lo_bit, int hi_bit, uint32_t *counts,
+                               uint32_t *totals, uint64_t **result) {
+  return sort_u64_passes(st, first, keys, tmp, ld, lo_bit, hi_bit, counts, totals, result);
 }
 
 hipError_t launch_col_changes(hipStream_t st, const void *keys, int is_f64, int64_t ld, int32_t F,

@@ -1414,9 +1414,9 @@ int ensure_fy_work(bsscl_engine *E, int64_t n, FyWork &w) {
   w.keys = w.keys_tmp = nullptr;
   w.counts = w.totals = nullptr;
   if (sorted && n > 1) {
-    const size_t ld = (size_t)sort_u64_ld(n - 1);
+    const size_t ld = (size_t)sort_u64_ld(n);
     for (auto &k : E->fy_keys) CHK(k.ensure(ld));
-    CHK(E->fy_counts.ensure((size_t)sort_u64_count_words(n - 1)));
+    CHK(E->fy_counts.ensure((size_t)sort_u64_count_words(n)));
     CHK(E->fy_totals.ensure(256));
     w.keys = E->fy_keys[0].p;
     w.keys_tmp = E->fy_keys[1].p;
@@ -1988,12 +1988,14 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
     const int cur = E->perm_cur;
     auto rows_launches = [&]() -> int {
       hipError_t e2 = hipSuccess;
+      // The sorted Fisher-Yates form flags the in-bag rows as it writes them.
+      const bool marked = fy && w.keys;
       if (fy)
         e2 = launch_fisher_yates(rs, w.draws_ref ? nullptr : sr.draws_dev, X.n, E->perm[cur].p,
-                                 E->perm[cur ^ 1].p, w);
+                                 E->perm[cur ^ 1].p, w, marked ? E->row_flags.p : nullptr, m);
       if (e2 == hipSuccess && rows_d)
         e2 = launch_sort_rows(rs, rows_d, m, E->row_flags.p, n_pad, E->sort_tmp.p,
-                              E->round_rows[s].p);
+                              E->round_rows[s].p, marked);
       if (e2 == hipSuccess && R.device_replay)
         e2 = launch_gather_codes(rs, X.codes.p, X.ld,
                                  reinterpret_cast<const int32_t *>(pre.dev[kPackFeat]), F_sel,

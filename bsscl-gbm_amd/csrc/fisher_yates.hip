@@ -203,29 +203,24 @@ __global__ __launch_bounds__(256) void k_fy_final(const uint32_t *__restrict__ d
 }
 
 // ---------------------------------------------------------------------------
-// Sorted form of the same lists.  Step k (1 <= k < n, j(k) != k) becomes the
-// key (j(k) << 32) | k; a stable sort by the high word puts each position's
-// steps together in ascending order.  The first step of a run is head[p];
-// the successor of step k in its position's list is the next key of the run.
+// Sorted form of the same lists.  Key s (s < n) is (j(s) << 32) | s for
+// every step s >= 1, self steps (j(s) = s) included, and (0 << 32) | 0 for
+// position 0 (FyKeysIn); the radix sort's first pass makes them from the
+// draws.  A stable sort by the high word puts each position's steps
+// together in ascending order.  A self step s, or position 0, is the first
+// key of position s's run (every other step choosing s is larger), and its
+// successor in the run is head[s] of the list form, so
+//   a_new[s] = v(successor) or a_old[s] without one
+// is the same rule as for the other steps (v(s) = v(head[s]) or a_old[s]);
+// head[p] itself skips it.
 // ---------------------------------------------------------------------------
 constexpr uint64_t kFyNoKey = ~0ull;
 
-__global__ __launch_bounds__(256) void k_fy_keys(const uint32_t *__restrict__ draws,
-                                                 const uint32_t *const *draws_ref, int64_t n,
-                                                 int64_t ld, uint64_t *__restrict__ keys) {
-  if (draws_ref) draws = *draws_ref;
-  for (int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; s < ld;
-       s += (int64_t)gridDim.x * blockDim.x) {
-    uint64_t key = kFyNoKey;
-    if (s < n - 1) {
-      const int64_t k = s + 1;
-      const uint32_t p = draws[n - 1 - k];
-      if ((int64_t)p != k) key = ((uint64_t)p << 32) | (uint64_t)k;
-    }
-    keys[s] = key;
-  }
-}
-
+// head[p] of every position with steps: the run's first step (the second
+// when the first is p itself).  (head is -1 everywhere on entry: positions
+// without steps keep it.  Writing those here instead, from each run start
+// over the positions before it, made the 10M round 10% longer: near the
+// top positions are chosen rarely, so single lanes looped over long gaps.)
 __global__ __launch_bounds__(256) void k_fy_links(const uint64_t *__restrict__ keys, int64_t ld,
                                                   int32_t *__restrict__ head) {
   for (int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; s < ld;
@@ -233,7 +228,11 @@ __global__ __launch_bounds__(256) void k_fy_links(const uint64_t *__restrict__ k
     const uint64_t key = keys[s];
     if (key == kFyNoKey) continue;
     const uint32_t p = (uint32_t)(key >> 32);
-    if (s == 0 || (uint32_t)(keys[s - 1] >> 32) != p) head[p] = (int32_t)(key & 0xffffffffu);
+    if (s > 0 && (uint32_t)(keys[s - 1] >> 32) == p) continue;  // not a run start
+    const int32_t k = (int32_t)(key & 0xffffffffu);
+    const uint64_t nk = s + 1 < ld ? keys[s + 1] : kFyNoKey;
+    const bool next_same = nk != kFyNoKey && (uint32_t)(nk >> 32) == p;
+    head[p] = k != (int32_t)p ? k : (next_same ? (int32_t)(nk & 0xffffffffu) : -1);
   }
 }
 
@@ -245,15 +244,16 @@ __device__ __forceinline__ int32_t fy_value(const int32_t *__restrict__ head,
   return a_old[x];
 }
 
-// a_new[k] for every step k with j(k) != k, in sorted order: v of the next
-// step of k's run, or a_old[p] for the last step of position p's run.  v is
-// resolved here, for the steps that follow another one in their run only
-// (about 37% of the steps for random draws), instead of for every step.
+// a_new[k] for every key, in sorted order: v of the next step of k's run
+// (resolved here, for the about 37% of the keys that have one), or a_old[p]
+// for the last key of position p's run.  With flags, flags[a_new[k]] = 1
+// for k < m.
 __global__ __launch_bounds__(256) void k_fy_final_sorted(const uint64_t *__restrict__ keys,
                                                          int64_t ld,
                                                          const int32_t *__restrict__ head,
                                                          const int32_t *__restrict__ a_old,
-                                                         int32_t *__restrict__ a_new) {
+                                                         int32_t *__restrict__ a_new,
+                                                         uint8_t *__restrict__ flags, int64_t m) {
   for (int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; s < ld;
        s += (int64_t)gridDim.x * blockDim.x) {
     const uint64_t key = keys[s];
@@ -262,45 +262,32 @@ __global__ __launch_bounds__(256) void k_fy_final_sorted(const uint64_t *__restr
     const int32_t k = (int32_t)(key & 0xffffffffu);
     const uint64_t nk = s + 1 < ld ? keys[s + 1] : kFyNoKey;
     const bool has_next = nk != kFyNoKey && (uint32_t)(nk >> 32) == p;
-    a_new[k] = has_next ? fy_value(head, a_old, (int32_t)(nk & 0xffffffffu)) : a_old[p];
-  }
-}
-
-// a_new[k] = v(k) for position 0 and every step with j(k) == k.
-__global__ __launch_bounds__(256) void k_fy_final_self(const uint32_t *__restrict__ draws,
-                                                       const uint32_t *const *draws_ref,
-                                                       int64_t n,
-                                                       const int32_t *__restrict__ head,
-                                                       const int32_t *__restrict__ a_old,
-                                                       int32_t *__restrict__ a_new) {
-  if (draws_ref) draws = *draws_ref;
-  for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < n;
-       k += (int64_t)gridDim.x * blockDim.x) {
-    if (k == 0 || (int64_t)draws[n - 1 - k] == k) a_new[k] = fy_value(head, a_old, (int32_t)k);
+    const int32_t v = has_next ? fy_value(head, a_old, (int32_t)(nk & 0xffffffffu)) : a_old[p];
+    a_new[k] = v;
+    if (flags && k < m) flags[v] = 1;
   }
 }
 
 }  // namespace
 
 hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
-                               const int32_t *a_old, int32_t *a_new, const FyWork &w) {
+                               const int32_t *a_old, int32_t *a_new, const FyWork &w,
+                               uint8_t *flags, int64_t m) {
   if (n <= 0) return hipSuccess;
   const dim3 g(blocks_for(n)), b(256);
-  if (w.keys && n > 1) {
-    const int64_t ld = sort_u64_ld(n - 1);
-    int bits = 0;
-    while (bits < 32 && ((uint64_t)(n - 1) >> bits) != 0) ++bits;  // positions < 2^bits
+  if (w.keys) {
+    const int64_t ld = sort_u64_ld(n);
+    int bits = 8;  // at least one pass, which makes the keys
+    while (bits < 32 && ((uint64_t)(n - 1) >> bits) != 0) bits += 8;  // positions < 2^bits
     const dim3 gk(blocks_for(ld));
-    hipLaunchKernelGGL(k_fill_neg, dim3(blocks_for((n + 3) / 4)), b, 0, st, w.head, n);
-    hipLaunchKernelGGL(k_fy_keys, gk, b, 0, st, draws, w.draws_ref, n, ld, w.keys);
     uint64_t *sorted = nullptr;
-    hipError_t e = launch_sort_u64(st, w.keys, w.keys_tmp, ld, 32, 32 + (bits + 7) / 8 * 8,
-                                   w.counts, w.totals, &sorted);
+    hipLaunchKernelGGL(k_fill_neg, dim3(blocks_for((n + 3) / 4)), b, 0, st, w.head, n);
+    hipError_t e = launch_sort_fy_keys(st, FyKeysIn{draws, w.draws_ref, n}, w.keys, w.keys_tmp,
+                                       ld, 32, 32 + bits, w.counts, w.totals, &sorted);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_fy_links, gk, b, 0, st, sorted, ld, w.head);
-    hipLaunchKernelGGL(k_fy_final_sorted, gk, b, 0, st, sorted, ld, w.head, a_old, a_new);
-    hipLaunchKernelGGL(k_fy_final_self, g, b, 0, st, draws, w.draws_ref, n, w.head, a_old,
-                       a_new);
+    hipLaunchKernelGGL(k_fy_final_sorted, gk, b, 0, st, sorted, ld, w.head, a_old, a_new, flags,
+                       m);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(k_fill_neg, dim3(blocks_for((n + 3) / 4)), b, 0, st, w.head, n);

@@ -259,7 +259,7 @@ hipError_t launch_grad_hess_f64(hipStream_t st, const double *F,
                                 double w1, double *g, double *h);
 hipError_t launch_sort_rows(hipStream_t st, const int32_t *rows, int64_t m,
                             uint8_t *flags, int64_t n_pad, int32_t *block_tmp,
-                            int32_t *out);
+                            int32_t *out, bool marked = false);
 int64_t sort_rows_flag_bytes(int64_t n);
 hipError_t launch_iota(hipStream_t st, int32_t *a, int64_t n);
 // a[0, n) = v.
@@ -268,8 +268,8 @@ hipError_t launch_fill_f64(hipStream_t st, double *a, int64_t n, double v);
 struct FyWork {
   int32_t *head, *next, *v;
   // Sorted form (used when keys is set): (position, step) keys, their sort
-  // buffer and counts (sort_u64_ld(n - 1) keys, sort_u64_count_words(n - 1)
-  // and 256 words).
+  // buffer and counts (sort_u64_ld(n) keys, sort_u64_count_words(n) and
+  // 256 words).
   uint64_t *keys = nullptr, *keys_tmp = nullptr;
   uint32_t *counts = nullptr, *totals = nullptr;
   // When set, the kernels read the draws' address from this device word
@@ -279,9 +279,11 @@ struct FyWork {
   const uint32_t *const *draws_ref = nullptr;
 };
 // a_new = a_old after the Fisher-Yates steps i = n-1 .. 1 with draws[t] =
-// j(n-1-t) <= n-1-t.
+// j(n-1-t) <= n-1-t.  With flags (sorted form only), flags[a_new[i]] is also
+// set to 1 for every i < m (the in-bag rows of launch_sort_rows).
 hipError_t launch_fisher_yates(hipStream_t st, const uint32_t *draws, int64_t n,
-                               const int32_t *a_old, int32_t *a_new, const FyWork &w);
+                               const int32_t *a_old, int32_t *a_new, const FyWork &w,
+                               uint8_t *flags = nullptr, int64_t m = 0);
 
 hipError_t launch_gather_root(hipStream_t st, const uint8_t *codes, int64_t ld,
                               const int32_t *feat, int32_t F_sel,
@@ -492,6 +494,27 @@ int64_t sort_u64_count_words(int64_t n);
 hipError_t launch_sort_u64(hipStream_t st, uint64_t *keys, uint64_t *tmp, int64_t ld,
                            int lo_bit, int hi_bit, uint32_t *counts, uint32_t *totals,
                            uint64_t **result);
+// Key s of the Fisher-Yates sort (s < n): (j(s) << 32) | s for every step
+// s >= 1 (self steps included) and (0 << 32) | 0 for position 0; the
+// largest key from n on.  draws[t] = j(n - 1 - t).
+struct FyKeysIn {
+  const uint32_t *draws;
+  const uint32_t *const *draws_ref;  // where the draws' address is, or null
+  int64_t n;
+  __device__ void prepare() {
+    if (draws_ref) draws = *draws_ref;
+  }
+  __device__ uint64_t operator()(int32_t, int64_t s) const {
+    if (s >= n) return ~0ull;
+    const uint64_t p = s > 0 ? (uint64_t)draws[n - 1 - s] : 0ull;
+    return (p << 32) | (uint64_t)s;
+  }
+};
+// The same sort with the first pass reading FyKeysIn (no key array), its
+// output in `keys`, later passes alternating with `tmp`.
+hipError_t launch_sort_fy_keys(hipStream_t st, FyKeysIn first, uint64_t *keys, uint64_t *tmp,
+                               int64_t ld, int lo_bit, int hi_bit, uint32_t *counts,
+                               uint32_t *totals, uint64_t **result);
 hipError_t launch_col_gather(hipStream_t st, const void *keys, int is_f64, int64_t ld,
                              int64_t count, const int32_t *col, const int64_t *pos, double *out);
 

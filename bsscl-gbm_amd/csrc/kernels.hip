@@ -412,12 +412,15 @@ __global__ __launch_bounds__(kFlagBlock) void k_flag_write(uint8_t *__restrict__
 }
 
 // flags: n_pad bytes (multiple of kFlagTile), zero on entry and on exit.
+// `marked`: the rows' flags are already set (launch_fisher_yates did it).
 hipError_t launch_sort_rows(hipStream_t st, const int32_t *rows, int64_t m,
                             uint8_t *flags, int64_t n_pad, int32_t *block_tmp,
-                            int32_t *out) {
+                            int32_t *out, bool marked) {
   if (m <= 0) return hipSuccess;
   const unsigned nb = (unsigned)(n_pad / kFlagTile);
-  hipLaunchKernelGGL(k_mark, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, rows, m, flags);
+  if (!marked)
+    hipLaunchKernelGGL(k_mark, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, rows, m,
+                       flags);
   hipLaunchKernelGGL(k_flag_count, dim3(nb), dim3(kFlagBlock), 0, st, flags, block_tmp);
   hipLaunchKernelGGL(k_block_scan, dim3(1), dim3(kFlagBlock), 0, st, block_tmp, (int32_t)nb);
   hipLaunchKernelGGL(k_flag_write, dim3(nb), dim3(kFlagBlock), 0, st, flags, block_tmp, out);
@@ -1319,6 +1322,13 @@ __device__ __forceinline__ void transpose4(uint32_t w0, uint32_t w1, uint32_t w2
 // per barrier through LDS bytes instead of four through words: the word
 // transposes of 16 rows need more registers than that.
 template <int R> struct ScatterWaves { static constexpr int value = 4; };
+// Features a 16-row tile stages per barrier: each thread's next Q codes
+// loads are in flight while it gathers the current ones.  At 10M x 50
+// (35 features) one feature per barrier kept about 16 KB of loads in flight
+// per CU and moved 2.9 TB/s; Q = 2, 4 and 8 ran the round in 2.49, 2.46 and
+// 2.56 ms against 2.54 (Q = 8: 74 KB of LDS, two blocks per CU).
+template <int R> struct ScatterQ { static constexpr int value = 1; };
+template <> struct ScatterQ<16> { static constexpr int value = 4; };
 
 // One of four values by a run index r in 0..3, as selects of values (an
 // array indexed by r would live in scratch memory).
@@ -1327,7 +1337,7 @@ __device__ __forceinline__ T sel4(int r, T a, T b, T c, T d) {
   return r == 0 ? a : r == 1 ? b : r == 2 ? c : d;
 }
 
-template <int R>
+template <int R, int Q = ScatterQ<R>::value>
 __global__ __launch_bounds__(kPartBlock) __attribute__((amdgpu_waves_per_eu(ScatterWaves<R>::value)))
 void k_part_scatter(
     const uint8_t *__restrict__ codes_src, uint8_t *__restrict__ codes_dst,
@@ -1344,10 +1354,10 @@ void k_part_scatter(
   constexpr int kTile = kPartBlock * R;
   __shared__ uint16_t inv[kTile];
   constexpr bool kQuads = R < 16;
-  // Four features' codes per tile row (16-row tiles: one feature's codes per
+  // Four features' codes per tile row (16-row tiles: Q features' codes per
   // thread), double buffered.
   __shared__ __align__(16) uint32_t rows4[2][kQuads ? kTile : 1];
-  __shared__ typename CodesR<R>::T cs[2][kQuads ? 1 : kPartBlock];
+  __shared__ typename CodesR<R>::T cs[2][kQuads ? 1 : Q * kPartBlock];
   const int32_t n_tiles = plan->n_tiles;
   const int tid = (int)threadIdx.x;
   for (int32_t ti = (int32_t)blockIdx.x; ti < n_tiles; ti += (int32_t)gridDim.x) {
@@ -1450,79 +1460,117 @@ void k_part_scatter(
       gh_dst[d] = gh_src[src];
       if (rid_dst) rid_dst[d] = rid_src[src];
     }
-    // Output chunks: each run's aligned R-byte chunks, runs in order.  Per
-    // owned chunk: its destination row and, per byte, the tile row it
-    // copies (0xffff: outside the run, not written).
+    // Output chunks: each run's aligned R-byte chunks, runs in order.
     int cum[4], n_chunks = 0;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       cum[r] = n_chunks;
       n_chunks += len[r] ? (int)((base[r] + len[r] + R - 1) / R - base[r] / R) : 0;
     }
-    int64_t cdst[kChunkSlots];
-    uint32_t csrc[kChunkSlots][R / 2];  // R x u16 tile rows
-    bool cfull[kChunkSlots], cown[kChunkSlots];
-#pragma unroll
-    for (int q = 0; q < kChunkSlots; ++q) {
-      const int c = tid + q * kPartBlock;
-      cown[q] = c < n_chunks;
-      const int r = (c >= cum[1] ? 1 : 0) + (c >= cum[2] ? 1 : 0) + (c >= cum[3] ? 1 : 0);
-      const int64_t D = sel4(r, base[0], base[1], base[2], base[3]);
-      const int L = sel4(r, len[0], len[1], len[2], len[3]);
-      const int S = sel4(r, off[0], off[1], off[2], off[3]);
-      const int64_t c0 =
-          (D & ~int64_t(R - 1)) + R * (int64_t)(c - sel4(r, cum[0], cum[1], cum[2], cum[3]));
-      cdst[q] = c0;
-      bool full = true;
-#pragma unroll
-      for (int k = 0; k < R; k += 2) {
-        uint32_t pairv = 0u;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int64_t dr = c0 + k + h;
-          const bool in = cown[q] && dr >= D && dr < D + L;
-          full = full && in;
-          const uint32_t src = in ? (uint32_t)inv[S + (int)(dr - D)] : 0xffffu;
-          pairv |= src << (16 * h);
-        }
-        csrc[q][k >> 1] = pairv;
-      }
-      cfull[q] = full;
-    }
-    // Codes, double buffered in LDS (one barrier per batch, the next batch's
-    // loads in flight meanwhile), then the owned chunks gathered and stored:
-    // 16-row tiles one feature per batch as bytes, narrower tiles four
-    // features per batch as one word of four codes per tile row.
     if constexpr (!kQuads) {
-      CodeWords<R> c1 = load_codes<R>(codes_src, row, lo, hi);
-      for (int f = 0, b = 0; f < F_sel; ++f, b ^= 1) {
-        cs[b][tid] = c1.v;
-        if (f + 1 < F_sel) c1 = load_codes<R>(codes_src + (int64_t)(f + 1) * ld_c, row, lo, hi);
+      // 16-row tiles.  Per owned chunk: its destination row, the slot (inv
+      // index) of its first byte and the bytes [klo, khi) that lie in its
+      // run (all 16 for a full chunk); each batch of Q features reads the
+      // chunk's 16 tile rows from inv once.
+      int64_t cdst[kChunkSlots];
+      int32_t cinv[kChunkSlots], kr[kChunkSlots];
+      bool cown[kChunkSlots];
+#pragma unroll
+      for (int q = 0; q < kChunkSlots; ++q) {
+        const int c = tid + q * kPartBlock;
+        cown[q] = c < n_chunks;
+        const int r = (c >= cum[1] ? 1 : 0) + (c >= cum[2] ? 1 : 0) + (c >= cum[3] ? 1 : 0);
+        const int64_t D = sel4(r, base[0], base[1], base[2], base[3]);
+        const int L = sel4(r, len[0], len[1], len[2], len[3]);
+        const int S = sel4(r, off[0], off[1], off[2], off[3]);
+        const int64_t c0 =
+            (D & ~int64_t(R - 1)) + R * (int64_t)(c - sel4(r, cum[0], cum[1], cum[2], cum[3]));
+        cdst[q] = c0;
+        cinv[q] = S + (int)(c0 - D);
+        const int klo = (int)max<int64_t>(0, D - c0);
+        const int khi = (int)min<int64_t>(R, D + L - c0);
+        kr[q] = klo | (khi << 8);
+      }
+      CodeWords<R> nxt[Q];
+#pragma unroll
+      for (int u = 0; u < Q; ++u)
+        nxt[u] = u < F_sel ? load_codes<R>(codes_src + (int64_t)u * ld_c, row, lo, hi)
+                           : zero_codes<R>();
+      for (int f0 = 0, b = 0; f0 < F_sel; f0 += Q, b ^= 1) {
+#pragma unroll
+        for (int u = 0; u < Q; ++u) cs[b][u * kPartBlock + tid] = nxt[u].v;
+#pragma unroll
+        for (int u = 0; u < Q; ++u)
+          if (f0 + Q + u < F_sel)
+            nxt[u] = load_codes<R>(codes_src + (int64_t)(f0 + Q + u) * ld_c, row, lo, hi);
         __syncthreads();
-        const uint8_t *tb = reinterpret_cast<const uint8_t *>(cs[b]);
-        uint8_t *dcol = codes_dst + (int64_t)f * ld_c;
+        const int nf = min(Q, F_sel - f0);
 #pragma unroll
         for (int q = 0; q < kChunkSlots; ++q) {
           if (!cown[q]) continue;
-          if (cfull[q]) {
-            CodeWords<R> o;
+          const int klo = kr[q] & 255, khi = kr[q] >> 8;
+          if (klo == 0 && khi == R) {
+            uint32_t src[R];
 #pragma unroll
-            for (int k = 0; k < R / 4; ++k) {
-              const uint32_t s01 = csrc[q][2 * k], s23 = csrc[q][2 * k + 1];
-              o.w[k] = (uint32_t)tb[s01 & 0xffffu] | ((uint32_t)tb[s01 >> 16] << 8) |
-                       ((uint32_t)tb[s23 & 0xffffu] << 16) | ((uint32_t)tb[s23 >> 16] << 24);
+            for (int k = 0; k < R; ++k) src[k] = inv[cinv[q] + k];
+#pragma unroll
+            for (int u = 0; u < Q; ++u) {
+              if (u >= nf) break;
+              const uint8_t *tb = reinterpret_cast<const uint8_t *>(cs[b] + u * kPartBlock);
+              CodeWords<R> o;
+#pragma unroll
+              for (int k = 0; k < R / 4; ++k)
+                o.w[k] = (uint32_t)tb[src[4 * k]] | ((uint32_t)tb[src[4 * k + 1]] << 8) |
+                         ((uint32_t)tb[src[4 * k + 2]] << 16) |
+                         ((uint32_t)tb[src[4 * k + 3]] << 24);
+              *reinterpret_cast<typename CodesR<R>::T *>(codes_dst + (int64_t)(f0 + u) * ld_c +
+                                                         cdst[q]) = o.v;
             }
-            *reinterpret_cast<typename CodesR<R>::T *>(dcol + cdst[q]) = o.v;
           } else {
-#pragma unroll
-            for (int k = 0; k < R; ++k) {
-              const uint32_t sv = (csrc[q][k >> 1] >> (16 * (k & 1))) & 0xffffu;
-              if (sv != 0xffffu) dcol[cdst[q] + k] = tb[sv];
+            for (int u = 0; u < nf; ++u) {
+              const uint8_t *tb = reinterpret_cast<const uint8_t *>(cs[b] + u * kPartBlock);
+              uint8_t *dcol = codes_dst + (int64_t)(f0 + u) * ld_c;
+              for (int k = klo; k < khi; ++k) dcol[cdst[q] + k] = tb[inv[cinv[q] + k]];
             }
           }
         }
       }
     } else {
+      // Per owned chunk: its destination row and, per byte, the tile row it
+      // copies (0xffff: outside the run, not written).
+      int64_t cdst[kChunkSlots];
+      uint32_t csrc[kChunkSlots][R / 2];  // R x u16 tile rows
+      bool cfull[kChunkSlots], cown[kChunkSlots];
+#pragma unroll
+      for (int q = 0; q < kChunkSlots; ++q) {
+        const int c = tid + q * kPartBlock;
+        cown[q] = c < n_chunks;
+        const int r = (c >= cum[1] ? 1 : 0) + (c >= cum[2] ? 1 : 0) + (c >= cum[3] ? 1 : 0);
+        const int64_t D = sel4(r, base[0], base[1], base[2], base[3]);
+        const int L = sel4(r, len[0], len[1], len[2], len[3]);
+        const int S = sel4(r, off[0], off[1], off[2], off[3]);
+        const int64_t c0 =
+            (D & ~int64_t(R - 1)) + R * (int64_t)(c - sel4(r, cum[0], cum[1], cum[2], cum[3]));
+        cdst[q] = c0;
+        bool full = true;
+#pragma unroll
+        for (int k = 0; k < R; k += 2) {
+          uint32_t pairv = 0u;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int64_t dr = c0 + k + h;
+            const bool in = cown[q] && dr >= D && dr < D + L;
+            full = full && in;
+            const uint32_t src = in ? (uint32_t)inv[S + (int)(dr - D)] : 0xffffu;
+            pairv |= src << (16 * h);
+          }
+          csrc[q][k >> 1] = pairv;
+        }
+        cfull[q] = full;
+      }
+      // Four features per batch, as one word of four codes per tile row,
+      // double buffered in LDS (one barrier per batch, the next batch's
+      // loads in flight meanwhile), then the owned chunks gathered and stored.
       CodeWords<R> cur[kQuad];
 #pragma unroll
       for (int u = 0; u < kQuad; ++u) {
@@ -1597,16 +1645,16 @@ hipError_t launch_part_scatter(hipStream_t st, const uint8_t *codes_src,
                                int64_t *parent_nleft, NodeSeg *segs, int32_t *hist_node,
                                int32_t min_samples_leaf, int32_t F_sel) {
   if (max_tiles <= 0) return hipSuccess;
-#define BSSCL_SCATTER(R)                                                                 \
-  hipLaunchKernelGGL(k_part_scatter<R>, dim3((unsigned)max_tiles), dim3(kPartBlock), 0, st, \
-                     codes_src, codes_dst, ld_c, gh_src, gh_dst, rid_src, rid_dst, parents, \
-                     groups, tiles, plan, tile_begin, tile_cnt, parent_nleft, segs,       \
-                     hist_node,                                                           \
+#define BSSCL_SCATTER(R, Q)                                                                   \
+  hipLaunchKernelGGL((k_part_scatter<R, Q>), dim3((unsigned)max_tiles), dim3(kPartBlock), 0, st, \
+                     codes_src, codes_dst, ld_c, gh_src, gh_dst, rid_src, rid_dst, parents,      \
+                     groups, tiles, plan, tile_begin, tile_cnt, parent_nleft, segs,            \
+                     hist_node,                                                                \
                      min_samples_leaf, F_sel)
   switch (part_rows) {
-    case 4: BSSCL_SCATTER(4); break;
-    case 8: BSSCL_SCATTER(8); break;
-    case 16: BSSCL_SCATTER(16); break;
+    case 4: BSSCL_SCATTER(4, ScatterQ<4>::value); break;
+    case 8: BSSCL_SCATTER(8, ScatterQ<8>::value); break;
+    case 16: BSSCL_SCATTER(16, ScatterQ<16>::value); break;
     default: return hipErrorInvalidValue;
   }
 #undef BSSCL_SCATTER

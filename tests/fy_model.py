@@ -63,32 +63,37 @@ def fisher_yates_lists(a_old, draws):
 
 
 def fisher_yates_sorted_keys(a_old, draws):
-    """The sorted form of the device kernels (k_fy_keys, k_fy_links,
-    k_fy_final_sorted, k_fy_final_self in fisher_yates.hip): step k with
-    j(k) != k becomes the key (j(k) << 32) | k, steps with j(k) == k the
-    largest key; a stable sort on the high word; run starts give head[];
-    each key's successor in its run gives a_new[k], with v resolved only at
-    the successors and the self steps."""
+    """The sorted form of the device kernels (FyKeysIn and the radix sort,
+    k_fy_links, k_fy_final_sorted in fisher_yates.hip): key s is
+    (j(s) << 32) | s for every step s >= 1, self steps included, and 0 for
+    position 0; a stable sort on the high word; a run's first key gives
+    head[p] unless it is p itself (a self step or position 0), when the
+    second does; every key's successor in its run gives a_new[k] (v of the
+    successor, or a_old[p] without one), with v resolved only at the
+    successors."""
     a_old = np.asarray(a_old)
     n = len(a_old)
     if n <= 1:
         return np.array(a_old, copy=True)
-    NO = np.uint64(0xFFFFFFFFFFFFFFFF)
-    k = np.arange(1, n, dtype=np.uint64)
-    p = np.asarray(draws, dtype=np.uint64)[n - 1 - np.arange(1, n)]
-    keys = np.where(p != k, (p << np.uint64(32)) | k, NO)
+    s = np.arange(n, dtype=np.uint64)
+    p = np.zeros(n, np.uint64)
+    p[1:] = np.asarray(draws, dtype=np.uint64)[n - 1 - np.arange(1, n)]
+    keys = (p << np.uint64(32)) | s
     keys = keys[np.argsort(keys >> np.uint64(32), kind="stable")]
-    valid = keys != NO
     hi = (keys >> np.uint64(32)).astype(np.int64)
     lo = (keys & np.uint64(0xFFFFFFFF)).astype(np.int64)
-    head = np.full(n, -1, np.int64)
-    start = valid.copy()
-    start[1:] &= hi[1:] != hi[:-1]
-    head[hi[start]] = lo[start]
+    nxt_same = np.zeros(n, bool)
+    nxt_same[:-1] = hi[1:] == hi[:-1]
+    succ = np.full(n, -1, np.int64)
+    succ[:-1] = np.where(nxt_same[:-1], lo[1:], -1)
+    start = np.ones(n, bool)
+    start[1:] = hi[1:] != hi[:-1]
+    head = np.full(n, -1, np.int64)  # positions without steps keep -1
+    head[hi[start]] = np.where(lo[start] != hi[start], lo[start], succ[start])
 
     def value(x):
         """v(x): a_old at the end of each x's chain x -> head[x] -> ...,
-        resolved only for the positions asked (as k_fy_final_* do)."""
+        resolved only for the positions asked (as k_fy_final_sorted does)."""
         root = np.array(x, dtype=np.int64, copy=True)
         while True:
             h = head[root]
@@ -99,15 +104,8 @@ def fisher_yates_sorted_keys(a_old, draws):
         return a_old[root]
 
     out = np.full(n, -12345, dtype=a_old.dtype)
-    nxt_same = np.zeros(len(keys), bool)
-    nxt_same[:-1] = valid[1:] & (hi[1:] == hi[:-1])
-    succ = np.full(len(keys), -1, np.int64)
-    succ[:-1] = np.where(nxt_same[:-1], lo[1:], -1)
-    idx = np.nonzero(valid)[0]
-    has = succ[idx] >= 0
-    res = a_old[hi[idx]].copy()
-    res[has] = value(succ[idx][has])
-    out[lo[idx]] = res
-    self_k = np.nonzero(np.concatenate([[True], p == k]))[0]
-    out[self_k] = value(self_k)
+    has = succ >= 0
+    res = a_old[hi].copy()
+    res[has] = value(succ[has])
+    out[lo] = res
     return out

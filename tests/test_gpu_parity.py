@@ -221,12 +221,13 @@ def _lockstep_case(engine, n, F, seed, n_bins, max_leaves, max_depth, msl, mcw,
     return out
 
 
-@pytest.mark.parametrize("n", [1, 2, 3, 5, 64, 1000, 4099])
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 64, 1000, 4099, 70_001])
 @pytest.mark.parametrize("form", ["lists", "sorted"])
 def test_fisher_yates_device_adversarial(engine, n, form, monkeypatch):
     """GPU swaps (per-position lists, or the sorted (position, step) form)
     against the sequential loop for draws no RNG would give: one position
-    chosen by every step, no swaps, a chain through all steps."""
+    chosen by every step, no swaps, a chain through all steps.  70,001 rows
+    sort their keys over 35 tiles in three passes."""
     from test_sampler import _adversarial_draws
     import fy_model
     monkeypatch.setenv("BSSCL_FY_SORTED", "1" if form == "sorted" else "0")
