@@ -53,6 +53,24 @@ def _engine(device: int) -> _native.Engine:
     return eng
 
 
+def _encode_labels(y):
+    """np.unique(y) and the labels as 0 .. K-1 (est:3124-3129), as
+    np.searchsorted(classes, y).  Integer labels that are already 0 .. K-1
+    (the usual case) skip the sort and the search: counting gives the
+    classes, and the labels are their own codes."""
+    y = np.asarray(y)
+    if y.ndim == 1 and y.size and (y.dtype.kind in "iu" or y.dtype == np.bool_):
+        lo, hi = int(y.min()), int(y.max())
+        if lo >= 0 and hi < (1 << 16):
+            present = np.bincount(y.astype(np.int64, copy=False), minlength=hi + 1) > 0
+            classes = np.nonzero(present)[0].astype(y.dtype)
+            if len(classes) == hi + 1:  # every value 0 .. hi occurs: codes = labels
+                return classes, y.astype(np.int64, copy=False)
+            return classes, np.searchsorted(classes, y).astype(np.int64)
+    classes = np.unique(y)
+    return classes, np.searchsorted(classes, y).astype(np.int64)
+
+
 def _to_dense(X):
     try:
         import scipy.sparse
@@ -466,15 +484,13 @@ class HybridHistGBMNumbaV1_0_1:
             raise ValueError(f"X has {X.shape[0]} rows but y has {len(y)} labels")
         self._check_supported()
 
-        self.classes_ = np.unique(y)
+        self.classes_, y = _encode_labels(y)
         self.n_classes_ = len(self.classes_)
         self._is_multiclass = self.n_classes_ > 2
         if self.n_classes_ < 2:
             raise NotImplementedError(
                 "the MI355X engine needs at least two classes; got "
                 f"{self.n_classes_}")
-        # est:3124-3129: labels become 0 .. K-1.
-        y = np.searchsorted(self.classes_, y).astype(np.int64)
         if y_val is not None:
             y_val = np.asarray(y_val)
             label_map = {c: i for i, c in enumerate(self.classes_)}
@@ -580,8 +596,11 @@ class HybridHistGBMNumbaV1_0_1:
         n_samples = len(y)
         n_features = self.n_features_in_
         w0, w1 = self._class_weight_pair(y)
-        sw = np.where(y == 1, w1, w0)
-        weighted_mean = np.average(y, weights=sw)
+        # np.average(y, weights=np.where(y == 1, w1, w0)) of the reference
+        # (est:2829-2834): sum(y * w) / sum(w) over the same float64 arrays,
+        # built by lookup (y holds 0 and 1), so the sums are NumPy's own.
+        sw = np.array([w0, w1])[y]
+        weighted_mean = np.array([0.0, w1])[y].sum() / sw.sum()
         p0 = np.clip(weighted_mean, 1e-7, 1.0 - 1e-7)
         self.base_score_ = np.log(p0 / (1.0 - p0))
         F_val = np.full(n_val, self.base_score_) if n_val else None
@@ -794,16 +813,20 @@ class HybridHistGBMNumbaV1_0_1:
         self._tree_offsets = packed['offsets']
 
     def _compute_feature_importances(self):
+        """est:2343-2363: every split's gain added to its feature, tree by
+        tree and node by node.  np.add.at adds in that same order (it is
+        unbuffered), so the float64 sums are the reference's."""
         gain_imp = np.zeros(self.n_features_in_, dtype=np.float64)
         split_cnt = np.zeros(self.n_features_in_, dtype=np.int64)
         tree_lists = self.mc_trees if self._is_multiclass else [self.trees]
-        for trees in tree_lists:
-            for tf, tt, tv, tl, tr, nc, sg in trees:
-                for node_idx in range(nc):
-                    feat = tf[node_idx]
-                    if feat >= 0:
-                        gain_imp[feat] += sg[node_idx]
-                        split_cnt[feat] += 1
+        feats = [np.asarray(tf[:nc]) for trees in tree_lists for tf, tt, tv, tl, tr, nc, sg in trees]
+        gains = [np.asarray(sg[:nc]) for trees in tree_lists for tf, tt, tv, tl, tr, nc, sg in trees]
+        if feats:
+            f = np.concatenate(feats).astype(np.int64)
+            g = np.concatenate(gains).astype(np.float64)
+            split = f >= 0
+            np.add.at(gain_imp, f[split], g[split])
+            np.add.at(split_cnt, f[split], 1)
         total = gain_imp.sum()
         self.feature_importances_ = gain_imp / total if total > 0 else np.zeros(self.n_features_in_)
         self.feature_split_counts_ = split_cnt

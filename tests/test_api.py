@@ -130,3 +130,51 @@ def test_sampler_rejects_bad_arguments():
         _native.Sampler(st, 10, 11, True, 3, 2, True, 1)
     with pytest.raises(ValueError):
         _native.Sampler(st, 10, 5, False, 3, 2, True, 1)
+
+
+def test_label_encoding_equals_unique_and_searchsorted():
+    """The estimator's label encoding (a counting path for integer labels
+    0 .. K-1) equals np.unique + np.searchsorted (est:3124-3129), dtype
+    included, and the base score's weighted mean built by lookup equals
+    np.average with the reference's np.where weights bit for bit."""
+    from bsscl_gbm.estimator import _encode_labels
+    rng = np.random.default_rng(5)
+    cases = [rng.integers(0, 2, 1000), rng.integers(0, 5, 1000).astype(np.int32),
+             np.array([3, 7, 3, 9]), rng.random(100) < 0.3, np.array(["b", "a", "b"]),
+             np.array([2, 2, 5]), np.array([-1, 1, -1]), rng.integers(0, 2, 10).astype(np.uint8),
+             np.array([0.0, 1.0, 1.0])]
+    for y in cases:
+        c, e = _encode_labels(y)
+        c2 = np.unique(y)
+        np.testing.assert_array_equal(c, c2)
+        assert c.dtype == c2.dtype and e.dtype == np.int64
+        np.testing.assert_array_equal(e, np.searchsorted(c2, y))
+    for n in (1, 7, 1000, 100_003):
+        y = (rng.random(n) < 0.3).astype(np.int64)
+        for w0, w1 in ((1.0, 1.0), (0.785, 7.31), (1.0, 6.0)):
+            want = np.average(y, weights=np.where(y == 1, w1, w0))
+            got = np.array([0.0, w1])[y].sum() / np.array([w0, w1])[y].sum()
+            assert got == want
+
+
+def test_feature_importances_equal_node_loop():
+    """feature_importances_ (est:2343-2363) equals the node-by-node loop of
+    the reference bit for bit, over random trees with leaves (-1) mixed in."""
+    rng = np.random.default_rng(7)
+    trees = []
+    for _ in range(60):
+        nc = int(rng.integers(1, 64))
+        tf = rng.integers(-1, 12, 130).astype(np.int32)
+        sg = rng.standard_normal(130) * 10.0 ** rng.integers(-6, 3)
+        trees.append((tf, None, None, None, None, nc, sg))
+    est = HybridHistGBMNumbaV1_0_1(verbose=False)
+    est.n_features_in_, est._is_multiclass, est.trees = 12, False, trees
+    est._compute_feature_importances()
+    gain, cnt = np.zeros(12), np.zeros(12, np.int64)
+    for tf, _, _, _, _, nc, sg in trees:
+        for i in range(nc):
+            if tf[i] >= 0:
+                gain[tf[i]] += sg[i]
+                cnt[tf[i]] += 1
+    np.testing.assert_array_equal(est.feature_importances_, gain / gain.sum())
+    np.testing.assert_array_equal(est.feature_split_counts_, cnt)
