@@ -43,8 +43,11 @@ _SIGS = {
     "bsscl_boost_grad_hess_max": [_P, _P],
     "bsscl_mc_begin": [_P, _P, _i64, _i32, _P],
     "bsscl_mc_round": [_P, _P, _i64],
+    "bsscl_mc_round_sampled": [_P, _P, _P],
     "bsscl_mc_build_tree": [_P, _i32, _P, _i32, _i32, _i32, _i32, _f64, _P, _i32, _f64,
                             _f64, _f64, _P, _P, _P, _P, _P, _P, _P],
+    "bsscl_mc_build_trees": [_P, _P, _i32, _i32, _i32, _i32, _f64, _P, _i32, _f64, _f64, _f64,
+                             _P, _P, _P, _P, _P, _P, _P],
     "bsscl_mc_loss": [_P, _P],
     "bsscl_mc_get_scores": [_P, _P],
     "bsscl_mc_get_grad_hess": [_P, _P, _P],
@@ -265,6 +268,12 @@ class Engine:
         si = np.ascontiguousarray(sample_indices, np.int64)
         check(lib().bsscl_mc_round(self.handle, ptr(si), len(si)))
 
+    def mc_round_sampled(self, sampler):
+        """mc_round with the sampler's next round; returns its feature subset."""
+        feats = np.empty(sampler.f_sub, np.int32)
+        check(lib().bsscl_mc_round_sampled(self.handle, sampler.handle, ptr(feats)))
+        return feats
+
     def mc_build_tree(self, k, feature_indices, max_leaves, max_depth, min_samples_leaf,
                       min_child_weight, bin_counts, max_bins, reg_lambda, gamma,
                       learning_rate):
@@ -277,6 +286,29 @@ class Engine:
             float(reg_lambda), float(gamma), float(learning_rate), ptr(tf), ptr(tt),
             ptr(tv), ptr(tl), ptr(tr), ptr(nc), ptr(sg)))
         return (tf, tt, tv, tl, tr, int(nc[0]), sg)
+
+    def mc_build_trees(self, feature_indices, max_leaves, max_depth, min_samples_leaf,
+                       min_child_weight, bin_counts, max_bins, reg_lambda, gamma,
+                       learning_rate):
+        """The round's K trees (classes 0..K-1) in one call; a list of K
+        7-tuples as mc_build_tree returns them."""
+        K = self._mc[1]
+        M = 2 * int(max_leaves) + 2
+        fi = np.ascontiguousarray(feature_indices, np.int32)
+        bc = np.ascontiguousarray(bin_counts, np.int32)
+        tf = np.full((K, M), -1, np.int32)
+        tt = np.zeros((K, M), np.int64)
+        tv = np.zeros((K, M), np.float64)
+        tl = np.full((K, M), -1, np.int32)
+        tr = np.full((K, M), -1, np.int32)
+        nc = np.zeros(K, np.int32)
+        sg = np.zeros((K, M), np.float64)
+        check(lib().bsscl_mc_build_trees(
+            self.handle, ptr(fi), len(fi), int(max_leaves), int(max_depth),
+            int(min_samples_leaf), float(min_child_weight), ptr(bc), int(max_bins),
+            float(reg_lambda), float(gamma), float(learning_rate), ptr(tf), ptr(tt),
+            ptr(tv), ptr(tl), ptr(tr), ptr(nc), ptr(sg)))
+        return [(tf[k], tt[k], tv[k], tl[k], tr[k], int(nc[k]), sg[k]) for k in range(K)]
 
     def mc_loss(self):
         out = np.zeros(1, np.float64)

@@ -540,8 +540,9 @@ class HybridHistGBMNumbaV1_0_1:
     def _make_sampler(self, eng, rng, n_samples):
         """The native RandomState.shuffle stream for this fit's rounds: rows
         and features per round (est:2502-2517), from rng's current state.
-        Binary fits hand the draws to the device (the engine applies the
-        swaps); multiclass fits take the rows back on the host."""
+        Binary fits, and multiclass fits whose scores stay on the device,
+        hand the draws to the device (the engine applies the swaps); other
+        multiclass fits take the rows back on the host."""
         n_features = self.n_features_in_
         n_sub = max(1, int(n_samples * self.subsample))
         f_sub = max(1, int(n_features * self.colsample_bytree))
@@ -551,7 +552,9 @@ class HybridHistGBMNumbaV1_0_1:
                                n_sub if do_rows else n_samples, do_rows,
                                n_features, f_sub if do_feats else n_features,
                                do_feats, int(self.n_estimators),
-                               device_rows=not self._is_multiclass, device=eng.device)
+                               device_rows=(not self._is_multiclass
+                                            or self.n_classes_ <= _native.MC_DEVICE_MAX_CLASSES),
+                               device=eng.device)
 
     def _fit_locked(self, eng, X, y, X_val, y_val, sample_weight, sampler):
         """Binning and the boosting loop, with the engine's lock held."""
@@ -718,14 +721,16 @@ class HybridHistGBMNumbaV1_0_1:
             eng.mc_begin(y, K, sample_weight)
         for m in range(self.n_estimators):
             if on_device:
-                sample_idx, feat_idx = sampler.next()
-                eng.mc_round(sample_idx)
-                for k in range(K):
-                    tree = eng.mc_build_tree(k, feat_idx, self.max_leaves, self.max_depth,
-                                             self.min_samples_leaf, self.min_child_weight,
-                                             self.feature_bin_counts, self._max_bins,
-                                             self.reg_lambda, self.gamma,
-                                             self.learning_rate)
+                # The round's bagging draw and every class's gradients and
+                # hessians (est:2996-3019), the rows permuted on the device.
+                feat_idx = eng.mc_round_sampled(sampler)
+                # The K trees of the round in one engine call (est:3016-3029).
+                trees = eng.mc_build_trees(feat_idx, self.max_leaves, self.max_depth,
+                                           self.min_samples_leaf, self.min_child_weight,
+                                           self.feature_bin_counts, self._max_bins,
+                                           self.reg_lambda, self.gamma,
+                                           self.learning_rate)
+                for k, tree in enumerate(trees):
                     self.mc_trees[k].append(tree)
                     if F_val is not None:
                         F_val[:, k] += self.learning_rate * eng.predict_tree(1, n_val, tree)

@@ -308,12 +308,18 @@ struct bsscl_engine {
   // Multiclass run on matrix 0: scores, gradients and hessians [K][n], the
   // rows' class and weight, each class's largest |g| and h of the round.
   int32_t mc_K = 0;
-  int64_t mc_m = 0;  // the round's in-bag rows (rows64)
+  int64_t mc_m = 0;  // the round's in-bag rows: mc_rows32 (int32) or, when null, rows64
+  const int32_t *mc_rows32 = nullptr;
   DevBuf<double> mc_F, mc_G, mc_H, mc_w, mc_part;
   DevBuf<int32_t> mc_y;
   DevBuf<unsigned long long> mc_max;
   std::vector<double> mc_gm, mc_hm;  // fixed-point multipliers per class
   std::vector<double> mc_hmax;       // largest hessian per class
+  // A multiclass round's K trees as the device replayed them: K blocks of
+  // round_out_bytes(2 * max_leaves + 2), and their pinned readback.
+  DevBuf<char> mc_out_d;
+  char *mc_out_pin = nullptr;
+  size_t mc_out_pin_bytes = 0;
 
   // Tree workspace.
   // Compact row sets: a tree uses sets set_base and set_base + 1 (levels
@@ -1470,6 +1476,35 @@ int32_t table_bound(bsscl_engine *E, int32_t run) {
   return (int32_t)std::min<int64_t>(most, E->node_cap);
 }
 
+// Arguments of the device replay of the tree just enqueued, with the
+// engine's current scales.
+ReplayArgs replay_args(bsscl_engine *E, const TreeParams &tp, int32_t M) {
+  ReplayArgs ra;
+  ra.gamma = tp.gamma;
+  ra.reg_lambda = tp.lam;
+  ra.g_scale = E->g_scale;
+  ra.h_scale = E->h_scale;
+  ra.dev = DevScale{nullptr, 0, 0};
+  ra.max_leaves = tp.max_leaves;
+  ra.out_len = M;
+  // (Test hook BSSCL_TEST_REPLAY_GLOBAL: 1 reads the node table from HBM,
+  // 2 keeps the candidate slots in LDS instead of registers.)
+  const char *rg = std::getenv("BSSCL_TEST_REPLAY_GLOBAL");
+  ra.stage_limit = !rg ? (1 << 30) : rg[0] == '1' ? 0 : rg[0] == '2' ? 1023 : (1 << 30);
+  ra.node_cap = E->node_cap;
+  ra.max_depth = tp.max_depth;
+  ra.pad = 0;
+  return ra;
+}
+
+// Whether trees of `max_leaves` go through the device replay (the
+// candidate slots hold max_leaves + 2 entries).  Test hook:
+// BSSCL_TEST_HOST_REPLAY=1 forces the host path.
+bool device_replay_fits(int32_t max_leaves) {
+  const char *force_host = std::getenv("BSSCL_TEST_HOST_REPLAY");
+  return max_leaves + 2 <= kReplaySlots && !(force_host && force_host[0] == '1');
+}
+
 // Profiling counters of one built tree from its node table: histogram
 // rows x features and algorithmic bytes (the root and the smaller child of
 // every kept split above the last level), nodes expanded, trees.
@@ -1885,9 +1920,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   const int32_t F_sel = (int32_t)R.feats.size();
   const int nb = update_F_blocks(X.n);
   // More candidate slots than the device replay holds: host replay only.
-  // (Test hook: BSSCL_TEST_HOST_REPLAY=1 forces the host path.)
-  const char *force_host = std::getenv("BSSCL_TEST_HOST_REPLAY");
-  R.device_replay = a.max_leaves + 2 <= kReplaySlots && !(force_host && force_host[0] == '1');
+  R.device_replay = device_replay_fits(a.max_leaves);
   R.table_readback = false;
   // The tree's compact row sets: 2s and 2s + 1.
   E->set_base = 2 * s;
@@ -2044,20 +2077,7 @@ int enqueue_round(bsscl_engine *E, bsscl_sampler *sampler, const RoundArgs &a, i
   }
   if (rc == BSSCL_OK && R.device_replay) {
     RoundHeader *hdr = reinterpret_cast<RoundHeader *>(E->round_d[s].p);
-    ReplayArgs ra;
-    ra.gamma = a.gamma;
-    ra.reg_lambda = a.reg_lambda;
-    ra.g_scale = E->g_scale;
-    ra.h_scale = E->h_scale;
-    ra.max_leaves = a.max_leaves;
-    ra.out_len = R.M;
-    // (Test hook BSSCL_TEST_REPLAY_GLOBAL: 1 reads the node table from HBM,
-    // 2 keeps the candidate slots in LDS instead of registers.)
-    const char *rg = std::getenv("BSSCL_TEST_REPLAY_GLOBAL");
-    ra.stage_limit = !rg ? (1 << 30) : rg[0] == '1' ? 0 : rg[0] == '2' ? 1023 : (1 << 30);
-    ra.node_cap = E->node_cap;
-    ra.max_depth = a.max_depth;
-    ra.pad = 0;
+    ReplayArgs ra = replay_args(E, tp, R.M);
     // The tree's fixed point from the largest |g| and h of the current F
     // (every row's; the in-bag rows are among them), which the previous
     // F update or boost_begin left on the device.
@@ -2259,6 +2279,198 @@ int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
   return BSSCL_OK;
 }
 
+// Every class's gradients and hessians from the scores at the round's start
+// (est:2996, 3013-3019) and each class's fixed point from its largest |g|
+// and h, read back; the round's m in-bag rows are already on the device.
+int mc_gradients(bsscl_engine *E, int64_t m) {
+  const int64_t n = E->mat[0].n;
+  const int32_t K = E->mc_K;
+  HIPCHK(hipMemsetAsync(E->mc_max.p, 0, 2 * (size_t)K * 8, E->st));
+  HIPCHK(launch_mc_grad_hess(E->st, E->mc_F.p, E->mc_y.p, E->mc_w.p, n, K, E->mc_G.p, E->mc_H.p,
+                             E->mc_max.p));
+  unsigned long long mx[2 * kMcMaxK];
+  HIPCHK(hipMemcpyAsync(mx, E->mc_max.p, 2 * (size_t)K * 8, hipMemcpyDeviceToHost, E->st));
+  HIPCHK(hipStreamSynchronize(E->st));
+  E->mc_gm.assign((size_t)K, 0.0);
+  E->mc_hm.assign((size_t)K, 0.0);
+  E->mc_hmax.assign((size_t)K, 0.0);
+  for (int32_t k = 0; k < K; ++k) {
+    double gmax, hmax;
+    std::memcpy(&gmax, &mx[2 * k], 8);
+    std::memcpy(&hmax, &mx[2 * k + 1], 8);
+    if (!std::isfinite(gmax) || !std::isfinite(hmax))
+      return set_error(BSSCL_EINVAL, "mc_round: gradients are not finite");
+    // The scale load_grad_hess would take from the same arrays.
+    E->mc_gm[(size_t)k] = fixed_mul(gmax, m);
+    E->mc_hm[(size_t)k] = fixed_mul(hmax, m);
+    E->mc_hmax[(size_t)k] = hmax;
+  }
+  E->mc_m = m;
+  return BSSCL_OK;
+}
+
+// The in-bag rows of a sampler's round on the device, into mc_rows32: every
+// row in order without row bagging; with device rows, the round's steps of
+// the reference's shuffle (est:2506) applied to the cumulative permutation
+// and its first n_sub entries sorted ascending, as a boosting round makes
+// them; otherwise the sampler's rows, in the reference's order.  (A tree's
+// histograms are exact integer sums and its partitions stable, so the
+// order of its rows does not enter it.)
+int mc_rows_from_sampler(bsscl_engine *E, bsscl_sampler *sampler, const SamplerShape &sh,
+                         const SamplerRound &sr) {
+  const Matrix &X = E->mat[0];
+  const int64_t m = sh.n_sub;
+  if (m <= 0) return set_error(BSSCL_EINVAL, "mc_round_sampled: no samples");
+  hipStream_t st = E->st;
+  if (!sh.do_rows) {
+    CHK(E->round_rows[0].ensure((size_t)m));
+    HIPCHK(launch_iota(st, E->round_rows[0].p, m));
+    E->mc_rows32 = E->round_rows[0].p;
+    return BSSCL_OK;
+  }
+  if (!sh.device_rows) {
+    CHK(E->rows_in.ensure((size_t)m));
+    HIPCHK(hipMemcpyAsync(E->rows_in.p, sr.rows, (size_t)m * 4, hipMemcpyHostToDevice, st));
+    E->mc_rows32 = E->rows_in.p;
+    return BSSCL_OK;
+  }
+  if (sh.device != E->device)
+    return set_error(BSSCL_EINVAL, "mc_round_sampled: the sampler copies its draws to another GPU");
+  // The cumulative permutation: identity before the sampler's first round.
+  if (sr.round == 0) {
+    CHK(E->perm[0].ensure((size_t)X.n));
+    CHK(E->perm[1].ensure((size_t)X.n));
+    E->perm_cur = 0;
+    E->perm_sampler = sampler;
+    E->perm_next_round = 0;
+    HIPCHK(launch_iota(st, E->perm[0].p, X.n));
+  } else if (E->perm_sampler != sampler || E->perm_next_round != sr.round) {
+    return set_error(BSSCL_EINVAL,
+                     "mc_round_sampled: the sampler's earlier rounds did not run on this engine");
+  }
+  const int64_t n_pad = sort_rows_flag_bytes(X.n);
+  CHK(E->round_rows[0].ensure((size_t)m));
+  CHK(E->sort_tmp.ensure((size_t)(n_pad / 4096 + 1)));
+  if (E->row_flags_n != n_pad) {
+    CHK(E->row_flags.ensure((size_t)n_pad));
+    HIPCHK(hipMemsetAsync(E->row_flags.p, 0, (size_t)n_pad, st));
+    E->row_flags_n = n_pad;
+  }
+  FyWork w;
+  CHK(ensure_fy_work(E, X.n, w));
+  HIPCHK(hipStreamWaitEvent(st, sr.draws_copied, 0));  // the sampler copied the draws
+  const int cur = E->perm_cur;
+  // The sorted Fisher-Yates form flags the in-bag rows as it writes them.
+  const bool marked = w.keys != nullptr;
+  HIPCHK(launch_fisher_yates(st, sr.draws_dev, X.n, E->perm[cur].p, E->perm[cur ^ 1].p, w,
+                             marked ? E->row_flags.p : nullptr, m));
+  HIPCHK(launch_sort_rows(st, E->perm[cur ^ 1].p, m, E->row_flags.p, n_pad, E->sort_tmp.p,
+                          E->round_rows[0].p, marked));
+  E->perm_cur = cur ^ 1;
+  E->perm_next_round = sr.round + 1;
+  E->mc_rows32 = E->round_rows[0].p;
+  return BSSCL_OK;
+}
+
+// Multiclass class k's fixed point: the round's largest |g| and h of the
+// class (bsscl_mc_round).
+void mc_class_scales(bsscl_engine *E, int32_t k) {
+  E->g_scale = 1.0 / E->mc_gm[(size_t)k];
+  E->h_scale = 1.0 / E->mc_hm[(size_t)k];
+  E->h_bound = E->mc_hmax[(size_t)k];
+}
+
+// Class k's tree of the multiclass round on the host-driven path (its node
+// table comes back and the host replays est:641-820), then
+// F[:, k] += lr * tree(X) (est:3029).
+int mc_tree_host(bsscl_engine *E, int32_t k, const std::vector<int32_t> &feats,
+                 const std::vector<int32_t> &nb_sel, const TreeParams &tp, double lr,
+                 TreeOut &out) {
+  const Matrix &X = E->mat[0];
+  const int64_t n = X.n;
+  mc_class_scales(E, k);
+  HIPCHK(launch_quantize(E->st, E->mc_G.p + (size_t)k * n, E->mc_H.p + (size_t)k * n, n,
+                         E->mc_gm[(size_t)k], E->mc_hm[(size_t)k], E->ghq.p));
+  E->set_base = 0;
+  CHK(build_tree_core(E, E->mc_rows32, E->mc_m, feats, nb_sel, tp, out));
+  // (upload_tree takes the tree in the engine's columns.)
+  CHK(upload_tree(E, out.features, out.thresholds, out.values, out.left, out.right,
+                  *out.node_count, X.cols()));
+  HIPCHK(launch_mc_apply(E->st, X.codes.p, X.ld, n, E->tree_d.p, nullptr, lr,
+                         E->mc_F.p + (size_t)k * n));
+  tree_to_reference(X, out);
+  return BSSCL_OK;
+}
+
+// The round's K trees back to back with no host wait between them: per
+// class its quantized gradients, the tree, the tree's replay on the device
+// and F[:, k] += lr * tree(X) (k_mc_apply skips it when the replay failed);
+// then one readback of the K trees.  The classes' gradients all come from
+// the scores before the round (est:3013-3019), so the order of the K
+// updates does not enter any tree, and a class whose device replay failed
+// is built again on the host-driven path from its unchanged gradients.
+// `out(k)` gives class k's output arrays.
+template <typename OutFn>
+int mc_trees_device(bsscl_engine *E, const std::vector<int32_t> &feats,
+                    const std::vector<int32_t> &nb_sel, const TreeParams &tp, double lr,
+                    OutFn out) {
+  const Matrix &X = E->mat[0];
+  const int64_t n = X.n, m = E->mc_m;
+  const int32_t K = E->mc_K, M = 2 * tp.max_leaves + 2;
+  const int32_t F_sel = (int32_t)feats.size();
+  const size_t per = round_out_bytes(M);
+  // (mc_out_d is released only when no copy reads it: the previous call
+  // ended with a synchronisation.)
+  CHK(E->tree_d.ensure((size_t)M));
+  CHK(E->mc_out_d.ensure(per * (size_t)K));
+  CHK(ensure_host_pinned(E, E->mc_out_pin, E->mc_out_pin_bytes, per * (size_t)K));
+  E->set_base = 0;
+  CHK(prepare_tree_buffers(E, m, F_sel, std::max(1, tp.max_depth), tp.max_leaves));
+  for (int32_t k = 0; k < K; ++k) {
+    mc_class_scales(E, k);
+    HIPCHK(launch_quantize(E->st, E->mc_G.p + (size_t)k * n, E->mc_H.p + (size_t)k * n, n,
+                           E->mc_gm[(size_t)k], E->mc_hm[(size_t)k], E->ghq.p));
+    int32_t run = 0;
+    CHK(launch_tree(E, E->mc_rows32, m, feats, nb_sel, tp, &run));
+    char *base = E->mc_out_d.p + (size_t)k * per;
+    RoundHeader *hdr = reinterpret_cast<RoundHeader *>(base);
+    HIPCHK(launch_replay(E->st, E->nodes_d, E->plan_d, E->feat_d, replay_args(E, tp, M),
+                         round_arrays(base, M), E->tree_d.p, hdr));
+    HIPCHK(launch_mc_apply(E->st, X.codes.p, X.ld, n, E->tree_d.p, &hdr->node_count, lr,
+                           E->mc_F.p + (size_t)k * n));
+  }
+  HIPCHK(hipMemcpyAsync(E->mc_out_pin, E->mc_out_d.p, per * (size_t)K, hipMemcpyDeviceToHost,
+                        E->st));
+  CHK(sync(E));
+  for (int32_t k = 0; k < K; ++k) {
+    TreeOut o = out(k);
+    const char *base = E->mc_out_pin + (size_t)k * per;
+    RoundHeader h;
+    std::memcpy(&h, base, sizeof(h));
+    if (h.status == 0) {
+      if (E->prof && h.expanded >= 0) tree_stats_add(E, m, F_sel, h.hist_rows, h.expanded);
+      const TreeArrays ha = round_arrays(const_cast<char *>(base), M);
+      std::memcpy(o.features, ha.features, (size_t)M * 4);
+      std::memcpy(o.thresholds, ha.thresholds, (size_t)M * 8);
+      std::memcpy(o.values, ha.values, (size_t)M * 8);
+      std::memcpy(o.left, ha.left, (size_t)M * 4);
+      std::memcpy(o.right, ha.right, (size_t)M * 4);
+      std::memcpy(o.gains, ha.gains, (size_t)M * 8);
+      *o.node_count = h.node_count;
+      tree_to_reference(X, o);
+      continue;
+    }
+    if (h.status != 1 && h.status != 4)
+      return set_error(BSSCL_EINTERNAL, "tree builder: device replay failed (status " +
+                                            std::to_string(h.status) + ")");
+    // The node table was too small, or the replay could not finish: F[:, k]
+    // was left alone.
+    if (h.status == 1) E->node_cap_floor = std::max(h.needed, 2 * E->node_cap);
+    CHK(mc_tree_host(E, k, feats, nb_sel, tp, lr, o));
+  }
+  return BSSCL_OK;
+}
+
 }  // namespace
 }  // namespace bsscl
 
@@ -2387,6 +2599,12 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->fy_totals.release();
 
   E->row_flags.release();
+  for (DevBuf<double> *b : {&E->mc_F, &E->mc_G, &E->mc_H, &E->mc_w, &E->mc_part}) b->release();
+  E->mc_y.release();
+  E->mc_max.release();
+  E->mc_out_d.release();
+  if (E->mc_out_pin) (void)hipHostFree(E->mc_out_pin);
+  E->level_args_d.release();
   E->lvl_d.release();
   E->table_d.release();
   if (E->table_pin) (void)hipHostFree(E->table_pin);
@@ -2781,6 +2999,7 @@ int bsscl_boost_begin(bsscl_engine *E, const int64_t *y, int64_t n, double w0,
   E->w0 = w0;
   E->w1 = w1;
   E->boosting = true;
+  E->node_cap_floor = 0;  // a new fit starts from the node table its trees' shape asks for
   return BSSCL_OK;
 }
 
@@ -2875,6 +3094,11 @@ int bsscl_mc_begin(bsscl_engine *E, const int64_t *y, int64_t n, int32_t n_class
   if (n != E->mat[0].n) return set_error(BSSCL_EINVAL, "mc_begin: y length differs from matrix rows");
   if (n_classes < 2 || n_classes > kMcMaxK)
     return set_error(BSSCL_EINVAL, "mc_begin: between 2 and " + std::to_string(kMcMaxK) + " classes");
+  if (E->ahead >= 0) {  // a boosting round enqueued ahead shares the row buffers
+    const int p = E->ahead;
+    E->ahead = -1;
+    CHK(drain_rounds(E, p));
+  }
   std::vector<int32_t> yi((size_t)n);
   for (int64_t i = 0; i < n; ++i) {
     if (y[i] < 0 || y[i] >= n_classes) return set_error(BSSCL_EINVAL, "mc_begin: label out of range");
@@ -2898,6 +3122,8 @@ int bsscl_mc_begin(bsscl_engine *E, const int64_t *y, int64_t n, int32_t n_class
   HIPCHK(hipStreamSynchronize(E->st));
   E->mc_K = n_classes;
   E->mc_m = 0;
+  E->mc_rows32 = nullptr;
+  E->node_cap_floor = 0;  // a new fit starts from the node table its trees' shape asks for
   return BSSCL_OK;
 }
 
@@ -2911,32 +3137,35 @@ int bsscl_mc_round(bsscl_engine *E, const int64_t *sample_indices, int64_t n_sam
     if (sample_indices[k] < 0 || sample_indices[k] >= n)
       return set_error(BSSCL_EINVAL, "mc_round: sample index out of range");
   HIPCHK(hipSetDevice(E->device));
-  const int32_t K = E->mc_K;
+  E->mc_m = 0;
   CHK(E->rows64.ensure((size_t)n_samples));
   HIPCHK(hipMemcpyAsync(E->rows64.p, sample_indices, (size_t)n_samples * 8,
                         hipMemcpyHostToDevice, E->st));
-  HIPCHK(hipMemsetAsync(E->mc_max.p, 0, 2 * (size_t)K * 8, E->st));
-  HIPCHK(launch_mc_grad_hess(E->st, E->mc_F.p, E->mc_y.p, E->mc_w.p, n, K, E->mc_G.p, E->mc_H.p,
-                             E->mc_max.p));
-  unsigned long long mx[2 * kMcMaxK];
-  HIPCHK(hipMemcpyAsync(mx, E->mc_max.p, 2 * (size_t)K * 8, hipMemcpyDeviceToHost, E->st));
-  HIPCHK(hipStreamSynchronize(E->st));
-  E->mc_gm.assign((size_t)K, 0.0);
-  E->mc_hm.assign((size_t)K, 0.0);
-  E->mc_hmax.assign((size_t)K, 0.0);
-  for (int32_t k = 0; k < K; ++k) {
-    double gmax, hmax;
-    std::memcpy(&gmax, &mx[2 * k], 8);
-    std::memcpy(&hmax, &mx[2 * k + 1], 8);
-    if (!std::isfinite(gmax) || !std::isfinite(hmax))
-      return set_error(BSSCL_EINVAL, "mc_round: gradients are not finite");
-    // The scale load_grad_hess would take from the same arrays.
-    E->mc_gm[(size_t)k] = fixed_mul(gmax, n_samples);
-    E->mc_hm[(size_t)k] = fixed_mul(hmax, n_samples);
-    E->mc_hmax[(size_t)k] = hmax;
+  E->mc_rows32 = nullptr;
+  return mc_gradients(E, n_samples);
+}
+
+int bsscl_mc_round_sampled(bsscl_engine *E, bsscl_sampler *sampler, int32_t *feats_out) {
+  if (!E || !sampler) return set_error(BSSCL_EINVAL, "mc_round_sampled: null argument");
+  if (E->mc_K < 2) return set_error(BSSCL_EINVAL, "mc_round_sampled: no multiclass run");
+  CHK(check_matrix(E, 0));
+  const SamplerShape sh = sampler_shape(sampler);
+  if (sh.n != E->mat[0].n)
+    return set_error(BSSCL_EINVAL, "mc_round_sampled: sampler rows differ from matrix rows");
+  HIPCHK(hipSetDevice(E->device));
+  E->mc_m = 0;
+  SamplerRound sr;
+  void *token = nullptr;
+  CHK(sampler_take(sampler, &sr, &token));
+  int rc = mc_rows_from_sampler(E, sampler, sh, sr);
+  if (rc == BSSCL_OK && feats_out) std::memcpy(feats_out, sr.feats, (size_t)sh.f_sub * 4);
+  if (rc == BSSCL_OK) rc = mc_gradients(E, sh.n_sub);  // (ends with a synchronisation)
+  if (rc != BSSCL_OK) {
+    (void)hipStreamSynchronize(E->st);
+    E->mc_m = 0;
   }
-  E->mc_m = n_samples;
-  return BSSCL_OK;
+  sampler_give_back(sampler, token);
+  return rc;
 }
 
 int bsscl_mc_build_tree(bsscl_engine *E, int32_t k, const int32_t *feature_indices,
@@ -2951,29 +3180,48 @@ int bsscl_mc_build_tree(bsscl_engine *E, int32_t k, const int32_t *feature_indic
   if (k < 0 || k >= E->mc_K) return set_error(BSSCL_EINVAL, "mc_build_tree: class out of range");
   CHK(check_matrix(E, 0));
   (void)max_bins;
-  const Matrix &X = E->mat[0];
-  const int64_t n = X.n;
   TreeOut out{out_features, out_thresholds, out_values, out_left, out_right,
               out_node_count, out_split_gains};
   std::vector<int32_t> feats, nb_sel;
   HIPCHK(hipSetDevice(E->device));
   CHK(validate_tree_args(E, feature_indices, n_selected, max_leaves,
                          min_samples_leaf, bin_counts, out, feats, nb_sel));
-  const double gm = E->mc_gm[(size_t)k], hm = E->mc_hm[(size_t)k];
-  E->g_scale = 1.0 / gm;
-  E->h_scale = 1.0 / hm;
-  E->h_bound = E->mc_hmax[(size_t)k];
-  HIPCHK(launch_quantize(E->st, E->mc_G.p + (size_t)k * n, E->mc_H.p + (size_t)k * n, n, gm, hm,
-                         E->ghq.p));
-  TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight, reg_lambda, gamma};
-  E->set_base = 0;
-  CHK(build_tree_core(E, nullptr, E->mc_m, feats, nb_sel, tp, out));
-  // F[:, k] += lr * tree(X) (est:3029), with the tree in the engine's columns.
-  CHK(upload_tree(E, out.features, out.thresholds, out.values, out.left, out.right,
-                  *out.node_count, X.cols()));
-  HIPCHK(launch_mc_apply(E->st, X.codes.p, X.ld, n, E->tree_d.p, learning_rate,
-                         E->mc_F.p + (size_t)k * n));
-  tree_to_reference(X, out);
+  const TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight, reg_lambda,
+                      gamma};
+  return mc_tree_host(E, k, feats, nb_sel, tp, learning_rate, out);
+}
+
+int bsscl_mc_build_trees(bsscl_engine *E, const int32_t *feature_indices, int32_t n_selected,
+                         int32_t max_leaves, int32_t max_depth, int32_t min_samples_leaf,
+                         double min_child_weight, const int32_t *bin_counts, int32_t max_bins,
+                         double reg_lambda, double gamma, double learning_rate,
+                         int32_t *out_features, int64_t *out_thresholds, double *out_values,
+                         int32_t *out_left, int32_t *out_right, int32_t *out_node_count,
+                         double *out_split_gains) {
+  if (!E) return set_error(BSSCL_EINVAL, "mc_build_trees: null argument");
+  if (E->mc_K < 2 || E->mc_m <= 0) return set_error(BSSCL_EINVAL, "mc_build_trees: no round");
+  CHK(check_matrix(E, 0));
+  (void)max_bins;
+  TreeOut out0{out_features, out_thresholds, out_values, out_left, out_right,
+               out_node_count, out_split_gains};
+  std::vector<int32_t> feats, nb_sel;
+  HIPCHK(hipSetDevice(E->device));
+  CHK(validate_tree_args(E, feature_indices, n_selected, max_leaves,
+                         min_samples_leaf, bin_counts, out0, feats, nb_sel));
+  const TreeParams tp{max_leaves, max_depth, min_samples_leaf, min_child_weight, reg_lambda,
+                      gamma};
+  const size_t M = 2 * (size_t)max_leaves + 2;
+  auto out = [&](int32_t k) {
+    const size_t o = (size_t)k * M;
+    return TreeOut{out_features + o, out_thresholds + o, out_values + o, out_left + o,
+                   out_right + o, out_node_count + k, out_split_gains + o};
+  };
+  if (device_replay_fits(max_leaves))
+    return mc_trees_device(E, feats, nb_sel, tp, learning_rate, out);
+  for (int32_t k = 0; k < E->mc_K; ++k) {
+    TreeOut o = out(k);
+    CHK(mc_tree_host(E, k, feats, nb_sel, tp, learning_rate, o));
+  }
   return BSSCL_OK;
 }
 

@@ -439,8 +439,11 @@ constexpr int kMcMaxK = 16;
 hipError_t launch_mc_grad_hess(hipStream_t st, const double *F, const int32_t *y, const double *w,
                                int64_t n, int32_t K, double *G, double *H,
                                unsigned long long *mx);
+// F[:, k] += lr * tree(X); nothing when node_count_d is given and holds 0
+// (a device replay that failed).
 hipError_t launch_mc_apply(hipStream_t st, const uint8_t *codes, int64_t ld, int64_t n,
-                           const TreeNodeDev *tree, double lr, double *Fk);
+                           const TreeNodeDev *tree, const int32_t *node_count_d, double lr,
+                           double *Fk);
 int64_t mc_loss_blocks(int64_t n);
 hipError_t launch_mc_loss(hipStream_t st, const double *F, const int32_t *y, int64_t n,
                           int32_t K, double *partials);

@@ -4463,9 +4463,11 @@ __global__ __launch_bounds__(256) void k_mc_grad_hess(
 // F[i] += lr * tree(x_i) for one class's scores (est:3029).
 __global__ __launch_bounds__(256) void k_mc_apply(const uint8_t *__restrict__ codes, int64_t ld,
                                                   int64_t n, const TreeNodeDev *__restrict__ tree,
+                                                  const int32_t *__restrict__ node_count_d,
                                                   double lr, double *__restrict__ Fk) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
+  // A device replay that failed left node_count at 0: F stays as it is.
+  if (i >= n || (node_count_d && *node_count_d <= 0)) return;
   Fk[i] = __dadd_rn(Fk[i], __dmul_rn(lr, tree[traverse(tree, codes, ld, i)].value));
 }
 
@@ -4517,10 +4519,11 @@ hipError_t launch_mc_grad_hess(hipStream_t st, const double *F, const int32_t *y
 }
 
 hipError_t launch_mc_apply(hipStream_t st, const uint8_t *codes, int64_t ld, int64_t n,
-                           const TreeNodeDev *tree, double lr, double *Fk) {
+                           const TreeNodeDev *tree, const int32_t *node_count_d, double lr,
+                           double *Fk) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_mc_apply, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, codes, ld,
-                     n, tree, lr, Fk);
+                     n, tree, node_count_d, lr, Fk);
   return hipGetLastError();
 }
 

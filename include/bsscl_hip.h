@@ -203,9 +203,20 @@ int bsscl_boost_grad_hess_max(bsscl_engine *eng, double *out);
  *                  2 <= n_classes <= 16
  *   mc_round       the round's in-bag rows (int64[n_samples], shared by its
  *                  K trees); computes every class's gradients and hessians
+ *   mc_round_sampled  as mc_round with the sampler's next round (est:2502-2517
+ *                  at est:2996): with BSSCL_SAMPLER_DEVICE_ROWS the rows are
+ *                  permuted on the GPU as bsscl_boost_round does; the round's
+ *                  ascending feature subset goes to feats_out (int32[f_sub],
+ *                  may be NULL)
  *   mc_build_tree  class k's tree from the round's rows and the features
  *                  (arguments and outputs as bsscl_build_tree), then adds
  *                  learning_rate * tree to class k's scores
+ *   mc_build_trees the round's K trees at once, classes 0..K-1, with the
+ *                  arguments of mc_build_tree but no k: the same trees and
+ *                  score updates, enqueued back to back and read back once.
+ *                  Outputs hold K blocks of M = 2 * max_leaves + 2 entries
+ *                  (class k's tree at k * M) and out_node_count K entries.
+ *                  Replaces the loop over k of est:3016-3029
  *   mc_loss        -mean log(clip(softmax(F)[y], 1e-15, 1 - 1e-15))
  *   mc_get_scores  F as float64[n_classes * n], class by class (row i of
  *                  class k at k * n + i)
@@ -216,6 +227,7 @@ int bsscl_boost_grad_hess_max(bsscl_engine *eng, double *out);
 int bsscl_mc_begin(bsscl_engine *eng, const int64_t *y, int64_t n, int32_t n_classes,
                    const double *sample_weight);
 int bsscl_mc_round(bsscl_engine *eng, const int64_t *sample_indices, int64_t n_samples);
+int bsscl_mc_round_sampled(bsscl_engine *eng, bsscl_sampler *sampler, int32_t *feats_out);
 int bsscl_mc_build_tree(bsscl_engine *eng, int32_t k, const int32_t *feature_indices,
                         int32_t n_selected, int32_t max_leaves, int32_t max_depth,
                         int32_t min_samples_leaf, double min_child_weight,
@@ -223,6 +235,13 @@ int bsscl_mc_build_tree(bsscl_engine *eng, int32_t k, const int32_t *feature_ind
                         double gamma, double learning_rate, int32_t *out_features,
                         int64_t *out_thresholds, double *out_values, int32_t *out_left,
                         int32_t *out_right, int32_t *out_node_count, double *out_split_gains);
+int bsscl_mc_build_trees(bsscl_engine *eng, const int32_t *feature_indices, int32_t n_selected,
+                         int32_t max_leaves, int32_t max_depth, int32_t min_samples_leaf,
+                         double min_child_weight, const int32_t *bin_counts, int32_t max_bins,
+                         double reg_lambda, double gamma, double learning_rate,
+                         int32_t *out_features, int64_t *out_thresholds, double *out_values,
+                         int32_t *out_left, int32_t *out_right, int32_t *out_node_count,
+                         double *out_split_gains);
 int bsscl_mc_loss(bsscl_engine *eng, double *out_loss);
 int bsscl_mc_get_scores(bsscl_engine *eng, double *out);
 int bsscl_mc_get_grad_hess(bsscl_engine *eng, double *grad_out, double *hess_out);

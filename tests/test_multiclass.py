@@ -292,3 +292,63 @@ def test_multiclass_device_grad_hess_equal_numpy(engine, K):
         assert same >= 0.75, (name, same)
         if K >= 8:
             assert same >= same_seq + 0.05, (name, same, same_seq)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K", [3, 9])
+def test_multiclass_round_paths_agree(engine, monkeypatch, K):
+    """A round's K trees in one call (mc_build_trees: device replay, one
+    readback) against the same trees one class at a time (mc_build_tree:
+    host replay per tree), against the rows in the reference's order from a
+    host-rows sampler instead of the device-permuted, sorted ones, and
+    against the batched call on its fallbacks: the host replay (forced), a
+    node table too small for the first round's trees (every class rebuilt
+    on the host-driven path, then grown) and the replay reading the node
+    table from HBM.  Trees, split gains, losses and scores must be
+    identical."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1, _native
+    X, y = _mc_data(9000, 9, K, seed=60 + K, nan_frac=0.05)
+    params = dict(n_estimators=3, max_depth=5, n_bins=255, random_state=7,
+                  class_weight="balanced_sqrt")
+    hooks = ("BSSCL_TEST_HOST_REPLAY", "BSSCL_TEST_NODE_CAP", "BSSCL_TEST_REPLAY_GLOBAL")
+
+    def per_class(self, feature_indices, max_leaves, *args):
+        return [self.mc_build_tree(k, feature_indices, max_leaves, *args)
+                for k in range(self._mc[1])]
+
+    sampler_init = _native.Sampler.__init__
+
+    def host_rows_sampler(self, *args, **kw):
+        sampler_init(self, *args, **dict(kw, device_rows=False))
+
+    fits = {}
+    for mode, env in [("batched", {}), ("per_class", {}), ("host_rows", {}),
+                      ("host", {"BSSCL_TEST_HOST_REPLAY": "1"}),
+                      ("regrow", {"BSSCL_TEST_NODE_CAP": "9"}),
+                      ("global", {"BSSCL_TEST_REPLAY_GLOBAL": "1"})]:
+        print(f"[case] multiclass round path {mode} K={K}", flush=True)
+        for k in hooks:
+            monkeypatch.delenv(k, raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        with monkeypatch.context() as mp:
+            if mode == "per_class":
+                mp.setattr(_native.Engine, "mc_build_trees", per_class)
+            if mode == "host_rows":
+                mp.setattr(_native.Sampler, "__init__", host_rows_sampler)
+            est = HybridHistGBMNumbaV1_0_1(verbose=False, **params).fit(X, y)
+        fits[mode] = (est, est.predict_proba(X))
+    for k in hooks:
+        monkeypatch.delenv(k, raising=False)
+    ref, ref_p = fits["batched"]
+    for mode in ("per_class", "host_rows", "host", "regrow", "global"):
+        got, got_p = fits[mode]
+        assert got.train_loss_history_ == ref.train_loss_history_, mode
+        for k in range(K):
+            assert len(got.mc_trees[k]) == len(ref.mc_trees[k]) == params["n_estimators"]
+            for a, b in zip(ref.mc_trees[k], got.mc_trees[k]):
+                nc = a[5]
+                assert nc == b[5], (mode, k)
+                for i in (0, 1, 2, 3, 4, 6):
+                    np.testing.assert_array_equal(a[i][:nc], b[i][:nc], err_msg=f"{mode} {k}")
+        np.testing.assert_array_equal(got_p, ref_p, err_msg=mode)
