@@ -7,9 +7,11 @@
   trees.
 * stress_10m (10,000,000 x 50, 10 columns 70% NaN, depth 8): bin edges and
   codes of all 10M rows against the oracle's; the first ten rounds of the
-  workload's fit; one depth-8 tree from 5M rows x 35 features; and the
-  500-tree fit scored on a fresh 10M-row batch, checked on all 10M rows
-  (codes bit-exact, raw scores within 1e-12, predict_proba within 1e-6).
+  workload's fit; one depth-8 tree from 5M rows x 35 features; rounds 250
+  and 499 of the workload's 500-tree fit, tree by tree, each from the
+  engine's own scores before the round; and the 500-tree fit scored on a
+  fresh 10M-row batch, checked on all 10M rows (codes bit-exact, raw scores
+  within 1e-12, predict_proba within 1e-6).
 
 Every fit compares each round in lockstep and end to end with the oracle,
 following certified gain ties (tests/fitcmp.py), then every round's loss
@@ -108,6 +110,66 @@ def test_stress_10m_tree(engine):
     out = treecmp.follow(got, codes, g, h, *args)
     print(f"[result] stress_10m tree: {got[5]} nodes, ties {out.ties}", flush=True)
     assert got[5] > 100
+
+
+def test_stress_10m_late_rounds(engine, monkeypatch):
+    """Rounds 250 and 499 of the workload's 500-tree fit, tree by tree.  The
+    engine's scores before each round come back from the device
+    (boost_get_F, rounds not pipelined); the oracle's expressions give the
+    round's gradients (est:2861, 2873-2874) and its builder the tree, from
+    that round's rows and features as a host-rows sampler started from the
+    fit's RandomState state draws them (the sampler equals rng.shuffle:
+    tests/test_sampler.py).  The estimator's tree must equal the oracle's,
+    following certified ties, and the loss it recorded after the previous
+    round must equal the loss of those scores."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1, _native
+    X, y, params = _workload("stress_10m")
+    picks = (250, 499)
+    print(f"[case] stress_10m rounds {picks} of the {params['n_estimators']}-tree fit",
+          flush=True)
+    made = []
+    init = _native.Sampler.__init__
+
+    def record(self, *args, **kw):
+        made.append((args, kw))
+        init(self, *args, **kw)
+
+    monkeypatch.setattr(_native.Sampler, "__init__", record)
+    F_at = {}
+    est = HybridHistGBMNumbaV1_0_1(**params)
+    est._pipeline_rounds = False
+    est._round_hook = lambda m, eng: (F_at.__setitem__(m, eng.boost_get_F(len(y)))
+                                      if m in picks else None)
+    est.fit(X, y)
+    monkeypatch.setattr(_native.Sampler, "__init__", init)
+    assert len(est.trees) == params["n_estimators"] and sorted(F_at) == list(picks)
+    assert len(made) == 1
+    args, kw = made[0]
+    sampler = _native.Sampler(*args, **dict(kw, device_rows=False))
+    draws = {}
+    for m in range(max(picks) + 1):
+        rows, feats = sampler.next()
+        if m in picks:
+            draws[m] = (rows.astype(np.int64), feats.copy())
+    sampler.close()
+    X_bin = om.bin_features(X, est.bin_edges, est.feature_bin_counts, est._nan_bin_id, "hybrid")
+    ref = om.OracleGBM(**{k: v for k, v in params.items() if k != "verbose"})
+    ref.n_classes_ = 2
+    w = ref._class_weights(y)
+    g = np.empty(len(y))
+    h = np.empty(len(y))
+    for m in picks:
+        F = F_at[m]
+        loss = om.binary_logloss(y, F)
+        assert abs(est.train_loss_history_[m - 1] - loss) <= 1e-9 * abs(loss), m
+        om.binary_grad_hess(F, y, w, g, h)
+        rows, feats = draws[m]
+        out = treecmp.follow(est.trees[m], X_bin, g, h, rows, feats, est.max_leaves,
+                             est.max_depth, est.min_samples_leaf, est.min_child_weight,
+                             np.asarray(est.feature_bin_counts), est._max_bins, est.reg_lambda,
+                             est.gamma)
+        print(f"[result] stress_10m round {m}: {est.trees[m][5]} nodes from {len(rows)} rows x "
+              f"{len(feats)} features, ties {out.n_ties}; loss before it {loss:.9f}", flush=True)
 
 
 def test_stress_10m_inference(engine):
