@@ -33,6 +33,9 @@ __all__ = ["HybridHistGBMNumbaV1_0_1"]
 
 _ENGINES: dict = {}
 _ENGINES_LOCK = threading.Lock()
+# Rows per device pass of the batch-parallel predictions (their codes and
+# scores on the device: about 1 GB at 50 features).
+_BATCH_ROWS = 1 << 24
 
 
 def _engine(device: int) -> _native.Engine:
@@ -880,6 +883,35 @@ class HybridHistGBMNumbaV1_0_1:
         if self._is_multiclass:
             return self.classes_[np.argmax(proba, axis=1)]
         return self.classes_[(proba[:, 1] > 0.5).astype(int)]
+
+    def score(self, X, y):
+        """Mean accuracy (est:3577-3578)."""
+        return np.mean(self.predict(X) == y)
+
+    # ------------------------------------------------------------------
+    # est:3842-3916.  The reference maps batches of batch_size rows over a
+    # process pool.  Here every batch goes through the device in this
+    # process: a row's prediction does not depend on its batch, so the
+    # result is the one the pool would return, and worker processes would
+    # each have to start their own HIP runtime.  n_workers is accepted for
+    # the same signature.
+    # ------------------------------------------------------------------
+    def predict_batch_parallel(self, X, n_workers=4, batch_size=10000):
+        return self._batched(self.predict, X, batch_size, np.concatenate)
+
+    def predict_proba_batch_parallel(self, X, n_workers=4, batch_size=10000):
+        return self._batched(self.predict_proba, X, batch_size, np.vstack)
+
+    @staticmethod
+    def _batched(fn, X, batch_size, join):
+        n = len(X)
+        if n <= batch_size:
+            return fn(X)
+        # The whole input in one device pass where it fits comfortably;
+        # otherwise slices of many batches each, joined as the reference
+        # joins its batches.
+        step = max(int(batch_size), _BATCH_ROWS // max(int(batch_size), 1) * int(batch_size))
+        return join([fn(X[i:i + step]) for i in range(0, n, step)])
 
     # ------------------------------------------------------------------
     # est:3773-3801

@@ -162,3 +162,22 @@ def test_threads_fit_and_predict_concurrently():
                 np.testing.assert_array_equal(a[1][:nc], b[1][:nc])
             np.testing.assert_array_equal(p, want[i])
             np.testing.assert_array_equal(p_other, want[1 - i])
+
+
+def test_score_and_batch_parallel_predictions(engine, bin_data, monkeypatch):
+    """score is the mean accuracy (est:3577-3578); the batch-parallel
+    predictions (est:3842-3916) equal predict and predict_proba, one batch
+    or many, also when the device passes are cut into several slices."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    from bsscl_gbm import estimator as est_mod
+    X, y = bin_data
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=20, max_depth=4, random_state=0,
+                                 verbose=False).fit(X, y)
+    pred, proba = m.predict(X), m.predict_proba(X)
+    assert m.score(X, y) == np.mean(pred == y)
+    for bs in (len(X), 100, 77):
+        np.testing.assert_array_equal(m.predict_batch_parallel(X, n_workers=2, batch_size=bs), pred)
+        np.testing.assert_array_equal(m.predict_proba_batch_parallel(X, batch_size=bs), proba)
+    monkeypatch.setattr(est_mod, "_BATCH_ROWS", 150)  # slices of 140 rows
+    np.testing.assert_array_equal(m.predict_batch_parallel(X, batch_size=70), pred)
+    np.testing.assert_array_equal(m.predict_proba_batch_parallel(X, batch_size=70), proba)
