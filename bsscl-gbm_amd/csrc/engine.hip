@@ -27,15 +27,19 @@
 // the host once per tree for the replay.
 #include <hip/hip_runtime.h>
 
+#include <unistd.h>
+
 #include <algorithm>
 #include <array>
 #include <atomic>
 #include <chrono>
 #include <cmath>
+#include <condition_variable>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "bsscl_internal.h"
@@ -410,6 +414,11 @@ struct bsscl_engine {
   DevBuf<int32_t> offsets_d;
   DevBuf<double> partials_d, loss_d, out_d;
   PinnedArena pin;
+  // Large host transfers go through these pinned chunks (host_upload,
+  // host_download), and binning of a host matrix through xchunk.
+  char *xfer_pin[3] = {nullptr, nullptr, nullptr};
+  hipEvent_t xfer_ev[3] = {nullptr, nullptr, nullptr};
+  DevBuf<unsigned char> xchunk;
 
   // Feature matrix staged by bsscl_stage_features (row-major, as given) and
   // its columns sorted by bsscl_sort_columns (keys [F][col_ld]).
@@ -588,6 +597,165 @@ int upload(bsscl_engine *E, DevBuf<T> &dst, const T *src, size_t count) {
   } else {
     HIPCHK(hipMemcpyAsync(dst.p, src, count * sizeof(T), hipMemcpyHostToDevice, E->st));
     HIPCHK(hipStreamSynchronize(E->st));
+  }
+  return BSSCL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Large host <-> device transfers.  A copy from pageable memory makes HIP
+// stage it through its own pinned buffers, one after the other (about
+// 19 GB/s for a 112 MB matrix).  Here host threads copy chunks into three
+// pinned buffers while the DMA engine moves the chunk before, so both run
+// at once.
+// ---------------------------------------------------------------------------
+
+// A few host threads that split a memcpy with the caller.  One pool per
+// process: a child made by fork() has none of its parent's threads, so it
+// starts its own.  The threads live until the process ends.
+class CopyPool {
+ public:
+  static CopyPool &get() {
+    static std::mutex mu;
+    static CopyPool *pool = nullptr;
+    static pid_t owner = 0;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!pool || owner != getpid()) {  // (the parent's pool is left as it is)
+      pool = new CopyPool();
+      owner = getpid();
+    }
+    return *pool;
+  }
+
+  void copy(void *dst, const void *src, size_t bytes) {
+    if (bytes < (1u << 20) || threads_.empty()) {
+      std::memcpy(dst, src, bytes);
+      return;
+    }
+    std::lock_guard<std::mutex> call(call_mu_);  // one copy at a time
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      dst_ = static_cast<char *>(dst);
+      src_ = static_cast<const char *>(src);
+      bytes_ = bytes;
+      pending_ = (int)threads_.size();
+      ++gen_;
+    }
+    cv_.notify_all();
+    part(0, dst_, src_, bytes);
+    std::unique_lock<std::mutex> lk(mu_);
+    done_.wait(lk, [&] { return pending_ == 0; });
+  }
+
+ private:
+  CopyPool() {
+    const unsigned hw = std::thread::hardware_concurrency();
+    const int n = (int)std::min<unsigned>(3, hw > 2 ? hw / 2 - 1 : 0);
+    for (int t = 0; t < n; ++t) {
+      try {
+        threads_.emplace_back([this, t] { run(t + 1); });
+      } catch (...) {
+        break;  // fewer threads
+      }
+    }
+    for (auto &th : threads_) th.detach();
+  }
+
+  // Part i of parts() pieces, cut at 64-byte boundaries.
+  void part(int i, char *d, const char *s, size_t b) const {
+    const size_t parts = threads_.size() + 1;
+    const size_t per = ((b + parts - 1) / parts + 63) & ~size_t(63);
+    const size_t off = per * (size_t)i;
+    if (off < b) std::memcpy(d + off, s + off, std::min(per, b - off));
+  }
+
+  void run(int i) {
+    uint64_t seen = 0;
+    std::unique_lock<std::mutex> lk(mu_);
+    for (;;) {
+      cv_.wait(lk, [&] { return gen_ != seen; });
+      seen = gen_;
+      char *d = dst_;
+      const char *s = src_;
+      const size_t b = bytes_;
+      lk.unlock();
+      part(i, d, s, b);
+      lk.lock();
+      if (--pending_ == 0) done_.notify_one();
+    }
+  }
+
+  std::mutex call_mu_, mu_;
+  std::condition_variable cv_, done_;
+  std::vector<std::thread> threads_;
+  uint64_t gen_ = 0;
+  int pending_ = 0;
+  char *dst_ = nullptr;
+  const char *src_ = nullptr;
+  size_t bytes_ = 0;
+};
+
+constexpr size_t kXferChunk = 8u << 20;
+
+int ensure_xfer(bsscl_engine *E) {
+  for (int b = 0; b < 3; ++b) {
+    if (!E->xfer_pin[b])
+      HIPCHK(hipHostMalloc(reinterpret_cast<void **>(&E->xfer_pin[b]), kXferChunk,
+                           hipHostMallocDefault));
+    if (!E->xfer_ev[b]) HIPCHK(hipEventCreateWithFlags(&E->xfer_ev[b], hipEventDisableTiming));
+  }
+  return BSSCL_OK;
+}
+
+// dst (device) = src (host, pageable) on E->st; returns once the copy is
+// complete.
+int host_upload(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
+  if (bytes < 2 * kXferChunk) {
+    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, E->st));
+    HIPCHK(hipStreamSynchronize(E->st));
+    return BSSCL_OK;
+  }
+  CHK(ensure_xfer(E));
+  CopyPool &pool = CopyPool::get();
+  size_t c = 0;
+  for (size_t off = 0; off < bytes; off += kXferChunk, ++c) {
+    const int b = (int)(c % 3);
+    const size_t len = std::min(kXferChunk, bytes - off);
+    if (c >= 3) HIPCHK(hipEventSynchronize(E->xfer_ev[b]));  // its previous chunk has gone
+    pool.copy(E->xfer_pin[b], static_cast<const char *>(src) + off, len);
+    HIPCHK(hipMemcpyAsync(static_cast<char *>(dst) + off, E->xfer_pin[b], len,
+                          hipMemcpyHostToDevice, E->st));
+    HIPCHK(hipEventRecord(E->xfer_ev[b], E->st));
+  }
+  HIPCHK(hipStreamSynchronize(E->st));
+  return BSSCL_OK;
+}
+
+// dst (host, pageable) = src (device) after the work already on E->st.
+int host_download(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
+  if (bytes < 2 * kXferChunk) {
+    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, E->st));
+    HIPCHK(hipStreamSynchronize(E->st));
+    return BSSCL_OK;
+  }
+  CHK(ensure_xfer(E));
+  CopyPool &pool = CopyPool::get();
+  const size_t n_chunks = (bytes + kXferChunk - 1) / kXferChunk;
+  auto enqueue = [&](size_t c) -> int {
+    const int b = (int)(c % 3);
+    const size_t off = c * kXferChunk;
+    HIPCHK(hipMemcpyAsync(E->xfer_pin[b], static_cast<const char *>(src) + off,
+                          std::min(kXferChunk, bytes - off), hipMemcpyDeviceToHost, E->st));
+    HIPCHK(hipEventRecord(E->xfer_ev[b], E->st));
+    return BSSCL_OK;
+  };
+  // Two chunks in flight ahead of the one being copied out.
+  for (size_t c = 0; c < std::min<size_t>(2, n_chunks); ++c) CHK(enqueue(c));
+  for (size_t c = 0; c < n_chunks; ++c) {
+    if (c + 2 < n_chunks) CHK(enqueue(c + 2));
+    const int b = (int)(c % 3);
+    HIPCHK(hipEventSynchronize(E->xfer_ev[b]));
+    const size_t off = c * kXferChunk;
+    pool.copy(static_cast<char *>(dst) + off, E->xfer_pin[b], std::min(kXferChunk, bytes - off));
   }
   return BSSCL_OK;
 }
@@ -2639,6 +2807,11 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->loss_d.release();
   E->out_d.release();
   E->pin.release();
+  for (int b = 0; b < 3; ++b) {
+    if (E->xfer_pin[b]) (void)hipHostFree(E->xfer_pin[b]);
+    if (E->xfer_ev[b]) (void)hipEventDestroy(E->xfer_ev[b]);
+  }
+  E->xchunk.release();
   E->xstage.release();
   E->col_keys.release();
   for (hipEvent_t ev : E->ev_pool) (void)hipEventDestroy(ev);
@@ -2696,23 +2869,25 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
     // Stream X through the device in row chunks of at most 256 MB.
     int64_t chunk = std::max<int64_t>(64, (int64_t)((256u << 20) / (esz * (size_t)F)) / 64 * 64);
     chunk = std::min<int64_t>(chunk, round_up(n, 64));
-    DevBuf<unsigned char> xd;
+    // (The chunk buffer stays allocated for the next host matrix.)
+    DevBuf<unsigned char> &xd = E->xchunk;
     int rc = xd.ensure((size_t)chunk * F * esz);
     if (rc != BSSCL_OK) { ed.release(); nb.release(); nid.release(); return rc; }
     for (int64_t r0 = 0; r0 < n; r0 += chunk) {
       const int64_t rows = std::min(chunk, n - r0);
-      hipError_t e = hipMemcpyAsync(xd.p, (const unsigned char *)X + (size_t)r0 * F * esz,
-                                    (size_t)rows * F * esz, hipMemcpyHostToDevice, E->st);
+      rc = host_upload(E, xd.p, (const unsigned char *)X + (size_t)r0 * F * esz,
+                       (size_t)rows * F * esz);
+      hipError_t e = rc == BSSCL_OK ? hipSuccess : hipErrorUnknown;
       if (e == hipSuccess)
         e = launch_bin(E->st, xd.p, x_is_f64, rows, F, ed.p, edge_stride, nb.p, nid.p,
                        has_any_nan, M.codes.p + r0, M.ld, tiers);
       if (e == hipSuccess) e = hipStreamSynchronize(E->st);
       if (e != hipSuccess) {
-        xd.release(); ed.release(); nb.release(); nid.release();
+        ed.release(); nb.release(); nid.release();
+        if (rc != BSSCL_OK) return rc;
         return set_error(BSSCL_EDEVICE, std::string("binning: ") + hipGetErrorString(e));
       }
     }
-    xd.release();
     ed.release();
     nb.release();
     nid.release();
@@ -2734,8 +2909,7 @@ int bsscl_stage_features(bsscl_engine *E, const void *X, int32_t x_is_f64, int64
   const size_t bytes = (size_t)n * F * (x_is_f64 ? 8 : 4);
   CHK(E->xstage.ensure(bytes));
   E->xs_n = 0;
-  HIPCHK(hipMemcpyAsync(E->xstage.p, X, bytes, hipMemcpyHostToDevice, E->st));
-  HIPCHK(hipStreamSynchronize(E->st));
+  CHK(host_upload(E, E->xstage.p, X, bytes));
   E->xs_n = n;
   E->xs_F = F;
   E->xs_f64 = x_is_f64 ? 1 : 0;
@@ -2885,9 +3059,14 @@ int bsscl_load_codes(bsscl_engine *E, int32_t slot, const void *codes,
   const size_t bytes = (size_t)n * F * (codes_u16 ? 2 : 1);
   DevBuf<unsigned char> tmp;
   CHK(tmp.ensure(bytes));
-  hipError_t e = hipMemcpyAsync(tmp.p, codes, bytes, hipMemcpyHostToDevice, E->st);
-  if (e == hipSuccess)
-    e = launch_load_codes(E->st, tmp.p, codes_u16, n, F, E->mat[slot].codes.p, E->mat[slot].ld,
+  {
+    const int rc = host_upload(E, tmp.p, codes, bytes);
+    if (rc != BSSCL_OK) {
+      tmp.release();
+      return rc;
+    }
+  }
+  hipError_t e = launch_load_codes(E->st, tmp.p, codes_u16, n, F, E->mat[slot].codes.p, E->mat[slot].ld,
                           tiers);
   if (e == hipSuccess) e = hipStreamSynchronize(E->st);
   tmp.release();
@@ -3357,7 +3536,7 @@ int bsscl_predict(bsscl_engine *E, int32_t slot, const int16_t *features,
   HIPCHK(launch_predict(E->st, M.codes.p, M.ld, M.n, M.cols(), E->tree_d.p, E->offsets_d.p,
                         n_trees, staged ? E->offsets_d.p + n_trees + 1 : nullptr, n_chunks,
                         learning_rate, E->out_d.p, start, stop));
-  HIPCHK(hipMemcpyAsync(out_F, E->out_d.p, (size_t)M.n * 8, hipMemcpyDeviceToHost, E->st));
+  CHK(host_download(E, out_F, E->out_d.p, (size_t)M.n * 8));
   CHK(sync(E));
   return BSSCL_OK;
 }
@@ -3468,7 +3647,7 @@ int bsscl_predict_tree(bsscl_engine *E, int32_t slot, const int32_t *features,
   CHK(upload_tree(E, f.data(), t.data(), values, left, right, node_count, M.cols()));
   CHK(E->out_d.ensure((size_t)M.n));
   HIPCHK(launch_predict_tree(E->st, M.codes.p, M.ld, M.n, E->tree_d.p, node_count, E->out_d.p));
-  HIPCHK(hipMemcpyAsync(out, E->out_d.p, (size_t)M.n * 8, hipMemcpyDeviceToHost, E->st));
+  CHK(host_download(E, out, E->out_d.p, (size_t)M.n * 8));
   CHK(sync(E));
   return BSSCL_OK;
 }
