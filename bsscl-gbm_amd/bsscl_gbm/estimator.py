@@ -97,6 +97,35 @@ def _sigmoid(F):
     return 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
 
 
+# Rows from which predict_proba's elementwise host work runs on threads.
+_PROBA_THREAD_ROWS = 1 << 19
+
+
+def _binary_proba_columns(F):
+    """np.column_stack([1 - p, p]) with p = _sigmoid(F) (est:3335-3336).
+    Large inputs go in row blocks over a few threads: NumPy's ufuncs release
+    the GIL, and every element is computed by the same NumPy loop, so the
+    values are bit-identical to the one-piece expression."""
+    n = len(F)
+    out = np.empty((n, 2), dtype=np.float64)
+
+    def block(a, b):
+        p = _sigmoid(F[a:b])
+        out[a:b, 0] = 1 - p
+        out[a:b, 1] = p
+
+    workers = min(8, os.cpu_count() or 1)
+    if n < _PROBA_THREAD_ROWS or workers < 2:
+        block(0, n)
+        return out
+    from concurrent.futures import ThreadPoolExecutor
+    step = -(-n // (4 * workers))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        for f in [ex.submit(block, a, min(a + step, n)) for a in range(0, n, step)]:
+            f.result()
+    return out
+
+
 def _percentile_ranks(m, q100, dtype):
     """Ranks np.percentile(col, q100) reads from a NaN-free column of m
     values of `dtype`, and its interpolation weights (NumPy 2.x 'linear'
@@ -875,8 +904,7 @@ class HybridHistGBMNumbaV1_0_1:
         F = self._raw_score(X)
         if self._is_multiclass:
             return self._softmax(F)
-        proba = _sigmoid(F)
-        return np.column_stack([1 - proba, proba])
+        return _binary_proba_columns(F)
 
     def predict(self, X):
         proba = self.predict_proba(X)
