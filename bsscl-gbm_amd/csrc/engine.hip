@@ -604,9 +604,9 @@ int upload(bsscl_engine *E, DevBuf<T> &dst, const T *src, size_t count) {
 // ---------------------------------------------------------------------------
 // Large host <-> device transfers.  A copy from pageable memory makes HIP
 // stage it through its own pinned buffers, one after the other (about
-// 19 GB/s for a 112 MB matrix).  Here host threads copy chunks into three
-// pinned buffers while the DMA engine moves the chunk before, so both run
-// at once.
+// 19 GB/s for a 112 MB matrix, 27-29 GB/s for 2 GB).  Here host threads
+// copy chunks into three pinned buffers while the DMA engine moves the
+// chunk before, so both run at once, and the DMA engine sets the rate.
 // ---------------------------------------------------------------------------
 
 // A few host threads that split a memcpy with the caller.  One pool per
@@ -694,12 +694,16 @@ class CopyPool {
   size_t bytes_ = 0;
 };
 
-constexpr size_t kXferChunk = 8u << 20;
+// Chunks of 8 MB keep small transfers pipelined; from 512 MB on, 32 MB
+// chunks reach 55 GB/s host to device against 52 (10M x 50 float32: 36 ms;
+// HIP's own pageable copy 69-73 ms).
+constexpr size_t kXferChunkMax = 32u << 20;
+size_t xfer_chunk(size_t bytes) { return bytes >= (512u << 20) ? kXferChunkMax : 8u << 20; }
 
 int ensure_xfer(bsscl_engine *E) {
   for (int b = 0; b < 3; ++b) {
     if (!E->xfer_pin[b])
-      HIPCHK(hipHostMalloc(reinterpret_cast<void **>(&E->xfer_pin[b]), kXferChunk,
+      HIPCHK(hipHostMalloc(reinterpret_cast<void **>(&E->xfer_pin[b]), kXferChunkMax,
                            hipHostMallocDefault));
     if (!E->xfer_ev[b]) HIPCHK(hipEventCreateWithFlags(&E->xfer_ev[b], hipEventDisableTiming));
   }
@@ -709,7 +713,8 @@ int ensure_xfer(bsscl_engine *E) {
 // dst (device) = src (host, pageable) on E->st; returns once the copy is
 // complete.
 int host_upload(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
-  if (bytes < 2 * kXferChunk) {
+  const size_t chunk = xfer_chunk(bytes);
+  if (bytes < 2 * chunk) {
     HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, E->st));
     HIPCHK(hipStreamSynchronize(E->st));
     return BSSCL_OK;
@@ -717,9 +722,9 @@ int host_upload(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
   CHK(ensure_xfer(E));
   CopyPool &pool = CopyPool::get();
   size_t c = 0;
-  for (size_t off = 0; off < bytes; off += kXferChunk, ++c) {
+  for (size_t off = 0; off < bytes; off += chunk, ++c) {
     const int b = (int)(c % 3);
-    const size_t len = std::min(kXferChunk, bytes - off);
+    const size_t len = std::min(chunk, bytes - off);
     if (c >= 3) HIPCHK(hipEventSynchronize(E->xfer_ev[b]));  // its previous chunk has gone
     pool.copy(E->xfer_pin[b], static_cast<const char *>(src) + off, len);
     HIPCHK(hipMemcpyAsync(static_cast<char *>(dst) + off, E->xfer_pin[b], len,
@@ -732,19 +737,20 @@ int host_upload(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
 
 // dst (host, pageable) = src (device) after the work already on E->st.
 int host_download(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
-  if (bytes < 2 * kXferChunk) {
+  const size_t chunk = xfer_chunk(bytes);
+  if (bytes < 2 * chunk) {
     HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, E->st));
     HIPCHK(hipStreamSynchronize(E->st));
     return BSSCL_OK;
   }
   CHK(ensure_xfer(E));
   CopyPool &pool = CopyPool::get();
-  const size_t n_chunks = (bytes + kXferChunk - 1) / kXferChunk;
+  const size_t n_chunks = (bytes + chunk - 1) / chunk;
   auto enqueue = [&](size_t c) -> int {
     const int b = (int)(c % 3);
-    const size_t off = c * kXferChunk;
+    const size_t off = c * chunk;
     HIPCHK(hipMemcpyAsync(E->xfer_pin[b], static_cast<const char *>(src) + off,
-                          std::min(kXferChunk, bytes - off), hipMemcpyDeviceToHost, E->st));
+                          std::min(chunk, bytes - off), hipMemcpyDeviceToHost, E->st));
     HIPCHK(hipEventRecord(E->xfer_ev[b], E->st));
     return BSSCL_OK;
   };
@@ -754,8 +760,8 @@ int host_download(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
     if (c + 2 < n_chunks) CHK(enqueue(c + 2));
     const int b = (int)(c % 3);
     HIPCHK(hipEventSynchronize(E->xfer_ev[b]));
-    const size_t off = c * kXferChunk;
-    pool.copy(static_cast<char *>(dst) + off, E->xfer_pin[b], std::min(kXferChunk, bytes - off));
+    const size_t off = c * chunk;
+    pool.copy(static_cast<char *>(dst) + off, E->xfer_pin[b], std::min(chunk, bytes - off));
   }
   return BSSCL_OK;
 }
@@ -2866,8 +2872,9 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
     if (e != hipSuccess)
       return set_error(BSSCL_EDEVICE, std::string("binning: ") + hipGetErrorString(e));
   } else {
-    // Stream X through the device in row chunks of at most 256 MB.
-    int64_t chunk = std::max<int64_t>(64, (int64_t)((256u << 20) / (esz * (size_t)F)) / 64 * 64);
+    // Stream X through the device in row chunks of at most 512 MB (each
+    // chunk's upload then takes the 32 MB pieces of host_upload).
+    int64_t chunk = std::max<int64_t>(64, (int64_t)((512u << 20) / (esz * (size_t)F)) / 64 * 64);
     chunk = std::min<int64_t>(chunk, round_up(n, 64));
     // (The chunk buffer stays allocated for the next host matrix.)
     DevBuf<unsigned char> &xd = E->xchunk;
