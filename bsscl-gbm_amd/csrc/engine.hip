@@ -81,9 +81,12 @@ template <typename T>
 struct DevBuf {
   T *p = nullptr;
   size_t cap = 0;
+  bool tracked = true;  // counted in g_alloc_gen (false: never used by a captured round)
+  DevBuf() = default;
+  explicit DevBuf(bool counted) : tracked(counted) {}
   int ensure(size_t count) {
     if (count <= cap && p) return BSSCL_OK;
-    g_alloc_gen.fetch_add(1, std::memory_order_relaxed);
+    if (tracked) g_alloc_gen.fetch_add(1, std::memory_order_relaxed);
     if (p) (void)hipFree(p);
     p = nullptr;
     cap = 0;
@@ -98,12 +101,19 @@ struct DevBuf {
   }
   void release() {
     if (p) {
-      g_alloc_gen.fetch_add(1, std::memory_order_relaxed);
+      if (tracked) g_alloc_gen.fetch_add(1, std::memory_order_relaxed);
       (void)hipFree(p);
     }
     p = nullptr;
     cap = 0;
   }
+};
+
+// A buffer of the binning and staging calls: no captured round uses it, so
+// allocating or freeing it leaves the captured rounds valid.
+template <typename T>
+struct TempBuf : DevBuf<T> {
+  TempBuf() : DevBuf<T>(false) {}
 };
 
 // Pinned host staging for the small per-level uploads and readbacks.  Reset
@@ -418,14 +428,14 @@ struct bsscl_engine {
   // host_download), and binning of a host matrix through xchunk.
   char *xfer_pin[3] = {nullptr, nullptr, nullptr};
   hipEvent_t xfer_ev[3] = {nullptr, nullptr, nullptr};
-  DevBuf<unsigned char> xchunk;
+  TempBuf<unsigned char> xchunk;
 
   // Feature matrix staged by bsscl_stage_features (row-major, as given) and
   // its columns sorted by bsscl_sort_columns (keys [F][col_ld]).
-  DevBuf<unsigned char> xstage;
+  TempBuf<unsigned char> xstage;
   int64_t xs_n = 0;
   int32_t xs_F = 0, xs_f64 = 0;
-  DevBuf<unsigned char> col_keys;
+  TempBuf<unsigned char> col_keys;
   int64_t col_ld = 0;
   bool cols_sorted = false;
   std::vector<int64_t> col_m;  // non-NaN values per sorted column
@@ -2854,8 +2864,8 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
   }
   HIPCHK(hipSetDevice(E->device));
   CHK(alloc_matrix(E, slot, n, F, tiers));
-  DevBuf<double> ed;
-  DevBuf<int32_t> nb, nid;
+  TempBuf<double> ed;
+  TempBuf<int32_t> nb, nid;
   CHK(ed.ensure((size_t)F * edge_stride));
   CHK(nb.ensure((size_t)F));
   CHK(nid.ensure((size_t)F));
@@ -2877,7 +2887,7 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
     int64_t chunk = std::max<int64_t>(64, (int64_t)((512u << 20) / (esz * (size_t)F)) / 64 * 64);
     chunk = std::min<int64_t>(chunk, round_up(n, 64));
     // (The chunk buffer stays allocated for the next host matrix.)
-    DevBuf<unsigned char> &xd = E->xchunk;
+    TempBuf<unsigned char> &xd = E->xchunk;
     int rc = xd.ensure((size_t)chunk * F * esz);
     if (rc != BSSCL_OK) { ed.release(); nb.release(); nid.release(); return rc; }
     for (int64_t r0 = 0; r0 < n; r0 += chunk) {
@@ -2935,10 +2945,10 @@ int bsscl_sort_columns(bsscl_engine *E, int64_t *nan_count, int64_t *n_unique) {
   const size_t ksz = f64 ? 8 : 4;
   E->cols_sorted = false;
   CHK(E->col_keys.ensure((size_t)F * ld * ksz));
-  DevBuf<unsigned char> tmp;
-  DevBuf<uint32_t> counts, totals;
-  DevBuf<int64_t> m_d;
-  DevBuf<unsigned long long> changes_d;
+  TempBuf<unsigned char> tmp;
+  TempBuf<uint32_t> counts, totals;
+  TempBuf<int64_t> m_d;
+  TempBuf<unsigned long long> changes_d;
   int rc = tmp.ensure((size_t)F * ld * ksz);
   if (rc == BSSCL_OK) rc = counts.ensure((size_t)col_sort_count_words(n, F, f64));
   if (rc == BSSCL_OK) rc = totals.ensure((size_t)F * 256);
@@ -2981,9 +2991,9 @@ int bsscl_sorted_gather(bsscl_engine *E, int64_t count, const int32_t *col, cons
       return set_error(BSSCL_EINVAL, "sorted_gather: position outside the column's values");
   }
   HIPCHK(hipSetDevice(E->device));
-  DevBuf<int32_t> c_d;
-  DevBuf<int64_t> p_d;
-  DevBuf<double> o_d;
+  TempBuf<int32_t> c_d;
+  TempBuf<int64_t> p_d;
+  TempBuf<double> o_d;
   CHK(c_d.ensure((size_t)count));
   CHK(p_d.ensure((size_t)count));
   CHK(o_d.ensure((size_t)count));
@@ -3011,8 +3021,8 @@ int bsscl_sorted_uniques(bsscl_engine *E, int32_t col, int32_t max_out, double *
   *count = 0;
   if (m == 0) return BSSCL_OK;
   HIPCHK(hipSetDevice(E->device));
-  DevBuf<int64_t> p_d;
-  DevBuf<unsigned int> cnt_d;
+  TempBuf<int64_t> p_d;
+  TempBuf<unsigned int> cnt_d;
   CHK(p_d.ensure((size_t)std::max(max_out, 1)));
   CHK(cnt_d.ensure(1));
   unsigned int cnt = 0;
@@ -3064,7 +3074,7 @@ int bsscl_load_codes(bsscl_engine *E, int32_t slot, const void *codes,
   }
   CHK(alloc_matrix(E, slot, n, F, tiers));
   const size_t bytes = (size_t)n * F * (codes_u16 ? 2 : 1);
-  DevBuf<unsigned char> tmp;
+  TempBuf<unsigned char> tmp;
   CHK(tmp.ensure(bytes));
   {
     const int rc = host_upload(E, tmp.p, codes, bytes);
@@ -3089,7 +3099,7 @@ int get_codes(bsscl_engine *E, int32_t slot, void *codes_out, int as_u16) {
   HIPCHK(hipSetDevice(E->device));
   const Matrix &M = E->mat[slot];
   const size_t bytes = (size_t)M.n * M.F * (as_u16 ? 2 : 1);
-  DevBuf<uint8_t> tmp;
+  TempBuf<uint8_t> tmp;
   CHK(tmp.ensure(bytes));
   hipError_t e = launch_get_codes(E->st, M.codes.p, M.ld, M.n, M.F, M.tiers, tmp.p, as_u16);
   if (e == hipSuccess) e = hipMemcpyAsync(codes_out, tmp.p, bytes, hipMemcpyDeviceToHost, E->st);
