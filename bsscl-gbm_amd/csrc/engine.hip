@@ -1860,7 +1860,7 @@ int load_grad_hess(bsscl_engine *E, const double *grad, const double *hess,
 int find_hot_bins(bsscl_engine *E) {
   const Matrix &M = E->mat[0];
   const int32_t C = M.cols();
-  DevBuf<unsigned int> cnt;
+  TempBuf<unsigned int> cnt;
   CHK(cnt.ensure((size_t)C * 256));
   std::vector<unsigned int> h((size_t)C * 256);
   hipError_t e = hipMemsetAsync(cnt.p, 0, (size_t)C * 256 * 4, E->st);
@@ -3796,8 +3796,8 @@ int bsscl_fisher_yates_apply(bsscl_engine *E, const uint32_t *draws, int64_t n,
   if (n <= 1) return BSSCL_OK;
   HIPCHK(hipSetDevice(E->device));
   HIPCHK(hipStreamSynchronize(E->st_rows));  // the work arrays are shared with the rounds
-  DevBuf<int32_t> a, b;
-  DevBuf<uint32_t> d;
+  TempBuf<int32_t> a, b;
+  TempBuf<uint32_t> d;
   FyWork w;
   int rc = BSSCL_OK;
   for (DevBuf<int32_t> *x : {&a, &b})

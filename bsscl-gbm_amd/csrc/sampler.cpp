@@ -47,6 +47,7 @@
 #include <immintrin.h>
 #include <pthread.h>
 #include <sys/mman.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <atomic>
@@ -201,8 +202,61 @@ void shuffle_inplace(MT &mt, T *a, int64_t n) {
   }
 }
 
+// Pinned host blocks outlive the sampler that allocated them: the
+// process's next sampler takes them.  A fit makes one sampler, and pinning
+// a round's draws buffer (4 bytes per row) when the round is first drawn
+// held up its first rounds by up to 1.3 ms each at 1M rows.  One list per
+// process (a child made by fork() starts an empty one).
+struct PinnedBlock {
+  void *p;
+  size_t bytes;
+};
+// (Never destroyed: a sampler released during the process's exit still
+// finds them.)
+std::mutex &g_pinned_mu = *new std::mutex;
+std::vector<PinnedBlock> &g_pinned = *new std::vector<PinnedBlock>;
+pid_t g_pinned_pid = 0;
+constexpr size_t kPinnedKept = 24;
+
+void pinned_list_for_this_process() {
+  if (g_pinned_pid != getpid()) {  // (the parent's blocks are not pinned here)
+    g_pinned.clear();
+    g_pinned_pid = getpid();
+  }
+}
+
+// The smallest kept block of at least `bytes` (and at most four times
+// that); null if none.
+void *take_pinned(size_t bytes, size_t *got) {
+  std::lock_guard<std::mutex> lk(g_pinned_mu);
+  pinned_list_for_this_process();
+  size_t best = g_pinned.size();
+  for (size_t i = 0; i < g_pinned.size(); ++i)
+    if (g_pinned[i].bytes >= bytes && g_pinned[i].bytes / 4 <= bytes &&
+        (best == g_pinned.size() || g_pinned[i].bytes < g_pinned[best].bytes))
+      best = i;
+  if (best == g_pinned.size()) return nullptr;
+  void *p = g_pinned[best].p;
+  *got = g_pinned[best].bytes;
+  g_pinned.erase(g_pinned.begin() + (std::ptrdiff_t)best);
+  return p;
+}
+
+void keep_pinned(void *p, size_t bytes) {
+  {
+    std::lock_guard<std::mutex> lk(g_pinned_mu);
+    pinned_list_for_this_process();
+    if (g_pinned.size() < kPinnedKept) {
+      g_pinned.push_back(PinnedBlock{p, bytes});
+      return;
+    }
+  }
+  (void)hipHostFree(p);
+}
+
 // Host buffer the engine copies from: pinned when a HIP device is present,
-// plain memory otherwise.
+// plain memory otherwise.  (A pinned block is kept for later buffers when
+// this one is released: no copy reads it by then.)
 template <typename T>
 struct HostBuf {
   T *p = nullptr;
@@ -211,8 +265,12 @@ struct HostBuf {
   void alloc(size_t count) {
     if (count <= n && p) return;
     release();
-    void *q = nullptr;
-    if (hipHostMalloc(&q, count * sizeof(T), hipHostMallocDefault) == hipSuccess) {
+    size_t got = 0;
+    void *q = take_pinned(count * sizeof(T), &got);
+    if (q) {
+      pinned = true;
+      count = got / sizeof(T);
+    } else if (hipHostMalloc(&q, count * sizeof(T), hipHostMallocDefault) == hipSuccess) {
       pinned = true;
     } else {
       (void)hipGetLastError();
@@ -225,7 +283,7 @@ struct HostBuf {
   }
   void release() {
     if (p) {
-      if (pinned) (void)hipHostFree(p);
+      if (pinned) keep_pinned(p, n * sizeof(T));
       else std::free(p);
     }
     p = nullptr;
@@ -785,6 +843,58 @@ bool draw_steps(Stream &s, uint32_t hi, uint32_t *out) {
   return use_avx512() ? draw_steps_avx512(s, hi, out) : draw_steps_scalar(s, hi, out);
 }
 
+// Device copies of the draws outlive their sampler: the process's next
+// sampler on the same GPU takes them.  A fit makes one sampler, and a
+// hipMalloc and hipEventCreate per round buffer, with their frees at the
+// end, cost its first rounds about a millisecond each.  One list per
+// process (a child made by fork() starts an empty one).
+struct DrawsBuf {
+  int device;
+  size_t bytes;
+  uint32_t *p;
+  hipEvent_t ev;
+};
+std::mutex &g_draws_mu = *new std::mutex;  // (never destroyed, as g_pinned)
+std::vector<DrawsBuf> &g_draws = *new std::vector<DrawsBuf>;
+pid_t g_draws_pid = 0;
+constexpr size_t kDrawsKept = 16;
+
+// The smallest kept buffer of `device` holding `bytes`; false if none.
+bool take_kept_draws(int device, size_t bytes, DrawsBuf *out) {
+  std::lock_guard<std::mutex> lk(g_draws_mu);
+  if (g_draws_pid != getpid()) {  // (the parent's buffers are not this process's)
+    g_draws.clear();
+    g_draws_pid = getpid();
+  }
+  size_t best = g_draws.size();
+  for (size_t i = 0; i < g_draws.size(); ++i)
+    if (g_draws[i].device == device && g_draws[i].bytes >= bytes &&
+        (best == g_draws.size() || g_draws[i].bytes < g_draws[best].bytes))
+      best = i;
+  if (best == g_draws.size()) return false;
+  *out = g_draws[best];
+  g_draws.erase(g_draws.begin() + (std::ptrdiff_t)best);
+  return true;
+}
+
+// Keeps an idle buffer (no copy or kernel uses it any more) for a later
+// sampler, or frees it when enough are kept.
+void keep_draws(const DrawsBuf &b) {
+  {
+    std::lock_guard<std::mutex> lk(g_draws_mu);
+    if (g_draws_pid != getpid()) {
+      g_draws.clear();
+      g_draws_pid = getpid();
+    }
+    if (g_draws.size() < kDrawsKept) {
+      g_draws.push_back(b);
+      return;
+    }
+  }
+  if (b.p) (void)hipFree(b.p);
+  if (b.ev) (void)hipEventDestroy(b.ev);
+}
+
 }  // namespace
 
 struct Sampler {
@@ -798,6 +908,7 @@ struct Sampler {
   struct Round {
     HostBuf<uint32_t> draws;     // j(i) of steps n-1 .. 1
     uint32_t *draws_d = nullptr; // device copy (device-rows mode)
+    size_t draws_d_bytes = 0;
     hipEvent_t copied = nullptr; // recorded after the copy on copy_st
     HostBuf<int32_t> rows;       // sample_idx (host mode)
     std::vector<int32_t> feats;  // ascending selected features
@@ -891,10 +1002,19 @@ struct Sampler {
       fail("sampler: no copy stream");
       return false;
     }
-    if (!R.draws_d && hipMalloc(reinterpret_cast<void **>(&R.draws_d), (size_t)n * 4) != hipSuccess) {
-      R.draws_d = nullptr;
-      fail("sampler: hipMalloc of the draws failed");
-      return false;
+    if (!R.draws_d) {
+      DrawsBuf kept;
+      if (take_kept_draws(device, (size_t)n * 4, &kept)) {
+        R.draws_d = kept.p;
+        R.draws_d_bytes = kept.bytes;
+        R.copied = kept.ev;
+      } else if (hipMalloc(reinterpret_cast<void **>(&R.draws_d), (size_t)n * 4) != hipSuccess) {
+        R.draws_d = nullptr;
+        fail("sampler: hipMalloc of the draws failed");
+        return false;
+      } else {
+        R.draws_d_bytes = (size_t)n * 4;
+      }
     }
     if (!R.copied && hipEventCreateWithFlags(&R.copied, hipEventDisableTiming) != hipSuccess) {
       R.copied = nullptr;
@@ -914,10 +1034,15 @@ struct Sampler {
     return true;
   }
 
+  // (Called after copy_st is drained, when no round of this sampler is in
+  // use on the device.)
   void free_device(Round &R) {
-    if (R.draws_d) (void)hipFree(R.draws_d);
-    if (R.copied) (void)hipEventDestroy(R.copied);
+    if (R.draws_d)
+      keep_draws(DrawsBuf{device, R.draws_d_bytes, R.draws_d, R.copied});
+    else if (R.copied)
+      (void)hipEventDestroy(R.copied);
     R.draws_d = nullptr;
+    R.draws_d_bytes = 0;
     R.copied = nullptr;
   }
 
