@@ -63,7 +63,13 @@ def _encode_labels(y):
     classes, and the labels are their own codes."""
     y = np.asarray(y)
     if y.ndim == 1 and y.size and (y.dtype.kind in "iu" or y.dtype == np.bool_):
-        lo, hi = int(y.min()), int(y.max())
+        ext = _row_blocks(len(y), lambda a, b: (int(y[a:b].min()), int(y[a:b].max())))
+        lo, hi = min(e[0] for e in ext), max(e[1] for e in ext)
+        if lo >= 0 and hi <= 1:  # 0/1 labels: which occur follows from one count
+            n1 = _count_nonzero(y)
+            classes = np.array([v for v, c in ((0, len(y) - n1), (1, n1)) if c], dtype=y.dtype)
+            codes = y.astype(np.int64, copy=False)
+            return classes, (codes if len(classes) == 2 or n1 == 0 else np.zeros(len(y), np.int64))
         if lo >= 0 and hi < (1 << 16):
             present = np.bincount(y.astype(np.int64, copy=False), minlength=hi + 1) > 0
             classes = np.nonzero(present)[0].astype(y.dtype)
@@ -97,8 +103,36 @@ def _sigmoid(F):
     return 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
 
 
-# Rows from which predict_proba's elementwise host work runs on threads.
+# Rows from which the estimator's elementwise and reducing host passes
+# (labels, class counts, the base score's weights, predict_proba's
+# probabilities) run in row blocks on a few threads: NumPy's loops release
+# the GIL, and each element, or each block's count, is NumPy's own.
 _PROBA_THREAD_ROWS = 1 << 19
+
+
+def _row_blocks(n, fn):
+    """[fn(a, b) for the row blocks [a, b) of [0, n)], on up to eight threads
+    when n is large; one block otherwise."""
+    workers = min(8, os.cpu_count() or 1)
+    if n < _PROBA_THREAD_ROWS or workers < 2:
+        return [fn(0, n)]
+    from concurrent.futures import ThreadPoolExecutor
+    step = -(-n // (4 * workers))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        futures = [ex.submit(fn, a, min(a + step, n)) for a in range(0, n, step)]
+        return [f.result() for f in futures]
+
+
+def _take(table, idx):
+    """table[idx] for a small float64 table and integer indices: the same
+    values, gathered in row blocks."""
+    out = np.empty(len(idx), dtype=np.float64)
+    _row_blocks(len(idx), lambda a, b: np.take(table, idx[a:b], out=out[a:b]))
+    return out
+
+
+def _count_nonzero(y):
+    return sum(_row_blocks(len(y), lambda a, b: int(np.count_nonzero(y[a:b]))))
 
 
 def _binary_proba_columns(F):
@@ -106,23 +140,14 @@ def _binary_proba_columns(F):
     Large inputs go in row blocks over a few threads: NumPy's ufuncs release
     the GIL, and every element is computed by the same NumPy loop, so the
     values are bit-identical to the one-piece expression."""
-    n = len(F)
-    out = np.empty((n, 2), dtype=np.float64)
+    out = np.empty((len(F), 2), dtype=np.float64)
 
     def block(a, b):
         p = _sigmoid(F[a:b])
         out[a:b, 0] = 1 - p
         out[a:b, 1] = p
 
-    workers = min(8, os.cpu_count() or 1)
-    if n < _PROBA_THREAD_ROWS or workers < 2:
-        block(0, n)
-        return out
-    from concurrent.futures import ThreadPoolExecutor
-    step = -(-n // (4 * workers))
-    with ThreadPoolExecutor(max_workers=workers) as ex:
-        for f in [ex.submit(block, a, min(a + step, n)) for a in range(0, n, step)]:
-            f.result()
+    _row_blocks(len(F), block)
     return out
 
 
@@ -476,7 +501,7 @@ class HybridHistGBMNumbaV1_0_1:
         if self.class_weight not in ('balanced', 'balanced_sqrt'):
             return 1.0, 1.0
         n = len(y)
-        n1 = int(np.count_nonzero(y))  # y holds 0 and 1
+        n1 = _count_nonzero(y)  # y holds 0 and 1
         w = []
         for k in range(2):
             n_k = n1 if k == 1 else n - n1
@@ -634,8 +659,8 @@ class HybridHistGBMNumbaV1_0_1:
         # np.average(y, weights=np.where(y == 1, w1, w0)) of the reference
         # (est:2829-2834): sum(y * w) / sum(w) over the same float64 arrays,
         # built by lookup (y holds 0 and 1), so the sums are NumPy's own.
-        sw = np.array([w0, w1])[y]
-        weighted_mean = np.array([0.0, w1])[y].sum() / sw.sum()
+        sw = _take(np.array([w0, w1]), y)
+        weighted_mean = _take(np.array([0.0, w1]), y).sum() / sw.sum()
         p0 = np.clip(weighted_mean, 1e-7, 1.0 - 1e-7)
         self.base_score_ = np.log(p0 / (1.0 - p0))
         F_val = np.full(n_val, self.base_score_) if n_val else None

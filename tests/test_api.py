@@ -137,23 +137,26 @@ def test_label_encoding_equals_unique_and_searchsorted():
     0 .. K-1) equals np.unique + np.searchsorted (est:3124-3129), dtype
     included, and the base score's weighted mean built by lookup equals
     np.average with the reference's np.where weights bit for bit."""
-    from bsscl_gbm.estimator import _encode_labels
+    from bsscl_gbm import estimator as em
     rng = np.random.default_rng(5)
     cases = [rng.integers(0, 2, 1000), rng.integers(0, 5, 1000).astype(np.int32),
              np.array([3, 7, 3, 9]), rng.random(100) < 0.3, np.array(["b", "a", "b"]),
              np.array([2, 2, 5]), np.array([-1, 1, -1]), rng.integers(0, 2, 10).astype(np.uint8),
-             np.array([0.0, 1.0, 1.0])]
+             np.array([0.0, 1.0, 1.0]), np.zeros(5, np.int64), np.ones(6, np.int64),
+             np.ones(4, bool), np.array([1, 0, 1], np.uint8), rng.integers(0, 2, 700_001),
+             np.ones(600_000, np.int64), rng.integers(0, 3, 600_000).astype(np.int16)]
     for y in cases:
-        c, e = _encode_labels(y)
+        c, e = em._encode_labels(y)
         c2 = np.unique(y)
         np.testing.assert_array_equal(c, c2)
         assert c.dtype == c2.dtype and e.dtype == np.int64
         np.testing.assert_array_equal(e, np.searchsorted(c2, y))
-    for n in (1, 7, 1000, 100_003):
+    for n in (1, 7, 1000, 100_003, 700_001):
         y = (rng.random(n) < 0.3).astype(np.int64)
+        assert em._count_nonzero(y) == np.count_nonzero(y)
         for w0, w1 in ((1.0, 1.0), (0.785, 7.31), (1.0, 6.0)):
             want = np.average(y, weights=np.where(y == 1, w1, w0))
-            got = np.array([0.0, w1])[y].sum() / np.array([w0, w1])[y].sum()
+            got = em._take(np.array([0.0, w1]), y).sum() / em._take(np.array([w0, w1]), y).sum()
             assert got == want
 
 
