@@ -103,24 +103,45 @@ def _sigmoid(F):
     return 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
 
 
-# Rows from which the estimator's elementwise and reducing host passes
-# (labels, class counts, the base score's weights, predict_proba's
-# probabilities) run in row blocks on a few threads: NumPy's loops release
-# the GIL, and each element, or each block's count, is NumPy's own.
+# Rows from which the estimator's elementwise and reducing host passes run
+# in row blocks on a few threads: NumPy's loops release the GIL, and each
+# element, or each block's count, is NumPy's own.  predict_proba's
+# probabilities (a few transcendental operations per row) gain from 1M rows
+# on; the label, count and lookup passes (one memory pass each) lost to the
+# threads' dispatch at 1M rows and gain at 10M.
 _PROBA_THREAD_ROWS = 1 << 19
+_PASS_THREAD_ROWS = 1 << 22
 
 
-def _row_blocks(n, fn):
-    """[fn(a, b) for the row blocks [a, b) of [0, n)], on up to eight threads
-    when n is large; one block otherwise."""
-    workers = min(8, os.cpu_count() or 1)
-    if n < _PROBA_THREAD_ROWS or workers < 2:
+_POOL = None  # (pid, ThreadPoolExecutor): one per process, made on first use
+_POOL_LOCK = threading.Lock()
+
+
+def _host_pool():
+    """The process's thread pool for _row_blocks, or None with fewer than
+    two CPUs (a child made by fork() makes its own)."""
+    global _POOL
+    with _POOL_LOCK:
+        if _POOL is None or _POOL[0] != os.getpid():
+            workers = min(8, os.cpu_count() or 1)
+            if workers < 2:
+                return None
+            from concurrent.futures import ThreadPoolExecutor
+            _POOL = (os.getpid(), ThreadPoolExecutor(max_workers=workers,
+                                                     thread_name_prefix="bsscl-host"))
+        return _POOL[1]
+
+
+def _row_blocks(n, fn, min_rows=None):
+    """[fn(a, b) for the row blocks [a, b) of [0, n)], on the process's
+    host threads from min_rows rows on (the label and count passes'
+    threshold by default); one block otherwise."""
+    pool = _host_pool() if n >= (_PASS_THREAD_ROWS if min_rows is None else min_rows) else None
+    if pool is None:
         return [fn(0, n)]
-    from concurrent.futures import ThreadPoolExecutor
-    step = -(-n // (4 * workers))
-    with ThreadPoolExecutor(max_workers=workers) as ex:
-        futures = [ex.submit(fn, a, min(a + step, n)) for a in range(0, n, step)]
-        return [f.result() for f in futures]
+    step = -(-n // (4 * pool._max_workers))
+    futures = [pool.submit(fn, a, min(a + step, n)) for a in range(0, n, step)]
+    return [f.result() for f in futures]
 
 
 def _take(table, idx):
@@ -147,7 +168,7 @@ def _binary_proba_columns(F):
         out[a:b, 0] = 1 - p
         out[a:b, 1] = p
 
-    _row_blocks(len(F), block)
+    _row_blocks(len(F), block, _PROBA_THREAD_ROWS)
     return out
 
 

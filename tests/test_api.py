@@ -132,12 +132,13 @@ def test_sampler_rejects_bad_arguments():
         _native.Sampler(st, 10, 5, False, 3, 2, True, 1)
 
 
-def test_label_encoding_equals_unique_and_searchsorted():
+def test_label_encoding_equals_unique_and_searchsorted(monkeypatch):
     """The estimator's label encoding (a counting path for integer labels
     0 .. K-1) equals np.unique + np.searchsorted (est:3124-3129), dtype
     included, and the base score's weighted mean built by lookup equals
     np.average with the reference's np.where weights bit for bit."""
     from bsscl_gbm import estimator as em
+    monkeypatch.setattr(em, "_PASS_THREAD_ROWS", 1 << 19)  # the large cases in row blocks
     rng = np.random.default_rng(5)
     cases = [rng.integers(0, 2, 1000), rng.integers(0, 5, 1000).astype(np.int32),
              np.array([3, 7, 3, 9]), rng.random(100) < 0.3, np.array(["b", "a", "b"]),
