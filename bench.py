@@ -10,7 +10,8 @@ Prints one JSON line with the fit rate (trees/s), the histogram kernel's
 roofline (algorithmic bytes per launch over its average execution time,
 from the first block's start to the last block's end as the kernel stamps
 them, against 8 TB/s HBM), a complete fit with the workload's own
-n_estimators (training-only and end-to-end trees/s), prediction through
+n_estimators (training-only and end-to-end trees/s; the median of three
+fits when one takes under half a second), prediction through
 that ensemble with its own roofline, and the oracle's CPU rates on a
 bounded sample (fit trees/s, histogram rows x features/s, predict rows/s).
 The same block is repeated for the 10M x 50 depth-8 workload: its
@@ -179,14 +180,11 @@ def run_gpu(name, steps, warmup, rounds_only=False):
     if not rounds_only:
         # A complete fit with the workload's own n_estimators: bin edges,
         # binning and every boosting round, from host float32 X.
-        full = HybridHistGBMNumbaV1_0_1(**full_params)
-        t = time.perf_counter()
-        full.fit(X, y)
-        t_full = time.perf_counter() - t
+        t_full, full, n_fits = timed_fit(full_params, X, y)
         fit_full = dict(n_estimators=int(full.n_trees_fitted_), seconds=round(t_full, 4),
                         trees_per_s=round(full.n_trees_fitted_ / t_full, 2),
                         binning_ms=round(full.times["binning"], 1),
-                        training_ms=round(full.times["training"], 1))
+                        training_ms=round(full.times["training"], 1), fits=n_fits)
         fit_full["training_trees_per_s"] = round(
             full.n_trees_fitted_ / (full.times["training"] / 1e3), 2)
         _progress(f"full fit: {fit_full}")
@@ -336,6 +334,23 @@ def run_cpu_baseline(name, rounds, data=None, model=None, Xp_sample=None):
     return out
 
 
+def timed_fit(params, X, y):
+    """A complete fit's wall time.  Fits under half a second are repeated
+    three times and the median fit is returned (with its own binning and
+    training times).  Returns (seconds, fitted estimator, fits run)."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    fits = []
+    while True:
+        est = HybridHistGBMNumbaV1_0_1(**params)
+        t = time.perf_counter()
+        est.fit(X, y)
+        fits.append((time.perf_counter() - t, est))
+        if len(fits) >= 3 or fits[0][0] >= 0.5:
+            break
+    t, est = sorted(fits, key=lambda f: f[0])[len(fits) // 2]
+    return t, est, len(fits)
+
+
 def run_fit_workload(name, cpu_rounds, cpu):
     """A smaller benchmark shape's complete fit (the workload's own
     n_estimators, from host float32, after one untimed fit of the same data)
@@ -345,10 +360,7 @@ def run_fit_workload(name, cpu_rounds, cpu):
     X, y, params = make_workload(name)
     _progress(f"{name}: {X.shape[0]} x {X.shape[1]}, complete fit")
     HybridHistGBMNumbaV1_0_1(**params).fit(X, y)
-    est = HybridHistGBMNumbaV1_0_1(**params)
-    t = time.perf_counter()
-    est.fit(X, y)
-    t = time.perf_counter() - t
+    t, est, n_fits = timed_fit(params, X, y)
     n_trees = int(est.n_trees_fitted_)
     out = {
         "config": {"rows": X.shape[0], "features": X.shape[1],
@@ -359,7 +371,8 @@ def run_fit_workload(name, cpu_rounds, cpu):
             "seconds": round(t, 4), "trees_per_s": round(n_trees / t, 2),
             "binning_ms": round(est.times["binning"], 1),
             "training_ms": round(est.times["training"], 1),
-            "training_trees_per_s": round(n_trees / (est.times["training"] / 1e3), 2)},
+            "training_trees_per_s": round(n_trees / (est.times["training"] / 1e3), 2),
+            "fits": n_fits},
     }
     out["predict"], sample = run_predict(est, name)
     if cpu:
