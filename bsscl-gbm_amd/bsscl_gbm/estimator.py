@@ -113,13 +113,13 @@ _PROBA_THREAD_ROWS = 1 << 19
 _PASS_THREAD_ROWS = 1 << 22
 
 
-_POOL = None  # (pid, ThreadPoolExecutor): one per process, made on first use
+_POOL = None  # (pid, ThreadPoolExecutor, workers): one per process, made on first use
 _POOL_LOCK = threading.Lock()
 
 
 def _host_pool():
-    """The process's thread pool for _row_blocks, or None with fewer than
-    two CPUs (a child made by fork() makes its own)."""
+    """The process's thread pool for _row_blocks and its thread count, or
+    None with fewer than two CPUs (a child made by fork() makes its own)."""
     global _POOL
     with _POOL_LOCK:
         if _POOL is None or _POOL[0] != os.getpid():
@@ -128,18 +128,19 @@ def _host_pool():
                 return None
             from concurrent.futures import ThreadPoolExecutor
             _POOL = (os.getpid(), ThreadPoolExecutor(max_workers=workers,
-                                                     thread_name_prefix="bsscl-host"))
-        return _POOL[1]
+                                                     thread_name_prefix="bsscl-host"), workers)
+        return _POOL[1:]
 
 
 def _row_blocks(n, fn, min_rows=None):
     """[fn(a, b) for the row blocks [a, b) of [0, n)], on the process's
     host threads from min_rows rows on (the label and count passes'
     threshold by default); one block otherwise."""
-    pool = _host_pool() if n >= (_PASS_THREAD_ROWS if min_rows is None else min_rows) else None
-    if pool is None:
+    hp = _host_pool() if n >= (_PASS_THREAD_ROWS if min_rows is None else min_rows) else None
+    if hp is None:
         return [fn(0, n)]
-    step = -(-n // (4 * pool._max_workers))
+    pool, workers = hp
+    step = -(-n // (4 * workers))
     futures = [pool.submit(fn, a, min(a + step, n)) for a in range(0, n, step)]
     return [f.result() for f in futures]
 
