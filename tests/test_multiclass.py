@@ -295,8 +295,8 @@ def test_multiclass_device_grad_hess_equal_numpy(engine, K):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("K", [3, 9])
-def test_multiclass_round_paths_agree(engine, monkeypatch, K):
+@pytest.mark.parametrize("K,subsample", [(3, None), (9, None), (4, 1.0)])
+def test_multiclass_round_paths_agree(engine, monkeypatch, K, subsample):
     """A round's K trees in one call (mc_build_trees: device replay, one
     readback) against the same trees one class at a time (mc_build_tree:
     host replay per tree), against the rows in the reference's order from a
@@ -305,11 +305,13 @@ def test_multiclass_round_paths_agree(engine, monkeypatch, K):
     node table too small for the first round's trees (every class rebuilt
     on the host-driven path, then grown) and the replay reading the node
     table from HBM.  Trees, split gains, losses and scores must be
-    identical."""
+    identical.  (subsample=1.0: every row in every round, without draws.)"""
     from bsscl_gbm import HybridHistGBMNumbaV1_0_1, _native
     X, y = _mc_data(9000, 9, K, seed=60 + K, nan_frac=0.05)
     params = dict(n_estimators=3, max_depth=5, n_bins=255, random_state=7,
                   class_weight="balanced_sqrt")
+    if subsample is not None:
+        params["subsample"] = subsample
     hooks = ("BSSCL_TEST_HOST_REPLAY", "BSSCL_TEST_NODE_CAP", "BSSCL_TEST_REPLAY_GLOBAL")
 
     def per_class(self, feature_indices, max_leaves, *args):
