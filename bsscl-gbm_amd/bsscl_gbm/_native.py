@@ -48,6 +48,8 @@ _SIGS = {
                             _f64, _f64, _P, _P, _P, _P, _P, _P, _P],
     "bsscl_mc_build_trees": [_P, _P, _i32, _i32, _i32, _i32, _f64, _P, _i32, _f64, _f64, _f64,
                              _P, _P, _P, _P, _P, _P, _P],
+    "bsscl_mc_round_trees": [_P, _P, _P, _i32, _i32, _i32, _f64, _P, _i32, _f64, _f64, _f64,
+                             _P, _P, _P, _P, _P, _P, _P, _P],
     "bsscl_mc_loss": [_P, _P],
     "bsscl_mc_get_scores": [_P, _P],
     "bsscl_mc_get_grad_hess": [_P, _P, _P],
@@ -309,6 +311,32 @@ class Engine:
             float(reg_lambda), float(gamma), float(learning_rate), ptr(tf), ptr(tt),
             ptr(tv), ptr(tl), ptr(tr), ptr(nc), ptr(sg)))
         return [(tf[k], tt[k], tv[k], tl[k], tr[k], int(nc[k]), sg[k]) for k in range(K)]
+
+    def mc_round_trees(self, sampler, max_leaves, max_depth, min_samples_leaf,
+                       min_child_weight, bin_counts, max_bins, reg_lambda, gamma,
+                       learning_rate):
+        """One multiclass round (the sampler's next round, the K trees, the
+        loss), with the following round's rows made meanwhile; returns
+        (feature subset, list of K 7-tuples, training loss)."""
+        K = self._mc[1]
+        M = 2 * int(max_leaves) + 2
+        feats = np.empty(sampler.f_sub, np.int32)
+        bc = np.ascontiguousarray(bin_counts, np.int32)
+        tf = np.full((K, M), -1, np.int32)
+        tt = np.zeros((K, M), np.int64)
+        tv = np.zeros((K, M), np.float64)
+        tl = np.full((K, M), -1, np.int32)
+        tr = np.full((K, M), -1, np.int32)
+        nc = np.zeros(K, np.int32)
+        sg = np.zeros((K, M), np.float64)
+        loss = np.zeros(1, np.float64)
+        check(lib().bsscl_mc_round_trees(
+            self.handle, sampler.handle, ptr(feats), int(max_leaves), int(max_depth),
+            int(min_samples_leaf), float(min_child_weight), ptr(bc), int(max_bins),
+            float(reg_lambda), float(gamma), float(learning_rate), ptr(tf), ptr(tt),
+            ptr(tv), ptr(tl), ptr(tr), ptr(nc), ptr(sg), ptr(loss)))
+        trees = [(tf[k], tt[k], tv[k], tl[k], tr[k], int(nc[k]), sg[k]) for k in range(K)]
+        return feats, trees, float(loss[0])
 
     def mc_loss(self):
         out = np.zeros(1, np.float64)

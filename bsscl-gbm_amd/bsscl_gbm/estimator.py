@@ -788,32 +788,40 @@ class HybridHistGBMNumbaV1_0_1:
             y_val_onehot = np.eye(K, dtype=np.float64)[y_val]
         sample_weight = self._class_weight_vector(y)
         self.mc_trees = [[] for _ in range(K)]
-        best_val_loss = np.inf
-        rounds_no_improve = 0
         # The reference's rng.shuffle stream (est:2502-2517), one draw per
-        # round shared by the K trees (the sampler made by fit); rows come
-        # back in the reference's order.
+        # round shared by the K trees (the sampler made by fit).
         # Up to MC_DEVICE_MAX_CLASSES classes the scores, gradients, score
         # updates and loss stay on the device (the engine's multiclass
         # rounds); more classes keep the (n, K) arithmetic on the host.
         if on_device:
             eng.mc_begin(y, K, sample_weight)
+        try:
+            self._mc_rounds(eng, y, K, on_device, sampler, sample_weight, y_onehot, F_train,
+                            F_val, y_val_onehot, n_val)
+        finally:
+            # A round the engine took ahead goes back before the sampler is closed.
+            eng.set_pipeline(False)
+        self.n_trees_fitted_ = sum(len(t) for t in self.mc_trees)
+
+    def _mc_rounds(self, eng, y, K, on_device, sampler, sample_weight, y_onehot, F_train,
+                   F_val, y_val_onehot, n_val):
+        n_samples = len(y)
+        best_val_loss = np.inf
+        rounds_no_improve = 0
         for m in range(self.n_estimators):
             if on_device:
-                # The round's bagging draw and every class's gradients and
-                # hessians (est:2996-3019), the rows permuted on the device.
-                feat_idx = eng.mc_round_sampled(sampler)
-                # The K trees of the round in one engine call (est:3016-3029).
-                trees = eng.mc_build_trees(feat_idx, self.max_leaves, self.max_depth,
-                                           self.min_samples_leaf, self.min_child_weight,
-                                           self.feature_bin_counts, self._max_bins,
-                                           self.reg_lambda, self.gamma,
-                                           self.learning_rate)
+                # One engine call per round: the round's bagging draw, every
+                # class's gradients and hessians (est:2996-3019), the K trees
+                # and score updates (est:3016-3029) and the loss (est:3035);
+                # the next round's rows are permuted meanwhile.
+                feat_idx, trees, train_loss = eng.mc_round_trees(
+                    sampler, self.max_leaves, self.max_depth, self.min_samples_leaf,
+                    self.min_child_weight, self.feature_bin_counts, self._max_bins,
+                    self.reg_lambda, self.gamma, self.learning_rate)
                 for k, tree in enumerate(trees):
                     self.mc_trees[k].append(tree)
                     if F_val is not None:
                         F_val[:, k] += self.learning_rate * eng.predict_tree(1, n_val, tree)
-                train_loss = eng.mc_loss()
             else:
                 proba = self._softmax(F_train)
                 sample_idx, feat_idx = sampler.next()
@@ -856,7 +864,6 @@ class HybridHistGBMNumbaV1_0_1:
                         for k in range(K):
                             self.mc_trees[k] = self.mc_trees[k][:self.best_iteration_ + 1]
                         break
-        self.n_trees_fitted_ = sum(len(t) for t in self.mc_trees)
 
     # ------------------------------------------------------------------
     # est:2192-2236, est:2343-2363

@@ -324,11 +324,26 @@ struct bsscl_engine {
   int32_t mc_K = 0;
   int64_t mc_m = 0;  // the round's in-bag rows: mc_rows32 (int32) or, when null, rows64
   const int32_t *mc_rows32 = nullptr;
+  // A round enqueued ahead by bsscl_mc_round_trees: its rows in
+  // round_rows[mc_next_slot], made on the rows stream (complete at
+  // mc_next_ev), its sampler round held until the next call.
+  bool mc_next = false;
+  int mc_next_slot = 0;
+  void *mc_next_token = nullptr;
+  bsscl_sampler *mc_next_sampler = nullptr;
+  std::vector<int32_t> mc_next_feats;
+  hipEvent_t mc_next_ev = nullptr;
+  int mc_slot = 0;  // round_rows slot of the next round taken directly
   DevBuf<double> mc_F, mc_G, mc_H, mc_w, mc_part;
   DevBuf<int32_t> mc_y;
   DevBuf<unsigned long long> mc_max;
   std::vector<double> mc_gm, mc_hm;  // fixed-point multipliers per class
   std::vector<double> mc_hmax;       // largest hessian per class
+  // Whether mc_gm, mc_hm and mc_hmax hold this round's values; a round of
+  // bsscl_mc_round_trees leaves its maxima on the device (mc_max) and its
+  // trees take their scales there.
+  bool mc_scales_host = false;
+  double mc_hbound = 0.0;  // no multiclass hessian exceeds this (max weight / 4)
   // A multiclass round's K trees as the device replayed them: K blocks of
   // round_out_bytes(2 * max_leaves + 2), and their pinned readback.
   DevBuf<char> mc_out_d;
@@ -2466,12 +2481,24 @@ int finish_round(bsscl_engine *E, int s, TreeOut &out, double *out_train_loss) {
 // Every class's gradients and hessians from the scores at the round's start
 // (est:2996, 3013-3019) and each class's fixed point from its largest |g|
 // and h, read back; the round's m in-bag rows are already on the device.
-int mc_gradients(bsscl_engine *E, int64_t m) {
+int mc_read_scales(bsscl_engine *E);
+
+int mc_gradients(bsscl_engine *E, int64_t m, bool read_back = true) {
   const int64_t n = E->mat[0].n;
   const int32_t K = E->mc_K;
   HIPCHK(hipMemsetAsync(E->mc_max.p, 0, 2 * (size_t)K * 8, E->st));
   HIPCHK(launch_mc_grad_hess(E->st, E->mc_F.p, E->mc_y.p, E->mc_w.p, n, K, E->mc_G.p, E->mc_H.p,
                              E->mc_max.p));
+  E->mc_m = m;
+  E->mc_scales_host = false;
+  return read_back ? mc_read_scales(E) : BSSCL_OK;
+}
+
+// Each class's fixed point from its largest |g| and h of the round, read
+// back from the device (mc_max) after the gradient kernel.
+int mc_read_scales(bsscl_engine *E) {
+  const int32_t K = E->mc_K;
+  const int64_t m = E->mc_m;
   unsigned long long mx[2 * kMcMaxK];
   HIPCHK(hipMemcpyAsync(mx, E->mc_max.p, 2 * (size_t)K * 8, hipMemcpyDeviceToHost, E->st));
   HIPCHK(hipStreamSynchronize(E->st));
@@ -2482,44 +2509,44 @@ int mc_gradients(bsscl_engine *E, int64_t m) {
     double gmax, hmax;
     std::memcpy(&gmax, &mx[2 * k], 8);
     std::memcpy(&hmax, &mx[2 * k + 1], 8);
-    if (!std::isfinite(gmax) || !std::isfinite(hmax))
+    if (!std::isfinite(gmax) || !std::isfinite(hmax)) {
+      E->mc_m = 0;
       return set_error(BSSCL_EINVAL, "mc_round: gradients are not finite");
+    }
     // The scale load_grad_hess would take from the same arrays.
     E->mc_gm[(size_t)k] = fixed_mul(gmax, m);
     E->mc_hm[(size_t)k] = fixed_mul(hmax, m);
     E->mc_hmax[(size_t)k] = hmax;
   }
-  E->mc_m = m;
+  E->mc_scales_host = true;
   return BSSCL_OK;
 }
 
-// The in-bag rows of a sampler's round on the device, into mc_rows32: every
-// row in order without row bagging; with device rows, the round's steps of
-// the reference's shuffle (est:2506) applied to the cumulative permutation
-// and its first n_sub entries sorted ascending, as a boosting round makes
-// them; otherwise the sampler's rows, in the reference's order.  (A tree's
-// histograms are exact integer sums and its partitions stable, so the
-// order of its rows does not enter it.)
+// The in-bag rows of a sampler's round on the device, into round_rows[slot]
+// on stream `st`: every row in order without row bagging; with device rows,
+// the round's steps of the reference's shuffle (est:2506) applied to the
+// cumulative permutation and its first n_sub entries sorted ascending, as a
+// boosting round makes them; otherwise the sampler's rows, in the
+// reference's order.  (A tree's histograms are exact integer sums and its
+// partitions stable, so the order of its rows does not enter it.)  The
+// sampler's round must stay taken until the work on `st` is done.
 int mc_rows_from_sampler(bsscl_engine *E, bsscl_sampler *sampler, const SamplerShape &sh,
-                         const SamplerRound &sr) {
+                         const SamplerRound &sr, int slot, hipStream_t st) {
   const Matrix &X = E->mat[0];
   const int64_t m = sh.n_sub;
-  if (m <= 0) return set_error(BSSCL_EINVAL, "mc_round_sampled: no samples");
-  hipStream_t st = E->st;
+  if (m <= 0) return set_error(BSSCL_EINVAL, "mc round: no samples");
+  CHK(E->round_rows[slot].ensure((size_t)m));
+  int32_t *out = E->round_rows[slot].p;
   if (!sh.do_rows) {
-    CHK(E->round_rows[0].ensure((size_t)m));
-    HIPCHK(launch_iota(st, E->round_rows[0].p, m));
-    E->mc_rows32 = E->round_rows[0].p;
+    HIPCHK(launch_iota(st, out, m));
     return BSSCL_OK;
   }
   if (!sh.device_rows) {
-    CHK(E->rows_in.ensure((size_t)m));
-    HIPCHK(hipMemcpyAsync(E->rows_in.p, sr.rows, (size_t)m * 4, hipMemcpyHostToDevice, st));
-    E->mc_rows32 = E->rows_in.p;
+    HIPCHK(hipMemcpyAsync(out, sr.rows, (size_t)m * 4, hipMemcpyHostToDevice, st));
     return BSSCL_OK;
   }
   if (sh.device != E->device)
-    return set_error(BSSCL_EINVAL, "mc_round_sampled: the sampler copies its draws to another GPU");
+    return set_error(BSSCL_EINVAL, "mc round: the sampler copies its draws to another GPU");
   // The cumulative permutation: identity before the sampler's first round.
   if (sr.round == 0) {
     CHK(E->perm[0].ensure((size_t)X.n));
@@ -2529,11 +2556,9 @@ int mc_rows_from_sampler(bsscl_engine *E, bsscl_sampler *sampler, const SamplerS
     E->perm_next_round = 0;
     HIPCHK(launch_iota(st, E->perm[0].p, X.n));
   } else if (E->perm_sampler != sampler || E->perm_next_round != sr.round) {
-    return set_error(BSSCL_EINVAL,
-                     "mc_round_sampled: the sampler's earlier rounds did not run on this engine");
+    return set_error(BSSCL_EINVAL, "mc round: the sampler's earlier rounds did not run on this engine");
   }
   const int64_t n_pad = sort_rows_flag_bytes(X.n);
-  CHK(E->round_rows[0].ensure((size_t)m));
   CHK(E->sort_tmp.ensure((size_t)(n_pad / 4096 + 1)));
   if (E->row_flags_n != n_pad) {
     CHK(E->row_flags.ensure((size_t)n_pad));
@@ -2548,20 +2573,32 @@ int mc_rows_from_sampler(bsscl_engine *E, bsscl_sampler *sampler, const SamplerS
   const bool marked = w.keys != nullptr;
   HIPCHK(launch_fisher_yates(st, sr.draws_dev, X.n, E->perm[cur].p, E->perm[cur ^ 1].p, w,
                              marked ? E->row_flags.p : nullptr, m));
-  HIPCHK(launch_sort_rows(st, E->perm[cur ^ 1].p, m, E->row_flags.p, n_pad, E->sort_tmp.p,
-                          E->round_rows[0].p, marked));
+  HIPCHK(launch_sort_rows(st, E->perm[cur ^ 1].p, m, E->row_flags.p, n_pad, E->sort_tmp.p, out,
+                          marked));
   E->perm_cur = cur ^ 1;
   E->perm_next_round = sr.round + 1;
-  E->mc_rows32 = E->round_rows[0].p;
   return BSSCL_OK;
+}
+
+// Hands back a multiclass round enqueued ahead (bsscl_mc_round_trees), once
+// the rows stream has finished with its draws.
+void mc_drop_next(bsscl_engine *E) {
+  if (!E->mc_next) return;
+  (void)hipStreamSynchronize(E->st_rows);
+  sampler_give_back(E->mc_next_sampler, E->mc_next_token);
+  E->mc_next = false;
+  E->mc_next_token = nullptr;
+  E->mc_next_sampler = nullptr;
 }
 
 // Multiclass class k's fixed point: the round's largest |g| and h of the
 // class (bsscl_mc_round).
-void mc_class_scales(bsscl_engine *E, int32_t k) {
+int mc_class_scales(bsscl_engine *E, int32_t k) {
+  if (!E->mc_scales_host) CHK(mc_read_scales(E));
   E->g_scale = 1.0 / E->mc_gm[(size_t)k];
   E->h_scale = 1.0 / E->mc_hm[(size_t)k];
   E->h_bound = E->mc_hmax[(size_t)k];
+  return BSSCL_OK;
 }
 
 // Class k's tree of the multiclass round on the host-driven path (its node
@@ -2572,7 +2609,7 @@ int mc_tree_host(bsscl_engine *E, int32_t k, const std::vector<int32_t> &feats,
                  TreeOut &out) {
   const Matrix &X = E->mat[0];
   const int64_t n = X.n;
-  mc_class_scales(E, k);
+  CHK(mc_class_scales(E, k));
   HIPCHK(launch_quantize(E->st, E->mc_G.p + (size_t)k * n, E->mc_H.p + (size_t)k * n, n,
                          E->mc_gm[(size_t)k], E->mc_hm[(size_t)k], E->ghq.p));
   E->set_base = 0;
@@ -2611,15 +2648,31 @@ int mc_trees_device(bsscl_engine *E, const std::vector<int32_t> &feats,
   E->set_base = 0;
   CHK(prepare_tree_buffers(E, m, F_sel, std::max(1, tp.max_depth), tp.max_leaves));
   for (int32_t k = 0; k < K; ++k) {
-    mc_class_scales(E, k);
+    // The class's fixed point: from the maxima the host read back, or from
+    // those on the device (the same multipliers, dev_fixed_mul), with the
+    // hessian bound max weight / 4 for the planner's kept-split rule.
+    DevScale dv{nullptr, 0, 0};
+    if (E->mc_scales_host) {
+      CHK(mc_class_scales(E, k));
+    } else {
+      dv = DevScale{E->mc_max.p + 2 * k, fixed_bits(m), 0};
+      E->g_scale = E->h_scale = 1.0;  // (the kernels take dv's)
+      E->h_bound = E->mc_hbound;
+    }
     HIPCHK(launch_quantize(E->st, E->mc_G.p + (size_t)k * n, E->mc_H.p + (size_t)k * n, n,
-                           E->mc_gm[(size_t)k], E->mc_hm[(size_t)k], E->ghq.p));
+                           dv.max ? 1.0 : E->mc_gm[(size_t)k], dv.max ? 1.0 : E->mc_hm[(size_t)k],
+                           E->ghq.p, dv));
     int32_t run = 0;
-    CHK(launch_tree(E, E->mc_rows32, m, feats, nb_sel, tp, &run));
+    E->round_dev = dv;
+    const int trc = launch_tree(E, E->mc_rows32, m, feats, nb_sel, tp, &run);
+    E->round_dev = DevScale{nullptr, 0, 0};
+    CHK(trc);
     char *base = E->mc_out_d.p + (size_t)k * per;
     RoundHeader *hdr = reinterpret_cast<RoundHeader *>(base);
-    HIPCHK(launch_replay(E->st, E->nodes_d, E->plan_d, E->feat_d, replay_args(E, tp, M),
-                         round_arrays(base, M), E->tree_d.p, hdr));
+    ReplayArgs ra = replay_args(E, tp, M);
+    ra.dev = dv;
+    HIPCHK(launch_replay(E->st, E->nodes_d, E->plan_d, E->feat_d, ra, round_arrays(base, M),
+                         E->tree_d.p, hdr));
     HIPCHK(launch_mc_apply(E->st, X.codes.p, X.ld, n, E->tree_d.p, &hdr->node_count, lr,
                            E->mc_F.p + (size_t)k * n));
   }
@@ -2750,6 +2803,8 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   if (E->ahead >= 0 && E->rslot[E->ahead].active)
     sampler_give_back(E->rslot[E->ahead].sampler, E->rslot[E->ahead].token);
   E->ahead = -1;
+  mc_drop_next(E);
+  if (E->mc_next_ev) (void)hipEventDestroy(E->mc_next_ev);
   for (int b = 0; b < 2; ++b) {
     release_graph(E->rows_graph[b]);
     release_graph(E->tree_graph[b]);
@@ -3276,6 +3331,7 @@ int bsscl_boost_set_pipeline(bsscl_engine *E, int32_t on) {
     E->ahead = -1;
     CHK(drain_rounds(E, p));
   }
+  if (!on) mc_drop_next(E);
   E->pipeline = on != 0;
   return BSSCL_OK;
 }
@@ -3295,12 +3351,15 @@ int bsscl_mc_begin(bsscl_engine *E, const int64_t *y, int64_t n, int32_t n_class
     E->ahead = -1;
     CHK(drain_rounds(E, p));
   }
+  mc_drop_next(E);
   std::vector<int32_t> yi((size_t)n);
+  double wmax = 0.0;
   for (int64_t i = 0; i < n; ++i) {
     if (y[i] < 0 || y[i] >= n_classes) return set_error(BSSCL_EINVAL, "mc_begin: label out of range");
     if (!(sample_weight[i] > 0.0) || !std::isfinite(sample_weight[i]))
       return set_error(BSSCL_EINVAL, "mc_begin: sample weights must be positive");
     yi[(size_t)i] = (int32_t)y[i];
+    wmax = std::max(wmax, sample_weight[i]);
   }
   HIPCHK(hipSetDevice(E->device));
   const size_t nk = (size_t)n * (size_t)n_classes;
@@ -3319,6 +3378,8 @@ int bsscl_mc_begin(bsscl_engine *E, const int64_t *y, int64_t n, int32_t n_class
   E->mc_K = n_classes;
   E->mc_m = 0;
   E->mc_rows32 = nullptr;
+  // h = w p (1 - p) <= w / 4, floored at 1e-8 (est:3019).
+  E->mc_hbound = std::max(0.25 * wmax, 1e-8);
   E->node_cap_floor = 0;  // a new fit starts from the node table its trees' shape asks for
   return BSSCL_OK;
 }
@@ -3333,6 +3394,7 @@ int bsscl_mc_round(bsscl_engine *E, const int64_t *sample_indices, int64_t n_sam
     if (sample_indices[k] < 0 || sample_indices[k] >= n)
       return set_error(BSSCL_EINVAL, "mc_round: sample index out of range");
   HIPCHK(hipSetDevice(E->device));
+  mc_drop_next(E);
   E->mc_m = 0;
   CHK(E->rows64.ensure((size_t)n_samples));
   HIPCHK(hipMemcpyAsync(E->rows64.p, sample_indices, (size_t)n_samples * 8,
@@ -3350,10 +3412,12 @@ int bsscl_mc_round_sampled(bsscl_engine *E, bsscl_sampler *sampler, int32_t *fea
     return set_error(BSSCL_EINVAL, "mc_round_sampled: sampler rows differ from matrix rows");
   HIPCHK(hipSetDevice(E->device));
   E->mc_m = 0;
+  mc_drop_next(E);  // (a round taken ahead by bsscl_mc_round_trees goes back)
   SamplerRound sr;
   void *token = nullptr;
   CHK(sampler_take(sampler, &sr, &token));
-  int rc = mc_rows_from_sampler(E, sampler, sh, sr);
+  int rc = mc_rows_from_sampler(E, sampler, sh, sr, 0, E->st);
+  if (rc == BSSCL_OK) E->mc_rows32 = E->round_rows[0].p;
   if (rc == BSSCL_OK && feats_out) std::memcpy(feats_out, sr.feats, (size_t)sh.f_sub * 4);
   if (rc == BSSCL_OK) rc = mc_gradients(E, sh.n_sub);  // (ends with a synchronisation)
   if (rc != BSSCL_OK) {
@@ -3418,6 +3482,99 @@ int bsscl_mc_build_trees(bsscl_engine *E, const int32_t *feature_indices, int32_
     TreeOut o = out(k);
     CHK(mc_tree_host(E, k, feats, nb_sel, tp, learning_rate, o));
   }
+  return BSSCL_OK;
+}
+
+int bsscl_mc_round_trees(bsscl_engine *E, bsscl_sampler *sampler, int32_t *feats_out,
+                         int32_t max_leaves, int32_t max_depth, int32_t min_samples_leaf,
+                         double min_child_weight, const int32_t *bin_counts, int32_t max_bins,
+                         double reg_lambda, double gamma, double learning_rate,
+                         int32_t *out_features, int64_t *out_thresholds, double *out_values,
+                         int32_t *out_left, int32_t *out_right, int32_t *out_node_count,
+                         double *out_split_gains, double *out_loss) {
+  if (!E || !sampler || !out_loss) return set_error(BSSCL_EINVAL, "mc_round_trees: null argument");
+  if (E->mc_K < 2) return set_error(BSSCL_EINVAL, "mc_round_trees: no multiclass run");
+  CHK(check_matrix(E, 0));
+  const SamplerShape sh = sampler_shape(sampler);
+  if (sh.n != E->mat[0].n)
+    return set_error(BSSCL_EINVAL, "mc_round_trees: sampler rows differ from matrix rows");
+  HIPCHK(hipSetDevice(E->device));
+  if (E->mc_next && E->mc_next_sampler != sampler) mc_drop_next(E);
+  E->mc_m = 0;
+  // This round's rows: made on the rows stream by the previous call, or now.
+  int slot = E->mc_slot;
+  void *token = nullptr;
+  std::vector<int32_t> feats_sel;
+  int rc = BSSCL_OK;
+  if (!E->mc_next_ev) HIPCHK(hipEventCreateWithFlags(&E->mc_next_ev, hipEventDisableTiming));
+  if (E->mc_next) {
+    slot = E->mc_next_slot;
+    token = E->mc_next_token;
+    feats_sel.swap(E->mc_next_feats);
+    E->mc_next = false;
+    E->mc_next_token = nullptr;
+  } else {
+    SamplerRound sr;
+    CHK(sampler_take(sampler, &sr, &token));
+    feats_sel.assign(sr.feats, sr.feats + sh.f_sub);
+    rc = mc_rows_from_sampler(E, sampler, sh, sr, slot, E->st_rows);
+    if (rc == BSSCL_OK && hipEventRecord(E->mc_next_ev, E->st_rows) != hipSuccess)
+      rc = set_error(BSSCL_EDEVICE, "mc_round_trees: event record failed");
+  }
+  auto release = [&](int code) {
+    (void)hipStreamSynchronize(E->st_rows);
+    (void)hipStreamSynchronize(E->st);
+    if (token) sampler_give_back(sampler, token);
+    E->mc_m = 0;
+    return code;
+  };
+  if (rc != BSSCL_OK) return release(rc);
+  // The trees read the round's rows after the rows stream has made them.
+  if (hipStreamWaitEvent(E->st, E->mc_next_ev, 0) != hipSuccess)
+    return release(set_error(BSSCL_EDEVICE, "mc_round_trees: stream wait failed"));
+  E->mc_rows32 = E->round_rows[slot].p;
+  E->mc_slot = slot ^ 1;
+  // The next round's rows on the rows stream, beside this round's
+  // gradients and trees (they touch the permutation, the row flags and the
+  // other slot's rows only).
+  if (sampler_remaining(sampler) > 0) {
+    SamplerRound sr2;
+    void *token2 = nullptr;
+    rc = sampler_take(sampler, &sr2, &token2);
+    if (rc == BSSCL_OK) {
+      rc = mc_rows_from_sampler(E, sampler, sh, sr2, slot ^ 1, E->st_rows);
+      if (rc == BSSCL_OK && hipEventRecord(E->mc_next_ev, E->st_rows) != hipSuccess)
+        rc = set_error(BSSCL_EDEVICE, "mc_round_trees: event record failed");
+      if (rc == BSSCL_OK) {
+        E->mc_next = true;
+        E->mc_next_slot = slot ^ 1;
+        E->mc_next_token = token2;
+        E->mc_next_sampler = sampler;
+        E->mc_next_feats.assign(sr2.feats, sr2.feats + sh.f_sub);
+      } else {
+        (void)hipStreamSynchronize(E->st_rows);
+        sampler_give_back(sampler, token2);
+      }
+    }
+    if (rc != BSSCL_OK) return release(rc);
+  }
+  // Gradients from the scores at the round's start (after the last round's
+  // updates on the same stream), their maxima left on the device for the
+  // trees' scales; then the trees, read back once.
+  rc = mc_gradients(E, sh.n_sub, false);
+  if (rc != BSSCL_OK) return release(rc);
+  if (feats_out) std::memcpy(feats_out, feats_sel.data(), feats_sel.size() * 4);
+  rc = bsscl_mc_build_trees(E, feats_sel.data(), (int32_t)feats_sel.size(), max_leaves, max_depth,
+                            min_samples_leaf, min_child_weight, bin_counts, max_bins, reg_lambda,
+                            gamma, learning_rate, out_features, out_thresholds, out_values,
+                            out_left, out_right, out_node_count, out_split_gains);
+  if (rc != BSSCL_OK) return release(rc);
+  // (The readback waited for the trees, which waited for this round's rows:
+  // its sampler round goes back.)
+  sampler_give_back(sampler, token);
+  token = nullptr;
+  rc = bsscl_mc_loss(E, out_loss);
+  if (rc != BSSCL_OK) return release(rc);
   return BSSCL_OK;
 }
 

@@ -249,8 +249,11 @@ hipError_t launch_load_codes(hipStream_t st, const void *src, int is_u16,
                              int64_t n, int32_t F, uint8_t *codes, int64_t ld, int32_t tiers);
 hipError_t launch_get_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
                             int64_t n, int32_t F, int32_t tiers, void *dst, int as_u16);
+// ghq = (g, h) in fixed point, multiplied by g_mul and h_mul, or by the
+// multipliers of the maxima dev holds (dev.max set).
 hipError_t launch_quantize(hipStream_t st, const double *g, const double *h,
-                           int64_t n, double g_mul, double h_mul, GH *ghq);
+                           int64_t n, double g_mul, double h_mul, GH *ghq,
+                           DevScale dev = DevScale{nullptr, 0, 0});
 hipError_t launch_grad_hess(hipStream_t st, const double *F, const uint8_t *y,
                             int64_t n, double w0, double w1, double g_mul,
                             double h_mul, GH *ghq);

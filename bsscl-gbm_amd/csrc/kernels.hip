@@ -258,21 +258,29 @@ hipError_t launch_get_codes(hipStream_t st, const uint8_t *codes, int64_t ld,
 // ---------------------------------------------------------------------------
 // Gradients / hessians.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ double dev_fixed_mul(unsigned long long max_bits, int32_t bits);
+
+// With dev.max set, the multipliers come from the maxima on the device
+// (dev_fixed_mul) instead of g_mul and h_mul.
 __global__ __launch_bounds__(256) void k_quantize(const double *__restrict__ g,
                                                   const double *__restrict__ h,
                                                   int64_t n, double g_mul,
-                                                  double h_mul,
+                                                  double h_mul, DevScale dev,
                                                   GH *__restrict__ ghq) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
+  if (dev.max) {
+    g_mul = dev_fixed_mul(dev.max[0], dev.bits);
+    h_mul = dev_fixed_mul(dev.max[1], dev.bits);
+  }
   ghq[i] = make_longlong2(__double2ll_rn(g[i] * g_mul), __double2ll_rn(h[i] * h_mul));
 }
 
 hipError_t launch_quantize(hipStream_t st, const double *g, const double *h,
-                           int64_t n, double g_mul, double h_mul, GH *ghq) {
+                           int64_t n, double g_mul, double h_mul, GH *ghq, DevScale dev) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_quantize, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                     st, g, h, n, g_mul, h_mul, ghq);
+                     st, g, h, n, g_mul, h_mul, dev, ghq);
   return hipGetLastError();
 }
 

@@ -217,6 +217,13 @@ int bsscl_boost_grad_hess_max(bsscl_engine *eng, double *out);
  *                  Outputs hold K blocks of M = 2 * max_leaves + 2 entries
  *                  (class k's tree at k * M) and out_node_count K entries.
  *                  Replaces the loop over k of est:3016-3029
+ *   mc_round_trees one whole round: mc_round_sampled, mc_build_trees and
+ *                  mc_loss in one call.  It also takes the sampler's next
+ *                  round and makes its rows on a second stream while this
+ *                  round's trees are built; the next call uses them.
+ *                  bsscl_boost_set_pipeline(eng, 0), mc_begin, mc_round and
+ *                  mc_round_sampled hand such a round back; the sampler
+ *                  must outlive it
  *   mc_loss        -mean log(clip(softmax(F)[y], 1e-15, 1 - 1e-15))
  *   mc_get_scores  F as float64[n_classes * n], class by class (row i of
  *                  class k at k * n + i)
@@ -242,6 +249,13 @@ int bsscl_mc_build_trees(bsscl_engine *eng, const int32_t *feature_indices, int3
                          int32_t *out_features, int64_t *out_thresholds, double *out_values,
                          int32_t *out_left, int32_t *out_right, int32_t *out_node_count,
                          double *out_split_gains);
+int bsscl_mc_round_trees(bsscl_engine *eng, bsscl_sampler *sampler, int32_t *feats_out,
+                         int32_t max_leaves, int32_t max_depth, int32_t min_samples_leaf,
+                         double min_child_weight, const int32_t *bin_counts, int32_t max_bins,
+                         double reg_lambda, double gamma, double learning_rate,
+                         int32_t *out_features, int64_t *out_thresholds, double *out_values,
+                         int32_t *out_left, int32_t *out_right, int32_t *out_node_count,
+                         double *out_split_gains, double *out_loss);
 int bsscl_mc_loss(bsscl_engine *eng, double *out_loss);
 int bsscl_mc_get_scores(bsscl_engine *eng, double *out);
 int bsscl_mc_get_grad_hess(bsscl_engine *eng, double *grad_out, double *hess_out);

@@ -297,15 +297,18 @@ def test_multiclass_device_grad_hess_equal_numpy(engine, K):
 @pytest.mark.gpu
 @pytest.mark.parametrize("K,subsample", [(3, None), (9, None), (4, 1.0)])
 def test_multiclass_round_paths_agree(engine, monkeypatch, K, subsample):
-    """A round's K trees in one call (mc_build_trees: device replay, one
-    readback) against the same trees one class at a time (mc_build_tree:
-    host replay per tree), against the rows in the reference's order from a
-    host-rows sampler instead of the device-permuted, sorted ones, and
-    against the batched call on its fallbacks: the host replay (forced), a
-    node table too small for the first round's trees (every class rebuilt
-    on the host-driven path, then grown) and the replay reading the node
-    table from HBM.  Trees, split gains, losses and scores must be
-    identical.  (subsample=1.0: every row in every round, without draws.)"""
+    """A round in one call (mc_round_trees: the K trees with device replay
+    and one readback, the next round's rows made meanwhile on the rows
+    stream) against the same round in separate calls without the look-ahead
+    (mc_round_sampled, mc_build_trees, mc_loss), against the K trees one
+    class at a time (mc_build_tree: host replay per tree), against the rows
+    in the reference's order from a host-rows sampler instead of the
+    device-permuted, sorted ones, and against the one-call round on its
+    fallbacks: the host replay (forced), a node table too small for the
+    first round's trees (every class rebuilt on the host-driven path, then
+    grown) and the replay reading the node table from HBM.  Trees, split
+    gains, losses and scores must be identical.  (subsample=1.0: every row
+    in every round, without draws.)"""
     from bsscl_gbm import HybridHistGBMNumbaV1_0_1, _native
     X, y = _mc_data(9000, 9, K, seed=60 + K, nan_frac=0.05)
     params = dict(n_estimators=3, max_depth=5, n_bins=255, random_state=7,
@@ -314,9 +317,16 @@ def test_multiclass_round_paths_agree(engine, monkeypatch, K, subsample):
         params["subsample"] = subsample
     hooks = ("BSSCL_TEST_HOST_REPLAY", "BSSCL_TEST_NODE_CAP", "BSSCL_TEST_REPLAY_GLOBAL")
 
-    def per_class(self, feature_indices, max_leaves, *args):
-        return [self.mc_build_tree(k, feature_indices, max_leaves, *args)
-                for k in range(self._mc[1])]
+    def separate(per_class):
+        def round_trees(self, sampler, max_leaves, *args):
+            feats = self.mc_round_sampled(sampler)
+            if per_class:
+                trees = [self.mc_build_tree(k, feats, max_leaves, *args)
+                         for k in range(self._mc[1])]
+            else:
+                trees = self.mc_build_trees(feats, max_leaves, *args)
+            return feats, trees, self.mc_loss()
+        return round_trees
 
     sampler_init = _native.Sampler.__init__
 
@@ -324,26 +334,26 @@ def test_multiclass_round_paths_agree(engine, monkeypatch, K, subsample):
         sampler_init(self, *args, **dict(kw, device_rows=False))
 
     fits = {}
-    for mode, env in [("batched", {}), ("per_class", {}), ("host_rows", {}),
+    for mode, env in [("one_call", {}), ("separate", {}), ("per_class", {}), ("host_rows", {}),
                       ("host", {"BSSCL_TEST_HOST_REPLAY": "1"}),
                       ("regrow", {"BSSCL_TEST_NODE_CAP": "9"}),
                       ("global", {"BSSCL_TEST_REPLAY_GLOBAL": "1"})]:
-        print(f"[case] multiclass round path {mode} K={K}", flush=True)
+        print(f"[case] multiclass round path {mode} K={K} subsample={subsample}", flush=True)
         for k in hooks:
             monkeypatch.delenv(k, raising=False)
         for k, v in env.items():
             monkeypatch.setenv(k, v)
         with monkeypatch.context() as mp:
-            if mode == "per_class":
-                mp.setattr(_native.Engine, "mc_build_trees", per_class)
+            if mode in ("separate", "per_class"):
+                mp.setattr(_native.Engine, "mc_round_trees", separate(mode == "per_class"))
             if mode == "host_rows":
                 mp.setattr(_native.Sampler, "__init__", host_rows_sampler)
             est = HybridHistGBMNumbaV1_0_1(verbose=False, **params).fit(X, y)
         fits[mode] = (est, est.predict_proba(X))
     for k in hooks:
         monkeypatch.delenv(k, raising=False)
-    ref, ref_p = fits["batched"]
-    for mode in ("per_class", "host_rows", "host", "regrow", "global"):
+    ref, ref_p = fits["one_call"]
+    for mode in ("separate", "per_class", "host_rows", "host", "regrow", "global"):
         got, got_p = fits[mode]
         assert got.train_loss_history_ == ref.train_loss_history_, mode
         for k in range(K):
@@ -354,3 +364,27 @@ def test_multiclass_round_paths_agree(engine, monkeypatch, K, subsample):
                 for i in (0, 1, 2, 3, 4, 6):
                     np.testing.assert_array_equal(a[i][:nc], b[i][:nc], err_msg=f"{mode} {k}")
         np.testing.assert_array_equal(got_p, ref_p, err_msg=mode)
+
+
+@pytest.mark.gpu
+def test_multiclass_round_ahead_handed_back(engine):
+    """An early-stopped multiclass fit leaves a round taken ahead by the
+    engine; the fit hands it back before closing its sampler, and the next
+    fits on the same engine (multiclass, then binary) equal fresh ones."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    X, y = _mc_data(8000, 9, 4, seed=71)
+    Xv, yv = _mc_data(2000, 9, 4, seed=72)
+    yv = np.random.default_rng(73).permutation(yv)  # labels unrelated to X: stops early
+    est = HybridHistGBMNumbaV1_0_1(verbose=False, n_estimators=40, max_depth=4, n_bins=64,
+                                   learning_rate=1.0, early_stopping_rounds=1, random_state=3)
+    est.fit(X, y, eval_set=[(Xv, yv)])
+    assert len(est.mc_trees[0]) < 40  # stopped early, with rounds left in the sampler
+    params = dict(verbose=False, n_estimators=3, max_depth=4, n_bins=64, random_state=5)
+    a = HybridHistGBMNumbaV1_0_1(**params).fit(X, y)
+    b = HybridHistGBMNumbaV1_0_1(**params).fit(X, y)
+    assert a.train_loss_history_ == b.train_loss_history_
+    np.testing.assert_array_equal(a.predict_proba(X), b.predict_proba(X))
+    yb = (y == y[0]).astype(np.int64)
+    c = HybridHistGBMNumbaV1_0_1(**params).fit(X, yb)
+    d = HybridHistGBMNumbaV1_0_1(**params).fit(X, yb)
+    assert c.train_loss_history_ == d.train_loss_history_
