@@ -54,6 +54,7 @@ _SIGS = {
     "bsscl_mc_get_scores": [_P, _P],
     "bsscl_mc_get_grad_hess": [_P, _P, _P],
     "bsscl_predict": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _P],
+    "bsscl_predict_proba": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _f64, _P],
     "bsscl_predict_tree": [_P, _i32, _P, _P, _P, _P, _P, _i32, _P],
     "bsscl_predict_noalloc": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _P],
     "bsscl_node_split": [_P, _P, _P, _P, _i64, _P, _i32, _P, _f64, _f64, _P, _P,
@@ -405,6 +406,20 @@ class Engine:
         check(lib().bsscl_predict(self.handle, int(slot), ptr(f), ptr(t), ptr(v),
                                   ptr(l), ptr(r), ptr(o), int(n_trees),
                                   float(learning_rate), ptr(out)))
+        return out
+
+    def predict_proba(self, slot, n, packed, n_trees, learning_rate, base_score):
+        """bsscl_predict_proba: a binary model's (1 - p, p), shape (n, 2)."""
+        out = np.empty((n, 2), np.float64)
+        f = np.ascontiguousarray(packed["features"], np.int16)
+        t = np.ascontiguousarray(packed["thresholds"], np.int64)
+        v = np.ascontiguousarray(packed["values"], np.float64)
+        l = np.ascontiguousarray(packed["left"], np.int32)
+        r = np.ascontiguousarray(packed["right"], np.int32)
+        o = np.ascontiguousarray(packed["offsets"], np.int32)
+        check(lib().bsscl_predict_proba(self.handle, int(slot), ptr(f), ptr(t), ptr(v),
+                                        ptr(l), ptr(r), ptr(o), int(n_trees),
+                                        float(learning_rate), float(base_score), ptr(out)))
         return out
 
     def predict_noalloc(self, slot, packed, n_trees, learning_rate, out_dev_ptr):

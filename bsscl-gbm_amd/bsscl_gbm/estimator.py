@@ -103,13 +103,11 @@ def _sigmoid(F):
     return 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
 
 
-# Rows from which the estimator's elementwise and reducing host passes run
-# in row blocks on a few threads: NumPy's loops release the GIL, and each
-# element, or each block's count, is NumPy's own.  predict_proba's
-# probabilities (a few transcendental operations per row) gain from 1M rows
-# on; the label, count and lookup passes (one memory pass each) lost to the
-# threads' dispatch at 1M rows and gain at 10M.
-_PROBA_THREAD_ROWS = 1 << 19
+# Rows from which the estimator's label, count and lookup passes (one
+# memory pass each) run in row blocks on a few threads: NumPy's loops
+# release the GIL, and each element, or each block's count, is NumPy's own.
+# The threads' dispatch cost more than they saved at 1M rows; at 10M they
+# gain.
 _PASS_THREAD_ROWS = 1 << 22
 
 
@@ -132,11 +130,10 @@ def _host_pool():
         return _POOL[1:]
 
 
-def _row_blocks(n, fn, min_rows=None):
+def _row_blocks(n, fn):
     """[fn(a, b) for the row blocks [a, b) of [0, n)], on the process's
-    host threads from min_rows rows on (the label and count passes'
-    threshold by default); one block otherwise."""
-    hp = _host_pool() if n >= (_PASS_THREAD_ROWS if min_rows is None else min_rows) else None
+    host threads from _PASS_THREAD_ROWS rows on; one block otherwise."""
+    hp = _host_pool() if n >= _PASS_THREAD_ROWS else None
     if hp is None:
         return [fn(0, n)]
     pool, workers = hp
@@ -155,22 +152,6 @@ def _take(table, idx):
 
 def _count_nonzero(y):
     return sum(_row_blocks(len(y), lambda a, b: int(np.count_nonzero(y[a:b]))))
-
-
-def _binary_proba_columns(F):
-    """np.column_stack([1 - p, p]) with p = _sigmoid(F) (est:3335-3336).
-    Large inputs go in row blocks over a few threads: NumPy's ufuncs release
-    the GIL, and every element is computed by the same NumPy loop, so the
-    values are bit-identical to the one-piece expression."""
-    out = np.empty((len(F), 2), dtype=np.float64)
-
-    def block(a, b):
-        p = _sigmoid(F[a:b])
-        out[a:b, 0] = 1 - p
-        out[a:b, 1] = p
-
-    _row_blocks(len(F), block, _PROBA_THREAD_ROWS)
-    return out
 
 
 def _percentile_ranks(m, q100, dtype):
@@ -925,8 +906,10 @@ class HybridHistGBMNumbaV1_0_1:
     # ------------------------------------------------------------------
     # est:3274-3368
     # ------------------------------------------------------------------
-    def _raw_score(self, X):
-        """F = sum_t lr * value_t + base_score_ (est:3318-3324)."""
+    def _raw_score(self, X, proba=False):
+        """F = sum_t lr * value_t + base_score_ (est:3318-3324); with `proba`,
+        a binary model's predict_proba columns instead (est:3335-3336),
+        computed on the device from that F."""
         X = _to_dense(X)
         if getattr(self, 'n_features_in_', None) is None:
             raise ValueError("This HybridHistGBMNumbaV1_0_1 instance is not fitted yet.")
@@ -949,16 +932,19 @@ class HybridHistGBMNumbaV1_0_1:
             packed = {'features': self._packed_features, 'thresholds': self._packed_thresholds,
                       'values': self._packed_values, 'left': self._packed_left,
                       'right': self._packed_right, 'offsets': self._tree_offsets}
-            F = eng.predict(1, X.shape[0], packed, len(self.trees),
-                            self.learning_rate) + getattr(self, 'base_score_', 0.0)
+            if proba:
+                out = eng.predict_proba(1, X.shape[0], packed, len(self.trees),
+                                        self.learning_rate, getattr(self, 'base_score_', 0.0))
+            else:
+                out = eng.predict(1, X.shape[0], packed, len(self.trees),
+                                  self.learning_rate) + getattr(self, 'base_score_', 0.0)
             self.times['inference'] = (time.perf_counter() - t0) * 1000
-        return F
+        return out
 
     def predict_proba(self, X):
-        F = self._raw_score(X)
         if self._is_multiclass:
-            return self._softmax(F)
-        return _binary_proba_columns(F)
+            return self._softmax(self._raw_score(X))
+        return self._raw_score(X, proba=True)
 
     def predict(self, X):
         proba = self.predict_proba(X)

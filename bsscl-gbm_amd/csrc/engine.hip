@@ -437,7 +437,7 @@ struct bsscl_engine {
   int32_t ahead = -1;      // slot of a round enqueued ahead, or -1
   uint64_t round_seq = 0;
   DevBuf<int32_t> offsets_d;
-  DevBuf<double> partials_d, loss_d, out_d;
+  DevBuf<double> partials_d, loss_d, out_d, proba_d;
   PinnedArena pin;
   // Large host transfers go through these pinned chunks (host_upload,
   // host_download), and binning of a host matrix through xchunk.
@@ -2736,6 +2736,75 @@ hipStream_t copy_stream(int device) {
 
 }  // namespace bsscl
 
+namespace bsscl {
+namespace {
+
+// The ensemble's F of matrix `slot` into E->out_d (est:863-884).
+int predict_to_device(bsscl_engine *E, int32_t slot, const int16_t *features,
+                      const int64_t *thresholds, const double *values,
+                      const int32_t *left, const int32_t *right,
+                      const int32_t *offsets, int32_t n_trees, double learning_rate) {
+  if (!E || (n_trees > 0 && (!features || !thresholds || !values || !left || !right || !offsets)))
+    return set_error(BSSCL_EINVAL, "predict: null argument");
+  CHK(check_matrix(E, slot));
+  if (n_trees < 0) return set_error(BSSCL_EINVAL, "predict: negative tree count");
+  HIPCHK(hipSetDevice(E->device));
+  const Matrix &M = E->mat[slot];
+  const int32_t total = n_trees > 0 ? offsets[n_trees] : 0;
+  std::vector<TreeNodeDev> nodes((size_t)std::max(total, 1));
+  bool adjacent = true;  // every right child is its left child + 1
+  for (int32_t t = 0; t < n_trees; ++t) {
+    const int32_t a = offsets[t], b = offsets[t + 1];
+    if (a < 0 || b <= a || b > total) return set_error(BSSCL_EINVAL, "predict: bad offsets");
+    for (int32_t i = a; i < b; ++i) {
+      TreeNodeDev &d = nodes[(size_t)i];
+      d.value = values[i];
+      d.feature = features[i];
+      if (d.feature >= 0) {
+        const int32_t l = left[i], r = right[i];
+        if (d.feature >= M.F || l < 0 || r < 0 || l >= b - a || r >= b - a || l <= i - a || r <= i - a)
+          return set_error(BSSCL_EINVAL, "predict: malformed tree " + std::to_string(t));
+        adjacent = adjacent && r == l + 1;
+        int64_t thr = thresholds[i];
+        split_to_engine(M, d.feature, thr);
+        d.threshold = (int32_t)std::max<int64_t>(-1, std::min<int64_t>(thr, 1 << 20));
+        d.left = l;
+        d.right = r;
+      } else {
+        d.feature = -1;
+        d.threshold = 0;
+        d.left = d.right = 0;
+      }
+    }
+  }
+  CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 8u << 20)));
+  // The offsets, then (for the LDS-staged kernel) the runs of whole trees it
+  // stages at a time.
+  int32_t max_nodes = 0;
+  for (int32_t t = 0; t < n_trees; ++t) max_nodes = std::max(max_nodes, offsets[t + 1] - offsets[t]);
+  // (Test hook BSSCL_TEST_PREDICT_GLOBAL=1: every row walks the trees in HBM.)
+  const bool staged = n_trees > 0 && predict_staged_ok(M.cols(), max_nodes, adjacent) &&
+                      !std::getenv("BSSCL_TEST_PREDICT_GLOBAL");
+  std::vector<int32_t> offs(offsets, offsets + n_trees + 1);
+  int32_t n_chunks = 0;
+  if (staged) {
+    offs.resize(2 * ((size_t)n_trees + 1));
+    n_chunks = predict_chunks(offsets, n_trees, offs.data() + n_trees + 1);
+  }
+  CHK(upload(E, E->tree_d, nodes.data(), nodes.size()));
+  CHK(upload(E, E->offsets_d, offs.data(), offs.size()));
+  CHK(E->out_d.ensure((size_t)M.n));
+  hipEvent_t start, stop;
+  CHK(prof_kernel(E, 4, &start, &stop));
+  HIPCHK(launch_predict(E->st, M.codes.p, M.ld, M.n, M.cols(), E->tree_d.p, E->offsets_d.p,
+                        n_trees, staged ? E->offsets_d.p + n_trees + 1 : nullptr, n_chunks,
+                        learning_rate, E->out_d.p, start, stop));
+  return BSSCL_OK;
+}
+
+}  // namespace
+}  // namespace bsscl
+
 extern "C" {
 
 const char *bsscl_last_error(void) { return g_last_error.c_str(); }
@@ -2877,6 +2946,7 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->ktime_d.release();
   E->loss_d.release();
   E->out_d.release();
+  E->proba_d.release();
   E->pin.release();
   for (int b = 0; b < 3; ++b) {
     if (E->xfer_pin[b]) (void)hipHostFree(E->xfer_pin[b]);
@@ -3655,62 +3725,26 @@ int bsscl_predict(bsscl_engine *E, int32_t slot, const int16_t *features,
                   const int32_t *left, const int32_t *right,
                   const int32_t *offsets, int32_t n_trees,
                   double learning_rate, double *out_F) {
-  if (!E || !out_F || (n_trees > 0 && (!features || !thresholds || !values || !left || !right || !offsets)))
-    return set_error(BSSCL_EINVAL, "predict: null argument");
-  CHK(check_matrix(E, slot));
-  if (n_trees < 0) return set_error(BSSCL_EINVAL, "predict: negative tree count");
-  HIPCHK(hipSetDevice(E->device));
-  const Matrix &M = E->mat[slot];
-  const int32_t total = n_trees > 0 ? offsets[n_trees] : 0;
-  std::vector<TreeNodeDev> nodes((size_t)std::max(total, 1));
-  bool adjacent = true;  // every right child is its left child + 1
-  for (int32_t t = 0; t < n_trees; ++t) {
-    const int32_t a = offsets[t], b = offsets[t + 1];
-    if (a < 0 || b <= a || b > total) return set_error(BSSCL_EINVAL, "predict: bad offsets");
-    for (int32_t i = a; i < b; ++i) {
-      TreeNodeDev &d = nodes[(size_t)i];
-      d.value = values[i];
-      d.feature = features[i];
-      if (d.feature >= 0) {
-        const int32_t l = left[i], r = right[i];
-        if (d.feature >= M.F || l < 0 || r < 0 || l >= b - a || r >= b - a || l <= i - a || r <= i - a)
-          return set_error(BSSCL_EINVAL, "predict: malformed tree " + std::to_string(t));
-        adjacent = adjacent && r == l + 1;
-        int64_t thr = thresholds[i];
-        split_to_engine(M, d.feature, thr);
-        d.threshold = (int32_t)std::max<int64_t>(-1, std::min<int64_t>(thr, 1 << 20));
-        d.left = l;
-        d.right = r;
-      } else {
-        d.feature = -1;
-        d.threshold = 0;
-        d.left = d.right = 0;
-      }
-    }
-  }
-  CHK(E->pin.reserve(std::max<size_t>(E->pin.cap, 8u << 20)));
-  // The offsets, then (for the LDS-staged kernel) the runs of whole trees it
-  // stages at a time.
-  int32_t max_nodes = 0;
-  for (int32_t t = 0; t < n_trees; ++t) max_nodes = std::max(max_nodes, offsets[t + 1] - offsets[t]);
-  // (Test hook BSSCL_TEST_PREDICT_GLOBAL=1: every row walks the trees in HBM.)
-  const bool staged = n_trees > 0 && predict_staged_ok(M.cols(), max_nodes, adjacent) &&
-                      !std::getenv("BSSCL_TEST_PREDICT_GLOBAL");
-  std::vector<int32_t> offs(offsets, offsets + n_trees + 1);
-  int32_t n_chunks = 0;
-  if (staged) {
-    offs.resize(2 * ((size_t)n_trees + 1));
-    n_chunks = predict_chunks(offsets, n_trees, offs.data() + n_trees + 1);
-  }
-  CHK(upload(E, E->tree_d, nodes.data(), nodes.size()));
-  CHK(upload(E, E->offsets_d, offs.data(), offs.size()));
-  CHK(E->out_d.ensure((size_t)M.n));
-  hipEvent_t start, stop;
-  CHK(prof_kernel(E, 4, &start, &stop));
-  HIPCHK(launch_predict(E->st, M.codes.p, M.ld, M.n, M.cols(), E->tree_d.p, E->offsets_d.p,
-                        n_trees, staged ? E->offsets_d.p + n_trees + 1 : nullptr, n_chunks,
-                        learning_rate, E->out_d.p, start, stop));
-  CHK(host_download(E, out_F, E->out_d.p, (size_t)M.n * 8));
+  if (!out_F) return set_error(BSSCL_EINVAL, "predict: null argument");
+  CHK(predict_to_device(E, slot, features, thresholds, values, left, right, offsets, n_trees,
+                        learning_rate));
+  CHK(host_download(E, out_F, E->out_d.p, (size_t)E->mat[slot].n * 8));
+  CHK(sync(E));
+  return BSSCL_OK;
+}
+
+int bsscl_predict_proba(bsscl_engine *E, int32_t slot, const int16_t *features,
+                        const int64_t *thresholds, const double *values,
+                        const int32_t *left, const int32_t *right,
+                        const int32_t *offsets, int32_t n_trees, double learning_rate,
+                        double base_score, double *out_proba) {
+  if (!out_proba) return set_error(BSSCL_EINVAL, "predict_proba: null argument");
+  CHK(predict_to_device(E, slot, features, thresholds, values, left, right, offsets, n_trees,
+                        learning_rate));
+  const int64_t n = E->mat[slot].n;
+  CHK(E->proba_d.ensure(2 * (size_t)n));
+  HIPCHK(launch_binary_proba(E->st, E->out_d.p, n, base_score, E->proba_d.p));
+  CHK(host_download(E, out_proba, E->proba_d.p, (size_t)n * 16));
   CHK(sync(E));
   return BSSCL_OK;
 }

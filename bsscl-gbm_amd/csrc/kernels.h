@@ -466,6 +466,10 @@ bool predict_staged_ok(int32_t n_cols, int32_t max_tree_nodes, bool right_follow
 // the first tree of each run and n_trees after the last (n_trees + 1 entries
 // at most); returns the number of runs.
 int32_t predict_chunks(const int32_t *offsets, int32_t n_trees, int32_t *chunks);
+// out[2i], out[2i + 1] = 1 - p, p with p = 1 / (1 + exp(-clip(F[i] + base,
+// -500, 500))); out 16-byte aligned.
+hipError_t launch_binary_proba(hipStream_t st, const double *F, int64_t n, double base,
+                               double *out);
 hipError_t launch_predict(hipStream_t st, const uint8_t *codes, int64_t ld,
                           int64_t n, int32_t n_cols, const TreeNodeDev *nodes,
                           const int32_t *offsets, int32_t n_trees, const int32_t *chunks,

@@ -4169,6 +4169,29 @@ __global__ __launch_bounds__(256) void k_predict(
 }
 #pragma clang fp contract(on)
 
+// predict_proba of a binary model (est:3318-3324, 3335-3336): F + base_score,
+// p = 1 / (1 + exp(-clip(F, -500, 500))) and the columns (1 - p, p), each
+// operation rounded separately as NumPy's are (clip keeps a NaN).
+#pragma clang fp contract(off)
+__global__ __launch_bounds__(256) void k_binary_proba(const double *__restrict__ F, int64_t n,
+                                                      double base, double2 *__restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const double f = __dadd_rn(F[i], base);
+  const double fc = isnan(f) ? f : fmin(fmax(f, -500.0), 500.0);
+  const double p = __ddiv_rn(1.0, __dadd_rn(1.0, exp(-fc)));
+  out[i] = make_double2(__dsub_rn(1.0, p), p);
+}
+#pragma clang fp contract(on)
+
+hipError_t launch_binary_proba(hipStream_t st, const double *F, int64_t n, double base,
+                               double *out) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_binary_proba, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, F, n,
+                     base, reinterpret_cast<double2 *>(out));
+  return hipGetLastError();
+}
+
 // Packed trees of _pack_tree_list (est:2192-2216) -> traversal nodes: the
 // host has checked every feature and child index.
 __global__ __launch_bounds__(256) void k_pack_trees(

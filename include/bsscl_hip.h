@@ -271,6 +271,17 @@ int bsscl_predict(bsscl_engine *eng, int32_t slot, const int16_t *features,
                   const int32_t *left, const int32_t *right,
                   const int32_t *offsets, int32_t n_trees,
                   double learning_rate, double *out_F);
+/*
+ * predict_proba of a binary model (est:3318-3336) from the same arrays:
+ * F as bsscl_predict, plus base_score, then p = 1 / (1 + exp(-clip(F, -500,
+ * 500))); out_proba float64[2 * n] holds (1 - p, p) row by row.  The device's
+ * exp may differ from NumPy's in the last bit.
+ */
+int bsscl_predict_proba(bsscl_engine *eng, int32_t slot, const int16_t *features,
+                        const int64_t *thresholds, const double *values,
+                        const int32_t *left, const int32_t *right,
+                        const int32_t *offsets, int32_t n_trees, double learning_rate,
+                        double base_score, double *out_proba);
 
 /*
  * Ensemble prediction that allocates nothing.  No counterpart in the

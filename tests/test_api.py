@@ -182,21 +182,3 @@ def test_feature_importances_equal_node_loop():
                 cnt[tf[i]] += 1
     np.testing.assert_array_equal(est.feature_importances_, gain / gain.sum())
     np.testing.assert_array_equal(est.feature_split_counts_, cnt)
-
-
-def test_binary_proba_columns_equal_numpy_expression(monkeypatch):
-    """predict_proba's host step, in row blocks on threads, equals
-    np.column_stack([1 - p, p]) with p = 1 / (1 + exp(-clip(F, -500, 500)))
-    (est:3335-3336) bit for bit, at saturating and tiny scores too."""
-    from bsscl_gbm import estimator as em
-    rng = np.random.default_rng(3)
-    F = np.concatenate([rng.standard_normal(700_001) * 8.0,
-                        np.array([-1e308, -750.0, -500.0, -36.7, -1e-300, 0.0, 5e-324, 36.7,
-                                  500.0, 750.0, np.inf, -np.inf])])
-    p = 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
-    want = np.column_stack([1 - p, p])
-    got = em._binary_proba_columns(F)
-    assert got.dtype == want.dtype and got.shape == want.shape
-    assert np.array_equal(got.view(np.uint64), want.view(np.uint64))
-    monkeypatch.setattr(em, "_PROBA_THREAD_ROWS", 1 << 40)  # the one-piece path
-    assert np.array_equal(em._binary_proba_columns(F).view(np.uint64), want.view(np.uint64))

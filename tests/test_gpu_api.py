@@ -181,3 +181,38 @@ def test_score_and_batch_parallel_predictions(engine, bin_data, monkeypatch):
     monkeypatch.setattr(est_mod, "_BATCH_ROWS", 150)  # slices of 140 rows
     np.testing.assert_array_equal(m.predict_batch_parallel(X, batch_size=70), pred)
     np.testing.assert_array_equal(m.predict_proba_batch_parallel(X, batch_size=70), proba)
+
+
+def test_predict_proba_device_equals_numpy_expression(engine, bin_data):
+    """A binary model's predict_proba, computed on the device from F
+    (bsscl_predict_proba), against NumPy's expression on the same F
+    (est:3335-3336): within 2 ulp of 1, and mostly bit-identical (the
+    device's exp and NumPy's may round a last bit differently).  Scores far
+    past the clip (|F| > 500) saturate as NumPy's do."""
+    from bsscl_gbm import estimator as est_mod
+    X, y = bin_data
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=30, max_depth=4, random_state=0,
+                                 verbose=False).fit(X, y)
+    rng = np.random.default_rng(1)
+    Xp = np.vstack([X, rng.standard_normal((20000, X.shape[1])) * 3.0])
+    F = m._raw_score(Xp)
+    p = 1.0 / (1.0 + np.exp(-np.clip(F, -500, 500)))
+    want = np.column_stack([1 - p, p])
+    got = m.predict_proba(Xp)
+    worst = float(np.max(np.abs(got - want))) / np.finfo(np.float64).eps
+    same = float(np.mean(got == want))
+    print(f"[result] predict_proba on the device: {100 * same:.3f}% bit-identical, "
+          f"max |diff| {worst:.2f} ulp(1)", flush=True)
+    assert worst <= 2.0 and same >= 0.9
+    np.testing.assert_array_equal(m.predict(Xp), m.classes_[(want[:, 1] > 0.5).astype(int)])
+    # One-leaf trees worth +-1000: F past the clip on either side (p then
+    # exactly 1, or exp(500)'s last bit apart), and exactly 0 (p = 0.5).
+    eng = est_mod._engine(0)
+    packed = {"features": np.array([-1, -1], np.int16), "thresholds": np.zeros(2, np.int64),
+              "values": np.array([1000.0, -1000.0]), "left": np.full(2, -1, np.int32),
+              "right": np.full(2, -1, np.int32), "offsets": np.array([0, 1, 2], np.int32)}
+    for n_trees, base in ((1, 0.0), (2, 0.0), (1, 1e4), (1, -2000.0)):
+        got = eng.predict_proba(1, len(Xp), packed, n_trees, 1.0, base)
+        F2 = eng.predict(1, len(Xp), packed, n_trees, 1.0) + base
+        p2 = 1.0 / (1.0 + np.exp(-np.clip(F2, -500, 500)))
+        np.testing.assert_allclose(got, np.column_stack([1 - p2, p2]), rtol=4.5e-16, atol=0)
