@@ -344,6 +344,7 @@ struct bsscl_engine {
   // trees take their scales there.
   bool mc_scales_host = false;
   double mc_hbound = 0.0;  // no multiclass hessian exceeds this (max weight / 4)
+  DevBuf<int32_t> mc_feat_d;  // the round's engine columns (its root codes' gather)
   // A multiclass round's K trees as the device replayed them: K blocks of
   // round_out_bytes(2 * max_leaves + 2), and their pinned readback.
   DevBuf<char> mc_out_d;
@@ -358,6 +359,12 @@ struct bsscl_engine {
   DevBuf<GH> gh_c[4];
   DevBuf<int32_t> rid_c[2];  // with set_base 0 only
   int32_t set_base = 0;
+  // A tree's root rows in another set than set_base (-1: set_base).  Its
+  // levels then never write it, so the root codes of a multiclass round,
+  // gathered once, serve all its classes (root_codes_ready: the root's
+  // gather brings the (g,h) alone).
+  int32_t root_set = -1;
+  bool root_codes_ready = false;
   // A boosting round's root inputs (RootPack), uploaded by the rows stream
   // into the slot's own arena.
   DevBuf<char> root_d[2];
@@ -1181,6 +1188,9 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
   for (int s = 0; s < 2; ++s)
     grow = grow || E->codes_c[b + s].cap < (size_t)ld_c * F_sel ||
            E->gh_c[b + s].cap < (size_t)ld_c || (b == 0 && E->rid_c[s].cap < (size_t)ld_c);
+  const int r = E->root_set;
+  if (r >= 0)
+    grow = grow || E->codes_c[r].cap < (size_t)ld_c * F_sel || E->gh_c[r].cap < (size_t)ld_c;
   int32_t cap = std::max(initial_node_cap(levels, max_leaves), E->node_cap_floor);
   // Test hook: a small starting node table, to exercise the regrowth path.
   if (const char *t = std::getenv("BSSCL_TEST_NODE_CAP")) {
@@ -1208,6 +1218,10 @@ int prepare_tree_buffers(bsscl_engine *E, int64_t m, int32_t F_sel, int32_t leve
     CHK(E->codes_c[b + s].ensure((size_t)ld_c * F_sel));
     CHK(E->gh_c[b + s].ensure((size_t)ld_c));
     if (b == 0) CHK(E->rid_c[s].ensure((size_t)ld_c));
+  }
+  if (r >= 0) {
+    CHK(E->codes_c[r].ensure((size_t)ld_c * F_sel));
+    CHK(E->gh_c[r].ensure((size_t)ld_c));
   }
   CHK(E->tiles_d.ensure((size_t)tcap));
   CHK(E->tile_cnt_d.ensure(4 * (size_t)tcap + 8));  // a 16-byte read past the last tile
@@ -1300,7 +1314,7 @@ int launch_root(bsscl_engine *E, const int32_t *rows32, int64_t m,
                 const std::vector<int32_t> &feats,
                 const std::vector<int32_t> &nb_sel, const TreeParams &tp, bool gathered,
                 const PreRoot *pre = nullptr) {
-  const int b = E->set_base;
+  const int b = E->root_set >= 0 ? E->root_set : E->set_base;
   const Matrix &X = E->mat[0];
   const int32_t F_sel = (int32_t)feats.size();
   std::vector<char *> dv;
@@ -1324,8 +1338,10 @@ int launch_root(bsscl_engine *E, const int32_t *rows32, int64_t m,
   E->hot_sel_d = E->nb_sel_d + F_sel;
   // (A boosting round's root rows are already in set b: launch_gather_codes
   // and launch_gather_gh.)
+  // (With the root's codes already in place, the gather brings the (g,h)
+  // alone: no feature columns.)
   if (!gathered)
-    HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, feat_d, F_sel,
+    HIPCHK(launch_gather_root(E->st, X.codes.p, X.ld, feat_d, E->root_codes_ready ? 0 : F_sel,
                               rows32, rows32 ? nullptr : E->rows64.p, m, E->ghq.p,
                               E->codes_c[b].p, E->ld_c, E->gh_c[b].p,
                               E->track_rid && b == 0 ? E->rid_c[0].p : nullptr,
@@ -1365,7 +1381,9 @@ int32_t level_mode(const bsscl_engine *E, int32_t level) {
 // a grouped level's: its grandparents'); a moving level writes the other
 // set of the tree's pair.
 int level_src(const bsscl_engine *E, int32_t level) {
-  return E->set_base + (E->pair_levels ? ((level >> 1) & 1) : (level & 1));
+  const int32_t q = E->pair_levels ? (level >> 1) : level;  // moves made before the level
+  if (q == 0 && E->root_set >= 0) return E->root_set;
+  return E->set_base + (q & 1);
 }
 
 // Whether every split a node can take is kept when popped (est:678-683):
@@ -1479,7 +1497,7 @@ int launch_level(bsscl_engine *E, int32_t level, bool last, int64_t m,
                  const TreeParams &tp, int32_t F_sel) {
   const int32_t mode = level_mode(E, level);
   const int src = level_src(E, level);
-  const int dst = E->set_base + ((src - E->set_base) ^ 1);
+  const int dst = level_src(E, level + 1);  // where a moving level writes its rows
   const PartParent *par = E->parents_d[level & 1].p;
   const PartGroup *grp = mode == kLevelGrouped ? E->groups_d.p : nullptr;
   const bool in_place = mode == kLevelInPlace;
@@ -2645,8 +2663,24 @@ int mc_trees_device(bsscl_engine *E, const std::vector<int32_t> &feats,
   CHK(E->tree_d.ensure((size_t)M));
   CHK(E->mc_out_d.ensure(per * (size_t)K));
   CHK(ensure_host_pinned(E, E->mc_out_pin, E->mc_out_pin_bytes, per * (size_t)K));
+  // The K trees share their rows and features: the round's root codes are
+  // gathered once into set 2, which the trees' levels never write (they
+  // alternate between sets 0 and 1), and each class's root gathers its
+  // (g,h) alone.
   E->set_base = 0;
+  E->root_set = 2;
+  struct RootReset {
+    bsscl_engine *e;
+    ~RootReset() {
+      e->root_set = -1;
+      e->root_codes_ready = false;
+    }
+  } root_reset{E};
   CHK(prepare_tree_buffers(E, m, F_sel, std::max(1, tp.max_depth), tp.max_leaves));
+  CHK(upload(E, E->mc_feat_d, feats.data(), feats.size()));
+  HIPCHK(launch_gather_codes(E->st, X.codes.p, X.ld, E->mc_feat_d.p, F_sel, E->mc_rows32, m,
+                             E->codes_c[2].p, E->ld_c, E->ld_c));
+  E->root_codes_ready = true;
   for (int32_t k = 0; k < K; ++k) {
     // The class's fixed point: from the maxima the host read back, or from
     // those on the device (the same multipliers, dev_fixed_mul), with the
@@ -2679,6 +2713,9 @@ int mc_trees_device(bsscl_engine *E, const std::vector<int32_t> &feats,
   HIPCHK(hipMemcpyAsync(E->mc_out_pin, E->mc_out_d.p, per * (size_t)K, hipMemcpyDeviceToHost,
                         E->st));
   CHK(sync(E));
+  // (A class rebuilt on the host-driven path below gathers its own root.)
+  E->root_set = -1;
+  E->root_codes_ready = false;
   for (int32_t k = 0; k < K; ++k) {
     TreeOut o = out(k);
     const char *base = E->mc_out_pin + (size_t)k * per;
@@ -2911,6 +2948,7 @@ void bsscl_engine_destroy(bsscl_engine *E) {
   E->mc_y.release();
   E->mc_max.release();
   E->mc_out_d.release();
+  E->mc_feat_d.release();
   if (E->mc_out_pin) (void)hipHostFree(E->mc_out_pin);
   E->level_args_d.release();
   E->lvl_d.release();
