@@ -2667,8 +2667,11 @@ int mc_trees_device(bsscl_engine *E, const std::vector<int32_t> &feats,
   // gathered once into set 2, which the trees' levels never write (they
   // alternate between sets 0 and 1), and each class's root gathers its
   // (g,h) alone.
+  // (Rows given as int64 by bsscl_mc_round have no int32 list for that
+  // gather: each class then gathers its root itself.)
+  const bool shared_root = E->mc_rows32 != nullptr;
   E->set_base = 0;
-  E->root_set = 2;
+  E->root_set = shared_root ? 2 : -1;
   struct RootReset {
     bsscl_engine *e;
     ~RootReset() {
@@ -2677,10 +2680,12 @@ int mc_trees_device(bsscl_engine *E, const std::vector<int32_t> &feats,
     }
   } root_reset{E};
   CHK(prepare_tree_buffers(E, m, F_sel, std::max(1, tp.max_depth), tp.max_leaves));
-  CHK(upload(E, E->mc_feat_d, feats.data(), feats.size()));
-  HIPCHK(launch_gather_codes(E->st, X.codes.p, X.ld, E->mc_feat_d.p, F_sel, E->mc_rows32, m,
-                             E->codes_c[2].p, E->ld_c, E->ld_c));
-  E->root_codes_ready = true;
+  if (shared_root) {
+    CHK(upload(E, E->mc_feat_d, feats.data(), feats.size()));
+    HIPCHK(launch_gather_codes(E->st, X.codes.p, X.ld, E->mc_feat_d.p, F_sel, E->mc_rows32, m,
+                               E->codes_c[2].p, E->ld_c, E->ld_c));
+    E->root_codes_ready = true;
+  }
   for (int32_t k = 0; k < K; ++k) {
     // The class's fixed point: from the maxima the host read back, or from
     // those on the device (the same multipliers, dev_fixed_mul), with the

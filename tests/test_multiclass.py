@@ -388,3 +388,43 @@ def test_multiclass_round_ahead_handed_back(engine):
     c = HybridHistGBMNumbaV1_0_1(**params).fit(X, yb)
     d = HybridHistGBMNumbaV1_0_1(**params).fit(X, yb)
     assert c.train_loss_history_ == d.train_loss_history_
+
+
+@pytest.mark.gpu
+def test_multiclass_trees_from_int64_rows(engine):
+    """A round whose rows come as int64 sample indices (bsscl_mc_round, in
+    the reference's order) has no int32 row list: mc_build_trees then
+    gathers each class's root itself.  Its trees and scores equal the
+    per-class path's (mc_build_tree) on a second engine from the same
+    state."""
+    from bsscl_gbm import _native
+    rng = np.random.default_rng(81)
+    n, F, K = 20000, 12, 4
+    codes = rng.integers(0, 40, (n, F)).astype(np.uint8)
+    y = rng.integers(0, K, n).astype(np.int64)
+    w = rng.uniform(0.5, 2.0, n)
+    bc = np.full(F, 40, np.int32)
+    rows = rng.permutation(n)[: int(0.8 * n)].astype(np.int64)
+    feats = np.sort(rng.permutation(F)[:9]).astype(np.int32)
+    args = (31, 5, 5, 3.0, bc, 40, 1.0, 0.0, 0.3)
+    other = _native.Engine(0)
+    try:
+        got = {}
+        for name, eng in (("batched", engine), ("per_class", other)):
+            eng.load_codes(0, codes)
+            eng.mc_begin(y, K, w)
+            eng.mc_round(rows)
+            if name == "batched":
+                trees = eng.mc_build_trees(feats, *args)
+            else:
+                trees = [eng.mc_build_tree(k, feats, *args) for k in range(K)]
+            got[name] = (trees, eng.mc_scores())
+        (ta, fa), (tb, fb) = got["batched"], got["per_class"]
+        for k in range(K):
+            nc = ta[k][5]
+            assert nc == tb[k][5] and nc > 1, k
+            for i in (0, 1, 2, 3, 4, 6):
+                np.testing.assert_array_equal(ta[k][i][:nc], tb[k][i][:nc], err_msg=str(k))
+        np.testing.assert_array_equal(fa, fb)
+    finally:
+        other.close()
