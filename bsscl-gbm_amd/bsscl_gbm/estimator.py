@@ -143,10 +143,12 @@ def _row_blocks(n, fn):
 
 
 def _take(table, idx):
-    """table[idx] for a small float64 table and integer indices: the same
-    values, gathered in row blocks."""
+    """table[idx] for a small float64 table and integer indices already in
+    range (encoded labels): the same values, gathered in row blocks.  (With
+    an output array, np.take's default mode buffers the whole gather to
+    check the indices; 'clip' writes in place, 2.6x faster at 1M rows.)"""
     out = np.empty(len(idx), dtype=np.float64)
-    _row_blocks(len(idx), lambda a, b: np.take(table, idx[a:b], out=out[a:b]))
+    _row_blocks(len(idx), lambda a, b: np.take(table, idx[a:b], out=out[a:b], mode='clip'))
     return out
 
 
@@ -154,11 +156,54 @@ def _count_nonzero(y):
     return sum(_row_blocks(len(y), lambda a, b: int(np.count_nonzero(y[a:b]))))
 
 
+class _HostPrep:
+    """A fit's host work that needs only the labels, on a thread of its own
+    while the caller stages and bins X: the bagging stream's sampler
+    (est:2502-2517) and, for a binary fit, its class weights and base score
+    (est:2570-2603, 2829-2834).  NumPy's loops and the native calls release
+    the GIL, so both threads run at once (1M x 28: the 2.6 ms of these
+    passes overlap the binning instead of preceding the first round)."""
+
+    def __init__(self, est, eng, rng, y):
+        self._sampler = None
+        self._binary = None
+        self._error = None
+        self._thread = threading.Thread(target=self._run, args=(est, eng, rng, y),
+                                        name="bsscl-fit-prep", daemon=True)
+        self._thread.start()
+
+    def _run(self, est, eng, rng, y):
+        # (The label passes first: the sampler's start contends less with
+        # the staging copy after it, and its first round still has the
+        # binning's remaining time to draw.)
+        try:
+            if not est._is_multiclass:
+                self._binary = est._binary_start(y)
+            self._sampler = est._make_sampler(eng, rng, len(y))
+        except BaseException as e:  # handed to the fitting thread
+            self._error = e
+
+    def result(self):
+        """(sampler, (w0, w1, base score) or None); raises what the thread
+        raised."""
+        self._thread.join()
+        if self._error is not None:
+            raise self._error
+        return self._sampler, self._binary
+
+    def close(self):
+        self._thread.join()
+        if self._sampler is not None:
+            self._sampler.close()
+            self._sampler = None
+
+
 def _percentile_ranks(m, q100, dtype):
     """Ranks np.percentile(col, q100) reads from a NaN-free column of m
     values of `dtype`, and its interpolation weights (NumPy 2.x 'linear'
     method: q = q100 / dtype(100), virtual index (m - 1) * q, neighbours
-    floor and floor + 1, both clamped to the last value at or beyond it)."""
+    floor and floor + 1, both clamped to the last value at or beyond it).
+    m may be a column vector of lengths: then row i is column i's."""
     q = np.true_divide(q100, dtype.type(100))
     vi = (m - 1) * q
     prev = np.floor(vi)
@@ -420,20 +465,30 @@ class HybridHistGBMNumbaV1_0_1:
                 edges[j] = e
             else:
                 lerp_cols.append((j, m, min(max_numeric_bins + 1, int(n_unique[j]))))
-        # One gather for every rank the percentiles read.
-        plans, cols, pos = [], [], []
+        # One gather for every rank the percentiles read.  Columns with the
+        # same number of quantiles share each NumPy call, one row per column
+        # (the arithmetic is elementwise, so every value is the one the
+        # column's own call gives).
+        by_k = {}
         for j, m, k in lerp_cols:
+            by_k.setdefault(k, []).append((j, m))
+        plans, cols, pos, off = [], [], [], 0
+        for k, members in by_k.items():
+            js = np.array([j for j, _ in members], dtype=np.int32)
+            ms = np.array([m for _, m in members], dtype=np.int64)[:, None]
             q = np.linspace(0, 1, k)
-            lo, hi, gamma = _percentile_ranks(m, q * 100, dtype)
-            plans.append((j, len(cols), k, gamma))
-            cols.extend([j] * (2 * k))
-            pos.extend(lo.tolist())
-            pos.extend(hi.tolist())
-        vals = eng.sorted_gather(cols, pos).astype(dtype) if cols else None
-        for j, off, k, gamma in plans:
-            a = vals[off:off + k]
-            b = vals[off + k:off + 2 * k]
-            edges[j] = np.unique(_percentile_lerp(a, b, gamma))
+            lo, hi, gamma = _percentile_ranks(ms, q * 100, dtype)
+            plans.append((js, off, k, gamma))
+            cols.append(np.repeat(js, 2 * k))
+            pos.append(np.concatenate([lo, hi], axis=1).ravel())
+            off += 2 * k * len(js)
+        if plans:
+            vals = eng.sorted_gather(np.concatenate(cols), np.concatenate(pos)).astype(dtype)
+            for js, off, k, gamma in plans:
+                v = vals[off:off + 2 * k * len(js)].reshape(len(js), 2 * k)
+                lerp = _percentile_lerp(v[:, :k], v[:, k:], gamma)
+                for i, j in enumerate(js):
+                    edges[j] = np.unique(lerp[i])
         for j in range(n_features):
             if bin_counts[j] == 1 and self._nan_bin_id[j] == 0 and nan_count[j] == n:
                 continue
@@ -582,12 +637,14 @@ class HybridHistGBMNumbaV1_0_1:
         with eng.lock:
             # The bagging stream (est:2502-2517) starts drawing now, so that its
             # first rounds are ready when the boosting loop begins: the draws
-            # run on host threads while the device bins X.
-            sampler = self._make_sampler(eng, rng, len(y))
+            # run on host threads while the device bins X.  The sampler is made,
+            # and a binary fit's class weights and base score are computed, on
+            # a thread of their own meanwhile: they need only the labels.
+            prep = _HostPrep(self, eng, rng, y)
             try:
-                self._fit_locked(eng, X, y, X_val, y_val, sample_weight, sampler)
+                self._fit_locked(eng, X, y, X_val, y_val, sample_weight, prep)
             finally:
-                sampler.close()
+                prep.close()
         self._pack_trees()
         self._compute_feature_importances()
         if self.verbose:
@@ -616,7 +673,7 @@ class HybridHistGBMNumbaV1_0_1:
                                             or self.n_classes_ <= _native.MC_DEVICE_MAX_CLASSES),
                                device=eng.device)
 
-    def _fit_locked(self, eng, X, y, X_val, y_val, sample_weight, sampler):
+    def _fit_locked(self, eng, X, y, X_val, y_val, sample_weight, prep):
         """Binning and the boosting loop, with the engine's lock held."""
         t0 = time.perf_counter()
         # Unweighted edges come from the device (X is staged once and binned
@@ -649,15 +706,16 @@ class HybridHistGBMNumbaV1_0_1:
             n_val = X_val.shape[0]
 
         t0_train = time.perf_counter()
+        sampler, binary_start = prep.result()
         if self._is_multiclass:
             self._fit_multiclass(eng, y, n_val, y_val, sampler)
         else:
-            self._fit_binary(eng, y, n_val, y_val, sampler)
+            self._fit_binary(eng, y, n_val, y_val, sampler, binary_start)
         self.times['training'] = (time.perf_counter() - t0_train) * 1000
 
-    def _fit_binary(self, eng, y, n_val, y_val, sampler):
-        n_samples = len(y)
-        n_features = self.n_features_in_
+    def _binary_start(self, y):
+        """A binary fit's class weights (w0, w1) and base score, from the
+        labels alone."""
         w0, w1 = self._class_weight_pair(y)
         # np.average(y, weights=np.where(y == 1, w1, w0)) of the reference
         # (est:2829-2834): sum(y * w) / sum(w) over the same float64 arrays,
@@ -665,7 +723,10 @@ class HybridHistGBMNumbaV1_0_1:
         sw = _take(np.array([w0, w1]), y)
         weighted_mean = _take(np.array([0.0, w1]), y).sum() / sw.sum()
         p0 = np.clip(weighted_mean, 1e-7, 1.0 - 1e-7)
-        self.base_score_ = np.log(p0 / (1.0 - p0))
+        return w0, w1, np.log(p0 / (1.0 - p0))
+
+    def _fit_binary(self, eng, y, n_val, y_val, sampler, binary_start):
+        w0, w1, self.base_score_ = binary_start
         F_val = np.full(n_val, self.base_score_) if n_val else None
         eng.boost_begin(y, w0, w1, self.base_score_)
         best_val_loss = np.inf

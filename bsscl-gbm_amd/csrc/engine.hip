@@ -116,6 +116,15 @@ struct TempBuf : DevBuf<T> {
   TempBuf() : DevBuf<T>(false) {}
 };
 
+// A TempBuf local to one call: freed when the call returns, on every path.
+template <typename T>
+struct ScopedBuf : TempBuf<T> {
+  ScopedBuf() = default;
+  ScopedBuf(const ScopedBuf &) = delete;
+  ScopedBuf &operator=(const ScopedBuf &) = delete;
+  ~ScopedBuf() { this->release(); }
+};
+
 // Pinned host staging for the small per-level uploads and readbacks.  Reset
 // only after a stream synchronisation, when no copy still reads from it.
 struct PinnedArena {
@@ -461,6 +470,16 @@ struct bsscl_engine {
   int64_t col_ld = 0;
   bool cols_sorted = false;
   std::vector<int64_t> col_m;  // non-NaN values per sorted column
+  // The column sort's work buffers: the keys' other half of each pass,
+  // digit counts and totals, per-column counts.
+  TempBuf<unsigned char> col_tmp;
+  TempBuf<uint32_t> col_counts, col_totals;
+  TempBuf<int64_t> col_m_d;
+  TempBuf<unsigned long long> col_changes_d;
+  // bsscl_sorted_gather's columns, ranks and values.
+  TempBuf<int32_t> gather_c;
+  TempBuf<int64_t> gather_p;
+  TempBuf<double> gather_o;
 
   // Histogram launch shape of the current tree (see read_hist_tuning,
   // hist_fchunk, hist_tile_rows); tunable with BSSCL_HIST_FC,
@@ -797,6 +816,28 @@ int host_download(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
   }
   return BSSCL_OK;
 }
+
+// The staged matrix, its sorted columns and the sort's work buffers.
+void release_staging(bsscl_engine *E) {
+  E->xstage.release();
+  E->col_keys.release();
+  E->col_tmp.release();
+  E->col_counts.release();
+  E->col_totals.release();
+  E->col_m_d.release();
+  E->col_changes_d.release();
+  E->gather_c.release();
+  E->gather_p.release();
+  E->gather_o.release();
+  E->xs_n = 0;
+  E->cols_sorted = false;
+  E->col_m.clear();
+}
+
+// Staging memory up to this size stays allocated for the next fit's
+// staging (1M x 28 float32: 0.75 ms of hipFree and the allocations again,
+// in a 47 ms fit); larger staging is freed when the edges are done.
+constexpr size_t kStagingKeptBytes = size_t(1) << 30;
 
 int check_matrix(bsscl_engine *E, int32_t slot) {
   if (slot < 0 || slot > 1) return set_error(BSSCL_EINVAL, "matrix slot must be 0 or 1");
@@ -2996,8 +3037,7 @@ void bsscl_engine_destroy(bsscl_engine *E) {
     if (E->xfer_ev[b]) (void)hipEventDestroy(E->xfer_ev[b]);
   }
   E->xchunk.release();
-  E->xstage.release();
-  E->col_keys.release();
+  release_staging(E);
   for (hipEvent_t ev : E->ev_pool) (void)hipEventDestroy(ev);
   for (hipEvent_t ev : E->rows_ready)
     if (ev) (void)hipEventDestroy(ev);
@@ -3089,7 +3129,6 @@ int bsscl_stage_features(bsscl_engine *E, const void *X, int32_t x_is_f64, int64
     return set_error(BSSCL_EINVAL, "stage_features: bad shape");
   HIPCHK(hipSetDevice(E->device));
   E->cols_sorted = false;
-  E->col_keys.release();
   E->col_m.clear();
   const size_t bytes = (size_t)n * F * (x_is_f64 ? 8 : 4);
   CHK(E->xstage.ensure(bytes));
@@ -3113,27 +3152,24 @@ int bsscl_sort_columns(bsscl_engine *E, int64_t *nan_count, int64_t *n_unique) {
   const size_t ksz = f64 ? 8 : 4;
   E->cols_sorted = false;
   CHK(E->col_keys.ensure((size_t)F * ld * ksz));
-  TempBuf<unsigned char> tmp;
-  TempBuf<uint32_t> counts, totals;
-  TempBuf<int64_t> m_d;
-  TempBuf<unsigned long long> changes_d;
-  int rc = tmp.ensure((size_t)F * ld * ksz);
-  if (rc == BSSCL_OK) rc = counts.ensure((size_t)col_sort_count_words(n, F, f64));
-  if (rc == BSSCL_OK) rc = totals.ensure((size_t)F * 256);
-  if (rc == BSSCL_OK) rc = m_d.ensure((size_t)F);
-  if (rc == BSSCL_OK) rc = changes_d.ensure((size_t)F);
-  if (rc != BSSCL_OK) return rc;
+  CHK(E->col_tmp.ensure((size_t)F * ld * ksz));
+  CHK(E->col_counts.ensure((size_t)col_sort_count_words(n, F, f64)));
+  CHK(E->col_totals.ensure((size_t)F * 256));
+  CHK(E->col_m_d.ensure((size_t)F));
+  CHK(E->col_changes_d.ensure((size_t)F));
   std::vector<int64_t> m(F);
   std::vector<unsigned long long> changes(F);
-  hipError_t e = launch_col_sort(E->st, E->xstage.p, f64, n, F, E->col_keys.p, tmp.p, ld,
-                                 counts.p, totals.p, m_d.p);
-  if (e == hipSuccess) e = hipMemsetAsync(changes_d.p, 0, (size_t)F * 8, E->st);
+  hipError_t e = launch_col_sort(E->st, E->xstage.p, f64, n, F, E->col_keys.p, E->col_tmp.p, ld,
+                                 E->col_counts.p, E->col_totals.p, E->col_m_d.p);
+  if (e == hipSuccess) e = hipMemsetAsync(E->col_changes_d.p, 0, (size_t)F * 8, E->st);
   if (e == hipSuccess)
-    e = launch_col_changes(E->st, E->col_keys.p, f64, ld, F, m_d.p, n, changes_d.p);
+    e = launch_col_changes(E->st, E->col_keys.p, f64, ld, F, E->col_m_d.p, n,
+                           E->col_changes_d.p);
   if (e == hipSuccess)
-    e = hipMemcpyAsync(m.data(), m_d.p, (size_t)F * 8, hipMemcpyDeviceToHost, E->st);
+    e = hipMemcpyAsync(m.data(), E->col_m_d.p, (size_t)F * 8, hipMemcpyDeviceToHost, E->st);
   if (e == hipSuccess)
-    e = hipMemcpyAsync(changes.data(), changes_d.p, (size_t)F * 8, hipMemcpyDeviceToHost, E->st);
+    e = hipMemcpyAsync(changes.data(), E->col_changes_d.p, (size_t)F * 8,
+                       hipMemcpyDeviceToHost, E->st);
   if (e == hipSuccess) e = hipStreamSynchronize(E->st);
   if (e != hipSuccess)
     return set_error(BSSCL_EDEVICE, std::string("sort_columns: ") + hipGetErrorString(e));
@@ -3159,19 +3195,18 @@ int bsscl_sorted_gather(bsscl_engine *E, int64_t count, const int32_t *col, cons
       return set_error(BSSCL_EINVAL, "sorted_gather: position outside the column's values");
   }
   HIPCHK(hipSetDevice(E->device));
-  TempBuf<int32_t> c_d;
-  TempBuf<int64_t> p_d;
-  TempBuf<double> o_d;
-  CHK(c_d.ensure((size_t)count));
-  CHK(p_d.ensure((size_t)count));
-  CHK(o_d.ensure((size_t)count));
-  hipError_t e = hipMemcpyAsync(c_d.p, col, (size_t)count * 4, hipMemcpyHostToDevice, E->st);
+  CHK(E->gather_c.ensure((size_t)count));
+  CHK(E->gather_p.ensure((size_t)count));
+  CHK(E->gather_o.ensure((size_t)count));
+  hipError_t e =
+      hipMemcpyAsync(E->gather_c.p, col, (size_t)count * 4, hipMemcpyHostToDevice, E->st);
   if (e == hipSuccess)
-    e = hipMemcpyAsync(p_d.p, pos, (size_t)count * 8, hipMemcpyHostToDevice, E->st);
+    e = hipMemcpyAsync(E->gather_p.p, pos, (size_t)count * 8, hipMemcpyHostToDevice, E->st);
   if (e == hipSuccess)
-    e = launch_col_gather(E->st, E->col_keys.p, E->xs_f64, E->col_ld, count, c_d.p, p_d.p, o_d.p);
+    e = launch_col_gather(E->st, E->col_keys.p, E->xs_f64, E->col_ld, count, E->gather_c.p,
+                          E->gather_p.p, E->gather_o.p);
   if (e == hipSuccess)
-    e = hipMemcpyAsync(out, o_d.p, (size_t)count * 8, hipMemcpyDeviceToHost, E->st);
+    e = hipMemcpyAsync(out, E->gather_o.p, (size_t)count * 8, hipMemcpyDeviceToHost, E->st);
   if (e == hipSuccess) e = hipStreamSynchronize(E->st);
   if (e != hipSuccess)
     return set_error(BSSCL_EDEVICE, std::string("sorted_gather: ") + hipGetErrorString(e));
@@ -3189,8 +3224,8 @@ int bsscl_sorted_uniques(bsscl_engine *E, int32_t col, int32_t max_out, double *
   *count = 0;
   if (m == 0) return BSSCL_OK;
   HIPCHK(hipSetDevice(E->device));
-  TempBuf<int64_t> p_d;
-  TempBuf<unsigned int> cnt_d;
+  ScopedBuf<int64_t> p_d;
+  ScopedBuf<unsigned int> cnt_d;
   CHK(p_d.ensure((size_t)std::max(max_out, 1)));
   CHK(cnt_d.ensure(1));
   unsigned int cnt = 0;
@@ -3218,12 +3253,15 @@ int bsscl_sorted_uniques(bsscl_engine *E, int32_t col, int32_t max_out, double *
 int bsscl_release_staged(bsscl_engine *E) {
   if (!E) return set_error(BSSCL_EINVAL, "release_staged: null engine");
   HIPCHK(hipSetDevice(E->device));
-  HIPCHK(hipStreamSynchronize(E->st));
-  E->xstage.release();
   E->xs_n = 0;
-  E->col_keys.release();
   E->cols_sorted = false;
   E->col_m.clear();
+  // (Kept buffers are next written by work on E->st, after what reads them.)
+  const size_t held = E->xstage.cap + E->col_keys.cap + E->col_tmp.cap;
+  if (held > kStagingKeptBytes) {
+    HIPCHK(hipStreamSynchronize(E->st));
+    release_staging(E);
+  }
   return BSSCL_OK;
 }
 

@@ -92,6 +92,10 @@ int bsscl_get_codes_u16(bsscl_engine *eng, int32_t slot, uint16_t *codes_out);
  *
  * bsscl_stage_features copies X (row-major n x F, float32 or float64) to the
  * device, where it stays until bsscl_release_staged or the next staging.
+ * bsscl_release_staged ends the staged matrix; its memory, with the sorted
+ * columns', stays allocated for the next staging while the three buffers
+ * hold at most 1 GiB together (freed by bsscl_engine_destroy), and is freed
+ * otherwise.
  * bsscl_bin_features with X = NULL then bins the staged matrix (same n, F
  * and dtype) without a second upload.
  *

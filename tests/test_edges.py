@@ -69,6 +69,27 @@ def test_percentile_restatement_is_bit_exact(name, k):
     assert _same_values(got, want)
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("k", [3, 256])
+def test_percentile_restatement_batched_over_columns(dtype, k):
+    """The estimator's batched form (one row per column, column lengths as a
+    column vector) gives every column np.percentile(col, q * 100) bit for
+    bit, as the single-column form does."""
+    rng = np.random.default_rng(11)
+    cols = [rng.standard_normal(m).astype(dtype) for m in (1, 2, 5, 999, 1000, 65_537)]
+    cols.append(np.round(rng.standard_normal(4000) * 2).astype(dtype))
+    q = np.linspace(0, 1, k)
+    ms = np.array([len(c) for c in cols], dtype=np.int64)[:, None]
+    lo, hi, gamma = est_mod._percentile_ranks(ms, q * 100, np.dtype(dtype))
+    assert lo.shape == hi.shape == gamma.shape == (len(cols), k)
+    s = [np.sort(c) for c in cols]
+    a = np.stack([s[i][lo[i]] for i in range(len(cols))])
+    b = np.stack([s[i][hi[i]] for i in range(len(cols))])
+    got = est_mod._percentile_lerp(a, b, gamma)
+    for i, c in enumerate(cols):
+        assert _same_values(got[i], np.percentile(c, q * 100)), i
+
+
 def test_percentile_restatement_detects_a_shifted_rank():
     """A plausible slip (rank from n instead of n - 1) changes the result:
     the bit-exact comparison above would catch it."""
@@ -211,3 +232,36 @@ def test_fit_codes_equal_reference_binning(engine):
     want = om.bin_features(X, we, wbc, wnid, "hybrid")
     got = _engine(0).get_codes(0, *X.shape)
     np.testing.assert_array_equal(got, np.minimum(want.astype(np.int64), 255).astype(np.uint8))
+
+
+@pytest.mark.gpu
+def test_staging_and_sorts_keep_device_memory_flat(engine):
+    """Staging, column sorts, gathers and releases, four times over, leave
+    the device's free memory where the first pass left it: the sort's work
+    buffers and the gathers' are kept for the next staging or freed, never
+    dropped (this shape's sort needs 256 MB of them)."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+
+    def free_bytes():
+        free, total = ctypes.c_size_t(), ctypes.c_size_t()
+        assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+        return free.value
+
+    _announce("staging memory over repeated sorts (2M x 16 float32)")
+    rng = np.random.default_rng(3)
+    X = rng.standard_normal((2_000_000, 16)).astype(np.float32)
+    X[:, 1] = rng.integers(0, 5, len(X))
+    frees = []
+    for _ in range(4):
+        engine.stage_features(X)
+        nan, uniq = engine.sort_columns(16)
+        assert nan.sum() == 0 and uniq[1] == 5
+        vals = engine.sorted_gather(np.arange(16), np.zeros(16, np.int64))
+        assert np.array_equal(vals, X.min(axis=0).astype(np.float64))
+        assert np.array_equal(engine.sorted_uniques(1, 8), np.arange(5.0))
+        engine.release_staged()
+        frees.append(free_bytes())
+    print(f"[result] free device memory after each pass (MiB): "
+          f"{[f >> 20 for f in frees]}", flush=True)
+    assert min(frees[1:]) >= frees[0] - (16 << 20), frees
