@@ -3072,8 +3072,8 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
   }
   HIPCHK(hipSetDevice(E->device));
   CHK(alloc_matrix(E, slot, n, F, tiers));
-  TempBuf<double> ed;
-  TempBuf<int32_t> nb, nid;
+  ScopedBuf<double> ed;  // (freed on the error returns as well)
+  ScopedBuf<int32_t> nb, nid;
   CHK(ed.ensure((size_t)F * edge_stride));
   CHK(nb.ensure((size_t)F));
   CHK(nid.ensure((size_t)F));
