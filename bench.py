@@ -204,7 +204,8 @@ CPU_PREDICT_ROWS = 200_000
 def run_predict(model, name, repeats=3):
     """predict_proba of a fresh batch of the workload through the model's
     whole ensemble: rows/s end to end (host float32 in, probabilities out)
-    and per k_predict launch (kernel execution time), with the kernel's
+    and over its k_predict launches (kernel execution time; one launch per
+    row chunk of the call), with the kernel's
     roofline over the algorithmic bytes n * (F + 16) of device-resident
     codes (one code byte per feature, 8 B of output and 8 B of F per row).
     Returns the line's entry and the batch's first CPU_PREDICT_ROWS rows
@@ -221,12 +222,14 @@ def run_predict(model, name, repeats=3):
     t_total = (time.perf_counter() - t) / repeats
     st = eng.stats()
     eng.set_profiling(0)
-    launches = max(st["predict_launches"], 1.0)
-    kernel_s = st["predict_ms"] / 1e3 / launches
+    # predict_proba walks the rows in row chunks, one launch each: a call's
+    # walk time is the sum of its launches'.
+    launches = max(st["predict_launches"] / repeats, 1.0)
+    kernel_s = st["predict_ms"] / 1e3 / repeats
     bytes_ = n * (F + 16)
     achieved = bytes_ / kernel_s / 1e9
-    _progress(f"predict: {n} rows x {len(model.trees)} trees, kernel {1e3 * kernel_s:.2f} ms, "
-              f"end to end {1e3 * t_total:.1f} ms")
+    _progress(f"predict: {n} rows x {len(model.trees)} trees, kernel {1e3 * kernel_s:.2f} ms "
+              f"({launches:.0f} launches), end to end {1e3 * t_total:.1f} ms")
     sample = np.ascontiguousarray(Xp[:CPU_PREDICT_ROWS])
     del Xp
     return {
@@ -236,7 +239,9 @@ def run_predict(model, name, repeats=3):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": None, "kernel": "k_predict",
-                     "avg_launch_us": round(1e6 * kernel_s, 1), "bytes_per_launch": bytes_},
+                     "launches_per_call": round(launches),
+                     "avg_launch_us": round(1e6 * kernel_s / launches, 1),
+                     "bytes_per_launch": round(bytes_ / launches)},
     }, sample
 
 

@@ -55,6 +55,8 @@ _SIGS = {
     "bsscl_mc_get_grad_hess": [_P, _P, _P],
     "bsscl_predict": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _P],
     "bsscl_predict_proba": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _f64, _P],
+    "bsscl_predict_proba_rows": [_P, _P, _i32, _i64, _i32, _P, _i32, _P, _P, _P, _P, _P, _P,
+                                 _P, _P, _i32, _f64, _f64, _P],
     "bsscl_predict_tree": [_P, _i32, _P, _P, _P, _P, _P, _i32, _P],
     "bsscl_predict_noalloc": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _P],
     "bsscl_node_split": [_P, _P, _P, _P, _i64, _P, _i32, _P, _f64, _f64, _P, _P,
@@ -420,6 +422,31 @@ class Engine:
         check(lib().bsscl_predict_proba(self.handle, int(slot), ptr(f), ptr(t), ptr(v),
                                         ptr(l), ptr(r), ptr(o), int(n_trees),
                                         float(learning_rate), float(base_score), ptr(out)))
+        return out
+
+    def predict_proba_rows(self, X, edges_2d, bin_counts, nan_bin_id, packed, n_trees,
+                           learning_rate, base_score):
+        """bsscl_predict_proba_rows: a binary model's (1 - p, p) of host rows
+        X, shape (n, 2), binned and walked on the device in overlapped row
+        chunks; matrix slots are left as they were."""
+        X = np.ascontiguousarray(X)
+        if X.dtype not in (np.float32, np.float64):
+            X = X.astype(np.float64)
+        n, F = X.shape
+        e = np.ascontiguousarray(edges_2d, dtype=np.float64)
+        bc = np.ascontiguousarray(bin_counts, dtype=np.int32)
+        ni = np.ascontiguousarray(nan_bin_id, dtype=np.int32)
+        f = np.ascontiguousarray(packed["features"], np.int16)
+        t = np.ascontiguousarray(packed["thresholds"], np.int64)
+        v = np.ascontiguousarray(packed["values"], np.float64)
+        l = np.ascontiguousarray(packed["left"], np.int32)
+        r = np.ascontiguousarray(packed["right"], np.int32)
+        o = np.ascontiguousarray(packed["offsets"], np.int32)
+        out = np.empty((n, 2), np.float64)
+        check(lib().bsscl_predict_proba_rows(
+            self.handle, ptr(X), int(X.dtype == np.float64), n, F, ptr(e), e.shape[1], ptr(bc),
+            ptr(ni), ptr(f), ptr(t), ptr(v), ptr(l), ptr(r), ptr(o), int(n_trees),
+            float(learning_rate), float(base_score), ptr(out)))
         return out
 
     def predict_noalloc(self, slot, packed, n_trees, learning_rate, out_dev_ptr):

@@ -978,6 +978,20 @@ class HybridHistGBMNumbaV1_0_1:
         if X.ndim != 2 or X.shape[1] != self.n_features_in_:
             raise ValueError(f"X must have {self.n_features_in_} features")
         eng = _engine(self._device_index())
+        if proba and not self._is_multiclass:
+            # Binning, walk and probabilities in one call, its row chunks'
+            # uploads overlapping the device's work on the chunk before.
+            packed = {'features': self._packed_features, 'thresholds': self._packed_thresholds,
+                      'values': self._packed_values, 'left': self._packed_left,
+                      'right': self._packed_right, 'offsets': self._tree_offsets}
+            with eng.lock:
+                t0 = time.perf_counter()
+                out = eng.predict_proba_rows(X, self.bin_edges, self.feature_bin_counts,
+                                             self._nan_bin_id, packed, len(self.trees),
+                                             self.learning_rate,
+                                             getattr(self, 'base_score_', 0.0))
+                self.times['inference'] = (time.perf_counter() - t0) * 1000
+            return out
         with eng.lock:  # matrix slot 1 holds this call's codes until it returns
             eng.bin_features(1, X, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
             t0 = time.perf_counter()
@@ -993,12 +1007,8 @@ class HybridHistGBMNumbaV1_0_1:
             packed = {'features': self._packed_features, 'thresholds': self._packed_thresholds,
                       'values': self._packed_values, 'left': self._packed_left,
                       'right': self._packed_right, 'offsets': self._tree_offsets}
-            if proba:
-                out = eng.predict_proba(1, X.shape[0], packed, len(self.trees),
-                                        self.learning_rate, getattr(self, 'base_score_', 0.0))
-            else:
-                out = eng.predict(1, X.shape[0], packed, len(self.trees),
-                                  self.learning_rate) + getattr(self, 'base_score_', 0.0)
+            out = eng.predict(1, X.shape[0], packed, len(self.trees),
+                              self.learning_rate) + getattr(self, 'base_score_', 0.0)
             self.times['inference'] = (time.perf_counter() - t0) * 1000
         return out
 

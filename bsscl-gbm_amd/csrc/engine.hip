@@ -459,7 +459,16 @@ struct bsscl_engine {
   // host_download), and binning of a host matrix through xchunk.
   char *xfer_pin[3] = {nullptr, nullptr, nullptr};
   hipEvent_t xfer_ev[3] = {nullptr, nullptr, nullptr};
+  int xfer_next = 0;  // the pinned chunk the next piece goes through
   TempBuf<unsigned char> xchunk;
+  // bsscl_predict_proba_rows: the second row chunk of X, one chunk's codes,
+  // and its events (chunk uploaded, chunk binned; two of each).
+  TempBuf<unsigned char> xchunk2;
+  TempBuf<uint8_t> pcodes;
+  hipEvent_t pipe_ev[4] = {nullptr, nullptr, nullptr, nullptr};
+  // The bin edges, bin counts and NaN bins of the last binning call.
+  TempBuf<double> edges_d;
+  TempBuf<int32_t> nbins_d, nanid_d;
 
   // Feature matrix staged by bsscl_stage_features (row-major, as given) and
   // its columns sorted by bsscl_sort_columns (keys [F][col_ld]).
@@ -761,27 +770,36 @@ int ensure_xfer(bsscl_engine *E) {
   return BSSCL_OK;
 }
 
-// dst (device) = src (host, pageable) on E->st; returns once the copy is
-// complete.
-int host_upload(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
-  const size_t chunk = xfer_chunk(bytes);
-  if (bytes < 2 * chunk) {
-    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, E->st));
-    HIPCHK(hipStreamSynchronize(E->st));
+// Enqueues dst (device) = src (host, pageable) on stream `st` in pieces of
+// `piece` bytes through the pinned chunks, and returns once the last piece
+// has been copied into its pinned chunk; the copies complete on `st`.  A
+// pinned chunk is refilled only after the copy that last read it, whichever
+// call or stream enqueued that one.
+int host_upload_async(bsscl_engine *E, hipStream_t st, void *dst, const void *src, size_t bytes,
+                      size_t piece) {
+  if (bytes < 2 * piece) {
+    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st));
     return BSSCL_OK;
   }
   CHK(ensure_xfer(E));
   CopyPool &pool = CopyPool::get();
-  size_t c = 0;
-  for (size_t off = 0; off < bytes; off += chunk, ++c) {
-    const int b = (int)(c % 3);
-    const size_t len = std::min(chunk, bytes - off);
-    if (c >= 3) HIPCHK(hipEventSynchronize(E->xfer_ev[b]));  // its previous chunk has gone
+  for (size_t off = 0; off < bytes; off += piece) {
+    const int b = E->xfer_next;
+    E->xfer_next = (b + 1) % 3;
+    const size_t len = std::min(piece, bytes - off);
+    HIPCHK(hipEventSynchronize(E->xfer_ev[b]));  // its previous piece has gone
     pool.copy(E->xfer_pin[b], static_cast<const char *>(src) + off, len);
     HIPCHK(hipMemcpyAsync(static_cast<char *>(dst) + off, E->xfer_pin[b], len,
-                          hipMemcpyHostToDevice, E->st));
-    HIPCHK(hipEventRecord(E->xfer_ev[b], E->st));
+                          hipMemcpyHostToDevice, st));
+    HIPCHK(hipEventRecord(E->xfer_ev[b], st));
   }
+  return BSSCL_OK;
+}
+
+// dst (device) = src (host, pageable) on E->st; returns once the copy is
+// complete.
+int host_upload(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
+  CHK(host_upload_async(E, E->st, dst, src, bytes, xfer_chunk(bytes)));
   HIPCHK(hipStreamSynchronize(E->st));
   return BSSCL_OK;
 }
@@ -800,6 +818,7 @@ int host_download(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
   auto enqueue = [&](size_t c) -> int {
     const int b = (int)(c % 3);
     const size_t off = c * chunk;
+    HIPCHK(hipEventSynchronize(E->xfer_ev[b]));  // no upload still reads the chunk
     HIPCHK(hipMemcpyAsync(E->xfer_pin[b], static_cast<const char *>(src) + off,
                           std::min(chunk, bytes - off), hipMemcpyDeviceToHost, E->st));
     HIPCHK(hipEventRecord(E->xfer_ev[b], E->st));
@@ -814,6 +833,37 @@ int host_download(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
     const size_t off = c * chunk;
     pool.copy(static_cast<char *>(dst) + off, E->xfer_pin[b], std::min(chunk, bytes - off));
   }
+  return BSSCL_OK;
+}
+
+// Code tiers and NaN presence of binning with these bin counts (checked).
+int bin_layout(int32_t F, int32_t edge_stride, const int32_t *bin_counts,
+               const int32_t *nan_bin_id, int32_t *tiers, int32_t *has_any_nan) {
+  *tiers = 1;
+  *has_any_nan = 0;
+  for (int32_t j = 0; j < F; ++j) {
+    if (bin_counts[j] < 1 || bin_counts[j] >= edge_stride)
+      return set_error(BSSCL_EINVAL, "bin_features: bin_counts must be in [1, edge_stride)");
+    if (bin_counts[j] > kMaxBinCount)
+      return set_error(BSSCL_EINVAL, "bin_features: more than 65536 bins");
+    // Training codes are at most nb - 1, which these tiers hold exactly.
+    *tiers = std::max(*tiers, tiers_for_bins(bin_counts[j]));
+    if (nan_bin_id[j] >= 0) *has_any_nan = 1;
+  }
+  return BSSCL_OK;
+}
+
+// A binning call's edges [F][edge_stride], bin counts and NaN bins into
+// E->edges_d, nbins_d and nanid_d (on E->st).
+int upload_edges(bsscl_engine *E, int32_t F, const double *edges_2d, int32_t edge_stride,
+                 const int32_t *bin_counts, const int32_t *nan_bin_id) {
+  CHK(E->edges_d.ensure((size_t)F * edge_stride));
+  CHK(E->nbins_d.ensure((size_t)F));
+  CHK(E->nanid_d.ensure((size_t)F));
+  HIPCHK(hipMemcpyAsync(E->edges_d.p, edges_2d, (size_t)F * edge_stride * 8,
+                        hipMemcpyHostToDevice, E->st));
+  HIPCHK(hipMemcpyAsync(E->nbins_d.p, bin_counts, (size_t)F * 4, hipMemcpyHostToDevice, E->st));
+  HIPCHK(hipMemcpyAsync(E->nanid_d.p, nan_bin_id, (size_t)F * 4, hipMemcpyHostToDevice, E->st));
   return BSSCL_OK;
 }
 
@@ -2823,16 +2873,13 @@ namespace bsscl {
 namespace {
 
 // The ensemble's F of matrix `slot` into E->out_d (est:863-884).
-int predict_to_device(bsscl_engine *E, int32_t slot, const int16_t *features,
-                      const int64_t *thresholds, const double *values,
-                      const int32_t *left, const int32_t *right,
-                      const int32_t *offsets, int32_t n_trees, double learning_rate) {
-  if (!E || (n_trees > 0 && (!features || !thresholds || !values || !left || !right || !offsets)))
-    return set_error(BSSCL_EINVAL, "predict: null argument");
-  CHK(check_matrix(E, slot));
-  if (n_trees < 0) return set_error(BSSCL_EINVAL, "predict: negative tree count");
-  HIPCHK(hipSetDevice(E->device));
-  const Matrix &M = E->mat[slot];
+// The packed trees (est:2192-2216) on the device in the engine's columns of
+// matrices with M's features and tiers: tree_d, and offsets_d with, for the
+// LDS-staged walk (*staged), its *n_chunks runs of whole trees after them.
+int upload_trees(bsscl_engine *E, const Matrix &M, const int16_t *features,
+                 const int64_t *thresholds, const double *values, const int32_t *left,
+                 const int32_t *right, const int32_t *offsets, int32_t n_trees, bool *staged_out,
+                 int32_t *n_chunks_out) {
   const int32_t total = n_trees > 0 ? offsets[n_trees] : 0;
   std::vector<TreeNodeDev> nodes((size_t)std::max(total, 1));
   bool adjacent = true;  // every right child is its left child + 1
@@ -2876,6 +2923,25 @@ int predict_to_device(bsscl_engine *E, int32_t slot, const int16_t *features,
   }
   CHK(upload(E, E->tree_d, nodes.data(), nodes.size()));
   CHK(upload(E, E->offsets_d, offs.data(), offs.size()));
+  *staged_out = staged;
+  *n_chunks_out = n_chunks;
+  return BSSCL_OK;
+}
+
+int predict_to_device(bsscl_engine *E, int32_t slot, const int16_t *features,
+                      const int64_t *thresholds, const double *values,
+                      const int32_t *left, const int32_t *right,
+                      const int32_t *offsets, int32_t n_trees, double learning_rate) {
+  if (!E || (n_trees > 0 && (!features || !thresholds || !values || !left || !right || !offsets)))
+    return set_error(BSSCL_EINVAL, "predict: null argument");
+  CHK(check_matrix(E, slot));
+  if (n_trees < 0) return set_error(BSSCL_EINVAL, "predict: negative tree count");
+  HIPCHK(hipSetDevice(E->device));
+  const Matrix &M = E->mat[slot];
+  bool staged = false;
+  int32_t n_chunks = 0;
+  CHK(upload_trees(E, M, features, thresholds, values, left, right, offsets, n_trees, &staged,
+                   &n_chunks));
   CHK(E->out_d.ensure((size_t)M.n));
   hipEvent_t start, stop;
   CHK(prof_kernel(E, 4, &start, &stop));
@@ -3037,6 +3103,13 @@ void bsscl_engine_destroy(bsscl_engine *E) {
     if (E->xfer_ev[b]) (void)hipEventDestroy(E->xfer_ev[b]);
   }
   E->xchunk.release();
+  E->xchunk2.release();
+  E->pcodes.release();
+  E->edges_d.release();
+  E->nbins_d.release();
+  E->nanid_d.release();
+  for (hipEvent_t ev : E->pipe_ev)
+    if (ev) (void)hipEventDestroy(ev);
   release_staging(E);
   for (hipEvent_t ev : E->ev_pool) (void)hipEventDestroy(ev);
   for (hipEvent_t ev : E->rows_ready)
@@ -3061,32 +3134,18 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
     return set_error(BSSCL_EINVAL,
                      "bin_features: X is NULL but no staged matrix of this shape and dtype");
   int32_t has_any_nan = 0, tiers = 1;
-  for (int32_t j = 0; j < F; ++j) {
-    if (bin_counts[j] < 1 || bin_counts[j] >= edge_stride)
-      return set_error(BSSCL_EINVAL, "bin_features: bin_counts must be in [1, edge_stride)");
-    if (bin_counts[j] > kMaxBinCount)
-      return set_error(BSSCL_EINVAL, "bin_features: more than 65536 bins");
-    // Training codes are at most nb - 1, which these tiers hold exactly.
-    tiers = std::max(tiers, tiers_for_bins(bin_counts[j]));
-    if (nan_bin_id[j] >= 0) has_any_nan = 1;
-  }
+  CHK(bin_layout(F, edge_stride, bin_counts, nan_bin_id, &tiers, &has_any_nan));
   HIPCHK(hipSetDevice(E->device));
   CHK(alloc_matrix(E, slot, n, F, tiers));
-  ScopedBuf<double> ed;  // (freed on the error returns as well)
-  ScopedBuf<int32_t> nb, nid;
-  CHK(ed.ensure((size_t)F * edge_stride));
-  CHK(nb.ensure((size_t)F));
-  CHK(nid.ensure((size_t)F));
-  HIPCHK(hipMemcpyAsync(ed.p, edges_2d, (size_t)F * edge_stride * 8, hipMemcpyHostToDevice, E->st));
-  HIPCHK(hipMemcpyAsync(nb.p, bin_counts, (size_t)F * 4, hipMemcpyHostToDevice, E->st));
-  HIPCHK(hipMemcpyAsync(nid.p, nan_bin_id, (size_t)F * 4, hipMemcpyHostToDevice, E->st));
+  CHK(upload_edges(E, F, edges_2d, edge_stride, bin_counts, nan_bin_id));
+  const double *ed = E->edges_d.p;
+  const int32_t *nb = E->nbins_d.p, *nid = E->nanid_d.p;
   Matrix &M = E->mat[slot];
   const size_t esz = x_is_f64 ? 8 : 4;
   if (staged) {
-    hipError_t e = launch_bin(E->st, E->xstage.p, x_is_f64, n, F, ed.p, edge_stride, nb.p,
-                              nid.p, has_any_nan, M.codes.p, M.ld, tiers);
+    hipError_t e = launch_bin(E->st, E->xstage.p, x_is_f64, n, F, ed, edge_stride, nb, nid,
+                              has_any_nan, M.codes.p, M.ld, tiers);
     if (e == hipSuccess) e = hipStreamSynchronize(E->st);
-    ed.release(); nb.release(); nid.release();
     if (e != hipSuccess)
       return set_error(BSSCL_EDEVICE, std::string("binning: ") + hipGetErrorString(e));
   } else {
@@ -3096,26 +3155,17 @@ int bsscl_bin_features(bsscl_engine *E, int32_t slot, const void *X,
     chunk = std::min<int64_t>(chunk, round_up(n, 64));
     // (The chunk buffer stays allocated for the next host matrix.)
     TempBuf<unsigned char> &xd = E->xchunk;
-    int rc = xd.ensure((size_t)chunk * F * esz);
-    if (rc != BSSCL_OK) { ed.release(); nb.release(); nid.release(); return rc; }
+    CHK(xd.ensure((size_t)chunk * F * esz));
     for (int64_t r0 = 0; r0 < n; r0 += chunk) {
       const int64_t rows = std::min(chunk, n - r0);
-      rc = host_upload(E, xd.p, (const unsigned char *)X + (size_t)r0 * F * esz,
-                       (size_t)rows * F * esz);
-      hipError_t e = rc == BSSCL_OK ? hipSuccess : hipErrorUnknown;
-      if (e == hipSuccess)
-        e = launch_bin(E->st, xd.p, x_is_f64, rows, F, ed.p, edge_stride, nb.p, nid.p,
-                       has_any_nan, M.codes.p + r0, M.ld, tiers);
+      CHK(host_upload(E, xd.p, (const unsigned char *)X + (size_t)r0 * F * esz,
+                      (size_t)rows * F * esz));
+      hipError_t e = launch_bin(E->st, xd.p, x_is_f64, rows, F, ed, edge_stride, nb, nid,
+                                has_any_nan, M.codes.p + r0, M.ld, tiers);
       if (e == hipSuccess) e = hipStreamSynchronize(E->st);
-      if (e != hipSuccess) {
-        ed.release(); nb.release(); nid.release();
-        if (rc != BSSCL_OK) return rc;
+      if (e != hipSuccess)
         return set_error(BSSCL_EDEVICE, std::string("binning: ") + hipGetErrorString(e));
-      }
     }
-    ed.release();
-    nb.release();
-    nid.release();
   }
   if (slot == 0) CHK(find_hot_bins(E));
   if (codes_out) return bsscl_get_codes(E, slot, codes_out);
@@ -3826,6 +3876,100 @@ int bsscl_predict_proba(bsscl_engine *E, int32_t slot, const int16_t *features,
   CHK(E->proba_d.ensure(2 * (size_t)n));
   HIPCHK(launch_binary_proba(E->st, E->out_d.p, n, base_score, E->proba_d.p));
   CHK(host_download(E, out_proba, E->proba_d.p, (size_t)n * 16));
+  CHK(sync(E));
+  return BSSCL_OK;
+}
+
+int bsscl_predict_proba_rows(bsscl_engine *E, const void *X, int32_t x_is_f64, int64_t n,
+                             int32_t F, const double *edges_2d, int32_t edge_stride,
+                             const int32_t *bin_counts, const int32_t *nan_bin_id,
+                             const int16_t *features, const int64_t *thresholds,
+                             const double *values, const int32_t *left, const int32_t *right,
+                             const int32_t *offsets, int32_t n_trees, double learning_rate,
+                             double base_score, double *out_proba) {
+  if (!E || !X || !edges_2d || !bin_counts || !nan_bin_id || !out_proba ||
+      (n_trees > 0 && (!features || !thresholds || !values || !left || !right || !offsets)))
+    return set_error(BSSCL_EINVAL, "predict_proba_rows: null argument");
+  if (n <= 0 || n > INT32_MAX || F <= 0)
+    return set_error(BSSCL_EINVAL, "predict_proba_rows: bad shape");
+  if (n_trees < 0) return set_error(BSSCL_EINVAL, "predict_proba_rows: negative tree count");
+  int32_t tiers = 1, has_any_nan = 0;
+  CHK(bin_layout(F, edge_stride, bin_counts, nan_bin_id, &tiers, &has_any_nan));
+  HIPCHK(hipSetDevice(E->device));
+  const size_t esz = x_is_f64 ? 8 : 4;
+  // Rows per chunk: about 256 MB of X, in whole blocks of the walk (512
+  // rows).  The walk hides its LDS latency only with many blocks per CU:
+  // 1M x 28 in eighths took 1.46 ms of walk against 0.36 ms in one launch,
+  // and 10M x 50 in 9 chunks 33 ms against 30 ms in 8.  (Test hook
+  // BSSCL_TEST_PREDICT_CHUNK_ROWS: another count.)
+  int64_t rows_c = (int64_t)((256u << 20) / (esz * (size_t)F));
+  if (const char *t = std::getenv("BSSCL_TEST_PREDICT_CHUNK_ROWS"))
+    rows_c = std::strtoll(t, nullptr, 10);
+  rows_c = std::min<int64_t>(std::max<int64_t>(512, rows_c / 512 * 512), round_up(n, 512));
+  // One chunk's codes, in the layout of a matrix of rows_c rows.
+  Matrix view;
+  view.n = rows_c;
+  view.ld = round_up(rows_c + 8, 256);
+  view.F = F;
+  view.tiers = tiers;
+  CHK(E->pcodes.ensure((size_t)view.ld * view.cols()));
+  bool staged = false;
+  int32_t n_chunks = 0;
+  CHK(upload_trees(E, view, features, thresholds, values, left, right, offsets, n_trees, &staged,
+                   &n_chunks));
+  CHK(upload_edges(E, F, edges_2d, edge_stride, bin_counts, nan_bin_id));
+  CHK(E->out_d.ensure((size_t)n));
+  CHK(E->proba_d.ensure(2 * (size_t)n));
+  const bool one_chunk = n <= rows_c;
+  const size_t xbytes = (size_t)rows_c * F * esz;
+  CHK(E->xchunk.ensure(xbytes));
+  if (!one_chunk) CHK(E->xchunk2.ensure(xbytes));
+  for (hipEvent_t &ev : E->pipe_ev)
+    if (!ev) HIPCHK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  // Chunk c goes up on the rows stream into buffer c % 2 (after the binning
+  // of chunk c - 2 has read it); the engine's stream bins it, walks it and
+  // turns its F into probabilities, while chunk c + 1 goes up.  (A single
+  // chunk goes up on the engine's stream, with nothing to overlap.)
+  hipStream_t up = one_chunk ? E->st : E->st_rows;
+  const size_t piece = xfer_chunk((size_t)n * F * esz);
+  const unsigned char *xs = static_cast<const unsigned char *>(X);
+  int rc = BSSCL_OK;
+  int c = 0;
+  for (int64_t r0 = 0; r0 < n && rc == BSSCL_OK; r0 += rows_c, ++c) {
+    const int64_t rows = std::min(rows_c, n - r0);
+    const int b = c & 1;
+    unsigned char *xb = b ? E->xchunk2.p : E->xchunk.p;
+    hipError_t e = hipSuccess;
+    if (c >= 2) e = hipStreamWaitEvent(up, E->pipe_ev[2 + b], 0);
+    if (e == hipSuccess) {
+      rc = host_upload_async(E, up, xb, xs + (size_t)r0 * F * esz, (size_t)rows * F * esz, piece);
+      if (rc != BSSCL_OK) break;
+      if (!one_chunk) e = hipEventRecord(E->pipe_ev[b], up);
+    }
+    if (e == hipSuccess && !one_chunk) e = hipStreamWaitEvent(E->st, E->pipe_ev[b], 0);
+    if (e == hipSuccess)
+      e = launch_bin(E->st, xb, x_is_f64, rows, F, E->edges_d.p, edge_stride, E->nbins_d.p,
+                     E->nanid_d.p, has_any_nan, E->pcodes.p, view.ld, tiers);
+    if (e == hipSuccess && !one_chunk) e = hipEventRecord(E->pipe_ev[2 + b], E->st);
+    hipEvent_t start = nullptr, stop = nullptr;
+    if (e == hipSuccess) {
+      rc = prof_kernel(E, 4, &start, &stop);
+      if (rc != BSSCL_OK) break;
+    }
+    if (e == hipSuccess)
+      e = launch_predict(E->st, E->pcodes.p, view.ld, rows, view.cols(), E->tree_d.p,
+                         E->offsets_d.p, n_trees, staged ? E->offsets_d.p + n_trees + 1 : nullptr,
+                         n_chunks, learning_rate, E->out_d.p + r0, start, stop);
+    if (e == hipSuccess)
+      e = launch_binary_proba(E->st, E->out_d.p + r0, rows, base_score, E->proba_d.p + 2 * r0);
+    if (e != hipSuccess)
+      rc = set_error(BSSCL_EDEVICE, std::string("predict_proba_rows: ") + hipGetErrorString(e));
+  }
+  if (rc == BSSCL_OK) rc = host_download(E, out_proba, E->proba_d.p, (size_t)n * 16);
+  // (Both streams drain before the buffers can be used again, on every path.)
+  (void)hipStreamSynchronize(E->st_rows);
+  (void)hipStreamSynchronize(E->st);
+  if (rc != BSSCL_OK) return rc;
   CHK(sync(E));
   return BSSCL_OK;
 }

@@ -286,6 +286,22 @@ int bsscl_predict_proba(bsscl_engine *eng, int32_t slot, const int16_t *features
                         const int32_t *left, const int32_t *right,
                         const int32_t *offsets, int32_t n_trees, double learning_rate,
                         double base_score, double *out_proba);
+/*
+ * The whole of a binary model's predict_proba from host rows: binning X
+ * (est:3289, as bsscl_bin_features with the same edges, bin counts and NaN
+ * bins), the walk and the probabilities (est:3318-3336, as
+ * bsscl_predict_proba), with identical results.  X streams through the
+ * device in row chunks of about 256 MB: a chunk's upload runs while the
+ * device bins and walks the chunk before it.  Leaves matrix slots 0 and 1
+ * as they were.
+ */
+int bsscl_predict_proba_rows(bsscl_engine *eng, const void *X, int32_t x_is_f64, int64_t n,
+                             int32_t F, const double *edges_2d, int32_t edge_stride,
+                             const int32_t *bin_counts, const int32_t *nan_bin_id,
+                             const int16_t *features, const int64_t *thresholds,
+                             const double *values, const int32_t *left, const int32_t *right,
+                             const int32_t *offsets, int32_t n_trees, double learning_rate,
+                             double base_score, double *out_proba);
 
 /*
  * Ensemble prediction that allocates nothing.  No counterpart in the

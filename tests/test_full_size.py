@@ -187,6 +187,9 @@ def test_stress_10m_inference(engine):
     assert p.shape == (n, 2) and np.all(np.isfinite(p))
     eng = est_mod._engine(0)
     k = n
+    # (predict_proba bins and walks the rows in chunks of its own; the codes
+    # and F are checked through the matrix the same binning fills.)
+    eng.bin_features(1, Xp, est.bin_edges, est.feature_bin_counts, est._nan_bin_id)
     codes = eng.get_codes(1, n, F)
     want = om.bin_features(Xp, est.bin_edges, est.feature_bin_counts, est._nan_bin_id,
                            "hybrid")

@@ -216,3 +216,42 @@ def test_predict_proba_device_equals_numpy_expression(engine, bin_data):
         F2 = eng.predict(1, len(Xp), packed, n_trees, 1.0) + base
         p2 = 1.0 / (1.0 + np.exp(-np.clip(F2, -500, 500)))
         np.testing.assert_allclose(got, np.column_stack([1 - p2, p2]), rtol=4.5e-16, atol=0)
+
+
+@pytest.mark.parametrize("case", ["chunks_f32_nan", "chunks_f64", "one_short_chunk",
+                                  "bins_300", "no_trees"])
+def test_predict_proba_rows_equals_binning_then_predict(engine, monkeypatch, case):
+    """bsscl_predict_proba_rows (binning, walk and probabilities of host rows
+    in overlapped row chunks) equals bsscl_bin_features followed by
+    bsscl_predict_proba bit for bit, over ragged last chunks, float64 rows,
+    fewer rows than one walk block, codes in two tiers and an empty model;
+    matrix slot 1 keeps the codes binned before it."""
+    from bsscl_gbm import estimator as est_mod
+    print(f"[case] predict_proba_rows {case}", flush=True)
+    rng = np.random.default_rng(7)
+    X, y = make_data(6000, 12, seed=5, nan_frac=0.1, nan_cols=[0, 3])
+    n_bins = 300 if case == "bins_300" else 255
+    n_est = 0 if case == "no_trees" else 25
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=max(n_est, 1), max_depth=5, n_bins=n_bins,
+                                 random_state=3, verbose=False).fit(X, y)
+    if n_est == 0:
+        m.trees = []
+        m._pack_trees()
+    n = {"one_short_chunk": 300, "chunks_f64": 40_001}.get(case, 50_003)
+    Xp = rng.standard_normal((n, 12)) * 1.5
+    Xp[rng.random(Xp.shape) < 0.05] = np.nan
+    Xp = Xp if case == "chunks_f64" else Xp.astype(np.float32)
+    if case != "one_short_chunk":
+        monkeypatch.setenv("BSSCL_TEST_PREDICT_CHUNK_ROWS", "4096")
+    eng = est_mod._engine(0)
+    packed = {"features": m._packed_features, "thresholds": m._packed_thresholds,
+              "values": m._packed_values, "left": m._packed_left, "right": m._packed_right,
+              "offsets": m._tree_offsets}
+    eng.bin_features(1, Xp, m.bin_edges, m.feature_bin_counts, m._nan_bin_id)
+    want = eng.predict_proba(1, n, packed, len(m.trees), m.learning_rate, m.base_score_)
+    codes_before = eng.get_codes(1, n, 12)
+    got = eng.predict_proba_rows(Xp, m.bin_edges, m.feature_bin_counts, m._nan_bin_id, packed,
+                                 len(m.trees), m.learning_rate, m.base_score_)
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(m.predict_proba(Xp), want)
+    np.testing.assert_array_equal(eng.get_codes(1, n, 12), codes_before)
