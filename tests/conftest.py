@@ -11,7 +11,7 @@ for p in (ROOT, os.path.join(ROOT, "bsscl-gbm_amd"), os.path.dirname(os.path.abs
 
 
 def pytest_configure(config):
-    config.addinivalue_line("markers", "gpu: needs an MI355X (runs on the GPU box)")
+    config.addinivalue_line("markers", "gpu: needs an MI355X GPU")
 
 
 @pytest.fixture(scope="session")
