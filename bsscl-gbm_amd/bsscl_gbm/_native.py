@@ -57,6 +57,7 @@ _SIGS = {
     "bsscl_predict_proba": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _f64, _P],
     "bsscl_predict_proba_rows": [_P, _P, _i32, _i64, _i32, _P, _i32, _P, _P, _P, _P, _P, _P,
                                  _P, _P, _i32, _f64, _f64, _P],
+    "bsscl_predict_proba_mc": [_P, _i32, _i32, _P, _P, _P, _P, _P, _P, _P, _f64, _P],
     "bsscl_predict_tree": [_P, _i32, _P, _P, _P, _P, _P, _i32, _P],
     "bsscl_predict_noalloc": [_P, _i32, _P, _P, _P, _P, _P, _P, _i32, _f64, _P],
     "bsscl_node_split": [_P, _P, _P, _P, _i64, _P, _i32, _P, _f64, _f64, _P, _P,
@@ -447,6 +448,29 @@ class Engine:
             self.handle, ptr(X), int(X.dtype == np.float64), n, F, ptr(e), e.shape[1], ptr(bc),
             ptr(ni), ptr(f), ptr(t), ptr(v), ptr(l), ptr(r), ptr(o), int(n_trees),
             float(learning_rate), float(base_score), ptr(out)))
+        return out
+
+    def predict_proba_mc(self, slot, n, packs, n_trees, learning_rate):
+        """bsscl_predict_proba_mc: a multiclass model's softmax probabilities
+        of matrix `slot`, shape (n, K); packs[k] is class k's packed trees
+        (None for a class without trees)."""
+        K = len(packs)
+        names = ("features", "thresholds", "values", "left", "right", "offsets")
+        dtypes = (np.int16, np.int64, np.float64, np.int32, np.int32, np.int32)
+        keep = []
+        tables = []
+        for name, dt in zip(names, dtypes):
+            arrs = [np.ascontiguousarray(p[name], dt) if p is not None else None for p in packs]
+            keep.append(arrs)
+            tables.append((ctypes.c_void_p * K)(*[a.ctypes.data if a is not None else None
+                                                 for a in arrs]))
+        nt = np.ascontiguousarray([int(t) if p is not None else 0
+                                   for p, t in zip(packs, n_trees)], np.int32)
+        out = np.empty((n, K), np.float64)
+        check(lib().bsscl_predict_proba_mc(self.handle, int(slot), K,
+                                           *[ctypes.cast(t, ctypes.c_void_p) for t in tables],
+                                           ptr(nt), float(learning_rate), ptr(out)))
+        del keep
         return out
 
     def predict_noalloc(self, slot, packed, n_trees, learning_rate, out_dev_ptr):

@@ -969,8 +969,9 @@ class HybridHistGBMNumbaV1_0_1:
     # ------------------------------------------------------------------
     def _raw_score(self, X, proba=False):
         """F = sum_t lr * value_t + base_score_ (est:3318-3324); with `proba`,
-        a binary model's predict_proba columns instead (est:3335-3336),
-        computed on the device from that F."""
+        the model's predict_proba instead (binary est:3335-3336, multiclass
+        the softmax of est:3315 with at most 16 classes), computed on the
+        device from that F."""
         X = _to_dense(X)
         if getattr(self, 'n_features_in_', None) is None:
             raise ValueError("This HybridHistGBMNumbaV1_0_1 instance is not fitted yet.")
@@ -995,6 +996,13 @@ class HybridHistGBMNumbaV1_0_1:
         with eng.lock:  # matrix slot 1 holds this call's codes until it returns
             eng.bin_features(1, X, self.bin_edges, self.feature_bin_counts, self._nan_bin_id)
             t0 = time.perf_counter()
+            if self._is_multiclass and proba:
+                # est:3293-3315 and the softmax (est:2327-2332) on the
+                # device, read back once.
+                out = eng.predict_proba_mc(1, X.shape[0], self._mc_packed,
+                                           [len(t) for t in self.mc_trees], self.learning_rate)
+                self.times['inference'] = (time.perf_counter() - t0) * 1000
+                return out
             if self._is_multiclass:
                 # est:3293-3315: per class, sum its trees from 0.0.
                 F = np.zeros((X.shape[0], self.n_classes_), dtype=np.float64)
@@ -1014,6 +1022,8 @@ class HybridHistGBMNumbaV1_0_1:
 
     def predict_proba(self, X):
         if self._is_multiclass:
+            if self.n_classes_ <= _native.MC_DEVICE_MAX_CLASSES:
+                return self._raw_score(X, proba=True)
             return self._softmax(self._raw_score(X))
         return self._raw_score(X, proba=True)
 

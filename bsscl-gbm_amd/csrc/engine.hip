@@ -2915,7 +2915,10 @@ int upload_trees(bsscl_engine *E, const Matrix &M, const int16_t *features,
   // (Test hook BSSCL_TEST_PREDICT_GLOBAL=1: every row walks the trees in HBM.)
   const bool staged = n_trees > 0 && predict_staged_ok(M.cols(), max_nodes, adjacent) &&
                       !std::getenv("BSSCL_TEST_PREDICT_GLOBAL");
-  std::vector<int32_t> offs(offsets, offsets + n_trees + 1);
+  // (A model without trees may pass no arrays at all: offsets is read only
+  // when there are trees.)
+  std::vector<int32_t> offs((size_t)n_trees + 1, 0);
+  if (n_trees > 0) std::copy(offsets, offsets + n_trees + 1, offs.begin());
   int32_t n_chunks = 0;
   if (staged) {
     offs.resize(2 * ((size_t)n_trees + 1));
@@ -3970,6 +3973,55 @@ int bsscl_predict_proba_rows(bsscl_engine *E, const void *X, int32_t x_is_f64, i
   (void)hipStreamSynchronize(E->st_rows);
   (void)hipStreamSynchronize(E->st);
   if (rc != BSSCL_OK) return rc;
+  CHK(sync(E));
+  return BSSCL_OK;
+}
+
+int bsscl_predict_proba_mc(bsscl_engine *E, int32_t slot, int32_t K,
+                           const int16_t *const *features, const int64_t *const *thresholds,
+                           const double *const *values, const int32_t *const *left,
+                           const int32_t *const *right, const int32_t *const *offsets,
+                           const int32_t *n_trees, double learning_rate, double *out_proba) {
+  if (!E || !out_proba || !n_trees || !features || !thresholds || !values || !left || !right ||
+      !offsets)
+    return set_error(BSSCL_EINVAL, "predict_proba_mc: null argument");
+  if (K < 2 || K > kMcMaxK)
+    return set_error(BSSCL_EINVAL, "predict_proba_mc: K must be in [2, " +
+                                       std::to_string(kMcMaxK) + "]");
+  CHK(check_matrix(E, slot));
+  int32_t max_total = 1, max_trees = 0;
+  for (int32_t k = 0; k < K; ++k) {
+    if (n_trees[k] < 0) return set_error(BSSCL_EINVAL, "predict_proba_mc: negative tree count");
+    if (n_trees[k] > 0 && (!features[k] || !thresholds[k] || !values[k] || !left[k] ||
+                           !right[k] || !offsets[k]))
+      return set_error(BSSCL_EINVAL, "predict_proba_mc: null tree array");
+    if (n_trees[k] > 0) max_total = std::max(max_total, offsets[k][n_trees[k]]);
+    max_trees = std::max(max_trees, n_trees[k]);
+  }
+  HIPCHK(hipSetDevice(E->device));
+  const Matrix &M = E->mat[slot];
+  const int64_t n = M.n;
+  // Every class's trees fit the tree buffers, so that no class's upload
+  // reallocates them under the walk of the class before.
+  CHK(E->tree_d.ensure((size_t)max_total));
+  CHK(E->offsets_d.ensure(2 * ((size_t)max_trees + 1)));
+  CHK(E->out_d.ensure((size_t)K * n));
+  CHK(E->proba_d.ensure((size_t)K * n));
+  // F[k] accumulated tree by tree from 0.0 (est:3293-3315), one walk per
+  // class, then the softmax of each row and one readback.
+  for (int32_t k = 0; k < K; ++k) {
+    bool staged = false;
+    int32_t n_chunks = 0;
+    CHK(upload_trees(E, M, features[k], thresholds[k], values[k], left[k], right[k], offsets[k],
+                     n_trees[k], &staged, &n_chunks));
+    hipEvent_t start, stop;
+    CHK(prof_kernel(E, 4, &start, &stop));
+    HIPCHK(launch_predict(E->st, M.codes.p, M.ld, n, M.cols(), E->tree_d.p, E->offsets_d.p,
+                          n_trees[k], staged ? E->offsets_d.p + n_trees[k] + 1 : nullptr,
+                          n_chunks, learning_rate, E->out_d.p + (size_t)k * n, start, stop));
+  }
+  HIPCHK(launch_mc_softmax(E->st, E->out_d.p, n, K, E->proba_d.p));
+  CHK(host_download(E, out_proba, E->proba_d.p, (size_t)n * K * 8));
   CHK(sync(E));
   return BSSCL_OK;
 }

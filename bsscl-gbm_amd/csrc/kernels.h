@@ -450,6 +450,8 @@ hipError_t launch_mc_apply(hipStream_t st, const uint8_t *codes, int64_t ld, int
 int64_t mc_loss_blocks(int64_t n);
 hipError_t launch_mc_loss(hipStream_t st, const double *F, const int32_t *y, int64_t n,
                           int32_t K, double *partials);
+// P[i][k] = softmax over the classes of F[k][i] (row-major n x K output).
+hipError_t launch_mc_softmax(hipStream_t st, const double *F, int64_t n, int32_t K, double *P);
 hipError_t launch_predict_tree(hipStream_t st, const uint8_t *codes,
                                int64_t ld, int64_t n, const TreeNodeDev *tree,
                                int32_t node_count, double *out);

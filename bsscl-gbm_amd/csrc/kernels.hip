@@ -4537,6 +4537,29 @@ __global__ __launch_bounds__(256) void k_mc_loss(const double *__restrict__ F,
   __syncthreads();
   if (threadIdx.x == 0) partials[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
 }
+
+// predict_proba of a multiclass model (est:3315 with est:2327-2332): row
+// i's softmax over its scores F[k][i] in the arithmetic of k_mc_grad_hess,
+// written row by row, P[i][k].
+__global__ __launch_bounds__(256) void k_mc_softmax(const double *__restrict__ F, int64_t n,
+                                                    int32_t K, double *__restrict__ P) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  double e[kMcMaxK];
+  double fmaxv = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kMcMaxK; ++k) {
+    e[k] = k < K ? F[(int64_t)k * n + i] : 0.0;
+    if (k < K) fmaxv = fmax(fmaxv, e[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < kMcMaxK; ++k)
+    if (k < K) e[k] = exp(__dsub_rn(e[k], fmaxv));
+  const double sum = numpy_row_sum(e, K);
+#pragma unroll
+  for (int k = 0; k < kMcMaxK; ++k)
+    if (k < K) P[i * K + k] = __ddiv_rn(e[k], sum);
+}
 #pragma clang fp contract(on)
 
 hipError_t launch_mc_grad_hess(hipStream_t st, const double *F, const int32_t *y, const double *w,
@@ -4555,6 +4578,14 @@ hipError_t launch_mc_apply(hipStream_t st, const uint8_t *codes, int64_t ld, int
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_mc_apply, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, codes, ld,
                      n, tree, node_count_d, lr, Fk);
+  return hipGetLastError();
+}
+
+hipError_t launch_mc_softmax(hipStream_t st, const double *F, int64_t n, int32_t K, double *P) {
+  if (n <= 0) return hipSuccess;
+  if (K < 2 || K > kMcMaxK) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_mc_softmax, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, F, n, K,
+                     P);
   return hipGetLastError();
 }
 

@@ -302,6 +302,20 @@ int bsscl_predict_proba_rows(bsscl_engine *eng, const void *X, int32_t x_is_f64,
                              const double *values, const int32_t *left, const int32_t *right,
                              const int32_t *offsets, int32_t n_trees, double learning_rate,
                              double base_score, double *out_proba);
+/*
+ * predict_proba of a multiclass model (est:3293-3315): per class k, F[:, k]
+ * accumulated tree by tree from 0.0 over the rows of matrix `slot` (class
+ * k's packed arrays, n_trees[k] of them, possibly none), then each row's
+ * softmax (est:2327-2332, in the arithmetic of the training rounds: the
+ * class sum in NumPy's pairwise order); out_proba float64[n * K], row by
+ * row.  2 <= K <= 16.  The device's exp may differ from NumPy's in the last
+ * bit.
+ */
+int bsscl_predict_proba_mc(bsscl_engine *eng, int32_t slot, int32_t K,
+                           const int16_t *const *features, const int64_t *const *thresholds,
+                           const double *const *values, const int32_t *const *left,
+                           const int32_t *const *right, const int32_t *const *offsets,
+                           const int32_t *n_trees, double learning_rate, double *out_proba);
 
 /*
  * Ensemble prediction that allocates nothing.  No counterpart in the

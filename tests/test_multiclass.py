@@ -428,3 +428,35 @@ def test_multiclass_trees_from_int64_rows(engine):
         np.testing.assert_array_equal(fa, fb)
     finally:
         other.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K", [3, 9, 16])
+def test_multiclass_predict_proba_device_equals_numpy_softmax(engine, K):
+    """A multiclass model's predict_proba with the softmax on the device
+    (bsscl_predict_proba_mc) against the reference's NumPy softmax
+    (est:2327-2332 at est:3315) of the same per-class scores: within 4 ulp
+    of 1 and mostly bit-identical (the device's exp may round a last bit
+    differently, more often with more classes per row: the same bar as the
+    gradients above).  A class without trees scores 0.0, as the reference's
+    zero-initialised column does."""
+    from bsscl_gbm import HybridHistGBMNumbaV1_0_1
+    print(f"[case] multiclass predict_proba on the device K={K}", flush=True)
+    X, y = _mc_data(8000, 9, K, seed=60 + K)
+    m = HybridHistGBMNumbaV1_0_1(n_estimators=6, max_depth=4, random_state=2,
+                                 verbose=False).fit(X, y)
+    Xp, _ = _mc_data(30000, 9, K, seed=70 + K, nan_frac=0.05)
+    for case in ("fitted", "empty_class"):
+        if case == "empty_class":
+            m.mc_trees[1] = []
+            m._pack_trees()
+        F = m._raw_score(Xp)
+        want = m._softmax(F)
+        got = m.predict_proba(Xp)
+        worst = float(np.max(np.abs(got - want))) / np.finfo(np.float64).eps
+        same = float(np.mean(got == want))
+        print(f"[result] multiclass K={K} {case} predict_proba on the device: "
+              f"{100 * same:.3f}% bit-identical, max |diff| {worst:.2f} ulp(1)", flush=True)
+        assert got.shape == (len(Xp), K)
+        assert worst <= 4.0 and same >= 0.75, (case, worst, same)
+        np.testing.assert_array_equal(m.predict(Xp), m.classes_[np.argmax(got, axis=1)])
