@@ -804,12 +804,13 @@ int host_upload(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
   return BSSCL_OK;
 }
 
-// dst (host, pageable) = src (device) after the work already on E->st.
-int host_download(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
+// dst (host, pageable) = src (device) after the work already on stream
+// `st`; returns once dst holds it.
+int host_download_on(bsscl_engine *E, hipStream_t st, void *dst, const void *src, size_t bytes) {
   const size_t chunk = xfer_chunk(bytes);
   if (bytes < 2 * chunk) {
-    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, E->st));
-    HIPCHK(hipStreamSynchronize(E->st));
+    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, st));
+    HIPCHK(hipStreamSynchronize(st));
     return BSSCL_OK;
   }
   CHK(ensure_xfer(E));
@@ -820,8 +821,8 @@ int host_download(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
     const size_t off = c * chunk;
     HIPCHK(hipEventSynchronize(E->xfer_ev[b]));  // no upload still reads the chunk
     HIPCHK(hipMemcpyAsync(E->xfer_pin[b], static_cast<const char *>(src) + off,
-                          std::min(chunk, bytes - off), hipMemcpyDeviceToHost, E->st));
-    HIPCHK(hipEventRecord(E->xfer_ev[b], E->st));
+                          std::min(chunk, bytes - off), hipMemcpyDeviceToHost, st));
+    HIPCHK(hipEventRecord(E->xfer_ev[b], st));
     return BSSCL_OK;
   };
   // Two chunks in flight ahead of the one being copied out.
@@ -834,6 +835,11 @@ int host_download(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
     pool.copy(static_cast<char *>(dst) + off, E->xfer_pin[b], std::min(chunk, bytes - off));
   }
   return BSSCL_OK;
+}
+
+// dst (host, pageable) = src (device) after the work already on E->st.
+int host_download(bsscl_engine *E, void *dst, const void *src, size_t bytes) {
+  return host_download_on(E, E->st, dst, src, bytes);
 }
 
 // Code tiers and NaN presence of binning with these bin counts (checked).
@@ -3936,6 +3942,7 @@ int bsscl_predict_proba_rows(bsscl_engine *E, const void *X, int32_t x_is_f64, i
   hipStream_t up = one_chunk ? E->st : E->st_rows;
   const size_t piece = xfer_chunk((size_t)n * F * esz);
   const unsigned char *xs = static_cast<const unsigned char *>(X);
+  std::vector<hipEvent_t> done;  // chunk c's probabilities are written
   int rc = BSSCL_OK;
   int c = 0;
   for (int64_t r0 = 0; r0 < n && rc == BSSCL_OK; r0 += rows_c, ++c) {
@@ -3965,13 +3972,33 @@ int bsscl_predict_proba_rows(bsscl_engine *E, const void *X, int32_t x_is_f64, i
                          n_chunks, learning_rate, E->out_d.p + r0, start, stop);
     if (e == hipSuccess)
       e = launch_binary_proba(E->st, E->out_d.p + r0, rows, base_score, E->proba_d.p + 2 * r0);
+    if (e == hipSuccess && !one_chunk) {
+      hipEvent_t ev = nullptr;
+      e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+      if (e == hipSuccess) {
+        done.push_back(ev);
+        e = hipEventRecord(ev, E->st);
+      }
+    }
     if (e != hipSuccess)
       rc = set_error(BSSCL_EDEVICE, std::string("predict_proba_rows: ") + hipGetErrorString(e));
   }
-  if (rc == BSSCL_OK) rc = host_download(E, out_proba, E->proba_d.p, (size_t)n * 16);
+  // The probabilities come back chunk by chunk on the rows stream, each as
+  // soon as its chunk is done, while the device works on the later chunks.
+  if (rc == BSSCL_OK && one_chunk) rc = host_download(E, out_proba, E->proba_d.p, (size_t)n * 16);
+  for (size_t k = 0; rc == BSSCL_OK && k < done.size(); ++k) {
+    const int64_t r0 = (int64_t)k * rows_c, rows = std::min(rows_c, n - r0);
+    if (hipStreamWaitEvent(E->st_rows, done[k], 0) != hipSuccess) {
+      rc = set_error(BSSCL_EDEVICE, "predict_proba_rows: stream wait failed");
+      break;
+    }
+    rc = host_download_on(E, E->st_rows, out_proba + 2 * r0, E->proba_d.p + 2 * r0,
+                          (size_t)rows * 16);
+  }
   // (Both streams drain before the buffers can be used again, on every path.)
   (void)hipStreamSynchronize(E->st_rows);
   (void)hipStreamSynchronize(E->st);
+  for (hipEvent_t ev : done) (void)hipEventDestroy(ev);
   if (rc != BSSCL_OK) return rc;
   CHK(sync(E));
   return BSSCL_OK;
